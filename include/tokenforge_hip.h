@@ -1,0 +1,137 @@
+/*
+ * tokenforge_hip.h — C ABI of the MI355X (gfx950) quantized-linear hot path.
+ *
+ * Every entry point takes plain device pointers, element counts and a HIP stream
+ * (passed as `void*`, i.e. a `hipStream_t`; NULL = the null stream). Nothing here
+ * allocates or frees device memory, synchronizes with the host, or reads tensor
+ * values on the host, with one documented exception (tf_pack_int4 writes a range
+ * flag that the caller may read). All kernels are launched asynchronously on the
+ * given stream. Outputs and workspaces are owned by the caller.
+ *
+ * Return value: 0 on success, otherwise a TF_E* code; tf_last_error() then returns a
+ * message (thread-local) naming the argument that was rejected, or the HIP error.
+ *
+ * Dtypes: fp16 buffers are `uint16_t` bit patterns (IEEE binary16); fp8 buffers are
+ * `uint8_t` OCP float8_e4m3fn codes; packed int4 buffers are `int32_t` words holding
+ * eight 4-bit values in the AWQ nibble order (nibble i holds offset AWQ_ORDER[i],
+ * AWQ_ORDER = {0,2,4,6,1,3,5,7}).
+ *
+ * The Python host side (tokenforge_amd.kernels) binds these with ctypes; the citations
+ * name the reference function (saransh-debugs/TokenForge) each entry point replaces.
+ */
+#ifndef TOKENFORGE_HIP_H
+#define TOKENFORGE_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TF_OK 0
+#define TF_EINVAL 1   /* bad argument: shape, alignment, group size, config */
+#define TF_ELAUNCH 2  /* HIP reported an error at launch */
+#define TF_ERANGE 3   /* value out of range (tf_pack_int4) */
+
+/* ABI version of this library. The autotune cache is keyed on it. */
+int tf_abi_version(void);
+
+/* Message for the last failing call on this host thread ("" if none). */
+const char* tf_last_error(void);
+
+/* --------------------------------------------------------------- packing / layout */
+
+/* pack.py:42-54 pack_int4. values int32 [rows, n] in [0,15] -> packed int32
+ * [rows, n/8], AWQ interleave. n % 8 == 0. If any value lies outside [0, 15],
+ * *range_flag (device int32, caller-zeroed) is set to 1; the packed output is then
+ * unspecified. range_flag may be NULL. */
+int tf_pack_int4(const int32_t* values, int32_t* packed, int64_t rows, int64_t n,
+                 int32_t* range_flag, void* stream);
+
+/* pack.py:57-67 unpack_int4. packed int32 [rows, words] -> int32 [rows, 8*words]. */
+int tf_unpack_int4(const int32_t* packed, int32_t* values, int64_t rows, int64_t words,
+                   void* stream);
+
+/* pack.py:141-143 repack_awq_to_tf. AWQ qweight int32 [k, n/8] (packed along N)
+ * -> qweight_t int32 [n, k/8] (packed along K, same nibble interleave). Bit-exact.
+ * k % 8 == 0, n % 8 == 0. */
+int tf_awq_to_tf(const int32_t* qweight, int32_t* qweight_t, int64_t k, int64_t n,
+                 void* stream);
+
+/* pack.py:146-148 repack_tf_to_awq. Exact inverse of tf_awq_to_tf. */
+int tf_tf_to_awq(const int32_t* qweight_t, int32_t* qweight, int64_t n, int64_t k,
+                 void* stream);
+
+/* --------------------------------------------------------------- dequant */
+
+/* w4a16.py:235-264 w4a16_dequant (== pack.py:189-194 dequantize_tf).
+ * qweight_t int32 [n, k/8], scales fp16 [k/g, n], qzeros int32 [k/g, n/8]
+ * -> out fp16 [n, k] with out[n][k] = fp16(q - z) * s (one fp16 rounding). */
+int tf_w4a16_dequant(const int32_t* qweight_t, const uint16_t* scales,
+                     const int32_t* qzeros, uint16_t* out, int64_t n, int64_t k,
+                     int32_t group_size, void* stream);
+
+/* --------------------------------------------------------------- W4A16 linear */
+
+/* Kernel families (the `kernel` field of tf_gemm_config). */
+#define TF_KERNEL_GEMV_DOT 0   /* decode: VALU dot2 + DPP reduce, M <= block_m <= 4   */
+#define TF_KERNEL_GEMV_MFMA 1  /* decode/skinny: in-register dequant + fp16 MFMA      */
+#define TF_KERNEL_GEMM_MFMA 2  /* prefill: LDS-staged dequant + fp16 MFMA, split-K    */
+
+/* Launch configuration; the counterpart of config.py:23-68 GemmConfig. The tuple
+ * (kernel, block_m, block_n, block_k, num_warps, num_stages) must name a compiled
+ * variant (see tf_num_variants / tf_get_variant); split_k is a runtime value. */
+typedef struct tf_gemm_config {
+  int32_t kernel;
+  int32_t block_m;
+  int32_t block_n;
+  int32_t block_k;
+  int32_t split_k;
+  int32_t num_warps;
+  int32_t num_stages;
+} tf_gemm_config;
+
+/* Number of compiled variants, and variant i (split_k set to 1). */
+int tf_num_variants(void);
+int tf_get_variant(int index, tf_gemm_config* out);
+
+/* Bytes of fp32 workspace tf_w4a16_linear needs for this problem and config
+ * (0 when split_k == 1 or the kernel reduces on chip). */
+int64_t tf_w4a16_workspace_bytes(int64_t m, int64_t n, int64_t k, int32_t group_size,
+                                 const tf_gemm_config* cfg);
+
+/* w4a16.py:178-232 w4a16_gemm and ops.py:86-88 _C.w4a16_gemv:
+ *   out[m][n] = fp16( sum_k fp32(x[m][k]) * fp32(fp16(q[n][k] - z) * s) + fp32(bias[n]) )
+ * x fp16 [m, k] with row stride ldx elements (16-byte aligned rows), qweight_t int32
+ * [n, k/8], scales fp16 [k/g, n], qzeros int32 [k/g, n/8], bias fp16 [n] or NULL,
+ * out fp16 [m, n] with row stride ldo. Split-K partials are reduced in a fixed order
+ * (bit-identical run to run). workspace: fp32, >= tf_w4a16_workspace_bytes. */
+int tf_w4a16_linear(const uint16_t* x, int64_t ldx, const int32_t* qweight_t,
+                    const uint16_t* scales, const int32_t* qzeros, const uint16_t* bias,
+                    uint16_t* out, int64_t ldo, int64_t m, int64_t n, int64_t k,
+                    int32_t group_size, const tf_gemm_config* cfg, float* workspace,
+                    int64_t workspace_bytes, void* stream);
+
+/* --------------------------------------------------------------- RMSNorm + FP8 */
+
+/* rmsnorm_fp8.py:76-117 rmsnorm_fp8_quant (semantics of reference.py:35-56):
+ *   y = fp16(fp16(x * rstd) * w),  rstd = 1 / sqrt(sum(x^2) / h + eps)
+ *   dynamic: scale[t] = max(amax|y| / 448, 1/(448*512)) is written;
+ *   static (static_scale != 0): scale[0] is read, not written.
+ *   q = e4m3fn(RNE(clamp(y / scale, -448, 448)))
+ * x fp16 [t, h] (row stride ldx), w fp16 [h], q uint8 [t, h] (row stride ldq),
+ * scale fp32 [t] (dynamic) or [1] (static). */
+int tf_rmsnorm_fp8_quant(const uint16_t* x, int64_t ldx, const uint16_t* weight,
+                         uint8_t* q, int64_t ldq, float* scale, int32_t static_scale,
+                         int64_t t, int64_t h, float eps, void* stream);
+
+/* Test hook for the e4m3fn encoder used by tf_rmsnorm_fp8_quant
+ * (rmsnorm_fp8.py:29-41 _round_to_e4m3_grid + cast): fp32 [count] -> uint8 [count].
+ * Inputs must lie in [-448, 448] or be NaN. */
+int tf_e4m3_encode(const float* in, uint8_t* out, int64_t count, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TOKENFORGE_HIP_H */

@@ -1,0 +1,141 @@
+"""Numpy restatement of the reference's numerics oracles (reference.py:1-56) and of the e4m3
+rounding of rmsnorm_fp8.py:29-41.
+
+Test infrastructure only (see ``oracle/__init__.py``).
+
+One deliberate, documented difference: :func:`rmsnorm` forms the sum of squares exactly
+(every x^2 of an fp16 x is exact; the fp64 sum is exact to ~2^-53) and rounds it once to
+fp32, where reference.py:37 uses torch's fp32 ``mean``, whose own summation order can land
+one ulp away. The HIP kernel sums the same exact way, so kernel and oracle agree bit for bit;
+:func:`rmsnorm_torch_order` restates reference.py:37-39 with torch's own reduction for the
+comparison against the reference as written.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+from oracle.pack import W4A16Weights, dequantize_tf
+
+FP8_E4M3_MAX = 448.0  # reference.py:9
+MIN_SCALE = 1.0 / (FP8_E4M3_MAX * 512.0)  # reference.py:10
+_F32_MIN_SCALE = np.float32(MIN_SCALE)
+_F32_MAX = np.float32(FP8_E4M3_MAX)
+
+
+def w4a16_reference(x: np.ndarray, weights: W4A16Weights, bias: np.ndarray | None = None) -> np.ndarray:
+    """reference.py:13-21: fp64 ``x @ W^T (+ bias)`` on the fp16-dequantized weights.
+
+    With non-finite inputs the product is formed elementwise, so inf * 0 -> NaN and
+    inf - inf -> NaN exactly as IEEE arithmetic (a BLAS may skip zero operands).
+    """
+    w = dequantize_tf(weights).astype(np.float64)
+    x64 = np.asarray(x).astype(np.float64)
+    if np.isfinite(x64).all():
+        y = x64 @ w.T
+    else:
+        y = (x64[:, None, :] * w[None, :, :]).sum(axis=-1)
+    if bias is not None:
+        y = y + np.asarray(bias).astype(np.float64)
+    return y
+
+
+def w4a16_fp32(x: np.ndarray, weights: W4A16Weights, bias: np.ndarray | None = None) -> np.ndarray:
+    """reference.py:24-32: dequantize per call, fp32 matmul, (+ bias in fp32), cast to fp16.
+
+    This is the reference's CPU path (ops.py:79-81), timed as the CPU baseline.
+    """
+    w = dequantize_tf(weights).astype(np.float32)
+    y = np.asarray(x).astype(np.float32) @ w.T
+    if bias is not None:
+        y = y + np.asarray(bias).astype(np.float32)
+    return y.astype(np.float16)
+
+
+def rmsnorm(x: np.ndarray, weight: np.ndarray, eps: float) -> np.ndarray:
+    """reference.py:35-39 (HF Qwen2 RMSNorm): fp32 normalize, round to fp16, times weight in
+    fp16. The fp32 mean is the correctly rounded sum divided by H (see module docstring)."""
+    x16 = np.asarray(x, dtype=np.float16)
+    h = x16.shape[-1]
+    xf = x16.astype(np.float32)
+    ss = np.sum(np.square(x16.astype(np.float64)), axis=-1, keepdims=True)
+    var = ss.astype(np.float32) / np.float32(h)
+    rstd = np.float32(1.0) / np.sqrt(var + np.float32(eps))
+    return (xf * rstd).astype(np.float16) * np.asarray(weight, dtype=np.float16)
+
+
+def rmsnorm_torch_order(x: np.ndarray, weight: np.ndarray, eps: float) -> np.ndarray:
+    """reference.py:35-39 with torch's own fp32 ``mean`` and ``rsqrt`` (library routines)."""
+    import torch
+
+    xt = torch.from_numpy(np.asarray(x, dtype=np.float16))
+    wt = torch.from_numpy(np.asarray(weight, dtype=np.float16))
+    xf = xt.to(torch.float32)
+    var = xf.pow(2).mean(dim=-1, keepdim=True)
+    return ((xf * torch.rsqrt(var + eps)).to(torch.float16) * wt).numpy()
+
+
+def e4m3_encode(values: np.ndarray) -> np.ndarray:
+    """Round fp32 values with |v| <= 448 (or NaN) to OCP e4m3fn codes, ties to even.
+
+    Follows the rounding of rmsnorm_fp8.py:29-41 (normals keep 3 mantissa bits with RNE in
+    fp32 bit space, subnormals use the fixed 2^-9 quantum, the sign is kept for +-0) and the
+    e4m3fn format: bias 7, S.1111.111 = NaN. Returns uint8 codes.
+    """
+    v = np.asarray(values, dtype=np.float32)
+    bits = v.view(np.uint32)
+    sign = (bits >> np.uint32(24)) & np.uint32(0x80)
+    a = bits & np.uint32(0x7FFFFFFF)
+    is_nan = a > np.uint32(0x7F800000)
+    is_sub = a < np.uint32(0x3C800000)
+    with np.errstate(over="ignore", invalid="ignore"):
+        sub = np.rint(a.view(np.float32) * np.float32(512.0)).astype(np.uint32)
+        r = a + np.uint32(0x7FFFF) + ((a >> np.uint32(20)) & np.uint32(1))
+        normal = (r >> np.uint32(20)) - np.uint32(120 << 3)
+    code = np.where(is_nan, np.uint32(0x7F), np.where(is_sub, sub, normal)) & np.uint32(0x7F)
+    return (code | sign).astype(np.uint8)
+
+
+_E4M3_TABLE: np.ndarray | None = None
+
+
+def e4m3_decode(codes: np.ndarray) -> np.ndarray:
+    """e4m3fn codes -> fp32 values from the format definition (NaN for S.1111.111)."""
+    global _E4M3_TABLE
+    if _E4M3_TABLE is None:
+        table = np.zeros(256, dtype=np.float32)
+        for c in range(256):
+            s = -1.0 if c & 0x80 else 1.0
+            e = (c >> 3) & 0xF
+            m = c & 7
+            if e == 0xF and m == 7:
+                table[c] = np.nan
+            elif e == 0:
+                table[c] = s * m * 2.0**-9
+            else:
+                table[c] = s * (1.0 + m / 8.0) * 2.0 ** (e - 7)
+        _E4M3_TABLE = table
+    return _E4M3_TABLE[np.asarray(codes, dtype=np.uint8)]
+
+
+def fp8_quant_reference(y: np.ndarray, scale: np.ndarray | None = None) -> tuple[np.ndarray, np.ndarray]:
+    """reference.py:42-50: per-token dynamic (or static) saturating e4m3 quantization.
+
+    Returns ``(codes uint8 [T, H], scale fp32 [T, 1] or the given static scale)``. NaN
+    propagates through amax, the clamp and the cast like torch's ops.
+    """
+    yf = np.asarray(y).astype(np.float32)
+    if scale is None:
+        amax = np.max(np.abs(yf), axis=-1, keepdims=True)
+        scale = np.maximum(amax / _F32_MAX, _F32_MIN_SCALE)
+    else:
+        scale = np.asarray(scale, dtype=np.float32)
+    q = np.clip(yf / scale, -_F32_MAX, _F32_MAX)
+    return e4m3_encode(q), scale.astype(np.float32)
+
+
+def rmsnorm_fp8_reference(
+    x: np.ndarray, weight: np.ndarray, eps: float, scale: np.ndarray | None = None
+) -> tuple[np.ndarray, np.ndarray]:
+    """reference.py:53-56."""
+    return fp8_quant_reference(rmsnorm(x, weight, eps), scale)

@@ -1,0 +1,164 @@
+"""T1/T2: fused RMSNorm + e4m3 HIP kernel vs the oracle and vs the reference's torch order.
+
+Bars (north star): codes and scales bit-exact against the oracle restatement of
+reference.py:35-56 (which forms the fp32 mean from the exact sum, as the kernel does);
+against the reference's literal torch order, codes within one e4m3 code on < 0.1% of the
+elements, caused only by last-ulp differences of torch's fp32 ``mean``. The reference's own
+assertions (every row reaches 448, dequantization within 2^-3, saturation, signed zeros,
+MIN_SCALE on a zero row) are kept.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import tokenforge_amd.kernels.ops  # noqa: F401
+from oracle import reference as oref
+from tokenforge_amd.kernels.hip.rmsnorm_fp8 import FP8_E4M3_MAX, e4m3_encode, rmsnorm_fp8_quant
+
+pytestmark = pytest.mark.gpu
+EPS = 1e-6
+
+
+def _inputs(t: int, h: int, seed: int, scale: float = 2.0) -> tuple[torch.Tensor, torch.Tensor]:
+    """The reference test's generator (test_rmsnorm_fp8.py:30-34)."""
+    gen = torch.Generator().manual_seed(seed)
+    x = (torch.randn((t, h), generator=gen) * scale).to(torch.float16)
+    w = (torch.rand((h,), generator=gen) + 0.5).to(torch.float16)
+    return x, w
+
+
+def baseline_inputs(t: int, h: int = 3584, seed: int = 0) -> tuple[torch.Tensor, torch.Tensor, list[int]]:
+    """x ~ N(0,1) with 8 fixed outlier channels x20, gamma ~ N(1, 0.1)."""
+    chan = torch.randperm(h, generator=torch.Generator().manual_seed(0))[:8].tolist()
+    gen = torch.Generator().manual_seed(1000 + seed)
+    x = torch.randn((t, h), generator=gen)
+    x[:, chan] *= 20.0
+    gamma = (1.0 + 0.1 * torch.randn((h,), generator=gen)).to(torch.float16)
+    return x.to(torch.float16), gamma, chan
+
+
+def _codes(q: torch.Tensor) -> np.ndarray:
+    return q.cpu().view(torch.uint8).numpy()
+
+
+def _code_distance(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """Distance in e4m3 codes between same-sign values (ordering of the low 7 bits)."""
+    a = a.astype(np.int16)
+    b = b.astype(np.int16)
+    mag_a, mag_b = a & 0x7F, b & 0x7F
+    same_sign = ((a & 0x80) == (b & 0x80)) | (mag_a == 0) | (mag_b == 0)
+    dist = np.abs(mag_a - mag_b)
+    dist[~same_sign] = 255
+    return dist
+
+
+def _check_against_torch_order(q: torch.Tensor, s: torch.Tensor, x: torch.Tensor, w: torch.Tensor) -> None:
+    y_t = oref.rmsnorm_torch_order(x.numpy(), w.numpy(), EPS)
+    q_t, s_t = oref.fp8_quant_reference(y_t)
+    dist = _code_distance(_codes(q), q_t)
+    assert int(dist.max()) <= 1, f"max code distance {int(dist.max())}"
+    assert float((dist > 0).mean()) < 1e-3, "more than 0.1% of codes differ from the torch order"
+    rel = np.abs(s.cpu().numpy() - s_t) / s_t
+    assert float(rel.max()) <= 1e-3
+
+
+@pytest.mark.parametrize("h", [896, 3584, 1000])
+@pytest.mark.parametrize("t", [1, 7, 33])
+def test_dynamic_per_token(t: int, h: int, device: torch.device) -> None:
+    x, w = _inputs(t, h, seed=t * h)
+    q, s = rmsnorm_fp8_quant(x.to(device), w.to(device), EPS)
+    q_ref, s_ref = oref.rmsnorm_fp8_reference(x.numpy(), w.numpy(), EPS)
+    assert q.dtype == torch.float8_e4m3fn
+    assert s.shape == (t, 1)
+    assert np.array_equal(_codes(q), q_ref)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+    _check_against_torch_order(q, s, x, w)
+    # Per-token scaling: every row hits the e4m3 maximum at its absmax.
+    assert bool((q.cpu().float().abs().amax(dim=-1) == FP8_E4M3_MAX).all())
+    # Dequantized values track the fp16 RMSNorm output to e4m3 precision (3 mantissa bits).
+    y = oref.rmsnorm(x.numpy(), w.numpy(), EPS).astype(np.float32)
+    deq = q.cpu().float().numpy() * s.cpu().numpy()
+    rel = np.abs(deq - y) / np.maximum(np.abs(y), float(s_ref.max()))
+    assert float(rel.max()) <= 2.0**-3
+
+
+@pytest.mark.parametrize("t", [1, 16, 512, 4096])
+def test_baseline_config2_bit_exact(t: int, device: torch.device) -> None:
+    x, gamma, _ = baseline_inputs(t)
+    q, s = rmsnorm_fp8_quant(x.to(device), gamma.to(device), EPS)
+    q_ref, s_ref = oref.rmsnorm_fp8_reference(x.numpy(), gamma.numpy(), EPS)
+    assert np.array_equal(_codes(q), q_ref)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+    _check_against_torch_order(q, s, x, gamma)
+
+
+def test_static_scale_saturates_exactly(device: torch.device) -> None:
+    x, w = _inputs(16, 896, seed=11, scale=3.0)
+    scale = np.array([2e-3], dtype=np.float32)
+    q, s_out = rmsnorm_fp8_quant(x.to(device), w.to(device), EPS, torch.from_numpy(scale).to(device))
+    q_ref, _ = oref.rmsnorm_fp8_reference(x.numpy(), w.numpy(), EPS, scale)
+    assert torch.equal(s_out.cpu(), torch.from_numpy(scale))
+    y = oref.rmsnorm(x.numpy(), w.numpy(), EPS).astype(np.float32) / scale
+    saturated = np.abs(y) >= FP8_E4M3_MAX
+    assert int(saturated.sum()) > 100, "test must exercise saturation"
+    qf = q.cpu().float().numpy()
+    assert np.array_equal(_codes(q), q_ref)
+    assert bool((np.abs(qf[saturated]) == FP8_E4M3_MAX).all())
+    assert not bool(np.isnan(qf).any()), "saturating cast must never emit NaN"
+
+
+def test_e4m3_rounding_is_bit_exact_at_every_midpoint(device: torch.device) -> None:
+    """Every e4m3 value, every midpoint between neighbours, and the fp32 values either side
+    of each midpoint round exactly like PyTorch's ``to(float8_e4m3fn)``, signs included."""
+    values = torch.arange(0, 0x7F, dtype=torch.uint8).view(torch.float8_e4m3fn).float()
+    mids = (values[1:] + values[:-1]) / 2
+    up, down = torch.tensor(1e9), torch.tensor(-1e9)
+    probe = torch.cat([values, mids, mids.nextafter(up), mids.nextafter(down)])
+    probe = torch.cat([probe, -probe, torch.tensor([0.0, -0.0])])
+    gen = torch.Generator().manual_seed(5)
+    probe = torch.cat([probe, (torch.rand(1 << 20, generator=gen) * 2 - 1) * 448,
+                       (torch.rand(1 << 18, generator=gen) * 2 - 1) * 0.03])
+    out = e4m3_encode(probe.to(device))
+    assert np.array_equal(_codes(out), probe.to(torch.float8_e4m3fn).view(torch.uint8).numpy())
+
+
+def test_zero_row_uses_min_scale(device: torch.device) -> None:
+    x = torch.zeros((2, 256), dtype=torch.float16)
+    w = torch.ones(256, dtype=torch.float16)
+    q, s = rmsnorm_fp8_quant(x.to(device), w.to(device), EPS)
+    assert bool((q.cpu().float() == 0).all())
+    assert np.array_equal(s.cpu().numpy(), np.full((2, 1), np.float32(oref.MIN_SCALE)))
+
+
+def test_op_matches_kernel_and_keeps_leading_dims(device: torch.device) -> None:
+    x, w = _inputs(6, 896, seed=3)
+    q, s = torch.ops.tokenforge.rmsnorm_fp8_quant(x.reshape(2, 3, 896).to(device), w.to(device), EPS, None)
+    assert q.shape == (2, 3, 896)
+    assert s.shape == (2, 3, 1)
+    qk, sk = rmsnorm_fp8_quant(x.to(device), w.to(device), EPS)
+    assert np.array_equal(_codes(q.reshape(6, 896)), _codes(qk))
+    assert torch.equal(s.reshape(6, 1).cpu(), sk.cpu())
+
+
+def test_unaligned_rows_take_the_scalar_path(device: torch.device) -> None:
+    x, w = _inputs(5, 1000, seed=9)
+    buf = torch.empty(5 * 1003 + 1, dtype=torch.float16, device=device)
+    xs = buf[1:].view(5, 1003)[:, :1000]
+    xs.copy_(x.to(device))
+    q, s = rmsnorm_fp8_quant(xs, w.to(device), EPS)
+    q_ref, s_ref = oref.rmsnorm_fp8_reference(x.numpy(), w.numpy(), EPS)
+    assert np.array_equal(_codes(q), q_ref)
+    assert np.array_equal(s.cpu().numpy(), s_ref)
+
+
+def test_rejects_bad_inputs(device: torch.device) -> None:
+    x, w = _inputs(2, 128, seed=0)
+    with pytest.raises(ValueError, match="2-D"):
+        rmsnorm_fp8_quant(x.reshape(-1).to(device), w.to(device), EPS)
+    with pytest.raises(ValueError, match="weight shape"):
+        rmsnorm_fp8_quant(x.to(device), w[:64].to(device), EPS)
+    with pytest.raises(ValueError, match="single fp32"):
+        rmsnorm_fp8_quant(x.to(device), w.to(device), EPS, torch.ones(2, device=device))

@@ -1,0 +1,338 @@
+"""T1: W4A16 HIP kernels vs the oracle's fp64 reference on the fp16-dequantized weights.
+
+Mirrors the reference's tests/numerics/test_w4a16.py: every kernel family and code path,
+ragged N, bias, split-K, leading dims, zero rows, misaligned and column-major x, bad
+layouts, F1 outliers, Inf/NaN propagation, zero and denormal scales, all-zero weights.
+Two bounds are checked on every output: the derived tolerance
+``c * sqrt(K) * eps_fp16 * max|x| * max|w|`` (c calibrated against the vendor fp16 GEMM on
+this GPU) and the north-star bound ``max|y - ref32| / max|ref32| <= 1e-2`` against an fp32
+dequant-then-matmul.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import tokenforge_amd.kernels.ops  # noqa: F401  (registers torch.ops.tokenforge)
+from oracle import pack as opack
+from oracle import reference as oref
+from tests.numerics import cases
+from tests.numerics.shapes import linear_shapes, m_values
+from tests.numerics.tolerance import NORMWISE_MAX, atol, normwise
+from tokenforge_amd.kernels.config import GemmConfig
+from tokenforge_amd.kernels.hip.w4a16 import w4a16_dequant, w4a16_gemm
+from tokenforge_amd.kernels.metrics import KERNEL_CALLS
+from tokenforge_amd.kernels.pack import W4A16Weights
+
+pytestmark = pytest.mark.gpu
+G = cases.GROUP_SIZE
+
+
+def _linear(x: torch.Tensor, w: W4A16Weights, bias: torch.Tensor | None = None) -> torch.Tensor:
+    return torch.ops.tokenforge.w4a16_linear(
+        x, w.qweight_t, w.scales, w.qzeros, bias, w.group_size, "hip"
+    )
+
+
+def _assert_close(y: torch.Tensor, x: torch.Tensor, w: opack.W4A16Weights, bias=None) -> None:
+    xn = x.detach().cpu().numpy()
+    bn = None if bias is None else bias.detach().cpu().numpy()
+    ref = oref.w4a16_reference(xn, w, bn)
+    y64 = y.detach().cpu().numpy().astype(np.float64)
+    w16 = opack.dequantize_tf(w)
+    tol = atol(xn, w16, "cuda")
+    err = float(np.abs(y64 - ref).max()) if y64.size else 0.0
+    assert err <= tol, f"max abs err {err:.3e} > derived tol {tol:.3e}"
+    ref32 = xn.astype(np.float32) @ w16.astype(np.float32).T
+    if bn is not None:
+        ref32 = ref32 + bn.astype(np.float32)
+    nw = normwise(y64, ref32)
+    assert nw <= NORMWISE_MAX, f"normwise error {nw:.3e} > {NORMWISE_MAX}"
+
+
+SHAPES = linear_shapes()
+
+
+@pytest.mark.parametrize("m", m_values())
+@pytest.mark.parametrize("shape", SHAPES, ids=[f"{s.model}/{s.layer}" for s in SHAPES])
+def test_linear_shape_suite(shape, m: int, device: torch.device) -> None:  # type: ignore[no-untyped-def]
+    for seed in cases.TEST_SEEDS:
+        w = cases.layer_weights(shape.n, shape.k, seed)
+        x = cases.activations(m, shape.k, seed)
+        y = _linear(x.to(device), cases.on_device(w, device))
+        assert y.shape == (m, shape.n)
+        assert y.dtype == torch.float16
+        _assert_close(y, x, w)
+
+
+PATH_CONFIGS = [
+    GemmConfig("gemv_dot", 1, 16, 128, 1, 1, 1),
+    GemmConfig("gemv_dot", 1, 64, 128, 1, 4, 2),
+    GemmConfig("gemv_dot", 1, 32, 128, 1, 16, 4),
+    GemmConfig("gemv_dot", 2, 32, 128, 1, 2, 2),
+    GemmConfig("gemv_dot", 4, 16, 128, 1, 8, 1),
+    GemmConfig("gemv_mfma", 16, 16, 128, 1, 1, 1),
+    GemmConfig("gemv_mfma", 16, 64, 128, 1, 8, 2),
+    GemmConfig("gemv_mfma", 16, 32, 128, 1, 16, 4),
+    GemmConfig("gemv_mfma", 32, 32, 128, 1, 4, 2),
+    GemmConfig("gemm_mfma", 64, 64, 64, 1, 4, 2),
+    GemmConfig("gemm_mfma", 64, 128, 64, 3, 4, 2),
+    GemmConfig("gemm_mfma", 128, 128, 32, 2, 4, 2),
+    GemmConfig("gemm_mfma", 256, 128, 64, 4, 4, 2),
+    GemmConfig("gemm_mfma", 128, 256, 64, 1, 4, 2),
+]
+
+
+def _m_list(cfg: GemmConfig) -> tuple[int, ...]:
+    if cfg.kernel == "gemv_dot":
+        return tuple(sorted({1, cfg.block_m}))
+    return (1, cfg.block_m - 1, cfg.block_m + 3)
+
+
+def _cfg_id(c: GemmConfig) -> str:
+    return f"{c.kernel}-bm{c.block_m}-bn{c.block_n}-bk{c.block_k}-sk{c.split_k}-w{c.num_warps}-st{c.num_stages}"
+
+
+@pytest.mark.parametrize("with_bias", [False, True])
+@pytest.mark.parametrize("cfg", PATH_CONFIGS, ids=_cfg_id)
+def test_every_code_path(cfg: GemmConfig, with_bias: bool, device: torch.device) -> None:
+    n, k = 200, 512  # N not a multiple of any block_n
+    w = cases.layer_weights(n, k, 0)
+    b = cases.bias(n, 0) if with_bias else None
+    wd = cases.on_device(w, device)
+    for m in _m_list(cfg):
+        x = cases.activations(m, k, 0)
+        y = w4a16_gemm(
+            x.to(device), wd.qweight_t, wd.scales, wd.qzeros, G, cfg, None if b is None else b.to(device)
+        )
+        _assert_close(y, x, w, b)
+
+
+@pytest.mark.parametrize("group_size", [32, 64])
+def test_small_group_sizes(group_size: int, device: torch.device) -> None:
+    n, k = 96, 384
+    w = cases.layer_weights(n, k, 0, group_size)
+    wd = cases.on_device(w, device)
+    configs = [
+        GemmConfig("gemv_dot", 1, 16, 128, 1, 2, 1),
+        GemmConfig("gemv_mfma", 16, 32, 128, 1, 2, 2),
+        GemmConfig("gemm_mfma", 64, 64, 32, 2, 4, 2),
+    ]
+    if group_size == 64:
+        configs.append(GemmConfig("gemm_mfma", 128, 128, 64, 1, 4, 2))
+    for cfg in configs:
+        for m in (1, 5, 40):
+            if cfg.kernel == "gemv_dot" and m > cfg.block_m:
+                continue
+            x = cases.activations(m, k, 1)
+            y = w4a16_gemm(x.to(device), wd.qweight_t, wd.scales, wd.qzeros, group_size, cfg)
+            _assert_close(y, x, w)
+    assert torch.equal(
+        w4a16_dequant(wd.qweight_t, wd.scales, wd.qzeros, group_size).cpu(),
+        torch.from_numpy(opack.dequantize_tf(w)),
+    )
+
+
+def test_dequant_kernel_is_exact(device: torch.device) -> None:
+    w = cases.layer_weights(200, 384, 0)
+    wd = cases.on_device(w, device)
+    out = w4a16_dequant(wd.qweight_t, wd.scales, wd.qzeros, G)
+    assert torch.equal(out.cpu(), torch.from_numpy(opack.dequantize_tf(w)))
+    op = torch.ops.tokenforge.w4a16_dequant(wd.qweight_t, wd.scales, wd.qzeros, G)
+    assert torch.equal(op, out)
+
+
+def test_large_m_routes_to_gemm(device: torch.device) -> None:
+    KERNEL_CALLS.reset()
+    w = cases.layer_weights(128, 256, 0)
+    x = cases.activations(300, 256, 0)
+    y = _linear(x.to(device), cases.on_device(w, device))
+    _assert_close(y, x, w)
+    assert KERNEL_CALLS.value(kernel="hip_gemm", bucket="512") == 1
+    x1 = cases.activations(3, 256, 0)
+    _linear(x1.to(device), cases.on_device(w, device))
+    assert KERNEL_CALLS.value(kernel="hip_gemv", bucket="4") == 1
+
+
+def test_leading_dims_and_bias_through_op(device: torch.device) -> None:
+    w = cases.layer_weights(64, 256, 0)
+    b = cases.bias(64, 0)
+    x = cases.activations(6, 256, 0)
+    y = _linear(x.reshape(2, 3, 256).to(device), cases.on_device(w, device), b.to(device))
+    assert y.shape == (2, 3, 64)
+    _assert_close(y.reshape(6, 64), x, w, b)
+
+
+def test_zero_rows(device: torch.device) -> None:
+    w = cases.on_device(cases.layer_weights(64, 256, 0), device)
+    y = _linear(torch.empty((0, 256), dtype=torch.float16, device=device), w)
+    assert y.shape == (0, 64)
+
+
+def test_non_contiguous_and_misaligned_inputs_are_handled(device: torch.device) -> None:
+    w = cases.layer_weights(64, 256, 0)
+    wd = cases.on_device(w, device)
+    x = cases.activations(4, 256, 0)
+    # Column-major view: the op makes it contiguous along K.
+    x_cm = x.t().contiguous().t().to(device)
+    assert x_cm.stride(1) != 1
+    _assert_close(_linear(x_cm, wd), x, w)
+    # Storage offset of one fp16 element: base pointer is not 16-byte aligned.
+    buf = torch.empty(4 * 256 + 1, dtype=torch.float16, device=device)
+    x_mis = buf[1:].view(4, 256)
+    x_mis.copy_(x.to(device))
+    assert x_mis.data_ptr() % 16 != 0
+    _assert_close(_linear(x_mis, wd), x, w)
+    # Row stride that is not a multiple of 8 elements.
+    big = torch.zeros((4, 260), dtype=torch.float16, device=device)
+    big[:, :256] = x.to(device)
+    x_str = big[:, :256]
+    assert x_str.stride(0) == 260
+    _assert_close(_linear(x_str, wd), x, w)
+
+
+def test_rejects_bad_weight_layouts(device: torch.device) -> None:
+    w = cases.on_device(cases.layer_weights(64, 256, 0), device)
+    x = cases.activations(1, 256, 0).to(device)
+    cfg = GemmConfig("gemv_dot", 1, 16, 128, 1, 1, 1)
+    with pytest.raises(ValueError, match="contiguous"):
+        w4a16_gemm(x, w.qweight_t.t().contiguous().t(), w.scales, w.qzeros, G, cfg)
+    with pytest.raises(ValueError, match="encodes K"):
+        w4a16_gemm(x[:, :128], w.qweight_t, w.scales, w.qzeros, G, cfg)
+    with pytest.raises(TypeError, match="fp16"):
+        w4a16_gemm(x.float(), w.qweight_t, w.scales, w.qzeros, G, cfg)
+    with pytest.raises(ValueError, match="divide"):
+        w4a16_gemm(x, w.qweight_t, w.scales, w.qzeros, G, GemmConfig("gemm_mfma", 64, 64, 256, 1, 4, 2))
+    with pytest.raises(ValueError, match="block_m"):
+        w4a16_gemm(x.expand(3, 256).contiguous(), w.qweight_t, w.scales, w.qzeros, G, cfg)
+
+
+def test_cpu_tensors_raise_instead_of_falling_back() -> None:
+    w = cases.layer_weights(64, 256, 0)
+    wc = cases.on_device(w, torch.device("cpu"))
+    with pytest.raises(RuntimeError, match="CPU"):
+        _linear(cases.activations(2, 256, 0), wc)
+
+
+# ----------------------------------------------------------------------------- F1 and edges
+
+
+def _weights_from_ints(q: torch.Tensor, z: torch.Tensor, s: torch.Tensor) -> opack.W4A16Weights:
+    """q [K, N] ints, z [K//G, N] ints, s [K//G, N] fp16 -> oracle TokenForge weights."""
+    qweight, qzeros = opack.awq_pack(q.to(torch.int32).numpy(), z.to(torch.int32).numpy())
+    return opack.pack_awq(qweight, qzeros, s.to(torch.float16).numpy(), G)
+
+
+F1_CONFIGS = (
+    GemmConfig("gemv_dot", 2, 16, 128, 1, 2, 1),
+    GemmConfig("gemv_mfma", 16, 16, 128, 1, 2, 1),
+    GemmConfig("gemm_mfma", 64, 64, 64, 2, 4, 2),
+)
+
+
+def test_f1_outliers_cancel_without_fp16_overflow(device: torch.device) -> None:
+    """Products of 6e4 x 1.6 overflow fp16; fp32 products + accumulation must cancel them."""
+    k, n = 256, 64
+    gen = torch.Generator().manual_seed(0)
+    q = torch.randint(0, 16, (k, n), generator=gen)
+    q[1] = q[0] = 15  # rows 0 and 1 share group 0 -> identical dequantized weights
+    z = torch.full((k // G, n), 7)
+    s = torch.full((k // G, n), 0.2)
+    w = _weights_from_ints(q, z, s)
+    wd = cases.on_device(w, device)
+    x = (torch.randn((2, k), generator=gen) * 0.5).to(torch.float16)
+    x[:, 0], x[:, 1] = 6e4, -6e4
+    for cfg in F1_CONFIGS:
+        y = w4a16_gemm(x.to(device), wd.qweight_t, wd.scales, wd.qzeros, G, cfg)
+        assert bool(torch.isfinite(y).all()), f"spurious Inf/NaN with {cfg}"
+        assert np.isfinite(oref.w4a16_reference(x.numpy(), w)).all()
+        _assert_close(y, x, w)
+
+
+def test_f1_real_inf_and_nan_propagate(device: torch.device) -> None:
+    w = cases.layer_weights(64, 256, 0)
+    wd = cases.on_device(w, device)
+    x = cases.activations(16, 256, 0)
+    x[0, 5] = float("inf")
+    x[1, 7] = float("-inf")
+    x[2, 9] = float("nan")
+    ref16 = torch.from_numpy(oref.w4a16_reference(x.numpy(), w)).to(torch.float16)
+    configs = (
+        GemmConfig("gemv_dot", 4, 16, 128, 1, 2, 1),
+        GemmConfig("gemv_mfma", 16, 16, 128, 1, 2, 1),
+        GemmConfig("gemm_mfma", 64, 64, 64, 2, 4, 2),
+    )
+    for cfg in configs:
+        rows = x[: 4 if cfg.kernel == "gemv_dot" else 16]
+        y = w4a16_gemm(rows.to(device), wd.qweight_t, wd.scales, wd.qzeros, G, cfg).cpu()
+        r = ref16[: rows.shape[0]]
+        assert torch.equal(torch.isnan(y), torch.isnan(r)), cfg
+        assert torch.equal(torch.isposinf(y), torch.isposinf(r)), cfg
+        assert torch.equal(torch.isneginf(y), torch.isneginf(r)), cfg
+        assert bool(torch.isfinite(y[3:]).all()), "Inf leaked into clean rows"
+
+
+@pytest.mark.parametrize("scale_value", [0.0, 2.0**-24, 6e-6])  # zero, min denormal, denormal
+def test_zero_and_denormal_scales(scale_value: float, device: torch.device) -> None:
+    k, n = 256, 64
+    gen = torch.Generator().manual_seed(1)
+    q = torch.randint(0, 16, (k, n), generator=gen)
+    z = torch.randint(0, 16, (k // G, n), generator=gen)
+    s = torch.rand((k // G, n), generator=gen) * 0.01 + 1e-3
+    s[0, :] = scale_value  # group 0 of every column
+    w = _weights_from_ints(q, z, s)
+    wd = cases.on_device(w, device)
+    x = cases.activations(3, k, 0)
+    for cfg in (GemmConfig("gemv_dot", 1, 16, 128, 1, 1, 1),) + F1_CONFIGS:
+        rows = x[: min(3, cfg.block_m)]
+        y = w4a16_gemm(rows.to(device), wd.qweight_t, wd.scales, wd.qzeros, G, cfg)
+        assert bool(torch.isfinite(y).all())
+        _assert_close(y, rows, w)
+    assert torch.equal(
+        w4a16_dequant(wd.qweight_t, wd.scales, wd.qzeros, G).cpu(),
+        torch.from_numpy(opack.dequantize_tf(w)),
+    )
+
+
+def test_all_zero_weights_are_exact(device: torch.device) -> None:
+    k, n = 128, 16
+    w = _weights_from_ints(torch.full((k, n), 9), torch.full((1, n), 9), torch.full((1, n), 0.5))
+    y = _linear(cases.activations(2, k, 0).to(device), cases.on_device(w, device))
+    assert bool((y == 0).all())
+
+
+# ----------------------------------------------------------------------------- determinism
+
+
+def test_split_k_is_deterministic_and_graph_safe(device: torch.device) -> None:
+    """F5: same inputs and config -> bit-identical output, eager and under HIP-graph replay."""
+    w = cases.on_device(cases.layer_weights(1152, 896, 0), device)
+    configs = [
+        GemmConfig("gemv_dot", 1, 32, 128, 1, 4, 2),
+        GemmConfig("gemv_mfma", 16, 16, 128, 1, 8, 2),
+        GemmConfig("gemm_mfma", 64, 64, 64, 7, 4, 2),
+    ]
+    for cfg in configs:
+        m = 1 if cfg.kernel == "gemv_dot" else 48
+        x = cases.activations(m, 896, 0).to(device)
+        first = w4a16_gemm(x, w.qweight_t, w.scales, w.qzeros, G, cfg)
+        for _ in range(3):
+            assert torch.equal(w4a16_gemm(x, w.qweight_t, w.scales, w.qzeros, G, cfg), first)
+        graph = torch.cuda.CUDAGraph()
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(stream):
+            w4a16_gemm(x, w.qweight_t, w.scales, w.qzeros, G, cfg)  # warm the allocator
+            with torch.cuda.graph(graph, stream=stream):
+                out = w4a16_gemm(x, w.qweight_t, w.scales, w.qzeros, G, cfg)
+        torch.cuda.current_stream().wait_stream(stream)
+        for _ in range(3):
+            out.zero_()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, first), cfg
+            eager = w4a16_gemm(x, w.qweight_t, w.scales, w.qzeros, G, cfg)
+            torch.cuda.synchronize()
+            assert torch.equal(eager, first)

@@ -1,0 +1,204 @@
+"""T0 + F4: the autotune cache is written atomically and never trusted when corrupt
+(test_autotune_cache.py in the reference, re-keyed on the gfx950 identity and kernel ABI)."""
+
+from __future__ import annotations
+
+import json
+import logging
+from pathlib import Path
+
+import pytest
+import torch
+
+from tokenforge_amd.kernels import autotune
+from tokenforge_amd.kernels.config import GemmConfig, candidate_configs, default_config
+
+GPU = "test-gpu-gfx950"
+N, K, G = 64, 256, 128
+TUNED_1 = GemmConfig("gemv_dot", 1, 32, 128, 1, 2, 2)
+TUNED_16 = GemmConfig("gemv_mfma", 16, 32, 128, 1, 4, 2)
+TUNED_256 = GemmConfig("gemm_mfma", 128, 128, 64, 2, 4, 2)
+
+
+def _fresh_cache() -> autotune.AutotuneCache:
+    autotune.reset_caches()
+    return autotune.get_cache(GPU)
+
+
+def _populated(cache: autotune.AutotuneCache) -> None:
+    cache.put(1, N, K, G, TUNED_1)
+    cache.put(16, N, K, G, TUNED_16)
+    cache.put(256, N, K, G, TUNED_256)
+    cache.save()
+
+
+def test_roundtrip_and_atomic_write() -> None:
+    cache = _fresh_cache()
+    assert len(cache) == 0
+    _populated(cache)
+    files = sorted(p.name for p in cache.path.parent.iterdir())
+    assert files == [cache.path.name], "temporary files must not survive a save"
+    doc = json.loads(cache.path.read_text())
+    assert doc["schema"] == autotune.SCHEMA_VERSION
+    assert doc["gpu"] == GPU
+    assert doc["hip"] == autotune.hip_abi()
+    reloaded = _fresh_cache()
+    assert reloaded.discarded_reason is None
+    assert reloaded.get(1, N, K, G) == TUNED_1
+    assert autotune.lookup(GPU, 16, N, K, G) == TUNED_16
+    assert autotune.lookup(GPU, 256, N, K, G) == TUNED_256
+    assert autotune.lookup(GPU, 32, N, K, G) == default_config(32, N, K, G)
+
+
+def test_cache_path_is_keyed_by_gpu_and_abi() -> None:
+    p = autotune.cache_path(GPU, "7")
+    assert p.name == f"{GPU}-hip7.json"
+    assert p.parent == autotune.cache_dir()
+
+
+def test_put_rejects_config_of_the_wrong_family() -> None:
+    cache = _fresh_cache()
+    with pytest.raises(ValueError, match="bucket"):
+        cache.put(256, N, K, G, TUNED_1)
+
+
+def _corruptions(path: Path) -> dict[str, str]:
+    good = json.loads(path.read_text())
+    entry_key = autotune.entry_key(1, N, K, G)
+
+    def with_entry(cfg: object, key: str = entry_key) -> str:
+        return json.dumps({**good, "entries": {key: cfg}})
+
+    text = path.read_text()
+    return {
+        "truncated": text[: len(text) // 2],
+        "garbled": "\x00\xff" + text[5:],
+        "empty": "",
+        "not_object": "[1, 2, 3]",
+        "wrong_schema": json.dumps({**good, "schema": 999}),
+        "wrong_gpu": json.dumps({**good, "gpu": "amd-instinct-mi300x-gfx942"}),
+        "wrong_abi": json.dumps({**good, "hip": "0"}),
+        "bad_key": json.dumps({**good, "entries": {"1:x:3:4": TUNED_1.to_dict()}}),
+        "bad_bucket": with_entry(TUNED_1.to_dict(), "3:64:256:128"),
+        "bad_block_k": with_entry({**TUNED_256.to_dict(), "block_k": 96}, "256:64:256:128"),
+        "unknown_field": with_entry({**TUNED_1.to_dict(), "evil": 1}),
+        "bool_value": with_entry({**TUNED_1.to_dict(), "split_k": True}),
+        "not_compiled": with_entry({**TUNED_1.to_dict(), "block_n": 48}),
+        "wrong_family": with_entry(TUNED_256.to_dict()),
+        "block_m_too_small": with_entry({**TUNED_1.to_dict(), "block_m": 1}, "2:64:256:128"),
+    }
+
+
+KINDS = [
+    "truncated", "garbled", "empty", "not_object", "wrong_schema", "wrong_gpu", "wrong_abi",
+    "bad_key", "bad_bucket", "bad_block_k", "unknown_field", "bool_value", "not_compiled",
+    "wrong_family", "block_m_too_small",
+]
+
+
+@pytest.mark.parametrize("kind", KINDS)
+def test_f4_corrupt_cache_is_discarded(kind: str, caplog: pytest.LogCaptureFixture) -> None:
+    cache = _fresh_cache()
+    _populated(cache)
+    cache.path.write_bytes(_corruptions(cache.path)[kind].encode("utf-8", "surrogatepass"))
+    with caplog.at_level(logging.WARNING, logger="tokenforge_amd.kernels.autotune"):
+        reloaded = _fresh_cache()
+    assert reloaded.discarded_reason is not None
+    assert len(reloaded) == 0, "a corrupt cache must be discarded whole"
+    assert any("discarded" in r.getMessage() for r in caplog.records)
+    assert autotune.lookup(GPU, 1, N, K, G) == default_config(1, N, K, G)
+
+
+def _fake_bench_prefers(winner: GemmConfig):  # type: ignore[no-untyped-def]
+    """Deterministic stand-in for event timing: ``winner`` is fastest."""
+    calls: list[object] = []
+
+    def bench(fn):  # type: ignore[no-untyped-def]
+        fn()
+        calls.append(fn)
+        return 1.0 if fn.args[-1] == winner else 2.0
+
+    return bench, calls
+
+
+def test_tune_skips_cached_buckets_and_needs_bench_off_gpu() -> None:
+    cache = _fresh_cache()
+    _populated(cache)
+    bench, calls = _fake_bench_prefers(TUNED_1)
+    winners = autotune.tune_layer(
+        N, K, G, device=torch.device("cpu"), gpu=GPU, buckets=(1, 16), bench_fn=bench,
+        candidates=lambda b, g: [TUNED_1],
+    )
+    assert winners == {1: TUNED_1, 16: TUNED_16}
+    assert calls == []
+    with pytest.raises(RuntimeError, match="CUDA"):
+        autotune.tune_layer(N, K, G, device=torch.device("cpu"), gpu=GPU, buckets=(2,))
+
+
+def test_save_failure_leaves_previous_file(monkeypatch: pytest.MonkeyPatch) -> None:
+    cache = _fresh_cache()
+    _populated(cache)
+    original = cache.path.read_text()
+
+    def boom(*_a, **_k):  # type: ignore[no-untyped-def]
+        raise OSError("disk full")
+
+    monkeypatch.setattr(autotune.os, "replace", boom)
+    cache.put(2, N, K, G, GemmConfig("gemv_dot", 2, 16, 128, 1, 1, 1))
+    with pytest.raises(OSError, match="disk full"):
+        cache.save()
+    assert cache.path.read_text() == original
+    assert sorted(p.name for p in cache.path.parent.iterdir()) == [cache.path.name]
+
+
+@pytest.mark.gpu
+def test_f4_retune_after_corruption_restores_outputs(caplog: pytest.LogCaptureFixture, device: torch.device) -> None:
+    """Corrupt -> discard + warn -> retune -> same winner -> bit-identical kernel output."""
+    from tokenforge_amd.kernels.hip.w4a16 import w4a16_gemm
+
+    candidates = [TUNED_1, GemmConfig("gemv_mfma", 16, 16, 128, 1, 2, 1)]
+    bench, _ = _fake_bench_prefers(TUNED_1)
+    cache = _fresh_cache()
+    winners = autotune.tune_layer(
+        N, K, G, device=device, gpu=GPU, buckets=(1,), bench_fn=bench, candidates=lambda b, g: candidates
+    )
+    assert winners == {1: TUNED_1}
+
+    qweight_t, scales, qzeros = autotune.synthetic_layer(N, K, G, device, seed=3)
+    x = torch.randn((1, K), device=device).to(torch.float16)
+    before = w4a16_gemm(x, qweight_t, scales, qzeros, G, autotune.lookup(GPU, 1, N, K, G))
+
+    cache.path.write_text(cache.path.read_text()[:17])  # truncate
+    with caplog.at_level(logging.WARNING):
+        corrupt = _fresh_cache()
+    assert corrupt.discarded_reason is not None
+    assert "discarded" in caplog.text
+
+    bench2, calls = _fake_bench_prefers(TUNED_1)
+    autotune.tune_layer(
+        N, K, G, device=device, gpu=GPU, buckets=(1,), bench_fn=bench2, candidates=lambda b, g: candidates
+    )
+    assert len(calls) == len(candidates), "every candidate is re-benchmarked after a discard"
+    assert _fresh_cache().get(1, N, K, G) == TUNED_1
+    after = w4a16_gemm(x, qweight_t, scales, qzeros, G, autotune.lookup(GPU, 1, N, K, G))
+    assert torch.equal(before, after)
+
+
+@pytest.mark.gpu
+def test_real_tuning_picks_a_correct_config(device: torch.device) -> None:
+    """tune_layer with the real event timer on a small layer: winners valid and cached."""
+    from tokenforge_amd.kernels.hip.w4a16 import w4a16_gemm
+
+    gpu = "tune-test-gfx950"
+    winners = autotune.tune_layer(
+        256, 512, G, device=device, gpu=gpu, buckets=(1, 4, 64),
+        candidates=lambda b, g: candidate_configs(b, g)[:6],
+    )
+    assert set(winners) == {1, 4, 64}
+    qweight_t, scales, qzeros = autotune.synthetic_layer(256, 512, G, device, seed=5)
+    for bucket, cfg in winners.items():
+        assert cfg.fits_bucket(bucket)
+        x = torch.randn((bucket, 512), device=device).to(torch.float16)
+        ref = w4a16_gemm(x, qweight_t, scales, qzeros, G, default_config(bucket, 256, 512, G)).float()
+        out = w4a16_gemm(x, qweight_t, scales, qzeros, G, cfg).float()
+        assert float((out - ref).abs().max()) <= 1e-2 * float(ref.abs().max()) + 1e-3

@@ -1,0 +1,186 @@
+"""T0: dispatcher decisions, counters and launch-config validity (test_dispatch.py in the
+reference, with the gfx950 buckets, arch key, kernel families and HIP-only policy)."""
+
+from __future__ import annotations
+
+import pytest
+from hypothesis import given
+from hypothesis import strategies as st
+
+from tokenforge_amd.kernels import dispatch
+from tokenforge_amd.kernels.config import (
+    GEMV_MAX_M,
+    M_BUCKETS,
+    VARIANTS,
+    GemmConfig,
+    candidate_configs,
+    default_config,
+    family_for_bucket,
+    m_bucket,
+)
+from tokenforge_amd.kernels.metrics import FALLBACKS, KERNEL_CALLS
+
+
+@pytest.fixture(autouse=True)
+def _reset_counters() -> None:
+    KERNEL_CALLS.reset()
+    FALLBACKS.reset()
+
+
+@given(st.integers(1, 4096))
+def test_m_bucket_is_tight(m: int) -> None:
+    b = m_bucket(m)
+    assert b in M_BUCKETS
+    assert b >= m
+    assert b == 1 or b // 2 < m
+
+
+def test_m_bucket_rejects_out_of_range() -> None:
+    with pytest.raises(ValueError, match=">= 1"):
+        m_bucket(0)
+    with pytest.raises(ValueError, match="exceeds"):
+        m_bucket(4097)
+
+
+@pytest.mark.parametrize(
+    ("n", "k", "group", "dtype", "arch", "backend", "expected"),
+    [
+        (1152, 896, 128, "float16", "gfx950", "hip", None),
+        (1152, 896, 128, "torch.float16", None, "triton", None),
+        (1152, 896, 128, "float16", "gfx950", "cuda", None),
+        (1152, 896 + 64, 128, "float16", "gfx950", "hip", "unsupported_shape"),  # F2
+        (1150, 896, 128, "float16", "gfx950", "hip", "unsupported_shape"),
+        (1152, 896, 256, "float16", "gfx950", "hip", "unsupported_group_size"),
+        (1152, 896, 128, "bfloat16", "gfx950", "hip", "unsupported_dtype"),
+        (1152, 896, 128, "float16", "gfx942", "hip", "unsupported_arch"),
+        (1152, 896, 128, "float16", "gfx950", "marlin", "kill_switch"),
+    ],
+)
+def test_layer_support(n, k, group, dtype, arch, backend, expected) -> None:  # type: ignore[no-untyped-def]
+    assert dispatch.layer_support(n, k, group, dtype, arch, backend) == expected
+
+
+@pytest.mark.parametrize(
+    ("m", "backend", "kernel", "bucket"),
+    [
+        (1, "hip", "hip_gemv", "1"),
+        (3, "triton", "hip_gemv", "4"),
+        (4, "cuda", "hip_gemv", "4"),
+        (5, "hip", "hip_gemv", "8"),
+        (32, "hip", "hip_gemv", "32"),
+        (33, "hip", "hip_gemm", "64"),
+        (128, "hip", "hip_gemm", "128"),
+        (129, "hip", "hip_gemm", "256"),
+        (4096, "cuda", "hip_gemm", "4096"),
+        (5000, "hip", "hip_gemm", ">4096"),
+    ],
+)
+def test_select(m, backend, kernel, bucket) -> None:  # type: ignore[no-untyped-def]
+    d = dispatch.select(m, backend=backend, on_gpu=True, hip_ok=True)
+    assert (d.kernel, d.bucket) == (kernel, bucket)
+
+
+def test_lookup_bucket_clamps_above_largest() -> None:
+    assert dispatch.lookup_bucket(5000) == 4096
+    assert dispatch.lookup_bucket(17) == 32
+
+
+def test_select_without_gpu_raises_instead_of_falling_back() -> None:
+    with pytest.raises(dispatch.HipUnavailableError, match="CPU"):
+        dispatch.select(8, backend="hip", on_gpu=False, hip_ok=False)
+    with pytest.raises(dispatch.HipUnavailableError, match="library"):
+        dispatch.select(8, backend="hip", on_gpu=True, hip_ok=False)
+
+
+def test_select_rejects_marlin_per_call() -> None:
+    with pytest.raises(ValueError, match="per layer"):
+        dispatch.select(1, backend="marlin", on_gpu=True, hip_ok=True)
+
+
+def test_record_counts_calls_and_layer_fallbacks() -> None:
+    d = dispatch.select(2, backend="hip", on_gpu=True, hip_ok=True)
+    dispatch.record(d)
+    dispatch.record(d)
+    assert KERNEL_CALLS.value(kernel="hip_gemv", bucket="2") == 2
+    dispatch.record_layer_fallback("unsupported_shape")
+    assert FALLBACKS.value(reason="unsupported_shape") == 1
+
+
+def test_backend_from_env(monkeypatch: pytest.MonkeyPatch) -> None:
+    monkeypatch.delenv(dispatch.BACKEND_ENV, raising=False)
+    assert dispatch.backend_from_env() == "hip"
+    monkeypatch.setenv(dispatch.BACKEND_ENV, " Marlin ")
+    assert dispatch.backend_from_env() == "marlin"
+    monkeypatch.setenv(dispatch.BACKEND_ENV, "Triton")
+    assert dispatch.backend_from_env() == "triton"
+    monkeypatch.setenv(dispatch.BACKEND_ENV, "cublas")
+    with pytest.raises(ValueError, match="TOKENFORGE_BACKEND"):
+        dispatch.backend_from_env()
+
+
+SHAPES = [(1152, 896), (896, 4864), (37888, 3584), (3584, 18944), (4608, 3584), (200, 256)]
+
+
+@pytest.mark.parametrize("group", [32, 64, 128])
+@pytest.mark.parametrize("bucket", M_BUCKETS)
+@pytest.mark.parametrize(("n", "k"), SHAPES)
+def test_default_config_is_valid(bucket: int, n: int, k: int, group: int) -> None:
+    cfg = default_config(bucket, n, k, group)
+    cfg.validate(group)
+    assert cfg.fits_bucket(bucket)
+    assert cfg.family == family_for_bucket(bucket)
+    if cfg.kernel == "gemm_mfma":
+        assert cfg.split_k <= k // cfg.block_k
+
+
+@pytest.mark.parametrize("group", [32, 64, 128])
+@pytest.mark.parametrize("bucket", M_BUCKETS)
+def test_candidates_are_valid(bucket: int, group: int) -> None:
+    cands = candidate_configs(bucket, group)
+    assert cands
+    for cfg in cands:
+        cfg.validate(group)
+        assert cfg.fits_bucket(bucket)
+    assert all(c.family == "gemv" for c in cands) == (bucket <= GEMV_MAX_M)
+
+
+def test_decode_buckets_offer_both_gemv_kernels() -> None:
+    kinds = {c.kernel for c in candidate_configs(1, 128)}
+    assert kinds == {"gemv_dot", "gemv_mfma"}
+    assert {c.kernel for c in candidate_configs(8, 128)} == {"gemv_mfma"}
+
+
+@pytest.mark.parametrize(
+    ("kwargs", "match"),
+    [
+        ({"kernel": "gemv_triton", "block_m": 1, "block_n": 16, "block_k": 128}, "kernel"),
+        ({"kernel": "gemv_dot", "block_m": 3, "block_n": 16, "block_k": 128, "num_warps": 1, "num_stages": 1}, "compiled variant"),
+        ({"kernel": "gemm_mfma", "block_m": 64, "block_n": 64, "block_k": 256}, "divide"),
+        ({"kernel": "gemm_mfma", "block_m": 64, "block_n": 64, "block_k": 64, "split_k": 0}, "split_k"),
+        ({"kernel": "gemv_mfma", "block_m": 16, "block_n": 16, "block_k": 128, "split_k": 2}, "split_k"),
+        ({"kernel": "gemm_mfma", "block_m": 64, "block_n": 64, "block_k": 64, "num_warps": 3}, "num_warps"),
+        ({"kernel": "gemm_mfma", "block_m": 64, "block_n": 64, "block_k": 64, "num_stages": 9}, "num_stages"),
+    ],
+)
+def test_config_validation(kwargs: dict, match: str) -> None:
+    with pytest.raises(ValueError, match=match):
+        GemmConfig(**kwargs).validate(128)
+
+
+def test_config_from_dict_strict() -> None:
+    good = GemmConfig("gemv_dot", 1, 16, 128, 1, 1, 1).to_dict()
+    assert GemmConfig.from_dict(good) == GemmConfig("gemv_dot", 1, 16, 128, 1, 1, 1)
+    with pytest.raises(ValueError, match="unknown"):
+        GemmConfig.from_dict({**good, "block_q": 1})
+    with pytest.raises(TypeError, match="integers"):
+        GemmConfig.from_dict({**good, "split_k": True})
+    with pytest.raises(TypeError, match="kernel"):
+        GemmConfig.from_dict({**good, "kernel": 2})
+    with pytest.raises(TypeError, match="object"):
+        GemmConfig.from_dict([1, 2])
+
+
+def test_variant_table_is_consistent() -> None:
+    assert len(set(VARIANTS)) == len(VARIANTS)
+    for kernel, bm, bn, bk, warps, stages in VARIANTS:
+        GemmConfig(kernel, bm, bn, bk, 1, warps, stages).validate(128)

@@ -1,0 +1,111 @@
+"""T0: op registration is torch.compile- and fake-tensor-safe (test_ops.py in the reference).
+
+Fake-tensor shape propagation runs on CPU; opcheck and torch.compile execute the real op,
+which needs the GPU (there is no CPU implementation behind the ops).
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+from torch.library import opcheck
+
+import tokenforge_amd.kernels.ops  # noqa: F401
+from tests.numerics import cases
+from tokenforge_amd.kernels.metrics import KERNEL_CALLS
+
+G = cases.GROUP_SIZE
+OPCHECK_TESTS = ("test_schema", "test_faketensor", "test_aot_dispatch_dynamic")
+
+
+def _layer(device: torch.device, n: int = 64, k: int = 256):  # type: ignore[no-untyped-def]
+    w = cases.on_device(cases.layer_weights(n, k, 0), device)
+    return w.qweight_t, w.scales, w.qzeros
+
+
+def test_fake_tensor_shapes() -> None:
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    qw, s, z = _layer(torch.device("cpu"))
+    with FakeTensorMode() as mode:
+        x = mode.from_tensor(cases.activations(2, 256, 0)).reshape(1, 2, 256)
+        out = torch.ops.tokenforge.w4a16_linear(
+            x, mode.from_tensor(qw), mode.from_tensor(s), mode.from_tensor(z), None, G, "hip"
+        )
+        assert out.shape == (1, 2, 64)
+        assert out.dtype == torch.float16
+        deq = torch.ops.tokenforge.w4a16_dequant(mode.from_tensor(qw), mode.from_tensor(s), mode.from_tensor(z), G)
+        assert deq.shape == (64, 256) and deq.dtype == torch.float16
+        xr = mode.from_tensor(cases.activations(6, 256, 1)).reshape(2, 3, 256)
+        q, sc = torch.ops.tokenforge.rmsnorm_fp8_quant(xr, mode.from_tensor(torch.ones(256, dtype=torch.float16)), 1e-6, None)
+        assert q.shape == (2, 3, 256) and q.dtype == torch.float8_e4m3fn
+        assert sc.shape == (2, 3, 1) and sc.dtype == torch.float32
+
+
+def test_rejects_marlin_at_op_level() -> None:
+    qw, s, z = _layer(torch.device("cpu"))
+    with pytest.raises(ValueError, match="op level"):
+        torch.ops.tokenforge.w4a16_linear(cases.activations(1, 256, 0), qw, s, z, None, G, "marlin")
+
+
+def test_schema_matches_reference() -> None:
+    schema = str(torch.ops.tokenforge.w4a16_linear.default._schema)
+    assert schema == (
+        "tokenforge::w4a16_linear(Tensor x, Tensor qweight_t, Tensor scales, Tensor qzeros, "
+        "Tensor? bias, SymInt group_size, str backend) -> Tensor"
+    )
+    assert str(torch.ops.tokenforge.w4a16_dequant.default._schema) == (
+        "tokenforge::w4a16_dequant(Tensor qweight_t, Tensor scales, Tensor qzeros, SymInt group_size) -> Tensor"
+    )
+    assert str(torch.ops.tokenforge.rmsnorm_fp8_quant.default._schema) == (
+        "tokenforge::rmsnorm_fp8_quant(Tensor x, Tensor weight, float eps, Tensor? scale) -> (Tensor, Tensor)"
+    )
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_opcheck_w4a16_linear(with_bias: bool, device: torch.device) -> None:
+    qw, s, z = _layer(device)
+    x = cases.activations(3, 256, 0).to(device)
+    b = cases.bias(64, 0).to(device) if with_bias else None
+    opcheck(torch.ops.tokenforge.w4a16_linear.default, (x, qw, s, z, b, G, "hip"), test_utils=OPCHECK_TESTS)
+
+
+@pytest.mark.gpu
+def test_opcheck_dequant_and_rmsnorm(device: torch.device) -> None:
+    qw, s, z = _layer(device)
+    opcheck(torch.ops.tokenforge.w4a16_dequant.default, (qw, s, z, G), test_utils=OPCHECK_TESTS)
+    x = cases.activations(4, 256, 1).to(device)
+    w = torch.ones(256, dtype=torch.float16, device=device)
+    opcheck(
+        torch.ops.tokenforge.rmsnorm_fp8_quant.default,
+        (x, w, 1e-6, None),
+        test_utils=("test_schema", "test_faketensor"),
+    )
+
+
+class _QLinear(torch.nn.Module):
+    def __init__(self, device: torch.device) -> None:
+        super().__init__()
+        qw, s, z = _layer(device)
+        self.register_buffer("qw", qw)
+        self.register_buffer("s", s)
+        self.register_buffer("z", z)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        h = torch.ops.tokenforge.w4a16_linear(x, self.qw, self.s, self.z, None, G, "hip")
+        return torch.relu(h) * 2
+
+
+@pytest.mark.gpu
+def test_torch_compile_fullgraph_no_graph_breaks(device: torch.device) -> None:
+    mod = _QLinear(device)
+    x = cases.activations(5, 256, 2).to(device)
+    eager = mod(x)
+    compiled = torch.compile(mod, backend="aot_eager", fullgraph=True, dynamic=True)
+    assert torch.equal(compiled(x), eager)
+    # A new M must reuse the dynamic graph and still dispatch by its own bucket.
+    KERNEL_CALLS.reset()
+    x2 = cases.activations(17, 256, 3).to(device)
+    assert torch.equal(compiled(x2), mod(x2))
+    assert KERNEL_CALLS.value(kernel="hip_gemv", bucket="32") == 2

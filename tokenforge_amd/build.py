@@ -1,0 +1,92 @@
+"""Build ``libtokenforge_hip.so`` (the C-ABI library of the gfx950 kernels) in-tree.
+
+    python -m tokenforge_amd.build [--jobs N] [--verbose]
+
+Every ``csrc/*.hip`` file is compiled separately with ``hipcc --offload-arch=gfx950`` (in
+parallel), then linked into ``tokenforge_amd/lib/libtokenforge_hip.so``. The library
+depends only on the HIP runtime; it has no PyTorch headers or symbols.
+"""
+
+from __future__ import annotations
+
+import argparse
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+CSRC = PKG / "csrc"
+BUILD_DIR = PKG.parent / "_build"
+LIB_DIR = PKG / "lib"
+LIB_NAME = "libtokenforge_hip.so"
+ARCH = "gfx950"
+
+# Packed-FP32 VALU forms are disabled: hipcc -O3 would otherwise emit v_pk_{add,mul,fma}_f32
+# from scalar float code.
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Wall",
+    "-Wno-unused-function",
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
+
+
+def _run(cmd: list[str], verbose: bool) -> None:
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    # hipcc's host pass warns that it does not know the packed-fp32 feature; that is benign.
+    noise = ("packed-fp32-ops", "not a recognized feature")
+    err = "\n".join(
+        line for line in proc.stderr.splitlines() if not any(n in line for n in noise)
+    ).strip()
+    if proc.returncode != 0:
+        raise RuntimeError(f"command failed ({proc.returncode}): {' '.join(cmd)}\n{err}")
+    if err and verbose:
+        print(err, file=sys.stderr)
+
+
+def build(jobs: int | None = None, verbose: bool = False) -> Path:
+    """Compile every kernel source and link the shared library. Returns its path."""
+    cc = hipcc()
+    BUILD_DIR.mkdir(parents=True, exist_ok=True)
+    LIB_DIR.mkdir(parents=True, exist_ok=True)
+    sources = sorted(CSRC.glob("*.hip"))
+    objects = [BUILD_DIR / (s.stem + ".o") for s in sources]
+    cmds = [[cc, *HIPCC_FLAGS, "-c", str(s), "-o", str(o)] for s, o in zip(sources, objects)]
+    with ThreadPoolExecutor(max_workers=jobs or min(8, os.cpu_count() or 1)) as pool:
+        list(pool.map(lambda c: _run(c, verbose), cmds))
+    out = LIB_DIR / LIB_NAME
+    tmp = out.with_suffix(".so.tmp")
+    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objects)], verbose)
+    os.replace(tmp, out)
+    return out
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--jobs", type=int, default=None)
+    ap.add_argument("--verbose", action="store_true")
+    args = ap.parse_args()
+    print(build(args.jobs, args.verbose))
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

@@ -1,0 +1,237 @@
+// Prefill-shaped W4A16 GEMM (M >= 16): LDS-staged tiles feeding v_mfma_f32_32x32x16_f16.
+//
+// Per K block (BK <= group size, so one scale and one zero per column per block):
+//   * x tile [BM][BK] fp16 is copied global -> registers -> LDS;
+//   * the packed qweight_t tile [BN][BK/8] is loaded with 128-bit loads, dequantized in
+//     registers (fp16(q - z) * s, one rounding) and stored to LDS as fp16 [BN][BK];
+//   * each wave reads its A/B fragments (8 consecutive K values per lane, the operand
+//     layout of the 32x32x16 MFMA) and accumulates fp32.
+// Two LDS buffers: the global loads of block i+1 are issued before the MFMAs of block i,
+// and their LDS stores after, so one barrier per K block suffices. LDS rows are padded by
+// 16 bytes so the 16-byte fragment reads of 16 consecutive rows hit distinct banks.
+//
+// Split-K (grid.z > 1) writes fp32 partials [split][M][N] to the caller's workspace; a
+// second kernel sums them in split order, adds the bias and rounds once (w4a16.py:227-232),
+// so the result does not depend on scheduling.
+#include "linear.h"
+
+namespace tf {
+namespace {
+
+template <int BM, int BN, int BK, int WM, int WN>
+__global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(LinearArgs a, float* __restrict__ ws,
+                                                            int split_k) {
+  constexpr int T = WM * WN * 64;
+  constexpr int LD = BK + 8;  // fp16 elements per LDS row
+  constexpr int TM = BM / WM / 32;
+  constexpr int TN = BN / WN / 32;
+  constexpr int A_CHUNKS = BM * BK / 8;     // 16-byte chunks of the x tile
+  constexpr int B_CHUNKS = BN * BK / 32;    // 16-byte chunks (4 words) of the weight tile
+  constexpr int A_PER = (A_CHUNKS + T - 1) / T;
+  constexpr int B_PER = (B_CHUNKS + T - 1) / T;
+  static_assert(TM >= 1 && TN >= 1, "wave tile must hold at least one 32x32 MFMA tile");
+  static_assert(BK % 32 == 0, "BK must be a multiple of 32");
+
+  __shared__ __attribute__((aligned(16))) _Float16 As[2][BM][LD];
+  __shared__ __attribute__((aligned(16))) _Float16 Bs[2][BN][LD];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave / WN;
+  const int wn = wave % WN;
+  const int m0 = blockIdx.y * BM;
+  const int n0 = blockIdx.x * BN;
+  const int z = blockIdx.z;
+  const int nkb = a.k / BK;
+  const int kb0 = (int)(((int64_t)z * nkb) / split_k);
+  const int kb1 = (int)(((int64_t)(z + 1) * nkb) / split_k);
+  const int64_t words_per_row = a.k >> 3;
+
+  u4 ra[A_PER];
+  u4 rb[B_PER];
+  uint32_t rs[B_PER];
+  uint32_t rz[B_PER];
+
+  auto load_global = [&](int kb) {
+    const int k0 = kb * BK;
+#pragma unroll
+    for (int i = 0; i < A_PER; ++i) {
+      const int id = tid + i * T;
+      const int row = id / (BK / 8);
+      const int c8 = id % (BK / 8);
+      const int m = m0 + row;
+      if (id < A_CHUNKS && m < a.m)
+        ra[i] = *reinterpret_cast<const u4*>(a.x + (int64_t)m * a.ldx + k0 + c8 * 8);
+      else
+        ra[i] = u4{0u, 0u, 0u, 0u};
+    }
+    const int grp = k0 >> a.log2g;
+#pragma unroll
+    for (int i = 0; i < B_PER; ++i) {
+      const int id = tid + i * T;
+      const int col = id / (BK / 32);
+      const int kc = id % (BK / 32);
+      const int n = n0 + col;
+      if (id < B_CHUNKS && n < a.n) {
+        rb[i] = *reinterpret_cast<const u4*>(a.qw + (int64_t)n * words_per_row + (k0 >> 3) + kc * 4);
+        rs[i] = a.scales[(int64_t)grp * a.n + n];
+        rz[i] = a.qz[(int64_t)grp * (a.n >> 3) + (n >> 3)];
+      } else {
+        rb[i] = u4{0u, 0u, 0u, 0u};
+        rs[i] = 0u;
+        rz[i] = 0u;
+      }
+    }
+  };
+
+  auto store_lds = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < A_PER; ++i) {
+      const int id = tid + i * T;
+      if (id < A_CHUNKS) {
+        const int row = id / (BK / 8);
+        const int c8 = id % (BK / 8);
+        *reinterpret_cast<u4*>(&As[buf][row][c8 * 8]) = ra[i];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < B_PER; ++i) {
+      const int id = tid + i * T;
+      if (id < B_CHUNKS) {
+        const int col = id / (BK / 32);
+        const int kc = id % (BK / 32);
+        const QuantParams p = make_params(zero_of(rz[i], (uint32_t)(n0 + col)), rs[i]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          h2 d[4];
+          dequant_word(rb[i][j], p, d);
+          u4 o;
+          o[0] = as_u32(d[0]);
+          o[1] = as_u32(d[1]);
+          o[2] = as_u32(d[2]);
+          o[3] = as_u32(d[3]);
+          *reinterpret_cast<u4*>(&Bs[buf][col][kc * 32 + j * 8]) = o;
+        }
+      }
+    }
+  };
+
+  f16v acc[TM][TN];
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[tm][tn][r] = 0.0f;
+
+  if (kb0 < kb1) {
+    load_global(kb0);
+    store_lds(0);
+  }
+  __syncthreads();
+
+  int buf = 0;
+  for (int kb = kb0; kb < kb1; ++kb) {
+    const bool more = kb + 1 < kb1;
+    if (more) load_global(kb + 1);
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      h8 af[TM];
+      h8 bf[TN];
+      const int kcol = kk * 16 + (lane >> 5) * 8;
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm)
+        af[tm] = *reinterpret_cast<const h8*>(&As[buf][(wm * TM + tm) * 32 + (lane & 31)][kcol]);
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn)
+        bf[tn] = *reinterpret_cast<const h8*>(&Bs[buf][(wn * TN + tn) * 32 + (lane & 31)][kcol]);
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn)
+          acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[tm], bf[tn], acc[tm][tn], 0, 0, 0);
+    }
+    if (more) store_lds(buf ^ 1);
+    __syncthreads();
+    buf ^= 1;
+  }
+
+  // D layout of the 32x32 MFMA: register r of lane l is row 8*(r/4) + 4*(l/32) + r%4,
+  // column l%32.
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) {
+      const int n = n0 + (wn * TN + tn) * 32 + (lane & 31);
+      if (n >= a.n) continue;
+      const float b = (split_k == 1 && a.bias) ? half_bits_to_float(a.bias[n]) : 0.0f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + (wm * TM + tm) * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
+        if (m >= a.m) continue;
+        if (split_k == 1)
+          a.out[(int64_t)m * a.ldo + n] = __builtin_bit_cast(uint16_t, (_Float16)(acc[tm][tn][r] + b));
+        else
+          ws[((int64_t)z * a.m + m) * a.n + n] = acc[tm][tn][r];
+      }
+    }
+}
+
+__global__ void splitk_reduce_kernel(const float* __restrict__ ws, const uint16_t* __restrict__ bias,
+                                     uint16_t* __restrict__ out, int64_t ldo, int m, int n, int split) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = (int64_t)m * n;
+  if (i >= total) return;
+  const int64_t row = i / n;
+  const int64_t col = i % n;
+  float v = ws[i];
+  for (int s = 1; s < split; ++s) v += ws[(int64_t)s * total + i];
+  if (bias) v += half_bits_to_float(bias[col]);
+  out[row * ldo + col] = __builtin_bit_cast(uint16_t, (_Float16)v);
+}
+
+int effective_split(const LinearArgs& a, const tf_gemm_config& cfg) {
+  const int nkb = a.k / cfg.block_k;
+  return cfg.split_k < nkb ? cfg.split_k : (nkb > 0 ? nkb : 1);
+}
+
+int64_t gemm_workspace(const LinearArgs& a, const tf_gemm_config& cfg) {
+  const int s = effective_split(a, cfg);
+  return s > 1 ? (int64_t)s * a.m * a.n * (int64_t)sizeof(float) : 0;
+}
+
+template <int BM, int BN, int BK, int WM, int WN>
+int launch_gemm(const LinearArgs& a, const tf_gemm_config& cfg, float* ws, hipStream_t stream) {
+  const int split = effective_split(a, cfg);
+  if (split > 1 && ws == nullptr) return fail(TF_EINVAL, "tf_w4a16_linear: split-K needs a workspace");
+  const dim3 grid((unsigned)cdiv(a.n, BN), (unsigned)cdiv(a.m, BM), (unsigned)split);
+  gemm_kernel<BM, BN, BK, WM, WN><<<grid, WM * WN * 64, 0, stream>>>(a, ws, split);
+  if (int rc = check_launch("tf_w4a16_linear(gemm_mfma)")) return rc;
+  if (split > 1) {
+    const int64_t total = (int64_t)a.m * a.n;
+    splitk_reduce_kernel<<<(unsigned)cdiv(total, 256), 256, 0, stream>>>(ws, a.bias, a.out, a.ldo, a.m,
+                                                                        a.n, split);
+    return check_launch("tf_w4a16_linear(splitk_reduce)");
+  }
+  return TF_OK;
+}
+
+#define TF_GEMM(BM, BN, BK, WM, WN) \
+  {{TF_KERNEL_GEMM_MFMA, BM, BN, BK, 1, WM * WN, 2}, (launch_gemm<BM, BN, BK, WM, WN>), gemm_workspace}
+
+const Variant kGemmVariants[] = {
+    TF_GEMM(64, 64, 64, 2, 2),   TF_GEMM(64, 128, 64, 2, 2),  TF_GEMM(128, 64, 64, 2, 2),
+    TF_GEMM(128, 128, 64, 2, 2), TF_GEMM(128, 256, 64, 2, 2), TF_GEMM(256, 128, 64, 2, 2),
+    TF_GEMM(256, 256, 64, 2, 2), TF_GEMM(64, 64, 32, 2, 2),   TF_GEMM(128, 128, 32, 2, 2),
+    TF_GEMM(256, 128, 32, 2, 2),
+};
+
+}  // namespace
+
+const Variant* gemm_variants(int* count) {
+  *count = (int)(sizeof(kGemmVariants) / sizeof(kGemmVariants[0]));
+  return kGemmVariants;
+}
+
+}  // namespace tf

@@ -1,0 +1,122 @@
+// tf_w4a16_linear: argument checks (w4a16.py:149-175 semantics) and variant dispatch.
+#include "linear.h"
+
+namespace tf {
+namespace {
+
+struct Table {
+  const Variant* gemv;
+  int n_gemv;
+  const Variant* gemm;
+  int n_gemm;
+  Table() {
+    gemv = gemv_variants(&n_gemv);
+    gemm = gemm_variants(&n_gemm);
+  }
+  int size() const { return n_gemv + n_gemm; }
+  const Variant& at(int i) const { return i < n_gemv ? gemv[i] : gemm[i - n_gemv]; }
+};
+
+const Table& table() {
+  static const Table t;
+  return t;
+}
+
+bool same_variant(const tf_gemm_config& a, const tf_gemm_config& b) {
+  return a.kernel == b.kernel && a.block_m == b.block_m && a.block_n == b.block_n &&
+         a.block_k == b.block_k && a.num_warps == b.num_warps && a.num_stages == b.num_stages;
+}
+
+const Variant* find_variant(const tf_gemm_config& cfg) {
+  const Table& t = table();
+  for (int i = 0; i < t.size(); ++i)
+    if (same_variant(t.at(i).cfg, cfg)) return &t.at(i);
+  return nullptr;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_config(const tf_gemm_config& cfg, int32_t group_size) {
+  if (cfg.split_k < 1 || cfg.split_k > kMaxSplitK)
+    return fail(TF_EINVAL, "tf_w4a16_linear: split_k must be in [1, 16]");
+  if (cfg.kernel != TF_KERNEL_GEMM_MFMA && cfg.split_k != 1)
+    return fail(TF_EINVAL, "tf_w4a16_linear: gemv kernels split K across waves (num_warps); split_k must be 1");
+  if (cfg.kernel == TF_KERNEL_GEMM_MFMA && (cfg.block_k > group_size || group_size % cfg.block_k))
+    return fail(TF_EINVAL, "tf_w4a16_linear: block_k must divide group_size");
+  return TF_OK;
+}
+
+}  // namespace
+}  // namespace tf
+
+using namespace tf;
+
+extern "C" int tf_num_variants(void) { return table().size(); }
+
+extern "C" int tf_get_variant(int index, tf_gemm_config* out) {
+  if (out == nullptr || index < 0 || index >= table().size())
+    return fail(TF_EINVAL, "tf_get_variant: index out of range");
+  *out = table().at(index).cfg;
+  return TF_OK;
+}
+
+static int make_args(const uint16_t* x, int64_t ldx, const int32_t* qweight_t, const uint16_t* scales,
+                     const int32_t* qzeros, const uint16_t* bias, uint16_t* out, int64_t ldo, int64_t m,
+                     int64_t n, int64_t k, int32_t group_size, LinearArgs* a) {
+  if (m < 0 || n < 0 || k < 0) return fail(TF_EINVAL, "tf_w4a16_linear: negative size");
+  if (m > 0x7FFFFFFF || n > 0x7FFFFFFF || k > 0x7FFFFFFF)
+    return fail(TF_EINVAL, "tf_w4a16_linear: size above 2^31");
+  if (n % 8) return fail(TF_EINVAL, "tf_w4a16_linear: N must be a multiple of 8");
+  if (int rc = check_group_size(group_size, k, "tf_w4a16_linear")) return rc;
+  if (ldx < k || ldo < n) return fail(TF_EINVAL, "tf_w4a16_linear: row stride smaller than the row");
+  if (ldx % 8) return fail(TF_EINVAL, "tf_w4a16_linear: x row stride must be a multiple of 8 elements");
+  a->x = x;
+  a->ldx = ldx;
+  a->qw = reinterpret_cast<const uint32_t*>(qweight_t);
+  a->scales = scales;
+  a->qz = reinterpret_cast<const uint32_t*>(qzeros);
+  a->bias = bias;
+  a->out = out;
+  a->ldo = ldo;
+  a->m = (int)m;
+  a->n = (int)n;
+  a->k = (int)k;
+  a->log2g = log2_group(group_size);
+  if (m == 0 || n == 0) return TF_OK;
+  if (!x || !qweight_t || !scales || !qzeros || !out) return fail(TF_EINVAL, "tf_w4a16_linear: null pointer");
+  if (!aligned16(x) || !aligned16(qweight_t))
+    return fail(TF_EINVAL, "tf_w4a16_linear: x and qweight_t must be 16-byte aligned");
+  return TF_OK;
+}
+
+extern "C" int64_t tf_w4a16_workspace_bytes(int64_t m, int64_t n, int64_t k, int32_t group_size,
+                                            const tf_gemm_config* cfg) {
+  if (cfg == nullptr) return 0;
+  const Variant* v = find_variant(*cfg);
+  if (v == nullptr || m <= 0 || n <= 0 || k <= 0 || cfg->block_k <= 0) return 0;
+  LinearArgs a{};
+  a.m = (int)m;
+  a.n = (int)n;
+  a.k = (int)k;
+  a.log2g = log2_group(group_size);
+  return v->workspace(a, *cfg);
+}
+
+extern "C" int tf_w4a16_linear(const uint16_t* x, int64_t ldx, const int32_t* qweight_t,
+                               const uint16_t* scales, const int32_t* qzeros, const uint16_t* bias,
+                               uint16_t* out, int64_t ldo, int64_t m, int64_t n, int64_t k,
+                               int32_t group_size, const tf_gemm_config* cfg, float* workspace,
+                               int64_t workspace_bytes, void* stream) {
+  if (cfg == nullptr) return fail(TF_EINVAL, "tf_w4a16_linear: null config");
+  LinearArgs a;
+  if (int rc = make_args(x, ldx, qweight_t, scales, qzeros, bias, out, ldo, m, n, k, group_size, &a))
+    return rc;
+  if (int rc = check_config(*cfg, group_size)) return rc;
+  const Variant* v = find_variant(*cfg);
+  if (v == nullptr) return fail(TF_EINVAL, "tf_w4a16_linear: config does not name a compiled variant");
+  if (m == 0 || n == 0) return TF_OK;
+  const int64_t need = v->workspace(a, *cfg);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+    return fail(TF_EINVAL, "tf_w4a16_linear: workspace too small for this split_k");
+  return v->launch(a, *cfg, workspace, (hipStream_t)stream);
+}

@@ -1,0 +1,116 @@
+// Shared device helpers for the gfx950 kernels of the quantized-linear path.
+//
+// Conventions:
+//  * fp16 values travel as raw 16-bit patterns (uint16_t) across the C ABI and as
+//    clang _Float16 vectors inside kernels, so every conversion is explicit.
+//  * Packed int4 words use the AWQ nibble order: nibble i (bits 4i..4i+3) holds offset
+//    AWQ_ORDER[i] = {0,2,4,6,1,3,5,7}[i]; offset j lives in nibble (j%2)*4 + j/2
+//    (pack.py:32-36 in the reference).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/tokenforge_hip.h"
+
+namespace tf {
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f16v __attribute__((ext_vector_type(16)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+
+// ------------------------------------------------------------------ host-side errors
+
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+int check_launch(const char* what);
+
+// ------------------------------------------------------------------ bit casts
+
+__device__ __forceinline__ h2 as_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
+__device__ __forceinline__ uint32_t as_u32(h2 v) { return __builtin_bit_cast(uint32_t, v); }
+__device__ __forceinline__ float as_f32(uint32_t v) { return __builtin_bit_cast(float, v); }
+__device__ __forceinline__ uint32_t as_u32(float v) { return __builtin_bit_cast(uint32_t, v); }
+__device__ __forceinline__ float half_bits_to_float(uint16_t b) {
+  return (float)__builtin_bit_cast(_Float16, b);
+}
+
+// Nibble position of offset j inside a packed word: AWQ_REVERSE_ORDER[j] = (j%2)*4 + j/2.
+__host__ __device__ __forceinline__ uint32_t awq_nibble_of(uint32_t j) {
+  return (j & 1u) * 4u + (j >> 1);
+}
+
+// ------------------------------------------------------------------ zero/scale operands
+
+// Per-(group, column) constants for the dequantization of one packed word.
+//   zlo = fp16x2(1024 + z): subtrahend for nibbles at bits 0-3 / 16-19 (0x6400 magic)
+//   zhi = fp16x2(64 + z):   subtrahend for nibbles at bits 4-7 / 20-23 (0x5400 magic)
+//   s   = fp16x2(scale)
+struct QuantParams {
+  h2 zlo;
+  h2 zhi;
+  h2 s;
+};
+
+__device__ __forceinline__ QuantParams make_params(uint32_t z, uint32_t scale_bits) {
+  QuantParams p;
+  const uint32_t lo = 0x6400u | z;          // 1024 + z  (ulp of 1024 is 1)
+  const uint32_t hi = 0x5400u | (z << 4);   // 64 + z    (ulp of 64 is 1/16)
+  p.zlo = as_h2(lo | (lo << 16));
+  p.zhi = as_h2(hi | (hi << 16));
+  p.s = as_h2(scale_bits | (scale_bits << 16));
+  return p;
+}
+
+// Zero-point nibble of column n from its qzeros word (pack.py:35; w4a16.py:38-40).
+__device__ __forceinline__ uint32_t zero_of(uint32_t zword, uint32_t n) {
+  return (zword >> (4u * awq_nibble_of(n & 7u))) & 0xFu;
+}
+
+// Dequantize the eight int4 values of one packed word into fp16, K order:
+// out[i] holds offsets (2i, 2i+1). (word & 0x000F000F) | 0x6400_6400 is the fp16x2
+// pair (1024 + q0, 1024 + q1) because nibble 0 holds offset 0 and nibble 4 offset 1;
+// the 0x00F0 nibbles become 64 + q with the 0x5400 magic. Subtracting (1024 + z) or
+// (64 + z) is exact in fp16, so fp16(q - z) * s rounds exactly once (v_pk_mul_f16),
+// matching pack.py:194 and w4a16.py:95 bit for bit.
+__device__ __forceinline__ void dequant_word(uint32_t w, const QuantParams& p, h2 out[4]) {
+  const uint32_t w8 = w >> 8;
+  const h2 a0 = as_h2((w & 0x000F000Fu) | 0x64006400u);
+  const h2 a1 = as_h2((w & 0x00F000F0u) | 0x54005400u);
+  const h2 a2 = as_h2((w8 & 0x000F000Fu) | 0x64006400u);
+  const h2 a3 = as_h2((w8 & 0x00F000F0u) | 0x54005400u);
+  out[0] = (a0 - p.zlo) * p.s;
+  out[1] = (a1 - p.zhi) * p.s;
+  out[2] = (a2 - p.zlo) * p.s;
+  out[3] = (a3 - p.zhi) * p.s;
+}
+
+__device__ __forceinline__ h8 pack_h8(const h2 v[4]) {
+  h8 r;
+  r[0] = v[0][0]; r[1] = v[0][1];
+  r[2] = v[1][0]; r[3] = v[1][1];
+  r[4] = v[2][0]; r[5] = v[2][1];
+  r[6] = v[3][0]; r[7] = v[3][1];
+  return r;
+}
+
+// ------------------------------------------------------------------ cross-lane (DPP)
+
+// Sum of v over the four lanes of each quad, fixed tree: (0+1)+(2+3) in every lane.
+__device__ __forceinline__ float quad_sum(float v) {
+  // quad_perm [1,0,3,2] = 0xB1, then [2,3,0,1] = 0x4E.
+  float t = as_f32(__builtin_amdgcn_update_dpp(0, (int)as_u32(v), 0xB1, 0xF, 0xF, false));
+  v = v + t;
+  t = as_f32(__builtin_amdgcn_update_dpp(0, (int)as_u32(v), 0x4E, 0xF, 0xF, false));
+  return v + t;
+}
+
+// ------------------------------------------------------------------ misc
+
+__host__ __device__ constexpr int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace tf

@@ -1,0 +1,306 @@
+"""Persistent autotune cache for the gfx950 W4A16 kernels (autotune.py:1-267 in the reference).
+
+Tuning runs eagerly at weight-load time (``process_weights_after_loading``), before HIP
+graphs are captured. The hot path only does a dict lookup and falls back to the heuristic
+:func:`config.default_config` on a miss, so a call never benchmarks, allocates for tuning, or
+synchronizes.
+
+The cache lives at ``$TOKENFORGE_CACHE_DIR`` (default ``~/.cache/tokenforge``) as
+``<gpu>-hip<abi>.json``: ``<gpu>`` is ``device.gpu_identity`` (e.g.
+``amd-instinct-mi355x-gfx950``) and ``<abi>`` the kernel library's ABI version, so a rebuilt
+library with different variants never reuses stale entries. Entries are keyed
+``"{bucket}:{n}:{k}:{group}"`` by M bucket. Writes are atomic (tmp -> fsync -> rename ->
+fsync dir). Anything unexpected on read (bad JSON, wrong schema, another GPU or ABI, an
+invalid config, a config of the wrong kernel family for its bucket) discards the whole file
+with a warning. A cache is never partially trusted.
+"""
+
+from __future__ import annotations
+
+import functools
+import json
+import logging
+import os
+import statistics
+import tempfile
+import threading
+from collections.abc import Callable, Iterable
+from pathlib import Path
+from typing import Any, Final
+
+import torch
+
+from tokenforge_amd.kernels import _lib
+from tokenforge_amd.kernels.config import M_BUCKETS, GemmConfig, candidate_configs, default_config
+
+log = logging.getLogger(__name__)
+
+SCHEMA_VERSION: Final = 1
+CACHE_DIR_ENV: Final = "TOKENFORGE_CACHE_DIR"
+
+
+def hip_abi() -> str:
+    return str(_lib.ABI_VERSION)
+
+
+def cache_dir() -> Path:
+    env = os.environ.get(CACHE_DIR_ENV)
+    return Path(env) if env else Path.home() / ".cache" / "tokenforge"
+
+
+def cache_path(gpu: str, abi: str) -> Path:
+    return cache_dir() / f"{gpu}-hip{abi}.json"
+
+
+def entry_key(bucket: int, n: int, k: int, group_size: int) -> str:
+    return f"{bucket}:{n}:{k}:{group_size}"
+
+
+class CacheRejectedError(ValueError):
+    """The on-disk cache failed validation."""
+
+
+def _parse_entries(raw: Any) -> dict[str, GemmConfig]:
+    if not isinstance(raw, dict):
+        raise CacheRejectedError("'entries' is not an object")
+    entries: dict[str, GemmConfig] = {}
+    for key, value in raw.items():
+        parts = key.split(":") if isinstance(key, str) else []
+        if len(parts) != 4 or not all(p.isdigit() for p in parts):
+            raise CacheRejectedError(f"malformed key {key!r}")
+        bucket, n, k, group = (int(p) for p in parts)
+        if bucket not in M_BUCKETS or n <= 0 or k <= 0 or group <= 0 or k % group:
+            raise CacheRejectedError(f"impossible key {key!r}")
+        try:
+            cfg = GemmConfig.from_dict(value)
+            cfg.validate(group)
+        except (TypeError, ValueError) as exc:
+            raise CacheRejectedError(f"invalid config for {key!r}: {exc}") from exc
+        if not cfg.fits_bucket(bucket):
+            raise CacheRejectedError(f"{cfg.kernel} block_m={cfg.block_m} does not fit bucket {bucket}")
+        entries[key] = cfg
+    return entries
+
+
+def atomic_write_json(path: Path, payload: Any) -> None:
+    path.parent.mkdir(parents=True, exist_ok=True)
+    fd, tmp = tempfile.mkstemp(prefix=f".{path.name}.", suffix=".tmp", dir=path.parent)
+    try:
+        with os.fdopen(fd, "w", encoding="utf-8") as f:
+            json.dump(payload, f, indent=1, sort_keys=True)
+            f.write("\n")
+            f.flush()
+            os.fsync(f.fileno())
+        os.replace(tmp, path)
+    except BaseException:
+        Path(tmp).unlink(missing_ok=True)
+        raise
+    dir_fd = os.open(path.parent, os.O_RDONLY)
+    try:
+        os.fsync(dir_fd)
+    finally:
+        os.close(dir_fd)
+
+
+class AutotuneCache:
+    def __init__(self, path: Path, gpu: str, abi: str) -> None:
+        self.path = path
+        self.gpu = gpu
+        self.abi = abi
+        self._entries: dict[str, GemmConfig] = {}
+        self._lock = threading.Lock()
+        self.discarded_reason: str | None = None
+
+    def load(self) -> None:
+        """Populate from disk. Missing file: empty cache. Invalid file: discard and warn."""
+        self.discarded_reason = None
+        try:
+            text = self.path.read_text(encoding="utf-8")
+        except FileNotFoundError:
+            self._entries = {}
+            return
+        except (OSError, UnicodeDecodeError) as exc:
+            self._discard(f"unreadable: {exc}")
+            return
+        try:
+            doc = json.loads(text)
+            if not isinstance(doc, dict):
+                raise CacheRejectedError("top level is not an object")
+            if doc.get("schema") != SCHEMA_VERSION:
+                raise CacheRejectedError(f"schema {doc.get('schema')!r} != {SCHEMA_VERSION}")
+            if doc.get("gpu") != self.gpu:
+                raise CacheRejectedError(f"built for gpu {doc.get('gpu')!r}, running on {self.gpu!r}")
+            if doc.get("hip") != self.abi:
+                raise CacheRejectedError(
+                    f"built for kernel ABI {doc.get('hip')!r}, running {self.abi!r}"
+                )
+            entries = _parse_entries(doc.get("entries"))
+        except (json.JSONDecodeError, CacheRejectedError) as exc:
+            self._discard(str(exc))
+            return
+        with self._lock:
+            self._entries = entries
+
+    def _discard(self, reason: str) -> None:
+        log.warning("autotune cache %s discarded (%s); configs will be retuned", self.path, reason)
+        self.discarded_reason = reason
+        with self._lock:
+            self._entries = {}
+
+    def get(self, bucket: int, n: int, k: int, group_size: int) -> GemmConfig | None:
+        return self._entries.get(entry_key(bucket, n, k, group_size))
+
+    def put(self, bucket: int, n: int, k: int, group_size: int, cfg: GemmConfig) -> None:
+        cfg.validate(group_size)
+        if not cfg.fits_bucket(bucket):
+            raise ValueError(f"{cfg} does not fit bucket {bucket}")
+        with self._lock:
+            self._entries[entry_key(bucket, n, k, group_size)] = cfg
+
+    def __len__(self) -> int:
+        return len(self._entries)
+
+    def save(self) -> None:
+        with self._lock:
+            payload = {
+                "schema": SCHEMA_VERSION,
+                "gpu": self.gpu,
+                "hip": self.abi,
+                "torch": torch.__version__,
+                "entries": {k: v.to_dict() for k, v in sorted(self._entries.items())},
+            }
+        atomic_write_json(self.path, payload)
+
+
+_CACHES: dict[tuple[str, str], AutotuneCache] = {}
+_CACHES_LOCK = threading.Lock()
+
+
+def get_cache(gpu: str) -> AutotuneCache:
+    abi = hip_abi()
+    with _CACHES_LOCK:
+        cache = _CACHES.get((gpu, abi))
+        if cache is None:
+            cache = AutotuneCache(cache_path(gpu, abi), gpu, abi)
+            cache.load()
+            _CACHES[(gpu, abi)] = cache
+        return cache
+
+
+def reset_caches() -> None:
+    with _CACHES_LOCK:
+        _CACHES.clear()
+
+
+def lookup(gpu: str, bucket: int, n: int, k: int, group_size: int) -> GemmConfig:
+    """Hot-path lookup: tuned config if cached, otherwise the heuristic default."""
+    cfg = get_cache(gpu).get(bucket, n, k, group_size)
+    return cfg if cfg is not None else default_config(bucket, n, k, group_size)
+
+
+BenchFn = Callable[[Callable[[], object]], float]
+
+_FLUSH_BYTES = 512 * 1024 * 1024
+"""Larger than MI355X's 256 MB Infinity Cache, so each timed call reads weights from HBM."""
+
+
+@functools.cache
+def _flush_buffer(index: int) -> torch.Tensor:
+    return torch.empty(_FLUSH_BYTES // 4, dtype=torch.int32, device=torch.device("cuda", index))
+
+
+def hip_bench(fn: Callable[[], object], warmup: int = 5, rep: int = 25) -> float:
+    """Median runtime of ``fn`` in ms, device caches flushed before every timed call."""
+    flush = _flush_buffer(torch.cuda.current_device())
+    for _ in range(warmup):
+        fn()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(rep)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(rep)]
+    for s, e in zip(starts, ends):
+        flush.zero_()
+        s.record()
+        fn()
+        e.record()
+    torch.cuda.synchronize()
+    return float(statistics.median(s.elapsed_time(e) for s, e in zip(starts, ends)))
+
+
+def synthetic_layer(
+    n: int, k: int, group_size: int, device: torch.device, seed: int = 0
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Random AWQ-distributed layer in TokenForge layout: nibbles and zero-points uniform in
+    [0, 15], fp16 scales uniform in [1e-3, 1e-2]. Returns ``(qweight_t, scales, qzeros)``."""
+    from tokenforge_amd.kernels.pack import pack_int4
+
+    gen = torch.Generator(device=device).manual_seed(seed)
+    q = torch.randint(0, 16, (n, k), generator=gen, device=device, dtype=torch.int32)
+    z = torch.randint(0, 16, (k // group_size, n), generator=gen, device=device, dtype=torch.int32)
+    s = (torch.rand((k // group_size, n), generator=gen, device=device) * 9e-3 + 1e-3).to(torch.float16)
+    return pack_int4(q), s, pack_int4(z)
+
+
+def tune_layer(
+    n: int,
+    k: int,
+    group_size: int,
+    *,
+    device: torch.device,
+    gpu: str,
+    buckets: Iterable[int] = M_BUCKETS,
+    bench_fn: BenchFn | None = None,
+    candidates: Callable[[int, int], list[GemmConfig]] = candidate_configs,
+    save: bool = True,
+) -> dict[int, GemmConfig]:
+    """Tune every M bucket for one (N, K) layer shape and persist the winners.
+
+    Each candidate is checked against the default config's output before it can win, so a
+    config that miscomputes is never cached. Buckets already in the cache are skipped, and
+    nothing touches the device when every bucket is cached.
+    """
+    from tokenforge_amd.kernels.hip.w4a16 import w4a16_gemm
+
+    cache = get_cache(gpu)
+    buckets = list(buckets)
+    winners: dict[int, GemmConfig] = {}
+    todo = []
+    for bucket in buckets:
+        cached = cache.get(bucket, n, k, group_size)
+        if cached is not None:
+            winners[bucket] = cached
+        else:
+            todo.append(bucket)
+    if not todo:
+        return winners
+    if bench_fn is None:
+        if device.type != "cuda":
+            raise RuntimeError("tuning needs a CUDA (HIP) device or an explicit bench_fn")
+        bench_fn = hip_bench
+
+    qweight_t, scales, qzeros = synthetic_layer(n, k, group_size, device)
+    gen = torch.Generator(device=device).manual_seed(1)
+    for bucket in todo:
+        x = (torch.randn((bucket, k), generator=gen, device=device) * 0.5).to(torch.float16)
+        base_cfg = default_config(bucket, n, k, group_size)
+        ref = w4a16_gemm(x, qweight_t, scales, qzeros, group_size, base_cfg).float()
+        tol = 1e-2 * float(ref.abs().max()) + 1e-3
+        best: tuple[float, GemmConfig] | None = None
+        for cfg in candidates(bucket, group_size):
+            try:
+                out = w4a16_gemm(x, qweight_t, scales, qzeros, group_size, cfg)
+                if float((out.float() - ref).abs().max()) > tol:
+                    log.warning("config %s miscomputes for %s; skipped", cfg, (bucket, n, k))
+                    continue
+                t = bench_fn(
+                    functools.partial(w4a16_gemm, x, qweight_t, scales, qzeros, group_size, cfg)
+                )
+            except (ValueError, RuntimeError) as exc:  # variant cannot run this shape
+                log.debug("config %s failed to run: %s", cfg, exc)
+                continue
+            if best is None or t < best[0]:
+                best = (t, cfg)
+        chosen = best[1] if best is not None else base_cfg
+        cache.put(bucket, n, k, group_size, chosen)
+        winners[bucket] = chosen
+    if save:
+        cache.save()
+    return winners

@@ -1,0 +1,208 @@
+"""M buckets and launch configurations of the gfx950 W4A16 kernels.
+
+Counterpart of the reference's ``config.py`` (config.py:8-117). Differences, each forced by
+the hardware or by the single HIP path:
+
+* ``M_BUCKETS`` runs up to 4096: every M, prefill included, is served by a HIP kernel chosen
+  through the bucket's autotune entry (the reference sends M > 128 to dequant + cuBLAS).
+* ``GemmConfig`` names a compiled kernel variant: ``kernel`` is one of ``KERNELS`` and the
+  tuple ``(kernel, block_m, block_n, block_k, num_warps, num_stages)`` must be in
+  ``VARIANTS`` (the table ``libtokenforge_hip.so`` exports; a CPU test keeps the two equal).
+  ``split_k`` is a runtime value.
+
+Field meaning per kernel family:
+
+========== =========================== ================================================
+kernel     block_m / block_n / block_k  split_k / num_warps / num_stages
+========== =========================== ================================================
+gemv_dot   max M (1,2,4) / rows per     1 / waves per workgroup, each a K slice reduced
+           workgroup (16*RT) / 128      on chip / K steps in flight per wave
+gemv_mfma  M per tile (16,32) / rows    same as gemv_dot
+           per workgroup / 128
+gemm_mfma  LDS tile M / tile N / tile K K slices across workgroups (fp32 workspace,
+                                        fixed-order reduce) / 4 waves / 2 LDS buffers
+========== =========================== ================================================
+"""
+
+from __future__ import annotations
+
+from dataclasses import asdict, dataclass
+from typing import Any
+
+M_BUCKETS: tuple[int, ...] = (1, 2, 4, 8, 16, 32, 64, 128, 256, 512, 1024, 2048, 4096)
+MAX_BUCKET_M = M_BUCKETS[-1]
+GEMV_MAX_M = 32
+"""Buckets up to this M use the streaming (gemv) kernels; larger ones the LDS GEMM."""
+
+KERNELS: tuple[str, ...] = ("gemv_dot", "gemv_mfma", "gemm_mfma")
+NUM_CUS = 256
+"""MI355X compute units; the split heuristics aim to put several waves on each."""
+
+_WAVES = (1, 2, 4, 8, 16)
+
+
+def _gemv_variants() -> list[tuple[str, int, int, int, int, int]]:
+    out = []
+    dot = [(1, 1, 1), (1, 1, 2), (1, 1, 4), (1, 2, 1), (1, 2, 2), (1, 2, 4), (1, 4, 1), (1, 4, 2),
+           (2, 1, 1), (2, 1, 2), (2, 2, 1), (2, 2, 2), (4, 1, 1), (4, 1, 2), (4, 2, 1)]
+    for bm, rt, st in dot:
+        out += [("gemv_dot", bm, 16 * rt, 128, w, st) for w in _WAVES]
+    mfma = [(1, 1, 1), (1, 1, 2), (1, 1, 4), (1, 2, 1), (1, 2, 2), (1, 2, 4), (1, 4, 1), (1, 4, 2),
+            (2, 1, 1), (2, 1, 2), (2, 2, 1), (2, 2, 2)]
+    for mt, rt, st in mfma:
+        out += [("gemv_mfma", 16 * mt, 16 * rt, 128, w, st) for w in _WAVES]
+    return out
+
+
+def _gemm_variants() -> list[tuple[str, int, int, int, int, int]]:
+    tiles = [(64, 64, 64), (64, 128, 64), (128, 64, 64), (128, 128, 64), (128, 256, 64),
+             (256, 128, 64), (256, 256, 64), (64, 64, 32), (128, 128, 32), (256, 128, 32)]
+    return [("gemm_mfma", bm, bn, bk, 4, 2) for bm, bn, bk in tiles]
+
+
+VARIANTS: tuple[tuple[str, int, int, int, int, int], ...] = tuple(_gemv_variants() + _gemm_variants())
+"""(kernel, block_m, block_n, block_k, num_warps, num_stages), in the library's order."""
+_VARIANT_SET = frozenset(VARIANTS)
+
+
+def m_bucket(m: int) -> int:
+    """Smallest bucket >= m (config.py:13-20). M above the largest bucket uses the largest."""
+    if m < 1:
+        raise ValueError(f"M must be >= 1, got {m}")
+    for b in M_BUCKETS:
+        if m <= b:
+            return b
+    raise ValueError(f"M={m} exceeds the largest bucket ({MAX_BUCKET_M})")
+
+
+def family_for_bucket(bucket: int) -> str:
+    """``gemv`` for decode-shaped buckets, ``gemm`` for prefill-shaped ones."""
+    return "gemv" if bucket <= GEMV_MAX_M else "gemm"
+
+
+@dataclass(frozen=True)
+class GemmConfig:
+    kernel: str
+    block_m: int
+    block_n: int
+    block_k: int
+    split_k: int = 1
+    num_warps: int = 4
+    num_stages: int = 2
+
+    @property
+    def path(self) -> str:
+        return self.kernel
+
+    @property
+    def family(self) -> str:
+        return "gemm" if self.kernel == "gemm_mfma" else "gemv"
+
+    def variant(self) -> tuple[str, int, int, int, int, int]:
+        return (self.kernel, self.block_m, self.block_n, self.block_k, self.num_warps, self.num_stages)
+
+    def validate(self, group_size: int) -> None:
+        """Raise ``ValueError`` if this config cannot run for ``group_size``."""
+        if self.kernel not in KERNELS:
+            raise ValueError(f"kernel={self.kernel!r} not in {KERNELS}")
+        if self.kernel == "gemm_mfma" and (
+            self.block_k <= 0 or self.block_k > group_size or group_size % self.block_k
+        ):
+            raise ValueError(f"block_k={self.block_k} must divide group_size={group_size}")
+        if not 1 <= self.split_k <= 16:
+            raise ValueError(f"split_k={self.split_k} must be in [1, 16]")
+        if self.kernel != "gemm_mfma" and self.split_k != 1:
+            raise ValueError(
+                f"split_k={self.split_k}: {self.kernel} splits K across its num_warps waves; "
+                "split_k must be 1"
+            )
+        if self.num_warps not in _WAVES:
+            raise ValueError(f"num_warps={self.num_warps} must be a power of two <= 16")
+        if not 1 <= self.num_stages <= 4:
+            raise ValueError(f"num_stages={self.num_stages} must be in [1, 4]")
+        if self.variant() not in _VARIANT_SET:
+            raise ValueError(f"{self.variant()} is not a compiled variant (block_m/block_n/block_k)")
+
+    def fits_bucket(self, bucket: int) -> bool:
+        """Whether this config may serve M values of ``bucket`` (cache validation)."""
+        if family_for_bucket(bucket) != self.family:
+            return False
+        if self.kernel == "gemv_dot":
+            return self.block_m >= bucket
+        return True
+
+    def to_dict(self) -> dict[str, Any]:
+        return asdict(self)
+
+    @classmethod
+    def from_dict(cls, d: Any) -> GemmConfig:
+        if not isinstance(d, dict):
+            raise TypeError(f"config must be an object, got {type(d).__name__}")
+        fields = set(cls.__dataclass_fields__)
+        unknown = set(d) - fields
+        if unknown:
+            raise ValueError(f"unknown config keys {sorted(unknown)}")
+        if not isinstance(d.get("kernel"), str):
+            raise TypeError("config 'kernel' must be a string")
+        ints = {k: v for k, v in d.items() if k != "kernel"}
+        if not all(isinstance(v, int) and not isinstance(v, bool) for v in ints.values()):
+            raise TypeError("config values must be integers")
+        return cls(**d)
+
+
+def _pow2_at_most(v: int, cap: int) -> int:
+    p = 1
+    while p * 2 <= min(v, cap):
+        p *= 2
+    return p
+
+
+def default_config(bucket: int, n: int, k: int, group_size: int) -> GemmConfig:
+    """Heuristic config used before tuning (config.py:71-92, re-derived for 256 CUs).
+
+    Streaming kernels: one workgroup per 16 output columns; add waves (on-chip K slices)
+    until the grid holds about 8 waves per CU, never more waves than 128-wide K steps.
+    LDS GEMM: tile by M, then split K across workgroups until the grid covers the CUs.
+    """
+    if family_for_bucket(bucket) == "gemv":
+        mt = 1 if bucket <= 16 else 2
+        tiles = -(-n // 16)
+        k_steps = max(1, -(-k // 128))
+        waves = _pow2_at_most(max(1, (8 * NUM_CUS) // tiles), min(16, k_steps))
+        if mt == 2:
+            waves = min(waves, 8)
+        return GemmConfig("gemv_mfma", 16 * mt, 16, 128, 1, waves, 2)
+    block_k = 64 if group_size >= 64 else 32
+    if bucket <= 64:
+        bm, bn = 64, 64
+    elif bucket <= 128:
+        bm, bn = 128, 128
+    else:
+        bm, bn = (256, 128) if block_k == 64 else (256, 128)
+    tiles = -(-n // bn) * -(-bucket // bm)
+    k_blocks = k // block_k
+    split = 1
+    while tiles * split < NUM_CUS and split * 2 <= min(16, k_blocks):
+        split *= 2
+    return GemmConfig("gemm_mfma", bm, bn, block_k, split, 4, 2)
+
+
+def candidate_configs(bucket: int, group_size: int) -> list[GemmConfig]:
+    """Autotune search space for one bucket: every compiled variant of the bucket's family."""
+    out: list[GemmConfig] = []
+    family = family_for_bucket(bucket)
+    for kernel, bm, bn, bk, warps, stages in VARIANTS:
+        cfg = GemmConfig(kernel, bm, bn, bk, 1, warps, stages)
+        if not cfg.fits_bucket(bucket):
+            continue
+        if family == "gemv":
+            if kernel == "gemv_mfma" and bm > 16 and bucket <= 16:
+                continue
+            out.append(cfg)
+            continue
+        if bk > group_size or group_size % bk:
+            continue
+        if bm > 2 * bucket:
+            continue
+        out.extend(GemmConfig(kernel, bm, bn, bk, s, warps, stages) for s in (1, 2, 4, 8))
+    return out

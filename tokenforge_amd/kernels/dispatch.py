@@ -1,0 +1,114 @@
+"""Pure-Python kernel dispatch (dispatch.py:1-104 in the reference).
+
+Two decisions, made at different times:
+
+* :func:`layer_support` runs once per layer at weight-load time. An unsupported layer is
+  left to the caller's own method and increments ``tokenforge_fallback_total{reason}``.
+* :func:`select` runs per call on (M, backend) only. It reads shapes, never tensor values,
+  so it is safe inside HIP-graph capture and opaque to torch.compile.
+
+There is one device path: hand-written HIP kernels for gfx950. ``backend`` keeps the
+reference's string argument; ``"hip"`` is canonical and the reference's ``"triton"`` and
+``"cuda"`` are accepted as aliases of the same path, so reference-shaped callers work
+unchanged. ``"marlin"`` remains the per-layer kill switch. A call that cannot run on the
+GPU (CPU tensor, library not built, another architecture) raises: there is no CPU
+fallback behind these ops.
+"""
+
+from __future__ import annotations
+
+import os
+from dataclasses import dataclass
+from typing import Final, Literal, get_args
+
+from tokenforge_amd.kernels.config import GEMV_MAX_M, MAX_BUCKET_M, m_bucket
+from tokenforge_amd.kernels.device import SUPPORTED_ARCHS
+from tokenforge_amd.kernels.metrics import FALLBACKS, KERNEL_CALLS
+from tokenforge_amd.kernels.pack import PACK_FACTOR, SUPPORTED_GROUP_SIZES
+
+Backend = Literal["hip", "triton", "cuda", "marlin"]
+Kernel = Literal["hip_gemv", "hip_gemm"]
+FallbackReason = Literal[
+    "kill_switch",
+    "unsupported_dtype",
+    "unsupported_group_size",
+    "unsupported_shape",
+    "unsupported_arch",
+]
+
+BACKENDS: Final[tuple[str, ...]] = get_args(Backend)
+HIP_BACKENDS: Final[tuple[str, ...]] = ("hip", "triton", "cuda")
+BACKEND_ENV: Final = "TOKENFORGE_BACKEND"
+
+
+class HipUnavailableError(RuntimeError):
+    """The call cannot run on the HIP kernels and this build has no other path."""
+
+
+def backend_from_env() -> Backend:
+    value = os.environ.get(BACKEND_ENV, "hip").strip().lower()
+    if value not in BACKENDS:
+        raise ValueError(f"{BACKEND_ENV}={value!r} is not one of {BACKENDS}")
+    return value  # type: ignore[return-value]
+
+
+def layer_support(
+    n: int, k: int, group_size: int, dtype: str, arch: str | None, backend: Backend
+) -> FallbackReason | None:
+    """``None`` if the HIP kernels can serve this layer, else the fallback reason.
+
+    ``arch`` is the device's gfx architecture (``device.device_arch``), None when unknown.
+    """
+    if backend == "marlin":
+        return "kill_switch"
+    if dtype not in ("float16", "torch.float16"):
+        return "unsupported_dtype"
+    if group_size not in SUPPORTED_GROUP_SIZES:
+        return "unsupported_group_size"
+    if k % group_size != 0 or k % PACK_FACTOR != 0 or n % PACK_FACTOR != 0 or n <= 0:
+        return "unsupported_shape"
+    if arch is not None and arch not in SUPPORTED_ARCHS:
+        return "unsupported_arch"
+    return None
+
+
+def record_layer_fallback(reason: FallbackReason) -> None:
+    FALLBACKS.inc(reason=reason)
+
+
+@dataclass(frozen=True)
+class Decision:
+    kernel: Kernel
+    bucket: str
+
+
+def bucket_label(m: int) -> str:
+    return f">{MAX_BUCKET_M}" if m > MAX_BUCKET_M else str(m_bucket(m))
+
+
+def lookup_bucket(m: int) -> int:
+    """Autotune bucket of a call with ``m`` rows (M above the largest bucket uses it)."""
+    return MAX_BUCKET_M if m > MAX_BUCKET_M else m_bucket(m)
+
+
+def select(m: int, *, backend: Backend, on_gpu: bool, hip_ok: bool) -> Decision:
+    """Kernel family for one call with ``m`` rows. The layer has passed :func:`layer_support`."""
+    if backend == "marlin":
+        raise ValueError("backend 'marlin' is resolved per layer, not per call")
+    if not on_gpu:
+        raise HipUnavailableError(
+            "tokenforge_amd kernels run on gfx950 GPU tensors only; got a CPU tensor "
+            "(this build has no CPU path)"
+        )
+    if not hip_ok:
+        raise HipUnavailableError(
+            "the HIP kernel library is not loaded or the GPU is not gfx950 "
+            "(build it with `python -m tokenforge_amd.build`)"
+        )
+    bucket = bucket_label(m)
+    kernel: Kernel = "hip_gemv" if m <= GEMV_MAX_M else "hip_gemm"
+    return Decision(kernel, bucket)
+
+
+def record(decision: Decision) -> None:
+    KERNEL_CALLS.inc(kernel=decision.kernel, bucket=decision.bucket)

@@ -1,0 +1,146 @@
+"""W4A16 linear and full-weight dequantization on gfx950 (counterpart of triton/w4a16.py).
+
+``w4a16_gemm`` keeps the reference's signature, checks and messages (w4a16.py:149-232); the
+config selects one of the compiled HIP kernels (``config.GemmConfig``). Split-K partials are
+reduced on chip (gemv kernels) or by a fixed-order reduction kernel (LDS GEMM), so eager and
+HIP-graph results are bit-identical.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from tokenforge_amd.kernels import _lib
+from tokenforge_amd.kernels.config import GemmConfig
+from tokenforge_amd.kernels.hip._common import on_device, ptr, require_gpu, stream_of
+
+
+def _check_inputs(
+    x: torch.Tensor,
+    qweight_t: torch.Tensor,
+    scales: torch.Tensor,
+    qzeros: torch.Tensor,
+    group_size: int,
+) -> tuple[int, int, int]:
+    """Shape, dtype and layout checks of w4a16.py:149-175 (same types and messages)."""
+    if x.dim() != 2:
+        raise ValueError(f"x must be 2-D [M, K], got shape {tuple(x.shape)}")
+    if x.dtype != torch.float16:
+        raise TypeError(f"x must be fp16, got {x.dtype}")
+    m, k = x.shape
+    n = qweight_t.shape[0]
+    if qweight_t.shape[1] * 8 != k:
+        raise ValueError(f"x has K={k} but qweight_t encodes K={qweight_t.shape[1] * 8}")
+    if k % group_size != 0:
+        raise ValueError(f"K={k} is not a multiple of group_size={group_size}")
+    if tuple(scales.shape) != (k // group_size, n):
+        raise ValueError(f"scales shape {tuple(scales.shape)} != {(k // group_size, n)}")
+    if tuple(qzeros.shape) != (k // group_size, n // 8):
+        raise ValueError(f"qzeros shape {tuple(qzeros.shape)} != {(k // group_size, n // 8)}")
+    if qweight_t.dtype != torch.int32 or qzeros.dtype != torch.int32:
+        raise TypeError("qweight_t and qzeros must be int32")
+    if scales.dtype != torch.float16:
+        raise TypeError(f"scales must be fp16, got {scales.dtype}")
+    for name, t in (("qweight_t", qweight_t), ("scales", scales), ("qzeros", qzeros)):
+        if not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous")
+    if x.stride(1) != 1:
+        raise ValueError("x must be contiguous along K (stride(1) == 1)")
+    return m, n, k
+
+
+def to_c_config(cfg: GemmConfig) -> _lib.TfGemmConfig:
+    return _lib.TfGemmConfig(
+        _lib.KERNEL_IDS[cfg.kernel],
+        cfg.block_m,
+        cfg.block_n,
+        cfg.block_k,
+        cfg.split_k,
+        cfg.num_warps,
+        cfg.num_stages,
+    )
+
+
+def _aligned_rows(x: torch.Tensor) -> torch.Tensor:
+    """x with 16-byte aligned rows (the kernels use 128-bit loads); copies only if needed."""
+    if x.data_ptr() % 16 == 0 and (x.stride(0) % 8 == 0 or x.shape[0] <= 1):
+        return x
+    return x.clone(memory_format=torch.contiguous_format)
+
+
+def workspace_bytes(m: int, n: int, k: int, group_size: int, cfg: GemmConfig) -> int:
+    c = to_c_config(cfg)
+    return int(_lib.lib().tf_w4a16_workspace_bytes(m, n, k, group_size, ctypes.byref(c)))
+
+
+def w4a16_gemm(
+    x: torch.Tensor,
+    qweight_t: torch.Tensor,
+    scales: torch.Tensor,
+    qzeros: torch.Tensor,
+    group_size: int,
+    config: GemmConfig,
+    bias: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """``x [M, K] fp16`` @ dequant(W)^T (+ bias) -> ``[M, N] fp16`` (w4a16.py:178-232)."""
+    m, n, k = _check_inputs(x, qweight_t, scales, qzeros, group_size)
+    config.validate(group_size)
+    if bias is not None:
+        if tuple(bias.shape) != (n,):
+            raise ValueError(f"bias shape {tuple(bias.shape)} != {(n,)}")
+        if bias.dtype != torch.float16:
+            raise TypeError(f"bias must be fp16, got {bias.dtype}")
+        bias = bias.contiguous()
+    dev = require_gpu("w4a16_gemm", x, qweight_t, scales, qzeros, *(() if bias is None else (bias,)))
+    out = torch.empty((m, n), dtype=torch.float16, device=dev)
+    if m == 0 or n == 0:
+        return out
+    x = _aligned_rows(x)
+    ldx = x.stride(0) if m > 1 else k
+    c = to_c_config(config)
+    h = _lib.lib()
+    need = int(h.tf_w4a16_workspace_bytes(m, n, k, group_size, ctypes.byref(c)))
+    ws = torch.empty((max(need, 4) + 3) // 4, dtype=torch.float32, device=dev) if need else None
+    with on_device(dev):
+        rc = h.tf_w4a16_linear(
+            x.data_ptr(), ldx, qweight_t.data_ptr(), scales.data_ptr(), qzeros.data_ptr(),
+            ptr(bias), out.data_ptr(), n, m, n, k, group_size, ctypes.byref(c),
+            ptr(ws), need, stream_of(dev),
+        )
+    _lib.check(rc, "tf_w4a16_linear")
+    return out
+
+
+def w4a16_dequant(
+    qweight_t: torch.Tensor,
+    scales: torch.Tensor,
+    qzeros: torch.Tensor,
+    group_size: int,
+) -> torch.Tensor:
+    """TokenForge layout -> fp16 ``[N, K]`` (w4a16.py:235-264), bit-exact with dequantize_tf."""
+    n = qweight_t.shape[0]
+    k = qweight_t.shape[1] * 8
+    if qweight_t.dtype != torch.int32 or qzeros.dtype != torch.int32:
+        raise TypeError("qweight_t and qzeros must be int32")
+    if scales.dtype != torch.float16:
+        raise TypeError(f"scales must be fp16, got {scales.dtype}")
+    if k % group_size != 0:
+        raise ValueError(f"K={k} is not a multiple of group_size={group_size}")
+    if tuple(scales.shape) != (k // group_size, n):
+        raise ValueError(f"scales shape {tuple(scales.shape)} != {(k // group_size, n)}")
+    if tuple(qzeros.shape) != (k // group_size, n // 8):
+        raise ValueError(f"qzeros shape {tuple(qzeros.shape)} != {(k // group_size, n // 8)}")
+    dev = require_gpu("w4a16_dequant", qweight_t, scales, qzeros)
+    qweight_t, scales, qzeros = (t.contiguous() for t in (qweight_t, scales, qzeros))
+    out = torch.empty((n, k), dtype=torch.float16, device=dev)
+    if out.numel() == 0:
+        return out
+    with on_device(dev):
+        rc = _lib.lib().tf_w4a16_dequant(
+            qweight_t.data_ptr(), scales.data_ptr(), qzeros.data_ptr(), out.data_ptr(), n, k,
+            group_size, stream_of(dev),
+        )
+    _lib.check(rc, "tf_w4a16_dequant")
+    return out

@@ -1,0 +1,118 @@
+"""``torch.library`` registration of the TokenForge ops on the gfx950 kernels (ops.py:1-156).
+
+Each op is a ``custom_op`` with a fake (meta) implementation, so torch.compile traces it as a
+single opaque node and HIP graphs capture it like any other kernel launch. The real
+implementations never read tensor values on the host and never synchronize.
+
+Ops (same names and schemas as the reference):
+
+* ``tokenforge::w4a16_linear(x, qweight_t, scales, qzeros, bias, group_size, backend)``
+* ``tokenforge::w4a16_dequant(qweight_t, scales, qzeros, group_size)``
+* ``tokenforge::rmsnorm_fp8_quant(x, weight, eps, scale)``
+
+All three run hand-written HIP kernels; a CPU tensor or a missing kernel library raises
+instead of falling back.
+"""
+
+from __future__ import annotations
+
+import functools
+
+import torch
+
+from tokenforge_amd.kernels import autotune, dispatch
+from tokenforge_amd.kernels.device import gpu_identity, hip_runnable
+from tokenforge_amd.kernels.hip import rmsnorm_fp8 as _rms
+from tokenforge_amd.kernels.hip import w4a16 as _w4a16
+
+
+@functools.cache
+def _gpu_id(device: torch.device) -> str:
+    return gpu_identity(device)
+
+
+@torch.library.custom_op("tokenforge::w4a16_linear", mutates_args=())
+def w4a16_linear(
+    x: torch.Tensor,
+    qweight_t: torch.Tensor,
+    scales: torch.Tensor,
+    qzeros: torch.Tensor,
+    bias: torch.Tensor | None,
+    group_size: int,
+    backend: str,
+) -> torch.Tensor:
+    k = x.shape[-1]
+    n = qweight_t.shape[0]
+    out_shape = (*x.shape[:-1], n)
+    x2 = x.reshape(-1, k)
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    m = x2.shape[0]
+    if m == 0:
+        return x.new_empty(out_shape)
+    if backend not in dispatch.HIP_BACKENDS:
+        raise ValueError(
+            f"backend must be 'hip' (or its aliases 'triton', 'cuda') at op level, got {backend!r}"
+        )
+
+    decision = dispatch.select(
+        m,
+        backend=backend,  # type: ignore[arg-type]
+        on_gpu=x.is_cuda,
+        hip_ok=hip_runnable(x2),
+    )
+    dispatch.record(decision)
+    cfg = autotune.lookup(_gpu_id(x.device), dispatch.lookup_bucket(m), n, k, group_size)
+    y = _w4a16.w4a16_gemm(x2, qweight_t, scales, qzeros, group_size, cfg, bias)
+    return y.reshape(out_shape)
+
+
+@w4a16_linear.register_fake
+def _w4a16_linear_fake(
+    x: torch.Tensor,
+    qweight_t: torch.Tensor,
+    scales: torch.Tensor,
+    qzeros: torch.Tensor,
+    bias: torch.Tensor | None,
+    group_size: int,
+    backend: str,
+) -> torch.Tensor:
+    return x.new_empty((*x.shape[:-1], qweight_t.shape[0]))
+
+
+@torch.library.custom_op("tokenforge::w4a16_dequant", mutates_args=())
+def w4a16_dequant(
+    qweight_t: torch.Tensor, scales: torch.Tensor, qzeros: torch.Tensor, group_size: int
+) -> torch.Tensor:
+    return _w4a16.w4a16_dequant(qweight_t, scales, qzeros, group_size)
+
+
+@w4a16_dequant.register_fake
+def _w4a16_dequant_fake(
+    qweight_t: torch.Tensor, scales: torch.Tensor, qzeros: torch.Tensor, group_size: int
+) -> torch.Tensor:
+    return qweight_t.new_empty((qweight_t.shape[0], qweight_t.shape[1] * 8), dtype=torch.float16)
+
+
+@torch.library.custom_op("tokenforge::rmsnorm_fp8_quant", mutates_args=())
+def rmsnorm_fp8_quant(
+    x: torch.Tensor, weight: torch.Tensor, eps: float, scale: torch.Tensor | None
+) -> tuple[torch.Tensor, torch.Tensor]:
+    h = x.shape[-1]
+    x2 = x.reshape(-1, h)
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    q, s = _rms.rmsnorm_fp8_quant(x2, weight, eps, scale)
+    if scale is not None:
+        s = s.clone()  # custom ops may not return an alias of an input
+    return q.reshape(x.shape), s.reshape((*x.shape[:-1], 1)) if scale is None else s
+
+
+@rmsnorm_fp8_quant.register_fake
+def _rmsnorm_fp8_quant_fake(
+    x: torch.Tensor, weight: torch.Tensor, eps: float, scale: torch.Tensor | None
+) -> tuple[torch.Tensor, torch.Tensor]:
+    q = x.new_empty(x.shape, dtype=torch.float8_e4m3fn)
+    if scale is None:
+        return q, x.new_empty((*x.shape[:-1], 1), dtype=torch.float32)
+    return q, torch.empty_like(scale)
