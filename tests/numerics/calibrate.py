@@ -15,6 +15,7 @@ import argparse
 import json
 import math
 import platform
+from pathlib import Path
 
 import numpy as np
 import torch
@@ -60,13 +61,16 @@ def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--device", choices=["cpu", "cuda"], required=True)
     ap.add_argument("--write", action="store_true", help="freeze the result in tolerances.json")
+    ap.add_argument("--out", type=str, default=None, help="write the updated tolerances.json here instead")
     args = ap.parse_args()
     result = calibrate(args.device)
     print(json.dumps(result, indent=2), flush=True)
-    if args.write:
+    if args.write or args.out:
         data = json.loads(TOLERANCES_PATH.read_text()) if TOLERANCES_PATH.exists() else {}
         data.setdefault("w4a16", {})[args.device] = result
-        TOLERANCES_PATH.write_text(json.dumps(data, indent=2, sort_keys=True) + "\n")
+        target = Path(args.out) if args.out else TOLERANCES_PATH
+        target.parent.mkdir(parents=True, exist_ok=True)
+        target.write_text(json.dumps(data, indent=2, sort_keys=True) + "\n")
 
 
 if __name__ == "__main__":

@@ -68,14 +68,17 @@ def test_linear_shape_suite(shape, m: int, device: torch.device) -> None:  # typ
 
 
 PATH_CONFIGS = [
-    GemmConfig("gemv_dot", 1, 16, 128, 1, 1, 1),
+    GemmConfig("gemv_dot", 1, 16, 128, 1, 1, 2),
     GemmConfig("gemv_dot", 1, 64, 128, 1, 4, 2),
-    GemmConfig("gemv_dot", 1, 32, 128, 1, 16, 4),
+    GemmConfig("gemv_dot", 1, 32, 128, 1, 8, 4),
+    GemmConfig("gemv_dot", 1, 64, 128, 1, 2, 3),
     GemmConfig("gemv_dot", 2, 32, 128, 1, 2, 2),
-    GemmConfig("gemv_dot", 4, 16, 128, 1, 8, 1),
-    GemmConfig("gemv_mfma", 16, 16, 128, 1, 1, 1),
+    GemmConfig("gemv_dot", 4, 16, 128, 1, 8, 2),
+    GemmConfig("gemv_mfma", 16, 16, 128, 1, 1, 2),
+    GemmConfig("gemv_mfma", 16, 16, 128, 1, 16, 4),
     GemmConfig("gemv_mfma", 16, 64, 128, 1, 8, 2),
-    GemmConfig("gemv_mfma", 16, 32, 128, 1, 16, 4),
+    GemmConfig("gemv_mfma", 16, 64, 128, 1, 4, 3),
+    GemmConfig("gemv_mfma", 16, 32, 128, 1, 8, 4),
     GemmConfig("gemv_mfma", 32, 32, 128, 1, 4, 2),
     GemmConfig("gemm_mfma", 64, 64, 64, 1, 4, 2),
     GemmConfig("gemm_mfma", 64, 128, 64, 3, 4, 2),
@@ -116,7 +119,7 @@ def test_small_group_sizes(group_size: int, device: torch.device) -> None:
     w = cases.layer_weights(n, k, 0, group_size)
     wd = cases.on_device(w, device)
     configs = [
-        GemmConfig("gemv_dot", 1, 16, 128, 1, 2, 1),
+        GemmConfig("gemv_dot", 1, 16, 128, 1, 2, 2),
         GemmConfig("gemv_mfma", 16, 32, 128, 1, 2, 2),
         GemmConfig("gemm_mfma", 64, 64, 32, 2, 4, 2),
     ]
@@ -196,7 +199,7 @@ def test_non_contiguous_and_misaligned_inputs_are_handled(device: torch.device) 
 def test_rejects_bad_weight_layouts(device: torch.device) -> None:
     w = cases.on_device(cases.layer_weights(64, 256, 0), device)
     x = cases.activations(1, 256, 0).to(device)
-    cfg = GemmConfig("gemv_dot", 1, 16, 128, 1, 1, 1)
+    cfg = GemmConfig("gemv_dot", 1, 16, 128, 1, 1, 2)
     with pytest.raises(ValueError, match="contiguous"):
         w4a16_gemm(x, w.qweight_t.t().contiguous().t(), w.scales, w.qzeros, G, cfg)
     with pytest.raises(ValueError, match="encodes K"):
@@ -226,8 +229,8 @@ def _weights_from_ints(q: torch.Tensor, z: torch.Tensor, s: torch.Tensor) -> opa
 
 
 F1_CONFIGS = (
-    GemmConfig("gemv_dot", 2, 16, 128, 1, 2, 1),
-    GemmConfig("gemv_mfma", 16, 16, 128, 1, 2, 1),
+    GemmConfig("gemv_dot", 2, 16, 128, 1, 2, 2),
+    GemmConfig("gemv_mfma", 16, 16, 128, 1, 2, 2),
     GemmConfig("gemm_mfma", 64, 64, 64, 2, 4, 2),
 )
 
@@ -260,8 +263,8 @@ def test_f1_real_inf_and_nan_propagate(device: torch.device) -> None:
     x[2, 9] = float("nan")
     ref16 = torch.from_numpy(oref.w4a16_reference(x.numpy(), w)).to(torch.float16)
     configs = (
-        GemmConfig("gemv_dot", 4, 16, 128, 1, 2, 1),
-        GemmConfig("gemv_mfma", 16, 16, 128, 1, 2, 1),
+        GemmConfig("gemv_dot", 4, 16, 128, 1, 2, 2),
+        GemmConfig("gemv_mfma", 16, 16, 128, 1, 2, 2),
         GemmConfig("gemm_mfma", 64, 64, 64, 2, 4, 2),
     )
     for cfg in configs:
@@ -285,7 +288,7 @@ def test_zero_and_denormal_scales(scale_value: float, device: torch.device) -> N
     w = _weights_from_ints(q, z, s)
     wd = cases.on_device(w, device)
     x = cases.activations(3, k, 0)
-    for cfg in (GemmConfig("gemv_dot", 1, 16, 128, 1, 1, 1),) + F1_CONFIGS:
+    for cfg in (GemmConfig("gemv_dot", 1, 16, 128, 1, 1, 2),) + F1_CONFIGS:
         rows = x[: min(3, cfg.block_m)]
         y = w4a16_gemm(rows.to(device), wd.qweight_t, wd.scales, wd.qzeros, G, cfg)
         assert bool(torch.isfinite(y).all())

@@ -144,7 +144,7 @@ def test_save_failure_leaves_previous_file(monkeypatch: pytest.MonkeyPatch) -> N
         raise OSError("disk full")
 
     monkeypatch.setattr(autotune.os, "replace", boom)
-    cache.put(2, N, K, G, GemmConfig("gemv_dot", 2, 16, 128, 1, 1, 1))
+    cache.put(2, N, K, G, GemmConfig("gemv_dot", 2, 16, 128, 1, 1, 2))
     with pytest.raises(OSError, match="disk full"):
         cache.save()
     assert cache.path.read_text() == original
@@ -156,7 +156,7 @@ def test_f4_retune_after_corruption_restores_outputs(caplog: pytest.LogCaptureFi
     """Corrupt -> discard + warn -> retune -> same winner -> bit-identical kernel output."""
     from tokenforge_amd.kernels.hip.w4a16 import w4a16_gemm
 
-    candidates = [TUNED_1, GemmConfig("gemv_mfma", 16, 16, 128, 1, 2, 1)]
+    candidates = [TUNED_1, GemmConfig("gemv_mfma", 16, 16, 128, 1, 2, 2)]
     bench, _ = _fake_bench_prefers(TUNED_1)
     cache = _fresh_cache()
     winners = autotune.tune_layer(

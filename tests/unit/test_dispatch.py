@@ -168,8 +168,8 @@ def test_config_validation(kwargs: dict, match: str) -> None:
 
 
 def test_config_from_dict_strict() -> None:
-    good = GemmConfig("gemv_dot", 1, 16, 128, 1, 1, 1).to_dict()
-    assert GemmConfig.from_dict(good) == GemmConfig("gemv_dot", 1, 16, 128, 1, 1, 1)
+    good = GemmConfig("gemv_dot", 1, 16, 128, 1, 1, 2).to_dict()
+    assert GemmConfig.from_dict(good) == GemmConfig("gemv_dot", 1, 16, 128, 1, 1, 2)
     with pytest.raises(ValueError, match="unknown"):
         GemmConfig.from_dict({**good, "block_q": 1})
     with pytest.raises(TypeError, match="integers"):

@@ -1,21 +1,26 @@
 // Decode-shaped W4A16 kernels (small M): stream the packed weights once, dequantize in
 // registers, accumulate in fp32.
 //
-// Both kernels tile N into 16-row tiles of qweight_t (block_n = 16 * RT rows per
-// workgroup). Inside a 16-row tile, a wavefront covers 16 rows x 4 consecutive 32-value
-// chunks of K per step: every lane issues one 128-bit load (4 packed words = 32 weights),
-// so each row receives a 64-byte contiguous run per load and adjacent steps complete the
-// 128-byte lines. The num_warps waves of a workgroup take disjoint, contiguous K ranges
-// of the same rows (on-chip split-K); their partial sums are added in wave order through
-// LDS, so results are bit-identical from run to run. No workspace, no atomics.
+// Work split: a workgroup owns block_n = 16 * RT consecutive rows of qweight_t (output
+// columns); its num_warps waves take disjoint, contiguous K ranges of those rows (on-chip
+// split-K) and their partial sums are added in wave order through LDS, so results are
+// bit-identical from run to run. No workspace, no atomics.
+//
+// Memory stream: a "step" is 16 rows x 128 K values. Per step each lane issues one 128-bit
+// buffer load per 16-row tile (4 packed words = 32 weights of one row), so each row receives
+// a 64-byte run per load and consecutive steps complete the 128-byte lines. Every wave keeps
+// a ring of P steps in flight: the loads of step s + P are issued as soon as step s has been
+// consumed, so the HBM queue never drains while the wave computes. Buffer loads return zeros
+// past the end of a tensor, which handles ragged N, partial last steps and unused M rows
+// without branches.
 //
 //  * gemv_dot  (TF_KERNEL_GEMV_DOT): lane = (row c = lane/4, chunk g = lane%4). Each lane
-//    accumulates its 32 products per row with v_dot2_f32_f16; quads are reduced with DPP.
-//  * gemv_mfma (TF_KERNEL_GEMV_MFMA): lane = (row c = lane%16, chunk g = lane/16), which is
-//    exactly the B-operand layout of v_mfma_f32_16x16x32_f16 (8 consecutive K values per
-//    lane = one packed word). The dequantized word goes straight into the MFMA; x rows are
-//    the A operand (M <= 16 per M tile). The matrix core replaces the VALU dot products,
-//    so VALU work per weight is only the unpack + (q - z) * s.
+//    accumulates its products with v_dot2_f32_f16; quads are reduced with DPP.
+//  * gemv_mfma (TF_KERNEL_GEMV_MFMA): lane = (row c = lane%16, chunk g = lane/16), exactly the
+//    B-operand layout of v_mfma_f32_16x16x32_f16 (8 consecutive K values per lane = one
+//    packed word). The dequantized word goes straight into the MFMA and x rows are the A
+//    operand, so the matrix core does the dot products and the VALU only unpacks and scales.
+//    A rows m >= M only feed output rows that are discarded, so they need no masking.
 #include "linear.h"
 
 namespace tf {
@@ -26,22 +31,88 @@ __device__ __forceinline__ void k_range(int wave, int waves, int nsteps, int* s0
   *s1 = (int)(((int64_t)(wave + 1) * nsteps) / waves);
 }
 
+// Buffer resources and per-launch constants shared by both kernels.
+struct Streams {
+  __amdgpu_buffer_rsrc_t qw, sc, qz, x;
+  uint32_t row_bytes;  // K / 2
+  int nchunks;         // K / 32
+  int log2g;
+  int n;
+};
+
+__device__ __forceinline__ Streams make_streams(const LinearArgs& a) {
+  Streams s;
+  s.row_bytes = (uint32_t)(a.k >> 1);
+  s.qw = make_rsrc(a.qw, (uint32_t)a.n * s.row_bytes);
+  s.sc = make_rsrc(a.scales, (uint32_t)((a.k >> a.log2g) * a.n * 2));
+  s.qz = make_rsrc(a.qz, (uint32_t)((a.k >> a.log2g) * (a.n >> 3) * 4));
+  s.x = make_rsrc(a.x, (uint32_t)(((int64_t)(a.m - 1) * a.ldx + a.k) * 2));
+  s.nchunks = a.k >> 5;
+  s.log2g = a.log2g;
+  s.n = a.n;
+  return s;
+}
+
+// Weights, scales and zero words of one step for RT row tiles.
+template <int RT>
+struct WeightSlot {
+  u4 w[RT];
+  uint32_t s[RT];
+  uint32_t z[RT];
+};
+
+// Loads of (row n_base + rt*16 + c, chunk ch) for every rt; zeros when invalid.
+template <int RT>
+__device__ __forceinline__ void issue_weights(WeightSlot<RT>& slot, const Streams& st, int n_base,
+                                              int c, int ch, bool kvalid) {
+  const uint32_t grp = (uint32_t)(ch << 5) >> st.log2g;
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    const int n = n_base + rt * 16 + c;
+    const bool ok = kvalid && n < st.n;
+    const uint32_t wo = ok ? (uint32_t)n * st.row_bytes + (uint32_t)ch * 16u : kOutOfRange;
+    const uint32_t so = ok ? (grp * (uint32_t)st.n + (uint32_t)n) * 2u : kOutOfRange;
+    const uint32_t zo = ok ? (grp * (uint32_t)(st.n >> 3) + (uint32_t)(n >> 3)) * 4u : kOutOfRange;
+    slot.w[rt] = load_b128(st.qw, wo);
+    slot.s[rt] = load_b16(st.sc, so);
+    slot.z[rt] = load_b32(st.qz, zo);
+  }
+}
+
 // ------------------------------------------------------------------------ gemv_dot
 
-template <int MAXM, int RT, int UNROLL>
-__global__ __launch_bounds__(1024) void gemv_dot_kernel(LinearArgs a) {
-  extern __shared__ float red[];  // [(waves - 1)][MAXM][RT][16]
+template <int MAXM, int RT>
+struct DotSlot {
+  WeightSlot<RT> wt;
+  u4 x[MAXM][4];  // x[m][32 values of this lane's chunk]
+};
+
+template <int MAXM, int RT, int P, int MAXW>
+__global__ __launch_bounds__(MAXW * 64) void gemv_dot_kernel(LinearArgs a) {
+  extern __shared__ __attribute__((aligned(16))) float red[];  // [(waves - 1)][MAXM][RT][16]
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int waves = blockDim.x >> 6;
   const int g = lane & 3;
   const int c = lane >> 2;
   const int n_base = blockIdx.x * 16 * RT;
-  const int nchunks = a.k >> 5;
-  const int nsteps = (nchunks + 3) >> 2;
-  const int64_t words_per_row = a.k >> 3;
+  const Streams st = make_streams(a);
+  const int nsteps = (st.nchunks + 3) >> 2;
   int s0, s1;
   k_range(wave, waves, nsteps, &s0, &s1);
+  const UnpackConsts uc = unpack_consts();
+
+  auto issue = [&](DotSlot<MAXM, RT>& slot, int step) {
+    const int ch = step * 4 + g;
+    const bool kvalid = step < s1 && ch < st.nchunks;
+    issue_weights<RT>(slot.wt, st, n_base, c, ch, kvalid);
+#pragma unroll
+    for (int m = 0; m < MAXM; ++m) {
+      const uint32_t xo = (kvalid && m < a.m) ? (uint32_t)(((int64_t)m * a.ldx + ch * 32) * 2) : kOutOfRange;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) slot.x[m][j] = load_b128(st.x, xo + 16u * j);
+    }
+  };
 
   float acc[MAXM][RT];
 #pragma unroll
@@ -49,60 +120,31 @@ __global__ __launch_bounds__(1024) void gemv_dot_kernel(LinearArgs a) {
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) acc[m][rt] = 0.0f;
 
-  for (int s = s0; s < s1; s += UNROLL) {
-    u4 wv[UNROLL][RT];
-    uint32_t sc[UNROLL][RT];
-    uint32_t zw[UNROLL][RT];
+  DotSlot<MAXM, RT> ring[P];
 #pragma unroll
-    for (int u = 0; u < UNROLL; ++u) {
-      const int ch = (s + u) * 4 + g;
-      const bool kvalid = (s + u < s1) && (ch < nchunks);
-      const int grp = (ch << 5) >> a.log2g;
+  for (int p = 0; p < P; ++p) issue(ring[p], s0 + p);
+
+  for (int s = s0; s < s1; s += P) {
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt) {
-        const int n = n_base + rt * 16 + c;
-        if (kvalid && n < a.n) {
-          wv[u][rt] = *reinterpret_cast<const u4*>(a.qw + (int64_t)n * words_per_row + ch * 4);
-          sc[u][rt] = a.scales[(int64_t)grp * a.n + n];
-          zw[u][rt] = a.qz[(int64_t)grp * (a.n >> 3) + (n >> 3)];
-        } else {
-          wv[u][rt] = u4{0u, 0u, 0u, 0u};
-          sc[u][rt] = 0u;
-          zw[u][rt] = 0u;
+    for (int p = 0; p < P; ++p) {
+      if (s + p < s1) {
+        DotSlot<MAXM, RT>& slot = ring[p];
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+          const int n = n_base + rt * 16 + c;
+          const QuantParams qp = make_params(zero_of(slot.wt.z[rt], (uint32_t)n), slot.wt.s[rt]);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            h2 wd[4];
+            dequant_word(slot.wt.w[rt][j], qp, uc, wd);
+#pragma unroll
+            for (int m = 0; m < MAXM; ++m)
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+                acc[m][rt] = __builtin_amdgcn_fdot2(as_h2(slot.x[m][j][i]), wd[i], acc[m][rt], false);
+          }
         }
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < UNROLL; ++u) {
-      const int ch = (s + u) * 4 + g;
-      const bool kvalid = (s + u < s1) && (ch < nchunks);
-      // x[m][32 values of this chunk] as 16 fp16 pairs.
-      u4 xv[MAXM][4];
-#pragma unroll
-      for (int m = 0; m < MAXM; ++m) {
-        if (kvalid && m < a.m) {
-          const u4* xp = reinterpret_cast<const u4*>(a.x + (int64_t)m * a.ldx + ch * 32);
-#pragma unroll
-          for (int j = 0; j < 4; ++j) xv[m][j] = xp[j];
-        } else {
-#pragma unroll
-          for (int j = 0; j < 4; ++j) xv[m][j] = u4{0u, 0u, 0u, 0u};
-        }
-      }
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt) {
-        const int n = n_base + rt * 16 + c;
-        const QuantParams p = make_params(zero_of(zw[u][rt], (uint32_t)n), sc[u][rt]);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          h2 wd[4];
-          dequant_word(wv[u][rt][j], p, wd);
-#pragma unroll
-          for (int m = 0; m < MAXM; ++m)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-              acc[m][rt] = __builtin_amdgcn_fdot2(as_h2(xv[m][j][i]), wd[i], acc[m][rt], false);
-        }
+        issue(slot, s + p + P);
       }
     }
   }
@@ -145,9 +187,15 @@ __global__ __launch_bounds__(1024) void gemv_dot_kernel(LinearArgs a) {
 
 // ------------------------------------------------------------------------ gemv_mfma
 
-template <int MT, int RT, int UNROLL>
-__global__ __launch_bounds__(1024) void gemv_mfma_kernel(LinearArgs a) {
-  extern __shared__ __attribute__((aligned(16))) float red[];  // [(waves - 1)][MT][RT][64 lanes][4]
+template <int MT, int RT>
+struct MfmaSlot {
+  WeightSlot<RT> wt;
+  h8 x[MT][4];  // A operand: row (m_base + mt*16 + c), the 32 values of this lane's chunk
+};
+
+template <int MT, int RT, int P, int MAXW>
+__global__ __launch_bounds__(MAXW * 64) void gemv_mfma_kernel(LinearArgs a) {
+  extern __shared__ __attribute__((aligned(16))) float red[];  // [(waves - 1)][MT][RT][64][4]
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int waves = blockDim.x >> 6;
@@ -155,11 +203,24 @@ __global__ __launch_bounds__(1024) void gemv_mfma_kernel(LinearArgs a) {
   const int g = lane >> 4;
   const int n_base = blockIdx.x * 16 * RT;
   const int m_base = blockIdx.y * 16 * MT;
-  const int nchunks = a.k >> 5;
-  const int nsteps = (nchunks + 3) >> 2;
-  const int64_t words_per_row = a.k >> 3;
+  const Streams st = make_streams(a);
+  const int nsteps = (st.nchunks + 3) >> 2;
   int s0, s1;
   k_range(wave, waves, nsteps, &s0, &s1);
+  const UnpackConsts uc = unpack_consts();
+
+  auto issue = [&](MfmaSlot<MT, RT>& slot, int step) {
+    const int ch = step * 4 + g;
+    const bool kvalid = step < s1 && ch < st.nchunks;
+    issue_weights<RT>(slot.wt, st, n_base, c, ch, kvalid);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = m_base + mt * 16 + c;
+      const uint32_t xo = (kvalid && m < a.m) ? (uint32_t)(((int64_t)m * a.ldx + ch * 32) * 2) : kOutOfRange;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) slot.x[mt][j] = __builtin_bit_cast(h8, load_b128(st.x, xo + 16u * j));
+    }
+  };
 
   f4 acc[MT][RT];
 #pragma unroll
@@ -167,60 +228,30 @@ __global__ __launch_bounds__(1024) void gemv_mfma_kernel(LinearArgs a) {
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) acc[mt][rt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  for (int s = s0; s < s1; s += UNROLL) {
-    u4 wv[UNROLL][RT];
-    uint32_t sc[UNROLL][RT];
-    uint32_t zw[UNROLL][RT];
+  MfmaSlot<MT, RT> ring[P];
 #pragma unroll
-    for (int u = 0; u < UNROLL; ++u) {
-      const int ch = (s + u) * 4 + g;
-      const bool kvalid = (s + u < s1) && (ch < nchunks);
-      const int grp = (ch << 5) >> a.log2g;
+  for (int p = 0; p < P; ++p) issue(ring[p], s0 + p);
+
+  for (int s = s0; s < s1; s += P) {
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt) {
-        const int n = n_base + rt * 16 + c;
-        if (kvalid && n < a.n) {
-          wv[u][rt] = *reinterpret_cast<const u4*>(a.qw + (int64_t)n * words_per_row + ch * 4);
-          sc[u][rt] = a.scales[(int64_t)grp * a.n + n];
-          zw[u][rt] = a.qz[(int64_t)grp * (a.n >> 3) + (n >> 3)];
-        } else {
-          wv[u][rt] = u4{0u, 0u, 0u, 0u};
-          sc[u][rt] = 0u;
-          zw[u][rt] = 0u;
+    for (int p = 0; p < P; ++p) {
+      if (s + p < s1) {
+        MfmaSlot<MT, RT>& slot = ring[p];
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+          const int n = n_base + rt * 16 + c;
+          const QuantParams qp = make_params(zero_of(slot.wt.z[rt], (uint32_t)n), slot.wt.s[rt]);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            h2 wd[4];
+            dequant_word(slot.wt.w[rt][j], qp, uc, wd);
+            const h8 b = pack_h8(wd);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+              acc[mt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(slot.x[mt][j], b, acc[mt][rt], 0, 0, 0);
+          }
         }
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < UNROLL; ++u) {
-      const int ch = (s + u) * 4 + g;
-      const bool kvalid = (s + u < s1) && (ch < nchunks);
-      // A operand: row (m_base + mt*16 + c) of x, the 32 values of this lane's chunk.
-      h8 xa[MT][4];
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const int m = m_base + mt * 16 + c;
-        if (kvalid && m < a.m) {
-          const h8* xp = reinterpret_cast<const h8*>(a.x + (int64_t)m * a.ldx + ch * 32);
-#pragma unroll
-          for (int j = 0; j < 4; ++j) xa[mt][j] = xp[j];
-        } else {
-#pragma unroll
-          for (int j = 0; j < 4; ++j) xa[mt][j] = h8{0, 0, 0, 0, 0, 0, 0, 0};
-        }
-      }
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt) {
-        const int n = n_base + rt * 16 + c;
-        const QuantParams p = make_params(zero_of(zw[u][rt], (uint32_t)n), sc[u][rt]);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          h2 wd[4];
-          dequant_word(wv[u][rt][j], p, wd);
-          const h8 b = pack_h8(wd);
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt)
-            acc[mt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[mt][j], b, acc[mt][rt], 0, 0, 0);
-        }
+        issue(slot, s + p + P);
       }
     }
   }
@@ -266,45 +297,55 @@ __global__ __launch_bounds__(1024) void gemv_mfma_kernel(LinearArgs a) {
 
 int64_t no_workspace(const LinearArgs&, const tf_gemm_config&) { return 0; }
 
-template <int MAXM, int RT, int UNROLL>
+// Buffer offsets are 32-bit: every byte offset into qweight_t, scales, qzeros and x must fit.
+int check_offsets(const LinearArgs& a) {
+  const int64_t x_bytes = ((int64_t)(a.m - 1) * a.ldx + a.k) * 2;
+  const int64_t w_bytes = (int64_t)a.n * (a.k / 2);
+  if (x_bytes >= (int64_t)kOutOfRange || w_bytes >= (int64_t)kOutOfRange)
+    return fail(TF_EINVAL, "tf_w4a16_linear: gemv kernels need x and qweight_t below 2 GiB");
+  return TF_OK;
+}
+
+template <int MAXM, int RT, int P, int MAXW>
 int launch_dot(const LinearArgs& a, const tf_gemm_config& cfg, float*, hipStream_t stream) {
   if (a.m > MAXM) return fail(TF_EINVAL, "tf_w4a16_linear: gemv_dot variant needs m <= block_m");
+  if (int rc = check_offsets(a)) return rc;
   const int waves = cfg.num_warps;
   const dim3 grid((unsigned)cdiv(a.n, 16 * RT));
   const size_t lds = (size_t)(waves - 1) * MAXM * RT * 16 * sizeof(float);
-  gemv_dot_kernel<MAXM, RT, UNROLL><<<grid, waves * 64, lds, stream>>>(a);
+  gemv_dot_kernel<MAXM, RT, P, MAXW><<<grid, waves * 64, lds, stream>>>(a);
   return check_launch("tf_w4a16_linear(gemv_dot)");
 }
 
-template <int MT, int RT, int UNROLL>
+template <int MT, int RT, int P, int MAXW>
 int launch_mfma(const LinearArgs& a, const tf_gemm_config& cfg, float*, hipStream_t stream) {
+  if (int rc = check_offsets(a)) return rc;
   const int waves = cfg.num_warps;
   const dim3 grid((unsigned)cdiv(a.n, 16 * RT), (unsigned)cdiv(a.m, 16 * MT));
   const size_t lds = (size_t)(waves - 1) * MT * RT * 64 * 4 * sizeof(float);
-  gemv_mfma_kernel<MT, RT, UNROLL><<<grid, waves * 64, lds, stream>>>(a);
+  gemv_mfma_kernel<MT, RT, P, MAXW><<<grid, waves * 64, lds, stream>>>(a);
   return check_launch("tf_w4a16_linear(gemv_mfma)");
 }
 
-#define TF_WAVES_5(KERNEL, BM, BN, ST, FN)                                              \
-  {{KERNEL, BM, BN, 128, 1, 1, ST}, FN, no_workspace},                                  \
-      {{KERNEL, BM, BN, 128, 1, 2, ST}, FN, no_workspace},                              \
-      {{KERNEL, BM, BN, 128, 1, 4, ST}, FN, no_workspace},                              \
-      {{KERNEL, BM, BN, 128, 1, 8, ST}, FN, no_workspace},                              \
-      {{KERNEL, BM, BN, 128, 1, 16, ST}, FN, no_workspace}
+// One table row per (variant, num_warps): num_warps ranges over 1..MAXW (powers of two).
+#define TF_W1(K, BM, BN, ST, FN) {{K, BM, BN, 128, 1, 1, ST}, FN, no_workspace}
+#define TF_W2(K, BM, BN, ST, FN) TF_W1(K, BM, BN, ST, FN), {{K, BM, BN, 128, 1, 2, ST}, FN, no_workspace}
+#define TF_W4(K, BM, BN, ST, FN) TF_W2(K, BM, BN, ST, FN), {{K, BM, BN, 128, 1, 4, ST}, FN, no_workspace}
+#define TF_W8(K, BM, BN, ST, FN) TF_W4(K, BM, BN, ST, FN), {{K, BM, BN, 128, 1, 8, ST}, FN, no_workspace}
+#define TF_W16(K, BM, BN, ST, FN) TF_W8(K, BM, BN, ST, FN), {{K, BM, BN, 128, 1, 16, ST}, FN, no_workspace}
 
-#define TF_DOT(BM, RT, ST) TF_WAVES_5(TF_KERNEL_GEMV_DOT, BM, 16 * RT, ST, (launch_dot<BM, RT, ST>))
-#define TF_MFMA(MT, RT, ST) TF_WAVES_5(TF_KERNEL_GEMV_MFMA, 16 * MT, 16 * RT, ST, (launch_mfma<MT, RT, ST>))
+#define TF_DOT(BM, RT, P, MAXW) \
+  TF_W##MAXW(TF_KERNEL_GEMV_DOT, BM, 16 * RT, P, (launch_dot<BM, RT, P, MAXW>))
+#define TF_MFMA(MT, RT, P, MAXW) \
+  TF_W##MAXW(TF_KERNEL_GEMV_MFMA, 16 * MT, 16 * RT, P, (launch_mfma<MT, RT, P, MAXW>))
 
 const Variant kGemvVariants[] = {
-    TF_DOT(1, 1, 1), TF_DOT(1, 1, 2), TF_DOT(1, 1, 4),
-    TF_DOT(1, 2, 1), TF_DOT(1, 2, 2), TF_DOT(1, 2, 4),
-    TF_DOT(1, 4, 1), TF_DOT(1, 4, 2),
-    TF_DOT(2, 1, 1), TF_DOT(2, 1, 2), TF_DOT(2, 2, 1), TF_DOT(2, 2, 2),
-    TF_DOT(4, 1, 1), TF_DOT(4, 1, 2), TF_DOT(4, 2, 1),
-    TF_MFMA(1, 1, 1), TF_MFMA(1, 1, 2), TF_MFMA(1, 1, 4),
-    TF_MFMA(1, 2, 1), TF_MFMA(1, 2, 2), TF_MFMA(1, 2, 4),
-    TF_MFMA(1, 4, 1), TF_MFMA(1, 4, 2),
-    TF_MFMA(2, 1, 1), TF_MFMA(2, 1, 2), TF_MFMA(2, 2, 1), TF_MFMA(2, 2, 2),
+    TF_DOT(1, 1, 2, 16), TF_DOT(1, 1, 4, 16), TF_DOT(1, 2, 2, 16), TF_DOT(1, 2, 4, 8),
+    TF_DOT(1, 4, 2, 8),  TF_DOT(1, 4, 3, 8),  TF_DOT(2, 1, 2, 16), TF_DOT(2, 2, 2, 8),
+    TF_DOT(4, 1, 2, 8),
+    TF_MFMA(1, 1, 2, 16), TF_MFMA(1, 1, 4, 16), TF_MFMA(1, 2, 2, 16), TF_MFMA(1, 2, 3, 16),
+    TF_MFMA(1, 2, 4, 8),  TF_MFMA(1, 4, 2, 8),  TF_MFMA(1, 4, 3, 8),  TF_MFMA(2, 1, 2, 16),
+    TF_MFMA(2, 2, 2, 8),
 };
 
 }  // namespace

@@ -13,6 +13,16 @@ namespace tf {
 namespace {
 
 constexpr float kFp8Max = 448.0f;
+
+// fp16(fp32(a * b)): reference.py:39 rounds x * rstd to fp32 and then to fp16. Left alone,
+// the backend folds the multiply and the conversion into v_fma_mixlo_f16, which rounds once,
+// straight to fp16, and differs from the double rounding on ~6e-5 of the elements. The empty
+// asm makes the fp32 product a register value, so it is rounded to fp32 first.
+__device__ __forceinline__ _Float16 mul_round_f32_then_f16(float a, float b) {
+  float p = a * b;
+  __asm__ volatile("" : "+v"(p));
+  return (_Float16)p;
+}
 constexpr float kMinScale = 1.0f / (448.0f * 512.0f);  // reference.py:10
 
 __device__ __forceinline__ float nan_max(float a, float b) { return (a > b || a != a) ? a : b; }
@@ -118,7 +128,7 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_fp8_kernel(
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       // reference.py:39: fp16(x * rstd) in fp32 then cast, times weight in fp16 (one rounding).
-      const _Float16 nrm = (_Float16)((float)xv[i][j] * rstd);
+      const _Float16 nrm = mul_round_f32_then_f16((float)xv[i][j], rstd);
       const _Float16 y = nrm * wv[j];
       xv[i][j] = y;  // the row is reused in place for y
       if (e0 + j < h) amax = nan_max(amax, __builtin_fabsf((float)y));

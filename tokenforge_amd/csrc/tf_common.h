@@ -44,6 +44,28 @@ __host__ __device__ __forceinline__ uint32_t awq_nibble_of(uint32_t j) {
   return (j & 1u) * 4u + (j >> 1);
 }
 
+// ------------------------------------------------------------------ buffer loads
+
+// Raw buffer resources (V#): base, byte size, no stride. A load whose byte offset lies at
+// or past the size returns zeros without touching memory, which is how the kernels handle
+// ragged edges without branches. Dword 3 = 0x00020000 selects the raw 32-bit data format of
+// the gfx9 family (gfx950 included).
+constexpr int kBufferFlags = 0x00020000;
+constexpr uint32_t kOutOfRange = 0x80000000u;  // any offset >= every size used here
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kBufferFlags);
+}
+__device__ __forceinline__ u4 load_b128(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+}
+__device__ __forceinline__ uint32_t load_b32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
+}
+__device__ __forceinline__ uint32_t load_b16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0);
+}
+
 // ------------------------------------------------------------------ zero/scale operands
 
 // Per-(group, column) constants for the dequantization of one packed word.
@@ -71,22 +93,43 @@ __device__ __forceinline__ uint32_t zero_of(uint32_t zword, uint32_t n) {
   return (zword >> (4u * awq_nibble_of(n & 7u))) & 0xFu;
 }
 
+// Unpack masks and magic exponents kept in VGPRs: gfx9 VOP3 takes no literal operands, so
+// with literals the compiler splits (w & m) | e into two instructions; from registers it is
+// a single v_and_or_b32.
+struct UnpackConsts {
+  uint32_t m_lo;  // 0x000F000F
+  uint32_t m_hi;  // 0x00F000F0
+  uint32_t e_lo;  // 0x64006400: fp16x2 1024
+  uint32_t e_hi;  // 0x54005400: fp16x2 64
+};
+
+__device__ __forceinline__ UnpackConsts unpack_consts() {
+  UnpackConsts c{0x000F000Fu, 0x00F000F0u, 0x64006400u, 0x54005400u};
+  __asm__ volatile("" : "+v"(c.m_lo), "+v"(c.m_hi), "+v"(c.e_lo), "+v"(c.e_hi));
+  return c;
+}
+
 // Dequantize the eight int4 values of one packed word into fp16, K order:
-// out[i] holds offsets (2i, 2i+1). (word & 0x000F000F) | 0x6400_6400 is the fp16x2
-// pair (1024 + q0, 1024 + q1) because nibble 0 holds offset 0 and nibble 4 offset 1;
-// the 0x00F0 nibbles become 64 + q with the 0x5400 magic. Subtracting (1024 + z) or
-// (64 + z) is exact in fp16, so fp16(q - z) * s rounds exactly once (v_pk_mul_f16),
-// matching pack.py:194 and w4a16.py:95 bit for bit.
-__device__ __forceinline__ void dequant_word(uint32_t w, const QuantParams& p, h2 out[4]) {
+// out[i] holds offsets (2i, 2i+1). (word & 0x000F000F) | 0x6400_6400 is the fp16x2 pair
+// (1024 + q0, 1024 + q1) because nibble 0 holds offset 0 and nibble 4 offset 1; the 0x00F0
+// nibbles become 64 + q with the 0x5400 magic. Subtracting (1024 + z) or (64 + z) is exact
+// in fp16, so fp16(q - z) * s rounds exactly once (v_pk_mul_f16), matching pack.py:194 and
+// w4a16.py:95 bit for bit.
+__device__ __forceinline__ void dequant_word(uint32_t w, const QuantParams& p, const UnpackConsts& k,
+                                             h2 out[4]) {
   const uint32_t w8 = w >> 8;
-  const h2 a0 = as_h2((w & 0x000F000Fu) | 0x64006400u);
-  const h2 a1 = as_h2((w & 0x00F000F0u) | 0x54005400u);
-  const h2 a2 = as_h2((w8 & 0x000F000Fu) | 0x64006400u);
-  const h2 a3 = as_h2((w8 & 0x00F000F0u) | 0x54005400u);
+  const h2 a0 = as_h2((w & k.m_lo) | k.e_lo);
+  const h2 a1 = as_h2((w & k.m_hi) | k.e_hi);
+  const h2 a2 = as_h2((w8 & k.m_lo) | k.e_lo);
+  const h2 a3 = as_h2((w8 & k.m_hi) | k.e_hi);
   out[0] = (a0 - p.zlo) * p.s;
   out[1] = (a1 - p.zhi) * p.s;
   out[2] = (a2 - p.zlo) * p.s;
   out[3] = (a3 - p.zhi) * p.s;
+}
+
+__device__ __forceinline__ void dequant_word(uint32_t w, const QuantParams& p, h2 out[4]) {
+  dequant_word(w, p, UnpackConsts{0x000F000Fu, 0x00F000F0u, 0x64006400u, 0x54005400u}, out);
 }
 
 __device__ __forceinline__ h8 pack_h8(const h2 v[4]) {

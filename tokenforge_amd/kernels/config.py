@@ -40,17 +40,23 @@ NUM_CUS = 256
 
 _WAVES = (1, 2, 4, 8, 16)
 
+# Compiled streaming variants: (block_m, row tiles RT, ring depth P, max waves). The wave cap
+# keeps each variant within the VGPR budget of its launch bound (no spills).
+GEMV_DOT_TEMPLATES: tuple[tuple[int, int, int, int], ...] = (
+    (1, 1, 2, 16), (1, 1, 4, 16), (1, 2, 2, 16), (1, 2, 4, 8), (1, 4, 2, 8), (1, 4, 3, 8),
+    (2, 1, 2, 16), (2, 2, 2, 8), (4, 1, 2, 8),
+)
+GEMV_MFMA_TEMPLATES: tuple[tuple[int, int, int, int], ...] = (
+    (16, 1, 2, 16), (16, 1, 4, 16), (16, 2, 2, 16), (16, 2, 3, 16), (16, 2, 4, 8), (16, 4, 2, 8),
+    (16, 4, 3, 8), (32, 1, 2, 16), (32, 2, 2, 8),
+)
+
 
 def _gemv_variants() -> list[tuple[str, int, int, int, int, int]]:
     out = []
-    dot = [(1, 1, 1), (1, 1, 2), (1, 1, 4), (1, 2, 1), (1, 2, 2), (1, 2, 4), (1, 4, 1), (1, 4, 2),
-           (2, 1, 1), (2, 1, 2), (2, 2, 1), (2, 2, 2), (4, 1, 1), (4, 1, 2), (4, 2, 1)]
-    for bm, rt, st in dot:
-        out += [("gemv_dot", bm, 16 * rt, 128, w, st) for w in _WAVES]
-    mfma = [(1, 1, 1), (1, 1, 2), (1, 1, 4), (1, 2, 1), (1, 2, 2), (1, 2, 4), (1, 4, 1), (1, 4, 2),
-            (2, 1, 1), (2, 1, 2), (2, 2, 1), (2, 2, 2)]
-    for mt, rt, st in mfma:
-        out += [("gemv_mfma", 16 * mt, 16 * rt, 128, w, st) for w in _WAVES]
+    for kernel, templates in (("gemv_dot", GEMV_DOT_TEMPLATES), ("gemv_mfma", GEMV_MFMA_TEMPLATES)):
+        for bm, rt, stages, max_waves in templates:
+            out += [(kernel, bm, 16 * rt, 128, w, stages) for w in _WAVES if w <= max_waves]
     return out
 
 
@@ -160,18 +166,19 @@ def _pow2_at_most(v: int, cap: int) -> int:
 def default_config(bucket: int, n: int, k: int, group_size: int) -> GemmConfig:
     """Heuristic config used before tuning (config.py:71-92, re-derived for 256 CUs).
 
-    Streaming kernels: one workgroup per 16 output columns; add waves (on-chip K slices)
-    until the grid holds about 8 waves per CU, never more waves than 128-wide K steps.
+    Streaming kernels: one workgroup per 32 output columns; add waves (on-chip K slices)
+    until the grid holds about 12 waves per CU, never more waves than 128-wide K steps.
     LDS GEMM: tile by M, then split K across workgroups until the grid covers the CUs.
     """
     if family_for_bucket(bucket) == "gemv":
-        mt = 1 if bucket <= 16 else 2
-        tiles = -(-n // 16)
+        bm = 16 if bucket <= 16 else 32
+        tiles = -(-n // 32)
         k_steps = max(1, -(-k // 128))
-        waves = _pow2_at_most(max(1, (8 * NUM_CUS) // tiles), min(16, k_steps))
-        if mt == 2:
+        waves = _pow2_at_most(max(1, -(-(12 * NUM_CUS) // tiles)), min(16, k_steps))
+        if bm == 32:
             waves = min(waves, 8)
-        return GemmConfig("gemv_mfma", 16 * mt, 16, 128, 1, waves, 2)
+        block_n = 32 if bm == 16 else 16
+        return GemmConfig("gemv_mfma", bm, block_n, 128, 1, waves, 2)
     block_k = 64 if group_size >= 64 else 32
     if bucket <= 64:
         bm, bn = 64, 64

@@ -37,9 +37,15 @@ def hip_runnable(t: torch.Tensor) -> bool:
 
 
 def gpu_identity(device: torch.device) -> str:
-    """Stable, filesystem-safe id of the device, e.g. ``amd-instinct-mi355x-gfx950``."""
+    """Stable, filesystem-safe id of the device, e.g. ``amd-gfx950-256cu`` for an MI355X.
+
+    Built from the architecture and the compute-unit count, which identify the kernel
+    tuning target. The marketing name is not used: ROCm reports it inconsistently (an
+    empty string under some profilers, a generic "AMD Radeon Graphics" elsewhere).
+    """
     if device.type != "cuda":
         return "cpu"
-    name = torch.cuda.get_device_name(device)
-    slug = re.sub(r"[^a-z0-9]+", "-", name.lower()).strip("-")
-    return f"{slug}-{device_arch(device)}"
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    cus = torch.cuda.get_device_properties(index).multi_processor_count
+    arch = re.sub(r"[^a-z0-9]+", "-", str(device_arch(device)).lower()).strip("-")
+    return f"amd-{arch}-{cus}cu"
