@@ -71,13 +71,14 @@ PATH_CONFIGS = [
     GemmConfig("gemv_dot", 1, 16, 128, 1, 1, 2),
     GemmConfig("gemv_dot", 1, 64, 128, 1, 4, 2),
     GemmConfig("gemv_dot", 1, 32, 128, 1, 8, 4),
-    GemmConfig("gemv_dot", 1, 64, 128, 1, 2, 3),
+    GemmConfig("gemv_mfma", 16, 16, 64, 1, 2, 2),
     GemmConfig("gemv_dot", 2, 32, 128, 1, 2, 2),
     GemmConfig("gemv_dot", 4, 16, 128, 1, 8, 2),
     GemmConfig("gemv_mfma", 16, 16, 128, 1, 1, 2),
     GemmConfig("gemv_mfma", 16, 16, 128, 1, 16, 4),
     GemmConfig("gemv_mfma", 16, 64, 128, 1, 8, 2),
-    GemmConfig("gemv_mfma", 16, 64, 128, 1, 4, 3),
+    GemmConfig("gemv_mfma", 16, 64, 64, 1, 4, 2),
+    GemmConfig("gemv_mfma", 32, 32, 64, 1, 4, 2),
     GemmConfig("gemv_mfma", 16, 32, 128, 1, 8, 4),
     GemmConfig("gemv_mfma", 32, 32, 128, 1, 4, 2),
     GemmConfig("gemm_mfma", 64, 64, 64, 1, 4, 2),

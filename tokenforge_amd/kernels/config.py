@@ -16,9 +16,9 @@ Field meaning per kernel family:
 kernel     block_m / block_n / block_k  split_k / num_warps / num_stages
 ========== =========================== ================================================
 gemv_dot   max M (1,2,4) / rows per     1 / waves per workgroup, each a K slice reduced
-           workgroup (16*RT) / 128      on chip / K steps in flight per wave
-gemv_mfma  M per tile (16,32) / rows    same as gemv_dot
-           per workgroup / 128
+           workgroup (16*RT) / 128      on chip / 128-wide K steps in flight per wave
+gemv_mfma  M per tile (16,32) / rows    same as gemv_dot; block_k 128 stages x in LDS,
+           per workgroup / 128 or 64    64 streams x from global memory
 gemm_mfma  LDS tile M / tile N / tile K K slices across workgroups (fp32 workspace,
                                         fixed-order reduce) / 4 waves / 2 LDS buffers
 ========== =========================== ================================================
@@ -40,23 +40,26 @@ NUM_CUS = 256
 
 _WAVES = (1, 2, 4, 8, 16)
 
-# Compiled streaming variants: (block_m, row tiles RT, ring depth P, max waves). The wave cap
-# keeps each variant within the VGPR budget of its launch bound (no spills).
-GEMV_DOT_TEMPLATES: tuple[tuple[int, int, int, int], ...] = (
-    (1, 1, 2, 16), (1, 1, 4, 16), (1, 2, 2, 16), (1, 2, 4, 8), (1, 4, 2, 8), (1, 4, 3, 8),
-    (2, 1, 2, 16), (2, 2, 2, 8), (4, 1, 2, 8),
-)
-GEMV_MFMA_TEMPLATES: tuple[tuple[int, int, int, int], ...] = (
-    (16, 1, 2, 16), (16, 1, 4, 16), (16, 2, 2, 16), (16, 2, 3, 16), (16, 2, 4, 8), (16, 4, 2, 8),
-    (16, 4, 3, 8), (32, 1, 2, 16), (32, 2, 2, 8),
+# Compiled streaming variants: (kernel, block_m, row tiles RT, block_k, ring depth P, max waves).
+# block_k = 128: x is staged in LDS once per wave; block_k = 64: x is streamed from global
+# memory with the weights (for M and K too large to stage). The wave cap keeps each variant
+# within the VGPR budget of its launch bound (no spills).
+GEMV_TEMPLATES: tuple[tuple[str, int, int, int, int, int], ...] = (
+    ("gemv_dot", 1, 1, 128, 2, 16), ("gemv_dot", 1, 1, 128, 4, 16), ("gemv_dot", 1, 1, 128, 8, 16),
+    ("gemv_dot", 1, 2, 128, 2, 16), ("gemv_dot", 1, 2, 128, 4, 8), ("gemv_dot", 1, 4, 128, 2, 8),
+    ("gemv_dot", 2, 1, 128, 2, 16), ("gemv_dot", 2, 2, 128, 2, 8), ("gemv_dot", 4, 1, 128, 2, 8),
+    ("gemv_mfma", 16, 1, 128, 2, 16), ("gemv_mfma", 16, 1, 128, 4, 16), ("gemv_mfma", 16, 1, 128, 8, 16),
+    ("gemv_mfma", 16, 2, 128, 2, 16), ("gemv_mfma", 16, 2, 128, 4, 16), ("gemv_mfma", 16, 4, 128, 2, 8),
+    ("gemv_mfma", 32, 1, 128, 2, 16), ("gemv_mfma", 32, 2, 128, 2, 8),
+    ("gemv_mfma", 16, 1, 64, 2, 16), ("gemv_mfma", 16, 2, 64, 2, 16), ("gemv_mfma", 16, 4, 64, 2, 8),
+    ("gemv_mfma", 32, 1, 64, 2, 16), ("gemv_mfma", 32, 2, 64, 2, 8),
 )
 
 
 def _gemv_variants() -> list[tuple[str, int, int, int, int, int]]:
     out = []
-    for kernel, templates in (("gemv_dot", GEMV_DOT_TEMPLATES), ("gemv_mfma", GEMV_MFMA_TEMPLATES)):
-        for bm, rt, stages, max_waves in templates:
-            out += [(kernel, bm, 16 * rt, 128, w, stages) for w in _WAVES if w <= max_waves]
+    for kernel, bm, rt, bk, stages, max_waves in GEMV_TEMPLATES:
+        out += [(kernel, bm, 16 * rt, bk, w, stages) for w in _WAVES if w <= max_waves]
     return out
 
 
@@ -178,7 +181,8 @@ def default_config(bucket: int, n: int, k: int, group_size: int) -> GemmConfig:
         if bm == 32:
             waves = min(waves, 8)
         block_n = 32 if bm == 16 else 16
-        return GemmConfig("gemv_mfma", bm, block_n, 128, 1, waves, 2)
+        block_k = 128 if bucket <= 4 else 64  # stage x in LDS only while it is small
+        return GemmConfig("gemv_mfma", bm, block_n, block_k, 1, waves, 2)
     block_k = 64 if group_size >= 64 else 32
     if bucket <= 64:
         bm, bn = 64, 64
