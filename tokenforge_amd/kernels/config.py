@@ -127,8 +127,8 @@ class GemmConfig:
             )
         if self.num_warps not in _WAVES:
             raise ValueError(f"num_warps={self.num_warps} must be a power of two <= 16")
-        if not 1 <= self.num_stages <= 4:
-            raise ValueError(f"num_stages={self.num_stages} must be in [1, 4]")
+        if not 1 <= self.num_stages <= 8:
+            raise ValueError(f"num_stages={self.num_stages} must be in [1, 8]")
         if self.variant() not in _VARIANT_SET:
             raise ValueError(f"{self.variant()} is not a compiled variant (block_m/block_n/block_k)")
 
