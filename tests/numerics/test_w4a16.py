@@ -114,6 +114,28 @@ def test_every_code_path(cfg: GemmConfig, with_bias: bool, device: torch.device)
         _assert_close(y, x, w, b)
 
 
+@pytest.mark.parametrize(
+    "cfg",
+    [
+        GemmConfig("gemv_mfma", 16, 64, 128, 1, 1, 2),
+        GemmConfig("gemv_mfma", 16, 32, 128, 1, 1, 4),
+        GemmConfig("gemv_mfma", 16, 64, 64, 1, 1, 2),
+        GemmConfig("gemv_dot", 1, 64, 128, 1, 1, 2),
+    ],
+    ids=_cfg_id,
+)
+def test_gemv_staging_windows(cfg: GemmConfig, device: torch.device) -> None:
+    """One wave over a long K with group 32: its dequantization operands (and x slice) exceed
+    the LDS, so the wave stages several windows. K = 8288 also ends in a partial 128-wide step."""
+    n, k, group = 200, 8288, 32
+    w = cases.layer_weights(n, k, 3, group)
+    wd = cases.on_device(w, device)
+    for m in _m_list(cfg):
+        x = cases.activations(m, k, 3)
+        y = w4a16_gemm(x.to(device), wd.qweight_t, wd.scales, wd.qzeros, group, cfg)
+        _assert_close(y, x, w)
+
+
 @pytest.mark.parametrize("group_size", [32, 64])
 def test_small_group_sizes(group_size: int, device: torch.device) -> None:
     n, k = 96, 384

@@ -31,9 +31,13 @@
 namespace tf {
 namespace {
 
+// K range [s0, s1) of 128-wide steps owned by `wave`; waves is a power of two (every compiled
+// variant's num_warps is). All arguments are wave-uniform, so the range and every loop bound
+// derived from it live in scalar registers.
 __device__ __forceinline__ void k_range(int wave, int waves, int nsteps, int* s0, int* s1) {
-  *s0 = (int)(((int64_t)wave * nsteps) / waves);
-  *s1 = (int)(((int64_t)(wave + 1) * nsteps) / waves);
+  const int sh = __builtin_ctz((unsigned)waves);
+  *s0 = (wave * nsteps) >> sh;
+  *s1 = ((wave + 1) * nsteps) >> sh;
 }
 
 // Buffer resources and per-launch constants shared by both kernels.
@@ -62,130 +66,156 @@ __device__ __forceinline__ Streams make_streams(const LinearArgs& a) {
   return s;
 }
 
-// Largest number of 128-wide K steps any wave gets, and the groups such a range can touch.
+// Largest number of 128-wide K steps any wave gets.
 __host__ __device__ __forceinline__ int max_steps(int nsteps, int waves) { return (nsteps + waves - 1) / waves; }
-__host__ __device__ __forceinline__ int max_groups(int steps, int log2g) {
-  // A range of `steps` steps starting at a multiple of 128 spans ceil(steps*128 / G) groups
-  // (G <= 128 divides 128).
-  return (steps * 128) >> log2g;
-}
 
-// Per-wave LDS staging area (in 32-bit words).
-struct WaveLds {
-  uint32_t* params;  // [groups_max][16*RT] x 3 words: fp16x2 (1024+z), (64+z), scale
-  _Float16* xs;      // [rows][xstride] x slice (XLDS variants)
-};
+// One staged (group, column) entry: fp16x2 (1024 + z), fp16x2 (64 + z), fp16x2 scale, unused;
+// four words so a lane fetches it with a single ds_read_b128.
+constexpr int kParamWords = 4;
 
-template <int RT>
-__device__ __forceinline__ int params_words(int groups_max) { return groups_max * 16 * RT * 3; }
-
-// Stage the dequantization operands of groups [g_lo, g_lo + ng) x columns [n_base, n_base+16RT)
-// into slots [0, slots). Slots past ng (the unused tail of a partial last step) get neutral
-// operands, zero point 0 and scale 0, so a zero weight word dequantizes to exactly 0 there.
-template <int RT>
-__device__ __forceinline__ void stage_params(uint32_t* p, const Streams& st, int n_base, int g_lo, int ng,
-                                             int slots, int lane) {
-  const int entries = slots * 16 * RT;
-  for (int e = lane; e < entries; e += 64) {
-    const int gi = e / (16 * RT);
-    const int col = e % (16 * RT);
-    const int n = n_base + col;
-    const bool ok = n < st.n && gi < ng;
-    const uint32_t grp = (uint32_t)(g_lo + gi);
-    const uint32_t sb = load_b16(st.sc, ok ? (grp * (uint32_t)st.n + (uint32_t)n) * 2u : kOutOfRange);
-    const uint32_t zw = load_b32(st.qz, ok ? (grp * (uint32_t)(st.n >> 3) + (uint32_t)(n >> 3)) * 4u : kOutOfRange);
-    const QuantParams q = make_params(zero_of(zw, (uint32_t)n), sb);
-    uint32_t* d = p + 3 * e;
-    d[0] = as_u32(q.zlo);
-    d[1] = as_u32(q.zhi);
-    d[2] = as_u32(q.s);
+// Stage one window of a wave's K range into its LDS region:
+//  * params: the dequantization operands of groups [g_lo, g_lo + ng) x columns
+//    [n_base, n_base + 16 RT), `slots` groups deep. Slots past ng get neutral operands (zero
+//    point 0, scale 0), so any word dequantizes to exactly 0 there.
+//  * x (rows > 0): x[m0 + r][k0, k0 + kn) for r < rows, row stride xstride halfs, zero at
+//    k >= K (buffer loads past the tensor return zeros only at its very end, so the K bound is
+//    explicit).
+// Each lane issues the loads of U entries of both kinds before any LDS write, so a batch of
+// 64 U entries costs one memory latency instead of one per entry.
+template <int RT, int U>
+__device__ __forceinline__ void stage_window(uint32_t* p, _Float16* xs, const LinearArgs& a, const Streams& st,
+                                             int n_base, int g_lo, int ng, int slots, int m0, int rows, int k0,
+                                             int kn, int xstride, int lane) {
+  constexpr int cols = 16 * RT;
+  const int pentries = slots * cols;
+  const int chunks = kn >> 3;  // 16-byte x chunks per row
+  const int xentries = rows * chunks;
+  const float inv_chunks = 1.0f / (float)(chunks > 0 ? chunks : 1);
+  const int total = max(pentries, xentries);
+  for (int base = 0; base < total; base += 64 * U) {
+    uint32_t sb[U], zw[U];
+    u4 xv[U];
+    int xr[U], xq[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int e = base + u * 64 + lane;
+      const int gi = e / cols;
+      const int n = n_base + e % cols;
+      const bool ok = e < pentries && n < st.n && gi < ng;
+      const uint32_t grp = (uint32_t)(g_lo + gi);
+      sb[u] = load_b16(st.sc, ok ? (grp * (uint32_t)st.n + (uint32_t)n) * 2u : kOutOfRange);
+      zw[u] = load_b32(st.qz, ok ? (grp * (uint32_t)(st.n >> 3) + (uint32_t)(n >> 3)) * 4u : kOutOfRange);
+      // e = r * chunks + q; the float quotient is off by at most one for e < 2^24.
+      int r = (int)((float)e * inv_chunks);
+      int q = e - r * chunks;
+      if (q < 0) {
+        r -= 1;
+        q += chunks;
+      } else if (q >= chunks) {
+        r += 1;
+        q -= chunks;
+      }
+      xr[u] = r;
+      xq[u] = q;
+      const int k = k0 + q * 8;
+      const bool xok = e < xentries && k < a.k;
+      xv[u] = load_b128(st.x, xok ? (uint32_t)((m0 + r) * a.ldx + k) * 2u : kOutOfRange);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int e = base + u * 64 + lane;
+      if (e < pentries) {
+        const int n = n_base + e % cols;
+        const QuantParams q = make_params(zero_of(zw[u], (uint32_t)n), sb[u]);
+        *reinterpret_cast<u4*>(p + kParamWords * e) = u4{as_u32(q.zlo), as_u32(q.zhi), as_u32(q.s), 0u};
+      }
+      if (e < xentries) *reinterpret_cast<u4*>(xs + xr[u] * xstride + xq[u] * 8) = xv[u];
+    }
   }
 }
 
-__device__ __forceinline__ QuantParams read_params(const uint32_t* p, int gi, int col, int cols) {
-  const uint32_t* d = p + 3 * (gi * cols + col);
+__device__ __forceinline__ QuantParams read_params(const uint32_t* p) {
+  const u4 v = *reinterpret_cast<const u4*>(p);
   QuantParams q;
-  q.zlo = as_h2(d[0]);
-  q.zhi = as_h2(d[1]);
-  q.s = as_h2(d[2]);
+  q.zlo = as_h2(v[0]);
+  q.zhi = as_h2(v[1]);
+  q.s = as_h2(v[2]);
   return q;
 }
 
-// Stage x[m0 + r][k0 .. k0 + kn) for r < rows into xs (row stride xstride halfs); values at
-// k >= K are zero (buffer loads past the tensor return zeros only at its very end, so the
-// K bound is explicit).
-__device__ __forceinline__ void stage_x(_Float16* xs, const LinearArgs& a, const Streams& st, int m0, int rows,
-                                        int k0, int kn, int xstride, int lane) {
-  const int chunks = kn >> 3;  // 16-byte chunks per row
-  for (int e = lane; e < rows * chunks; e += 64) {
-    const int r = e / chunks;
-    const int q = e % chunks;
-    const int k = k0 + q * 8;
-    const uint32_t off = (k < a.k) ? (uint32_t)(((int64_t)(m0 + r) * a.ldx + k) * 2) : kOutOfRange;
-    *reinterpret_cast<u4*>(xs + r * xstride + q * 8) = load_b128(st.x, off);
-  }
-}
-
-// Weights of one step for RT row tiles.
+// Per-lane view of the weight stream: the lane reads 16 bytes (chunk g = 32 K values) of one
+// row per row tile and step. off[rt] is the byte offset of that run in step 0 (kOutOfRange
+// past N, and still out of range after adding any step offset); lane_end is the first step
+// whose chunk lies past K for this lane or past the wave's range.
 template <int RT>
-struct WeightSlot {
-  u4 w[RT];
+struct LaneStream {
+  uint32_t off[RT];
+  int lane_end;
+
+  __device__ __forceinline__ LaneStream(const Streams& st, int n0, int g, int s1) {
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      const int n = n0 + rt * 16;
+      off[rt] = n < st.n ? (uint32_t)n * st.row_bytes + (uint32_t)g * 16u : kOutOfRange;
+    }
+    lane_end = min(s1, (st.nchunks - g + 3) >> 2);
+  }
+
+  // Every call issues exactly RT loads (zeros when the step is out of range), so the ring
+  // below has the same loads in flight on every path and the compiler's vmcnt waits stay
+  // exact instead of draining the ring.
+  __device__ __forceinline__ void issue(u4 (&w)[RT], const Streams& st, int step) const {
+    const bool v = step < lane_end;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) w[rt] = load_b128(st.qw, v ? off[rt] + (uint32_t)step * 64u : kOutOfRange);
+  }
 };
 
-template <int RT>
-__device__ __forceinline__ void issue_weights(WeightSlot<RT>& slot, const Streams& st, const uint32_t* row_off,
-                                              int ch, bool kvalid) {
-#pragma unroll
-  for (int rt = 0; rt < RT; ++rt) {
-    const uint32_t wo = (kvalid && row_off[rt] != kOutOfRange) ? row_off[rt] + (uint32_t)ch * 16u : kOutOfRange;
-    slot.w[rt] = load_b128(st.qw, wo);
-  }
+// LDS carve-up of one launch. Each wave stages a window of `win` steps: its params for the
+// window's groups and (XLDS) the window's x slice; a wave whose range is longer re-stages per
+// window. When a range takes several windows, each holds a multiple of the ring depth, so ring
+// slot p always holds a step with (step - s0) % P == p.
+struct GemvLds {
+  int pwords;      // params words per wave
+  int xstride;     // halfs per staged x row
+  int wave_words;  // params + x words per wave
+};
+
+__host__ __device__ __forceinline__ GemvLds gemv_lds_layout(int win, int log2g, int cols, int x_rows) {
+  GemvLds l;
+  l.pwords = win * (128 >> log2g) * cols * kParamWords;
+  l.xstride = win * 128 + 8;
+  l.wave_words = l.pwords + (x_rows * l.xstride) / 2;
+  return l;
 }
 
 // ------------------------------------------------------------------------ gemv_dot
 
-template <int MAXM, int RT>
-struct DotSlot {
-  WeightSlot<RT> wt;
-};
-
 template <int MAXM, int RT, int P, int MAXW>
-__global__ __launch_bounds__(MAXW * 64) void gemv_dot_kernel(LinearArgs a) {
+__global__ __launch_bounds__(MAXW * 64) void gemv_dot_kernel(LinearArgs a, int win) {
   extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int waves = blockDim.x >> 6;
   const int g = lane & 3;
   const int c = lane >> 2;
-  const int n_base = blockIdx.x * 16 * RT;
+  constexpr int cols = 16 * RT;
+  const int n_base = blockIdx.x * cols;
   const Streams st = make_streams(a);
   int s0, s1;
   k_range(wave, waves, st.nsteps, &s0, &s1);
-  const int steps_max = max_steps(st.nsteps, waves);
-  const int groups_max = max_groups(steps_max, st.log2g);
+  const int gps = 128 >> st.log2g;
   const int xrows = a.m < MAXM ? a.m : MAXM;
-  const int xstride = steps_max * 128 + 8;
-  const int wave_words = params_words<RT>(groups_max) + (xrows * xstride) / 2;
-  uint32_t* my = lds + wave * wave_words;
-  uint32_t* prm = my;
-  _Float16* xs = reinterpret_cast<_Float16*>(my + params_words<RT>(groups_max));
+  const GemvLds L = gemv_lds_layout(win, st.log2g, cols, xrows);
+  uint32_t* prm = lds + wave * L.wave_words;
+  _Float16* xs = reinterpret_cast<_Float16*>(prm + L.pwords);
   const UnpackConsts uc = unpack_consts();
-  const int g_lo = (s0 * 128) >> st.log2g;
-  const int g_hi = min(st.groups, ((s1 * 128) >> st.log2g));
+  const LaneStream<RT> ls_w(st, n_base + c, g, s1);
 
-  stage_params<RT>(prm, st, n_base, g_lo, g_hi - g_lo, groups_max, lane);
-  stage_x(xs, a, st, 0, xrows, s0 * 128, (s1 - s0) * 128, xstride, lane);
-
-  uint32_t row_off[RT];
-#pragma unroll
-  for (int rt = 0; rt < RT; ++rt) {
-    const int n = n_base + rt * 16 + c;
-    row_off[rt] = n < a.n ? (uint32_t)n * st.row_bytes : kOutOfRange;
-  }
-  auto issue = [&](DotSlot<MAXM, RT>& slot, int step) {
-    const int ch = step * 4 + g;
-    issue_weights<RT>(slot.wt, st, row_off, ch, step < s1 && ch < st.nchunks);
-  };
+  // Lane bases in LDS; a step adds a wave-uniform offset.
+  const uint32_t* plane = prm + kParamWords * ((((g * 32) >> st.log2g) * cols) + c);
+  const int pstep = kParamWords * gps * cols;
+  const _Float16* xl = xs + g * 32;
 
   float acc[MAXM][RT];
 #pragma unroll
@@ -193,39 +223,49 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_dot_kernel(LinearArgs a) {
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) acc[m][rt] = 0.0f;
 
-  DotSlot<MAXM, RT> ring[P];
+  u4 ring[P][RT];
 #pragma unroll
-  for (int p = 0; p < P; ++p) issue(ring[p], s0 + p);
+  for (int p = 0; p < P; ++p) {
+    ls_w.issue(ring[p], st, s0 + p);
+    __builtin_amdgcn_sched_barrier(0);  // keep slot order: slot 0 must be the oldest load
+  }
 
-  for (int s = s0; s < s1; s += P) {
+  for (int w0 = s0; w0 < s1; w0 += win) {
+    const int w1 = min(s1, w0 + win);
+    const int g_lo = (w0 * 128) >> st.log2g;
+    const int ng = min(st.groups, (w1 * 128) >> st.log2g) - g_lo;
+    stage_window<RT, 2>(prm, xs, a, st, n_base, g_lo, ng, win * gps, 0, xrows, w0 * 128, (w1 - w0) * 128,
+                        L.xstride, lane);
+    for (int s = w0; s < w1; s += P) {
 #pragma unroll
-    for (int p = 0; p < P; ++p) {
-      if (s + p < s1) {
-        DotSlot<MAXM, RT>& slot = ring[p];
-        const int local = (s + p - s0) * 128 + g * 32;  // this lane's K offset inside the slice
-        const int gi = (((s + p) * 128 + g * 32) >> st.log2g) - g_lo;
-        u4 xv[MAXM][4];
+      for (int p = 0; p < P; ++p) {
+        const int step = s + p;
+        if (step < w1) {
+          const int ls = step - w0;
+          u4 xv[MAXM][4];
 #pragma unroll
-        for (int m = 0; m < MAXM; ++m) {
-          const int row = m < xrows ? m : 0;  // rows past M only feed accumulators never stored
+          for (int m = 0; m < MAXM; ++m) {
+            const int row = m < xrows ? m : 0;  // rows past M only feed accumulators never stored
 #pragma unroll
-          for (int j = 0; j < 4; ++j) xv[m][j] = *reinterpret_cast<const u4*>(xs + row * xstride + local + j * 8);
-        }
+            for (int j = 0; j < 4; ++j)
+              xv[m][j] = *reinterpret_cast<const u4*>(xl + row * L.xstride + ls * 128 + j * 8);
+          }
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) {
-          const QuantParams qp = read_params(prm, gi, rt * 16 + c, 16 * RT);
+          for (int rt = 0; rt < RT; ++rt) {
+            const QuantParams qp = read_params(plane + ls * pstep + rt * 16 * kParamWords);
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            h2 wd[4];
-            dequant_word(slot.wt.w[rt][j], qp, uc, wd);
+            for (int j = 0; j < 4; ++j) {
+              h2 wd[4];
+              dequant_word(ring[p][rt][j], qp, uc, wd);
 #pragma unroll
-            for (int m = 0; m < MAXM; ++m)
+              for (int m = 0; m < MAXM; ++m)
 #pragma unroll
-              for (int i = 0; i < 4; ++i)
-                acc[m][rt] = __builtin_amdgcn_fdot2(as_h2(xv[m][j][i]), wd[i], acc[m][rt], false);
+                for (int i = 0; i < 4; ++i)
+                  acc[m][rt] = __builtin_amdgcn_fdot2(as_h2(xv[m][j][i]), wd[i], acc[m][rt], false);
+            }
           }
         }
-        issue(slot, s + p + P);
+        ls_w.issue(ring[p], st, step + P);
       }
     }
   }
@@ -236,7 +276,7 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_dot_kernel(LinearArgs a) {
     for (int rt = 0; rt < RT; ++rt) acc[m][rt] = quad_sum(acc[m][rt]);
 
   if (waves > 1) {
-    float* red = reinterpret_cast<float*>(lds + waves * wave_words);  // [(waves - 1)][MAXM][RT][16]
+    float* red = reinterpret_cast<float*>(lds + waves * L.wave_words);  // [(waves - 1)][MAXM][RT][16]
     if (wave > 0 && g == 0) {
 #pragma unroll
       for (int m = 0; m < MAXM; ++m)
@@ -269,62 +309,44 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_dot_kernel(LinearArgs a) {
 
 // ------------------------------------------------------------------------ gemv_mfma
 
-template <int MT, int RT, bool XLDS>
-struct MfmaSlot {
-  WeightSlot<RT> wt;
-  h8 x[XLDS ? 1 : MT][XLDS ? 1 : 4];  // A operand from global when x is not staged
-};
-
 template <int MT, int RT, int P, int MAXW, bool XLDS>
-__global__ __launch_bounds__(MAXW * 64) void gemv_mfma_kernel(LinearArgs a) {
+__global__ __launch_bounds__(MAXW * 64) void gemv_mfma_kernel(LinearArgs a, int win) {
   extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int waves = blockDim.x >> 6;
   const int c = lane & 15;
   const int g = lane >> 4;
-  const int n_base = blockIdx.x * 16 * RT;
+  constexpr int cols = 16 * RT;
+  const int n_base = blockIdx.x * cols;
   const int m_base = blockIdx.y * 16 * MT;
   const Streams st = make_streams(a);
   int s0, s1;
   k_range(wave, waves, st.nsteps, &s0, &s1);
-  const int steps_max = max_steps(st.nsteps, waves);
-  const int groups_max = max_groups(steps_max, st.log2g);
-  const int xrows = min(16 * MT, a.m - m_base);   // rows staged by this workgroup
-  const int xalloc = min(16 * MT, a.m);           // rows allocated per wave (same in every workgroup)
-  const int xstride = steps_max * 128 + 8;
-  const int wave_words = params_words<RT>(groups_max) + (XLDS ? (xalloc * xstride) / 2 : 0);
-  uint32_t* my = lds + wave * wave_words;
-  uint32_t* prm = my;
-  _Float16* xs = reinterpret_cast<_Float16*>(my + params_words<RT>(groups_max));
+  const int gps = 128 >> st.log2g;
+  const int xrows = min(16 * MT, a.m - m_base);  // rows staged by this workgroup
+  const int xalloc = min(16 * MT, a.m);          // rows allocated per wave (same in every workgroup)
+  const GemvLds L = gemv_lds_layout(win, st.log2g, cols, XLDS ? xalloc : 0);
+  uint32_t* prm = lds + wave * L.wave_words;
+  _Float16* xs = reinterpret_cast<_Float16*>(prm + L.pwords);
   const UnpackConsts uc = unpack_consts();
-  const int g_lo = (s0 * 128) >> st.log2g;
-  const int g_hi = min(st.groups, ((s1 * 128) >> st.log2g));
+  const LaneStream<RT> ls_w(st, n_base + c, g, s1);
 
-  stage_params<RT>(prm, st, n_base, g_lo, g_hi - g_lo, groups_max, lane);
-  if (XLDS) stage_x(xs, a, st, m_base, xrows, s0 * 128, (s1 - s0) * 128, xstride, lane);
-
-  uint32_t row_off[RT];
+  const uint32_t* plane = prm + kParamWords * ((((g * 32) >> st.log2g) * cols) + c);
+  const int pstep = kParamWords * gps * cols;
+  const _Float16* xl[MT];
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt) {
-    const int n = n_base + rt * 16 + c;
-    row_off[rt] = n < a.n ? (uint32_t)n * st.row_bytes : kOutOfRange;
+  for (int mt = 0; mt < MT; ++mt) {
+    const int r = mt * 16 + c;
+    xl[mt] = xs + (r < xrows ? r : 0) * L.xstride + g * 32;  // rows past M feed discarded outputs
   }
-  auto issue = [&](MfmaSlot<MT, RT, XLDS>& slot, int step) {
-    const int ch = step * 4 + g;
-    const bool kvalid = step < s1 && ch < st.nchunks;
-    issue_weights<RT>(slot.wt, st, row_off, ch, kvalid);
-    if (!XLDS) {
+  // x streamed with the weights (block_k 64 variants): 64 bytes of row m per lane and step.
+  uint32_t xoff[MT];
 #pragma unroll
-      for (int mt = 0; mt < (XLDS ? 0 : MT); ++mt) {
-        const int m = m_base + mt * 16 + c;
-        const uint32_t xo = (kvalid && m < a.m) ? (uint32_t)(((int64_t)m * a.ldx + ch * 32) * 2) : kOutOfRange;
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          slot.x[XLDS ? 0 : mt][XLDS ? 0 : j] = __builtin_bit_cast(h8, load_b128(st.x, xo + 16u * j));
-      }
-    }
-  };
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = m_base + mt * 16 + c;
+    xoff[mt] = m < a.m ? (uint32_t)(((int64_t)m * a.ldx + g * 32) * 2) : kOutOfRange;
+  }
 
   f4 acc[MT][RT];
 #pragma unroll
@@ -332,52 +354,66 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_mfma_kernel(LinearArgs a) {
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) acc[mt][rt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  MfmaSlot<MT, RT, XLDS> ring[P];
+  u4 ring[P][RT];
+  u4 xring[XLDS ? 1 : P][XLDS ? 1 : MT][4];
+  auto issue = [&](int p, int step) {
+    ls_w.issue(ring[p], st, step);
+    if (!XLDS) {
+      const bool v = step < ls_w.lane_end;
 #pragma unroll
-  for (int p = 0; p < P; ++p) issue(ring[p], s0 + p);
+      for (int mt = 0; mt < (XLDS ? 0 : MT); ++mt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          xring[XLDS ? 0 : p][mt][j] =
+              load_b128(st.x, v ? xoff[mt] + (uint32_t)step * 256u + 16u * j : kOutOfRange);
+    }
+  };
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    issue(p, s0 + p);
+    __builtin_amdgcn_sched_barrier(0);  // keep slot order: slot 0 must be the oldest load
+  }
 
-  for (int s = s0; s < s1; s += P) {
+  for (int w0 = s0; w0 < s1; w0 += win) {
+    const int w1 = min(s1, w0 + win);
+    const int g_lo = (w0 * 128) >> st.log2g;
+    const int ng = min(st.groups, (w1 * 128) >> st.log2g) - g_lo;
+    stage_window<RT, 2>(prm, xs, a, st, n_base, g_lo, ng, win * gps, m_base, XLDS ? xrows : 0, w0 * 128,
+                        (w1 - w0) * 128, L.xstride, lane);
+    for (int s = w0; s < w1; s += P) {
 #pragma unroll
-    for (int p = 0; p < P; ++p) {
-      if (s + p < s1) {
-        MfmaSlot<MT, RT, XLDS>& slot = ring[p];
-        const int local = (s + p - s0) * 128 + g * 32;
-        const int gi = (((s + p) * 128 + g * 32) >> st.log2g) - g_lo;
-        h8 xa[MT][4];
-        if (XLDS) {
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt) {
-            const int r = mt * 16 + c;
-            const int row = r < xrows ? r : 0;  // rows past M feed discarded outputs
-#pragma unroll
-            for (int j = 0; j < 4; ++j) xa[mt][j] = *reinterpret_cast<const h8*>(xs + row * xstride + local + j * 8);
-          }
-        } else {
+      for (int p = 0; p < P; ++p) {
+        const int step = s + p;
+        if (step < w1) {
+          const int ls = step - w0;
+          h8 xa[MT][4];
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) xa[mt][j] = slot.x[XLDS ? 0 : mt][XLDS ? 0 : j];
-        }
+            for (int j = 0; j < 4; ++j)
+              xa[mt][j] = XLDS ? *reinterpret_cast<const h8*>(xl[mt] + ls * 128 + j * 8)
+                               : __builtin_bit_cast(h8, xring[XLDS ? 0 : p][mt][j]);
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) {
-          const QuantParams qp = read_params(prm, gi, rt * 16 + c, 16 * RT);
+          for (int rt = 0; rt < RT; ++rt) {
+            const QuantParams qp = read_params(plane + ls * pstep + rt * 16 * kParamWords);
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            h2 wd[4];
-            dequant_word(slot.wt.w[rt][j], qp, uc, wd);
-            const h8 b = pack_h8(wd);
+            for (int j = 0; j < 4; ++j) {
+              h2 wd[4];
+              dequant_word(ring[p][rt][j], qp, uc, wd);
+              const h8 b = pack_h8(wd);
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-              acc[mt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[mt][j], b, acc[mt][rt], 0, 0, 0);
+              for (int mt = 0; mt < MT; ++mt)
+                acc[mt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[mt][j], b, acc[mt][rt], 0, 0, 0);
+            }
           }
         }
-        issue(slot, s + p + P);
+        issue(p, step + P);
       }
     }
   }
 
   if (waves > 1) {
-    float* red = reinterpret_cast<float*>(lds + waves * wave_words);  // [(waves - 1)][MT][RT][64][4]
+    float* red = reinterpret_cast<float*>(lds + waves * L.wave_words);  // [(waves - 1)][MT][RT][64][4]
     if (wave > 0) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
@@ -436,9 +472,6 @@ size_t device_max_lds() {
 // Dynamic LDS above 64 KiB must be enabled per kernel before the launch.
 template <typename Kernel>
 int reserve_lds(Kernel kernel, size_t bytes, const char* name) {
-  if (bytes > device_max_lds())
-    return fail(TF_EINVAL, std::string("tf_w4a16_linear: ") + name +
-                               " variant needs more LDS than the device has for this K; use more waves");
   if (bytes > 64 * 1024 &&
       hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
                           (int)bytes) != hipSuccess)
@@ -455,13 +488,27 @@ int check_offsets(const LinearArgs& a) {
   return TF_OK;
 }
 
-// LDS bytes of a gemv launch: per-wave staging plus the cross-wave reduction buffer.
-size_t gemv_lds(const LinearArgs& a, int waves, int rt, int x_rows, size_t red_per_wave) {
+// Staging window (in steps) and LDS bytes of a gemv launch. The window covers a wave's whole
+// K range when that fits the device's LDS (one window, so its length is free); otherwise it is
+// the largest multiple of the ring depth that fits. win = 0 when not even one ring's worth fits.
+struct GemvPlan {
+  int win;
+  size_t lds;
+};
+
+GemvPlan plan_gemv(const LinearArgs& a, int waves, int rt, int depth, int x_rows, size_t red_per_wave) {
   const int nsteps = ((a.k >> 5) + 3) >> 2;
   const int steps = max_steps(nsteps, waves);
-  const int groups = max_groups(steps, a.log2g);
-  const size_t words = (size_t)groups * 16 * rt * 3 + (size_t)(x_rows * (steps * 128 + 8)) / 2;
-  return (size_t)waves * words * 4 + (size_t)(waves - 1) * red_per_wave;
+  const size_t cap = device_max_lds();
+  auto bytes = [&](int win) {
+    const GemvLds l = gemv_lds_layout(win, a.log2g, 16 * rt, x_rows);
+    return (size_t)waves * (size_t)l.wave_words * 4 + (size_t)(waves - 1) * red_per_wave;
+  };
+  if (bytes(steps) <= cap) return GemvPlan{steps, bytes(steps)};
+  int win = (steps - 1) / depth * depth;
+  while (win > depth && bytes(win) > cap) win -= depth;
+  if (win < depth || bytes(win) > cap) return GemvPlan{0, 0};
+  return GemvPlan{win, bytes(win)};
 }
 
 template <int MAXM, int RT, int P, int MAXW>
@@ -469,10 +516,11 @@ int launch_dot(const LinearArgs& a, const tf_gemm_config& cfg, float*, hipStream
   if (a.m > MAXM) return fail(TF_EINVAL, "tf_w4a16_linear: gemv_dot variant needs m <= block_m");
   if (int rc = check_offsets(a)) return rc;
   const int waves = cfg.num_warps;
-  const size_t lds = gemv_lds(a, waves, RT, a.m < MAXM ? a.m : MAXM, (size_t)MAXM * RT * 16 * sizeof(float));
-  if (int rc = reserve_lds(gemv_dot_kernel<MAXM, RT, P, MAXW>, lds, "gemv_dot")) return rc;
+  const GemvPlan plan = plan_gemv(a, waves, RT, P, a.m < MAXM ? a.m : MAXM, (size_t)MAXM * RT * 16 * sizeof(float));
+  if (plan.win == 0) return fail(TF_EINVAL, "tf_w4a16_linear: gemv_dot variant does not fit the device's LDS");
+  if (int rc = reserve_lds(gemv_dot_kernel<MAXM, RT, P, MAXW>, plan.lds, "gemv_dot")) return rc;
   const dim3 grid((unsigned)cdiv(a.n, 16 * RT));
-  gemv_dot_kernel<MAXM, RT, P, MAXW><<<grid, waves * 64, lds, stream>>>(a);
+  gemv_dot_kernel<MAXM, RT, P, MAXW><<<grid, waves * 64, plan.lds, stream>>>(a, plan.win);
   return check_launch("tf_w4a16_linear(gemv_dot)");
 }
 
@@ -480,11 +528,12 @@ template <int MT, int RT, int P, int MAXW, bool XLDS>
 int launch_mfma(const LinearArgs& a, const tf_gemm_config& cfg, float*, hipStream_t stream) {
   if (int rc = check_offsets(a)) return rc;
   const int waves = cfg.num_warps;
-  const size_t lds = gemv_lds(a, waves, RT, XLDS ? (a.m < 16 * MT ? a.m : 16 * MT) : 0,
-                              (size_t)MT * RT * 64 * 4 * sizeof(float));
-  if (int rc = reserve_lds(gemv_mfma_kernel<MT, RT, P, MAXW, XLDS>, lds, "gemv_mfma")) return rc;
+  const GemvPlan plan = plan_gemv(a, waves, RT, P, XLDS ? (a.m < 16 * MT ? a.m : 16 * MT) : 0,
+                                  (size_t)MT * RT * 64 * 4 * sizeof(float));
+  if (plan.win == 0) return fail(TF_EINVAL, "tf_w4a16_linear: gemv_mfma variant does not fit the device's LDS");
+  if (int rc = reserve_lds(gemv_mfma_kernel<MT, RT, P, MAXW, XLDS>, plan.lds, "gemv_mfma")) return rc;
   const dim3 grid((unsigned)cdiv(a.n, 16 * RT), (unsigned)cdiv(a.m, 16 * MT));
-  gemv_mfma_kernel<MT, RT, P, MAXW, XLDS><<<grid, waves * 64, lds, stream>>>(a);
+  gemv_mfma_kernel<MT, RT, P, MAXW, XLDS><<<grid, waves * 64, plan.lds, stream>>>(a, plan.win);
   return check_launch("tf_w4a16_linear(gemv_mfma)");
 }
 
