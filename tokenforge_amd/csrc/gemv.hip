@@ -73,64 +73,104 @@ __host__ __device__ __forceinline__ int max_steps(int nsteps, int waves) { retur
 // four words so a lane fetches it with a single ds_read_b128.
 constexpr int kParamWords = 4;
 
-// Stage one window of a wave's K range into its LDS region:
+// Staging of one window of a wave's K range into its LDS region:
 //  * params: the dequantization operands of groups [g_lo, g_lo + ng) x columns
 //    [n_base, n_base + 16 RT), `slots` groups deep. Slots past ng get neutral operands (zero
 //    point 0, scale 0), so any word dequantizes to exactly 0 there.
 //  * x (rows > 0): x[m0 + r][k0, k0 + kn) for r < rows, row stride xstride halfs, zero at
 //    k >= K (buffer loads past the tensor return zeros only at its very end, so the K bound is
 //    explicit).
-// Each lane issues the loads of U entries of both kinds before any LDS write, so a batch of
-// 64 U entries costs one memory latency instead of one per entry.
+// Work is split into batches of 64 U entries of each kind: load_batch issues a batch's loads
+// into registers, store_batch writes them to LDS, so a batch costs one memory latency and the
+// first batch can be issued ahead of the weight ring.
+struct Window {
+  int n_base, g_lo, ng, pentries;
+  int m0, rows, k0, chunks, xentries, xstride;
+  float inv_chunks;
+  int total;  // max(pentries, xentries)
+};
+
+template <int RT>
+__device__ __forceinline__ Window make_window(const Streams& st, int n_base, int w0, int w1, int slots, int m0,
+                                              int rows, int xstride) {
+  Window w;
+  w.n_base = n_base;
+  w.g_lo = (w0 * 128) >> st.log2g;
+  w.ng = min(st.groups, (w1 * 128) >> st.log2g) - w.g_lo;
+  w.pentries = w1 > w0 ? slots * 16 * RT : 0;
+  w.m0 = m0;
+  w.rows = rows;
+  w.k0 = w0 * 128;
+  w.chunks = (w1 - w0) * 16;  // 16-byte x chunks per row
+  w.xentries = rows * w.chunks;
+  w.xstride = xstride;
+  w.inv_chunks = 1.0f / (float)(w.chunks > 0 ? w.chunks : 1);
+  w.total = max(w.pentries, w.xentries);
+  return w;
+}
+
+template <int U>
+struct StageBatch {
+  uint32_t sb[U], zw[U];
+  u4 xv[U];
+  int xr[U], xq[U];
+};
+
 template <int RT, int U>
-__device__ __forceinline__ void stage_window(uint32_t* p, _Float16* xs, const LinearArgs& a, const Streams& st,
-                                             int n_base, int g_lo, int ng, int slots, int m0, int rows, int k0,
-                                             int kn, int xstride, int lane) {
+__device__ __forceinline__ void load_batch(StageBatch<U>& b, const Window& w, const LinearArgs& a,
+                                           const Streams& st, int base, int lane) {
   constexpr int cols = 16 * RT;
-  const int pentries = slots * cols;
-  const int chunks = kn >> 3;  // 16-byte x chunks per row
-  const int xentries = rows * chunks;
-  const float inv_chunks = 1.0f / (float)(chunks > 0 ? chunks : 1);
-  const int total = max(pentries, xentries);
-  for (int base = 0; base < total; base += 64 * U) {
-    uint32_t sb[U], zw[U];
-    u4 xv[U];
-    int xr[U], xq[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int e = base + u * 64 + lane;
-      const int gi = e / cols;
-      const int n = n_base + e % cols;
-      const bool ok = e < pentries && n < st.n && gi < ng;
-      const uint32_t grp = (uint32_t)(g_lo + gi);
-      sb[u] = load_b16(st.sc, ok ? (grp * (uint32_t)st.n + (uint32_t)n) * 2u : kOutOfRange);
-      zw[u] = load_b32(st.qz, ok ? (grp * (uint32_t)(st.n >> 3) + (uint32_t)(n >> 3)) * 4u : kOutOfRange);
-      // e = r * chunks + q; the float quotient is off by at most one for e < 2^24.
-      int r = (int)((float)e * inv_chunks);
-      int q = e - r * chunks;
-      if (q < 0) {
-        r -= 1;
-        q += chunks;
-      } else if (q >= chunks) {
-        r += 1;
-        q -= chunks;
-      }
-      xr[u] = r;
-      xq[u] = q;
-      const int k = k0 + q * 8;
-      const bool xok = e < xentries && k < a.k;
-      xv[u] = load_b128(st.x, xok ? (uint32_t)((m0 + r) * a.ldx + k) * 2u : kOutOfRange);
+  for (int u = 0; u < U; ++u) {
+    const int e = base + u * 64 + lane;
+    const int gi = e / cols;
+    const int n = w.n_base + e % cols;
+    const bool ok = e < w.pentries && n < st.n && gi < w.ng;
+    const uint32_t grp = (uint32_t)(w.g_lo + gi);
+    b.sb[u] = load_b16(st.sc, ok ? (grp * (uint32_t)st.n + (uint32_t)n) * 2u : kOutOfRange);
+    b.zw[u] = load_b32(st.qz, ok ? (grp * (uint32_t)(st.n >> 3) + (uint32_t)(n >> 3)) * 4u : kOutOfRange);
+    // e = r * chunks + q; the float quotient is off by at most one for e < 2^24.
+    int r = (int)((float)e * w.inv_chunks);
+    int q = e - r * w.chunks;
+    if (q < 0) {
+      r -= 1;
+      q += w.chunks;
+    } else if (q >= w.chunks) {
+      r += 1;
+      q -= w.chunks;
     }
+    b.xr[u] = r;
+    b.xq[u] = q;
+    const int k = w.k0 + q * 8;
+    const bool xok = e < w.xentries && k < a.k;
+    b.xv[u] = load_b128(st.x, xok ? (uint32_t)((w.m0 + r) * a.ldx + k) * 2u : kOutOfRange);
+  }
+}
+
+template <int RT, int U>
+__device__ __forceinline__ void store_batch(uint32_t* p, _Float16* xs, const StageBatch<U>& b, const Window& w,
+                                            int base, int lane) {
+  constexpr int cols = 16 * RT;
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int e = base + u * 64 + lane;
-      if (e < pentries) {
-        const int n = n_base + e % cols;
-        const QuantParams q = make_params(zero_of(zw[u], (uint32_t)n), sb[u]);
-        *reinterpret_cast<u4*>(p + kParamWords * e) = u4{as_u32(q.zlo), as_u32(q.zhi), as_u32(q.s), 0u};
-      }
-      if (e < xentries) *reinterpret_cast<u4*>(xs + xr[u] * xstride + xq[u] * 8) = xv[u];
+  for (int u = 0; u < U; ++u) {
+    const int e = base + u * 64 + lane;
+    if (e < w.pentries) {
+      const int n = w.n_base + e % cols;
+      const QuantParams q = make_params(zero_of(b.zw[u], (uint32_t)n), b.sb[u]);
+      *reinterpret_cast<u4*>(p + kParamWords * e) = u4{as_u32(q.zlo), as_u32(q.zhi), as_u32(q.s), 0u};
     }
+    if (e < w.xentries) *reinterpret_cast<u4*>(xs + b.xr[u] * w.xstride + b.xq[u] * 8) = b.xv[u];
+  }
+}
+
+// Stage the batches of a window from `first` on.
+template <int RT, int U>
+__device__ __forceinline__ void stage_rest(uint32_t* p, _Float16* xs, const Window& w, const LinearArgs& a,
+                                           const Streams& st, int first, int lane) {
+  for (int base = first; base < w.total; base += 64 * U) {
+    StageBatch<U> b;
+    load_batch<RT, U>(b, w, a, st, base, lane);
+    store_batch<RT, U>(p, xs, b, w, base, lane);
   }
 }
 
@@ -191,6 +231,8 @@ __host__ __device__ __forceinline__ GemvLds gemv_lds_layout(int win, int log2g, 
 
 // ------------------------------------------------------------------------ gemv_dot
 
+constexpr int kStageU = 2;  // staging entries per lane and batch
+
 template <int MAXM, int RT, int P, int MAXW>
 __global__ __launch_bounds__(MAXW * 64) void gemv_dot_kernel(LinearArgs a, int win) {
   extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
@@ -223,19 +265,25 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_dot_kernel(LinearArgs a, int w
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) acc[m][rt] = 0.0f;
 
+  // The first staging batch goes out ahead of the weight ring: every wave of the grid issues
+  // its ring at once, and the operands that gate the first step must not queue behind it.
+  Window win0 = make_window<RT>(st, n_base, s0, min(s1, s0 + win), win * gps, 0, xrows, L.xstride);
+  StageBatch<kStageU> first;
+  load_batch<RT, kStageU>(first, win0, a, st, 0, lane);
+  __builtin_amdgcn_sched_barrier(0);
   u4 ring[P][RT];
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     ls_w.issue(ring[p], st, s0 + p);
-    __builtin_amdgcn_sched_barrier(0);  // keep slot order: slot 0 must be the oldest load
+    __builtin_amdgcn_sched_barrier(0);  // keep slot order: slot 0 must be the oldest ring load
   }
+  store_batch<RT, kStageU>(prm, xs, first, win0, 0, lane);
+  stage_rest<RT, kStageU>(prm, xs, win0, a, st, 64 * kStageU, lane);
 
   for (int w0 = s0; w0 < s1; w0 += win) {
     const int w1 = min(s1, w0 + win);
-    const int g_lo = (w0 * 128) >> st.log2g;
-    const int ng = min(st.groups, (w1 * 128) >> st.log2g) - g_lo;
-    stage_window<RT, 2>(prm, xs, a, st, n_base, g_lo, ng, win * gps, 0, xrows, w0 * 128, (w1 - w0) * 128,
-                        L.xstride, lane);
+    if (w0 != s0) stage_rest<RT, kStageU>(prm, xs, make_window<RT>(st, n_base, w0, w1, win * gps, 0, xrows, L.xstride),
+                                         a, st, 0, lane);
     for (int s = w0; s < w1; s += P) {
 #pragma unroll
       for (int p = 0; p < P; ++p) {
@@ -368,18 +416,25 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_mfma_kernel(LinearArgs a, int 
               load_b128(st.x, v ? xoff[mt] + (uint32_t)step * 256u + 16u * j : kOutOfRange);
     }
   };
+  // The first staging batch goes out ahead of the weight ring (see gemv_dot_kernel).
+  const int srows = XLDS ? xrows : 0;
+  Window win0 = make_window<RT>(st, n_base, s0, min(s1, s0 + win), win * gps, m_base, srows, L.xstride);
+  StageBatch<kStageU> first;
+  load_batch<RT, kStageU>(first, win0, a, st, 0, lane);
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     issue(p, s0 + p);
-    __builtin_amdgcn_sched_barrier(0);  // keep slot order: slot 0 must be the oldest load
+    __builtin_amdgcn_sched_barrier(0);  // keep slot order: slot 0 must be the oldest ring load
   }
+  store_batch<RT, kStageU>(prm, xs, first, win0, 0, lane);
+  stage_rest<RT, kStageU>(prm, xs, win0, a, st, 64 * kStageU, lane);
 
   for (int w0 = s0; w0 < s1; w0 += win) {
     const int w1 = min(s1, w0 + win);
-    const int g_lo = (w0 * 128) >> st.log2g;
-    const int ng = min(st.groups, (w1 * 128) >> st.log2g) - g_lo;
-    stage_window<RT, 2>(prm, xs, a, st, n_base, g_lo, ng, win * gps, m_base, XLDS ? xrows : 0, w0 * 128,
-                        (w1 - w0) * 128, L.xstride, lane);
+    if (w0 != s0)
+      stage_rest<RT, kStageU>(prm, xs, make_window<RT>(st, n_base, w0, w1, win * gps, m_base, srows, L.xstride), a,
+                             st, 0, lane);
     for (int s = w0; s < w1; s += P) {
 #pragma unroll
       for (int p = 0; p < P; ++p) {
