@@ -1,6 +1,7 @@
 """Benchmark of the MI355X quantized-linear hot path (the round driver's bench contract).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-tune] [--no-cpu] [--detail PATH]
+    python bench.py --traffic-probe      (eager launches for rocprofv3 --pmc, see below)
 
 Workload (BASELINE.json metric "W4A16 GEMV HBM GB/s at M=1 + GEMM TFLOP/s at M=256"):
 one step is one decode pass at M=1 through the four Qwen2.5-7B decoder linears (qkv
@@ -18,7 +19,12 @@ so host launch overhead is not measured; inputs are resident in HBM.
 Extra objects on the same JSON line:
 * ``roofline``: the dominant kernel (gate_up GEMV, M=1): algorithmic bytes per launch / its
   average launch duration, timed with HIP events on the stream it is launched on, against the
-  8 TB/s HBM peak.
+  8 TB/s HBM peak. ``traffic`` is the HBM bytes per launch that rocprofv3 counted
+  (FETCH_SIZE + WRITE_SIZE, each scaled by the ratio of known bytes to counted bytes of a
+  plain elementwise kernel in the same run), read from the committed summary
+  ``profiles/gemv_gate_up_m1_traffic.md`` when it was measured with the config in use, else
+  null. ``--traffic-probe`` runs exactly what those counter passes measure: the tuned gate_up
+  GEMV on the rotating cold copies, then the calibration kernel (torch.neg, 256 MiB in and out).
 * ``gemm_m256``: the prefill GEMM at M=256 on gate_up and down, TFLOP/s and fraction of the
   2.5 PFLOP/s fp16 dense MFMA peak.
 * ``cpu_baseline``: reference.py's CPU path (dequantize per call + fp32 matmul), restated in
@@ -51,6 +57,29 @@ SHAPES = [  # (layer, N, K)
     ("down_proj", 3584, 18944),
 ]
 COLD_BYTES = 1.1e9
+TRAFFIC_SUMMARY = ROOT / "profiles" / "gemv_gate_up_m1_traffic.md"
+CALIB_BYTES = 256 << 20
+
+
+def committed_traffic(cfg_dict: dict) -> float | None:  # type: ignore[type-arg]
+    """HBM bytes per launch of the dominant kernel from the committed counter summary, if that
+    summary was measured with ``cfg_dict``; the summary's lines ``config: {json}`` and
+    ``traffic_bytes_per_launch: N`` carry the two values."""
+    if not TRAFFIC_SUMMARY.is_file():
+        return None
+    cfg = traffic = None
+    for line in TRAFFIC_SUMMARY.read_text().splitlines():
+        if line.startswith("config: "):
+            try:
+                cfg = json.loads(line[len("config: "):])
+            except ValueError:
+                return None
+        elif line.startswith("traffic_bytes_per_launch: "):
+            try:
+                traffic = float(line.split(":", 1)[1])
+            except ValueError:
+                return None
+    return traffic if cfg == cfg_dict else None
 
 
 def bytes_moved(m: int, n: int, k: int, group: int = GROUP) -> int:
@@ -146,6 +175,8 @@ def main() -> int:
     ap.add_argument("--no-tune", action="store_true", help="use cached/default configs only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--detail", type=str, default=None, help="write per-shape details as JSON")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="eager gate_up GEMV launches + a calibration kernel, for rocprofv3 --pmc")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(
@@ -195,6 +226,22 @@ def main() -> int:
 
     gen = torch.Generator(device=dev).manual_seed(7)
     xs = [torch.randn((1, k), generator=gen, device=dev).to(torch.float16) for _, _, k in SHAPES]
+
+    if args.traffic_probe:
+        qw_s_z = [layers[c][2] for c in range(copies)]
+        for c in range(2 * copies):  # cold: each launch reads a copy the previous ones evicted
+            qw, sc, qz = qw_s_z[c % copies]
+            w4a16_gemm(xs[2], qw, sc, qz, GROUP, cfg1[2])
+        src = torch.randn(CALIB_BYTES // 4, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(4):
+            torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        print(json.dumps({"traffic_probe": {"kernel": "gate_up GEMV M=1", "launches": 2 * copies,
+                                            "config": cfg1[2].to_dict(), "calibration": "torch.neg",
+                                            "calibration_bytes_in": CALIB_BYTES,
+                                            "calibration_bytes_out": CALIB_BYTES}}), flush=True)
+        return 0
 
     def launcher(c: int, i: int, m_x: list, cfgs: list):  # type: ignore[no-untyped-def]
         qw, s, z = layers[c][i]
@@ -279,7 +326,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": dom["gbps"] / HBM_PEAK_GBPS,
-            "traffic": None,
+            "traffic": committed_traffic(cfg1[2].to_dict()),
             "bytes_per_launch": bytes_moved(1, gate_n, gate_k),
             "avg_launch_us": dom["us"],
         },
