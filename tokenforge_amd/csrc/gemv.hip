@@ -242,7 +242,7 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_dot_kernel(LinearArgs a, int w
   const int g = lane & 3;
   const int c = lane >> 2;
   constexpr int cols = 16 * RT;
-  const int n_base = blockIdx.x * cols;
+  const int n_base = xcd_tile(blockIdx.x, gridDim.x) * cols;
   const Streams st = make_streams(a);
   int s0, s1;
   k_range(wave, waves, st.nsteps, &s0, &s1);
@@ -366,7 +366,7 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_mfma_kernel(LinearArgs a, int 
   const int c = lane & 15;
   const int g = lane >> 4;
   constexpr int cols = 16 * RT;
-  const int n_base = blockIdx.x * cols;
+  const int n_base = xcd_tile(blockIdx.x, gridDim.x) * cols;
   const int m_base = blockIdx.y * 16 * MT;
   const Streams st = make_streams(a);
   int s0, s1;

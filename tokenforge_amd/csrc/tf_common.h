@@ -152,6 +152,21 @@ __device__ __forceinline__ float quad_sum(float v) {
   return v + t;
 }
 
+// ------------------------------------------------------------------ XCD placement
+
+// MI355X hands workgroup b of a launch to XCD b % 8 (round robin over its 8 XCDs, each with
+// its own L2). xcd_tile renumbers workgroups so every XCD works on one contiguous range of
+// tiles: neighbouring tiles share cache lines (per-column scales and zero points, operand
+// panels), which are then fetched into one L2 instead of several. A bijection on [0, nb).
+constexpr int kXcds = 8;
+
+__device__ __forceinline__ int xcd_tile(int b, int nb) {
+  const int q = nb / kXcds;
+  const int r = nb % kXcds;
+  const int x = b % kXcds;
+  return x * q + (x < r ? x : r) + b / kXcds;
+}
+
 // ------------------------------------------------------------------ misc
 
 __host__ __device__ constexpr int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }

@@ -6,13 +6,19 @@ graphs are captured. The hot path only does a dict lookup and falls back to the 
 synchronizes.
 
 The cache lives at ``$TOKENFORGE_CACHE_DIR`` (default ``~/.cache/tokenforge``) as
-``<gpu>-hip<abi>.json``: ``<gpu>`` is ``device.gpu_identity`` (e.g.
-``amd-instinct-mi355x-gfx950``) and ``<abi>`` the kernel library's ABI version, so a rebuilt
+``<gpu>-hip<abi>.json``: ``<gpu>`` is ``device.gpu_identity`` (e.g. ``amd-gfx950-256cu``)
+and ``<abi>`` the kernel library's ABI version, so a rebuilt
 library with different variants never reuses stale entries. Entries are keyed
 ``"{bucket}:{n}:{k}:{group}"`` by M bucket. Writes are atomic (tmp -> fsync -> rename ->
 fsync dir). Anything unexpected on read (bad JSON, wrong schema, another GPU or ABI, an
 invalid config, a config of the wrong kernel family for its bucket) discards the whole file
 with a warning. A cache is never partially trusted.
+
+Timing (the reference benchmarks each candidate with a cache flush before the call): a
+candidate is launched once per copy of the layer's synthetic weights from one HIP graph, the
+copies together larger than twice the 256 MB Infinity Cache, so every launch streams its
+weights from HBM as consecutive decode layers do and host launch overhead is not measured.
+Every candidate's output is first checked against the default config's.
 """
 
 from __future__ import annotations
@@ -225,6 +231,40 @@ def hip_bench(fn: Callable[[], object], warmup: int = 5, rep: int = 25) -> float
     return float(statistics.median(s.elapsed_time(e) for s, e in zip(starts, ends)))
 
 
+_COLD_BYTES = 640 * 1024 * 1024
+"""Weight bytes the default tuner rotates through: more than twice the 256 MB Infinity Cache."""
+_MAX_COPIES = 64
+
+
+def graph_bench(fns: list[Callable[[], object]], reps: int = 3) -> float:
+    """Per-launch time in ms of one HIP-graph replay launching each of ``fns`` once, best of
+    ``reps`` replays. The graph removes host launch overhead; ``fns`` rotate over distinct
+    weight copies so each launch reads its weights from HBM, as consecutive decode layers do."""
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        for f in fns[:2]:
+            f()
+        stream.synchronize()
+        with torch.cuda.graph(graph, stream=stream):
+            for f in fns:
+                f()
+    torch.cuda.current_stream().wait_stream(stream)
+    graph.replay()
+    torch.cuda.synchronize()
+    best = float("inf")
+    for _ in range(reps):
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+        best = min(best, start.elapsed_time(end) / len(fns))
+    return best
+
+
 def synthetic_layer(
     n: int, k: int, group_size: int, device: torch.device, seed: int = 0
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
@@ -271,12 +311,16 @@ def tune_layer(
             todo.append(bucket)
     if not todo:
         return winners
-    if bench_fn is None:
-        if device.type != "cuda":
-            raise RuntimeError("tuning needs a CUDA (HIP) device or an explicit bench_fn")
-        bench_fn = hip_bench
+    rotating = bench_fn is None
+    if rotating and device.type != "cuda":
+        raise RuntimeError("tuning needs a CUDA (HIP) device or an explicit bench_fn")
 
-    qweight_t, scales, qzeros = synthetic_layer(n, k, group_size, device)
+    # Default timing: a HIP graph over `copies` distinct weight copies (see graph_bench).
+    copies = 1
+    if rotating:
+        copies = max(2, min(_MAX_COPIES, -(-_COLD_BYTES // max(1, n * k // 2))))
+    layers = [synthetic_layer(n, k, group_size, device, seed=i) for i in range(copies)]
+    qweight_t, scales, qzeros = layers[0]
     gen = torch.Generator(device=device).manual_seed(1)
     for bucket in todo:
         x = (torch.randn((bucket, k), generator=gen, device=device) * 0.5).to(torch.float16)
@@ -290,9 +334,15 @@ def tune_layer(
                 if float((out.float() - ref).abs().max()) > tol:
                     log.warning("config %s miscomputes for %s; skipped", cfg, (bucket, n, k))
                     continue
-                t = bench_fn(
-                    functools.partial(w4a16_gemm, x, qweight_t, scales, qzeros, group_size, cfg)
-                )
+                if rotating:
+                    t = graph_bench(
+                        [functools.partial(w4a16_gemm, x, *lay, group_size, cfg) for lay in layers]
+                    )
+                else:
+                    assert bench_fn is not None
+                    t = bench_fn(
+                        functools.partial(w4a16_gemm, x, qweight_t, scales, qzeros, group_size, cfg)
+                    )
             except (ValueError, RuntimeError) as exc:  # variant cannot run this shape
                 log.debug("config %s failed to run: %s", cfg, exc)
                 continue
@@ -301,6 +351,7 @@ def tune_layer(
         chosen = best[1] if best is not None else base_cfg
         cache.put(bucket, n, k, group_size, chosen)
         winners[bucket] = chosen
+    del layers
     if save:
         cache.save()
     return winners
