@@ -1,6 +1,6 @@
 """Benchmark of the MI355X quantized-linear hot path (the round driver's bench contract).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-tune] [--no-cpu] [--detail PATH]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-tune] [--no-cpu] [--detail PATH] [--full]
     python bench.py --traffic-probe      (eager launches for rocprofv3 --pmc, see below)
 
 Workload (BASELINE.json metric "W4A16 GEMV HBM GB/s at M=1 + GEMM TFLOP/s at M=256"):
@@ -27,6 +27,11 @@ Extra objects on the same JSON line:
   GEMV on the rotating cold copies, then the calibration kernel (torch.neg, 256 MiB in and out).
 * ``gemm_m256``: the prefill GEMM at M=256 on gate_up and down, TFLOP/s and fraction of the
   2.5 PFLOP/s fp16 dense MFMA peak.
+* ``rmsnorm_fp8``: the fused RMSNorm + e4m3fn quant (configs[1]: H=3584, eight outlier
+  channels x20, gamma = 1 + 0.1 N(0,1), eps 1e-6, dynamic per-token scale) at T in
+  {1, 16, 512, 4096}; algorithmic bytes T*H*2 + H*2 + T*H + 4*T over rotating cold inputs.
+* with ``--full`` only (written to ``--detail``): ``gemm_sweep``, configs[3]: M in
+  {16, 32, 64, 128, 256, 1024, 4096} on gate_up and down, each bucket autotuned first.
 * ``cpu_baseline``: reference.py's CPU path (dequantize per call + fp32 matmul), restated in
   torch on the host cores, on a bounded sample of the same step.
 """
@@ -134,6 +139,34 @@ def time_graph(graph: torch.cuda.CUDAGraph, reps: int = 1) -> float:
     return float(start.elapsed_time(end))
 
 
+def rmsnorm_bench(dev: torch.device) -> list[dict]:  # type: ignore[type-arg]
+    """fused RMSNorm + FP8 at H=3584 over rotating cold inputs, per T."""
+    from tokenforge_amd.kernels.hip.rmsnorm_fp8 import rmsnorm_fp8_quant
+
+    h = 3584
+    gen = torch.Generator(device="cpu").manual_seed(0)
+    outliers = torch.randperm(h, generator=gen)[:8].to(dev)
+    gamma = (1 + 0.1 * torch.randn(h, generator=gen)).to(torch.float16).to(dev)
+    res = []
+    for t in (1, 16, 512, 4096):
+        copies = max(2, min(64, int(-(-COLD_BYTES // (t * h * 2)))))
+        xs = []
+        for _ in range(copies):
+            x = torch.randn((t, h), device=dev)
+            x[:, outliers] *= 20
+            xs.append(x.to(torch.float16))
+        g, _ = capture([lambda x=x: rmsnorm_fp8_quant(x, gamma, 1e-6, None) for x in xs])
+        time_graph(g)
+        ms = min(time_graph(g) for _ in range(3)) / copies
+        nbytes = t * h * 2 + h * 2 + t * h + 4 * t
+        gbps = nbytes / (ms * 1e-3) / 1e9
+        res.append({"t": t, "h": h, "us": ms * 1e3, "gbps": gbps, "frac_hbm": gbps / HBM_PEAK_GBPS,
+                    "bytes": nbytes})
+        log(f"  rmsnorm_fp8   T={t:<5d} {ms * 1e3:8.2f} us {gbps:7.0f} GB/s ({100 * gbps / HBM_PEAK_GBPS:.1f}% of 8 TB/s)")
+        del xs, g
+    return res
+
+
 def cpu_baseline(layers: list, budget_s: float = 12.0) -> dict:  # type: ignore[type-arg]
     """reference.py:24-32 restated in torch on the host cores, one decode step (M=1)."""
     from oracle.cpu_path import w4a16_torch_cpu
@@ -175,6 +208,8 @@ def main() -> int:
     ap.add_argument("--no-tune", action="store_true", help="use cached/default configs only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--detail", type=str, default=None, help="write per-shape details as JSON")
+    ap.add_argument("--full", action="store_true",
+                    help="also sweep the GEMM over M in {16..4096} (configs[3]) into --detail")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="eager gate_up GEMV launches + a calibration kernel, for rocprofv3 --pmc")
     args = ap.parse_args()
@@ -290,6 +325,30 @@ def main() -> int:
                      "frac_mfma": tflops / FP16_MFMA_PEAK_TFLOPS, "config": cfg.to_dict()})
         log(f"  {name:13s} M=256 {ms * 1e3:8.2f} us {tflops:7.1f} TFLOP/s ({100 * tflops / FP16_MFMA_PEAK_TFLOPS:.1f}% of 2.5 PF)")
 
+    norm = rmsnorm_bench(dev)
+
+    sweep = None
+    if args.full:
+        sweep = []
+        for i in (2, 3):
+            name, n, k = SHAPES[i]
+            for m in (16, 32, 64, 128, 256, 1024, 4096):
+                if not args.no_tune:
+                    autotune.tune_layer(n, k, GROUP, device=dev, gpu=gpu, buckets=(m,))
+                cfg = autotune.lookup(gpu, m, n, k, GROUP)
+                xm = [None] * len(SHAPES)
+                xm[i] = torch.randn((m, k), generator=gen, device=dev).to(torch.float16)
+                g, _ = capture([launcher(r % copies, i, xm, [cfg] * len(SHAPES)) for r in range(copies)])
+                time_graph(g)
+                ms = min(time_graph(g) for _ in range(3)) / copies
+                tflops = 2 * m * n * k / (ms * 1e-3) / 1e12
+                gbps = bytes_moved(m, n, k) / (ms * 1e-3) / 1e9
+                sweep.append({"layer": name, "m": m, "n": n, "k": k, "us": ms * 1e3, "tflops": tflops,
+                              "frac_mfma": tflops / FP16_MFMA_PEAK_TFLOPS, "gbps": gbps,
+                              "frac_hbm": gbps / HBM_PEAK_GBPS, "config": cfg.to_dict()})
+                log(f"  {name:13s} M={m:<5d} {ms * 1e3:9.2f} us {tflops:7.1f} TFLOP/s {gbps:7.0f} GB/s  {cfg}")
+                del g, xm
+
     cpu = None
     if not args.no_cpu:
         t0 = time.perf_counter()
@@ -331,14 +390,16 @@ def main() -> int:
             "avg_launch_us": dom["us"],
         },
         "gemm_m256": gemm,
+        "rmsnorm_fp8": norm,
         "repack_gate_up_gbps": (gate_n * gate_k) / (rep_ms * 1e-3) / 1e9,
         "per_shape": per_shape,
         "cpu_baseline": cpu,
         "gpu": gpu,
     }
     if args.detail:
+        detail = dict(result, gemm_sweep=sweep) if sweep is not None else result
         Path(args.detail).parent.mkdir(parents=True, exist_ok=True)
-        Path(args.detail).write_text(json.dumps(result, indent=1) + "\n")
+        Path(args.detail).write_text(json.dumps(detail, indent=1) + "\n")
     print(json.dumps(result), flush=True)
     return 0
 
