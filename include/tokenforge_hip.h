@@ -125,8 +125,9 @@ int tf_rmsnorm_fp8_quant(const uint16_t* x, int64_t ldx, const uint16_t* weight,
                          uint8_t* q, int64_t ldq, float* scale, int32_t static_scale,
                          int64_t t, int64_t h, float eps, void* stream);
 
-/* Test hook for the e4m3fn encoder used by tf_rmsnorm_fp8_quant
- * (rmsnorm_fp8.py:29-41 _round_to_e4m3_grid + cast): fp32 [count] -> uint8 [count].
+/* Test hook for the e4m3fn encoding used by tf_rmsnorm_fp8_quant
+ * (rmsnorm_fp8.py:29-41 _round_to_e4m3_grid + cast): fp32 [count] -> uint8 [count], through
+ * the same hardware conversion (v_cvt_pk_fp8_f32) and NaN handling as that kernel.
  * Inputs must lie in [-448, 448] or be NaN. */
 int tf_e4m3_encode(const float* in, uint8_t* out, int64_t count, void* stream);
 

@@ -117,12 +117,49 @@ def test_e4m3_rounding_is_bit_exact_at_every_midpoint(device: torch.device) -> N
     mids = (values[1:] + values[:-1]) / 2
     up, down = torch.tensor(1e9), torch.tensor(-1e9)
     probe = torch.cat([values, mids, mids.nextafter(up), mids.nextafter(down)])
-    probe = torch.cat([probe, -probe, torch.tensor([0.0, -0.0])])
+    probe = torch.cat([probe, -probe, torch.tensor([0.0, -0.0, float("nan"), -float("nan")])])
     gen = torch.Generator().manual_seed(5)
     probe = torch.cat([probe, (torch.rand(1 << 20, generator=gen) * 2 - 1) * 448,
                        (torch.rand(1 << 18, generator=gen) * 2 - 1) * 0.03])
     out = e4m3_encode(probe.to(device))
     assert np.array_equal(_codes(out), probe.to(torch.float8_e4m3fn).view(torch.uint8).numpy())
+
+
+def _assert_codes_match_nan_aware(codes: np.ndarray, ref: np.ndarray) -> None:
+    """Bit-exact, except that a NaN code (0x7F / 0xFF) matches either NaN code: the sign of a
+    NaN that an invalid operation creates (0/0, inf*0) is the hardware's default NaN, which
+    is negative on x86 (the oracle) and positive on the GPU."""
+    nan_k, nan_r = (codes & 0x7F) == 0x7F, (ref & 0x7F) == 0x7F
+    assert np.array_equal(nan_k, nan_r), "NaN positions differ"
+    assert np.array_equal(codes[~nan_k], ref[~nan_r])
+
+
+def test_special_values_rows_and_scales(device: torch.device) -> None:
+    """Rows with +inf, NaN, an fp16 overflow of y, zeros and -inf (dynamic scale), and static
+    scales 0, inf, NaN, negative and tiny: the kernel's exact-rounding slow path."""
+    h = 896
+    gen = torch.Generator().manual_seed(21)
+    x = (torch.randn((6, h), generator=gen) * 2).to(torch.float16)
+    w = (torch.rand((h,), generator=gen) + 0.5).to(torch.float16)
+    w[5] = 4000.0  # x[2, 5] * rstd * 4000 overflows fp16
+    x[0, 3] = float("inf")
+    x[1, 7] = float("nan")
+    x[2, 5] = 1000.0
+    x[3] = 0.0
+    x[5, 9] = float("-inf")
+    with np.errstate(all="ignore"):
+        q_ref, s_ref = oref.rmsnorm_fp8_reference(x.numpy(), w.numpy(), EPS)
+    q, s = rmsnorm_fp8_quant(x.to(device), w.to(device), EPS)
+    _assert_codes_match_nan_aware(_codes(q), q_ref)
+    s_k = s.cpu().numpy()
+    assert np.array_equal(np.isnan(s_k), np.isnan(s_ref))
+    assert np.array_equal(s_k[~np.isnan(s_k)].view(np.uint32), s_ref[~np.isnan(s_ref)].view(np.uint32))
+    for sc in (0.0, float("inf"), float("nan"), -2e-3, 1e-30):
+        scale = np.array([sc], dtype=np.float32)
+        with np.errstate(all="ignore"):
+            q_ref, _ = oref.rmsnorm_fp8_reference(x.numpy(), w.numpy(), EPS, scale)
+        q, _ = rmsnorm_fp8_quant(x.to(device), w.to(device), EPS, torch.from_numpy(scale).to(device))
+        _assert_codes_match_nan_aware(_codes(q), q_ref)
 
 
 def test_zero_row_uses_min_scale(device: torch.device) -> None:

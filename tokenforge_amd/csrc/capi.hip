@@ -28,7 +28,7 @@ namespace {
 __global__ void e4m3_encode_kernel(const float* __restrict__ in, uint8_t* __restrict__ out,
                                    int64_t count) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < count) out[i] = e4m3_encode(in[i]);
+  if (i < count) out[i] = e4m3_encode_hw(in[i]);
 }
 }  // namespace
 

@@ -1,11 +1,26 @@
 // Fused RMSNorm + OCP e4m3fn quantization: one HBM read of x, one write of the codes.
 //
-// One workgroup per token row. The row stays in registers between the two reductions
-// (sum of squares, then absmax). The sum of squares is accumulated in fp64: every x^2 of
-// an fp16 x is exact, so the fp64 total is the exact sum up to ~2^-53 relative and its
-// rounding to fp32 does not depend on the summation order. The kernel is therefore
-// deterministic and matches a correctly rounded fp32 restatement bit for bit; torch's
-// fp32 `mean` (reference.py:37) can differ from it by an ulp of var on some rows.
+// One workgroup per token row; x and the weight are loaded together up front and the row
+// stays in registers between the two reductions (sum of squares, then absmax). The sum of
+// squares is accumulated in fp64: every x^2 of an fp16 x is exact, so the fp64 total is the
+// exact sum up to ~2^-53 relative and its rounding to fp32 does not depend on the summation
+// order. The kernel is therefore deterministic and matches a correctly rounded fp32
+// restatement bit for bit; torch's fp32 `mean` (reference.py:37) can differ from it by an ulp
+// of var on some rows.
+//
+// Quotient y / scale (reference.py:47-49): computed as fp32(fp64(y) * fp64(1 / scale)) with
+// the reciprocal correctly rounded in fp64. This equals the IEEE fp32 division for every
+// fp16 y and fp32 scale: the fp64 product is within 2^-52 (relative) of y / scale, while a
+// quotient of an 11-bit by a 24-bit significand that is not exactly representable lies at
+// least ~2^-49 (relative) away from every fp32 rounding boundary, so both round alike (the
+// zero, infinite and NaN cases follow IEEE multiplication by 0, inf or NaN the same way).
+//
+// Encoding: rows whose absmax and scale are finite (scale > 0) hold no NaN quotient, so they
+// clamp with v_med3 and encode two values per v_cvt_pk_fp8_f32. That instruction rounds to
+// nearest even onto e4m3fn exactly like e4m3_encode on every fp32 with |v| <= 448 (checked
+// exhaustively on MI355X) but writes 0xFF for every NaN, where torch's cast keeps the sign
+// (0x7F for +NaN); the remaining rows therefore clamp with NaN-preserving compares and use
+// e4m3_encode.
 #include "fp8.h"
 #include "tf_common.h"
 
@@ -25,8 +40,6 @@ __device__ __forceinline__ _Float16 mul_round_f32_then_f16(float a, float b) {
 }
 constexpr float kMinScale = 1.0f / (448.0f * 512.0f);  // reference.py:10
 
-__device__ __forceinline__ float nan_max(float a, float b) { return (a > b || a != a) ? a : b; }
-
 template <int WAVES>
 __device__ __forceinline__ double block_sum(double v, double* red) {
 #pragma unroll
@@ -40,18 +53,26 @@ __device__ __forceinline__ double block_sum(double v, double* red) {
   return t;
 }
 
+// Max of |y| as fp16 bit patterns: for non-NaN values the unsigned order of (bits & 0x7FFF)
+// is the order of |y|, and every NaN pattern is above +inf, so a NaN anywhere wins (the NaN
+// propagation of torch's amax).
 template <int WAVES>
-__device__ __forceinline__ float block_nan_max(float v, float* red) {
+__device__ __forceinline__ uint32_t block_max_u32(uint32_t v, uint32_t* red) {
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v = nan_max(v, __shfl_xor(v, off, 64));
+  for (int off = 32; off >= 1; off >>= 1) {
+    const uint32_t o = (uint32_t)__shfl_xor((int)v, off, 64);
+    v = v > o ? v : o;
+  }
   const int wave = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) red[wave] = v;
   __syncthreads();
-  float t = red[0];
+  uint32_t t = red[0];
 #pragma unroll
-  for (int i = 1; i < WAVES; ++i) t = nan_max(t, red[i]);
+  for (int i = 1; i < WAVES; ++i) t = t > red[i] ? t : red[i];
   return t;
 }
+
+__device__ __forceinline__ float quotient(_Float16 y, double rcp) { return (float)((double)(float)y * rcp); }
 
 // CPT: 8-element chunks per thread. VEC: 16-byte x / weight loads and 8-byte code stores.
 template <int WAVES, int CPT, bool VEC>
@@ -61,117 +82,129 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_fp8_kernel(
     float eps) {
   constexpr int kThreads = WAVES * 64;
   __shared__ double red_d[WAVES];
-  __shared__ float red_f[WAVES];
+  __shared__ uint32_t red_u[WAVES];
 
   const int64_t row = blockIdx.x;
   const uint16_t* xr = x + row * ldx;
   const int tid = threadIdx.x;
 
-  _Float16 xv[CPT][8];
-  double ss = 0.0;
+  // All inputs are requested before anything waits on any of them. Values stay packed as
+  // fp16 pairs (pair j of chunk i holds elements 2j, 2j+1).
+  const float s_static = static_scale ? scale[0] : 0.0f;
+  h2 xv[CPT][4];
+  h2 wv[CPT][4];
 #pragma unroll
   for (int i = 0; i < CPT; ++i) {
     const int e0 = (tid + i * kThreads) * 8;
     if (VEC) {
+      u4 rx = u4{0u, 0u, 0u, 0u}, rw = u4{0u, 0u, 0u, 0u};
       if (e0 < h) {
-        const u4 raw = *reinterpret_cast<const u4*>(xr + e0);
+        rx = *reinterpret_cast<const u4*>(xr + e0);
+        rw = *reinterpret_cast<const u4*>(w + e0);
+      }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const h2 p = as_h2(raw[j]);
-          xv[i][2 * j] = p[0];
-          xv[i][2 * j + 1] = p[1];
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) xv[i][j] = (_Float16)0.0f;
+      for (int j = 0; j < 4; ++j) {
+        xv[i][j] = as_h2(rx[j]);
+        wv[i][j] = as_h2(rw[j]);
       }
     } else {
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        xv[i][j] = (e0 + j < h) ? __builtin_bit_cast(_Float16, xr[e0 + j]) : (_Float16)0.0f;
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const double d = (double)(float)xv[i][j];
-      ss += d * d;
+      for (int j = 0; j < 4; ++j) {
+        const int e = e0 + 2 * j;
+        const uint32_t x0 = e < h ? xr[e] : 0u, x1 = e + 1 < h ? xr[e + 1] : 0u;
+        const uint32_t w0 = e < h ? w[e] : 0u, w1 = e + 1 < h ? w[e + 1] : 0u;
+        xv[i][j] = as_h2(x0 | (x1 << 16));
+        wv[i][j] = as_h2(w0 | (w1 << 16));
+      }
     }
   }
+
+  double ss = 0.0;
+#pragma unroll
+  for (int i = 0; i < CPT; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const double d = (double)(float)xv[i][j][k];
+        ss += d * d;
+      }
   const double total = block_sum<WAVES>(ss, red_d);
 
   // reference.py:37-38: var = mean(x^2) in fp32, rstd = 1 / sqrt(var + eps), IEEE ops.
   const float var = (float)total / (float)h;
   const float rstd = 1.0f / __builtin_sqrtf(var + eps);
 
-  float amax = 0.0f;
+  uint32_t amax_bits = 0;
 #pragma unroll
   for (int i = 0; i < CPT; ++i) {
     const int e0 = (tid + i * kThreads) * 8;
-    _Float16 wv[8];
-    if (VEC) {
-      if (e0 < h) {
-        const u4 raw = *reinterpret_cast<const u4*>(w + e0);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const h2 p = as_h2(raw[j]);
-          wv[2 * j] = p[0];
-          wv[2 * j + 1] = p[1];
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) wv[j] = (_Float16)0.0f;
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-        wv[j] = (e0 + j < h) ? __builtin_bit_cast(_Float16, w[e0 + j]) : (_Float16)0.0f;
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < 4; ++j) {
       // reference.py:39: fp16(x * rstd) in fp32 then cast, times weight in fp16 (one rounding).
-      const _Float16 nrm = mul_round_f32_then_f16((float)xv[i][j], rstd);
-      const _Float16 y = nrm * wv[j];
+      h2 nrm;
+      nrm[0] = mul_round_f32_then_f16((float)xv[i][j][0], rstd);
+      nrm[1] = mul_round_f32_then_f16((float)xv[i][j][1], rstd);
+      const h2 y = nrm * wv[i][j];
       xv[i][j] = y;  // the row is reused in place for y
-      if (e0 + j < h) amax = nan_max(amax, __builtin_fabsf((float)y));
+      const uint32_t yb = as_u32(y);
+      const uint32_t a0 = e0 + 2 * j < h ? (yb & 0x7FFFu) : 0u;
+      const uint32_t a1 = e0 + 2 * j + 1 < h ? ((yb >> 16) & 0x7FFFu) : 0u;
+      const uint32_t am = a0 > a1 ? a0 : a1;
+      amax_bits = amax_bits > am ? amax_bits : am;
     }
   }
+  const uint32_t m_bits = block_max_u32<WAVES>(amax_bits, red_u);
+  const float amax = (float)__builtin_bit_cast(_Float16, (uint16_t)m_bits);
 
   float s;
   if (static_scale) {
-    s = scale[0];
+    s = s_static;
   } else {
-    __syncthreads();  // red_f is disjoint from red_d, but keep the two reductions ordered
-    const float m = block_nan_max<WAVES>(amax, red_f);
-    const float raw = m / kFp8Max;
+    const float raw = amax / kFp8Max;
     s = (raw < kMinScale) ? kMinScale : raw;  // clamp(min=...) keeps NaN
     if (tid == 0) scale[row] = s;
   }
+  const double rcp = 1.0 / (double)s;
+  const bool fast = __builtin_isfinite(amax) && __builtin_isfinite(s) && s > 0.0f;
 
   uint8_t* qr = q + row * ldq;
 #pragma unroll
   for (int i = 0; i < CPT; ++i) {
     const int e0 = (tid + i * kThreads) * 8;
-    uint8_t codes[8];
+    uint32_t lo, hi;
+    if (fast) {
+      uint32_t pk[4];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      float v = (float)xv[i][j] / s;
-      v = (v < -kFp8Max) ? -kFp8Max : v;
-      v = (v > kFp8Max) ? kFp8Max : v;
-      codes[j] = e4m3_encode(v);
+      for (int j = 0; j < 4; ++j) {
+        const float a = __builtin_amdgcn_fmed3f(quotient(xv[i][j][0], rcp), -kFp8Max, kFp8Max);
+        const float b = __builtin_amdgcn_fmed3f(quotient(xv[i][j][1], rcp), -kFp8Max, kFp8Max);
+        pk[j] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false) & 0xFFFFu;
+      }
+      lo = pk[0] | (pk[1] << 16);
+      hi = pk[2] | (pk[3] << 16);
+    } else {
+      uint8_t codes[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float v = quotient(xv[i][j >> 1][j & 1], rcp);
+        v = (v < -kFp8Max) ? -kFp8Max : v;
+        v = (v > kFp8Max) ? kFp8Max : v;
+        codes[j] = e4m3_encode(v);
+      }
+      lo = hi = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        lo |= (uint32_t)codes[j] << (8 * j);
+        hi |= (uint32_t)codes[4 + j] << (8 * j);
+      }
     }
     if (VEC) {
-      if (e0 < h) {
-        uint32_t lo = 0, hi = 0;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          lo |= (uint32_t)codes[j] << (8 * j);
-          hi |= (uint32_t)codes[4 + j] << (8 * j);
-        }
-        *reinterpret_cast<uint2*>(qr + e0) = make_uint2(lo, hi);
-      }
+      if (e0 < h) *reinterpret_cast<uint2*>(qr + e0) = make_uint2(lo, hi);
     } else {
 #pragma unroll
       for (int j = 0; j < 8; ++j)
-        if (e0 + j < h) qr[e0 + j] = codes[j];
+        if (e0 + j < h) qr[e0 + j] = (uint8_t)((j < 4 ? lo : hi) >> (8 * (j & 3)));
     }
   }
 }
@@ -218,7 +251,9 @@ extern "C" int tf_rmsnorm_fp8_quant(const uint16_t* x, int64_t ldx, const uint16
   if (h > 16 * 8 * 256) return fail(TF_EINVAL, "tf_rmsnorm_fp8_quant: h above 32768 is not supported");
   if (t == 0) return TF_OK;
   const int64_t chunks = cdiv(h, 8);
-  const int waves = chunks >= 512 ? 4 : (chunks >= 256 ? 2 : 1);
+  // Up to 4 waves per row, at most a few chunks per thread: short rows stay latency-bound,
+  // and long ones keep the per-wave register footprint low enough for full occupancy.
+  const int waves = chunks >= 256 ? 4 : (chunks >= 128 ? 2 : 1);
   const int64_t per = cdiv(chunks, waves * 64);
   const int cpt = per <= 1 ? 1 : per <= 2 ? 2 : per <= 4 ? 4 : per <= 8 ? 8 : 16;
   const bool vec = (h % 8 == 0) && (ldx % 8 == 0) && (ldq % 8 == 0) && aligned(x, 16) &&
