@@ -86,6 +86,23 @@ PATH_CONFIGS = [
     GemmConfig("gemm_mfma", 128, 128, 32, 2, 4, 2),
     GemmConfig("gemm_mfma", 256, 128, 64, 4, 4, 2),
     GemmConfig("gemm_mfma", 128, 256, 64, 1, 4, 2),
+    # pipelined form: x in three (num_stages 4) or two (3) LDS stages, weights two blocks
+    # ahead, 4 or 8 waves; split_k 3 over the 8 K blocks gives slices of 2 and 3 blocks (the
+    # odd tail iteration)
+    GemmConfig("gemm_mfma", 256, 160, 64, 1, 4, 4),
+    GemmConfig("gemm_mfma", 128, 128, 64, 3, 4, 4),
+    GemmConfig("gemm_mfma", 64, 256, 64, 2, 4, 4),
+    GemmConfig("gemm_mfma", 256, 192, 64, 1, 4, 4),
+    GemmConfig("gemm_mfma", 256, 96, 64, 3, 4, 4),
+    GemmConfig("gemm_mfma", 128, 192, 64, 1, 4, 4),
+    GemmConfig("gemm_mfma", 256, 128, 64, 1, 4, 4),
+    GemmConfig("gemm_mfma", 128, 256, 64, 1, 4, 4),
+    GemmConfig("gemm_mfma", 256, 256, 64, 1, 8, 3),
+    GemmConfig("gemm_mfma", 256, 192, 64, 3, 8, 3),
+    GemmConfig("gemm_mfma", 256, 192, 64, 1, 8, 4),
+    GemmConfig("gemm_mfma", 256, 128, 64, 2, 8, 3),
+    GemmConfig("gemm_mfma", 128, 256, 64, 3, 8, 3),
+    GemmConfig("gemm_mfma", 256, 160, 64, 1, 8, 3),
 ]
 
 
@@ -148,6 +165,8 @@ def test_small_group_sizes(group_size: int, device: torch.device) -> None:
     ]
     if group_size == 64:
         configs.append(GemmConfig("gemm_mfma", 128, 128, 64, 1, 4, 2))
+        configs.append(GemmConfig("gemm_mfma", 128, 128, 64, 2, 4, 4))
+        configs.append(GemmConfig("gemm_mfma", 256, 128, 64, 2, 8, 3))
     for cfg in configs:
         for m in (1, 5, 40):
             if cfg.kernel == "gemv_dot" and m > cfg.block_m:

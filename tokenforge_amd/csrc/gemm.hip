@@ -191,6 +191,17 @@ __global__ void splitk_reduce_kernel(const float* __restrict__ ws, const uint16_
   out[row * ldo + col] = __builtin_bit_cast(uint16_t, (_Float16)v);
 }
 
+}  // namespace
+
+int splitk_reduce(const LinearArgs& a, const float* ws, int split, hipStream_t stream) {
+  const int64_t total = (int64_t)a.m * a.n;
+  splitk_reduce_kernel<<<(unsigned)cdiv(total, 256), 256, 0, stream>>>(ws, a.bias, a.out, a.ldo, a.m, a.n,
+                                                                      split);
+  return check_launch("tf_w4a16_linear(splitk_reduce)");
+}
+
+namespace {
+
 int effective_split(const LinearArgs& a, const tf_gemm_config& cfg) {
   const int nkb = a.k / cfg.block_k;
   return cfg.split_k < nkb ? cfg.split_k : (nkb > 0 ? nkb : 1);
@@ -208,12 +219,7 @@ int launch_gemm(const LinearArgs& a, const tf_gemm_config& cfg, float* ws, hipSt
   const dim3 grid((unsigned)cdiv(a.n, BN), (unsigned)cdiv(a.m, BM), (unsigned)split);
   gemm_kernel<BM, BN, BK, WM, WN><<<grid, WM * WN * 64, 0, stream>>>(a, ws, split);
   if (int rc = check_launch("tf_w4a16_linear(gemm_mfma)")) return rc;
-  if (split > 1) {
-    const int64_t total = (int64_t)a.m * a.n;
-    splitk_reduce_kernel<<<(unsigned)cdiv(total, 256), 256, 0, stream>>>(ws, a.bias, a.out, a.ldo, a.m,
-                                                                        a.n, split);
-    return check_launch("tf_w4a16_linear(splitk_reduce)");
-  }
+  if (split > 1) return splitk_reduce(a, ws, split, stream);
   return TF_OK;
 }
 

@@ -1,0 +1,345 @@
+// Prefill-shaped W4A16 GEMM, pipelined form (M >= 64, group size 64 or 128).
+//
+// A workgroup of 4 or 8 waves (WM x WN) computes a BM x BN tile of y = x W^T with
+// v_mfma_f32_32x32x16_f16, K in blocks of 64. With 8 waves two waves share each SIMD, so one
+// wave's MFMAs overlap the other's dequantization, LDS traffic and waits. Per block:
+//   * the x tile [BM][64] fp16 streams from global memory straight into LDS (buffer loads
+//     with the LDS destination, 16 bytes per lane, no registers), S stages deep;
+//   * the packed weight tile [BN][64/8] and its scales / zero points are loaded into a
+//     two-block register ring, dequantized once per workgroup (fp16(q - z) * s, one rounding)
+//     and written to one of two fp16 LDS buffers;
+//   * each wave reads 32x16 operand fragments (8 consecutive K per lane, the 32x32x16 MFMA
+//     layout) and accumulates a (BM/WM) x (BN/WN) sub-tile in fp32.
+// Iteration kb waits for x block kb (issued S - 1 iterations earlier), issues x block
+// kb + S - 1, multiplies block kb, dequantizes block kb + 1 into the other B buffer, then issues
+// the weights of block kb + 3: weight latency is covered by two blocks of MFMA work (x comes
+// from L2 and is covered by S - 1 blocks), and there is one barrier per block. With S = 2 the
+// stage of a block is a compile-time value of the two-iteration loop body. The loop body is straight-line (loads past the K range are issued
+// with out-of-range offsets and return zeros), so the count of loads in flight is the same on
+// every path and the waits stay exact.
+//
+// LDS rows hold 8 chunks of 16 bytes; chunk c of row r sits in slot c ^ (r % 8), so the 8
+// lanes of each 16-byte read phase hit 8 distinct bank groups.
+//
+// Tile order: the grid is one-dimensional; workgroups are numbered XCD by XCD (xcd_tile) and
+// within an XCD the M tiles of one N tile are adjacent, so a weight panel is fetched into one
+// L2 and reused there by every M tile.
+//
+// Split-K (split_k > 1): each K slice writes fp32 partials [split][M][N] to the caller's
+// workspace; splitk_reduce (gemm.hip) sums them in split order, adds the bias and rounds once.
+#include <type_traits>
+
+#include "linear.h"
+
+namespace tf {
+
+int splitk_reduce(const LinearArgs& a, const float* ws, int split, hipStream_t stream);
+
+namespace {
+
+constexpr int kBK = 64;           // K per block
+constexpr int kRowChunks = 8;     // 16-byte chunks per 64-wide fp16 row
+constexpr uint32_t kChunkBytes = 16;
+
+__device__ __forceinline__ uint32_t swz(int row, int chunk) {
+  return (uint32_t)(row * kRowChunks + (chunk ^ (row & 7))) * kChunkBytes;
+}
+
+template <int BM, int BN, int WM, int WN, int S>
+struct G2 {
+  static constexpr int kWaves = WM * WN;
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int TM = BM / WM / 32;
+  static constexpr int TN = BN / WN / 32;
+  static constexpr int kAStage = BM * kBK * 2;       // bytes of one x stage
+  static constexpr int kBStage = BN * kBK * 2;       // bytes of one fp16 weight buffer
+  static constexpr int kADma = kAStage / 1024;       // 1 KB LDS-load instructions per stage
+  static constexpr int kAPerWave = kADma / kWaves;
+  static constexpr int kBChunks = BN * kBK / 32;     // 16-byte packed chunks (32 K of a column)
+  static constexpr int kBPer = (kBChunks + kThreads - 1) / kThreads;
+  static constexpr int kLds = S * kAStage + 2 * kBStage;
+  static_assert(kWaves == 4 || kWaves == 8, "four or eight waves");
+  static_assert(TM >= 1 && TN >= 1 && BM % (32 * WM) == 0 && BN % (32 * WN) == 0, "wave tile");
+  static_assert(kADma % kWaves == 0, "x stage must split evenly over the waves");
+  static_assert(S == 2 || S == 3, "x stages");
+  // VMEM issued after x block kb (S - 1 iterations back) when iteration kb waits for it:
+  // weights kb + 4 - S, then S - 2 whole iterations (x block, weights).
+  static constexpr int kAfterA = 3 * kBPer + (S - 2) * (kAPerWave + 3 * kBPer);
+};
+
+// Block barrier at the top of an iteration: at most N vector-memory loads of this wave still
+// in flight (s_waitcnt vmcnt(N) lgkmcnt(0): its x-block loads into LDS and its LDS writes
+// are done), then s_barrier. Written out instead of __syncthreads so that no wider wait than
+// vmcnt(N) is added; the scheduling barriers keep every LDS access on its side.
+template <int N>
+__device__ __forceinline__ void block_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0x0 << 8) | ((N >> 4) << 14));
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+template <int BM, int BN, int WM, int WN, int S>
+__global__ __launch_bounds__(64 * WM * WN) void gemm2_kernel(LinearArgs a, float* __restrict__ ws, int split_k,
+                                                    int tiles_n, int tiles_m) {
+  using C = G2<BM, BN, WM, WN, S>;
+  constexpr int TM = C::TM, TN = C::TN, BP = C::kBPer;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  uint8_t* const a_lds = smem;
+  uint8_t* const b_lds = smem + S * C::kAStage;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WN;
+  const int wn = wave % WN;
+
+  const int per_split = tiles_n * tiles_m;
+  const int t = xcd_tile(blockIdx.x, gridDim.x);
+  const int z = t / per_split;
+  const int r = t - z * per_split;
+  const int m0 = (r % tiles_m) * BM;
+  const int n0 = (r / tiles_m) * BN;
+
+  const int nkb = a.k / kBK;
+  const int kb0 = (int)(((int64_t)z * nkb) / split_k);
+  const int kb1 = (int)(((int64_t)(z + 1) * nkb) / split_k);
+
+  const uint32_t row_bytes = (uint32_t)(a.k >> 1);
+  const int groups = a.k >> a.log2g;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, (uint32_t)(((int64_t)(a.m - 1) * a.ldx + a.k) * 2));
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc(a.qw, (uint32_t)a.n * row_bytes);
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.scales, (uint32_t)(groups * a.n * 2));
+  const __amdgpu_buffer_rsrc_t rz = make_rsrc(a.qz, (uint32_t)(groups * (a.n >> 3) * 4));
+  const UnpackConsts uc = unpack_consts();
+
+  // ---- x block kb -> LDS stage st (LDS-destination loads; lane l of instruction j writes
+  // 16-byte slot 64 j + l of the stage).
+  uint32_t a_off[C::kAPerWave];  // byte offset of this lane's chunk in block 0 (or out of range)
+#pragma unroll
+  for (int i = 0; i < C::kAPerWave; ++i) {
+    const int p = (wave + C::kWaves * i) * 64 + lane;
+    const int row = p >> 3;
+    const int c = (p & 7) ^ (row & 7);
+    const int m = m0 + row;
+    a_off[i] = m < a.m ? (uint32_t)(((int64_t)m * a.ldx + c * 8) * 2) : kOutOfRange;
+  }
+  auto issue_a = [&](int kb, int st) {
+    const bool ok = kb < kb1;
+#pragma unroll
+    for (int i = 0; i < C::kAPerWave; ++i) {
+      const uint32_t off = ok ? a_off[i] + (uint32_t)kb * (kBK * 2) : kOutOfRange;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rx, (__attribute__((address_space(3))) void*)(a_lds + st * C::kAStage + (wave + C::kWaves * i) * 1024), 16, off,
+          0, 0, 0);
+    }
+  };
+
+  // ---- packed weights of block kb -> register slot
+  uint32_t b_off[BP];
+  int b_col[BP];
+#pragma unroll
+  for (int i = 0; i < BP; ++i) {
+    const int id = tid + i * C::kThreads;
+    const int col = id >> 1;
+    const int n = n0 + col;
+    b_col[i] = col;
+    b_off[i] = (id < C::kBChunks && n < a.n) ? (uint32_t)n * row_bytes + (uint32_t)(id & 1) * 16u : kOutOfRange;
+  }
+  u4 braw[2][BP];
+  uint32_t bsc[2][BP], bzw[2][BP];
+  auto issue_b = [&](int kb, int slot) {
+    const bool ok = kb < kb1;
+    const uint32_t grp = (uint32_t)((kb * kBK) >> a.log2g);
+#pragma unroll
+    for (int i = 0; i < BP; ++i) {
+      const bool v = ok && b_off[i] != kOutOfRange;
+      const uint32_t n = (uint32_t)(n0 + b_col[i]);
+      braw[slot][i] = load_b128(rq, v ? b_off[i] + (uint32_t)kb * 32u : kOutOfRange);
+      bsc[slot][i] = load_b16(rs, v ? (grp * (uint32_t)a.n + n) * 2u : kOutOfRange);
+      bzw[slot][i] = load_b32(rz, v ? (grp * (uint32_t)(a.n >> 3) + (n >> 3)) * 4u : kOutOfRange);
+    }
+  };
+  // Dequantization operands of a register slot, one per packed chunk.
+  auto slot_params = [&](int slot, QuantParams (&qp)[BP]) {
+#pragma unroll
+    for (int i = 0; i < BP; ++i) qp[i] = make_params(zero_of(bzw[slot][i], (uint32_t)(n0 + b_col[i])), bsc[slot][i]);
+  };
+  // Word j of every chunk of a register slot -> fp16 buffer `buf` (chunk h*4 + j of the
+  // column's row); the four words of a block are spread over its four 16-wide K steps.
+  auto store_b_word = [&](int slot, int buf, int j, const QuantParams (&qp)[BP]) {
+#pragma unroll
+    for (int i = 0; i < BP; ++i) {
+      const int id = tid + i * C::kThreads;
+      if (id < C::kBChunks) {
+        h2 d[4];
+        dequant_word(braw[slot][i][j], qp[i], uc, d);
+        *reinterpret_cast<u4*>(b_lds + buf * C::kBStage + swz(b_col[i], (id & 1) * 4 + j)) =
+            u4{as_u32(d[0]), as_u32(d[1]), as_u32(d[2]), as_u32(d[3])};
+      }
+    }
+  };
+  auto store_b = [&](int slot, int buf) {
+    QuantParams qp[BP];
+    slot_params(slot, qp);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) store_b_word(slot, buf, j, qp);
+  };
+
+  f16v acc[TM][TN];
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+      for (int q = 0; q < 16; ++q) acc[tm][tn][q] = 0.0f;
+
+  const int a_row0 = wm * TM * 32 + (lane & 31);
+  const int b_row0 = wn * TN * 32 + (lane & 31);
+  // Operand fragments of the kk-th 16-wide K step: lane l holds row / column l % 32 and the
+  // 8 K values of chunk 2 kk + l / 32.
+  auto read_frags = [&](const uint8_t* A, const uint8_t* B, int kk, h8 (&af)[TM], h8 (&bf)[TN]) {
+    const int c = 2 * kk + (lane >> 5);
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm) af[tm] = *reinterpret_cast<const h8*>(A + swz(a_row0 + tm * 32, c));
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) bf[tn] = *reinterpret_cast<const h8*>(B + swz(b_row0 + tn * 32, c));
+  };
+  auto mfmas = [&](const h8 (&af)[TM], const h8 (&bf)[TN]) {
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn)
+        acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[tm], bf[tn], acc[tm][tn], 0, 0, 0);
+  };
+
+  // ---- prologue: x blocks kb0 .. kb0 + S - 2 in flight; block kb0 dequantized into buffer 0;
+  // the register slots hold blocks kb0 + 1 (slot 1) and kb0 + 2 (slot 0).
+#pragma unroll
+  for (int i = 0; i < S - 1; ++i) issue_a(kb0 + i, i);
+  __builtin_amdgcn_sched_barrier(0);
+  issue_b(kb0, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  issue_b(kb0 + 1, 1);
+  __builtin_amdgcn_sched_barrier(0);
+  store_b(0, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  issue_b(kb0 + 2, 0);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // One iteration; `odd` is (kb - kb0) & 1, compile-time so the register slots are static.
+  constexpr int kAfterA = C::kAfterA;
+  auto iteration = [&](int kb, int st, auto odd_tag) {
+    constexpr int odd = decltype(odd_tag)::value;
+    // Every wave's part of x block kb has landed in LDS and the B buffer of block kb is
+    // written; buffer odd ^ 1 and the stage read in the previous iteration are free.
+    block_barrier<kAfterA>();
+    issue_a(kb + S - 1, (st + S - 1) % S);
+    const uint8_t* A = a_lds + st * C::kAStage;
+    const uint8_t* B = b_lds + odd * C::kBStage;
+    // Fragments of step kk + 1 are read while the MFMAs of step kk run; one word of each
+    // chunk of block kb + 1 is dequantized into the other buffer per step.
+    h8 af[2][TM], bf[2][TN];
+    read_frags(A, B, 0, af[0], bf[0]);
+    QuantParams qp[BP];
+    slot_params(odd ^ 1, qp);
+#pragma unroll
+    for (int kk = 0; kk < kBK / 16; ++kk) {
+      if (kk + 1 < kBK / 16) read_frags(A, B, kk + 1, af[(kk + 1) & 1], bf[(kk + 1) & 1]);
+      mfmas(af[kk & 1], bf[kk & 1]);
+      store_b_word(odd ^ 1, odd ^ 1, kk, qp);  // block kb + 1
+    }
+    issue_b(kb + 3, odd ^ 1);
+  };
+
+  int kb = kb0;
+  int st = 0;  // stage of block kb; with S = 2 it equals (kb - kb0) & 1
+  for (; kb + 1 < kb1; kb += 2) {
+    iteration(kb, S == 2 ? 0 : st, std::integral_constant<int, 0>{});
+    st = (st + 1 == S) ? 0 : st + 1;
+    iteration(kb + 1, S == 2 ? 1 : st, std::integral_constant<int, 1>{});
+    st = (st + 1 == S) ? 0 : st + 1;
+  }
+  if (kb < kb1) iteration(kb, S == 2 ? 0 : st, std::integral_constant<int, 0>{});
+
+  // ---- epilogue. D layout of the 32x32 MFMA: register q of lane l is row
+  // 8 (q / 4) + 4 (l / 32) + q % 4, column l % 32.
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) {
+      const int n = n0 + (wn * TN + tn) * 32 + (lane & 31);
+      if (n >= a.n) continue;
+      const float b = (split_k == 1 && a.bias) ? half_bits_to_float(a.bias[n]) : 0.0f;
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const int m = m0 + (wm * TM + tm) * 32 + 8 * (q / 4) + 4 * (lane >> 5) + (q % 4);
+        if (m >= a.m) continue;
+        if (split_k == 1)
+          a.out[(int64_t)m * a.ldo + n] = __builtin_bit_cast(uint16_t, (_Float16)(acc[tm][tn][q] + b));
+        else
+          ws[((int64_t)z * a.m + m) * a.n + n] = acc[tm][tn][q];
+      }
+    }
+}
+
+int effective_split2(const LinearArgs& a, const tf_gemm_config& cfg) {
+  const int nkb = a.k / kBK;
+  return cfg.split_k < nkb ? cfg.split_k : (nkb > 0 ? nkb : 1);
+}
+
+int64_t gemm2_workspace(const LinearArgs& a, const tf_gemm_config& cfg) {
+  const int s = effective_split2(a, cfg);
+  return s > 1 ? (int64_t)s * a.m * a.n * (int64_t)sizeof(float) : 0;
+}
+
+template <int BM, int BN, int WM, int WN, int S>
+int launch_gemm2(const LinearArgs& a, const tf_gemm_config& cfg, float* ws, hipStream_t stream) {
+  using C = G2<BM, BN, WM, WN, S>;
+  if ((1 << a.log2g) < kBK)
+    return fail(TF_EINVAL, "tf_w4a16_linear: this gemm_mfma variant needs group_size >= 64 (block_k 64)");
+  const int64_t x_bytes = ((int64_t)(a.m - 1) * a.ldx + a.k) * 2;
+  const int64_t w_bytes = (int64_t)a.n * (a.k / 2);
+  if (x_bytes >= (int64_t)kOutOfRange || w_bytes >= (int64_t)kOutOfRange)
+    return fail(TF_EINVAL, "tf_w4a16_linear: this gemm_mfma variant needs x and qweight_t below 2 GiB");
+  const int split = effective_split2(a, cfg);
+  if (split > 1 && ws == nullptr) return fail(TF_EINVAL, "tf_w4a16_linear: split-K needs a workspace");
+  const int tiles_n = (int)cdiv(a.n, BN);
+  const int tiles_m = (int)cdiv(a.m, BM);
+  const int64_t grid = (int64_t)tiles_n * tiles_m * split;
+  if (grid > 0x7FFFFFFF) return fail(TF_EINVAL, "tf_w4a16_linear: too many tiles");
+  auto kernel = gemm2_kernel<BM, BN, WM, WN, S>;
+  if (C::kLds > 64 * 1024 &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          C::kLds) != hipSuccess)
+    return fail(TF_ELAUNCH, "tf_w4a16_linear: cannot reserve LDS for gemm_mfma");
+  kernel<<<(unsigned)grid, C::kThreads, C::kLds, stream>>>(a, ws, split, tiles_n, tiles_m);
+  if (int rc = check_launch("tf_w4a16_linear(gemm_mfma)")) return rc;
+  if (split > 1) return splitk_reduce(a, ws, split, stream);
+  return TF_OK;
+}
+
+// num_stages = S + 1 (3: two x stages, 4: three) tells these variants apart from the
+// two-buffer kernel (num_stages 2); num_warps = WM * WN.
+#define TF_GEMM2(BM, BN, WM, WN, S) \
+  {{TF_KERNEL_GEMM_MFMA, BM, BN, 64, 1, WM * WN, S + 1}, (launch_gemm2<BM, BN, WM, WN, S>), gemm2_workspace}
+
+const Variant kGemm2Variants[] = {
+    // four waves, three x stages
+    TF_GEMM2(256, 160, 4, 1, 3), TF_GEMM2(256, 128, 2, 2, 3), TF_GEMM2(128, 256, 2, 2, 3),
+    TF_GEMM2(128, 128, 2, 2, 3), TF_GEMM2(256, 192, 2, 2, 3), TF_GEMM2(256, 96, 4, 1, 3),
+    TF_GEMM2(64, 256, 1, 4, 3),  TF_GEMM2(128, 192, 2, 2, 3),
+    // eight waves (two per SIMD)
+    TF_GEMM2(256, 256, 4, 2, 2), TF_GEMM2(256, 192, 4, 2, 2), TF_GEMM2(256, 192, 4, 2, 3),
+    TF_GEMM2(256, 128, 4, 2, 2), TF_GEMM2(128, 256, 2, 4, 2), TF_GEMM2(256, 160, 8, 1, 2),
+};
+
+}  // namespace
+
+const Variant* gemm2_variants(int* count) {
+  *count = (int)(sizeof(kGemm2Variants) / sizeof(kGemm2Variants[0]));
+  return kGemm2Variants;
+}
+
+}  // namespace tf

@@ -9,12 +9,19 @@ struct Table {
   int n_gemv;
   const Variant* gemm;
   int n_gemm;
+  const Variant* gemm2;
+  int n_gemm2;
   Table() {
     gemv = gemv_variants(&n_gemv);
     gemm = gemm_variants(&n_gemm);
+    gemm2 = gemm2_variants(&n_gemm2);
   }
-  int size() const { return n_gemv + n_gemm; }
-  const Variant& at(int i) const { return i < n_gemv ? gemv[i] : gemm[i - n_gemv]; }
+  int size() const { return n_gemv + n_gemm + n_gemm2; }
+  const Variant& at(int i) const {
+    if (i < n_gemv) return gemv[i];
+    i -= n_gemv;
+    return i < n_gemm ? gemm[i] : gemm2[i - n_gemm];
+  }
 };
 
 const Table& table() {

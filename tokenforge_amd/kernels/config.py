@@ -20,7 +20,9 @@ gemv_dot   max M (1,2,4) / rows per     1 / waves per workgroup, each a K slice 
 gemv_mfma  M per tile (16,32) / rows    same as gemv_dot; block_k 128 stages x in LDS,
            per workgroup / 128 or 64    64 streams x from global memory
 gemm_mfma  LDS tile M / tile N / tile K K slices across workgroups (fp32 workspace,
-                                        fixed-order reduce) / 4 waves / 2 LDS buffers
+                                        fixed-order reduce) / 4 or 8 waves / 2: two LDS
+                                        buffers, 3 and 4: pipelined with 2 and 3 x stages
+                                        (block_k 64)
 ========== =========================== ================================================
 """
 
@@ -64,9 +66,18 @@ def _gemv_variants() -> list[tuple[str, int, int, int, int, int]]:
 
 
 def _gemm_variants() -> list[tuple[str, int, int, int, int, int]]:
+    # num_stages 2: two LDS buffers, operands staged through registers (any group size).
     tiles = [(64, 64, 64), (64, 128, 64), (128, 64, 64), (128, 128, 64), (128, 256, 64),
              (256, 128, 64), (256, 256, 64), (64, 64, 32), (128, 128, 32), (256, 128, 32)]
-    return [("gemm_mfma", bm, bn, bk, 4, 2) for bm, bn, bk in tiles]
+    out = [("gemm_mfma", bm, bn, bk, 4, 2) for bm, bn, bk in tiles]
+    # num_stages 3 / 4: pipelined form, x streamed into 2 / 3 LDS stages, weights prefetched two
+    # blocks ahead (block_k 64, group size 64 or 128); 4 or 8 waves.
+    tiles3 = [(256, 160), (256, 128), (128, 256), (128, 128), (256, 192), (256, 96), (64, 256), (128, 192)]
+    out += [("gemm_mfma", bm, bn, 64, 4, 4) for bm, bn in tiles3]
+    out += [("gemm_mfma", 256, 256, 64, 8, 3), ("gemm_mfma", 256, 192, 64, 8, 3),
+            ("gemm_mfma", 256, 192, 64, 8, 4), ("gemm_mfma", 256, 128, 64, 8, 3),
+            ("gemm_mfma", 128, 256, 64, 8, 3), ("gemm_mfma", 256, 160, 64, 8, 3)]
+    return out
 
 
 VARIANTS: tuple[tuple[str, int, int, int, int, int], ...] = tuple(_gemv_variants() + _gemm_variants())
