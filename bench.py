@@ -14,7 +14,9 @@ would) before anything is timed.
 
 ``value`` = algorithmic bytes of the K timed steps (micro.py:82-86 formula, summed over the
 four linears) / wall time of the K steps, in GB/s. The steps are replayed from a HIP graph
-so host launch overhead is not measured; inputs are resident in HBM.
+so host launch overhead is not measured; inputs are resident in HBM. Per-kernel figures
+(``per_shape``, ``gemm_m256``, ``rmsnorm_fp8``, ``gemm_sweep``) are the median over 5 replays
+of a graph of launches rotating over the cold copies.
 
 Extra objects on the same JSON line:
 * ``roofline``: the dominant kernel (gate_up GEMV, M=1): algorithmic bytes per launch / its
@@ -126,6 +128,13 @@ def capture(fns: list, warm: int = 4) -> tuple[torch.cuda.CUDAGraph, list]:  # t
     return graph, outs
 
 
+def median_replay_ms(graph: torch.cuda.CUDAGraph, launches: int, replays: int = 5) -> float:
+    """Median over ``replays`` replays of the per-launch milliseconds of a graph of ``launches``
+    launches (one untimed replay first)."""
+    time_graph(graph)
+    return statistics.median(time_graph(graph) / launches for _ in range(replays))
+
+
 def time_graph(graph: torch.cuda.CUDAGraph, reps: int = 1) -> float:
     """Milliseconds of ``reps`` replays, HIP events on the replay stream, synced both sides."""
     torch.cuda.synchronize()
@@ -156,8 +165,7 @@ def rmsnorm_bench(dev: torch.device) -> list[dict]:  # type: ignore[type-arg]
             x[:, outliers] *= 20
             xs.append(x.to(torch.float16))
         g, _ = capture([lambda x=x: rmsnorm_fp8_quant(x, gamma, 1e-6, None) for x in xs])
-        time_graph(g)
-        ms = min(time_graph(g) for _ in range(3)) / copies
+        ms = median_replay_ms(g, copies)
         nbytes = t * h * 2 + h * 2 + t * h + 4 * t
         gbps = nbytes / (ms * 1e-3) / 1e9
         res.append({"t": t, "h": h, "us": ms * 1e3, "gbps": gbps, "frac_hbm": gbps / HBM_PEAK_GBPS,
@@ -302,8 +310,7 @@ def main() -> int:
     reps = 4 * copies
     for i, (name, n, k) in enumerate(SHAPES):
         g, _ = capture([launcher(r % copies, i, xs, cfg1) for r in range(reps)])
-        time_graph(g)
-        ms = time_graph(g) / reps
+        ms = median_replay_ms(g, reps)
         gbps = bytes_moved(1, n, k) / (ms * 1e-3) / 1e9
         per_shape.append({"layer": name, "m": 1, "n": n, "k": k, "us": ms * 1e3, "gbps": gbps,
                           "frac_hbm": gbps / HBM_PEAK_GBPS, "config": cfg1[i].to_dict()})
@@ -318,8 +325,7 @@ def main() -> int:
         x256 = [None] * len(SHAPES)
         x256[i] = torch.randn((256, k), generator=gen, device=dev).to(torch.float16)
         g, _ = capture([launcher(r % copies, i, x256, [cfg] * len(SHAPES)) for r in range(2 * copies)])
-        time_graph(g)
-        ms = time_graph(g) / (2 * copies)
+        ms = median_replay_ms(g, 2 * copies)
         tflops = 2 * 256 * n * k / (ms * 1e-3) / 1e12
         gemm.append({"layer": name, "m": 256, "n": n, "k": k, "us": ms * 1e3, "tflops": tflops,
                      "frac_mfma": tflops / FP16_MFMA_PEAK_TFLOPS, "config": cfg.to_dict()})
@@ -339,8 +345,7 @@ def main() -> int:
                 xm = [None] * len(SHAPES)
                 xm[i] = torch.randn((m, k), generator=gen, device=dev).to(torch.float16)
                 g, _ = capture([launcher(r % copies, i, xm, [cfg] * len(SHAPES)) for r in range(copies)])
-                time_graph(g)
-                ms = min(time_graph(g) for _ in range(3)) / copies
+                ms = median_replay_ms(g, copies)
                 tflops = 2 * m * n * k / (ms * 1e-3) / 1e12
                 gbps = bytes_moved(m, n, k) / (ms * 1e-3) / 1e9
                 sweep.append({"layer": name, "m": m, "n": n, "k": k, "us": ms * 1e3, "tflops": tflops,
