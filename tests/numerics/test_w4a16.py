@@ -103,6 +103,13 @@ PATH_CONFIGS = [
     GemmConfig("gemm_mfma", 256, 128, 64, 2, 8, 3),
     GemmConfig("gemm_mfma", 128, 256, 64, 3, 8, 3),
     GemmConfig("gemm_mfma", 256, 160, 64, 1, 8, 3),
+    # skinny form (block_k 128): weights streamed into MFMA registers, x in LDS stages
+    GemmConfig("gemm_mfma", 16, 64, 128, 1, 4, 3),
+    GemmConfig("gemm_mfma", 32, 128, 128, 3, 4, 3),
+    GemmConfig("gemm_mfma", 64, 256, 128, 1, 4, 3),
+    GemmConfig("gemm_mfma", 128, 64, 128, 2, 4, 3),
+    GemmConfig("gemm_mfma", 64, 128, 128, 1, 4, 2),
+    GemmConfig("gemm_mfma", 128, 128, 128, 1, 4, 3),
 ]
 
 
@@ -149,6 +156,25 @@ def test_gemv_staging_windows(cfg: GemmConfig, device: torch.device) -> None:
     wd = cases.on_device(w, device)
     for m in _m_list(cfg):
         x = cases.activations(m, k, 3)
+        y = w4a16_gemm(x.to(device), wd.qweight_t, wd.scales, wd.qzeros, group, cfg)
+        _assert_close(y, x, w)
+
+
+@pytest.mark.parametrize("group", [32, 64, 128])
+@pytest.mark.parametrize(
+    "cfg",
+    [GemmConfig("gemm_mfma", 16, 64, 128, 1, 4, 3), GemmConfig("gemm_mfma", 64, 128, 128, 3, 4, 2),
+     GemmConfig("gemm_mfma", 128, 64, 128, 1, 4, 3)],
+    ids=_cfg_id,
+)
+def test_skinny_gemm_groups_and_partial_k(cfg: GemmConfig, group: int, device: torch.device) -> None:
+    """The skinny kernel reads each lane's group itself (any group size); for groups 32 and 64
+    K ends in a partial 128-wide step whose chunks past K read as zeros."""
+    n, k = 200, {32: 8288, 64: 8256, 128: 8320}[group]
+    w = cases.layer_weights(n, k, 4, group)
+    wd = cases.on_device(w, device)
+    for m in (16, 37, cfg.block_m + 3):
+        x = cases.activations(m, k, 4)
         y = w4a16_gemm(x.to(device), wd.qweight_t, wd.scales, wd.qzeros, group, cfg)
         _assert_close(y, x, w)
 

@@ -9,6 +9,7 @@ from hypothesis import strategies as st
 
 from tokenforge_amd.kernels import dispatch
 from tokenforge_amd.kernels.config import (
+    GEMM_MIN_M,
     GEMV_MAX_M,
     M_BUCKETS,
     VARIANTS,
@@ -67,7 +68,9 @@ def test_layer_support(n, k, group, dtype, arch, backend, expected) -> None:  # 
         (3, "triton", "hip_gemv", "4"),
         (4, "cuda", "hip_gemv", "4"),
         (5, "hip", "hip_gemv", "8"),
-        (32, "hip", "hip_gemv", "32"),
+        (8, "hip", "hip_gemv", "8"),
+        (9, "hip", "hip_gemm", "16"),  # bucket 16 starts the GEMM family
+        (32, "hip", "hip_gemm", "32"),
         (33, "hip", "hip_gemm", "64"),
         (128, "hip", "hip_gemm", "128"),
         (129, "hip", "hip_gemm", "256"),
@@ -141,7 +144,13 @@ def test_candidates_are_valid(bucket: int, group: int) -> None:
     for cfg in cands:
         cfg.validate(group)
         assert cfg.fits_bucket(bucket)
-    assert all(c.family == "gemv" for c in cands) == (bucket <= GEMV_MAX_M)
+    families = {c.family for c in cands}
+    if bucket < GEMM_MIN_M:
+        assert families == {"gemv"}
+    elif bucket > GEMV_MAX_M:
+        assert families == {"gemm"}
+    else:  # the tuner weighs both families where both serve
+        assert families == {"gemv", "gemm"}
 
 
 def test_decode_buckets_offer_both_gemv_kernels() -> None:

@@ -11,16 +11,21 @@ struct Table {
   int n_gemm;
   const Variant* gemm2;
   int n_gemm2;
+  const Variant* gemm3;
+  int n_gemm3;
   Table() {
     gemv = gemv_variants(&n_gemv);
     gemm = gemm_variants(&n_gemm);
     gemm2 = gemm2_variants(&n_gemm2);
+    gemm3 = gemm3_variants(&n_gemm3);
   }
-  int size() const { return n_gemv + n_gemm + n_gemm2; }
+  int size() const { return n_gemv + n_gemm + n_gemm2 + n_gemm3; }
   const Variant& at(int i) const {
     if (i < n_gemv) return gemv[i];
     i -= n_gemv;
-    return i < n_gemm ? gemm[i] : gemm2[i - n_gemm];
+    if (i < n_gemm) return gemm[i];
+    i -= n_gemm;
+    return i < n_gemm2 ? gemm2[i] : gemm3[i - n_gemm2];
   }
 };
 
@@ -48,7 +53,10 @@ int check_config(const tf_gemm_config& cfg, int32_t group_size) {
     return fail(TF_EINVAL, "tf_w4a16_linear: split_k must be in [1, 16]");
   if (cfg.kernel != TF_KERNEL_GEMM_MFMA && cfg.split_k != 1)
     return fail(TF_EINVAL, "tf_w4a16_linear: gemv kernels split K across waves (num_warps); split_k must be 1");
-  if (cfg.kernel == TF_KERNEL_GEMM_MFMA && (cfg.block_k > group_size || group_size % cfg.block_k))
+  // block_k 128 marks the skinny kernel (gemm3.hip), which reads each lane's group itself;
+  // the LDS-tile kernels need one scale per column and block.
+  if (cfg.kernel == TF_KERNEL_GEMM_MFMA && cfg.block_k != 128 &&
+      (cfg.block_k > group_size || group_size % cfg.block_k))
     return fail(TF_EINVAL, "tf_w4a16_linear: block_k must divide group_size");
   return TF_OK;
 }

@@ -22,7 +22,8 @@ gemv_mfma  M per tile (16,32) / rows    same as gemv_dot; block_k 128 stages x i
 gemm_mfma  LDS tile M / tile N / tile K K slices across workgroups (fp32 workspace,
                                         fixed-order reduce) / 4 or 8 waves / 2: two LDS
                                         buffers, 3 and 4: pipelined with 2 and 3 x stages
-                                        (block_k 64)
+                                        (block_k 64); block_k 128: skinny form, num_stages
+                                        = x stages
 ========== =========================== ================================================
 """
 
@@ -34,7 +35,9 @@ from typing import Any
 M_BUCKETS: tuple[int, ...] = (1, 2, 4, 8, 16, 32, 64, 128, 256, 512, 1024, 2048, 4096)
 MAX_BUCKET_M = M_BUCKETS[-1]
 GEMV_MAX_M = 32
-"""Buckets up to this M use the streaming (gemv) kernels; larger ones the LDS GEMM."""
+"""Largest bucket the streaming (gemv) kernels serve; by default larger ones use the GEMM."""
+GEMM_MIN_M = 16
+"""Smallest bucket the gemm_mfma kernels may serve (the tuner weighs both families at 16, 32)."""
 
 KERNELS: tuple[str, ...] = ("gemv_dot", "gemv_mfma", "gemm_mfma")
 NUM_CUS = 256
@@ -77,6 +80,11 @@ def _gemm_variants() -> list[tuple[str, int, int, int, int, int]]:
     out += [("gemm_mfma", 256, 256, 64, 8, 3), ("gemm_mfma", 256, 192, 64, 8, 3),
             ("gemm_mfma", 256, 192, 64, 8, 4), ("gemm_mfma", 256, 128, 64, 8, 3),
             ("gemm_mfma", 128, 256, 64, 8, 3), ("gemm_mfma", 256, 160, 64, 8, 3)]
+    # block_k 128: skinny form (M <= 128), weights streamed into MFMA registers, 4 waves,
+    # num_stages = x stages in LDS.
+    skinny = [(1, 1, 3), (1, 2, 3), (1, 4, 3), (2, 1, 3), (2, 2, 3), (2, 4, 3), (4, 1, 3), (4, 2, 3),
+              (4, 4, 3), (8, 1, 3), (8, 2, 3), (2, 2, 2), (4, 2, 2)]
+    out += [("gemm_mfma", 16 * mt, 64 * rt, 128, 4, st) for mt, rt, st in skinny]
     return out
 
 
@@ -96,8 +104,9 @@ def m_bucket(m: int) -> int:
 
 
 def family_for_bucket(bucket: int) -> str:
-    """``gemv`` for decode-shaped buckets, ``gemm`` for prefill-shaped ones."""
-    return "gemv" if bucket <= GEMV_MAX_M else "gemm"
+    """Default family of a bucket: ``gemv`` below GEMM_MIN_M, ``gemm`` from it on (the tuner
+    may still pick a gemv kernel up to GEMV_MAX_M)."""
+    return "gemv" if bucket < GEMM_MIN_M else "gemm"
 
 
 @dataclass(frozen=True)
@@ -115,6 +124,11 @@ class GemmConfig:
         return self.kernel
 
     @property
+    def skinny(self) -> bool:
+        """The skinny gemm_mfma form (block_k 128), which reads each lane's group itself."""
+        return self.kernel == "gemm_mfma" and self.block_k == 128
+
+    @property
     def family(self) -> str:
         return "gemm" if self.kernel == "gemm_mfma" else "gemv"
 
@@ -125,7 +139,7 @@ class GemmConfig:
         """Raise ``ValueError`` if this config cannot run for ``group_size``."""
         if self.kernel not in KERNELS:
             raise ValueError(f"kernel={self.kernel!r} not in {KERNELS}")
-        if self.kernel == "gemm_mfma" and (
+        if self.kernel == "gemm_mfma" and not self.skinny and (
             self.block_k <= 0 or self.block_k > group_size or group_size % self.block_k
         ):
             raise ValueError(f"block_k={self.block_k} must divide group_size={group_size}")
@@ -144,8 +158,12 @@ class GemmConfig:
             raise ValueError(f"{self.variant()} is not a compiled variant (block_m/block_n/block_k)")
 
     def fits_bucket(self, bucket: int) -> bool:
-        """Whether this config may serve M values of ``bucket`` (cache validation)."""
-        if family_for_bucket(bucket) != self.family:
+        """Whether this config may serve M values of ``bucket`` (cache validation): the gemv
+        kernels serve buckets up to GEMV_MAX_M (gemv_dot only up to its block_m), gemm_mfma
+        buckets from GEMM_MIN_M on."""
+        if self.family == "gemm":
+            return bucket >= GEMM_MIN_M
+        if bucket > GEMV_MAX_M:
             return False
         if self.kernel == "gemv_dot":
             return self.block_m >= bucket
@@ -180,20 +198,37 @@ def _pow2_at_most(v: int, cap: int) -> int:
 def default_config(bucket: int, n: int, k: int, group_size: int) -> GemmConfig:
     """Heuristic config used before tuning (config.py:71-92, re-derived for 256 CUs).
 
-    Streaming kernels: one workgroup per 32 output columns; add waves (on-chip K slices)
-    until the grid holds about 12 waves per CU, never more waves than 128-wide K steps.
-    LDS GEMM: tile by M, then split K across workgroups until the grid covers the CUs.
+    Streaming kernels (M < 16): one workgroup per 32 output columns; add waves (on-chip K
+    slices) until the grid holds about 12 waves per CU, never more waves than 128-wide K steps.
+    Skinny GEMM (16 <= M <= 128): 16-64 rows x 64 or 128 columns per workgroup, K split until
+    the grid holds about 1.5 workgroups per CU.
+    Pipelined GEMM (M >= 256, group >= 64): 256 x 192 tiles of 8 waves (256 x 256 from M 1024);
+    two-buffer GEMM for group 32.
     """
     if family_for_bucket(bucket) == "gemv":
-        bm = 16 if bucket <= 16 else 32
+        bm = 16
         tiles = -(-n // 32)
         k_steps = max(1, -(-k // 128))
         waves = _pow2_at_most(max(1, -(-(12 * NUM_CUS) // tiles)), min(16, k_steps))
-        if bm == 32:
-            waves = min(waves, 8)
-        block_n = 32 if bm == 16 else 16
         block_k = 128 if bucket <= 4 else 64  # stage x in LDS only while it is small
-        return GemmConfig("gemv_mfma", bm, block_n, block_k, 1, waves, 2)
+        return GemmConfig("gemv_mfma", bm, 32, block_k, 1, waves, 2)
+    if bucket <= 128:
+        bm = min(bucket, 64)
+        bn = 64 if bucket <= 64 else 128
+        tiles = -(-n // bn) * -(-bucket // bm)
+        k_steps = max(1, -(-k // 128))
+        split = 1
+        while tiles * split * 2 <= 3 * NUM_CUS and split * 2 <= min(8, k_steps):
+            split *= 2
+        return GemmConfig("gemm_mfma", bm, bn, 128, split, 4, 3)
+    if group_size >= 64:
+        bm, bn = (256, 192) if bucket <= 512 else (256, 256)
+        tiles = -(-n // bn) * -(-bucket // bm)
+        k_blocks = k // 64
+        split = 1
+        while tiles * split < NUM_CUS and split * 2 <= min(8, k_blocks):
+            split *= 2
+        return GemmConfig("gemm_mfma", bm, bn, 64, split, 8, 3)
     block_k = 64 if group_size >= 64 else 32
     if bucket <= 64:
         bm, bn = 64, 64
@@ -210,19 +245,19 @@ def default_config(bucket: int, n: int, k: int, group_size: int) -> GemmConfig:
 
 
 def candidate_configs(bucket: int, group_size: int) -> list[GemmConfig]:
-    """Autotune search space for one bucket: every compiled variant of the bucket's family."""
+    """Autotune search space for one bucket: every compiled variant that fits the bucket (both
+    families for buckets GEMM_MIN_M..GEMV_MAX_M)."""
     out: list[GemmConfig] = []
-    family = family_for_bucket(bucket)
     for kernel, bm, bn, bk, warps, stages in VARIANTS:
         cfg = GemmConfig(kernel, bm, bn, bk, 1, warps, stages)
         if not cfg.fits_bucket(bucket):
             continue
-        if family == "gemv":
+        if cfg.family == "gemv":
             if kernel == "gemv_mfma" and bm > 16 and bucket <= 16:
                 continue
             out.append(cfg)
             continue
-        if bk > group_size or group_size % bk:
+        if bk != 128 and (bk > group_size or group_size % bk):
             continue
         if bm > 2 * bucket:
             continue

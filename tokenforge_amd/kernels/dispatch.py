@@ -21,7 +21,7 @@ import os
 from dataclasses import dataclass
 from typing import Final, Literal, get_args
 
-from tokenforge_amd.kernels.config import GEMV_MAX_M, MAX_BUCKET_M, m_bucket
+from tokenforge_amd.kernels.config import MAX_BUCKET_M, family_for_bucket, m_bucket
 from tokenforge_amd.kernels.device import SUPPORTED_ARCHS
 from tokenforge_amd.kernels.metrics import FALLBACKS, KERNEL_CALLS
 from tokenforge_amd.kernels.pack import PACK_FACTOR, SUPPORTED_GROUP_SIZES
@@ -106,7 +106,7 @@ def select(m: int, *, backend: Backend, on_gpu: bool, hip_ok: bool) -> Decision:
             "(build it with `python -m tokenforge_amd.build`)"
         )
     bucket = bucket_label(m)
-    kernel: Kernel = "hip_gemv" if m <= GEMV_MAX_M else "hip_gemm"
+    kernel: Kernel = "hip_gemv" if family_for_bucket(lookup_bucket(m)) == "gemv" else "hip_gemm"
     return Decision(kernel, bucket)
 
 

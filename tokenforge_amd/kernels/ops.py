@@ -61,8 +61,9 @@ def w4a16_linear(
         on_gpu=x.is_cuda,
         hip_ok=hip_runnable(x2),
     )
-    dispatch.record(decision)
     cfg = autotune.lookup(_gpu_id(x.device), dispatch.lookup_bucket(m), n, k, group_size)
+    # The tuned config may pick the other family in the buckets both serve.
+    dispatch.record(dispatch.Decision("hip_gemm" if cfg.family == "gemm" else "hip_gemv", decision.bucket))
     y = _w4a16.w4a16_gemm(x2, qweight_t, scales, qzeros, group_size, cfg, bias)
     return y.reshape(out_shape)
 
