@@ -108,4 +108,6 @@ def test_torch_compile_fullgraph_no_graph_breaks(device: torch.device) -> None:
     KERNEL_CALLS.reset()
     x2 = cases.activations(17, 256, 3).to(device)
     assert torch.equal(compiled(x2), mod(x2))
-    assert KERNEL_CALLS.value(kernel="hip_gemv", bucket="32") == 2
+    # Bucket 32 is served by either family (the tuned config decides; untuned it is the GEMM).
+    calls = [KERNEL_CALLS.value(kernel=k, bucket="32") for k in ("hip_gemv", "hip_gemm")]
+    assert sum(calls) == 2
