@@ -110,6 +110,9 @@ PATH_CONFIGS = [
     GemmConfig("gemm_mfma", 128, 64, 128, 2, 4, 3),
     GemmConfig("gemm_mfma", 64, 128, 128, 1, 4, 2),
     GemmConfig("gemm_mfma", 128, 128, 128, 1, 4, 3),
+    # ... with two waves along M
+    GemmConfig("gemm_mfma", 256, 160, 128, 1, 4, 2),
+    GemmConfig("gemm_mfma", 256, 160, 128, 3, 4, 2),
 ]
 
 
@@ -164,7 +167,7 @@ def test_gemv_staging_windows(cfg: GemmConfig, device: torch.device) -> None:
 @pytest.mark.parametrize(
     "cfg",
     [GemmConfig("gemm_mfma", 16, 64, 128, 1, 4, 3), GemmConfig("gemm_mfma", 64, 128, 128, 3, 4, 2),
-     GemmConfig("gemm_mfma", 128, 64, 128, 1, 4, 3)],
+     GemmConfig("gemm_mfma", 128, 64, 128, 1, 4, 3), GemmConfig("gemm_mfma", 256, 160, 128, 2, 4, 2)],
     ids=_cfg_id,
 )
 def test_skinny_gemm_groups_and_partial_k(cfg: GemmConfig, group: int, device: torch.device) -> None:

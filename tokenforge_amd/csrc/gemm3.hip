@@ -1,12 +1,14 @@
-// Skinny W4A16 GEMM (16 <= M <= 128): weights streamed straight into MFMA operand registers.
+// Register-streamed W4A16 GEMM: weights go straight from memory into MFMA operand registers.
 //
 // For small M the weight stream is the cost, so the kernel is shaped like the decode GEMV
-// rather than like a tiled GEMM:
-//   * a workgroup of 4 waves covers BN = 4 * 16 * RT output columns and BM = 16 * MT rows of M;
-//     each wave owns 16 * RT columns and streams their packed weights, scales and zero
-//     points into a register ring (P steps of 128 K ahead), dequantizes each packed word once
-//     (fp16(q - z) * s, one rounding) straight into the B operand of v_mfma_f32_16x16x32_f16
-//     and reuses it for all MT row tiles;
+// rather than like a tiled GEMM; with waves along M the same structure serves larger M
+// without the dequantized-weight LDS buffer of the LDS-tile kernels:
+//   * a workgroup of 4 waves, WM along M and WN = 4 / WM along N, covers BM = WM * 16 * MT
+//     rows and BN = WN * 16 * RT columns; each wave owns 16 * MT rows and 16 * RT columns and
+//     streams the packed weights, scales and zero points of its columns into a register ring
+//     (P steps of 128 K ahead), dequantizes each packed word (fp16(q - z) * s, one rounding)
+//     straight into the B operand of v_mfma_f32_16x16x32_f16 and reuses it for its MT row
+//     tiles (the WM waves of a column set load and dequantize the same words);
 //   * the x tile [BM][128] of each step is shared by the 4 waves: it streams from global
 //     memory into S LDS stages through buffer loads with the LDS destination, issued S - 1
 //     steps ahead, with one barrier per step;
@@ -38,20 +40,25 @@ __device__ __forceinline__ uint32_t swz16(int row, int chunk) {
   return (uint32_t)(row * kStageRowChunks + (chunk ^ (row & 15))) * 16u;
 }
 
-template <int MT, int RT, int P, int S>
+template <int MT, int RT, int WM, int P, int S>
 struct G3 {
   static constexpr int kThreads = 256;
-  static constexpr int BM = 16 * MT;
-  static constexpr int BN = 64 * RT;
+  static constexpr int WN = 4 / WM;
+  static constexpr int BM = 16 * MT * WM;
+  static constexpr int BN = 16 * RT * WN;
   static constexpr int kStage = BM * kStepK * 2;  // bytes of one x stage
   static constexpr int kDmaPerWave = kStage / 1024 / 4;
   static constexpr int kLds = S * kStage;
   // VMEM issued after x step s (S - 1 iterations back) when iteration s waits for it:
-  // weights of step s - S + 1 + P, then S - 2 whole iterations (x step, weights).
+  // weights of step s - S + 1 + P, then S - 2 whole iterations (x step, weights). (The first
+  // iteration may have more in flight; its wait is then longer, never too short.)
   static constexpr int kAfterA = 3 * RT + (S - 2) * (kDmaPerWave + 3 * RT);
+  static_assert(WM == 1 || WM == 2 || WM == 4, "waves along M");
   static_assert(kDmaPerWave >= 1 && kStage % 4096 == 0, "x stage must split evenly over the waves");
   static_assert(S == 2 || S == 3, "x stages");
-  static_assert(P == 2, "register ring of two steps");
+  static_assert(P >= 2 && P <= 4, "register ring of two to four steps");
+  static_assert(kLds <= 160 * 1024, "x stages exceed the LDS");
+  static_assert(kAfterA < 64, "vmcnt range");
 };
 
 template <int N>
@@ -63,10 +70,10 @@ __device__ __forceinline__ void step_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-template <int MT, int RT, int P, int S>
+template <int MT, int RT, int WM, int P, int S>
 __global__ __launch_bounds__(256) void gemm3_kernel(LinearArgs a, float* __restrict__ ws, int split_k,
                                                     int tiles_n, int tiles_m) {
-  using C = G3<MT, RT, P, S>;
+  using C = G3<MT, RT, WM, P, S>;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
 
   const int tid = threadIdx.x;
@@ -74,13 +81,16 @@ __global__ __launch_bounds__(256) void gemm3_kernel(LinearArgs a, float* __restr
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 15;
   const int g = lane >> 4;
+  const int wm = wave / C::WN;
+  const int wn = wave % C::WN;
 
   const int per_split = tiles_n * tiles_m;
   const int t = xcd_tile(blockIdx.x, gridDim.x);
   const int z = t / per_split;
   const int r = t - z * per_split;
   const int m0 = (r % tiles_m) * C::BM;
-  const int n0 = (r / tiles_m) * C::BN + wave * 16 * RT;  // this wave's first column
+  const int n0 = (r / tiles_m) * C::BN + wn * 16 * RT;  // this wave's first column
+  const int wrow = wm * 16 * MT;                          // this wave's first row in the tile
 
   const int nchunks = a.k >> 5;
   const int nsteps = (nchunks + 3) >> 2;
@@ -108,7 +118,7 @@ __global__ __launch_bounds__(256) void gemm3_kernel(LinearArgs a, float* __restr
     x_k[i] = ch * 8;
     x_off[i] = m < a.m ? (uint32_t)(((int64_t)m * a.ldx + ch * 8) * 2) : kOutOfRange;
   }
-  auto issue_x = [&](int s, int st) {
+  auto issue_x = [&](int s, int st) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < C::kDmaPerWave; ++i) {
       const bool ok = s < s1 && s * kStepK + x_k[i] < a.k;
@@ -131,7 +141,7 @@ __global__ __launch_bounds__(256) void gemm3_kernel(LinearArgs a, float* __restr
   const int lane_end = min(s1, (nchunks - g + 3) >> 2);  // steps whose chunk g lies inside K
   u4 wraw[P][RT];
   uint32_t wsc[P][RT], wzw[P][RT];
-  auto issue_w = [&](int s, int slot) {
+  auto issue_w = [&](int s, int slot) __attribute__((always_inline)) {
     const bool ok = s < lane_end;
     const uint32_t grp = (uint32_t)((s * kStepK + g * 32) >> a.log2g);
 #pragma unroll
@@ -149,7 +159,7 @@ __global__ __launch_bounds__(256) void gemm3_kernel(LinearArgs a, float* __restr
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) acc[mt][rt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  auto compute = [&](int st, int slot) {
+  auto compute = [&](int st, int slot) __attribute__((always_inline)) {
     const uint8_t* X = smem + st * C::kStage;
     QuantParams qp[RT];
 #pragma unroll
@@ -158,7 +168,7 @@ __global__ __launch_bounds__(256) void gemm3_kernel(LinearArgs a, float* __restr
     for (int j = 0; j < 4; ++j) {
       h8 xa[MT];
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) xa[mt] = *reinterpret_cast<const h8*>(X + swz16(mt * 16 + c, g * 4 + j));
+      for (int mt = 0; mt < MT; ++mt) xa[mt] = *reinterpret_cast<const h8*>(X + swz16(wrow + mt * 16 + c, g * 4 + j));
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
         h2 wd[4];
@@ -171,34 +181,57 @@ __global__ __launch_bounds__(256) void gemm3_kernel(LinearArgs a, float* __restr
     }
   };
 
-  // ---- prologue: x steps s0 .. s0 + S - 2 in flight, weights of s0 (slot 0) and s0 + 1 (slot 1)
+  // ---- prologue: x steps s0 .. s0 + S - 2 in flight, weights of s0 + i in slot i (i < P)
 #pragma unroll
   for (int i = 0; i < S - 1; ++i) issue_x(s0 + i, i);
   __builtin_amdgcn_sched_barrier(0);
-  issue_w(s0, 0);
-  __builtin_amdgcn_sched_barrier(0);
-  issue_w(s0 + 1, 1);
-  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    issue_w(s0 + i, i);
+    __builtin_amdgcn_sched_barrier(0);
+  }
 
-  // Iteration s (slot = (s - s0) & 1, compile-time): wait for x step s, issue x step
-  // s + S - 1, multiply step s, issue the weights of step s + 2 into the freed slot.
-  auto iteration = [&](int s, int st, auto slot_tag) {
+  // Iteration s (slot = (s - s0) % P, compile-time): wait for x step s, issue x step
+  // s + S - 1, multiply step s, issue the weights of step s + P into the freed slot.
+  auto iteration = [&](int s, int st, auto slot_tag) __attribute__((always_inline)) {
     constexpr int slot = decltype(slot_tag)::value;
     step_barrier<C::kAfterA>();
     issue_x(s + S - 1, (st + S - 1) % S);
     compute(st, slot);
-    issue_w(s + 2, slot);
+    issue_w(s + P, slot);
   };
+  auto next_stage = [](int st) { return st + 1 == S ? 0 : st + 1; };
 
   int s = s0;
-  int st = 0;  // stage of step s; with S = 2 it equals (s - s0) & 1
-  for (; s + 1 < s1; s += 2) {
-    iteration(s, S == 2 ? 0 : st, std::integral_constant<int, 0>{});
-    st = (st + 1 == S) ? 0 : st + 1;
-    iteration(s + 1, S == 2 ? 1 : st, std::integral_constant<int, 1>{});
-    st = (st + 1 == S) ? 0 : st + 1;
+  int st = 0;  // stage of step s
+  for (; s + P - 1 < s1; s += P) {
+    iteration(s, st, std::integral_constant<int, 0>{});
+    st = next_stage(st);
+    iteration(s + 1, st, std::integral_constant<int, 1>{});
+    st = next_stage(st);
+    if constexpr (P > 2) {
+      iteration(s + 2, st, std::integral_constant<int, 2>{});
+      st = next_stage(st);
+    }
+    if constexpr (P > 3) {
+      iteration(s + 3, st, std::integral_constant<int, 3>{});
+      st = next_stage(st);
+    }
   }
-  if (s < s1) iteration(s, S == 2 ? 0 : st, std::integral_constant<int, 0>{});
+  // Fewer than P steps remain.
+  if (s < s1) {
+    iteration(s, st, std::integral_constant<int, 0>{});
+    st = next_stage(st);
+  }
+  if constexpr (P > 2) {
+    if (s + 1 < s1) {
+      iteration(s + 1, st, std::integral_constant<int, 1>{});
+      st = next_stage(st);
+    }
+  }
+  if constexpr (P > 3) {
+    if (s + 2 < s1) iteration(s + 2, st, std::integral_constant<int, 2>{});
+  }
 
   // ---- epilogue. D layout of v_mfma_f32_16x16x32_f16: lane holds rows 4 (lane / 16) + r,
   // column lane % 16.
@@ -211,7 +244,7 @@ __global__ __launch_bounds__(256) void gemm3_kernel(LinearArgs a, float* __restr
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int m = m0 + mt * 16 + 4 * g + q;
+        const int m = m0 + wrow + mt * 16 + 4 * g + q;
         if (m >= a.m) continue;
         if (split_k == 1)
           a.out[(int64_t)m * a.ldo + n] = __builtin_bit_cast(uint16_t, (_Float16)(acc[mt][rt][q] + b));
@@ -231,9 +264,9 @@ int64_t gemm3_workspace(const LinearArgs& a, const tf_gemm_config& cfg) {
   return s > 1 ? (int64_t)s * a.m * a.n * (int64_t)sizeof(float) : 0;
 }
 
-template <int MT, int RT, int P, int S>
+template <int MT, int RT, int WM, int P, int S>
 int launch_gemm3(const LinearArgs& a, const tf_gemm_config& cfg, float* ws, hipStream_t stream) {
-  using C = G3<MT, RT, P, S>;
+  using C = G3<MT, RT, WM, P, S>;
   const int64_t x_bytes = ((int64_t)(a.m - 1) * a.ldx + a.k) * 2;
   const int64_t w_bytes = (int64_t)a.n * (a.k / 2);
   if (x_bytes >= (int64_t)kOutOfRange || w_bytes >= (int64_t)kOutOfRange)
@@ -244,7 +277,7 @@ int launch_gemm3(const LinearArgs& a, const tf_gemm_config& cfg, float* ws, hipS
   const int tiles_m = (int)cdiv(a.m, C::BM);
   const int64_t grid = (int64_t)tiles_n * tiles_m * split;
   if (grid > 0x7FFFFFFF) return fail(TF_EINVAL, "tf_w4a16_linear: too many tiles");
-  auto kernel = gemm3_kernel<MT, RT, P, S>;
+  auto kernel = gemm3_kernel<MT, RT, WM, P, S>;
   if (C::kLds > 64 * 1024 &&
       hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
                           C::kLds) != hipSuccess)
@@ -256,14 +289,18 @@ int launch_gemm3(const LinearArgs& a, const tf_gemm_config& cfg, float* ws, hipS
 }
 
 // block_k 128 (one 128-wide step per barrier) tells these variants apart from the LDS-tile
-// kernels; num_stages = S (x stages).
+// kernels; num_stages = S (x stages). TF_GEMM3: one wave along M; TF_GEMM3W: WM waves along
+// M (its tile shapes do not occur among the one-wave variants).
 #define TF_GEMM3(MT, RT, S) \
-  {{TF_KERNEL_GEMM_MFMA, 16 * MT, 64 * RT, 128, 1, 4, S}, (launch_gemm3<MT, RT, 2, S>), gemm3_workspace}
+  {{TF_KERNEL_GEMM_MFMA, 16 * MT, 64 * RT, 128, 1, 4, S}, (launch_gemm3<MT, RT, 1, 2, S>), gemm3_workspace}
+#define TF_GEMM3W(MT, RT, WM, S)                                                                  \
+  {{TF_KERNEL_GEMM_MFMA, 16 * MT * WM, 16 * RT * (4 / WM), 128, 1, 4, S}, (launch_gemm3<MT, RT, WM, 2, S>), \
+   gemm3_workspace}
 
 const Variant kGemm3Variants[] = {
     TF_GEMM3(1, 1, 3), TF_GEMM3(1, 2, 3), TF_GEMM3(1, 4, 3), TF_GEMM3(2, 1, 3), TF_GEMM3(2, 2, 3),
     TF_GEMM3(2, 4, 3), TF_GEMM3(4, 1, 3), TF_GEMM3(4, 2, 3), TF_GEMM3(4, 4, 3), TF_GEMM3(8, 1, 3),
-    TF_GEMM3(8, 2, 3), TF_GEMM3(2, 2, 2), TF_GEMM3(4, 2, 2),
+    TF_GEMM3(8, 2, 3), TF_GEMM3(2, 2, 2), TF_GEMM3(4, 2, 2), TF_GEMM3W(8, 5, 2, 2),
 };
 
 }  // namespace

@@ -85,6 +85,8 @@ def _gemm_variants() -> list[tuple[str, int, int, int, int, int]]:
     skinny = [(1, 1, 3), (1, 2, 3), (1, 4, 3), (2, 1, 3), (2, 2, 3), (2, 4, 3), (4, 1, 3), (4, 2, 3),
               (4, 4, 3), (8, 1, 3), (8, 2, 3), (2, 2, 2), (4, 2, 2)]
     out += [("gemm_mfma", 16 * mt, 64 * rt, 128, 4, st) for mt, rt, st in skinny]
+    # ... and with two waves along M: 256 x 160 tiles (gate_up at M >= 256: 237 tiles).
+    out += [("gemm_mfma", 256, 160, 128, 4, 2)]
     return out
 
 
