@@ -1,6 +1,6 @@
 """Benchmark of the MI355X quantized-linear hot path (the round driver's bench contract).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-tune] [--no-cpu] [--detail PATH] [--full]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-tune] [--no-cpu] [--detail PATH] [--full] [--stack]
     python bench.py --traffic-probe      (eager launches for rocprofv3 --pmc, see below)
 
 Workload (BASELINE.json metric "W4A16 GEMV HBM GB/s at M=1 + GEMM TFLOP/s at M=256"):
@@ -34,6 +34,13 @@ Extra objects on the same JSON line:
   {1, 16, 512, 4096}; algorithmic bytes T*H*2 + H*2 + T*H + 4*T over rotating cold inputs.
 * with ``--full`` only (written to ``--detail``): ``gemm_sweep``, configs[3]: M in
   {16, 32, 64, 128, 256, 1024, 4096} on gate_up and down, each bucket autotuned first.
+* ``stack``: 28 Qwen2.5-7B decoder layers of distinct synthetic weights (3.39 GB
+  int4 + scales + zeros; qkv with an fp16 bias), one pass per step: RMSNorm + FP8 -> fp16(q *
+  scale) -> qkv -> attention as identity on the value slice (query head h takes KV group
+  h // 7) -> o_proj -> residual add -> RMSNorm + FP8 -> fp16(q * scale) -> gate_up -> SiLU(gate)
+  * up -> down -> residual add. The linears and the norms are this library's kernels, the
+  glue is torch; a pass is one HIP graph, tokens/s = M / time per pass. M=1 on every run;
+  ``--stack`` or ``--full`` add M in {8, 32} (decode) and 2048 (prefill).
 * ``cpu_baseline``: reference.py's CPU path (dequantize per call + fp32 matmul), restated in
   torch on the host cores, on a bounded sample of the same step.
 """
@@ -175,6 +182,77 @@ def rmsnorm_bench(dev: torch.device) -> list[dict]:  # type: ignore[type-arg]
     return res
 
 
+STACK_LAYERS = 28
+HEAD_DIM = 128
+KV_HEADS = 4
+
+
+def stack_bench(dev: torch.device, gpu: str, ms: tuple[int, ...], tune: bool) -> list[dict]:  # type: ignore[type-arg]
+    """tokens/s of one pass through 28 decoder layers, per M (module docstring)."""
+    from tokenforge_amd.kernels import autotune
+
+    eps = 1e-6
+    h = SHAPES[1][1]
+    inter = SHAPES[2][1] // 2
+    layers = []
+    total = 0
+    for li in range(STACK_LAYERS):
+        ws = [make_layer(n, k, dev, seed=50_000 + 10 * li + i)[:3] for i, (_, n, k) in enumerate(SHAPES)]
+        gen = torch.Generator(device=dev).manual_seed(60_000 + li)
+        bias = (torch.randn((SHAPES[0][1],), generator=gen, device=dev) * 0.1).to(torch.float16)
+        g1 = (1 + 0.1 * torch.randn((h,), generator=gen, device=dev)).to(torch.float16)
+        g2 = (1 + 0.1 * torch.randn((h,), generator=gen, device=dev)).to(torch.float16)
+        layers.append((ws, bias, g1, g2))
+        total += sum(t.numel() * t.element_size() for w in ws for t in w)
+    if tune:
+        for _, n, k in SHAPES:
+            autotune.tune_layer(n, k, GROUP, device=dev, gpu=gpu, buckets=tuple(sorted(set(ms))))
+    ops = torch.ops.tokenforge
+    q_width = SHAPES[0][1] - 2 * KV_HEADS * HEAD_DIM  # 3584 query columns, then k and v
+
+    def layer_pass(x: torch.Tensor, layer: tuple) -> torch.Tensor:  # type: ignore[type-arg]
+        (qkv, o, gu, down), bias, g1, g2 = layer
+        m = x.shape[0]
+        q8, s = ops.rmsnorm_fp8_quant(x, g1, eps, None)
+        a = (q8.to(torch.float32) * s).to(torch.float16)
+        y = ops.w4a16_linear(a, *qkv, bias, GROUP, "hip")
+        v = y[:, q_width + KV_HEADS * HEAD_DIM:].reshape(m, KV_HEADS, 1, HEAD_DIM)
+        attn = v.expand(m, KV_HEADS, h // (KV_HEADS * HEAD_DIM), HEAD_DIM).reshape(m, h)
+        x = x + ops.w4a16_linear(attn, *o, None, GROUP, "hip")
+        q8, s = ops.rmsnorm_fp8_quant(x, g2, eps, None)
+        a = (q8.to(torch.float32) * s).to(torch.float16)
+        y = ops.w4a16_linear(a, *gu, None, GROUP, "hip")
+        act = torch.nn.functional.silu(y[:, :inter]) * y[:, inter:]
+        return x + ops.w4a16_linear(act, *down, None, GROUP, "hip")
+
+    res = []
+    gen = torch.Generator(device=dev).manual_seed(11)
+    for m in ms:
+        x0 = torch.randn((m, h), generator=gen, device=dev).to(torch.float16)
+
+        def full_pass(x0: torch.Tensor = x0) -> torch.Tensor:
+            x = x0
+            for layer in layers:
+                x = layer_pass(x, layer)
+            return x
+
+        g, outs = capture([full_pass], warm=1)
+        ms_pass = median_replay_ms(g, 1)  # replays the graph: outs[0] holds the pass's output
+        if not bool(torch.isfinite(outs[0]).all()):
+            raise RuntimeError(f"stack pass at M={m} produced non-finite values")
+        step_bytes = sum(bytes_moved(m, n, k) for _, n, k in SHAPES) * STACK_LAYERS
+        flops = 2 * m * sum(n * k for _, n, k in SHAPES) * STACK_LAYERS
+        res.append({"m": m, "layers": STACK_LAYERS, "ms_per_pass": ms_pass, "tokens_per_s": m / (ms_pass * 1e-3),
+                    "linear_gbps": step_bytes / (ms_pass * 1e-3) / 1e9,
+                    "linear_tflops": flops / (ms_pass * 1e-3) / 1e12, "weight_bytes": total})
+        log(f"  stack M={m:<5d} {ms_pass * 1e3:9.1f} us/pass {m / (ms_pass * 1e-3):9.0f} tok/s "
+            f"({step_bytes / (ms_pass * 1e-3) / 1e9:.0f} GB/s of linear bytes)")
+        del g, outs
+    del layers
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(layers: list, budget_s: float = 12.0) -> dict:  # type: ignore[type-arg]
     """reference.py:24-32 restated in torch on the host cores, one decode step (M=1)."""
     from oracle.cpu_path import w4a16_torch_cpu
@@ -218,6 +296,8 @@ def main() -> int:
     ap.add_argument("--detail", type=str, default=None, help="write per-shape details as JSON")
     ap.add_argument("--full", action="store_true",
                     help="also sweep the GEMM over M in {16..4096} (configs[3]) into --detail")
+    ap.add_argument("--stack", action="store_true",
+                    help="stack (configs[4]) also at M in {8, 32, 2048}, not only M=1")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="eager gate_up GEMV launches + a calibration kernel, for rocprofv3 --pmc")
     args = ap.parse_args()
@@ -354,6 +434,8 @@ def main() -> int:
                 log(f"  {name:13s} M={m:<5d} {ms * 1e3:9.2f} us {tflops:7.1f} TFLOP/s {gbps:7.0f} GB/s  {cfg}")
                 del g, xm
 
+    stack = stack_bench(dev, gpu, (1, 8, 32, 2048) if (args.stack or args.full) else (1,), not args.no_tune)
+
     cpu = None
     if not args.no_cpu:
         t0 = time.perf_counter()
@@ -398,6 +480,7 @@ def main() -> int:
         "rmsnorm_fp8": norm,
         "repack_gate_up_gbps": (gate_n * gate_k) / (rep_ms * 1e-3) / 1e9,
         "per_shape": per_shape,
+        "stack": stack,
         "cpu_baseline": cpu,
         "gpu": gpu,
     }

@@ -182,6 +182,38 @@ def test_skinny_gemm_groups_and_partial_k(cfg: GemmConfig, group: int, device: t
         _assert_close(y, x, w)
 
 
+@pytest.mark.parametrize(
+    ("m", "cfg"),
+    [
+        (32, GemmConfig("gemm_mfma", 32, 128, 128, 1, 4, 2)),
+        (32, GemmConfig("gemm_mfma", 32, 128, 128, 8, 4, 3)),
+        (256, GemmConfig("gemm_mfma", 32, 64, 128, 8, 4, 3)),
+        (256, GemmConfig("gemm_mfma", 256, 160, 128, 1, 4, 2)),
+        (256, GemmConfig("gemm_mfma", 256, 192, 64, 1, 8, 3)),
+    ],
+    ids=lambda v: _cfg_id(v) if isinstance(v, GemmConfig) else f"m{v}",
+)
+def test_staged_x_waits_at_full_size(m: int, cfg: GemmConfig, device: torch.device) -> None:
+    """Regression: the x tile streams into LDS stages and each barrier waits for a counted
+    number of later loads; when the compiler moved weight loads above the x loads of a step,
+    some workgroups read a stage before it landed (wrong rows, varying run to run). Full
+    gate_up width, three runs: bit-identical to each other and close to an fp32 product of
+    the exact dequantized weights."""
+    from tokenforge_amd.kernels.autotune import synthetic_layer
+
+    n, k = 37888, 3584
+    qweight_t, scales, qzeros = synthetic_layer(n, k, G, device, seed=5)
+    gen = torch.Generator(device=device).manual_seed(6)
+    x = torch.randn((m, k), generator=gen, device=device).to(torch.float16)
+    wt = w4a16_dequant(qweight_t, scales, qzeros, G).float().t().contiguous()
+    ref = x.float() @ wt
+    runs = [w4a16_gemm(x, qweight_t, scales, qzeros, G, cfg) for _ in range(3)]
+    for y in runs[1:]:
+        assert torch.equal(y, runs[0]), "results differ between runs"
+    rel = float((runs[0].float() - ref).abs().max()) / float(ref.abs().max())
+    assert rel <= 2e-3, f"max error {rel:.3e} of max |y|"
+
+
 @pytest.mark.parametrize("group_size", [32, 64])
 def test_small_group_sizes(group_size: int, device: torch.device) -> None:
     n, k = 96, 384

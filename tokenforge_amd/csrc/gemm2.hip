@@ -236,6 +236,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm2_kernel(LinearArgs a, float
     // written; buffer odd ^ 1 and the stage read in the previous iteration are free.
     block_barrier<kAfterA>();
     issue_a(kb + S - 1, (st + S - 1) % S);
+    // The waits count the loads issued after each x block: no later load may move above it.
+    __builtin_amdgcn_sched_barrier(0);
     const uint8_t* A = a_lds + st * C::kAStage;
     const uint8_t* B = b_lds + odd * C::kBStage;
     // Fragments of step kk + 1 are read while the MFMAs of step kk run; one word of each

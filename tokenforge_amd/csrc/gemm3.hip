@@ -197,6 +197,8 @@ __global__ __launch_bounds__(256) void gemm3_kernel(LinearArgs a, float* __restr
     constexpr int slot = decltype(slot_tag)::value;
     step_barrier<C::kAfterA>();
     issue_x(s + S - 1, (st + S - 1) % S);
+    // The waits count the loads issued after each x step: no later load may move above it.
+    __builtin_amdgcn_sched_barrier(0);
     compute(st, slot);
     issue_w(s + P, slot);
   };
