@@ -33,7 +33,10 @@ Extra objects on the same JSON line:
   channels x20, gamma = 1 + 0.1 N(0,1), eps 1e-6, dynamic per-token scale) at T in
   {1, 16, 512, 4096}; algorithmic bytes T*H*2 + H*2 + T*H + 4*T over rotating cold inputs.
 * with ``--full`` only (written to ``--detail``): ``gemm_sweep``, configs[3]: M in
-  {16, 32, 64, 128, 256, 1024, 4096} on gate_up and down, each bucket autotuned first.
+  {16, 32, 64, 128, 256, 1024, 4096} on gate_up and down, each bucket autotuned first; and
+  ``vendor_fp16_gemm``, the vendor's dense fp16 GEMM (torch.matmul, hipBLASLt) on the same
+  shapes at M in {256, 1024, 4096} with fp16 weights, as a reference point for the MFMA
+  fraction this box reaches on these shapes.
 * ``stack``: 28 Qwen2.5-7B decoder layers of distinct synthetic weights (3.39 GB
   int4 + scales + zeros; qkv with an fp16 bias), one pass per step: RMSNorm + FP8 -> fp16(q *
   scale) -> qkv -> attention as identity on the value slice (query head h takes KV group
@@ -434,6 +437,24 @@ def main() -> int:
                 log(f"  {name:13s} M={m:<5d} {ms * 1e3:9.2f} us {tflops:7.1f} TFLOP/s {gbps:7.0f} GB/s  {cfg}")
                 del g, xm
 
+    vendor = None
+    if args.full:
+        vendor = []
+        for i in (2, 3):
+            name, n, k = SHAPES[i]
+            wt = (torch.randn((k, n), generator=gen, device=dev) * 0.03).to(torch.float16)
+            for m in (256, 1024, 4096):
+                xm = torch.randn((m, k), generator=gen, device=dev).to(torch.float16)
+                om = torch.empty((m, n), device=dev, dtype=torch.float16)
+                g, _ = capture([lambda xm=xm, om=om: torch.matmul(xm, wt, out=om)] * 8, warm=2)
+                ms = median_replay_ms(g, 8)
+                tflops = 2 * m * n * k / (ms * 1e-3) / 1e12
+                vendor.append({"layer": name, "m": m, "n": n, "k": k, "us": ms * 1e3, "tflops": tflops,
+                               "frac_mfma": tflops / FP16_MFMA_PEAK_TFLOPS})
+                log(f"  vendor fp16   {name:13s} M={m:<5d} {ms * 1e3:9.2f} us {tflops:7.1f} TFLOP/s")
+                del g, xm, om
+            del wt
+
     stack = stack_bench(dev, gpu, (1, 8, 32, 2048) if (args.stack or args.full) else (1,), not args.no_tune)
 
     cpu = None
@@ -485,7 +506,7 @@ def main() -> int:
         "gpu": gpu,
     }
     if args.detail:
-        detail = dict(result, gemm_sweep=sweep) if sweep is not None else result
+        detail = dict(result, gemm_sweep=sweep, vendor_fp16_gemm=vendor) if sweep is not None else result
         Path(args.detail).parent.mkdir(parents=True, exist_ok=True)
         Path(args.detail).write_text(json.dumps(detail, indent=1) + "\n")
     print(json.dumps(result), flush=True)

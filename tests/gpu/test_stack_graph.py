@@ -1,0 +1,79 @@
+"""A decoder-layer stack of the library's ops, captured in one HIP graph: every replay equals
+the eager pass bit for bit, with eager work on other inputs between replays (the split-K
+reductions are fixed-order and no kernel depends on launch timing).
+
+Layers at the Qwen2.5-7B shapes (qkv 4608x3584 with bias, o_proj, gate_up 37888x3584, down
+3584x18944), RMSNorm + FP8 in front of qkv and gate_up, fp16(q * scale) as the linear input,
+attention as the identity on the value slice, SiLU(gate) * up, residual adds. Configs are
+the library defaults for each M (the GEMV, register-streamed and pipelined GEMM families).
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import tokenforge_amd.kernels.ops  # noqa: F401  (registers torch.ops.tokenforge)
+from tokenforge_amd.kernels.autotune import synthetic_layer
+
+pytestmark = pytest.mark.gpu
+G = 128
+H, QKV, INTER = 3584, 4608, 18944
+SHAPES = [(QKV, H), (H, H), (2 * INTER, H), (H, INTER)]
+
+
+def _layers(device: torch.device, count: int) -> list:  # type: ignore[type-arg]
+    out = []
+    for li in range(count):
+        ws = [synthetic_layer(n, k, G, device, seed=100 * li + i) for i, (n, k) in enumerate(SHAPES)]
+        gen = torch.Generator(device=device).manual_seed(7 + li)
+        bias = (0.1 * torch.randn((QKV,), generator=gen, device=device)).to(torch.float16)
+        g1 = (1 + 0.1 * torch.randn((H,), generator=gen, device=device)).to(torch.float16)
+        g2 = (1 + 0.1 * torch.randn((H,), generator=gen, device=device)).to(torch.float16)
+        out.append((ws, bias, g1, g2))
+    return out
+
+
+def _pass(x: torch.Tensor, layers: list) -> torch.Tensor:  # type: ignore[type-arg]
+    ops = torch.ops.tokenforge
+    m = x.shape[0]
+    for (qkv, o, gu, down), bias, g1, g2 in layers:
+        q8, s = ops.rmsnorm_fp8_quant(x, g1, 1e-6, None)
+        a = (q8.to(torch.float32) * s).to(torch.float16)
+        y = ops.w4a16_linear(a, *qkv, bias, G, "hip")
+        v = y[:, QKV - 512:].reshape(m, 4, 1, 128)
+        attn = v.expand(m, 4, 7, 128).reshape(m, H)
+        x = x + ops.w4a16_linear(attn, *o, None, G, "hip")
+        q8, s = ops.rmsnorm_fp8_quant(x, g2, 1e-6, None)
+        a = (q8.to(torch.float32) * s).to(torch.float16)
+        y = ops.w4a16_linear(a, *gu, None, G, "hip")
+        act = torch.nn.functional.silu(y[:, :INTER]) * y[:, INTER:]
+        x = x + ops.w4a16_linear(act, *down, None, G, "hip")
+    return x
+
+
+@pytest.mark.parametrize("m", [1, 24, 300])
+def test_stack_replay_is_bit_identical_to_eager(m: int, device: torch.device) -> None:
+    layers = _layers(device, 2)
+    gen = torch.Generator(device=device).manual_seed(m)
+    x = torch.randn((m, H), generator=gen, device=device).to(torch.float16)
+    other = torch.randn((m, H), generator=gen, device=device).to(torch.float16)
+    eager = _pass(x, layers)
+    assert bool(torch.isfinite(eager).all())
+
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        _pass(x, layers)  # warm-up on the capture stream
+        stream.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            out = _pass(x, layers)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), "graph replay differs from the eager pass"
+        _pass(other, layers)  # eager work between replays
+        torch.cuda.synchronize()
