@@ -112,6 +112,35 @@ int tf_w4a16_linear(const uint16_t* x, int64_t ldx, const int32_t* qweight_t,
                     int32_t group_size, const tf_gemm_config* cfg, float* workspace,
                     int64_t workspace_bytes, void* stream);
 
+/* Fused epilogues of the linear. No counterpart in the reference, which runs these as
+ * separate torch ops after the linear; for callers that would otherwise round-trip [m, n]
+ * through memory between the linear and the next elementwise op.
+ *   TF_EPILOGUE_NONE      out[m][n] = y[m][n]                           (tf_w4a16_linear)
+ *   TF_EPILOGUE_RESIDUAL  out[m][n] = fp16(residual[m][n] + fp16(y[m][n]))
+ *                         residual fp16 [m, n] with row stride ldr; out may be residual
+ *                         itself (same pointer and stride), nothing else may overlap.
+ *   TF_EPILOGUE_SILU_MUL  out[m][j] = fp16(fp16(silu(fp16(y[m][j]))) * fp16(y[m][n/2 + j]))
+ *                         for j < n/2 (gate columns first, then up); n a multiple of 16;
+ *                         silu(v) = v / (1 + exp(-v)) in fp32.
+ * Each equals the unfused torch composition on fp16 tensors (the same roundings). */
+#define TF_EPILOGUE_NONE 0
+#define TF_EPILOGUE_RESIDUAL 1
+#define TF_EPILOGUE_SILU_MUL 2
+
+/* Workspace bytes of tf_w4a16_linear_ex (the LDS-tile GEMMs reduce a SiLU*mul epilogue
+ * through fp32 partials even without split-K). */
+int64_t tf_w4a16_workspace_bytes_ex(int64_t m, int64_t n, int64_t k, int32_t group_size,
+                                    const tf_gemm_config* cfg, int32_t epilogue);
+
+/* tf_w4a16_linear with an epilogue (see above); residual and ldr only for
+ * TF_EPILOGUE_RESIDUAL. */
+int tf_w4a16_linear_ex(const uint16_t* x, int64_t ldx, const int32_t* qweight_t,
+                       const uint16_t* scales, const int32_t* qzeros, const uint16_t* bias,
+                       uint16_t* out, int64_t ldo, int64_t m, int64_t n, int64_t k,
+                       int32_t group_size, const tf_gemm_config* cfg, int32_t epilogue,
+                       const uint16_t* residual, int64_t ldr, float* workspace,
+                       int64_t workspace_bytes, void* stream);
+
 /* --------------------------------------------------------------- RMSNorm + FP8 */
 
 /* rmsnorm_fp8.py:76-117 rmsnorm_fp8_quant (semantics of reference.py:35-56):

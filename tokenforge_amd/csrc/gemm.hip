@@ -158,45 +158,60 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(LinearArgs a, float*
   }
 
   // D layout of the 32x32 MFMA: register r of lane l is row 8*(r/4) + 4*(l/32) + r%4,
-  // column l%32.
+  // column l%32. A SiLU*mul epilogue pairs columns n and n + N/2 of different tiles, so it
+  // goes through fp32 partials and the reduce kernel, like split-K.
+  const bool partials = split_k > 1 || a.epilogue == TF_EPILOGUE_SILU_MUL;
 #pragma unroll
   for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
     for (int tn = 0; tn < TN; ++tn) {
       const int n = n0 + (wn * TN + tn) * 32 + (lane & 31);
       if (n >= a.n) continue;
-      const float b = (split_k == 1 && a.bias) ? half_bits_to_float(a.bias[n]) : 0.0f;
+      const float b = (!partials && a.bias) ? half_bits_to_float(a.bias[n]) : 0.0f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int m = m0 + (wm * TM + tm) * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
         if (m >= a.m) continue;
-        if (split_k == 1)
-          a.out[(int64_t)m * a.ldo + n] = __builtin_bit_cast(uint16_t, (_Float16)(acc[tm][tn][r] + b));
+        if (!partials)
+          store_out(a, m, n, acc[tm][tn][r] + b);
         else
           ws[((int64_t)z * a.m + m) * a.n + n] = acc[tm][tn][r];
       }
     }
 }
 
-__global__ void splitk_reduce_kernel(const float* __restrict__ ws, const uint16_t* __restrict__ bias,
-                                     uint16_t* __restrict__ out, int64_t ldo, int m, int n, int split) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t total = (int64_t)m * n;
-  if (i >= total) return;
-  const int64_t row = i / n;
-  const int64_t col = i % n;
+// Sum of the split partials of element (row, col) in split order, plus bias.
+__device__ __forceinline__ float reduce_partials(const float* __restrict__ ws, const uint16_t* __restrict__ bias,
+                                                 int64_t total, int64_t i, int64_t col, int split) {
   float v = ws[i];
   for (int s = 1; s < split; ++s) v += ws[(int64_t)s * total + i];
   if (bias) v += half_bits_to_float(bias[col]);
-  out[row * ldo + col] = __builtin_bit_cast(uint16_t, (_Float16)v);
+  return v;
+}
+
+// One thread per output element; under SiLU*mul the output has N/2 columns and each thread
+// reduces its gate column j and up column N/2 + j.
+__global__ void splitk_reduce_kernel(LinearArgs a, const float* __restrict__ ws, int split) {
+  const int n_out = a.epilogue == TF_EPILOGUE_SILU_MUL ? a.n >> 1 : a.n;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)a.m * n_out) return;
+  const int64_t row = i / n_out;
+  const int64_t col = i % n_out;
+  const int64_t total = (int64_t)a.m * a.n;
+  const float v = reduce_partials(ws, a.bias, total, row * a.n + col, col, split);
+  if (a.epilogue == TF_EPILOGUE_SILU_MUL) {
+    const float u = reduce_partials(ws, a.bias, total, row * a.n + n_out + col, n_out + col, split);
+    a.out[row * a.ldo + col] = finish_silu_mul(v, u);
+  } else {
+    store_out(a, (int)row, (int)col, v);
+  }
 }
 
 }  // namespace
 
 int splitk_reduce(const LinearArgs& a, const float* ws, int split, hipStream_t stream) {
-  const int64_t total = (int64_t)a.m * a.n;
-  splitk_reduce_kernel<<<(unsigned)cdiv(total, 256), 256, 0, stream>>>(ws, a.bias, a.out, a.ldo, a.m, a.n,
-                                                                      split);
+  const int64_t total = (int64_t)a.m * (a.epilogue == TF_EPILOGUE_SILU_MUL ? a.n >> 1 : a.n);
+  splitk_reduce_kernel<<<(unsigned)cdiv(total, 256), 256, 0, stream>>>(a, ws, split);
   return check_launch("tf_w4a16_linear(splitk_reduce)");
 }
 
@@ -209,17 +224,19 @@ int effective_split(const LinearArgs& a, const tf_gemm_config& cfg) {
 
 int64_t gemm_workspace(const LinearArgs& a, const tf_gemm_config& cfg) {
   const int s = effective_split(a, cfg);
-  return s > 1 ? (int64_t)s * a.m * a.n * (int64_t)sizeof(float) : 0;
+  const bool partials = s > 1 || a.epilogue == TF_EPILOGUE_SILU_MUL;
+  return partials ? (int64_t)s * a.m * a.n * (int64_t)sizeof(float) : 0;
 }
 
 template <int BM, int BN, int BK, int WM, int WN>
 int launch_gemm(const LinearArgs& a, const tf_gemm_config& cfg, float* ws, hipStream_t stream) {
   const int split = effective_split(a, cfg);
-  if (split > 1 && ws == nullptr) return fail(TF_EINVAL, "tf_w4a16_linear: split-K needs a workspace");
+  const bool partials = split > 1 || a.epilogue == TF_EPILOGUE_SILU_MUL;
+  if (partials && ws == nullptr) return fail(TF_EINVAL, "tf_w4a16_linear: this config needs a workspace");
   const dim3 grid((unsigned)cdiv(a.n, BN), (unsigned)cdiv(a.m, BM), (unsigned)split);
   gemm_kernel<BM, BN, BK, WM, WN><<<grid, WM * WN * 64, 0, stream>>>(a, ws, split);
   if (int rc = check_launch("tf_w4a16_linear(gemm_mfma)")) return rc;
-  if (split > 1) return splitk_reduce(a, ws, split, stream);
+  if (partials) return splitk_reduce(a, ws, split, stream);
   return TF_OK;
 }
 

@@ -89,7 +89,8 @@ __global__ __launch_bounds__(256) void gemm3_kernel(LinearArgs a, float* __restr
   const int z = t / per_split;
   const int r = t - z * per_split;
   const int m0 = (r % tiles_m) * C::BM;
-  const int n0 = (r / tiles_m) * C::BN + wn * 16 * RT;  // this wave's first column
+  const int n_base = (r / tiles_m) * C::BN;  // the tile's first column
+  const int wl = wn * 16 * RT;                 // this wave's first column in the tile
   const int wrow = wm * 16 * MT;                          // this wave's first row in the tile
 
   const int nchunks = a.k >> 5;
@@ -134,9 +135,10 @@ __global__ __launch_bounds__(256) void gemm3_kernel(LinearArgs a, float* __restr
   uint32_t col[RT];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
-    const int n = n0 + rt * 16 + c;
+    const int l = wl + rt * 16 + c;
+    const int n = phys_col(a, n_base, l);
     col[rt] = (uint32_t)n;
-    w_off[rt] = n < a.n ? (uint32_t)n * row_bytes + (uint32_t)g * 16u : kOutOfRange;
+    w_off[rt] = col_valid(a, n_base, l) ? (uint32_t)n * row_bytes + (uint32_t)g * 16u : kOutOfRange;
   }
   const int lane_end = min(s1, (nchunks - g + 3) >> 2);  // steps whose chunk g lies inside K
   u4 wraw[P][RT];
@@ -236,22 +238,31 @@ __global__ __launch_bounds__(256) void gemm3_kernel(LinearArgs a, float* __restr
   }
 
   // ---- epilogue. D layout of v_mfma_f32_16x16x32_f16: lane holds rows 4 (lane / 16) + r,
-  // column lane % 16.
+  // column lane % 16. Under SiLU*mul, lanes c and c ^ 8 hold the gate and up columns of one
+  // output column (phys_col); the partner value comes over with a lane shuffle that every
+  // lane executes, before any per-lane branch.
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
+    const int l = wl + rt * 16 + c;
     const int n = (int)col[rt];
-    if (n >= a.n) continue;
-    const float b = (split_k == 1 && a.bias) ? half_bits_to_float(a.bias[n]) : 0.0f;
+    const bool valid = col_valid(a, n_base, l);
+    const float b = (split_k == 1 && a.bias && valid) ? half_bits_to_float(a.bias[n]) : 0.0f;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int m = m0 + wrow + mt * 16 + 4 * g + q;
-        if (m >= a.m) continue;
-        if (split_k == 1)
-          a.out[(int64_t)m * a.ldo + n] = __builtin_bit_cast(uint16_t, (_Float16)(acc[mt][rt][q] + b));
-        else
-          ws[((int64_t)z * a.m + m) * a.n + n] = acc[mt][rt][q];
+        const float v = acc[mt][rt][q] + b;
+        if (split_k == 1 && a.epilogue == TF_EPILOGUE_SILU_MUL) {
+          const float u = __shfl_xor(v, 8);
+          if (valid && !(l & 8) && m < a.m)
+            a.out[(int64_t)m * a.ldo + silu_out_col(n_base, l)] = finish_silu_mul(v, u);
+        } else if (valid && m < a.m) {
+          if (split_k == 1)
+            store_out(a, m, n, v);
+          else
+            ws[((int64_t)z * a.m + m) * a.n + n] = acc[mt][rt][q];
+        }
       }
   }
 }

@@ -75,7 +75,7 @@ constexpr int kParamWords = 4;
 
 // Staging of one window of a wave's K range into its LDS region:
 //  * params: the dequantization operands of groups [g_lo, g_lo + ng) x columns
-//    [n_base, n_base + 16 RT), `slots` groups deep. Slots past ng get neutral operands (zero
+//    the tile's 16 RT columns (phys_col), `slots` groups deep. Slots past ng get neutral operands (zero
 //    point 0, scale 0), so any word dequantizes to exactly 0 there.
 //  * x (rows > 0): x[m0 + r][k0, k0 + kn) for r < rows, row stride xstride halfs, zero at
 //    k >= K (buffer loads past the tensor return zeros only at its very end, so the K bound is
@@ -124,8 +124,8 @@ __device__ __forceinline__ void load_batch(StageBatch<U>& b, const Window& w, co
   for (int u = 0; u < U; ++u) {
     const int e = base + u * 64 + lane;
     const int gi = e / cols;
-    const int n = w.n_base + e % cols;
-    const bool ok = e < w.pentries && n < st.n && gi < w.ng;
+    const int n = phys_col(a, w.n_base, e % cols);
+    const bool ok = e < w.pentries && col_valid(a, w.n_base, e % cols) && gi < w.ng;
     const uint32_t grp = (uint32_t)(w.g_lo + gi);
     b.sb[u] = load_b16(st.sc, ok ? (grp * (uint32_t)st.n + (uint32_t)n) * 2u : kOutOfRange);
     b.zw[u] = load_b32(st.qz, ok ? (grp * (uint32_t)(st.n >> 3) + (uint32_t)(n >> 3)) * 4u : kOutOfRange);
@@ -149,13 +149,13 @@ __device__ __forceinline__ void load_batch(StageBatch<U>& b, const Window& w, co
 
 template <int RT, int U>
 __device__ __forceinline__ void store_batch(uint32_t* p, _Float16* xs, const StageBatch<U>& b, const Window& w,
-                                            int base, int lane) {
+                                            const LinearArgs& a, int base, int lane) {
   constexpr int cols = 16 * RT;
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const int e = base + u * 64 + lane;
     if (e < w.pentries) {
-      const int n = w.n_base + e % cols;
+      const int n = phys_col(a, w.n_base, e % cols);
       const QuantParams q = make_params(zero_of(b.zw[u], (uint32_t)n), b.sb[u]);
       *reinterpret_cast<u4*>(p + kParamWords * e) = u4{as_u32(q.zlo), as_u32(q.zhi), as_u32(q.s), 0u};
     }
@@ -170,7 +170,7 @@ __device__ __forceinline__ void stage_rest(uint32_t* p, _Float16* xs, const Wind
   for (int base = first; base < w.total; base += 64 * U) {
     StageBatch<U> b;
     load_batch<RT, U>(b, w, a, st, base, lane);
-    store_batch<RT, U>(p, xs, b, w, base, lane);
+    store_batch<RT, U>(p, xs, b, w, a, base, lane);
   }
 }
 
@@ -184,19 +184,21 @@ __device__ __forceinline__ QuantParams read_params(const uint32_t* p) {
 }
 
 // Per-lane view of the weight stream: the lane reads 16 bytes (chunk g = 32 K values) of one
-// row per row tile and step. off[rt] is the byte offset of that run in step 0 (kOutOfRange
-// past N, and still out of range after adding any step offset); lane_end is the first step
-// whose chunk lies past K for this lane or past the wave's range.
+// row per row tile and step; its rows are local columns l0 + 16 rt of the tile at n_base
+// (phys_col). off[rt] is the byte offset of that run in step 0 (kOutOfRange past N, and still
+// out of range after adding any step offset); lane_end is the first step whose chunk lies past
+// K for this lane or past the wave's range.
 template <int RT>
 struct LaneStream {
   uint32_t off[RT];
   int lane_end;
 
-  __device__ __forceinline__ LaneStream(const Streams& st, int n0, int g, int s1) {
+  __device__ __forceinline__ LaneStream(const LinearArgs& a, const Streams& st, int n_base, int l0, int g, int s1) {
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-      const int n = n0 + rt * 16;
-      off[rt] = n < st.n ? (uint32_t)n * st.row_bytes + (uint32_t)g * 16u : kOutOfRange;
+      const int l = l0 + rt * 16;
+      off[rt] = col_valid(a, n_base, l) ? (uint32_t)phys_col(a, n_base, l) * st.row_bytes + (uint32_t)g * 16u
+                                        : kOutOfRange;
     }
     lane_end = min(s1, (st.nchunks - g + 3) >> 2);
   }
@@ -252,7 +254,7 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_dot_kernel(LinearArgs a, int w
   uint32_t* prm = lds + wave * L.wave_words;
   _Float16* xs = reinterpret_cast<_Float16*>(prm + L.pwords);
   const UnpackConsts uc = unpack_consts();
-  const LaneStream<RT> ls_w(st, n_base + c, g, s1);
+  const LaneStream<RT> ls_w(a, st, n_base, c, g, s1);
 
   // Lane bases in LDS; a step adds a wave-uniform offset.
   const uint32_t* plane = prm + kParamWords * ((((g * 32) >> st.log2g) * cols) + c);
@@ -277,7 +279,7 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_dot_kernel(LinearArgs a, int w
     ls_w.issue(ring[p], st, s0 + p);
     __builtin_amdgcn_sched_barrier(0);  // keep slot order: slot 0 must be the oldest ring load
   }
-  store_batch<RT, kStageU>(prm, xs, first, win0, 0, lane);
+  store_batch<RT, kStageU>(prm, xs, first, win0, a, 0, lane);
   stage_rest<RT, kStageU>(prm, xs, win0, a, st, 64 * kStageU, lane);
 
   for (int w0 = s0; w0 < s1; w0 += win) {
@@ -340,16 +342,25 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_dot_kernel(LinearArgs a, int w
           for (int rt = 0; rt < RT; ++rt) acc[m][rt] += red[(((w - 1) * MAXM + m) * RT + rt) * 16 + c];
     }
   }
-  if (wave == 0 && g == 0) {
+  // Lane 4 c (g == 0) holds row c of each row tile. Under SiLU*mul rows c and c ^ 8 are the
+  // gate and up columns of one output (phys_col): lanes 4c and 4c ^ 32 swap their values.
+  if (wave == 0) {
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-      const int n = n_base + rt * 16 + c;
-      if (n >= a.n) continue;
-      const float b = a.bias ? half_bits_to_float(a.bias[n]) : 0.0f;
+      const int l = rt * 16 + c;
+      const int n = phys_col(a, n_base, l);
+      const bool valid = g == 0 && col_valid(a, n_base, l);
+      const float b = (a.bias && valid) ? half_bits_to_float(a.bias[n]) : 0.0f;
 #pragma unroll
       for (int m = 0; m < MAXM; ++m) {
-        if (m < a.m)
-          a.out[(int64_t)m * a.ldo + n] = __builtin_bit_cast(uint16_t, (_Float16)(acc[m][rt] + b));
+        const float v = acc[m][rt] + b;
+        if (a.epilogue == TF_EPILOGUE_SILU_MUL) {
+          const float u = __shfl_xor(v, 32);
+          if (valid && !(l & 8) && m < a.m)
+            a.out[(int64_t)m * a.ldo + silu_out_col(n_base, l)] = finish_silu_mul(v, u);
+        } else if (valid && m < a.m) {
+          store_out(a, m, n, v);
+        }
       }
     }
   }
@@ -378,7 +389,7 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_mfma_kernel(LinearArgs a, int 
   uint32_t* prm = lds + wave * L.wave_words;
   _Float16* xs = reinterpret_cast<_Float16*>(prm + L.pwords);
   const UnpackConsts uc = unpack_consts();
-  const LaneStream<RT> ls_w(st, n_base + c, g, s1);
+  const LaneStream<RT> ls_w(a, st, n_base, c, g, s1);
 
   const uint32_t* plane = prm + kParamWords * ((((g * 32) >> st.log2g) * cols) + c);
   const int pstep = kParamWords * gps * cols;
@@ -427,7 +438,7 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_mfma_kernel(LinearArgs a, int 
     issue(p, s0 + p);
     __builtin_amdgcn_sched_barrier(0);  // keep slot order: slot 0 must be the oldest ring load
   }
-  store_batch<RT, kStageU>(prm, xs, first, win0, 0, lane);
+  store_batch<RT, kStageU>(prm, xs, first, win0, a, 0, lane);
   stage_rest<RT, kStageU>(prm, xs, win0, a, st, 64 * kStageU, lane);
 
   for (int w0 = s0; w0 < s1; w0 += win) {
@@ -488,18 +499,26 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_mfma_kernel(LinearArgs a, int 
   }
   if (wave == 0) {
     // D layout of v_mfma_f32_16x16x32_f16: lane holds rows 4*(lane/16) + r, column lane%16.
+    // Under SiLU*mul lanes c and c ^ 8 hold the gate and up columns of one output.
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-      const int n = n_base + rt * 16 + c;
-      if (n >= a.n) continue;
-      const float b = a.bias ? half_bits_to_float(a.bias[n]) : 0.0f;
+      const int l = rt * 16 + c;
+      const int n = phys_col(a, n_base, l);
+      const bool valid = col_valid(a, n_base, l);
+      const float b = (a.bias && valid) ? half_bits_to_float(a.bias[n]) : 0.0f;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int m = m_base + mt * 16 + 4 * g + r;
-          if (m < a.m)
-            a.out[(int64_t)m * a.ldo + n] = __builtin_bit_cast(uint16_t, (_Float16)(acc[mt][rt][r] + b));
+          const float v = acc[mt][rt][r] + b;
+          if (a.epilogue == TF_EPILOGUE_SILU_MUL) {
+            const float u = __shfl_xor(v, 8);
+            if (valid && !(l & 8) && m < a.m)
+              a.out[(int64_t)m * a.ldo + silu_out_col(n_base, l)] = finish_silu_mul(v, u);
+          } else if (valid && m < a.m) {
+            store_out(a, m, n, v);
+          }
         }
     }
   }

@@ -20,7 +20,59 @@ struct LinearArgs {
   int n;
   int k;
   int log2g;               // log2(group_size)
+  // Epilogue (TF_EPILOGUE_*): NONE writes y; RESIDUAL writes fp16(residual + fp16(y)) (out may
+  // be residual itself, element for element); SILU_MUL writes [m, n / 2]:
+  // fp16(fp16(silu(fp16(y[:, j]))) * fp16(y[:, n / 2 + j])).
+  int epilogue = TF_EPILOGUE_NONE;
+  const uint16_t* residual = nullptr;  // fp16 [m, n], row stride ldr
+  int64_t ldr = 0;
 };
+
+// Column mapping of the fused SiLU*mul epilogue for kernels that hold a 16-column group in
+// one row of 16 lanes: local column l of the tile at n_base takes the gate row
+// n_base / 2 + 8 (l / 16) + l % 8 when l % 16 < 8, else the up row n / 2 + that; lanes l and
+// l ^ 8 then hold the gate and up values of one output column. Without the epilogue the
+// mapping is the identity n_base + l.
+__device__ __forceinline__ int phys_col(const LinearArgs& a, int n_base, int l) {
+  if (a.epilogue != TF_EPILOGUE_SILU_MUL) return n_base + l;
+  const int j = (n_base >> 1) + ((l >> 4) << 3) + (l & 7);
+  return (l & 8) ? (a.n >> 1) + j : j;
+}
+
+// Output column of local column l under the SiLU*mul mapping (valid on the gate lanes).
+__device__ __forceinline__ int silu_out_col(int n_base, int l) { return (n_base >> 1) + ((l >> 4) << 3) + (l & 7); }
+
+// True when the physical column of local column l holds data (inside N; for SiLU*mul, its
+// output column inside n / 2).
+__device__ __forceinline__ bool col_valid(const LinearArgs& a, int n_base, int l) {
+  if (a.epilogue != TF_EPILOGUE_SILU_MUL) return n_base + l < a.n;
+  return silu_out_col(n_base, l) < (a.n >> 1);
+}
+
+__device__ __forceinline__ uint16_t f16_bits(float v) { return __builtin_bit_cast(uint16_t, (_Float16)v); }
+
+// fp16(residual + fp16(v)): the unfused `residual + linear(x)` of two fp16 tensors.
+__device__ __forceinline__ uint16_t finish_residual(float v, uint16_t r) {
+  const float y = (float)(_Float16)v;
+  return f16_bits(y + half_bits_to_float(r));
+}
+
+// fp16(fp16(silu(fp16(g))) * fp16(u)): torch's fp16 silu (x / (1 + exp(-x)) in fp32, one
+// rounding) followed by its fp16 multiply, on the rounded linear outputs.
+__device__ __forceinline__ uint16_t finish_silu_mul(float g, float u) {
+  const float g16 = (float)(_Float16)g;
+  const float u16 = (float)(_Float16)u;
+  const float s16 = (float)(_Float16)(g16 / (1.0f + expf(-g16)));
+  return f16_bits(s16 * u16);
+}
+
+// Write one output value v (= acc + bias, fp32) of row m, physical column n under the
+// NONE / RESIDUAL epilogues.
+__device__ __forceinline__ void store_out(const LinearArgs& a, int m, int n, float v) {
+  uint16_t r = f16_bits(v);
+  if (a.epilogue == TF_EPILOGUE_RESIDUAL) r = finish_residual(v, a.residual[(int64_t)m * a.ldr + n]);
+  a.out[(int64_t)m * a.ldo + n] = r;
+}
 
 using LaunchFn = int (*)(const LinearArgs&, const tf_gemm_config&, float* workspace,
                          hipStream_t stream);

@@ -77,13 +77,27 @@ extern "C" int tf_get_variant(int index, tf_gemm_config* out) {
 
 static int make_args(const uint16_t* x, int64_t ldx, const int32_t* qweight_t, const uint16_t* scales,
                      const int32_t* qzeros, const uint16_t* bias, uint16_t* out, int64_t ldo, int64_t m,
-                     int64_t n, int64_t k, int32_t group_size, LinearArgs* a) {
+                     int64_t n, int64_t k, int32_t group_size, int32_t epilogue, const uint16_t* residual,
+                     int64_t ldr, LinearArgs* a) {
   if (m < 0 || n < 0 || k < 0) return fail(TF_EINVAL, "tf_w4a16_linear: negative size");
   if (m > 0x7FFFFFFF || n > 0x7FFFFFFF || k > 0x7FFFFFFF)
     return fail(TF_EINVAL, "tf_w4a16_linear: size above 2^31");
   if (n % 8) return fail(TF_EINVAL, "tf_w4a16_linear: N must be a multiple of 8");
   if (int rc = check_group_size(group_size, k, "tf_w4a16_linear")) return rc;
-  if (ldx < k || ldo < n) return fail(TF_EINVAL, "tf_w4a16_linear: row stride smaller than the row");
+  if (epilogue != TF_EPILOGUE_NONE && epilogue != TF_EPILOGUE_RESIDUAL && epilogue != TF_EPILOGUE_SILU_MUL)
+    return fail(TF_EINVAL, "tf_w4a16_linear_ex: unknown epilogue");
+  if (epilogue == TF_EPILOGUE_SILU_MUL && n % 16)
+    return fail(TF_EINVAL, "tf_w4a16_linear_ex: the SiLU*mul epilogue needs N to be a multiple of 16");
+  const int64_t n_out = epilogue == TF_EPILOGUE_SILU_MUL ? n / 2 : n;
+  if (ldx < k || ldo < n_out) return fail(TF_EINVAL, "tf_w4a16_linear: row stride smaller than the row");
+  if (epilogue == TF_EPILOGUE_RESIDUAL) {
+    if (ldr < n) return fail(TF_EINVAL, "tf_w4a16_linear_ex: residual row stride smaller than the row");
+    if (residual == out && ldr != ldo)
+      return fail(TF_EINVAL, "tf_w4a16_linear_ex: a residual that is the output needs the output's row stride");
+  }
+  a->epilogue = epilogue;
+  a->residual = epilogue == TF_EPILOGUE_RESIDUAL ? residual : nullptr;
+  a->ldr = ldr;
   if (ldx % 8) return fail(TF_EINVAL, "tf_w4a16_linear: x row stride must be a multiple of 8 elements");
   a->x = x;
   a->ldx = ldx;
@@ -99,13 +113,15 @@ static int make_args(const uint16_t* x, int64_t ldx, const int32_t* qweight_t, c
   a->log2g = log2_group(group_size);
   if (m == 0 || n == 0) return TF_OK;
   if (!x || !qweight_t || !scales || !qzeros || !out) return fail(TF_EINVAL, "tf_w4a16_linear: null pointer");
+  if (epilogue == TF_EPILOGUE_RESIDUAL && !residual)
+    return fail(TF_EINVAL, "tf_w4a16_linear_ex: the residual epilogue needs a residual tensor");
   if (!aligned16(x) || !aligned16(qweight_t))
     return fail(TF_EINVAL, "tf_w4a16_linear: x and qweight_t must be 16-byte aligned");
   return TF_OK;
 }
 
-extern "C" int64_t tf_w4a16_workspace_bytes(int64_t m, int64_t n, int64_t k, int32_t group_size,
-                                            const tf_gemm_config* cfg) {
+extern "C" int64_t tf_w4a16_workspace_bytes_ex(int64_t m, int64_t n, int64_t k, int32_t group_size,
+                                               const tf_gemm_config* cfg, int32_t epilogue) {
   if (cfg == nullptr) return 0;
   const Variant* v = find_variant(*cfg);
   if (v == nullptr || m <= 0 || n <= 0 || k <= 0 || cfg->block_k <= 0) return 0;
@@ -114,17 +130,25 @@ extern "C" int64_t tf_w4a16_workspace_bytes(int64_t m, int64_t n, int64_t k, int
   a.n = (int)n;
   a.k = (int)k;
   a.log2g = log2_group(group_size);
+  a.epilogue = epilogue;
   return v->workspace(a, *cfg);
 }
 
-extern "C" int tf_w4a16_linear(const uint16_t* x, int64_t ldx, const int32_t* qweight_t,
-                               const uint16_t* scales, const int32_t* qzeros, const uint16_t* bias,
-                               uint16_t* out, int64_t ldo, int64_t m, int64_t n, int64_t k,
-                               int32_t group_size, const tf_gemm_config* cfg, float* workspace,
-                               int64_t workspace_bytes, void* stream) {
+extern "C" int64_t tf_w4a16_workspace_bytes(int64_t m, int64_t n, int64_t k, int32_t group_size,
+                                            const tf_gemm_config* cfg) {
+  return tf_w4a16_workspace_bytes_ex(m, n, k, group_size, cfg, TF_EPILOGUE_NONE);
+}
+
+extern "C" int tf_w4a16_linear_ex(const uint16_t* x, int64_t ldx, const int32_t* qweight_t,
+                                  const uint16_t* scales, const int32_t* qzeros, const uint16_t* bias,
+                                  uint16_t* out, int64_t ldo, int64_t m, int64_t n, int64_t k,
+                                  int32_t group_size, const tf_gemm_config* cfg, int32_t epilogue,
+                                  const uint16_t* residual, int64_t ldr, float* workspace,
+                                  int64_t workspace_bytes, void* stream) {
   if (cfg == nullptr) return fail(TF_EINVAL, "tf_w4a16_linear: null config");
   LinearArgs a;
-  if (int rc = make_args(x, ldx, qweight_t, scales, qzeros, bias, out, ldo, m, n, k, group_size, &a))
+  if (int rc = make_args(x, ldx, qweight_t, scales, qzeros, bias, out, ldo, m, n, k, group_size, epilogue,
+                         residual, ldr, &a))
     return rc;
   if (int rc = check_config(*cfg, group_size)) return rc;
   const Variant* v = find_variant(*cfg);
@@ -134,4 +158,13 @@ extern "C" int tf_w4a16_linear(const uint16_t* x, int64_t ldx, const int32_t* qw
   if (need > 0 && (workspace == nullptr || workspace_bytes < need))
     return fail(TF_EINVAL, "tf_w4a16_linear: workspace too small for this split_k");
   return v->launch(a, *cfg, workspace, (hipStream_t)stream);
+}
+
+extern "C" int tf_w4a16_linear(const uint16_t* x, int64_t ldx, const int32_t* qweight_t,
+                               const uint16_t* scales, const int32_t* qzeros, const uint16_t* bias,
+                               uint16_t* out, int64_t ldo, int64_t m, int64_t n, int64_t k,
+                               int32_t group_size, const tf_gemm_config* cfg, float* workspace,
+                               int64_t workspace_bytes, void* stream) {
+  return tf_w4a16_linear_ex(x, ldx, qweight_t, scales, qzeros, bias, out, ldo, m, n, k, group_size, cfg,
+                            TF_EPILOGUE_NONE, nullptr, 0, workspace, workspace_bytes, stream);
 }

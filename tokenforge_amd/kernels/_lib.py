@@ -12,7 +12,7 @@ import functools
 import os
 from pathlib import Path
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 """Must equal ``tf_abi_version()`` of the loaded library."""
 
 LIB_ENV = "TOKENFORGE_HIP_LIB"
@@ -24,6 +24,9 @@ TF_ELAUNCH = 2
 TF_ERANGE = 3
 
 KERNEL_IDS = {"gemv_dot": 0, "gemv_mfma": 1, "gemm_mfma": 2}
+EPILOGUE_NONE = 0
+EPILOGUE_RESIDUAL = 1
+EPILOGUE_SILU_MUL = 2
 KERNEL_NAMES = {v: k for k, v in KERNEL_IDS.items()}
 
 
@@ -70,6 +73,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         ctypes.c_int,
         [_p, _i64, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i32,
          ctypes.POINTER(TfGemmConfig), _p, _i64, _p],
+    ),
+    "tf_w4a16_workspace_bytes_ex": (_i64, [_i64, _i64, _i64, _i32, ctypes.POINTER(TfGemmConfig), _i32]),
+    "tf_w4a16_linear_ex": (
+        ctypes.c_int,
+        [_p, _i64, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i32,
+         ctypes.POINTER(TfGemmConfig), _i32, _p, _i64, _p, _i64, _p],
     ),
     "tf_rmsnorm_fp8_quant": (ctypes.c_int, [_p, _i64, _p, _p, _i64, _p, _i32, _i64, _i64, _f32, _p]),
     "tf_e4m3_encode": (ctypes.c_int, [_p, _p, _i64, _p]),

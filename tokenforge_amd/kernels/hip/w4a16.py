@@ -75,6 +75,9 @@ def workspace_bytes(m: int, n: int, k: int, group_size: int, cfg: GemmConfig) ->
     return int(_lib.lib().tf_w4a16_workspace_bytes(m, n, k, group_size, ctypes.byref(c)))
 
 
+EPILOGUES = {"none": _lib.EPILOGUE_NONE, "residual": _lib.EPILOGUE_RESIDUAL, "silu_mul": _lib.EPILOGUE_SILU_MUL}
+
+
 def w4a16_gemm(
     x: torch.Tensor,
     qweight_t: torch.Tensor,
@@ -85,31 +88,68 @@ def w4a16_gemm(
     bias: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """``x [M, K] fp16`` @ dequant(W)^T (+ bias) -> ``[M, N] fp16`` (w4a16.py:178-232)."""
+    return w4a16_gemm_ex(x, qweight_t, scales, qzeros, group_size, config, bias)
+
+
+def w4a16_gemm_ex(
+    x: torch.Tensor,
+    qweight_t: torch.Tensor,
+    scales: torch.Tensor,
+    qzeros: torch.Tensor,
+    group_size: int,
+    config: GemmConfig,
+    bias: torch.Tensor | None = None,
+    epilogue: str = "none",
+    residual: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """:func:`w4a16_gemm` with a fused epilogue (``tf_w4a16_linear_ex``):
+
+    * ``"none"``: ``y``;
+    * ``"residual"``: ``residual + y`` for an fp16 ``residual [M, N]`` (one fp16 add after the
+      fp16 ``y``, as the unfused torch expression rounds);
+    * ``"silu_mul"``: ``silu(y[:, :N/2]) * y[:, N/2:]`` -> ``[M, N/2]`` (torch's fp16 silu and
+      multiply on the fp16 ``y``); N a multiple of 16.
+    """
     m, n, k = _check_inputs(x, qweight_t, scales, qzeros, group_size)
     config.validate(group_size)
+    if epilogue not in EPILOGUES:
+        raise ValueError(f"epilogue must be one of {sorted(EPILOGUES)}, got {epilogue!r}")
     if bias is not None:
         if tuple(bias.shape) != (n,):
             raise ValueError(f"bias shape {tuple(bias.shape)} != {(n,)}")
         if bias.dtype != torch.float16:
             raise TypeError(f"bias must be fp16, got {bias.dtype}")
         bias = bias.contiguous()
-    dev = require_gpu("w4a16_gemm", x, qweight_t, scales, qzeros, *(() if bias is None else (bias,)))
-    out = torch.empty((m, n), dtype=torch.float16, device=dev)
+    if epilogue == "residual":
+        if residual is None or tuple(residual.shape) != (m, n) or residual.dtype != torch.float16:
+            raise ValueError(f"the residual epilogue needs an fp16 residual of shape {(m, n)}")
+        if residual.stride(-1) != 1:
+            residual = residual.contiguous()
+    elif residual is not None:
+        raise ValueError("residual is only used by the residual epilogue")
+    if epilogue == "silu_mul" and n % 16:
+        raise ValueError(f"the silu_mul epilogue needs N to be a multiple of 16, got {n}")
+    tensors = (x, qweight_t, scales, qzeros) + tuple(t for t in (bias, residual) if t is not None)
+    dev = require_gpu("w4a16_gemm", *tensors)
+    n_out = n // 2 if epilogue == "silu_mul" else n
+    out = torch.empty((m, n_out), dtype=torch.float16, device=dev)
     if m == 0 or n == 0:
         return out
     x = _aligned_rows(x)
     ldx = x.stride(0) if m > 1 else k
+    ldr = (residual.stride(0) if m > 1 else n) if residual is not None else 0
+    code = EPILOGUES[epilogue]
     c = to_c_config(config)
     h = _lib.lib()
-    need = int(h.tf_w4a16_workspace_bytes(m, n, k, group_size, ctypes.byref(c)))
+    need = int(h.tf_w4a16_workspace_bytes_ex(m, n, k, group_size, ctypes.byref(c), code))
     ws = torch.empty((max(need, 4) + 3) // 4, dtype=torch.float32, device=dev) if need else None
     with on_device(dev):
-        rc = h.tf_w4a16_linear(
+        rc = h.tf_w4a16_linear_ex(
             x.data_ptr(), ldx, qweight_t.data_ptr(), scales.data_ptr(), qzeros.data_ptr(),
-            ptr(bias), out.data_ptr(), n, m, n, k, group_size, ctypes.byref(c),
-            ptr(ws), need, stream_of(dev),
+            ptr(bias), out.data_ptr(), n_out, m, n, k, group_size, ctypes.byref(c), code,
+            ptr(residual), ldr, ptr(ws), need, stream_of(dev),
         )
-    _lib.check(rc, "tf_w4a16_linear")
+    _lib.check(rc, "tf_w4a16_linear_ex")
     return out
 
 

@@ -10,8 +10,17 @@ Ops (same names and schemas as the reference):
 * ``tokenforge::w4a16_dequant(qweight_t, scales, qzeros, group_size)``
 * ``tokenforge::rmsnorm_fp8_quant(x, weight, eps, scale)``
 
-All three run hand-written HIP kernels; a CPU tensor or a missing kernel library raises
-instead of falling back.
+and two fused forms of the linear with no counterpart in the reference (which runs the same
+arithmetic as separate torch ops after ``w4a16_linear``):
+
+* ``tokenforge::w4a16_linear_residual(x, qweight_t, scales, qzeros, bias, residual, group_size,
+  backend)`` = ``residual + w4a16_linear(...)``
+* ``tokenforge::w4a16_linear_silu_mul(x, qweight_t, scales, qzeros, bias, group_size, backend)``
+  = ``silu(y[..., :N/2]) * y[..., N/2:]`` with ``y = w4a16_linear(...)``
+
+Each equals its unfused torch expression on fp16 tensors bit for bit (same roundings). All
+run hand-written HIP kernels; a CPU tensor or a missing kernel library raises instead of
+falling back.
 """
 
 from __future__ import annotations
@@ -31,8 +40,7 @@ def _gpu_id(device: torch.device) -> str:
     return gpu_identity(device)
 
 
-@torch.library.custom_op("tokenforge::w4a16_linear", mutates_args=())
-def w4a16_linear(
+def _linear(
     x: torch.Tensor,
     qweight_t: torch.Tensor,
     scales: torch.Tensor,
@@ -40,10 +48,13 @@ def w4a16_linear(
     bias: torch.Tensor | None,
     group_size: int,
     backend: str,
+    epilogue: str = "none",
+    residual: torch.Tensor | None = None,
 ) -> torch.Tensor:
     k = x.shape[-1]
     n = qweight_t.shape[0]
-    out_shape = (*x.shape[:-1], n)
+    n_out = n // 2 if epilogue == "silu_mul" else n
+    out_shape = (*x.shape[:-1], n_out)
     x2 = x.reshape(-1, k)
     if x2.stride(-1) != 1:
         x2 = x2.contiguous()
@@ -64,8 +75,26 @@ def w4a16_linear(
     cfg = autotune.lookup(_gpu_id(x.device), dispatch.lookup_bucket(m), n, k, group_size)
     # The tuned config may pick the other family in the buckets both serve.
     dispatch.record(dispatch.Decision("hip_gemm" if cfg.family == "gemm" else "hip_gemv", decision.bucket))
-    y = _w4a16.w4a16_gemm(x2, qweight_t, scales, qzeros, group_size, cfg, bias)
+    r2 = None
+    if residual is not None:
+        if tuple(residual.shape) != (*x.shape[:-1], n):
+            raise ValueError(f"residual shape {tuple(residual.shape)} != {(*x.shape[:-1], n)}")
+        r2 = residual.reshape(-1, n)
+    y = _w4a16.w4a16_gemm_ex(x2, qweight_t, scales, qzeros, group_size, cfg, bias, epilogue, r2)
     return y.reshape(out_shape)
+
+
+@torch.library.custom_op("tokenforge::w4a16_linear", mutates_args=())
+def w4a16_linear(
+    x: torch.Tensor,
+    qweight_t: torch.Tensor,
+    scales: torch.Tensor,
+    qzeros: torch.Tensor,
+    bias: torch.Tensor | None,
+    group_size: int,
+    backend: str,
+) -> torch.Tensor:
+    return _linear(x, qweight_t, scales, qzeros, bias, group_size, backend)
 
 
 @w4a16_linear.register_fake
@@ -79,6 +108,60 @@ def _w4a16_linear_fake(
     backend: str,
 ) -> torch.Tensor:
     return x.new_empty((*x.shape[:-1], qweight_t.shape[0]))
+
+
+@torch.library.custom_op("tokenforge::w4a16_linear_residual", mutates_args=())
+def w4a16_linear_residual(
+    x: torch.Tensor,
+    qweight_t: torch.Tensor,
+    scales: torch.Tensor,
+    qzeros: torch.Tensor,
+    bias: torch.Tensor | None,
+    residual: torch.Tensor,
+    group_size: int,
+    backend: str,
+) -> torch.Tensor:
+    return _linear(x, qweight_t, scales, qzeros, bias, group_size, backend, "residual", residual)
+
+
+@w4a16_linear_residual.register_fake
+def _w4a16_linear_residual_fake(
+    x: torch.Tensor,
+    qweight_t: torch.Tensor,
+    scales: torch.Tensor,
+    qzeros: torch.Tensor,
+    bias: torch.Tensor | None,
+    residual: torch.Tensor,
+    group_size: int,
+    backend: str,
+) -> torch.Tensor:
+    return x.new_empty((*x.shape[:-1], qweight_t.shape[0]))
+
+
+@torch.library.custom_op("tokenforge::w4a16_linear_silu_mul", mutates_args=())
+def w4a16_linear_silu_mul(
+    x: torch.Tensor,
+    qweight_t: torch.Tensor,
+    scales: torch.Tensor,
+    qzeros: torch.Tensor,
+    bias: torch.Tensor | None,
+    group_size: int,
+    backend: str,
+) -> torch.Tensor:
+    return _linear(x, qweight_t, scales, qzeros, bias, group_size, backend, "silu_mul")
+
+
+@w4a16_linear_silu_mul.register_fake
+def _w4a16_linear_silu_mul_fake(
+    x: torch.Tensor,
+    qweight_t: torch.Tensor,
+    scales: torch.Tensor,
+    qzeros: torch.Tensor,
+    bias: torch.Tensor | None,
+    group_size: int,
+    backend: str,
+) -> torch.Tensor:
+    return x.new_empty((*x.shape[:-1], qweight_t.shape[0] // 2))
 
 
 @torch.library.custom_op("tokenforge::w4a16_dequant", mutates_args=())
