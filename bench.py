@@ -42,8 +42,10 @@ Extra objects on the same JSON line:
   scale) -> qkv -> attention as identity on the value slice (query head h takes KV group
   h // 7) -> o_proj -> residual add -> RMSNorm + FP8 -> fp16(q * scale) -> gate_up -> SiLU(gate)
   * up -> down -> residual add. The linears and the norms are this library's kernels, the
-  glue is torch; a pass is one HIP graph, tokens/s = M / time per pass. M=1 on every run;
-  ``--stack`` or ``--full`` add M in {8, 32} (decode) and 2048 (prefill).
+  rest is torch glue ("unfused"), or the residual adds and SiLU*mul run as the linears'
+  fused epilogues ("fused", same bits; ``tokens_per_s`` is this one). A pass is one HIP
+  graph, tokens/s = M / time per pass. M=1 on every run; ``--stack`` or ``--full`` add M in
+  {8, 32} (decode) and 2048 (prefill).
 * ``cpu_baseline``: reference.py's CPU path (dequantize per call + fp32 matmul), restated in
   torch on the host cores, on a bounded sample of the same step.
 """
@@ -191,7 +193,9 @@ KV_HEADS = 4
 
 
 def stack_bench(dev: torch.device, gpu: str, ms: tuple[int, ...], tune: bool) -> list[dict]:  # type: ignore[type-arg]
-    """tokens/s of one pass through 28 decoder layers, per M (module docstring)."""
+    """configs[4]: tokens/s of one pass through 28 decoder layers, per M (module docstring);
+    each M timed with the unfused torch glue and with the fused epilogues (residual adds in
+    o_proj and down, SiLU*mul in gate_up), which give the same bits."""
     from tokenforge_amd.kernels import autotune
 
     eps = 1e-6
@@ -221,15 +225,22 @@ def stack_bench(dev: torch.device, gpu: str, ms: tuple[int, ...], tune: bool) ->
         y = ops.w4a16_linear(a, *qkv, bias, GROUP, "hip")
         v = y[:, q_width + KV_HEADS * HEAD_DIM:].reshape(m, KV_HEADS, 1, HEAD_DIM)
         attn = v.expand(m, KV_HEADS, h // (KV_HEADS * HEAD_DIM), HEAD_DIM).reshape(m, h)
-        x = x + ops.w4a16_linear(attn, *o, None, GROUP, "hip")
+        if not fused:
+            x = x + ops.w4a16_linear(attn, *o, None, GROUP, "hip")
+        else:
+            x = ops.w4a16_linear_residual(attn, *o, None, x, GROUP, "hip")
         q8, s = ops.rmsnorm_fp8_quant(x, g2, eps, None)
         a = (q8.to(torch.float32) * s).to(torch.float16)
-        y = ops.w4a16_linear(a, *gu, None, GROUP, "hip")
-        act = torch.nn.functional.silu(y[:, :inter]) * y[:, inter:]
-        return x + ops.w4a16_linear(act, *down, None, GROUP, "hip")
+        if not fused:
+            y = ops.w4a16_linear(a, *gu, None, GROUP, "hip")
+            act = torch.nn.functional.silu(y[:, :inter]) * y[:, inter:]
+            return x + ops.w4a16_linear(act, *down, None, GROUP, "hip")
+        act = ops.w4a16_linear_silu_mul(a, *gu, None, GROUP, "hip")
+        return ops.w4a16_linear_residual(act, *down, None, x, GROUP, "hip")
 
     res = []
     gen = torch.Generator(device=dev).manual_seed(11)
+    fused = False
     for m in ms:
         x0 = torch.randn((m, h), generator=gen, device=dev).to(torch.float16)
 
@@ -239,18 +250,27 @@ def stack_bench(dev: torch.device, gpu: str, ms: tuple[int, ...], tune: bool) ->
                 x = layer_pass(x, layer)
             return x
 
-        g, outs = capture([full_pass], warm=1)
-        ms_pass = median_replay_ms(g, 1)  # replays the graph: outs[0] holds the pass's output
-        if not bool(torch.isfinite(outs[0]).all()):
-            raise RuntimeError(f"stack pass at M={m} produced non-finite values")
-        step_bytes = sum(bytes_moved(m, n, k) for _, n, k in SHAPES) * STACK_LAYERS
-        flops = 2 * m * sum(n * k for _, n, k in SHAPES) * STACK_LAYERS
-        res.append({"m": m, "layers": STACK_LAYERS, "ms_per_pass": ms_pass, "tokens_per_s": m / (ms_pass * 1e-3),
-                    "linear_gbps": step_bytes / (ms_pass * 1e-3) / 1e9,
-                    "linear_tflops": flops / (ms_pass * 1e-3) / 1e12, "weight_bytes": total})
-        log(f"  stack M={m:<5d} {ms_pass * 1e3:9.1f} us/pass {m / (ms_pass * 1e-3):9.0f} tok/s "
-            f"({step_bytes / (ms_pass * 1e-3) / 1e9:.0f} GB/s of linear bytes)")
-        del g, outs
+        row: dict = {"m": m, "layers": STACK_LAYERS, "weight_bytes": total}  # type: ignore[type-arg]
+        outs_by_mode = {}
+        for fused in (False, True):
+            g, outs = capture([full_pass], warm=1)
+            ms_pass = median_replay_ms(g, 1)  # replays the graph: outs[0] holds the pass's output
+            if not bool(torch.isfinite(outs[0]).all()):
+                raise RuntimeError(f"stack pass at M={m} produced non-finite values")
+            outs_by_mode[fused] = outs[0]
+            step_bytes = sum(bytes_moved(m, n, k) for _, n, k in SHAPES) * STACK_LAYERS
+            flops = 2 * m * sum(n * k for _, n, k in SHAPES) * STACK_LAYERS
+            key = "fused" if fused else "unfused"
+            row[key] = {"ms_per_pass": ms_pass, "tokens_per_s": m / (ms_pass * 1e-3),
+                        "linear_gbps": step_bytes / (ms_pass * 1e-3) / 1e9,
+                        "linear_tflops": flops / (ms_pass * 1e-3) / 1e12}
+            log(f"  stack M={m:<5d} {key:8s} {ms_pass * 1e3:9.1f} us/pass {m / (ms_pass * 1e-3):9.0f} tok/s "
+                f"({step_bytes / (ms_pass * 1e-3) / 1e9:.0f} GB/s of linear bytes)")
+            del g, outs
+        row["fused_equals_unfused"] = bool(torch.equal(outs_by_mode[False], outs_by_mode[True]))
+        row["tokens_per_s"] = row["fused"]["tokens_per_s"]
+        res.append(row)
+        del outs_by_mode
     del layers
     torch.cuda.empty_cache()
     return res

@@ -34,7 +34,8 @@ def _layers(device: torch.device, count: int) -> list:  # type: ignore[type-arg]
     return out
 
 
-def _pass(x: torch.Tensor, layers: list) -> torch.Tensor:  # type: ignore[type-arg]
+def _pass(x: torch.Tensor, layers: list, fused: bool = False) -> torch.Tensor:  # type: ignore[type-arg]
+    """One pass; ``fused`` runs the residual adds and SiLU*mul as linear epilogues."""
     ops = torch.ops.tokenforge
     m = x.shape[0]
     for (qkv, o, gu, down), bias, g1, g2 in layers:
@@ -43,37 +44,47 @@ def _pass(x: torch.Tensor, layers: list) -> torch.Tensor:  # type: ignore[type-a
         y = ops.w4a16_linear(a, *qkv, bias, G, "hip")
         v = y[:, QKV - 512:].reshape(m, 4, 1, 128)
         attn = v.expand(m, 4, 7, 128).reshape(m, H)
-        x = x + ops.w4a16_linear(attn, *o, None, G, "hip")
+        if fused:
+            x = ops.w4a16_linear_residual(attn, *o, None, x, G, "hip")
+        else:
+            x = x + ops.w4a16_linear(attn, *o, None, G, "hip")
         q8, s = ops.rmsnorm_fp8_quant(x, g2, 1e-6, None)
         a = (q8.to(torch.float32) * s).to(torch.float16)
-        y = ops.w4a16_linear(a, *gu, None, G, "hip")
-        act = torch.nn.functional.silu(y[:, :INTER]) * y[:, INTER:]
-        x = x + ops.w4a16_linear(act, *down, None, G, "hip")
+        if fused:
+            act = ops.w4a16_linear_silu_mul(a, *gu, None, G, "hip")
+            x = ops.w4a16_linear_residual(act, *down, None, x, G, "hip")
+        else:
+            y = ops.w4a16_linear(a, *gu, None, G, "hip")
+            act = torch.nn.functional.silu(y[:, :INTER]) * y[:, INTER:]
+            x = x + ops.w4a16_linear(act, *down, None, G, "hip")
     return x
 
 
+@pytest.mark.parametrize("fused", [False, True], ids=["unfused", "fused"])
 @pytest.mark.parametrize("m", [1, 24, 300])
-def test_stack_replay_is_bit_identical_to_eager(m: int, device: torch.device) -> None:
+def test_stack_replay_is_bit_identical_to_eager(m: int, fused: bool, device: torch.device) -> None:
     layers = _layers(device, 2)
     gen = torch.Generator(device=device).manual_seed(m)
     x = torch.randn((m, H), generator=gen, device=device).to(torch.float16)
     other = torch.randn((m, H), generator=gen, device=device).to(torch.float16)
-    eager = _pass(x, layers)
+    eager = _pass(x, layers, fused)
     assert bool(torch.isfinite(eager).all())
+    if fused:  # the fused epilogues round exactly like the unfused torch glue
+        assert torch.equal(eager, _pass(x, layers))
 
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(stream):
-        _pass(x, layers)  # warm-up on the capture stream
+        _pass(x, layers, fused)  # warm-up on the capture stream
         stream.synchronize()
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, stream=stream):
-            out = _pass(x, layers)
+            out = _pass(x, layers, fused)
     torch.cuda.current_stream().wait_stream(stream)
     torch.cuda.synchronize()
     for _ in range(3):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager), "graph replay differs from the eager pass"
-        _pass(other, layers)  # eager work between replays
+        _pass(other, layers, fused)  # eager work between replays
         torch.cuda.synchronize()

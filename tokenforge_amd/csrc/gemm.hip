@@ -158,9 +158,11 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(LinearArgs a, float*
   }
 
   // D layout of the 32x32 MFMA: register r of lane l is row 8*(r/4) + 4*(l/32) + r%4,
-  // column l%32. A SiLU*mul epilogue pairs columns n and n + N/2 of different tiles, so it
-  // goes through fp32 partials and the reduce kernel, like split-K.
-  const bool partials = split_k > 1 || a.epilogue == TF_EPILOGUE_SILU_MUL;
+  // column l%32. A SiLU*mul epilogue pairs columns n and n + N/2 of different tiles: without
+  // split-K the fp16 y goes to the workspace for silu_mul_kernel, with split-K the fp32
+  // partials go to the reduce kernel.
+  const bool partials = split_k > 1;
+  const bool stage_y = !partials && a.epilogue == TF_EPILOGUE_SILU_MUL;
 #pragma unroll
   for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
@@ -172,7 +174,9 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(LinearArgs a, float*
       for (int r = 0; r < 16; ++r) {
         const int m = m0 + (wm * TM + tm) * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
         if (m >= a.m) continue;
-        if (!partials)
+        if (stage_y)
+          reinterpret_cast<uint16_t*>(ws)[(int64_t)m * a.n + n] = f16_bits(acc[tm][tn][r] + b);
+        else if (!partials)
           store_out(a, m, n, acc[tm][tn][r] + b);
         else
           ws[((int64_t)z * a.m + m) * a.n + n] = acc[tm][tn][r];
@@ -209,10 +213,42 @@ __global__ void splitk_reduce_kernel(LinearArgs a, const float* __restrict__ ws,
 
 }  // namespace
 
+// SiLU*mul over an fp16 y [m, n] (row stride n) staged in the workspace.
+__global__ void silu_mul_kernel(LinearArgs a, const uint16_t* __restrict__ y) {
+  const int half = a.n >> 1;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)a.m * half) return;
+  const int64_t row = i / half;
+  const int64_t col = i % half;
+  a.out[row * a.ldo + col] =
+      finish_silu_mul(half_bits_to_float(y[row * a.n + col]), half_bits_to_float(y[row * a.n + half + col]));
+}
+
+int silu_mul_staged(const LinearArgs& a, const float* ws, hipStream_t stream) {
+  const int64_t total = (int64_t)a.m * (a.n >> 1);
+  silu_mul_kernel<<<(unsigned)cdiv(total, 256), 256, 0, stream>>>(a, reinterpret_cast<const uint16_t*>(ws));
+  return check_launch("tf_w4a16_linear(silu_mul)");
+}
+
 int splitk_reduce(const LinearArgs& a, const float* ws, int split, hipStream_t stream) {
   const int64_t total = (int64_t)a.m * (a.epilogue == TF_EPILOGUE_SILU_MUL ? a.n >> 1 : a.n);
   splitk_reduce_kernel<<<(unsigned)cdiv(total, 256), 256, 0, stream>>>(a, ws, split);
   return check_launch("tf_w4a16_linear(splitk_reduce)");
+}
+
+// Workspace of an LDS-tile GEMM launch: fp32 partials under split-K, the fp16 y under a
+// SiLU*mul epilogue without split-K, else none.
+int64_t lds_gemm_workspace(const LinearArgs& a, int split) {
+  if (split > 1) return (int64_t)split * a.m * a.n * (int64_t)sizeof(float);
+  if (a.epilogue == TF_EPILOGUE_SILU_MUL) return (int64_t)a.m * a.n * 2;
+  return 0;
+}
+
+// The kernel after an LDS-tile GEMM launch, if any.
+int lds_gemm_finish(const LinearArgs& a, const float* ws, int split, hipStream_t stream) {
+  if (split > 1) return splitk_reduce(a, ws, split, stream);
+  if (a.epilogue == TF_EPILOGUE_SILU_MUL) return silu_mul_staged(a, ws, stream);
+  return TF_OK;
 }
 
 namespace {
@@ -223,20 +259,18 @@ int effective_split(const LinearArgs& a, const tf_gemm_config& cfg) {
 }
 
 int64_t gemm_workspace(const LinearArgs& a, const tf_gemm_config& cfg) {
-  const int s = effective_split(a, cfg);
-  const bool partials = s > 1 || a.epilogue == TF_EPILOGUE_SILU_MUL;
-  return partials ? (int64_t)s * a.m * a.n * (int64_t)sizeof(float) : 0;
+  return lds_gemm_workspace(a, effective_split(a, cfg));
 }
 
 template <int BM, int BN, int BK, int WM, int WN>
 int launch_gemm(const LinearArgs& a, const tf_gemm_config& cfg, float* ws, hipStream_t stream) {
   const int split = effective_split(a, cfg);
-  const bool partials = split > 1 || a.epilogue == TF_EPILOGUE_SILU_MUL;
-  if (partials && ws == nullptr) return fail(TF_EINVAL, "tf_w4a16_linear: this config needs a workspace");
+  if (lds_gemm_workspace(a, split) > 0 && ws == nullptr)
+    return fail(TF_EINVAL, "tf_w4a16_linear: this config needs a workspace");
   const dim3 grid((unsigned)cdiv(a.n, BN), (unsigned)cdiv(a.m, BM), (unsigned)split);
   gemm_kernel<BM, BN, BK, WM, WN><<<grid, WM * WN * 64, 0, stream>>>(a, ws, split);
   if (int rc = check_launch("tf_w4a16_linear(gemm_mfma)")) return rc;
-  if (partials) return splitk_reduce(a, ws, split, stream);
+  return lds_gemm_finish(a, ws, split, stream);
   return TF_OK;
 }
 

@@ -34,6 +34,8 @@
 namespace tf {
 
 int splitk_reduce(const LinearArgs& a, const float* ws, int split, hipStream_t stream);
+int64_t lds_gemm_workspace(const LinearArgs& a, int split);
+int lds_gemm_finish(const LinearArgs& a, const float* ws, int split, hipStream_t stream);
 
 namespace {
 
@@ -266,9 +268,11 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm2_kernel(LinearArgs a, float
   if (kb < kb1) iteration(kb, S == 2 ? 0 : st, std::integral_constant<int, 0>{});
 
   // ---- epilogue. D layout of the 32x32 MFMA: register q of lane l is row
-  // 8 (q / 4) + 4 (l / 32) + q % 4, column l % 32. A SiLU*mul epilogue goes through fp32
-  // partials and the reduce kernel (its column pairs span tiles).
-  const bool partials = split_k > 1 || a.epilogue == TF_EPILOGUE_SILU_MUL;
+  // 8 (q / 4) + 4 (l / 32) + q % 4, column l % 32. A SiLU*mul epilogue pairs columns of
+  // different tiles: without split-K the fp16 y goes to the workspace for the SiLU*mul
+  // kernel, with split-K the fp32 partials go to the reduce kernel.
+  const bool partials = split_k > 1;
+  const bool stage_y = !partials && a.epilogue == TF_EPILOGUE_SILU_MUL;
 #pragma unroll
   for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
@@ -280,7 +284,9 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm2_kernel(LinearArgs a, float
       for (int q = 0; q < 16; ++q) {
         const int m = m0 + (wm * TM + tm) * 32 + 8 * (q / 4) + 4 * (lane >> 5) + (q % 4);
         if (m >= a.m) continue;
-        if (!partials)
+        if (stage_y)
+          reinterpret_cast<uint16_t*>(ws)[(int64_t)m * a.n + n] = f16_bits(acc[tm][tn][q] + b);
+        else if (!partials)
           store_out(a, m, n, acc[tm][tn][q] + b);
         else
           ws[((int64_t)z * a.m + m) * a.n + n] = acc[tm][tn][q];
@@ -294,9 +300,7 @@ int effective_split2(const LinearArgs& a, const tf_gemm_config& cfg) {
 }
 
 int64_t gemm2_workspace(const LinearArgs& a, const tf_gemm_config& cfg) {
-  const int s = effective_split2(a, cfg);
-  const bool partials = s > 1 || a.epilogue == TF_EPILOGUE_SILU_MUL;
-  return partials ? (int64_t)s * a.m * a.n * (int64_t)sizeof(float) : 0;
+  return lds_gemm_workspace(a, effective_split2(a, cfg));
 }
 
 template <int BM, int BN, int WM, int WN, int S>
@@ -309,8 +313,8 @@ int launch_gemm2(const LinearArgs& a, const tf_gemm_config& cfg, float* ws, hipS
   if (x_bytes >= (int64_t)kOutOfRange || w_bytes >= (int64_t)kOutOfRange)
     return fail(TF_EINVAL, "tf_w4a16_linear: this gemm_mfma variant needs x and qweight_t below 2 GiB");
   const int split = effective_split2(a, cfg);
-  const bool partials = split > 1 || a.epilogue == TF_EPILOGUE_SILU_MUL;
-  if (partials && ws == nullptr) return fail(TF_EINVAL, "tf_w4a16_linear: this config needs a workspace");
+  if (lds_gemm_workspace(a, split) > 0 && ws == nullptr)
+    return fail(TF_EINVAL, "tf_w4a16_linear: this config needs a workspace");
   const int tiles_n = (int)cdiv(a.n, BN);
   const int tiles_m = (int)cdiv(a.m, BM);
   const int64_t grid = (int64_t)tiles_n * tiles_m * split;
@@ -322,7 +326,7 @@ int launch_gemm2(const LinearArgs& a, const tf_gemm_config& cfg, float* ws, hipS
     return fail(TF_ELAUNCH, "tf_w4a16_linear: cannot reserve LDS for gemm_mfma");
   kernel<<<(unsigned)grid, C::kThreads, C::kLds, stream>>>(a, ws, split, tiles_n, tiles_m);
   if (int rc = check_launch("tf_w4a16_linear(gemm_mfma)")) return rc;
-  if (partials) return splitk_reduce(a, ws, split, stream);
+  return lds_gemm_finish(a, ws, split, stream);
   return TF_OK;
 }
 
