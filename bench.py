@@ -1,6 +1,7 @@
 """Benchmark of the MI355X quantized-linear hot path (the round driver's bench contract).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-tune] [--no-cpu] [--detail PATH] [--full] [--stack]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-tune] [--no-cpu] [--detail PATH] [--full]
+                    [--stack | --no-stack]
     python bench.py --traffic-probe      (eager launches for rocprofv3 --pmc, see below)
 
 Workload (BASELINE.json metric "W4A16 GEMV HBM GB/s at M=1 + GEMM TFLOP/s at M=256"):
@@ -321,6 +322,7 @@ def main() -> int:
                     help="also sweep the GEMM over M in {16..4096} (configs[3]) into --detail")
     ap.add_argument("--stack", action="store_true",
                     help="stack (configs[4]) also at M in {8, 32, 2048}, not only M=1")
+    ap.add_argument("--no-stack", action="store_true", help="skip the stack (configs[4])")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="eager gate_up GEMV launches + a calibration kernel, for rocprofv3 --pmc")
     args = ap.parse_args()
@@ -475,7 +477,9 @@ def main() -> int:
                 del g, xm, om
             del wt
 
-    stack = stack_bench(dev, gpu, (1, 8, 32, 2048) if (args.stack or args.full) else (1,), not args.no_tune)
+    stack = None
+    if not args.no_stack:
+        stack = stack_bench(dev, gpu, (1, 8, 32, 2048) if (args.stack or args.full) else (1,), not args.no_tune)
 
     cpu = None
     if not args.no_cpu:
