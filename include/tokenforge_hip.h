@@ -141,6 +141,24 @@ int tf_w4a16_linear_ex(const uint16_t* x, int64_t ldx, const int32_t* qweight_t,
                        const uint16_t* residual, int64_t ldr, float* workspace,
                        int64_t workspace_bytes, void* stream);
 
+/* W4A8: the linear on FP8 activations, e.g. tf_rmsnorm_fp8_quant's codes and scales. No
+ * counterpart in the reference, which never feeds its FP8 output to a linear.
+ *   out[m][n] = fp16( xscale[m] * sum_k e4m3(x8[m][k]) * fp16((q[n][k] - z) * s) + bias[n] )
+ * x8 e4m3fn codes [m, k], row stride ldx8 bytes (a multiple of 8; 16-byte aligned base);
+ * xscale fp32, row m at xscale[m * xscale_stride] (stride 0: one scale for every row).
+ * e4m3 values are exact in fp16, so with xscale = 1 this equals tf_w4a16_linear on the
+ * decoded x bit for bit. Epilogues as tf_w4a16_linear_ex (applied after the row scale).
+ * The GEMV configs with x staged in LDS (gemv_dot; gemv_mfma with block_k 128) decode the
+ * codes while staging; other configs decode x to fp16 into the workspace first. */
+int64_t tf_w4a8_workspace_bytes_ex(int64_t m, int64_t n, int64_t k, int32_t group_size,
+                                   const tf_gemm_config* cfg, int32_t epilogue);
+int tf_w4a8_linear_ex(const uint8_t* x8, int64_t ldx8, const float* xscale, int64_t xscale_stride,
+                      const int32_t* qweight_t, const uint16_t* scales, const int32_t* qzeros,
+                      const uint16_t* bias, uint16_t* out, int64_t ldo, int64_t m, int64_t n,
+                      int64_t k, int32_t group_size, const tf_gemm_config* cfg, int32_t epilogue,
+                      const uint16_t* residual, int64_t ldr, float* workspace,
+                      int64_t workspace_bytes, void* stream);
+
 /* --------------------------------------------------------------- RMSNorm + FP8 */
 
 /* rmsnorm_fp8.py:76-117 rmsnorm_fp8_quant (semantics of reference.py:35-56):

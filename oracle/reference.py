@@ -118,6 +118,22 @@ def e4m3_decode(codes: np.ndarray) -> np.ndarray:
     return _E4M3_TABLE[np.asarray(codes, dtype=np.uint8)]
 
 
+def w4a8_reference(
+    codes: np.ndarray, x_scale: np.ndarray, weights: W4A16Weights, bias: np.ndarray | None = None
+) -> np.ndarray:
+    """W4A8 (no counterpart in the reference; the build's definition): fp64
+    ``x_scale[m] * (e4m3(codes) @ W^T) (+ bias)``: :func:`w4a16_reference` (reference.py:13-21)
+    on the decoded activations, times the row scale, before the bias. ``x_scale`` holds one
+    scale or one per row."""
+    x = e4m3_decode(codes).astype(np.float64)
+    y = w4a16_reference(x, weights)
+    s = np.asarray(x_scale, dtype=np.float64).reshape(-1)
+    y = y * (s[:, None] if s.size > 1 else s[0])
+    if bias is not None:
+        y = y + np.asarray(bias).astype(np.float64)
+    return y
+
+
 def fp8_quant_reference(y: np.ndarray, scale: np.ndarray | None = None) -> tuple[np.ndarray, np.ndarray]:
     """reference.py:42-50: per-token dynamic (or static) saturating e4m3 quantization.
 

@@ -153,3 +153,29 @@ def test_dequant_matches_scalar_fp16(group: int) -> None:
             g = kk // group
             expect = np.float16(float(q[nn, kk] - z[g, nn])) * w.scales[g, nn]
             assert deq[nn, kk] == expect
+
+
+def test_w4a8_reference_exact_on_tiny_inputs() -> None:
+    """Exact rational arithmetic: y = s_m * sum_k e4m3(c[m, k]) * w[n, k] + b[n]."""
+    w = cases.layer_weights(16, 128, 7)
+    gen = np.random.default_rng(3)
+    codes = gen.integers(0, 256, size=(3, 128), dtype=np.uint8)
+    codes[(codes & 0x7F) == 0x7F] = 0x38  # no NaN codes: 1.0 instead
+    xs = np.array([0.5, 3.0, 2.0**-7], dtype=np.float32)
+    b = cases.bias(16, 1).numpy()
+    y = R.w4a8_reference(codes, xs, w, b)
+    wd = P.dequantize_tf(w)
+    for m in range(3):
+        for n in (0, 7, 15):
+            acc = sum(Fraction(float(R.e4m3_decode(codes[m, k]))) * Fraction(float(wd[n, k])) for k in range(128))
+            exact = Fraction(float(xs[m])) * acc + Fraction(float(b[n]))
+            assert float(exact) == pytest.approx(y[m, n], rel=1e-12, abs=1e-12)
+
+
+def test_w4a8_reference_reduces_to_w4a16_and_is_linear_in_scale() -> None:
+    w = cases.layer_weights(32, 256, 8)
+    codes = np.random.default_rng(4).integers(0, 0x7F, size=(4, 256), dtype=np.uint8)
+    one = R.w4a8_reference(codes, np.ones(1, dtype=np.float32), w)
+    assert np.array_equal(one, R.w4a16_reference(R.e4m3_decode(codes), w))
+    per_row = R.w4a8_reference(codes, np.array([2.0, 4.0, 0.25, 1.0], dtype=np.float32), w)
+    assert np.array_equal(per_row, one * np.array([2.0, 4.0, 0.25, 1.0])[:, None])

@@ -174,21 +174,24 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(LinearArgs a, float*
       for (int r = 0; r < 16; ++r) {
         const int m = m0 + (wm * TM + tm) * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
         if (m >= a.m) continue;
+        const float v = acc[tm][tn][r] * row_scale(a, m) + b;
         if (stage_y)
-          reinterpret_cast<uint16_t*>(ws)[(int64_t)m * a.n + n] = f16_bits(acc[tm][tn][r] + b);
+          reinterpret_cast<uint16_t*>(ws)[(int64_t)m * a.n + n] = f16_bits(v);
         else if (!partials)
-          store_out(a, m, n, acc[tm][tn][r] + b);
+          store_out(a, m, n, v);
         else
           ws[((int64_t)z * a.m + m) * a.n + n] = acc[tm][tn][r];
       }
     }
 }
 
-// Sum of the split partials of element (row, col) in split order, plus bias.
+// Sum of the split partials of element (row, col) in split order, times the row scale, plus
+// bias.
 __device__ __forceinline__ float reduce_partials(const float* __restrict__ ws, const uint16_t* __restrict__ bias,
-                                                 int64_t total, int64_t i, int64_t col, int split) {
+                                                 int64_t total, int64_t i, int64_t col, int split, float rs) {
   float v = ws[i];
   for (int s = 1; s < split; ++s) v += ws[(int64_t)s * total + i];
+  v = v * rs;
   if (bias) v += half_bits_to_float(bias[col]);
   return v;
 }
@@ -202,9 +205,10 @@ __global__ void splitk_reduce_kernel(LinearArgs a, const float* __restrict__ ws,
   const int64_t row = i / n_out;
   const int64_t col = i % n_out;
   const int64_t total = (int64_t)a.m * a.n;
-  const float v = reduce_partials(ws, a.bias, total, row * a.n + col, col, split);
+  const float rs = row_scale(a, (int)row);
+  const float v = reduce_partials(ws, a.bias, total, row * a.n + col, col, split, rs);
   if (a.epilogue == TF_EPILOGUE_SILU_MUL) {
-    const float u = reduce_partials(ws, a.bias, total, row * a.n + n_out + col, n_out + col, split);
+    const float u = reduce_partials(ws, a.bias, total, row * a.n + n_out + col, n_out + col, split, rs);
     a.out[row * a.ldo + col] = finish_silu_mul(v, u);
   } else {
     store_out(a, (int)row, (int)col, v);

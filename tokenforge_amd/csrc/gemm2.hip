@@ -284,10 +284,11 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm2_kernel(LinearArgs a, float
       for (int q = 0; q < 16; ++q) {
         const int m = m0 + (wm * TM + tm) * 32 + 8 * (q / 4) + 4 * (lane >> 5) + (q % 4);
         if (m >= a.m) continue;
+        const float v = acc[tm][tn][q] * row_scale(a, m) + b;
         if (stage_y)
-          reinterpret_cast<uint16_t*>(ws)[(int64_t)m * a.n + n] = f16_bits(acc[tm][tn][q] + b);
+          reinterpret_cast<uint16_t*>(ws)[(int64_t)m * a.n + n] = f16_bits(v);
         else if (!partials)
-          store_out(a, m, n, acc[tm][tn][q] + b);
+          store_out(a, m, n, v);
         else
           ws[((int64_t)z * a.m + m) * a.n + n] = acc[tm][tn][q];
       }

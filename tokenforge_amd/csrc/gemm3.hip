@@ -252,7 +252,7 @@ __global__ __launch_bounds__(256) void gemm3_kernel(LinearArgs a, float* __restr
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int m = m0 + wrow + mt * 16 + 4 * g + q;
-        const float v = acc[mt][rt][q] + b;
+        const float v = acc[mt][rt][q] * row_scale(a, m) + b;
         if (split_k == 1 && a.epilogue == TF_EPILOGUE_SILU_MUL) {
           const float u = __shfl_xor(v, 8);
           if (valid && !(l & 8) && m < a.m)

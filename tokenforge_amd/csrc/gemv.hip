@@ -42,7 +42,7 @@ __device__ __forceinline__ void k_range(int wave, int waves, int nsteps, int* s0
 
 // Buffer resources and per-launch constants shared by both kernels.
 struct Streams {
-  __amdgpu_buffer_rsrc_t qw, sc, qz, x;
+  __amdgpu_buffer_rsrc_t qw, sc, qz, x, x8;
   uint32_t row_bytes;  // K / 2
   int nchunks;         // K / 32
   int nsteps;          // ceil(K / 128)
@@ -59,6 +59,7 @@ __device__ __forceinline__ Streams make_streams(const LinearArgs& a) {
   s.sc = make_rsrc(a.scales, (uint32_t)(s.groups * a.n * 2));
   s.qz = make_rsrc(a.qz, (uint32_t)(s.groups * (a.n >> 3) * 4));
   s.x = make_rsrc(a.x, (uint32_t)(((int64_t)(a.m - 1) * a.ldx + a.k) * 2));
+  s.x8 = make_rsrc(a.x8, (uint32_t)((int64_t)(a.m - 1) * a.ldx8 + a.k));
   s.nchunks = a.k >> 5;
   s.nsteps = (s.nchunks + 3) >> 2;
   s.log2g = a.log2g;
@@ -143,7 +144,12 @@ __device__ __forceinline__ void load_batch(StageBatch<U>& b, const Window& w, co
     b.xq[u] = q;
     const int k = w.k0 + q * 8;
     const bool xok = e < w.xentries && k < a.k;
-    b.xv[u] = load_b128(st.x, xok ? (uint32_t)((w.m0 + r) * a.ldx + k) * 2u : kOutOfRange);
+    if (a.x8 != nullptr) {  // e4m3 codes, converted to fp16 when stored
+      const u2 c = load_b64(st.x8, xok ? (uint32_t)((int64_t)(w.m0 + r) * a.ldx8 + k) : kOutOfRange);
+      b.xv[u] = u4{c[0], c[1], 0u, 0u};
+    } else {
+      b.xv[u] = load_b128(st.x, xok ? (uint32_t)((w.m0 + r) * a.ldx + k) * 2u : kOutOfRange);
+    }
   }
 }
 
@@ -159,7 +165,9 @@ __device__ __forceinline__ void store_batch(uint32_t* p, _Float16* xs, const Sta
       const QuantParams q = make_params(zero_of(b.zw[u], (uint32_t)n), b.sb[u]);
       *reinterpret_cast<u4*>(p + kParamWords * e) = u4{as_u32(q.zlo), as_u32(q.zhi), as_u32(q.s), 0u};
     }
-    if (e < w.xentries) *reinterpret_cast<u4*>(xs + b.xr[u] * w.xstride + b.xq[u] * 8) = b.xv[u];
+    if (e < w.xentries)
+      *reinterpret_cast<u4*>(xs + b.xr[u] * w.xstride + b.xq[u] * 8) =
+          a.x8 != nullptr ? e4m3x8_to_f16(u2{b.xv[u][0], b.xv[u][1]}) : b.xv[u];
   }
 }
 
@@ -353,7 +361,7 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_dot_kernel(LinearArgs a, int w
       const float b = (a.bias && valid) ? half_bits_to_float(a.bias[n]) : 0.0f;
 #pragma unroll
       for (int m = 0; m < MAXM; ++m) {
-        const float v = acc[m][rt] + b;
+        const float v = acc[m][rt] * row_scale(a, m) + b;
         if (a.epilogue == TF_EPILOGUE_SILU_MUL) {
           const float u = __shfl_xor(v, 32);
           if (valid && !(l & 8) && m < a.m)
@@ -511,7 +519,7 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_mfma_kernel(LinearArgs a, int 
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int m = m_base + mt * 16 + 4 * g + r;
-          const float v = acc[mt][rt][r] + b;
+          const float v = acc[mt][rt][r] * row_scale(a, m) + b;
           if (a.epilogue == TF_EPILOGUE_SILU_MUL) {
             const float u = __shfl_xor(v, 8);
             if (valid && !(l & 8) && m < a.m)

@@ -26,7 +26,19 @@ struct LinearArgs {
   int epilogue = TF_EPILOGUE_NONE;
   const uint16_t* residual = nullptr;  // fp16 [m, n], row stride ldr
   int64_t ldr = 0;
+  // W4A8 input (tf_w4a8_linear_ex): e4m3fn codes [m, k] with row stride ldx8 bytes, read by
+  // the kernels that stage x (others get x converted to fp16 in `x`), and the fp32 row scales
+  // of x applied to each row's sum before the bias: y = xscale[m] * sum + bias.
+  const uint8_t* x8 = nullptr;
+  int64_t ldx8 = 0;
+  const float* xscale = nullptr;  // [m] with stride xscale_stride (0: one scale for all rows)
+  int64_t xscale_stride = 0;
 };
+
+// Row scale of row m (1 without a W4A8 input, and for rows past m, which are never stored).
+__device__ __forceinline__ float row_scale(const LinearArgs& a, int m) {
+  return (a.xscale != nullptr && m < a.m) ? a.xscale[(int64_t)m * a.xscale_stride] : 1.0f;
+}
 
 // Column mapping of the fused SiLU*mul epilogue for kernels that hold a 16-column group in
 // one row of 16 lanes: local column l of the tile at n_base takes the gate row

@@ -61,6 +61,27 @@ int check_config(const tf_gemm_config& cfg, int32_t group_size) {
   return TF_OK;
 }
 
+// Configs whose kernels read e4m3 x themselves (they stage x in LDS): the dot GEMV and the
+// MFMA GEMV with block_k 128. Every other config gets x converted to fp16 first.
+bool fuses_x8(const tf_gemm_config& cfg) {
+  return cfg.kernel == TF_KERNEL_GEMV_DOT || (cfg.kernel == TF_KERNEL_GEMV_MFMA && cfg.block_k == 128);
+}
+
+constexpr int64_t kWsAlign = 256;
+int64_t align_ws(int64_t b) { return (b + kWsAlign - 1) / kWsAlign * kWsAlign; }
+
+// e4m3 [m, k] (row stride ldx8 bytes) -> fp16 [m, k] (row stride k); 8 values per thread.
+__global__ void e4m3_rows_to_f16_kernel(const uint8_t* __restrict__ x8, int64_t ldx8, uint16_t* __restrict__ out,
+                                        int m, int k) {
+  const int64_t chunks = (int64_t)m * (k / 8);
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= chunks) return;
+  const int64_t row = i / (k / 8);
+  const int64_t c = i % (k / 8);
+  const u2 codes = *reinterpret_cast<const u2*>(x8 + row * ldx8 + c * 8);
+  *reinterpret_cast<u4*>(out + row * k + c * 8) = e4m3x8_to_f16(codes);
+}
+
 }  // namespace
 }  // namespace tf
 
@@ -167,4 +188,65 @@ extern "C" int tf_w4a16_linear(const uint16_t* x, int64_t ldx, const int32_t* qw
                                int64_t workspace_bytes, void* stream) {
   return tf_w4a16_linear_ex(x, ldx, qweight_t, scales, qzeros, bias, out, ldo, m, n, k, group_size, cfg,
                             TF_EPILOGUE_NONE, nullptr, 0, workspace, workspace_bytes, stream);
+}
+
+extern "C" int64_t tf_w4a8_workspace_bytes_ex(int64_t m, int64_t n, int64_t k, int32_t group_size,
+                                              const tf_gemm_config* cfg, int32_t epilogue) {
+  if (cfg == nullptr || m <= 0 || n <= 0 || k <= 0) return 0;
+  const int64_t own = tf_w4a16_workspace_bytes_ex(m, n, k, group_size, cfg, epilogue);
+  return fuses_x8(*cfg) ? own : align_ws(m * k * 2) + own;
+}
+
+extern "C" int tf_w4a8_linear_ex(const uint8_t* x8, int64_t ldx8, const float* xscale, int64_t xscale_stride,
+                                 const int32_t* qweight_t, const uint16_t* scales, const int32_t* qzeros,
+                                 const uint16_t* bias, uint16_t* out, int64_t ldo, int64_t m, int64_t n, int64_t k,
+                                 int32_t group_size, const tf_gemm_config* cfg, int32_t epilogue,
+                                 const uint16_t* residual, int64_t ldr, float* workspace, int64_t workspace_bytes,
+                                 void* stream) {
+  if (cfg == nullptr) return fail(TF_EINVAL, "tf_w4a8_linear_ex: null config");
+  if (ldx8 < k || ldx8 % 8) return fail(TF_EINVAL, "tf_w4a8_linear_ex: x row stride must be >= K and a multiple of 8");
+  if (xscale_stride < 0) return fail(TF_EINVAL, "tf_w4a8_linear_ex: negative scale stride");
+  if (m > 0 && n > 0) {
+    if (x8 == nullptr || xscale == nullptr) return fail(TF_EINVAL, "tf_w4a8_linear_ex: null pointer");
+    if ((reinterpret_cast<uintptr_t>(x8) & 15u) != 0)
+      return fail(TF_EINVAL, "tf_w4a8_linear_ex: x must be 16-byte aligned");
+  }
+  const int64_t need = tf_w4a8_workspace_bytes_ex(m, n, k, group_size, cfg, epilogue);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+    return fail(TF_EINVAL, "tf_w4a8_linear_ex: workspace too small");
+  const bool fused = fuses_x8(*cfg);
+  // The kernels that stage x read the codes; for the others x is converted to fp16 into the
+  // front of the workspace and the rest of the workspace is theirs.
+  const uint16_t* x16 = reinterpret_cast<const uint16_t*>(x8);
+  float* ws = workspace;
+  int64_t ws_bytes = workspace_bytes;
+  if (!fused && m > 0 && n > 0 && k > 0) {
+    uint16_t* conv = reinterpret_cast<uint16_t*>(workspace);
+    const int64_t chunks = m * (k / 8);
+    e4m3_rows_to_f16_kernel<<<(unsigned)cdiv(chunks, 256), 256, 0, (hipStream_t)stream>>>(x8, ldx8, conv, (int)m,
+                                                                                         (int)k);
+    if (int rc = check_launch("tf_w4a8_linear_ex(e4m3 to fp16)")) return rc;
+    x16 = conv;
+    const int64_t front = align_ws(m * k * 2);
+    ws = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) + front);
+    ws_bytes = workspace_bytes - front;
+  }
+  LinearArgs a;
+  if (int rc = make_args(x16, k, qweight_t, scales, qzeros, bias, out, ldo, m, n, k, group_size, epilogue,
+                         residual, ldr, &a))
+    return rc;
+  if (fused) {
+    a.x = nullptr;
+    a.x8 = x8;
+    a.ldx8 = ldx8;
+  }
+  a.xscale = xscale;
+  a.xscale_stride = xscale_stride;
+  if (int rc = check_config(*cfg, group_size)) return rc;
+  const Variant* v = find_variant(*cfg);
+  if (v == nullptr) return fail(TF_EINVAL, "tf_w4a8_linear_ex: config does not name a compiled variant");
+  if (m == 0 || n == 0) return TF_OK;
+  const int64_t own = v->workspace(a, *cfg);
+  if (own > 0 && (ws == nullptr || ws_bytes < own)) return fail(TF_EINVAL, "tf_w4a8_linear_ex: workspace too small");
+  return v->launch(a, *cfg, ws, (hipStream_t)stream);
 }

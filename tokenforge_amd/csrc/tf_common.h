@@ -22,6 +22,7 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef float f16v __attribute__((ext_vector_type(16)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u2 __attribute__((ext_vector_type(2)));
 
 // ------------------------------------------------------------------ host-side errors
 
@@ -64,6 +65,23 @@ __device__ __forceinline__ uint32_t load_b32(__amdgpu_buffer_rsrc_t r, uint32_t 
 }
 __device__ __forceinline__ uint32_t load_b16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0);
+}
+__device__ __forceinline__ u2 load_b64(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0);
+}
+
+// Eight OCP e4m3fn codes (two words) -> eight fp16 values, exactly (every e4m3fn value, NaN
+// included, is an fp16 value; the round-toward-zero pack therefore does not round).
+__device__ __forceinline__ u4 e4m3x8_to_f16(u2 codes) {
+  u4 r;
+#pragma unroll
+  for (int w = 0; w < 2; ++w) {
+    const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)codes[w], false);
+    const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)codes[w], true);
+    r[2 * w] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo[0], lo[1]));
+    r[2 * w + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(hi[0], hi[1]));
+  }
+  return r;
 }
 
 // ------------------------------------------------------------------ zero/scale operands

@@ -12,7 +12,7 @@ import functools
 import os
 from pathlib import Path
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 """Must equal ``tf_abi_version()`` of the loaded library."""
 
 LIB_ENV = "TOKENFORGE_HIP_LIB"
@@ -78,6 +78,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "tf_w4a16_linear_ex": (
         ctypes.c_int,
         [_p, _i64, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i32,
+         ctypes.POINTER(TfGemmConfig), _i32, _p, _i64, _p, _i64, _p],
+    ),
+    "tf_w4a8_workspace_bytes_ex": (_i64, [_i64, _i64, _i64, _i32, ctypes.POINTER(TfGemmConfig), _i32]),
+    "tf_w4a8_linear_ex": (
+        ctypes.c_int,
+        [_p, _i64, _p, _i64, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i32,
          ctypes.POINTER(TfGemmConfig), _i32, _p, _i64, _p, _i64, _p],
     ),
     "tf_rmsnorm_fp8_quant": (ctypes.c_int, [_p, _i64, _p, _p, _i64, _p, _i32, _i64, _i64, _f32, _p]),

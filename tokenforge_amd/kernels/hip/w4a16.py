@@ -184,3 +184,79 @@ def w4a16_dequant(
         )
     _lib.check(rc, "tf_w4a16_dequant")
     return out
+
+
+def _x_scale_stride(x_scale: torch.Tensor, m: int) -> int:
+    if x_scale.dtype != torch.float32:
+        raise TypeError(f"x_scale must be fp32, got {x_scale.dtype}")
+    if x_scale.numel() == 1:
+        return 0
+    if x_scale.numel() != m:
+        raise ValueError(f"x_scale must hold one scale or one per row ({m}), got shape {tuple(x_scale.shape)}")
+    return int(x_scale.reshape(m).stride(0))
+
+
+def w4a8_gemm_ex(
+    x8: torch.Tensor,
+    x_scale: torch.Tensor,
+    qweight_t: torch.Tensor,
+    scales: torch.Tensor,
+    qzeros: torch.Tensor,
+    group_size: int,
+    config: GemmConfig,
+    bias: torch.Tensor | None = None,
+    epilogue: str = "none",
+    residual: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """W4A8: ``x_scale[m] * (e4m3(x8) @ dequant(W)^T) (+ bias)`` -> fp16, with the epilogues of
+    :func:`w4a16_gemm_ex` (``tf_w4a8_linear_ex``). ``x8`` float8_e4m3fn ``[M, K]`` (as
+    ``rmsnorm_fp8_quant`` returns it), ``x_scale`` fp32 with one value or one per row."""
+    if x8.dim() != 2:
+        raise ValueError(f"x8 must be 2-D [M, K], got shape {tuple(x8.shape)}")
+    if x8.dtype != torch.float8_e4m3fn:
+        raise TypeError(f"x8 must be float8_e4m3fn, got {x8.dtype}")
+    m, k = x8.shape
+    n = qweight_t.shape[0]
+    # Shape checks of the fp16 path on a stand-in of x's shape.
+    _check_inputs(torch.empty((m, k), dtype=torch.float16, device="meta"), qweight_t, scales, qzeros, group_size)
+    config.validate(group_size)
+    if epilogue not in EPILOGUES:
+        raise ValueError(f"epilogue must be one of {sorted(EPILOGUES)}, got {epilogue!r}")
+    if bias is not None:
+        if tuple(bias.shape) != (n,) or bias.dtype != torch.float16:
+            raise ValueError(f"bias must be fp16 of shape {(n,)}")
+        bias = bias.contiguous()
+    if epilogue == "residual":
+        if residual is None or tuple(residual.shape) != (m, n) or residual.dtype != torch.float16:
+            raise ValueError(f"the residual epilogue needs an fp16 residual of shape {(m, n)}")
+        if residual.stride(-1) != 1:
+            residual = residual.contiguous()
+    elif residual is not None:
+        raise ValueError("residual is only used by the residual epilogue")
+    if epilogue == "silu_mul" and n % 16:
+        raise ValueError(f"the silu_mul epilogue needs N to be a multiple of 16, got {n}")
+    xs_stride = _x_scale_stride(x_scale, m)
+    tensors = (x8, x_scale, qweight_t, scales, qzeros) + tuple(t for t in (bias, residual) if t is not None)
+    dev = require_gpu("w4a8_gemm", *tensors)
+    n_out = n // 2 if epilogue == "silu_mul" else n
+    out = torch.empty((m, n_out), dtype=torch.float16, device=dev)
+    if m == 0 or n == 0:
+        return out
+    ldx8 = x8.stride(0) if m > 1 else k
+    if x8.stride(-1) != 1 or ldx8 % 8 or x8.data_ptr() % 16:
+        x8 = x8.clone(memory_format=torch.contiguous_format)  # a fresh, aligned allocation
+        ldx8 = k
+    ldr = (residual.stride(0) if m > 1 else n) if residual is not None else 0
+    code = EPILOGUES[epilogue]
+    c = to_c_config(config)
+    h = _lib.lib()
+    need = int(h.tf_w4a8_workspace_bytes_ex(m, n, k, group_size, ctypes.byref(c), code))
+    ws = torch.empty((max(need, 4) + 3) // 4, dtype=torch.float32, device=dev) if need else None
+    with on_device(dev):
+        rc = h.tf_w4a8_linear_ex(
+            x8.data_ptr(), ldx8, x_scale.data_ptr(), xs_stride, qweight_t.data_ptr(), scales.data_ptr(),
+            qzeros.data_ptr(), ptr(bias), out.data_ptr(), n_out, m, n, k, group_size, ctypes.byref(c), code,
+            ptr(residual), ldr, ptr(ws), need, stream_of(dev),
+        )
+    _lib.check(rc, "tf_w4a8_linear_ex")
+    return out

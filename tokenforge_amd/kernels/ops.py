@@ -18,7 +18,13 @@ arithmetic as separate torch ops after ``w4a16_linear``):
 * ``tokenforge::w4a16_linear_silu_mul(x, qweight_t, scales, qzeros, bias, group_size, backend)``
   = ``silu(y[..., :N/2]) * y[..., N/2:]`` with ``y = w4a16_linear(...)``
 
-Each equals its unfused torch expression on fp16 tensors bit for bit (same roundings). All
+Each equals its unfused torch expression on fp16 tensors bit for bit (same roundings). And
+the W4A8 form, which takes ``rmsnorm_fp8_quant``'s output directly (no counterpart either):
+
+* ``tokenforge::w4a8_linear(x8, x_scale, qweight_t, scales, qzeros, bias, group_size, backend,
+  epilogue, residual)`` = ``x_scale * (e4m3(x8) @ W^T) + bias`` (then the epilogue)
+
+All
 run hand-written HIP kernels; a CPU tensor or a missing kernel library raises instead of
 falling back.
 """
@@ -162,6 +168,60 @@ def _w4a16_linear_silu_mul_fake(
     backend: str,
 ) -> torch.Tensor:
     return x.new_empty((*x.shape[:-1], qweight_t.shape[0] // 2))
+
+
+@torch.library.custom_op("tokenforge::w4a8_linear", mutates_args=())
+def w4a8_linear(
+    x8: torch.Tensor,
+    x_scale: torch.Tensor,
+    qweight_t: torch.Tensor,
+    scales: torch.Tensor,
+    qzeros: torch.Tensor,
+    bias: torch.Tensor | None,
+    group_size: int,
+    backend: str,
+    epilogue: str = "none",
+    residual: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """W4A8 linear on FP8 activations: ``x_scale * (e4m3(x8) @ dequant(W)^T) + bias`` with an
+    optional epilogue ("none", "residual", "silu_mul"); ``x8``/``x_scale`` as
+    ``rmsnorm_fp8_quant`` returns them (scale [..., 1] per row, or one static scale)."""
+    k = x8.shape[-1]
+    n = qweight_t.shape[0]
+    n_out = n // 2 if epilogue == "silu_mul" else n
+    out_shape = (*x8.shape[:-1], n_out)
+    x2 = x8.reshape(-1, k)
+    m = x2.shape[0]
+    if m == 0:
+        return x8.new_empty(out_shape, dtype=torch.float16)
+    if backend not in dispatch.HIP_BACKENDS:
+        raise ValueError(
+            f"backend must be 'hip' (or its aliases 'triton', 'cuda') at op level, got {backend!r}"
+        )
+    decision = dispatch.select(m, backend=backend, on_gpu=x8.is_cuda, hip_ok=hip_runnable(x2))  # type: ignore[arg-type]
+    cfg = autotune.lookup(_gpu_id(x8.device), dispatch.lookup_bucket(m), n, k, group_size)
+    dispatch.record(dispatch.Decision("hip_gemm" if cfg.family == "gemm" else "hip_gemv", decision.bucket))
+    s2 = x_scale.reshape(-1) if x_scale.numel() > 1 else x_scale.reshape(1)
+    r2 = residual.reshape(-1, n) if residual is not None else None
+    y = _w4a16.w4a8_gemm_ex(x2, s2, qweight_t, scales, qzeros, group_size, cfg, bias, epilogue, r2)
+    return y.reshape(out_shape)
+
+
+@w4a8_linear.register_fake
+def _w4a8_linear_fake(
+    x8: torch.Tensor,
+    x_scale: torch.Tensor,
+    qweight_t: torch.Tensor,
+    scales: torch.Tensor,
+    qzeros: torch.Tensor,
+    bias: torch.Tensor | None,
+    group_size: int,
+    backend: str,
+    epilogue: str = "none",
+    residual: torch.Tensor | None = None,
+) -> torch.Tensor:
+    n = qweight_t.shape[0]
+    return x8.new_empty((*x8.shape[:-1], n // 2 if epilogue == "silu_mul" else n), dtype=torch.float16)
 
 
 @torch.library.custom_op("tokenforge::w4a16_dequant", mutates_args=())
