@@ -44,9 +44,11 @@ Extra objects on the same JSON line:
   h // 7) -> o_proj -> residual add -> RMSNorm + FP8 -> fp16(q * scale) -> gate_up -> SiLU(gate)
   * up -> down -> residual add. The linears and the norms are this library's kernels, the
   rest is torch glue ("unfused"), or the residual adds and SiLU*mul run as the linears'
-  fused epilogues ("fused", same bits; ``tokens_per_s`` is this one). A pass is one HIP
-  graph, tokens/s = M / time per pass. M=1 on every run; ``--stack`` or ``--full`` add M in
-  {8, 32} (decode) and 2048 (prefill).
+  fused epilogues ("fused", same bits; ``tokens_per_s`` is this one), or in addition qkv and
+  gate_up take the FP8 codes and scales directly as W4A8 linears ("w4a8", no fp16(q * scale)
+  glue; not bit-equal: the scale multiplies each row's sum instead of each element). A pass
+  is one HIP graph, tokens/s = M / time per pass. M=1 on every run; ``--stack`` or ``--full``
+  add M in {8, 32} (decode) and 2048 (prefill).
 * ``cpu_baseline``: reference.py's CPU path (dequantize per call + fp32 matmul), restated in
   torch on the host cores, on a bounded sample of the same step.
 """
@@ -195,8 +197,8 @@ KV_HEADS = 4
 
 def stack_bench(dev: torch.device, gpu: str, ms: tuple[int, ...], tune: bool) -> list[dict]:  # type: ignore[type-arg]
     """configs[4]: tokens/s of one pass through 28 decoder layers, per M (module docstring);
-    each M timed with the unfused torch glue and with the fused epilogues (residual adds in
-    o_proj and down, SiLU*mul in gate_up), which give the same bits."""
+    each M timed with the unfused torch glue, with the fused epilogues (residual adds in
+    o_proj and down, SiLU*mul in gate_up; same bits) and with W4A8 qkv and gate_up."""
     from tokenforge_amd.kernels import autotune
 
     eps = 1e-6
@@ -222,17 +224,23 @@ def stack_bench(dev: torch.device, gpu: str, ms: tuple[int, ...], tune: bool) ->
         (qkv, o, gu, down), bias, g1, g2 = layer
         m = x.shape[0]
         q8, s = ops.rmsnorm_fp8_quant(x, g1, eps, None)
-        a = (q8.to(torch.float32) * s).to(torch.float16)
-        y = ops.w4a16_linear(a, *qkv, bias, GROUP, "hip")
+        if mode == "w4a8":
+            y = ops.w4a8_linear(q8, s, *qkv, bias, GROUP, "hip")
+        else:
+            a = (q8.to(torch.float32) * s).to(torch.float16)
+            y = ops.w4a16_linear(a, *qkv, bias, GROUP, "hip")
         v = y[:, q_width + KV_HEADS * HEAD_DIM:].reshape(m, KV_HEADS, 1, HEAD_DIM)
         attn = v.expand(m, KV_HEADS, h // (KV_HEADS * HEAD_DIM), HEAD_DIM).reshape(m, h)
-        if not fused:
+        if mode == "unfused":
             x = x + ops.w4a16_linear(attn, *o, None, GROUP, "hip")
         else:
             x = ops.w4a16_linear_residual(attn, *o, None, x, GROUP, "hip")
         q8, s = ops.rmsnorm_fp8_quant(x, g2, eps, None)
+        if mode == "w4a8":
+            act = ops.w4a8_linear(q8, s, *gu, None, GROUP, "hip", "silu_mul")
+            return ops.w4a16_linear_residual(act, *down, None, x, GROUP, "hip")
         a = (q8.to(torch.float32) * s).to(torch.float16)
-        if not fused:
+        if mode == "unfused":
             y = ops.w4a16_linear(a, *gu, None, GROUP, "hip")
             act = torch.nn.functional.silu(y[:, :inter]) * y[:, inter:]
             return x + ops.w4a16_linear(act, *down, None, GROUP, "hip")
@@ -241,7 +249,7 @@ def stack_bench(dev: torch.device, gpu: str, ms: tuple[int, ...], tune: bool) ->
 
     res = []
     gen = torch.Generator(device=dev).manual_seed(11)
-    fused = False
+    mode = "unfused"
     for m in ms:
         x0 = torch.randn((m, h), generator=gen, device=dev).to(torch.float16)
 
@@ -253,22 +261,24 @@ def stack_bench(dev: torch.device, gpu: str, ms: tuple[int, ...], tune: bool) ->
 
         row: dict = {"m": m, "layers": STACK_LAYERS, "weight_bytes": total}  # type: ignore[type-arg]
         outs_by_mode = {}
-        for fused in (False, True):
+        for mode in ("unfused", "fused", "w4a8"):
             g, outs = capture([full_pass], warm=1)
             ms_pass = median_replay_ms(g, 1)  # replays the graph: outs[0] holds the pass's output
             if not bool(torch.isfinite(outs[0]).all()):
                 raise RuntimeError(f"stack pass at M={m} produced non-finite values")
-            outs_by_mode[fused] = outs[0]
+            outs_by_mode[mode] = outs[0]
             step_bytes = sum(bytes_moved(m, n, k) for _, n, k in SHAPES) * STACK_LAYERS
             flops = 2 * m * sum(n * k for _, n, k in SHAPES) * STACK_LAYERS
-            key = "fused" if fused else "unfused"
+            key = mode
             row[key] = {"ms_per_pass": ms_pass, "tokens_per_s": m / (ms_pass * 1e-3),
                         "linear_gbps": step_bytes / (ms_pass * 1e-3) / 1e9,
                         "linear_tflops": flops / (ms_pass * 1e-3) / 1e12}
             log(f"  stack M={m:<5d} {key:8s} {ms_pass * 1e3:9.1f} us/pass {m / (ms_pass * 1e-3):9.0f} tok/s "
                 f"({step_bytes / (ms_pass * 1e-3) / 1e9:.0f} GB/s of linear bytes)")
             del g, outs
-        row["fused_equals_unfused"] = bool(torch.equal(outs_by_mode[False], outs_by_mode[True]))
+        row["fused_equals_unfused"] = bool(torch.equal(outs_by_mode["unfused"], outs_by_mode["fused"]))
+        ref = outs_by_mode["fused"].float()
+        row["w4a8_normwise_vs_fp16_input"] = float((outs_by_mode["w4a8"].float() - ref).abs().max() / ref.abs().max())
         row["tokens_per_s"] = row["fused"]["tokens_per_s"]
         res.append(row)
         del outs_by_mode
