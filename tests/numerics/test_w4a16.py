@@ -152,8 +152,9 @@ def test_every_code_path(cfg: GemmConfig, with_bias: bool, device: torch.device)
     ids=_cfg_id,
 )
 def test_gemv_staging_windows(cfg: GemmConfig, device: torch.device) -> None:
-    """One wave over a long K with group 32: its dequantization operands (and x slice) exceed
-    the LDS, so the wave stages several windows. K = 8288 also ends in a partial 128-wide step."""
+    """One wave over a long K with group 32: its x slice (16 rows for the MFMA variants)
+    exceeds the LDS, so the wave stages several windows. K = 8288 also ends in a partial
+    128-wide step (the kernels that check each step's bounds per lane)."""
     n, k, group = 200, 8288, 32
     w = cases.layer_weights(n, k, 3, group)
     wd = cases.on_device(w, device)

@@ -8,16 +8,16 @@
 //
 // Memory stream: a "step" is 16 rows x 128 K values. Per step each lane issues one 128-bit
 // buffer load per 16-row tile (4 packed words = 32 weights of one row), so each row receives
-// a 64-byte run per load and consecutive steps complete the 128-byte lines. Every wave keeps
-// a ring of P steps in flight: the loads of step s + P are issued as soon as step s has been
-// consumed. Buffer loads return zeros past the end of a tensor, which handles ragged N and a
-// partial last step without branches.
+// a 64-byte run per load and consecutive steps complete the 128-byte lines, plus the scale and
+// the zero-point word of that row and the lane's group. Every wave keeps a register ring of P
+// steps in flight: the loads of step s + P are issued as soon as step s has been consumed.
+// Buffer loads return zeros past the end of a tensor, which handles ragged N and a partial last
+// step without branches. When K is a multiple of 128 the per-step part of every offset is
+// wave-uniform and travels in the scalar offset of the load (no address arithmetic per step).
 //
-// Only the weight stream uses the vector-memory path inside the loop. Before the loop each
-// wave stages what it will reuse in its own LDS region (no barrier needed, a wave reads only
-// what it wrote): the dequantization operands (1024 + z, 64 + z, scale as fp16 pairs) of every
-// (group, column) of its K range, and, in the XLDS variants, its slice of x. Measured on
-// MI355X, per-step scale/zero/x loads cost more than the dequantization arithmetic.
+// Before the loop each wave stages its slice of x in its own LDS region (no barrier needed, a
+// wave reads only what it wrote). Measured on MI355X, the scale/zero loads in the ring beat
+// staging the dequantization operands in LDS per wave (gate_up and down at M = 1 ~12% faster).
 //
 //  * gemv_dot  (TF_KERNEL_GEMV_DOT): lane = (row c = lane/4, chunk g = lane%4). Each lane
 //    accumulates its products with v_dot2_f32_f16; quads are reduced with DPP.
@@ -43,12 +43,15 @@ __device__ __forceinline__ void k_range(int wave, int waves, int nsteps, int* s0
 // Buffer resources and per-launch constants shared by both kernels.
 struct Streams {
   __amdgpu_buffer_rsrc_t qw, sc, qz, x, x8;
+  __amdgpu_buffer_rsrc_t none;  // zero records: every load through it returns zeros, no traffic
   uint32_t row_bytes;  // K / 2
   int nchunks;         // K / 32
   int nsteps;          // ceil(K / 128)
   int groups;          // K / G
   int log2g;
   int n;
+  int sc_step;         // bytes of scales per 128-wide step: (128 / G) * N * 2
+  int qz_step;         // bytes of qzeros per step: (128 / G) * (N / 8) * 4
 };
 
 __device__ __forceinline__ Streams make_streams(const LinearArgs& a) {
@@ -60,45 +63,31 @@ __device__ __forceinline__ Streams make_streams(const LinearArgs& a) {
   s.qz = make_rsrc(a.qz, (uint32_t)(s.groups * (a.n >> 3) * 4));
   s.x = make_rsrc(a.x, (uint32_t)(((int64_t)(a.m - 1) * a.ldx + a.k) * 2));
   s.x8 = make_rsrc(a.x8, (uint32_t)((int64_t)(a.m - 1) * a.ldx8 + a.k));
+  s.none = make_rsrc(a.qw, 0u);
   s.nchunks = a.k >> 5;
   s.nsteps = (s.nchunks + 3) >> 2;
   s.log2g = a.log2g;
   s.n = a.n;
+  s.sc_step = (128 >> a.log2g) * a.n * 2;
+  s.qz_step = (128 >> a.log2g) * (a.n >> 3) * 4;
   return s;
 }
 
 // Largest number of 128-wide K steps any wave gets.
 __host__ __device__ __forceinline__ int max_steps(int nsteps, int waves) { return (nsteps + waves - 1) / waves; }
 
-// One staged (group, column) entry: fp16x2 (1024 + z), fp16x2 (64 + z), fp16x2 scale, unused;
-// four words so a lane fetches it with a single ds_read_b128.
-constexpr int kParamWords = 4;
-
-// Staging of one window of a wave's K range into its LDS region:
-//  * params: the dequantization operands of groups [g_lo, g_lo + ng) x columns
-//    the tile's 16 RT columns (phys_col), `slots` groups deep. Slots past ng get neutral operands (zero
-//    point 0, scale 0), so any word dequantizes to exactly 0 there.
-//  * x (rows > 0): x[m0 + r][k0, k0 + kn) for r < rows, row stride xstride halfs, zero at
-//    k >= K (buffer loads past the tensor return zeros only at its very end, so the K bound is
-//    explicit).
-// Work is split into batches of 64 U entries of each kind: load_batch issues a batch's loads
-// into registers, store_batch writes them to LDS, so a batch costs one memory latency and the
-// first batch can be issued ahead of the weight ring.
+// Staging of one window of a wave's x slice into its LDS region: x[m0 + r][k0, k0 + kn) for
+// r < rows, row stride xstride halfs, zero at k >= K (buffer loads past the tensor return zeros
+// only at its very end, so the K bound is explicit). Work is split into batches of 64 U 16-byte
+// chunks: load_batch issues a batch's loads into registers, store_batch writes them to LDS, so
+// a batch costs one memory latency and the first batch can be issued ahead of the weight ring.
 struct Window {
-  int n_base, g_lo, ng, pentries;
   int m0, rows, k0, chunks, xentries, xstride;
   float inv_chunks;
-  int total;  // max(pentries, xentries)
 };
 
-template <int RT>
-__device__ __forceinline__ Window make_window(const Streams& st, int n_base, int w0, int w1, int slots, int m0,
-                                              int rows, int xstride) {
+__device__ __forceinline__ Window make_window(int w0, int w1, int m0, int rows, int xstride) {
   Window w;
-  w.n_base = n_base;
-  w.g_lo = (w0 * 128) >> st.log2g;
-  w.ng = min(st.groups, (w1 * 128) >> st.log2g) - w.g_lo;
-  w.pentries = w1 > w0 ? slots * 16 * RT : 0;
   w.m0 = m0;
   w.rows = rows;
   w.k0 = w0 * 128;
@@ -106,30 +95,21 @@ __device__ __forceinline__ Window make_window(const Streams& st, int n_base, int
   w.xentries = rows * w.chunks;
   w.xstride = xstride;
   w.inv_chunks = 1.0f / (float)(w.chunks > 0 ? w.chunks : 1);
-  w.total = max(w.pentries, w.xentries);
   return w;
 }
 
 template <int U>
 struct StageBatch {
-  uint32_t sb[U], zw[U];
   u4 xv[U];
   int xr[U], xq[U];
 };
 
-template <int RT, int U>
+template <int U>
 __device__ __forceinline__ void load_batch(StageBatch<U>& b, const Window& w, const LinearArgs& a,
                                            const Streams& st, int base, int lane) {
-  constexpr int cols = 16 * RT;
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const int e = base + u * 64 + lane;
-    const int gi = e / cols;
-    const int n = phys_col(a, w.n_base, e % cols);
-    const bool ok = e < w.pentries && col_valid(a, w.n_base, e % cols) && gi < w.ng;
-    const uint32_t grp = (uint32_t)(w.g_lo + gi);
-    b.sb[u] = load_b16(st.sc, ok ? (grp * (uint32_t)st.n + (uint32_t)n) * 2u : kOutOfRange);
-    b.zw[u] = load_b32(st.qz, ok ? (grp * (uint32_t)(st.n >> 3) + (uint32_t)(n >> 3)) * 4u : kOutOfRange);
     // e = r * chunks + q; the float quotient is off by at most one for e < 2^24.
     int r = (int)((float)e * w.inv_chunks);
     int q = e - r * w.chunks;
@@ -153,18 +133,12 @@ __device__ __forceinline__ void load_batch(StageBatch<U>& b, const Window& w, co
   }
 }
 
-template <int RT, int U>
-__device__ __forceinline__ void store_batch(uint32_t* p, _Float16* xs, const StageBatch<U>& b, const Window& w,
+template <int U>
+__device__ __forceinline__ void store_batch(_Float16* xs, const StageBatch<U>& b, const Window& w,
                                             const LinearArgs& a, int base, int lane) {
-  constexpr int cols = 16 * RT;
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const int e = base + u * 64 + lane;
-    if (e < w.pentries) {
-      const int n = phys_col(a, w.n_base, e % cols);
-      const QuantParams q = make_params(zero_of(b.zw[u], (uint32_t)n), b.sb[u]);
-      *reinterpret_cast<u4*>(p + kParamWords * e) = u4{as_u32(q.zlo), as_u32(q.zhi), as_u32(q.s), 0u};
-    }
     if (e < w.xentries)
       *reinterpret_cast<u4*>(xs + b.xr[u] * w.xstride + b.xq[u] * 8) =
           a.x8 != nullptr ? e4m3x8_to_f16(u2{b.xv[u][0], b.xv[u][1]}) : b.xv[u];
@@ -172,78 +146,119 @@ __device__ __forceinline__ void store_batch(uint32_t* p, _Float16* xs, const Sta
 }
 
 // Stage the batches of a window from `first` on.
-template <int RT, int U>
-__device__ __forceinline__ void stage_rest(uint32_t* p, _Float16* xs, const Window& w, const LinearArgs& a,
-                                           const Streams& st, int first, int lane) {
-  for (int base = first; base < w.total; base += 64 * U) {
+template <int U>
+__device__ __forceinline__ void stage_rest(_Float16* xs, const Window& w, const LinearArgs& a, const Streams& st,
+                                           int first, int lane) {
+  for (int base = first; base < w.xentries; base += 64 * U) {
     StageBatch<U> b;
-    load_batch<RT, U>(b, w, a, st, base, lane);
-    store_batch<RT, U>(p, xs, b, w, a, base, lane);
+    load_batch<U>(b, w, a, st, base, lane);
+    store_batch<U>(xs, b, w, a, base, lane);
   }
 }
 
-__device__ __forceinline__ QuantParams read_params(const uint32_t* p) {
-  const u4 v = *reinterpret_cast<const u4*>(p);
-  QuantParams q;
-  q.zlo = as_h2(v[0]);
-  q.zhi = as_h2(v[1]);
-  q.s = as_h2(v[2]);
-  return q;
-}
-
-// Per-lane view of the weight stream: the lane reads 16 bytes (chunk g = 32 K values) of one
-// row per row tile and step; its rows are local columns l0 + 16 rt of the tile at n_base
-// (phys_col). off[rt] is the byte offset of that run in step 0 (kOutOfRange past N, and still
-// out of range after adding any step offset); lane_end is the first step whose chunk lies past
-// K for this lane or past the wave's range.
+// One ring slot: per row tile, the lane's 16 bytes of packed weights, the scales word holding
+// that row's scale (and its even/odd neighbour's) and the qzeros word of that row, for the
+// lane's group. Whole words: no extension of a 16-bit load sits between a load and its use,
+// where the compiler would wait for it early.
 template <int RT>
+struct Slot {
+  u4 w[RT];
+  uint32_t sw[RT], zw[RT];
+};
+
+// Per-lane view of the streams: the lane reads 16 bytes (chunk g = 32 K values, one group) of
+// one row per row tile and step; its rows are local columns l0 + 16 rt of the tile at n_base
+// (phys_col). The offsets are those of step 0 (kOutOfRange past N, and still out of range after
+// adding any step offset); lane_end is the first step whose chunk lies past K for this lane or
+// past the wave's range.
+//
+// FULLK (K a multiple of 128): every lane's chunk is inside K on every step of the range, so
+// the step part of each offset is wave-uniform and goes into the loads' scalar offset. That
+// part is not range-checked by the hardware; it never leaves the tensors because issued steps
+// stay below the wave's end (steps past it go through a resource with zero records) and the
+// vector part addresses a valid row and group (or is out of range, which stays out of range).
+template <int RT, bool FULLK>
 struct LaneStream {
-  uint32_t off[RT];
+  uint32_t woff[RT], soff[RT], zoff[RT], zsh[RT], ssel[RT];
   int lane_end;
+  int wave_end;  // s1, wave-uniform
 
   __device__ __forceinline__ LaneStream(const LinearArgs& a, const Streams& st, int n_base, int l0, int g, int s1) {
+    const uint32_t gl = (uint32_t)((g * 32) >> st.log2g);  // the lane's group inside a step
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
       const int l = l0 + rt * 16;
-      off[rt] = col_valid(a, n_base, l) ? (uint32_t)phys_col(a, n_base, l) * st.row_bytes + (uint32_t)g * 16u
-                                        : kOutOfRange;
+      const bool ok = col_valid(a, n_base, l);
+      const uint32_t n = (uint32_t)phys_col(a, n_base, l);
+      woff[rt] = ok ? n * st.row_bytes + (uint32_t)g * 16u : kOutOfRange;
+      soff[rt] = ok ? (gl * (uint32_t)st.n + (n & ~1u)) * 2u : kOutOfRange;  // N is a multiple of 8
+      ssel[rt] = (n & 1u) ? 0x03020302u : 0x01000100u;  // v_perm: this column's half in both halves
+      zoff[rt] = ok ? (gl * (uint32_t)(st.n >> 3) + (n >> 3)) * 4u : kOutOfRange;
+      zsh[rt] = 4u * awq_nibble_of(n & 7u);
     }
     lane_end = min(s1, (st.nchunks - g + 3) >> 2);
+    wave_end = s1;
   }
 
-  // Every call issues exactly RT loads (zeros when the step is out of range), so the ring
-  // below has the same loads in flight on every path and the compiler's vmcnt waits stay
-  // exact instead of draining the ring.
-  __device__ __forceinline__ void issue(u4 (&w)[RT], const Streams& st, int step) const {
-    const bool v = step < lane_end;
+  // Every call issues exactly 3 RT loads (zeros when the step is out of range), so the ring
+  // below has the same loads in flight on every path and the compiler's vmcnt waits stay exact
+  // instead of draining the ring.
+  __device__ __forceinline__ void issue(Slot<RT>& sl, const Streams& st, int step) const {
+    if (FULLK) {
+      const bool in = step < wave_end;
+      const __amdgpu_buffer_rsrc_t rw = in ? st.qw : st.none;
+      const __amdgpu_buffer_rsrc_t rs = in ? st.sc : st.none;
+      const __amdgpu_buffer_rsrc_t rz = in ? st.qz : st.none;
+      const int st_ = in ? step : 0;
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt) w[rt] = load_b128(st.qw, v ? off[rt] + (uint32_t)step * 64u : kOutOfRange);
+      for (int rt = 0; rt < RT; ++rt) {
+        sl.w[rt] = __builtin_amdgcn_raw_buffer_load_b128(rw, (int)woff[rt], st_ * 64, 0);
+        sl.sw[rt] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)soff[rt], st_ * st.sc_step, 0);
+        sl.zw[rt] = __builtin_amdgcn_raw_buffer_load_b32(rz, (int)zoff[rt], st_ * st.qz_step, 0);
+      }
+    } else {
+      const bool v = step < lane_end;
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        sl.w[rt] = load_b128(st.qw, v ? woff[rt] + (uint32_t)step * 64u : kOutOfRange);
+        sl.sw[rt] = load_b32(st.sc, v ? soff[rt] + (uint32_t)(step * st.sc_step) : kOutOfRange);
+        sl.zw[rt] = load_b32(st.qz, v ? zoff[rt] + (uint32_t)(step * st.qz_step) : kOutOfRange);
+      }
+    }
+  }
+
+  // Dequantization operands of row tile rt from a landed slot.
+  __device__ __forceinline__ QuantParams params(const Slot<RT>& sl, int rt) const {
+    const uint32_t z = (sl.zw[rt] >> zsh[rt]) & 0xFu;
+    const uint32_t zz = z | (z << 16);
+    QuantParams q;
+    q.zlo = as_h2(zz | 0x64006400u);         // 1024 + z (see make_params)
+    q.zhi = as_h2((zz << 4) | 0x54005400u);  // 64 + z
+    q.s = as_h2(__builtin_amdgcn_perm(sl.sw[rt], sl.sw[rt], ssel[rt]));
+    return q;
   }
 };
 
-// LDS carve-up of one launch. Each wave stages a window of `win` steps: its params for the
-// window's groups and (XLDS) the window's x slice; a wave whose range is longer re-stages per
-// window. When a range takes several windows, each holds a multiple of the ring depth, so ring
-// slot p always holds a step with (step - s0) % P == p.
+// LDS carve-up of one launch. Each wave stages a window of `win` steps of its x slice; a wave
+// whose range is longer re-stages per window. When a range takes several windows, each holds a
+// multiple of the ring depth, so ring slot p always holds a step with (step - s0) % P == p.
 struct GemvLds {
-  int pwords;      // params words per wave
   int xstride;     // halfs per staged x row
-  int wave_words;  // params + x words per wave
+  int wave_words;  // x words per wave
 };
 
-__host__ __device__ __forceinline__ GemvLds gemv_lds_layout(int win, int log2g, int cols, int x_rows) {
+__host__ __device__ __forceinline__ GemvLds gemv_lds_layout(int win, int x_rows) {
   GemvLds l;
-  l.pwords = win * (128 >> log2g) * cols * kParamWords;
   l.xstride = win * 128 + 8;
-  l.wave_words = l.pwords + (x_rows * l.xstride) / 2;
+  l.wave_words = (x_rows * l.xstride) / 2;
   return l;
 }
 
 // ------------------------------------------------------------------------ gemv_dot
 
-constexpr int kStageU = 2;  // staging entries per lane and batch
+constexpr int kStageU = 2;  // x staging chunks per lane and batch
 
-template <int MAXM, int RT, int P, int MAXW>
+template <int MAXM, int RT, int P, int MAXW, bool FULLK>
 __global__ __launch_bounds__(MAXW * 64) void gemv_dot_kernel(LinearArgs a, int win) {
   extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
   const int lane = threadIdx.x & 63;
@@ -256,17 +271,11 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_dot_kernel(LinearArgs a, int w
   const Streams st = make_streams(a);
   int s0, s1;
   k_range(wave, waves, st.nsteps, &s0, &s1);
-  const int gps = 128 >> st.log2g;
   const int xrows = a.m < MAXM ? a.m : MAXM;
-  const GemvLds L = gemv_lds_layout(win, st.log2g, cols, xrows);
-  uint32_t* prm = lds + wave * L.wave_words;
-  _Float16* xs = reinterpret_cast<_Float16*>(prm + L.pwords);
+  const GemvLds L = gemv_lds_layout(win, xrows);
+  _Float16* xs = reinterpret_cast<_Float16*>(lds + wave * L.wave_words);
   const UnpackConsts uc = unpack_consts();
-  const LaneStream<RT> ls_w(a, st, n_base, c, g, s1);
-
-  // Lane bases in LDS; a step adds a wave-uniform offset.
-  const uint32_t* plane = prm + kParamWords * ((((g * 32) >> st.log2g) * cols) + c);
-  const int pstep = kParamWords * gps * cols;
+  const LaneStream<RT, FULLK> ls_w(a, st, n_base, c, g, s1);
   const _Float16* xl = xs + g * 32;
 
   float acc[MAXM][RT];
@@ -276,24 +285,23 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_dot_kernel(LinearArgs a, int w
     for (int rt = 0; rt < RT; ++rt) acc[m][rt] = 0.0f;
 
   // The first staging batch goes out ahead of the weight ring: every wave of the grid issues
-  // its ring at once, and the operands that gate the first step must not queue behind it.
-  Window win0 = make_window<RT>(st, n_base, s0, min(s1, s0 + win), win * gps, 0, xrows, L.xstride);
+  // its ring at once, and the x chunks that gate the first step must not queue behind it.
+  Window win0 = make_window(s0, min(s1, s0 + win), 0, xrows, L.xstride);
   StageBatch<kStageU> first;
-  load_batch<RT, kStageU>(first, win0, a, st, 0, lane);
+  load_batch<kStageU>(first, win0, a, st, 0, lane);
   __builtin_amdgcn_sched_barrier(0);
-  u4 ring[P][RT];
+  Slot<RT> ring[P];
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     ls_w.issue(ring[p], st, s0 + p);
     __builtin_amdgcn_sched_barrier(0);  // keep slot order: slot 0 must be the oldest ring load
   }
-  store_batch<RT, kStageU>(prm, xs, first, win0, a, 0, lane);
-  stage_rest<RT, kStageU>(prm, xs, win0, a, st, 64 * kStageU, lane);
+  store_batch<kStageU>(xs, first, win0, a, 0, lane);
+  stage_rest<kStageU>(xs, win0, a, st, 64 * kStageU, lane);
 
   for (int w0 = s0; w0 < s1; w0 += win) {
     const int w1 = min(s1, w0 + win);
-    if (w0 != s0) stage_rest<RT, kStageU>(prm, xs, make_window<RT>(st, n_base, w0, w1, win * gps, 0, xrows, L.xstride),
-                                         a, st, 0, lane);
+    if (w0 != s0) stage_rest<kStageU>(xs, make_window(w0, w1, 0, xrows, L.xstride), a, st, 0, lane);
     for (int s = w0; s < w1; s += P) {
 #pragma unroll
       for (int p = 0; p < P; ++p) {
@@ -310,11 +318,11 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_dot_kernel(LinearArgs a, int w
           }
 #pragma unroll
           for (int rt = 0; rt < RT; ++rt) {
-            const QuantParams qp = read_params(plane + ls * pstep + rt * 16 * kParamWords);
+            const QuantParams qp = ls_w.params(ring[p], rt);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
               h2 wd[4];
-              dequant_word(ring[p][rt][j], qp, uc, wd);
+              dequant_word(ring[p].w[rt][j], qp, uc, wd);
 #pragma unroll
               for (int m = 0; m < MAXM; ++m)
 #pragma unroll
@@ -324,6 +332,9 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_dot_kernel(LinearArgs a, int w
           }
         }
         ls_w.issue(ring[p], st, step + P);
+        // Slot boundary: keep the next slot's operand work (which waits for its loads) from
+        // being hoisted above this point, where it would wait for more of the ring than needed.
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
   }
@@ -376,7 +387,7 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_dot_kernel(LinearArgs a, int w
 
 // ------------------------------------------------------------------------ gemv_mfma
 
-template <int MT, int RT, int P, int MAXW, bool XLDS>
+template <int MT, int RT, int P, int MAXW, bool XLDS, bool FULLK>
 __global__ __launch_bounds__(MAXW * 64) void gemv_mfma_kernel(LinearArgs a, int win) {
   extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
   const int lane = threadIdx.x & 63;
@@ -390,17 +401,13 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_mfma_kernel(LinearArgs a, int 
   const Streams st = make_streams(a);
   int s0, s1;
   k_range(wave, waves, st.nsteps, &s0, &s1);
-  const int gps = 128 >> st.log2g;
   const int xrows = min(16 * MT, a.m - m_base);  // rows staged by this workgroup
   const int xalloc = min(16 * MT, a.m);          // rows allocated per wave (same in every workgroup)
-  const GemvLds L = gemv_lds_layout(win, st.log2g, cols, XLDS ? xalloc : 0);
-  uint32_t* prm = lds + wave * L.wave_words;
-  _Float16* xs = reinterpret_cast<_Float16*>(prm + L.pwords);
+  const GemvLds L = gemv_lds_layout(win, XLDS ? xalloc : 0);
+  _Float16* xs = reinterpret_cast<_Float16*>(lds + wave * L.wave_words);
   const UnpackConsts uc = unpack_consts();
-  const LaneStream<RT> ls_w(a, st, n_base, c, g, s1);
+  const LaneStream<RT, FULLK> ls_w(a, st, n_base, c, g, s1);
 
-  const uint32_t* plane = prm + kParamWords * ((((g * 32) >> st.log2g) * cols) + c);
-  const int pstep = kParamWords * gps * cols;
   const _Float16* xl[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
@@ -421,7 +428,7 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_mfma_kernel(LinearArgs a, int 
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) acc[mt][rt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  u4 ring[P][RT];
+  Slot<RT> ring[P];
   u4 xring[XLDS ? 1 : P][XLDS ? 1 : MT][4];
   auto issue = [&](int p, int step) {
     ls_w.issue(ring[p], st, step);
@@ -437,23 +444,24 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_mfma_kernel(LinearArgs a, int 
   };
   // The first staging batch goes out ahead of the weight ring (see gemv_dot_kernel).
   const int srows = XLDS ? xrows : 0;
-  Window win0 = make_window<RT>(st, n_base, s0, min(s1, s0 + win), win * gps, m_base, srows, L.xstride);
+  Window win0 = make_window(s0, min(s1, s0 + win), m_base, srows, L.xstride);
   StageBatch<kStageU> first;
-  load_batch<RT, kStageU>(first, win0, a, st, 0, lane);
+  if (XLDS) load_batch<kStageU>(first, win0, a, st, 0, lane);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     issue(p, s0 + p);
     __builtin_amdgcn_sched_barrier(0);  // keep slot order: slot 0 must be the oldest ring load
   }
-  store_batch<RT, kStageU>(prm, xs, first, win0, a, 0, lane);
-  stage_rest<RT, kStageU>(prm, xs, win0, a, st, 64 * kStageU, lane);
+  if (XLDS) {
+    store_batch<kStageU>(xs, first, win0, a, 0, lane);
+    stage_rest<kStageU>(xs, win0, a, st, 64 * kStageU, lane);
+  }
 
   for (int w0 = s0; w0 < s1; w0 += win) {
     const int w1 = min(s1, w0 + win);
-    if (w0 != s0)
-      stage_rest<RT, kStageU>(prm, xs, make_window<RT>(st, n_base, w0, w1, win * gps, m_base, srows, L.xstride), a,
-                             st, 0, lane);
+    if (XLDS && w0 != s0)
+      stage_rest<kStageU>(xs, make_window(w0, w1, m_base, srows, L.xstride), a, st, 0, lane);
     for (int s = w0; s < w1; s += P) {
 #pragma unroll
       for (int p = 0; p < P; ++p) {
@@ -469,11 +477,11 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_mfma_kernel(LinearArgs a, int 
                                : __builtin_bit_cast(h8, xring[XLDS ? 0 : p][mt][j]);
 #pragma unroll
           for (int rt = 0; rt < RT; ++rt) {
-            const QuantParams qp = read_params(plane + ls * pstep + rt * 16 * kParamWords);
+            const QuantParams qp = ls_w.params(ring[p], rt);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
               h2 wd[4];
-              dequant_word(ring[p][rt][j], qp, uc, wd);
+              dequant_word(ring[p].w[rt][j], qp, uc, wd);
               const h8 b = pack_h8(wd);
 #pragma unroll
               for (int mt = 0; mt < MT; ++mt)
@@ -482,6 +490,7 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_mfma_kernel(LinearArgs a, int 
           }
         }
         issue(p, step + P);
+        __builtin_amdgcn_sched_barrier(0);  // slot boundary (see gemv_dot_kernel)
       }
     }
   }
@@ -578,12 +587,12 @@ struct GemvPlan {
   size_t lds;
 };
 
-GemvPlan plan_gemv(const LinearArgs& a, int waves, int rt, int depth, int x_rows, size_t red_per_wave) {
+GemvPlan plan_gemv(const LinearArgs& a, int waves, int depth, int x_rows, size_t red_per_wave) {
   const int nsteps = ((a.k >> 5) + 3) >> 2;
   const int steps = max_steps(nsteps, waves);
   const size_t cap = device_max_lds();
   auto bytes = [&](int win) {
-    const GemvLds l = gemv_lds_layout(win, a.log2g, 16 * rt, x_rows);
+    const GemvLds l = gemv_lds_layout(win, x_rows);
     return (size_t)waves * (size_t)l.wave_words * 4 + (size_t)(waves - 1) * red_per_wave;
   };
   if (bytes(steps) <= cap) return GemvPlan{steps, bytes(steps)};
@@ -593,30 +602,43 @@ GemvPlan plan_gemv(const LinearArgs& a, int waves, int rt, int depth, int x_rows
   return GemvPlan{win, bytes(win)};
 }
 
+// K a multiple of 128 selects the kernels that carry the step offsets in scalar registers.
+bool full_steps(const LinearArgs& a) { return (a.k & 127) == 0; }
+
+template <int MAXM, int RT, int P, int MAXW, bool FULLK>
+int launch_dot_k(const LinearArgs& a, int waves, hipStream_t stream) {
+  const GemvPlan plan = plan_gemv(a, waves, P, a.m < MAXM ? a.m : MAXM, (size_t)MAXM * RT * 16 * sizeof(float));
+  if (plan.win == 0) return fail(TF_EINVAL, "tf_w4a16_linear: gemv_dot variant does not fit the device's LDS");
+  if (int rc = reserve_lds(gemv_dot_kernel<MAXM, RT, P, MAXW, FULLK>, plan.lds, "gemv_dot")) return rc;
+  const dim3 grid((unsigned)cdiv(a.n, 16 * RT));
+  gemv_dot_kernel<MAXM, RT, P, MAXW, FULLK><<<grid, waves * 64, plan.lds, stream>>>(a, plan.win);
+  return check_launch("tf_w4a16_linear(gemv_dot)");
+}
+
 template <int MAXM, int RT, int P, int MAXW>
 int launch_dot(const LinearArgs& a, const tf_gemm_config& cfg, float*, hipStream_t stream) {
   if (a.m > MAXM) return fail(TF_EINVAL, "tf_w4a16_linear: gemv_dot variant needs m <= block_m");
   if (int rc = check_offsets(a)) return rc;
-  const int waves = cfg.num_warps;
-  const GemvPlan plan = plan_gemv(a, waves, RT, P, a.m < MAXM ? a.m : MAXM, (size_t)MAXM * RT * 16 * sizeof(float));
-  if (plan.win == 0) return fail(TF_EINVAL, "tf_w4a16_linear: gemv_dot variant does not fit the device's LDS");
-  if (int rc = reserve_lds(gemv_dot_kernel<MAXM, RT, P, MAXW>, plan.lds, "gemv_dot")) return rc;
-  const dim3 grid((unsigned)cdiv(a.n, 16 * RT));
-  gemv_dot_kernel<MAXM, RT, P, MAXW><<<grid, waves * 64, plan.lds, stream>>>(a, plan.win);
-  return check_launch("tf_w4a16_linear(gemv_dot)");
+  return full_steps(a) ? launch_dot_k<MAXM, RT, P, MAXW, true>(a, cfg.num_warps, stream)
+                       : launch_dot_k<MAXM, RT, P, MAXW, false>(a, cfg.num_warps, stream);
+}
+
+template <int MT, int RT, int P, int MAXW, bool XLDS, bool FULLK>
+int launch_mfma_k(const LinearArgs& a, int waves, hipStream_t stream) {
+  const GemvPlan plan = plan_gemv(a, waves, P, XLDS ? (a.m < 16 * MT ? a.m : 16 * MT) : 0,
+                                  (size_t)MT * RT * 64 * 4 * sizeof(float));
+  if (plan.win == 0) return fail(TF_EINVAL, "tf_w4a16_linear: gemv_mfma variant does not fit the device's LDS");
+  if (int rc = reserve_lds(gemv_mfma_kernel<MT, RT, P, MAXW, XLDS, FULLK>, plan.lds, "gemv_mfma")) return rc;
+  const dim3 grid((unsigned)cdiv(a.n, 16 * RT), (unsigned)cdiv(a.m, 16 * MT));
+  gemv_mfma_kernel<MT, RT, P, MAXW, XLDS, FULLK><<<grid, waves * 64, plan.lds, stream>>>(a, plan.win);
+  return check_launch("tf_w4a16_linear(gemv_mfma)");
 }
 
 template <int MT, int RT, int P, int MAXW, bool XLDS>
 int launch_mfma(const LinearArgs& a, const tf_gemm_config& cfg, float*, hipStream_t stream) {
   if (int rc = check_offsets(a)) return rc;
-  const int waves = cfg.num_warps;
-  const GemvPlan plan = plan_gemv(a, waves, RT, P, XLDS ? (a.m < 16 * MT ? a.m : 16 * MT) : 0,
-                                  (size_t)MT * RT * 64 * 4 * sizeof(float));
-  if (plan.win == 0) return fail(TF_EINVAL, "tf_w4a16_linear: gemv_mfma variant does not fit the device's LDS");
-  if (int rc = reserve_lds(gemv_mfma_kernel<MT, RT, P, MAXW, XLDS>, plan.lds, "gemv_mfma")) return rc;
-  const dim3 grid((unsigned)cdiv(a.n, 16 * RT), (unsigned)cdiv(a.m, 16 * MT));
-  gemv_mfma_kernel<MT, RT, P, MAXW, XLDS><<<grid, waves * 64, plan.lds, stream>>>(a, plan.win);
-  return check_launch("tf_w4a16_linear(gemv_mfma)");
+  return full_steps(a) ? launch_mfma_k<MT, RT, P, MAXW, XLDS, true>(a, cfg.num_warps, stream)
+                       : launch_mfma_k<MT, RT, P, MAXW, XLDS, false>(a, cfg.num_warps, stream);
 }
 
 // One table row per (variant, num_warps): num_warps ranges over 1..MAXW (powers of two).
