@@ -25,9 +25,11 @@ Extra objects on the same JSON line:
   8 TB/s HBM peak. ``traffic`` is the HBM bytes per launch that rocprofv3 counted
   (FETCH_SIZE + WRITE_SIZE, each scaled by the ratio of known bytes to counted bytes of a
   plain elementwise kernel in the same run), read from the committed summary
-  ``profiles/gemv_gate_up_m1_traffic.md`` when it was measured with the config in use, else
-  null. ``--traffic-probe`` runs exactly what those counter passes measure: the tuned gate_up
-  GEMV on the rotating cold copies, then the calibration kernel (torch.neg, 256 MiB in and out).
+  ``profiles/gemv_gate_up_m1_traffic.md``, which holds one row per autotune candidate of the
+  gate_up M=1 bucket (null if the config in use has no row). ``--traffic-probe`` runs exactly
+  what those counter passes measure: every candidate in turn on the rotating cold copies, then
+  the calibration kernel (torch.neg, 256 MiB in and out); ``--traffic-summary FETCH_DIR
+  WRITE_DIR PROBE_LOG`` turns the two counter runs into that summary.
 * ``gemm_m256``: the prefill GEMM at M=256 on gate_up and down, TFLOP/s and fraction of the
   2.5 PFLOP/s fp16 dense MFMA peak.
 * ``rmsnorm_fp8``: the fused RMSNorm + e4m3fn quant (configs[1]: H=3584, eight outlier
@@ -84,24 +86,92 @@ CALIB_BYTES = 256 << 20
 
 
 def committed_traffic(cfg_dict: dict) -> float | None:  # type: ignore[type-arg]
-    """HBM bytes per launch of the dominant kernel from the committed counter summary, if that
-    summary was measured with ``cfg_dict``; the summary's lines ``config: {json}`` and
-    ``traffic_bytes_per_launch: N`` carry the two values."""
+    """HBM bytes per launch of the dominant kernel with config ``cfg_dict`` from the committed
+    counter summary; its lines ``traffic: <bytes per launch> <config json>`` carry one config
+    each."""
     if not TRAFFIC_SUMMARY.is_file():
         return None
-    cfg = traffic = None
     for line in TRAFFIC_SUMMARY.read_text().splitlines():
-        if line.startswith("config: "):
-            try:
-                cfg = json.loads(line[len("config: "):])
-            except ValueError:
-                return None
-        elif line.startswith("traffic_bytes_per_launch: "):
-            try:
-                traffic = float(line.split(":", 1)[1])
-            except ValueError:
-                return None
-    return traffic if cfg == cfg_dict else None
+        if not line.startswith("traffic: "):
+            continue
+        try:
+            value, cfg = line[len("traffic: "):].split(" ", 1)
+            if json.loads(cfg) == cfg_dict:
+                return float(value)
+        except ValueError:
+            return None
+    return None
+
+
+def traffic_summary(fetch_dir: str, write_dir: str, probe_log: str) -> int:
+    """Write ``TRAFFIC_SUMMARY`` from two ``rocprofv3 --pmc`` runs of ``--traffic-probe`` (one
+    with FETCH_SIZE, one with WRITE_SIZE) and the probe's own output line. The GEMV dispatches
+    of each run are grouped in launch order, ``launches`` per candidate; each counter is scaled
+    by known bytes / counted bytes of the calibration kernel in the same run."""
+    import csv
+    import glob
+
+    probe = None
+    for line in Path(probe_log).read_text().splitlines():
+        if line.startswith('{"traffic_probe"'):
+            probe = json.loads(line)["traffic_probe"]
+    if probe is None:
+        print(f"no traffic_probe line in {probe_log}", file=sys.stderr)
+        return 1
+
+    def counter(d: str, name: str) -> tuple[list, float]:  # type: ignore[type-arg]
+        rows = []
+        for f in glob.glob(f"{d}/**/*counter_collection.csv", recursive=True):
+            rows += [r for r in csv.DictReader(open(f)) if r["Counter_Name"] == name]
+        rows.sort(key=lambda r: int(r["Dispatch_Id"]))
+        gemv = [float(r["Counter_Value"]) * 1024 for r in rows if "gemv_" in r["Kernel_Name"]]
+        calib = [float(r["Counter_Value"]) * 1024 for r in rows if "neg_kernel" in r["Kernel_Name"]]
+        if not calib or len(gemv) != probe["launches"] * len(probe["configs"]):
+            raise ValueError(f"{d}: {len(gemv)} GEMV dispatches, {len(calib)} calibration dispatches")
+        return gemv, probe["calibration_bytes_in"] / statistics.mean(calib)
+
+    fetch, f_scale = counter(fetch_dir, "FETCH_SIZE")
+    write, w_scale = counter(write_dir, "WRITE_SIZE")
+    n_launch = probe["launches"]
+    alg = probe["algorithmic_bytes"]
+    lines = [
+        "# HBM traffic of the dominant kernel: gate_up GEMV at M=1 (37888 x 3584, g128)",
+        "",
+        "Commands (on the MI355X box; one counter per run, each run a separate process):",
+        "",
+        "```",
+        "cd /tmp && export TMPDIR=/tmp && R=<repo root>",
+        "timeout -s KILL 150 rocprofv3 --pmc FETCH_SIZE --output-format csv -d $R/gpurun_out/pmc_fetch -- \\",
+        "    python $R/bench.py --traffic-probe > $R/gpurun_out/pmc_fetch.log",
+        "timeout -s KILL 150 rocprofv3 --pmc WRITE_SIZE --output-format csv -d $R/gpurun_out/pmc_write -- \\",
+        "    python $R/bench.py --traffic-probe > $R/gpurun_out/pmc_write.log",
+        "python $R/bench.py --traffic-summary $R/gpurun_out/pmc_fetch $R/gpurun_out/pmc_write \\",
+        "    $R/gpurun_out/pmc_fetch.log",
+        "```",
+        "",
+        f"`--traffic-probe` launches every autotune candidate of the gate_up M=1 bucket {n_launch} times",
+        "over the rotating cold layer copies, then the calibration kernel `torch.neg` on a 256 MiB",
+        "fp32 tensor (256 MiB read, 256 MiB written) 4 times. Counters are KiB per dispatch;",
+        f"scale = known / counted bytes of the calibration kernel: FETCH_SIZE x {f_scale:.4f},",
+        f"WRITE_SIZE x {w_scale:.4f}. Algorithmic bytes per launch (weights N*K/2 + scales + zero",
+        f"points + x + y): {alg}. Rows: mean over the launches of each candidate.",
+        "",
+        "| config | FETCH bytes | WRITE bytes | traffic / launch | x algorithmic |",
+        "|---|---:|---:|---:|---:|",
+    ]
+    machine = []
+    for i, cfg in enumerate(probe["configs"]):
+        fb = statistics.mean(fetch[i * n_launch:(i + 1) * n_launch]) * f_scale
+        wb = statistics.mean(write[i * n_launch:(i + 1) * n_launch]) * w_scale
+        t = fb + wb
+        name = (f"{cfg['kernel']} bm{cfg['block_m']} bn{cfg['block_n']} bk{cfg['block_k']} "
+                f"w{cfg['num_warps']} st{cfg['num_stages']}")
+        lines.append(f"| {name} | {fb:.0f} | {wb:.0f} | {t:.0f} | {t / alg:.3f} |")
+        machine.append(f"traffic: {t:.0f} {json.dumps(cfg)}")
+    lines += ["", "Machine-readable (bench.py reads the row of the config in use):", "", "```", *machine, "```", ""]
+    TRAFFIC_SUMMARY.write_text("\n".join(lines))
+    print(f"wrote {TRAFFIC_SUMMARY} ({len(probe['configs'])} configs)")
+    return 0
 
 
 def bytes_moved(m: int, n: int, k: int, group: int = GROUP) -> int:
@@ -335,7 +405,11 @@ def main() -> int:
     ap.add_argument("--no-stack", action="store_true", help="skip the stack (configs[4])")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="eager gate_up GEMV launches + a calibration kernel, for rocprofv3 --pmc")
+    ap.add_argument("--traffic-summary", nargs=3, metavar=("FETCH_DIR", "WRITE_DIR", "PROBE_LOG"),
+                    help="write the committed traffic summary from two --traffic-probe counter runs")
     args = ap.parse_args()
+    if args.traffic_summary:
+        return traffic_summary(*args.traffic_summary)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(
             "bench.py measures one GPU: this build's hot path is single-GPU (no collectives); "
@@ -372,7 +446,7 @@ def main() -> int:
     torch.cuda.synchronize()
     log(f"setup: {copies} layer copies ({copies * step_bytes / 1e9:.2f} GB) in {time.perf_counter() - t0:.1f}s")
 
-    if not args.no_tune:
+    if not args.no_tune and not args.traffic_probe:  # the probe runs every candidate
         t0 = time.perf_counter()
         for _, n, k in SHAPES:
             buckets = (1, 256) if n in (37888,) or k == 18944 else (1,)
@@ -386,18 +460,24 @@ def main() -> int:
     xs = [torch.randn((1, k), generator=gen, device=dev).to(torch.float16) for _, _, k in SHAPES]
 
     if args.traffic_probe:
+        from tokenforge_amd.kernels.config import candidate_configs
+
         qw_s_z = [layers[c][2] for c in range(copies)]
-        for c in range(2 * copies):  # cold: each launch reads a copy the previous ones evicted
-            qw, sc, qz = qw_s_z[c % copies]
-            w4a16_gemm(xs[2], qw, sc, qz, GROUP, cfg1[2])
+        cands = candidate_configs(1, GROUP)
+        for cfg in cands:
+            for c in range(copies):  # cold: each launch reads a copy the previous ones evicted
+                qw, sc, qz = qw_s_z[c % copies]
+                w4a16_gemm(xs[2], qw, sc, qz, GROUP, cfg)
         src = torch.randn(CALIB_BYTES // 4, device=dev)
         dst = torch.empty_like(src)
         for _ in range(4):
             torch.neg(src, out=dst)
         torch.cuda.synchronize()
-        print(json.dumps({"traffic_probe": {"kernel": "gate_up GEMV M=1", "launches": 2 * copies,
-                                            "config": cfg1[2].to_dict(), "calibration": "torch.neg",
-                                            "calibration_bytes_in": CALIB_BYTES,
+        _, n_g, k_g = SHAPES[2]
+        print(json.dumps({"traffic_probe": {"kernel": "gate_up GEMV M=1", "launches": copies,
+                                            "configs": [c.to_dict() for c in cands],
+                                            "algorithmic_bytes": bytes_moved(1, n_g, k_g),
+                                            "calibration": "torch.neg", "calibration_bytes_in": CALIB_BYTES,
                                             "calibration_bytes_out": CALIB_BYTES}}), flush=True)
         return 0
 

@@ -1,0 +1,84 @@
+"""bench.py's HBM-traffic bookkeeping: ``--traffic-summary`` turns two counter runs of
+``--traffic-probe`` into the committed summary, and ``committed_traffic`` finds the row of the
+config in use. Synthetic counter files with known values; no GPU."""
+
+from __future__ import annotations
+
+import csv
+import json
+from pathlib import Path
+
+import pytest
+
+import bench
+
+CFGS = [
+    {"kernel": "gemv_dot", "block_m": 1, "block_n": 16, "block_k": 128, "split_k": 1, "num_warps": 4, "num_stages": 2},
+    {"kernel": "gemv_mfma", "block_m": 16, "block_n": 16, "block_k": 128, "split_k": 1, "num_warps": 4, "num_stages": 4},
+]
+LAUNCHES = 3
+CALIB = 256 << 20
+
+
+def _write_run(d: Path, counter: str, gemv_kib: list[float], calib_kib: float) -> None:
+    d.mkdir(parents=True)
+    rows = []
+    did = 1
+    for v in gemv_kib:
+        rows.append({"Dispatch_Id": did, "Kernel_Name": "void tf::gemv_dot_kernel<1, 1, 2, 16, true>(...)",
+                     "Counter_Name": counter, "Counter_Value": v})
+        did += 1
+    for _ in range(4):
+        rows.append({"Dispatch_Id": did, "Kernel_Name": "void at::native::neg_kernel(...)",
+                     "Counter_Name": counter, "Counter_Value": calib_kib})
+        did += 1
+    rows.reverse()  # the summary must order by dispatch id, not by file order
+    with open(d / "pmc_counter_collection.csv", "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=list(rows[0]))
+        w.writeheader()
+        w.writerows(rows)
+
+
+def test_summary_rows_and_lookup(tmp_path: Path, monkeypatch: pytest.MonkeyPatch) -> None:
+    summary = tmp_path / "traffic.md"
+    monkeypatch.setattr(bench, "TRAFFIC_SUMMARY", summary)
+    # FETCH_SIZE counts half the bytes (scale 2), WRITE_SIZE all of them (scale 1).
+    fetch = [1000.0] * LAUNCHES + [2000.0] * LAUNCHES
+    write = [10.0] * LAUNCHES + [30.0] * LAUNCHES
+    _write_run(tmp_path / "f", "FETCH_SIZE", fetch, CALIB / 1024 / 2)
+    _write_run(tmp_path / "w", "WRITE_SIZE", write, CALIB / 1024)
+    probe = {"traffic_probe": {"launches": LAUNCHES, "configs": CFGS, "algorithmic_bytes": 4096000,
+                               "calibration_bytes_in": CALIB, "calibration_bytes_out": CALIB}}
+    log = tmp_path / "probe.log"
+    log.write_text("noise\n" + json.dumps(probe) + "\n")
+    assert bench.traffic_summary(str(tmp_path / "f"), str(tmp_path / "w"), str(log)) == 0
+    text = summary.read_text()
+    assert "| gemv_dot bm1 bn16 bk128 w4 st2 |" in text
+    assert bench.committed_traffic(CFGS[0]) == pytest.approx(1000 * 1024 * 2 + 10 * 1024)
+    assert bench.committed_traffic(CFGS[1]) == pytest.approx(2000 * 1024 * 2 + 30 * 1024)
+    other = dict(CFGS[0], num_warps=8)
+    assert bench.committed_traffic(other) is None
+
+
+def test_summary_rejects_a_dispatch_count_mismatch(tmp_path: Path, monkeypatch: pytest.MonkeyPatch) -> None:
+    monkeypatch.setattr(bench, "TRAFFIC_SUMMARY", tmp_path / "traffic.md")
+    _write_run(tmp_path / "f", "FETCH_SIZE", [1.0] * (LAUNCHES * 2 - 1), 1.0)
+    _write_run(tmp_path / "w", "WRITE_SIZE", [1.0] * (LAUNCHES * 2), 1.0)
+    log = tmp_path / "probe.log"
+    log.write_text(json.dumps({"traffic_probe": {"launches": LAUNCHES, "configs": CFGS, "algorithmic_bytes": 1,
+                                                 "calibration_bytes_in": CALIB}}) + "\n")
+    with pytest.raises(ValueError, match="GEMV dispatches"):
+        bench.traffic_summary(str(tmp_path / "f"), str(tmp_path / "w"), str(log))
+    assert not (tmp_path / "traffic.md").exists()
+
+
+def test_committed_summary_parses() -> None:
+    """The committed summary (if any) is well formed: every machine line names a config."""
+    if not bench.TRAFFIC_SUMMARY.is_file():
+        pytest.skip("no committed traffic summary")
+    lines = [ln for ln in bench.TRAFFIC_SUMMARY.read_text().splitlines() if ln.startswith("traffic: ")]
+    assert lines
+    for ln in lines:
+        value, cfg = ln[len("traffic: "):].split(" ", 1)
+        assert float(value) > 0
+        assert bench.committed_traffic(json.loads(cfg)) == float(value)
