@@ -43,7 +43,8 @@ __device__ __forceinline__ void k_range(int wave, int waves, int nsteps, int* s0
 // Buffer resources and per-launch constants shared by both kernels.
 struct Streams {
   __amdgpu_buffer_rsrc_t qw, sc, qz, x, x8;
-  __amdgpu_buffer_rsrc_t none;  // zero records: every load through it returns zeros, no traffic
+  const void *qw_ptr, *sc_ptr, *qz_ptr;
+  uint32_t qw_bytes, sc_bytes, qz_bytes;
   uint32_t row_bytes;  // K / 2
   int nchunks;         // K / 32
   int nsteps;          // ceil(K / 128)
@@ -63,7 +64,12 @@ __device__ __forceinline__ Streams make_streams(const LinearArgs& a) {
   s.qz = make_rsrc(a.qz, (uint32_t)(s.groups * (a.n >> 3) * 4));
   s.x = make_rsrc(a.x, (uint32_t)(((int64_t)(a.m - 1) * a.ldx + a.k) * 2));
   s.x8 = make_rsrc(a.x8, (uint32_t)((int64_t)(a.m - 1) * a.ldx8 + a.k));
-  s.none = make_rsrc(a.qw, 0u);
+  s.qw_ptr = a.qw;
+  s.sc_ptr = a.scales;
+  s.qz_ptr = a.qz;
+  s.qw_bytes = (uint32_t)a.n * s.row_bytes;
+  s.sc_bytes = (uint32_t)(s.groups * a.n * 2);
+  s.qz_bytes = (uint32_t)(s.groups * (a.n >> 3) * 4);
   s.nchunks = a.k >> 5;
   s.nsteps = (s.nchunks + 3) >> 2;
   s.log2g = a.log2g;
@@ -110,15 +116,19 @@ __device__ __forceinline__ void load_batch(StageBatch<U>& b, const Window& w, co
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const int e = base + u * 64 + lane;
-    // e = r * chunks + q; the float quotient is off by at most one for e < 2^24.
-    int r = (int)((float)e * w.inv_chunks);
-    int q = e - r * w.chunks;
-    if (q < 0) {
-      r -= 1;
-      q += w.chunks;
-    } else if (q >= w.chunks) {
-      r += 1;
-      q -= w.chunks;
+    // e = r * chunks + q; the float quotient is off by at most one for e < 2^24. One row (the
+    // decode case) needs no division.
+    int r = 0, q = e;
+    if (w.rows > 1) {
+      r = (int)((float)e * w.inv_chunks);
+      q = e - r * w.chunks;
+      if (q < 0) {
+        r -= 1;
+        q += w.chunks;
+      } else if (q >= w.chunks) {
+        r += 1;
+        q -= w.chunks;
+      }
     }
     b.xr[u] = r;
     b.xq[u] = q;
@@ -205,10 +215,11 @@ struct LaneStream {
   // instead of draining the ring.
   __device__ __forceinline__ void issue(Slot<RT>& sl, const Streams& st, int step) const {
     if (FULLK) {
+      // Steps past the wave's range read through resources with zero records: zeros, no traffic.
       const bool in = step < wave_end;
-      const __amdgpu_buffer_rsrc_t rw = in ? st.qw : st.none;
-      const __amdgpu_buffer_rsrc_t rs = in ? st.sc : st.none;
-      const __amdgpu_buffer_rsrc_t rz = in ? st.qz : st.none;
+      const __amdgpu_buffer_rsrc_t rw = make_rsrc(st.qw_ptr, in ? st.qw_bytes : 0u);
+      const __amdgpu_buffer_rsrc_t rs = make_rsrc(st.sc_ptr, in ? st.sc_bytes : 0u);
+      const __amdgpu_buffer_rsrc_t rz = make_rsrc(st.qz_ptr, in ? st.qz_bytes : 0u);
       const int st_ = in ? step : 0;
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
