@@ -74,6 +74,10 @@ PATH_CONFIGS = [
     GemmConfig("gemv_mfma", 16, 16, 64, 1, 2, 2),
     GemmConfig("gemv_dot", 2, 32, 128, 1, 2, 2),
     GemmConfig("gemv_dot", 4, 16, 128, 1, 8, 2),
+    # block_k 256: waves over row tiles (200 rows: the last workgroup's last waves are empty)
+    GemmConfig("gemv_dot", 1, 16, 256, 1, 4, 4),
+    GemmConfig("gemv_dot", 1, 32, 256, 1, 2, 4),
+    GemmConfig("gemv_dot", 4, 16, 256, 1, 8, 4),
     GemmConfig("gemv_mfma", 16, 16, 128, 1, 1, 2),
     GemmConfig("gemv_mfma", 16, 16, 128, 1, 16, 4),
     GemmConfig("gemv_mfma", 16, 64, 128, 1, 8, 2),
@@ -148,6 +152,7 @@ def test_every_code_path(cfg: GemmConfig, with_bias: bool, device: torch.device)
         GemmConfig("gemv_mfma", 16, 32, 128, 1, 1, 4),
         GemmConfig("gemv_mfma", 16, 64, 64, 1, 1, 2),
         GemmConfig("gemv_dot", 1, 64, 128, 1, 1, 2),
+        GemmConfig("gemv_dot", 1, 16, 256, 1, 2, 8),  # one shared x, partial last step
     ],
     ids=_cfg_id,
 )
@@ -314,6 +319,17 @@ def test_rejects_bad_weight_layouts(device: torch.device) -> None:
         w4a16_gemm(x, w.qweight_t, w.scales, w.qzeros, G, GemmConfig("gemm_mfma", 64, 64, 256, 1, 4, 2))
     with pytest.raises(ValueError, match="block_m"):
         w4a16_gemm(x.expand(3, 256).contiguous(), w.qweight_t, w.scales, w.qzeros, G, cfg)
+
+
+def test_shared_x_variant_rejects_x_larger_than_the_lds(device: torch.device) -> None:
+    """block_k 256 keeps all of x in LDS: 4 rows of K = 32768 (256 KiB) cannot run."""
+    w = cases.on_device(cases.layer_weights(16, 32768, 1), device)
+    x = cases.activations(4, 32768, 1).to(device)
+    with pytest.raises(ValueError, match="fit"):
+        w4a16_gemm(x, w.qweight_t, w.scales, w.qzeros, G, GemmConfig("gemv_dot", 4, 16, 256, 1, 8, 4))
+    # one row fits (64 KiB)
+    y = w4a16_gemm(x[:1].contiguous(), w.qweight_t, w.scales, w.qzeros, G, GemmConfig("gemv_dot", 4, 16, 256, 1, 8, 4))
+    _assert_close(y, cases.activations(4, 32768, 1)[:1], cases.layer_weights(16, 32768, 1))
 
 
 def test_cpu_tensors_raise_instead_of_falling_back() -> None:

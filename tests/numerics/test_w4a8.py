@@ -33,6 +33,7 @@ CONFIGS = [
     # decode while staging x
     GemmConfig("gemv_dot", 1, 16, 128, 1, 4, 2),
     GemmConfig("gemv_dot", 4, 16, 128, 1, 8, 2),
+    GemmConfig("gemv_dot", 1, 16, 256, 1, 4, 4),
     GemmConfig("gemv_mfma", 16, 16, 128, 1, 16, 4),
     GemmConfig("gemv_mfma", 32, 32, 128, 1, 4, 2),
     # decode into the workspace first
@@ -97,7 +98,12 @@ def test_rmsnorm_fp8_output_against_oracle(cfg: GemmConfig, device: torch.device
         assert normwise(y64, ref) <= NORMWISE_MAX
 
 
-@pytest.mark.parametrize("cfg", [CONFIGS[2], CONFIGS[4], CONFIGS[7]], ids=_id)
+@pytest.mark.parametrize(
+    "cfg",
+    [GemmConfig("gemv_mfma", 16, 16, 128, 1, 16, 4), GemmConfig("gemv_mfma", 16, 32, 64, 1, 4, 2),
+     GemmConfig("gemm_mfma", 256, 192, 64, 2, 8, 3)],
+    ids=_id,
+)
 def test_epilogues_and_nan_rows(cfg: GemmConfig, device: torch.device) -> None:
     n, k, m = 400, 512, 5
     w = cases.on_device(cases.layer_weights(n, k, 9), device)

@@ -20,7 +20,11 @@
 // staging the dequantization operands in LDS per wave (gate_up and down at M = 1 ~12% faster).
 //
 //  * gemv_dot  (TF_KERNEL_GEMV_DOT): lane = (row c = lane/4, chunk g = lane%4). Each lane
-//    accumulates its products with v_dot2_f32_f16; quads are reduced with DPP.
+//    accumulates its products with v_dot2_f32_f16; quads are reduced with DPP. SPLITN variants
+//    (block_k 256) turn the split around: the waves of a workgroup take different row tiles,
+//    each over the whole K, and share one copy of x staged cooperatively (one barrier); no
+//    cross-wave reduction. For shapes with many row tiles this removes the per-wave prologue
+//    and reduction that short K slices pay for every few steps.
 //  * gemv_mfma (TF_KERNEL_GEMV_MFMA): lane = (row c = lane%16, chunk g = lane/16), exactly the
 //    B-operand layout of v_mfma_f32_16x16x32_f16 (8 consecutive K values per lane = one
 //    packed word). The dequantized word goes straight into the MFMA and x rows are the A
@@ -269,7 +273,7 @@ __host__ __device__ __forceinline__ GemvLds gemv_lds_layout(int win, int x_rows)
 
 constexpr int kStageU = 2;  // x staging chunks per lane and batch
 
-template <int MAXM, int RT, int P, int MAXW, bool FULLK>
+template <int MAXM, int RT, int P, int MAXW, bool FULLK, bool SPLITN>
 __global__ __launch_bounds__(MAXW * 64) void gemv_dot_kernel(LinearArgs a, int win) {
   extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
   const int lane = threadIdx.x & 63;
@@ -278,13 +282,14 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_dot_kernel(LinearArgs a, int w
   const int g = lane & 3;
   const int c = lane >> 2;
   constexpr int cols = 16 * RT;
-  const int n_base = xcd_tile(blockIdx.x, gridDim.x) * cols;
+  const int n_base = SPLITN ? (xcd_tile(blockIdx.x, gridDim.x) * waves + wave) * cols
+                            : xcd_tile(blockIdx.x, gridDim.x) * cols;
   const Streams st = make_streams(a);
-  int s0, s1;
-  k_range(wave, waves, st.nsteps, &s0, &s1);
+  int s0 = 0, s1 = st.nsteps;
+  if (!SPLITN) k_range(wave, waves, st.nsteps, &s0, &s1);
   const int xrows = a.m < MAXM ? a.m : MAXM;
   const GemvLds L = gemv_lds_layout(win, xrows);
-  _Float16* xs = reinterpret_cast<_Float16*>(lds + wave * L.wave_words);
+  _Float16* xs = reinterpret_cast<_Float16*>(lds + (SPLITN ? 0 : wave * L.wave_words));
   const UnpackConsts uc = unpack_consts();
   const LaneStream<RT, FULLK> ls_w(a, st, n_base, c, g, s1);
   const _Float16* xl = xs + g * 32;
@@ -297,9 +302,12 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_dot_kernel(LinearArgs a, int w
 
   // The first staging batch goes out ahead of the weight ring: every wave of the grid issues
   // its ring at once, and the x chunks that gate the first step must not queue behind it.
+  // SPLITN: the waves stage the workgroup's one copy together, batch b by wave b % waves.
   Window win0 = make_window(s0, min(s1, s0 + win), 0, xrows, L.xstride);
+  const int first_base = SPLITN ? wave * 64 * kStageU : 0;
+  const int batch_stride = SPLITN ? waves * 64 * kStageU : 64 * kStageU;
   StageBatch<kStageU> first;
-  load_batch<kStageU>(first, win0, a, st, 0, lane);
+  load_batch<kStageU>(first, win0, a, st, first_base, lane);
   __builtin_amdgcn_sched_barrier(0);
   Slot<RT> ring[P];
 #pragma unroll
@@ -307,8 +315,13 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_dot_kernel(LinearArgs a, int w
     ls_w.issue(ring[p], st, s0 + p);
     __builtin_amdgcn_sched_barrier(0);  // keep slot order: slot 0 must be the oldest ring load
   }
-  store_batch<kStageU>(xs, first, win0, a, 0, lane);
-  stage_rest<kStageU>(xs, win0, a, st, 64 * kStageU, lane);
+  store_batch<kStageU>(xs, first, win0, a, first_base, lane);
+  for (int base = first_base + batch_stride; base < win0.xentries; base += batch_stride) {
+    StageBatch<kStageU> b;
+    load_batch<kStageU>(b, win0, a, st, base, lane);
+    store_batch<kStageU>(xs, b, win0, a, base, lane);
+  }
+  if (SPLITN) __syncthreads();  // x is whole before any wave reads it (one window: win == s1)
 
   for (int w0 = s0; w0 < s1; w0 += win) {
     const int w1 = min(s1, w0 + win);
@@ -355,7 +368,7 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_dot_kernel(LinearArgs a, int w
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) acc[m][rt] = quad_sum(acc[m][rt]);
 
-  if (waves > 1) {
+  if (!SPLITN && waves > 1) {
     float* red = reinterpret_cast<float*>(lds + waves * L.wave_words);  // [(waves - 1)][MAXM][RT][16]
     if (wave > 0 && g == 0) {
 #pragma unroll
@@ -374,7 +387,7 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_dot_kernel(LinearArgs a, int w
   }
   // Lane 4 c (g == 0) holds row c of each row tile. Under SiLU*mul rows c and c ^ 8 are the
   // gate and up columns of one output (phys_col): lanes 4c and 4c ^ 32 swap their values.
-  if (wave == 0) {
+  if (SPLITN || wave == 0) {
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
       const int l = rt * 16 + c;
@@ -616,22 +629,32 @@ GemvPlan plan_gemv(const LinearArgs& a, int waves, int depth, int x_rows, size_t
 // K a multiple of 128 selects the kernels that carry the step offsets in scalar registers.
 bool full_steps(const LinearArgs& a) { return (a.k & 127) == 0; }
 
-template <int MAXM, int RT, int P, int MAXW, bool FULLK>
+template <int MAXM, int RT, int P, int MAXW, bool FULLK, bool SPLITN>
 int launch_dot_k(const LinearArgs& a, int waves, hipStream_t stream) {
-  const GemvPlan plan = plan_gemv(a, waves, P, a.m < MAXM ? a.m : MAXM, (size_t)MAXM * RT * 16 * sizeof(float));
-  if (plan.win == 0) return fail(TF_EINVAL, "tf_w4a16_linear: gemv_dot variant does not fit the device's LDS");
-  if (int rc = reserve_lds(gemv_dot_kernel<MAXM, RT, P, MAXW, FULLK>, plan.lds, "gemv_dot")) return rc;
-  const dim3 grid((unsigned)cdiv(a.n, 16 * RT));
-  gemv_dot_kernel<MAXM, RT, P, MAXW, FULLK><<<grid, waves * 64, plan.lds, stream>>>(a, plan.win);
+  const int xrows = a.m < MAXM ? a.m : MAXM;
+  GemvPlan plan;
+  if (SPLITN) {  // one shared copy of all of x, no reduction buffer
+    const int nsteps = ((a.k >> 5) + 3) >> 2;
+    plan = GemvPlan{nsteps, (size_t)gemv_lds_layout(nsteps, xrows).wave_words * 4};
+    if (plan.lds > device_max_lds())
+      return fail(TF_EINVAL, "tf_w4a16_linear: gemv_dot variant (block_k 256) needs x to fit the device's LDS");
+  } else {
+    plan = plan_gemv(a, waves, P, xrows, (size_t)MAXM * RT * 16 * sizeof(float));
+    if (plan.win == 0) return fail(TF_EINVAL, "tf_w4a16_linear: gemv_dot variant does not fit the device's LDS");
+  }
+  if (int rc = reserve_lds(gemv_dot_kernel<MAXM, RT, P, MAXW, FULLK, SPLITN>, plan.lds, "gemv_dot")) return rc;
+  const int tiles = (int)cdiv(a.n, 16 * RT);
+  const dim3 grid((unsigned)(SPLITN ? cdiv(tiles, waves) : tiles));
+  gemv_dot_kernel<MAXM, RT, P, MAXW, FULLK, SPLITN><<<grid, waves * 64, plan.lds, stream>>>(a, plan.win);
   return check_launch("tf_w4a16_linear(gemv_dot)");
 }
 
-template <int MAXM, int RT, int P, int MAXW>
+template <int MAXM, int RT, int P, int MAXW, bool SPLITN>
 int launch_dot(const LinearArgs& a, const tf_gemm_config& cfg, float*, hipStream_t stream) {
   if (a.m > MAXM) return fail(TF_EINVAL, "tf_w4a16_linear: gemv_dot variant needs m <= block_m");
   if (int rc = check_offsets(a)) return rc;
-  return full_steps(a) ? launch_dot_k<MAXM, RT, P, MAXW, true>(a, cfg.num_warps, stream)
-                       : launch_dot_k<MAXM, RT, P, MAXW, false>(a, cfg.num_warps, stream);
+  return full_steps(a) ? launch_dot_k<MAXM, RT, P, MAXW, true, SPLITN>(a, cfg.num_warps, stream)
+                       : launch_dot_k<MAXM, RT, P, MAXW, false, SPLITN>(a, cfg.num_warps, stream);
 }
 
 template <int MT, int RT, int P, int MAXW, bool XLDS, bool FULLK>
@@ -659,9 +682,13 @@ int launch_mfma(const LinearArgs& a, const tf_gemm_config& cfg, float*, hipStrea
 #define TF_W8(K, BM, BN, BK, ST, FN) TF_W4(K, BM, BN, BK, ST, FN), {{K, BM, BN, BK, 1, 8, ST}, FN, no_workspace}
 #define TF_W16(K, BM, BN, BK, ST, FN) TF_W8(K, BM, BN, BK, ST, FN), {{K, BM, BN, BK, 1, 16, ST}, FN, no_workspace}
 
-// block_k = 128 marks x staged in LDS, 64 marks x streamed from global with the weights.
+// block_k = 128 marks x staged in LDS (per wave, K split across waves), 64 marks x streamed
+// from global with the weights, 256 (gemv_dot) marks waves over row tiles with one shared x
+// (block_n is then the rows of one wave; a workgroup covers num_warps times as many).
 #define TF_DOT(BM, RT, P, MAXW) \
-  TF_W##MAXW(TF_KERNEL_GEMV_DOT, BM, 16 * RT, 128, P, (launch_dot<BM, RT, P, MAXW>))
+  TF_W##MAXW(TF_KERNEL_GEMV_DOT, BM, 16 * RT, 128, P, (launch_dot<BM, RT, P, MAXW, false>))
+#define TF_DOT_N(BM, RT, P, MAXW) \
+  TF_W##MAXW(TF_KERNEL_GEMV_DOT, BM, 16 * RT, 256, P, (launch_dot<BM, RT, P, MAXW, true>))
 #define TF_MFMA(MT, RT, P, MAXW) \
   TF_W##MAXW(TF_KERNEL_GEMV_MFMA, 16 * MT, 16 * RT, 128, P, (launch_mfma<MT, RT, P, MAXW, true>))
 #define TF_MFMA_GX(MT, RT, P, MAXW) \
@@ -671,6 +698,7 @@ const Variant kGemvVariants[] = {
     TF_DOT(1, 1, 2, 16), TF_DOT(1, 1, 4, 16), TF_DOT(1, 1, 8, 16), TF_DOT(1, 2, 2, 16),
     TF_DOT(1, 2, 4, 8),  TF_DOT(1, 4, 2, 8),  TF_DOT(2, 1, 2, 16), TF_DOT(2, 2, 2, 8),
     TF_DOT(4, 1, 2, 8),
+    TF_DOT_N(1, 1, 4, 8), TF_DOT_N(1, 1, 8, 8), TF_DOT_N(1, 2, 4, 8), TF_DOT_N(2, 1, 4, 8), TF_DOT_N(4, 1, 4, 8),
     TF_MFMA(1, 1, 2, 16), TF_MFMA(1, 1, 4, 16), TF_MFMA(1, 1, 8, 16), TF_MFMA(1, 2, 2, 16),
     TF_MFMA(1, 2, 4, 16), TF_MFMA(1, 4, 2, 8),  TF_MFMA(2, 1, 2, 16), TF_MFMA(2, 2, 2, 8),
     TF_MFMA_GX(1, 1, 2, 16), TF_MFMA_GX(1, 2, 2, 16), TF_MFMA_GX(1, 4, 2, 8), TF_MFMA_GX(2, 1, 2, 16),

@@ -16,7 +16,10 @@ Field meaning per kernel family:
 kernel     block_m / block_n / block_k  split_k / num_warps / num_stages
 ========== =========================== ================================================
 gemv_dot   max M (1,2,4) / rows per     1 / waves per workgroup, each a K slice reduced
-           workgroup (16*RT) / 128      on chip / 128-wide K steps in flight per wave
+           workgroup (16*RT) / 128      on chip / 128-wide K steps in flight per wave.
+           or 256                       block_k 256: the waves take different row tiles
+                                        (block_n rows each) over the whole K and share
+                                        one staged x
 gemv_mfma  M per tile (16,32) / rows    same as gemv_dot; block_k 128 stages x in LDS,
            per workgroup / 128 or 64    64 streams x from global memory
 gemm_mfma  LDS tile M / tile N / tile K K slices across workgroups (fp32 workspace,
@@ -47,12 +50,15 @@ _WAVES = (1, 2, 4, 8, 16)
 
 # Compiled streaming variants: (kernel, block_m, row tiles RT, block_k, ring depth P, max waves).
 # block_k = 128: x is staged in LDS once per wave; block_k = 64: x is streamed from global
-# memory with the weights (for M and K too large to stage). The wave cap keeps each variant
-# within the VGPR budget of its launch bound (no spills).
+# memory with the weights (for M and K too large to stage); block_k = 256 (gemv_dot): the
+# waves of a workgroup take different row tiles over the whole K and share one copy of x. The
+# wave cap keeps each variant within the VGPR budget of its launch bound (no spills).
 GEMV_TEMPLATES: tuple[tuple[str, int, int, int, int, int], ...] = (
     ("gemv_dot", 1, 1, 128, 2, 16), ("gemv_dot", 1, 1, 128, 4, 16), ("gemv_dot", 1, 1, 128, 8, 16),
     ("gemv_dot", 1, 2, 128, 2, 16), ("gemv_dot", 1, 2, 128, 4, 8), ("gemv_dot", 1, 4, 128, 2, 8),
     ("gemv_dot", 2, 1, 128, 2, 16), ("gemv_dot", 2, 2, 128, 2, 8), ("gemv_dot", 4, 1, 128, 2, 8),
+    ("gemv_dot", 1, 1, 256, 4, 8), ("gemv_dot", 1, 1, 256, 8, 8), ("gemv_dot", 1, 2, 256, 4, 8),
+    ("gemv_dot", 2, 1, 256, 4, 8), ("gemv_dot", 4, 1, 256, 4, 8),
     ("gemv_mfma", 16, 1, 128, 2, 16), ("gemv_mfma", 16, 1, 128, 4, 16), ("gemv_mfma", 16, 1, 128, 8, 16),
     ("gemv_mfma", 16, 2, 128, 2, 16), ("gemv_mfma", 16, 2, 128, 4, 16), ("gemv_mfma", 16, 4, 128, 2, 8),
     ("gemv_mfma", 32, 1, 128, 2, 16), ("gemv_mfma", 32, 2, 128, 2, 8),
