@@ -32,6 +32,7 @@ CONFIGS = [
     GemmConfig("gemv_dot", 4, 16, 128, 1, 8, 2),
     GemmConfig("gemv_dot", 1, 16, 256, 1, 4, 4),
     GemmConfig("gemv_dot", 2, 16, 256, 1, 8, 4),
+    GemmConfig("gemv_mfma", 16, 16, 256, 1, 4, 2),
     GemmConfig("gemv_mfma", 16, 16, 128, 1, 16, 4),
     GemmConfig("gemv_mfma", 16, 64, 128, 1, 2, 2),
     GemmConfig("gemv_mfma", 16, 32, 64, 1, 4, 2),

@@ -78,6 +78,8 @@ PATH_CONFIGS = [
     GemmConfig("gemv_dot", 1, 16, 256, 1, 4, 4),
     GemmConfig("gemv_dot", 1, 32, 256, 1, 2, 4),
     GemmConfig("gemv_dot", 4, 16, 256, 1, 8, 4),
+    GemmConfig("gemv_mfma", 16, 16, 256, 1, 4, 4),
+    GemmConfig("gemv_mfma", 16, 32, 256, 1, 2, 2),
     GemmConfig("gemv_mfma", 16, 16, 128, 1, 1, 2),
     GemmConfig("gemv_mfma", 16, 16, 128, 1, 16, 4),
     GemmConfig("gemv_mfma", 16, 64, 128, 1, 8, 2),
@@ -327,9 +329,12 @@ def test_shared_x_variant_rejects_x_larger_than_the_lds(device: torch.device) ->
     x = cases.activations(4, 32768, 1).to(device)
     with pytest.raises(ValueError, match="fit"):
         w4a16_gemm(x, w.qweight_t, w.scales, w.qzeros, G, GemmConfig("gemv_dot", 4, 16, 256, 1, 8, 4))
+    with pytest.raises(ValueError, match="fit"):
+        w4a16_gemm(x, w.qweight_t, w.scales, w.qzeros, G, GemmConfig("gemv_mfma", 16, 16, 256, 1, 4, 2))
     # one row fits (64 KiB)
-    y = w4a16_gemm(x[:1].contiguous(), w.qweight_t, w.scales, w.qzeros, G, GemmConfig("gemv_dot", 4, 16, 256, 1, 8, 4))
-    _assert_close(y, cases.activations(4, 32768, 1)[:1], cases.layer_weights(16, 32768, 1))
+    for cfg in (GemmConfig("gemv_dot", 4, 16, 256, 1, 8, 4), GemmConfig("gemv_mfma", 16, 16, 256, 1, 4, 2)):
+        y = w4a16_gemm(x[:1].contiguous(), w.qweight_t, w.scales, w.qzeros, G, cfg)
+        _assert_close(y, cases.activations(4, 32768, 1)[:1], cases.layer_weights(16, 32768, 1))
 
 
 def test_cpu_tensors_raise_instead_of_falling_back() -> None:

@@ -34,6 +34,7 @@ CONFIGS = [
     GemmConfig("gemv_dot", 1, 16, 128, 1, 4, 2),
     GemmConfig("gemv_dot", 4, 16, 128, 1, 8, 2),
     GemmConfig("gemv_dot", 1, 16, 256, 1, 4, 4),
+    GemmConfig("gemv_mfma", 16, 16, 256, 1, 8, 4),
     GemmConfig("gemv_mfma", 16, 16, 128, 1, 16, 4),
     GemmConfig("gemv_mfma", 32, 32, 128, 1, 4, 2),
     # decode into the workspace first

@@ -411,8 +411,9 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_dot_kernel(LinearArgs a, int w
 
 // ------------------------------------------------------------------------ gemv_mfma
 
-template <int MT, int RT, int P, int MAXW, bool XLDS, bool FULLK>
+template <int MT, int RT, int P, int MAXW, bool XLDS, bool FULLK, bool SPLITN>
 __global__ __launch_bounds__(MAXW * 64) void gemv_mfma_kernel(LinearArgs a, int win) {
+  static_assert(!SPLITN || XLDS, "waves over row tiles share x staged in LDS");
   extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -420,15 +421,16 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_mfma_kernel(LinearArgs a, int 
   const int c = lane & 15;
   const int g = lane >> 4;
   constexpr int cols = 16 * RT;
-  const int n_base = xcd_tile(blockIdx.x, gridDim.x) * cols;
+  const int n_base = SPLITN ? (xcd_tile(blockIdx.x, gridDim.x) * waves + wave) * cols
+                            : xcd_tile(blockIdx.x, gridDim.x) * cols;
   const int m_base = blockIdx.y * 16 * MT;
   const Streams st = make_streams(a);
-  int s0, s1;
-  k_range(wave, waves, st.nsteps, &s0, &s1);
+  int s0 = 0, s1 = st.nsteps;
+  if (!SPLITN) k_range(wave, waves, st.nsteps, &s0, &s1);
   const int xrows = min(16 * MT, a.m - m_base);  // rows staged by this workgroup
   const int xalloc = min(16 * MT, a.m);          // rows allocated per wave (same in every workgroup)
   const GemvLds L = gemv_lds_layout(win, XLDS ? xalloc : 0);
-  _Float16* xs = reinterpret_cast<_Float16*>(lds + wave * L.wave_words);
+  _Float16* xs = reinterpret_cast<_Float16*>(lds + (SPLITN ? 0 : wave * L.wave_words));
   const UnpackConsts uc = unpack_consts();
   const LaneStream<RT, FULLK> ls_w(a, st, n_base, c, g, s1);
 
@@ -469,8 +471,10 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_mfma_kernel(LinearArgs a, int 
   // The first staging batch goes out ahead of the weight ring (see gemv_dot_kernel).
   const int srows = XLDS ? xrows : 0;
   Window win0 = make_window(s0, min(s1, s0 + win), m_base, srows, L.xstride);
+  const int first_base = SPLITN ? wave * 64 * kStageU : 0;  // SPLITN: batch b by wave b % waves
+  const int batch_stride = SPLITN ? waves * 64 * kStageU : 64 * kStageU;
   StageBatch<kStageU> first;
-  if (XLDS) load_batch<kStageU>(first, win0, a, st, 0, lane);
+  if (XLDS) load_batch<kStageU>(first, win0, a, st, first_base, lane);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int p = 0; p < P; ++p) {
@@ -478,9 +482,14 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_mfma_kernel(LinearArgs a, int 
     __builtin_amdgcn_sched_barrier(0);  // keep slot order: slot 0 must be the oldest ring load
   }
   if (XLDS) {
-    store_batch<kStageU>(xs, first, win0, a, 0, lane);
-    stage_rest<kStageU>(xs, win0, a, st, 64 * kStageU, lane);
+    store_batch<kStageU>(xs, first, win0, a, first_base, lane);
+    for (int base = first_base + batch_stride; base < win0.xentries; base += batch_stride) {
+      StageBatch<kStageU> b;
+      load_batch<kStageU>(b, win0, a, st, base, lane);
+      store_batch<kStageU>(xs, b, win0, a, base, lane);
+    }
   }
+  if (SPLITN) __syncthreads();  // x is whole before any wave reads it (one window: win == s1)
 
   for (int w0 = s0; w0 < s1; w0 += win) {
     const int w1 = min(s1, w0 + win);
@@ -519,7 +528,7 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_mfma_kernel(LinearArgs a, int 
     }
   }
 
-  if (waves > 1) {
+  if (!SPLITN && waves > 1) {
     float* red = reinterpret_cast<float*>(lds + waves * L.wave_words);  // [(waves - 1)][MT][RT][64][4]
     if (wave > 0) {
 #pragma unroll
@@ -538,7 +547,7 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_mfma_kernel(LinearArgs a, int 
             acc[mt][rt] += *reinterpret_cast<const f4*>(&red[((((w - 1) * MT + mt) * RT + rt) * 64 + lane) * 4]);
     }
   }
-  if (wave == 0) {
+  if (SPLITN || wave == 0) {
     // D layout of v_mfma_f32_16x16x32_f16: lane holds rows 4*(lane/16) + r, column lane%16.
     // Under SiLU*mul lanes c and c ^ 8 hold the gate and up columns of one output.
 #pragma unroll
@@ -657,22 +666,31 @@ int launch_dot(const LinearArgs& a, const tf_gemm_config& cfg, float*, hipStream
                        : launch_dot_k<MAXM, RT, P, MAXW, false, SPLITN>(a, cfg.num_warps, stream);
 }
 
-template <int MT, int RT, int P, int MAXW, bool XLDS, bool FULLK>
+template <int MT, int RT, int P, int MAXW, bool XLDS, bool FULLK, bool SPLITN>
 int launch_mfma_k(const LinearArgs& a, int waves, hipStream_t stream) {
-  const GemvPlan plan = plan_gemv(a, waves, P, XLDS ? (a.m < 16 * MT ? a.m : 16 * MT) : 0,
-                                  (size_t)MT * RT * 64 * 4 * sizeof(float));
-  if (plan.win == 0) return fail(TF_EINVAL, "tf_w4a16_linear: gemv_mfma variant does not fit the device's LDS");
-  if (int rc = reserve_lds(gemv_mfma_kernel<MT, RT, P, MAXW, XLDS, FULLK>, plan.lds, "gemv_mfma")) return rc;
-  const dim3 grid((unsigned)cdiv(a.n, 16 * RT), (unsigned)cdiv(a.m, 16 * MT));
-  gemv_mfma_kernel<MT, RT, P, MAXW, XLDS, FULLK><<<grid, waves * 64, plan.lds, stream>>>(a, plan.win);
+  const int xrows = XLDS ? (a.m < 16 * MT ? a.m : 16 * MT) : 0;
+  GemvPlan plan;
+  if (SPLITN) {  // one shared copy of all of x, no reduction buffer
+    const int nsteps = ((a.k >> 5) + 3) >> 2;
+    plan = GemvPlan{nsteps, (size_t)gemv_lds_layout(nsteps, xrows).wave_words * 4};
+    if (plan.lds > device_max_lds())
+      return fail(TF_EINVAL, "tf_w4a16_linear: gemv_mfma variant (block_k 256) needs x to fit the device's LDS");
+  } else {
+    plan = plan_gemv(a, waves, P, xrows, (size_t)MT * RT * 64 * 4 * sizeof(float));
+    if (plan.win == 0) return fail(TF_EINVAL, "tf_w4a16_linear: gemv_mfma variant does not fit the device's LDS");
+  }
+  if (int rc = reserve_lds(gemv_mfma_kernel<MT, RT, P, MAXW, XLDS, FULLK, SPLITN>, plan.lds, "gemv_mfma")) return rc;
+  const int tiles = (int)cdiv(a.n, 16 * RT);
+  const dim3 grid((unsigned)(SPLITN ? cdiv(tiles, waves) : tiles), (unsigned)cdiv(a.m, 16 * MT));
+  gemv_mfma_kernel<MT, RT, P, MAXW, XLDS, FULLK, SPLITN><<<grid, waves * 64, plan.lds, stream>>>(a, plan.win);
   return check_launch("tf_w4a16_linear(gemv_mfma)");
 }
 
-template <int MT, int RT, int P, int MAXW, bool XLDS>
+template <int MT, int RT, int P, int MAXW, bool XLDS, bool SPLITN = false>
 int launch_mfma(const LinearArgs& a, const tf_gemm_config& cfg, float*, hipStream_t stream) {
   if (int rc = check_offsets(a)) return rc;
-  return full_steps(a) ? launch_mfma_k<MT, RT, P, MAXW, XLDS, true>(a, cfg.num_warps, stream)
-                       : launch_mfma_k<MT, RT, P, MAXW, XLDS, false>(a, cfg.num_warps, stream);
+  return full_steps(a) ? launch_mfma_k<MT, RT, P, MAXW, XLDS, true, SPLITN>(a, cfg.num_warps, stream)
+                       : launch_mfma_k<MT, RT, P, MAXW, XLDS, false, SPLITN>(a, cfg.num_warps, stream);
 }
 
 // One table row per (variant, num_warps): num_warps ranges over 1..MAXW (powers of two).
@@ -683,8 +701,8 @@ int launch_mfma(const LinearArgs& a, const tf_gemm_config& cfg, float*, hipStrea
 #define TF_W16(K, BM, BN, BK, ST, FN) TF_W8(K, BM, BN, BK, ST, FN), {{K, BM, BN, BK, 1, 16, ST}, FN, no_workspace}
 
 // block_k = 128 marks x staged in LDS (per wave, K split across waves), 64 marks x streamed
-// from global with the weights, 256 (gemv_dot) marks waves over row tiles with one shared x
-// (block_n is then the rows of one wave; a workgroup covers num_warps times as many).
+// from global with the weights, 256 marks waves over row tiles with one shared x (block_n is
+// then the rows of one wave; a workgroup covers num_warps times as many).
 #define TF_DOT(BM, RT, P, MAXW) \
   TF_W##MAXW(TF_KERNEL_GEMV_DOT, BM, 16 * RT, 128, P, (launch_dot<BM, RT, P, MAXW, false>))
 #define TF_DOT_N(BM, RT, P, MAXW) \
@@ -693,6 +711,8 @@ int launch_mfma(const LinearArgs& a, const tf_gemm_config& cfg, float*, hipStrea
   TF_W##MAXW(TF_KERNEL_GEMV_MFMA, 16 * MT, 16 * RT, 128, P, (launch_mfma<MT, RT, P, MAXW, true>))
 #define TF_MFMA_GX(MT, RT, P, MAXW) \
   TF_W##MAXW(TF_KERNEL_GEMV_MFMA, 16 * MT, 16 * RT, 64, P, (launch_mfma<MT, RT, P, MAXW, false>))
+#define TF_MFMA_N(MT, RT, P, MAXW) \
+  TF_W##MAXW(TF_KERNEL_GEMV_MFMA, 16 * MT, 16 * RT, 256, P, (launch_mfma<MT, RT, P, MAXW, true, true>))
 
 const Variant kGemvVariants[] = {
     TF_DOT(1, 1, 2, 16), TF_DOT(1, 1, 4, 16), TF_DOT(1, 1, 8, 16), TF_DOT(1, 2, 2, 16),
@@ -703,6 +723,7 @@ const Variant kGemvVariants[] = {
     TF_MFMA(1, 2, 4, 16), TF_MFMA(1, 4, 2, 8),  TF_MFMA(2, 1, 2, 16), TF_MFMA(2, 2, 2, 8),
     TF_MFMA_GX(1, 1, 2, 16), TF_MFMA_GX(1, 2, 2, 16), TF_MFMA_GX(1, 4, 2, 8), TF_MFMA_GX(2, 1, 2, 16),
     TF_MFMA_GX(2, 2, 2, 8),
+    TF_MFMA_N(1, 1, 2, 8), TF_MFMA_N(1, 1, 4, 8), TF_MFMA_N(1, 2, 2, 8),
 };
 
 }  // namespace

@@ -62,9 +62,9 @@ int check_config(const tf_gemm_config& cfg, int32_t group_size) {
 }
 
 // Configs whose kernels read e4m3 x themselves (they stage x in LDS): the dot GEMV and the
-// MFMA GEMV with block_k 128. Every other config gets x converted to fp16 first.
+// MFMA GEMV with block_k 128 or 256. Every other config gets x converted to fp16 first.
 bool fuses_x8(const tf_gemm_config& cfg) {
-  return cfg.kernel == TF_KERNEL_GEMV_DOT || (cfg.kernel == TF_KERNEL_GEMV_MFMA && cfg.block_k == 128);
+  return cfg.kernel == TF_KERNEL_GEMV_DOT || (cfg.kernel == TF_KERNEL_GEMV_MFMA && cfg.block_k != 64);
 }
 
 constexpr int64_t kWsAlign = 256;

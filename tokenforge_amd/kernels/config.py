@@ -21,7 +21,8 @@ gemv_dot   max M (1,2,4) / rows per     1 / waves per workgroup, each a K slice 
                                         (block_n rows each) over the whole K and share
                                         one staged x
 gemv_mfma  M per tile (16,32) / rows    same as gemv_dot; block_k 128 stages x in LDS,
-           per workgroup / 128 or 64    64 streams x from global memory
+           per workgroup / 128, 64 or   64 streams x from global memory, 256 as for
+           256                          gemv_dot
 gemm_mfma  LDS tile M / tile N / tile K K slices across workgroups (fp32 workspace,
                                         fixed-order reduce) / 4 or 8 waves / 2: two LDS
                                         buffers, 3 and 4: pipelined with 2 and 3 x stages
@@ -50,9 +51,9 @@ _WAVES = (1, 2, 4, 8, 16)
 
 # Compiled streaming variants: (kernel, block_m, row tiles RT, block_k, ring depth P, max waves).
 # block_k = 128: x is staged in LDS once per wave; block_k = 64: x is streamed from global
-# memory with the weights (for M and K too large to stage); block_k = 256 (gemv_dot): the
-# waves of a workgroup take different row tiles over the whole K and share one copy of x. The
-# wave cap keeps each variant within the VGPR budget of its launch bound (no spills).
+# memory with the weights (for M and K too large to stage); block_k = 256: the waves of a
+# workgroup take different row tiles over the whole K and share one copy of x. The wave cap
+# keeps each variant within the VGPR budget of its launch bound (no spills).
 GEMV_TEMPLATES: tuple[tuple[str, int, int, int, int, int], ...] = (
     ("gemv_dot", 1, 1, 128, 2, 16), ("gemv_dot", 1, 1, 128, 4, 16), ("gemv_dot", 1, 1, 128, 8, 16),
     ("gemv_dot", 1, 2, 128, 2, 16), ("gemv_dot", 1, 2, 128, 4, 8), ("gemv_dot", 1, 4, 128, 2, 8),
@@ -64,6 +65,7 @@ GEMV_TEMPLATES: tuple[tuple[str, int, int, int, int, int], ...] = (
     ("gemv_mfma", 32, 1, 128, 2, 16), ("gemv_mfma", 32, 2, 128, 2, 8),
     ("gemv_mfma", 16, 1, 64, 2, 16), ("gemv_mfma", 16, 2, 64, 2, 16), ("gemv_mfma", 16, 4, 64, 2, 8),
     ("gemv_mfma", 32, 1, 64, 2, 16), ("gemv_mfma", 32, 2, 64, 2, 8),
+    ("gemv_mfma", 16, 1, 256, 2, 8), ("gemv_mfma", 16, 1, 256, 4, 8), ("gemv_mfma", 16, 2, 256, 2, 8),
 )
 
 
