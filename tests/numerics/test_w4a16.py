@@ -222,6 +222,36 @@ def test_staged_x_waits_at_full_size(m: int, cfg: GemmConfig, device: torch.devi
     assert rel <= 2e-3, f"max error {rel:.3e} of max |y|"
 
 
+@pytest.mark.parametrize(
+    ("layer", "n", "k"),
+    [("qkv", 4608, 3584), ("o", 3584, 3584), ("gate_up", 37888, 3584), ("down", 3584, 18944)],
+)
+def test_decode_full_size_config3(layer: str, n: int, k: int, device: torch.device) -> None:
+    """BASELINE config 3 at full size: M in {1, 2, 4} on every Qwen2.5-7B decoder linear,
+    through the op (default configs) and through each GEMV form (K split over the waves, waves
+    over row tiles, MFMA), against an fp32 product of the exactly dequantized weights (the
+    dequant kernel is bit-exact with the oracle's). The same inputs give the same bits in every
+    config of one form on repeated calls."""
+    from tokenforge_amd.kernels.autotune import synthetic_layer
+
+    qweight_t, scales, qzeros = synthetic_layer(n, k, G, device, seed=11)
+    wt = w4a16_dequant(qweight_t, scales, qzeros, G).float().t().contiguous()
+    forms = [GemmConfig("gemv_dot", 4, 16, 128, 1, 8, 2), GemmConfig("gemv_dot", 4, 16, 256, 1, 4, 4),
+             GemmConfig("gemv_mfma", 16, 16, 128, 1, 8, 4), GemmConfig("gemv_mfma", 16, 16, 256, 1, 4, 2)]
+    for m in (1, 2, 4):
+        gen = torch.Generator(device=device).manual_seed(m)
+        x = torch.randn((m, k), generator=gen, device=device).to(torch.float16)
+        ref = x.float() @ wt
+        scale = float(ref.abs().max())
+        outs = [torch.ops.tokenforge.w4a16_linear(x, qweight_t, scales, qzeros, None, G, "hip")]
+        outs += [w4a16_gemm(x, qweight_t, scales, qzeros, G, cfg) for cfg in forms]
+        for cfg, y in zip(["op"] + forms, outs):
+            rel = float((y.float() - ref).abs().max()) / scale
+            assert rel <= 2e-3, f"{layer} m={m} {cfg}: max error {rel:.3e} of max |y|"
+        again = w4a16_gemm(x, qweight_t, scales, qzeros, G, forms[1])
+        assert torch.equal(again, outs[2])
+
+
 @pytest.mark.parametrize("group_size", [32, 64])
 def test_small_group_sizes(group_size: int, device: torch.device) -> None:
     n, k = 96, 384
