@@ -42,6 +42,27 @@ def test_fake_tensor_shapes() -> None:
         assert sc.shape == (2, 3, 1) and sc.dtype == torch.float32
 
 
+def test_fake_tensor_shapes_of_the_added_ops() -> None:
+    """The fused-epilogue and W4A8 ops (no counterpart in the reference) propagate shapes too."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    qw, s, z = _layer(torch.device("cpu"))
+    with FakeTensorMode() as mode:
+        f = mode.from_tensor
+        x = f(cases.activations(6, 256, 0)).reshape(2, 3, 256)
+        r = f(torch.zeros((2, 3, 64), dtype=torch.float16))
+        out = torch.ops.tokenforge.w4a16_linear_residual(x, f(qw), f(s), f(z), None, r, G, "hip")
+        assert out.shape == (2, 3, 64) and out.dtype == torch.float16
+        out = torch.ops.tokenforge.w4a16_linear_silu_mul(x, f(qw), f(s), f(z), None, G, "hip")
+        assert out.shape == (2, 3, 32) and out.dtype == torch.float16
+        x8 = f(torch.zeros((2, 3, 256), dtype=torch.float8_e4m3fn))
+        sc = f(torch.ones((2, 3, 1), dtype=torch.float32))
+        out = torch.ops.tokenforge.w4a8_linear(x8, sc, f(qw), f(s), f(z), None, G, "hip")
+        assert out.shape == (2, 3, 64) and out.dtype == torch.float16
+        out = torch.ops.tokenforge.w4a8_linear(x8, sc, f(qw), f(s), f(z), None, G, "hip", "silu_mul")
+        assert out.shape == (2, 3, 32)
+
+
 def test_rejects_marlin_at_op_level() -> None:
     qw, s, z = _layer(torch.device("cpu"))
     with pytest.raises(ValueError, match="op level"):
@@ -84,6 +105,23 @@ def test_opcheck_dequant_and_rmsnorm(device: torch.device) -> None:
     )
 
 
+@pytest.mark.gpu
+def test_opcheck_added_ops(device: torch.device) -> None:
+    qw, s, z = _layer(device)
+    x = cases.activations(3, 256, 0).to(device)
+    r = cases.activations(3, 64, 1).to(device)
+    b = cases.bias(64, 0).to(device)
+    ops = torch.ops.tokenforge
+    opcheck(ops.w4a16_linear_residual.default, (x, qw, s, z, b, r, G, "hip"), test_utils=OPCHECK_TESTS)
+    opcheck(ops.w4a16_linear_silu_mul.default, (x, qw, s, z, None, G, "hip"), test_utils=OPCHECK_TESTS)
+    q8, sc = ops.rmsnorm_fp8_quant(x, torch.ones(256, dtype=torch.float16, device=device), 1e-6, None)
+    # opcheck's schema test does arithmetic on the inputs, which torch has no kernel for in
+    # float8_e4m3fn; the fake-tensor and dynamic-shape AOT checks run.
+    w4a8_tests = ("test_faketensor", "test_aot_dispatch_dynamic")
+    opcheck(ops.w4a8_linear.default, (q8, sc, qw, s, z, b, G, "hip"), test_utils=w4a8_tests)
+    opcheck(ops.w4a8_linear.default, (q8, sc, qw, s, z, None, G, "hip", "residual", r), test_utils=w4a8_tests)
+
+
 class _QLinear(torch.nn.Module):
     def __init__(self, device: torch.device) -> None:
         super().__init__()
@@ -111,3 +149,31 @@ def test_torch_compile_fullgraph_no_graph_breaks(device: torch.device) -> None:
     # Bucket 32 is served by either family (the tuned config decides; untuned it is the GEMM).
     calls = [KERNEL_CALLS.value(kernel=k, bucket="32") for k in ("hip_gemv", "hip_gemm")]
     assert sum(calls) == 2
+
+
+class _FusedMlp(torch.nn.Module):
+    """RMSNorm + FP8 -> W4A8 gate_up with SiLU*mul -> W4A16 down with the residual add."""
+
+    def __init__(self, device: torch.device) -> None:
+        super().__init__()
+        gq, gs, gz = _layer(device, 512, 256)  # gate and up halves of 256 each
+        dq, ds, dz = _layer(device, 256, 256)
+        for name, t in (("gq", gq), ("gs", gs), ("gz", gz), ("dq", dq), ("ds", ds), ("dz", dz)):
+            self.register_buffer(name, t)
+        self.register_buffer("gamma", torch.ones(256, dtype=torch.float16, device=device))
+
+    def forward(self, h: torch.Tensor) -> torch.Tensor:
+        ops = torch.ops.tokenforge
+        q8, sc = ops.rmsnorm_fp8_quant(h, self.gamma, 1e-6, None)
+        act = ops.w4a8_linear(q8, sc, self.gq, self.gs, self.gz, None, G, "hip", "silu_mul")
+        return ops.w4a16_linear_residual(act, self.dq, self.ds, self.dz, None, h, G, "hip")
+
+
+@pytest.mark.gpu
+def test_torch_compile_fullgraph_added_ops(device: torch.device) -> None:
+    mod = _FusedMlp(device)
+    h = cases.activations(5, 256, 4).to(device)
+    compiled = torch.compile(mod, backend="aot_eager", fullgraph=True, dynamic=True)
+    assert torch.equal(compiled(h), mod(h))
+    h2 = cases.activations(9, 256, 5).to(device)
+    assert torch.equal(compiled(h2), mod(h2))
