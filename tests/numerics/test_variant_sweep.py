@@ -1,0 +1,72 @@
+"""Every compiled kernel variant on its own seeded random case.
+
+The code-path tests pick representative configs; this sweep runs all of ``VARIANTS`` (the
+library's table) once each, with the shape, group size, M, split_k, bias and epilogue drawn
+from a generator seeded by the variant's index, against the fp64 oracle with the derived
+tolerance and the normwise bound (and the fused epilogues against their unfused torch expressions, bit for bit).
+N is sometimes ragged against the tile; K sometimes ends in a partial 128-wide step.
+"""
+
+from __future__ import annotations
+
+import random
+
+import pytest
+import torch
+
+from tests.numerics import cases
+from tests.numerics.test_w4a16 import _assert_close
+from tokenforge_amd.kernels.config import VARIANTS, GemmConfig
+from tokenforge_amd.kernels.hip.w4a16 import w4a16_gemm, w4a16_gemm_ex
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(index: int, variant: tuple) -> dict:  # type: ignore[type-arg]
+    kernel, bm, bn, bk, warps, stages = variant
+    rng = random.Random(1000 + index)
+    if kernel == "gemm_mfma" and bk != 128:
+        group = rng.choice([g for g in (32, 64, 128) if g >= bk and g % bk == 0])
+    else:
+        group = rng.choice((32, 64, 128))
+    k = group * rng.randint(2, 8) if rng.random() < 0.5 else 128 * rng.randint(2, 6)
+    k = max(k, group)
+    n = 8 * rng.randint(8, 64)
+    if rng.random() < 0.5:
+        n = 16 * rng.randint(4, 32)  # a multiple of 16 (the SiLU*mul epilogue needs it)
+    if kernel == "gemv_dot":
+        m = rng.randint(1, bm)
+    elif kernel == "gemv_mfma":
+        m = rng.randint(1, 2 * bm + 3)
+    else:
+        m = rng.randint(1, 2 * bm + 5)
+    split = rng.choice((1, 2, 3)) if kernel == "gemm_mfma" else 1
+    epilogue = rng.choice(("none", "none", "residual", "silu_mul")) if n % 16 == 0 else "none"
+    return {"cfg": GemmConfig(kernel, bm, bn, bk, split, warps, stages), "group": group, "k": k, "n": n, "m": m,
+            "bias": rng.random() < 0.5, "epilogue": epilogue, "seed": index}
+
+
+@pytest.mark.parametrize("index", range(len(VARIANTS)))
+def test_every_variant(index: int, device: torch.device) -> None:
+    c = _case(index, VARIANTS[index])
+    cfg, g, k, n, m = c["cfg"], c["group"], c["k"], c["n"], c["m"]
+    w = cases.layer_weights(n, k, c["seed"], g)
+    wd = cases.on_device(w, device)
+    x = cases.activations(m, k, c["seed"])
+    b = cases.bias(n, c["seed"]) if c["bias"] else None
+    xd, bd = x.to(device), None if b is None else b.to(device)
+    print(f"variant {index}: {cfg} k={k} n={n} m={m} g={g}", flush=True)
+    try:
+        y = w4a16_gemm(xd, wd.qweight_t, wd.scales, wd.qzeros, g, cfg, bd)
+    except ValueError as e:
+        # The only refusals a drawn case may meet: an LDS bound of the shared-x GEMV forms.
+        assert "fit" in str(e), f"{cfg} k={k} n={n} m={m} g={g}: {e}"
+        return
+    _assert_close(y, x, w, b)
+    if c["epilogue"] == "silu_mul":
+        fused = w4a16_gemm_ex(xd, wd.qweight_t, wd.scales, wd.qzeros, g, cfg, bd, "silu_mul")
+        assert torch.equal(fused, torch.nn.functional.silu(y[:, : n // 2]) * y[:, n // 2 :]), str(cfg)
+    elif c["epilogue"] == "residual":
+        r = cases.activations(m, n, c["seed"] + 1).to(device)
+        fused = w4a16_gemm_ex(xd, wd.qweight_t, wd.scales, wd.qzeros, g, cfg, bd, "residual", r)
+        assert torch.equal(fused, r + y), str(cfg)
