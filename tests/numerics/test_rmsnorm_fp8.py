@@ -162,6 +162,27 @@ def test_special_values_rows_and_scales(device: torch.device) -> None:
         _assert_codes_match_nan_aware(_codes(q), q_ref)
 
 
+@pytest.mark.parametrize("eps", [0.0, -1.0])
+def test_rows_with_infinite_or_nan_rstd(eps: float, device: torch.device) -> None:
+    """eps = 0 on an all-zero row makes rstd = inf (every y = 0 * inf = NaN); eps = -1 makes it
+    NaN on rows whose mean square is below 1. H = 896 leaves the last 8-element chunks of every
+    thread past the row, which load zeros: their y must not change the row's absmax (the
+    vector path takes the max of all chunks without a mask)."""
+    h = 896
+    gen = torch.Generator().manual_seed(31)
+    x = (torch.randn((4, h), generator=gen) * 0.5).to(torch.float16)
+    w = (torch.rand((h,), generator=gen) + 0.5).to(torch.float16)
+    x[1] = 0.0
+    x[3] = (torch.randn((h,), generator=gen) * 3).to(torch.float16)
+    with np.errstate(all="ignore"):
+        q_ref, s_ref = oref.rmsnorm_fp8_reference(x.numpy(), w.numpy(), eps)
+    q, s = rmsnorm_fp8_quant(x.to(device), w.to(device), eps)
+    _assert_codes_match_nan_aware(_codes(q), q_ref)
+    s_k = s.cpu().numpy()
+    assert np.array_equal(np.isnan(s_k), np.isnan(s_ref))
+    assert np.array_equal(s_k[~np.isnan(s_k)].view(np.uint32), s_ref[~np.isnan(s_ref)].view(np.uint32))
+
+
 def test_zero_row_uses_min_scale(device: torch.device) -> None:
     x = torch.zeros((2, 256), dtype=torch.float16)
     w = torch.ones(256, dtype=torch.float16)

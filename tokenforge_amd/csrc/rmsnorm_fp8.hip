@@ -28,6 +28,7 @@ namespace tf {
 namespace {
 
 constexpr float kFp8Max = 448.0f;
+typedef unsigned short us2 __attribute__((ext_vector_type(2)));
 
 // fp16(fp32(a * b)): reference.py:39 rounds x * rstd to fp32 and then to fp16. Left alone,
 // the backend folds the multiply and the conversion into v_fma_mixlo_f16, which rounds once,
@@ -136,6 +137,7 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_fp8_kernel(
   const float rstd = 1.0f / __builtin_sqrtf(var + eps);
 
   uint32_t amax_bits = 0;
+  us2 amax_pk = {0, 0};
 #pragma unroll
   for (int i = 0; i < CPT; ++i) {
     const int e0 = (tid + i * kThreads) * 8;
@@ -147,13 +149,21 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_fp8_kernel(
       nrm[1] = mul_round_f32_then_f16((float)xv[i][j][1], rstd);
       const h2 y = nrm * wv[i][j];
       xv[i][j] = y;  // the row is reused in place for y
-      const uint32_t yb = as_u32(y);
-      const uint32_t a0 = e0 + 2 * j < h ? (yb & 0x7FFFu) : 0u;
-      const uint32_t a1 = e0 + 2 * j + 1 < h ? ((yb >> 16) & 0x7FFFu) : 0u;
-      const uint32_t am = a0 > a1 ? a0 : a1;
-      amax_bits = amax_bits > am ? amax_bits : am;
+      const uint32_t yb = as_u32(y) & 0x7FFF7FFFu;
+      if (VEC) {
+        // Whole 8-element chunks past h load x = 0 and weight = 0, so their y is fp16(0 * rstd) * 0:
+        // 0 when rstd is finite, NaN only when rstd is inf or NaN, and then every y of the row is
+        // NaN as well (0 * inf, x * NaN). No mask is needed; both halves go into one packed max.
+        amax_pk = __builtin_elementwise_max(amax_pk, __builtin_bit_cast(us2, yb));
+      } else {
+        const uint32_t a0 = e0 + 2 * j < h ? (yb & 0xFFFFu) : 0u;
+        const uint32_t a1 = e0 + 2 * j + 1 < h ? (yb >> 16) : 0u;
+        const uint32_t am = a0 > a1 ? a0 : a1;
+        amax_bits = amax_bits > am ? amax_bits : am;
+      }
     }
   }
+  if (VEC) amax_bits = amax_pk[0] > amax_pk[1] ? amax_pk[0] : amax_pk[1];
   const uint32_t m_bits = block_max_u32<WAVES>(amax_bits, red_u);
   const float amax = (float)__builtin_bit_cast(_Float16, (uint16_t)m_bits);
 
