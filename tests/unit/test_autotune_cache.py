@@ -202,3 +202,42 @@ def test_real_tuning_picks_a_correct_config(device: torch.device) -> None:
         ref = w4a16_gemm(x, qweight_t, scales, qzeros, G, default_config(bucket, 256, 512, G)).float()
         out = w4a16_gemm(x, qweight_t, scales, qzeros, G, cfg).float()
         assert float((out - ref).abs().max()) <= 1e-2 * float(ref.abs().max()) + 1e-3
+
+
+def _cfgs(n: int) -> list[GemmConfig]:
+    return [GemmConfig("gemv_dot", 1, 16, 128, 1, w, s) for w in (1, 2, 4, 8) for s in (2, 4, 8)][:n]
+
+
+def test_finalist_selection_prefers_the_steady_median_over_a_lucky_screen() -> None:
+    """The screen's fastest config (a lucky single sample) loses to one whose re-timings are
+    lower; only the screen's best FINALISTS are re-timed, each FINAL_ROUNDS times."""
+    cfgs = _cfgs(10)
+    steady = {c: 1.0 + 0.01 * i for i, c in enumerate(cfgs)}  # cfgs[0] is truly fastest ...
+    lucky = cfgs[5]
+    steady[lucky] = 1.08
+    screened = [(steady[c], c) for c in cfgs]
+    screened[5] = (0.9, lucky)  # ... but cfgs[5] won the screen by chance
+    calls: list[GemmConfig] = []
+
+    def time_cfg(c: GemmConfig) -> float:
+        calls.append(c)
+        return steady[c]
+
+    assert autotune.select_finalist(screened, time_cfg) == cfgs[0]
+    finalists = {c for _, c in sorted(screened, key=lambda r: r[0])[: autotune.FINALISTS]}
+    assert set(calls) == finalists
+    assert len(calls) == autotune.FINALISTS * autotune.FINAL_ROUNDS
+    # interleaved: every round times each finalist once, starting one later each round
+    rounds = [calls[r * autotune.FINALISTS:(r + 1) * autotune.FINALISTS] for r in range(autotune.FINAL_ROUNDS)]
+    assert all(set(r) == finalists for r in rounds)
+    assert len({r[0] for r in rounds}) == autotune.FINAL_ROUNDS
+
+
+def test_finalist_selection_median_ignores_one_outlier_and_breaks_ties_by_screen() -> None:
+    a, b = _cfgs(2)
+    samples = {a: iter([0.5, 2.0, 2.0, 2.0, 2.0]), b: iter([1.5] * 5)}
+    assert autotune.select_finalist([(1.0, a), (1.1, b)], lambda c: next(samples[c])) == b
+    assert autotune.select_finalist([(1.1, a), (1.0, b)], lambda c: 1.0) == b  # tie: screen order
+    assert autotune.select_finalist([(1.0, a)], lambda c: pytest.fail("one candidate: no re-timing")) == a
+    with pytest.raises(ValueError):
+        autotune.select_finalist([], lambda c: 1.0)
