@@ -32,6 +32,8 @@ Extra objects on the same JSON line:
   WRITE_DIR PROBE_LOG`` turns the two counter runs into that summary.
 * ``gemm_m256``: the prefill GEMM at M=256 on gate_up and down, TFLOP/s and fraction of the
   2.5 PFLOP/s fp16 dense MFMA peak.
+* ``per_shape`` and ``gemv_m2_m4``: the GEMV on each of the four shapes at
+  M = 1, and at M = 2 and 4 (buckets 2 and 4 autotuned), average launch duration and GB/s.
 * ``rmsnorm_fp8``: the fused RMSNorm + e4m3fn quant (configs[1]: H=3584, eight outlier
   channels x20, gamma = 1 + 0.1 N(0,1), eps 1e-6, dynamic per-token scale) at T in
   {1, 16, 512, 4096}; algorithmic bytes T*H*2 + H*2 + T*H + 4*T over rotating cold inputs.
@@ -449,7 +451,7 @@ def main() -> int:
     if not args.no_tune and not args.traffic_probe:  # the probe runs every candidate
         t0 = time.perf_counter()
         for _, n, k in SHAPES:
-            buckets = (1, 256) if n in (37888,) or k == 18944 else (1,)
+            buckets = (1, 2, 4, 256) if n in (37888,) or k == 18944 else (1, 2, 4)
             autotune.tune_layer(n, k, GROUP, device=dev, gpu=gpu, buckets=buckets)
         log(f"autotune: {time.perf_counter() - t0:.1f}s")
     cfg1 = [autotune.lookup(gpu, 1, n, k, GROUP) for _, n, k in SHAPES]
@@ -511,6 +513,20 @@ def main() -> int:
                           "frac_hbm": gbps / HBM_PEAK_GBPS, "config": cfg1[i].to_dict()})
         log(f"  {name:13s} M=1 {ms * 1e3:8.2f} us {gbps:7.0f} GB/s ({100 * gbps / HBM_PEAK_GBPS:.1f}% of 8 TB/s)")
     dom = per_shape[2]
+
+    # the GEMV at M = 2 and 4 on the four shapes (M = 1 is per_shape), tuned buckets.
+    gemv_m24 = []
+    for m in (2, 4):
+        xm_all = [torch.randn((m, k), generator=gen, device=dev).to(torch.float16) for _, _, k in SHAPES]
+        cfgm = [autotune.lookup(gpu, m, n, k, GROUP) for _, n, k in SHAPES]
+        for i, (name, n, k) in enumerate(SHAPES):
+            g, _ = capture([launcher(r % copies, i, xm_all, cfgm) for r in range(reps)])
+            ms = median_replay_ms(g, reps)
+            gbps = bytes_moved(m, n, k) / (ms * 1e-3) / 1e9
+            gemv_m24.append({"layer": name, "m": m, "n": n, "k": k, "us": ms * 1e3, "gbps": gbps,
+                             "frac_hbm": gbps / HBM_PEAK_GBPS, "config": cfgm[i].to_dict()})
+            log(f"  {name:13s} M={m} {ms * 1e3:8.2f} us {gbps:7.0f} GB/s ({100 * gbps / HBM_PEAK_GBPS:.1f}% of 8 TB/s)")
+            del g
 
     # Prefill GEMM at M=256 on gate_up and down.
     gemm = []
@@ -615,6 +631,7 @@ def main() -> int:
         "rmsnorm_fp8": norm,
         "repack_gate_up_gbps": (gate_n * gate_k) / (rep_ms * 1e-3) / 1e9,
         "per_shape": per_shape,
+        "gemv_m2_m4": gemv_m24,
         "stack": stack,
         "cpu_baseline": cpu,
         "gpu": gpu,
