@@ -48,7 +48,8 @@ Extra objects on the same JSON line:
   h // 7) -> o_proj -> residual add -> RMSNorm + FP8 -> fp16(q * scale) -> gate_up -> SiLU(gate)
   * up -> down -> residual add. The linears and the norms are this library's kernels, the
   rest is torch glue ("unfused"), or the residual adds and SiLU*mul run as the linears'
-  fused epilogues ("fused", same bits; ``tokens_per_s`` is this one), or in addition qkv and
+  fused epilogues and the norms write fp16(q * scale) themselves ("fused", same bits;
+  ``tokens_per_s`` is this one), or in addition qkv and
   gate_up take the FP8 codes and scales directly as W4A8 linears ("w4a8", no fp16(q * scale)
   glue; not bit-equal: the scale multiplies each row's sum instead of each element). A pass
   is one HIP graph, tokens/s = M / time per pass. M=1 on every run; ``--stack`` or ``--full``
@@ -295,18 +296,26 @@ def stack_bench(dev: torch.device, gpu: str, ms: tuple[int, ...], tune: bool) ->
     def layer_pass(x: torch.Tensor, layer: tuple) -> torch.Tensor:  # type: ignore[type-arg]
         (qkv, o, gu, down), bias, g1, g2 = layer
         m = x.shape[0]
-        q8, s = ops.rmsnorm_fp8_quant(x, g1, eps, None)
-        if mode == "w4a8":
-            y = ops.w4a8_linear(q8, s, *qkv, bias, GROUP, "hip")
-        else:
-            a = (q8.to(torch.float32) * s).to(torch.float16)
+        if mode == "fused":  # the norm also writes fp16(q * scale), the qkv input
+            _, _, a = ops.rmsnorm_fp8_quant_dequant(x, g1, eps, None)
             y = ops.w4a16_linear(a, *qkv, bias, GROUP, "hip")
+        else:
+            q8, s = ops.rmsnorm_fp8_quant(x, g1, eps, None)
+            if mode == "w4a8":
+                y = ops.w4a8_linear(q8, s, *qkv, bias, GROUP, "hip")
+            else:
+                a = (q8.to(torch.float32) * s).to(torch.float16)
+                y = ops.w4a16_linear(a, *qkv, bias, GROUP, "hip")
         v = y[:, q_width + KV_HEADS * HEAD_DIM:].reshape(m, KV_HEADS, 1, HEAD_DIM)
         attn = v.expand(m, KV_HEADS, h // (KV_HEADS * HEAD_DIM), HEAD_DIM).reshape(m, h)
         if mode == "unfused":
             x = x + ops.w4a16_linear(attn, *o, None, GROUP, "hip")
         else:
             x = ops.w4a16_linear_residual(attn, *o, None, x, GROUP, "hip")
+        if mode == "fused":
+            _, _, a = ops.rmsnorm_fp8_quant_dequant(x, g2, eps, None)
+            act = ops.w4a16_linear_silu_mul(a, *gu, None, GROUP, "hip")
+            return ops.w4a16_linear_residual(act, *down, None, x, GROUP, "hip")
         q8, s = ops.rmsnorm_fp8_quant(x, g2, eps, None)
         if mode == "w4a8":
             act = ops.w4a8_linear(q8, s, *gu, None, GROUP, "hip", "silu_mul")

@@ -172,6 +172,17 @@ int tf_rmsnorm_fp8_quant(const uint16_t* x, int64_t ldx, const uint16_t* weight,
                          uint8_t* q, int64_t ldq, float* scale, int32_t static_scale,
                          int64_t t, int64_t h, float eps, void* stream);
 
+/* tf_rmsnorm_fp8_quant that also writes dq fp16 [t, h] (row stride lddq) =
+ * fp16(fp32(q) * scale): the fp16 activation a W4A16 linear reads when it is fed from the
+ * codes, which the reference computes as a separate torch expression
+ * `(q.to(torch.float32) * scale).to(torch.float16)` (no kernel counterpart in the reference;
+ * for callers that feed a W4A16 linear from the norm's FP8 output in one launch).
+ * dq == NULL is tf_rmsnorm_fp8_quant. */
+int tf_rmsnorm_fp8_quant_dq(const uint16_t* x, int64_t ldx, const uint16_t* weight,
+                            uint8_t* q, int64_t ldq, float* scale, int32_t static_scale,
+                            uint16_t* dq, int64_t lddq, int64_t t, int64_t h, float eps,
+                            void* stream);
+
 /* Test hook for the e4m3fn encoding used by tf_rmsnorm_fp8_quant
  * (rmsnorm_fp8.py:29-41 _round_to_e4m3_grid + cast): fp32 [count] -> uint8 [count], through
  * the same hardware conversion (v_cvt_pk_fp8_f32) and NaN handling as that kernel.

@@ -16,7 +16,12 @@ import torch
 
 import tokenforge_amd.kernels.ops  # noqa: F401
 from oracle import reference as oref
-from tokenforge_amd.kernels.hip.rmsnorm_fp8 import FP8_E4M3_MAX, e4m3_encode, rmsnorm_fp8_quant
+from tokenforge_amd.kernels.hip.rmsnorm_fp8 import (
+    FP8_E4M3_MAX,
+    e4m3_encode,
+    rmsnorm_fp8_quant,
+    rmsnorm_fp8_quant_dequant,
+)
 
 pytestmark = pytest.mark.gpu
 EPS = 1e-6
@@ -181,6 +186,50 @@ def test_rows_with_infinite_or_nan_rstd(eps: float, device: torch.device) -> Non
     s_k = s.cpu().numpy()
     assert np.array_equal(np.isnan(s_k), np.isnan(s_ref))
     assert np.array_equal(s_k[~np.isnan(s_k)].view(np.uint32), s_ref[~np.isnan(s_ref)].view(np.uint32))
+
+
+def _assert_f16_match_nan_aware(a: torch.Tensor, b: torch.Tensor) -> None:
+    an, bn = torch.isnan(a), torch.isnan(b)
+    assert torch.equal(an, bn)
+    assert torch.equal(a[~an].view(torch.int16), b[~bn].view(torch.int16))
+
+
+@pytest.mark.parametrize(("t", "h", "aligned"), [(1, 3584, True), (7, 896, True), (33, 3584, True), (5, 1000, False)])
+def test_dequantized_output_equals_the_torch_expression(t: int, h: int, aligned: bool, device: torch.device) -> None:
+    """rmsnorm_fp8_quant_dequant: the codes and scales are rmsnorm_fp8_quant's, bit for bit, and
+    the fp16 output is `(q.to(float32) * scale).to(float16)` bit for bit (dynamic and static
+    scales, the large one leaving mostly subnormal and zero codes; the scalar path for an
+    unaligned x)."""
+    x, w = baseline_inputs(t, h, seed=5)[:2] if h == 3584 else _inputs(t, h, seed=5)
+    xd = x.to(device)
+    if not aligned:
+        buf = torch.empty(t * (h + 3) + 1, dtype=torch.float16, device=device)
+        xd = buf[1:].view(t, h + 3)[:, :h]
+        xd.copy_(x.to(device))
+    wd = w.to(device)
+    for sc in (None, torch.full((1,), 0.05, device=device), torch.full((1,), 400.0, device=device)):
+        q, s, a = rmsnorm_fp8_quant_dequant(xd, wd, EPS, sc)
+        q0, s0 = rmsnorm_fp8_quant(xd, wd, EPS, sc)
+        assert np.array_equal(_codes(q), _codes(q0))
+        assert torch.equal(s, s0)
+        _assert_f16_match_nan_aware(a, (q.to(torch.float32) * s).to(torch.float16))
+
+
+def test_dequantized_output_of_special_rows(device: torch.device) -> None:
+    """Rows with inf, NaN and zeros (the kernel's NaN-preserving slow path) and the op's leading dims."""
+    h = 896
+    gen = torch.Generator().manual_seed(23)
+    x = (torch.randn((6, h), generator=gen) * 2).to(torch.float16)
+    w = (torch.rand((h,), generator=gen) + 0.5).to(torch.float16)
+    x[0, 3] = float("inf")
+    x[1, 7] = float("nan")
+    x[3] = 0.0
+    x[5, 9] = float("-inf")
+    q, s, a = torch.ops.tokenforge.rmsnorm_fp8_quant_dequant(x.reshape(2, 3, h).to(device), w.to(device), EPS, None)
+    assert q.shape == a.shape == (2, 3, h) and s.shape == (2, 3, 1)
+    q0, s0 = rmsnorm_fp8_quant(x.to(device), w.to(device), EPS)
+    assert np.array_equal(_codes(q.reshape(6, h)), _codes(q0))
+    _assert_f16_match_nan_aware(a.reshape(6, h), (q0.to(torch.float32) * s0).to(torch.float16))
 
 
 def test_zero_row_uses_min_scale(device: torch.device) -> None:

@@ -61,6 +61,13 @@ def test_fake_tensor_shapes_of_the_added_ops() -> None:
         assert out.shape == (2, 3, 64) and out.dtype == torch.float16
         out = torch.ops.tokenforge.w4a8_linear(x8, sc, f(qw), f(s), f(z), None, G, "hip", "silu_mul")
         assert out.shape == (2, 3, 32)
+        gamma = f(torch.ones(256, dtype=torch.float16))
+        q, qs, a = torch.ops.tokenforge.rmsnorm_fp8_quant_dequant(x, gamma, 1e-6, None)
+        assert q.shape == (2, 3, 256) and q.dtype == torch.float8_e4m3fn
+        assert qs.shape == (2, 3, 1) and qs.dtype == torch.float32
+        assert a.shape == (2, 3, 256) and a.dtype == torch.float16
+        q, qs, a = torch.ops.tokenforge.rmsnorm_fp8_quant_dequant(x, gamma, 1e-6, f(torch.ones(1)))
+        assert qs.shape == (1,) and a.shape == (2, 3, 256)
 
 
 def test_rejects_marlin_at_op_level() -> None:
@@ -120,6 +127,10 @@ def test_opcheck_added_ops(device: torch.device) -> None:
     w4a8_tests = ("test_faketensor", "test_aot_dispatch_dynamic")
     opcheck(ops.w4a8_linear.default, (q8, sc, qw, s, z, b, G, "hip"), test_utils=w4a8_tests)
     opcheck(ops.w4a8_linear.default, (q8, sc, qw, s, z, None, G, "hip", "residual", r), test_utils=w4a8_tests)
+    gamma = torch.ones(256, dtype=torch.float16, device=device)
+    opcheck(ops.rmsnorm_fp8_quant_dequant.default, (x, gamma, 1e-6, None), test_utils=w4a8_tests)
+    opcheck(ops.rmsnorm_fp8_quant_dequant.default, (x, gamma, 1e-6, torch.full((1,), 0.01, device=device)),
+            test_utils=w4a8_tests)
 
 
 class _QLinear(torch.nn.Module):

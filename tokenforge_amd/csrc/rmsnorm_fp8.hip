@@ -75,12 +75,28 @@ __device__ __forceinline__ uint32_t block_max_u32(uint32_t v, uint32_t* red) {
 
 __device__ __forceinline__ float quotient(_Float16 y, double rcp) { return (float)((double)(float)y * rcp); }
 
+__device__ __forceinline__ uint32_t f16_bits_of(_Float16 v) { return __builtin_bit_cast(uint16_t, v); }
+
+// fp16(fp32(code) * s) of four codes (one word): the activation a W4A16 linear reads when it is
+// fed from the codes, as `(q.to(float32) * scale).to(float16)` computes it. Every e4m3fn code,
+// NaN included, decodes exactly; the product is rounded to fp32 and then to fp16.
+__device__ __forceinline__ u2 dequant_codes4(uint32_t codes, float s) {
+  const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)codes, false);
+  const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)codes, true);
+  const uint32_t h0 = f16_bits_of(mul_round_f32_then_f16(lo[0], s));
+  const uint32_t h1 = f16_bits_of(mul_round_f32_then_f16(lo[1], s));
+  const uint32_t h2 = f16_bits_of(mul_round_f32_then_f16(hi[0], s));
+  const uint32_t h3 = f16_bits_of(mul_round_f32_then_f16(hi[1], s));
+  return u2{h0 | (h1 << 16), h2 | (h3 << 16)};
+}
+
 // CPT: 8-element chunks per thread. VEC: 16-byte x / weight loads and 8-byte code stores.
-template <int WAVES, int CPT, bool VEC>
+// DQ: also write dq[T, H] fp16 = fp16(fp32(code) * scale) (16-byte stores when VEC).
+template <int WAVES, int CPT, bool VEC, bool DQ>
 __global__ __launch_bounds__(WAVES * 64) void rmsnorm_fp8_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* __restrict__ w,
-    uint8_t* __restrict__ q, int64_t ldq, float* __restrict__ scale, int static_scale, int h,
-    float eps) {
+    uint8_t* __restrict__ q, int64_t ldq, float* __restrict__ scale, int static_scale,
+    uint16_t* __restrict__ dq, int64_t lddq, int h, float eps) {
   constexpr int kThreads = WAVES * 64;
   __shared__ double red_d[WAVES];
   __shared__ uint32_t red_u[WAVES];
@@ -216,31 +232,60 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_fp8_kernel(
       for (int j = 0; j < 8; ++j)
         if (e0 + j < h) qr[e0 + j] = (uint8_t)((j < 4 ? lo : hi) >> (8 * (j & 3)));
     }
+    if (DQ) {
+      const u2 a = dequant_codes4(lo, s), b = dequant_codes4(hi, s);
+      uint16_t* dr = dq + row * lddq;
+      if (VEC) {
+        if (e0 < h) *reinterpret_cast<u4*>(dr + e0) = u4{a[0], a[1], b[0], b[1]};
+      } else {
+        const uint32_t words[4] = {a[0], a[1], b[0], b[1]};
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          if (e0 + j < h) dr[e0 + j] = (uint16_t)(words[j >> 1] >> (16 * (j & 1)));
+      }
+    }
   }
 }
 
-template <int WAVES, int CPT>
-int launch_cpt(bool vec, const uint16_t* x, int64_t ldx, const uint16_t* w, uint8_t* q, int64_t ldq,
-               float* scale, int static_scale, int64_t t, int h, float eps, hipStream_t stream) {
-  if (vec)
-    rmsnorm_fp8_kernel<WAVES, CPT, true>
-        <<<(unsigned)t, WAVES * 64, 0, stream>>>(x, ldx, w, q, ldq, scale, static_scale, h, eps);
+struct NormArgs {
+  const uint16_t* x;
+  int64_t ldx;
+  const uint16_t* w;
+  uint8_t* q;
+  int64_t ldq;
+  float* scale;
+  int static_scale;
+  uint16_t* dq;  // nullptr: codes and scales only
+  int64_t lddq;
+  int64_t t;
+  int h;
+  float eps;
+};
+
+template <int WAVES, int CPT, bool VEC>
+int launch_vec(const NormArgs& n, hipStream_t stream) {
+  if (n.dq)
+    rmsnorm_fp8_kernel<WAVES, CPT, VEC, true><<<(unsigned)n.t, WAVES * 64, 0, stream>>>(
+        n.x, n.ldx, n.w, n.q, n.ldq, n.scale, n.static_scale, n.dq, n.lddq, n.h, n.eps);
   else
-    rmsnorm_fp8_kernel<WAVES, CPT, false>
-        <<<(unsigned)t, WAVES * 64, 0, stream>>>(x, ldx, w, q, ldq, scale, static_scale, h, eps);
+    rmsnorm_fp8_kernel<WAVES, CPT, VEC, false><<<(unsigned)n.t, WAVES * 64, 0, stream>>>(
+        n.x, n.ldx, n.w, n.q, n.ldq, n.scale, n.static_scale, nullptr, 0, n.h, n.eps);
   return check_launch("tf_rmsnorm_fp8_quant");
 }
 
+template <int WAVES, int CPT>
+int launch_cpt(bool vec, const NormArgs& n, hipStream_t stream) {
+  return vec ? launch_vec<WAVES, CPT, true>(n, stream) : launch_vec<WAVES, CPT, false>(n, stream);
+}
+
 template <int WAVES>
-int launch_waves(int cpt, bool vec, const uint16_t* x, int64_t ldx, const uint16_t* w, uint8_t* q,
-                 int64_t ldq, float* scale, int static_scale, int64_t t, int h, float eps,
-                 hipStream_t stream) {
+int launch_waves(int cpt, bool vec, const NormArgs& n, hipStream_t stream) {
   switch (cpt) {
-    case 1: return launch_cpt<WAVES, 1>(vec, x, ldx, w, q, ldq, scale, static_scale, t, h, eps, stream);
-    case 2: return launch_cpt<WAVES, 2>(vec, x, ldx, w, q, ldq, scale, static_scale, t, h, eps, stream);
-    case 4: return launch_cpt<WAVES, 4>(vec, x, ldx, w, q, ldq, scale, static_scale, t, h, eps, stream);
-    case 8: return launch_cpt<WAVES, 8>(vec, x, ldx, w, q, ldq, scale, static_scale, t, h, eps, stream);
-    default: return launch_cpt<WAVES, 16>(vec, x, ldx, w, q, ldq, scale, static_scale, t, h, eps, stream);
+    case 1: return launch_cpt<WAVES, 1>(vec, n, stream);
+    case 2: return launch_cpt<WAVES, 2>(vec, n, stream);
+    case 4: return launch_cpt<WAVES, 4>(vec, n, stream);
+    case 8: return launch_cpt<WAVES, 8>(vec, n, stream);
+    default: return launch_cpt<WAVES, 16>(vec, n, stream);
   }
 }
 
@@ -251,12 +296,14 @@ bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p
 
 using namespace tf;
 
-extern "C" int tf_rmsnorm_fp8_quant(const uint16_t* x, int64_t ldx, const uint16_t* weight,
-                                    uint8_t* q, int64_t ldq, float* scale, int32_t static_scale,
-                                    int64_t t, int64_t h, float eps, void* stream) {
+extern "C" int tf_rmsnorm_fp8_quant_dq(const uint16_t* x, int64_t ldx, const uint16_t* weight,
+                                       uint8_t* q, int64_t ldq, float* scale, int32_t static_scale,
+                                       uint16_t* dq, int64_t lddq, int64_t t, int64_t h, float eps,
+                                       void* stream) {
   if (!x || !weight || !q || !scale) return fail(TF_EINVAL, "tf_rmsnorm_fp8_quant: null pointer");
   if (t < 0 || h <= 0) return fail(TF_EINVAL, "tf_rmsnorm_fp8_quant: need t >= 0 and h > 0");
   if (ldx < h || ldq < h) return fail(TF_EINVAL, "tf_rmsnorm_fp8_quant: row stride smaller than h");
+  if (dq && lddq < h) return fail(TF_EINVAL, "tf_rmsnorm_fp8_quant_dq: dq row stride smaller than h");
   if (t > 0x7FFFFFFF) return fail(TF_EINVAL, "tf_rmsnorm_fp8_quant: too many rows");
   if (h > 16 * 8 * 256) return fail(TF_EINVAL, "tf_rmsnorm_fp8_quant: h above 32768 is not supported");
   if (t == 0) return TF_OK;
@@ -267,12 +314,18 @@ extern "C" int tf_rmsnorm_fp8_quant(const uint16_t* x, int64_t ldx, const uint16
   const int64_t per = cdiv(chunks, waves * 64);
   const int cpt = per <= 1 ? 1 : per <= 2 ? 2 : per <= 4 ? 4 : per <= 8 ? 8 : 16;
   const bool vec = (h % 8 == 0) && (ldx % 8 == 0) && (ldq % 8 == 0) && aligned(x, 16) &&
-                   aligned(weight, 16) && aligned(q, 8);
+                   aligned(weight, 16) && aligned(q, 8) && (!dq || (lddq % 8 == 0 && aligned(dq, 16)));
   hipStream_t s = (hipStream_t)stream;
-  const int hh = (int)h;
+  const NormArgs n{x, ldx, weight, q, ldq, scale, static_scale, dq, lddq, t, (int)h, eps};
   switch (waves) {
-    case 1: return launch_waves<1>(cpt, vec, x, ldx, weight, q, ldq, scale, static_scale, t, hh, eps, s);
-    case 2: return launch_waves<2>(cpt, vec, x, ldx, weight, q, ldq, scale, static_scale, t, hh, eps, s);
-    default: return launch_waves<4>(cpt, vec, x, ldx, weight, q, ldq, scale, static_scale, t, hh, eps, s);
+    case 1: return launch_waves<1>(cpt, vec, n, s);
+    case 2: return launch_waves<2>(cpt, vec, n, s);
+    default: return launch_waves<4>(cpt, vec, n, s);
   }
+}
+
+extern "C" int tf_rmsnorm_fp8_quant(const uint16_t* x, int64_t ldx, const uint16_t* weight,
+                                    uint8_t* q, int64_t ldq, float* scale, int32_t static_scale,
+                                    int64_t t, int64_t h, float eps, void* stream) {
+  return tf_rmsnorm_fp8_quant_dq(x, ldx, weight, q, ldq, scale, static_scale, nullptr, 0, t, h, eps, stream);
 }

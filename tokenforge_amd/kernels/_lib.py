@@ -12,7 +12,7 @@ import functools
 import os
 from pathlib import Path
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 """Must equal ``tf_abi_version()`` of the loaded library."""
 
 LIB_ENV = "TOKENFORGE_HIP_LIB"
@@ -87,6 +87,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          ctypes.POINTER(TfGemmConfig), _i32, _p, _i64, _p, _i64, _p],
     ),
     "tf_rmsnorm_fp8_quant": (ctypes.c_int, [_p, _i64, _p, _p, _i64, _p, _i32, _i64, _i64, _f32, _p]),
+    "tf_rmsnorm_fp8_quant_dq": (ctypes.c_int, [_p, _i64, _p, _p, _i64, _p, _i32, _p, _i64, _i64, _i64, _f32, _p]),
     "tf_e4m3_encode": (ctypes.c_int, [_p, _p, _i64, _p]),
 }
 

@@ -27,6 +27,27 @@ def rmsnorm_fp8_quant(
     ``scale`` is ``[T, 1]`` fp32 for dynamic per-token quantization, or the given ``[1]``
     fp32 tensor for static per-tensor quantization (read, not written).
     """
+    q, s, _ = _launch(x, weight, eps, scale, dequant=False)
+    return q, s
+
+
+def rmsnorm_fp8_quant_dequant(
+    x: torch.Tensor,
+    weight: torch.Tensor,
+    eps: float,
+    scale: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """:func:`rmsnorm_fp8_quant` plus ``a [T, H]`` fp16 = ``(q.to(float32) * scale).to(float16)``,
+    the fp16 activation a W4A16 linear reads when it is fed from the codes, in the same launch
+    (no counterpart in the reference, which would run that expression as separate torch ops)."""
+    q, s, a = _launch(x, weight, eps, scale, dequant=True)
+    assert a is not None
+    return q, s, a
+
+
+def _launch(
+    x: torch.Tensor, weight: torch.Tensor, eps: float, scale: torch.Tensor | None, dequant: bool
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor | None]:
     if x.dim() != 2:
         raise ValueError(f"x must be 2-D [T, H], got {tuple(x.shape)}")
     t, h = x.shape
@@ -43,16 +64,17 @@ def rmsnorm_fp8_quant(
     out = torch.empty((t, h), dtype=torch.float8_e4m3fn, device=dev)
     static = scale is not None
     scale_out = scale if static else torch.empty((t, 1), dtype=torch.float32, device=dev)
+    a = torch.empty((t, h), dtype=torch.float16, device=dev) if dequant else None
     if t == 0 or h == 0:
-        return out, scale_out
+        return out, scale_out, a
     ldx = x.stride(0) if t > 1 else h
     with on_device(dev):
-        rc = _lib.lib().tf_rmsnorm_fp8_quant(
+        rc = _lib.lib().tf_rmsnorm_fp8_quant_dq(
             x.data_ptr(), ldx, weight.data_ptr(), out.data_ptr(), h, scale_out.data_ptr(),
-            1 if static else 0, t, h, float(eps), stream_of(dev),
+            1 if static else 0, 0 if a is None else a.data_ptr(), h, t, h, float(eps), stream_of(dev),
         )
-    _lib.check(rc, "tf_rmsnorm_fp8_quant")
-    return out, scale_out
+    _lib.check(rc, "tf_rmsnorm_fp8_quant_dq")
+    return out, scale_out, a
 
 
 def e4m3_encode(values: torch.Tensor) -> torch.Tensor:

@@ -24,6 +24,11 @@ the W4A8 form, which takes ``rmsnorm_fp8_quant``'s output directly (no counterpa
 * ``tokenforge::w4a8_linear(x8, x_scale, qweight_t, scales, qzeros, bias, group_size, backend,
   epilogue, residual)`` = ``x_scale * (e4m3(x8) @ W^T) + bias`` (then the epilogue)
 
+and the norm with the fp16 activation a W4A16 linear reads from its codes (no counterpart):
+
+* ``tokenforge::rmsnorm_fp8_quant_dequant(x, weight, eps, scale)`` = ``(q, scale, a)`` with
+  ``(q, scale) = rmsnorm_fp8_quant(...)`` and ``a = (q.to(float32) * scale).to(float16)``
+
 All
 run hand-written HIP kernels; a CPU tensor or a missing kernel library raises instead of
 falling back.
@@ -260,3 +265,27 @@ def _rmsnorm_fp8_quant_fake(
     if scale is None:
         return q, x.new_empty((*x.shape[:-1], 1), dtype=torch.float32)
     return q, torch.empty_like(scale)
+
+
+@torch.library.custom_op("tokenforge::rmsnorm_fp8_quant_dequant", mutates_args=())
+def rmsnorm_fp8_quant_dequant(
+    x: torch.Tensor, weight: torch.Tensor, eps: float, scale: torch.Tensor | None
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """``rmsnorm_fp8_quant`` plus ``(q.to(float32) * scale).to(float16)`` from one launch (no
+    counterpart in the reference): the fp16 activation of a W4A16 linear fed from the codes."""
+    h = x.shape[-1]
+    x2 = x.reshape(-1, h)
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    q, s, a = _rms.rmsnorm_fp8_quant_dequant(x2, weight, eps, scale)
+    if scale is not None:
+        s = s.clone()  # custom ops may not return an alias of an input
+    return q.reshape(x.shape), s.reshape((*x.shape[:-1], 1)) if scale is None else s, a.reshape(x.shape)
+
+
+@rmsnorm_fp8_quant_dequant.register_fake
+def _rmsnorm_fp8_quant_dequant_fake(
+    x: torch.Tensor, weight: torch.Tensor, eps: float, scale: torch.Tensor | None
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    q, s = _rmsnorm_fp8_quant_fake(x, weight, eps, scale)
+    return q, s, x.new_empty(x.shape, dtype=torch.float16)
