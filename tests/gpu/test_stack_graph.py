@@ -3,7 +3,8 @@ the eager pass bit for bit, with eager work on other inputs between replays (the
 reductions are fixed-order and no kernel depends on launch timing).
 
 Layers at the Qwen2.5-7B shapes (qkv 4608x3584 with bias, o_proj, gate_up 37888x3584, down
-3584x18944), RMSNorm + FP8 in front of qkv and gate_up, fp16(q * scale) as the linear input,
+3584x18944), RMSNorm + FP8 in front of qkv and gate_up, fp16(q * scale) as the linear input
+(the torch expression, or the norm's own fp16 output in the fused pass),
 attention as the identity on the value slice, SiLU(gate) * up, residual adds. Configs are
 the library defaults for each M (the GEMV, register-streamed and pipelined GEMM families).
 """
@@ -34,13 +35,23 @@ def _layers(device: torch.device, count: int) -> list:  # type: ignore[type-arg]
     return out
 
 
+def _norm_to_f16(x: torch.Tensor, gamma: torch.Tensor, fused: bool) -> torch.Tensor:
+    """RMSNorm + FP8, then the fp16 linear input fp16(q * scale): from the norm's own second
+    output (``fused``) or as the torch expression."""
+    ops = torch.ops.tokenforge
+    if fused:
+        return ops.rmsnorm_fp8_quant_dequant(x, gamma, 1e-6, None)[2]
+    q8, s = ops.rmsnorm_fp8_quant(x, gamma, 1e-6, None)
+    return (q8.to(torch.float32) * s).to(torch.float16)
+
+
 def _pass(x: torch.Tensor, layers: list, fused: bool = False) -> torch.Tensor:  # type: ignore[type-arg]
-    """One pass; ``fused`` runs the residual adds and SiLU*mul as linear epilogues."""
+    """One pass; ``fused`` runs the residual adds and SiLU*mul as linear epilogues and takes
+    the linear inputs from the norm's fp16 output."""
     ops = torch.ops.tokenforge
     m = x.shape[0]
     for (qkv, o, gu, down), bias, g1, g2 in layers:
-        q8, s = ops.rmsnorm_fp8_quant(x, g1, 1e-6, None)
-        a = (q8.to(torch.float32) * s).to(torch.float16)
+        a = _norm_to_f16(x, g1, fused)
         y = ops.w4a16_linear(a, *qkv, bias, G, "hip")
         v = y[:, QKV - 512:].reshape(m, 4, 1, 128)
         attn = v.expand(m, 4, 7, 128).reshape(m, H)
@@ -48,8 +59,7 @@ def _pass(x: torch.Tensor, layers: list, fused: bool = False) -> torch.Tensor:  
             x = ops.w4a16_linear_residual(attn, *o, None, x, G, "hip")
         else:
             x = x + ops.w4a16_linear(attn, *o, None, G, "hip")
-        q8, s = ops.rmsnorm_fp8_quant(x, g2, 1e-6, None)
-        a = (q8.to(torch.float32) * s).to(torch.float16)
+        a = _norm_to_f16(x, g2, fused)
         if fused:
             act = ops.w4a16_linear_silu_mul(a, *gu, None, G, "hip")
             x = ops.w4a16_linear_residual(act, *down, None, x, G, "hip")
@@ -69,7 +79,7 @@ def test_stack_replay_is_bit_identical_to_eager(m: int, fused: bool, device: tor
     other = torch.randn((m, H), generator=gen, device=device).to(torch.float16)
     eager = _pass(x, layers, fused)
     assert bool(torch.isfinite(eager).all())
-    if fused:  # the fused epilogues round exactly like the unfused torch glue
+    if fused:  # the fused epilogues and the norm's fp16 output round exactly like the torch glue
         assert torch.equal(eager, _pass(x, layers))
 
     stream = torch.cuda.Stream()
