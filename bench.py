@@ -32,6 +32,8 @@ Extra objects on the same JSON line:
   WRITE_DIR PROBE_LOG`` turns the two counter runs into that summary.
 * ``gemm_m256``: the prefill GEMM at M=256 on gate_up and down, TFLOP/s and fraction of the
   2.5 PFLOP/s fp16 dense MFMA peak.
+* ``device_copy_gbps``: the box's achievable bandwidth of a plain device copy (torch, 1 GiB
+  read and written), read + write bytes per second, next to the 8 TB/s peak.
 * ``per_shape`` and ``gemv_m2_m4``: the GEMV on each of the four shapes at
   M = 1, and at M = 2 and 4 (buckets 2 and 4 autotuned), average launch duration and GB/s.
 * ``rmsnorm_fp8``: the fused RMSNorm + e4m3fn quant (configs[1]: H=3584, eight outlier
@@ -86,6 +88,7 @@ SHAPES = [  # (layer, N, K)
 COLD_BYTES = 1.1e9
 TRAFFIC_SUMMARY = ROOT / "profiles" / "gemv_gate_up_m1_traffic.md"
 CALIB_BYTES = 256 << 20
+COPY_BYTES = 1 << 30
 
 
 def committed_traffic(cfg_dict: dict) -> float | None:  # type: ignore[type-arg]
@@ -553,6 +556,18 @@ def main() -> int:
 
     norm = rmsnorm_bench(dev)
 
+    # The box's achievable copy bandwidth (torch's device copy, 1 GiB in and out over 4 launches
+    # of 256 MiB), the yardstick next to the 8 TB/s HBM peak.
+    src = torch.empty(COPY_BYTES // 2, dtype=torch.float16, device=dev).normal_()
+    dst = torch.empty_like(src)
+    chunk = src.numel() // 4
+    g_copy, _ = capture([lambda i=i: dst[i * chunk:(i + 1) * chunk].copy_(src[i * chunk:(i + 1) * chunk])
+                         for i in range(4)], warm=1)
+    copy_ms = median_replay_ms(g_copy, 1)
+    copy_gbps = 2 * COPY_BYTES / (copy_ms * 1e-3) / 1e9
+    log(f"device copy: {copy_gbps:.0f} GB/s (read + write)")
+    del g_copy, src, dst
+
     sweep = None
     if args.full:
         sweep = []
@@ -639,6 +654,7 @@ def main() -> int:
         "gemm_m256": gemm,
         "rmsnorm_fp8": norm,
         "repack_gate_up_gbps": (gate_n * gate_k) / (rep_ms * 1e-3) / 1e9,
+        "device_copy_gbps": copy_gbps,
         "per_shape": per_shape,
         "gemv_m2_m4": gemv_m24,
         "stack": stack,
