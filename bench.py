@@ -87,8 +87,13 @@ SHAPES = [  # (layer, N, K)
 ]
 COLD_BYTES = 1.1e9
 TRAFFIC_SUMMARY = ROOT / "profiles" / "gemv_gate_up_m1_traffic.md"
+MFMA_SUMMARY = ROOT / "profiles" / "gemm_m256_mfma_busy.md"
+MFMA_COUNTERS = ("SQ_VALU_MFMA_BUSY_CYCLES", "GRBM_GUI_ACTIVE", "SQ_BUSY_CYCLES", "SQ_WAVES")
+NUM_SIMDS = 256 * 4
+NUM_XCDS = 8
 CALIB_BYTES = 256 << 20
 COPY_BYTES = 1 << 30
+MFMA_LAUNCHES = 8
 
 
 def committed_traffic(cfg_dict: dict) -> float | None:  # type: ignore[type-arg]
@@ -177,6 +182,81 @@ def traffic_summary(fetch_dir: str, write_dir: str, probe_log: str) -> int:
     lines += ["", "Machine-readable (bench.py reads the row of the config in use):", "", "```", *machine, "```", ""]
     TRAFFIC_SUMMARY.write_text("\n".join(lines))
     print(f"wrote {TRAFFIC_SUMMARY} ({len(probe['configs'])} configs)")
+    return 0
+
+
+def _probe_line(log: str, key: str) -> dict | None:  # type: ignore[type-arg]
+    for line in Path(log).read_text().splitlines():
+        if line.startswith('{"' + key + '"'):
+            return json.loads(line)[key]
+    return None
+
+
+def mfma_summary(pmc_dir: str, probe_log: str, timing_log: str) -> int:
+    """Write ``MFMA_SUMMARY`` from one ``rocprofv3 --pmc`` run of ``--mfma-probe`` (its log is
+    ``probe_log``) and one plain run of it (``timing_log``: the profiler slows graph replays, so
+    the event timing comes from a run without it): per GEMM launch, SQ_VALU_MFMA_BUSY_CYCLES
+    (summed over every SIMD) over the kernel's cycles (GRBM_GUI_ACTIVE, counted once per XCD)
+    times the SIMD count, next to the fraction of the 2.5 PFLOP/s fp16 dense peak."""
+    import csv
+    import glob
+
+    probe, timing = _probe_line(probe_log, "mfma_probe"), _probe_line(timing_log, "mfma_probe")
+    if probe is None or timing is None:
+        print(f"no mfma_probe line in {probe_log} or {timing_log}", file=sys.stderr)
+        return 1
+    if [r["config"] for r in probe["runs"]] != [r["config"] for r in timing["runs"]]:
+        raise ValueError("the counter run and the timing run used different configs")
+    per: dict = {}  # type: ignore[type-arg]
+    for f in glob.glob(f"{pmc_dir}/**/*counter_collection.csv", recursive=True):
+        for r in csv.DictReader(open(f)):
+            if "gemm" in r["Kernel_Name"] and "reduce" not in r["Kernel_Name"]:
+                per.setdefault(int(r["Dispatch_Id"]), {})[r["Counter_Name"]] = float(r["Counter_Value"])
+    ids = sorted(per)
+    n_launch = probe["launches"]
+    # The probe's eager launches come first (layer by layer); later GEMM dispatches belong to
+    # its graph timing.
+    if len(ids) < n_launch * len(probe["runs"]):
+        raise ValueError(f"{pmc_dir}: {len(ids)} GEMM dispatches, expected >= {n_launch * len(probe['runs'])}")
+    ids = ids[: n_launch * len(probe["runs"])]
+    lines = [
+        "# MFMA utilisation of the prefill GEMM at M=256 (gate_up and down, tuned configs)",
+        "",
+        "Commands (on the MI355X box, after `bench.py` filled the autotune cache):",
+        "",
+        "```",
+        "cd /tmp && export TMPDIR=/tmp && R=<repo root>",
+        f"timeout -s KILL 150 rocprofv3 --pmc {' '.join(MFMA_COUNTERS)} --output-format csv \\",
+        "    -d $R/gpurun_out/pmc_mfma -- python $R/bench.py --mfma-probe > $R/gpurun_out/pmc_mfma.log",
+        "python $R/bench.py --mfma-probe > $R/gpurun_out/mfma_timing.log",
+        "python $R/bench.py --mfma-summary $R/gpurun_out/pmc_mfma $R/gpurun_out/pmc_mfma.log \\",
+        "    $R/gpurun_out/mfma_timing.log",
+        "```",
+        "",
+        f"`--mfma-probe` launches each layer's tuned M=256 GEMM {n_launch} times over rotating cold",
+        "weight copies (counters, eager) and times the same launches from a HIP graph (events, taken",
+        "from the run without the profiler).",
+        f"MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / {NUM_XCDS} XCDs x {NUM_SIMDS} SIMDs): the",
+        "share of the kernel's cycles in which an average SIMD's matrix core is busy. The split-K",
+        "reduce kernel of down runs no MFMA and is not counted. Rows: mean over the launches.",
+        "",
+        "| layer | config | MFMA busy (counters) | us / launch (events) | TFLOP/s | of 2.5 PF |",
+        "|---|---|---:|---:|---:|---:|",
+    ]
+    for j, run in enumerate(timing["runs"]):
+        vals = [per[d] for d in ids[j * n_launch:(j + 1) * n_launch]]
+        busy = statistics.mean(v["SQ_VALU_MFMA_BUSY_CYCLES"] / (v["GRBM_GUI_ACTIVE"] / NUM_XCDS * NUM_SIMDS) for v in vals)
+        c = run["config"]
+        name = f"{c['kernel']} bm{c['block_m']} bn{c['block_n']} bk{c['block_k']} sk{c['split_k']} w{c['num_warps']} st{c['num_stages']}"
+        lines.append(f"| {run['layer']} | {name} | {100 * busy:.1f}% | {run['us']:.2f} | {run['tflops']:.1f} | "
+                     f"{100 * run['tflops'] / FP16_MFMA_PEAK_TFLOPS:.1f}% |")
+    lines += ["", "Raw counters per launch (mean):", "", "| layer | " + " | ".join(MFMA_COUNTERS) + " |",
+              "|---|" + "---:|" * len(MFMA_COUNTERS)]
+    for j, run in enumerate(probe["runs"]):
+        vals = [per[d] for d in ids[j * n_launch:(j + 1) * n_launch]]
+        lines.append(f"| {run['layer']} | " + " | ".join(f"{statistics.mean(v[c] for v in vals):.0f}" for c in MFMA_COUNTERS) + " |")
+    MFMA_SUMMARY.write_text("\n".join(lines) + "\n")
+    print(f"wrote {MFMA_SUMMARY}")
     return 0
 
 
@@ -421,9 +501,16 @@ def main() -> int:
                     help="eager gate_up GEMV launches + a calibration kernel, for rocprofv3 --pmc")
     ap.add_argument("--traffic-summary", nargs=3, metavar=("FETCH_DIR", "WRITE_DIR", "PROBE_LOG"),
                     help="write the committed traffic summary from two --traffic-probe counter runs")
+    ap.add_argument("--mfma-probe", action="store_true",
+                    help="eager + graph-timed launches of the tuned M=256 GEMMs, for rocprofv3 --pmc")
+    ap.add_argument("--mfma-summary", nargs=3, metavar=("PMC_DIR", "PROBE_LOG", "TIMING_LOG"),
+                    help="write the committed MFMA-utilisation summary from a --mfma-probe counter run "
+                         "and a plain --mfma-probe run")
     args = ap.parse_args()
     if args.traffic_summary:
         return traffic_summary(*args.traffic_summary)
+    if args.mfma_summary:
+        return mfma_summary(*args.mfma_summary)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(
             "bench.py measures one GPU: this build's hot path is single-GPU (no collectives); "
@@ -460,7 +547,7 @@ def main() -> int:
     torch.cuda.synchronize()
     log(f"setup: {copies} layer copies ({copies * step_bytes / 1e9:.2f} GB) in {time.perf_counter() - t0:.1f}s")
 
-    if not args.no_tune and not args.traffic_probe:  # the probe runs every candidate
+    if not args.no_tune and not args.traffic_probe and not args.mfma_probe:  # probes use the cache
         t0 = time.perf_counter()
         for _, n, k in SHAPES:
             buckets = (1, 2, 4, 256) if n in (37888,) or k == 18944 else (1, 2, 4)
@@ -499,6 +586,28 @@ def main() -> int:
         qw, s, z = layers[c][i]
         x, cfg = m_x[i], cfgs[i]
         return lambda: w4a16_gemm(x, qw, s, z, GROUP, cfg)
+
+    if args.mfma_probe:
+        # First the eager launches the counters see (each layer's in turn), then the graph
+        # timing of the same launches (its dispatches come after and are not counted).
+        cfgs = {i: autotune.lookup(gpu, 256, SHAPES[i][1], SHAPES[i][2], GROUP) for i in (2, 3)}
+        xms = {}
+        for i in (2, 3):
+            xms[i] = [None] * len(SHAPES)
+            xms[i][i] = torch.randn((256, SHAPES[i][2]), generator=gen, device=dev).to(torch.float16)
+            for c in range(MFMA_LAUNCHES):
+                launcher(c % copies, i, xms[i], [cfgs[i]] * len(SHAPES))()
+        torch.cuda.synchronize()
+        runs = []
+        for i in (2, 3):
+            name, n, k = SHAPES[i]
+            g, _ = capture([launcher(r % copies, i, xms[i], [cfgs[i]] * len(SHAPES)) for r in range(2 * copies)])
+            ms = median_replay_ms(g, 2 * copies)
+            runs.append({"layer": name, "m": 256, "n": n, "k": k, "config": cfgs[i].to_dict(), "us": ms * 1e3,
+                         "tflops": 2 * 256 * n * k / (ms * 1e-3) / 1e12})
+            del g
+        print(json.dumps({"mfma_probe": {"launches": MFMA_LAUNCHES, "runs": runs}}), flush=True)
+        return 0
 
     def steps(count: int, offset: int = 0) -> list:  # type: ignore[type-arg]
         fns = []

@@ -82,3 +82,42 @@ def test_committed_summary_parses() -> None:
         value, cfg = ln[len("traffic: "):].split(" ", 1)
         assert float(value) > 0
         assert bench.committed_traffic(json.loads(cfg)) == float(value)
+
+
+def test_mfma_summary_from_synthetic_counters(tmp_path: Path, monkeypatch: pytest.MonkeyPatch) -> None:
+    """--mfma-summary: the first `launches` GEMM dispatches per layer (in dispatch order) are the
+    counted ones; busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / XCDs * SIMDs)."""
+    monkeypatch.setattr(bench, "MFMA_SUMMARY", tmp_path / "mfma.md")
+    d = tmp_path / "pmc"
+    d.mkdir()
+    rows = []
+    did = 1
+    cycles = 200_000.0  # per XCD
+    for layer_busy in (0.30, 0.20):
+        for _ in range(bench.MFMA_LAUNCHES):
+            for c in bench.MFMA_COUNTERS:
+                v = {"SQ_VALU_MFMA_BUSY_CYCLES": layer_busy * cycles * bench.NUM_SIMDS,
+                     "GRBM_GUI_ACTIVE": cycles * bench.NUM_XCDS}.get(c, 1.0)
+                rows.append({"Dispatch_Id": did, "Kernel_Name": "void tf::gemm2_kernel<256, 192, 4, 2, 3>(...)",
+                             "Counter_Name": c, "Counter_Value": v})
+            did += 1
+    for c in bench.MFMA_COUNTERS:  # a reduce kernel and a later (graph-timing) dispatch: ignored
+        rows.append({"Dispatch_Id": did, "Kernel_Name": "void tf::splitk_reduce_kernel(...)",
+                     "Counter_Name": c, "Counter_Value": 5.0})
+        rows.append({"Dispatch_Id": did + 1, "Kernel_Name": "void tf::gemm2_kernel<256, 192, 4, 2, 3>(...)",
+                     "Counter_Name": c, "Counter_Value": 9.0})
+    rows.reverse()
+    with open(d / "pmc_counter_collection.csv", "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=list(rows[0]))
+        w.writeheader()
+        w.writerows(rows)
+    cfg = {"kernel": "gemm_mfma", "block_m": 256, "block_n": 192, "block_k": 64, "split_k": 1, "num_warps": 8,
+           "num_stages": 3}
+    runs = [{"layer": "gate_up_proj", "m": 256, "n": 37888, "k": 3584, "config": cfg, "us": 100.0, "tflops": 700.0},
+            {"layer": "down_proj", "m": 256, "n": 3584, "k": 18944, "config": cfg, "us": 60.0, "tflops": 580.0}]
+    log = tmp_path / "probe.log"
+    log.write_text(json.dumps({"mfma_probe": {"launches": bench.MFMA_LAUNCHES, "runs": runs}}) + "\n")
+    assert bench.mfma_summary(str(d), str(log), str(log)) == 0
+    text = (tmp_path / "mfma.md").read_text()
+    assert "| gate_up_proj | gemm_mfma bm256 bn192 bk64 sk1 w8 st3 | 30.0% | 100.00 | 700.0 | 28.0% |" in text
+    assert "| down_proj | gemm_mfma bm256 bn192 bk64 sk1 w8 st3 | 20.0% |" in text
