@@ -88,6 +88,7 @@ SHAPES = [  # (layer, N, K)
 COLD_BYTES = 1.1e9
 TRAFFIC_SUMMARY = ROOT / "profiles" / "gemv_gate_up_m1_traffic.md"
 MFMA_SUMMARY = ROOT / "profiles" / "gemm_m256_mfma_busy.md"
+STATS_SUMMARY = ROOT / "profiles" / "bench_decode_m1_kernel_stats.md"
 MFMA_COUNTERS = ("SQ_VALU_MFMA_BUSY_CYCLES", "GRBM_GUI_ACTIVE", "SQ_BUSY_CYCLES", "SQ_WAVES")
 NUM_SIMDS = 256 * 4
 NUM_XCDS = 8
@@ -182,6 +183,146 @@ def traffic_summary(fetch_dir: str, write_dir: str, probe_log: str) -> int:
     lines += ["", "Machine-readable (bench.py reads the row of the config in use):", "", "```", *machine, "```", ""]
     TRAFFIC_SUMMARY.write_text("\n".join(lines))
     print(f"wrote {TRAFFIC_SUMMARY} ({len(probe['configs'])} configs)")
+    return 0
+
+
+def stats_summary(prof_dir: str, bench_log: str) -> int:
+    """Write ``STATS_SUMMARY`` from a ``rocprofv3 --kernel-trace --stats`` run of bench.py
+    (``prof_dir``) and the JSON line of the bench run before it (``bench_log``): the kernel
+    table, the event-timed per-shape averages and, per shape and M, the rocprofv3 average of
+    the tuned kernel instance next to the event-timed one."""
+    import csv
+    import glob
+
+    bench = None
+    for line in Path(bench_log).read_text().splitlines():
+        if line.startswith("{") and '"metric"' in line:
+            bench = json.loads(line)
+    if bench is None:
+        print(f"no bench JSON line in {bench_log}", file=sys.stderr)
+        return 1
+    PRE = "cd /tmp && export TMPDIR=/tmp && R=<repo root>"
+    BENCH_CMD = "python $R/bench.py --steps 100 --warmup 10 > $R/gpurun_out/bench.log   # tunes the cache"
+    # ---------------------------------------------------------------- kernel stats
+    f = glob.glob(f"{prof_dir}/**/*_kernel_stats.csv", recursive=True)[0]
+    rows = list(csv.DictReader(open(f)))
+    lines = [
+        "# Kernel statistics: decode step at M=1 + prefill GEMM at M=256 (bench.py)",
+        "",
+        "Command (on the MI355X box, after the bench command below filled the autotune cache):",
+        "",
+        "```",
+        PRE,
+        BENCH_CMD,
+        "rocprofv3 --kernel-trace --stats --output-format csv -d $R/gpurun_out/prof_bench -- \\",
+        "    python $R/bench.py --steps 20 --warmup 5 --no-cpu --no-tune --no-stack",
+        "python $R/bench.py --stats-summary $R/gpurun_out/prof_bench $R/gpurun_out/bench.log",
+        "```",
+        "",
+        "`*_kernel_stats.csv`, kernels of this library plus the largest setup kernels (torch RNG,",
+        "fills). The GEMV rows are the four decode shapes at M = 1 (graph replays, the per-shape",
+        "timing graphs and the warmup) and the M = 2 and 4 timing graphs; the gemm rows are the",
+        "M=256 prefill timing.",
+        "",
+        "| kernel | calls | avg us | min us | max us | % time |",
+        "|---|---:|---:|---:|---:|---:|",
+    ]
+    for r in rows[:16]:
+        name = r["Name"].replace("(anonymous namespace)::", "")
+        name = name.split("(tf::")[0].split("(unsigned")[0].split("(int")[0].split("(float")[0].replace("void ", "")
+        if len(name) > 90:
+            name = name[:90] + "..."
+        lines.append(f"| `{name}` | {r['Calls']} | {float(r['AverageNs'])/1e3:.2f} | {float(r['MinNs'])/1e3:.2f} | "
+                     f"{float(r['MaxNs'])/1e3:.2f} | {float(r['Percentage']):.1f} |")
+    ps = {p["layer"]: p for p in bench["per_shape"]}
+    lines += [
+        "",
+        "Event-timed averages from the bench run before it (HIP events around graph replays on the",
+        "launch stream, `per_shape` and `gemm_m256` of the bench JSON line):",
+        "",
+        "| shape | config | event-timed avg us |",
+        "|---|---|---:|",
+    ]
+    for p in bench["per_shape"]:
+        c = p["config"]
+        lines.append(f"| {p['layer']} M=1 | {c['kernel']} bm{c['block_m']} bn{c['block_n']} bk{c['block_k']} "
+                     f"w{c['num_warps']} st{c['num_stages']} | {p['us']:.2f} |")
+    for g in bench["gemm_m256"]:
+        c = g["config"]
+        lines.append(f"| {g['layer']} M=256 | {c['kernel']} bm{c['block_m']} bn{c['block_n']} bk{c['block_k']} "
+                     f"sk{c['split_k']} | {g['us']:.2f} |")
+    # Per-shape averages from the per-dispatch trace: a GEMV launch of shape (N, K) with config
+    # block_n, num_warps has grid (ceil(N / block_n) * 64 * num_warps) threads in x.
+    tr = glob.glob(f"{prof_dir}/**/*_kernel_trace.csv", recursive=True)[0]
+    disp = list(csv.DictReader(open(tr)))
+    shapes = {"qkv_proj": (4608, 3584), "o_proj": (3584, 3584), "gate_up_proj": (37888, 3584), "down_proj": (3584, 18944)}
+    lines += ["", "Per-shape rocprofv3 averages (dispatches of the tuned kernel instance with the shape's grid,",
+              "from `*_kernel_trace.csv`) next to the event-timed averages (`per_shape`, and",
+              "`gemv_m2_m4` for M = 2 and 4). Where one kernel instance and grid serve several rows,",
+              "dispatches of different M are told apart by bench phase (M = 1, 2, 4 run one after the",
+              "other; a phase starts at the first dispatch of an instance only that M uses), and shapes",
+              "of the same M (o_proj and down can coincide) by duration, split at the midpoint of the",
+              "two event-timed averages.", "",
+              "| shape | kernel instance | grid (threads) | dispatches | rocprofv3 avg us | event-timed avg us |",
+              "|---|---|---:|---:|---:|---:|"]
+    def grid_of(c, n):
+        tiles = -(-n // c["block_n"])
+        if c["block_k"] == 256:  # waves over row tiles: one workgroup per num_warps tiles
+            tiles = -(-tiles // c["num_warps"])
+        return tiles * 64 * c["num_warps"]
+    def instance(c):
+        """(name prefix, name suffix) of the template instance a GEMV config runs (K % 128 == 0)."""
+        splitn = "true" if c["block_k"] == 256 else "false"
+        if c["kernel"] == "gemv_dot":
+            return f"gemv_dot_kernel<{c['block_m']}, {c['block_n'] // 16}, {c['num_stages']}, ", f", true, {splitn}>"
+        xlds = "false" if c["block_k"] == 64 else "true"
+        return (f"gemv_mfma_kernel<{c['block_m'] // 16}, {c['block_n'] // 16}, {c['num_stages']}, ",
+                f", {xlds}, true, {splitn}>")
+    groups = {}
+    for p_ in bench["per_shape"] + bench.get("gemv_m2_m4", []):
+        c = p_["config"]
+        n, k = shapes[p_["layer"]]
+        key = (instance(c), grid_of(c, n), 64 * c["num_warps"])
+        groups.setdefault(key, []).append(p_)
+    rows_out = []
+    def dispatches(pre, suf, grid, wg):
+        return sorted(((int(d["Start_Timestamp"]), (int(d["End_Timestamp"]) - int(d["Start_Timestamp"])) / 1e3) for d in disp
+                       if pre in d["Kernel_Name"] and (suf + "(") in d["Kernel_Name"].replace("> (", ">(")
+                       and int(d["Grid_Size_X"]) == grid and int(d["Workgroup_Size_X"]) == wg))
+    # The bench measures M = 1, then 2, then 4: a phase starts at the first dispatch of any kernel
+    # instance that only that M uses.
+    phase_start = {}
+    for ((pre, suf), grid, wg), members in groups.items():
+        ms = {q["m"] for q in members}
+        ds = dispatches(pre, suf, grid, wg)
+        if len(ms) == 1 and ds:
+            m = ms.pop()
+            phase_start[m] = min(phase_start.get(m, ds[0][0]), ds[0][0])
+    for ((pre, suf), grid, wg), members in groups.items():
+        ds = dispatches(pre, suf, grid, wg)
+        ms = sorted({q["m"] for q in members})
+        segments = {m: [] for m in ms}
+        for t, dur in ds:
+            started = [m for m in ms if phase_start.get(m, float("inf")) <= t]
+            segments[max(started) if started else ms[0]].append(dur)
+        for m, seg in segments.items():
+            durs = sorted(seg)
+            mem = sorted((q for q in members if q["m"] == m), key=lambda q: q["us"])
+            # Same M, same instance and grid (o_proj and down can): split at the midpoint of the
+            # two event-timed averages.
+            cuts = [(a["us"] + b["us"]) / 2 for a, b in zip(mem, mem[1:])] + [float("inf")]
+            lo = float("-inf")
+            for p_, hi in zip(mem, cuts):
+                part = [d for d in durs if lo < d <= hi]
+                lo = hi
+                if part:
+                    inst = pre + "…" + suf
+                    rows_out.append((p_["m"], list(shapes).index(p_["layer"]),
+                                     f"| {p_['layer']} M={p_['m']} | `{inst}` | {grid} | {len(part)} | "
+                                     f"{sum(part) / len(part):.2f} | {p_['us']:.2f} |"))
+    lines += [r[2] for r in sorted(rows_out)]
+    STATS_SUMMARY.write_text("\n".join(lines) + "\n")
+    print(f"wrote {STATS_SUMMARY}")
     return 0
 
 
@@ -506,7 +647,11 @@ def main() -> int:
     ap.add_argument("--mfma-summary", nargs=3, metavar=("PMC_DIR", "PROBE_LOG", "TIMING_LOG"),
                     help="write the committed MFMA-utilisation summary from a --mfma-probe counter run "
                          "and a plain --mfma-probe run")
+    ap.add_argument("--stats-summary", nargs=2, metavar=("PROF_DIR", "BENCH_LOG"),
+                    help="write the committed kernel-statistics summary from a rocprofv3 kernel-trace run")
     args = ap.parse_args()
+    if args.stats_summary:
+        return stats_summary(*args.stats_summary)
     if args.traffic_summary:
         return traffic_summary(*args.traffic_summary)
     if args.mfma_summary:

@@ -121,3 +121,53 @@ def test_mfma_summary_from_synthetic_counters(tmp_path: Path, monkeypatch: pytes
     text = (tmp_path / "mfma.md").read_text()
     assert "| gate_up_proj | gemm_mfma bm256 bn192 bk64 sk1 w8 st3 | 30.0% | 100.00 | 700.0 | 28.0% |" in text
     assert "| down_proj | gemm_mfma bm256 bn192 bk64 sk1 w8 st3 | 20.0% |" in text
+
+
+def test_stats_summary_matches_dispatches_to_shapes(tmp_path: Path, monkeypatch: pytest.MonkeyPatch) -> None:
+    """--stats-summary: per shape and M, the rocprofv3 rows are the dispatches of the tuned
+    kernel instance with the shape's grid; different M sharing an instance split by phase."""
+    monkeypatch.setattr(bench, "STATS_SUMMARY", tmp_path / "stats.md")
+    d = tmp_path / "prof" / "vm"
+    d.mkdir(parents=True)
+    with open(d / "1_kernel_stats.csv", "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=["Name", "Calls", "AverageNs", "MinNs", "MaxNs", "Percentage"])
+        w.writeheader()
+        w.writerow({"Name": "void tf::(anonymous namespace)::gemv_dot_kernel<1, 1, 4, 8, true, true>(tf::LinearArgs, int)",
+                    "Calls": 3, "AverageNs": 20000, "MinNs": 19000, "MaxNs": 21000, "Percentage": 50.0})
+    dot = {"kernel": "gemv_dot", "block_m": 1, "block_n": 16, "block_k": 256, "split_k": 1, "num_warps": 4, "num_stages": 4}
+    mfma = {"kernel": "gemv_mfma", "block_m": 16, "block_n": 16, "block_k": 256, "split_k": 1, "num_warps": 4,
+            "num_stages": 2}
+    grid = -(-(-(-37888 // 16)) // 4) * 64 * 4
+    trace = []
+    t = 0
+    for name, dur, n in (("gemv_dot_kernel<1, 1, 4, 8, true, true>", 20_000, 3),
+                         ("gemv_mfma_kernel<1, 1, 2, 8, true, true, true>", 21_000, 2),   # M = 2
+                         ("gemv_dot_kernel<2, 1, 2, 16, true, false>", 5_000, 1),          # M = 2, only M = 2 uses it
+                         ("gemv_mfma_kernel<1, 2, 2, 16, false, true, false>", 7_000, 1),  # M = 4, only M = 4
+                         ("gemv_mfma_kernel<1, 1, 2, 8, true, true, true>", 23_000, 2)):  # M = 4
+        for _ in range(n):
+            g, wg = (229376, 1024) if "<2, 1, 2, 16" in name else (36864, 256) if "<1, 2, 2" in name else (grid, 256)
+            trace.append({"Kernel_Name": f"void tf::(anonymous namespace)::{name}(tf::LinearArgs, int)",
+                          "Start_Timestamp": t, "End_Timestamp": t + dur, "Grid_Size_X": g,
+                          "Workgroup_Size_X": wg})
+            t += dur + 1000
+    with open(d / "1_kernel_trace.csv", "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=list(trace[0]))
+        w.writeheader()
+        w.writerows(trace)
+    o2 = {"kernel": "gemv_dot", "block_m": 2, "block_n": 16, "block_k": 128, "split_k": 1, "num_warps": 16,
+          "num_stages": 2}
+    line = {"metric": "m", "per_shape": [{"layer": "gate_up_proj", "m": 1, "us": 20.5, "config": dot}],
+            "gemv_m2_m4": [{"layer": "gate_up_proj", "m": 2, "us": 21.2, "config": mfma},
+                           {"layer": "o_proj", "m": 2, "us": 5.1, "config": o2},
+                           {"layer": "qkv_proj", "m": 4, "us": 7.2,
+                            "config": dict(mfma, block_n=32, block_k=64, num_warps=4)},
+                           {"layer": "gate_up_proj", "m": 4, "us": 22.9, "config": mfma}],
+            "gemm_m256": []}
+    log = tmp_path / "bench.log"
+    log.write_text("noise\n" + json.dumps(line) + "\n")
+    assert bench.stats_summary(str(tmp_path / "prof"), str(log)) == 0
+    text = (tmp_path / "stats.md").read_text()
+    assert "| gate_up_proj M=1 | `gemv_dot_kernel<1, 1, 4, …, true, true>` | 151552 | 3 | 20.00 | 20.50 |" in text
+    assert "| gate_up_proj M=2 | `gemv_mfma_kernel<1, 1, 2, …, true, true, true>` | 151552 | 2 | 21.00 | 21.20 |" in text
+    assert "| gate_up_proj M=4 | `gemv_mfma_kernel<1, 1, 2, …, true, true, true>` | 151552 | 2 | 23.00 | 22.90 |" in text
