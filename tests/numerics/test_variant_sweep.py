@@ -4,7 +4,9 @@ The code-path tests pick representative configs; this sweep runs all of ``VARIAN
 library's table) once each, with the shape, group size, M, split_k, bias and epilogue drawn
 from a generator seeded by the variant's index, against the fp64 oracle with the derived
 tolerance and the normwise bound (and the fused epilogues against their unfused torch expressions, bit for bit).
-N is sometimes ragged against the tile; K sometimes ends in a partial 128-wide step.
+N is sometimes ragged against the tile; K sometimes ends in a partial 128-wide step. The
+W4A8 form of every variant (x as e4m3fn codes, decoded while staging or into the workspace)
+must equal the W4A16 result on the decoded x bit for bit when the row scale is 1.
 """
 
 from __future__ import annotations
@@ -17,7 +19,7 @@ import torch
 from tests.numerics import cases
 from tests.numerics.test_w4a16 import _assert_close
 from tokenforge_amd.kernels.config import VARIANTS, GemmConfig
-from tokenforge_amd.kernels.hip.w4a16 import w4a16_gemm, w4a16_gemm_ex
+from tokenforge_amd.kernels.hip.w4a16 import w4a8_gemm_ex, w4a16_gemm, w4a16_gemm_ex
 
 pytestmark = pytest.mark.gpu
 
@@ -70,3 +72,24 @@ def test_every_variant(index: int, device: torch.device) -> None:
         r = cases.activations(m, n, c["seed"] + 1).to(device)
         fused = w4a16_gemm_ex(xd, wd.qweight_t, wd.scales, wd.qzeros, g, cfg, bd, "residual", r)
         assert torch.equal(fused, r + y), str(cfg)
+
+
+@pytest.mark.parametrize("index", range(len(VARIANTS)))
+def test_every_variant_w4a8_unit_scale(index: int, device: torch.device) -> None:
+    c = _case(index, VARIANTS[index])
+    cfg, g, k, n, m = c["cfg"], c["group"], c["k"], c["n"], c["m"]
+    wd = cases.on_device(cases.layer_weights(n, k, c["seed"], g), device)
+    b = cases.bias(n, c["seed"]).to(device) if c["bias"] else None
+    gen = torch.Generator().manual_seed(5000 + index)
+    codes = torch.randint(0, 256, (m, k), generator=gen, dtype=torch.uint8)
+    codes[(codes & 0x7F) == 0x7F] = 0x38  # no NaN codes
+    x8 = codes.to(device).view(torch.float8_e4m3fn)
+    one = torch.ones(1, dtype=torch.float32, device=device)
+    print(f"variant {index}: {cfg} k={k} n={n} m={m} g={g} (w4a8)", flush=True)
+    try:
+        y8 = w4a8_gemm_ex(x8, one, wd.qweight_t, wd.scales, wd.qzeros, g, cfg, b)
+    except ValueError as e:
+        assert "fit" in str(e), f"{cfg} k={k} n={n} m={m} g={g}: {e}"
+        return
+    y16 = w4a16_gemm(x8.to(torch.float16), wd.qweight_t, wd.scales, wd.qzeros, g, cfg, b)
+    assert torch.equal(y8, y16), f"{cfg} k={k} n={n} m={m} g={g}"
