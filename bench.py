@@ -1,8 +1,12 @@
-"""Benchmark of the MI355X quantized-linear hot path (the round driver's bench contract).
+"""Benchmark of the MI355X quantized-linear hot path (one JSON result line on stdout).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-tune] [--no-cpu] [--detail PATH] [--full]
                     [--stack | --no-stack]
     python bench.py --traffic-probe      (eager launches for rocprofv3 --pmc, see below)
+    python bench.py --mfma-probe         (the tuned M=256 GEMMs, for rocprofv3 --pmc)
+    python bench.py --traffic-summary FETCH_DIR WRITE_DIR PROBE_LOG   (write the profiles/ summaries
+    python bench.py --mfma-summary PMC_DIR PROBE_LOG TIMING_LOG        from the profiler's output)
+    python bench.py --stats-summary PROF_DIR BENCH_LOG
 
 Workload (BASELINE.json metric "W4A16 GEMV HBM GB/s at M=1 + GEMM TFLOP/s at M=256"):
 one step is one decode pass at M=1 through the four Qwen2.5-7B decoder linears (qkv
