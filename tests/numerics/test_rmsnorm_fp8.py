@@ -232,6 +232,20 @@ def test_dequantized_output_of_special_rows(device: torch.device) -> None:
     _assert_f16_match_nan_aware(a.reshape(6, h), (q0.to(torch.float32) * s0).to(torch.float16))
 
 
+@pytest.mark.parametrize("static", [False, True])
+def test_zero_tokens(static: bool, device: torch.device) -> None:
+    """T = 0: empty codes and fp16 output, no launch; the dynamic scale is [0, 1], a static
+    scale comes back as given."""
+    x = torch.empty((0, 896), dtype=torch.float16, device=device)
+    w = torch.ones(896, dtype=torch.float16, device=device)
+    sc = torch.full((1,), 0.25, device=device) if static else None
+    q, s, a = rmsnorm_fp8_quant_dequant(x, w, EPS, sc)
+    assert q.shape == a.shape == (0, 896) and q.dtype == torch.float8_e4m3fn and a.dtype == torch.float16
+    assert s.shape == ((1,) if static else (0, 1))
+    q, s, a = torch.ops.tokenforge.rmsnorm_fp8_quant_dequant(x.reshape(0, 1, 896), w, EPS, sc)
+    assert q.shape == a.shape == (0, 1, 896)
+
+
 def test_zero_row_uses_min_scale(device: torch.device) -> None:
     x = torch.zeros((2, 256), dtype=torch.float16)
     w = torch.ones(256, dtype=torch.float16)
