@@ -4,6 +4,7 @@
                     [--stack | --no-stack]
     python bench.py --traffic-probe      (eager launches for rocprofv3 --pmc, see below)
     python bench.py --mfma-probe         (the tuned M=256 GEMMs, for rocprofv3 --pmc)
+    python bench.py --probe              (memory floors of the GEMV's access patterns)
     python bench.py --traffic-summary FETCH_DIR WRITE_DIR PROBE_LOG   (write the profiles/ summaries
     python bench.py --mfma-summary PMC_DIR PROBE_LOG TIMING_LOG        from the profiler's output)
     python bench.py --stats-summary PROF_DIR BENCH_LOG
@@ -416,7 +417,7 @@ def log(msg: str) -> None:
 
 def make_layer(n: int, k: int, dev: torch.device, seed: int):  # type: ignore[no-untyped-def]
     """AWQ-format synthetic layer converted with the GPU repack -> (qweight_t, scales, qzeros)."""
-    from tokenforge_amd.kernels.pack import pack_awq, pack_int4
+    from tokenforge.kernels.pack import pack_awq, pack_int4
 
     gen = torch.Generator(device=dev).manual_seed(seed)
     intweight = torch.randint(0, 16, (k, n), generator=gen, device=dev, dtype=torch.int32)
@@ -466,7 +467,7 @@ def time_graph(graph: torch.cuda.CUDAGraph, reps: int = 1) -> float:
 
 def rmsnorm_bench(dev: torch.device) -> list[dict]:  # type: ignore[type-arg]
     """fused RMSNorm + FP8 at H=3584 over rotating cold inputs, per T."""
-    from tokenforge_amd.kernels.hip.rmsnorm_fp8 import rmsnorm_fp8_quant
+    from tokenforge.kernels.hip.rmsnorm_fp8 import rmsnorm_fp8_quant
 
     h = 3584
     gen = torch.Generator(device="cpu").manual_seed(0)
@@ -500,7 +501,7 @@ def stack_bench(dev: torch.device, gpu: str, ms: tuple[int, ...], tune: bool) ->
     """configs[4]: tokens/s of one pass through 28 decoder layers, per M (module docstring);
     each M timed with the unfused torch glue, with the fused epilogues (residual adds in
     o_proj and down, SiLU*mul in gate_up; same bits) and with W4A8 qkv and gate_up."""
-    from tokenforge_amd.kernels import autotune
+    from tokenforge.kernels import autotune
 
     eps = 1e-6
     h = SHAPES[1][1]
@@ -629,6 +630,68 @@ def cpu_baseline(layers: list, budget_s: float = 12.0) -> dict:  # type: ignore[
     }
 
 
+def read_probes(dev: torch.device, layers: list, copies: int, xs: list, cfgs: list) -> int:  # type: ignore[type-arg]
+    """--probe: pure-read kernels with the decode GEMV's grid and access patterns (no arithmetic)
+    on the same rotating cold copies, against the GEMV itself, plus the fixed cost of a launch.
+    Prints a table to stderr and one JSON line {"read_probe": ...} to stdout."""
+    import ctypes
+
+    from tokenforge.kernels.hip.w4a16 import w4a16_gemm
+
+    plib = ctypes.CDLL(str(ROOT / "tokenforge_amd" / "lib" / "libtokenforge_probes.so"))
+    p_, i64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32
+    plib.tfp_read.argtypes = [i32, p_, p_, p_, i64, i64, i32, i32, p_, p_]
+    plib.tfp_out_words.argtypes = [i64, i32]
+    plib.tfp_out_words.restype = i64
+    plib.tfp_empty.argtypes = [i32, p_]
+    stream = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+    rows = []
+
+    for grid in (256, 2368):
+        g, _ = capture([lambda grid=grid: plib.tfp_empty(grid, stream())] * 200)
+        us = median_replay_ms(g, 200) * 1e3
+        rows.append({"probe": "empty", "grid": grid, "us": us})
+        log(f"  empty kernel grid {grid:5d}: {us:.2f} us per launch")
+        del g
+    names = {0: "tile", 1: "tile+meta", 2: "rows", 3: "stream"}
+    for i, (name, n, k) in enumerate(SHAPES):
+        weight_bytes = n * k // 2
+        meta_bytes = (k // GROUP) * n * 2 + (k // GROUP) * n // 2
+        x, cfg = xs[i], cfgs[i]
+        g, _ = capture([lambda c=c: w4a16_gemm(x, *layers[c][i], GROUP, cfg) for c in range(copies)])
+        us = median_replay_ms(g, copies) * 1e3
+        rows.append({"probe": "gemv", "layer": name, "n": n, "k": k, "config": cfg.to_dict(), "us": us,
+                     "gbps": bytes_moved(1, n, k) / us / 1e3})
+        log(f"  {name:13s} GEMV {cfg.kernel} bn{cfg.block_n} bk{cfg.block_k} w{cfg.num_warps} "
+            f"st{cfg.num_stages}: {us:6.2f} us {bytes_moved(1, n, k) / us / 1e3:6.0f} GB/s")
+        del g
+        best: dict[int, tuple[float, int, int]] = {}
+        for pattern in (0, 1, 2, 3):
+            combos = [(w, d) for w in (1, 2, 4, 8, 16) for d in (2, 4, 8)] if pattern < 3 else \
+                [(g_, 0) for g_ in (512, 1024, 2048, 4096)]
+            for waves, depth in combos:
+                words = plib.tfp_out_words(n, waves) if pattern < 3 else waves * 256
+                out = torch.empty(words, dtype=torch.int32, device=dev)
+                fns = [lambda c=c, waves=waves, depth=depth, pattern=pattern, out=out: plib.tfp_read(
+                    pattern, layers[c][i][0].data_ptr(), layers[c][i][1].data_ptr(), layers[c][i][2].data_ptr(),
+                    n, k, waves, depth, out.data_ptr(), stream()) for c in range(copies)]
+                assert fns[0]() == 0, (pattern, waves, depth)
+                g, _ = capture(fns)
+                us = median_replay_ms(g, copies) * 1e3
+                del g
+                nbytes = weight_bytes + (meta_bytes if pattern == 1 else 0)
+                rows.append({"probe": names[pattern], "layer": name, "n": n, "k": k, "waves": waves,
+                             "depth": depth, "us": us, "gbps": nbytes / us / 1e3})
+                if pattern not in best or us < best[pattern][0]:
+                    best[pattern] = (us, waves, depth)
+        for pattern, (us, waves, depth) in sorted(best.items()):
+            nbytes = weight_bytes + (meta_bytes if pattern == 1 else 0)
+            log(f"  {name:13s} {names[pattern]:9s} best {us:6.2f} us {nbytes / us / 1e3:6.0f} GB/s "
+                f"(waves {waves}, depth {depth})")
+    print(json.dumps({"read_probe": rows}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -653,6 +716,11 @@ def main() -> int:
                          "and a plain --mfma-probe run")
     ap.add_argument("--stats-summary", nargs=2, metavar=("PROF_DIR", "BENCH_LOG"),
                     help="write the committed kernel-statistics summary from a rocprofv3 kernel-trace run")
+    ap.add_argument("--kernel-probe", action="store_true",
+                    help="eager launches of the M=1 decode GEMVs (cached configs), for rocprofv3 --pmc")
+    ap.add_argument("--probe", action="store_true",
+                    help="memory floors of the GEMV's access patterns (libtokenforge_probes.so), "
+                         "next to the GEMV itself on the cached or default configs")
     args = ap.parse_args()
     if args.stats_summary:
         return stats_summary(*args.stats_summary)
@@ -671,10 +739,10 @@ def main() -> int:
         print("bench.py needs an MI355X (gfx950) GPU", file=sys.stderr)
         return 1
 
-    import tokenforge_amd.kernels.ops  # noqa: F401
-    from tokenforge_amd.kernels import autotune
-    from tokenforge_amd.kernels.device import gpu_identity
-    from tokenforge_amd.kernels.hip.w4a16 import w4a16_gemm
+    import tokenforge.kernels.ops  # noqa: F401
+    from tokenforge.kernels import autotune
+    from tokenforge.kernels.device import gpu_identity
+    from tokenforge.kernels.hip.w4a16 import w4a16_gemm
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -686,7 +754,7 @@ def main() -> int:
     t0 = time.perf_counter()
     layers = [[make_layer(n, k, dev, seed=1000 * c + i) for i, (_, n, k) in enumerate(SHAPES)] for c in range(copies)]
     # Load-time repack throughput (pack.py:141-143) on the largest weight, for the record.
-    from tokenforge_amd.kernels.pack import repack_awq_to_tf
+    from tokenforge.kernels.pack import repack_awq_to_tf
 
     gate_awq = layers[0][2][3]
     g_rep, _ = capture([lambda: repack_awq_to_tf(gate_awq)] * 8, warm=2)
@@ -696,7 +764,7 @@ def main() -> int:
     torch.cuda.synchronize()
     log(f"setup: {copies} layer copies ({copies * step_bytes / 1e9:.2f} GB) in {time.perf_counter() - t0:.1f}s")
 
-    if not args.no_tune and not args.traffic_probe and not args.mfma_probe:  # probes use the cache
+    if not (args.no_tune or args.traffic_probe or args.mfma_probe or args.probe or args.kernel_probe):  # probes use the cache
         t0 = time.perf_counter()
         for _, n, k in SHAPES:
             buckets = (1, 2, 4, 256) if n in (37888,) or k == 18944 else (1, 2, 4)
@@ -709,8 +777,11 @@ def main() -> int:
     gen = torch.Generator(device=dev).manual_seed(7)
     xs = [torch.randn((1, k), generator=gen, device=dev).to(torch.float16) for _, _, k in SHAPES]
 
+    if args.probe:
+        return read_probes(dev, layers, copies, xs, cfg1)
+
     if args.traffic_probe:
-        from tokenforge_amd.kernels.config import candidate_configs
+        from tokenforge.kernels.config import candidate_configs
 
         qw_s_z = [layers[c][2] for c in range(copies)]
         cands = candidate_configs(1, GROUP)
@@ -735,6 +806,17 @@ def main() -> int:
         qw, s, z = layers[c][i]
         x, cfg = m_x[i], cfgs[i]
         return lambda: w4a16_gemm(x, qw, s, z, GROUP, cfg)
+
+    if args.kernel_probe:
+        # Eager launches of the M=1 decode GEMVs on the cached (or default) configs, each layer
+        # `copies` times over the rotating cold copies, for rocprofv3 counter runs.
+        for i, (name, n, k) in enumerate(SHAPES):
+            for c in range(copies):
+                launcher(c, i, xs, cfg1)()
+        torch.cuda.synchronize()
+        print(json.dumps({"kernel_probe": {"launches": copies, "m": 1, "configs": {
+            name: cfg1[i].to_dict() for i, (name, _, _) in enumerate(SHAPES)}}}), flush=True)
+        return 0
 
     if args.mfma_probe:
         # First the eager launches the counters see (each layer's in turn), then the graph

@@ -16,7 +16,7 @@
  * eight 4-bit values in the AWQ nibble order (nibble i holds offset AWQ_ORDER[i],
  * AWQ_ORDER = {0,2,4,6,1,3,5,7}).
  *
- * The Python host side (tokenforge_amd.kernels) binds these with ctypes; the citations
+ * The Python host side (tokenforge.kernels) binds these with ctypes; the citations
  * name the reference function (saransh-debugs/TokenForge) each entry point replaces.
  */
 #ifndef TOKENFORGE_HIP_H
@@ -62,10 +62,41 @@ int tf_awq_to_tf(const int32_t* qweight, int32_t* qweight_t, int64_t k, int64_t 
 int tf_tf_to_awq(const int32_t* qweight_t, int32_t* qweight, int64_t n, int64_t k,
                  void* stream);
 
+/* The gfx950 tile layout: what pack_awq produces and every kernel below reads. Same
+ * shapes and dtypes as the reference's TokenForge layout (qweight_t int32 [n, k/8], scales
+ * fp16 [k/g, n], qzeros int32 [k/g, n/8]); positions differ. Rows come in tiles of 16
+ * (t = row / 16, c = row % 16, r_t = min(16, n - 16 t)); with Q = k/32 and P = k/g:
+ *   16-byte weight chunk (row, q) [its words 4q..4q+3 of the TokenForge layout]
+ *                          -> chunk 16 t Q + 4 r_t (q / 4) + (q % 4) r_t + c
+ *   scale (p, row)         -> element 16 t P + p r_t + c
+ *   zero word (p, w)       -> word 2 t P + p (r_t / 8) + (w - 2 t), t = w / 2
+ * so each 16-row x 128-K step of qweight_t is one contiguous 1 KB block in which lane
+ * 16 g + c of a wave finds the MFMA B operand of column c, K block g. */
+
+/* pack.py:171-181 pack_awq (the layout step; the AWQ -> TokenForge transposition is
+ * tf_awq_to_tf): TokenForge-layout qweight_t, scales, qzeros -> the same three tensors in the
+ * tile layout. No counterpart kernel in the reference, whose pack_awq keeps the TokenForge
+ * layout. n % 8 == 0, k % group_size == 0; qweight buffers 16-byte aligned; out-of-place. */
+int tf_tile_pack(const int32_t* qweight_t, const uint16_t* scales, const int32_t* qzeros,
+                 int32_t* qweight_tile, uint16_t* scales_tile, int32_t* qzeros_tile, int64_t n,
+                 int64_t k, int32_t group_size, void* stream);
+
+/* pack.py:184-186 unpack_to_awq (the layout step): exact inverse of tf_tile_pack. */
+int tf_tile_unpack(const int32_t* qweight_tile, const uint16_t* scales_tile,
+                   const int32_t* qzeros_tile, int32_t* qweight_t, uint16_t* scales,
+                   int32_t* qzeros, int64_t n, int64_t k, int32_t group_size, void* stream);
+
+/* pack.py:83-107 awq_quantize: min-max asymmetric int4 of an fp32 weight [n, k] (finite
+ * values) into AWQ format: qweight int32 [k, n/8], qzeros int32 [k/g, n/8], scales fp16
+ * [k/g, n]; scale = fp16(max(max - min, 1e-5) / 15), zero = clamp(-rint(min / scale), 0,
+ * 15), q = clamp(rint(w / scale) + zero, 0, 15), IEEE fp32 division, round half to even. */
+int tf_awq_quantize(const float* weight, int64_t n, int64_t k, int32_t group_size,
+                    int32_t* qweight, int32_t* qzeros, uint16_t* scales, void* stream);
+
 /* --------------------------------------------------------------- dequant */
 
 /* w4a16.py:235-264 w4a16_dequant (== pack.py:189-194 dequantize_tf).
- * qweight_t int32 [n, k/8], scales fp16 [k/g, n], qzeros int32 [k/g, n/8]
+ * qweight_t, scales, qzeros in the tile layout (above)
  * -> out fp16 [n, k] with out[n][k] = fp16(q - z) * s (one fp16 rounding). */
 int tf_w4a16_dequant(const int32_t* qweight_t, const uint16_t* scales,
                      const int32_t* qzeros, uint16_t* out, int64_t n, int64_t k,
@@ -74,8 +105,7 @@ int tf_w4a16_dequant(const int32_t* qweight_t, const uint16_t* scales,
 /* --------------------------------------------------------------- W4A16 linear */
 
 /* Kernel families (the `kernel` field of tf_gemm_config). */
-#define TF_KERNEL_GEMV_DOT 0   /* decode: VALU dot2 + DPP reduce, M <= block_m <= 4   */
-#define TF_KERNEL_GEMV_MFMA 1  /* decode/skinny: in-register dequant + fp16 MFMA      */
+#define TF_KERNEL_GEMV_MFMA 1  /* decode: in-register dequant + fp16 MFMA (M <= 32)   */
 #define TF_KERNEL_GEMM_MFMA 2  /* prefill: LDS-staged dequant + fp16 MFMA, split-K    */
 
 /* Launch configuration; the counterpart of config.py:23-68 GemmConfig. The tuple
@@ -102,8 +132,8 @@ int64_t tf_w4a16_workspace_bytes(int64_t m, int64_t n, int64_t k, int32_t group_
 
 /* w4a16.py:178-232 w4a16_gemm and ops.py:86-88 _C.w4a16_gemv:
  *   out[m][n] = fp16( sum_k fp32(x[m][k]) * fp32(fp16(q[n][k] - z) * s) + fp32(bias[n]) )
- * x fp16 [m, k] with row stride ldx elements (16-byte aligned rows), qweight_t int32
- * [n, k/8], scales fp16 [k/g, n], qzeros int32 [k/g, n/8], bias fp16 [n] or NULL,
+ * x fp16 [m, k] with row stride ldx elements (16-byte aligned rows), qweight_t, scales and
+ * qzeros in the tile layout (above), bias fp16 [n] or NULL,
  * out fp16 [m, n] with row stride ldo. Split-K partials are reduced in a fixed order
  * (bit-identical run to run). workspace: fp32, >= tf_w4a16_workspace_bytes. */
 int tf_w4a16_linear(const uint16_t* x, int64_t ldx, const int32_t* qweight_t,
@@ -148,8 +178,8 @@ int tf_w4a16_linear_ex(const uint16_t* x, int64_t ldx, const int32_t* qweight_t,
  * xscale fp32, row m at xscale[m * xscale_stride] (stride 0: one scale for every row).
  * e4m3 values are exact in fp16, so with xscale = 1 this equals tf_w4a16_linear on the
  * decoded x bit for bit. Epilogues as tf_w4a16_linear_ex (applied after the row scale).
- * The GEMV configs with x staged in LDS (gemv_dot; gemv_mfma with block_k 128) decode the
- * codes while staging; other configs decode x to fp16 into the workspace first. */
+ * The GEMV configs decode the codes while staging x in LDS; the GEMM configs decode x to fp16
+ * into the workspace first. Every check runs before anything is launched. */
 int64_t tf_w4a8_workspace_bytes_ex(int64_t m, int64_t n, int64_t k, int32_t group_size,
                                    const tf_gemm_config* cfg, int32_t epilogue);
 int tf_w4a8_linear_ex(const uint8_t* x8, int64_t ldx8, const float* xscale, int64_t xscale_stride,

@@ -148,3 +148,109 @@ def dequantize_tf(weights: W4A16Weights) -> np.ndarray:
     z = np.repeat(unpack_int4(weights.qzeros), weights.group_size, axis=0).T
     s = np.repeat(np.asarray(weights.scales, dtype=np.float16), weights.group_size, axis=0).T
     return (q - z).astype(np.float16) * s
+
+
+# --------------------------------------------------------------------------- gfx950 tile layout
+#
+# The layout this build's pack_awq emits (no counterpart in the reference, whose pack_awq keeps
+# the TokenForge layout above; the kernels' tokenforge_amd/csrc/tile_layout.h states the same
+# maps). Rows come in tiles of 16 (t = n // 16, c = n % 16, r_t = min(16, N - 16 t)). qweight_t
+# moves in 16-byte chunks (chunk q of row n = its words 4q..4q+3, K offsets 32q..32q+31):
+#   chunk (n, q)  -> 16 t Q + 4 r_t (q // 4) + (q % 4) r_t + c       (Q = K / 32)
+#   scale (p, n)  -> 16 t P + p r_t + c                               (P = K / G)
+#   zero  (p, w)  -> 2 t P + p (r_t // 8) + (w - 2 t),  t = w // 2
+# tile_order_* below define the same layout a second way, by the order in which a tile's
+# 128-wide K steps, chunk columns and rows are laid down; the tests require both to agree.
+
+
+def _tile_rows(n_total: int, t: np.ndarray) -> np.ndarray:
+    return np.minimum(16, n_total - 16 * t)
+
+
+def tile_chunk_index(n: np.ndarray, q: np.ndarray, n_total: int, q_total: int) -> np.ndarray:
+    t, c = n // 16, n % 16
+    rt = _tile_rows(n_total, t)
+    return 16 * t * q_total + 4 * rt * (q // 4) + (q % 4) * rt + c
+
+
+def tile_scale_index(p: np.ndarray, n: np.ndarray, n_total: int, p_total: int) -> np.ndarray:
+    t = n // 16
+    return 16 * t * p_total + p * _tile_rows(n_total, t) + n % 16
+
+
+def tile_zero_index(p: np.ndarray, w: np.ndarray, n_total: int, p_total: int) -> np.ndarray:
+    t = w // 2
+    return 2 * t * p_total + p * (_tile_rows(n_total, t) // 8) + (w - 2 * t)
+
+
+def tile_pack(
+    qweight_t: np.ndarray, scales: np.ndarray, qzeros: np.ndarray, group_size: int
+) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """TokenForge-layout (qweight_t, scales, qzeros) -> the same tensors in the tile layout."""
+    n, words = qweight_t.shape
+    q_total, p_total = words // 4, (words * 8) // group_size
+    chunks = np.ascontiguousarray(qweight_t).reshape(n, q_total, 4)
+    nn, qq = np.meshgrid(np.arange(n), np.arange(q_total), indexing="ij")
+    qw = np.empty((n * q_total, 4), dtype=np.int32)
+    qw[tile_chunk_index(nn, qq, n, q_total).ravel()] = chunks.reshape(-1, 4)
+    pp, ns = np.meshgrid(np.arange(p_total), np.arange(n), indexing="ij")
+    sc = np.empty(p_total * n, dtype=np.float16)
+    sc[tile_scale_index(pp, ns, n, p_total).ravel()] = np.asarray(scales).ravel()
+    pz, wz = np.meshgrid(np.arange(p_total), np.arange(n // 8), indexing="ij")
+    qz = np.empty(p_total * (n // 8), dtype=np.int32)
+    qz[tile_zero_index(pz, wz, n, p_total).ravel()] = np.asarray(qzeros).ravel()
+    return qw.reshape(n, words), sc.reshape(p_total, n), qz.reshape(p_total, n // 8)
+
+
+def tile_unpack(
+    qweight_tile: np.ndarray, scales_tile: np.ndarray, qzeros_tile: np.ndarray, group_size: int
+) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """Inverse of :func:`tile_pack`."""
+    n, words = qweight_tile.shape
+    q_total, p_total = words // 4, (words * 8) // group_size
+    nn, qq = np.meshgrid(np.arange(n), np.arange(q_total), indexing="ij")
+    qw = np.ascontiguousarray(qweight_tile).reshape(-1, 4)[tile_chunk_index(nn, qq, n, q_total)]
+    pp, ns = np.meshgrid(np.arange(p_total), np.arange(n), indexing="ij")
+    sc = np.asarray(scales_tile).ravel()[tile_scale_index(pp, ns, n, p_total)]
+    pz, wz = np.meshgrid(np.arange(p_total), np.arange(n // 8), indexing="ij")
+    qz = np.asarray(qzeros_tile).ravel()[tile_zero_index(pz, wz, n, p_total)]
+    return qw.reshape(n, words), sc.astype(np.float16), qz.astype(np.int32)
+
+
+def tile_order_chunks(n_total: int, q_total: int) -> list[tuple[int, int]]:
+    """(row, chunk) pairs in the order the tile layout stores them: tile by tile, 128-wide K
+    step by step, chunk column g by g, row by row."""
+    out = []
+    for t in range((n_total + 15) // 16):
+        rows = min(16, n_total - 16 * t)
+        for j in range((q_total + 3) // 4):
+            for g in range(min(4, q_total - 4 * j)):
+                out += [(16 * t + c, 4 * j + g) for c in range(rows)]
+    return out
+
+
+def tile_order_scales(n_total: int, p_total: int) -> list[tuple[int, int]]:
+    """(group, row) pairs in storage order: tile by tile, group by group, row by row."""
+    out = []
+    for t in range((n_total + 15) // 16):
+        rows = min(16, n_total - 16 * t)
+        for p in range(p_total):
+            out += [(p, 16 * t + c) for c in range(rows)]
+    return out
+
+
+def tile_order_zeros(n_total: int, p_total: int) -> list[tuple[int, int]]:
+    """(group, zero word) pairs in storage order: tile by tile, group by group, word by word."""
+    out = []
+    for t in range((n_total + 15) // 16):
+        words = min(16, n_total - 16 * t) // 8
+        for p in range(p_total):
+            out += [(p, 2 * t + w) for w in range(words)]
+    return out
+
+
+def pack_awq_tiles(qweight: np.ndarray, qzeros: np.ndarray, scales: np.ndarray, group_size: int) -> W4A16Weights:
+    """This build's pack_awq: the reference's pack_awq (pack.py:171-181), then the tile layout."""
+    w = pack_awq(qweight, qzeros, scales, group_size)
+    qw, sc, qz = tile_pack(w.qweight_t, w.scales, w.qzeros, group_size)
+    return W4A16Weights(qweight_t=qw, scales=sc, qzeros=qz, group_size=group_size)

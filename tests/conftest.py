@@ -43,7 +43,7 @@ def device() -> torch.device:
 def _isolated_cache_dir(tmp_path_factory: pytest.TempPathFactory, monkeypatch: pytest.MonkeyPatch):
     """Every test gets its own autotune cache dir; nothing leaks into ~/.cache."""
     monkeypatch.setenv("TOKENFORGE_CACHE_DIR", str(tmp_path_factory.mktemp("tf-cache")))
-    from tokenforge_amd.kernels import autotune
+    from tokenforge.kernels import autotune
 
     autotune.reset_caches()
     yield

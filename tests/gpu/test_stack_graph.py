@@ -14,8 +14,8 @@ from __future__ import annotations
 import pytest
 import torch
 
-import tokenforge_amd.kernels.ops  # noqa: F401  (registers torch.ops.tokenforge)
-from tokenforge_amd.kernels.autotune import synthetic_layer
+import tokenforge.kernels.ops  # noqa: F401  (registers torch.ops.tokenforge)
+from tokenforge.kernels.autotune import synthetic_layer
 
 pytestmark = pytest.mark.gpu
 G = 128

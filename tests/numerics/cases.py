@@ -14,7 +14,7 @@ import numpy as np
 import torch
 
 from oracle import pack as opack
-from tokenforge_amd.kernels.pack import W4A16Weights
+from tokenforge.kernels.pack import W4A16Weights
 
 GROUP_SIZE = 128
 TEST_SEEDS = (0,)
@@ -44,11 +44,13 @@ def bias(n: int, seed: int) -> torch.Tensor:
 
 
 def on_device(w: opack.W4A16Weights, device: torch.device) -> W4A16Weights:
-    """Oracle numpy weights -> product weights (torch tensors) on ``device``."""
+    """Oracle numpy weights (TokenForge layout) -> product weights on ``device``, in the tile
+    layout the kernels read (laid out by the oracle's restatement of it)."""
+    qw, sc, qz = opack.tile_pack(w.qweight_t, w.scales, w.qzeros, w.group_size)
     return W4A16Weights(
-        torch.from_numpy(np.ascontiguousarray(w.qweight_t)).to(device),
-        torch.from_numpy(np.ascontiguousarray(w.scales)).to(device),
-        torch.from_numpy(np.ascontiguousarray(w.qzeros)).to(device),
+        torch.from_numpy(np.ascontiguousarray(qw)).to(device),
+        torch.from_numpy(np.ascontiguousarray(sc)).to(device),
+        torch.from_numpy(np.ascontiguousarray(qz)).to(device),
         w.group_size,
     )
 

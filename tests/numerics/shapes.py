@@ -1,4 +1,15 @@
-"""The shape suite shared by numerics tests, calibration and benchmarks (shapes.py:1-51)."""
+"""Linear shapes of the numerics suite, derived from each model's decoder dimensions.
+
+A decoder layer has four quantized linears as an engine sees them at TP=1 (q/k/v fused,
+gate/up fused): qkv ``hidden -> hidden + 2 * kv``, o ``hidden -> hidden``, gate_up
+``hidden -> 2 * intermediate`` and down ``intermediate -> hidden``; ``n`` is the output
+width and ``k`` the reduction length. Two synthetic layers add N that no tile width divides
+(still a multiple of 8, as AWQ packing requires). The reference's suite holds the same shapes
+(tests/numerics/shapes.py:16-35).
+
+``TOKENFORGE_SHAPE_SUITE=full`` selects every shape and the long M list; the default quick
+suite keeps the small model, the ragged layers and a few M values.
+"""
 
 from __future__ import annotations
 
@@ -13,27 +24,31 @@ class LinearShape(NamedTuple):
     k: int
 
 
-# q/k/v and gate/up are fused, as an engine sees them at TP=1.
-QWEN25_05B = [
-    LinearShape("qwen2.5-0.5b", "qkv_proj", 896 + 2 * 128, 896),
-    LinearShape("qwen2.5-0.5b", "o_proj", 896, 896),
-    LinearShape("qwen2.5-0.5b", "gate_up_proj", 2 * 4864, 896),
-    LinearShape("qwen2.5-0.5b", "down_proj", 896, 4864),
-]
-QWEN25_7B = [
-    LinearShape("qwen2.5-7b", "qkv_proj", 3584 + 2 * 512, 3584),
-    LinearShape("qwen2.5-7b", "o_proj", 3584, 3584),
-    LinearShape("qwen2.5-7b", "gate_up_proj", 2 * 18944, 3584),
-    LinearShape("qwen2.5-7b", "down_proj", 3584, 18944),
-]
-# N not divisible by any tile size (still a multiple of 8, as AWQ packing requires).
-RAGGED = [
-    LinearShape("synthetic", "n_ragged_small", 200, 256),
-    LinearShape("synthetic", "n_ragged", 1000, 1024),
-]
+# model -> (hidden, fused k+v width / 2, intermediate)
+_DECODERS: dict[str, tuple[int, int, int]] = {
+    "qwen2.5-0.5b": (896, 128, 4864),
+    "qwen2.5-7b": (3584, 512, 18944),
+}
+_RAGGED: tuple[tuple[str, int, int], ...] = (("n_ragged_small", 200, 256), ("n_ragged", 1000, 1024))
 
-M_SUITE = (1, 2, 3, 4, 7, 8, 15, 16, 31, 32, 33, 64, 127, 128, 129, 256)
-M_SUITE_QUICK = (1, 3, 8, 16, 31, 129)
+
+def decoder_linears(model: str) -> list[LinearShape]:
+    hidden, kv, inter = _DECODERS[model]
+    widths = {
+        "qkv_proj": (hidden + 2 * kv, hidden),
+        "o_proj": (hidden, hidden),
+        "gate_up_proj": (2 * inter, hidden),
+        "down_proj": (hidden, inter),
+    }
+    return [LinearShape(model, layer, n, k) for layer, (n, k) in widths.items()]
+
+
+def ragged_linears() -> list[LinearShape]:
+    return [LinearShape("synthetic", layer, n, k) for layer, n, k in _RAGGED]
+
+
+_M_FULL = (1, 2, 3, 4, 7, 8, 15, 16, 31, 32, 33, 64, 127, 128, 129, 256)
+_M_QUICK = (1, 3, 8, 16, 31, 129)
 
 
 def suite() -> str:
@@ -42,10 +57,9 @@ def suite() -> str:
 
 
 def linear_shapes() -> list[LinearShape]:
-    if suite() == "full":
-        return QWEN25_05B + QWEN25_7B + RAGGED
-    return QWEN25_05B + RAGGED
+    models = list(_DECODERS) if suite() == "full" else ["qwen2.5-0.5b"]
+    return [s for model in models for s in decoder_linears(model)] + ragged_linears()
 
 
 def m_values() -> tuple[int, ...]:
-    return M_SUITE if suite() == "full" else M_SUITE_QUICK
+    return _M_FULL if suite() == "full" else _M_QUICK

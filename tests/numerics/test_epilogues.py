@@ -16,26 +16,27 @@ import ctypes
 import pytest
 import torch
 
-import tokenforge_amd.kernels.ops  # noqa: F401  (registers torch.ops.tokenforge)
+import tokenforge.kernels.ops  # noqa: F401  (registers torch.ops.tokenforge)
 from tests.numerics import cases
-from tokenforge_amd.kernels import _lib
-from tokenforge_amd.kernels.config import GemmConfig
-from tokenforge_amd.kernels.hip._common import stream_of
-from tokenforge_amd.kernels.hip.w4a16 import to_c_config, w4a16_gemm, w4a16_gemm_ex
+from tokenforge.kernels import _lib
+from tokenforge.kernels.config import GemmConfig
+from tokenforge.kernels.hip._common import stream_of
+from tokenforge.kernels.hip.w4a16 import to_c_config, w4a16_gemm, w4a16_gemm_ex
 
 pytestmark = pytest.mark.gpu
 G = cases.GROUP_SIZE
 
 CONFIGS = [
-    GemmConfig("gemv_dot", 1, 16, 128, 1, 4, 2),
-    GemmConfig("gemv_dot", 2, 32, 128, 1, 2, 2),
-    GemmConfig("gemv_dot", 4, 16, 128, 1, 8, 2),
-    GemmConfig("gemv_dot", 1, 16, 256, 1, 4, 4),
-    GemmConfig("gemv_dot", 2, 16, 256, 1, 8, 4),
+    GemmConfig("gemv_mfma", 16, 16, 128, 1, 4, 2),
+    GemmConfig("gemv_mfma", 16, 32, 128, 1, 2, 2),
+    GemmConfig("gemv_mfma", 16, 16, 128, 1, 8, 2),
+    GemmConfig("gemv_mfma", 16, 16, 256, 1, 4, 4),
+    GemmConfig("gemv_mfma", 16, 16, 256, 1, 8, 4),
     GemmConfig("gemv_mfma", 16, 16, 256, 1, 4, 2),
     GemmConfig("gemv_mfma", 16, 16, 128, 1, 16, 4),
     GemmConfig("gemv_mfma", 16, 64, 128, 1, 2, 2),
-    GemmConfig("gemv_mfma", 16, 32, 64, 1, 4, 2),
+    GemmConfig("gemv_mfma", 16, 32, 256, 1, 4, 2),
+    GemmConfig("gemv_mfma", 16, 64, 128, 1, 4, 2),
     GemmConfig("gemv_mfma", 32, 32, 128, 1, 4, 2),
     GemmConfig("gemm_mfma", 64, 128, 64, 1, 4, 2),
     GemmConfig("gemm_mfma", 128, 128, 32, 2, 4, 2),
@@ -53,8 +54,6 @@ def _id(c: GemmConfig) -> str:
 
 
 def _m_list(cfg: GemmConfig) -> tuple[int, ...]:
-    if cfg.kernel == "gemv_dot":
-        return tuple(sorted({1, cfg.block_m}))
     return (1, cfg.block_m - 1, cfg.block_m + 3)
 
 

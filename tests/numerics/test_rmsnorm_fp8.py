@@ -14,9 +14,9 @@ import numpy as np
 import pytest
 import torch
 
-import tokenforge_amd.kernels.ops  # noqa: F401
+import tokenforge.kernels.ops  # noqa: F401
 from oracle import reference as oref
-from tokenforge_amd.kernels.hip.rmsnorm_fp8 import (
+from tokenforge.kernels.hip.rmsnorm_fp8 import (
     FP8_E4M3_MAX,
     e4m3_encode,
     rmsnorm_fp8_quant,

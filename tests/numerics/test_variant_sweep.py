@@ -18,8 +18,8 @@ import torch
 
 from tests.numerics import cases
 from tests.numerics.test_w4a16 import _assert_close
-from tokenforge_amd.kernels.config import VARIANTS, GemmConfig
-from tokenforge_amd.kernels.hip.w4a16 import w4a8_gemm_ex, w4a16_gemm, w4a16_gemm_ex
+from tokenforge.kernels.config import VARIANTS, GemmConfig
+from tokenforge.kernels.hip.w4a16 import w4a8_gemm_ex, w4a16_gemm, w4a16_gemm_ex
 
 pytestmark = pytest.mark.gpu
 
@@ -36,9 +36,7 @@ def _case(index: int, variant: tuple) -> dict:  # type: ignore[type-arg]
     n = 8 * rng.randint(8, 64)
     if rng.random() < 0.5:
         n = 16 * rng.randint(4, 32)  # a multiple of 16 (the SiLU*mul epilogue needs it)
-    if kernel == "gemv_dot":
-        m = rng.randint(1, bm)
-    elif kernel == "gemv_mfma":
+    if kernel == "gemv_mfma":
         m = rng.randint(1, 2 * bm + 3)
     else:
         m = rng.randint(1, 2 * bm + 5)

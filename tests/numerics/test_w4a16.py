@@ -15,16 +15,16 @@ import numpy as np
 import pytest
 import torch
 
-import tokenforge_amd.kernels.ops  # noqa: F401  (registers torch.ops.tokenforge)
+import tokenforge.kernels.ops  # noqa: F401  (registers torch.ops.tokenforge)
 from oracle import pack as opack
 from oracle import reference as oref
 from tests.numerics import cases
 from tests.numerics.shapes import linear_shapes, m_values
 from tests.numerics.tolerance import NORMWISE_MAX, atol, normwise
-from tokenforge_amd.kernels.config import GemmConfig
-from tokenforge_amd.kernels.hip.w4a16 import w4a16_dequant, w4a16_gemm
-from tokenforge_amd.kernels.metrics import KERNEL_CALLS
-from tokenforge_amd.kernels.pack import W4A16Weights
+from tokenforge.kernels.config import GemmConfig
+from tokenforge.kernels.hip.w4a16 import w4a16_dequant, w4a16_gemm
+from tokenforge.kernels.metrics import KERNEL_CALLS
+from tokenforge.kernels.pack import W4A16Weights
 
 pytestmark = pytest.mark.gpu
 G = cases.GROUP_SIZE
@@ -68,23 +68,25 @@ def test_linear_shape_suite(shape, m: int, device: torch.device) -> None:  # typ
 
 
 PATH_CONFIGS = [
-    GemmConfig("gemv_dot", 1, 16, 128, 1, 1, 2),
-    GemmConfig("gemv_dot", 1, 64, 128, 1, 4, 2),
-    GemmConfig("gemv_dot", 1, 32, 128, 1, 8, 4),
-    GemmConfig("gemv_mfma", 16, 16, 64, 1, 2, 2),
-    GemmConfig("gemv_dot", 2, 32, 128, 1, 2, 2),
-    GemmConfig("gemv_dot", 4, 16, 128, 1, 8, 2),
+    GemmConfig("gemv_mfma", 16, 16, 128, 1, 1, 2),
+    GemmConfig("gemv_mfma", 16, 64, 128, 1, 4, 2),
+    GemmConfig("gemv_mfma", 16, 32, 128, 1, 8, 4),
+    GemmConfig("gemv_mfma", 16, 16, 128, 1, 2, 8),
+    GemmConfig("gemv_mfma", 16, 32, 128, 1, 2, 2),
+    GemmConfig("gemv_mfma", 16, 16, 128, 1, 8, 2),
     # block_k 256: waves over row tiles (200 rows: the last workgroup's last waves are empty)
-    GemmConfig("gemv_dot", 1, 16, 256, 1, 4, 4),
-    GemmConfig("gemv_dot", 1, 32, 256, 1, 2, 4),
-    GemmConfig("gemv_dot", 4, 16, 256, 1, 8, 4),
+    GemmConfig("gemv_mfma", 16, 16, 256, 1, 4, 4),
+    GemmConfig("gemv_mfma", 16, 32, 256, 1, 2, 4),
+    GemmConfig("gemv_mfma", 16, 16, 256, 1, 8, 4),
     GemmConfig("gemv_mfma", 16, 16, 256, 1, 4, 4),
     GemmConfig("gemv_mfma", 16, 32, 256, 1, 2, 2),
     GemmConfig("gemv_mfma", 16, 16, 128, 1, 1, 2),
     GemmConfig("gemv_mfma", 16, 16, 128, 1, 16, 4),
     GemmConfig("gemv_mfma", 16, 64, 128, 1, 8, 2),
-    GemmConfig("gemv_mfma", 16, 64, 64, 1, 4, 2),
-    GemmConfig("gemv_mfma", 32, 32, 64, 1, 4, 2),
+    GemmConfig("gemv_mfma", 16, 64, 128, 1, 2, 2),
+    GemmConfig("gemv_mfma", 32, 32, 128, 1, 2, 2),
+    GemmConfig("gemv_mfma", 32, 16, 256, 1, 4, 2),
+    GemmConfig("gemv_mfma", 16, 32, 256, 1, 8, 4),
     GemmConfig("gemv_mfma", 16, 32, 128, 1, 8, 4),
     GemmConfig("gemv_mfma", 32, 32, 128, 1, 4, 2),
     GemmConfig("gemm_mfma", 64, 64, 64, 1, 4, 2),
@@ -123,8 +125,6 @@ PATH_CONFIGS = [
 
 
 def _m_list(cfg: GemmConfig) -> tuple[int, ...]:
-    if cfg.kernel == "gemv_dot":
-        return tuple(sorted({1, cfg.block_m}))
     return (1, cfg.block_m - 1, cfg.block_m + 3)
 
 
@@ -152,21 +152,26 @@ def test_every_code_path(cfg: GemmConfig, with_bias: bool, device: torch.device)
     [
         GemmConfig("gemv_mfma", 16, 64, 128, 1, 1, 2),
         GemmConfig("gemv_mfma", 16, 32, 128, 1, 1, 4),
-        GemmConfig("gemv_mfma", 16, 64, 64, 1, 1, 2),
-        GemmConfig("gemv_dot", 1, 64, 128, 1, 1, 2),
-        GemmConfig("gemv_dot", 1, 16, 256, 1, 2, 8),  # one shared x, partial last step
+        GemmConfig("gemv_mfma", 32, 16, 128, 1, 1, 2),
+        GemmConfig("gemv_mfma", 16, 16, 128, 1, 1, 8),
+        GemmConfig("gemv_mfma", 16, 16, 256, 1, 2, 8),  # one shared x, partial last step
     ],
     ids=_cfg_id,
 )
 def test_gemv_staging_windows(cfg: GemmConfig, device: torch.device) -> None:
-    """One wave over a long K with group 32: its x slice (16 rows for the MFMA variants)
-    exceeds the LDS, so the wave stages several windows. K = 8288 also ends in a partial
-    128-wide step (the kernels that check each step's bounds per lane)."""
+    """One wave over a long K with group 32: its x slice (up to 32 rows) exceeds the LDS, so
+    the wave stages several windows. K = 8288 also ends in a partial 128-wide step (the
+    kernels that check each step's bounds per lane). The shared-x form (block_k 256) stages all
+    of x once: one row fits, 15 rows do not and the call is rejected before any launch."""
     n, k, group = 200, 8288, 32
     w = cases.layer_weights(n, k, 3, group)
     wd = cases.on_device(w, device)
     for m in _m_list(cfg):
         x = cases.activations(m, k, 3)
+        if cfg.block_k == 256 and m > 1:
+            with pytest.raises(ValueError, match="fit the device's LDS"):
+                w4a16_gemm(x.to(device), wd.qweight_t, wd.scales, wd.qzeros, group, cfg)
+            continue
         y = w4a16_gemm(x.to(device), wd.qweight_t, wd.scales, wd.qzeros, group, cfg)
         _assert_close(y, x, w)
 
@@ -207,7 +212,7 @@ def test_staged_x_waits_at_full_size(m: int, cfg: GemmConfig, device: torch.devi
     some workgroups read a stage before it landed (wrong rows, varying run to run). Full
     gate_up width, three runs: bit-identical to each other and close to an fp32 product of
     the exact dequantized weights."""
-    from tokenforge_amd.kernels.autotune import synthetic_layer
+    from tokenforge.kernels.autotune import synthetic_layer
 
     n, k = 37888, 3584
     qweight_t, scales, qzeros = synthetic_layer(n, k, G, device, seed=5)
@@ -232,11 +237,11 @@ def test_decode_full_size_config3(layer: str, n: int, k: int, device: torch.devi
     over row tiles, MFMA), against an fp32 product of the exactly dequantized weights (the
     dequant kernel is bit-exact with the oracle's). The same inputs give the same bits in every
     config of one form on repeated calls."""
-    from tokenforge_amd.kernels.autotune import synthetic_layer
+    from tokenforge.kernels.autotune import synthetic_layer
 
     qweight_t, scales, qzeros = synthetic_layer(n, k, G, device, seed=11)
     wt = w4a16_dequant(qweight_t, scales, qzeros, G).float().t().contiguous()
-    forms = [GemmConfig("gemv_dot", 4, 16, 128, 1, 8, 2), GemmConfig("gemv_dot", 4, 16, 256, 1, 4, 4),
+    forms = [GemmConfig("gemv_mfma", 16, 16, 128, 1, 8, 2), GemmConfig("gemv_mfma", 16, 16, 256, 1, 4, 4),
              GemmConfig("gemv_mfma", 16, 16, 128, 1, 8, 4), GemmConfig("gemv_mfma", 16, 16, 256, 1, 4, 2)]
     for m in (1, 2, 4):
         gen = torch.Generator(device=device).manual_seed(m)
@@ -258,7 +263,7 @@ def test_small_group_sizes(group_size: int, device: torch.device) -> None:
     w = cases.layer_weights(n, k, 0, group_size)
     wd = cases.on_device(w, device)
     configs = [
-        GemmConfig("gemv_dot", 1, 16, 128, 1, 2, 2),
+        GemmConfig("gemv_mfma", 16, 16, 128, 1, 2, 2),
         GemmConfig("gemv_mfma", 16, 32, 128, 1, 2, 2),
         GemmConfig("gemm_mfma", 64, 64, 32, 2, 4, 2),
     ]
@@ -268,8 +273,6 @@ def test_small_group_sizes(group_size: int, device: torch.device) -> None:
         configs.append(GemmConfig("gemm_mfma", 256, 128, 64, 2, 8, 3))
     for cfg in configs:
         for m in (1, 5, 40):
-            if cfg.kernel == "gemv_dot" and m > cfg.block_m:
-                continue
             x = cases.activations(m, k, 1)
             y = w4a16_gemm(x.to(device), wd.qweight_t, wd.scales, wd.qzeros, group_size, cfg)
             _assert_close(y, x, w)
@@ -340,7 +343,7 @@ def test_non_contiguous_and_misaligned_inputs_are_handled(device: torch.device) 
 def test_rejects_bad_weight_layouts(device: torch.device) -> None:
     w = cases.on_device(cases.layer_weights(64, 256, 0), device)
     x = cases.activations(1, 256, 0).to(device)
-    cfg = GemmConfig("gemv_dot", 1, 16, 128, 1, 1, 2)
+    cfg = GemmConfig("gemv_mfma", 16, 16, 128, 1, 1, 2)
     with pytest.raises(ValueError, match="contiguous"):
         w4a16_gemm(x, w.qweight_t.t().contiguous().t(), w.scales, w.qzeros, G, cfg)
     with pytest.raises(ValueError, match="encodes K"):
@@ -349,8 +352,8 @@ def test_rejects_bad_weight_layouts(device: torch.device) -> None:
         w4a16_gemm(x.float(), w.qweight_t, w.scales, w.qzeros, G, cfg)
     with pytest.raises(ValueError, match="divide"):
         w4a16_gemm(x, w.qweight_t, w.scales, w.qzeros, G, GemmConfig("gemm_mfma", 64, 64, 256, 1, 4, 2))
-    with pytest.raises(ValueError, match="block_m"):
-        w4a16_gemm(x.expand(3, 256).contiguous(), w.qweight_t, w.scales, w.qzeros, G, cfg)
+    with pytest.raises(ValueError, match="compiled variant"):
+        w4a16_gemm(x, w.qweight_t, w.scales, w.qzeros, G, GemmConfig("gemv_mfma", 48, 16, 128, 1, 1, 2))
 
 
 def test_shared_x_variant_rejects_x_larger_than_the_lds(device: torch.device) -> None:
@@ -358,11 +361,11 @@ def test_shared_x_variant_rejects_x_larger_than_the_lds(device: torch.device) ->
     w = cases.on_device(cases.layer_weights(16, 32768, 1), device)
     x = cases.activations(4, 32768, 1).to(device)
     with pytest.raises(ValueError, match="fit"):
-        w4a16_gemm(x, w.qweight_t, w.scales, w.qzeros, G, GemmConfig("gemv_dot", 4, 16, 256, 1, 8, 4))
+        w4a16_gemm(x, w.qweight_t, w.scales, w.qzeros, G, GemmConfig("gemv_mfma", 16, 16, 256, 1, 8, 4))
     with pytest.raises(ValueError, match="fit"):
         w4a16_gemm(x, w.qweight_t, w.scales, w.qzeros, G, GemmConfig("gemv_mfma", 16, 16, 256, 1, 4, 2))
     # one row fits (64 KiB)
-    for cfg in (GemmConfig("gemv_dot", 4, 16, 256, 1, 8, 4), GemmConfig("gemv_mfma", 16, 16, 256, 1, 4, 2)):
+    for cfg in (GemmConfig("gemv_mfma", 16, 16, 256, 1, 8, 4), GemmConfig("gemv_mfma", 16, 16, 256, 1, 4, 2)):
         y = w4a16_gemm(x[:1].contiguous(), w.qweight_t, w.scales, w.qzeros, G, cfg)
         _assert_close(y, cases.activations(4, 32768, 1)[:1], cases.layer_weights(16, 32768, 1))
 
@@ -384,7 +387,7 @@ def _weights_from_ints(q: torch.Tensor, z: torch.Tensor, s: torch.Tensor) -> opa
 
 
 F1_CONFIGS = (
-    GemmConfig("gemv_dot", 2, 16, 128, 1, 2, 2),
+    GemmConfig("gemv_mfma", 16, 16, 128, 1, 2, 2),
     GemmConfig("gemv_mfma", 16, 16, 128, 1, 2, 2),
     GemmConfig("gemm_mfma", 64, 64, 64, 2, 4, 2),
 )
@@ -418,12 +421,12 @@ def test_f1_real_inf_and_nan_propagate(device: torch.device) -> None:
     x[2, 9] = float("nan")
     ref16 = torch.from_numpy(oref.w4a16_reference(x.numpy(), w)).to(torch.float16)
     configs = (
-        GemmConfig("gemv_dot", 4, 16, 128, 1, 2, 2),
+        GemmConfig("gemv_mfma", 16, 16, 128, 1, 2, 2),
         GemmConfig("gemv_mfma", 16, 16, 128, 1, 2, 2),
         GemmConfig("gemm_mfma", 64, 64, 64, 2, 4, 2),
     )
     for cfg in configs:
-        rows = x[: 4 if cfg.kernel == "gemv_dot" else 16]
+        rows = x[:16]
         y = w4a16_gemm(rows.to(device), wd.qweight_t, wd.scales, wd.qzeros, G, cfg).cpu()
         r = ref16[: rows.shape[0]]
         assert torch.equal(torch.isnan(y), torch.isnan(r)), cfg
@@ -443,7 +446,7 @@ def test_zero_and_denormal_scales(scale_value: float, device: torch.device) -> N
     w = _weights_from_ints(q, z, s)
     wd = cases.on_device(w, device)
     x = cases.activations(3, k, 0)
-    for cfg in (GemmConfig("gemv_dot", 1, 16, 128, 1, 1, 2),) + F1_CONFIGS:
+    for cfg in (GemmConfig("gemv_mfma", 16, 16, 128, 1, 1, 2),) + F1_CONFIGS:
         rows = x[: min(3, cfg.block_m)]
         y = w4a16_gemm(rows.to(device), wd.qweight_t, wd.scales, wd.qzeros, G, cfg)
         assert bool(torch.isfinite(y).all())
@@ -468,12 +471,12 @@ def test_split_k_is_deterministic_and_graph_safe(device: torch.device) -> None:
     """F5: same inputs and config -> bit-identical output, eager and under HIP-graph replay."""
     w = cases.on_device(cases.layer_weights(1152, 896, 0), device)
     configs = [
-        GemmConfig("gemv_dot", 1, 32, 128, 1, 4, 2),
+        GemmConfig("gemv_mfma", 16, 32, 128, 1, 4, 2),
         GemmConfig("gemv_mfma", 16, 16, 128, 1, 8, 2),
         GemmConfig("gemm_mfma", 64, 64, 64, 7, 4, 2),
     ]
     for cfg in configs:
-        m = 1 if cfg.kernel == "gemv_dot" else 48
+        m = 1 if cfg is configs[0] else 48
         x = cases.activations(m, 896, 0).to(device)
         first = w4a16_gemm(x, w.qweight_t, w.scales, w.qzeros, G, cfg)
         for _ in range(3):

@@ -17,28 +17,28 @@ import numpy as np
 import pytest
 import torch
 
-import tokenforge_amd.kernels.ops  # noqa: F401  (registers torch.ops.tokenforge)
+import tokenforge.kernels.ops  # noqa: F401  (registers torch.ops.tokenforge)
 from oracle import pack as opack
 from oracle import reference as oref
 from tests.numerics import cases
 from tests.numerics.tolerance import NORMWISE_MAX, atol, normwise
-from tokenforge_amd.kernels.config import GemmConfig
-from tokenforge_amd.kernels.hip.rmsnorm_fp8 import rmsnorm_fp8_quant
-from tokenforge_amd.kernels.hip.w4a16 import w4a8_gemm_ex, w4a16_gemm, w4a16_gemm_ex
+from tokenforge.kernels.config import GemmConfig
+from tokenforge.kernels.hip.rmsnorm_fp8 import rmsnorm_fp8_quant
+from tokenforge.kernels.hip.w4a16 import w4a8_gemm_ex, w4a16_gemm, w4a16_gemm_ex
 
 pytestmark = pytest.mark.gpu
 G = cases.GROUP_SIZE
 
 CONFIGS = [
     # decode while staging x
-    GemmConfig("gemv_dot", 1, 16, 128, 1, 4, 2),
-    GemmConfig("gemv_dot", 4, 16, 128, 1, 8, 2),
-    GemmConfig("gemv_dot", 1, 16, 256, 1, 4, 4),
+    GemmConfig("gemv_mfma", 16, 16, 128, 1, 4, 2),
+    GemmConfig("gemv_mfma", 16, 16, 128, 1, 8, 2),
+    GemmConfig("gemv_mfma", 16, 16, 256, 1, 4, 4),
     GemmConfig("gemv_mfma", 16, 16, 256, 1, 8, 4),
     GemmConfig("gemv_mfma", 16, 16, 128, 1, 16, 4),
     GemmConfig("gemv_mfma", 32, 32, 128, 1, 4, 2),
+    GemmConfig("gemv_mfma", 16, 32, 256, 1, 4, 2),
     # decode into the workspace first
-    GemmConfig("gemv_mfma", 16, 32, 64, 1, 4, 2),
     GemmConfig("gemm_mfma", 32, 128, 128, 3, 4, 3),
     GemmConfig("gemm_mfma", 64, 128, 64, 1, 4, 2),
     GemmConfig("gemm_mfma", 256, 192, 64, 2, 8, 3),
@@ -50,8 +50,6 @@ def _id(c: GemmConfig) -> str:
 
 
 def _m_list(cfg: GemmConfig) -> tuple[int, ...]:
-    if cfg.kernel == "gemv_dot":
-        return tuple(sorted({1, cfg.block_m}))
     return (1, cfg.block_m - 1, cfg.block_m + 3)
 
 
@@ -101,7 +99,7 @@ def test_rmsnorm_fp8_output_against_oracle(cfg: GemmConfig, device: torch.device
 
 @pytest.mark.parametrize(
     "cfg",
-    [GemmConfig("gemv_mfma", 16, 16, 128, 1, 16, 4), GemmConfig("gemv_mfma", 16, 32, 64, 1, 4, 2),
+    [GemmConfig("gemv_mfma", 16, 16, 128, 1, 16, 4), GemmConfig("gemv_mfma", 32, 32, 128, 1, 4, 2),
      GemmConfig("gemm_mfma", 256, 192, 64, 2, 8, 3)],
     ids=_id,
 )
@@ -138,7 +136,7 @@ def test_op_with_leading_dims_and_static_scale(device: torch.device) -> None:
     assert torch.equal(y.reshape(6, n), ref)
     with pytest.raises(TypeError, match="float8_e4m3fn"):
         w4a8_gemm_ex(c.reshape(6, k).view(torch.uint8), s, w.qweight_t, w.scales, w.qzeros, G,
-                     GemmConfig("gemv_dot", 1, 16, 128, 1, 4, 2))
+                     GemmConfig("gemv_mfma", 16, 16, 128, 1, 4, 2))
     with pytest.raises(ValueError, match="one per row"):
         w4a8_gemm_ex(c.reshape(6, k), torch.ones(4, device=device), w.qweight_t, w.scales, w.qzeros, G,
                      GemmConfig("gemv_mfma", 16, 16, 128, 1, 4, 2))

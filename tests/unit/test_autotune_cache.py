@@ -10,13 +10,13 @@ from pathlib import Path
 import pytest
 import torch
 
-from tokenforge_amd.kernels import autotune
-from tokenforge_amd.kernels.config import GemmConfig, candidate_configs, default_config
+from tokenforge.kernels import autotune
+from tokenforge.kernels.config import GemmConfig, candidate_configs, default_config
 
 GPU = "test-gpu-gfx950"
 N, K, G = 64, 256, 128
-TUNED_1 = GemmConfig("gemv_dot", 1, 32, 128, 1, 2, 2)
-TUNED_16 = GemmConfig("gemv_mfma", 16, 32, 128, 1, 4, 2)
+TUNED_1 = GemmConfig("gemv_mfma", 16, 32, 128, 1, 2, 2)
+TUNED_16 = GemmConfig("gemv_mfma", 32, 16, 128, 1, 4, 2)
 TUNED_256 = GemmConfig("gemm_mfma", 128, 128, 64, 2, 4, 2)
 
 
@@ -85,14 +85,14 @@ def _corruptions(path: Path) -> dict[str, str]:
         "bool_value": with_entry({**TUNED_1.to_dict(), "split_k": True}),
         "not_compiled": with_entry({**TUNED_1.to_dict(), "block_n": 48}),
         "wrong_family": with_entry(TUNED_256.to_dict()),
-        "block_m_too_small": with_entry({**TUNED_1.to_dict(), "block_m": 1}, "2:64:256:128"),
+        "gemv_above_its_buckets": with_entry(TUNED_1.to_dict(), "64:64:256:128"),
     }
 
 
 KINDS = [
     "truncated", "garbled", "empty", "not_object", "wrong_schema", "wrong_gpu", "wrong_abi",
     "bad_key", "bad_bucket", "bad_block_k", "unknown_field", "bool_value", "not_compiled",
-    "wrong_family", "block_m_too_small",
+    "wrong_family", "gemv_above_its_buckets",
 ]
 
 
@@ -101,7 +101,7 @@ def test_f4_corrupt_cache_is_discarded(kind: str, caplog: pytest.LogCaptureFixtu
     cache = _fresh_cache()
     _populated(cache)
     cache.path.write_bytes(_corruptions(cache.path)[kind].encode("utf-8", "surrogatepass"))
-    with caplog.at_level(logging.WARNING, logger="tokenforge_amd.kernels.autotune"):
+    with caplog.at_level(logging.WARNING, logger="tokenforge.kernels.autotune"):
         reloaded = _fresh_cache()
     assert reloaded.discarded_reason is not None
     assert len(reloaded) == 0, "a corrupt cache must be discarded whole"
@@ -144,7 +144,7 @@ def test_save_failure_leaves_previous_file(monkeypatch: pytest.MonkeyPatch) -> N
         raise OSError("disk full")
 
     monkeypatch.setattr(autotune.os, "replace", boom)
-    cache.put(2, N, K, G, GemmConfig("gemv_dot", 2, 16, 128, 1, 1, 2))
+    cache.put(2, N, K, G, GemmConfig("gemv_mfma", 16, 16, 128, 1, 1, 2))
     with pytest.raises(OSError, match="disk full"):
         cache.save()
     assert cache.path.read_text() == original
@@ -154,7 +154,7 @@ def test_save_failure_leaves_previous_file(monkeypatch: pytest.MonkeyPatch) -> N
 @pytest.mark.gpu
 def test_f4_retune_after_corruption_restores_outputs(caplog: pytest.LogCaptureFixture, device: torch.device) -> None:
     """Corrupt -> discard + warn -> retune -> same winner -> bit-identical kernel output."""
-    from tokenforge_amd.kernels.hip.w4a16 import w4a16_gemm
+    from tokenforge.kernels.hip.w4a16 import w4a16_gemm
 
     candidates = [TUNED_1, GemmConfig("gemv_mfma", 16, 16, 128, 1, 2, 2)]
     bench, _ = _fake_bench_prefers(TUNED_1)
@@ -187,7 +187,7 @@ def test_f4_retune_after_corruption_restores_outputs(caplog: pytest.LogCaptureFi
 @pytest.mark.gpu
 def test_real_tuning_picks_a_correct_config(device: torch.device) -> None:
     """tune_layer with the real event timer on a small layer: winners valid and cached."""
-    from tokenforge_amd.kernels.hip.w4a16 import w4a16_gemm
+    from tokenforge.kernels.hip.w4a16 import w4a16_gemm
 
     gpu = "tune-test-gfx950"
     winners = autotune.tune_layer(
@@ -205,7 +205,7 @@ def test_real_tuning_picks_a_correct_config(device: torch.device) -> None:
 
 
 def _cfgs(n: int) -> list[GemmConfig]:
-    return [GemmConfig("gemv_dot", 1, 16, 128, 1, w, s) for w in (1, 2, 4, 8) for s in (2, 4, 8)][:n]
+    return [GemmConfig("gemv_mfma", 16, 16, 128, 1, w, s) for w in (1, 2, 4, 8) for s in (2, 4, 8)][:n]
 
 
 def test_finalist_selection_prefers_the_steady_median_over_a_lucky_screen() -> None:

@@ -10,8 +10,8 @@ import ctypes
 import re
 from pathlib import Path
 
-from tokenforge_amd.kernels import _lib
-from tokenforge_amd.kernels.config import VARIANTS
+from tokenforge.kernels import _lib
+from tokenforge.kernels.config import VARIANTS
 
 INCLUDE = Path(__file__).resolve().parents[2] / "include"
 

@@ -11,8 +11,8 @@ import pytest
 import torch
 from safetensors.torch import save_file
 
-from tokenforge_amd.kernels import checkpoint as ck
-from tokenforge_amd.kernels.dispatch import HipUnavailableError
+from tokenforge.kernels import checkpoint as ck
+from tokenforge.kernels.dispatch import HipUnavailableError
 
 G = 128
 H, KV, INTER = 256, 64, 384

@@ -7,8 +7,8 @@ import pytest
 from hypothesis import given
 from hypothesis import strategies as st
 
-from tokenforge_amd.kernels import dispatch
-from tokenforge_amd.kernels.config import (
+from tokenforge.kernels import dispatch
+from tokenforge.kernels.config import (
     GEMM_MIN_M,
     GEMV_MAX_M,
     M_BUCKETS,
@@ -19,7 +19,7 @@ from tokenforge_amd.kernels.config import (
     family_for_bucket,
     m_bucket,
 )
-from tokenforge_amd.kernels.metrics import FALLBACKS, KERNEL_CALLS
+from tokenforge.kernels.metrics import FALLBACKS, KERNEL_CALLS
 
 
 @pytest.fixture(autouse=True)
@@ -79,8 +79,10 @@ def test_layer_support(n, k, group, dtype, arch, backend, expected) -> None:  # 
     ],
 )
 def test_select(m, backend, kernel, bucket) -> None:  # type: ignore[no-untyped-def]
-    d = dispatch.select(m, backend=backend, on_gpu=True, hip_ok=True)
-    assert (d.kernel, d.bucket) == (kernel, bucket)
+    d = dispatch.select(m, backend=backend, on_gpu=True, triton_ok=True, cuda_ext_available=True)
+    assert (d.kernel, d.bucket, d.fallback) == (kernel, bucket, None)
+    # hip_ok is this build's name for the same flag; either keyword may be given.
+    assert dispatch.select(m, backend=backend, on_gpu=True, hip_ok=True) == d
 
 
 def test_lookup_bucket_clamps_above_largest() -> None:
@@ -88,25 +90,44 @@ def test_lookup_bucket_clamps_above_largest() -> None:
     assert dispatch.lookup_bucket(17) == 32
 
 
-def test_select_without_gpu_raises_instead_of_falling_back() -> None:
+def test_select_without_gpu_is_the_reference_decision() -> None:
+    """The reference's table (test_dispatch.py:75-80): a call that cannot run the compiled
+    kernels is a ``torch_reference`` decision, with the reference's keyword call."""
+    d = dispatch.select(8, backend="triton", on_gpu=False, triton_ok=False, cuda_ext_available=False)
+    assert d.kernel == "torch_reference"
+    assert dispatch.select(8, backend="hip", on_gpu=True, triton_ok=False).kernel == "torch_reference"
+    assert dispatch.select(8, backend="hip", on_gpu=True, hip_ok=False).kernel == "torch_reference"
+    # cuda_ext_available names the reference's separate CUDA GEMV extension; the HIP library is
+    # this build's one compiled extension, so the flag never splits the decision.
+    d = dispatch.select(2, backend="cuda", on_gpu=True, triton_ok=True, cuda_ext_available=False)
+    assert (d.kernel, d.fallback) == ("hip_gemv", None)
+
+
+def test_torch_reference_decision_raises_at_the_op() -> None:
+    """This build has no CPU path: the op turns a torch_reference decision into an error."""
+    d = dispatch.select(8, backend="hip", on_gpu=False, triton_ok=False)
     with pytest.raises(dispatch.HipUnavailableError, match="CPU"):
-        dispatch.select(8, backend="hip", on_gpu=False, hip_ok=False)
+        dispatch.require_gpu_decision(d, on_gpu=False)
+    d = dispatch.select(8, backend="hip", on_gpu=True, triton_ok=False)
     with pytest.raises(dispatch.HipUnavailableError, match="library"):
-        dispatch.select(8, backend="hip", on_gpu=True, hip_ok=False)
+        dispatch.require_gpu_decision(d, on_gpu=True)
+    dispatch.require_gpu_decision(dispatch.select(8, backend="hip", on_gpu=True, triton_ok=True), on_gpu=True)
 
 
 def test_select_rejects_marlin_per_call() -> None:
     with pytest.raises(ValueError, match="per layer"):
-        dispatch.select(1, backend="marlin", on_gpu=True, hip_ok=True)
+        dispatch.select(1, backend="marlin", on_gpu=True, triton_ok=True, cuda_ext_available=True)
 
 
 def test_record_counts_calls_and_layer_fallbacks() -> None:
-    d = dispatch.select(2, backend="hip", on_gpu=True, hip_ok=True)
+    d = dispatch.select(2, backend="hip", on_gpu=True, triton_ok=True, cuda_ext_available=True)
     dispatch.record(d)
     dispatch.record(d)
     assert KERNEL_CALLS.value(kernel="hip_gemv", bucket="2") == 2
     dispatch.record_layer_fallback("unsupported_shape")
     assert FALLBACKS.value(reason="unsupported_shape") == 1
+    dispatch.record(dispatch.Decision("hip_gemv", "4", fallback="cuda_ext_unavailable"))
+    assert FALLBACKS.value(reason="cuda_ext_unavailable") == 1
 
 
 def test_backend_from_env(monkeypatch: pytest.MonkeyPatch) -> None:
@@ -153,17 +174,18 @@ def test_candidates_are_valid(bucket: int, group: int) -> None:
         assert families == {"gemv", "gemm"}
 
 
-def test_decode_buckets_offer_both_gemv_kernels() -> None:
-    kinds = {c.kernel for c in candidate_configs(1, 128)}
-    assert kinds == {"gemv_dot", "gemv_mfma"}
-    assert {c.kernel for c in candidate_configs(8, 128)} == {"gemv_mfma"}
+def test_decode_buckets_offer_both_gemv_work_splits() -> None:
+    cands = candidate_configs(1, 128)
+    assert {c.kernel for c in cands} == {"gemv_mfma"}
+    assert {c.block_k for c in cands} == {128, 256}  # K split over the waves, or columns split
+    assert {c.block_m for c in candidate_configs(32, 128) if c.family == "gemv"} == {16, 32}
 
 
 @pytest.mark.parametrize(
     ("kwargs", "match"),
     [
         ({"kernel": "gemv_triton", "block_m": 1, "block_n": 16, "block_k": 128}, "kernel"),
-        ({"kernel": "gemv_dot", "block_m": 3, "block_n": 16, "block_k": 128, "num_warps": 1, "num_stages": 1}, "compiled variant"),
+        ({"kernel": "gemv_mfma", "block_m": 48, "block_n": 16, "block_k": 128, "num_warps": 1, "num_stages": 1}, "compiled variant"),
         ({"kernel": "gemm_mfma", "block_m": 64, "block_n": 64, "block_k": 256}, "divide"),
         ({"kernel": "gemm_mfma", "block_m": 64, "block_n": 64, "block_k": 64, "split_k": 0}, "split_k"),
         ({"kernel": "gemv_mfma", "block_m": 16, "block_n": 16, "block_k": 128, "split_k": 2}, "split_k"),
@@ -177,8 +199,8 @@ def test_config_validation(kwargs: dict, match: str) -> None:
 
 
 def test_config_from_dict_strict() -> None:
-    good = GemmConfig("gemv_dot", 1, 16, 128, 1, 1, 2).to_dict()
-    assert GemmConfig.from_dict(good) == GemmConfig("gemv_dot", 1, 16, 128, 1, 1, 2)
+    good = GemmConfig("gemv_mfma", 16, 16, 128, 1, 1, 2).to_dict()
+    assert GemmConfig.from_dict(good) == GemmConfig("gemv_mfma", 16, 16, 128, 1, 1, 2)
     with pytest.raises(ValueError, match="unknown"):
         GemmConfig.from_dict({**good, "block_q": 1})
     with pytest.raises(TypeError, match="integers"):

@@ -62,9 +62,9 @@ def test_config2_fixture_matches_oracle() -> None:
 
 @pytest.mark.gpu
 def test_gpu_kernels_match_fixtures(device: torch.device) -> None:
-    import tokenforge_amd.kernels.ops  # noqa: F401
-    from tokenforge_amd.kernels import pack as tp
-    from tokenforge_amd.kernels.hip.rmsnorm_fp8 import e4m3_encode, rmsnorm_fp8_quant
+    import tokenforge.kernels.ops  # noqa: F401
+    from tokenforge.kernels import pack as tp
+    from tokenforge.kernels.hip.rmsnorm_fp8 import e4m3_encode, rmsnorm_fp8_quant
     from tests.numerics.tolerance import atol
 
     codes = np.array(GOLDEN["e4m3"]["codes"], dtype=np.uint8)
@@ -79,7 +79,11 @@ def test_gpu_kernels_match_fixtures(device: torch.device) -> None:
     g1 = GOLDEN["gemv_config1"]
     qweight, qzeros, scales, x = MG.config1_inputs()
     w = tp.pack_awq(*(torch.from_numpy(a).to(device) for a in (qweight, qzeros, scales)), 128)
-    assert _sha(w.qweight_t.cpu().numpy()) == g1["sha256_qweight_t"]
+    tiled = P.pack_awq_tiles(qweight, qzeros, scales, 128)
+    assert np.array_equal(w.qweight_t.cpu().numpy(), tiled.qweight_t)
+    # Undoing the tile layout gives the reference's TokenForge layout of the fixture.
+    back = P.tile_unpack(w.qweight_t.cpu().numpy(), w.scales.cpu().numpy(), w.qzeros.cpu().numpy(), 128)
+    assert _sha(back[0]) == g1["sha256_qweight_t"]
     y = torch.ops.tokenforge.w4a16_linear(torch.from_numpy(x).to(device), w.qweight_t, w.scales, w.qzeros,
                                           None, 128, "hip").cpu().numpy().astype(np.float64)
     tol = atol(x, P.dequantize_tf(P.pack_awq(qweight, qzeros, scales, 128)), "cuda")

@@ -1,0 +1,78 @@
+"""The shape table, the tolerance constants and the counters the parity tests rely on."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from tests.numerics import shapes
+from tests.numerics.calibrate import round_up_2sig
+from tests.numerics.tolerance import EPS_FP16, Calibration, atol, error_scale, normwise
+from tokenforge.kernels.metrics import LabeledCounter
+
+
+def test_qwen_shapes_match_the_model_dimensions() -> None:
+    got = {(s.layer, s.n, s.k) for s in shapes.decoder_linears("qwen2.5-7b")}
+    assert got == {
+        ("qkv_proj", 4608, 3584), ("o_proj", 3584, 3584),
+        ("gate_up_proj", 37888, 3584), ("down_proj", 3584, 18944),
+    }
+    small = {(s.layer, s.n, s.k) for s in shapes.decoder_linears("qwen2.5-0.5b")}
+    assert small == {
+        ("qkv_proj", 1152, 896), ("o_proj", 896, 896),
+        ("gate_up_proj", 9728, 896), ("down_proj", 896, 4864),
+    }
+    for s in shapes.ragged_linears():
+        assert s.n % 16 == 8  # a multiple of 8 that no 16-column tile divides
+
+
+def test_suite_selection(monkeypatch: pytest.MonkeyPatch) -> None:
+    monkeypatch.delenv("TOKENFORGE_SHAPE_SUITE", raising=False)
+    assert {s.model for s in shapes.linear_shapes()} == {"qwen2.5-0.5b", "synthetic"}
+    assert shapes.m_values() == (1, 3, 8, 16, 31, 129)
+    monkeypatch.setenv("TOKENFORGE_SHAPE_SUITE", "full")
+    assert {s.model for s in shapes.linear_shapes()} == {"qwen2.5-0.5b", "qwen2.5-7b", "synthetic"}
+    assert 256 in shapes.m_values()
+
+
+def test_error_scale_and_frozen_constants() -> None:
+    x = np.array([[1.0, -3.0, 2.0, 0.5]])
+    w = np.array([[0.25, -0.5, 0.1, 0.0]])
+    assert error_scale(x, w) == pytest.approx(2.0 * EPS_FP16 * 3.0 * 0.5)
+    x_inf = np.array([[np.inf, -3.0, 2.0, 0.5]])
+    assert error_scale(x_inf, w) == error_scale(x, w)  # non-finite entries are left out
+    for dev in ("cpu", "cuda"):
+        assert Calibration.load(dev).c == 0.13
+        assert atol(x, w, dev) == pytest.approx(0.13 * error_scale(x, w))
+    with pytest.raises(LookupError, match="calibrate"):
+        Calibration.load("tpu")
+
+
+def test_normwise_and_rounding_of_c() -> None:
+    ref = np.array([1.0, -4.0, np.nan])
+    assert normwise(np.array([1.02, -4.0, 0.0]), ref) == pytest.approx(0.02 / 4.0)
+    assert round_up_2sig(0.1245726352188545) == 0.13
+    assert round_up_2sig(0.13) == 0.13
+    assert round_up_2sig(0.0071) == 0.0071
+    assert round_up_2sig(2.01) == 2.1
+
+
+def test_labeled_counter() -> None:
+    c = LabeledCounter("tokenforge_test_counter", "test", ("kernel", "bucket"))
+    c.inc(kernel="hip_gemv", bucket="1")
+    c.inc(2.0, kernel="hip_gemv", bucket="1")
+    c.inc(kernel="hip_gemm", bucket="256")
+    assert c.value(kernel="hip_gemv", bucket="1") == 3.0
+    assert c.value(kernel="hip_gemm", bucket="1") == 0.0
+    assert c.total() == 4.0
+    assert c.snapshot() == {("hip_gemv", "1"): 3.0, ("hip_gemm", "256"): 1.0}
+    with pytest.raises(ValueError, match="missing"):
+        c.inc(kernel="hip_gemv")
+    with pytest.raises(ValueError, match="unexpected"):
+        c.value(kernel="hip_gemv", bucket="1", reason="x")
+    c.reset()
+    assert c.total() == 0.0
+    # A second family of the same name (a module imported twice) shares the exporter.
+    again = LabeledCounter("tokenforge_test_counter", "test", ("kernel", "bucket"))
+    again.inc(kernel="hip_gemv", bucket="1")
+    assert again.value(kernel="hip_gemv", bucket="1") == 1.0

@@ -10,9 +10,9 @@ import pytest
 import torch
 from torch.library import opcheck
 
-import tokenforge_amd.kernels.ops  # noqa: F401
+import tokenforge.kernels.ops  # noqa: F401
 from tests.numerics import cases
-from tokenforge_amd.kernels.metrics import KERNEL_CALLS
+from tokenforge.kernels.metrics import KERNEL_CALLS
 
 G = cases.GROUP_SIZE
 OPCHECK_TESTS = ("test_schema", "test_faketensor", "test_aot_dispatch_dynamic")

@@ -107,12 +107,12 @@ def test_repack_brute_force_single_nibbles() -> None:
             assert np.count_nonzero(qt) == 1
 
 
-def _random_awq(n: int, k: int, seed: int) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+def _random_awq(n: int, k: int, seed: int, group: int = G) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
     rng = np.random.default_rng(seed)
     intweight = rng.integers(0, 16, (k, n), dtype=np.int32)
-    zeros = rng.integers(0, 16, (k // G, n), dtype=np.int32)
+    zeros = rng.integers(0, 16, (k // group, n), dtype=np.int32)
     zeros[0, 0], zeros[-1, -1] = 0, 15
-    scales = (rng.random((k // G, n), dtype=np.float32) * 0.01 + 1e-3).astype(np.float16)
+    scales = (rng.random((k // group, n), dtype=np.float32) * 0.01 + 1e-3).astype(np.float16)
     qweight, qzeros = P.awq_pack(intweight, zeros)
     return qweight, qzeros, scales
 
@@ -203,6 +203,70 @@ def test_validate_awq_rejects_group_and_k() -> None:
         P.validate_awq(qweight[:-8], qzeros, scales, G)
 
 
+# ------------------------------------------------------------------ gfx950 tile layout (oracle)
+
+TILE_SHAPES = [(16, 128, 128), (8, 32, 32), (24, 96, 32), (40, 192, 64), (200, 256, 128), (48, 160, 32), (64, 384, 64)]
+
+
+@pytest.mark.parametrize(("n", "k", "group"), TILE_SHAPES)
+def test_tile_layout_formula_matches_its_storage_order(n: int, k: int, group: int) -> None:
+    """The closed-form positions equal the storage order that defines the layout (tile by
+    tile, K step by step, chunk column by column, row by row), for every chunk, scale and zero
+    word, so each map is a bijection."""
+    q_total, p_total = k // 32, k // group
+    for i, (row, q) in enumerate(P.tile_order_chunks(n, q_total)):
+        assert P.tile_chunk_index(np.array(row), np.array(q), n, q_total) == i
+    assert len(P.tile_order_chunks(n, q_total)) == n * q_total
+    for i, (grp, row) in enumerate(P.tile_order_scales(n, p_total)):
+        assert P.tile_scale_index(np.array(grp), np.array(row), n, p_total) == i
+    for i, (grp, word) in enumerate(P.tile_order_zeros(n, p_total)):
+        assert P.tile_zero_index(np.array(grp), np.array(word), n, p_total) == i
+    assert len(P.tile_order_zeros(n, p_total)) == p_total * n // 8
+
+
+@pytest.mark.parametrize(("n", "k", "group"), TILE_SHAPES)
+def test_tile_layout_round_trip_and_content(n: int, k: int, group: int) -> None:
+    rng = np.random.default_rng(n * 31 + k)
+    qw = rng.integers(-(2**31), 2**31 - 1, (n, k // 8), dtype=np.int64).astype(np.int32)
+    sc = rng.random((k // group, n)).astype(np.float16)
+    qz = rng.integers(-(2**31), 2**31 - 1, (k // group, n // 8), dtype=np.int64).astype(np.int32)
+    tiled = P.tile_pack(qw, sc, qz, group)
+    assert [t.shape for t in tiled] == [qw.shape, sc.shape, qz.shape]
+    back = P.tile_unpack(*tiled, group)
+    assert all(np.array_equal(a, b) for a, b in zip(back, (qw, sc, qz)))
+    # Chunk content is untouched: the multiset of 16-byte chunks is the same.
+    rows = lambda a: sorted(map(bytes, a.reshape(-1, 4)))  # noqa: E731
+    assert rows(tiled[0]) == rows(qw)
+
+
+def test_tile_layout_step_blocks_are_the_mfma_operand() -> None:
+    """A full tile's 128-wide K step is one contiguous 1 KB block whose 16-byte slot l holds
+    row l % 16, K offsets 128 j + 32 (l // 16) .. + 31: the B operand of lane l."""
+    n, k = 48, 512
+    rng = np.random.default_rng(1)
+    vals = rng.integers(0, 16, (n, k), dtype=np.int32)
+    qw = P.pack_int4(vals)  # TokenForge layout [N, K/8]
+    tiled, _, _ = P.tile_pack(qw, np.zeros((k // 128, n), np.float16), np.zeros((k // 128, n // 8), np.int32), 128)
+    flat = tiled.reshape(-1, 4)  # 16-byte slots
+    q_total = k // 32
+    for t in range(n // 16):
+        for j in range(k // 128):
+            block = flat[16 * t * q_total + 64 * j: 16 * t * q_total + 64 * (j + 1)]
+            for lane in range(64):
+                row, g = 16 * t + lane % 16, lane // 16
+                want = vals[row, 128 * j + 32 * g: 128 * j + 32 * g + 32]
+                assert np.array_equal(P.unpack_int4(block[lane]), want)
+
+
+def test_tile_layout_pack_awq_tiles_dequantizes_like_the_reference() -> None:
+    qweight, qzeros, scales = _random_awq(n=40, k=256, seed=3, group=64)
+    tiled = P.pack_awq_tiles(qweight, qzeros, scales, 64)
+    back = P.tile_unpack(tiled.qweight_t, tiled.scales, tiled.qzeros, 64)
+    ref = P.pack_awq(qweight, qzeros, scales, 64)
+    assert np.array_equal(back[0], ref.qweight_t)
+    assert np.array_equal(back[2], ref.qzeros)
+
+
 # ------------------------------------------------------------------ product on the GPU
 
 
@@ -213,7 +277,7 @@ def _t(a: np.ndarray, device: torch.device) -> torch.Tensor:
 @pytest.mark.gpu
 @pytest.mark.parametrize(("k", "n"), [(8, 8), (128, 64), (264, 200), (384, 1000), (2048, 520), (4096, 256)])
 def test_gpu_repack_bit_exact(k: int, n: int, device: torch.device) -> None:
-    from tokenforge_amd.kernels import pack as tp
+    from tokenforge.kernels import pack as tp
 
     rng = np.random.default_rng(k * 7 + n)
     qweight = rng.integers(-(2**31), 2**31 - 1, (k, n // 8), dtype=np.int64).astype(np.int32)
@@ -225,7 +289,7 @@ def test_gpu_repack_bit_exact(k: int, n: int, device: torch.device) -> None:
 
 @pytest.mark.gpu
 def test_gpu_pack_unpack_and_range_check(device: torch.device) -> None:
-    from tokenforge_amd.kernels import pack as tp
+    from tokenforge.kernels import pack as tp
 
     rng = np.random.default_rng(0)
     values = rng.integers(0, 16, (37, 96), dtype=np.int32)
@@ -243,30 +307,66 @@ def test_gpu_pack_unpack_and_range_check(device: torch.device) -> None:
 
 
 @pytest.mark.gpu
-def test_gpu_pack_awq_and_dequant_bit_exact(device: torch.device) -> None:
-    from tokenforge_amd.kernels import pack as tp
+@pytest.mark.parametrize(("n", "k", "group"), [(200, 3 * G, G), (64, 96, 32), (40, 192, 64), (256, 4 * G, G)])
+def test_gpu_pack_awq_tile_layout_and_dequant_bit_exact(n: int, k: int, group: int, device: torch.device) -> None:
+    """pack_awq emits the gfx950 tile layout bit for bit as the oracle restates it (ragged N,
+    K not a multiple of 128), unpack_to_awq inverts it, and the dequant reading the tile layout
+    equals the reference's dequantize_tf on the TokenForge layout."""
+    from tokenforge.kernels import pack as tp
 
-    qweight, qzeros, scales = _random_awq(n=200, k=3 * G, seed=11)
-    w = tp.pack_awq(_t(qweight, device), _t(qzeros, device), _t(scales, device), G)
-    ow = P.pack_awq(qweight, qzeros, scales, G)
+    qweight, qzeros, scales = _random_awq(n=n, k=k, seed=11 + n, group=group)
+    w = tp.pack_awq(_t(qweight, device), _t(qzeros, device), _t(scales, device), group)
+    ow = P.pack_awq_tiles(qweight, qzeros, scales, group)
     assert np.array_equal(w.qweight_t.cpu().numpy(), ow.qweight_t)
-    assert np.array_equal(tp.dequantize_tf(w).cpu().numpy(), P.dequantize_tf(ow))
+    assert np.array_equal(w.scales.cpu().numpy().view(np.uint16), ow.scales.view(np.uint16))
+    assert np.array_equal(w.qzeros.cpu().numpy(), ow.qzeros)
+    assert (w.n, w.k) == (n, k)
+    ref = P.dequantize_tf(P.pack_awq(qweight, qzeros, scales, group))
+    assert np.array_equal(tp.dequantize_tf(w).cpu().numpy().view(np.uint16), ref.view(np.uint16))
     assert np.array_equal(
-        tp.awq_dequantize(_t(qweight, device), _t(qzeros, device), _t(scales, device), G).cpu().numpy(),
-        P.awq_dequantize(qweight, qzeros, scales, G),
+        tp.awq_dequantize(_t(qweight, device), _t(qzeros, device), _t(scales, device), group).cpu().numpy(),
+        P.awq_dequantize(qweight, qzeros, scales, group),
     )
     back = tp.unpack_to_awq(w)
     assert np.array_equal(back[0].cpu().numpy(), qweight)
+    assert np.array_equal(back[1].cpu().numpy(), qzeros)
+    assert np.array_equal(back[2].cpu().numpy().view(np.uint16), scales.view(np.uint16))
     with pytest.raises(ValueError, match="qzeros shape"):
-        tp.pack_awq(_t(qweight, device), _t(qzeros[:1], device), _t(scales, device), G)
+        tp.pack_awq(_t(qweight, device), _t(qzeros[:1], device), _t(scales, device), group)
 
 
 @pytest.mark.gpu
-def test_gpu_cpu_tensor_raises() -> None:
-    from tokenforge_amd.kernels import pack as tp
+def test_gpu_load_time_functions_accept_host_tensors(device: torch.device) -> None:
+    """Like the reference's, the load-time functions take host tensors: the kernel runs on the
+    GPU and the result comes back on the host, bit-exact."""
+    from tokenforge.kernels import pack as tp
 
-    with pytest.raises(RuntimeError, match="CPU|cpu"):
-        tp.repack_awq_to_tf(torch.zeros((8, 1), dtype=torch.int32))
+    qweight, qzeros, scales = _random_awq(n=64, k=2 * G, seed=5)
+    qt = tp.repack_awq_to_tf(torch.from_numpy(qweight))
+    assert qt.device.type == "cpu" and np.array_equal(qt.numpy(), P.repack_awq_to_tf(qweight))
+    w = tp.pack_awq(torch.from_numpy(qweight), torch.from_numpy(qzeros), torch.from_numpy(scales), G)
+    assert w.qweight_t.device.type == "cpu"
+    assert np.array_equal(w.qweight_t.numpy(), P.pack_awq_tiles(qweight, qzeros, scales, G).qweight_t)
+    assert np.array_equal(tp.dequantize_tf(w).numpy(), P.dequantize_tf(P.pack_awq(qweight, qzeros, scales, G)))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize(("n", "k", "group"), [(64, 256, 128), (200, 384, 64), (48, 96, 32), (1024, 1024, 128)])
+def test_gpu_awq_quantize_bit_exact(n: int, k: int, group: int, device: torch.device) -> None:
+    """awq_quantize (pack.py:83-107) on the GPU equals the oracle's fp32 restatement bit for bit,
+    on the device and from host tensors."""
+    from tokenforge.kernels import pack as tp
+
+    gen = torch.Generator().manual_seed(n + k + group)
+    weight = torch.randn((n, k), generator=gen) * 0.02
+    weight[0, :group] = 0.0  # a constant group: the 1e-5 clamp of the range
+    want = P.awq_quantize(weight.numpy(), group)
+    for got in (tp.awq_quantize(weight.to(device), group), tp.awq_quantize(weight, group)):
+        assert np.array_equal(got[0].cpu().numpy(), want[0])
+        assert np.array_equal(got[1].cpu().numpy(), want[1])
+        assert np.array_equal(got[2].cpu().numpy().view(np.uint16), want[2].view(np.uint16))
+    with pytest.raises(ValueError, match="multiple of group_size"):
+        tp.awq_quantize(weight[:, :-8].to(device), group)
 
 
 @pytest.mark.gpu
@@ -276,8 +376,17 @@ def test_gpu_cpu_tensor_raises() -> None:
 )
 def test_gpu_repack_qwen7b_full_size(layer: str, n: int, k: int, device: torch.device) -> None:
     """AWQ repack of every Qwen2.5-7B decoder linear, bit-exact."""
-    from tokenforge_amd.kernels import pack as tp
+    from tokenforge.kernels import pack as tp
 
     qweight, qzeros, scales = cases.baseline_layer(n, k, seed=0)
     qt = tp.repack_awq_to_tf(_t(qweight, device)).cpu().numpy()
     assert np.array_equal(qt, P.repack_awq_to_tf(qweight)), layer
+    # ... and pack_awq's tile layout, bit-exact, with an exact round trip back to AWQ.
+    w = tp.pack_awq(_t(qweight, device), _t(qzeros, device), _t(scales, device), G)
+    want = P.tile_pack(qt, scales, qzeros, G)
+    assert np.array_equal(w.qweight_t.cpu().numpy(), want[0]), layer
+    assert np.array_equal(w.scales.cpu().numpy().view(np.uint16), want[1].view(np.uint16)), layer
+    assert np.array_equal(w.qzeros.cpu().numpy(), want[2]), layer
+    back = tp.unpack_to_awq(w)
+    for got, ref in zip(back, (qweight, qzeros, scales)):
+        assert np.array_equal(got.cpu().numpy().view(np.int16), ref.view(np.int16)), layer

@@ -9,10 +9,10 @@ from __future__ import annotations
 
 import torch
 
-from tokenforge_amd.kernels import autotune
-from tokenforge_amd.kernels.config import GEMV_MAX_M, m_bucket
-from tokenforge_amd.kernels.device import gpu_identity
-from tokenforge_amd.kernels.hip.w4a16 import w4a16_gemm
+from tokenforge.kernels import autotune
+from tokenforge.kernels.config import GEMV_MAX_M, m_bucket
+from tokenforge.kernels.device import gpu_identity
+from tokenforge.kernels.hip.w4a16 import w4a16_gemm
 
 
 def w4a16_gemv(

@@ -1,14 +1,15 @@
 """L1 kernels on MI355X: W4A16 GEMV/GEMM, fused RMSNorm + FP8 quant, AWQ repacking, dispatch.
 
 Drop-in for the reference's ``tokenforge.kernels`` package (``tokenforge/kernels/__init__.py``).
-Importing :mod:`tokenforge_amd.kernels.ops` registers the ``torch.ops.tokenforge`` namespace.
+Importing :mod:`tokenforge.kernels.ops` registers the ``torch.ops.tokenforge`` namespace.
 """
 
-from tokenforge_amd.kernels.pack import (
+from tokenforge.kernels.pack import (
     AWQ_ORDER,
     AWQ_REVERSE_ORDER,
     W4A16Weights,
     awq_dequantize,
+    awq_quantize,
     dequantize_tf,
     pack_awq,
     unpack_to_awq,
@@ -19,6 +20,7 @@ __all__ = [
     "AWQ_REVERSE_ORDER",
     "W4A16Weights",
     "awq_dequantize",
+    "awq_quantize",
     "dequantize_tf",
     "pack_awq",
     "unpack_to_awq",

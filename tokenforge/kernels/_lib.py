@@ -12,18 +12,18 @@ import functools
 import os
 from pathlib import Path
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 """Must equal ``tf_abi_version()`` of the loaded library."""
 
 LIB_ENV = "TOKENFORGE_HIP_LIB"
-LIB_PATH = Path(__file__).resolve().parent.parent / "lib" / "libtokenforge_hip.so"
+LIB_PATH = Path(__file__).resolve().parents[2] / "tokenforge_amd" / "lib" / "libtokenforge_hip.so"
 
 TF_OK = 0
 TF_EINVAL = 1
 TF_ELAUNCH = 2
 TF_ERANGE = 3
 
-KERNEL_IDS = {"gemv_dot": 0, "gemv_mfma": 1, "gemm_mfma": 2}
+KERNEL_IDS = {"gemv_mfma": 1, "gemm_mfma": 2}
 EPILOGUE_NONE = 0
 EPILOGUE_RESIDUAL = 1
 EPILOGUE_SILU_MUL = 2
@@ -65,6 +65,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "tf_unpack_int4": (ctypes.c_int, [_p, _p, _i64, _i64, _p]),
     "tf_awq_to_tf": (ctypes.c_int, [_p, _p, _i64, _i64, _p]),
     "tf_tf_to_awq": (ctypes.c_int, [_p, _p, _i64, _i64, _p]),
+    "tf_tile_pack": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _p]),
+    "tf_tile_unpack": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _p]),
+    "tf_awq_quantize": (ctypes.c_int, [_p, _i64, _i64, _i32, _p, _p, _p, _p]),
     "tf_w4a16_dequant": (ctypes.c_int, [_p, _p, _p, _p, _i64, _i64, _i32, _p]),
     "tf_num_variants": (ctypes.c_int, []),
     "tf_get_variant": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(TfGemmConfig)]),
@@ -104,7 +107,7 @@ def lib() -> ctypes.CDLL:
     if not path.exists():
         raise HipLibraryError(
             f"{path} is missing: build it with `python -m tokenforge_amd.build` "
-            "(tokenforge_amd has no CPU or fallback path)"
+            "(tokenforge.kernels has no CPU or fallback path)"
         )
     try:
         handle = ctypes.CDLL(str(path))

@@ -43,8 +43,8 @@ from typing import Any, Final
 
 import torch
 
-from tokenforge_amd.kernels import _lib
-from tokenforge_amd.kernels.config import M_BUCKETS, GemmConfig, candidate_configs, default_config
+from tokenforge.kernels import _lib
+from tokenforge.kernels.config import M_BUCKETS, GemmConfig, candidate_configs, default_config
 
 log = logging.getLogger(__name__)
 
@@ -73,40 +73,81 @@ class CacheRejectedError(ValueError):
     """The on-disk cache failed validation."""
 
 
-def _parse_entries(raw: Any) -> dict[str, GemmConfig]:
+def _decode_key(key: object) -> tuple[int, int, int, int]:
+    """``"{bucket}:{n}:{k}:{group}"`` -> its four integers, or CacheRejectedError."""
+    fields = key.split(":") if isinstance(key, str) else ()
+    if len(fields) != 4 or not all(f.isdigit() for f in fields):
+        raise CacheRejectedError(f"malformed key {key!r}")
+    bucket, n, k, group = map(int, fields)
+    if bucket not in M_BUCKETS or min(n, k, group) <= 0 or k % group:
+        raise CacheRejectedError(f"impossible key {key!r}")
+    return bucket, n, k, group
+
+
+def _decode_config(key: str, bucket: int, group: int, raw: object) -> GemmConfig:
+    try:
+        cfg = GemmConfig.from_dict(raw)
+        cfg.validate(group)
+    except (TypeError, ValueError) as exc:
+        raise CacheRejectedError(f"invalid config for {key!r}: {exc}") from exc
+    if not cfg.fits_bucket(bucket):
+        raise CacheRejectedError(f"{cfg.kernel} block_m={cfg.block_m} does not fit bucket {bucket}")
+    return cfg
+
+
+def _decode_document(text: str, gpu: str, abi: str) -> dict[str, GemmConfig]:
+    """Parse and check a whole cache file; any problem rejects all of it."""
+    try:
+        doc = json.loads(text)
+    except json.JSONDecodeError as exc:
+        raise CacheRejectedError(f"not JSON: {exc}") from exc
+    if not isinstance(doc, dict):
+        raise CacheRejectedError("top level is not an object")
+    header = (("schema", SCHEMA_VERSION, "schema"), ("gpu", gpu, "gpu"), ("hip", abi, "kernel ABI"))
+    for field, expected, what in header:
+        if doc.get(field) != expected:
+            raise CacheRejectedError(f"{what} {doc.get(field)!r} != {expected!r} of this process")
+    raw = doc.get("entries")
     if not isinstance(raw, dict):
         raise CacheRejectedError("'entries' is not an object")
-    entries: dict[str, GemmConfig] = {}
+    table: dict[str, GemmConfig] = {}
     for key, value in raw.items():
-        parts = key.split(":") if isinstance(key, str) else []
-        if len(parts) != 4 or not all(p.isdigit() for p in parts):
-            raise CacheRejectedError(f"malformed key {key!r}")
-        bucket, n, k, group = (int(p) for p in parts)
-        if bucket not in M_BUCKETS or n <= 0 or k <= 0 or group <= 0 or k % group:
-            raise CacheRejectedError(f"impossible key {key!r}")
-        try:
-            cfg = GemmConfig.from_dict(value)
-            cfg.validate(group)
-        except (TypeError, ValueError) as exc:
-            raise CacheRejectedError(f"invalid config for {key!r}: {exc}") from exc
-        if not cfg.fits_bucket(bucket):
-            raise CacheRejectedError(f"{cfg.kernel} block_m={cfg.block_m} does not fit bucket {bucket}")
-        entries[key] = cfg
-    return entries
+        bucket, _n, _k, group = _decode_key(key)
+        table[key] = _decode_config(key, bucket, group, value)
+    return table
 
 
-def atomic_write_json(path: Path, payload: Any) -> None:
+def _encode_document(gpu: str, abi: str, table: dict[str, GemmConfig]) -> str:
+    doc = {
+        "schema": SCHEMA_VERSION,
+        "gpu": gpu,
+        "hip": abi,
+        "torch": torch.__version__,
+        "entries": {key: table[key].to_dict() for key in sorted(table)},
+    }
+    return json.dumps(doc, indent=1, sort_keys=True) + "\n"
+
+
+def _replace_file(path: Path, text: str) -> None:
+    """Write ``text`` to ``path`` so a reader sees the old file or the whole new one: a
+    temporary file in the same directory is synced, renamed over ``path``, and the directory
+    entry is synced. A failure removes the temporary file and leaves ``path`` untouched."""
     path.parent.mkdir(parents=True, exist_ok=True)
-    fd, tmp = tempfile.mkstemp(prefix=f".{path.name}.", suffix=".tmp", dir=path.parent)
+    with tempfile.NamedTemporaryFile(
+        "w", encoding="utf-8", dir=path.parent, prefix=f".{path.name}.", suffix=".tmp", delete=False
+    ) as tmp:
+        staged = Path(tmp.name)
+        try:
+            tmp.write(text)
+            tmp.flush()
+            os.fsync(tmp.fileno())
+        except BaseException:
+            staged.unlink(missing_ok=True)
+            raise
     try:
-        with os.fdopen(fd, "w", encoding="utf-8") as f:
-            json.dump(payload, f, indent=1, sort_keys=True)
-            f.write("\n")
-            f.flush()
-            os.fsync(f.fileno())
-        os.replace(tmp, path)
+        os.replace(staged, path)
     except BaseException:
-        Path(tmp).unlink(missing_ok=True)
+        staged.unlink(missing_ok=True)
         raise
     dir_fd = os.open(path.parent, os.O_RDONLY)
     try:
@@ -116,99 +157,81 @@ def atomic_write_json(path: Path, payload: Any) -> None:
 
 
 class AutotuneCache:
+    """The tuned configs of one (GPU, kernel ABI) pair, backed by one JSON file."""
+
     def __init__(self, path: Path, gpu: str, abi: str) -> None:
         self.path = path
         self.gpu = gpu
         self.abi = abi
-        self._entries: dict[str, GemmConfig] = {}
-        self._lock = threading.Lock()
         self.discarded_reason: str | None = None
+        self._table: dict[str, GemmConfig] = {}
+        self._mutex = threading.Lock()
 
     def load(self) -> None:
-        """Populate from disk. Missing file: empty cache. Invalid file: discard and warn."""
+        """Read the file: a missing file is an empty cache, an invalid one is discarded whole."""
         self.discarded_reason = None
         try:
-            text = self.path.read_text(encoding="utf-8")
+            table = _decode_document(self.path.read_text(encoding="utf-8"), self.gpu, self.abi)
         except FileNotFoundError:
-            self._entries = {}
-            return
+            table = {}
         except (OSError, UnicodeDecodeError) as exc:
-            self._discard(f"unreadable: {exc}")
+            self._reject(f"unreadable: {exc}")
             return
-        try:
-            doc = json.loads(text)
-            if not isinstance(doc, dict):
-                raise CacheRejectedError("top level is not an object")
-            if doc.get("schema") != SCHEMA_VERSION:
-                raise CacheRejectedError(f"schema {doc.get('schema')!r} != {SCHEMA_VERSION}")
-            if doc.get("gpu") != self.gpu:
-                raise CacheRejectedError(f"built for gpu {doc.get('gpu')!r}, running on {self.gpu!r}")
-            if doc.get("hip") != self.abi:
-                raise CacheRejectedError(
-                    f"built for kernel ABI {doc.get('hip')!r}, running {self.abi!r}"
-                )
-            entries = _parse_entries(doc.get("entries"))
-        except (json.JSONDecodeError, CacheRejectedError) as exc:
-            self._discard(str(exc))
+        except CacheRejectedError as exc:
+            self._reject(str(exc))
             return
-        with self._lock:
-            self._entries = entries
+        with self._mutex:
+            self._table = table
 
-    def _discard(self, reason: str) -> None:
+    def _reject(self, reason: str) -> None:
         log.warning("autotune cache %s discarded (%s); configs will be retuned", self.path, reason)
         self.discarded_reason = reason
-        with self._lock:
-            self._entries = {}
+        with self._mutex:
+            self._table = {}
 
     def get(self, bucket: int, n: int, k: int, group_size: int) -> GemmConfig | None:
-        return self._entries.get(entry_key(bucket, n, k, group_size))
+        return self._table.get(entry_key(bucket, n, k, group_size))
 
     def put(self, bucket: int, n: int, k: int, group_size: int, cfg: GemmConfig) -> None:
         cfg.validate(group_size)
         if not cfg.fits_bucket(bucket):
             raise ValueError(f"{cfg} does not fit bucket {bucket}")
-        with self._lock:
-            self._entries[entry_key(bucket, n, k, group_size)] = cfg
+        with self._mutex:
+            self._table = {**self._table, entry_key(bucket, n, k, group_size): cfg}
 
     def __len__(self) -> int:
-        return len(self._entries)
+        return len(self._table)
 
     def save(self) -> None:
-        with self._lock:
-            payload = {
-                "schema": SCHEMA_VERSION,
-                "gpu": self.gpu,
-                "hip": self.abi,
-                "torch": torch.__version__,
-                "entries": {k: v.to_dict() for k, v in sorted(self._entries.items())},
-            }
-        atomic_write_json(self.path, payload)
+        with self._mutex:
+            text = _encode_document(self.gpu, self.abi, self._table)
+        _replace_file(self.path, text)
 
 
-_CACHES: dict[tuple[str, str], AutotuneCache] = {}
-_CACHES_LOCK = threading.Lock()
+_REGISTRY: dict[tuple[str, str], AutotuneCache] = {}
+_REGISTRY_MUTEX = threading.Lock()
 
 
 def get_cache(gpu: str) -> AutotuneCache:
-    abi = hip_abi()
-    with _CACHES_LOCK:
-        cache = _CACHES.get((gpu, abi))
-        if cache is None:
-            cache = AutotuneCache(cache_path(gpu, abi), gpu, abi)
+    """The process-wide cache of ``gpu`` for the loaded kernel ABI, read from disk once."""
+    key = (gpu, hip_abi())
+    with _REGISTRY_MUTEX:
+        if key not in _REGISTRY:
+            cache = AutotuneCache(cache_path(*key), *key)
             cache.load()
-            _CACHES[(gpu, abi)] = cache
-        return cache
+            _REGISTRY[key] = cache
+        return _REGISTRY[key]
 
 
 def reset_caches() -> None:
-    with _CACHES_LOCK:
-        _CACHES.clear()
+    with _REGISTRY_MUTEX:
+        _REGISTRY.clear()
 
 
 def lookup(gpu: str, bucket: int, n: int, k: int, group_size: int) -> GemmConfig:
     """Hot-path lookup: tuned config if cached, otherwise the heuristic default."""
-    cfg = get_cache(gpu).get(bucket, n, k, group_size)
-    return cfg if cfg is not None else default_config(bucket, n, k, group_size)
+    tuned = get_cache(gpu).get(bucket, n, k, group_size)
+    return default_config(bucket, n, k, group_size) if tuned is None else tuned
 
 
 BenchFn = Callable[[Callable[[], object]], float]
@@ -305,15 +328,17 @@ def select_finalist(
 def synthetic_layer(
     n: int, k: int, group_size: int, device: torch.device, seed: int = 0
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """Random AWQ-distributed layer in TokenForge layout: nibbles and zero-points uniform in
-    [0, 15], fp16 scales uniform in [1e-3, 1e-2]. Returns ``(qweight_t, scales, qzeros)``."""
-    from tokenforge_amd.kernels.pack import pack_int4
+    """Random AWQ-distributed layer in the tile layout the kernels read: nibbles and
+    zero-points uniform in [0, 15], fp16 scales uniform in [1e-3, 1e-2]. Returns
+    ``(qweight_t, scales, qzeros)``."""
+    from tokenforge.kernels.hip.layout import tile_pack
+    from tokenforge.kernels.pack import pack_int4
 
     gen = torch.Generator(device=device).manual_seed(seed)
     q = torch.randint(0, 16, (n, k), generator=gen, device=device, dtype=torch.int32)
     z = torch.randint(0, 16, (k // group_size, n), generator=gen, device=device, dtype=torch.int32)
     s = (torch.rand((k // group_size, n), generator=gen, device=device) * 9e-3 + 1e-3).to(torch.float16)
-    return pack_int4(q), s, pack_int4(z)
+    return tile_pack(pack_int4(q), s, pack_int4(z), group_size)
 
 
 def tune_layer(
@@ -334,7 +359,7 @@ def tune_layer(
     config that miscomputes is never cached. Buckets already in the cache are skipped, and
     nothing touches the device when every bucket is cached.
     """
-    from tokenforge_amd.kernels.hip.w4a16 import w4a16_gemm
+    from tokenforge.kernels.hip.w4a16 import w4a16_gemm
 
     cache = get_cache(gpu)
     buckets = list(buckets)

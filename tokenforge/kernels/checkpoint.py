@@ -33,9 +33,9 @@ from typing import Iterable, Mapping
 
 import torch
 
-from tokenforge_amd.kernels import autotune, dispatch
-from tokenforge_amd.kernels.config import M_BUCKETS
-from tokenforge_amd.kernels.pack import PACK_FACTOR, W4A16Weights, pack_awq
+from tokenforge.kernels import autotune, dispatch
+from tokenforge.kernels.config import M_BUCKETS
+from tokenforge.kernels.pack import PACK_FACTOR, W4A16Weights, pack_awq
 
 AWQ_PARTS = ("qweight", "qzeros", "scales")
 QWEN2_FUSIONS: Mapping[str, tuple[str, ...]] = {
@@ -198,7 +198,7 @@ def load_awq_checkpoint(
     fuse: Mapping[str, Iterable[str]] | None = QWEN2_FUSIONS,
 ) -> LoadedCheckpoint:
     """Read, validate, repack on the GPU and tune (``tune_buckets``; None or empty skips tuning)."""
-    from tokenforge_amd.kernels.device import device_arch, gpu_identity
+    from tokenforge.kernels.device import device_arch, gpu_identity
 
     if device.type != "cuda":
         raise dispatch.HipUnavailableError(

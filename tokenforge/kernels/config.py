@@ -15,20 +15,20 @@ Field meaning per kernel family:
 ========== =========================== ================================================
 kernel     block_m / block_n / block_k  split_k / num_warps / num_stages
 ========== =========================== ================================================
-gemv_dot   max M (1,2,4) / rows per     1 / waves per workgroup, each a K slice reduced
-           workgroup (16*RT) / 128      on chip / 128-wide K steps in flight per wave.
-           or 256                       block_k 256: the waves take different row tiles
-                                        (block_n rows each) over the whole K and share
-                                        one staged x
-gemv_mfma  M per tile (16,32) / rows    same as gemv_dot; block_k 128 stages x in LDS,
-           per workgroup / 128, 64 or   64 streams x from global memory, 256 as for
-           256                          gemv_dot
+gemv_mfma  M per tile (16,32) / columns 1 / waves per workgroup / 128-wide K steps in
+           per workgroup (16*RT) / 128  flight per wave. block_k 128: the waves split
+           or 256                       K over the same columns and add their partials
+                                        on chip; block_k 256: the waves take different
+                                        column sets (block_n each) over the whole K and
+                                        share one staged x
 gemm_mfma  LDS tile M / tile N / tile K K slices across workgroups (fp32 workspace,
                                         fixed-order reduce) / 4 or 8 waves / 2: two LDS
                                         buffers, 3 and 4: pipelined with 2 and 3 x stages
                                         (block_k 64); block_k 128: skinny form, num_stages
                                         = x stages
 ========== =========================== ================================================
+
+Every kernel reads the weights in the gfx950 tile layout that ``pack.pack_awq`` produces.
 """
 
 from __future__ import annotations
@@ -43,29 +43,22 @@ GEMV_MAX_M = 32
 GEMM_MIN_M = 16
 """Smallest bucket the gemm_mfma kernels may serve (the tuner weighs both families at 16, 32)."""
 
-KERNELS: tuple[str, ...] = ("gemv_dot", "gemv_mfma", "gemm_mfma")
+KERNELS: tuple[str, ...] = ("gemv_mfma", "gemm_mfma")
 NUM_CUS = 256
 """MI355X compute units; the split heuristics aim to put several waves on each."""
 
 _WAVES = (1, 2, 4, 8, 16)
 
-# Compiled streaming variants: (kernel, block_m, row tiles RT, block_k, ring depth P, max waves).
-# block_k = 128: x is staged in LDS once per wave; block_k = 64: x is streamed from global
-# memory with the weights (for M and K too large to stage); block_k = 256: the waves of a
-# workgroup take different row tiles over the whole K and share one copy of x. The wave cap
-# keeps each variant within the VGPR budget of its launch bound (no spills).
+# Compiled streaming variants: (kernel, block_m, column tiles RT, block_k, ring depth P, max
+# waves). block_k = 128: the waves of a workgroup split K and x is staged in LDS per wave;
+# block_k = 256: the waves take different column tiles over the whole K and share one copy of
+# x. The wave cap keeps each variant within the VGPR budget of its launch bound (no spills).
 GEMV_TEMPLATES: tuple[tuple[str, int, int, int, int, int], ...] = (
-    ("gemv_dot", 1, 1, 128, 2, 16), ("gemv_dot", 1, 1, 128, 4, 16), ("gemv_dot", 1, 1, 128, 8, 16),
-    ("gemv_dot", 1, 2, 128, 2, 16), ("gemv_dot", 1, 2, 128, 4, 8), ("gemv_dot", 1, 4, 128, 2, 8),
-    ("gemv_dot", 2, 1, 128, 2, 16), ("gemv_dot", 2, 2, 128, 2, 8), ("gemv_dot", 4, 1, 128, 2, 8),
-    ("gemv_dot", 1, 1, 256, 4, 8), ("gemv_dot", 1, 1, 256, 8, 8), ("gemv_dot", 1, 2, 256, 4, 8),
-    ("gemv_dot", 2, 1, 256, 4, 8), ("gemv_dot", 4, 1, 256, 4, 8),
     ("gemv_mfma", 16, 1, 128, 2, 16), ("gemv_mfma", 16, 1, 128, 4, 16), ("gemv_mfma", 16, 1, 128, 8, 16),
-    ("gemv_mfma", 16, 2, 128, 2, 16), ("gemv_mfma", 16, 2, 128, 4, 16), ("gemv_mfma", 16, 4, 128, 2, 8),
+    ("gemv_mfma", 16, 2, 128, 2, 16), ("gemv_mfma", 16, 2, 128, 4, 8), ("gemv_mfma", 16, 4, 128, 2, 8),
     ("gemv_mfma", 32, 1, 128, 2, 16), ("gemv_mfma", 32, 2, 128, 2, 8),
-    ("gemv_mfma", 16, 1, 64, 2, 16), ("gemv_mfma", 16, 2, 64, 2, 16), ("gemv_mfma", 16, 4, 64, 2, 8),
-    ("gemv_mfma", 32, 1, 64, 2, 16), ("gemv_mfma", 32, 2, 64, 2, 8),
-    ("gemv_mfma", 16, 1, 256, 2, 8), ("gemv_mfma", 16, 1, 256, 4, 8), ("gemv_mfma", 16, 2, 256, 2, 8),
+    ("gemv_mfma", 16, 1, 256, 2, 8), ("gemv_mfma", 16, 1, 256, 4, 8), ("gemv_mfma", 16, 1, 256, 8, 8),
+    ("gemv_mfma", 16, 2, 256, 2, 8), ("gemv_mfma", 16, 2, 256, 4, 8), ("gemv_mfma", 32, 1, 256, 2, 8),
 )
 
 
@@ -169,15 +162,10 @@ class GemmConfig:
 
     def fits_bucket(self, bucket: int) -> bool:
         """Whether this config may serve M values of ``bucket`` (cache validation): the gemv
-        kernels serve buckets up to GEMV_MAX_M (gemv_dot only up to its block_m), gemm_mfma
-        buckets from GEMM_MIN_M on."""
+        kernels serve buckets up to GEMV_MAX_M, gemm_mfma buckets from GEMM_MIN_M on."""
         if self.family == "gemm":
             return bucket >= GEMM_MIN_M
-        if bucket > GEMV_MAX_M:
-            return False
-        if self.kernel == "gemv_dot":
-            return self.block_m >= bucket
-        return True
+        return bucket <= GEMV_MAX_M
 
     def to_dict(self) -> dict[str, Any]:
         return asdict(self)
@@ -216,12 +204,10 @@ def default_config(bucket: int, n: int, k: int, group_size: int) -> GemmConfig:
     two-buffer GEMM for group 32.
     """
     if family_for_bucket(bucket) == "gemv":
-        bm = 16
         tiles = -(-n // 32)
         k_steps = max(1, -(-k // 128))
         waves = _pow2_at_most(max(1, -(-(12 * NUM_CUS) // tiles)), min(16, k_steps))
-        block_k = 128 if bucket <= 4 else 64  # stage x in LDS only while it is small
-        return GemmConfig("gemv_mfma", bm, 32, block_k, 1, waves, 2)
+        return GemmConfig("gemv_mfma", 16, 32, 128, 1, waves, 2)
     if bucket <= 128:
         bm = min(bucket, 64)
         bn = 64 if bucket <= 64 else 128

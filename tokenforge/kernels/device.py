@@ -12,7 +12,7 @@ import re
 
 import torch
 
-from tokenforge_amd.kernels import _lib
+from tokenforge.kernels import _lib
 
 SUPPORTED_ARCHS: tuple[str, ...] = ("gfx950",)
 

@@ -10,9 +10,13 @@ Two decisions, made at different times:
 There is one device path: hand-written HIP kernels for gfx950. ``backend`` keeps the
 reference's string argument; ``"hip"`` is canonical and the reference's ``"triton"`` and
 ``"cuda"`` are accepted as aliases of the same path, so reference-shaped callers work
-unchanged. ``"marlin"`` remains the per-layer kill switch. A call that cannot run on the
-GPU (CPU tensor, library not built, another architecture) raises: there is no CPU
-fallback behind these ops.
+unchanged. ``"marlin"`` remains the per-layer kill switch.
+
+:func:`select` takes the reference's keywords (``on_gpu``, ``triton_ok``,
+``cuda_ext_available``) and returns the reference's decision for a call that cannot run on
+the GPU: ``torch_reference``. This build has no CPU path behind that decision; the ops turn
+it into :class:`HipUnavailableError` naming the reason, so such a call fails loudly instead
+of running a slow fallback.
 """
 
 from __future__ import annotations
@@ -21,19 +25,20 @@ import os
 from dataclasses import dataclass
 from typing import Final, Literal, get_args
 
-from tokenforge_amd.kernels.config import MAX_BUCKET_M, family_for_bucket, m_bucket
-from tokenforge_amd.kernels.device import SUPPORTED_ARCHS
-from tokenforge_amd.kernels.metrics import FALLBACKS, KERNEL_CALLS
-from tokenforge_amd.kernels.pack import PACK_FACTOR, SUPPORTED_GROUP_SIZES
+from tokenforge.kernels.config import MAX_BUCKET_M, family_for_bucket, m_bucket
+from tokenforge.kernels.device import SUPPORTED_ARCHS
+from tokenforge.kernels.metrics import FALLBACKS, KERNEL_CALLS
+from tokenforge.kernels.pack import PACK_FACTOR, SUPPORTED_GROUP_SIZES
 
 Backend = Literal["hip", "triton", "cuda", "marlin"]
-Kernel = Literal["hip_gemv", "hip_gemm"]
+Kernel = Literal["hip_gemv", "hip_gemm", "torch_reference"]
 FallbackReason = Literal[
     "kill_switch",
     "unsupported_dtype",
     "unsupported_group_size",
     "unsupported_shape",
     "unsupported_arch",
+    "cuda_ext_unavailable",
 ]
 
 BACKENDS: Final[tuple[str, ...]] = get_args(Backend)
@@ -80,6 +85,7 @@ def record_layer_fallback(reason: FallbackReason) -> None:
 class Decision:
     kernel: Kernel
     bucket: str
+    fallback: FallbackReason | None = None
 
 
 def bucket_label(m: int) -> str:
@@ -91,24 +97,49 @@ def lookup_bucket(m: int) -> int:
     return MAX_BUCKET_M if m > MAX_BUCKET_M else m_bucket(m)
 
 
-def select(m: int, *, backend: Backend, on_gpu: bool, hip_ok: bool) -> Decision:
-    """Kernel family for one call with ``m`` rows. The layer has passed :func:`layer_support`."""
+def select(
+    m: int,
+    *,
+    backend: Backend,
+    on_gpu: bool,
+    triton_ok: bool | None = None,
+    cuda_ext_available: bool | None = None,
+    hip_ok: bool | None = None,
+) -> Decision:
+    """Kernel family for one call with ``m`` rows. The layer has passed :func:`layer_support`.
+
+    ``triton_ok`` (the reference's name) and ``hip_ok`` both mean "the compiled kernels can
+    run this call" (library loaded, gfx950 device); either may be given, and an omitted flag
+    counts as true. ``cuda_ext_available`` is accepted for the reference's signature: the one
+    HIP library is this build's compiled extension, so it never splits the decision.
+    """
+    del cuda_ext_available
     if backend == "marlin":
         raise ValueError("backend 'marlin' is resolved per layer, not per call")
-    if not on_gpu:
-        raise HipUnavailableError(
-            "tokenforge_amd kernels run on gfx950 GPU tensors only; got a CPU tensor "
-            "(this build has no CPU path)"
-        )
-    if not hip_ok:
-        raise HipUnavailableError(
-            "the HIP kernel library is not loaded or the GPU is not gfx950 "
-            "(build it with `python -m tokenforge_amd.build`)"
-        )
     bucket = bucket_label(m)
+    runnable = (triton_ok is None or triton_ok) and (hip_ok is None or hip_ok)
+    if not on_gpu or not runnable:
+        return Decision("torch_reference", bucket)
     kernel: Kernel = "hip_gemv" if family_for_bucket(lookup_bucket(m)) == "gemv" else "hip_gemm"
     return Decision(kernel, bucket)
 
 
+def require_gpu_decision(decision: Decision, *, on_gpu: bool) -> None:
+    """Raise :class:`HipUnavailableError` for a ``torch_reference`` decision (no CPU path)."""
+    if decision.kernel != "torch_reference":
+        return
+    if not on_gpu:
+        raise HipUnavailableError(
+            "tokenforge.kernels runs on gfx950 GPU tensors only; got a CPU tensor "
+            "(this build has no CPU path)"
+        )
+    raise HipUnavailableError(
+        "the HIP kernel library is not loaded or the GPU is not gfx950 "
+        "(build it with `python -m tokenforge_amd.build`)"
+    )
+
+
 def record(decision: Decision) -> None:
     KERNEL_CALLS.inc(kernel=decision.kernel, bucket=decision.bucket)
+    if decision.fallback is not None:
+        FALLBACKS.inc(reason=decision.fallback)

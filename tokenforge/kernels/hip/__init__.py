@@ -3,5 +3,5 @@
 Each launcher checks its inputs with the reference's exception types and messages,
 allocates outputs with the torch caching allocator and launches on torch's current stream
 through the C ABI. None of them synchronizes or reads tensor values on the host, except the
-load-time range check of :func:`tokenforge_amd.kernels.hip.layout.pack_int4`.
+load-time range check of :func:`tokenforge.kernels.hip.layout.pack_int4`.
 """

@@ -9,8 +9,8 @@ from __future__ import annotations
 
 import torch
 
-from tokenforge_amd.kernels import _lib
-from tokenforge_amd.kernels.hip._common import on_device, require_gpu, stream_of
+from tokenforge.kernels import _lib
+from tokenforge.kernels.hip._common import on_device, require_gpu, stream_of
 
 FP8_E4M3_MAX = 448.0
 MIN_SCALE = 1.0 / (FP8_E4M3_MAX * 512.0)

@@ -12,9 +12,9 @@ import ctypes
 
 import torch
 
-from tokenforge_amd.kernels import _lib
-from tokenforge_amd.kernels.config import GemmConfig
-from tokenforge_amd.kernels.hip._common import on_device, ptr, require_gpu, stream_of
+from tokenforge.kernels import _lib
+from tokenforge.kernels.config import GemmConfig
+from tokenforge.kernels.hip._common import on_device, ptr, require_gpu, stream_of
 
 
 def _check_inputs(
@@ -186,14 +186,16 @@ def w4a16_dequant(
     return out
 
 
-def _x_scale_stride(x_scale: torch.Tensor, m: int) -> int:
+def _row_scales(x_scale: torch.Tensor, m: int) -> tuple[torch.Tensor, int]:
+    """``x_scale`` as the vector the kernel reads and its element stride (0: one scale for every
+    row). The vector is contiguous, so its data pointer and stride describe the same memory."""
     if x_scale.dtype != torch.float32:
         raise TypeError(f"x_scale must be fp32, got {x_scale.dtype}")
     if x_scale.numel() == 1:
-        return 0
+        return x_scale.reshape(1).contiguous(), 0
     if x_scale.numel() != m:
         raise ValueError(f"x_scale must hold one scale or one per row ({m}), got shape {tuple(x_scale.shape)}")
-    return int(x_scale.reshape(m).stride(0))
+    return x_scale.reshape(m).contiguous(), 1
 
 
 def w4a8_gemm_ex(
@@ -235,7 +237,7 @@ def w4a8_gemm_ex(
         raise ValueError("residual is only used by the residual epilogue")
     if epilogue == "silu_mul" and n % 16:
         raise ValueError(f"the silu_mul epilogue needs N to be a multiple of 16, got {n}")
-    xs_stride = _x_scale_stride(x_scale, m)
+    x_scale, xs_stride = _row_scales(x_scale, m)
     tensors = (x8, x_scale, qweight_t, scales, qzeros) + tuple(t for t in (bias, residual) if t is not None)
     dev = require_gpu("w4a8_gemm", *tensors)
     n_out = n // 2 if epilogue == "silu_mul" else n

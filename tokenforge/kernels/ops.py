@@ -36,19 +36,45 @@ falling back.
 
 from __future__ import annotations
 
+import dataclasses
 import functools
 
 import torch
 
-from tokenforge_amd.kernels import autotune, dispatch
-from tokenforge_amd.kernels.device import gpu_identity, hip_runnable
-from tokenforge_amd.kernels.hip import rmsnorm_fp8 as _rms
-from tokenforge_amd.kernels.hip import w4a16 as _w4a16
+from tokenforge.kernels import _lib, autotune, dispatch
+from tokenforge.kernels.config import MAX_BUCKET_M, NUM_CUS, GemmConfig
+from tokenforge.kernels.device import gpu_identity, hip_runnable
+from tokenforge.kernels.hip import rmsnorm_fp8 as _rms
+from tokenforge.kernels.hip import w4a16 as _w4a16
 
 
 @functools.cache
 def _gpu_id(device: torch.device) -> str:
     return gpu_identity(device)
+
+
+def _decide(x2: torch.Tensor, m: int, n: int, k: int, group_size: int, backend: str) -> GemmConfig:
+    """Dispatch decision (the reference's ``select`` keywords) and the bucket's launch config.
+
+    A ``torch_reference`` decision (CPU tensor, library missing, other GPU) raises: this build
+    has no CPU path. The tuned config may pick the other kernel family in the buckets both
+    serve; the counter records the family that runs.
+    """
+    decision = dispatch.select(
+        m,
+        backend=backend,  # type: ignore[arg-type]
+        on_gpu=x2.is_cuda,
+        triton_ok=hip_runnable(x2),
+        cuda_ext_available=_lib.available(),
+    )
+    dispatch.require_gpu_decision(decision, on_gpu=x2.is_cuda)
+    cfg = autotune.lookup(_gpu_id(x2.device), dispatch.lookup_bucket(m), n, k, group_size)
+    if m > MAX_BUCKET_M and cfg.split_k > 1 and -(-m // cfg.block_m) * -(-n // cfg.block_n) >= NUM_CUS:
+        # Above the largest bucket its config is reused; once the M tiles alone fill the CUs a
+        # K split only adds the fp32 workspace (split * M * N * 4 bytes) and its reduction.
+        cfg = dataclasses.replace(cfg, split_k=1)
+    dispatch.record(dispatch.Decision("hip_gemm" if cfg.family == "gemm" else "hip_gemv", decision.bucket))
+    return cfg
 
 
 def _linear(
@@ -77,15 +103,7 @@ def _linear(
             f"backend must be 'hip' (or its aliases 'triton', 'cuda') at op level, got {backend!r}"
         )
 
-    decision = dispatch.select(
-        m,
-        backend=backend,  # type: ignore[arg-type]
-        on_gpu=x.is_cuda,
-        hip_ok=hip_runnable(x2),
-    )
-    cfg = autotune.lookup(_gpu_id(x.device), dispatch.lookup_bucket(m), n, k, group_size)
-    # The tuned config may pick the other family in the buckets both serve.
-    dispatch.record(dispatch.Decision("hip_gemm" if cfg.family == "gemm" else "hip_gemv", decision.bucket))
+    cfg = _decide(x2, m, n, k, group_size, backend)
     r2 = None
     if residual is not None:
         if tuple(residual.shape) != (*x.shape[:-1], n):
@@ -203,10 +221,9 @@ def w4a8_linear(
         raise ValueError(
             f"backend must be 'hip' (or its aliases 'triton', 'cuda') at op level, got {backend!r}"
         )
-    decision = dispatch.select(m, backend=backend, on_gpu=x8.is_cuda, hip_ok=hip_runnable(x2))  # type: ignore[arg-type]
-    cfg = autotune.lookup(_gpu_id(x8.device), dispatch.lookup_bucket(m), n, k, group_size)
-    dispatch.record(dispatch.Decision("hip_gemm" if cfg.family == "gemm" else "hip_gemv", decision.bucket))
-    s2 = x_scale.reshape(-1) if x_scale.numel() > 1 else x_scale.reshape(1)
+    cfg = _decide(x2, m, n, k, group_size, backend)
+    # One contiguous scale vector: the kernel reads its data pointer with the stride of this view.
+    s2 = (x_scale.reshape(-1) if x_scale.numel() > 1 else x_scale.reshape(1)).contiguous()
     r2 = residual.reshape(-1, n) if residual is not None else None
     y = _w4a16.w4a8_gemm_ex(x2, s2, qweight_t, scales, qzeros, group_size, cfg, bias, epilogue, r2)
     return y.reshape(out_shape)

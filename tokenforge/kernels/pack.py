@@ -1,26 +1,27 @@
-"""AWQ GEMM-format packing and the TokenForge kernel layout (pack.py:1-194 in the reference).
+"""AWQ checkpoint format, the TokenForge layout and the gfx950 tile layout (pack.py:1-194).
 
-AWQ GEMM layout (AutoAWQ ``WQLinear_GEMM``), the on-disk format every engine reads:
+Three layouts of one W4A16 layer (K input features, N output features, group size G):
 
-* ``qweight``: int32 ``[K, N // 8]``. Eight 4-bit weights per word, packed along N.
-* ``qzeros``:  int32 ``[K // G, N // 8]``. Zero-points, packed the same way.
-* ``scales``:  fp16  ``[K // G, N]``.
-
-Inside a word, nibble ``i`` holds offset ``AWQ_ORDER[i]``: offsets ``(2j, 2j+1)`` sit in
-nibbles ``(j, j+4)``, so ``word & 0x000F000F`` OR-ed with the fp16 pattern ``0x6400`` is the
-fp16x2 pair ``(1024 + q[2j], 1024 + q[2j+1])`` that gfx950's packed-fp16 VALU consumes.
-
-TokenForge layout (what the kernels read), bit-identical to the reference's:
-
-* ``qweight_t``: int32 ``[N, K // 8]``, packed along K with the same nibble interleave. A
-  lane that owns output row ``n`` streams contiguous K with 128-bit loads.
-* ``scales`` and ``qzeros`` stay in AWQ layout.
+* **AWQ GEMM format** (AutoAWQ ``WQLinear_GEMM``, what checkpoints hold): ``qweight`` int32
+  ``[K, N/8]`` packed along N, ``qzeros`` int32 ``[K/G, N/8]``, ``scales`` fp16 ``[K/G, N]``.
+  A word holds eight 4-bit values in the nibble order ``AWQ_ORDER`` (offsets ``2j, 2j+1`` in
+  nibbles ``j, j+4``), so masking a word with ``0x000F000F`` and OR-ing the fp16 exponent
+  ``0x6400`` gives the fp16 pair ``(1024 + q[2j], 1024 + q[2j+1])``.
+* **TokenForge layout** (the reference's, bit-identical here): ``qweight_t`` int32 ``[N, K/8]``
+  packed along K (:func:`repack_awq_to_tf`), scales and zero points as in AWQ.
+* **gfx950 tile layout** (what :func:`pack_awq` returns and every kernel reads): the same three
+  shapes and dtypes, with rows grouped in tiles of 16. Each 16-row x 128-K step of
+  ``qweight_t`` is one contiguous 1 KB block of 16-byte chunks (32 K values of one row), in
+  which lane ``16 g + c`` of a wave finds the MFMA B operand of column ``c``, K block ``g``;
+  a tile's scales and zero points are contiguous, group after group. The exact index maps are
+  in ``tokenforge_amd/csrc/tile_layout.h``.
 
 Dequantization is ``w[k, n] = fp16(q[k, n] - z[k // G, n]) * s[k // G, n]`` (one rounding).
 
-Every tensor-producing function here runs a HIP kernel on a gfx950 GPU tensor; CPU tensors
-raise (the CPU restatement used to check these kernels lives in the repository's ``oracle``
-test package, not here).
+Every tensor-producing function runs a HIP kernel on a gfx950 GPU. These are load-time
+functions, so they also accept host tensors (as the reference's callers pass them): the
+inputs are copied to the current GPU, the kernel runs there, and the results come back on
+the inputs' device. Without a visible GPU they raise; there is no CPU implementation here.
 """
 
 from __future__ import annotations
@@ -29,7 +30,7 @@ from dataclasses import dataclass
 
 import torch
 
-from tokenforge_amd.kernels.hip import layout as _layout
+from tokenforge.kernels.hip import layout as _layout
 
 AWQ_ORDER: tuple[int, ...] = (0, 2, 4, 6, 1, 3, 5, 7)
 """Nibble ``i`` of a packed word holds offset ``AWQ_ORDER[i]``."""
@@ -61,13 +62,21 @@ def awq_unpack(qweight: torch.Tensor) -> torch.Tensor:
     return unpack_int4(qweight)
 
 
+def awq_quantize(weight: torch.Tensor, group_size: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Min-max asymmetric int4 quantization of an ``nn.Linear`` weight ``[N, K]`` into AWQ format
+    (AutoAWQ's rounding rules): ``(qweight [K, N/8], qzeros [K/G, N/8], scales [K/G, N] fp16)``.
+    A fixture generator for tests and benchmarks; production loads real AWQ checkpoints."""
+    return _layout.awq_quantize(weight, group_size)
+
+
 @dataclass(frozen=True)
 class W4A16Weights:
-    """One linear layer's weights in TokenForge layout."""
+    """One linear layer's weights as the kernels read them (the gfx950 tile layout when built
+    by :func:`pack_awq`); the shapes and dtypes are the reference's."""
 
-    qweight_t: torch.Tensor  # int32 [N, K // 8], packed along K
+    qweight_t: torch.Tensor  # int32 [N, K // 8]
     scales: torch.Tensor  # fp16 [K // G, N]
-    qzeros: torch.Tensor  # int32 [K // G, N // 8], AWQ layout
+    qzeros: torch.Tensor  # int32 [K // G, N // 8]
     group_size: int
 
     @property
@@ -112,26 +121,27 @@ def validate_awq(
 def pack_awq(
     qweight: torch.Tensor, qzeros: torch.Tensor, scales: torch.Tensor, group_size: int
 ) -> W4A16Weights:
-    """Load-time conversion of one AWQ layer into the TokenForge layout (GPU repack)."""
+    """Load-time conversion of one AWQ layer into the gfx950 tile layout: the GPU repack to the
+    TokenForge layout, then the tile permutation of the weights, scales and zero points."""
     validate_awq(qweight, qzeros, scales, group_size)
-    return W4A16Weights(
-        qweight_t=repack_awq_to_tf(qweight),
-        scales=scales.contiguous(),
-        qzeros=qzeros.contiguous(),
-        group_size=group_size,
-    )
+    qw, sc, qz = _layout.tile_pack(repack_awq_to_tf(qweight), scales, qzeros, group_size)
+    return W4A16Weights(qweight_t=qw, scales=sc, qzeros=qz, group_size=group_size)
 
 
 def unpack_to_awq(weights: W4A16Weights) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """Inverse of :func:`pack_awq`: returns ``(qweight, qzeros, scales)``."""
-    return repack_tf_to_awq(weights.qweight_t), weights.qzeros, weights.scales
+    """Inverse of :func:`pack_awq`: returns ``(qweight, qzeros, scales)`` in AWQ format."""
+    qw, sc, qz = _layout.tile_unpack(weights.qweight_t, weights.scales, weights.qzeros, weights.group_size)
+    return repack_tf_to_awq(qw), qz, sc
 
 
 def dequantize_tf(weights: W4A16Weights) -> torch.Tensor:
-    """TokenForge layout -> fp16 ``[N, K]`` (the ``nn.Linear.weight`` layout)."""
-    from tokenforge_amd.kernels.hip.w4a16 import w4a16_dequant
+    """Tile-layout weights -> fp16 ``[N, K]`` (the ``nn.Linear.weight`` layout)."""
+    from tokenforge.kernels.hip._common import load_time_devices
+    from tokenforge.kernels.hip.w4a16 import w4a16_dequant
 
-    return w4a16_dequant(weights.qweight_t, weights.scales, weights.qzeros, weights.group_size)
+    run, home = load_time_devices("dequantize_tf", weights.qweight_t, weights.scales, weights.qzeros)
+    qw, sc, qz = (t.to(run) for t in (weights.qweight_t, weights.scales, weights.qzeros))
+    return w4a16_dequant(qw, sc, qz, weights.group_size).to(home)
 
 
 def awq_dequantize(

@@ -22,6 +22,8 @@ CSRC = PKG / "csrc"
 BUILD_DIR = PKG.parent / "_build"
 LIB_DIR = PKG / "lib"
 LIB_NAME = "libtokenforge_hip.so"
+PROBES = PKG / "probes"
+PROBE_LIB_NAME = "libtokenforge_probes.so"  # bench.py --probe only
 ARCH = "gfx950"
 
 # Packed-FP32 VALU forms are disabled: hipcc -O3 would otherwise emit v_pk_{add,mul,fma}_f32
@@ -62,20 +64,30 @@ def _run(cmd: list[str], verbose: bool) -> None:
         print(err, file=sys.stderr)
 
 
+def _link(cc: str, objects: list[Path], out: Path, verbose: bool) -> None:
+    tmp = out.with_suffix(".so.tmp")
+    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objects)], verbose)
+    os.replace(tmp, out)
+
+
 def build(jobs: int | None = None, verbose: bool = False) -> Path:
-    """Compile every kernel source and link the shared library. Returns its path."""
+    """Compile every kernel source and link the shared library (and, separately, the
+    measurement probes' library, which the product never loads). Returns the library path."""
     cc = hipcc()
     BUILD_DIR.mkdir(parents=True, exist_ok=True)
     LIB_DIR.mkdir(parents=True, exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
+    probe_sources = sorted(PROBES.glob("*.hip"))
     objects = [BUILD_DIR / (s.stem + ".o") for s in sources]
-    cmds = [[cc, *HIPCC_FLAGS, "-c", str(s), "-o", str(o)] for s, o in zip(sources, objects)]
+    probe_objects = [BUILD_DIR / ("probe_" + s.stem + ".o") for s in probe_sources]
+    cmds = [[cc, *HIPCC_FLAGS, "-c", str(s), "-o", str(o)]
+            for s, o in zip(sources + probe_sources, objects + probe_objects)]
     with ThreadPoolExecutor(max_workers=jobs or min(8, os.cpu_count() or 1)) as pool:
         list(pool.map(lambda c: _run(c, verbose), cmds))
     out = LIB_DIR / LIB_NAME
-    tmp = out.with_suffix(".so.tmp")
-    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objects)], verbose)
-    os.replace(tmp, out)
+    _link(cc, objects, out, verbose)
+    if probe_objects:
+        _link(cc, probe_objects, LIB_DIR / PROBE_LIB_NAME, verbose)
     return out
 
 

@@ -2,7 +2,7 @@
 //
 // Per K block (BK <= group size, so one scale and one zero per column per block):
 //   * x tile [BM][BK] fp16 is copied global -> registers -> LDS;
-//   * the packed qweight_t tile [BN][BK/8] is loaded with 128-bit loads, dequantized in
+//   * the packed weight tile (BN columns x BK, tile layout) is loaded with 128-bit loads, dequantized in
 //     registers (fp16(q - z) * s, one rounding) and stored to LDS as fp16 [BN][BK];
 //   * each wave reads its A/B fragments (8 consecutive K values per lane, the operand
 //     layout of the 32x32x16 MFMA) and accumulates fp32.
@@ -14,6 +14,7 @@
 // second kernel sums them in split order, adds the bias and rounds once (w4a16.py:227-232),
 // so the result does not depend on scheduling.
 #include "linear.h"
+#include "tile_layout.h"
 
 namespace tf {
 namespace {
@@ -46,7 +47,8 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(LinearArgs a, float*
   const int nkb = a.k / BK;
   const int kb0 = (int)(((int64_t)z * nkb) / split_k);
   const int kb1 = (int)(((int64_t)(z + 1) * nkb) / split_k);
-  const int64_t words_per_row = a.k >> 3;
+  const int64_t q_total = a.k >> 5;
+  const int64_t groups = a.k >> a.log2g;
 
   u4 ra[A_PER];
   u4 rb[B_PER];
@@ -73,10 +75,10 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(LinearArgs a, float*
       const int col = id / (BK / 32);
       const int kc = id % (BK / 32);
       const int n = n0 + col;
-      if (id < B_CHUNKS && n < a.n) {
-        rb[i] = *reinterpret_cast<const u4*>(a.qw + (int64_t)n * words_per_row + (k0 >> 3) + kc * 4);
-        rs[i] = a.scales[(int64_t)grp * a.n + n];
-        rz[i] = a.qz[(int64_t)grp * (a.n >> 3) + (n >> 3)];
+      if (id < B_CHUNKS && n < a.n) {  // tile layout (tile_layout.h)
+        rb[i] = *reinterpret_cast<const u4*>(a.qw + tile_chunk(n, (k0 >> 5) + kc, a.n, q_total) * 4);
+        rs[i] = a.scales[tile_scale(grp, n, a.n, groups)];
+        rz[i] = a.qz[tile_zero(grp, n >> 3, a.n, groups)];
       } else {
         rb[i] = u4{0u, 0u, 0u, 0u};
         rs[i] = 0u;

@@ -30,6 +30,7 @@
 #include <type_traits>
 
 #include "linear.h"
+#include "tile_layout.h"
 
 namespace tf {
 
@@ -138,16 +139,30 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm2_kernel(LinearArgs a, float
     }
   };
 
-  // ---- packed weights of block kb -> register slot
-  uint32_t b_off[BP];
-  int b_col[BP];
+  // ---- packed weights of block kb -> register slot. Tile layout: block kb of column n is
+  // chunks q = 2 kb + half (half = 0, 1) at chunk index 16 t Q + half rows + cc + 2 kb rows
+  // (t = n / 16, cc = n % 16, rows = the tile's row count), i.e. each 16-column tile's block is
+  // 512 contiguous bytes. Thread id takes half (id / 16) % 2 of column 16 (id / 32) + id % 16,
+  // so 32 consecutive threads read one tile's 512 bytes in order. Scale and zero word of
+  // column n, group grp: element 16 t P + grp rows + cc, word 2 t P + grp (rows / 8) + cc / 8.
+  const uint32_t q_total = (uint32_t)(a.k >> 5);
+  uint32_t b_off[BP], b_step[BP], b_sbase[BP], b_zbase[BP], b_rows[BP];
+  int b_col[BP], b_half[BP];
 #pragma unroll
   for (int i = 0; i < BP; ++i) {
     const int id = tid + i * C::kThreads;
-    const int col = id >> 1;
+    const int col = ((id >> 5) << 4) | (id & 15);
+    const int half = (id >> 4) & 1;
     const int n = n0 + col;
     b_col[i] = col;
-    b_off[i] = (id < C::kBChunks && n < a.n) ? (uint32_t)n * row_bytes + (uint32_t)(id & 1) * 16u : kOutOfRange;
+    b_half[i] = half;
+    const uint32_t tt = (uint32_t)n >> 4, cc = (uint32_t)n & 15u;
+    const uint32_t rows = (uint32_t)tile_rows(a.n, tt);
+    b_rows[i] = rows;
+    b_off[i] = (id < C::kBChunks && n < a.n) ? (tt * q_total * 16u + (uint32_t)half * rows + cc) * 16u : kOutOfRange;
+    b_step[i] = rows * 32u;
+    b_sbase[i] = tt * 16u * (uint32_t)groups + cc;
+    b_zbase[i] = tt * 2u * (uint32_t)groups + (cc >> 3);
   }
   u4 braw[2][BP];
   uint32_t bsc[2][BP], bzw[2][BP];
@@ -157,10 +172,9 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm2_kernel(LinearArgs a, float
 #pragma unroll
     for (int i = 0; i < BP; ++i) {
       const bool v = ok && b_off[i] != kOutOfRange;
-      const uint32_t n = (uint32_t)(n0 + b_col[i]);
-      braw[slot][i] = load_b128(rq, v ? b_off[i] + (uint32_t)kb * 32u : kOutOfRange);
-      bsc[slot][i] = load_b16(rs, v ? (grp * (uint32_t)a.n + n) * 2u : kOutOfRange);
-      bzw[slot][i] = load_b32(rz, v ? (grp * (uint32_t)(a.n >> 3) + (n >> 3)) * 4u : kOutOfRange);
+      braw[slot][i] = load_b128(rq, v ? b_off[i] + (uint32_t)kb * b_step[i] : kOutOfRange);
+      bsc[slot][i] = load_b16(rs, v ? (b_sbase[i] + grp * b_rows[i]) * 2u : kOutOfRange);
+      bzw[slot][i] = load_b32(rz, v ? (b_zbase[i] + grp * (b_rows[i] >> 3)) * 4u : kOutOfRange);
     }
   };
   // Dequantization operands of a register slot, one per packed chunk.
@@ -177,7 +191,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm2_kernel(LinearArgs a, float
       if (id < C::kBChunks) {
         h2 d[4];
         dequant_word(braw[slot][i][j], qp[i], uc, d);
-        *reinterpret_cast<u4*>(b_lds + buf * C::kBStage + swz(b_col[i], (id & 1) * 4 + j)) =
+        *reinterpret_cast<u4*>(b_lds + buf * C::kBStage + swz(b_col[i], b_half[i] * 4 + j)) =
             u4{as_u32(d[0]), as_u32(d[1]), as_u32(d[2]), as_u32(d[3])};
       }
     }

@@ -14,7 +14,8 @@
 //     steps ahead, with one barrier per step;
 //   * lane (c = lane % 16, g = lane / 16) holds 32 consecutive K values (chunk g) of column c,
 //     the B layout of the 16x16x32 MFMA; MFMA j takes word j of every lane group, so its K set
-//     is {g * 32 + j * 8 + e}, and the A fragments read x at the same K positions.
+//     is {g * 32 + j * 8 + e}, and the A fragments read x at the same K positions. In the tile
+//     layout the 64 lanes of a 16-column tile read one contiguous 1 KB block per step.
 // Rows of a stage hold 16 chunks of 16 bytes; chunk c of row r sits in slot c ^ (r % 16), so
 // the 8 lanes of each 16-byte read phase hit distinct bank groups.
 // K may end in a partial 128-wide step: chunks past K read as zeros (per-lane bounds). Loads
@@ -26,6 +27,7 @@
 #include <type_traits>
 
 #include "linear.h"
+#include "tile_layout.h"
 
 namespace tf {
 
@@ -130,15 +132,25 @@ __global__ __launch_bounds__(256) void gemm3_kernel(LinearArgs a, float* __restr
     }
   };
 
-  // ---- weights, scales and zero points of step s -> register slot
-  uint32_t w_off[RT];
+  // ---- weights, scales and zero points of step s -> register slot. Tile layout: the lane's
+  // chunk (column n, K block g) of step s sits at chunk 16 t Q + 4 rows s + g rows + cc
+  // (t = n / 16, cc = n % 16, rows = the tile's row count), its scale at element
+  // 16 t P + grp rows + cc and its zero word at 2 t P + grp (rows / 8) + cc / 8.
+  const uint32_t q_total = (uint32_t)nchunks;
+  uint32_t w_off[RT], w_step[RT], s_base[RT], z_base[RT], t_rows[RT];
   uint32_t col[RT];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     const int l = wl + rt * 16 + c;
     const int n = phys_col(a, n_base, l);
     col[rt] = (uint32_t)n;
-    w_off[rt] = col_valid(a, n_base, l) ? (uint32_t)n * row_bytes + (uint32_t)g * 16u : kOutOfRange;
+    const uint32_t t = (uint32_t)n >> 4, cc = (uint32_t)n & 15u;
+    const uint32_t rows = (uint32_t)tile_rows(a.n, t);
+    t_rows[rt] = rows;
+    w_off[rt] = col_valid(a, n_base, l) ? (t * q_total * 16u + (uint32_t)g * rows + cc) * 16u : kOutOfRange;
+    w_step[rt] = rows * 64u;
+    s_base[rt] = t * 16u * (uint32_t)groups + cc;
+    z_base[rt] = t * 2u * (uint32_t)groups + (cc >> 3);
   }
   const int lane_end = min(s1, (nchunks - g + 3) >> 2);  // steps whose chunk g lies inside K
   u4 wraw[P][RT];
@@ -149,9 +161,9 @@ __global__ __launch_bounds__(256) void gemm3_kernel(LinearArgs a, float* __restr
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
       const bool v = ok && w_off[rt] != kOutOfRange;
-      wraw[slot][rt] = load_b128(rq, v ? w_off[rt] + (uint32_t)s * 64u : kOutOfRange);
-      wsc[slot][rt] = load_b16(rs, v ? (grp * (uint32_t)a.n + col[rt]) * 2u : kOutOfRange);
-      wzw[slot][rt] = load_b32(rz, v ? (grp * (uint32_t)(a.n >> 3) + (col[rt] >> 3)) * 4u : kOutOfRange);
+      wraw[slot][rt] = load_b128(rq, v ? w_off[rt] + (uint32_t)s * w_step[rt] : kOutOfRange);
+      wsc[slot][rt] = load_b16(rs, v ? (s_base[rt] + grp * t_rows[rt]) * 2u : kOutOfRange);
+      wzw[slot][rt] = load_b32(rz, v ? (z_base[rt] + grp * (t_rows[rt] >> 3)) * 4u : kOutOfRange);
     }
   };
 

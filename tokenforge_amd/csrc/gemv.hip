@@ -1,40 +1,39 @@
-// Decode-shaped W4A16 kernels (small M): stream the packed weights once, dequantize in
-// registers, accumulate in fp32.
+// Decode-shaped W4A16 kernel (small M) on the gfx950 tile layout: stream the packed weights
+// once, dequantize in registers (fp16(q - z) * s, one rounding), multiply on the matrix cores.
 //
-// Work split: a workgroup owns block_n = 16 * RT consecutive rows of qweight_t (output
-// columns); its num_warps waves take disjoint, contiguous K ranges of those rows (on-chip
-// split-K) and their partial sums are added in wave order through LDS, so results are
-// bit-identical from run to run. No workspace, no atomics.
+// Lane l = 16 g + c of a wave owns column c of a 16-row tile and K block g of every 128-wide K
+// step: its 16 bytes of a step are chunk (c, g) of the tile layout, which sits at byte 16 l of
+// the step's 1 KB block, so one 128-bit buffer load per wave reads one whole block (two full
+// 128-byte lines per 16 lanes). Those 16 bytes (32 K values, one group for G >= 32) are exactly
+// the B operand of v_mfma_f32_16x16x32_f16 for four MFMAs: MFMA j takes word j of every lane,
+// K set {32 g + 8 j + e}; x rows are the A operand, read from LDS at the same K positions. The
+// matrix core does the dot products and the VALU only unpacks and scales (13 instructions per
+// packed word); rows m >= M of the A operand feed output rows that are never stored.
 //
-// Memory stream: a "step" is 16 rows x 128 K values. Per step each lane issues one 128-bit
-// buffer load per 16-row tile (4 packed words = 32 weights of one row), so each row receives
-// a 64-byte run per load and consecutive steps complete the 128-byte lines, plus the scale and
-// the zero-point word of that row and the lane's group. Every wave keeps a register ring of P
-// steps in flight: the loads of step s + P are issued as soon as step s has been consumed.
-// Buffer loads return zeros past the end of a tensor, which handles ragged N and a partial last
-// step without branches. When K is a multiple of 128 the per-step part of every offset is
-// wave-uniform and travels in the scalar offset of the load (no address arithmetic per step).
+// Work split: a workgroup owns block_n = 16 * RT consecutive columns (RT tiles). block_k 128:
+// its num_warps waves take disjoint, contiguous K ranges of those columns (on-chip split-K) and
+// add their partial sums in wave order through LDS (bit-identical from run to run, no
+// workspace, no atomics). block_k 256: the waves take different column sets over the whole K
+// and share one copy of x staged cooperatively (one barrier, no reduction).
 //
-// Before the loop each wave stages its slice of x in its own LDS region (no barrier needed, a
-// wave reads only what it wrote). Measured on MI355X, the scale/zero loads in the ring beat
-// staging the dequantization operands in LDS per wave (gate_up and down at M = 1 ~12% faster).
+// Memory stream: every wave keeps a register ring of P steps in flight: per tile the 16 weight
+// bytes, the scales word holding its column's scale and the qzeros word of its column and
+// group. The loads of step s + P are issued as soon as step s has been consumed. Buffer loads
+// return zeros past the end of a tensor (and for chunks past K), so ragged N and a partial last
+// step need no branches. When every tile is full and K is a multiple of 128 ("uniform"), the
+// step part of every offset is wave-uniform and rides in the loads' scalar offset.
 //
-//  * gemv_dot  (TF_KERNEL_GEMV_DOT): lane = (row c = lane/4, chunk g = lane%4). Each lane
-//    accumulates its products with v_dot2_f32_f16; quads are reduced with DPP. SPLITN variants
-//    (block_k 256) turn the split around: the waves of a workgroup take different row tiles,
-//    each over the whole K, and share one copy of x staged cooperatively (one barrier); no
-//    cross-wave reduction. For shapes with many row tiles this removes the per-wave prologue
-//    and reduction that short K slices pay for every few steps.
-//  * gemv_mfma (TF_KERNEL_GEMV_MFMA): lane = (row c = lane%16, chunk g = lane/16), exactly the
-//    B-operand layout of v_mfma_f32_16x16x32_f16 (8 consecutive K values per lane = one
-//    packed word). The dequantized word goes straight into the MFMA and x rows are the A
-//    operand, so the matrix core does the dot products and the VALU only unpacks and scales.
-//    A rows m >= M only feed output rows that are discarded, so they read any staged row.
+// Before the loop each wave stages its slice of x in its own LDS region (no barrier: a wave
+// reads only what it wrote); the first staging batch is issued ahead of the weight ring.
 #include "linear.h"
+#include "tile_layout.h"
+
+#ifndef TF_GEMV_EARLY
+#define TF_GEMV_EARLY 0
+#endif
 
 namespace tf {
 namespace {
-
 // K range [s0, s1) of 128-wide steps owned by `wave`; waves is a power of two (every compiled
 // variant's num_warps is). All arguments are wave-uniform, so the range and every loop bound
 // derived from it live in scalar registers.
@@ -44,42 +43,36 @@ __device__ __forceinline__ void k_range(int wave, int waves, int nsteps, int* s0
   *s1 = ((wave + 1) * nsteps) >> sh;
 }
 
-// Buffer resources and per-launch constants shared by both kernels.
+// Buffer resources and per-launch constants.
 struct Streams {
   __amdgpu_buffer_rsrc_t qw, sc, qz, x, x8;
   const void *qw_ptr, *sc_ptr, *qz_ptr;
   uint32_t qw_bytes, sc_bytes, qz_bytes;
-  uint32_t row_bytes;  // K / 2
-  int nchunks;         // K / 32
-  int nsteps;          // ceil(K / 128)
-  int groups;          // K / G
+  int q_total;  // K / 32: 16-byte chunks per row
+  int nsteps;   // ceil(K / 128)
+  int groups;   // K / G
   int log2g;
   int n;
-  int sc_step;         // bytes of scales per 128-wide step: (128 / G) * N * 2
-  int qz_step;         // bytes of qzeros per step: (128 / G) * (N / 8) * 4
 };
 
 __device__ __forceinline__ Streams make_streams(const LinearArgs& a) {
   Streams s;
-  s.row_bytes = (uint32_t)(a.k >> 1);
   s.groups = a.k >> a.log2g;
-  s.qw = make_rsrc(a.qw, (uint32_t)a.n * s.row_bytes);
-  s.sc = make_rsrc(a.scales, (uint32_t)(s.groups * a.n * 2));
-  s.qz = make_rsrc(a.qz, (uint32_t)(s.groups * (a.n >> 3) * 4));
+  s.q_total = a.k >> 5;
+  s.nsteps = (s.q_total + 3) >> 2;
+  s.qw_bytes = (uint32_t)a.n * (uint32_t)(a.k >> 1);
+  s.sc_bytes = (uint32_t)(s.groups * a.n * 2);
+  s.qz_bytes = (uint32_t)(s.groups * (a.n >> 3) * 4);
+  s.qw = make_rsrc(a.qw, s.qw_bytes);
+  s.sc = make_rsrc(a.scales, s.sc_bytes);
+  s.qz = make_rsrc(a.qz, s.qz_bytes);
   s.x = make_rsrc(a.x, (uint32_t)(((int64_t)(a.m - 1) * a.ldx + a.k) * 2));
   s.x8 = make_rsrc(a.x8, (uint32_t)((int64_t)(a.m - 1) * a.ldx8 + a.k));
   s.qw_ptr = a.qw;
   s.sc_ptr = a.scales;
   s.qz_ptr = a.qz;
-  s.qw_bytes = (uint32_t)a.n * s.row_bytes;
-  s.sc_bytes = (uint32_t)(s.groups * a.n * 2);
-  s.qz_bytes = (uint32_t)(s.groups * (a.n >> 3) * 4);
-  s.nchunks = a.k >> 5;
-  s.nsteps = (s.nchunks + 3) >> 2;
   s.log2g = a.log2g;
   s.n = a.n;
-  s.sc_step = (128 >> a.log2g) * a.n * 2;
-  s.qz_step = (128 >> a.log2g) * (a.n >> 3) * 4;
   return s;
 }
 
@@ -170,79 +163,95 @@ __device__ __forceinline__ void stage_rest(_Float16* xs, const Window& w, const 
   }
 }
 
-// One ring slot: per row tile, the lane's 16 bytes of packed weights, the scales word holding
-// that row's scale (and its even/odd neighbour's) and the qzeros word of that row, for the
-// lane's group. Whole words: no extension of a 16-bit load sits between a load and its use,
-// where the compiler would wait for it early.
+// One ring slot: per tile, the lane's 16 weight bytes, the scales word holding its column's
+// scale (and its even/odd neighbour's) and the qzeros word of its column, for the lane's group.
+// Whole words: no extension of a 16-bit load sits between a load and its use, where the
+// compiler would wait for it early.
 template <int RT>
 struct Slot {
   u4 w[RT];
   uint32_t sw[RT], zw[RT];
 };
 
-// Per-lane view of the streams: the lane reads 16 bytes (chunk g = 32 K values, one group) of
-// one row per row tile and step; its rows are local columns l0 + 16 rt of the tile at n_base
-// (phys_col). The offsets are those of step 0 (kOutOfRange past N, and still out of range after
-// adding any step offset); lane_end is the first step whose chunk lies past K for this lane or
-// past the wave's range.
+// Per-lane view of the three streams in the tile layout. The lane reads chunk (column, K block
+// g) of each of its RT tiles per step; its columns are local columns c + 16 rt of the set at
+// n_base (phys_col). Offsets are those of step 0 (kOutOfRange past N, and still out of range
+// after adding any step offset); *step are the per-step byte strides (for a full tile: 1 KB of
+// weights, (128 / G) * 32 bytes of scales, (128 / G) * 8 bytes of zero words). lane_end is the
+// first step whose chunk lies past K for this lane, or the wave's end.
 //
-// FULLK (K a multiple of 128): every lane's chunk is inside K on every step of the range, so
-// the step part of each offset is wave-uniform and goes into the loads' scalar offset. That
-// part is not range-checked by the hardware; it never leaves the tensors because issued steps
-// stay below the wave's end (steps past it go through a resource with zero records) and the
-// vector part addresses a valid row and group (or is out of range, which stays out of range).
-template <int RT, bool FULLK>
+// UNIFORM (every tile full, K a multiple of 128): the strides are the same in every lane and
+// every chunk of the wave's range is inside K, so the step part of each offset is wave-uniform
+// and goes into the loads' scalar offset. That part is not range-checked by the hardware; it
+// never leaves the tensors because issued steps stay below the wave's end (steps past it go
+// through resources with zero records) and the vector part addresses a valid chunk, scale and
+// zero word (or is out of range, which stays out of range).
+template <int RT, bool UNIFORM>
 struct LaneStream {
   uint32_t woff[RT], soff[RT], zoff[RT], zsh[RT], ssel[RT];
+  uint32_t wstep[RT], sstep[RT], zstep[RT];
   int lane_end;
   int wave_end;  // s1, wave-uniform
 
   __device__ __forceinline__ LaneStream(const LinearArgs& a, const Streams& st, int n_base, int l0, int g, int s1) {
     const uint32_t gl = (uint32_t)((g * 32) >> st.log2g);  // the lane's group inside a step
+    const uint32_t gps = (uint32_t)(128 >> st.log2g);       // groups per step
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
       const int l = l0 + rt * 16;
       const bool ok = col_valid(a, n_base, l);
       const uint32_t n = (uint32_t)phys_col(a, n_base, l);
-      woff[rt] = ok ? n * st.row_bytes + (uint32_t)g * 16u : kOutOfRange;
-      soff[rt] = ok ? (gl * (uint32_t)st.n + (n & ~1u)) * 2u : kOutOfRange;  // N is a multiple of 8
-      ssel[rt] = (n & 1u) ? 0x03020302u : 0x01000100u;  // v_perm: this column's half in both halves
-      zoff[rt] = ok ? (gl * (uint32_t)(st.n >> 3) + (n >> 3)) * 4u : kOutOfRange;
+      const uint32_t t = n >> 4, cc = n & 15u;
+      const uint32_t rows = (uint32_t)tile_rows(st.n, t);
+      woff[rt] = ok ? (t * (uint32_t)st.q_total * 16u + (uint32_t)g * rows + cc) * 16u : kOutOfRange;
+      wstep[rt] = rows * 64u;
+      const uint32_t e = t * 16u * (uint32_t)st.groups + gl * rows + cc;  // scale element index
+      soff[rt] = ok ? (e & ~1u) * 2u : kOutOfRange;
+      sstep[rt] = gps * rows * 2u;
+      ssel[rt] = (cc & 1u) ? 0x03020302u : 0x01000100u;  // v_perm: this column's half in both halves
+      zoff[rt] = ok ? (t * 2u * (uint32_t)st.groups + gl * (rows >> 3) + (cc >> 3)) * 4u : kOutOfRange;
+      zstep[rt] = gps * (rows >> 3) * 4u;
       zsh[rt] = 4u * awq_nibble_of(n & 7u);
     }
-    lane_end = min(s1, (st.nchunks - g + 3) >> 2);
+    lane_end = min(s1, (st.q_total - g + 3) >> 2);
     wave_end = s1;
   }
 
   // Every call issues exactly 3 RT loads (zeros when the step is out of range), so the ring
-  // below has the same loads in flight on every path and the compiler's vmcnt waits stay exact
+  // has the same loads in flight on every path and the compiler's vmcnt waits stay exact
   // instead of draining the ring.
   __device__ __forceinline__ void issue(Slot<RT>& sl, const Streams& st, int step) const {
-    if (FULLK) {
+    if (UNIFORM) {
       // Steps past the wave's range read through resources with zero records: zeros, no traffic.
+      // Every stride is a scalar here (full 16-row tiles): 1 KB of weights, (128 / G) 32-byte
+      // groups of scales and (128 / G) 8-byte groups of zero words per step.
       const bool in = step < wave_end;
       const __amdgpu_buffer_rsrc_t rw = make_rsrc(st.qw_ptr, in ? st.qw_bytes : 0u);
       const __amdgpu_buffer_rsrc_t rs = make_rsrc(st.sc_ptr, in ? st.sc_bytes : 0u);
       const __amdgpu_buffer_rsrc_t rz = make_rsrc(st.qz_ptr, in ? st.qz_bytes : 0u);
       const int st_ = in ? step : 0;
+      const int gps_step = st_ << (7 - st.log2g);  // groups before this step
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
-        sl.w[rt] = __builtin_amdgcn_raw_buffer_load_b128(rw, (int)woff[rt], st_ * 64, 0);
-        sl.sw[rt] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)soff[rt], st_ * st.sc_step, 0);
-        sl.zw[rt] = __builtin_amdgcn_raw_buffer_load_b32(rz, (int)zoff[rt], st_ * st.qz_step, 0);
+        sl.w[rt] = __builtin_amdgcn_raw_buffer_load_b128(rw, (int)woff[rt], st_ * 1024, 0);
+        sl.sw[rt] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)soff[rt], gps_step * 32, 0);
+        sl.zw[rt] = __builtin_amdgcn_raw_buffer_load_b32(rz, (int)zoff[rt], gps_step * 8, 0);
       }
     } else {
+      // Per-lane strides (a tile of 8 rows, or a partial last step); 24-bit products are exact
+      // here (step < 2^16, strides <= 1 KB) and issue at the full VALU rate.
       const bool v = step < lane_end;
+      const uint32_t us = (uint32_t)step;
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
-        sl.w[rt] = load_b128(st.qw, v ? woff[rt] + (uint32_t)step * 64u : kOutOfRange);
-        sl.sw[rt] = load_b32(st.sc, v ? soff[rt] + (uint32_t)(step * st.sc_step) : kOutOfRange);
-        sl.zw[rt] = load_b32(st.qz, v ? zoff[rt] + (uint32_t)(step * st.qz_step) : kOutOfRange);
+        sl.w[rt] = load_b128(st.qw, v ? woff[rt] + __umul24(us, wstep[rt]) : kOutOfRange);
+        sl.sw[rt] = load_b32(st.sc, v ? soff[rt] + __umul24(us, sstep[rt]) : kOutOfRange);
+        sl.zw[rt] = load_b32(st.qz, v ? zoff[rt] + __umul24(us, zstep[rt]) : kOutOfRange);
       }
     }
   }
 
-  // Dequantization operands of row tile rt from a landed slot.
+  // Dequantization operands of tile rt from a landed slot.
   __device__ __forceinline__ QuantParams params(const Slot<RT>& sl, int rt) const {
     const uint32_t z = (sl.zw[rt] >> zsh[rt]) & 0xFu;
     const uint32_t zz = z | (z << 16);
@@ -269,41 +278,49 @@ __host__ __device__ __forceinline__ GemvLds gemv_lds_layout(int win, int x_rows)
   return l;
 }
 
-// ------------------------------------------------------------------------ gemv_dot
-
 constexpr int kStageU = 2;  // x staging chunks per lane and batch
 
-template <int MAXM, int RT, int P, int MAXW, bool FULLK, bool SPLITN>
-__global__ __launch_bounds__(MAXW * 64) void gemv_dot_kernel(LinearArgs a, int win) {
+// ------------------------------------------------------------------------ kernel
+
+template <int MT, int RT, int P, int MAXW, bool UNIFORM, bool SPLITN>
+__global__ __launch_bounds__(MAXW * 64) void gemv_kernel(LinearArgs a, int win) {
   extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int waves = blockDim.x >> 6;
-  const int g = lane & 3;
-  const int c = lane >> 2;
+  const int c = lane & 15;
+  const int g = lane >> 4;
   constexpr int cols = 16 * RT;
   const int n_base = SPLITN ? (xcd_tile(blockIdx.x, gridDim.x) * waves + wave) * cols
                             : xcd_tile(blockIdx.x, gridDim.x) * cols;
+  const int m_base = blockIdx.y * 16 * MT;
   const Streams st = make_streams(a);
   int s0 = 0, s1 = st.nsteps;
   if (!SPLITN) k_range(wave, waves, st.nsteps, &s0, &s1);
-  const int xrows = a.m < MAXM ? a.m : MAXM;
-  const GemvLds L = gemv_lds_layout(win, xrows);
+  const int xrows = min(16 * MT, a.m - m_base);  // rows staged by this workgroup
+  const int xalloc = min(16 * MT, a.m);          // rows allocated per wave (same in every workgroup)
+  const GemvLds L = gemv_lds_layout(win, xalloc);
   _Float16* xs = reinterpret_cast<_Float16*>(lds + (SPLITN ? 0 : wave * L.wave_words));
   const UnpackConsts uc = unpack_consts();
-  const LaneStream<RT, FULLK> ls_w(a, st, n_base, c, g, s1);
-  const _Float16* xl = xs + g * 32;
+  const LaneStream<RT, UNIFORM> ls_w(a, st, n_base, c, g, s1);
 
-  float acc[MAXM][RT];
+  const _Float16* xl[MT];
 #pragma unroll
-  for (int m = 0; m < MAXM; ++m)
+  for (int mt = 0; mt < MT; ++mt) {
+    const int r = mt * 16 + c;
+    xl[mt] = xs + (r < xrows ? r : 0) * L.xstride + g * 32;  // rows past M feed discarded outputs
+  }
+
+  f4 acc[MT][RT];
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt) acc[m][rt] = 0.0f;
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) acc[mt][rt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 
   // The first staging batch goes out ahead of the weight ring: every wave of the grid issues
   // its ring at once, and the x chunks that gate the first step must not queue behind it.
   // SPLITN: the waves stage the workgroup's one copy together, batch b by wave b % waves.
-  Window win0 = make_window(s0, min(s1, s0 + win), 0, xrows, L.xstride);
+  Window win0 = make_window(s0, min(s1, s0 + win), m_base, xrows, L.xstride);
   const int first_base = SPLITN ? wave * 64 * kStageU : 0;
   const int batch_stride = SPLITN ? waves * 64 * kStageU : 64 * kStageU;
   StageBatch<kStageU> first;
@@ -325,196 +342,32 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_dot_kernel(LinearArgs a, int w
 
   for (int w0 = s0; w0 < s1; w0 += win) {
     const int w1 = min(s1, w0 + win);
-    if (w0 != s0) stage_rest<kStageU>(xs, make_window(w0, w1, 0, xrows, L.xstride), a, st, 0, lane);
+    if (w0 != s0) stage_rest<kStageU>(xs, make_window(w0, w1, m_base, xrows, L.xstride), a, st, 0, lane);
     for (int s = w0; s < w1; s += P) {
 #pragma unroll
       for (int p = 0; p < P; ++p) {
         const int step = s + p;
-        if (step < w1) {
-          const int ls = step - w0;
-          u4 xv[MAXM][4];
-#pragma unroll
-          for (int m = 0; m < MAXM; ++m) {
-            const int row = m < xrows ? m : 0;  // rows past M only feed accumulators never stored
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-              xv[m][j] = *reinterpret_cast<const u4*>(xl + row * L.xstride + ls * 128 + j * 8);
-          }
-#pragma unroll
-          for (int rt = 0; rt < RT; ++rt) {
-            const QuantParams qp = ls_w.params(ring[p], rt);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              h2 wd[4];
-              dequant_word(ring[p].w[rt][j], qp, uc, wd);
-#pragma unroll
-              for (int m = 0; m < MAXM; ++m)
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                  acc[m][rt] = __builtin_amdgcn_fdot2(as_h2(xv[m][j][i]), wd[i], acc[m][rt], false);
-            }
-          }
-        }
+#if TF_GEMV_EARLY
+        const Slot<RT> cur = ring[p];
         ls_w.issue(ring[p], st, step + P);
-        // Slot boundary: keep the next slot's operand work (which waits for its loads) from
-        // being hoisted above this point, where it would wait for more of the ring than needed.
         __builtin_amdgcn_sched_barrier(0);
-      }
-    }
-  }
-
-#pragma unroll
-  for (int m = 0; m < MAXM; ++m)
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) acc[m][rt] = quad_sum(acc[m][rt]);
-
-  if (!SPLITN && waves > 1) {
-    float* red = reinterpret_cast<float*>(lds + waves * L.wave_words);  // [(waves - 1)][MAXM][RT][16]
-    if (wave > 0 && g == 0) {
-#pragma unroll
-      for (int m = 0; m < MAXM; ++m)
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt) red[(((wave - 1) * MAXM + m) * RT + rt) * 16 + c] = acc[m][rt];
-    }
-    __syncthreads();
-    if (wave == 0) {
-      for (int w = 1; w < waves; ++w)
-#pragma unroll
-        for (int m = 0; m < MAXM; ++m)
-#pragma unroll
-          for (int rt = 0; rt < RT; ++rt) acc[m][rt] += red[(((w - 1) * MAXM + m) * RT + rt) * 16 + c];
-    }
-  }
-  // Lane 4 c (g == 0) holds row c of each row tile. Under SiLU*mul rows c and c ^ 8 are the
-  // gate and up columns of one output (phys_col): lanes 4c and 4c ^ 32 swap their values.
-  if (SPLITN || wave == 0) {
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-      const int l = rt * 16 + c;
-      const int n = phys_col(a, n_base, l);
-      const bool valid = g == 0 && col_valid(a, n_base, l);
-      const float b = (a.bias && valid) ? half_bits_to_float(a.bias[n]) : 0.0f;
-#pragma unroll
-      for (int m = 0; m < MAXM; ++m) {
-        const float v = acc[m][rt] * row_scale(a, m) + b;
-        if (a.epilogue == TF_EPILOGUE_SILU_MUL) {
-          const float u = __shfl_xor(v, 32);
-          if (valid && !(l & 8) && m < a.m)
-            a.out[(int64_t)m * a.ldo + silu_out_col(n_base, l)] = finish_silu_mul(v, u);
-        } else if (valid && m < a.m) {
-          store_out(a, m, n, v);
-        }
-      }
-    }
-  }
-}
-
-// ------------------------------------------------------------------------ gemv_mfma
-
-template <int MT, int RT, int P, int MAXW, bool XLDS, bool FULLK, bool SPLITN>
-__global__ __launch_bounds__(MAXW * 64) void gemv_mfma_kernel(LinearArgs a, int win) {
-  static_assert(!SPLITN || XLDS, "waves over row tiles share x staged in LDS");
-  extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int waves = blockDim.x >> 6;
-  const int c = lane & 15;
-  const int g = lane >> 4;
-  constexpr int cols = 16 * RT;
-  const int n_base = SPLITN ? (xcd_tile(blockIdx.x, gridDim.x) * waves + wave) * cols
-                            : xcd_tile(blockIdx.x, gridDim.x) * cols;
-  const int m_base = blockIdx.y * 16 * MT;
-  const Streams st = make_streams(a);
-  int s0 = 0, s1 = st.nsteps;
-  if (!SPLITN) k_range(wave, waves, st.nsteps, &s0, &s1);
-  const int xrows = min(16 * MT, a.m - m_base);  // rows staged by this workgroup
-  const int xalloc = min(16 * MT, a.m);          // rows allocated per wave (same in every workgroup)
-  const GemvLds L = gemv_lds_layout(win, XLDS ? xalloc : 0);
-  _Float16* xs = reinterpret_cast<_Float16*>(lds + (SPLITN ? 0 : wave * L.wave_words));
-  const UnpackConsts uc = unpack_consts();
-  const LaneStream<RT, FULLK> ls_w(a, st, n_base, c, g, s1);
-
-  const _Float16* xl[MT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int r = mt * 16 + c;
-    xl[mt] = xs + (r < xrows ? r : 0) * L.xstride + g * 32;  // rows past M feed discarded outputs
-  }
-  // x streamed with the weights (block_k 64 variants): 64 bytes of row m per lane and step.
-  uint32_t xoff[MT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int m = m_base + mt * 16 + c;
-    xoff[mt] = m < a.m ? (uint32_t)(((int64_t)m * a.ldx + g * 32) * 2) : kOutOfRange;
-  }
-
-  f4 acc[MT][RT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) acc[mt][rt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-
-  Slot<RT> ring[P];
-  u4 xring[XLDS ? 1 : P][XLDS ? 1 : MT][4];
-  auto issue = [&](int p, int step) {
-    ls_w.issue(ring[p], st, step);
-    if (!XLDS) {
-      const bool v = step < ls_w.lane_end;
-#pragma unroll
-      for (int mt = 0; mt < (XLDS ? 0 : MT); ++mt)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          xring[XLDS ? 0 : p][mt][j] =
-              load_b128(st.x, v ? xoff[mt] + (uint32_t)step * 256u + 16u * j : kOutOfRange);
-    }
-  };
-  // The first staging batch goes out ahead of the weight ring (see gemv_dot_kernel).
-  const int srows = XLDS ? xrows : 0;
-  Window win0 = make_window(s0, min(s1, s0 + win), m_base, srows, L.xstride);
-  const int first_base = SPLITN ? wave * 64 * kStageU : 0;  // SPLITN: batch b by wave b % waves
-  const int batch_stride = SPLITN ? waves * 64 * kStageU : 64 * kStageU;
-  StageBatch<kStageU> first;
-  if (XLDS) load_batch<kStageU>(first, win0, a, st, first_base, lane);
-  __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int p = 0; p < P; ++p) {
-    issue(p, s0 + p);
-    __builtin_amdgcn_sched_barrier(0);  // keep slot order: slot 0 must be the oldest ring load
-  }
-  if (XLDS) {
-    store_batch<kStageU>(xs, first, win0, a, first_base, lane);
-    for (int base = first_base + batch_stride; base < win0.xentries; base += batch_stride) {
-      StageBatch<kStageU> b;
-      load_batch<kStageU>(b, win0, a, st, base, lane);
-      store_batch<kStageU>(xs, b, win0, a, base, lane);
-    }
-  }
-  if (SPLITN) __syncthreads();  // x is whole before any wave reads it (one window: win == s1)
-
-  for (int w0 = s0; w0 < s1; w0 += win) {
-    const int w1 = min(s1, w0 + win);
-    if (XLDS && w0 != s0)
-      stage_rest<kStageU>(xs, make_window(w0, w1, m_base, srows, L.xstride), a, st, 0, lane);
-    for (int s = w0; s < w1; s += P) {
-#pragma unroll
-      for (int p = 0; p < P; ++p) {
-        const int step = s + p;
+#else
+        const Slot<RT>& cur = ring[p];
+#endif
         if (step < w1) {
           const int ls = step - w0;
           h8 xa[MT][4];
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-              xa[mt][j] = XLDS ? *reinterpret_cast<const h8*>(xl[mt] + ls * 128 + j * 8)
-                               : __builtin_bit_cast(h8, xring[XLDS ? 0 : p][mt][j]);
+            for (int j = 0; j < 4; ++j) xa[mt][j] = *reinterpret_cast<const h8*>(xl[mt] + ls * 128 + j * 8);
 #pragma unroll
           for (int rt = 0; rt < RT; ++rt) {
-            const QuantParams qp = ls_w.params(ring[p], rt);
+            const QuantParams qp = ls_w.params(cur, rt);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
               h2 wd[4];
-              dequant_word(ring[p].w[rt][j], qp, uc, wd);
+              dequant_word(cur.w[rt][j], qp, uc, wd);
               const h8 b = pack_h8(wd);
 #pragma unroll
               for (int mt = 0; mt < MT; ++mt)
@@ -522,8 +375,12 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_mfma_kernel(LinearArgs a, int 
             }
           }
         }
-        issue(p, step + P);
-        __builtin_amdgcn_sched_barrier(0);  // slot boundary (see gemv_dot_kernel)
+#if !TF_GEMV_EARLY
+        ls_w.issue(ring[p], st, step + P);
+#endif
+        // Slot boundary: keep the next slot's operand work (which waits for its loads) from
+        // being hoisted above this point, where it would wait for more of the ring than needed.
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
   }
@@ -635,95 +492,71 @@ GemvPlan plan_gemv(const LinearArgs& a, int waves, int depth, int x_rows, size_t
   return GemvPlan{win, bytes(win)};
 }
 
-// K a multiple of 128 selects the kernels that carry the step offsets in scalar registers.
-bool full_steps(const LinearArgs& a) { return (a.k & 127) == 0; }
+// Every tile full and K a multiple of 128 selects the kernels that carry the step offsets in
+// scalar registers.
+bool uniform_steps(const LinearArgs& a) { return (a.k & 127) == 0 && (a.n & 15) == 0; }
 
-template <int MAXM, int RT, int P, int MAXW, bool FULLK, bool SPLITN>
-int launch_dot_k(const LinearArgs& a, int waves, hipStream_t stream) {
-  const int xrows = a.m < MAXM ? a.m : MAXM;
-  GemvPlan plan;
+// LDS bytes and staging window of a launch; win == 0 when it does not fit the device.
+template <int MT, int RT, int P, bool SPLITN>
+GemvPlan gemv_plan(const LinearArgs& a, int waves) {
+  const int xrows = a.m < 16 * MT ? a.m : 16 * MT;
   if (SPLITN) {  // one shared copy of all of x, no reduction buffer
     const int nsteps = ((a.k >> 5) + 3) >> 2;
-    plan = GemvPlan{nsteps, (size_t)gemv_lds_layout(nsteps, xrows).wave_words * 4};
-    if (plan.lds > device_max_lds())
-      return fail(TF_EINVAL, "tf_w4a16_linear: gemv_dot variant (block_k 256) needs x to fit the device's LDS");
-  } else {
-    plan = plan_gemv(a, waves, P, xrows, (size_t)MAXM * RT * 16 * sizeof(float));
-    if (plan.win == 0) return fail(TF_EINVAL, "tf_w4a16_linear: gemv_dot variant does not fit the device's LDS");
+    const GemvPlan p{nsteps, (size_t)gemv_lds_layout(nsteps, xrows).wave_words * 4};
+    return p.lds <= device_max_lds() ? p : GemvPlan{0, 0};
   }
-  if (int rc = reserve_lds(gemv_dot_kernel<MAXM, RT, P, MAXW, FULLK, SPLITN>, plan.lds, "gemv_dot")) return rc;
-  const int tiles = (int)cdiv(a.n, 16 * RT);
-  const dim3 grid((unsigned)(SPLITN ? cdiv(tiles, waves) : tiles));
-  gemv_dot_kernel<MAXM, RT, P, MAXW, FULLK, SPLITN><<<grid, waves * 64, plan.lds, stream>>>(a, plan.win);
-  return check_launch("tf_w4a16_linear(gemv_dot)");
+  return plan_gemv(a, waves, P, xrows, (size_t)MT * RT * 64 * 4 * sizeof(float));
 }
 
-template <int MAXM, int RT, int P, int MAXW, bool SPLITN>
-int launch_dot(const LinearArgs& a, const tf_gemm_config& cfg, float*, hipStream_t stream) {
-  if (a.m > MAXM) return fail(TF_EINVAL, "tf_w4a16_linear: gemv_dot variant needs m <= block_m");
+template <int MT, int RT, int P, int MAXW, bool SPLITN>
+int check_gemv(const LinearArgs& a, const tf_gemm_config& cfg) {
   if (int rc = check_offsets(a)) return rc;
-  return full_steps(a) ? launch_dot_k<MAXM, RT, P, MAXW, true, SPLITN>(a, cfg.num_warps, stream)
-                       : launch_dot_k<MAXM, RT, P, MAXW, false, SPLITN>(a, cfg.num_warps, stream);
+  if (gemv_plan<MT, RT, P, SPLITN>(a, cfg.num_warps).win == 0)
+    return fail(TF_EINVAL, SPLITN ? "tf_w4a16_linear: gemv variant (block_k 256) needs x to fit the device's LDS"
+                                  : "tf_w4a16_linear: gemv variant does not fit the device's LDS");
+  return TF_OK;
 }
 
-template <int MT, int RT, int P, int MAXW, bool XLDS, bool FULLK, bool SPLITN>
-int launch_mfma_k(const LinearArgs& a, int waves, hipStream_t stream) {
-  const int xrows = XLDS ? (a.m < 16 * MT ? a.m : 16 * MT) : 0;
-  GemvPlan plan;
-  if (SPLITN) {  // one shared copy of all of x, no reduction buffer
-    const int nsteps = ((a.k >> 5) + 3) >> 2;
-    plan = GemvPlan{nsteps, (size_t)gemv_lds_layout(nsteps, xrows).wave_words * 4};
-    if (plan.lds > device_max_lds())
-      return fail(TF_EINVAL, "tf_w4a16_linear: gemv_mfma variant (block_k 256) needs x to fit the device's LDS");
-  } else {
-    plan = plan_gemv(a, waves, P, xrows, (size_t)MT * RT * 64 * 4 * sizeof(float));
-    if (plan.win == 0) return fail(TF_EINVAL, "tf_w4a16_linear: gemv_mfma variant does not fit the device's LDS");
-  }
-  if (int rc = reserve_lds(gemv_mfma_kernel<MT, RT, P, MAXW, XLDS, FULLK, SPLITN>, plan.lds, "gemv_mfma")) return rc;
+template <int MT, int RT, int P, int MAXW, bool UNIFORM, bool SPLITN>
+int launch_k(const LinearArgs& a, int waves, const GemvPlan& plan, hipStream_t stream) {
+  auto kernel = gemv_kernel<MT, RT, P, MAXW, UNIFORM, SPLITN>;
+  if (int rc = reserve_lds(kernel, plan.lds, "gemv")) return rc;
   const int tiles = (int)cdiv(a.n, 16 * RT);
   const dim3 grid((unsigned)(SPLITN ? cdiv(tiles, waves) : tiles), (unsigned)cdiv(a.m, 16 * MT));
-  gemv_mfma_kernel<MT, RT, P, MAXW, XLDS, FULLK, SPLITN><<<grid, waves * 64, plan.lds, stream>>>(a, plan.win);
-  return check_launch("tf_w4a16_linear(gemv_mfma)");
+  kernel<<<grid, waves * 64, plan.lds, stream>>>(a, plan.win);
+  return check_launch("tf_w4a16_linear(gemv)");
 }
 
-template <int MT, int RT, int P, int MAXW, bool XLDS, bool SPLITN = false>
-int launch_mfma(const LinearArgs& a, const tf_gemm_config& cfg, float*, hipStream_t stream) {
-  if (int rc = check_offsets(a)) return rc;
-  return full_steps(a) ? launch_mfma_k<MT, RT, P, MAXW, XLDS, true, SPLITN>(a, cfg.num_warps, stream)
-                       : launch_mfma_k<MT, RT, P, MAXW, XLDS, false, SPLITN>(a, cfg.num_warps, stream);
+template <int MT, int RT, int P, int MAXW, bool SPLITN>
+int launch_gemv(const LinearArgs& a, const tf_gemm_config& cfg, float*, hipStream_t stream) {
+  if (int rc = check_gemv<MT, RT, P, MAXW, SPLITN>(a, cfg)) return rc;
+  const GemvPlan plan = gemv_plan<MT, RT, P, SPLITN>(a, cfg.num_warps);
+  return uniform_steps(a) ? launch_k<MT, RT, P, MAXW, true, SPLITN>(a, cfg.num_warps, plan, stream)
+                          : launch_k<MT, RT, P, MAXW, false, SPLITN>(a, cfg.num_warps, plan, stream);
 }
 
 // One table row per (variant, num_warps): num_warps ranges over 1..MAXW (powers of two).
-#define TF_W1(K, BM, BN, BK, ST, FN) {{K, BM, BN, BK, 1, 1, ST}, FN, no_workspace}
-#define TF_W2(K, BM, BN, BK, ST, FN) TF_W1(K, BM, BN, BK, ST, FN), {{K, BM, BN, BK, 1, 2, ST}, FN, no_workspace}
-#define TF_W4(K, BM, BN, BK, ST, FN) TF_W2(K, BM, BN, BK, ST, FN), {{K, BM, BN, BK, 1, 4, ST}, FN, no_workspace}
-#define TF_W8(K, BM, BN, BK, ST, FN) TF_W4(K, BM, BN, BK, ST, FN), {{K, BM, BN, BK, 1, 8, ST}, FN, no_workspace}
-#define TF_W16(K, BM, BN, BK, ST, FN) TF_W8(K, BM, BN, BK, ST, FN), {{K, BM, BN, BK, 1, 16, ST}, FN, no_workspace}
+#define TF_W1(K, BM, BN, BK, ST, FN, CK) {{K, BM, BN, BK, 1, 1, ST}, FN, no_workspace, CK}
+#define TF_W2(K, BM, BN, BK, ST, FN, CK) TF_W1(K, BM, BN, BK, ST, FN, CK), {{K, BM, BN, BK, 1, 2, ST}, FN, no_workspace, CK}
+#define TF_W4(K, BM, BN, BK, ST, FN, CK) TF_W2(K, BM, BN, BK, ST, FN, CK), {{K, BM, BN, BK, 1, 4, ST}, FN, no_workspace, CK}
+#define TF_W8(K, BM, BN, BK, ST, FN, CK) TF_W4(K, BM, BN, BK, ST, FN, CK), {{K, BM, BN, BK, 1, 8, ST}, FN, no_workspace, CK}
+#define TF_W16(K, BM, BN, BK, ST, FN, CK) TF_W8(K, BM, BN, BK, ST, FN, CK), {{K, BM, BN, BK, 1, 16, ST}, FN, no_workspace, CK}
 
-// block_k = 128 marks x staged in LDS (per wave, K split across waves), 64 marks x streamed
-// from global with the weights, 256 marks waves over row tiles with one shared x (block_n is
-// then the rows of one wave; a workgroup covers num_warps times as many).
-#define TF_DOT(BM, RT, P, MAXW) \
-  TF_W##MAXW(TF_KERNEL_GEMV_DOT, BM, 16 * RT, 128, P, (launch_dot<BM, RT, P, MAXW, false>))
-#define TF_DOT_N(BM, RT, P, MAXW) \
-  TF_W##MAXW(TF_KERNEL_GEMV_DOT, BM, 16 * RT, 256, P, (launch_dot<BM, RT, P, MAXW, true>))
-#define TF_MFMA(MT, RT, P, MAXW) \
-  TF_W##MAXW(TF_KERNEL_GEMV_MFMA, 16 * MT, 16 * RT, 128, P, (launch_mfma<MT, RT, P, MAXW, true>))
-#define TF_MFMA_GX(MT, RT, P, MAXW) \
-  TF_W##MAXW(TF_KERNEL_GEMV_MFMA, 16 * MT, 16 * RT, 64, P, (launch_mfma<MT, RT, P, MAXW, false>))
-#define TF_MFMA_N(MT, RT, P, MAXW) \
-  TF_W##MAXW(TF_KERNEL_GEMV_MFMA, 16 * MT, 16 * RT, 256, P, (launch_mfma<MT, RT, P, MAXW, true, true>))
+// block_k = 128 marks the K split across the waves of a workgroup (x staged per wave), 256
+// waves over column sets with one shared x (block_n is then the columns of one wave; a
+// workgroup covers num_warps times as many).
+#define TF_GEMV(MT, RT, P, MAXW) \
+  TF_W##MAXW(TF_KERNEL_GEMV_MFMA, 16 * MT, 16 * RT, 128, P, (launch_gemv<MT, RT, P, MAXW, false>), \
+             (check_gemv<MT, RT, P, MAXW, false>))
+#define TF_GEMV_N(MT, RT, P, MAXW) \
+  TF_W##MAXW(TF_KERNEL_GEMV_MFMA, 16 * MT, 16 * RT, 256, P, (launch_gemv<MT, RT, P, MAXW, true>), \
+             (check_gemv<MT, RT, P, MAXW, true>))
 
 const Variant kGemvVariants[] = {
-    TF_DOT(1, 1, 2, 16), TF_DOT(1, 1, 4, 16), TF_DOT(1, 1, 8, 16), TF_DOT(1, 2, 2, 16),
-    TF_DOT(1, 2, 4, 8),  TF_DOT(1, 4, 2, 8),  TF_DOT(2, 1, 2, 16), TF_DOT(2, 2, 2, 8),
-    TF_DOT(4, 1, 2, 8),
-    TF_DOT_N(1, 1, 4, 8), TF_DOT_N(1, 1, 8, 8), TF_DOT_N(1, 2, 4, 8), TF_DOT_N(2, 1, 4, 8), TF_DOT_N(4, 1, 4, 8),
-    TF_MFMA(1, 1, 2, 16), TF_MFMA(1, 1, 4, 16), TF_MFMA(1, 1, 8, 16), TF_MFMA(1, 2, 2, 16),
-    TF_MFMA(1, 2, 4, 16), TF_MFMA(1, 4, 2, 8),  TF_MFMA(2, 1, 2, 16), TF_MFMA(2, 2, 2, 8),
-    TF_MFMA_GX(1, 1, 2, 16), TF_MFMA_GX(1, 2, 2, 16), TF_MFMA_GX(1, 4, 2, 8), TF_MFMA_GX(2, 1, 2, 16),
-    TF_MFMA_GX(2, 2, 2, 8),
-    TF_MFMA_N(1, 1, 2, 8), TF_MFMA_N(1, 1, 4, 8), TF_MFMA_N(1, 2, 2, 8),
+    TF_GEMV(1, 1, 2, 16), TF_GEMV(1, 1, 4, 16), TF_GEMV(1, 1, 8, 16), TF_GEMV(1, 2, 2, 16),
+    TF_GEMV(1, 2, 4, 8),  TF_GEMV(1, 4, 2, 8),  TF_GEMV(2, 1, 2, 16), TF_GEMV(2, 2, 2, 8),
+    TF_GEMV_N(1, 1, 2, 8), TF_GEMV_N(1, 1, 4, 8), TF_GEMV_N(1, 1, 8, 8), TF_GEMV_N(1, 2, 2, 8),
+    TF_GEMV_N(1, 2, 4, 8), TF_GEMV_N(2, 1, 2, 8),
 };
 
 }  // namespace

@@ -89,13 +89,18 @@ __device__ __forceinline__ void store_out(const LinearArgs& a, int m, int n, flo
 using LaunchFn = int (*)(const LinearArgs&, const tf_gemm_config&, float* workspace,
                          hipStream_t stream);
 using WorkspaceFn = int64_t (*)(const LinearArgs&, const tf_gemm_config&);
+// The checks a launch function makes before it launches anything (TF_OK or an error), for
+// callers that must reject a call before they queue work of their own (tf_w4a8_linear_ex).
+using CheckFn = int (*)(const LinearArgs&, const tf_gemm_config&);
 
 // A compiled kernel variant: cfg holds (kernel, block_m, block_n, block_k, num_warps,
-// num_stages) with split_k = 1.
+// num_stages) with split_k = 1. check may be null when the launch function rejects nothing
+// beyond what tf_w4a16_linear_ex checks first.
 struct Variant {
   tf_gemm_config cfg;
   LaunchFn launch;
   WorkspaceFn workspace;
+  CheckFn check = nullptr;
 };
 
 const Variant* gemv_variants(int* count);

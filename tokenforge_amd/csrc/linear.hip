@@ -61,11 +61,9 @@ int check_config(const tf_gemm_config& cfg, int32_t group_size) {
   return TF_OK;
 }
 
-// Configs whose kernels read e4m3 x themselves (they stage x in LDS): the dot GEMV and the
-// MFMA GEMV with block_k 128 or 256. Every other config gets x converted to fp16 first.
-bool fuses_x8(const tf_gemm_config& cfg) {
-  return cfg.kernel == TF_KERNEL_GEMV_DOT || (cfg.kernel == TF_KERNEL_GEMV_MFMA && cfg.block_k != 64);
-}
+// Configs whose kernels read e4m3 x themselves (they stage x in LDS): every GEMV config. The
+// GEMM configs get x converted to fp16 first.
+bool fuses_x8(const tf_gemm_config& cfg) { return cfg.kernel == TF_KERNEL_GEMV_MFMA; }
 
 constexpr int64_t kWsAlign = 256;
 int64_t align_ws(int64_t b) { return (b + kWsAlign - 1) / kWsAlign * kWsAlign; }
@@ -215,18 +213,15 @@ extern "C" int tf_w4a8_linear_ex(const uint8_t* x8, int64_t ldx8, const float* x
   if (need > 0 && (workspace == nullptr || workspace_bytes < need))
     return fail(TF_EINVAL, "tf_w4a8_linear_ex: workspace too small");
   const bool fused = fuses_x8(*cfg);
+  const bool convert = !fused && m > 0 && n > 0 && k > 0;
   // The kernels that stage x read the codes; for the others x is converted to fp16 into the
-  // front of the workspace and the rest of the workspace is theirs.
+  // front of the workspace and the rest of the workspace is theirs. Every check runs before
+  // anything is launched, so a rejected call leaves nothing queued on the stream.
   const uint16_t* x16 = reinterpret_cast<const uint16_t*>(x8);
   float* ws = workspace;
   int64_t ws_bytes = workspace_bytes;
-  if (!fused && m > 0 && n > 0 && k > 0) {
-    uint16_t* conv = reinterpret_cast<uint16_t*>(workspace);
-    const int64_t chunks = m * (k / 8);
-    e4m3_rows_to_f16_kernel<<<(unsigned)cdiv(chunks, 256), 256, 0, (hipStream_t)stream>>>(x8, ldx8, conv, (int)m,
-                                                                                         (int)k);
-    if (int rc = check_launch("tf_w4a8_linear_ex(e4m3 to fp16)")) return rc;
-    x16 = conv;
+  if (convert) {
+    x16 = reinterpret_cast<const uint16_t*>(workspace);
     const int64_t front = align_ws(m * k * 2);
     ws = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) + front);
     ws_bytes = workspace_bytes - front;
@@ -248,5 +243,14 @@ extern "C" int tf_w4a8_linear_ex(const uint8_t* x8, int64_t ldx8, const float* x
   if (m == 0 || n == 0) return TF_OK;
   const int64_t own = v->workspace(a, *cfg);
   if (own > 0 && (ws == nullptr || ws_bytes < own)) return fail(TF_EINVAL, "tf_w4a8_linear_ex: workspace too small");
+  if (v->check != nullptr)
+    if (int rc = v->check(a, *cfg)) return rc;
+  if (convert) {
+    uint16_t* conv = reinterpret_cast<uint16_t*>(workspace);
+    const int64_t chunks = m * (k / 8);
+    e4m3_rows_to_f16_kernel<<<(unsigned)cdiv(chunks, 256), 256, 0, (hipStream_t)stream>>>(x8, ldx8, conv, (int)m,
+                                                                                         (int)k);
+    if (int rc = check_launch("tf_w4a8_linear_ex(e4m3 to fp16)")) return rc;
+  }
   return v->launch(a, *cfg, ws, (hipStream_t)stream);
 }

@@ -5,9 +5,19 @@
 // qweight_t[8*nb + j][kb] (j = 0..7). Each thread moves whole 8x8 blocks in registers
 // (three masked-swap stages) and the tile is staged through LDS so that both the reads
 // and the writes are 128-byte coalesced rows.
+//
+// pack_awq's layout is the gfx950 tile layout (tile_layout.h): the tile kernels move 16-byte
+// weight chunks, scales and zero-point words between the reference's TokenForge layout and
+// it, one thread per destination element. awq_quantize (the test and benchmark fixture
+// generator) quantizes an fp32 [N, K] weight straight into AWQ format.
 #include "tf_common.h"
+#include "tile_layout.h"
 
 namespace tf {
+
+int log2_group(int32_t g);
+int check_group_size(int32_t group_size, int64_t k, const char* name);
+
 namespace {
 
 // AWQ_ORDER[i]: offset held by nibble i (pack.py:32).
@@ -133,20 +143,22 @@ __global__ void unpack_int4_kernel(const int32_t* __restrict__ packed, int32_t* 
   for (int j = 0; j < 8; ++j) v[j] = (int32_t)((w >> (4 * awq_nibble_of(j))) & 0xFu);
 }
 
-// qweight_t [n, k/8] -> out fp16 [n, k]; one thread per 4 packed words (32 values).
+// Tile-layout weights -> out fp16 [n, k] (nn.Linear layout); one thread per 16-byte chunk (32
+// values of one row), threads in row-major chunk order so the 64-byte stores are contiguous.
 __global__ void dequant_kernel(const uint32_t* __restrict__ qw, const uint16_t* __restrict__ scales,
                                const uint32_t* __restrict__ qzeros, uint16_t* __restrict__ out,
                                int64_t n, int64_t k, int log2_group) {
-  const int64_t chunks_per_row = k / 32;
+  const int64_t q_total = k / 32;
+  const int64_t p_total = k >> log2_group;
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n * chunks_per_row) return;
-  const int64_t row = i / chunks_per_row;
-  const int64_t ch = i % chunks_per_row;
-  const u4 words = *reinterpret_cast<const u4*>(qw + row * (k / 8) + ch * 4);
-  const int64_t grp = (ch * 32) >> log2_group;
-  const uint32_t zw = qzeros[grp * (n / 8) + row / 8];
-  const QuantParams p = make_params(zero_of(zw, (uint32_t)row), scales[grp * n + row]);
-  u4* dst = reinterpret_cast<u4*>(out + row * k + ch * 32);
+  if (i >= n * q_total) return;
+  const int64_t row = i / q_total;
+  const int64_t q = i % q_total;
+  const u4 words = *reinterpret_cast<const u4*>(qw + tile_chunk(row, q, n, q_total) * 4);
+  const int64_t grp = (q * 32) >> log2_group;
+  const uint32_t zw = qzeros[tile_zero(grp, row >> 3, n, p_total)];
+  const QuantParams p = make_params(zero_of(zw, (uint32_t)row), scales[tile_scale(grp, row, n, p_total)]);
+  u4* dst = reinterpret_cast<u4*>(out + row * k + q * 32);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     h2 v[4];
@@ -157,6 +169,108 @@ __global__ void dequant_kernel(const uint32_t* __restrict__ qw, const uint16_t* 
     o[2] = as_u32(v[2]);
     o[3] = as_u32(v[3]);
     dst[j] = o;
+  }
+}
+
+// One of the three tensors of a layer, moved between the TokenForge layout ("natural" index)
+// and the tile layout; TO_TILE gathers destination index i of the tile layout from its
+// natural source, the other direction gathers natural index i from its tile position.
+enum TileTensor { kTileWeights = 0, kTileScales = 1, kTileZeros = 2 };
+
+template <typename T, int KIND, bool TO_TILE>
+__global__ void tile_permute_kernel(const T* __restrict__ src, T* __restrict__ dst, int64_t count,
+                                    int64_t n, int64_t k, int log2_group) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= count) return;
+  const int64_t q_total = k / 32;
+  const int64_t p_total = k >> log2_group;
+  int64_t from;
+  if (KIND == kTileWeights) {
+    if (TO_TILE) {
+      int64_t row, q;
+      tile_chunk_source(i, n, q_total, &row, &q);
+      from = row * q_total + q;
+    } else {
+      from = tile_chunk(i / q_total, i % q_total, n, q_total);
+    }
+  } else if (KIND == kTileScales) {
+    if (TO_TILE) {
+      int64_t grp, row;
+      tile_scale_source(i, n, p_total, &grp, &row);
+      from = grp * n + row;
+    } else {
+      from = tile_scale(i / n, i % n, n, p_total);
+    }
+  } else {
+    const int64_t words = n / 8;
+    if (TO_TILE) {
+      int64_t grp, w;
+      tile_zero_source(i, n, p_total, &grp, &w);
+      from = grp * words + w;
+    } else {
+      from = tile_zero(i / words, i % words, n, p_total);
+    }
+  }
+  dst[i] = src[from];
+}
+
+template <bool TO_TILE>
+int launch_tile(const int32_t* qw, const uint16_t* sc, const int32_t* qz, int32_t* qw_out, uint16_t* sc_out,
+                int32_t* qz_out, int64_t n, int64_t k, int32_t group_size, hipStream_t stream, const char* name) {
+  const int lg = log2_group(group_size);
+  const int64_t chunks = n * (k / 32);
+  const int64_t groups = k / group_size;
+  if (chunks > 0)
+    tile_permute_kernel<u4, kTileWeights, TO_TILE><<<(unsigned)cdiv(chunks, 256), 256, 0, stream>>>(
+        reinterpret_cast<const u4*>(qw), reinterpret_cast<u4*>(qw_out), chunks, n, k, lg);
+  if (groups * n > 0)
+    tile_permute_kernel<uint16_t, kTileScales, TO_TILE><<<(unsigned)cdiv(groups * n, 256), 256, 0, stream>>>(
+        sc, sc_out, groups * n, n, k, lg);
+  if (groups * (n / 8) > 0)
+    tile_permute_kernel<uint32_t, kTileZeros, TO_TILE><<<(unsigned)cdiv(groups * (n / 8), 256), 256, 0, stream>>>(
+        reinterpret_cast<const uint32_t*>(qz), reinterpret_cast<uint32_t*>(qz_out), groups * (n / 8), n, k, lg);
+  return check_launch(name);
+}
+
+// AWQ min-max quantization of fp32 weight [n, k] (pack.py:83-107), one thread per (group p,
+// eight rows 8o..8o+7): the eight rows' statistics over the group, then the group's k words of
+// AWQ qweight [k, n/8] (word o of each row k), its qzeros word and its eight scales.
+//   scale = fp16(max(max - min, 1e-5) / 15), zero = clamp(-rint(min / scale), 0, 15),
+//   q = clamp(rint(w / scale) + zero, 0, 15); fp32 IEEE division, rint = round half to even.
+__global__ void awq_quantize_kernel(const float* __restrict__ w, int64_t n, int64_t k, int group,
+                                    uint32_t* __restrict__ qweight, uint32_t* __restrict__ qzeros,
+                                    uint16_t* __restrict__ scales) {
+  const int64_t octets = n / 8;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= octets * (k / group)) return;
+  const int64_t o = i % octets;  // consecutive threads: consecutive words of one qweight row
+  const int64_t p = i / octets;
+  float s[8], z[8];
+  uint32_t zword = 0;
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    const float* row = w + (o * 8 + r) * k + p * group;
+    float lo = row[0], hi = row[0];
+    for (int e = 1; e < group; ++e) {
+      lo = fminf(lo, row[e]);
+      hi = fmaxf(hi, row[e]);
+    }
+    const _Float16 s16 = (_Float16)(fmaxf(hi - lo, 1e-5f) / 15.0f);
+    s[r] = (float)s16;
+    z[r] = fminf(fmaxf(-__builtin_rintf(lo / s[r]), 0.0f), 15.0f);
+    scales[p * n + o * 8 + r] = __builtin_bit_cast(uint16_t, s16);
+    zword |= (uint32_t)z[r] << (4 * awq_nibble_of((uint32_t)r));
+  }
+  qzeros[p * octets + o] = zword;
+  for (int e = 0; e < group; ++e) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const float v = w[(o * 8 + r) * k + p * group + e];
+      const float q = fminf(fmaxf(__builtin_rintf(v / s[r]) + z[r], 0.0f), 15.0f);
+      word |= (uint32_t)q << (4 * awq_nibble_of((uint32_t)r));
+    }
+    qweight[(p * group + e) * octets + o] = word;
   }
 }
 
@@ -243,4 +357,46 @@ extern "C" int tf_w4a16_dequant(const int32_t* qweight_t, const uint16_t* scales
       reinterpret_cast<const uint32_t*>(qweight_t), scales, reinterpret_cast<const uint32_t*>(qzeros),
       out, n, k, log2_group(group_size));
   return check_launch("tf_w4a16_dequant");
+}
+
+static int check_tile_args(const void* a, const void* b, const void* c, const void* d, const void* e,
+                           const void* f, int64_t n, int64_t k, int32_t group_size, const char* name) {
+  if (!a || !b || !c || !d || !e || !f) return fail(TF_EINVAL, std::string(name) + ": null pointer");
+  if (n < 0 || k < 0 || n % 8) return fail(TF_EINVAL, std::string(name) + ": N must be a multiple of 8");
+  if (int rc = check_group_size(group_size, k, name)) return rc;
+  if (!aligned16(a) || !aligned16(d)) return fail(TF_EINVAL, std::string(name) + ": qweight must be 16-byte aligned");
+  return TF_OK;
+}
+
+extern "C" int tf_tile_pack(const int32_t* qweight_t, const uint16_t* scales, const int32_t* qzeros,
+                            int32_t* qweight_tile, uint16_t* scales_tile, int32_t* qzeros_tile, int64_t n,
+                            int64_t k, int32_t group_size, void* stream) {
+  if (int rc = check_tile_args(qweight_t, scales, qzeros, qweight_tile, scales_tile, qzeros_tile, n, k,
+                               group_size, "tf_tile_pack"))
+    return rc;
+  return launch_tile<true>(qweight_t, scales, qzeros, qweight_tile, scales_tile, qzeros_tile, n, k, group_size,
+                           (hipStream_t)stream, "tf_tile_pack");
+}
+
+extern "C" int tf_tile_unpack(const int32_t* qweight_tile, const uint16_t* scales_tile, const int32_t* qzeros_tile,
+                              int32_t* qweight_t, uint16_t* scales, int32_t* qzeros, int64_t n, int64_t k,
+                              int32_t group_size, void* stream) {
+  if (int rc = check_tile_args(qweight_tile, scales_tile, qzeros_tile, qweight_t, scales, qzeros, n, k,
+                               group_size, "tf_tile_unpack"))
+    return rc;
+  return launch_tile<false>(qweight_tile, scales_tile, qzeros_tile, qweight_t, scales, qzeros, n, k, group_size,
+                            (hipStream_t)stream, "tf_tile_unpack");
+}
+
+extern "C" int tf_awq_quantize(const float* weight, int64_t n, int64_t k, int32_t group_size, int32_t* qweight,
+                               int32_t* qzeros, uint16_t* scales, void* stream) {
+  if (!weight || !qweight || !qzeros || !scales) return fail(TF_EINVAL, "tf_awq_quantize: null pointer");
+  if (n < 0 || k < 0 || n % 8) return fail(TF_EINVAL, "tf_awq_quantize: N must be a multiple of 8");
+  if (group_size <= 0 || k % group_size)
+    return fail(TF_EINVAL, "tf_awq_quantize: K is not a multiple of group_size");
+  const int64_t threads = (n / 8) * (k / group_size);
+  if (threads == 0) return TF_OK;
+  awq_quantize_kernel<<<(unsigned)cdiv(threads, 256), 256, 0, (hipStream_t)stream>>>(
+      weight, n, k, group_size, reinterpret_cast<uint32_t*>(qweight), reinterpret_cast<uint32_t*>(qzeros), scales);
+  return check_launch("tf_awq_quantize");
 }
