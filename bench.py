@@ -636,6 +636,7 @@ def read_probes(dev: torch.device, layers: list, copies: int, xs: list, cfgs: li
     Prints a table to stderr and one JSON line {"read_probe": ...} to stdout."""
     import ctypes
 
+    from tokenforge.kernels.config import candidate_configs
     from tokenforge.kernels.hip.w4a16 import w4a16_gemm
 
     plib = ctypes.CDLL(str(ROOT / "tokenforge_amd" / "lib" / "libtokenforge_probes.so"))
@@ -657,14 +658,19 @@ def read_probes(dev: torch.device, layers: list, copies: int, xs: list, cfgs: li
     for i, (name, n, k) in enumerate(SHAPES):
         weight_bytes = n * k // 2
         meta_bytes = (k // GROUP) * n * 2 + (k // GROUP) * n // 2
-        x, cfg = xs[i], cfgs[i]
-        g, _ = capture([lambda c=c: w4a16_gemm(x, *layers[c][i], GROUP, cfg) for c in range(copies)])
-        us = median_replay_ms(g, copies) * 1e3
-        rows.append({"probe": "gemv", "layer": name, "n": n, "k": k, "config": cfg.to_dict(), "us": us,
-                     "gbps": bytes_moved(1, n, k) / us / 1e3})
-        log(f"  {name:13s} GEMV {cfg.kernel} bn{cfg.block_n} bk{cfg.block_k} w{cfg.num_warps} "
-            f"st{cfg.num_stages}: {us:6.2f} us {bytes_moved(1, n, k) / us / 1e3:6.0f} GB/s")
-        del g
+        x = xs[i]
+        sweep = []
+        for cfg in [cfgs[i]] + [c for c in candidate_configs(1, GROUP) if c != cfgs[i]]:
+            g, _ = capture([lambda c=c, cfg=cfg: w4a16_gemm(x, *layers[c][i], GROUP, cfg) for c in range(copies)])
+            us = median_replay_ms(g, copies) * 1e3
+            del g
+            sweep.append((us, cfg))
+            rows.append({"probe": "gemv", "layer": name, "n": n, "k": k, "config": cfg.to_dict(), "us": us,
+                         "gbps": bytes_moved(1, n, k) / us / 1e3, "tuned": cfg == cfgs[i]})
+        for us, cfg in [sweep[0]] + sorted(sweep[1:], key=lambda t: t[0])[:4]:
+            log(f"  {name:13s} GEMV {'tuned' if cfg == cfgs[i] else 'cand '} bm{cfg.block_m} bn{cfg.block_n} "
+                f"bk{cfg.block_k} w{cfg.num_warps} st{cfg.num_stages}: {us:6.2f} us "
+                f"{bytes_moved(1, n, k) / us / 1e3:6.0f} GB/s")
         best: dict[int, tuple[float, int, int]] = {}
         for pattern in (0, 1, 2, 3):
             combos = [(w, d) for w in (1, 2, 4, 8, 16) for d in (2, 4, 8)] if pattern < 3 else \

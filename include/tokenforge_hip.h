@@ -105,6 +105,7 @@ int tf_w4a16_dequant(const int32_t* qweight_t, const uint16_t* scales,
 /* --------------------------------------------------------------- W4A16 linear */
 
 /* Kernel families (the `kernel` field of tf_gemm_config). */
+#define TF_KERNEL_GEMV_DOT 0   /* decode: in-register dequant + VALU dot2, M <= 4     */
 #define TF_KERNEL_GEMV_MFMA 1  /* decode: in-register dequant + fp16 MFMA (M <= 32)   */
 #define TF_KERNEL_GEMM_MFMA 2  /* prefill: LDS-staged dequant + fp16 MFMA, split-K    */
 

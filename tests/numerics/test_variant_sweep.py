@@ -36,7 +36,9 @@ def _case(index: int, variant: tuple) -> dict:  # type: ignore[type-arg]
     n = 8 * rng.randint(8, 64)
     if rng.random() < 0.5:
         n = 16 * rng.randint(4, 32)  # a multiple of 16 (the SiLU*mul epilogue needs it)
-    if kernel == "gemv_mfma":
+    if kernel == "gemv_dot":
+        m = rng.randint(1, bm)
+    elif kernel == "gemv_mfma":
         m = rng.randint(1, 2 * bm + 3)
     else:
         m = rng.randint(1, 2 * bm + 5)

@@ -68,6 +68,12 @@ def test_linear_shape_suite(shape, m: int, device: torch.device) -> None:  # typ
 
 
 PATH_CONFIGS = [
+    GemmConfig("gemv_dot", 1, 16, 128, 1, 4, 2),
+    GemmConfig("gemv_dot", 1, 32, 128, 1, 2, 2),
+    GemmConfig("gemv_dot", 2, 16, 128, 1, 2, 2),
+    GemmConfig("gemv_dot", 4, 16, 128, 1, 8, 2),
+    GemmConfig("gemv_dot", 1, 16, 256, 1, 4, 4),
+    GemmConfig("gemv_dot", 4, 16, 256, 1, 8, 4),
     GemmConfig("gemv_mfma", 16, 16, 128, 1, 1, 2),
     GemmConfig("gemv_mfma", 16, 64, 128, 1, 4, 2),
     GemmConfig("gemv_mfma", 16, 32, 128, 1, 8, 4),
@@ -125,6 +131,8 @@ PATH_CONFIGS = [
 
 
 def _m_list(cfg: GemmConfig) -> tuple[int, ...]:
+    if cfg.kernel == "gemv_dot":
+        return tuple(sorted({1, cfg.block_m}))
     return (1, cfg.block_m - 1, cfg.block_m + 3)
 
 

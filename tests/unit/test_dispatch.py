@@ -174,10 +174,12 @@ def test_candidates_are_valid(bucket: int, group: int) -> None:
         assert families == {"gemv", "gemm"}
 
 
-def test_decode_buckets_offer_both_gemv_work_splits() -> None:
+def test_decode_buckets_offer_both_gemv_forms_and_work_splits() -> None:
     cands = candidate_configs(1, 128)
-    assert {c.kernel for c in cands} == {"gemv_mfma"}
+    assert {c.kernel for c in cands} == {"gemv_dot", "gemv_mfma"}
     assert {c.block_k for c in cands} == {128, 256}  # K split over the waves, or columns split
+    assert {c.kernel for c in candidate_configs(8, 128)} == {"gemv_mfma"}  # dot form: M <= 4
+    assert {c.block_m for c in candidate_configs(4, 128) if c.kernel == "gemv_dot"} == {4}
     assert {c.block_m for c in candidate_configs(32, 128) if c.family == "gemv"} == {16, 32}
 
 

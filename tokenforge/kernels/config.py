@@ -15,6 +15,9 @@ Field meaning per kernel family:
 ========== =========================== ================================================
 kernel     block_m / block_n / block_k  split_k / num_warps / num_stages
 ========== =========================== ================================================
+gemv_dot   max M (1,2,4) / columns per  1 / waves per workgroup / 128-wide K steps in
+           workgroup (16*RT) / 128 or   flight per wave; block_k as for gemv_mfma
+           256
 gemv_mfma  M per tile (16,32) / columns 1 / waves per workgroup / 128-wide K steps in
            per workgroup (16*RT) / 128  flight per wave. block_k 128: the waves split
            or 256                       K over the same columns and add their partials
@@ -43,7 +46,7 @@ GEMV_MAX_M = 32
 GEMM_MIN_M = 16
 """Smallest bucket the gemm_mfma kernels may serve (the tuner weighs both families at 16, 32)."""
 
-KERNELS: tuple[str, ...] = ("gemv_mfma", "gemm_mfma")
+KERNELS: tuple[str, ...] = ("gemv_dot", "gemv_mfma", "gemm_mfma")
 NUM_CUS = 256
 """MI355X compute units; the split heuristics aim to put several waves on each."""
 
@@ -54,6 +57,10 @@ _WAVES = (1, 2, 4, 8, 16)
 # block_k = 256: the waves take different column tiles over the whole K and share one copy of
 # x. The wave cap keeps each variant within the VGPR budget of its launch bound (no spills).
 GEMV_TEMPLATES: tuple[tuple[str, int, int, int, int, int], ...] = (
+    ("gemv_dot", 1, 1, 128, 2, 16), ("gemv_dot", 1, 1, 128, 4, 16), ("gemv_dot", 1, 2, 128, 2, 16),
+    ("gemv_dot", 2, 1, 128, 2, 16), ("gemv_dot", 4, 1, 128, 2, 16),
+    ("gemv_dot", 1, 1, 256, 2, 8), ("gemv_dot", 1, 1, 256, 4, 8), ("gemv_dot", 2, 1, 256, 4, 8),
+    ("gemv_dot", 4, 1, 256, 4, 8),
     ("gemv_mfma", 16, 1, 128, 2, 16), ("gemv_mfma", 16, 1, 128, 4, 16), ("gemv_mfma", 16, 1, 128, 8, 16),
     ("gemv_mfma", 16, 2, 128, 2, 16), ("gemv_mfma", 16, 2, 128, 4, 8), ("gemv_mfma", 16, 4, 128, 2, 8),
     ("gemv_mfma", 32, 1, 128, 2, 16), ("gemv_mfma", 32, 2, 128, 2, 8),
@@ -162,10 +169,13 @@ class GemmConfig:
 
     def fits_bucket(self, bucket: int) -> bool:
         """Whether this config may serve M values of ``bucket`` (cache validation): the gemv
-        kernels serve buckets up to GEMV_MAX_M, gemm_mfma buckets from GEMM_MIN_M on."""
+        kernels serve buckets up to GEMV_MAX_M (gemv_dot only up to its block_m), gemm_mfma
+        buckets from GEMM_MIN_M on."""
         if self.family == "gemm":
             return bucket >= GEMM_MIN_M
-        return bucket <= GEMV_MAX_M
+        if bucket > GEMV_MAX_M:
+            return False
+        return self.kernel != "gemv_dot" or self.block_m >= bucket
 
     def to_dict(self) -> dict[str, Any]:
         return asdict(self)

@@ -28,10 +28,6 @@
 #include "linear.h"
 #include "tile_layout.h"
 
-#ifndef TF_GEMV_EARLY
-#define TF_GEMV_EARLY 0
-#endif
-
 namespace tf {
 namespace {
 // K range [s0, s1) of 128-wide steps owned by `wave`; waves is a power of two (every compiled
@@ -282,8 +278,14 @@ constexpr int kStageU = 2;  // x staging chunks per lane and batch
 
 // ------------------------------------------------------------------------ kernel
 
-template <int MT, int RT, int P, int MAXW, bool UNIFORM, bool SPLITN>
+// DOTM == 0: the MFMA form (MT tiles of 16 rows). DOTM = 1, 2 or 4: the dot form for M <= DOTM
+// (MT = 1): each lane multiplies its 32 K values of its column with v_dot2_f32_f16 for every
+// row of x, and the four lanes of a column (K blocks g = 0..3) are added at the end in a fixed
+// order. The dot form keeps the products on the VALU, next to the dequantization, instead of
+// in the matrix core's dependent chain.
+template <int MT, int RT, int P, int MAXW, bool UNIFORM, bool SPLITN, int DOTM = 0>
 __global__ __launch_bounds__(MAXW * 64) void gemv_kernel(LinearArgs a, int win) {
+  static_assert(DOTM == 0 || MT == 1, "the dot form serves one M tile");
   extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -304,18 +306,25 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_kernel(LinearArgs a, int win) 
   const UnpackConsts uc = unpack_consts();
   const LaneStream<RT, UNIFORM> ls_w(a, st, n_base, c, g, s1);
 
-  const _Float16* xl[MT];
+  // MFMA form: lane c reads row c of each M tile (the A operand); dot form: every lane reads
+  // rows 0 .. DOTM - 1. Rows past M read a staged row and feed outputs that are never stored.
+  constexpr int XP = DOTM ? DOTM : MT;
+  const _Float16* xl[XP];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int r = mt * 16 + c;
-    xl[mt] = xs + (r < xrows ? r : 0) * L.xstride + g * 32;  // rows past M feed discarded outputs
+  for (int i = 0; i < XP; ++i) {
+    const int r = DOTM ? i : i * 16 + c;
+    xl[i] = xs + (r < xrows ? r : 0) * L.xstride + g * 32;
   }
 
-  f4 acc[MT][RT];
+  f4 acc[DOTM ? 1 : MT][RT];
+  float dacc[DOTM ? DOTM : 1][RT];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
+  for (int rt = 0; rt < RT; ++rt) {
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt) acc[mt][rt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int mt = 0; mt < (DOTM ? 1 : MT); ++mt) acc[mt][rt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int m = 0; m < (DOTM ? DOTM : 1); ++m) dacc[m][rt] = 0.0f;
+  }
 
   // The first staging batch goes out ahead of the weight ring: every wave of the grid issues
   // its ring at once, and the x chunks that gate the first step must not queue behind it.
@@ -347,20 +356,14 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_kernel(LinearArgs a, int win) 
 #pragma unroll
       for (int p = 0; p < P; ++p) {
         const int step = s + p;
-#if TF_GEMV_EARLY
-        const Slot<RT> cur = ring[p];
-        ls_w.issue(ring[p], st, step + P);
-        __builtin_amdgcn_sched_barrier(0);
-#else
         const Slot<RT>& cur = ring[p];
-#endif
         if (step < w1) {
           const int ls = step - w0;
-          h8 xa[MT][4];
+          h8 xa[XP][4];
 #pragma unroll
-          for (int mt = 0; mt < MT; ++mt)
+          for (int i = 0; i < XP; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) xa[mt][j] = *reinterpret_cast<const h8*>(xl[mt] + ls * 128 + j * 8);
+            for (int j = 0; j < 4; ++j) xa[i][j] = *reinterpret_cast<const h8*>(xl[i] + ls * 128 + j * 8);
 #pragma unroll
           for (int rt = 0; rt < RT; ++rt) {
             const QuantParams qp = ls_w.params(cur, rt);
@@ -368,16 +371,24 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_kernel(LinearArgs a, int win) 
             for (int j = 0; j < 4; ++j) {
               h2 wd[4];
               dequant_word(cur.w[rt][j], qp, uc, wd);
-              const h8 b = pack_h8(wd);
+              if constexpr (DOTM == 0) {
+                const h8 b = pack_h8(wd);
 #pragma unroll
-              for (int mt = 0; mt < MT; ++mt)
-                acc[mt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[mt][j], b, acc[mt][rt], 0, 0, 0);
+                for (int mt = 0; mt < MT; ++mt)
+                  acc[mt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[mt][j], b, acc[mt][rt], 0, 0, 0);
+              } else {
+#pragma unroll
+                for (int m = 0; m < DOTM; ++m) {
+                  const u4 xv = __builtin_bit_cast(u4, xa[m][j]);
+#pragma unroll
+                  for (int e = 0; e < 4; ++e)
+                    dacc[m][rt] = __builtin_amdgcn_fdot2(as_h2(xv[e]), wd[e], dacc[m][rt], false);
+                }
+              }
             }
           }
         }
-#if !TF_GEMV_EARLY
         ls_w.issue(ring[p], st, step + P);
-#endif
         // Slot boundary: keep the next slot's operand work (which waits for its loads) from
         // being hoisted above this point, where it would wait for more of the ring than needed.
         __builtin_amdgcn_sched_barrier(0);
@@ -385,40 +396,72 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_kernel(LinearArgs a, int win) 
     }
   }
 
+  if constexpr (DOTM != 0) {
+    // The four K blocks of each column (lanes c, c + 16, c + 32, c + 48): one fixed tree, whose
+    // result lane c (g == 0) stores.
+#pragma unroll
+    for (int m = 0; m < DOTM; ++m)
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        dacc[m][rt] += __shfl_xor(dacc[m][rt], 16);
+        dacc[m][rt] += __shfl_xor(dacc[m][rt], 32);
+      }
+  }
+
   if (!SPLITN && waves > 1) {
-    float* red = reinterpret_cast<float*>(lds + waves * L.wave_words);  // [(waves - 1)][MT][RT][64][4]
-    if (wave > 0) {
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt)
-          *reinterpret_cast<f4*>(&red[((((wave - 1) * MT + mt) * RT + rt) * 64 + lane) * 4]) = acc[mt][rt];
-    }
-    __syncthreads();
-    if (wave == 0) {
-      for (int w = 1; w < waves; ++w)
+    float* red = reinterpret_cast<float*>(lds + waves * L.wave_words);
+    if constexpr (DOTM == 0) {  // [(waves - 1)][MT][RT][64][4]
+      if (wave > 0) {
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
           for (int rt = 0; rt < RT; ++rt)
-            acc[mt][rt] += *reinterpret_cast<const f4*>(&red[((((w - 1) * MT + mt) * RT + rt) * 64 + lane) * 4]);
+            *reinterpret_cast<f4*>(&red[((((wave - 1) * MT + mt) * RT + rt) * 64 + lane) * 4]) = acc[mt][rt];
+      }
+      __syncthreads();
+      if (wave == 0) {
+        for (int w = 1; w < waves; ++w)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt)
+              acc[mt][rt] += *reinterpret_cast<const f4*>(&red[((((w - 1) * MT + mt) * RT + rt) * 64 + lane) * 4]);
+      }
+    } else {  // [(waves - 1)][DOTM][RT][16]
+      if (wave > 0 && g == 0) {
+#pragma unroll
+        for (int m = 0; m < DOTM; ++m)
+#pragma unroll
+          for (int rt = 0; rt < RT; ++rt) red[(((wave - 1) * DOTM + m) * RT + rt) * 16 + c] = dacc[m][rt];
+      }
+      __syncthreads();
+      if (wave == 0) {
+        for (int w = 1; w < waves; ++w)
+#pragma unroll
+          for (int m = 0; m < DOTM; ++m)
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) dacc[m][rt] += red[(((w - 1) * DOTM + m) * RT + rt) * 16 + c];
+      }
     }
   }
   if (SPLITN || wave == 0) {
-    // D layout of v_mfma_f32_16x16x32_f16: lane holds rows 4*(lane/16) + r, column lane%16.
-    // Under SiLU*mul lanes c and c ^ 8 hold the gate and up columns of one output.
+    // MFMA form, D layout of v_mfma_f32_16x16x32_f16: lane holds rows 4*(lane/16) + r, column
+    // lane%16. Dot form: lane c (g == 0) holds column c of every row. Under SiLU*mul lanes c
+    // and c ^ 8 hold the gate and up columns of one output.
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
       const int l = rt * 16 + c;
       const int n = phys_col(a, n_base, l);
-      const bool valid = col_valid(a, n_base, l);
+      const bool valid = col_valid(a, n_base, l) && (DOTM == 0 || g == 0);
       const float b = (a.bias && valid) ? half_bits_to_float(a.bias[n]) : 0.0f;
+      constexpr int ROWS = DOTM ? DOTM : 4;
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+      for (int mt = 0; mt < (DOTM ? 1 : MT); ++mt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int m = m_base + mt * 16 + 4 * g + r;
-          const float v = acc[mt][rt][r] * row_scale(a, m) + b;
+        for (int r = 0; r < ROWS; ++r) {
+          const int m = DOTM ? r : m_base + mt * 16 + 4 * g + r;
+          const float sum = DOTM ? dacc[DOTM ? r : 0][rt] : acc[mt][rt][DOTM ? 0 : r];
+          const float v = sum * row_scale(a, m) + b;
           if (a.epilogue == TF_EPILOGUE_SILU_MUL) {
             const float u = __shfl_xor(v, 8);
             if (valid && !(l & 8) && m < a.m)
@@ -497,29 +540,31 @@ GemvPlan plan_gemv(const LinearArgs& a, int waves, int depth, int x_rows, size_t
 bool uniform_steps(const LinearArgs& a) { return (a.k & 127) == 0 && (a.n & 15) == 0; }
 
 // LDS bytes and staging window of a launch; win == 0 when it does not fit the device.
-template <int MT, int RT, int P, bool SPLITN>
+template <int MT, int RT, int P, bool SPLITN, int DOTM = 0>
 GemvPlan gemv_plan(const LinearArgs& a, int waves) {
   const int xrows = a.m < 16 * MT ? a.m : 16 * MT;
+  const size_t red_per_wave = DOTM ? (size_t)DOTM * RT * 16 * sizeof(float) : (size_t)MT * RT * 64 * 4 * sizeof(float);
   if (SPLITN) {  // one shared copy of all of x, no reduction buffer
     const int nsteps = ((a.k >> 5) + 3) >> 2;
     const GemvPlan p{nsteps, (size_t)gemv_lds_layout(nsteps, xrows).wave_words * 4};
     return p.lds <= device_max_lds() ? p : GemvPlan{0, 0};
   }
-  return plan_gemv(a, waves, P, xrows, (size_t)MT * RT * 64 * 4 * sizeof(float));
+  return plan_gemv(a, waves, P, xrows, red_per_wave);
 }
 
-template <int MT, int RT, int P, int MAXW, bool SPLITN>
+template <int MT, int RT, int P, int MAXW, bool SPLITN, int DOTM = 0>
 int check_gemv(const LinearArgs& a, const tf_gemm_config& cfg) {
+  if (DOTM != 0 && a.m > DOTM) return fail(TF_EINVAL, "tf_w4a16_linear: gemv_dot variant needs m <= block_m");
   if (int rc = check_offsets(a)) return rc;
-  if (gemv_plan<MT, RT, P, SPLITN>(a, cfg.num_warps).win == 0)
+  if (gemv_plan<MT, RT, P, SPLITN, DOTM>(a, cfg.num_warps).win == 0)
     return fail(TF_EINVAL, SPLITN ? "tf_w4a16_linear: gemv variant (block_k 256) needs x to fit the device's LDS"
                                   : "tf_w4a16_linear: gemv variant does not fit the device's LDS");
   return TF_OK;
 }
 
-template <int MT, int RT, int P, int MAXW, bool UNIFORM, bool SPLITN>
+template <int MT, int RT, int P, int MAXW, bool UNIFORM, bool SPLITN, int DOTM>
 int launch_k(const LinearArgs& a, int waves, const GemvPlan& plan, hipStream_t stream) {
-  auto kernel = gemv_kernel<MT, RT, P, MAXW, UNIFORM, SPLITN>;
+  auto kernel = gemv_kernel<MT, RT, P, MAXW, UNIFORM, SPLITN, DOTM>;
   if (int rc = reserve_lds(kernel, plan.lds, "gemv")) return rc;
   const int tiles = (int)cdiv(a.n, 16 * RT);
   const dim3 grid((unsigned)(SPLITN ? cdiv(tiles, waves) : tiles), (unsigned)cdiv(a.m, 16 * MT));
@@ -527,12 +572,12 @@ int launch_k(const LinearArgs& a, int waves, const GemvPlan& plan, hipStream_t s
   return check_launch("tf_w4a16_linear(gemv)");
 }
 
-template <int MT, int RT, int P, int MAXW, bool SPLITN>
+template <int MT, int RT, int P, int MAXW, bool SPLITN, int DOTM = 0>
 int launch_gemv(const LinearArgs& a, const tf_gemm_config& cfg, float*, hipStream_t stream) {
-  if (int rc = check_gemv<MT, RT, P, MAXW, SPLITN>(a, cfg)) return rc;
-  const GemvPlan plan = gemv_plan<MT, RT, P, SPLITN>(a, cfg.num_warps);
-  return uniform_steps(a) ? launch_k<MT, RT, P, MAXW, true, SPLITN>(a, cfg.num_warps, plan, stream)
-                          : launch_k<MT, RT, P, MAXW, false, SPLITN>(a, cfg.num_warps, plan, stream);
+  if (int rc = check_gemv<MT, RT, P, MAXW, SPLITN, DOTM>(a, cfg)) return rc;
+  const GemvPlan plan = gemv_plan<MT, RT, P, SPLITN, DOTM>(a, cfg.num_warps);
+  return uniform_steps(a) ? launch_k<MT, RT, P, MAXW, true, SPLITN, DOTM>(a, cfg.num_warps, plan, stream)
+                          : launch_k<MT, RT, P, MAXW, false, SPLITN, DOTM>(a, cfg.num_warps, plan, stream);
 }
 
 // One table row per (variant, num_warps): num_warps ranges over 1..MAXW (powers of two).
@@ -552,7 +597,16 @@ int launch_gemv(const LinearArgs& a, const tf_gemm_config& cfg, float*, hipStrea
   TF_W##MAXW(TF_KERNEL_GEMV_MFMA, 16 * MT, 16 * RT, 256, P, (launch_gemv<MT, RT, P, MAXW, true>), \
              (check_gemv<MT, RT, P, MAXW, true>))
 
+#define TF_DOT(BM, RT, P, MAXW) \
+  TF_W##MAXW(TF_KERNEL_GEMV_DOT, BM, 16 * RT, 128, P, (launch_gemv<1, RT, P, MAXW, false, BM>), \
+             (check_gemv<1, RT, P, MAXW, false, BM>))
+#define TF_DOT_N(BM, RT, P, MAXW) \
+  TF_W##MAXW(TF_KERNEL_GEMV_DOT, BM, 16 * RT, 256, P, (launch_gemv<1, RT, P, MAXW, true, BM>), \
+             (check_gemv<1, RT, P, MAXW, true, BM>))
+
 const Variant kGemvVariants[] = {
+    TF_DOT(1, 1, 2, 16), TF_DOT(1, 1, 4, 16), TF_DOT(1, 2, 2, 16), TF_DOT(2, 1, 2, 16), TF_DOT(4, 1, 2, 16),
+    TF_DOT_N(1, 1, 2, 8), TF_DOT_N(1, 1, 4, 8), TF_DOT_N(2, 1, 4, 8), TF_DOT_N(4, 1, 4, 8),
     TF_GEMV(1, 1, 2, 16), TF_GEMV(1, 1, 4, 16), TF_GEMV(1, 1, 8, 16), TF_GEMV(1, 2, 2, 16),
     TF_GEMV(1, 2, 4, 8),  TF_GEMV(1, 4, 2, 8),  TF_GEMV(2, 1, 2, 16), TF_GEMV(2, 2, 2, 8),
     TF_GEMV_N(1, 1, 2, 8), TF_GEMV_N(1, 1, 4, 8), TF_GEMV_N(1, 1, 8, 8), TF_GEMV_N(1, 2, 2, 8),

@@ -63,7 +63,9 @@ int check_config(const tf_gemm_config& cfg, int32_t group_size) {
 
 // Configs whose kernels read e4m3 x themselves (they stage x in LDS): every GEMV config. The
 // GEMM configs get x converted to fp16 first.
-bool fuses_x8(const tf_gemm_config& cfg) { return cfg.kernel == TF_KERNEL_GEMV_MFMA; }
+bool fuses_x8(const tf_gemm_config& cfg) {
+  return cfg.kernel == TF_KERNEL_GEMV_MFMA || cfg.kernel == TF_KERNEL_GEMV_DOT;
+}
 
 constexpr int64_t kWsAlign = 256;
 int64_t align_ws(int64_t b) { return (b + kWsAlign - 1) / kWsAlign * kWsAlign; }
