@@ -172,6 +172,22 @@ int tf_w4a16_linear_ex(const uint16_t* x, int64_t ldx, const int32_t* qweight_t,
                        const uint16_t* residual, int64_t ldr, float* workspace,
                        int64_t workspace_bytes, void* stream);
 
+/* tf_w4a16_linear_ex that allocates nothing. No counterpart in the reference: for callers that
+ * cannot allocate device memory (code under HIP-graph capture that must not call hipMalloc,
+ * tight serving loops, harnesses that forbid allocation). The workspace the kernels need
+ * (split-K partials, the SiLU*mul rows of the LDS-tile GEMMs) comes from a fixed device array
+ * of tf_noalloc_scratch_bytes() bytes (32 MiB) that each GPU holds until the process ends; a
+ * call needing more is rejected (TF_EINVAL). Nothing needs clearing between calls. All calls
+ * on one GPU share that array: calls that overlap in time on one GPU (other streams, other
+ * host threads) race, and the caller must serialize them. Arguments as tf_w4a16_linear_ex
+ * without the workspace. */
+int64_t tf_noalloc_scratch_bytes(void);
+int tf_w4a16_linear_ex_noalloc(const uint16_t* x, int64_t ldx, const int32_t* qweight_t,
+                               const uint16_t* scales, const int32_t* qzeros, const uint16_t* bias,
+                               uint16_t* out, int64_t ldo, int64_t m, int64_t n, int64_t k,
+                               int32_t group_size, const tf_gemm_config* cfg, int32_t epilogue,
+                               const uint16_t* residual, int64_t ldr, void* stream);
+
 /* W4A8: the linear on FP8 activations, e.g. tf_rmsnorm_fp8_quant's codes and scales. No
  * counterpart in the reference, which never feeds its FP8 output to a linear.
  *   out[m][n] = fp16( xscale[m] * sum_k e4m3(x8[m][k]) * fp16((q[n][k] - z) * s) + bias[n] )

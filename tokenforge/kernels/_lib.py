@@ -83,6 +83,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_p, _i64, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i32,
          ctypes.POINTER(TfGemmConfig), _i32, _p, _i64, _p, _i64, _p],
     ),
+    "tf_noalloc_scratch_bytes": (_i64, []),
+    "tf_w4a16_linear_ex_noalloc": (
+        ctypes.c_int,
+        [_p, _i64, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i32,
+         ctypes.POINTER(TfGemmConfig), _i32, _p, _i64, _p],
+    ),
     "tf_w4a8_workspace_bytes_ex": (_i64, [_i64, _i64, _i64, _i32, ctypes.POINTER(TfGemmConfig), _i32]),
     "tf_w4a8_linear_ex": (
         ctypes.c_int,
