@@ -68,3 +68,45 @@ def test_workspace_query_is_host_only() -> None:
     assert h.tf_w4a16_workspace_bytes(1, 3584, 3584, 128, ctypes.byref(gemv)) == 0
     unknown = _lib.TfGemmConfig(2, 96, 128, 64, 1, 4, 2)
     assert h.tf_w4a16_workspace_bytes(256, 3584, 3584, 128, ctypes.byref(unknown)) == 0
+
+
+# Fake device addresses: 16-byte aligned, never dereferenced (every call below is rejected on
+# the host before anything is launched, so this runs without a GPU).
+_X, _W, _S, _Z, _O, _WS = (0x10000 * (i + 1) for i in range(6))
+
+
+def test_w4a8_rejects_before_launching() -> None:
+    """A W4A8 call on a GEMM config (which would first convert x into the workspace) that names
+    no compiled variant is rejected with TF_EINVAL before the conversion kernel is queued; a
+    launch attempt without a GPU would have returned TF_ELAUNCH instead."""
+    h = _lib.lib()
+    bad = _lib.TfGemmConfig(2, 96, 128, 64, 1, 4, 2)  # no such gemm_mfma tile
+    rc = h.tf_w4a8_linear_ex(_X, 256, _S, 1, _W, _S, _Z, None, _O, 1152, 64, 1152, 256, 128,
+                             ctypes.byref(bad), 0, None, 0, _WS, 1 << 20, None)
+    assert rc == _lib.TF_EINVAL
+    assert b"compiled variant" in h.tf_last_error()
+    # A good config with a workspace that is too small: also rejected on the host.
+    good = _lib.TfGemmConfig(2, 128, 128, 64, 2, 4, 2)
+    rc = h.tf_w4a8_linear_ex(_X, 256, _S, 1, _W, _S, _Z, None, _O, 1152, 64, 1152, 256, 128,
+                             ctypes.byref(good), 0, None, 0, _WS, 16, None)
+    assert rc == _lib.TF_EINVAL
+    assert b"workspace too small" in h.tf_last_error()
+    # A GEMV config whose own launch checks fail (x of 4 rows at K = 131072 does not fit the
+    # shared-x form's LDS): rejected by the variant's check, before any launch.
+    gemv = _lib.TfGemmConfig(1, 16, 16, 256, 1, 4, 2)
+    rc = h.tf_w4a8_linear_ex(_X, 131072, _S, 1, _W, _S, _Z, None, _O, 64, 4, 64, 131072, 128,
+                             ctypes.byref(gemv), 0, None, 0, None, 0, None)
+    assert rc == _lib.TF_EINVAL
+    assert b"LDS" in h.tf_last_error()
+
+
+def test_noalloc_rejects_a_workspace_above_its_array_on_the_host() -> None:
+    h = _lib.lib()
+    cfg = _lib.TfGemmConfig(2, 128, 128, 64, 8, 4, 2)
+    m, n, k = 4096, 37888, 3584
+    assert h.tf_w4a16_workspace_bytes_ex(m, n, k, 128, ctypes.byref(cfg), 0) > h.tf_noalloc_scratch_bytes()
+    rc = h.tf_w4a16_linear_ex_noalloc(_X, k, _W, _S, _Z, None, _O, n, m, n, k, 128, ctypes.byref(cfg), 0,
+                                      None, 0, None)
+    assert rc == _lib.TF_EINVAL
+    assert b"bytes of workspace" in h.tf_last_error()
+    assert h.tf_noalloc_scratch_bytes() == 32 << 20
