@@ -1,0 +1,155 @@
+"""BASELINE configs 4 and 5 at full Qwen2.5-7B size on the GPU.
+
+Config 4 (prefill GEMM): gate_up (37888 x 3584) and down (3584 x 18944), int4 group 128 with
+nibbles and zero points uniform in [0, 15] and scales uniform in [1e-3, 1e-2], x ~ N(0, 1) with
+ceil(1% M) rows (randperm) scaled x10, for M in {16, 32, 64, 128, 256, 1024, 4096}: every M
+goes through torch.ops.tokenforge.w4a16_linear, i.e. dispatch and a cache tuned for these
+shapes in this test. Each output is compared with an fp32 product of the exactly dequantized
+weights (the dequant kernel is bit-exact with the oracle's dequantize_tf): within the derived
+bound c sqrt(K) eps16 max|x| max|w| plus half an fp16 ulp of the output (the result is rounded
+to fp16 once; at these weights |y| reaches ~10-100, where that rounding exceeds a bound made
+for |y| of order one) and within 1e-2 normwise; a second call gives the same bits. The M=256
+configs the benchmark has run (including down's split-K 8 with its reduce) are pinned as well.
+
+Config 5 (decoder layer): one layer at M in {8, 32}; every stage is checked against the fp64
+oracle on the input the stage actually received (norm codes and scales bit-exact, each linear
+within the bounds above, the attention stand-in exact), and the fused pass (epilogues, the
+norm's fp16 output) equals the unfused torch composition bit for bit.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import tokenforge.kernels.ops  # noqa: F401  (registers torch.ops.tokenforge)
+from oracle import reference as oref
+from tests.numerics import cases
+from tests.numerics.tolerance import EPS_FP16, NORMWISE_MAX, Calibration, normwise
+from tokenforge.kernels import autotune
+from tokenforge.kernels.config import GemmConfig
+from tokenforge.kernels.device import gpu_identity
+from tokenforge.kernels.hip.w4a16 import w4a16_dequant, w4a16_gemm
+from tokenforge.kernels.pack import pack_awq
+
+pytestmark = pytest.mark.gpu
+G = 128
+CONFIG4_M = (16, 32, 64, 128, 256, 1024, 4096)
+
+
+def _baseline_weights(n: int, k: int, device: torch.device, seed: int = 0):  # type: ignore[no-untyped-def]
+    qweight, qzeros, scales = cases.baseline_layer(n, k, seed)
+    w = pack_awq(*(torch.from_numpy(a).to(device) for a in (qweight, qzeros, scales)), G)
+    return w
+
+
+def _x_with_outliers(m: int, k: int, device: torch.device, seed: int) -> torch.Tensor:
+    gen = torch.Generator(device="cpu").manual_seed(seed)
+    x = torch.randn((m, k), generator=gen)
+    rows = torch.randperm(m, generator=gen)[: math.ceil(0.01 * m)]
+    x[rows] *= 10
+    return x.to(torch.float16).to(device)
+
+
+def _check(y: torch.Tensor, x: torch.Tensor, wt32: torch.Tensor, w_absmax: float, what: str,
+           bias: torch.Tensor | None = None) -> None:
+    """y fp16 [M, N] against the fp32 product x @ wt32 (+ bias): derived bound plus half an
+    ulp of the rounded output, and the normwise bound."""
+    ref = x.float() @ wt32
+    if bias is not None:
+        ref = ref + bias.float()
+    half_ulp = torch.from_numpy(np.spacing(np.abs(ref.cpu().numpy()).astype(np.float16)).astype(np.float32)).to(y.device) / 2
+    # c sqrt(K) eps16 max|x| max|w| (tests/numerics/tolerance.py), maxima taken on the device
+    tol = Calibration.load("cuda").c * math.sqrt(x.shape[1]) * EPS_FP16 * float(x.float().abs().max()) * w_absmax
+    excess = float(((y.float() - ref).abs() - half_ulp).max())
+    assert excess <= tol, f"{what}: error {excess:.3e} above half an ulp exceeds the derived bound {tol:.3e}"
+    nw = normwise(y.float().cpu().numpy(), ref.cpu().numpy())
+    assert nw <= NORMWISE_MAX, f"{what}: normwise error {nw:.3e}"
+
+
+@pytest.mark.parametrize(("layer", "n", "k"), [("gate_up", 37888, 3584), ("down", 3584, 18944)])
+def test_config4_prefill_through_dispatch_and_a_tuned_cache(layer: str, n: int, k: int, device: torch.device) -> None:
+    w = _baseline_weights(n, k, device)
+    gpu = gpu_identity(device)
+    tuned = autotune.tune_layer(n, k, G, device=device, gpu=gpu, buckets=CONFIG4_M)
+    wt32 = w4a16_dequant(w.qweight_t, w.scales, w.qzeros, G).float().t().contiguous()
+    w_absmax = float(wt32.abs().max())
+    for m in CONFIG4_M:
+        x = _x_with_outliers(m, k, device, seed=m)
+        y = torch.ops.tokenforge.w4a16_linear(x, w.qweight_t, w.scales, w.qzeros, None, G, "hip")
+        cfg = autotune.lookup(gpu, m, n, k, G)
+        assert cfg == tuned[m]
+        _check(y, x, wt32, w_absmax, f"{layer} M={m} {cfg}")
+        again = torch.ops.tokenforge.w4a16_linear(x, w.qweight_t, w.scales, w.qzeros, None, G, "hip")
+        assert torch.equal(y, again), f"{layer} M={m} {cfg}: reruns differ"
+
+
+BENCH_M256 = [
+    ("gate_up", 37888, 3584, GemmConfig("gemm_mfma", 256, 192, 64, 1, 8, 3)),
+    ("down", 3584, 18944, GemmConfig("gemm_mfma", 128, 256, 64, 8, 8, 3)),
+    ("down", 3584, 18944, GemmConfig("gemm_mfma", 256, 128, 64, 8, 8, 3)),
+]
+
+
+@pytest.mark.parametrize(("layer", "n", "k", "cfg"), BENCH_M256, ids=lambda v: str(v))
+def test_config4_the_benchmarked_m256_configs(layer: str, n: int, k: int, cfg: GemmConfig, device: torch.device) -> None:
+    w = _baseline_weights(n, k, device, seed=1)
+    wt32 = w4a16_dequant(w.qweight_t, w.scales, w.qzeros, G).float().t().contiguous()
+    x = _x_with_outliers(256, k, device, seed=256)
+    y = w4a16_gemm(x, w.qweight_t, w.scales, w.qzeros, G, cfg)
+    _check(y, x, wt32, float(wt32.abs().max()), f"{layer} M=256 {cfg}")
+    for _ in range(2):
+        assert torch.equal(w4a16_gemm(x, w.qweight_t, w.scales, w.qzeros, G, cfg), y)
+
+
+# ----------------------------------------------------------------------------- config 5
+
+H, QKV, INTER = 3584, 4608, 18944
+
+
+def _norm(x: torch.Tensor, gamma: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    q8, s, a = torch.ops.tokenforge.rmsnorm_fp8_quant_dequant(x, gamma, 1e-6, None)
+    qo, so = oref.rmsnorm_fp8_reference(x.cpu().numpy(), gamma.cpu().numpy(), 1e-6)
+    assert np.array_equal(q8.cpu().view(torch.uint8).numpy(), qo), "norm codes"
+    assert np.array_equal(s.cpu().numpy(), so), "norm scales"
+    assert torch.equal(a, (q8.to(torch.float32) * s).to(torch.float16)), "norm fp16 output"
+    return q8, s, a
+
+
+@pytest.mark.parametrize("m", [8, 32])
+def test_config5_decoder_layer_stage_by_stage(m: int, device: torch.device) -> None:
+    ops = torch.ops.tokenforge
+    ws = [_baseline_weights(n, k, device, seed=50 + i) for i, (n, k) in
+          enumerate([(QKV, H), (H, H), (2 * INTER, H), (H, INTER)])]
+    wt = [w4a16_dequant(w.qweight_t, w.scales, w.qzeros, G).float().t().contiguous() for w in ws]
+    wmax = [float(t.abs().max()) for t in wt]
+    gen = torch.Generator(device="cpu").manual_seed(m)
+    bias = (0.1 * torch.randn((QKV,), generator=gen)).to(torch.float16).to(device)
+    g1 = (1 + 0.1 * torch.randn((H,), generator=gen)).to(torch.float16).to(device)
+    g2 = (1 + 0.1 * torch.randn((H,), generator=gen)).to(torch.float16).to(device)
+    x = torch.randn((m, H), generator=gen).to(torch.float16).to(device)
+    qkv, o, gu, down = ((w.qweight_t, w.scales, w.qzeros) for w in ws)
+
+    _, _, a = _norm(x, g1)
+    y = ops.w4a16_linear(a, *qkv, bias, G, "hip")
+    _check(y, a, wt[0], wmax[0], f"qkv M={m}", bias)
+    v = y[:, QKV - 512:].reshape(m, 4, 1, 128)
+    attn = v.expand(m, 4, 7, 128).reshape(m, H)  # query head h reads KV group h // 7
+    assert torch.equal(attn.reshape(m, 4, 7, 128)[:, :, 3], y[:, QKV - 512:].reshape(m, 4, 128))
+    yo = ops.w4a16_linear(attn, *o, None, G, "hip")
+    _check(yo, attn, wt[1], wmax[1], f"o_proj M={m}")
+    h1 = ops.w4a16_linear_residual(attn, *o, None, x, G, "hip")
+    assert torch.equal(h1, x + yo)
+    _, _, a2 = _norm(h1, g2)
+    ygu = ops.w4a16_linear(a2, *gu, None, G, "hip")
+    _check(ygu, a2, wt[2], wmax[2], f"gate_up M={m}")
+    act = ops.w4a16_linear_silu_mul(a2, *gu, None, G, "hip")
+    assert torch.equal(act, torch.nn.functional.silu(ygu[:, :INTER]) * ygu[:, INTER:])
+    yd = ops.w4a16_linear(act, *down, None, G, "hip")
+    _check(yd, act, wt[3], wmax[3], f"down M={m}")
+    out = ops.w4a16_linear_residual(act, *down, None, h1, G, "hip")
+    assert torch.equal(out, h1 + yd)
+    assert bool(torch.isfinite(out).all())
