@@ -41,3 +41,35 @@ def w4a16_torch_cpu(
     if bias is not None:
         y = y + bias.to(torch.float32)
     return y.to(x.dtype)
+
+
+_AWQ_ORDER = (0, 2, 4, 6, 1, 3, 5, 7)
+
+
+def pack_int4(values: torch.Tensor) -> torch.Tensor:
+    """pack.py:42-54 (without the range check): word = sum_i v[..., AWQ_ORDER[i]] << 4i in
+    int64, wrapped to the int32 bit pattern."""
+    *lead, n = values.shape
+    v = values.to(torch.int64).reshape(*lead, n // 8, 8)
+    word = torch.zeros(v.shape[:-1], dtype=torch.int64)
+    for nibble, offset in enumerate(_AWQ_ORDER):
+        word |= v[..., offset] << (4 * nibble)
+    return word.to(torch.int32)
+
+
+def repack_awq_to_tf_cpu(qweight: torch.Tensor) -> torch.Tensor:
+    """pack.py:141-143 on CPU tensors: pack_int4(awq_unpack(qweight).t())."""
+    return pack_int4(unpack_int4(qweight).t().contiguous())
+
+
+def rmsnorm_fp8_torch_cpu(x: torch.Tensor, weight: torch.Tensor, eps: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """reference.py:35-56 on CPU tensors (dynamic per-token scale): HF RMSNorm in fp32 rounded
+    to fp16, times the fp16 weight, then per-row scale = max(amax / 448, 1 / (448 * 512)) and
+    the e4m3fn cast of y / scale."""
+    xf = x.to(torch.float32)
+    var = xf.pow(2).mean(-1, keepdim=True)
+    y = (xf * torch.rsqrt(var + eps)).to(torch.float16) * weight
+    amax = y.abs().amax(-1, keepdim=True).to(torch.float32)
+    scale = torch.clamp(amax / 448.0, min=1.0 / (448.0 * 512.0))
+    q = (y.to(torch.float32) / scale).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+    return q, scale

@@ -241,3 +241,43 @@ def test_finalist_selection_median_ignores_one_outlier_and_breaks_ties_by_screen
     assert autotune.select_finalist([(1.0, a)], lambda c: pytest.fail("one candidate: no re-timing")) == a
     with pytest.raises(ValueError):
         autotune.select_finalist([], lambda c: 1.0)
+
+
+def _ship(tmp_path: Path, monkeypatch: pytest.MonkeyPatch, text: str) -> None:
+    ship = tmp_path / "shipped"
+    ship.mkdir(exist_ok=True)
+    (ship / autotune.cache_path(GPU, autotune.hip_abi()).name).write_text(text)
+    monkeypatch.setattr(autotune, "SHIPPED_DIR", ship)
+    autotune.shipped_table.cache_clear()
+
+
+def test_shipped_table_is_the_fallback_between_cache_and_default(tmp_path: Path, monkeypatch: pytest.MonkeyPatch) -> None:
+    doc = {"schema": autotune.SCHEMA_VERSION, "gpu": GPU, "hip": autotune.hip_abi(),
+           "entries": {autotune.entry_key(1, N, K, G): TUNED_1.to_dict(),
+                       autotune.entry_key(256, N, K, G): TUNED_256.to_dict()}}
+    _ship(tmp_path, monkeypatch, json.dumps(doc))
+    cache = _fresh_cache()
+    assert autotune.lookup(GPU, 1, N, K, G) == TUNED_1
+    assert autotune.config_source(GPU, 1, N, K, G) == "shipped"
+    assert autotune.lookup(GPU, 32, N, K, G) == default_config(32, N, K, G)
+    assert autotune.config_source(GPU, 32, N, K, G) == "default"
+    other = GemmConfig("gemv_mfma", 16, 16, 128, 1, 8, 2)
+    cache.put(1, N, K, G, other)  # a config tuned on this machine wins over the shipped one
+    assert autotune.lookup(GPU, 1, N, K, G) == other
+    assert autotune.config_source(GPU, 1, N, K, G) == "cache"
+    autotune.shipped_table.cache_clear()
+
+
+@pytest.mark.parametrize("kind", ["truncated", "wrong_abi", "bad_block_k"])
+def test_a_bad_shipped_table_is_not_used(kind: str, tmp_path: Path, monkeypatch: pytest.MonkeyPatch,
+                                         caplog: pytest.LogCaptureFixture) -> None:
+    cache = _fresh_cache()
+    _populated(cache)
+    text = _corruptions(cache.path)[kind]
+    autotune.reset_caches()
+    cache.path.unlink()
+    _ship(tmp_path, monkeypatch, text)
+    with caplog.at_level(logging.WARNING, logger="tokenforge.kernels.autotune"):
+        assert autotune.lookup(GPU, 1, N, K, G) == default_config(1, N, K, G)
+    assert any("ignored" in r.getMessage() for r in caplog.records)
+    autotune.shipped_table.cache_clear()

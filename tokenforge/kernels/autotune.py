@@ -5,6 +5,9 @@ graphs are captured. The hot path only does a dict lookup and falls back to the 
 :func:`config.default_config` on a miss, so a call never benchmarks, allocates for tuning, or
 synchronizes.
 
+Lookups fall back to a table shipped in ``tokenforge/kernels/tuned/`` (same format, tuned on
+MI355X for the Qwen2.5-7B decoder shapes) and then to the heuristic default.
+
 The cache lives at ``$TOKENFORGE_CACHE_DIR`` (default ``~/.cache/tokenforge``) as
 ``<gpu>-hip<abi>.json``: ``<gpu>`` is ``device.gpu_identity`` (e.g. ``amd-gfx950-256cu``)
 and ``<abi>`` the kernel library's ABI version, so a rebuilt
@@ -228,10 +231,41 @@ def reset_caches() -> None:
         _REGISTRY.clear()
 
 
+SHIPPED_DIR: Final = Path(__file__).resolve().parent / "tuned"
+"""Tuned tables shipped with the package, one file per (GPU, kernel ABI) in the cache format."""
+
+
+@functools.cache
+def shipped_table(gpu: str, abi: str) -> dict[str, GemmConfig]:
+    """The shipped table for this GPU and kernel ABI (empty when there is none). It is read with
+    the cache's own strict decoder: a file that fails any check is not used at all."""
+    path = SHIPPED_DIR / cache_path(gpu, abi).name
+    try:
+        return _decode_document(path.read_text(encoding="utf-8"), gpu, abi)
+    except FileNotFoundError:
+        return {}
+    except (OSError, UnicodeDecodeError, CacheRejectedError) as exc:
+        log.warning("shipped autotune table %s ignored (%s)", path, exc)
+        return {}
+
+
+def config_source(gpu: str, bucket: int, n: int, k: int, group_size: int) -> str:
+    """Where :func:`lookup` takes this entry from: "cache", "shipped" or "default"."""
+    if get_cache(gpu).get(bucket, n, k, group_size) is not None:
+        return "cache"
+    if entry_key(bucket, n, k, group_size) in shipped_table(gpu, hip_abi()):
+        return "shipped"
+    return "default"
+
+
 def lookup(gpu: str, bucket: int, n: int, k: int, group_size: int) -> GemmConfig:
-    """Hot-path lookup: tuned config if cached, otherwise the heuristic default."""
+    """Hot-path lookup: the config tuned on this machine if cached, else the table shipped for
+    this GPU and kernel ABI, else the heuristic default."""
     tuned = get_cache(gpu).get(bucket, n, k, group_size)
-    return default_config(bucket, n, k, group_size) if tuned is None else tuned
+    if tuned is not None:
+        return tuned
+    shipped = shipped_table(gpu, hip_abi()).get(entry_key(bucket, n, k, group_size))
+    return default_config(bucket, n, k, group_size) if shipped is None else shipped
 
 
 BenchFn = Callable[[Callable[[], object]], float]
