@@ -1,13 +1,23 @@
 """Benchmark of the MI355X quantized-linear hot path (one JSON result line on stdout).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-tune] [--no-cpu] [--detail PATH] [--full]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--tune] [--no-cpu] [--detail PATH] [--full]
                     [--stack | --no-stack]
     python bench.py --traffic-probe      (eager launches for rocprofv3 --pmc, see below)
-    python bench.py --mfma-probe         (the tuned M=256 GEMMs, for rocprofv3 --pmc)
+    python bench.py --mfma-probe         (the M=256 GEMMs, for rocprofv3 --pmc)
+    python bench.py --kernel-probe       (eager launches of every timed kernel, for rocprofv3)
     python bench.py --probe              (memory floors of the GEMV's access patterns)
     python bench.py --traffic-summary FETCH_DIR WRITE_DIR PROBE_LOG   (write the profiles/ summaries
     python bench.py --mfma-summary PMC_DIR PROBE_LOG TIMING_LOG        from the profiler's output)
-    python bench.py --stats-summary PROF_DIR BENCH_LOG
+    python bench.py --stats-summary PROF_DIR BENCH_LOG PROF_LOG KPROF_DIR KPROBE_LOG
+    python bench.py --probe-summary PROBE_LOG
+
+Configs: every timed launch uses the config ``autotune.lookup`` returns, i.e. the autotune
+cache, else the table shipped for this GPU in ``tokenforge/kernels/tuned/``, else the heuristic
+default; each JSON entry carries its ``config`` and ``config_source``. ``--tune`` first retunes
+every timed shape and bucket into the cache (as process_weights_after_loading would); that is
+how the shipped table is made. The committed profiles are made with the same configs as the
+bench line, and the summary steps refuse to write when the runs they combine used different
+ones.
 
 Workload (BASELINE.json metric "W4A16 GEMV HBM GB/s at M=1 + GEMM TFLOP/s at M=256"):
 one step is one decode pass at M=1 through the four Qwen2.5-7B decoder linears (qkv
@@ -15,8 +25,8 @@ one step is one decode pass at M=1 through the four Qwen2.5-7B decoder linears (
 AWQ int4 group-128 weights: nibbles and zero-points uniform in [0, 15], fp16 scales uniform
 in [1e-3, 1e-2], x ~ N(0, 1) fp16. Ten layer copies (1.21 GB) rotate so every step reads its
 weights from HBM, not from the 256 MB Infinity Cache. Weights are built in AWQ format and
-converted with the GPU repack, then every shape is autotuned (as process_weights_after_loading
-would) before anything is timed.
+converted with the GPU repack (AWQ -> TokenForge layout -> gfx950 tile layout) before anything
+is timed.
 
 ``value`` = algorithmic bytes of the K timed steps (micro.py:82-86 formula, summed over the
 four linears) / wall time of the K steps, in GB/s. The steps are replayed from a HIP graph
@@ -35,8 +45,10 @@ Extra objects on the same JSON line:
   what those counter passes measure: every candidate in turn on the rotating cold copies, then
   the calibration kernel (torch.neg, 256 MiB in and out); ``--traffic-summary FETCH_DIR
   WRITE_DIR PROBE_LOG`` turns the two counter runs into that summary.
-* ``gemm_m256``: the prefill GEMM at M=256 on gate_up and down, TFLOP/s and fraction of the
-  2.5 PFLOP/s fp16 dense MFMA peak.
+* ``gemm_m256`` and ``gemm_m1024_m4096``: the prefill GEMM at M=256, 1024 and 4096 on gate_up
+  and down, TFLOP/s and fraction of the 2.5 PFLOP/s fp16 dense MFMA peak.
+* ``repack_gate_up``: the load-time AWQ -> TokenForge repack (pack.py:141-143) of gate_up's
+  qweight, int4 values per second (and the bytes read + written per second).
 * ``device_copy_gbps``: the box's achievable bandwidth of a plain device copy (torch, 1 GiB
   read and written), read + write bytes per second, next to the 8 TB/s peak.
 * ``per_shape`` and ``gemv_m2_m4``: the GEMV on each of the four shapes at
@@ -62,7 +74,10 @@ Extra objects on the same JSON line:
   is one HIP graph, tokens/s = M / time per pass. M=1 on every run; ``--stack`` or ``--full``
   add M in {8, 32} (decode) and 2048 (prefill).
 * ``cpu_baseline``: reference.py's CPU path (dequantize per call + fp32 matmul), restated in
-  torch on the host cores, on a bounded sample of the same step.
+  torch on the host cores (``oracle/cpu_path.py``), on a bounded sample of the same step, with
+  the host CPU's model name and the threads used. The same restatements are timed beside the
+  M=256 GEMMs (``gemm_m256[i].cpu``), the RMSNorm + FP8 at T=4096 (``rmsnorm_fp8[..].cpu``) and
+  the repack (``repack_gate_up.cpu``).
 """
 
 from __future__ import annotations
@@ -100,6 +115,10 @@ NUM_XCDS = 8
 CALIB_BYTES = 256 << 20
 COPY_BYTES = 1 << 30
 MFMA_LAUNCHES = 8
+PREFILL_M = (256, 1024, 4096)
+SWEEP_M = (16, 32, 64, 128, 256, 1024, 4096)
+NORM_H = 3584
+NORM_T = (1, 16, 512, 4096)
 
 
 def committed_traffic(cfg_dict: dict) -> float | None:  # type: ignore[type-arg]
@@ -191,141 +210,118 @@ def traffic_summary(fetch_dir: str, write_dir: str, probe_log: str) -> int:
     return 0
 
 
-def stats_summary(prof_dir: str, bench_log: str) -> int:
-    """Write ``STATS_SUMMARY`` from a ``rocprofv3 --kernel-trace --stats`` run of bench.py
-    (``prof_dir``) and the JSON line of the bench run before it (``bench_log``): the kernel
-    table, the event-timed per-shape averages and, per shape and M, the rocprofv3 average of
-    the tuned kernel instance next to the event-timed one."""
+def _bench_line(log_path: str) -> dict | None:  # type: ignore[type-arg]
+    bench = None
+    for line in Path(log_path).read_text().splitlines():
+        if line.startswith("{") and '"metric"' in line:
+            bench = json.loads(line)
+    return bench
+
+
+def _configs_of(bench: dict) -> dict:  # type: ignore[type-arg]
+    """(section, layer, M) -> config of every timed kernel entry of a bench JSON line."""
+    out = {}
+    for sec in ("per_shape", "gemv_m2_m4", "gemm_m256", "gemm_m1024_m4096"):
+        for e in bench.get(sec) or []:
+            out[(sec, e["layer"], e["m"])] = e["config"]
+    return out
+
+
+def stats_summary(prof_dir: str, bench_log: str, prof_log: str, kprof_dir: str, kprobe_log: str) -> int:
+    """Write ``STATS_SUMMARY`` from two ``rocprofv3 --kernel-trace --stats`` runs: one of the
+    bench itself (``prof_dir``, its stdout in ``prof_log``: the kernel table) and one of
+    ``--kernel-probe`` (``kprof_dir``, stdout in ``kprobe_log``: each timed entry's launches in
+    dispatch order), next to the event-timed averages of the plain bench run before them
+    (``bench_log``). Refuses to write when the three runs used different configs for any timed
+    shape, or when a probe entry's dispatches are not all of one kernel."""
     import csv
     import glob
 
-    bench = None
-    for line in Path(bench_log).read_text().splitlines():
-        if line.startswith("{") and '"metric"' in line:
-            bench = json.loads(line)
-    if bench is None:
-        print(f"no bench JSON line in {bench_log}", file=sys.stderr)
+    bench, prof = _bench_line(bench_log), _bench_line(prof_log)
+    kprobe = _probe_line(kprobe_log, "kernel_probe")
+    if bench is None or prof is None or kprobe is None:
+        print(f"no bench JSON line in {bench_log} or {prof_log}, or no kernel_probe line in {kprobe_log}",
+              file=sys.stderr)
+        return 1
+    cb, cp = _configs_of(bench), _configs_of(prof)
+    ck = {(e["layer"], e["m"]): e["config"] for e in kprobe["entries"]}
+    differ = sorted(str(key) for key in set(cb) & set(cp) if cb[key] != cp[key])
+    differ += sorted(str(key) for key in cb if (key[1], key[2]) in ck and ck[(key[1], key[2])] != cb[key])
+    if differ or not set(cb) & set(cp) or not set(ck) >= {(key[1], key[2]) for key in cb}:
+        print(f"the bench, profiled and probe runs used different configs: {differ}", file=sys.stderr)
         return 1
     PRE = "cd /tmp && export TMPDIR=/tmp && R=<repo root>"
-    BENCH_CMD = "python $R/bench.py --steps 100 --warmup 10 > $R/gpurun_out/bench.log   # tunes the cache"
     # ---------------------------------------------------------------- kernel stats
     f = glob.glob(f"{prof_dir}/**/*_kernel_stats.csv", recursive=True)[0]
     rows = list(csv.DictReader(open(f)))
     lines = [
-        "# Kernel statistics: decode step at M=1 + prefill GEMM at M=256 (bench.py)",
+        "# Kernel statistics: decode GEMVs at M = 1, 2, 4 and prefill GEMMs at M = 256, 1024, 4096",
         "",
-        "Command (on the MI355X box, after the bench command below filled the autotune cache):",
+        "Commands (on the MI355X box, fresh autotune cache, so every run takes its configs from",
+        "the table shipped in tokenforge/kernels/tuned/; the summary step checks that they agree):",
         "",
         "```",
         PRE,
-        BENCH_CMD,
+        "python $R/bench.py --steps 100 --warmup 10 > $R/gpurun_out/bench.log",
         "rocprofv3 --kernel-trace --stats --output-format csv -d $R/gpurun_out/prof_bench -- \\",
-        "    python $R/bench.py --steps 20 --warmup 5 --no-cpu --no-tune --no-stack",
-        "python $R/bench.py --stats-summary $R/gpurun_out/prof_bench $R/gpurun_out/bench.log",
+        "    python $R/bench.py --steps 20 --warmup 5 --no-cpu --no-stack > $R/gpurun_out/prof_bench.log",
+        "rocprofv3 --kernel-trace --stats --output-format csv -d $R/gpurun_out/prof_kprobe -- \\",
+        "    python $R/bench.py --kernel-probe > $R/gpurun_out/kprobe.log",
+        "python $R/bench.py --stats-summary $R/gpurun_out/prof_bench $R/gpurun_out/bench.log \\",
+        "    $R/gpurun_out/prof_bench.log $R/gpurun_out/prof_kprobe $R/gpurun_out/kprobe.log",
         "```",
         "",
-        "`*_kernel_stats.csv`, kernels of this library plus the largest setup kernels (torch RNG,",
-        "fills). The GEMV rows are the four decode shapes at M = 1 (graph replays, the per-shape",
-        "timing graphs and the warmup) and the M = 2 and 4 timing graphs; the gemm rows are the",
-        "M=256 prefill timing.",
+        "Kernel table: `*_kernel_stats.csv` of the profiled bench run, the kernels of this library",
+        "plus the largest setup kernels (torch RNG, fills). The GEMV rows are the decode shapes at",
+        "M = 1, 2 and 4 (graph replays, the per-shape timing graphs and the warmup); the gemm rows",
+        "the prefill timing at M = 256, 1024 and 4096.",
         "",
         "| kernel | calls | avg us | min us | max us | % time |",
         "|---|---:|---:|---:|---:|---:|",
     ]
-    for r in rows[:16]:
+    for r in rows[:18]:
         name = r["Name"].replace("(anonymous namespace)::", "")
         name = name.split("(tf::")[0].split("(unsigned")[0].split("(int")[0].split("(float")[0].replace("void ", "")
         if len(name) > 90:
             name = name[:90] + "..."
         lines.append(f"| `{name}` | {r['Calls']} | {float(r['AverageNs'])/1e3:.2f} | {float(r['MinNs'])/1e3:.2f} | "
                      f"{float(r['MaxNs'])/1e3:.2f} | {float(r['Percentage']):.1f} |")
-    ps = {p["layer"]: p for p in bench["per_shape"]}
+    # ---------------------------------------------------------------- per entry
+    tr = glob.glob(f"{kprof_dir}/**/*_kernel_trace.csv", recursive=True)[0]
+    disp = sorted((d for d in csv.DictReader(open(tr))
+                   if ("gemv_kernel" in d["Kernel_Name"] or "gemm" in d["Kernel_Name"])
+                   and "reduce" not in d["Kernel_Name"]),
+                  key=lambda d: int(d["Dispatch_Id"]))
+    n_launch = kprobe["launches"]
+    entries = kprobe["entries"]
+    if len(disp) != n_launch * len(entries):
+        raise ValueError(f"{kprof_dir}: {len(disp)} GEMV/GEMM dispatches, expected {n_launch * len(entries)}")
+    timed = {(e["layer"], e["m"]): e for sec in ("per_shape", "gemv_m2_m4", "gemm_m256", "gemm_m1024_m4096")
+             for e in bench.get(sec) or []}
     lines += [
         "",
-        "Event-timed averages from the bench run before it (HIP events around graph replays on the",
-        "launch stream, `per_shape` and `gemm_m256` of the bench JSON line):",
+        f"Per entry: rocprofv3 average duration of the entry's {n_launch} eager launches in the",
+        "`--kernel-probe` trace (the same kernels on the same rotating cold copies, taken in",
+        "dispatch order; split-K reduce kernels not counted) next to the event-timed average of the",
+        "plain bench run (HIP events around graph replays on the launch stream).",
         "",
-        "| shape | config | event-timed avg us |",
-        "|---|---|---:|",
+        "| shape | config | kernel instance | rocprofv3 avg us | event-timed avg us | ratio |",
+        "|---|---|---|---:|---:|---:|",
     ]
-    for p in bench["per_shape"]:
-        c = p["config"]
-        lines.append(f"| {p['layer']} M=1 | {c['kernel']} bm{c['block_m']} bn{c['block_n']} bk{c['block_k']} "
-                     f"w{c['num_warps']} st{c['num_stages']} | {p['us']:.2f} |")
-    for g in bench["gemm_m256"]:
-        c = g["config"]
-        lines.append(f"| {g['layer']} M=256 | {c['kernel']} bm{c['block_m']} bn{c['block_n']} bk{c['block_k']} "
-                     f"sk{c['split_k']} | {g['us']:.2f} |")
-    # Per-shape averages from the per-dispatch trace: a GEMV launch of shape (N, K) with config
-    # block_n, num_warps has grid (ceil(N / block_n) * 64 * num_warps) threads in x.
-    tr = glob.glob(f"{prof_dir}/**/*_kernel_trace.csv", recursive=True)[0]
-    disp = list(csv.DictReader(open(tr)))
-    shapes = {"qkv_proj": (4608, 3584), "o_proj": (3584, 3584), "gate_up_proj": (37888, 3584), "down_proj": (3584, 18944)}
-    lines += ["", "Per-shape rocprofv3 averages (dispatches of the tuned kernel instance with the shape's grid,",
-              "from `*_kernel_trace.csv`) next to the event-timed averages (`per_shape`, and",
-              "`gemv_m2_m4` for M = 2 and 4). Where one kernel instance and grid serve several rows,",
-              "dispatches of different M are told apart by bench phase (M = 1, 2, 4 run one after the",
-              "other; a phase starts at the first dispatch of an instance only that M uses), and shapes",
-              "of the same M (o_proj and down can coincide) by duration, split at the midpoint of the",
-              "two event-timed averages.", "",
-              "| shape | kernel instance | grid (threads) | dispatches | rocprofv3 avg us | event-timed avg us |",
-              "|---|---|---:|---:|---:|---:|"]
-    def grid_of(c, n):
-        tiles = -(-n // c["block_n"])
-        if c["block_k"] == 256:  # waves over row tiles: one workgroup per num_warps tiles
-            tiles = -(-tiles // c["num_warps"])
-        return tiles * 64 * c["num_warps"]
-    def instance(c):
-        """(name prefix, name suffix) of the template instance a GEMV config runs (K % 128 == 0)."""
-        splitn = "true" if c["block_k"] == 256 else "false"
-        if c["kernel"] == "gemv_dot":
-            return f"gemv_dot_kernel<{c['block_m']}, {c['block_n'] // 16}, {c['num_stages']}, ", f", true, {splitn}>"
-        xlds = "false" if c["block_k"] == 64 else "true"
-        return (f"gemv_mfma_kernel<{c['block_m'] // 16}, {c['block_n'] // 16}, {c['num_stages']}, ",
-                f", {xlds}, true, {splitn}>")
-    groups = {}
-    for p_ in bench["per_shape"] + bench.get("gemv_m2_m4", []):
-        c = p_["config"]
-        n, k = shapes[p_["layer"]]
-        key = (instance(c), grid_of(c, n), 64 * c["num_warps"])
-        groups.setdefault(key, []).append(p_)
-    rows_out = []
-    def dispatches(pre, suf, grid, wg):
-        return sorted(((int(d["Start_Timestamp"]), (int(d["End_Timestamp"]) - int(d["Start_Timestamp"])) / 1e3) for d in disp
-                       if pre in d["Kernel_Name"] and (suf + "(") in d["Kernel_Name"].replace("> (", ">(")
-                       and int(d["Grid_Size_X"]) == grid and int(d["Workgroup_Size_X"]) == wg))
-    # The bench measures M = 1, then 2, then 4: a phase starts at the first dispatch of any kernel
-    # instance that only that M uses.
-    phase_start = {}
-    for ((pre, suf), grid, wg), members in groups.items():
-        ms = {q["m"] for q in members}
-        ds = dispatches(pre, suf, grid, wg)
-        if len(ms) == 1 and ds:
-            m = ms.pop()
-            phase_start[m] = min(phase_start.get(m, ds[0][0]), ds[0][0])
-    for ((pre, suf), grid, wg), members in groups.items():
-        ds = dispatches(pre, suf, grid, wg)
-        ms = sorted({q["m"] for q in members})
-        segments = {m: [] for m in ms}
-        for t, dur in ds:
-            started = [m for m in ms if phase_start.get(m, float("inf")) <= t]
-            segments[max(started) if started else ms[0]].append(dur)
-        for m, seg in segments.items():
-            durs = sorted(seg)
-            mem = sorted((q for q in members if q["m"] == m), key=lambda q: q["us"])
-            # Same M, same instance and grid (o_proj and down can): split at the midpoint of the
-            # two event-timed averages.
-            cuts = [(a["us"] + b["us"]) / 2 for a, b in zip(mem, mem[1:])] + [float("inf")]
-            lo = float("-inf")
-            for p_, hi in zip(mem, cuts):
-                part = [d for d in durs if lo < d <= hi]
-                lo = hi
-                if part:
-                    inst = pre + "…" + suf
-                    rows_out.append((p_["m"], list(shapes).index(p_["layer"]),
-                                     f"| {p_['layer']} M={p_['m']} | `{inst}` | {grid} | {len(part)} | "
-                                     f"{sum(part) / len(part):.2f} | {p_['us']:.2f} |"))
-    lines += [r[2] for r in sorted(rows_out)]
+    for j, e in enumerate(entries):
+        ds = disp[j * n_launch:(j + 1) * n_launch]
+        names = {d["Kernel_Name"] for d in ds}
+        if len(names) != 1:
+            raise ValueError(f"entry {e['layer']} M={e['m']}: dispatches of {len(names)} kernels")
+        inst = names.pop().replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0]
+        avg = statistics.mean((int(d["End_Timestamp"]) - int(d["Start_Timestamp"])) / 1e3 for d in ds)
+        c = e["config"]
+        cfg = (f"{c['kernel']} bm{c['block_m']} bn{c['block_n']} bk{c['block_k']} sk{c['split_k']} "
+               f"w{c['num_warps']} st{c['num_stages']}")
+        ev = timed.get((e["layer"], e["m"]))
+        ev_us = f"{ev['us']:.2f}" if ev else "-"
+        ratio = f"{avg / ev['us']:.2f}" if ev else "-"
+        lines.append(f"| {e['layer']} M={e['m']} | {cfg} | `{inst}` | {avg:.2f} | {ev_us} | {ratio} |")
     STATS_SUMMARY.write_text("\n".join(lines) + "\n")
     print(f"wrote {STATS_SUMMARY}")
     return 0
@@ -366,9 +362,9 @@ def mfma_summary(pmc_dir: str, probe_log: str, timing_log: str) -> int:
         raise ValueError(f"{pmc_dir}: {len(ids)} GEMM dispatches, expected >= {n_launch * len(probe['runs'])}")
     ids = ids[: n_launch * len(probe["runs"])]
     lines = [
-        "# MFMA utilisation of the prefill GEMM at M=256 (gate_up and down, tuned configs)",
+        "# MFMA utilisation of the prefill GEMM at M=256 (gate_up and down, the bench's configs)",
         "",
-        "Commands (on the MI355X box, after `bench.py` filled the autotune cache):",
+        "Commands (on the MI355X box, fresh autotune cache: the configs are the shipped table's):",
         "",
         "```",
         "cd /tmp && export TMPDIR=/tmp && R=<repo root>",
@@ -379,7 +375,7 @@ def mfma_summary(pmc_dir: str, probe_log: str, timing_log: str) -> int:
         "    $R/gpurun_out/mfma_timing.log",
         "```",
         "",
-        f"`--mfma-probe` launches each layer's tuned M=256 GEMM {n_launch} times over rotating cold",
+        f"`--mfma-probe` launches each layer's M=256 GEMM {n_launch} times over rotating cold",
         "weight copies (counters, eager) and times the same launches from a HIP graph (events, taken",
         "from the run without the profiler).",
         f"MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / {NUM_XCDS} XCDs x {NUM_SIMDS} SIMDs): the",
@@ -403,6 +399,77 @@ def mfma_summary(pmc_dir: str, probe_log: str, timing_log: str) -> int:
         lines.append(f"| {run['layer']} | " + " | ".join(f"{statistics.mean(v[c] for v in vals):.0f}" for c in MFMA_COUNTERS) + " |")
     MFMA_SUMMARY.write_text("\n".join(lines) + "\n")
     print(f"wrote {MFMA_SUMMARY}")
+    return 0
+
+
+PROBE_SUMMARY = ROOT / "profiles" / "gemv_m1_memory_floors.md"
+
+
+def probe_summary(probe_log: str) -> int:
+    """Write ``PROBE_SUMMARY`` from the ``{"read_probe": ...}`` line of a ``--probe`` run: per
+    decode shape, the GEMV on the config in use and on the best candidate next to the fastest
+    pure-read kernel of each access pattern (the floor the memory system sets for it), and the
+    fixed cost of one launch inside a graph."""
+    rows = _probe_line(probe_log, "read_probe")
+    if rows is None:
+        print(f"no read_probe line in {probe_log}", file=sys.stderr)
+        return 1
+    lines = [
+        "# Memory floors of the M=1 decode GEMV (pure-read probes next to the GEMV)",
+        "",
+        "Command (on the MI355X box, fresh autotune cache: the GEMV configs are the shipped table's):",
+        "",
+        "```",
+        "cd /tmp && export TMPDIR=/tmp && R=<repo root>",
+        "python $R/bench.py --probe > $R/gpurun_out/probe.log",
+        "python $R/bench.py --probe-summary $R/gpurun_out/probe.log",
+        "```",
+        "",
+        "Every figure is the median over 5 replays of a HIP graph of launches rotating over the",
+        "bench's cold layer copies (HIP events on the replay stream), in us per launch. The probes",
+        "(tokenforge_amd/probes/read_probes.hip, a library of their own) read with the GEMV's grid",
+        "and 128-bit buffer loads and do no arithmetic:",
+        "",
+        "* tile: the gfx950 tile layout, one workgroup per 16-row tile, its waves splitting the",
+        "  tile's 128-wide K steps, each wave step one contiguous 1 KB;",
+        "* tile+meta: as tile, plus the step's scale and zero-point words (the GEMV's three loads);",
+        "* rows: the TokenForge row-major layout, 16 runs of 64 bytes per load instruction;",
+        "* stream: a plain grid-stride read of the weights.",
+        "",
+        "Best over waves in {1, 2, 4, 8, 16} x ring depth in {2, 4, 8} (stream: grid in {512 .. 4096}).",
+        "GB/s are weight bytes (tile+meta: plus scales and zeros) per second; the GEMV's are its",
+        "algorithmic bytes (weights, scales, zeros, x, y) per second.",
+        "",
+    ]
+    empty = [r for r in rows if r["probe"] == "empty"]
+    lines += ["| launch | us |", "|---|---:|"]
+    lines += [f"| empty kernel, grid {r['grid']} | {r['us']:.2f} |" for r in empty]
+    lines += ["", "| shape | GEMV in use | best GEMV candidate | tile | tile+meta | rows | stream | in use / tile+meta |",
+              "|---|---:|---:|---:|---:|---:|---:|---:|"]
+    for name, n, k in SHAPES:
+        mine = [r for r in rows if r.get("layer") == name]
+        gemv = [r for r in mine if r["probe"] == "gemv"]
+        used = next(r for r in gemv if r["tuned"])
+        best = min(gemv, key=lambda r: r["us"])
+        floor = {}
+        for pat in ("tile", "tile+meta", "rows", "stream"):
+            floor[pat] = min((r for r in mine if r["probe"] == pat), key=lambda r: r["us"])
+        cell = lambda r: f"{r['us']:.2f} ({r['gbps']:.0f} GB/s)"  # noqa: E731
+        lines.append(f"| {name} {n}x{k} | {cell(used)} | {cell(best)} | " +
+                     " | ".join(cell(floor[p]) for p in ("tile", "tile+meta", "rows", "stream")) +
+                     f" | {used['us'] / floor['tile+meta']['us']:.2f} |")
+    lines += ["", "Configs (GEMV in use, best candidate) and probe shapes (waves, depth):", ""]
+    for name, n, k in SHAPES:
+        mine = [r for r in rows if r.get("layer") == name]
+        gemv = [r for r in mine if r["probe"] == "gemv"]
+        used = next(r for r in gemv if r["tuned"])
+        best = min(gemv, key=lambda r: r["us"])
+        fl = {p: min((r for r in mine if r["probe"] == p), key=lambda r: r["us"]) for p in ("tile", "tile+meta", "rows", "stream")}
+        lines.append(f"* {name}: in use `{json.dumps(used['config'])}`; best `{json.dumps(best['config'])}`; " +
+                     ", ".join(f"{p} w{fl[p]['waves']} d{fl[p]['depth']}" for p in ("tile", "tile+meta", "rows")) +
+                     f", stream grid {fl['stream']['waves']}")
+    PROBE_SUMMARY.write_text("\n".join(lines) + "\n")
+    print(f"wrote {PROBE_SUMMARY}")
     return 0
 
 
@@ -465,16 +532,17 @@ def time_graph(graph: torch.cuda.CUDAGraph, reps: int = 1) -> float:
     return float(start.elapsed_time(end))
 
 
-def rmsnorm_bench(dev: torch.device) -> list[dict]:  # type: ignore[type-arg]
-    """fused RMSNorm + FP8 at H=3584 over rotating cold inputs, per T."""
+def rmsnorm_bench(dev: torch.device) -> tuple[list[dict], torch.Tensor]:  # type: ignore[type-arg]
+    """fused RMSNorm + FP8 at H=3584 over rotating cold inputs, per T; returns the
+    rows and gamma."""
     from tokenforge.kernels.hip.rmsnorm_fp8 import rmsnorm_fp8_quant
 
-    h = 3584
+    h = NORM_H
     gen = torch.Generator(device="cpu").manual_seed(0)
     outliers = torch.randperm(h, generator=gen)[:8].to(dev)
     gamma = (1 + 0.1 * torch.randn(h, generator=gen)).to(torch.float16).to(dev)
     res = []
-    for t in (1, 16, 512, 4096):
+    for t in NORM_T:
         copies = max(2, min(64, int(-(-COLD_BYTES // (t * h * 2)))))
         xs = []
         for _ in range(copies):
@@ -489,7 +557,7 @@ def rmsnorm_bench(dev: torch.device) -> list[dict]:  # type: ignore[type-arg]
                     "bytes": nbytes})
         log(f"  rmsnorm_fp8   T={t:<5d} {ms * 1e3:8.2f} us {gbps:7.0f} GB/s ({100 * gbps / HBM_PEAK_GBPS:.1f}% of 8 TB/s)")
         del xs, g
-    return res
+    return res, gamma
 
 
 STACK_LAYERS = 28
@@ -597,37 +665,81 @@ def stack_bench(dev: torch.device, gpu: str, ms: tuple[int, ...], tune: bool) ->
     return res
 
 
-def cpu_baseline(layers: list, budget_s: float = 12.0) -> dict:  # type: ignore[type-arg]
-    """reference.py:24-32 restated in torch on the host cores, one decode step (M=1)."""
-    from oracle.cpu_path import w4a16_torch_cpu
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), or the platform's processor string."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
 
-    torch.set_num_threads(os.cpu_count() or 1)
-    cpu = [(t[0].cpu(), t[1].cpu(), t[2].cpu(), n, k) for t, (_, n, k) in zip(layers, SHAPES)]
-    xs = [torch.randn((1, k)).half() for *_, k in cpu]
+    return platform.processor() or "unknown"
+
+
+def _median_s(fn, runs: int, budget_s: float) -> tuple[float, int]:  # type: ignore[no-untyped-def]
+    """Median seconds of ``fn`` over up to ``runs`` runs within about ``budget_s`` (one warmup)."""
+    fn()
+    times: list[float] = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < runs and (not times or time.perf_counter() < t_end):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
+def cpu_baselines(layers_tf: list, gate_awq: torch.Tensor, norm_gamma: torch.Tensor,  # type: ignore[type-arg]
+                  budget_s: float = 12.0) -> dict:  # type: ignore[type-arg]
+    """reference.py's CPU path restated in torch on the host cores (oracle/cpu_path.py), on
+    bounded samples of the benchmarked work: the M=1 decode step (the headline baseline), the
+    M=256 GEMM of gate_up and down, the fused RMSNorm + FP8 at T=4096 and the AWQ -> TokenForge
+    repack of gate_up. ``layers_tf``: the four linears in the TokenForge layout on the host."""
+    from oracle.cpu_path import repack_awq_to_tf_cpu, rmsnorm_fp8_torch_cpu, w4a16_torch_cpu
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    model = cpu_model()
+    gen = torch.Generator().manual_seed(3)
+    xs = [torch.randn((1, k), generator=gen).half() for _, _, k in SHAPES]
 
     def step() -> None:
-        for (qw, s, z, _, _), x in zip(cpu, xs):
-            w4a16_torch_cpu(x, qw, s, z, GROUP)
+        for (qw, sc, qz), x in zip(layers_tf, xs):
+            w4a16_torch_cpu(x, qw, sc, qz, GROUP)
 
-    step()  # warmup
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while len(times) < 20 and (not times or time.perf_counter() < t_end):
-        t0 = time.perf_counter()
-        step()
-        times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
+    med, runs = _median_s(step, 20, budget_s)
     step_bytes = sum(bytes_moved(1, n, k) for _, n, k in SHAPES)
-    return {
+    out = {
         "value": step_bytes / med / 1e9,
         "unit": "GB/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
+        "cpu_model": model,
         "sample": f"one M=1 decode step over the 4 Qwen2.5-7B linears (dequantize per call + fp32 "
-                  f"matmul, reference.py:24-32 in torch), median of {len(times)} runs, "
-                  f"{med * 1e3:.0f} ms/step",
+                  f"matmul, reference.py:24-32 in torch), median of {runs} runs, {med * 1e3:.0f} ms/step",
         "ms_per_step": med * 1e3,
     }
+    gemm = {}
+    for i in (2, 3):
+        name, n, k = SHAPES[i]
+        x = torch.randn((256, k), generator=gen).half()
+        qw, sc, qz = layers_tf[i]
+        med, runs = _median_s(lambda: w4a16_torch_cpu(x, qw, sc, qz, GROUP), 3, budget_s / 2)
+        gemm[name] = {"tflops": 2 * 256 * n * k / med / 1e12, "ms": med * 1e3, "runs": runs}
+    t = NORM_T[-1]
+    x = torch.randn((t, NORM_H), generator=gen)
+    x[:, torch.randperm(NORM_H, generator=gen)[:8]] *= 20
+    x = x.half()
+    med, runs = _median_s(lambda: rmsnorm_fp8_torch_cpu(x, norm_gamma, 1e-6), 10, budget_s / 4)
+    nbytes = t * NORM_H * 2 + NORM_H * 2 + t * NORM_H + 4 * t
+    norm = {"t": t, "gbps": nbytes / med / 1e9, "us": med * 1e6, "runs": runs}
+    med, runs = _median_s(lambda: repack_awq_to_tf_cpu(gate_awq), 3, budget_s / 2)
+    n, k = SHAPES[2][1], SHAPES[2][2]
+    repack = {"gvalues_per_s": n * k / med / 1e9, "gbps": n * k / med / 1e9, "ms": med * 1e3, "runs": runs}
+    common = {"cores": out["cores"], "kind": "port", "cpu_model": model}
+    return {"decode": out, "gemm_m256": {kk: dict(v, **common) for kk, v in gemm.items()},
+            "rmsnorm_t4096": dict(norm, **common), "repack_gate_up": dict(repack, **common)}
 
 
 def read_probes(dev: torch.device, layers: list, copies: int, xs: list, cfgs: list) -> int:  # type: ignore[type-arg]
@@ -703,7 +815,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--no-tune", action="store_true", help="use cached/default configs only")
+    ap.add_argument("--tune", action="store_true",
+                    help="retune every timed shape and bucket into the autotune cache first")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--detail", type=str, default=None, help="write per-shape details as JSON")
     ap.add_argument("--full", action="store_true",
@@ -720,16 +833,21 @@ def main() -> int:
     ap.add_argument("--mfma-summary", nargs=3, metavar=("PMC_DIR", "PROBE_LOG", "TIMING_LOG"),
                     help="write the committed MFMA-utilisation summary from a --mfma-probe counter run "
                          "and a plain --mfma-probe run")
-    ap.add_argument("--stats-summary", nargs=2, metavar=("PROF_DIR", "BENCH_LOG"),
+    ap.add_argument("--stats-summary", nargs=5,
+                    metavar=("PROF_DIR", "BENCH_LOG", "PROF_LOG", "KPROF_DIR", "KPROBE_LOG"),
                     help="write the committed kernel-statistics summary from a rocprofv3 kernel-trace run")
+    ap.add_argument("--probe-summary", metavar="PROBE_LOG",
+                    help="write the committed memory-floor summary from a --probe run's output")
     ap.add_argument("--kernel-probe", action="store_true",
-                    help="eager launches of the M=1 decode GEMVs (cached configs), for rocprofv3 --pmc")
+                    help="eager launches of every kernel the bench line times, in order, for rocprofv3")
     ap.add_argument("--probe", action="store_true",
                     help="memory floors of the GEMV's access patterns (libtokenforge_probes.so), "
                          "next to the GEMV itself on the cached or default configs")
     args = ap.parse_args()
     if args.stats_summary:
         return stats_summary(*args.stats_summary)
+    if args.probe_summary:
+        return probe_summary(args.probe_summary)
     if args.traffic_summary:
         return traffic_summary(*args.traffic_summary)
     if args.mfma_summary:
@@ -764,21 +882,31 @@ def main() -> int:
 
     gate_awq = layers[0][2][3]
     g_rep, _ = capture([lambda: repack_awq_to_tf(gate_awq)] * 8, warm=2)
-    rep_ms = time_graph(g_rep) / 8
+    rep_ms = median_replay_ms(g_rep, 8)
+    del g_rep
+    gate_awq_host = None if args.no_cpu else gate_awq.cpu()
+    del gate_awq
     for c in range(copies):
         layers[c] = [t[:3] for t in layers[c]]
     torch.cuda.synchronize()
     log(f"setup: {copies} layer copies ({copies * step_bytes / 1e9:.2f} GB) in {time.perf_counter() - t0:.1f}s")
 
-    if not (args.no_tune or args.traffic_probe or args.mfma_probe or args.probe or args.kernel_probe):  # probes use the cache
+    if args.tune:
         t0 = time.perf_counter()
         for _, n, k in SHAPES:
-            buckets = (1, 2, 4, 256) if n in (37888,) or k == 18944 else (1, 2, 4)
+            buckets = (1, 2, 4) + (PREFILL_M if n == 37888 or k == 18944 else ())
+            if args.full and (n == 37888 or k == 18944):
+                buckets = tuple(sorted(set(buckets) | set(SWEEP_M)))
             autotune.tune_layer(n, k, GROUP, device=dev, gpu=gpu, buckets=buckets)
         log(f"autotune: {time.perf_counter() - t0:.1f}s")
-    cfg1 = [autotune.lookup(gpu, 1, n, k, GROUP) for _, n, k in SHAPES]
-    for (name, _, _), c in zip(SHAPES, cfg1):
-        log(f"config M=1 {name}: {c}")
+
+    def config(m: int, n: int, k: int) -> tuple:  # type: ignore[type-arg]
+        """(config, where it came from) that the hot path's lookup returns for this call."""
+        return autotune.lookup(gpu, m, n, k, GROUP), autotune.config_source(gpu, m, n, k, GROUP)
+
+    cfg1, src1 = zip(*(config(1, n, k) for _, n, k in SHAPES))
+    for (name, _, _), c, src in zip(SHAPES, cfg1, src1):
+        log(f"config M=1 {name}: {c} ({src})")
 
     gen = torch.Generator(device=dev).manual_seed(7)
     xs = [torch.randn((1, k), generator=gen, device=dev).to(torch.float16) for _, _, k in SHAPES]
@@ -814,20 +942,33 @@ def main() -> int:
         return lambda: w4a16_gemm(x, qw, s, z, GROUP, cfg)
 
     if args.kernel_probe:
-        # Eager launches of the M=1 decode GEMVs on the cached (or default) configs, each layer
-        # `copies` times over the rotating cold copies, for rocprofv3 counter runs.
-        for i, (name, n, k) in enumerate(SHAPES):
+        # Eager launches of every kernel the bench line times (the M = 1, 2, 4 GEMVs on the four
+        # shapes, then the prefill GEMMs), each entry `copies` times over the rotating cold
+        # copies, one entry after the other, for rocprofv3 runs that take dispatches in order.
+        entries = []
+        for m in (1, 2, 4):
+            xm = xs if m == 1 else [torch.randn((m, k), generator=gen, device=dev).to(torch.float16) for _, _, k in SHAPES]
+            for i, (name, n, k) in enumerate(SHAPES):
+                cfg = config(m, n, k)[0]
+                entries.append(({"layer": name, "m": m, "config": cfg.to_dict()}, i, xm, cfg))
+        for m in PREFILL_M:
+            for i in (2, 3):
+                name, n, k = SHAPES[i]
+                xm = [None] * len(SHAPES)
+                xm[i] = torch.randn((m, k), generator=gen, device=dev).to(torch.float16)
+                cfg = config(m, n, k)[0]
+                entries.append(({"layer": name, "m": m, "config": cfg.to_dict()}, i, xm, cfg))
+        for _, i, xm, cfg in entries:
             for c in range(copies):
-                launcher(c, i, xs, cfg1)()
-        torch.cuda.synchronize()
-        print(json.dumps({"kernel_probe": {"launches": copies, "m": 1, "configs": {
-            name: cfg1[i].to_dict() for i, (name, _, _) in enumerate(SHAPES)}}}), flush=True)
+                launcher(c, i, xm, [cfg] * len(SHAPES))()
+            torch.cuda.synchronize()
+        print(json.dumps({"kernel_probe": {"launches": copies, "entries": [e[0] for e in entries]}}), flush=True)
         return 0
 
     if args.mfma_probe:
         # First the eager launches the counters see (each layer's in turn), then the graph
         # timing of the same launches (its dispatches come after and are not counted).
-        cfgs = {i: autotune.lookup(gpu, 256, SHAPES[i][1], SHAPES[i][2], GROUP) for i in (2, 3)}
+        cfgs = {i: config(256, SHAPES[i][1], SHAPES[i][2])[0] for i in (2, 3)}
         xms = {}
         for i in (2, 3):
             xms[i] = [None] * len(SHAPES)
@@ -868,7 +1009,7 @@ def main() -> int:
         ms = median_replay_ms(g, reps)
         gbps = bytes_moved(1, n, k) / (ms * 1e-3) / 1e9
         per_shape.append({"layer": name, "m": 1, "n": n, "k": k, "us": ms * 1e3, "gbps": gbps,
-                          "frac_hbm": gbps / HBM_PEAK_GBPS, "config": cfg1[i].to_dict()})
+                          "frac_hbm": gbps / HBM_PEAK_GBPS, "config": cfg1[i].to_dict(), "config_source": src1[i]})
         log(f"  {name:13s} M=1 {ms * 1e3:8.2f} us {gbps:7.0f} GB/s ({100 * gbps / HBM_PEAK_GBPS:.1f}% of 8 TB/s)")
     dom = per_shape[2]
 
@@ -876,31 +1017,36 @@ def main() -> int:
     gemv_m24 = []
     for m in (2, 4):
         xm_all = [torch.randn((m, k), generator=gen, device=dev).to(torch.float16) for _, _, k in SHAPES]
-        cfgm = [autotune.lookup(gpu, m, n, k, GROUP) for _, n, k in SHAPES]
+        cfgm, srcm = zip(*(config(m, n, k) for _, n, k in SHAPES))
         for i, (name, n, k) in enumerate(SHAPES):
             g, _ = capture([launcher(r % copies, i, xm_all, cfgm) for r in range(reps)])
             ms = median_replay_ms(g, reps)
             gbps = bytes_moved(m, n, k) / (ms * 1e-3) / 1e9
             gemv_m24.append({"layer": name, "m": m, "n": n, "k": k, "us": ms * 1e3, "gbps": gbps,
-                             "frac_hbm": gbps / HBM_PEAK_GBPS, "config": cfgm[i].to_dict()})
+                             "frac_hbm": gbps / HBM_PEAK_GBPS, "config": cfgm[i].to_dict(),
+                             "config_source": srcm[i]})
             log(f"  {name:13s} M={m} {ms * 1e3:8.2f} us {gbps:7.0f} GB/s ({100 * gbps / HBM_PEAK_GBPS:.1f}% of 8 TB/s)")
             del g
 
-    # Prefill GEMM at M=256 on gate_up and down.
+    # Prefill GEMM at M = 256, 1024 and 4096 on gate_up and down.
     gemm = []
-    for i in (2, 3):
-        name, n, k = SHAPES[i]
-        cfg = autotune.lookup(gpu, 256, n, k, GROUP)
-        x256 = [None] * len(SHAPES)
-        x256[i] = torch.randn((256, k), generator=gen, device=dev).to(torch.float16)
-        g, _ = capture([launcher(r % copies, i, x256, [cfg] * len(SHAPES)) for r in range(2 * copies)])
-        ms = median_replay_ms(g, 2 * copies)
-        tflops = 2 * 256 * n * k / (ms * 1e-3) / 1e12
-        gemm.append({"layer": name, "m": 256, "n": n, "k": k, "us": ms * 1e3, "tflops": tflops,
-                     "frac_mfma": tflops / FP16_MFMA_PEAK_TFLOPS, "config": cfg.to_dict()})
-        log(f"  {name:13s} M=256 {ms * 1e3:8.2f} us {tflops:7.1f} TFLOP/s ({100 * tflops / FP16_MFMA_PEAK_TFLOPS:.1f}% of 2.5 PF)")
+    for m in PREFILL_M:
+        for i in (2, 3):
+            name, n, k = SHAPES[i]
+            cfg, src = config(m, n, k)
+            xm = [None] * len(SHAPES)
+            xm[i] = torch.randn((m, k), generator=gen, device=dev).to(torch.float16)
+            launches = 2 * copies if m <= 256 else copies
+            g, _ = capture([launcher(r % copies, i, xm, [cfg] * len(SHAPES)) for r in range(launches)])
+            ms = median_replay_ms(g, launches)
+            del g, xm
+            tflops = 2 * m * n * k / (ms * 1e-3) / 1e12
+            gemm.append({"layer": name, "m": m, "n": n, "k": k, "us": ms * 1e3, "tflops": tflops,
+                         "frac_mfma": tflops / FP16_MFMA_PEAK_TFLOPS, "config": cfg.to_dict(), "config_source": src})
+            log(f"  {name:13s} M={m:<4d} {ms * 1e3:8.2f} us {tflops:7.1f} TFLOP/s "
+                f"({100 * tflops / FP16_MFMA_PEAK_TFLOPS:.1f}% of 2.5 PF)  {cfg} ({src})")
 
-    norm = rmsnorm_bench(dev)
+    norm, norm_gamma = rmsnorm_bench(dev)
 
     # The box's achievable copy bandwidth (torch's device copy, 1 GiB in and out over 4 launches
     # of 256 MiB), the yardstick next to the 8 TB/s HBM peak.
@@ -919,10 +1065,8 @@ def main() -> int:
         sweep = []
         for i in (2, 3):
             name, n, k = SHAPES[i]
-            for m in (16, 32, 64, 128, 256, 1024, 4096):
-                if not args.no_tune:
-                    autotune.tune_layer(n, k, GROUP, device=dev, gpu=gpu, buckets=(m,))
-                cfg = autotune.lookup(gpu, m, n, k, GROUP)
+            for m in SWEEP_M:
+                cfg, src = config(m, n, k)
                 xm = [None] * len(SHAPES)
                 xm[i] = torch.randn((m, k), generator=gen, device=dev).to(torch.float16)
                 g, _ = capture([launcher(r % copies, i, xm, [cfg] * len(SHAPES)) for r in range(copies)])
@@ -931,7 +1075,7 @@ def main() -> int:
                 gbps = bytes_moved(m, n, k) / (ms * 1e-3) / 1e9
                 sweep.append({"layer": name, "m": m, "n": n, "k": k, "us": ms * 1e3, "tflops": tflops,
                               "frac_mfma": tflops / FP16_MFMA_PEAK_TFLOPS, "gbps": gbps,
-                              "frac_hbm": gbps / HBM_PEAK_GBPS, "config": cfg.to_dict()})
+                              "frac_hbm": gbps / HBM_PEAK_GBPS, "config": cfg.to_dict(), "config_source": src})
                 log(f"  {name:13s} M={m:<5d} {ms * 1e3:9.2f} us {tflops:7.1f} TFLOP/s {gbps:7.0f} GB/s  {cfg}")
                 del g, xm
 
@@ -955,15 +1099,32 @@ def main() -> int:
 
     stack = None
     if not args.no_stack:
-        stack = stack_bench(dev, gpu, (1, 8, 32, 2048) if (args.stack or args.full) else (1,), not args.no_tune)
-
-    cpu = None
-    if not args.no_cpu:
-        t0 = time.perf_counter()
-        cpu = cpu_baseline(layers[0])
-        log(f"cpu baseline: {cpu['value']:.2f} GB/s on {cpu['cores']} threads ({time.perf_counter() - t0:.1f}s)")
+        stack = stack_bench(dev, gpu, (1, 8, 32, 2048) if (args.stack or args.full) else (1,), args.tune)
 
     gate_n, gate_k = SHAPES[2][1], SHAPES[2][2]
+    repack = {"gvalues_per_s": gate_n * gate_k / (rep_ms * 1e-3) / 1e9,
+              "gbps": gate_n * gate_k / (rep_ms * 1e-3) / 1e9, "us": rep_ms * 1e3}
+    cpu = None
+    if not args.no_cpu:
+        from tokenforge.kernels.hip.layout import tile_unpack
+
+        t0 = time.perf_counter()
+        layers_tf = [tuple(t.cpu() for t in tile_unpack(*layers[0][i], GROUP)) for i in range(len(SHAPES))]
+        legs = cpu_baselines(layers_tf, gate_awq_host, norm_gamma.cpu())
+        cpu = legs["decode"]
+        for g in gemm:
+            if g["m"] == 256:
+                g["cpu"] = legs["gemm_m256"][g["layer"]]
+        for r in norm:
+            if r["t"] == legs["rmsnorm_t4096"]["t"]:
+                r["cpu"] = legs["rmsnorm_t4096"]
+        repack["cpu"] = legs["repack_gate_up"]
+        log(f"cpu baselines ({cpu['cores']} threads, {cpu['cpu_model']}, {time.perf_counter() - t0:.1f}s): decode "
+            f"{cpu['value']:.2f} GB/s; M=256 gate_up {legs['gemm_m256']['gate_up_proj']['tflops']:.2f} TFLOP/s, "
+            f"down {legs['gemm_m256']['down_proj']['tflops']:.2f}; rmsnorm T=4096 "
+            f"{legs['rmsnorm_t4096']['gbps']:.1f} GB/s; repack {legs['repack_gate_up']['gbps']:.2f} GB/s")
+        del layers_tf
+
     result = {
         "metric": "W4A16 GEMV HBM GB/s at M=1 (% of peak) + GEMM TFLOP/s at M=256, Qwen-7B shapes",
         "value": value,
@@ -996,10 +1157,13 @@ def main() -> int:
             "traffic": committed_traffic(cfg1[2].to_dict()),
             "bytes_per_launch": bytes_moved(1, gate_n, gate_k),
             "avg_launch_us": dom["us"],
+            "config": cfg1[2].to_dict(),
+            "config_source": src1[2],
         },
-        "gemm_m256": gemm,
+        "gemm_m256": [g for g in gemm if g["m"] == 256],
+        "gemm_m1024_m4096": [g for g in gemm if g["m"] != 256],
         "rmsnorm_fp8": norm,
-        "repack_gate_up_gbps": (gate_n * gate_k) / (rep_ms * 1e-3) / 1e9,
+        "repack_gate_up": repack,
         "device_copy_gbps": copy_gbps,
         "per_shape": per_shape,
         "gemv_m2_m4": gemv_m24,

@@ -25,7 +25,7 @@ def _write_run(d: Path, counter: str, gemv_kib: list[float], calib_kib: float) -
     rows = []
     did = 1
     for v in gemv_kib:
-        rows.append({"Dispatch_Id": did, "Kernel_Name": "void tf::gemv_dot_kernel<1, 1, 2, 16, true>(...)",
+        rows.append({"Dispatch_Id": did, "Kernel_Name": "void tf::gemv_kernel<1, 1, 2, 16, true, false, 1>(...)",
                      "Counter_Name": counter, "Counter_Value": v})
         did += 1
     for _ in range(4):
@@ -123,51 +123,88 @@ def test_mfma_summary_from_synthetic_counters(tmp_path: Path, monkeypatch: pytes
     assert "| down_proj | gemm_mfma bm256 bn192 bk64 sk1 w8 st3 | 20.0% |" in text
 
 
-def test_stats_summary_matches_dispatches_to_shapes(tmp_path: Path, monkeypatch: pytest.MonkeyPatch) -> None:
-    """--stats-summary: per shape and M, the rocprofv3 rows are the dispatches of the tuned
-    kernel instance with the shape's grid; different M sharing an instance split by phase."""
-    monkeypatch.setattr(bench, "STATS_SUMMARY", tmp_path / "stats.md")
+def test_stats_summary_slices_the_probe_trace_in_dispatch_order(tmp_path: Path,
+                                                                monkeypatch: pytest.MonkeyPatch) -> None:
+    """--stats-summary: the kernel table comes from the bench trace; entry j of the kernel probe
+    owns dispatches j * launches .. (j + 1) * launches of its GEMV/GEMM kernels (reduce kernels
+    and other kernels skipped), averaged and set beside the bench's event-timed average."""
+    out = tmp_path / "stats.md"
+    monkeypatch.setattr(bench, "STATS_SUMMARY", out)
     d = tmp_path / "prof" / "vm"
     d.mkdir(parents=True)
     with open(d / "1_kernel_stats.csv", "w", newline="") as f:
         w = csv.DictWriter(f, fieldnames=["Name", "Calls", "AverageNs", "MinNs", "MaxNs", "Percentage"])
         w.writeheader()
-        w.writerow({"Name": "void tf::(anonymous namespace)::gemv_dot_kernel<1, 1, 4, 8, true, true>(tf::LinearArgs, int)",
+        w.writerow({"Name": "void tf::(anonymous namespace)::gemv_kernel<1, 1, 2, 16, true, false, 1>(tf::LinearArgs, int)",
                     "Calls": 3, "AverageNs": 20000, "MinNs": 19000, "MaxNs": 21000, "Percentage": 50.0})
-    dot = {"kernel": "gemv_dot", "block_m": 1, "block_n": 16, "block_k": 256, "split_k": 1, "num_warps": 4, "num_stages": 4}
-    mfma = {"kernel": "gemv_mfma", "block_m": 16, "block_n": 16, "block_k": 256, "split_k": 1, "num_warps": 4,
-            "num_stages": 2}
-    grid = -(-(-(-37888 // 16)) // 4) * 64 * 4
-    trace = []
-    t = 0
-    for name, dur, n in (("gemv_dot_kernel<1, 1, 4, 8, true, true>", 20_000, 3),
-                         ("gemv_mfma_kernel<1, 1, 2, 8, true, true, true>", 21_000, 2),   # M = 2
-                         ("gemv_dot_kernel<2, 1, 2, 16, true, false>", 5_000, 1),          # M = 2, only M = 2 uses it
-                         ("gemv_mfma_kernel<1, 2, 2, 16, false, true, false>", 7_000, 1),  # M = 4, only M = 4
-                         ("gemv_mfma_kernel<1, 1, 2, 8, true, true, true>", 23_000, 2)):  # M = 4
-        for _ in range(n):
-            g, wg = (229376, 1024) if "<2, 1, 2, 16" in name else (36864, 256) if "<1, 2, 2" in name else (grid, 256)
-            trace.append({"Kernel_Name": f"void tf::(anonymous namespace)::{name}(tf::LinearArgs, int)",
-                          "Start_Timestamp": t, "End_Timestamp": t + dur, "Grid_Size_X": g,
-                          "Workgroup_Size_X": wg})
-            t += dur + 1000
-    with open(d / "1_kernel_trace.csv", "w", newline="") as f:
+    gemm = {"kernel": "gemm_mfma", "block_m": 128, "block_n": 256, "block_k": 64, "split_k": 8, "num_warps": 8,
+            "num_stages": 3}
+    entries = [{"layer": "gate_up_proj", "m": 1, "config": CFGS[0]},
+               {"layer": "down_proj", "m": 256, "config": gemm}]
+    launches = 2
+    trace, did, t = [], 1, 0
+    for name, dur in (("gemv_kernel<1, 1, 2, 16, true, false, 1>", 20_000), ("gemv_kernel<1, 1, 2, 16, true, false, 1>", 22_000),
+                      ("gemm2_kernel<128, 256, 4, 2, 3>", 60_000), ("splitk_reduce_kernel", 8_000),
+                      ("gemm2_kernel<128, 256, 4, 2, 3>", 64_000), ("splitk_reduce_kernel", 8_000)):
+        trace.append({"Dispatch_Id": did, "Kernel_Name": f"void tf::(anonymous namespace)::{name}(tf::LinearArgs, int)",
+                      "Start_Timestamp": t, "End_Timestamp": t + dur})
+        did, t = did + 1, t + dur + 1000
+    trace.reverse()  # ordered by dispatch id, not by file order
+    k = tmp_path / "kprof" / "vm"
+    k.mkdir(parents=True)
+    with open(k / "2_kernel_trace.csv", "w", newline="") as f:
         w = csv.DictWriter(f, fieldnames=list(trace[0]))
         w.writeheader()
         w.writerows(trace)
-    o2 = {"kernel": "gemv_dot", "block_m": 2, "block_n": 16, "block_k": 128, "split_k": 1, "num_warps": 16,
-          "num_stages": 2}
-    line = {"metric": "m", "per_shape": [{"layer": "gate_up_proj", "m": 1, "us": 20.5, "config": dot}],
-            "gemv_m2_m4": [{"layer": "gate_up_proj", "m": 2, "us": 21.2, "config": mfma},
-                           {"layer": "o_proj", "m": 2, "us": 5.1, "config": o2},
-                           {"layer": "qkv_proj", "m": 4, "us": 7.2,
-                            "config": dict(mfma, block_n=32, block_k=64, num_warps=4)},
-                           {"layer": "gate_up_proj", "m": 4, "us": 22.9, "config": mfma}],
-            "gemm_m256": []}
+    line = {"metric": "m", "per_shape": [{"layer": "gate_up_proj", "m": 1, "us": 20.5, "config": CFGS[0]}],
+            "gemv_m2_m4": [], "gemm_m256": [{"layer": "down_proj", "m": 256, "us": 63.0, "config": gemm}],
+            "gemm_m1024_m4096": []}
     log = tmp_path / "bench.log"
     log.write_text("noise\n" + json.dumps(line) + "\n")
-    assert bench.stats_summary(str(tmp_path / "prof"), str(log)) == 0
-    text = (tmp_path / "stats.md").read_text()
-    assert "| gate_up_proj M=1 | `gemv_dot_kernel<1, 1, 4, …, true, true>` | 151552 | 3 | 20.00 | 20.50 |" in text
-    assert "| gate_up_proj M=2 | `gemv_mfma_kernel<1, 1, 2, …, true, true, true>` | 151552 | 2 | 21.00 | 21.20 |" in text
-    assert "| gate_up_proj M=4 | `gemv_mfma_kernel<1, 1, 2, …, true, true, true>` | 151552 | 2 | 23.00 | 22.90 |" in text
+    kp = tmp_path / "kprobe.log"
+    kp.write_text(json.dumps({"kernel_probe": {"launches": launches, "entries": entries}}) + "\n")
+    args = [str(tmp_path / "prof"), str(log), str(log), str(tmp_path / "kprof"), str(kp)]
+    assert bench.stats_summary(*args) == 0
+    text = out.read_text()
+    assert "| gate_up_proj M=1 | gemv_dot bm1 bn16 bk128 sk1 w4 st2 | `tf::gemv_kernel<1, 1, 2, 16, true, false, 1>` | 21.00 | 20.50 | 1.02 |" in text
+    assert "| down_proj M=256 | gemm_mfma bm128 bn256 bk64 sk8 w8 st3 | `tf::gemm2_kernel<128, 256, 4, 2, 3>` | 62.00 | 63.00 | 0.98 |" in text
+    # A probe run on another config is refused.
+    kp.write_text(json.dumps({"kernel_probe": {"launches": launches, "entries": [dict(entries[0], config=CFGS[1]),
+                                                                                 entries[1]]}}) + "\n")
+    out.unlink()
+    assert bench.stats_summary(*args) == 1
+    assert not out.exists()
+
+
+def _bench_log(path: Path, cfg: dict) -> str:  # type: ignore[type-arg]
+    line = {"metric": "m", "per_shape": [{"layer": "gate_up_proj", "m": 1, "us": 18.0, "config": cfg}],
+            "gemm_m256": [], "gemm_m1024_m4096": []}
+    path.write_text("setup\n" + json.dumps(line) + "\n")
+    return str(path)
+
+
+def test_stats_summary_refuses_runs_on_different_configs(tmp_path: Path, monkeypatch: pytest.MonkeyPatch) -> None:
+    out = tmp_path / "stats.md"
+    monkeypatch.setattr(bench, "STATS_SUMMARY", out)
+    a = _bench_log(tmp_path / "a.log", CFGS[0])
+    b = _bench_log(tmp_path / "b.log", CFGS[1])
+    assert bench.stats_summary(str(tmp_path / "prof"), a, b, str(tmp_path / "kprof"), a) == 1
+    assert not out.exists()
+
+
+def test_probe_summary_table(tmp_path: Path, monkeypatch: pytest.MonkeyPatch) -> None:
+    out = tmp_path / "floors.md"
+    monkeypatch.setattr(bench, "PROBE_SUMMARY", out)
+    rows = [{"probe": "empty", "grid": 256, "us": 1.6}]
+    for name, n, k in bench.SHAPES:
+        rows += [{"probe": "gemv", "layer": name, "config": CFGS[0], "us": 20.0, "gbps": 4000.0, "tuned": True},
+                 {"probe": "gemv", "layer": name, "config": CFGS[1], "us": 19.0, "gbps": 4200.0, "tuned": False}]
+        for pat, us in (("tile", 14.0), ("tile+meta", 15.0), ("rows", 17.0), ("stream", 13.0)):
+            rows += [{"probe": pat, "layer": name, "waves": 4, "depth": 4, "us": us, "gbps": 5000.0},
+                     {"probe": pat, "layer": name, "waves": 8, "depth": 2, "us": us + 1, "gbps": 4000.0}]
+    log = tmp_path / "probe.log"
+    log.write_text(json.dumps({"read_probe": rows}) + "\n")
+    assert bench.probe_summary(str(log)) == 0
+    text = out.read_text()
+    assert "| gate_up_proj 37888x3584 | 20.00 (4000 GB/s) | 19.00 (4200 GB/s) | 14.00 (5000 GB/s) |" in text
+    assert "| 1.33 |" in text  # 20 / 15
