@@ -28,7 +28,7 @@ import torch
 import tokenforge.kernels.ops  # noqa: F401  (registers torch.ops.tokenforge)
 from oracle import reference as oref
 from tests.numerics import cases
-from tests.numerics.tolerance import EPS_FP16, NORMWISE_MAX, Calibration, normwise
+from tests.numerics.tolerance import EPS_FP16, NORMWISE_MAX, contract, relative_max_error
 from tokenforge.kernels import autotune
 from tokenforge.kernels.config import GemmConfig
 from tokenforge.kernels.device import gpu_identity
@@ -63,10 +63,10 @@ def _check(y: torch.Tensor, x: torch.Tensor, wt32: torch.Tensor, w_absmax: float
         ref = ref + bias.float()
     half_ulp = torch.from_numpy(np.spacing(np.abs(ref.cpu().numpy()).astype(np.float16)).astype(np.float32)).to(y.device) / 2
     # c sqrt(K) eps16 max|x| max|w| (tests/numerics/tolerance.py), maxima taken on the device
-    tol = Calibration.load("cuda").c * math.sqrt(x.shape[1]) * EPS_FP16 * float(x.float().abs().max()) * w_absmax
+    tol = contract("cuda").c * math.sqrt(x.shape[1]) * EPS_FP16 * float(x.float().abs().max()) * w_absmax
     excess = float(((y.float() - ref).abs() - half_ulp).max())
     assert excess <= tol, f"{what}: error {excess:.3e} above half an ulp exceeds the derived bound {tol:.3e}"
-    nw = normwise(y.float().cpu().numpy(), ref.cpu().numpy())
+    nw = relative_max_error(y.float().cpu().numpy(), ref.cpu().numpy())
     assert nw <= NORMWISE_MAX, f"{what}: normwise error {nw:.3e}"
 
 

@@ -16,7 +16,7 @@ from safetensors.torch import save_file
 import tokenforge.kernels.ops  # noqa: F401  (registers torch.ops.tokenforge)
 from oracle import pack as opack
 from oracle import reference as oref
-from tests.numerics.tolerance import NORMWISE_MAX, atol, normwise
+from tests.numerics.tolerance import NORMWISE_MAX, contract, relative_max_error
 from tokenforge.kernels import autotune
 from tokenforge.kernels import checkpoint as ck
 
@@ -93,8 +93,8 @@ def test_load_repack_tune_and_run(tmp_path: Path, monkeypatch: pytest.MonkeyPatc
             # fp16 once, which the bound (made for |y| of order 1) does not cover at |y| ~ 10.
             half_ulp = np.spacing(np.abs(r64).astype(np.float16)).astype(np.float64) / 2
             excess = np.abs(y64 - r64) - half_ulp
-            assert float(excess.max()) <= atol(xr, opack.dequantize_tf(ref), "cuda")
-            assert normwise(y64, oref.w4a16_fp32(xr, ref, b_ref)) <= NORMWISE_MAX
+            assert float(excess.max()) <= contract("cuda").atol(xr, opack.dequantize_tf(ref))
+            assert relative_max_error(y64, oref.w4a16_fp32(xr, ref, b_ref)) <= NORMWISE_MAX
     shapes = {(w.n, w.k) for w, _ in loaded.layers.values()}
     assert set(loaded.tuned) == shapes
     cache = list((tmp_path / "cache").glob("*.json"))

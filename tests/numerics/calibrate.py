@@ -1,13 +1,14 @@
-"""Measure the tolerance constant ``c`` on the vendor fp16 GEMM and freeze it.
+"""Measure the constant ``c`` of the derived bound on the vendor fp16 GEMM, and freeze it.
 
     python -m tests.numerics.calibrate --device cpu --write    # ATen fp16 matmul
     TOKENFORGE_SHAPE_SUITE=full python -m tests.numerics.calibrate --device cuda --write
 
-For every (shape, M, seed) the numerics tests use, plus extra seeds, the vendor GEMM's
-error against an fp64 product of the same fp16 operands is divided by
-``tolerance.error_scale``; ``c`` is the largest such ratio rounded up to two significant
-digits (the reference's calibration procedure, tests/numerics/calibrate.py:1-72). On the GPU
-the vendor GEMM is ``F.linear`` in fp16 on ROCm (hipBLASLt / rocBLAS).
+Every (shape, M) of the active shape suite is run on the numerics tests' inputs for each
+calibration seed. Each run's error (vendor fp16 ``F.linear`` against the fp64 product of the
+same fp16 operands) is expressed in units of ``tolerance.roundoff_scale``; ``c`` is the
+largest such ratio rounded up to two significant digits, so the vendor GEMM itself just meets
+the bound (the reference's procedure, tests/numerics/calibrate.py:1-72). On ROCm the vendor
+GEMM is hipBLASLt / rocBLAS.
 """
 
 from __future__ import annotations
@@ -16,68 +17,81 @@ import argparse
 import json
 import math
 import platform
-from collections.abc import Iterator
+from dataclasses import dataclass
 from pathlib import Path
 
 import numpy as np
 import torch
 
 from oracle.pack import dequantize_tf
-from tests.numerics import cases
-from tests.numerics.shapes import linear_shapes, m_values, suite
-from tests.numerics.tolerance import TOLERANCES_PATH, error_scale
+from tests.numerics import cases, shapes
+from tests.numerics.tolerance import TOLERANCES_PATH, roundoff_scale
 
 
-def _vendor_ratios(device: str) -> Iterator[tuple[float, tuple[object, ...]]]:
-    """(error / error_scale, case id) of the vendor fp16 GEMM on every calibration case."""
-    for shape in linear_shapes():
+@dataclass(frozen=True)
+class Sample:
+    layer: str
+    n: int
+    k: int
+    m: int
+    seed: int
+    ratio: float  # vendor error / roundoff_scale
+
+
+def measure(device: str, suite: shapes.ShapeSuite) -> list[Sample]:
+    samples = []
+    for shape in suite.shapes:
         for seed in cases.CALIBRATION_SEEDS:
             w16 = dequantize_tf(cases.layer_weights(shape.n, shape.k, seed))
-            w_on_device = torch.from_numpy(w16).to(device)
-            for m in m_values():
+            w_dev = torch.from_numpy(w16).to(device)
+            w64 = w16.astype(np.float64)
+            for m in suite.m_values:
                 x16 = cases.activations(m, shape.k, seed)
-                exact = x16.numpy().astype(np.float64) @ w16.astype(np.float64).T
-                got = torch.nn.functional.linear(x16.to(device), w_on_device).cpu().numpy()
-                err = float(np.abs(got.astype(np.float64) - exact).max())
-                yield err / error_scale(x16.numpy(), w16), (shape.layer, shape.n, shape.k, m, seed)
+                vendor = torch.nn.functional.linear(x16.to(device), w_dev).cpu().numpy().astype(np.float64)
+                err = float(np.abs(vendor - x16.numpy().astype(np.float64) @ w64.T).max())
+                samples.append(Sample(shape.layer, shape.n, shape.k, m, seed, err / roundoff_scale(x16.numpy(), w16)))
+    return samples
 
 
-def round_up_2sig(v: float) -> float:
-    """Smallest two-significant-digit number >= v (v > 0)."""
-    step = 10.0 ** (math.floor(math.log10(v)) - 1)
-    return round(math.ceil(v / step) * step, 6)
+def two_digits_up(v: float) -> float:
+    """The smallest number with two significant digits that is >= v (v > 0)."""
+    unit = 10.0 ** (math.floor(math.log10(v)) - 1)
+    return round(math.ceil(v / unit) * unit, 6)
 
 
-def calibrate(device: str) -> dict[str, object]:
-    ratios = list(_vendor_ratios(device))
-    worst, worst_case = max(ratios, key=lambda r: r[0])
+def table_entry(device: str, suite: shapes.ShapeSuite, samples: list[Sample]) -> dict[str, object]:
+    worst = max(samples, key=lambda s: s.ratio)
     return {
-        "c": round_up_2sig(worst),
-        "observed_max": worst,
-        "worst_case": list(worst_case),
-        "cases": len(ratios),
-        "suite": suite(),
+        "c": two_digits_up(worst.ratio),
+        "observed_max": worst.ratio,
+        "worst_case": [worst.layer, worst.n, worst.k, worst.m, worst.seed],
+        "cases": len(samples),
+        "suite": suite.name,
         "vendor_gemm": "rocm-F.linear-fp16" if device == "cuda" else "aten-cpu-fp16",
         "device_name": torch.cuda.get_device_name() if device == "cuda" else platform.machine(),
         "torch": torch.__version__,
     }
 
 
+def freeze(device: str, entry: dict[str, object], target: Path) -> None:
+    """Merge ``entry`` into the tolerances table at ``target`` (read from the committed table)."""
+    table = json.loads(TOLERANCES_PATH.read_text()) if TOLERANCES_PATH.exists() else {}
+    table.setdefault("w4a16", {})[device] = entry
+    target.parent.mkdir(parents=True, exist_ok=True)
+    target.write_text(json.dumps(table, indent=2, sort_keys=True) + "\n")
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--device", choices=["cpu", "cuda"], required=True)
     ap.add_argument("--write", action="store_true", help="freeze the result in tolerances.json")
-    ap.add_argument("--out", type=str, default=None, help="write the updated tolerances.json here instead")
+    ap.add_argument("--out", type=Path, default=None, help="write the updated table here instead")
     args = ap.parse_args()
-    entry = calibrate(args.device)
+    suite = shapes.active()
+    entry = table_entry(args.device, suite, measure(args.device, suite))
     print(json.dumps(entry, indent=2), flush=True)
-    if not (args.write or args.out):
-        return
-    table = json.loads(TOLERANCES_PATH.read_text()) if TOLERANCES_PATH.exists() else {}
-    table.setdefault("w4a16", {})[args.device] = entry
-    target = Path(args.out) if args.out else TOLERANCES_PATH
-    target.parent.mkdir(parents=True, exist_ok=True)
-    target.write_text(json.dumps(table, indent=2, sort_keys=True) + "\n")
+    if args.write or args.out:
+        freeze(args.device, entry, args.out or TOLERANCES_PATH)
 
 
 if __name__ == "__main__":

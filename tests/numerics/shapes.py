@@ -1,20 +1,23 @@
-"""Linear shapes of the numerics suite, derived from each model's decoder dimensions.
+"""Which layer shapes and batch sizes the numerics suite runs.
 
-A decoder layer has four quantized linears as an engine sees them at TP=1 (q/k/v fused,
-gate/up fused): qkv ``hidden -> hidden + 2 * kv``, o ``hidden -> hidden``, gate_up
-``hidden -> 2 * intermediate`` and down ``intermediate -> hidden``; ``n`` is the output
-width and ``k`` the reduction length. Two synthetic layers add N that no tile width divides
-(still a multiple of 8, as AWQ packing requires). The reference's suite holds the same shapes
-(tests/numerics/shapes.py:16-35).
+Shapes come from each model's decoder dimensions, as an engine sees its four quantized linears
+at TP=1 (q/k/v fused, gate/up fused): qkv maps ``hidden -> hidden + 2 * kv``, o
+``hidden -> hidden``, gate_up ``hidden -> 2 * intermediate`` and down ``intermediate -> hidden``
+(``n`` = output width, ``k`` = reduction length). Two synthetic layers have an N that no tile
+width divides (still a multiple of 8, as AWQ packing needs). The table equals the reference's
+suite (tests/numerics/shapes.py:16-35).
 
-``TOKENFORGE_SHAPE_SUITE=full`` selects every shape and the long M list; the default quick
-suite keeps the small model, the ragged layers and a few M values.
+Two suites: ``quick`` (the default: the small model, the ragged layers, six M values) and
+``full`` (both models and the long M list), chosen by ``TOKENFORGE_SHAPE_SUITE``.
 """
 
 from __future__ import annotations
 
 import os
+from dataclasses import dataclass
 from typing import NamedTuple
+
+SUITE_ENV = "TOKENFORGE_SHAPE_SUITE"
 
 
 class LinearShape(NamedTuple):
@@ -24,42 +27,47 @@ class LinearShape(NamedTuple):
     k: int
 
 
-# model -> (hidden, fused k+v width / 2, intermediate)
-_DECODERS: dict[str, tuple[int, int, int]] = {
-    "qwen2.5-0.5b": (896, 128, 4864),
-    "qwen2.5-7b": (3584, 512, 18944),
+@dataclass(frozen=True)
+class Decoder:
+    """A decoder's widths: hidden size, the K (= V) projection width, the MLP width."""
+
+    model: str
+    hidden: int
+    kv: int
+    intermediate: int
+
+    def linears(self) -> list[LinearShape]:
+        h, kv, i = self.hidden, self.kv, self.intermediate
+        return [
+            LinearShape(self.model, "qkv_proj", h + 2 * kv, h),
+            LinearShape(self.model, "o_proj", h, h),
+            LinearShape(self.model, "gate_up_proj", 2 * i, h),
+            LinearShape(self.model, "down_proj", h, i),
+        ]
+
+
+QWEN25_05B = Decoder("qwen2.5-0.5b", 896, 128, 4864)
+QWEN25_7B = Decoder("qwen2.5-7b", 3584, 512, 18944)
+RAGGED = (LinearShape("synthetic", "n_ragged_small", 200, 256), LinearShape("synthetic", "n_ragged", 1000, 1024))
+
+
+@dataclass(frozen=True)
+class ShapeSuite:
+    name: str
+    decoders: tuple[Decoder, ...]
+    m_values: tuple[int, ...]
+
+    @property
+    def shapes(self) -> list[LinearShape]:
+        return [s for d in self.decoders for s in d.linears()] + list(RAGGED)
+
+
+SUITES = {
+    "quick": ShapeSuite("quick", (QWEN25_05B,), (1, 3, 8, 16, 31, 129)),
+    "full": ShapeSuite("full", (QWEN25_05B, QWEN25_7B), (1, 2, 3, 4, 7, 8, 15, 16, 31, 32, 33, 64, 127, 128, 129, 256)),
 }
-_RAGGED: tuple[tuple[str, int, int], ...] = (("n_ragged_small", 200, 256), ("n_ragged", 1000, 1024))
 
 
-def decoder_linears(model: str) -> list[LinearShape]:
-    hidden, kv, inter = _DECODERS[model]
-    widths = {
-        "qkv_proj": (hidden + 2 * kv, hidden),
-        "o_proj": (hidden, hidden),
-        "gate_up_proj": (2 * inter, hidden),
-        "down_proj": (hidden, inter),
-    }
-    return [LinearShape(model, layer, n, k) for layer, (n, k) in widths.items()]
-
-
-def ragged_linears() -> list[LinearShape]:
-    return [LinearShape("synthetic", layer, n, k) for layer, n, k in _RAGGED]
-
-
-_M_FULL = (1, 2, 3, 4, 7, 8, 15, 16, 31, 32, 33, 64, 127, 128, 129, 256)
-_M_QUICK = (1, 3, 8, 16, 31, 129)
-
-
-def suite() -> str:
-    """``quick`` unless ``TOKENFORGE_SHAPE_SUITE=full``."""
-    return os.environ.get("TOKENFORGE_SHAPE_SUITE", "quick")
-
-
-def linear_shapes() -> list[LinearShape]:
-    models = list(_DECODERS) if suite() == "full" else ["qwen2.5-0.5b"]
-    return [s for model in models for s in decoder_linears(model)] + ragged_linears()
-
-
-def m_values() -> tuple[int, ...]:
-    return _M_FULL if suite() == "full" else _M_QUICK
+def active() -> ShapeSuite:
+    """The suite ``TOKENFORGE_SHAPE_SUITE`` names ("full"), else the quick one."""
+    return SUITES["full"] if os.environ.get(SUITE_ENV) == "full" else SUITES["quick"]

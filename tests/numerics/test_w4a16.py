@@ -19,8 +19,8 @@ import tokenforge.kernels.ops  # noqa: F401  (registers torch.ops.tokenforge)
 from oracle import pack as opack
 from oracle import reference as oref
 from tests.numerics import cases
-from tests.numerics.shapes import linear_shapes, m_values
-from tests.numerics.tolerance import NORMWISE_MAX, atol, normwise
+from tests.numerics import shapes
+from tests.numerics.tolerance import contract
 from tokenforge.kernels.config import GemmConfig
 from tokenforge.kernels.hip.w4a16 import w4a16_dequant, w4a16_gemm
 from tokenforge.kernels.metrics import KERNEL_CALLS
@@ -42,20 +42,18 @@ def _assert_close(y: torch.Tensor, x: torch.Tensor, w: opack.W4A16Weights, bias=
     ref = oref.w4a16_reference(xn, w, bn)
     y64 = y.detach().cpu().numpy().astype(np.float64)
     w16 = opack.dequantize_tf(w)
-    tol = atol(xn, w16, "cuda")
-    err = float(np.abs(y64 - ref).max()) if y64.size else 0.0
-    assert err <= tol, f"max abs err {err:.3e} > derived tol {tol:.3e}"
     ref32 = xn.astype(np.float32) @ w16.astype(np.float32).T
     if bn is not None:
         ref32 = ref32 + bn.astype(np.float32)
-    nw = normwise(y64, ref32)
-    assert nw <= NORMWISE_MAX, f"normwise error {nw:.3e} > {NORMWISE_MAX}"
+    outcome = contract("cuda").check(y64, ref, ref32, xn, w16)
+    assert outcome.ok, str(outcome)
 
 
-SHAPES = linear_shapes()
+SUITE = shapes.active()
+SHAPES = SUITE.shapes
 
 
-@pytest.mark.parametrize("m", m_values())
+@pytest.mark.parametrize("m", SUITE.m_values)
 @pytest.mark.parametrize("shape", SHAPES, ids=[f"{s.model}/{s.layer}" for s in SHAPES])
 def test_linear_shape_suite(shape, m: int, device: torch.device) -> None:  # type: ignore[no-untyped-def]
     for seed in cases.TEST_SEEDS:

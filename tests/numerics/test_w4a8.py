@@ -21,7 +21,7 @@ import tokenforge.kernels.ops  # noqa: F401  (registers torch.ops.tokenforge)
 from oracle import pack as opack
 from oracle import reference as oref
 from tests.numerics import cases
-from tests.numerics.tolerance import NORMWISE_MAX, atol, normwise
+from tests.numerics.tolerance import NORMWISE_MAX, contract, relative_max_error
 from tokenforge.kernels.config import GemmConfig
 from tokenforge.kernels.hip.rmsnorm_fp8 import rmsnorm_fp8_quant
 from tokenforge.kernels.hip.w4a16 import w4a8_gemm_ex, w4a16_gemm, w4a16_gemm_ex
@@ -91,10 +91,10 @@ def test_rmsnorm_fp8_output_against_oracle(cfg: GemmConfig, device: torch.device
         ref = oref.w4a8_reference(codes, sc, wn, b.numpy())
         x_eff = oref.e4m3_decode(codes).astype(np.float64) * sc[:, None]
         y64 = y.cpu().numpy().astype(np.float64)
-        tol = atol(x_eff, opack.dequantize_tf(wn), "cuda")
+        tol = contract("cuda").atol(x_eff, opack.dequantize_tf(wn))
         half_ulp = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64) / 2
         assert float((np.abs(y64 - ref) - half_ulp).max()) <= tol
-        assert normwise(y64, ref) <= NORMWISE_MAX
+        assert relative_max_error(y64, ref) <= NORMWISE_MAX
 
 
 @pytest.mark.parametrize(

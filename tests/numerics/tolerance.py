@@ -1,22 +1,23 @@
-"""Tolerances of the W4A16 parity tests.
+"""The parity contract of the W4A16 / W4A8 tests: two bounds a kernel's output must meet.
 
-Two bounds, both against references computed from the same fp16 inputs:
+A kernel's fp16 result ``y`` for ``x @ w.T`` (fp16 operands, K = reduction length) is held to
 
-* **Derived absolute bound** (the reference's measurement contract, tests/numerics/
-  tolerance.py:1-46): with fp32 accumulation the rounding error of a length-K dot product
-  grows like sqrt(K) times the unit roundoff times the largest operands, so a kernel's error
-  against the fp64 product is bounded by ``c * sqrt(K) * eps_fp16 * max|x| * max|w|``. The
-  constant ``c`` is measured once per device class on the vendor fp16 GEMM
-  (``python -m tests.numerics.calibrate``) and frozen in ``tolerances.json``: a kernel that
-  needs a looser constant than the vendor GEMM fails.
-* **Normwise bound** (the north-star contract): ``max|y - ref| / max|ref| <= 1e-2`` against
-  an fp32 dequant-then-matmul.
+* the derived absolute bound ``c * sqrt(K) * eps_fp16 * max|x| * max|w|`` against the fp64
+  product of the same operands: fp32 accumulation makes a length-K dot product's rounding
+  error grow like sqrt(K) unit roundoffs of the largest terms, and ``c`` is what the vendor's
+  own fp16 GEMM needs on that device class (measured by ``python -m tests.numerics.calibrate``
+  and frozen in ``tolerances.json``), so a kernel may be no less accurate than the vendor
+  GEMM. This is the reference's measurement contract (tests/numerics/tolerance.py:1-46).
+* the normwise bound ``max|y - ref| / max|ref| <= 1e-2`` against an fp32 dequant-then-matmul,
+  the north-star's accuracy target.
 
-Non-finite entries are left out of both (they are checked for propagation separately).
+Non-finite entries take no part in either bound; their propagation is tested on its own.
+Usage: ``contract("cuda").atol(x, w)``, ``contract("cuda").check(y, ref64, ref32, x, w)``.
 """
 
 from __future__ import annotations
 
+import functools
 import json
 import math
 from dataclasses import dataclass
@@ -25,57 +26,81 @@ from pathlib import Path
 import numpy as np
 
 EPS_FP16 = float(np.finfo(np.float16).eps)  # 2**-10
-TOLERANCES_PATH = Path(__file__).with_name("tolerances.json")
 NORMWISE_MAX = 1e-2
+TOLERANCES_PATH = Path(__file__).with_name("tolerances.json")
 
 
-def _finite_absmax(a: np.ndarray) -> float:
-    v = np.abs(np.asarray(a, dtype=np.float64))
-    v = v[np.isfinite(v)]
-    return float(v.max()) if v.size else 0.0
+def _largest_finite(a: np.ndarray) -> float:
+    mags = np.abs(np.asarray(a, dtype=np.float64)).ravel()
+    mags = mags[np.isfinite(mags)]
+    return float(mags.max()) if mags.size else 0.0
 
 
-def error_scale(x: np.ndarray, w: np.ndarray) -> float:
-    """``sqrt(K) * eps_fp16 * max|x| * max|w|`` (K = x's last dimension)."""
-    return math.sqrt(x.shape[-1]) * EPS_FP16 * _finite_absmax(x) * _finite_absmax(w)
+def roundoff_scale(x: np.ndarray, w: np.ndarray) -> float:
+    """``sqrt(K) * eps_fp16 * max|x| * max|w|`` over finite entries (K = x.shape[-1])."""
+    return EPS_FP16 * math.sqrt(x.shape[-1]) * _largest_finite(x) * _largest_finite(w)
+
+
+def relative_max_error(y: np.ndarray, ref: np.ndarray) -> float:
+    """``max|y - ref| / max|ref|`` over the entries where ``ref`` is finite (the absolute
+    error when ``ref`` is all zero)."""
+    r = np.asarray(ref, dtype=np.float64)
+    finite = np.isfinite(r)
+    if not finite.any():
+        return 0.0
+    err = float(np.max(np.abs(np.asarray(y, dtype=np.float64)[finite] - r[finite])))
+    peak = float(np.max(np.abs(r[finite])))
+    return err / peak if peak > 0 else err
 
 
 @dataclass(frozen=True)
-class Calibration:
-    """One frozen entry of ``tolerances.json``: the constant and where it came from."""
+class Outcome:
+    """Measured errors of one output next to the bounds they are held to."""
 
-    device_type: str
+    abs_err: float
+    atol: float
+    normwise: float
+
+    @property
+    def ok(self) -> bool:
+        return self.abs_err <= self.atol and self.normwise <= NORMWISE_MAX
+
+    def __str__(self) -> str:
+        return f"abs {self.abs_err:.3e} (bound {self.atol:.3e}), normwise {self.normwise:.3e} (bound {NORMWISE_MAX})"
+
+
+@dataclass(frozen=True)
+class Contract:
+    """The bounds of one device class ("cpu" or "cuda"), with its frozen constant ``c``."""
+
+    device: str
     c: float
 
-    @classmethod
-    def load(cls, device_type: str, path: Path = TOLERANCES_PATH) -> Calibration:
-        table = json.loads(path.read_text()).get("w4a16", {})
-        if device_type not in table:
-            raise LookupError(
-                f"no calibrated tolerance for device '{device_type}'; run "
-                f"`python -m tests.numerics.calibrate --device {device_type} --write` once and commit it"
-            )
-        return cls(device_type, float(table[device_type]["c"]))
+    def atol(self, x: np.ndarray, w: np.ndarray) -> float:
+        return self.c * roundoff_scale(x, w)
 
-    def bound(self, x: np.ndarray, w: np.ndarray) -> float:
-        return self.c * error_scale(x, w)
-
-
-def load_constant(device_type: str) -> float:
-    return Calibration.load(device_type).c
+    def check(self, y: np.ndarray, ref64: np.ndarray, ref32: np.ndarray, x: np.ndarray, w: np.ndarray) -> Outcome:
+        """``y`` against the fp64 product ``ref64`` (absolute bound, finite entries) and the
+        fp32 dequant-then-matmul ``ref32`` (normwise bound)."""
+        y64 = np.asarray(y, dtype=np.float64)
+        r64 = np.asarray(ref64, dtype=np.float64)
+        finite = np.isfinite(r64)
+        abs_err = float(np.max(np.abs(y64[finite] - r64[finite]))) if finite.any() else 0.0
+        return Outcome(abs_err, self.atol(x, w), relative_max_error(y64, ref32))
 
 
-def atol(x: np.ndarray, w: np.ndarray, device_type: str) -> float:
-    """Derived absolute bound for ``x @ w.T`` on ``device_type`` ("cuda" or "cpu")."""
-    return Calibration.load(device_type).bound(x, w)
+@functools.cache
+def _frozen_table(path: Path) -> dict:  # type: ignore[type-arg]
+    return json.loads(path.read_text()).get("w4a16", {})
 
 
-def normwise(y: np.ndarray, ref: np.ndarray) -> float:
-    """``max|y - ref| / max|ref|`` over the entries where ``ref`` is finite."""
-    r = np.asarray(ref, dtype=np.float64)
-    keep = np.isfinite(r)
-    if not keep.any():
-        return 0.0
-    diff = float(np.abs(np.asarray(y, dtype=np.float64)[keep] - r[keep]).max())
-    scale = float(np.abs(r[keep]).max())
-    return diff / scale if scale > 0 else diff
+def contract(device: str, path: Path = TOLERANCES_PATH) -> Contract:
+    """The contract frozen in ``tolerances.json`` for ``device``; LookupError if it was never
+    calibrated there."""
+    table = _frozen_table(path)
+    if device not in table:
+        raise LookupError(
+            f"no calibrated tolerance for device '{device}'; run "
+            f"`python -m tests.numerics.calibrate --device {device} --write` once and commit it"
+        )
+    return Contract(device, float(table[device]["c"]))

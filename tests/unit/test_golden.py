@@ -65,7 +65,7 @@ def test_gpu_kernels_match_fixtures(device: torch.device) -> None:
     import tokenforge.kernels.ops  # noqa: F401
     from tokenforge.kernels import pack as tp
     from tokenforge.kernels.hip.rmsnorm_fp8 import e4m3_encode, rmsnorm_fp8_quant
-    from tests.numerics.tolerance import atol
+    from tests.numerics.tolerance import contract
 
     codes = np.array(GOLDEN["e4m3"]["codes"], dtype=np.uint8)
     got = e4m3_encode(torch.from_numpy(_probe()).to(device)).cpu().view(torch.uint8).numpy()
@@ -86,7 +86,7 @@ def test_gpu_kernels_match_fixtures(device: torch.device) -> None:
     assert _sha(back[0]) == g1["sha256_qweight_t"]
     y = torch.ops.tokenforge.w4a16_linear(torch.from_numpy(x).to(device), w.qweight_t, w.scales, w.qzeros,
                                           None, 128, "hip").cpu().numpy().astype(np.float64)
-    tol = atol(x, P.dequantize_tf(P.pack_awq(qweight, qzeros, scales, 128)), "cuda")
+    tol = contract("cuda").atol(x, P.dequantize_tf(P.pack_awq(qweight, qzeros, scales, 128)))
     assert float(np.abs(y[0, :32] - np.array(g1["ref_first32"])).max()) <= tol
     assert abs(float(y.sum()) - g1["ref_sum"]) <= 3584 * tol
 

@@ -6,55 +6,75 @@ import numpy as np
 import pytest
 
 from tests.numerics import shapes
-from tests.numerics.calibrate import round_up_2sig
-from tests.numerics.tolerance import EPS_FP16, Calibration, atol, error_scale, normwise
+from tests.numerics.calibrate import two_digits_up
+from tests.numerics.tolerance import EPS_FP16, contract, relative_max_error, roundoff_scale
 from tokenforge.kernels.metrics import LabeledCounter
 
 
 def test_qwen_shapes_match_the_model_dimensions() -> None:
-    got = {(s.layer, s.n, s.k) for s in shapes.decoder_linears("qwen2.5-7b")}
+    got = {(s.layer, s.n, s.k) for s in shapes.QWEN25_7B.linears()}
     assert got == {
         ("qkv_proj", 4608, 3584), ("o_proj", 3584, 3584),
         ("gate_up_proj", 37888, 3584), ("down_proj", 3584, 18944),
     }
-    small = {(s.layer, s.n, s.k) for s in shapes.decoder_linears("qwen2.5-0.5b")}
+    small = {(s.layer, s.n, s.k) for s in shapes.QWEN25_05B.linears()}
     assert small == {
         ("qkv_proj", 1152, 896), ("o_proj", 896, 896),
         ("gate_up_proj", 9728, 896), ("down_proj", 896, 4864),
     }
-    for s in shapes.ragged_linears():
+    for s in shapes.RAGGED:
         assert s.n % 16 == 8  # a multiple of 8 that no 16-column tile divides
 
 
 def test_suite_selection(monkeypatch: pytest.MonkeyPatch) -> None:
     monkeypatch.delenv("TOKENFORGE_SHAPE_SUITE", raising=False)
-    assert {s.model for s in shapes.linear_shapes()} == {"qwen2.5-0.5b", "synthetic"}
-    assert shapes.m_values() == (1, 3, 8, 16, 31, 129)
+    quick = shapes.active()
+    assert quick.name == "quick"
+    assert {s.model for s in quick.shapes} == {"qwen2.5-0.5b", "synthetic"}
+    assert len(quick.shapes) == 6
+    assert quick.m_values == (1, 3, 8, 16, 31, 129)
     monkeypatch.setenv("TOKENFORGE_SHAPE_SUITE", "full")
-    assert {s.model for s in shapes.linear_shapes()} == {"qwen2.5-0.5b", "qwen2.5-7b", "synthetic"}
-    assert 256 in shapes.m_values()
+    full = shapes.active()
+    assert {s.model for s in full.shapes} == {"qwen2.5-0.5b", "qwen2.5-7b", "synthetic"}
+    assert len(full.shapes) == 10
+    assert 256 in full.m_values
 
 
 def test_error_scale_and_frozen_constants() -> None:
     x = np.array([[1.0, -3.0, 2.0, 0.5]])
     w = np.array([[0.25, -0.5, 0.1, 0.0]])
-    assert error_scale(x, w) == pytest.approx(2.0 * EPS_FP16 * 3.0 * 0.5)
+    assert roundoff_scale(x, w) == pytest.approx(2.0 * EPS_FP16 * 3.0 * 0.5)
     x_inf = np.array([[np.inf, -3.0, 2.0, 0.5]])
-    assert error_scale(x_inf, w) == error_scale(x, w)  # non-finite entries are left out
+    assert roundoff_scale(x_inf, w) == roundoff_scale(x, w)  # non-finite entries are left out
     for dev in ("cpu", "cuda"):
-        assert Calibration.load(dev).c == 0.13
-        assert atol(x, w, dev) == pytest.approx(0.13 * error_scale(x, w))
+        assert contract(dev).c == 0.13
+        assert contract(dev).atol(x, w) == pytest.approx(0.13 * roundoff_scale(x, w))
     with pytest.raises(LookupError, match="calibrate"):
-        Calibration.load("tpu")
+        contract("tpu")
+
+
+def test_contract_check_measures_both_bounds() -> None:
+    x = np.array([[1.0, -3.0, 2.0, 0.5]])
+    w = np.array([[0.25, -0.5, 0.1, 0.0], [1.0, 0.0, 0.0, 0.0]])
+    ref = x @ w.T
+    c = contract("cuda")
+    exact = c.check(ref, ref, ref, x, w)
+    assert exact.ok and exact.abs_err == 0.0 and exact.normwise == 0.0
+    off = ref + np.array([[0.0, 1e-3]])  # above the derived bound (~7.6e-4), within 1e-2 normwise
+    got = c.check(off, ref, ref, x, w)
+    assert not got.ok and got.abs_err == pytest.approx(1e-3) and got.normwise < 1e-2
+    ref_nan = ref.copy()
+    ref_nan[0, 1] = np.nan  # a non-finite reference entry takes no part
+    assert c.check(off, ref_nan, ref_nan, x, w).ok
 
 
 def test_normwise_and_rounding_of_c() -> None:
     ref = np.array([1.0, -4.0, np.nan])
-    assert normwise(np.array([1.02, -4.0, 0.0]), ref) == pytest.approx(0.02 / 4.0)
-    assert round_up_2sig(0.1245726352188545) == 0.13
-    assert round_up_2sig(0.13) == 0.13
-    assert round_up_2sig(0.0071) == 0.0071
-    assert round_up_2sig(2.01) == 2.1
+    assert relative_max_error(np.array([1.02, -4.0, 0.0]), ref) == pytest.approx(0.02 / 4.0)
+    assert two_digits_up(0.1245726352188545) == 0.13
+    assert two_digits_up(0.13) == 0.13
+    assert two_digits_up(0.0071) == 0.0071
+    assert two_digits_up(2.01) == 2.1
 
 
 def test_labeled_counter() -> None:

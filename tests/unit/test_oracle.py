@@ -16,7 +16,7 @@ import torch
 from oracle import pack as P
 from oracle import reference as R
 from tests.numerics import cases
-from tests.numerics.tolerance import atol
+from tests.numerics.tolerance import contract
 
 
 def _midpoint_probe() -> torch.Tensor:
@@ -139,7 +139,7 @@ def test_fp32_cpu_path_within_derived_tolerance() -> None:
         x = cases.activations(3, k, 0).numpy()
         y = R.w4a16_fp32(x, w).astype(np.float64)
         ref = R.w4a16_reference(x, w)
-        assert float(np.abs(y - ref).max()) <= atol(x, P.dequantize_tf(w), "cpu")
+        assert float(np.abs(y - ref).max()) <= contract("cpu").atol(x, P.dequantize_tf(w))
 
 
 @pytest.mark.parametrize("group", [32, 64, 128])
