@@ -55,9 +55,11 @@ Extra objects on the same JSON line:
   M = 1, and at M = 2 and 4 (buckets 2 and 4 autotuned), average launch duration and GB/s.
 * ``rmsnorm_fp8``: the fused RMSNorm + e4m3fn quant (configs[1]: H=3584, eight outlier
   channels x20, gamma = 1 + 0.1 N(0,1), eps 1e-6, dynamic per-token scale) at T in
-  {1, 16, 512, 4096}; algorithmic bytes T*H*2 + H*2 + T*H + 4*T over rotating cold inputs.
+  {1, 16, 512, 4096}; algorithmic bytes T*H*2 + H*2 + T*H + 4*T over rotating cold inputs;
+  ``us`` is the form the hot path picks, ``us_by_form`` each kernel form (row per workgroup,
+  row per wave).
 * with ``--full`` only (written to ``--detail``): ``gemm_sweep``, configs[3]: M in
-  {16, 32, 64, 128, 256, 1024, 4096} on gate_up and down, each bucket autotuned first; and
+  {16, 32, 64, 128, 256, 1024, 4096} on gate_up and down (configs as above); and
   ``vendor_fp16_gemm``, the vendor's dense fp16 GEMM (torch.matmul, hipBLASLt) on the same
   shapes at M in {256, 1024, 4096} with fp16 weights, as a reference point for the MFMA
   fraction this box reaches on these shapes.
@@ -549,14 +551,19 @@ def rmsnorm_bench(dev: torch.device) -> tuple[list[dict], torch.Tensor]:  # type
             x = torch.randn((t, h), device=dev)
             x[:, outliers] *= 20
             xs.append(x.to(torch.float16))
-        g, _ = capture([lambda x=x: rmsnorm_fp8_quant(x, gamma, 1e-6, None) for x in xs])
-        ms = median_replay_ms(g, copies)
         nbytes = t * h * 2 + h * 2 + t * h + 4 * t
-        gbps = nbytes / (ms * 1e-3) / 1e9
-        res.append({"t": t, "h": h, "us": ms * 1e3, "gbps": gbps, "frac_hbm": gbps / HBM_PEAK_GBPS,
-                    "bytes": nbytes})
-        log(f"  rmsnorm_fp8   T={t:<5d} {ms * 1e3:8.2f} us {gbps:7.0f} GB/s ({100 * gbps / HBM_PEAK_GBPS:.1f}% of 8 TB/s)")
-        del xs, g
+        by_form = {}
+        for form in ("auto", "row_per_block", "row_per_wave"):
+            g, _ = capture([lambda x=x, form=form: rmsnorm_fp8_quant(x, gamma, 1e-6, None, form=form) for x in xs])
+            by_form[form] = median_replay_ms(g, copies) * 1e3
+            del g
+        us = by_form["auto"]
+        gbps = nbytes / (us * 1e-6) / 1e9
+        res.append({"t": t, "h": h, "us": us, "gbps": gbps, "frac_hbm": gbps / HBM_PEAK_GBPS,
+                    "bytes": nbytes, "us_by_form": by_form})
+        log(f"  rmsnorm_fp8   T={t:<5d} {us:8.2f} us {gbps:7.0f} GB/s ({100 * gbps / HBM_PEAK_GBPS:.1f}% of 8 TB/s)"
+            f"  [row/block {by_form['row_per_block']:.2f} us, row/wave {by_form['row_per_wave']:.2f} us]")
+        del xs
     return res, gamma
 
 

@@ -230,6 +230,20 @@ int tf_rmsnorm_fp8_quant_dq(const uint16_t* x, int64_t ldx, const uint16_t* weig
                             uint16_t* dq, int64_t lddq, int64_t t, int64_t h, float eps,
                             void* stream);
 
+/* Kernel forms of the norm (same bits either way): */
+#define TF_NORM_AUTO 0           /* the library's choice (currently row per workgroup)               */
+#define TF_NORM_ROW_PER_BLOCK 1  /* up to 4 waves share a row, LDS reductions (any h, any alignment)  */
+#define TF_NORM_ROW_PER_WAVE 2   /* 4 independent rows per workgroup, one per wave, wave reductions;
+                                    needs h % 8 == 0, 16-byte aligned rows (and 8-byte q) and h <= 8192 */
+
+/* tf_rmsnorm_fp8_quant_dq with the kernel form chosen by the caller (for tuning and tests;
+ * the reference has a single Triton kernel, rmsnorm_fp8.py:44-73). TF_EINVAL when the form
+ * does not apply to the arguments. */
+int tf_rmsnorm_fp8_quant_ex(const uint16_t* x, int64_t ldx, const uint16_t* weight, uint8_t* q,
+                            int64_t ldq, float* scale, int32_t static_scale, uint16_t* dq,
+                            int64_t lddq, int64_t t, int64_t h, float eps, int32_t form,
+                            void* stream);
+
 /* Test hook for the e4m3fn encoding used by tf_rmsnorm_fp8_quant
  * (rmsnorm_fp8.py:29-41 _round_to_e4m3_grid + cast): fp32 [count] -> uint8 [count], through
  * the same hardware conversion (v_cvt_pk_fp8_f32) and NaN handling as that kernel.

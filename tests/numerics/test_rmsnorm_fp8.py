@@ -5,7 +5,8 @@ reference.py:35-56 (which forms the fp32 mean from the exact sum, as the kernel 
 against the reference's literal torch order, codes within one e4m3 code on < 0.1% of the
 elements, caused only by last-ulp differences of torch's fp32 ``mean``. The reference's own
 assertions (every row reaches 448, dequantization within 2^-3, saturation, signed zeros,
-MIN_SCALE on a zero row) are kept.
+MIN_SCALE on a zero row) are kept. The kernel's two forms (a row per workgroup, a row per
+wave) are each held to the same bars; "auto" is the form the hot path picks.
 """
 
 from __future__ import annotations
@@ -25,6 +26,12 @@ from tokenforge.kernels.hip.rmsnorm_fp8 import (
 
 pytestmark = pytest.mark.gpu
 EPS = 1e-6
+FORMS = ("auto", "row_per_block", "row_per_wave")
+
+
+def _form_applies(form: str, h: int) -> bool:
+    """The row-per-wave form needs 16-byte rows (h % 8 == 0) and h <= 8192."""
+    return form != "row_per_wave" or (h % 8 == 0 and h <= 8192)
 
 
 def _inputs(t: int, h: int, seed: int, scale: float = 2.0) -> tuple[torch.Tensor, torch.Tensor]:
@@ -70,11 +77,14 @@ def _check_against_torch_order(q: torch.Tensor, s: torch.Tensor, x: torch.Tensor
     assert float(rel.max()) <= 1e-3
 
 
-@pytest.mark.parametrize("h", [896, 3584, 1000])
+@pytest.mark.parametrize("form", FORMS)
+@pytest.mark.parametrize("h", [896, 3584, 1000, 8192])
 @pytest.mark.parametrize("t", [1, 7, 33])
-def test_dynamic_per_token(t: int, h: int, device: torch.device) -> None:
+def test_dynamic_per_token(t: int, h: int, form: str, device: torch.device) -> None:
+    if not _form_applies(form, h):
+        pytest.skip(f"{form} does not apply at h={h}")
     x, w = _inputs(t, h, seed=t * h)
-    q, s = rmsnorm_fp8_quant(x.to(device), w.to(device), EPS)
+    q, s = rmsnorm_fp8_quant(x.to(device), w.to(device), EPS, form=form)
     q_ref, s_ref = oref.rmsnorm_fp8_reference(x.numpy(), w.numpy(), EPS)
     assert q.dtype == torch.float8_e4m3fn
     assert s.shape == (t, 1)
@@ -90,10 +100,11 @@ def test_dynamic_per_token(t: int, h: int, device: torch.device) -> None:
     assert float(rel.max()) <= 2.0**-3
 
 
+@pytest.mark.parametrize("form", FORMS)
 @pytest.mark.parametrize("t", [1, 16, 512, 4096])
-def test_baseline_config2_bit_exact(t: int, device: torch.device) -> None:
+def test_baseline_config2_bit_exact(t: int, form: str, device: torch.device) -> None:
     x, gamma, _ = baseline_inputs(t)
-    q, s = rmsnorm_fp8_quant(x.to(device), gamma.to(device), EPS)
+    q, s = rmsnorm_fp8_quant(x.to(device), gamma.to(device), EPS, form=form)
     q_ref, s_ref = oref.rmsnorm_fp8_reference(x.numpy(), gamma.numpy(), EPS)
     assert np.array_equal(_codes(q), q_ref)
     assert np.array_equal(s.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
@@ -139,7 +150,23 @@ def _assert_codes_match_nan_aware(codes: np.ndarray, ref: np.ndarray) -> None:
     assert np.array_equal(codes[~nan_k], ref[~nan_r])
 
 
-def test_special_values_rows_and_scales(device: torch.device) -> None:
+@pytest.mark.parametrize(("t", "h"), [(2050, 3584), (4099, 896), (4100, 8192), (5000, 3584)])
+def test_row_per_wave_long_and_ragged_batches(t: int, h: int, device: torch.device) -> None:
+    """The row-per-wave form at long batches whose row count leaves the last workgroup with
+    fewer than four rows: every code, scale and fp16 output bit-exact."""
+    x, gamma, _ = baseline_inputs(t, h, seed=t)
+    q, s = rmsnorm_fp8_quant(x.to(device), gamma.to(device), EPS, form="row_per_wave")
+    q_ref, s_ref = oref.rmsnorm_fp8_reference(x.numpy(), gamma.numpy(), EPS)
+    assert np.array_equal(_codes(q), q_ref)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+    qd, sd, a = rmsnorm_fp8_quant_dequant(x.to(device), gamma.to(device), EPS, form="row_per_wave")
+    assert np.array_equal(_codes(qd), q_ref)
+    assert torch.equal(sd, s)
+    _assert_f16_match_nan_aware(a, (qd.to(torch.float32) * sd).to(torch.float16))
+
+
+@pytest.mark.parametrize("form", FORMS[1:])
+def test_special_values_rows_and_scales(form: str, device: torch.device) -> None:
     """Rows with +inf, NaN, an fp16 overflow of y, zeros and -inf (dynamic scale), and static
     scales 0, inf, NaN, negative and tiny: the kernel's exact-rounding slow path."""
     h = 896
@@ -154,7 +181,7 @@ def test_special_values_rows_and_scales(device: torch.device) -> None:
     x[5, 9] = float("-inf")
     with np.errstate(all="ignore"):
         q_ref, s_ref = oref.rmsnorm_fp8_reference(x.numpy(), w.numpy(), EPS)
-    q, s = rmsnorm_fp8_quant(x.to(device), w.to(device), EPS)
+    q, s = rmsnorm_fp8_quant(x.to(device), w.to(device), EPS, form=form)
     _assert_codes_match_nan_aware(_codes(q), q_ref)
     s_k = s.cpu().numpy()
     assert np.array_equal(np.isnan(s_k), np.isnan(s_ref))
@@ -163,12 +190,13 @@ def test_special_values_rows_and_scales(device: torch.device) -> None:
         scale = np.array([sc], dtype=np.float32)
         with np.errstate(all="ignore"):
             q_ref, _ = oref.rmsnorm_fp8_reference(x.numpy(), w.numpy(), EPS, scale)
-        q, _ = rmsnorm_fp8_quant(x.to(device), w.to(device), EPS, torch.from_numpy(scale).to(device))
+        q, _ = rmsnorm_fp8_quant(x.to(device), w.to(device), EPS, torch.from_numpy(scale).to(device), form=form)
         _assert_codes_match_nan_aware(_codes(q), q_ref)
 
 
+@pytest.mark.parametrize("form", FORMS[1:])
 @pytest.mark.parametrize("eps", [0.0, -1.0])
-def test_rows_with_infinite_or_nan_rstd(eps: float, device: torch.device) -> None:
+def test_rows_with_infinite_or_nan_rstd(eps: float, form: str, device: torch.device) -> None:
     """eps = 0 on an all-zero row makes rstd = inf (every y = 0 * inf = NaN); eps = -1 makes it
     NaN on rows whose mean square is below 1. H = 896 leaves the last 8-element chunks of every
     thread past the row, which load zeros: their y must not change the row's absmax (the
@@ -181,7 +209,7 @@ def test_rows_with_infinite_or_nan_rstd(eps: float, device: torch.device) -> Non
     x[3] = (torch.randn((h,), generator=gen) * 3).to(torch.float16)
     with np.errstate(all="ignore"):
         q_ref, s_ref = oref.rmsnorm_fp8_reference(x.numpy(), w.numpy(), eps)
-    q, s = rmsnorm_fp8_quant(x.to(device), w.to(device), eps)
+    q, s = rmsnorm_fp8_quant(x.to(device), w.to(device), eps, form=form)
     _assert_codes_match_nan_aware(_codes(q), q_ref)
     s_k = s.cpu().numpy()
     assert np.array_equal(np.isnan(s_k), np.isnan(s_ref))
@@ -194,12 +222,16 @@ def _assert_f16_match_nan_aware(a: torch.Tensor, b: torch.Tensor) -> None:
     assert torch.equal(a[~an].view(torch.int16), b[~bn].view(torch.int16))
 
 
+@pytest.mark.parametrize("form", FORMS)
 @pytest.mark.parametrize(("t", "h", "aligned"), [(1, 3584, True), (7, 896, True), (33, 3584, True), (5, 1000, False)])
-def test_dequantized_output_equals_the_torch_expression(t: int, h: int, aligned: bool, device: torch.device) -> None:
+def test_dequantized_output_equals_the_torch_expression(t: int, h: int, aligned: bool, form: str,
+                                                        device: torch.device) -> None:
     """rmsnorm_fp8_quant_dequant: the codes and scales are rmsnorm_fp8_quant's, bit for bit, and
     the fp16 output is `(q.to(float32) * scale).to(float16)` bit for bit (dynamic and static
     scales, the large one leaving mostly subnormal and zero codes; the scalar path for an
     unaligned x)."""
+    if form == "row_per_wave" and not (aligned and _form_applies(form, h)):
+        pytest.skip("the row-per-wave form needs aligned 16-byte rows")
     x, w = baseline_inputs(t, h, seed=5)[:2] if h == 3584 else _inputs(t, h, seed=5)
     xd = x.to(device)
     if not aligned:
@@ -208,8 +240,8 @@ def test_dequantized_output_equals_the_torch_expression(t: int, h: int, aligned:
         xd.copy_(x.to(device))
     wd = w.to(device)
     for sc in (None, torch.full((1,), 0.05, device=device), torch.full((1,), 400.0, device=device)):
-        q, s, a = rmsnorm_fp8_quant_dequant(xd, wd, EPS, sc)
-        q0, s0 = rmsnorm_fp8_quant(xd, wd, EPS, sc)
+        q, s, a = rmsnorm_fp8_quant_dequant(xd, wd, EPS, sc, form=form)
+        q0, s0 = rmsnorm_fp8_quant(xd, wd, EPS, sc, form="row_per_block")
         assert np.array_equal(_codes(q), _codes(q0))
         assert torch.equal(s, s0)
         _assert_f16_match_nan_aware(a, (q.to(torch.float32) * s).to(torch.float16))

@@ -110,3 +110,18 @@ def test_noalloc_rejects_a_workspace_above_its_array_on_the_host() -> None:
     assert rc == _lib.TF_EINVAL
     assert b"bytes of workspace" in h.tf_last_error()
     assert h.tf_noalloc_scratch_bytes() == 32 << 20
+
+
+def test_norm_form_is_checked_before_any_launch() -> None:
+    """tf_rmsnorm_fp8_quant_ex rejects an unknown form, and the row-per-wave form where it cannot
+    read the rows (h % 8 != 0, h above 8192, unaligned x), on the host."""
+    h = _lib.lib()
+    args = (_X, 1004, _W, _O, 1004, _S, 0, None, 0, 4)  # h = 1004: not a whole number of 16-byte chunks
+    assert h.tf_rmsnorm_fp8_quant_ex(*args, 1004, 1e-6, 7, None) == _lib.TF_EINVAL
+    assert b"unknown form" in h.tf_last_error()
+    assert h.tf_rmsnorm_fp8_quant_ex(*args, 1004, 1e-6, 2, None) == _lib.TF_EINVAL
+    assert b"row-per-wave" in h.tf_last_error()
+    big = (_X, 8200, _W, _O, 8200, _S, 0, None, 0, 4)
+    assert h.tf_rmsnorm_fp8_quant_ex(*big, 8200, 1e-6, 2, None) == _lib.TF_EINVAL
+    unaligned = (_X + 2, 1024, _W, _O, 1024, _S, 0, None, 0, 4)
+    assert h.tf_rmsnorm_fp8_quant_ex(*unaligned, 1024, 1e-6, 2, None) == _lib.TF_EINVAL

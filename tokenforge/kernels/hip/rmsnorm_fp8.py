@@ -1,8 +1,9 @@
 """Fused RMSNorm + FP8 (e4m3fn) quantization on gfx950 (counterpart of triton/rmsnorm_fp8.py).
 
-One workgroup per token row; the row is read from HBM once. Semantics follow reference.py:35-56
-(HF Qwen2 RMSNorm, then per-token dynamic or static per-tensor e4m3 quantization with an IEEE
-division and round-to-nearest-even onto the e4m3 grid).
+Each row is read from HBM once, by one workgroup ("row_per_block", the default) or by one wave
+("row_per_wave"); ``form`` picks the kernel form explicitly (same bits either way). Semantics follow
+reference.py:35-56 (HF Qwen2 RMSNorm, then per-token dynamic or static per-tensor e4m3
+quantization with an IEEE division and round-to-nearest-even onto the e4m3 grid).
 """
 
 from __future__ import annotations
@@ -14,6 +15,7 @@ from tokenforge.kernels.hip._common import on_device, require_gpu, stream_of
 
 FP8_E4M3_MAX = 448.0
 MIN_SCALE = 1.0 / (FP8_E4M3_MAX * 512.0)
+FORMS = {"auto": 0, "row_per_block": 1, "row_per_wave": 2}  # TF_NORM_* of the C header
 
 
 def rmsnorm_fp8_quant(
@@ -21,13 +23,15 @@ def rmsnorm_fp8_quant(
     weight: torch.Tensor,
     eps: float,
     scale: torch.Tensor | None = None,
+    *,
+    form: str = "auto",
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """``x [T, H]`` -> ``(q [T, H] float8_e4m3fn, scale)`` (rmsnorm_fp8.py:76-117).
 
     ``scale`` is ``[T, 1]`` fp32 for dynamic per-token quantization, or the given ``[1]``
     fp32 tensor for static per-tensor quantization (read, not written).
     """
-    q, s, _ = _launch(x, weight, eps, scale, dequant=False)
+    q, s, _ = _launch(x, weight, eps, scale, dequant=False, form=form)
     return q, s
 
 
@@ -36,18 +40,23 @@ def rmsnorm_fp8_quant_dequant(
     weight: torch.Tensor,
     eps: float,
     scale: torch.Tensor | None = None,
+    *,
+    form: str = "auto",
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """:func:`rmsnorm_fp8_quant` plus ``a [T, H]`` fp16 = ``(q.to(float32) * scale).to(float16)``,
     the fp16 activation a W4A16 linear reads when it is fed from the codes, in the same launch
     (no counterpart in the reference, which would run that expression as separate torch ops)."""
-    q, s, a = _launch(x, weight, eps, scale, dequant=True)
+    q, s, a = _launch(x, weight, eps, scale, dequant=True, form=form)
     assert a is not None
     return q, s, a
 
 
 def _launch(
-    x: torch.Tensor, weight: torch.Tensor, eps: float, scale: torch.Tensor | None, dequant: bool
+    x: torch.Tensor, weight: torch.Tensor, eps: float, scale: torch.Tensor | None, dequant: bool,
+    form: str = "auto",
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor | None]:
+    if form not in FORMS:
+        raise ValueError(f"form must be one of {sorted(FORMS)}, got {form!r}")
     if x.dim() != 2:
         raise ValueError(f"x must be 2-D [T, H], got {tuple(x.shape)}")
     t, h = x.shape
@@ -69,11 +78,12 @@ def _launch(
         return out, scale_out, a
     ldx = x.stride(0) if t > 1 else h
     with on_device(dev):
-        rc = _lib.lib().tf_rmsnorm_fp8_quant_dq(
+        rc = _lib.lib().tf_rmsnorm_fp8_quant_ex(
             x.data_ptr(), ldx, weight.data_ptr(), out.data_ptr(), h, scale_out.data_ptr(),
-            1 if static else 0, 0 if a is None else a.data_ptr(), h, t, h, float(eps), stream_of(dev),
+            1 if static else 0, 0 if a is None else a.data_ptr(), h, t, h, float(eps), FORMS[form],
+            stream_of(dev),
         )
-    _lib.check(rc, "tf_rmsnorm_fp8_quant_dq")
+    _lib.check(rc, "tf_rmsnorm_fp8_quant_ex")
     return out, scale_out, a
 
 

@@ -1,10 +1,17 @@
 // Fused RMSNorm + OCP e4m3fn quantization: one HBM read of x, one write of the codes.
 //
-// One workgroup per token row; x and the weight are loaded together up front and the row
-// stays in registers between the two reductions (sum of squares, then absmax). The sum of
-// squares is accumulated in fp64: every x^2 of an fp16 x is exact, so the fp64 total is the
-// exact sum up to ~2^-53 relative and its rounding to fp32 does not depend on the summation
-// order. The kernel is therefore deterministic and matches a correctly rounded fp32
+// Two forms, same bits. Row per workgroup (the default): up to 4 waves share a row and reduce
+// through LDS with a barrier per reduction. Row per wave: each wave owns one row and reduces it
+// with wave shuffles (no LDS, no barrier); four independent rows per workgroup. Either way x
+// and the weight are loaded up front and a row stays in registers between the two reductions
+// (sum of squares, then absmax). On MI355X the two forms time alike (H = 3584: 14.4 vs 15.5 us
+// at T = 4096, 24.1 vs 24.3 us at T = 8192): the kernel costs the HBM stream plus the encode of
+// the last rows to arrive, not barrier waits. Giving a wave several rows, with the next row
+// requested once the current row's data is in, was slower at every T (fewer waves per SIMD
+// leave the fp64 latency of the encode exposed), so each wave takes one row.
+// The sum of squares is accumulated in fp64: every x^2 of an fp16 x is exact, so the fp64
+// total is the exact sum up to ~2^-53 relative and its rounding to fp32 does not depend on the
+// summation order. The kernel is therefore deterministic and matches a correctly rounded fp32
 // restatement bit for bit; torch's fp32 `mean` (reference.py:37) can differ from it by an ulp
 // of var on some rows.
 //
@@ -45,6 +52,7 @@ template <int WAVES>
 __device__ __forceinline__ double block_sum(double v, double* red) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  if (WAVES == 1) return v;  // the row is one wave's: no LDS, no barrier
   const int wave = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) red[wave] = v;
   __syncthreads();
@@ -64,6 +72,7 @@ __device__ __forceinline__ uint32_t block_max_u32(uint32_t v, uint32_t* red) {
     const uint32_t o = (uint32_t)__shfl_xor((int)v, off, 64);
     v = v > o ? v : o;
   }
+  if (WAVES == 1) return v;
   const int wave = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) red[wave] = v;
   __syncthreads();
@@ -90,53 +99,35 @@ __device__ __forceinline__ u2 dequant_codes4(uint32_t codes, float s) {
   return u2{h0 | (h1 << 16), h2 | (h3 << 16)};
 }
 
-// CPT: 8-element chunks per thread. VEC: 16-byte x / weight loads and 8-byte code stores.
-// DQ: also write dq[T, H] fp16 = fp16(fp32(code) * scale) (16-byte stores when VEC).
-template <int WAVES, int CPT, bool VEC, bool DQ>
-__global__ __launch_bounds__(WAVES * 64) void rmsnorm_fp8_kernel(
-    const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* __restrict__ w,
-    uint8_t* __restrict__ q, int64_t ldq, float* __restrict__ scale, int static_scale,
-    uint16_t* __restrict__ dq, int64_t lddq, int h, float eps) {
-  constexpr int kThreads = WAVES * 64;
-  __shared__ double red_d[WAVES];
-  __shared__ uint32_t red_u[WAVES];
-
-  const int64_t row = blockIdx.x;
-  const uint16_t* xr = x + row * ldx;
-  const int tid = threadIdx.x;
-
-  // All inputs are requested before anything waits on any of them. Values stay packed as
-  // fp16 pairs (pair j of chunk i holds elements 2j, 2j+1).
-  const float s_static = static_scale ? scale[0] : 0.0f;
-  h2 xv[CPT][4];
-  h2 wv[CPT][4];
+// One row's x (or the weight) into registers as fp16 pairs: pair j of chunk i holds elements
+// 2j, 2j+1 of the chunk at (lane + i * threads) * 8. Chunks past h read as zeros. VEC: one
+// 16-byte buffer load per chunk through a resource bounded by the row, so chunks past h come
+// back as zeros without a branch (h % 8 == 0 and 16-byte aligned rows); else element loads.
+template <int CPT, int THREADS, bool VEC>
+__device__ __forceinline__ void load_row(const uint16_t* __restrict__ src, int tid, int h, h2 (&v)[CPT][4]) {
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(src, (uint32_t)h * 2u);
 #pragma unroll
   for (int i = 0; i < CPT; ++i) {
-    const int e0 = (tid + i * kThreads) * 8;
+    const int e0 = (tid + i * THREADS) * 8;
     if (VEC) {
-      u4 rx = u4{0u, 0u, 0u, 0u}, rw = u4{0u, 0u, 0u, 0u};
-      if (e0 < h) {
-        rx = *reinterpret_cast<const u4*>(xr + e0);
-        rw = *reinterpret_cast<const u4*>(w + e0);
-      }
+      const u4 r = load_b128(rs, (uint32_t)e0 * 2u);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        xv[i][j] = as_h2(rx[j]);
-        wv[i][j] = as_h2(rw[j]);
-      }
+      for (int j = 0; j < 4; ++j) v[i][j] = as_h2(r[j]);
     } else {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int e = e0 + 2 * j;
-        const uint32_t x0 = e < h ? xr[e] : 0u, x1 = e + 1 < h ? xr[e + 1] : 0u;
-        const uint32_t w0 = e < h ? w[e] : 0u, w1 = e + 1 < h ? w[e + 1] : 0u;
-        xv[i][j] = as_h2(x0 | (x1 << 16));
-        wv[i][j] = as_h2(w0 | (w1 << 16));
+        const uint32_t a = e < h ? src[e] : 0u, b = e + 1 < h ? src[e + 1] : 0u;
+        v[i][j] = as_h2(a | (b << 16));
       }
     }
   }
+}
 
-  double ss = 0.0;
+// Sum of squares of one row held in registers, over the WAVES waves that share it.
+template <int WAVES, int CPT>
+__device__ __forceinline__ double row_sum_squares(const h2 (&xv)[CPT][4], double* red_d) {
+  double ss[2] = {0.0, 0.0};  // two chains: fp64 adds are long-latency
 #pragma unroll
   for (int i = 0; i < CPT; ++i)
 #pragma unroll
@@ -144,9 +135,20 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_fp8_kernel(
 #pragma unroll
       for (int k = 0; k < 2; ++k) {
         const double d = (double)(float)xv[i][j][k];
-        ss += d * d;
+        ss[k] += d * d;
       }
-  const double total = block_sum<WAVES>(ss, red_d);
+  return block_sum<WAVES>(ss[0] + ss[1], red_d);
+}
+
+// Everything after the sum of squares (``total``) for one row held in registers (xv is
+// overwritten with y): rstd -> y -> absmax -> scale -> codes (and dq). WAVES waves share the
+// row (the absmax meets in red_u behind a barrier; WAVES == 1 reduces in the wave).
+template <int WAVES, int CPT, bool VEC, bool DQ>
+__device__ __forceinline__ void finish_row(h2 (&xv)[CPT][4], const h2 (&wv)[CPT][4], double total, int64_t row,
+                                           int tid, uint8_t* __restrict__ q, int64_t ldq, float* __restrict__ scale,
+                                           int static_scale, float s_static, uint16_t* __restrict__ dq,
+                                           int64_t lddq, int h, float eps, uint32_t* red_u) {
+  constexpr int kThreads = WAVES * 64;
 
   // reference.py:37-38: var = mean(x^2) in fp32, rstd = 1 / sqrt(var + eps), IEEE ops.
   const float var = (float)total / (float)h;
@@ -247,6 +249,45 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_fp8_kernel(
   }
 }
 
+// Row per workgroup: WAVES waves share one row (blockIdx.x). CPT: 8-element chunks per thread.
+// DQ: also write dq[T, H] fp16 = fp16(fp32(code) * scale) (16-byte stores when VEC).
+template <int WAVES, int CPT, bool VEC, bool DQ>
+__global__ __launch_bounds__(WAVES * 64) void rmsnorm_fp8_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* __restrict__ w,
+    uint8_t* __restrict__ q, int64_t ldq, float* __restrict__ scale, int static_scale,
+    uint16_t* __restrict__ dq, int64_t lddq, int h, float eps) {
+  __shared__ double red_d[WAVES];
+  __shared__ uint32_t red_u[WAVES];
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
+  // All inputs are requested before anything waits on any of them.
+  const float s_static = static_scale ? scale[0] : 0.0f;
+  h2 xv[CPT][4], wv[CPT][4];
+  load_row<CPT, WAVES * 64, VEC>(x + row * ldx, tid, h, xv);
+  load_row<CPT, WAVES * 64, VEC>(w, tid, h, wv);
+  const double total = row_sum_squares<WAVES, CPT>(xv, red_d);
+  finish_row<WAVES, CPT, VEC, DQ>(xv, wv, total, row, tid, q, ldq, scale, static_scale, s_static, dq, lddq, h, eps,
+                                  red_u);
+}
+
+// Row per wave: wave g of the grid (4 per workgroup) takes row g. Needs VEC (16-byte rows).
+template <int CPT, bool DQ>
+__global__ __launch_bounds__(256) void rmsnorm_fp8_wave_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* __restrict__ w,
+    uint8_t* __restrict__ q, int64_t ldq, float* __restrict__ scale, int static_scale,
+    uint16_t* __restrict__ dq, int64_t lddq, int64_t t, int h, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= t) return;  // the whole wave: no row for it, and no barrier follows
+  const float s_static = static_scale ? scale[0] : 0.0f;
+  h2 xv[CPT][4], wv[CPT][4];
+  load_row<CPT, 64, true>(x + row * ldx, lane, h, xv);
+  load_row<CPT, 64, true>(w, lane, h, wv);
+  const double total = row_sum_squares<1, CPT>(xv, nullptr);
+  finish_row<1, CPT, true, DQ>(xv, wv, total, row, lane, q, ldq, scale, static_scale, s_static, dq, lddq, h, eps,
+                               nullptr);
+}
+
 struct NormArgs {
   const uint16_t* x;
   int64_t ldx;
@@ -289,6 +330,30 @@ int launch_waves(int cpt, bool vec, const NormArgs& n, hipStream_t stream) {
   }
 }
 
+// Row per wave: one wave per row, four per workgroup; cpt = 16-byte chunks per lane.
+template <int CPT>
+int launch_wave(const NormArgs& n, hipStream_t stream) {
+  const unsigned grid = (unsigned)((n.t + 3) / 4);
+  if (n.dq)
+    rmsnorm_fp8_wave_kernel<CPT, true><<<grid, 256, 0, stream>>>(n.x, n.ldx, n.w, n.q, n.ldq, n.scale,
+                                                                 n.static_scale, n.dq, n.lddq, n.t, n.h, n.eps);
+  else
+    rmsnorm_fp8_wave_kernel<CPT, false><<<grid, 256, 0, stream>>>(n.x, n.ldx, n.w, n.q, n.ldq, n.scale,
+                                                                  n.static_scale, nullptr, 0, n.t, n.h, n.eps);
+  return check_launch("tf_rmsnorm_fp8_quant");
+}
+
+int launch_row_per_wave(int cpt, const NormArgs& n, hipStream_t stream) {
+  switch (cpt) {
+    case 1: return launch_wave<1>(n, stream);
+    case 2: return launch_wave<2>(n, stream);
+    case 4: return launch_wave<4>(n, stream);
+    case 7: return launch_wave<7>(n, stream);
+    case 8: return launch_wave<8>(n, stream);
+    default: return launch_wave<16>(n, stream);
+  }
+}
+
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
 }  // namespace
@@ -296,32 +361,53 @@ bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p
 
 using namespace tf;
 
-extern "C" int tf_rmsnorm_fp8_quant_dq(const uint16_t* x, int64_t ldx, const uint16_t* weight,
-                                       uint8_t* q, int64_t ldq, float* scale, int32_t static_scale,
-                                       uint16_t* dq, int64_t lddq, int64_t t, int64_t h, float eps,
-                                       void* stream) {
+extern "C" int tf_rmsnorm_fp8_quant_ex(const uint16_t* x, int64_t ldx, const uint16_t* weight, uint8_t* q,
+                                       int64_t ldq, float* scale, int32_t static_scale, uint16_t* dq, int64_t lddq,
+                                       int64_t t, int64_t h, float eps, int32_t form, void* stream) {
   if (!x || !weight || !q || !scale) return fail(TF_EINVAL, "tf_rmsnorm_fp8_quant: null pointer");
   if (t < 0 || h <= 0) return fail(TF_EINVAL, "tf_rmsnorm_fp8_quant: need t >= 0 and h > 0");
   if (ldx < h || ldq < h) return fail(TF_EINVAL, "tf_rmsnorm_fp8_quant: row stride smaller than h");
   if (dq && lddq < h) return fail(TF_EINVAL, "tf_rmsnorm_fp8_quant_dq: dq row stride smaller than h");
   if (t > 0x7FFFFFFF) return fail(TF_EINVAL, "tf_rmsnorm_fp8_quant: too many rows");
   if (h > 16 * 8 * 256) return fail(TF_EINVAL, "tf_rmsnorm_fp8_quant: h above 32768 is not supported");
-  if (t == 0) return TF_OK;
+  if (form < TF_NORM_AUTO || form > TF_NORM_ROW_PER_WAVE)
+    return fail(TF_EINVAL, "tf_rmsnorm_fp8_quant_ex: unknown form " + std::to_string(form));
   const int64_t chunks = cdiv(h, 8);
+  const bool vec = (h % 8 == 0) && (ldx % 8 == 0) && (ldq % 8 == 0) && aligned(x, 16) &&
+                   aligned(weight, 16) && aligned(q, 8) && (!dq || (lddq % 8 == 0 && aligned(dq, 16)));
+  // Row per wave needs 16-byte accesses and at most 16 chunks per lane (h <= 8192).
+  const bool wave_ok = vec && chunks <= 16 * 64;
+  if (form == TF_NORM_ROW_PER_WAVE && !wave_ok)
+    return fail(TF_EINVAL, "tf_rmsnorm_fp8_quant_ex: the row-per-wave form needs h % 8 == 0, 16-byte "
+                           "aligned rows and h <= 8192");
+  if (t == 0) return TF_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const NormArgs n{x, ldx, weight, q, ldq, scale, static_scale, dq, lddq, t, (int)h, eps};
+  // Auto is the row per workgroup: it is as fast as the row per wave at long batches and faster
+  // at short ones, where more lanes per row shorten each row's dependent steps.
+  if (form == TF_NORM_ROW_PER_WAVE) {
+    const int64_t per = cdiv(chunks, 64);
+    const int cpt = per <= 1 ? 1 : per <= 2 ? 2 : per <= 4 ? 4 : per == 7 ? 7 : per <= 8 ? 8 : 16;
+    return launch_row_per_wave(cpt, n, s);
+  }
   // Up to 4 waves per row, at most a few chunks per thread: short rows stay latency-bound,
   // and long ones keep the per-wave register footprint low enough for full occupancy.
   const int waves = chunks >= 256 ? 4 : (chunks >= 128 ? 2 : 1);
   const int64_t per = cdiv(chunks, waves * 64);
   const int cpt = per <= 1 ? 1 : per <= 2 ? 2 : per <= 4 ? 4 : per <= 8 ? 8 : 16;
-  const bool vec = (h % 8 == 0) && (ldx % 8 == 0) && (ldq % 8 == 0) && aligned(x, 16) &&
-                   aligned(weight, 16) && aligned(q, 8) && (!dq || (lddq % 8 == 0 && aligned(dq, 16)));
-  hipStream_t s = (hipStream_t)stream;
-  const NormArgs n{x, ldx, weight, q, ldq, scale, static_scale, dq, lddq, t, (int)h, eps};
   switch (waves) {
     case 1: return launch_waves<1>(cpt, vec, n, s);
     case 2: return launch_waves<2>(cpt, vec, n, s);
     default: return launch_waves<4>(cpt, vec, n, s);
   }
+}
+
+extern "C" int tf_rmsnorm_fp8_quant_dq(const uint16_t* x, int64_t ldx, const uint16_t* weight,
+                                       uint8_t* q, int64_t ldq, float* scale, int32_t static_scale,
+                                       uint16_t* dq, int64_t lddq, int64_t t, int64_t h, float eps,
+                                       void* stream) {
+  return tf_rmsnorm_fp8_quant_ex(x, ldx, weight, q, ldq, scale, static_scale, dq, lddq, t, h, eps, TF_NORM_AUTO,
+                                 stream);
 }
 
 extern "C" int tf_rmsnorm_fp8_quant(const uint16_t* x, int64_t ldx, const uint16_t* weight,
