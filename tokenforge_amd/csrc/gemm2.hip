@@ -18,8 +18,9 @@
 // with out-of-range offsets and return zeros), so the count of loads in flight is the same on
 // every path and the waits stay exact.
 //
-// LDS rows hold 8 chunks of 16 bytes; chunk c of row r sits in slot c ^ (r % 8), so the 8
-// lanes of each 16-byte read phase hit 8 distinct bank groups.
+// LDS rows hold 8 chunks of 16 bytes, two rows to a 256-byte bank line; chunk c of row r sits
+// in slot c ^ ((r / 2) % 8), so 16 consecutive rows at one chunk (the 16 lanes of a 16-byte
+// read or write phase on gfx950) hit 16 distinct 16-byte bank groups.
 //
 // Tile order: the grid is one-dimensional; workgroups are numbered XCD by XCD (xcd_tile) and
 // within an XCD the M tiles of one N tile are adjacent, so a weight panel is fetched into one
@@ -45,7 +46,7 @@ constexpr int kRowChunks = 8;     // 16-byte chunks per 64-wide fp16 row
 constexpr uint32_t kChunkBytes = 16;
 
 __device__ __forceinline__ uint32_t swz(int row, int chunk) {
-  return (uint32_t)(row * kRowChunks + (chunk ^ (row & 7))) * kChunkBytes;
+  return (uint32_t)(row * kRowChunks + (chunk ^ ((row >> 1) & 7))) * kChunkBytes;
 }
 
 template <int BM, int BN, int WM, int WN, int S>
@@ -124,7 +125,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm2_kernel(LinearArgs a, float
   for (int i = 0; i < C::kAPerWave; ++i) {
     const int p = (wave + C::kWaves * i) * 64 + lane;
     const int row = p >> 3;
-    const int c = (p & 7) ^ (row & 7);
+    const int c = (p & 7) ^ ((row >> 1) & 7);
     const int m = m0 + row;
     a_off[i] = m < a.m ? (uint32_t)(((int64_t)m * a.ldx + c * 8) * 2) : kOutOfRange;
   }
@@ -265,7 +266,12 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm2_kernel(LinearArgs a, float
 #pragma unroll
     for (int kk = 0; kk < kBK / 16; ++kk) {
       if (kk + 1 < kBK / 16) read_frags(A, B, kk + 1, af[(kk + 1) & 1], bf[(kk + 1) & 1]);
+      // Raised priority while this wave queues its MFMAs: the SIMD's other wave then runs its
+      // LDS reads and dequantization in the shadow of these MFMAs instead of competing for
+      // issue slots with them (measured 6-8% on the M = 256 gate_up shape).
+      __builtin_amdgcn_s_setprio(1);
       mfmas(af[kk & 1], bf[kk & 1]);
+      __builtin_amdgcn_s_setprio(0);
       store_b_word(odd ^ 1, odd ^ 1, kk, qp);  // block kb + 1
     }
     issue_b(kb + 3, odd ^ 1);
