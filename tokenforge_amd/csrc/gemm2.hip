@@ -69,6 +69,9 @@ struct G2 {
   // VMEM issued after x block kb (S - 1 iterations back) when iteration kb waits for it:
   // weights kb + 4 - S, then S - 2 whole iterations (x block, weights).
   static constexpr int kAfterA = 3 * kBPer + (S - 2) * (kAPerWave + 3 * kBPer);
+  // 16-wide K steps whose operand fragments are in flight ahead of the MFMAs: two where the
+  // registers allow it without lowering occupancy (LDS latency is the exposed cost), else one.
+  static constexpr int kAhead = (kWaves == 8 && TM * TN <= 6) || (kWaves == 4 && TM * TN <= 8) ? 2 : 1;
 };
 
 // Block barrier at the top of an iteration: at most N vector-memory loads of this wave still
@@ -257,20 +260,23 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm2_kernel(LinearArgs a, float
     __builtin_amdgcn_sched_barrier(0);
     const uint8_t* A = a_lds + st * C::kAStage;
     const uint8_t* B = b_lds + odd * C::kBStage;
-    // Fragments of step kk + 1 are read while the MFMAs of step kk run; one word of each
-    // chunk of block kb + 1 is dequantized into the other buffer per step.
-    h8 af[2][TM], bf[2][TN];
-    read_frags(A, B, 0, af[0], bf[0]);
+    // Fragments of step kk + D are read while the MFMAs of step kk run (D = kAhead steps in
+    // flight); one word of each chunk of block kb + 1 is dequantized into the other buffer per
+    // step.
+    constexpr int D = C::kAhead;
+    h8 af[kBK / 16][TM], bf[kBK / 16][TN];
+#pragma unroll
+    for (int kk = 0; kk < D; ++kk) read_frags(A, B, kk, af[kk], bf[kk]);
     QuantParams qp[BP];
     slot_params(odd ^ 1, qp);
 #pragma unroll
     for (int kk = 0; kk < kBK / 16; ++kk) {
-      if (kk + 1 < kBK / 16) read_frags(A, B, kk + 1, af[(kk + 1) & 1], bf[(kk + 1) & 1]);
+      if (kk + D < kBK / 16) read_frags(A, B, kk + D, af[kk + D], bf[kk + D]);
       // Raised priority while this wave queues its MFMAs: the SIMD's other wave then runs its
       // LDS reads and dequantization in the shadow of these MFMAs instead of competing for
       // issue slots with them (measured 6-8% on the M = 256 gate_up shape).
       __builtin_amdgcn_s_setprio(1);
-      mfmas(af[kk & 1], bf[kk & 1]);
+      mfmas(af[kk], bf[kk]);
       __builtin_amdgcn_s_setprio(0);
       store_b_word(odd ^ 1, odd ^ 1, kk, qp);  // block kb + 1
     }
