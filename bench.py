@@ -47,6 +47,9 @@ Extra objects on the same JSON line:
   WRITE_DIR PROBE_LOG`` turns the two counter runs into that summary.
 * ``gemm_m256`` and ``gemm_m1024_m4096``: the prefill GEMM at M=256, 1024 and 4096 on gate_up
   and down, TFLOP/s and fraction of the 2.5 PFLOP/s fp16 dense MFMA peak.
+* ``gemm_w4a8_fp8``: the W4A8 linear at the same M and shapes on e4m3 activations with per-row
+  scales, run by the fp8-MFMA GEMM the op picks there (``fp8_gemm_config``), TFLOP/s against
+  the 2.5 PF fp16 and 5 PF fp8 dense peaks.
 * ``repack_gate_up``: the load-time AWQ -> TokenForge repack (pack.py:141-143) of gate_up's
   qweight, int4 values per second (and the bytes read + written per second).
 * ``device_copy_gbps``: the box's achievable bandwidth of a plain device copy (torch, 1 GiB
@@ -72,7 +75,8 @@ Extra objects on the same JSON line:
   fused epilogues and the norms write fp16(q * scale) themselves ("fused", same bits;
   ``tokens_per_s`` is this one), or in addition qkv and
   gate_up take the FP8 codes and scales directly as W4A8 linears ("w4a8", no fp16(q * scale)
-  glue; not bit-equal: the scale multiplies each row's sum instead of each element). A pass
+  glue; not bit-equal: the scale multiplies each row's sum instead of each element; from M = 128
+  these run on the fp8-MFMA GEMM, which also applies the group scale exactly). A pass
   is one HIP graph, tokens/s = M / time per pass. M=1 on every run; ``--stack`` or ``--full``
   add M in {8, 32} (decode) and 2048 (prefill).
 * ``cpu_baseline``: reference.py's CPU path (dequantize per call + fp32 matmul), restated in
@@ -100,6 +104,7 @@ import torch  # noqa: E402
 
 HBM_PEAK_GBPS = 8000.0
 FP16_MFMA_PEAK_TFLOPS = 2500.0
+FP8_MFMA_PEAK_TFLOPS = 5000.0
 GROUP = 128
 SHAPES = [  # (layer, N, K)
     ("qkv_proj", 4608, 3584),
@@ -1053,6 +1058,30 @@ def main() -> int:
             log(f"  {name:13s} M={m:<4d} {ms * 1e3:8.2f} us {tflops:7.1f} TFLOP/s "
                 f"({100 * tflops / FP16_MFMA_PEAK_TFLOPS:.1f}% of 2.5 PF)  {cfg} ({src})")
 
+    # W4A8 prefill on the fp8 matrix cores (the op's choice at these M): e4m3 x with per-row
+    # scales, same weights and M as the W4A16 prefill GEMM above.
+    from tokenforge.kernels.config import fp8_gemm_config
+    from tokenforge.kernels.hip.w4a16 import w4a8_gemm_ex
+
+    gemm8 = []
+    for m in PREFILL_M:
+        for i in (2, 3):
+            name, n, k = SHAPES[i]
+            cfg = fp8_gemm_config(m, n, k)
+            x8 = (torch.randn((m, k), generator=gen, device=dev) * 50).to(torch.float8_e4m3fn)
+            xs8 = torch.rand((m,), generator=gen, device=dev) * 0.01 + 0.001
+            launches = 2 * copies if m <= 256 else copies
+            g, _ = capture([lambda r=r, x8=x8, xs8=xs8, cfg=cfg, i=i: w4a8_gemm_ex(x8, xs8, *layers[r % copies][i], GROUP, cfg)
+                            for r in range(launches)])
+            ms = median_replay_ms(g, launches)
+            del g, x8
+            tflops = 2 * m * n * k / (ms * 1e-3) / 1e12
+            gemm8.append({"layer": name, "m": m, "n": n, "k": k, "us": ms * 1e3, "tflops": tflops,
+                          "frac_fp16_mfma": tflops / FP16_MFMA_PEAK_TFLOPS, "frac_fp8_mfma": tflops / FP8_MFMA_PEAK_TFLOPS,
+                          "config": cfg.to_dict(), "config_source": "fp8_gemm_config"})
+            log(f"  {name:13s} M={m:<4d} W4A8 fp8 {ms * 1e3:8.2f} us {tflops:7.1f} TFLOP/s "
+                f"({100 * tflops / FP16_MFMA_PEAK_TFLOPS:.1f}% of 2.5 PF fp16, {100 * tflops / FP8_MFMA_PEAK_TFLOPS:.1f}% of 5 PF fp8)  {cfg}")
+
     norm, norm_gamma = rmsnorm_bench(dev)
 
     # The box's achievable copy bandwidth (torch's device copy, 1 GiB in and out over 4 launches
@@ -1169,6 +1198,7 @@ def main() -> int:
         },
         "gemm_m256": [g for g in gemm if g["m"] == 256],
         "gemm_m1024_m4096": [g for g in gemm if g["m"] != 256],
+        "gemm_w4a8_fp8": gemm8,
         "rmsnorm_fp8": norm,
         "repack_gate_up": repack,
         "device_copy_gbps": copy_gbps,

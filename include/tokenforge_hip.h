@@ -108,6 +108,9 @@ int tf_w4a16_dequant(const int32_t* qweight_t, const uint16_t* scales,
 #define TF_KERNEL_GEMV_DOT 0   /* decode: in-register dequant + VALU dot2, M <= 4     */
 #define TF_KERNEL_GEMV_MFMA 1  /* decode: in-register dequant + fp16 MFMA (M <= 32)   */
 #define TF_KERNEL_GEMM_MFMA 2  /* prefill: LDS-staged dequant + fp16 MFMA, split-K    */
+#define TF_KERNEL_GEMM_FP8 3   /* W4A8 prefill (tf_w4a8_linear_ex only): e4m3 x and exact
+                                  e4m3 (q - z) on the fp8 MFMA, group scale in fp32 after each
+                                  128-K group; group_size 128, N % 16 == 0, split-K           */
 
 /* Launch configuration; the counterpart of config.py:23-68 GemmConfig. The tuple
  * (kernel, block_m, block_n, block_k, num_warps, num_stages) must name a compiled

@@ -134,6 +134,30 @@ def w4a8_reference(
     return y
 
 
+def w4a8_exact_reference(
+    codes: np.ndarray, x_scale: np.ndarray, weights: W4A16Weights, bias: np.ndarray | None = None
+) -> np.ndarray:
+    """W4A8 on exact weights (no counterpart in the reference; the build's definition for its
+    fp8 GEMM): fp64 ``x_scale[m] * sum_g s[g][n] * sum_{k in g} e4m3(codes[m][k]) * (q - z)``
+    (+ bias). Unlike :func:`w4a8_reference` the weights are not rounded to fp16: ``(q - z) * s``
+    is exact in fp64 (a 5-bit integer times an fp16 scale). ``x_scale`` holds one scale or one
+    per row."""
+    from oracle.pack import unpack_int4
+
+    g = weights.group_size
+    q = unpack_int4(weights.qweight_t).astype(np.float64)  # [N, K]
+    z = np.repeat(unpack_int4(weights.qzeros), g, axis=0).T.astype(np.float64)
+    sc = np.repeat(np.asarray(weights.scales, dtype=np.float16), g, axis=0).T.astype(np.float64)
+    w = (q - z) * sc
+    x = e4m3_decode(codes).astype(np.float64)
+    y = x @ w.T if np.isfinite(x).all() else (x[:, None, :] * w[None, :, :]).sum(axis=-1)
+    s = np.asarray(x_scale, dtype=np.float64).reshape(-1)
+    y = y * (s[:, None] if s.size > 1 else s[0])
+    if bias is not None:
+        y = y + np.asarray(bias).astype(np.float64)
+    return y
+
+
 def fp8_quant_reference(y: np.ndarray, scale: np.ndarray | None = None) -> tuple[np.ndarray, np.ndarray]:
     """reference.py:42-50: per-token dynamic (or static) saturating e4m3 quantization.
 

@@ -125,3 +125,19 @@ def test_norm_form_is_checked_before_any_launch() -> None:
     assert h.tf_rmsnorm_fp8_quant_ex(*big, 8200, 1e-6, 2, None) == _lib.TF_EINVAL
     unaligned = (_X + 2, 1024, _W, _O, 1024, _S, 0, None, 0, 4)
     assert h.tf_rmsnorm_fp8_quant_ex(*unaligned, 1024, 1e-6, 2, None) == _lib.TF_EINVAL
+
+
+def test_fp8_gemm_configs_are_w4a8_only_and_checked_before_any_launch() -> None:
+    """A gemm_fp8 config is rejected by the W4A16 entry point, and by the W4A8 one where it does
+    not apply (group 64, N not a multiple of 16), both on the host."""
+    h = _lib.lib()
+    fp8 = _lib.TfGemmConfig(3, 256, 192, 128, 1, 8, 3)
+    rc = h.tf_w4a16_linear_ex(_X, 1024, _W, _S, _Z, None, _O, 1152, 256, 1152, 1024, 128, ctypes.byref(fp8), 0,
+                              None, 0, None, 0, None)
+    assert rc == _lib.TF_EINVAL and b"e4m3" in h.tf_last_error()
+    rc = h.tf_w4a8_linear_ex(_X, 1024, _S, 1, _W, _S, _Z, None, _O, 1152, 256, 1152, 1024, 64,
+                             ctypes.byref(fp8), 0, None, 0, None, 0, None)
+    assert rc == _lib.TF_EINVAL and b"group_size 128" in h.tf_last_error()
+    rc = h.tf_w4a8_linear_ex(_X, 1024, _S, 1, _W, _S, _Z, None, _O, 1160, 256, 1160, 1024, 128,
+                             ctypes.byref(fp8), 0, None, 0, None, 0, None)
+    assert rc == _lib.TF_EINVAL and b"multiple of 16" in h.tf_last_error()

@@ -179,3 +179,41 @@ def test_w4a8_reference_reduces_to_w4a16_and_is_linear_in_scale() -> None:
     assert np.array_equal(one, R.w4a16_reference(R.e4m3_decode(codes), w))
     per_row = R.w4a8_reference(codes, np.array([2.0, 4.0, 0.25, 1.0], dtype=np.float32), w)
     assert np.array_equal(per_row, one * np.array([2.0, 4.0, 0.25, 1.0])[:, None])
+
+
+def test_w4a8_exact_reference_exact_on_tiny_inputs() -> None:
+    """fp64 exact-weight W4A8 vs rational arithmetic: (q - z) * s from the integer nibbles and
+    the fp16 scales, never rounded."""
+    w = cases.layer_weights(8, 256, 1)
+    rng = np.random.default_rng(5)
+    codes = rng.integers(0, 256, (2, 256)).astype(np.uint8)
+    codes[(codes & 0x7F) == 0x7F] = 0x38  # finite codes only
+    xs = np.array([0.5, 3.0], dtype=np.float32)
+    b = cases.bias(8, 1).numpy()
+    y = R.w4a8_exact_reference(codes, xs, w, b)
+    q = P.unpack_int4(w.qweight_t)
+    z = P.unpack_int4(w.qzeros)
+    for m in range(2):
+        for n in range(8):
+            acc = Fraction(0)
+            for k in range(256):
+                grp = k // w.group_size
+                wk = (int(q[n, k]) - int(z[grp, n])) * Fraction(float(w.scales[grp, n]))
+                acc += Fraction(float(R.e4m3_decode(codes[m, k]))) * wk
+            exact = acc * Fraction(float(xs[m])) + Fraction(float(b[n]))
+            assert abs(float(exact) - y[m, n]) <= 1e-12 * max(1.0, abs(float(exact)))
+
+
+def test_w4a8_exact_reference_differs_from_the_fp16_weight_form_by_the_weight_rounding() -> None:
+    """Against w4a8_reference (weights rounded to fp16 first) the difference is at most the
+    fp16 rounding of each weight, half an ulp: |dy| <= sum_k |x_k| * ulp(|w_k|) / 2."""
+    w = cases.layer_weights(64, 512, 2)
+    rng = np.random.default_rng(6)
+    codes = rng.integers(0, 0x7F, (3, 512)).astype(np.uint8)
+    xs = np.ones(1, dtype=np.float32)
+    exact = R.w4a8_exact_reference(codes, xs, w)
+    rounded = R.w4a8_reference(codes, xs, w)
+    w16 = np.abs(P.dequantize_tf(w).astype(np.float64))
+    bound = np.abs(R.e4m3_decode(codes).astype(np.float64)) @ (np.spacing(w16.astype(np.float16)).astype(np.float64) / 2).T
+    assert np.all(np.abs(exact - rounded) <= bound + 1e-12)
+    assert np.abs(exact - rounded).max() > 0  # the two forms are not the same function

@@ -23,7 +23,7 @@ TF_EINVAL = 1
 TF_ELAUNCH = 2
 TF_ERANGE = 3
 
-KERNEL_IDS = {"gemv_dot": 0, "gemv_mfma": 1, "gemm_mfma": 2}
+KERNEL_IDS = {"gemv_dot": 0, "gemv_mfma": 1, "gemm_mfma": 2, "gemm_fp8": 3}
 EPILOGUE_NONE = 0
 EPILOGUE_RESIDUAL = 1
 EPILOGUE_SILU_MUL = 2

@@ -29,6 +29,10 @@ gemm_mfma  LDS tile M / tile N / tile K K slices across workgroups (fp32 workspa
                                         buffers, 3 and 4: pipelined with 2 and 3 x stages
                                         (block_k 64); block_k 128: skinny form, num_stages
                                         = x stages
+gemm_fp8   LDS tile M / tile N / 128    as gemm_mfma (8 waves, num_stages = x stages +
+           (one group per block)        1). W4A8 only: e4m3 x on the fp8 MFMA, the group
+                                        scale applied in fp32 after each group; chosen by
+                                        ``fp8_gemm_config``, not by the W4A16 tuner
 ========== =========================== ================================================
 
 Every kernel reads the weights in the gfx950 tile layout that ``pack.pack_awq`` produces.
@@ -46,7 +50,7 @@ GEMV_MAX_M = 32
 GEMM_MIN_M = 16
 """Smallest bucket the gemm_mfma kernels may serve (the tuner weighs both families at 16, 32)."""
 
-KERNELS: tuple[str, ...] = ("gemv_dot", "gemv_mfma", "gemm_mfma")
+KERNELS: tuple[str, ...] = ("gemv_dot", "gemv_mfma", "gemm_mfma", "gemm_fp8")
 NUM_CUS = 256
 """MI355X compute units; the split heuristics aim to put several waves on each."""
 
@@ -98,7 +102,21 @@ def _gemm_variants() -> list[tuple[str, int, int, int, int, int]]:
     return out
 
 
-VARIANTS: tuple[tuple[str, int, int, int, int, int], ...] = tuple(_gemv_variants() + _gemm_variants())
+# W4A8 fp8 GEMM tiles (block_m, block_n, waves along M, waves along N, x stages), in the
+# library's order.
+FP8_TILES: tuple[tuple[int, int, int, int, int], ...] = (
+    (256, 192, 4, 2, 2), (256, 128, 4, 2, 2), (128, 256, 2, 4, 2), (256, 160, 8, 1, 2), (128, 128, 2, 4, 2),
+    (256, 192, 4, 2, 3),
+)
+
+
+def _fp8_variants() -> list[tuple[str, int, int, int, int, int]]:
+    return [("gemm_fp8", bm, bn, 128, wm * wn, s + 1) for bm, bn, wm, wn, s in FP8_TILES]
+
+
+VARIANTS: tuple[tuple[str, int, int, int, int, int], ...] = tuple(
+    _gemv_variants() + _gemm_variants() + _fp8_variants()
+)
 """(kernel, block_m, block_n, block_k, num_warps, num_stages), in the library's order."""
 _VARIANT_SET = frozenset(VARIANTS)
 
@@ -140,7 +158,7 @@ class GemmConfig:
 
     @property
     def family(self) -> str:
-        return "gemm" if self.kernel == "gemm_mfma" else "gemv"
+        return "gemm" if self.kernel in ("gemm_mfma", "gemm_fp8") else "gemv"
 
     def variant(self) -> tuple[str, int, int, int, int, int]:
         return (self.kernel, self.block_m, self.block_n, self.block_k, self.num_warps, self.num_stages)
@@ -155,7 +173,7 @@ class GemmConfig:
             raise ValueError(f"block_k={self.block_k} must divide group_size={group_size}")
         if not 1 <= self.split_k <= 16:
             raise ValueError(f"split_k={self.split_k} must be in [1, 16]")
-        if self.kernel != "gemm_mfma" and self.split_k != 1:
+        if self.family != "gemm" and self.split_k != 1:
             raise ValueError(
                 f"split_k={self.split_k}: {self.kernel} splits K across its num_warps waves; "
                 "split_k must be 1"
@@ -255,6 +273,8 @@ def candidate_configs(bucket: int, group_size: int) -> list[GemmConfig]:
     families for buckets GEMM_MIN_M..GEMV_MAX_M)."""
     out: list[GemmConfig] = []
     for kernel, bm, bn, bk, warps, stages in VARIANTS:
+        if kernel == "gemm_fp8":  # W4A8 only (fp8_gemm_config), never a W4A16 candidate
+            continue
         cfg = GemmConfig(kernel, bm, bn, bk, 1, warps, stages)
         if not cfg.fits_bucket(bucket):
             continue
@@ -269,3 +289,49 @@ def candidate_configs(bucket: int, group_size: int) -> list[GemmConfig]:
             continue
         out.extend(GemmConfig(kernel, bm, bn, bk, s, warps, stages) for s in (1, 2, 4, 8))
     return out
+
+
+FP8_MIN_BUCKET = 128
+"""W4A8 calls from this M bucket on run the fp8 GEMM (where it applies); smaller M stay on the
+kernels that read the weights once per call (GEMV, skinny GEMM), which decode the codes to fp16."""
+
+
+def fp8_gemm_applies(bucket: int, n: int, k: int, group_size: int) -> bool:
+    """Whether a W4A8 call of this shape runs on the fp8 GEMM: prefill M, group_size 128,
+    K % 128 == 0 and N % 16 == 0 (what ``gemm_fp8`` requires)."""
+    return bucket >= FP8_MIN_BUCKET and group_size == 128 and k % 128 == 0 and n % 16 == 0
+
+
+# Makespan model of the fp8 GEMM on MI355X (fit to its measured times on the Qwen2.5-7B shapes):
+# a workgroup runs one 128-K block of a BM x BN tile at about 4.2 TFLOP/s, the 256 x 160 tile 5%
+# slower per FLOP; a K split adds about 3 us plus its fp32 partials (split * M * N * 4 bytes
+# written and read back) at about 4 TB/s.
+_FP8_CU_FLOP_PER_US = 4.2e6
+_FP8_SPLIT_US = 3.0
+_FP8_PARTIAL_BYTES_PER_US = 4.0e6
+
+
+def fp8_gemm_config(bucket: int, n: int, k: int) -> GemmConfig:
+    """Launch config of the W4A8 fp8 GEMM for one bucket: the tile and K split with the lowest
+    modelled time (rounds of workgroups over the CUs x blocks per workgroup x block time, plus
+    the split's partials). On the Qwen2.5-7B shapes it picks the configs measured fastest:
+    gate_up 256 x 160 at M = 256 and 256 x 128 above; down 256 x 128 with split 8 / 2 / 1 at
+    M = 256 / 1024 / 4096."""
+    tiles_by_m = ((256, 128), (256, 160), (256, 192)) if bucket >= 256 else ((128, 256), (128, 128))
+    k_blocks = max(1, k // 128)
+    best: tuple[float, int, int, int] | None = None
+    for bm, bn in tiles_by_m:
+        tiles = -(-n // bn) * -(-bucket // bm)
+        block_us = bm * bn * 128 * 2 / _FP8_CU_FLOP_PER_US * (1.05 if bn == 160 else 1.0)
+        for split in (1, 2, 4, 8):
+            if split > 1 and split * 4 > k_blocks:
+                break
+            rounds = -(-tiles * split // NUM_CUS)
+            us = rounds * -(-k_blocks // split) * block_us
+            if split > 1:
+                us += _FP8_SPLIT_US + split * bucket * n * 8 / _FP8_PARTIAL_BYTES_PER_US
+            if best is None or us < best[0]:
+                best = (us, bm, bn, split)
+    assert best is not None
+    _, bm, bn, split = best
+    return GemmConfig("gemm_fp8", bm, bn, 128, split, 8, 3)

@@ -42,7 +42,7 @@ import functools
 import torch
 
 from tokenforge.kernels import _lib, autotune, dispatch
-from tokenforge.kernels.config import MAX_BUCKET_M, NUM_CUS, GemmConfig
+from tokenforge.kernels.config import MAX_BUCKET_M, NUM_CUS, GemmConfig, fp8_gemm_applies, fp8_gemm_config
 from tokenforge.kernels.device import gpu_identity, hip_runnable
 from tokenforge.kernels.hip import rmsnorm_fp8 as _rms
 from tokenforge.kernels.hip import w4a16 as _w4a16
@@ -222,6 +222,11 @@ def w4a8_linear(
             f"backend must be 'hip' (or its aliases 'triton', 'cuda') at op level, got {backend!r}"
         )
     cfg = _decide(x2, m, n, k, group_size, backend)
+    bucket = dispatch.lookup_bucket(m)
+    if cfg.family == "gemm" and fp8_gemm_applies(bucket, n, k, group_size):
+        # Prefill M: the e4m3 codes go straight into the fp8 MFMA (weights as exact e4m3
+        # (q - z), the group scale applied in fp32) instead of being decoded to fp16.
+        cfg = fp8_gemm_config(bucket, n, k)
     # One contiguous scale vector: the kernel reads its data pointer with the stride of this view.
     s2 = (x_scale.reshape(-1) if x_scale.numel() > 1 else x_scale.reshape(1)).contiguous()
     r2 = residual.reshape(-1, n) if residual is not None else None

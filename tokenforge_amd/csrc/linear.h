@@ -107,6 +107,7 @@ const Variant* gemv_variants(int* count);
 const Variant* gemm_variants(int* count);
 const Variant* gemm2_variants(int* count);
 const Variant* gemm3_variants(int* count);
+const Variant* gemm8_variants(int* count);
 
 int check_group_size(int32_t group_size, int64_t k, const char* name);
 int log2_group(int32_t g);

@@ -13,19 +13,24 @@ struct Table {
   int n_gemm2;
   const Variant* gemm3;
   int n_gemm3;
+  const Variant* gemm8;
+  int n_gemm8;
   Table() {
     gemv = gemv_variants(&n_gemv);
     gemm = gemm_variants(&n_gemm);
     gemm2 = gemm2_variants(&n_gemm2);
     gemm3 = gemm3_variants(&n_gemm3);
+    gemm8 = gemm8_variants(&n_gemm8);
   }
-  int size() const { return n_gemv + n_gemm + n_gemm2 + n_gemm3; }
+  int size() const { return n_gemv + n_gemm + n_gemm2 + n_gemm3 + n_gemm8; }
   const Variant& at(int i) const {
     if (i < n_gemv) return gemv[i];
     i -= n_gemv;
     if (i < n_gemm) return gemm[i];
     i -= n_gemm;
-    return i < n_gemm2 ? gemm2[i] : gemm3[i - n_gemm2];
+    if (i < n_gemm2) return gemm2[i];
+    i -= n_gemm2;
+    return i < n_gemm3 ? gemm3[i] : gemm8[i - n_gemm3];
   }
 };
 
@@ -51,7 +56,7 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 int check_config(const tf_gemm_config& cfg, int32_t group_size) {
   if (cfg.split_k < 1 || cfg.split_k > kMaxSplitK)
     return fail(TF_EINVAL, "tf_w4a16_linear: split_k must be in [1, 16]");
-  if (cfg.kernel != TF_KERNEL_GEMM_MFMA && cfg.split_k != 1)
+  if (cfg.kernel != TF_KERNEL_GEMM_MFMA && cfg.kernel != TF_KERNEL_GEMM_FP8 && cfg.split_k != 1)
     return fail(TF_EINVAL, "tf_w4a16_linear: gemv kernels split K across waves (num_warps); split_k must be 1");
   // block_k 128 marks the skinny kernel (gemm3.hip), which reads each lane's group itself;
   // the LDS-tile kernels need one scale per column and block.
@@ -61,10 +66,11 @@ int check_config(const tf_gemm_config& cfg, int32_t group_size) {
   return TF_OK;
 }
 
-// Configs whose kernels read e4m3 x themselves (they stage x in LDS): every GEMV config. The
-// GEMM configs get x converted to fp16 first.
+// Configs whose kernels read e4m3 x themselves: every GEMV config (they decode while staging x
+// in LDS) and the fp8 GEMM (which multiplies the codes). The fp16 GEMM configs get x converted
+// to fp16 first.
 bool fuses_x8(const tf_gemm_config& cfg) {
-  return cfg.kernel == TF_KERNEL_GEMV_MFMA || cfg.kernel == TF_KERNEL_GEMV_DOT;
+  return cfg.kernel == TF_KERNEL_GEMV_MFMA || cfg.kernel == TF_KERNEL_GEMV_DOT || cfg.kernel == TF_KERNEL_GEMM_FP8;
 }
 
 constexpr int64_t kWsAlign = 256;
@@ -174,6 +180,8 @@ extern "C" int tf_w4a16_linear_ex(const uint16_t* x, int64_t ldx, const int32_t*
   if (int rc = check_config(*cfg, group_size)) return rc;
   const Variant* v = find_variant(*cfg);
   if (v == nullptr) return fail(TF_EINVAL, "tf_w4a16_linear: config does not name a compiled variant");
+  if (cfg->kernel == TF_KERNEL_GEMM_FP8)
+    return fail(TF_EINVAL, "tf_w4a16_linear: the gemm_fp8 kernels take e4m3 activations (tf_w4a8_linear_ex)");
   if (m == 0 || n == 0) return TF_OK;
   const int64_t need = v->workspace(a, *cfg);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need))
