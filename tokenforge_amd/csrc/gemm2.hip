@@ -92,6 +92,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm2_kernel(LinearArgs a, float
                                                     int tiles_n, int tiles_m) {
   using C = G2<BM, BN, WM, WN, S>;
   constexpr int TM = C::TM, TN = C::TN, BP = C::kBPer;
+  constexpr bool kEvenB = C::kBChunks % C::kThreads == 0;  // every thread holds BP chunks
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   uint8_t* const a_lds = smem;
   uint8_t* const b_lds = smem + S * C::kAStage;
@@ -149,6 +150,10 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm2_kernel(LinearArgs a, float
   // 512 contiguous bytes. Thread id takes half (id / 16) % 2 of column 16 (id / 32) + id % 16,
   // so 32 consecutive threads read one tile's 512 bytes in order. Scale and zero word of
   // column n, group grp: element 16 t P + grp rows + cc, word 2 t P + grp (rows / 8) + cc / 8.
+  // Where the chunks divide evenly over the threads (kEvenB) no thread checks its chunk id, so
+  // the loop has no per-thread branch (a branch splits it into blocks the scheduler cannot
+  // interleave with the MFMAs); otherwise the threads past the last chunk skip the
+  // conversion (measured faster than having them redo other threads' chunks).
   const uint32_t q_total = (uint32_t)(a.k >> 5);
   uint32_t b_off[BP], b_step[BP], b_sbase[BP], b_zbase[BP], b_rows[BP];
   int b_col[BP], b_half[BP];
@@ -163,7 +168,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm2_kernel(LinearArgs a, float
     const uint32_t tt = (uint32_t)n >> 4, cc = (uint32_t)n & 15u;
     const uint32_t rows = (uint32_t)tile_rows(a.n, tt);
     b_rows[i] = rows;
-    b_off[i] = (id < C::kBChunks && n < a.n) ? (tt * q_total * 16u + (uint32_t)half * rows + cc) * 16u : kOutOfRange;
+    b_off[i] = ((kEvenB || id < C::kBChunks) && n < a.n) ? (tt * q_total * 16u + (uint32_t)half * rows + cc) * 16u
+                                                          : kOutOfRange;
     b_step[i] = rows * 32u;
     b_sbase[i] = tt * 16u * (uint32_t)groups + cc;
     b_zbase[i] = tt * 2u * (uint32_t)groups + (cc >> 3);
@@ -175,10 +181,15 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm2_kernel(LinearArgs a, float
     const uint32_t grp = (uint32_t)((kb * kBK) >> a.log2g);
 #pragma unroll
     for (int i = 0; i < BP; ++i) {
+      // Offsets computed unconditionally, then selected (a conditional arm holding a multiply
+      // becomes a per-lane branch around each load).
       const bool v = ok && b_off[i] != kOutOfRange;
-      braw[slot][i] = load_b128(rq, v ? b_off[i] + (uint32_t)kb * b_step[i] : kOutOfRange);
-      bsc[slot][i] = load_b16(rs, v ? (b_sbase[i] + grp * b_rows[i]) * 2u : kOutOfRange);
-      bzw[slot][i] = load_b32(rz, v ? (b_zbase[i] + grp * (b_rows[i] >> 3)) * 4u : kOutOfRange);
+      const uint32_t wo = b_off[i] + (uint32_t)kb * b_step[i];
+      const uint32_t so = (b_sbase[i] + grp * b_rows[i]) * 2u;
+      const uint32_t zo = (b_zbase[i] + grp * (b_rows[i] >> 3)) * 4u;
+      braw[slot][i] = load_b128(rq, v ? wo : kOutOfRange);
+      bsc[slot][i] = load_b16(rs, v ? so : kOutOfRange);
+      bzw[slot][i] = load_b32(rz, v ? zo : kOutOfRange);
     }
   };
   // Dequantization operands of a register slot, one per packed chunk.
@@ -191,8 +202,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm2_kernel(LinearArgs a, float
   auto store_b_word = [&](int slot, int buf, int j, const QuantParams (&qp)[BP]) {
 #pragma unroll
     for (int i = 0; i < BP; ++i) {
-      const int id = tid + i * C::kThreads;
-      if (id < C::kBChunks) {
+      if (kEvenB || tid + i * C::kThreads < C::kBChunks) {
         h2 d[4];
         dequant_word(braw[slot][i][j], qp[i], uc, d);
         *reinterpret_cast<u4*>(b_lds + buf * C::kBStage + swz(b_col[i], b_half[i] * 4 + j)) =

@@ -160,10 +160,16 @@ __global__ __launch_bounds__(256) void gemm3_kernel(LinearArgs a, float* __restr
     const uint32_t grp = (uint32_t)((s * kStepK + g * 32) >> a.log2g);
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
+      // Offsets are computed unconditionally and then selected: a conditional arm holding a
+      // multiply is compiled as a per-lane branch around each load, which splits the loop
+      // into scheduling regions and forces a full vmcnt drain where the branches rejoin.
       const bool v = ok && w_off[rt] != kOutOfRange;
-      wraw[slot][rt] = load_b128(rq, v ? w_off[rt] + (uint32_t)s * w_step[rt] : kOutOfRange);
-      wsc[slot][rt] = load_b16(rs, v ? (s_base[rt] + grp * t_rows[rt]) * 2u : kOutOfRange);
-      wzw[slot][rt] = load_b32(rz, v ? (z_base[rt] + grp * (t_rows[rt] >> 3)) * 4u : kOutOfRange);
+      const uint32_t wo = w_off[rt] + (uint32_t)s * w_step[rt];
+      const uint32_t so = (s_base[rt] + grp * t_rows[rt]) * 2u;
+      const uint32_t zo = (z_base[rt] + grp * (t_rows[rt] >> 3)) * 4u;
+      wraw[slot][rt] = load_b128(rq, v ? wo : kOutOfRange);
+      wsc[slot][rt] = load_b16(rs, v ? so : kOutOfRange);
+      wzw[slot][rt] = load_b32(rz, v ? zo : kOutOfRange);
     }
   };
 
