@@ -36,14 +36,20 @@ def _case(index: int, variant: tuple) -> dict:  # type: ignore[type-arg]
     n = 8 * rng.randint(8, 64)
     if rng.random() < 0.5:
         n = 16 * rng.randint(4, 32)  # a multiple of 16 (the SiLU*mul epilogue needs it)
-    if kernel == "gemv_dot":
+    if kernel == "gemv_mfma" and bk == 512:
+        # The stream form: N % 16 == 0 (N % 32 == 0 under SiLU*mul), K % 128 == 0 with a step
+        # per wave, M <= block_m.
+        n = 32 * rng.randint(2, 24) + (16 if rng.random() < 0.3 else 0)
+        k = 128 * rng.randint(max(2, warps), max(2, warps) + 6)
+    if kernel == "gemv_dot" or (kernel == "gemv_mfma" and bk == 512):
         m = rng.randint(1, bm)
     elif kernel == "gemv_mfma":
         m = rng.randint(1, 2 * bm + 3)
     else:
         m = rng.randint(1, 2 * bm + 5)
     split = rng.choice((1, 2, 3)) if kernel == "gemm_mfma" else 1
-    epilogue = rng.choice(("none", "none", "residual", "silu_mul")) if n % 16 == 0 else "none"
+    silu_ok = n % 32 == 0 if (kernel == "gemv_mfma" and bk == 512) else n % 16 == 0
+    epilogue = rng.choice(("none", "none", "residual", "silu_mul")) if silu_ok else "none"
     return {"cfg": GemmConfig(kernel, bm, bn, bk, split, warps, stages), "group": group, "k": k, "n": n, "m": m,
             "bias": rng.random() < 0.5, "epilogue": epilogue, "seed": index}
 

@@ -263,6 +263,72 @@ def test_decode_full_size_config3(layer: str, n: int, k: int, device: torch.devi
         assert torch.equal(again, outs[2])
 
 
+STREAM_FORMS = [GemmConfig("gemv_mfma", 4, 16, 512, 1, w, p) for p in (2, 4) for w in (4, 8, 16)]
+
+
+@pytest.mark.parametrize(
+    ("layer", "n", "k"),
+    [("qkv", 4608, 3584), ("o", 3584, 3584), ("gate_up", 37888, 3584), ("down", 3584, 18944)],
+)
+def test_stream_form_full_size(layer: str, n: int, k: int, device: torch.device) -> None:
+    """The GEMV stream form (block_k 512) on every Qwen2.5-7B decoder linear at M in {1, 2, 4}
+    (M = 4 on down_proj does not fit its x staging and is rejected before any launch): every
+    ring depth and wave count against an fp32 product of the exactly dequantized weights,
+    bit-identical on a second call; the residual and SiLU*mul epilogues bit-equal to torch
+    applied to its own plain output; the W4A8 form on e4m3-representable x equal to the W4A16
+    result at unit scale."""
+    from tokenforge.kernels.autotune import synthetic_layer
+    from tokenforge.kernels.config import stream_form_applies
+    from tokenforge.kernels.hip.w4a16 import w4a8_gemm_ex, w4a16_gemm_ex
+
+    qweight_t, scales, qzeros = synthetic_layer(n, k, G, device, seed=13)
+    wt = w4a16_dequant(qweight_t, scales, qzeros, G).float().t().contiguous()
+    for m in (1, 2, 4):
+        gen = torch.Generator(device=device).manual_seed(20 + m)
+        x = torch.randn((m, k), generator=gen, device=device).to(torch.float16)
+        ref = x.float() @ wt
+        scale = float(ref.abs().max())
+        for cfg in STREAM_FORMS:
+            print(f"{layer} m={m} {cfg}", flush=True)
+            if not stream_form_applies(m, n, k, cfg.num_warps) and m * (k + 8) * 2 > 96 * 1024:
+                with pytest.raises(ValueError, match="stream form"):
+                    w4a16_gemm(x, qweight_t, scales, qzeros, G, cfg)
+                continue
+            y = w4a16_gemm(x, qweight_t, scales, qzeros, G, cfg)
+            rel = float((y.float() - ref).abs().max()) / scale
+            assert rel <= 2e-3, f"{layer} m={m} {cfg}: max error {rel:.3e} of max |y|"
+            assert torch.equal(w4a16_gemm(x, qweight_t, scales, qzeros, G, cfg), y)
+            r = torch.randn((m, n), generator=gen, device=device).to(torch.float16)
+            fused = w4a16_gemm_ex(x, qweight_t, scales, qzeros, G, cfg, None, "residual", r)
+            assert torch.equal(fused, r + y), f"{layer} m={m} {cfg}: residual"
+            if n % 32 == 0:
+                fused = w4a16_gemm_ex(x, qweight_t, scales, qzeros, G, cfg, None, "silu_mul")
+                expect = torch.nn.functional.silu(y[:, : n // 2]) * y[:, n // 2 :]
+                assert torch.equal(fused, expect), f"{layer} m={m} {cfg}: silu_mul"
+            x8 = x.to(torch.float8_e4m3fn)
+            one = torch.ones(1, dtype=torch.float32, device=device)
+            y8 = w4a8_gemm_ex(x8, one, qweight_t, scales, qzeros, G, cfg, None)
+            assert torch.equal(y8, w4a16_gemm(x8.to(torch.float16), qweight_t, scales, qzeros, G, cfg))
+
+
+def test_stream_form_falls_back_outside_its_shapes(device: torch.device) -> None:
+    """The op keeps the stream form's bucket config only where the form applies: on N % 32 ==
+    16 the plain call and its SiLU*mul twin both run the K-split GEMV and agree bit for bit."""
+    from tokenforge.kernels import autotune
+    from tokenforge.kernels.device import gpu_identity
+
+    n, k = 48, 1024
+    w = cases.layer_weights(n, k, 9)
+    wd = cases.on_device(w, device)
+    gpu = gpu_identity(device)
+    autotune.get_cache(gpu).put(1, n, k, G, GemmConfig("gemv_mfma", 4, 16, 512, 1, 8, 2))
+    x = cases.activations(1, k, 9).to(device)
+    y = torch.ops.tokenforge.w4a16_linear(x, wd.qweight_t, wd.scales, wd.qzeros, None, G, "hip")
+    fused = torch.ops.tokenforge.w4a16_linear_silu_mul(x, wd.qweight_t, wd.scales, wd.qzeros, None, G, "hip")
+    assert torch.equal(fused, torch.nn.functional.silu(y[:, : n // 2]) * y[:, n // 2 :])
+    _assert_close(y, x.cpu(), w)
+
+
 @pytest.mark.parametrize("group_size", [32, 64])
 def test_small_group_sizes(group_size: int, device: torch.device) -> None:
     n, k = 96, 384

@@ -177,8 +177,11 @@ def test_candidates_are_valid(bucket: int, group: int) -> None:
 def test_decode_buckets_offer_both_gemv_forms_and_work_splits() -> None:
     cands = candidate_configs(1, 128)
     assert {c.kernel for c in cands} == {"gemv_dot", "gemv_mfma"}
-    assert {c.block_k for c in cands} == {128, 256}  # K split over the waves, or columns split
+    # K split over the waves, columns split over the waves, or the stream form
+    assert {c.block_k for c in cands} == {128, 256, 512}
     assert {c.kernel for c in candidate_configs(8, 128)} == {"gemv_mfma"}  # dot form: M <= 4
+    assert {c.block_k for c in candidate_configs(8, 128)} == {128, 256}  # stream form: M <= 4
+    assert any(c.stream for c in candidate_configs(4, 128))
     assert {c.block_m for c in candidate_configs(4, 128) if c.kernel == "gemv_dot"} == {4}
     assert {c.block_m for c in candidate_configs(32, 128) if c.family == "gemv"} == {16, 32}
 
@@ -198,6 +201,28 @@ def test_decode_buckets_offer_both_gemv_forms_and_work_splits() -> None:
 def test_config_validation(kwargs: dict, match: str) -> None:
     with pytest.raises(ValueError, match=match):
         GemmConfig(**kwargs).validate(128)
+
+
+def test_stream_form_rules() -> None:
+    """The stream form serves buckets up to 4; the heuristic default picks it where it applies
+    under every epilogue and keeps the K-split GEMV elsewhere."""
+    from tokenforge.kernels.config import default_config, split_k_gemv_config, stream_form_applies
+
+    s = GemmConfig("gemv_mfma", 4, 16, 512, 1, 8, 2)
+    assert s.stream and s.family == "gemv"
+    assert [b for b in M_BUCKETS if s.fits_bucket(b)] == [1, 2, 4]
+    assert stream_form_applies(1, 37888, 3584, 8)
+    assert stream_form_applies(2, 3584, 18944, 16)
+    assert not stream_form_applies(4, 3584, 18944, 8)  # x does not fit 96 KiB of LDS
+    assert not stream_form_applies(5, 4608, 3584, 8)
+    assert not stream_form_applies(1, 48, 1024, 8)  # N % 32 == 16: SiLU*mul could not pair it
+    assert not stream_form_applies(1, 200, 1024, 8)  # N % 16 == 8
+    assert not stream_form_applies(1, 256, 1000, 1)  # K % 128 != 0
+    assert not stream_form_applies(1, 256, 896, 8)  # 7 steps for 8 waves
+    assert default_config(1, 37888, 3584, 128) == s
+    assert default_config(4, 3584, 18944, 128) == split_k_gemv_config(3584, 18944)
+    assert default_config(1, 200, 1024, 128) == split_k_gemv_config(200, 1024)
+    assert not default_config(8, 4608, 3584, 128).stream
 
 
 def test_config_from_dict_strict() -> None:

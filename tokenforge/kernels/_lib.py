@@ -12,7 +12,7 @@ import functools
 import os
 from pathlib import Path
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 """Must equal ``tf_abi_version()`` of the loaded library."""
 
 LIB_ENV = "TOKENFORGE_HIP_LIB"

@@ -24,6 +24,10 @@ gemv_mfma  M per tile (16,32) / columns 1 / waves per workgroup / 128-wide K ste
                                         on chip; block_k 256: the waves take different
                                         column sets (block_n each) over the whole K and
                                         share one staged x
+gemv_mfma  max M (4) / 16 / 512: the    1 / waves per workgroup / steps in flight per wave.
+(stream)   stream form                  Workgroups own tile ranges sized so the grid is
+                                        resident; their waves take the range's 128-wide
+                                        steps round robin (neighbouring blocks in flight)
 gemm_mfma  LDS tile M / tile N / tile K K slices across workgroups (fp32 workspace,
                                         fixed-order reduce) / 4 or 8 waves / 2: two LDS
                                         buffers, 3 and 4: pipelined with 2 and 3 x stages
@@ -80,6 +84,33 @@ def _gemv_variants() -> list[tuple[str, int, int, int, int, int]]:
     return out
 
 
+STREAM_BLOCK_K = 512
+"""``block_k`` of the GEMV stream form (gemv_mfma, M <= STREAM_MAX_M)."""
+STREAM_MAX_M = 4
+STREAM_MAX_X_BYTES = 96 * 1024
+"""The stream form stages all of x in LDS: M rows of K + 8 fp16 values must fit this."""
+
+
+def _stream_variants() -> list[tuple[str, int, int, int, int, int]]:
+    # Ring depth 2 and 4, every wave count.
+    return [("gemv_mfma", STREAM_MAX_M, 16, STREAM_BLOCK_K, w, p) for p in (2, 4) for w in _WAVES]
+
+
+def stream_form_applies(m: int, n: int, k: int, num_warps: int) -> bool:
+    """Whether the op runs a call of this shape on the GEMV stream form when its bucket's config
+    is that form: M <= 4, N % 32 == 0, K % 128 == 0 with at least one 128-wide step per wave,
+    and x small enough to stage in LDS. The rule does not depend on the epilogue, so a plain
+    call and its fused SiLU*mul or residual twin run the same kernel and agree bit for bit (the
+    library itself runs plain and residual calls on N % 16 == 0 as well)."""
+    return (
+        1 <= m <= STREAM_MAX_M
+        and n % 32 == 0
+        and k % 128 == 0
+        and k // 128 >= num_warps
+        and m * (k + 8) * 2 <= STREAM_MAX_X_BYTES
+    )
+
+
 def _gemm_variants() -> list[tuple[str, int, int, int, int, int]]:
     # num_stages 2: two LDS buffers, operands staged through registers (any group size).
     tiles = [(64, 64, 64), (64, 128, 64), (128, 64, 64), (128, 128, 64), (128, 256, 64),
@@ -115,7 +146,7 @@ def _fp8_variants() -> list[tuple[str, int, int, int, int, int]]:
 
 
 VARIANTS: tuple[tuple[str, int, int, int, int, int], ...] = tuple(
-    _gemv_variants() + _gemm_variants() + _fp8_variants()
+    _gemv_variants() + _stream_variants() + _gemm_variants() + _fp8_variants()
 )
 """(kernel, block_m, block_n, block_k, num_warps, num_stages), in the library's order."""
 _VARIANT_SET = frozenset(VARIANTS)
@@ -157,6 +188,11 @@ class GemmConfig:
         return self.kernel == "gemm_mfma" and self.block_k == 128
 
     @property
+    def stream(self) -> bool:
+        """The GEMV stream form (gemv_mfma, block_k 512), which serves M <= 4."""
+        return self.kernel == "gemv_mfma" and self.block_k == STREAM_BLOCK_K
+
+    @property
     def family(self) -> str:
         return "gemm" if self.kernel in ("gemm_mfma", "gemm_fp8") else "gemv"
 
@@ -187,12 +223,14 @@ class GemmConfig:
 
     def fits_bucket(self, bucket: int) -> bool:
         """Whether this config may serve M values of ``bucket`` (cache validation): the gemv
-        kernels serve buckets up to GEMV_MAX_M (gemv_dot only up to its block_m), gemm_mfma
-        buckets from GEMM_MIN_M on."""
+        kernels serve buckets up to GEMV_MAX_M (gemv_dot and the stream form only up to their
+        block_m), gemm_mfma buckets from GEMM_MIN_M on."""
         if self.family == "gemm":
             return bucket >= GEMM_MIN_M
         if bucket > GEMV_MAX_M:
             return False
+        if self.stream:
+            return bucket <= self.block_m
         return self.kernel != "gemv_dot" or self.block_m >= bucket
 
     def to_dict(self) -> dict[str, Any]:
@@ -221,21 +259,32 @@ def _pow2_at_most(v: int, cap: int) -> int:
     return p
 
 
+def split_k_gemv_config(n: int, k: int) -> GemmConfig:
+    """The GEMV form that runs every shape (K split over the waves of a workgroup): one
+    workgroup per 32 output columns, waves added until the grid holds about 12 per CU, never
+    more waves than 128-wide K steps."""
+    tiles = -(-n // 32)
+    k_steps = max(1, -(-k // 128))
+    waves = _pow2_at_most(max(1, -(-(12 * NUM_CUS) // tiles)), min(16, k_steps))
+    return GemmConfig("gemv_mfma", 16, 32, 128, 1, waves, 2)
+
+
 def default_config(bucket: int, n: int, k: int, group_size: int) -> GemmConfig:
     """Heuristic config used before tuning (config.py:71-92, re-derived for 256 CUs).
 
-    Streaming kernels (M < 16): one workgroup per 32 output columns; add waves (on-chip K
-    slices) until the grid holds about 12 waves per CU, never more waves than 128-wide K steps.
+    Streaming kernels (M < 16): for M <= 4 the stream form with 8 waves and a ring of 2 where
+    it applies; otherwise one workgroup per 32 output columns, adding
+    waves (on-chip K slices) until the grid holds about 12 waves per CU, never more waves than
+    128-wide K steps.
     Skinny GEMM (16 <= M <= 128): 16-64 rows x 64 or 128 columns per workgroup, K split until
     the grid holds about 1.5 workgroups per CU.
     Pipelined GEMM (M >= 256, group >= 64): 256 x 192 tiles of 8 waves (256 x 256 from M 1024);
     two-buffer GEMM for group 32.
     """
     if family_for_bucket(bucket) == "gemv":
-        tiles = -(-n // 32)
-        k_steps = max(1, -(-k // 128))
-        waves = _pow2_at_most(max(1, -(-(12 * NUM_CUS) // tiles)), min(16, k_steps))
-        return GemmConfig("gemv_mfma", 16, 32, 128, 1, waves, 2)
+        if bucket <= STREAM_MAX_M and stream_form_applies(bucket, n, k, 8):
+            return GemmConfig("gemv_mfma", STREAM_MAX_M, 16, STREAM_BLOCK_K, 1, 8, 2)
+        return split_k_gemv_config(n, k)
     if bucket <= 128:
         bm = min(bucket, 64)
         bn = 64 if bucket <= 64 else 128

@@ -42,7 +42,15 @@ import functools
 import torch
 
 from tokenforge.kernels import _lib, autotune, dispatch
-from tokenforge.kernels.config import MAX_BUCKET_M, NUM_CUS, GemmConfig, fp8_gemm_applies, fp8_gemm_config
+from tokenforge.kernels.config import (
+    MAX_BUCKET_M,
+    NUM_CUS,
+    GemmConfig,
+    fp8_gemm_applies,
+    fp8_gemm_config,
+    split_k_gemv_config,
+    stream_form_applies,
+)
 from tokenforge.kernels.device import gpu_identity, hip_runnable
 from tokenforge.kernels.hip import rmsnorm_fp8 as _rms
 from tokenforge.kernels.hip import w4a16 as _w4a16
@@ -73,6 +81,10 @@ def _decide(x2: torch.Tensor, m: int, n: int, k: int, group_size: int, backend: 
         # Above the largest bucket its config is reused; once the M tiles alone fill the CUs a
         # K split only adds the fp32 workspace (split * M * N * 4 bytes) and its reduction.
         cfg = dataclasses.replace(cfg, split_k=1)
+    if cfg.stream and not stream_form_applies(m, n, k, cfg.num_warps):
+        # The bucket's config is the stream form but this call is outside it (N % 32 == 16, or
+        # an x too long to stage): the K-split GEMV runs it, whatever the epilogue.
+        cfg = split_k_gemv_config(n, k)
     dispatch.record(dispatch.Decision("hip_gemm" if cfg.family == "gemm" else "hip_gemv", decision.bucket))
     return cfg
 

@@ -36,7 +36,7 @@ __global__ void e4m3_encode_kernel(const float* __restrict__ in, uint8_t* __rest
 
 using namespace tf;
 
-extern "C" int tf_abi_version(void) { return 6; }
+extern "C" int tf_abi_version(void) { return 7; }
 
 extern "C" const char* tf_last_error(void) { return g_last_error.c_str(); }
 

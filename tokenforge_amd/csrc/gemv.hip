@@ -478,40 +478,6 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_kernel(LinearArgs a, int win) 
 
 int64_t no_workspace(const LinearArgs&, const tf_gemm_config&) { return 0; }
 
-// LDS bytes one workgroup may use on the current device (160 KiB on gfx950), queried once
-// per device.
-size_t device_max_lds() {
-  static size_t cache[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 64 * 1024;
-  if (cache[dev] == 0) {
-    int v = 0;
-    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0)
-      v = 64 * 1024;
-    cache[dev] = (size_t)v;
-  }
-  return cache[dev];
-}
-
-// Dynamic LDS above 64 KiB must be enabled per kernel before the launch.
-template <typename Kernel>
-int reserve_lds(Kernel kernel, size_t bytes, const char* name) {
-  if (bytes > 64 * 1024 &&
-      hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                          (int)bytes) != hipSuccess)
-    return fail(TF_ELAUNCH, std::string("tf_w4a16_linear: cannot reserve LDS for ") + name);
-  return TF_OK;
-}
-
-// Buffer offsets are 32-bit: every byte offset into qweight_t, scales, qzeros and x must fit.
-int check_offsets(const LinearArgs& a) {
-  const int64_t x_bytes = ((int64_t)(a.m - 1) * a.ldx + a.k) * 2;
-  const int64_t w_bytes = (int64_t)a.n * (a.k / 2);
-  if (x_bytes >= (int64_t)kOutOfRange || w_bytes >= (int64_t)kOutOfRange)
-    return fail(TF_EINVAL, "tf_w4a16_linear: gemv kernels need x and qweight_t below 2 GiB");
-  return TF_OK;
-}
-
 // Staging window (in steps) and LDS bytes of a gemv launch. The window covers a wave's whole
 // K range when that fits the device's LDS (one window, so its length is free); otherwise it is
 // the largest multiple of the ring depth that fits. win = 0 when not even one ring's worth fits.

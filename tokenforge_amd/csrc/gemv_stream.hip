@@ -1,0 +1,344 @@
+// Decode W4A16 kernel for M <= 4 in the interleaved-stream form, on the gfx950 tile layout.
+//
+// Work split. Workgroup b owns a contiguous range of 16-row tiles [t0, t1) (XCD-aware order),
+// i.e. (t1 - t0) * nst consecutive 1 KB step blocks of qweight_t (nst = K / 128; in the tile
+// layout the blocks of consecutive tiles and steps are consecutive in memory). Its W waves take
+// each tile's steps round robin (wave w every W-th step, from a per-tile phase), so at any
+// moment the waves of a workgroup read W neighbouring 1 KB blocks, and their scale and zero
+// words are neighbours too, instead of every wave streaming its own distant range: on MI355X the
+// same bytes read with neighbouring addresses in flight come back 10-25% sooner, most of it on
+// the small scale and zero reads. The grid is sized to be resident at once, with about 32 KB of
+// weights in flight per CU (workgroups per CU = 32 / (W * P), within the occupancy the kernel
+// allows): more bytes in flight per CU were measured slower, fewer leave HBM idle.
+//
+// Per step a lane does what the MFMA GEMV does: lane 16 g + c holds chunk (column c, K block g)
+// of the step block, the 16 bytes that are the B operand of four v_mfma_f32_16x16x32_f16; the
+// exact dequantization fp16(q - z) * s (one rounding) runs in registers; x rows are the A
+// operand, read from one copy of x staged in LDS. D rows 0..3 (lanes 0..15) are the outputs.
+// When a wave's next step lies in a later tile it writes its partial sums for the tile to LDS;
+// after one barrier the workgroup adds each tile's partials in wave order and applies bias, row
+// scale and epilogue. A column's sum order depends only on its tile, K and W (not on the grid),
+// so results are bit-identical from run to run and between the epilogues.
+//
+// SiLU*mul: virtual tile v covers outputs 8v..8v+7: lanes c < 8 read gate rows 8v + c, lanes
+// c >= 8 the up rows N/2 + 8v + c - 8, i.e. half (v % 2) of physical tile v / 2 and of tile
+// N/32 + v / 2 (N % 32 == 0). The lane part of every address is then a per-lane constant and
+// the step part a wave-uniform scalar, as without the epilogue.
+#include "linear.h"
+
+#include <algorithm>
+
+namespace tf {
+namespace {
+
+constexpr int kStreamMaxM = 4;                 // D rows 0..3 live in lanes 0..15
+constexpr int kStreamMaxXBytes = 96 * 1024;    // staged x: M rows of K + 8 halfs
+constexpr int kStreamInflightKB = 32;          // weight bytes in flight per CU (KB)
+
+__host__ __device__ __forceinline__ int stream_xstride(int k) { return k + 8; }
+
+// Scalar (wave-uniform) byte offsets of step s of virtual tile v in the three streams.
+struct StepOff {
+  int w, s, z;
+};
+
+struct StreamGeo {
+  int tiles, nst, groups, gps, half_tiles;  // half_tiles = N / 32 (SiLU*mul up rows)
+  bool silu;
+  __device__ __forceinline__ StepOff at(int v, int s) const {
+    StepOff o;
+    if (silu) {
+      const int th = v >> 1, h = v & 1;
+      o.w = (th * nst + s) * 1024 + h * 128;
+      o.s = th * groups * 32 + s * gps * 32 + h * 16;
+      o.z = th * groups * 8 + s * gps * 8 + h * 4;
+    } else {
+      o.w = (v * nst + s) * 1024;
+      o.s = v * groups * 32 + s * gps * 32;
+      o.z = v * groups * 8 + s * gps * 8;
+    }
+    return o;
+  }
+};
+
+template <int P, int MAXW>
+__global__ __launch_bounds__(MAXW * 64) void gemv_stream_kernel(LinearArgs a, int nwg, int tpw) {
+  extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int W = blockDim.x >> 6;
+  const int c = lane & 15, g = lane >> 4;
+
+  StreamGeo geo;
+  geo.silu = a.epilogue == TF_EPILOGUE_SILU_MUL;
+  geo.tiles = a.n >> 4;
+  geo.nst = a.k >> 7;
+  geo.groups = a.k >> a.log2g;
+  geo.gps = 128 >> a.log2g;
+  geo.half_tiles = a.n >> 5;
+  const int nst = geo.nst;
+
+  const int b = xcd_tile(blockIdx.x, nwg);
+  const int t0 = (int)((int64_t)geo.tiles * b / nwg);
+  const int t1 = (int)((int64_t)geo.tiles * (b + 1) / nwg);
+  const int xstride = stream_xstride(a.k);
+  _Float16* xs = reinterpret_cast<_Float16*>(lds);
+  f4* part = reinterpret_cast<f4*>(lds + (a.m * xstride) / 2);  // [W][tpw][16]
+
+  // Per-lane parts of the three offsets (see the SiLU*mul note above).
+  const uint32_t gl = (uint32_t)((g * 32) >> a.log2g);  // the lane's group inside a step
+  uint32_t wl, sl, zl;
+  if (geo.silu) {
+    const bool up = c >= 8;
+    const uint32_t cl = (uint32_t)(c & 7);
+    wl = (up ? (uint32_t)geo.half_tiles * (uint32_t)nst * 1024u : 0u) + (16u * g + cl) * 16u;
+    sl = (up ? (uint32_t)geo.half_tiles * (uint32_t)geo.groups * 32u : 0u) + 32u * gl + 2u * (cl & ~1u);
+    zl = (up ? (uint32_t)geo.half_tiles * (uint32_t)geo.groups * 8u : 0u) + 8u * gl;
+  } else {
+    wl = (16u * g + (uint32_t)c) * 16u;
+    sl = 32u * gl + 2u * ((uint32_t)c & ~1u);
+    zl = 8u * gl + 4u * ((uint32_t)c >> 3);
+  }
+  const uint32_t zsh = 4u * awq_nibble_of((uint32_t)c & 7u);
+  const uint32_t ssel = (c & 1) ? 0x03020302u : 0x01000100u;  // v_perm: this column's scale half
+  const uint32_t qw_bytes = (uint32_t)a.n * (uint32_t)(a.k >> 1);
+  const uint32_t sc_bytes = (uint32_t)(geo.groups * a.n * 2);
+  const uint32_t qz_bytes = (uint32_t)(geo.groups * (a.n >> 3) * 4);
+
+  // Which wave takes which step. Step s of a tile goes to wave (phase(tile) + s) % W, and the
+  // phase depends only on the tile's physical position: a column's K steps are summed in the
+  // same order whatever the grid (so on any CU count) and under SiLU*mul, whose gate and up
+  // tiles u and N/32 + u get one phase (the phase of tile t is that of t mod N/32 when N %
+  // 32 == 0). Inside a tile a wave takes every W-th step, so the workgroup's waves read
+  // neighbouring blocks; W <= nst gives every wave at least one step of every tile.
+  const int wmask = W - 1;
+  const int pair_tiles = (a.n & 31) ? geo.tiles : geo.half_tiles;
+  auto first_step = [&](int v) {
+    const int t = geo.silu ? (v >> 1) : (v >= pair_tiles ? v - pair_tiles : v);
+    return (wave - t * nst) & wmask;
+  };
+
+  // Ring of P steps in flight; (iv, is) is the next step this wave issues.
+  u4 rw[P];
+  uint32_t rs[P], rz[P];
+  int iv = t0, is = first_step(t0);
+  auto issue = [&](int p) {
+    const bool in = iv < t1;
+    const StepOff o = geo.at(in ? iv : 0, in ? is : 0);
+    rw[p] = __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(a.qw, in ? qw_bytes : 0u), (int)wl, o.w, 0);
+    rs[p] = __builtin_amdgcn_raw_buffer_load_b32(make_rsrc(a.scales, in ? sc_bytes : 0u), (int)sl, o.s, 0);
+    rz[p] = __builtin_amdgcn_raw_buffer_load_b32(make_rsrc(a.qz, in ? qz_bytes : 0u), (int)zl, o.z, 0);
+    is += W;
+    if (is >= nst) {
+      ++iv;
+      is = first_step(iv);
+    }
+  };
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    issue(p);
+    __builtin_amdgcn_sched_barrier(0);  // slot 0 is the oldest load of the ring
+  }
+
+  // Stage x (all M rows, all of K) and clear the partial sums, then one barrier.
+  {
+    const int chunks = a.k >> 3;
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, (uint32_t)(((int64_t)(a.m - 1) * a.ldx + a.k) * 2));
+    const __amdgpu_buffer_rsrc_t rx8 = make_rsrc(a.x8, (uint32_t)((int64_t)(a.m - 1) * a.ldx8 + a.k));
+    constexpr int U = 4;
+    for (int r = 0; r < a.m; ++r) {
+      for (int q0 = threadIdx.x; q0 < chunks; q0 += U * (int)blockDim.x) {
+        u4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int q = q0 + u * (int)blockDim.x;
+          const bool ok = q < chunks;
+          if (a.x8 != nullptr) {
+            const u2 cd = load_b64(rx8, ok ? (uint32_t)((int64_t)r * a.ldx8 + q * 8) : kOutOfRange);
+            v[u] = u4{cd[0], cd[1], 0u, 0u};
+          } else {
+            v[u] = load_b128(rx, ok ? (uint32_t)(((int64_t)r * a.ldx + q * 8) * 2) : kOutOfRange);
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int q = q0 + u * (int)blockDim.x;
+          if (q < chunks)
+            *reinterpret_cast<u4*>(xs + r * xstride + q * 8) =
+                a.x8 != nullptr ? e4m3x8_to_f16(u2{v[u][0], v[u][1]}) : v[u];
+        }
+      }
+    }
+    for (int e = threadIdx.x; e < W * tpw * 16; e += blockDim.x) part[e] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+  __syncthreads();
+
+  const UnpackConsts uc = unpack_consts();
+  const _Float16* xrow = xs + (c < a.m ? c : 0) * xstride + g * 32;  // A operand: row c of x
+  f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  int cv = t0, cs = first_step(t0);  // the step this wave consumes next
+  while (cv < t1) {
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      if (cv < t1) {
+        const _Float16* xp = xrow + cs * 128;
+        h8 xa[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) xa[q] = *reinterpret_cast<const h8*>(xp + q * 8);
+        const uint32_t z = (rz[p] >> zsh) & 0xFu;
+        const uint32_t zz = z | (z << 16);
+        QuantParams qp;
+        qp.zlo = as_h2(zz | 0x64006400u);         // 1024 + z (see make_params)
+        qp.zhi = as_h2((zz << 4) | 0x54005400u);  // 64 + z
+        qp.s = as_h2(__builtin_amdgcn_perm(rs[p], rs[p], ssel));
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          h2 wd[4];
+          dequant_word(rw[p][q], qp, uc, wd);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[q], pack_h8(wd), acc, 0, 0, 0);
+        }
+        cs += W;
+        if (cs >= nst) {  // the wave leaves this tile: park its partial sums
+          if (lane < 16) part[(wave * tpw + (cv - t0)) * 16 + lane] = acc;
+          acc = f4{0.0f, 0.0f, 0.0f, 0.0f};
+          ++cv;
+          cs = first_step(cv);
+        }
+      }
+      issue(p);
+      // Slot boundary: the next slot's work waits for its own loads, not for more of the ring.
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  __syncthreads();
+
+  // Each tile's partials in wave order, then bias, row scale and the epilogue.
+  const int ntl = t1 - t0;
+  if (geo.silu) {
+    const int count = ntl * 8 * a.m;
+    for (int e = threadIdx.x; e < count; e += blockDim.x) {
+      const int tl = e / (8 * a.m), rem = e - tl * 8 * a.m;
+      const int r = rem >> 3, jc = rem & 7;
+      float gs = 0.0f, us = 0.0f;
+      for (int w = 0; w < W; ++w) {
+        gs += part[(w * tpw + tl) * 16 + jc][r];
+        us += part[(w * tpw + tl) * 16 + 8 + jc][r];
+      }
+      const int ng = 8 * (t0 + tl) + jc, nu = (a.n >> 1) + ng;
+      const float rsc = row_scale(a, r);
+      const float vg = gs * rsc + (a.bias ? half_bits_to_float(a.bias[ng]) : 0.0f);
+      const float vu = us * rsc + (a.bias ? half_bits_to_float(a.bias[nu]) : 0.0f);
+      a.out[(int64_t)r * a.ldo + ng] = finish_silu_mul(vg, vu);
+    }
+  } else {
+    const int count = ntl * 16 * a.m;
+    for (int e = threadIdx.x; e < count; e += blockDim.x) {
+      const int tl = e / (16 * a.m), rem = e - tl * 16 * a.m;
+      const int r = rem >> 4, cc = rem & 15;
+      float sum = 0.0f;
+      for (int w = 0; w < W; ++w) sum += part[(w * tpw + tl) * 16 + cc][r];
+      const int n = 16 * (t0 + tl) + cc;
+      const float v = sum * row_scale(a, r) + (a.bias ? half_bits_to_float(a.bias[n]) : 0.0f);
+      store_out(a, r, n, v);
+    }
+  }
+}
+
+// ------------------------------------------------------------------------ launch plan
+
+struct StreamPlan {
+  int nwg = 0;
+  int tpw = 0;
+  size_t lds = 0;
+};
+
+int device_cus() {
+  static int cache[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+    cache[dev] = v;
+  }
+  return cache[dev];
+}
+
+// Workgroups, tiles per workgroup and LDS bytes of a launch (nwg = 0: it does not fit).
+template <typename Kernel>
+StreamPlan plan_stream(Kernel kernel, const LinearArgs& a, int waves, int depth) {
+  StreamPlan p;
+  const int tiles = a.n >> 4;
+  const size_t xbytes = (size_t)a.m * stream_xstride(a.k) * 2;
+  const size_t cap = device_max_lds();
+  if (xbytes > (size_t)kStreamMaxXBytes || xbytes + (size_t)waves * 256 > cap) return p;
+  const int per_wave = 256;  // bytes of partials per (wave, tile)
+  // Fewest tiles per workgroup the LDS allows.
+  const int tpw_cap = (int)((cap - xbytes) / ((size_t)waves * per_wave));
+  const int min_wg = (int)cdiv(tiles, tpw_cap);
+  int per_cu = std::max(1, kStreamInflightKB / (waves * depth));
+  for (int pass = 0; pass < 2; ++pass) {
+    p.nwg = std::max(min_wg, std::min(tiles, device_cus() * per_cu));
+    p.tpw = (int)cdiv(tiles, p.nwg);
+    p.lds = xbytes + (size_t)waves * p.tpw * per_wave;
+    int occ = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, waves * 64, p.lds) != hipSuccess || occ <= 0) {
+      p.nwg = 0;
+      return p;
+    }
+    if (occ >= per_cu) break;
+    per_cu = occ;  // keep the whole grid resident
+  }
+  return p;
+}
+
+// The host-side conditions of the form, before any launch.
+int check_stream_shape(const LinearArgs& a, int waves) {
+  if (a.m > kStreamMaxM) return fail(TF_EINVAL, "tf_w4a16_linear: the gemv stream form (block_k 512) serves M <= 4");
+  if ((a.n & 15) || (a.k & 127))
+    return fail(TF_EINVAL, "tf_w4a16_linear: the gemv stream form needs N % 16 == 0 and K % 128 == 0");
+  if (a.epilogue == TF_EPILOGUE_SILU_MUL && (a.n & 31))
+    return fail(TF_EINVAL, "tf_w4a16_linear: the gemv stream form's SiLU*mul epilogue needs N % 32 == 0");
+  if ((a.k >> 7) < waves)
+    return fail(TF_EINVAL, "tf_w4a16_linear: the gemv stream form needs K >= 128 * num_warps");
+  if ((size_t)a.m * stream_xstride(a.k) * 2 > (size_t)kStreamMaxXBytes)
+    return fail(TF_EINVAL, "tf_w4a16_linear: the gemv stream form needs x (M * (K + 8) halfs) to fit 96 KiB of LDS");
+  return check_offsets(a);
+}
+
+template <int P, int MAXW>
+int check_stream(const LinearArgs& a, const tf_gemm_config& cfg) {
+  if (int rc = check_stream_shape(a, cfg.num_warps)) return rc;
+  if (plan_stream(gemv_stream_kernel<P, MAXW>, a, cfg.num_warps, P).nwg == 0)
+    return fail(TF_EINVAL, "tf_w4a16_linear: gemv stream variant does not fit the device's LDS");
+  return TF_OK;
+}
+
+template <int P, int MAXW>
+int launch_stream(const LinearArgs& a, const tf_gemm_config& cfg, float*, hipStream_t stream) {
+  if (int rc = check_stream_shape(a, cfg.num_warps)) return rc;
+  auto kernel = gemv_stream_kernel<P, MAXW>;
+  const StreamPlan plan = plan_stream(kernel, a, cfg.num_warps, P);
+  if (plan.nwg == 0) return fail(TF_EINVAL, "tf_w4a16_linear: gemv stream variant does not fit the device's LDS");
+  if (int rc = reserve_lds(kernel, plan.lds, "gemv_stream")) return rc;
+  kernel<<<plan.nwg, cfg.num_warps * 64, plan.lds, stream>>>(a, plan.nwg, plan.tpw);
+  return check_launch("tf_w4a16_linear(gemv stream)");
+}
+
+int64_t no_stream_workspace(const LinearArgs&, const tf_gemm_config&) { return 0; }
+
+#define TF_SW(P, W) \
+  {{TF_KERNEL_GEMV_MFMA, 4, 16, 512, 1, W, P}, launch_stream<P, 16>, no_stream_workspace, check_stream<P, 16>}
+#define TF_SW5(P) TF_SW(P, 1), TF_SW(P, 2), TF_SW(P, 4), TF_SW(P, 8), TF_SW(P, 16)
+
+// block_k 512 marks the stream form; block_m 4 is its largest M; num_stages the ring depth.
+const Variant kStreamVariants[] = {TF_SW5(2), TF_SW5(4)};
+
+}  // namespace
+
+const Variant* gemv_stream_variants(int* count) {
+  *count = (int)(sizeof(kStreamVariants) / sizeof(kStreamVariants[0]));
+  return kStreamVariants;
+}
+
+}  // namespace tf

@@ -86,6 +86,43 @@ __device__ __forceinline__ void store_out(const LinearArgs& a, int m, int n, flo
   a.out[(int64_t)m * a.ldo + n] = r;
 }
 
+// ------------------------------------------------------------------ launch helpers
+
+// LDS bytes one workgroup may use on the current device (160 KiB on gfx950), queried once
+// per device.
+inline size_t device_max_lds() {
+  static size_t cache[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 64 * 1024;
+  if (cache[dev] == 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0)
+      v = 64 * 1024;
+    cache[dev] = (size_t)v;
+  }
+  return cache[dev];
+}
+
+// Dynamic LDS above 64 KiB must be enabled per kernel before the launch.
+template <typename Kernel>
+inline int reserve_lds(Kernel kernel, size_t bytes, const char* name) {
+  if (bytes > 64 * 1024 &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)bytes) != hipSuccess)
+    return fail(TF_ELAUNCH, std::string("tf_w4a16_linear: cannot reserve LDS for ") + name);
+  return TF_OK;
+}
+
+// Buffer offsets are 32-bit: every byte offset into qweight_t, scales, qzeros and x must fit
+// (the streaming kernels address them through buffer resources).
+inline int check_offsets(const LinearArgs& a) {
+  const int64_t x_bytes = ((int64_t)(a.m - 1) * a.ldx + a.k) * 2;
+  const int64_t w_bytes = (int64_t)a.n * (a.k / 2);
+  if (x_bytes >= (int64_t)kOutOfRange || w_bytes >= (int64_t)kOutOfRange)
+    return fail(TF_EINVAL, "tf_w4a16_linear: gemv kernels need x and qweight_t below 2 GiB");
+  return TF_OK;
+}
+
 using LaunchFn = int (*)(const LinearArgs&, const tf_gemm_config&, float* workspace,
                          hipStream_t stream);
 using WorkspaceFn = int64_t (*)(const LinearArgs&, const tf_gemm_config&);
@@ -104,6 +141,7 @@ struct Variant {
 };
 
 const Variant* gemv_variants(int* count);
+const Variant* gemv_stream_variants(int* count);
 const Variant* gemm_variants(int* count);
 const Variant* gemm2_variants(int* count);
 const Variant* gemm3_variants(int* count);

@@ -7,6 +7,8 @@ namespace {
 struct Table {
   const Variant* gemv;
   int n_gemv;
+  const Variant* stream;
+  int n_stream;
   const Variant* gemm;
   int n_gemm;
   const Variant* gemm2;
@@ -17,15 +19,18 @@ struct Table {
   int n_gemm8;
   Table() {
     gemv = gemv_variants(&n_gemv);
+    stream = gemv_stream_variants(&n_stream);
     gemm = gemm_variants(&n_gemm);
     gemm2 = gemm2_variants(&n_gemm2);
     gemm3 = gemm3_variants(&n_gemm3);
     gemm8 = gemm8_variants(&n_gemm8);
   }
-  int size() const { return n_gemv + n_gemm + n_gemm2 + n_gemm3 + n_gemm8; }
+  int size() const { return n_gemv + n_stream + n_gemm + n_gemm2 + n_gemm3 + n_gemm8; }
   const Variant& at(int i) const {
     if (i < n_gemv) return gemv[i];
     i -= n_gemv;
+    if (i < n_stream) return stream[i];
+    i -= n_stream;
     if (i < n_gemm) return gemm[i];
     i -= n_gemm;
     if (i < n_gemm2) return gemm2[i];
