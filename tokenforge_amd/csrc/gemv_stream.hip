@@ -37,50 +37,47 @@ constexpr int kStreamInflightKB = 32;          // weight bytes in flight per CU 
 
 __host__ __device__ __forceinline__ int stream_xstride(int k) { return k + 8; }
 
-// Scalar (wave-uniform) byte offsets of step s of virtual tile v in the three streams.
-struct StepOff {
-  int w, s, z;
-};
-
+// Scalar (wave-uniform) byte offsets of step s of (virtual) tile v in the three streams, and
+// the steps' strides. SILU: virtual tile v is half v % 2 of physical tiles v / 2 (gate rows)
+// and N/32 + v / 2 (up rows; the up part of the offset is in the lane's constant part).
+template <bool SILU>
 struct StreamGeo {
-  int tiles, nst, groups, gps, half_tiles;  // half_tiles = N / 32 (SiLU*mul up rows)
-  bool silu;
-  __device__ __forceinline__ StepOff at(int v, int s) const {
-    StepOff o;
-    if (silu) {
-      const int th = v >> 1, h = v & 1;
-      o.w = (th * nst + s) * 1024 + h * 128;
-      o.s = th * groups * 32 + s * gps * 32 + h * 16;
-      o.z = th * groups * 8 + s * gps * 8 + h * 4;
-    } else {
-      o.w = (v * nst + s) * 1024;
-      o.s = v * groups * 32 + s * gps * 32;
-      o.z = v * groups * 8 + s * gps * 8;
-    }
-    return o;
+  int nst, groups, gps;
+  __device__ __forceinline__ void at(int v, int s, int& ow, int& os, int& oz) const {
+    const int t = SILU ? (v >> 1) : v;
+    const int h = SILU ? (v & 1) : 0;
+    ow = (t * nst + s) * 1024 + h * 128;
+    os = (t * groups + s * gps) * 32 + h * 16;
+    oz = (t * groups + s * gps) * 8 + h * 4;
   }
 };
 
-template <int P, int MAXW>
+template <int P, int MAXW, bool SILU, bool X8>
 __global__ __launch_bounds__(MAXW * 64) void gemv_stream_kernel(LinearArgs a, int nwg, int tpw) {
   extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+  // Every argument the kernel reads, in SGPRs from the first instruction on: otherwise the
+  // compiler loads them next to their first use (x staging, epilogue), each a scalar-memory
+  // round trip on the critical path of a short kernel.
+  __asm__ volatile("" ::"s"(a.x), "s"(a.x8), "s"(a.ldx), "s"(a.ldx8), "s"(a.qw), "s"(a.scales), "s"(a.qz),
+                   "s"(a.bias), "s"(a.out), "s"(a.ldo), "s"(a.residual), "s"(a.ldr), "s"(a.xscale),
+                   "s"(a.xscale_stride), "s"(a.m), "s"(a.n), "s"(a.k), "s"(a.log2g), "s"(a.epilogue));
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int W = blockDim.x >> 6;
   const int c = lane & 15, g = lane >> 4;
 
-  StreamGeo geo;
-  geo.silu = a.epilogue == TF_EPILOGUE_SILU_MUL;
-  geo.tiles = a.n >> 4;
+  StreamGeo<SILU> geo;
   geo.nst = a.k >> 7;
   geo.groups = a.k >> a.log2g;
   geo.gps = 128 >> a.log2g;
-  geo.half_tiles = a.n >> 5;
   const int nst = geo.nst;
+  const int tiles = a.n >> 4;
+  const int half_tiles = a.n >> 5;
 
   const int b = xcd_tile(blockIdx.x, nwg);
-  const int t0 = (int)((int64_t)geo.tiles * b / nwg);
-  const int t1 = (int)((int64_t)geo.tiles * (b + 1) / nwg);
+  // tiles * nwg < 2^31 (checked on the host): 32-bit divisions, far shorter than 64-bit ones.
+  const int t0 = (int)((uint32_t)(tiles * b) / (uint32_t)nwg);
+  const int t1 = (int)((uint32_t)(tiles * (b + 1)) / (uint32_t)nwg);
   const int xstride = stream_xstride(a.k);
   _Float16* xs = reinterpret_cast<_Float16*>(lds);
   f4* part = reinterpret_cast<f4*>(lds + (a.m * xstride) / 2);  // [W][tpw][16]
@@ -88,12 +85,12 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_stream_kernel(LinearArgs a, in
   // Per-lane parts of the three offsets (see the SiLU*mul note above).
   const uint32_t gl = (uint32_t)((g * 32) >> a.log2g);  // the lane's group inside a step
   uint32_t wl, sl, zl;
-  if (geo.silu) {
+  if (SILU) {
     const bool up = c >= 8;
     const uint32_t cl = (uint32_t)(c & 7);
-    wl = (up ? (uint32_t)geo.half_tiles * (uint32_t)nst * 1024u : 0u) + (16u * g + cl) * 16u;
-    sl = (up ? (uint32_t)geo.half_tiles * (uint32_t)geo.groups * 32u : 0u) + 32u * gl + 2u * (cl & ~1u);
-    zl = (up ? (uint32_t)geo.half_tiles * (uint32_t)geo.groups * 8u : 0u) + 8u * gl;
+    wl = (up ? (uint32_t)half_tiles * (uint32_t)nst * 1024u : 0u) + (16u * g + cl) * 16u;
+    sl = (up ? (uint32_t)half_tiles * (uint32_t)geo.groups * 32u : 0u) + 32u * gl + 2u * (cl & ~1u);
+    zl = (up ? (uint32_t)half_tiles * (uint32_t)geo.groups * 8u : 0u) + 8u * gl;
   } else {
     wl = (16u * g + (uint32_t)c) * 16u;
     sl = 32u * gl + 2u * ((uint32_t)c & ~1u);
@@ -112,26 +109,85 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_stream_kernel(LinearArgs a, in
   // 32 == 0). Inside a tile a wave takes every W-th step, so the workgroup's waves read
   // neighbouring blocks; W <= nst gives every wave at least one step of every tile.
   const int wmask = W - 1;
-  const int pair_tiles = (a.n & 31) ? geo.tiles : geo.half_tiles;
+  const int pair_tiles = (a.n & 31) ? tiles : half_tiles;
   auto first_step = [&](int v) {
-    const int t = geo.silu ? (v >> 1) : (v >= pair_tiles ? v - pair_tiles : v);
+    const int t = SILU ? (v >> 1) : (v >= pair_tiles ? v - pair_tiles : v);
     return (wave - t * nst) & wmask;
   };
+  const int dw = W * 1024, ds = W * geo.gps * 32, dz = W * geo.gps * 8;  // per-issue strides
 
-  // Ring of P steps in flight; (iv, is) is the next step this wave issues.
+  // x (all M rows, all of K) is staged in batches of U 16-byte chunks per thread over the
+  // flattened (row, chunk) index. The first batch is issued before the weight ring: loads
+  // return in order, so x issued behind the ring would reach the workgroup barrier only with
+  // the slowest wave's HBM reads (x itself comes from L2 after the first workgroups).
+  const int chunks = a.k >> 3;
+  const int total = a.m * chunks;
+  const int T = blockDim.x;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, (uint32_t)(((int64_t)(a.m - 1) * a.ldx + a.k) * 2));
+  const __amdgpu_buffer_rsrc_t rx8 = make_rsrc(a.x8, (uint32_t)((int64_t)(a.m - 1) * a.ldx8 + a.k));
+  constexpr int U = 4;
+  u4 xv[U];
+  auto row_of = [&](int e) { return (int)(e >= chunks) + (int)(e >= 2 * chunks) + (int)(e >= 3 * chunks); };
+  auto load_x = [&](int e0) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int e = e0 + u * T;
+      const int r = row_of(e), q = e - r * chunks;
+      const bool ok = e < total;
+      if (X8) {
+        const u2 cd = load_b64(rx8, ok ? (uint32_t)((int64_t)r * a.ldx8 + q * 8) : kOutOfRange);
+        xv[u] = u4{cd[0], cd[1], 0u, 0u};
+      } else {
+        xv[u] = load_b128(rx, ok ? (uint32_t)(((int64_t)r * a.ldx + q * 8) * 2) : kOutOfRange);
+      }
+    }
+  };
+  auto store_x = [&](int e0) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int e = e0 + u * T;
+      const int r = row_of(e), q = e - r * chunks;
+      if (e < total)
+        *reinterpret_cast<u4*>(xs + r * xstride + q * 8) = X8 ? e4m3x8_to_f16(u2{xv[u][0], xv[u][1]}) : xv[u];
+    }
+  };
+  // One chunk per thread when x is short (M = 1 up to K = 8 T): a single load, no batch.
+  const bool one = total <= T;
+  u4 x1 = {0u, 0u, 0u, 0u};
+  if (one) {
+    const int e = threadIdx.x;
+    const int r = row_of(e), q = e - r * chunks;
+    const bool ok = e < total;
+    if (X8) {
+      const u2 cd = load_b64(rx8, ok ? (uint32_t)((int64_t)r * a.ldx8 + q * 8) : kOutOfRange);
+      x1 = u4{cd[0], cd[1], 0u, 0u};
+    } else {
+      x1 = load_b128(rx, ok ? (uint32_t)(((int64_t)r * a.ldx + q * 8) * 2) : kOutOfRange);
+    }
+  } else {
+    load_x(threadIdx.x);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // Ring of P steps in flight; (iv, is) is the next step this wave issues and (ow, os, oz) its
+  // offsets, advanced by the strides inside a tile and recomputed when the wave changes tile.
   u4 rw[P];
   uint32_t rs[P], rz[P];
-  int iv = t0, is = first_step(t0);
+  int iv = t0, is = first_step(t0), ow, os, oz;
+  geo.at(iv, is, ow, os, oz);
   auto issue = [&](int p) {
     const bool in = iv < t1;
-    const StepOff o = geo.at(in ? iv : 0, in ? is : 0);
-    rw[p] = __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(a.qw, in ? qw_bytes : 0u), (int)wl, o.w, 0);
-    rs[p] = __builtin_amdgcn_raw_buffer_load_b32(make_rsrc(a.scales, in ? sc_bytes : 0u), (int)sl, o.s, 0);
-    rz[p] = __builtin_amdgcn_raw_buffer_load_b32(make_rsrc(a.qz, in ? qz_bytes : 0u), (int)zl, o.z, 0);
+    rw[p] = __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(a.qw, in ? qw_bytes : 0u), (int)wl, in ? ow : 0, 0);
+    rs[p] = __builtin_amdgcn_raw_buffer_load_b32(make_rsrc(a.scales, in ? sc_bytes : 0u), (int)sl, in ? os : 0, 0);
+    rz[p] = __builtin_amdgcn_raw_buffer_load_b32(make_rsrc(a.qz, in ? qz_bytes : 0u), (int)zl, in ? oz : 0, 0);
     is += W;
+    ow += dw;
+    os += ds;
+    oz += dz;
     if (is >= nst) {
       ++iv;
       is = first_step(iv);
+      geo.at(iv, is, ow, os, oz);
     }
   };
 #pragma unroll
@@ -139,38 +195,18 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_stream_kernel(LinearArgs a, in
     issue(p);
     __builtin_amdgcn_sched_barrier(0);  // slot 0 is the oldest load of the ring
   }
-
-  // Stage x (all M rows, all of K) and clear the partial sums, then one barrier.
-  {
-    const int chunks = a.k >> 3;
-    const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, (uint32_t)(((int64_t)(a.m - 1) * a.ldx + a.k) * 2));
-    const __amdgpu_buffer_rsrc_t rx8 = make_rsrc(a.x8, (uint32_t)((int64_t)(a.m - 1) * a.ldx8 + a.k));
-    constexpr int U = 4;
-    for (int r = 0; r < a.m; ++r) {
-      for (int q0 = threadIdx.x; q0 < chunks; q0 += U * (int)blockDim.x) {
-        u4 v[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const int q = q0 + u * (int)blockDim.x;
-          const bool ok = q < chunks;
-          if (a.x8 != nullptr) {
-            const u2 cd = load_b64(rx8, ok ? (uint32_t)((int64_t)r * a.ldx8 + q * 8) : kOutOfRange);
-            v[u] = u4{cd[0], cd[1], 0u, 0u};
-          } else {
-            v[u] = load_b128(rx, ok ? (uint32_t)(((int64_t)r * a.ldx + q * 8) * 2) : kOutOfRange);
-          }
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const int q = q0 + u * (int)blockDim.x;
-          if (q < chunks)
-            *reinterpret_cast<u4*>(xs + r * xstride + q * 8) =
-                a.x8 != nullptr ? e4m3x8_to_f16(u2{v[u][0], v[u][1]}) : v[u];
-        }
-      }
+  if (one) {
+    const int e = threadIdx.x;
+    const int r = row_of(e), q = e - r * chunks;
+    if (e < total) *reinterpret_cast<u4*>(xs + r * xstride + q * 8) = X8 ? e4m3x8_to_f16(u2{x1[0], x1[1]}) : x1;
+  } else {
+    store_x(threadIdx.x);
+    for (int e0 = threadIdx.x + U * T; e0 < total; e0 += U * T) {
+      load_x(e0);
+      store_x(e0);
     }
-    for (int e = threadIdx.x; e < W * tpw * 16; e += blockDim.x) part[e] = f4{0.0f, 0.0f, 0.0f, 0.0f};
   }
+  for (int e = threadIdx.x; e < W * tpw * 16; e += T) part[e] = f4{0.0f, 0.0f, 0.0f, 0.0f};
   __syncthreads();
 
   const UnpackConsts uc = unpack_consts();
@@ -212,13 +248,19 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_stream_kernel(LinearArgs a, in
   }
   __syncthreads();
 
-  // Each tile's partials in wave order, then bias, row scale and the epilogue.
+  // Each tile's partials in wave order, then bias, row scale and the epilogue. Thread e takes
+  // column e % 16 (SiLU*mul: e % 8) of row r and tile tl, (tl, r) = divmod(e / 16, M).
   const int ntl = t1 - t0;
-  if (geo.silu) {
-    const int count = ntl * 8 * a.m;
-    for (int e = threadIdx.x; e < count; e += blockDim.x) {
-      const int tl = e / (8 * a.m), rem = e - tl * 8 * a.m;
-      const int r = rem >> 3, jc = rem & 7;
+  const int m = a.m;
+  auto split = [&](int rest, int& tl, int& r) {
+    tl = m == 1 ? rest : m == 2 ? (rest >> 1) : m == 4 ? (rest >> 2) : rest / 3;
+    r = rest - tl * m;
+  };
+  if (SILU) {
+    for (int e = threadIdx.x; e < ntl * 8 * m; e += T) {
+      int tl, r;
+      split(e >> 3, tl, r);
+      const int jc = e & 7;
       float gs = 0.0f, us = 0.0f;
       for (int w = 0; w < W; ++w) {
         gs += part[(w * tpw + tl) * 16 + jc][r];
@@ -231,10 +273,10 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_stream_kernel(LinearArgs a, in
       a.out[(int64_t)r * a.ldo + ng] = finish_silu_mul(vg, vu);
     }
   } else {
-    const int count = ntl * 16 * a.m;
-    for (int e = threadIdx.x; e < count; e += blockDim.x) {
-      const int tl = e / (16 * a.m), rem = e - tl * 16 * a.m;
-      const int r = rem >> 4, cc = rem & 15;
+    for (int e = threadIdx.x; e < ntl * 16 * m; e += T) {
+      int tl, r;
+      split(e >> 4, tl, r);
+      const int cc = e & 15;
       float sum = 0.0f;
       for (int w = 0; w < W; ++w) sum += part[(w * tpw + tl) * 16 + cc][r];
       const int n = 16 * (t0 + tl) + cc;
@@ -299,6 +341,8 @@ int check_stream_shape(const LinearArgs& a, int waves) {
     return fail(TF_EINVAL, "tf_w4a16_linear: the gemv stream form needs N % 16 == 0 and K % 128 == 0");
   if (a.epilogue == TF_EPILOGUE_SILU_MUL && (a.n & 31))
     return fail(TF_EINVAL, "tf_w4a16_linear: the gemv stream form's SiLU*mul epilogue needs N % 32 == 0");
+  if ((int64_t)(a.n >> 4) * 65536 >= ((int64_t)1 << 31))
+    return fail(TF_EINVAL, "tf_w4a16_linear: the gemv stream form needs N < 2^19");
   if ((a.k >> 7) < waves)
     return fail(TF_EINVAL, "tf_w4a16_linear: the gemv stream form needs K >= 128 * num_warps");
   if ((size_t)a.m * stream_xstride(a.k) * 2 > (size_t)kStreamMaxXBytes)
@@ -309,20 +353,30 @@ int check_stream_shape(const LinearArgs& a, int waves) {
 template <int P, int MAXW>
 int check_stream(const LinearArgs& a, const tf_gemm_config& cfg) {
   if (int rc = check_stream_shape(a, cfg.num_warps)) return rc;
-  if (plan_stream(gemv_stream_kernel<P, MAXW>, a, cfg.num_warps, P).nwg == 0)
+  // Every instantiation has the same launch plan (one of them stands for all).
+  const StreamPlan plan = plan_stream(gemv_stream_kernel<P, MAXW, false, false>, a, cfg.num_warps, P);
+  if (plan.nwg == 0)
     return fail(TF_EINVAL, "tf_w4a16_linear: gemv stream variant does not fit the device's LDS");
   return TF_OK;
+}
+
+template <int P, int MAXW, bool SILU, bool X8>
+int launch_stream_k(const LinearArgs& a, int waves, hipStream_t stream) {
+  auto kernel = gemv_stream_kernel<P, MAXW, SILU, X8>;
+  const StreamPlan plan = plan_stream(kernel, a, waves, P);
+  if (plan.nwg == 0) return fail(TF_EINVAL, "tf_w4a16_linear: gemv stream variant does not fit the device's LDS");
+  if (int rc = reserve_lds(kernel, plan.lds, "gemv_stream")) return rc;
+  kernel<<<plan.nwg, waves * 64, plan.lds, stream>>>(a, plan.nwg, plan.tpw);
+  return check_launch("tf_w4a16_linear(gemv stream)");
 }
 
 template <int P, int MAXW>
 int launch_stream(const LinearArgs& a, const tf_gemm_config& cfg, float*, hipStream_t stream) {
   if (int rc = check_stream_shape(a, cfg.num_warps)) return rc;
-  auto kernel = gemv_stream_kernel<P, MAXW>;
-  const StreamPlan plan = plan_stream(kernel, a, cfg.num_warps, P);
-  if (plan.nwg == 0) return fail(TF_EINVAL, "tf_w4a16_linear: gemv stream variant does not fit the device's LDS");
-  if (int rc = reserve_lds(kernel, plan.lds, "gemv_stream")) return rc;
-  kernel<<<plan.nwg, cfg.num_warps * 64, plan.lds, stream>>>(a, plan.nwg, plan.tpw);
-  return check_launch("tf_w4a16_linear(gemv stream)");
+  const bool silu = a.epilogue == TF_EPILOGUE_SILU_MUL, x8 = a.x8 != nullptr;
+  const int w = cfg.num_warps;
+  if (silu) return x8 ? launch_stream_k<P, MAXW, true, true>(a, w, stream) : launch_stream_k<P, MAXW, true, false>(a, w, stream);
+  return x8 ? launch_stream_k<P, MAXW, false, true>(a, w, stream) : launch_stream_k<P, MAXW, false, false>(a, w, stream);
 }
 
 int64_t no_stream_workspace(const LinearArgs&, const tf_gemm_config&) { return 0; }
