@@ -296,7 +296,7 @@ def stats_summary(prof_dir: str, bench_log: str, prof_log: str, kprof_dir: str, 
     # ---------------------------------------------------------------- per entry
     tr = glob.glob(f"{kprof_dir}/**/*_kernel_trace.csv", recursive=True)[0]
     disp = sorted((d for d in csv.DictReader(open(tr))
-                   if ("gemv_kernel" in d["Kernel_Name"] or "gemm" in d["Kernel_Name"])
+                   if ("gemv_" in d["Kernel_Name"] or "gemm" in d["Kernel_Name"])
                    and "reduce" not in d["Kernel_Name"]),
                   key=lambda d: int(d["Dispatch_Id"]))
     n_launch = kprobe["launches"]
