@@ -441,30 +441,46 @@ def probe_summary(probe_log: str) -> int:
         "  tile's 128-wide K steps, each wave step one contiguous 1 KB;",
         "* tile+meta: as tile, plus the step's scale and zero-point words (the GEMV's three loads);",
         "* rows: the TokenForge row-major layout, 16 runs of 64 bytes per load instruction;",
-        "* stream: a plain grid-stride read of the weights.",
+        "* stream: a plain grid-stride read of the weights;",
+        "* wave / group / grid: the weights as the tile layout's linear sequence of 1 KB step blocks,",
+        "  with each block's scale and zero words (all three loads of a GEMV step), on resident",
+        "  grids (256 x 1, 2 or 4 workgroups of 4, 8 or 16 waves, ring depth 2 or 4): every wave",
+        "  streaming its own contiguous range (wave), each workgroup owning a contiguous range that",
+        "  its waves take round robin (group: the stream form's pattern), or the whole grid taking",
+        "  the blocks round robin (grid).",
         "",
         "Best over waves in {1, 2, 4, 8, 16} x ring depth in {2, 4, 8} (stream: grid in {512 .. 4096}).",
-        "GB/s are weight bytes (tile+meta: plus scales and zeros) per second; the GEMV's are its",
-        "algorithmic bytes (weights, scales, zeros, x, y) per second.",
+        "GB/s are weight bytes (tile+meta, wave, group, grid: plus scales and zeros) per second; the",
+        "GEMV's are its algorithmic bytes (weights, scales, zeros, x, y) per second. \"K-split GEMV\" is",
+        "the fastest candidate of the K-split form (block_k 128), the decode default before the stream",
+        "form.",
         "",
     ]
     empty = [r for r in rows if r["probe"] == "empty"]
     lines += ["| launch | us |", "|---|---:|"]
     lines += [f"| empty kernel, grid {r['grid']} | {r['us']:.2f} |" for r in empty]
-    lines += ["", "| shape | GEMV in use | best GEMV candidate | tile | tile+meta | rows | stream | in use / tile+meta |",
+    lines += ["", "| shape | GEMV in use | best GEMV candidate | K-split GEMV | tile | tile+meta | rows | stream |",
               "|---|---:|---:|---:|---:|---:|---:|---:|"]
+    pats = ("tile", "tile+meta", "rows", "stream")
     for name, n, k in SHAPES:
         mine = [r for r in rows if r.get("layer") == name]
         gemv = [r for r in mine if r["probe"] == "gemv"]
         used = next(r for r in gemv if r["tuned"])
         best = min(gemv, key=lambda r: r["us"])
-        floor = {}
-        for pat in ("tile", "tile+meta", "rows", "stream"):
-            floor[pat] = min((r for r in mine if r["probe"] == pat), key=lambda r: r["us"])
+        ksplit = min((r for r in gemv if r["config"]["block_k"] == 128), key=lambda r: r["us"])
+        floor = {p: min((r for r in mine if r["probe"] == p), key=lambda r: r["us"]) for p in pats}
         cell = lambda r: f"{r['us']:.2f} ({r['gbps']:.0f} GB/s)"  # noqa: E731
-        lines.append(f"| {name} {n}x{k} | {cell(used)} | {cell(best)} | " +
-                     " | ".join(cell(floor[p]) for p in ("tile", "tile+meta", "rows", "stream")) +
-                     f" | {used['us'] / floor['tile+meta']['us']:.2f} |")
+        lines.append(f"| {name} {n}x{k} | {cell(used)} | {cell(best)} | {cell(ksplit)} | " +
+                     " | ".join(cell(floor[p]) for p in pats) + " |")
+    lines += ["", "Which blocks are in flight together (weights + scales + zeros, best over the resident grids):", "",
+              "| shape | wave | group | grid | GEMV in use / group |", "|---|---:|---:|---:|---:|"]
+    for name, n, k in SHAPES:
+        mine = [r for r in rows if r.get("layer") == name]
+        used = next(r for r in mine if r["probe"] == "gemv" and r["tuned"])
+        fl = {p: min((r for r in mine if r["probe"] == p), key=lambda r: r["us"]) for p in ("wave", "group", "grid")}
+        cell = lambda r: f"{r['us']:.2f} ({r['gbps']:.0f} GB/s)"  # noqa: E731
+        lines.append(f"| {name} {n}x{k} | " + " | ".join(cell(fl[p]) for p in ("wave", "group", "grid")) +
+                     f" | {used['us'] / fl['group']['us']:.2f} |")
     lines += ["", "Configs (GEMV in use, best candidate) and probe shapes (waves, depth):", ""]
     for name, n, k in SHAPES:
         mine = [r for r in rows if r.get("layer") == name]
@@ -472,9 +488,11 @@ def probe_summary(probe_log: str) -> int:
         used = next(r for r in gemv if r["tuned"])
         best = min(gemv, key=lambda r: r["us"])
         fl = {p: min((r for r in mine if r["probe"] == p), key=lambda r: r["us"]) for p in ("tile", "tile+meta", "rows", "stream")}
+        fb = {p: min((r for r in mine if r["probe"] == p), key=lambda r: r["us"]) for p in ("wave", "group", "grid")}
         lines.append(f"* {name}: in use `{json.dumps(used['config'])}`; best `{json.dumps(best['config'])}`; " +
                      ", ".join(f"{p} w{fl[p]['waves']} d{fl[p]['depth']}" for p in ("tile", "tile+meta", "rows")) +
-                     f", stream grid {fl['stream']['waves']}")
+                     f", stream grid {fl['stream']['waves']}; " +
+                     ", ".join(f"{p} grid {fb[p]['grid']} w{fb[p]['waves']} d{fb[p]['depth']}" for p in ("wave", "group", "grid")))
     PROBE_SUMMARY.write_text("\n".join(lines) + "\n")
     print(f"wrote {PROBE_SUMMARY}")
     return 0
@@ -769,6 +787,7 @@ def read_probes(dev: torch.device, layers: list, copies: int, xs: list, cfgs: li
     plib.tfp_out_words.argtypes = [i64, i32]
     plib.tfp_out_words.restype = i64
     plib.tfp_empty.argtypes = [i32, p_]
+    plib.tfp_read_blocks.argtypes = [i32, p_, p_, p_, i64, i64, i32, i32, i32, p_, p_]
     stream = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
     rows = []
 
@@ -818,6 +837,32 @@ def read_probes(dev: torch.device, layers: list, copies: int, xs: list, cfgs: li
             nbytes = weight_bytes + (meta_bytes if pattern == 1 else 0)
             log(f"  {name:13s} {names[pattern]:9s} best {us:6.2f} us {nbytes / us / 1e3:6.0f} GB/s "
                 f"(waves {waves}, depth {depth})")
+        # The stream form's question: which blocks should be in flight together (patterns 4-6,
+        # weights plus scale and zero reads, on resident grids of 256 x per-CU workgroups).
+        for pattern, pname in ((4, "wave"), (5, "group"), (6, "grid")):
+            top = None
+            for waves in (4, 8, 16):
+                for per_cu in (1, 2, 4):
+                    if waves * per_cu > 32:
+                        continue
+                    for depth in (2, 4):
+                        grid = 256 * per_cu
+                        out = torch.empty(grid * waves * 64, dtype=torch.int32, device=dev)
+                        fns = [lambda c=c, waves=waves, depth=depth, pattern=pattern, out=out, grid=grid:
+                               plib.tfp_read_blocks(pattern, layers[c][i][0].data_ptr(), layers[c][i][1].data_ptr(),
+                                                    layers[c][i][2].data_ptr(), n, k, grid, waves, depth,
+                                                    out.data_ptr(), stream()) for c in range(copies)]
+                        assert fns[0]() == 0, (pattern, grid, waves, depth)
+                        g, _ = capture(fns)
+                        us = median_replay_ms(g, copies) * 1e3
+                        del g
+                        gbps = (weight_bytes + meta_bytes) / us / 1e3
+                        rows.append({"probe": pname, "layer": name, "n": n, "k": k, "grid": grid, "waves": waves,
+                                     "depth": depth, "us": us, "gbps": gbps})
+                        if top is None or us < top[0]:
+                            top = (us, grid, waves, depth)
+            assert top is not None
+            log(f"  {name:13s} {pname:9s} best {top[0]:6.2f} us (grid {top[1]}, waves {top[2]}, depth {top[3]})")
     print(json.dumps({"read_probe": rows}), flush=True)
     return 0
 

@@ -11,6 +11,13 @@
 //   2 rows:    the TokenForge layout: lane (row l / 4, chunk l % 4) reads 16 bytes of each of the
 //              tile's 16 rows per step (16 runs of 64 bytes per instruction).
 //   3 stream:  a plain grid-stride read of the whole buffer, 16 bytes per lane per load.
+//   4 wave:    the weights as the linear sequence of 1 KB step blocks they are in the tile layout
+//              (tile-major, step-minor; full tiles), each wave streaming its own contiguous range;
+//   5 group:   each workgroup owns a contiguous range of blocks and its waves take them round
+//              robin (neighbouring blocks in flight: the GEMV stream form's pattern);
+//   6 grid:    the whole grid takes the blocks round robin.
+//   Patterns 4-6 also read each block's 32-byte scale group and 8-byte zero group as the GEMV
+//   does (a 32-bit word per lane), on a grid of their own (workgroups x waves x ring depth).
 // The empty kernel measures the fixed cost of one launch inside a graph.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -79,6 +86,55 @@ __global__ __launch_bounds__(256) void stream_read_kernel(const u4* __restrict__
   out[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
 }
 
+// Patterns 4-6 over nblk 1 KB blocks (plus 32-byte scale and 8-byte zero groups per block).
+template <int P, int MODE>
+__global__ __launch_bounds__(1024) void block_read_kernel(const void* w, const void* sc, const void* qz, int nblk,
+                                                          uint32_t* out) {
+  const int lane = threadIdx.x & 63;
+  const int W = blockDim.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int V = gridDim.x * W;
+  const int v = blockIdx.x * W + wave;
+  int i0, i1, di;
+  if (MODE == 0) {  // each wave its own contiguous range
+    i0 = (int)((int64_t)nblk * v / V);
+    i1 = (int)((int64_t)nblk * (v + 1) / V);
+    di = 1;
+  } else if (MODE == 1) {  // workgroup range, waves round robin inside it
+    i0 = (int)((int64_t)nblk * blockIdx.x / gridDim.x) + wave;
+    i1 = (int)((int64_t)nblk * (blockIdx.x + 1) / gridDim.x);
+    di = W;
+  } else {  // whole grid round robin
+    i0 = v;
+    i1 = nblk;
+    di = V;
+  }
+  const uint32_t wb = (uint32_t)nblk * 1024u, sb = (uint32_t)nblk * 32u, zb = (uint32_t)nblk * 8u;
+  const int c = lane & 15;
+  u4 acc = {0u, 0u, 0u, 0u};
+  u4 rw[P];
+  uint32_t rs[P], rz[P];
+  auto issue = [&](int p, int i) {
+    const bool in = i < i1;
+    const int ii = in ? i : 0;
+    rw[p] = __builtin_amdgcn_raw_buffer_load_b128(rsrc(w, in ? wb : 0u), lane * 16, ii * 1024, 0);
+    rs[p] = __builtin_amdgcn_raw_buffer_load_b32(rsrc(sc, in ? sb : 0u), (c & ~1) * 2, ii * 32, 0);
+    rz[p] = __builtin_amdgcn_raw_buffer_load_b32(rsrc(qz, in ? zb : 0u), (c >> 3) * 4, ii * 8, 0);
+  };
+#pragma unroll
+  for (int p = 0; p < P; ++p) issue(p, i0 + p * di);
+  for (int s = i0; s < i1; s += P * di) {
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      acc ^= rw[p];
+      acc[0] ^= rs[p] ^ rz[p];
+      issue(p, s + (p + P) * di);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  out[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
+}
+
 template <int P, int PATTERN>
 int launch_tile(const void* w, int64_t n, int64_t k, int64_t groups, const void* sc, const void* qz, int waves,
                 uint32_t* out, hipStream_t stream) {
@@ -126,5 +182,27 @@ extern "C" int tfp_read(int pattern, const void* w, const void* sc, const void* 
 // One empty kernel launch (grid x 64 threads): the fixed cost of a launch.
 extern "C" int tfp_empty(int grid, void* stream) {
   empty_kernel<<<grid, 64, 0, (hipStream_t)stream>>>();
+  return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
+// Patterns 4-6 (see above) on a grid of `grid` workgroups of `waves` waves with a ring of
+// `depth` blocks (2 or 4). n % 16 == 0, k % 128 == 0; the buffers as for tfp_read. out:
+// grid * waves * 64 words. Returns 0, 1 (bad arguments) or 2 (launch error).
+extern "C" int tfp_read_blocks(int pattern, const void* w, const void* sc, const void* qz, int64_t n, int64_t k,
+                               int grid, int waves, int depth, uint32_t* out, void* stream) {
+  const hipStream_t s = (hipStream_t)stream;
+  if (!w || !sc || !qz || !out || n <= 0 || k <= 0 || n % 16 || k % 128 || grid < 1 || waves < 1 || waves > 16)
+    return 1;
+  const int nblk = (int)(n / 16 * (k / 128));
+  const dim3 g(grid), b(waves * 64);
+  switch (pattern * 16 + depth) {
+    case 4 * 16 + 2: block_read_kernel<2, 0><<<g, b, 0, s>>>(w, sc, qz, nblk, out); break;
+    case 4 * 16 + 4: block_read_kernel<4, 0><<<g, b, 0, s>>>(w, sc, qz, nblk, out); break;
+    case 5 * 16 + 2: block_read_kernel<2, 1><<<g, b, 0, s>>>(w, sc, qz, nblk, out); break;
+    case 5 * 16 + 4: block_read_kernel<4, 1><<<g, b, 0, s>>>(w, sc, qz, nblk, out); break;
+    case 6 * 16 + 2: block_read_kernel<2, 2><<<g, b, 0, s>>>(w, sc, qz, nblk, out); break;
+    case 6 * 16 + 4: block_read_kernel<4, 2><<<g, b, 0, s>>>(w, sc, qz, nblk, out); break;
+    default: return 1;
+  }
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
