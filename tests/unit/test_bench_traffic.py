@@ -202,9 +202,15 @@ def test_probe_summary_table(tmp_path: Path, monkeypatch: pytest.MonkeyPatch) ->
         for pat, us in (("tile", 14.0), ("tile+meta", 15.0), ("rows", 17.0), ("stream", 13.0)):
             rows += [{"probe": pat, "layer": name, "waves": 4, "depth": 4, "us": us, "gbps": 5000.0},
                      {"probe": pat, "layer": name, "waves": 8, "depth": 2, "us": us + 1, "gbps": 4000.0}]
+        for pat, us in (("wave", 16.0), ("group", 12.5), ("grid", 12.0)):
+            rows += [{"probe": pat, "layer": name, "grid": 512, "waves": 8, "depth": 2, "us": us, "gbps": 5600.0},
+                     {"probe": pat, "layer": name, "grid": 256, "waves": 16, "depth": 4, "us": us + 2, "gbps": 4800.0}]
     log = tmp_path / "probe.log"
     log.write_text(json.dumps({"read_probe": rows}) + "\n")
     assert bench.probe_summary(str(log)) == 0
     text = out.read_text()
-    assert "| gate_up_proj 37888x3584 | 20.00 (4000 GB/s) | 19.00 (4200 GB/s) | 14.00 (5000 GB/s) |" in text
-    assert "| 1.33 |" in text  # 20 / 15
+    # in use, best candidate, best K-split candidate (CFGS[1] has block_k 128), then the floors
+    assert ("| gate_up_proj 37888x3584 | 20.00 (4000 GB/s) | 19.00 (4200 GB/s) | 19.00 (4200 GB/s) | "
+            "14.00 (5000 GB/s) |") in text
+    assert "| 1.60 |" in text  # in use / group: 20 / 12.5
+    assert "group grid 512 w8 d2" in text
