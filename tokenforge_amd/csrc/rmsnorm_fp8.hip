@@ -1,26 +1,42 @@
 // Fused RMSNorm + OCP e4m3fn quantization: one HBM read of x, one write of the codes.
 //
-// Two forms, same bits. Row per workgroup (the default): up to 4 waves share a row and reduce
-// through LDS with a barrier per reduction. Row per wave: each wave owns one row and reduces it
-// with wave shuffles (no LDS, no barrier); four independent rows per workgroup. Either way x
-// and the weight are loaded up front and a row stays in registers between the two reductions
-// (sum of squares, then absmax). On MI355X the two forms time alike (H = 3584: 14.4 vs 15.5 us
-// at T = 4096, 24.1 vs 24.3 us at T = 8192): the kernel costs the HBM stream plus the encode of
-// the last rows to arrive, not barrier waits. Giving a wave several rows, with the next row
-// requested once the current row's data is in, was slower at every T (fewer waves per SIMD
-// leave the fp64 latency of the encode exposed), so each wave takes one row.
+// Two forms, same bits. Row per workgroup (the default): up to 4 waves share a row; each wave
+// reduces in registers (DPP lane exchanges, then four lane reads) and the waves meet in LDS
+// behind a barrier. Row per wave: each wave owns one row and reduces it without LDS or a
+// barrier; four independent rows per workgroup. Either way x and the weight are loaded up front
+// and a row stays in registers between the two reductions (sum of squares, then absmax). x is
+// loaded and the codes are stored non-temporally (each is touched once), which took the
+// H = 3584, T = 4096 row per workgroup from ~14.5 to ~12 us on MI355X (compute alone: ~10 us,
+// ~290 VALU instructions per wave). The two forms time alike at T = 4096 (~12 us); at T =
+// 8192 the row per wave is ~5% faster. Giving a wave several rows, with the next row requested
+// once the current row's data is in, was slower at every T (fewer waves per SIMD leave the
+// latency of each row's dependent steps exposed), so each wave takes one row.
 // The sum of squares is accumulated in fp64: every x^2 of an fp16 x is exact, so the fp64
 // total is the exact sum up to ~2^-53 relative and its rounding to fp32 does not depend on the
 // summation order. The kernel is therefore deterministic and matches a correctly rounded fp32
 // restatement bit for bit; torch's fp32 `mean` (reference.py:37) can differ from it by an ulp
 // of var on some rows.
 //
-// Quotient y / scale (reference.py:47-49): computed as fp32(fp64(y) * fp64(1 / scale)) with
-// the reciprocal correctly rounded in fp64. This equals the IEEE fp32 division for every
-// fp16 y and fp32 scale: the fp64 product is within 2^-52 (relative) of y / scale, while a
-// quotient of an 11-bit by a 24-bit significand that is not exactly representable lies at
-// least ~2^-49 (relative) away from every fp32 rounding boundary, so both round alike (the
-// zero, infinite and NaN cases follow IEEE multiplication by 0, inf or NaN the same way).
+// Quotient y / scale (reference.py:47-49), two exact forms:
+// * static scales: fp32(fp64(y) * fp64(1 / scale)) with the reciprocal correctly rounded in
+//   fp64. This equals the IEEE fp32 division for every fp16 y and fp32 scale: the fp64 product
+//   is within 2^-52 (relative) of y / scale, while a quotient of an 11-bit by a 24-bit
+//   significand that is not exactly representable lies at least ~2^-49 (relative) away from
+//   every fp32 rounding boundary, so both round alike (the zero, infinite and NaN cases follow
+//   IEEE multiplication by 0, inf or NaN the same way).
+// * dynamic scales: Markstein's correction in fp32, r = fp32(1 / scale) correctly rounded,
+//   q0 = y * r, e = fma(q0, scale, -y) (exact), q = fma(-e, r, q0). Three fp32 operations on
+//   the fp16 y instead of two conversions and an fp64 product. It equals the IEEE division
+//   for every finite fp16 y and every scale a row can produce, max(fp32(amax / 448),
+//   1 / (448 * 512)) over all finite fp16 amax: checked exhaustively on MI355X (31743 scales
+//   x 63488 y). The residual is formed as q0 * scale - y, not y - q0 * scale, so that y = -0
+//   gives q = -0 (the other sign order would sum +0 and -0 to +0).
+//
+// Per-row divisions: mean = fp32(fp64(sum) * fp64(1 / h)) and amax / 448 =
+// fp32(fp64(amax) * fp64(1 / 448)) equal the IEEE fp32 quotients. A quotient of a 24-bit
+// (11-bit) significand by an integer below 2^15 is either exactly representable, or at least
+// 2^-40 (relative) away from every fp32 rounding boundary, as its significand is an integer
+// over the divisor's odd part; the fp64 product is within 2^-52 of it.
 //
 // Encoding: rows whose absmax and scale are finite (scale > 0) hold no NaN quotient, so they
 // clamp with v_med3 and encode two values per v_cvt_pk_fp8_f32. That instruction rounds to
@@ -48,10 +64,39 @@ __device__ __forceinline__ _Float16 mul_round_f32_then_f16(float a, float b) {
 }
 constexpr float kMinScale = 1.0f / (448.0f * 512.0f);  // reference.py:10
 
+// Lane exchanges inside a row of 16 lanes (DPP, no LDS): swap neighbours, swap pairs, mirror
+// each half row, mirror the row. Applied in that order, each pairs every lane with one holding
+// a disjoint set of the row's lanes, so four steps leave the row's total in all 16 lanes.
+constexpr int kDppQuadXor1 = 0xB1;      // quad_perm [1, 0, 3, 2]
+constexpr int kDppQuadXor2 = 0x4E;      // quad_perm [2, 3, 0, 1]
+constexpr int kDppHalfRowMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+  const uint64_t b = __builtin_bit_cast(uint64_t, v);
+  const uint64_t lo = dpp_u32<CTRL>((uint32_t)b), hi = dpp_u32<CTRL>((uint32_t)(b >> 32));
+  return __builtin_bit_cast(double, lo | (hi << 32));
+}
+__device__ __forceinline__ double readlane_f64(double v, int lane) {
+  const uint64_t b = __builtin_bit_cast(uint64_t, v);
+  const uint64_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, lane);
+  const uint64_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), lane);
+  return __builtin_bit_cast(double, lo | (hi << 32));
+}
+
+// Sum over the WAVES waves of the workgroup (every lane active); the result is wave-uniform.
 template <int WAVES>
 __device__ __forceinline__ double block_sum(double v, double* red) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  v += dpp_f64<kDppQuadXor1>(v);
+  v += dpp_f64<kDppQuadXor2>(v);
+  v += dpp_f64<kDppHalfRowMirror>(v);
+  v += dpp_f64<kDppRowMirror>(v);
+  v = (readlane_f64(v, 0) + readlane_f64(v, 16)) + (readlane_f64(v, 32) + readlane_f64(v, 48));
   if (WAVES == 1) return v;  // the row is one wave's: no LDS, no barrier
   const int wave = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) red[wave] = v;
@@ -64,14 +109,16 @@ __device__ __forceinline__ double block_sum(double v, double* red) {
 
 // Max of |y| as fp16 bit patterns: for non-NaN values the unsigned order of (bits & 0x7FFF)
 // is the order of |y|, and every NaN pattern is above +inf, so a NaN anywhere wins (the NaN
-// propagation of torch's amax).
+// propagation of torch's amax). The result is wave-uniform.
 template <int WAVES>
 __device__ __forceinline__ uint32_t block_max_u32(uint32_t v, uint32_t* red) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const uint32_t o = (uint32_t)__shfl_xor((int)v, off, 64);
-    v = v > o ? v : o;
-  }
+  v = __builtin_elementwise_max(v, dpp_u32<kDppQuadXor1>(v));
+  v = __builtin_elementwise_max(v, dpp_u32<kDppQuadXor2>(v));
+  v = __builtin_elementwise_max(v, dpp_u32<kDppHalfRowMirror>(v));
+  v = __builtin_elementwise_max(v, dpp_u32<kDppRowMirror>(v));
+  const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+  const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+  v = __builtin_elementwise_max(__builtin_elementwise_max(a, b), __builtin_elementwise_max(c, d));
   if (WAVES == 1) return v;
   const int wave = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) red[wave] = v;
@@ -83,6 +130,35 @@ __device__ __forceinline__ uint32_t block_max_u32(uint32_t v, uint32_t* red) {
 }
 
 __device__ __forceinline__ float quotient(_Float16 y, double rcp) { return (float)((double)(float)y * rcp); }
+
+// fp32(y) * r for the fp16 y in the low (HI false) or high half of `pair`, as one v_fma_mix_f32
+// that reads the fp16 operand directly (the backend does not form it from a multiply). The
+// addend is -0, so the sum is the rounded product for every sign, zeros included.
+template <bool HI>
+__device__ __forceinline__ float mul_f16_f32(uint32_t pair, float r) {
+  float q;
+  if (HI)
+    __asm__("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(q) : "v"(pair), "v"(r), "v"(-0.0f));
+  else
+    __asm__("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(q) : "v"(pair), "v"(r), "v"(-0.0f));
+  return q;
+}
+
+// y / s for the fp16 y in half HI of `pair` and a dynamic scale s, given r = fp32(1 / s)
+// (Markstein's correction, see above).
+template <bool HI>
+__device__ __forceinline__ float quotient_dynamic(h2 pair, float s, float r) {
+  const float yf = (float)pair[HI ? 1 : 0];
+  const float q0 = mul_f16_f32<HI>(as_u32(pair), r);
+  const float e = __builtin_fmaf(q0, s, -yf);
+  return __builtin_fmaf(-e, r, q0);
+}
+
+// Four clamped fp32 values -> four e4m3fn codes in one word (bytes in order).
+__device__ __forceinline__ uint32_t encode4_clamped(float a, float b, float c, float d) {
+  const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, __builtin_bit_cast(int, a), false);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true);
+}
 
 __device__ __forceinline__ uint32_t f16_bits_of(_Float16 v) { return __builtin_bit_cast(uint16_t, v); }
 
@@ -99,18 +175,24 @@ __device__ __forceinline__ u2 dequant_codes4(uint32_t codes, float s) {
   return u2{h0 | (h1 << 16), h2 | (h3 << 16)};
 }
 
+// Cache policy of the 16-byte loads: x is read once, so its loads are non-temporal (nt); the
+// weight is read by every row and loads with the default policy.
+constexpr int kLoadOnce = 2;  // nt
+constexpr int kLoadReused = 0;
+
 // One row's x (or the weight) into registers as fp16 pairs: pair j of chunk i holds elements
 // 2j, 2j+1 of the chunk at (lane + i * threads) * 8. Chunks past h read as zeros. VEC: one
-// 16-byte buffer load per chunk through a resource bounded by the row, so chunks past h come
-// back as zeros without a branch (h % 8 == 0 and 16-byte aligned rows); else element loads.
-template <int CPT, int THREADS, bool VEC>
+// 16-byte buffer load per chunk (cache policy AUX) through a resource bounded by the row, so
+// chunks past h come back as zeros without a branch (h % 8 == 0 and 16-byte aligned rows);
+// else element loads.
+template <int CPT, int THREADS, bool VEC, int AUX>
 __device__ __forceinline__ void load_row(const uint16_t* __restrict__ src, int tid, int h, h2 (&v)[CPT][4]) {
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(src, (uint32_t)h * 2u);
 #pragma unroll
   for (int i = 0; i < CPT; ++i) {
     const int e0 = (tid + i * THREADS) * 8;
     if (VEC) {
-      const u4 r = load_b128(rs, (uint32_t)e0 * 2u);
+      const u4 r = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)((uint32_t)e0 * 2u), 0, AUX);
 #pragma unroll
       for (int j = 0; j < 4; ++j) v[i][j] = as_h2(r[j]);
     } else {
@@ -147,11 +229,12 @@ template <int WAVES, int CPT, bool VEC, bool DQ>
 __device__ __forceinline__ void finish_row(h2 (&xv)[CPT][4], const h2 (&wv)[CPT][4], double total, int64_t row,
                                            int tid, uint8_t* __restrict__ q, int64_t ldq, float* __restrict__ scale,
                                            int static_scale, float s_static, uint16_t* __restrict__ dq,
-                                           int64_t lddq, int h, float eps, uint32_t* red_u) {
+                                           int64_t lddq, int h, double inv_h, float eps, uint32_t* red_u) {
   constexpr int kThreads = WAVES * 64;
 
-  // reference.py:37-38: var = mean(x^2) in fp32, rstd = 1 / sqrt(var + eps), IEEE ops.
-  const float var = (float)total / (float)h;
+  // reference.py:37-38: var = mean(x^2) in fp32, rstd = 1 / sqrt(var + eps), IEEE ops (the
+  // mean as an exact reciprocal product, inv_h = fp64(1 / h)).
+  const float var = (float)((double)(float)total * inv_h);
   const float rstd = 1.0f / __builtin_sqrtf(var + eps);
 
   uint32_t amax_bits = 0;
@@ -189,28 +272,37 @@ __device__ __forceinline__ void finish_row(h2 (&xv)[CPT][4], const h2 (&wv)[CPT]
   if (static_scale) {
     s = s_static;
   } else {
-    const float raw = amax / kFp8Max;
+    const float raw = (float)((double)amax * (1.0 / (double)kFp8Max));  // = fp32(amax / 448)
     s = (raw < kMinScale) ? kMinScale : raw;  // clamp(min=...) keeps NaN
     if (tid == 0) scale[row] = s;
   }
-  const double rcp = 1.0 / (double)s;
   const bool fast = __builtin_isfinite(amax) && __builtin_isfinite(s) && s > 0.0f;
+  // Dynamic rows with a finite absmax take the fp32 quotient; static scales keep the fp64 one.
+  const bool dynamic_fast = fast && !static_scale;
+  const float r32 = dynamic_fast ? 1.0f / s : 0.0f;
+  const double rcp = dynamic_fast ? 0.0 : 1.0 / (double)s;
 
   uint8_t* qr = q + row * ldq;
 #pragma unroll
   for (int i = 0; i < CPT; ++i) {
     const int e0 = (tid + i * kThreads) * 8;
     uint32_t lo, hi;
-    if (fast) {
-      uint32_t pk[4];
+    if (dynamic_fast) {
+      float v[8];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const float a = __builtin_amdgcn_fmed3f(quotient(xv[i][j][0], rcp), -kFp8Max, kFp8Max);
-        const float b = __builtin_amdgcn_fmed3f(quotient(xv[i][j][1], rcp), -kFp8Max, kFp8Max);
-        pk[j] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false) & 0xFFFFu;
+        v[2 * j] = __builtin_amdgcn_fmed3f(quotient_dynamic<false>(xv[i][j], s, r32), -kFp8Max, kFp8Max);
+        v[2 * j + 1] = __builtin_amdgcn_fmed3f(quotient_dynamic<true>(xv[i][j], s, r32), -kFp8Max, kFp8Max);
       }
-      lo = pk[0] | (pk[1] << 16);
-      hi = pk[2] | (pk[3] << 16);
+      lo = encode4_clamped(v[0], v[1], v[2], v[3]);
+      hi = encode4_clamped(v[4], v[5], v[6], v[7]);
+    } else if (fast) {
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        v[j] = __builtin_amdgcn_fmed3f(quotient(xv[i][j >> 1][j & 1], rcp), -kFp8Max, kFp8Max);
+      lo = encode4_clamped(v[0], v[1], v[2], v[3]);
+      hi = encode4_clamped(v[4], v[5], v[6], v[7]);
     } else {
       uint8_t codes[8];
 #pragma unroll
@@ -228,7 +320,8 @@ __device__ __forceinline__ void finish_row(h2 (&xv)[CPT][4], const h2 (&wv)[CPT]
       }
     }
     if (VEC) {
-      if (e0 < h) *reinterpret_cast<uint2*>(qr + e0) = make_uint2(lo, hi);
+      // Non-temporal stores: the codes are written once and not read back by this kernel.
+      if (e0 < h) __builtin_nontemporal_store(u2{lo, hi}, reinterpret_cast<u2*>(qr + e0));
     } else {
 #pragma unroll
       for (int j = 0; j < 8; ++j)
@@ -238,7 +331,7 @@ __device__ __forceinline__ void finish_row(h2 (&xv)[CPT][4], const h2 (&wv)[CPT]
       const u2 a = dequant_codes4(lo, s), b = dequant_codes4(hi, s);
       uint16_t* dr = dq + row * lddq;
       if (VEC) {
-        if (e0 < h) *reinterpret_cast<u4*>(dr + e0) = u4{a[0], a[1], b[0], b[1]};
+        if (e0 < h) __builtin_nontemporal_store(u4{a[0], a[1], b[0], b[1]}, reinterpret_cast<u4*>(dr + e0));
       } else {
         const uint32_t words[4] = {a[0], a[1], b[0], b[1]};
 #pragma unroll
@@ -255,7 +348,7 @@ template <int WAVES, int CPT, bool VEC, bool DQ>
 __global__ __launch_bounds__(WAVES * 64) void rmsnorm_fp8_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* __restrict__ w,
     uint8_t* __restrict__ q, int64_t ldq, float* __restrict__ scale, int static_scale,
-    uint16_t* __restrict__ dq, int64_t lddq, int h, float eps) {
+    uint16_t* __restrict__ dq, int64_t lddq, int h, double inv_h, float eps) {
   __shared__ double red_d[WAVES];
   __shared__ uint32_t red_u[WAVES];
   const int64_t row = blockIdx.x;
@@ -263,11 +356,11 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_fp8_kernel(
   // All inputs are requested before anything waits on any of them.
   const float s_static = static_scale ? scale[0] : 0.0f;
   h2 xv[CPT][4], wv[CPT][4];
-  load_row<CPT, WAVES * 64, VEC>(x + row * ldx, tid, h, xv);
-  load_row<CPT, WAVES * 64, VEC>(w, tid, h, wv);
+  load_row<CPT, WAVES * 64, VEC, kLoadOnce>(x + row * ldx, tid, h, xv);
+  load_row<CPT, WAVES * 64, VEC, kLoadReused>(w, tid, h, wv);
   const double total = row_sum_squares<WAVES, CPT>(xv, red_d);
-  finish_row<WAVES, CPT, VEC, DQ>(xv, wv, total, row, tid, q, ldq, scale, static_scale, s_static, dq, lddq, h, eps,
-                                  red_u);
+  finish_row<WAVES, CPT, VEC, DQ>(xv, wv, total, row, tid, q, ldq, scale, static_scale, s_static, dq, lddq, h, inv_h,
+                                  eps, red_u);
 }
 
 // Row per wave: wave g of the grid (4 per workgroup) takes row g. Needs VEC (16-byte rows).
@@ -275,17 +368,17 @@ template <int CPT, bool DQ>
 __global__ __launch_bounds__(256) void rmsnorm_fp8_wave_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* __restrict__ w,
     uint8_t* __restrict__ q, int64_t ldq, float* __restrict__ scale, int static_scale,
-    uint16_t* __restrict__ dq, int64_t lddq, int64_t t, int h, float eps) {
+    uint16_t* __restrict__ dq, int64_t lddq, int64_t t, int h, double inv_h, float eps) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= t) return;  // the whole wave: no row for it, and no barrier follows
   const float s_static = static_scale ? scale[0] : 0.0f;
   h2 xv[CPT][4], wv[CPT][4];
-  load_row<CPT, 64, true>(x + row * ldx, lane, h, xv);
-  load_row<CPT, 64, true>(w, lane, h, wv);
+  load_row<CPT, 64, true, kLoadOnce>(x + row * ldx, lane, h, xv);
+  load_row<CPT, 64, true, kLoadReused>(w, lane, h, wv);
   const double total = row_sum_squares<1, CPT>(xv, nullptr);
-  finish_row<1, CPT, true, DQ>(xv, wv, total, row, lane, q, ldq, scale, static_scale, s_static, dq, lddq, h, eps,
-                               nullptr);
+  finish_row<1, CPT, true, DQ>(xv, wv, total, row, lane, q, ldq, scale, static_scale, s_static, dq, lddq, h, inv_h,
+                               eps, nullptr);
 }
 
 struct NormArgs {
@@ -300,6 +393,7 @@ struct NormArgs {
   int64_t lddq;
   int64_t t;
   int h;
+  double inv_h;  // fp64(1 / h)
   float eps;
 };
 
@@ -307,10 +401,10 @@ template <int WAVES, int CPT, bool VEC>
 int launch_vec(const NormArgs& n, hipStream_t stream) {
   if (n.dq)
     rmsnorm_fp8_kernel<WAVES, CPT, VEC, true><<<(unsigned)n.t, WAVES * 64, 0, stream>>>(
-        n.x, n.ldx, n.w, n.q, n.ldq, n.scale, n.static_scale, n.dq, n.lddq, n.h, n.eps);
+        n.x, n.ldx, n.w, n.q, n.ldq, n.scale, n.static_scale, n.dq, n.lddq, n.h, n.inv_h, n.eps);
   else
     rmsnorm_fp8_kernel<WAVES, CPT, VEC, false><<<(unsigned)n.t, WAVES * 64, 0, stream>>>(
-        n.x, n.ldx, n.w, n.q, n.ldq, n.scale, n.static_scale, nullptr, 0, n.h, n.eps);
+        n.x, n.ldx, n.w, n.q, n.ldq, n.scale, n.static_scale, nullptr, 0, n.h, n.inv_h, n.eps);
   return check_launch("tf_rmsnorm_fp8_quant");
 }
 
@@ -336,10 +430,10 @@ int launch_wave(const NormArgs& n, hipStream_t stream) {
   const unsigned grid = (unsigned)((n.t + 3) / 4);
   if (n.dq)
     rmsnorm_fp8_wave_kernel<CPT, true><<<grid, 256, 0, stream>>>(n.x, n.ldx, n.w, n.q, n.ldq, n.scale,
-                                                                 n.static_scale, n.dq, n.lddq, n.t, n.h, n.eps);
+                                                                 n.static_scale, n.dq, n.lddq, n.t, n.h, n.inv_h, n.eps);
   else
     rmsnorm_fp8_wave_kernel<CPT, false><<<grid, 256, 0, stream>>>(n.x, n.ldx, n.w, n.q, n.ldq, n.scale,
-                                                                  n.static_scale, nullptr, 0, n.t, n.h, n.eps);
+                                                                  n.static_scale, nullptr, 0, n.t, n.h, n.inv_h, n.eps);
   return check_launch("tf_rmsnorm_fp8_quant");
 }
 
@@ -382,7 +476,7 @@ extern "C" int tf_rmsnorm_fp8_quant_ex(const uint16_t* x, int64_t ldx, const uin
                            "aligned rows and h <= 8192");
   if (t == 0) return TF_OK;
   hipStream_t s = (hipStream_t)stream;
-  const NormArgs n{x, ldx, weight, q, ldq, scale, static_scale, dq, lddq, t, (int)h, eps};
+  const NormArgs n{x, ldx, weight, q, ldq, scale, static_scale, dq, lddq, t, (int)h, 1.0 / (double)h, eps};
   // Auto is the row per workgroup: it is as fast as the row per wave at long batches and faster
   // at short ones, where more lanes per row shorten each row's dependent steps.
   if (form == TF_NORM_ROW_PER_WAVE) {
