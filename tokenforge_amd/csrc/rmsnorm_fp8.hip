@@ -17,26 +17,8 @@
 // restatement bit for bit; torch's fp32 `mean` (reference.py:37) can differ from it by an ulp
 // of var on some rows.
 //
-// Quotient y / scale (reference.py:47-49), two exact forms:
-// * static scales: fp32(fp64(y) * fp64(1 / scale)) with the reciprocal correctly rounded in
-//   fp64. This equals the IEEE fp32 division for every fp16 y and fp32 scale: the fp64 product
-//   is within 2^-52 (relative) of y / scale, while a quotient of an 11-bit by a 24-bit
-//   significand that is not exactly representable lies at least ~2^-49 (relative) away from
-//   every fp32 rounding boundary, so both round alike (the zero, infinite and NaN cases follow
-//   IEEE multiplication by 0, inf or NaN the same way).
-// * dynamic scales: Markstein's correction in fp32, r = fp32(1 / scale) correctly rounded,
-//   q0 = y * r, e = fma(q0, scale, -y) (exact), q = fma(-e, r, q0). Three fp32 operations on
-//   the fp16 y instead of two conversions and an fp64 product. It equals the IEEE division
-//   for every finite fp16 y and every scale a row can produce, max(fp32(amax / 448),
-//   1 / (448 * 512)) over all finite fp16 amax: checked exhaustively on MI355X (31743 scales
-//   x 63488 y). The residual is formed as q0 * scale - y, not y - q0 * scale, so that y = -0
-//   gives q = -0 (the other sign order would sum +0 and -0 to +0).
-//
-// Per-row divisions: mean = fp32(fp64(sum) * fp64(1 / h)) and amax / 448 =
-// fp32(fp64(amax) * fp64(1 / 448)) equal the IEEE fp32 quotients. A quotient of a 24-bit
-// (11-bit) significand by an integer below 2^15 is either exactly representable, or at least
-// 2^-40 (relative) away from every fp32 rounding boundary, as its significand is an integer
-// over the divisor's odd part; the fp64 product is within 2^-52 of it.
+// Quotient y / scale (reference.py:47-49) and the per-row divisions: exact forms in
+// norm_quotient.h.
 //
 // Encoding: rows whose absmax and scale are finite (scale > 0) hold no NaN quotient, so they
 // clamp with v_med3 and encode two values per v_cvt_pk_fp8_f32. That instruction rounds to
@@ -45,12 +27,12 @@
 // (0x7F for +NaN); the remaining rows therefore clamp with NaN-preserving compares and use
 // e4m3_encode.
 #include "fp8.h"
+#include "norm_quotient.h"
 #include "tf_common.h"
 
 namespace tf {
 namespace {
 
-constexpr float kFp8Max = 448.0f;
 typedef unsigned short us2 __attribute__((ext_vector_type(2)));
 
 // fp16(fp32(a * b)): reference.py:39 rounds x * rstd to fp32 and then to fp16. Left alone,
@@ -62,7 +44,6 @@ __device__ __forceinline__ _Float16 mul_round_f32_then_f16(float a, float b) {
   __asm__ volatile("" : "+v"(p));
   return (_Float16)p;
 }
-constexpr float kMinScale = 1.0f / (448.0f * 512.0f);  // reference.py:10
 
 // Lane exchanges inside a row of 16 lanes (DPP, no LDS): swap neighbours, swap pairs, mirror
 // each half row, mirror the row. Applied in that order, each pairs every lane with one holding
@@ -127,37 +108,6 @@ __device__ __forceinline__ uint32_t block_max_u32(uint32_t v, uint32_t* red) {
 #pragma unroll
   for (int i = 1; i < WAVES; ++i) t = t > red[i] ? t : red[i];
   return t;
-}
-
-__device__ __forceinline__ float quotient(_Float16 y, double rcp) { return (float)((double)(float)y * rcp); }
-
-// fp32(y) * r for the fp16 y in the low (HI false) or high half of `pair`, as one v_fma_mix_f32
-// that reads the fp16 operand directly (the backend does not form it from a multiply). The
-// addend is -0, so the sum is the rounded product for every sign, zeros included.
-template <bool HI>
-__device__ __forceinline__ float mul_f16_f32(uint32_t pair, float r) {
-  float q;
-  if (HI)
-    __asm__("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(q) : "v"(pair), "v"(r), "v"(-0.0f));
-  else
-    __asm__("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(q) : "v"(pair), "v"(r), "v"(-0.0f));
-  return q;
-}
-
-// y / s for the fp16 y in half HI of `pair` and a dynamic scale s, given r = fp32(1 / s)
-// (Markstein's correction, see above).
-template <bool HI>
-__device__ __forceinline__ float quotient_dynamic(h2 pair, float s, float r) {
-  const float yf = (float)pair[HI ? 1 : 0];
-  const float q0 = mul_f16_f32<HI>(as_u32(pair), r);
-  const float e = __builtin_fmaf(q0, s, -yf);
-  return __builtin_fmaf(-e, r, q0);
-}
-
-// Four clamped fp32 values -> four e4m3fn codes in one word (bytes in order).
-__device__ __forceinline__ uint32_t encode4_clamped(float a, float b, float c, float d) {
-  const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, __builtin_bit_cast(int, a), false);
-  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true);
 }
 
 __device__ __forceinline__ uint32_t f16_bits_of(_Float16 v) { return __builtin_bit_cast(uint16_t, v); }
@@ -272,8 +222,7 @@ __device__ __forceinline__ void finish_row(h2 (&xv)[CPT][4], const h2 (&wv)[CPT]
   if (static_scale) {
     s = s_static;
   } else {
-    const float raw = (float)((double)amax * (1.0 / (double)kFp8Max));  // = fp32(amax / 448)
-    s = (raw < kMinScale) ? kMinScale : raw;  // clamp(min=...) keeps NaN
+    s = dynamic_scale(amax);
     if (tid == 0) scale[row] = s;
   }
   const bool fast = __builtin_isfinite(amax) && __builtin_isfinite(s) && s > 0.0f;
