@@ -72,8 +72,10 @@ Extra objects on the same JSON line:
   h // 7) -> o_proj -> residual add -> RMSNorm + FP8 -> fp16(q * scale) -> gate_up -> SiLU(gate)
   * up -> down -> residual add. The linears and the norms are this library's kernels, the
   rest is torch glue ("unfused"), or the residual adds and SiLU*mul run as the linears'
-  fused epilogues and the norms write fp16(q * scale) themselves ("fused", same bits;
-  ``tokens_per_s`` is this one), or in addition qkv and
+  fused epilogues and each norm with fp16(q * scale) runs inside the linear that reads it
+  (rmsnorm_fp8_w4a16_linear: the decode GEMV's prologue at M <= 4, the norm kernel writing
+  fp16(q * scale) itself above) ("fused", same bits; ``tokens_per_s`` is this one), or in
+  addition qkv and
   gate_up take the FP8 codes and scales directly as W4A8 linears ("w4a8", no fp16(q * scale)
   glue; not bit-equal: the scale multiplies each row's sum instead of each element; from M = 128
   these run on the fp8-MFMA GEMM, which also applies the group scale exactly). A pass
@@ -623,9 +625,8 @@ def stack_bench(dev: torch.device, gpu: str, ms: tuple[int, ...], tune: bool) ->
     def layer_pass(x: torch.Tensor, layer: tuple) -> torch.Tensor:  # type: ignore[type-arg]
         (qkv, o, gu, down), bias, g1, g2 = layer
         m = x.shape[0]
-        if mode == "fused":  # the norm also writes fp16(q * scale), the qkv input
-            _, _, a = ops.rmsnorm_fp8_quant_dequant(x, g1, eps, None)
-            y = ops.w4a16_linear(a, *qkv, bias, GROUP, "hip")
+        if mode == "fused":  # norm, fp16(q * scale) and qkv: one kernel at M <= 4, else two
+            y = ops.rmsnorm_fp8_w4a16_linear(x, g1, eps, *qkv, bias, GROUP, "hip", "none")
         else:
             q8, s = ops.rmsnorm_fp8_quant(x, g1, eps, None)
             if mode == "w4a8":
@@ -640,8 +641,7 @@ def stack_bench(dev: torch.device, gpu: str, ms: tuple[int, ...], tune: bool) ->
         else:
             x = ops.w4a16_linear_residual(attn, *o, None, x, GROUP, "hip")
         if mode == "fused":
-            _, _, a = ops.rmsnorm_fp8_quant_dequant(x, g2, eps, None)
-            act = ops.w4a16_linear_silu_mul(a, *gu, None, GROUP, "hip")
+            act = ops.rmsnorm_fp8_w4a16_linear(x, g2, eps, *gu, None, GROUP, "hip", "silu_mul")
             return ops.w4a16_linear_residual(act, *down, None, x, GROUP, "hip")
         q8, s = ops.rmsnorm_fp8_quant(x, g2, eps, None)
         if mode == "w4a8":

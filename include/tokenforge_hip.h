@@ -247,6 +247,20 @@ int tf_rmsnorm_fp8_quant_ex(const uint16_t* x, int64_t ldx, const uint16_t* weig
                             int64_t lddq, int64_t t, int64_t h, float eps, int32_t form,
                             void* stream);
 
+/* tf_rmsnorm_fp8_quant_dq (dynamic scale) followed by tf_w4a16_linear_ex on its dq output, in
+ * one decode launch: out = linear(dq(rmsnorm_fp8_quant(x, norm_weight, eps))), bit for bit the
+ * two calls. No counterpart in the reference, which runs rmsnorm_fp8_quant (rmsnorm_fp8.py:76)
+ * and the linear (ops.py:48) as separate kernels; for decode callers (M <= 4) that would
+ * otherwise launch the norm on its own. Only the gemv stream form runs it (cfg gemv_mfma with
+ * block_k 512; M <= 4); epilogue NONE or SILU_MUL; the codes and scales are not written.
+ * x fp16 [m, k] (row stride ldx), norm_weight fp16 [k] (16-byte aligned); the linear's other
+ * arguments as tf_w4a16_linear_ex (no workspace). */
+int tf_rmsnorm_fp8_w4a16_linear(const uint16_t* x, int64_t ldx, const uint16_t* norm_weight, float eps,
+                                const int32_t* qweight_t, const uint16_t* scales, const int32_t* qzeros,
+                                const uint16_t* bias, uint16_t* out, int64_t ldo, int64_t m, int64_t n,
+                                int64_t k, int32_t group_size, const tf_gemm_config* cfg,
+                                int32_t epilogue, void* stream);
+
 /* Test hook for the e4m3fn encoding used by tf_rmsnorm_fp8_quant
  * (rmsnorm_fp8.py:29-41 _round_to_e4m3_grid + cast): fp32 [count] -> uint8 [count], through
  * the same hardware conversion (v_cvt_pk_fp8_f32) and NaN handling as that kernel.

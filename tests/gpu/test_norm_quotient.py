@@ -1,4 +1,4 @@
-"""The RMSNorm+FP8 kernel's exact-division forms (tokenforge_amd/csrc/norm_quotient.h).
+"""The RMSNorm+FP8 kernel's exact-division forms (tokenforge_amd/csrc/norm_row.h).
 
 GPU: the dynamic-scale quotient, y / s by Markstein's correction in fp32 followed by the
 v_med3 clamp and the packed e4m3 conversion, gives the codes of the IEEE fp32 division

@@ -1,4 +1,4 @@
-"""The RMSNorm+FP8 kernel's per-row divisions (tokenforge_amd/csrc/norm_quotient.h): amax / 448
+"""The RMSNorm+FP8 kernel's per-row divisions (tokenforge_amd/csrc/norm_row.h): amax / 448
 and the mean sum / h are computed as fp32(fp64(value) * fp64(1 / divisor)). Both equal the IEEE
 fp32 quotients: every positive finite fp16 amax, and sampled fp32 sums (exact multiples of h,
 and values across fp16's squared range) with every row width h up to 32768. The dynamic-scale

@@ -99,6 +99,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "tf_rmsnorm_fp8_quant_dq": (ctypes.c_int, [_p, _i64, _p, _p, _i64, _p, _i32, _p, _i64, _i64, _i64, _f32, _p]),
     "tf_rmsnorm_fp8_quant_ex": (
         ctypes.c_int, [_p, _i64, _p, _p, _i64, _p, _i32, _p, _i64, _i64, _i64, _f32, _i32, _p]),
+    "tf_rmsnorm_fp8_w4a16_linear": (
+        ctypes.c_int,
+        [_p, _i64, _p, _f32, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i32,
+         ctypes.POINTER(TfGemmConfig), _i32, _p]),
     "tf_e4m3_encode": (ctypes.c_int, [_p, _p, _i64, _p]),
 }
 

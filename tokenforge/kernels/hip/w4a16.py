@@ -262,3 +262,59 @@ def w4a8_gemm_ex(
         )
     _lib.check(rc, "tf_w4a8_linear_ex")
     return out
+
+
+def rmsnorm_fp8_w4a16_gemm_ex(
+    x: torch.Tensor,
+    norm_weight: torch.Tensor,
+    eps: float,
+    qweight_t: torch.Tensor,
+    scales: torch.Tensor,
+    qzeros: torch.Tensor,
+    group_size: int,
+    config: GemmConfig,
+    bias: torch.Tensor | None = None,
+    epilogue: str = "none",
+) -> torch.Tensor:
+    """``w4a16_gemm_ex(a, ...)`` with ``a`` the fp16 activation of ``rmsnorm_fp8_quant_dequant(x,
+    norm_weight, eps)`` (dynamic scale), in one decode launch (``tf_rmsnorm_fp8_w4a16_linear``;
+    no counterpart in the reference, which runs the norm and the linear as separate kernels).
+    Same bits as the two calls. ``config`` must be the gemv stream form (``config.stream``, M
+    <= 4); epilogue ``"none"`` or ``"silu_mul"``."""
+    m, n, k = _check_inputs(x, qweight_t, scales, qzeros, group_size)
+    config.validate(group_size)
+    if not config.stream:
+        raise ValueError(f"the RMSNorm prologue runs in the gemv stream form (M <= 4), got config {config}")
+    if epilogue not in ("none", "silu_mul"):
+        raise ValueError(f"epilogue must be 'none' or 'silu_mul', got {epilogue!r}")
+    if tuple(norm_weight.shape) != (k,):
+        raise ValueError(f"norm weight shape {tuple(norm_weight.shape)} != {(k,)}")
+    if norm_weight.dtype != torch.float16:
+        raise TypeError(f"norm weight must be fp16, got {norm_weight.dtype}")
+    if bias is not None:
+        if tuple(bias.shape) != (n,):
+            raise ValueError(f"bias shape {tuple(bias.shape)} != {(n,)}")
+        if bias.dtype != torch.float16:
+            raise TypeError(f"bias must be fp16, got {bias.dtype}")
+        bias = bias.contiguous()
+    if epilogue == "silu_mul" and n % 16:
+        raise ValueError(f"the silu_mul epilogue needs N to be a multiple of 16, got {n}")
+    tensors = (x, norm_weight, qweight_t, scales, qzeros) + (() if bias is None else (bias,))
+    dev = require_gpu("rmsnorm_fp8_w4a16_gemm", *tensors)
+    n_out = n // 2 if epilogue == "silu_mul" else n
+    out = torch.empty((m, n_out), dtype=torch.float16, device=dev)
+    if m == 0 or n == 0:
+        return out
+    x = _aligned_rows(x)
+    if norm_weight.stride(0) != 1 or norm_weight.data_ptr() % 16:
+        norm_weight = norm_weight.clone(memory_format=torch.contiguous_format)
+    ldx = x.stride(0) if m > 1 else k
+    c = to_c_config(config)
+    with on_device(dev):
+        rc = _lib.lib().tf_rmsnorm_fp8_w4a16_linear(
+            x.data_ptr(), ldx, norm_weight.data_ptr(), float(eps), qweight_t.data_ptr(), scales.data_ptr(),
+            qzeros.data_ptr(), ptr(bias), out.data_ptr(), n_out, m, n, k, group_size, ctypes.byref(c),
+            EPILOGUES[epilogue], stream_of(dev),
+        )
+    _lib.check(rc, "tf_rmsnorm_fp8_w4a16_linear")
+    return out

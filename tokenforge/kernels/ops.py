@@ -29,6 +29,13 @@ and the norm with the fp16 activation a W4A16 linear reads from its codes (no co
 * ``tokenforge::rmsnorm_fp8_quant_dequant(x, weight, eps, scale)`` = ``(q, scale, a)`` with
   ``(q, scale) = rmsnorm_fp8_quant(...)`` and ``a = (q.to(float32) * scale).to(float16)``
 
+and the decode norm-then-linear in one launch (no counterpart either):
+
+* ``tokenforge::rmsnorm_fp8_w4a16_linear(x, norm_weight, eps, qweight_t, scales, qzeros, bias,
+  group_size, backend, epilogue)`` = ``w4a16_linear(a, ...)`` (or its SiLU*mul form) with ``a``
+  from ``rmsnorm_fp8_quant_dequant(x, norm_weight, eps, None)``; one kernel where the bucket's
+  config is the GEMV stream form (M <= 4), the two kernels otherwise; same bits either way.
+
 All
 run hand-written HIP kernels; a CPU tensor or a missing kernel library raises instead of
 falling back.
@@ -323,3 +330,63 @@ def _rmsnorm_fp8_quant_dequant_fake(
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     q, s = _rmsnorm_fp8_quant_fake(x, weight, eps, scale)
     return q, s, x.new_empty(x.shape, dtype=torch.float16)
+
+
+@torch.library.custom_op("tokenforge::rmsnorm_fp8_w4a16_linear", mutates_args=())
+def rmsnorm_fp8_w4a16_linear(
+    x: torch.Tensor,
+    norm_weight: torch.Tensor,
+    eps: float,
+    qweight_t: torch.Tensor,
+    scales: torch.Tensor,
+    qzeros: torch.Tensor,
+    bias: torch.Tensor | None,
+    group_size: int,
+    backend: str,
+    epilogue: str,
+) -> torch.Tensor:
+    """The linear (epilogue ``"none"`` or ``"silu_mul"``) on the fp16 activation of
+    ``rmsnorm_fp8_quant_dequant(x, norm_weight, eps, None)`` (no counterpart in the reference):
+    the GEMV stream form normalizes and quantizes x in its prologue (one launch, M <= 4); other
+    configs run the norm kernel, then the linear. Bit for bit the two ops."""
+    if epilogue not in ("none", "silu_mul"):
+        raise ValueError(f"epilogue must be 'none' or 'silu_mul', got {epilogue!r}")
+    k = x.shape[-1]
+    n = qweight_t.shape[0]
+    out_shape = (*x.shape[:-1], n // 2 if epilogue == "silu_mul" else n)
+    x2 = x.reshape(-1, k)
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    m = x2.shape[0]
+    if m == 0:
+        return x.new_empty(out_shape)
+    if backend not in dispatch.HIP_BACKENDS:
+        raise ValueError(
+            f"backend must be 'hip' (or its aliases 'triton', 'cuda') at op level, got {backend!r}"
+        )
+    cfg = _decide(x2, m, n, k, group_size, backend)
+    if cfg.stream:
+        y = _w4a16.rmsnorm_fp8_w4a16_gemm_ex(
+            x2, norm_weight, eps, qweight_t, scales, qzeros, group_size, cfg, bias, epilogue
+        )
+    else:
+        _, _, a = _rms.rmsnorm_fp8_quant_dequant(x2, norm_weight, eps, None)
+        y = _w4a16.w4a16_gemm_ex(a, qweight_t, scales, qzeros, group_size, cfg, bias, epilogue)
+    return y.reshape(out_shape)
+
+
+@rmsnorm_fp8_w4a16_linear.register_fake
+def _rmsnorm_fp8_w4a16_linear_fake(
+    x: torch.Tensor,
+    norm_weight: torch.Tensor,
+    eps: float,
+    qweight_t: torch.Tensor,
+    scales: torch.Tensor,
+    qzeros: torch.Tensor,
+    bias: torch.Tensor | None,
+    group_size: int,
+    backend: str,
+    epilogue: str,
+) -> torch.Tensor:
+    n = qweight_t.shape[0]
+    return x.new_empty((*x.shape[:-1], n // 2 if epilogue == "silu_mul" else n))

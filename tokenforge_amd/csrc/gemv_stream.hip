@@ -24,7 +24,15 @@
 // c >= 8 the up rows N/2 + 8v + c - 8, i.e. half (v % 2) of physical tile v / 2 and of tile
 // N/32 + v / 2 (N % 32 == 0). The lane part of every address is then a per-lane constant and
 // the step part a wave-uniform scalar, as without the epilogue.
+//
+// RMSNorm prologue (NORM, tf_rmsnorm_fp8_w4a16_linear): x holds the rows before an RMSNorm +
+// e4m3 quantization. Once x is staged, every workgroup turns each row in LDS into fp16(code *
+// scale), the activation rmsnorm_fp8_quant_dq writes, with the norm kernel's arithmetic
+// (norm_row.h); the weight ring is already in flight meanwhile. For M <= 4 rows this costs
+// each workgroup a few hundred instructions per thread and removes the norm's own launch and
+// its round trip through HBM.
 #include "linear.h"
+#include "norm_row.h"
 
 #include <algorithm>
 
@@ -34,6 +42,7 @@ namespace {
 constexpr int kStreamMaxM = 4;                 // D rows 0..3 live in lanes 0..15
 constexpr int kStreamMaxXBytes = 96 * 1024;    // staged x: M rows of K + 8 halfs
 constexpr int kStreamInflightKB = 32;          // weight bytes in flight per CU (KB)
+constexpr int kNormScratchBytes = 1024;        // prologue reductions: [16][4] doubles and words
 
 __host__ __device__ __forceinline__ int stream_xstride(int k) { return k + 8; }
 
@@ -52,7 +61,170 @@ struct StreamGeo {
   }
 };
 
-template <int P, int MAXW, bool SILU, bool X8>
+// The RMSNorm + e4m3 prologue over the m rows of x staged in LDS (row r at xs + r * xstride),
+// in place: each row becomes fp16(code * scale) as rmsnorm_fp8.hip computes it for the row
+// (reference.py:35-50; dynamic scale): fp64 sum of squares, var = fp32(sum * (1 / k)), rstd =
+// 1 / sqrt(var + eps), y = fp16(fp32(x * rstd)) * w in fp16, absmax, scale, codes, then the
+// codes times the scale. Thread t takes the 8-element chunks t, t + T, ...; the workgroup's W
+// waves meet in red_d / red_u (W entries each), in wave order.
+__device__ __forceinline__ void norm_rows(const LinearArgs& a, _Float16* xs, int xstride, double* red_d,
+                                          uint32_t* red_u, int W, int wave, int lane) {
+  const int T = W * 64;
+  const int chunks = a.k >> 3;
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.norm_w, (uint32_t)a.k * 2u);
+  for (int r = 0; r < a.m; ++r) {
+    u4* row = reinterpret_cast<u4*>(xs + r * xstride);
+    double ss0 = 0.0, ss1 = 0.0;  // two chains: fp64 adds are long-latency
+    for (int q = threadIdx.x; q < chunks; q += T) {
+      const u4 v = row[q];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const h2 p = as_h2(v[j]);
+        const double d0 = (double)(float)p[0], d1 = (double)(float)p[1];
+        ss0 += d0 * d0;
+        ss1 += d1 * d1;
+      }
+    }
+    const double wsum = wave_sum_f64(ss0 + ss1);
+    if (lane == 0) red_d[wave] = wsum;
+    __syncthreads();
+    double total = red_d[0];
+    for (int w = 1; w < W; ++w) total += red_d[w];
+    const float var = (float)((double)(float)total * a.norm_inv_k);
+    const float rstd = 1.0f / __builtin_sqrtf(var + a.norm_eps);
+
+    uint32_t am = 0;
+    for (int q = threadIdx.x; q < chunks; q += T) {
+      u4 v = row[q];
+      const u4 gw = load_b128(rw, (uint32_t)q * 16u);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const h2 x = as_h2(v[j]);
+        h2 nrm;
+        nrm[0] = mul_round_f32_then_f16((float)x[0], rstd);
+        nrm[1] = mul_round_f32_then_f16((float)x[1], rstd);
+        v[j] = as_u32(nrm * as_h2(gw[j]));
+        const uint32_t yb = v[j] & 0x7FFF7FFFu;
+        am = __builtin_elementwise_max(am, __builtin_elementwise_max(yb & 0xFFFFu, yb >> 16));
+      }
+      row[q] = v;
+    }
+    const uint32_t wmax = wave_max_u32(am);
+    if (lane == 0) red_u[wave] = wmax;
+    __syncthreads();
+    uint32_t m_bits = red_u[0];
+    for (int w = 1; w < W; ++w) m_bits = __builtin_elementwise_max(m_bits, red_u[w]);
+    const float amax = (float)__builtin_bit_cast(_Float16, (uint16_t)m_bits);
+    const float s = dynamic_scale(amax);
+    const bool fast = __builtin_isfinite(amax) && __builtin_isfinite(s) && s > 0.0f;
+    const float r32 = fast ? 1.0f / s : 0.0f;
+    const double rcp = fast ? 0.0 : 1.0 / (double)s;
+
+    for (int q = threadIdx.x; q < chunks; q += T) {
+      const u4 v = row[q];
+      uint32_t lo, hi;
+      if (fast) {
+        float e[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          e[2 * j] = __builtin_amdgcn_fmed3f(quotient_dynamic<false>(as_h2(v[j]), s, r32), -kFp8Max, kFp8Max);
+          e[2 * j + 1] = __builtin_amdgcn_fmed3f(quotient_dynamic<true>(as_h2(v[j]), s, r32), -kFp8Max, kFp8Max);
+        }
+        lo = encode4_clamped(e[0], e[1], e[2], e[3]);
+        hi = encode4_clamped(e[4], e[5], e[6], e[7]);
+      } else {
+        lo = hi = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const uint32_t code = encode_slow(as_h2(v[j >> 1])[j & 1], rcp);
+          if (j < 4) lo |= code << (8 * j);
+          else hi |= code << (8 * (j - 4));
+        }
+      }
+      const u2 d0 = dequant_codes4(lo, s), d1 = dequant_codes4(hi, s);
+      row[q] = u4{d0[0], d0[1], d1[0], d1[1]};
+    }
+  }
+}
+
+// The same prologue when every thread holds at most one 8-element chunk of x (M * K <= 8 T, the
+// decode case): the thread's chunk x1 (row r, chunk q; ok false past the end) and its weight
+// chunk g1 are already in registers, so the arithmetic runs there and only the M row totals
+// and maxima meet in LDS (red_d / red_u: [W][4], one barrier each). x1 becomes the fp16(code *
+// scale) chunk.
+__device__ __forceinline__ void norm_chunk(const LinearArgs& a, u4& x1, const u4 g1, int r, bool ok, double* red_d,
+                                           uint32_t* red_u, int W, int wave, int lane) {
+  double ss0 = 0.0, ss1 = 0.0;
+  if (ok) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const h2 p = as_h2(x1[j]);
+      const double d0 = (double)(float)p[0], d1 = (double)(float)p[1];
+      ss0 += d0 * d0;
+      ss1 += d1 * d1;
+    }
+  }
+  const double ss = ss0 + ss1;
+  for (int rr = 0; rr < a.m; ++rr) {
+    const double wsum = wave_sum_f64(r == rr ? ss : 0.0);
+    if (lane == 0) red_d[wave * 4 + rr] = wsum;
+  }
+  __syncthreads();
+  const int rs = ok ? r : 0;  // threads past the end follow row 0 (their results are not stored)
+  double total = red_d[rs];
+  for (int w = 1; w < W; ++w) total += red_d[w * 4 + rs];
+  const float var = (float)((double)(float)total * a.norm_inv_k);
+  const float rstd = 1.0f / __builtin_sqrtf(var + a.norm_eps);
+
+  uint32_t am = 0;
+  u4 y;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const h2 x = as_h2(x1[j]);
+    h2 nrm;
+    nrm[0] = mul_round_f32_then_f16((float)x[0], rstd);
+    nrm[1] = mul_round_f32_then_f16((float)x[1], rstd);
+    y[j] = as_u32(nrm * as_h2(g1[j]));
+    const uint32_t yb = y[j] & 0x7FFF7FFFu;
+    am = __builtin_elementwise_max(am, __builtin_elementwise_max(yb & 0xFFFFu, yb >> 16));
+  }
+  if (!ok) am = 0;
+  for (int rr = 0; rr < a.m; ++rr) {
+    const uint32_t wmax = wave_max_u32(r == rr ? am : 0u);
+    if (lane == 0) red_u[wave * 4 + rr] = wmax;
+  }
+  __syncthreads();
+  uint32_t m_bits = red_u[rs];
+  for (int w = 1; w < W; ++w) m_bits = __builtin_elementwise_max(m_bits, red_u[w * 4 + rs]);
+  const float amax = (float)__builtin_bit_cast(_Float16, (uint16_t)m_bits);
+  const float s = dynamic_scale(amax);
+  const bool fast = __builtin_isfinite(amax) && __builtin_isfinite(s) && s > 0.0f;
+  uint32_t lo, hi;
+  if (fast) {
+    const float r32 = 1.0f / s;
+    float e[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      e[2 * j] = __builtin_amdgcn_fmed3f(quotient_dynamic<false>(as_h2(y[j]), s, r32), -kFp8Max, kFp8Max);
+      e[2 * j + 1] = __builtin_amdgcn_fmed3f(quotient_dynamic<true>(as_h2(y[j]), s, r32), -kFp8Max, kFp8Max);
+    }
+    lo = encode4_clamped(e[0], e[1], e[2], e[3]);
+    hi = encode4_clamped(e[4], e[5], e[6], e[7]);
+  } else {
+    const double rcp = 1.0 / (double)s;
+    lo = hi = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t code = encode_slow(as_h2(y[j >> 1])[j & 1], rcp);
+      if (j < 4) lo |= code << (8 * j);
+      else hi |= code << (8 * (j - 4));
+    }
+  }
+  const u2 d0 = dequant_codes4(lo, s), d1 = dequant_codes4(hi, s);
+  x1 = u4{d0[0], d0[1], d1[0], d1[1]};
+}
+
+template <int P, int MAXW, bool SILU, bool X8, bool NORM>
 __global__ __launch_bounds__(MAXW * 64) void gemv_stream_kernel(LinearArgs a, int nwg, int tpw) {
   extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
   // Every argument the kernel reads, in SGPRs from the first instruction on: otherwise the
@@ -60,7 +232,8 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_stream_kernel(LinearArgs a, in
   // round trip on the critical path of a short kernel.
   __asm__ volatile("" ::"s"(a.x), "s"(a.x8), "s"(a.ldx), "s"(a.ldx8), "s"(a.qw), "s"(a.scales), "s"(a.qz),
                    "s"(a.bias), "s"(a.out), "s"(a.ldo), "s"(a.residual), "s"(a.ldr), "s"(a.xscale),
-                   "s"(a.xscale_stride), "s"(a.m), "s"(a.n), "s"(a.k), "s"(a.log2g), "s"(a.epilogue));
+                   "s"(a.xscale_stride), "s"(a.m), "s"(a.n), "s"(a.k), "s"(a.log2g), "s"(a.epilogue), "s"(a.norm_w),
+                   "s"(a.norm_eps), "s"(a.norm_inv_k));
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int W = blockDim.x >> 6;
@@ -154,6 +327,7 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_stream_kernel(LinearArgs a, in
   // One chunk per thread when x is short (M = 1 up to K = 8 T): a single load, no batch.
   const bool one = total <= T;
   u4 x1 = {0u, 0u, 0u, 0u};
+  u4 g1 = {0u, 0u, 0u, 0u};  // the norm weight of the thread's chunk (NORM)
   if (one) {
     const int e = threadIdx.x;
     const int r = row_of(e), q = e - r * chunks;
@@ -164,6 +338,7 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_stream_kernel(LinearArgs a, in
     } else {
       x1 = load_b128(rx, ok ? (uint32_t)(((int64_t)r * a.ldx + q * 8) * 2) : kOutOfRange);
     }
+    if (NORM) g1 = load_b128(make_rsrc(a.norm_w, (uint32_t)a.k * 2u), ok ? (uint32_t)q * 16u : kOutOfRange);
   } else {
     load_x(threadIdx.x);
   }
@@ -195,9 +370,12 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_stream_kernel(LinearArgs a, in
     issue(p);
     __builtin_amdgcn_sched_barrier(0);  // slot 0 is the oldest load of the ring
   }
+  double* red_d = reinterpret_cast<double*>(part + W * tpw * 16);  // NORM scratch, [W][4]
+  uint32_t* red_u = reinterpret_cast<uint32_t*>(red_d + 64);
   if (one) {
     const int e = threadIdx.x;
     const int r = row_of(e), q = e - r * chunks;
+    if (NORM) norm_chunk(a, x1, g1, r, e < total, red_d, red_u, W, wave, lane);
     if (e < total) *reinterpret_cast<u4*>(xs + r * xstride + q * 8) = X8 ? e4m3x8_to_f16(u2{x1[0], x1[1]}) : x1;
   } else {
     store_x(threadIdx.x);
@@ -205,6 +383,10 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_stream_kernel(LinearArgs a, in
       load_x(e0);
       store_x(e0);
     }
+  }
+  if (NORM && !one) {
+    __syncthreads();  // every row of x is in LDS
+    norm_rows(a, xs, xstride, red_d, red_u, W, wave, lane);
   }
   for (int e = threadIdx.x; e < W * tpw * 16; e += T) part[e] = f4{0.0f, 0.0f, 0.0f, 0.0f};
   __syncthreads();
@@ -311,7 +493,8 @@ template <typename Kernel>
 StreamPlan plan_stream(Kernel kernel, const LinearArgs& a, int waves, int depth) {
   StreamPlan p;
   const int tiles = a.n >> 4;
-  const size_t xbytes = (size_t)a.m * stream_xstride(a.k) * 2;
+  // The staged x, plus the prologue's reduction scratch behind the partials when it has one.
+  const size_t xbytes = (size_t)a.m * stream_xstride(a.k) * 2 + (a.norm_w ? kNormScratchBytes : 0);
   const size_t cap = device_max_lds();
   if (xbytes > (size_t)kStreamMaxXBytes || xbytes + (size_t)waves * 256 > cap) return p;
   const int per_wave = 256;  // bytes of partials per (wave, tile)
@@ -354,15 +537,15 @@ template <int P, int MAXW>
 int check_stream(const LinearArgs& a, const tf_gemm_config& cfg) {
   if (int rc = check_stream_shape(a, cfg.num_warps)) return rc;
   // Every instantiation has the same launch plan (one of them stands for all).
-  const StreamPlan plan = plan_stream(gemv_stream_kernel<P, MAXW, false, false>, a, cfg.num_warps, P);
+  const StreamPlan plan = plan_stream(gemv_stream_kernel<P, MAXW, false, false, false>, a, cfg.num_warps, P);
   if (plan.nwg == 0)
     return fail(TF_EINVAL, "tf_w4a16_linear: gemv stream variant does not fit the device's LDS");
   return TF_OK;
 }
 
-template <int P, int MAXW, bool SILU, bool X8>
+template <int P, int MAXW, bool SILU, bool X8, bool NORM>
 int launch_stream_k(const LinearArgs& a, int waves, hipStream_t stream) {
-  auto kernel = gemv_stream_kernel<P, MAXW, SILU, X8>;
+  auto kernel = gemv_stream_kernel<P, MAXW, SILU, X8, NORM>;
   const StreamPlan plan = plan_stream(kernel, a, waves, P);
   if (plan.nwg == 0) return fail(TF_EINVAL, "tf_w4a16_linear: gemv stream variant does not fit the device's LDS");
   if (int rc = reserve_lds(kernel, plan.lds, "gemv_stream")) return rc;
@@ -373,10 +556,17 @@ int launch_stream_k(const LinearArgs& a, int waves, hipStream_t stream) {
 template <int P, int MAXW>
 int launch_stream(const LinearArgs& a, const tf_gemm_config& cfg, float*, hipStream_t stream) {
   if (int rc = check_stream_shape(a, cfg.num_warps)) return rc;
-  const bool silu = a.epilogue == TF_EPILOGUE_SILU_MUL, x8 = a.x8 != nullptr;
+  const bool silu = a.epilogue == TF_EPILOGUE_SILU_MUL, x8 = a.x8 != nullptr, norm = a.norm_w != nullptr;
   const int w = cfg.num_warps;
-  if (silu) return x8 ? launch_stream_k<P, MAXW, true, true>(a, w, stream) : launch_stream_k<P, MAXW, true, false>(a, w, stream);
-  return x8 ? launch_stream_k<P, MAXW, false, true>(a, w, stream) : launch_stream_k<P, MAXW, false, false>(a, w, stream);
+  if (norm && x8) return fail(TF_EINVAL, "tf_w4a16_linear: the RMSNorm prologue takes fp16 x");
+  if (norm)
+    return silu ? launch_stream_k<P, MAXW, true, false, true>(a, w, stream)
+                : launch_stream_k<P, MAXW, false, false, true>(a, w, stream);
+  if (silu)
+    return x8 ? launch_stream_k<P, MAXW, true, true, false>(a, w, stream)
+              : launch_stream_k<P, MAXW, true, false, false>(a, w, stream);
+  return x8 ? launch_stream_k<P, MAXW, false, true, false>(a, w, stream)
+            : launch_stream_k<P, MAXW, false, false, false>(a, w, stream);
 }
 
 int64_t no_stream_workspace(const LinearArgs&, const tf_gemm_config&) { return 0; }

@@ -33,6 +33,13 @@ struct LinearArgs {
   int64_t ldx8 = 0;
   const float* xscale = nullptr;  // [m] with stride xscale_stride (0: one scale for all rows)
   int64_t xscale_stride = 0;
+  // RMSNorm + e4m3 prologue (tf_rmsnorm_fp8_w4a16_linear, decode GEMV stream form only): x holds
+  // the rows before the norm; the kernel normalizes each with weight norm_w (fp16 [k], 16-byte
+  // aligned) and norm_eps, quantizes it to e4m3 with its dynamic scale and multiplies with
+  // fp16(code * scale), the activation rmsnorm_fp8_quant_dq writes for the row.
+  const uint16_t* norm_w = nullptr;
+  float norm_eps = 0.0f;
+  double norm_inv_k = 0.0;  // fp64(1 / k)
 };
 
 // Row scale of row m (1 without a W4A8 input, and for rows past m, which are never stored).

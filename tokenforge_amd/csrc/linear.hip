@@ -269,3 +269,32 @@ extern "C" int tf_w4a8_linear_ex(const uint8_t* x8, int64_t ldx8, const float* x
   }
   return v->launch(a, *cfg, ws, (hipStream_t)stream);
 }
+
+extern "C" int tf_rmsnorm_fp8_w4a16_linear(const uint16_t* x, int64_t ldx, const uint16_t* norm_weight, float eps,
+                                           const int32_t* qweight_t, const uint16_t* scales, const int32_t* qzeros,
+                                           const uint16_t* bias, uint16_t* out, int64_t ldo, int64_t m, int64_t n,
+                                           int64_t k, int32_t group_size, const tf_gemm_config* cfg,
+                                           int32_t epilogue, void* stream) {
+  if (cfg == nullptr) return fail(TF_EINVAL, "tf_rmsnorm_fp8_w4a16_linear: null config");
+  if (cfg->kernel != TF_KERNEL_GEMV_MFMA || cfg->block_k != 512)
+    return fail(TF_EINVAL, "tf_rmsnorm_fp8_w4a16_linear: the RMSNorm prologue runs in the gemv stream form "
+                           "(gemv_mfma, block_k 512, M <= 4)");
+  if (epilogue == TF_EPILOGUE_RESIDUAL)
+    return fail(TF_EINVAL, "tf_rmsnorm_fp8_w4a16_linear: epilogue none or silu_mul");
+  LinearArgs a;
+  if (int rc = make_args(x, ldx, qweight_t, scales, qzeros, bias, out, ldo, m, n, k, group_size, epilogue, nullptr,
+                         0, &a))
+    return rc;
+  if (m > 0 && n > 0) {
+    if (norm_weight == nullptr) return fail(TF_EINVAL, "tf_rmsnorm_fp8_w4a16_linear: null norm weight");
+    if (!aligned16(norm_weight)) return fail(TF_EINVAL, "tf_rmsnorm_fp8_w4a16_linear: norm weight must be 16-byte aligned");
+  }
+  a.norm_w = norm_weight;
+  a.norm_eps = eps;
+  a.norm_inv_k = k > 0 ? 1.0 / (double)k : 0.0;
+  if (int rc = check_config(*cfg, group_size)) return rc;
+  const Variant* v = find_variant(*cfg);
+  if (v == nullptr) return fail(TF_EINVAL, "tf_rmsnorm_fp8_w4a16_linear: config does not name a compiled variant");
+  if (m == 0 || n == 0) return TF_OK;
+  return v->launch(a, *cfg, nullptr, (hipStream_t)stream);
+}

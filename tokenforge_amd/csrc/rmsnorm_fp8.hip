@@ -18,7 +18,7 @@
 // of var on some rows.
 //
 // Quotient y / scale (reference.py:47-49) and the per-row divisions: exact forms in
-// norm_quotient.h.
+// norm_row.h.
 //
 // Encoding: rows whose absmax and scale are finite (scale > 0) hold no NaN quotient, so they
 // clamp with v_med3 and encode two values per v_cvt_pk_fp8_f32. That instruction rounds to
@@ -27,7 +27,7 @@
 // (0x7F for +NaN); the remaining rows therefore clamp with NaN-preserving compares and use
 // e4m3_encode.
 #include "fp8.h"
-#include "norm_quotient.h"
+#include "norm_row.h"
 #include "tf_common.h"
 
 namespace tf {
@@ -35,49 +35,10 @@ namespace {
 
 typedef unsigned short us2 __attribute__((ext_vector_type(2)));
 
-// fp16(fp32(a * b)): reference.py:39 rounds x * rstd to fp32 and then to fp16. Left alone,
-// the backend folds the multiply and the conversion into v_fma_mixlo_f16, which rounds once,
-// straight to fp16, and differs from the double rounding on ~6e-5 of the elements. The empty
-// asm makes the fp32 product a register value, so it is rounded to fp32 first.
-__device__ __forceinline__ _Float16 mul_round_f32_then_f16(float a, float b) {
-  float p = a * b;
-  __asm__ volatile("" : "+v"(p));
-  return (_Float16)p;
-}
-
-// Lane exchanges inside a row of 16 lanes (DPP, no LDS): swap neighbours, swap pairs, mirror
-// each half row, mirror the row. Applied in that order, each pairs every lane with one holding
-// a disjoint set of the row's lanes, so four steps leave the row's total in all 16 lanes.
-constexpr int kDppQuadXor1 = 0xB1;      // quad_perm [1, 0, 3, 2]
-constexpr int kDppQuadXor2 = 0x4E;      // quad_perm [2, 3, 0, 1]
-constexpr int kDppHalfRowMirror = 0x141;
-constexpr int kDppRowMirror = 0x140;
-
-template <int CTRL>
-__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
-  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, false);
-}
-template <int CTRL>
-__device__ __forceinline__ double dpp_f64(double v) {
-  const uint64_t b = __builtin_bit_cast(uint64_t, v);
-  const uint64_t lo = dpp_u32<CTRL>((uint32_t)b), hi = dpp_u32<CTRL>((uint32_t)(b >> 32));
-  return __builtin_bit_cast(double, lo | (hi << 32));
-}
-__device__ __forceinline__ double readlane_f64(double v, int lane) {
-  const uint64_t b = __builtin_bit_cast(uint64_t, v);
-  const uint64_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, lane);
-  const uint64_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), lane);
-  return __builtin_bit_cast(double, lo | (hi << 32));
-}
-
 // Sum over the WAVES waves of the workgroup (every lane active); the result is wave-uniform.
 template <int WAVES>
 __device__ __forceinline__ double block_sum(double v, double* red) {
-  v += dpp_f64<kDppQuadXor1>(v);
-  v += dpp_f64<kDppQuadXor2>(v);
-  v += dpp_f64<kDppHalfRowMirror>(v);
-  v += dpp_f64<kDppRowMirror>(v);
-  v = (readlane_f64(v, 0) + readlane_f64(v, 16)) + (readlane_f64(v, 32) + readlane_f64(v, 48));
+  v = wave_sum_f64(v);
   if (WAVES == 1) return v;  // the row is one wave's: no LDS, no barrier
   const int wave = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) red[wave] = v;
@@ -93,13 +54,7 @@ __device__ __forceinline__ double block_sum(double v, double* red) {
 // propagation of torch's amax). The result is wave-uniform.
 template <int WAVES>
 __device__ __forceinline__ uint32_t block_max_u32(uint32_t v, uint32_t* red) {
-  v = __builtin_elementwise_max(v, dpp_u32<kDppQuadXor1>(v));
-  v = __builtin_elementwise_max(v, dpp_u32<kDppQuadXor2>(v));
-  v = __builtin_elementwise_max(v, dpp_u32<kDppHalfRowMirror>(v));
-  v = __builtin_elementwise_max(v, dpp_u32<kDppRowMirror>(v));
-  const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
-  const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
-  v = __builtin_elementwise_max(__builtin_elementwise_max(a, b), __builtin_elementwise_max(c, d));
+  v = wave_max_u32(v);
   if (WAVES == 1) return v;
   const int wave = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) red[wave] = v;
@@ -108,21 +63,6 @@ __device__ __forceinline__ uint32_t block_max_u32(uint32_t v, uint32_t* red) {
 #pragma unroll
   for (int i = 1; i < WAVES; ++i) t = t > red[i] ? t : red[i];
   return t;
-}
-
-__device__ __forceinline__ uint32_t f16_bits_of(_Float16 v) { return __builtin_bit_cast(uint16_t, v); }
-
-// fp16(fp32(code) * s) of four codes (one word): the activation a W4A16 linear reads when it is
-// fed from the codes, as `(q.to(float32) * scale).to(float16)` computes it. Every e4m3fn code,
-// NaN included, decodes exactly; the product is rounded to fp32 and then to fp16.
-__device__ __forceinline__ u2 dequant_codes4(uint32_t codes, float s) {
-  const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)codes, false);
-  const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)codes, true);
-  const uint32_t h0 = f16_bits_of(mul_round_f32_then_f16(lo[0], s));
-  const uint32_t h1 = f16_bits_of(mul_round_f32_then_f16(lo[1], s));
-  const uint32_t h2 = f16_bits_of(mul_round_f32_then_f16(hi[0], s));
-  const uint32_t h3 = f16_bits_of(mul_round_f32_then_f16(hi[1], s));
-  return u2{h0 | (h1 << 16), h2 | (h3 << 16)};
 }
 
 // Cache policy of the 16-byte loads: x is read once, so its loads are non-temporal (nt); the
@@ -256,10 +196,7 @@ __device__ __forceinline__ void finish_row(h2 (&xv)[CPT][4], const h2 (&wv)[CPT]
       uint8_t codes[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        float v = quotient(xv[i][j >> 1][j & 1], rcp);
-        v = (v < -kFp8Max) ? -kFp8Max : v;
-        v = (v > kFp8Max) ? kFp8Max : v;
-        codes[j] = e4m3_encode(v);
+        codes[j] = encode_slow(xv[i][j >> 1][j & 1], rcp);
       }
       lo = hi = 0;
 #pragma unroll

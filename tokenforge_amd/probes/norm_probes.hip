@@ -1,4 +1,4 @@
-// Exhaustive on-device check of the RMSNorm+FP8 dynamic-scale quotient (norm_quotient.h), run
+// Exhaustive on-device check of the RMSNorm+FP8 dynamic-scale quotient (norm_row.h), run
 // by tests/gpu/test_norm_quotient.py. Built into the probes library
 // (libtokenforge_probes.so), which the product library never contains or calls.
 //
@@ -12,7 +12,7 @@
 //   uncorrected: y for which fp32(y * r) alone differs from y / s, which shows that the
 //                correction is needed and that the check sees a wrong quotient.
 #include "../csrc/fp8.h"
-#include "../csrc/norm_quotient.h"
+#include "../csrc/norm_row.h"
 
 namespace {
 
