@@ -371,8 +371,13 @@ extern "C" int tf_rmsnorm_fp8_quant_ex(const uint16_t* x, int64_t ldx, const uin
     return launch_row_per_wave(cpt, n, s);
   }
   // Up to 4 waves per row, at most a few chunks per thread: short rows stay latency-bound,
-  // and long ones keep the per-wave register footprint low enough for full occupancy.
-  const int waves = chunks >= 256 ? 4 : (chunks >= 128 ? 2 : 1);
+  // and long ones keep the per-wave register footprint low enough for full occupancy. From
+  // 2048 rows on, a row of up to 512 chunks takes 2 waves instead of 4: each wave repeats the
+  // row's scalar steps (~120 of its ~290 instructions at 4 waves), and with enough rows in
+  // flight the fewer, longer waves win (H = 3584 on MI355X: T = 4096 10.8 vs 11.6 us, T =
+  // 8192 18.0-18.5 vs 19.1 us; T = 512 5.3 vs 4.7 us the other way).
+  const bool long_batch = t >= 2048 && chunks <= 512;
+  const int waves = chunks >= 256 ? (long_batch ? 2 : 4) : (chunks >= 128 ? 2 : 1);
   const int64_t per = cdiv(chunks, waves * 64);
   const int cpt = per <= 1 ? 1 : per <= 2 ? 2 : per <= 4 ? 4 : per <= 8 ? 8 : 16;
   switch (waves) {
