@@ -9,7 +9,7 @@ weights (the dequant kernel is bit-exact with the oracle's dequantize_tf): withi
 bound c sqrt(K) eps16 max|x| max|w| plus half an fp16 ulp of the output (the result is rounded
 to fp16 once; at these weights |y| reaches ~10-100, where that rounding exceeds a bound made
 for |y| of order one) and within 1e-2 normwise; a second call gives the same bits. The M=256
-configs the benchmark has run (including down's split-K 8 with its reduce) are pinned as well.
+configs the benchmark has run (including down's split-K 8 and 9 with their reduce) are pinned as well.
 
 Config 5 (decoder layer): one layer at M in {8, 32}; every stage is checked against the fp64
 oracle on the input the stage actually received (norm codes and scales bit-exact, each linear
@@ -91,6 +91,8 @@ BENCH_M256 = [
     ("gate_up", 37888, 3584, GemmConfig("gemm_mfma", 256, 192, 64, 1, 8, 3)),
     ("down", 3584, 18944, GemmConfig("gemm_mfma", 128, 256, 64, 8, 8, 3)),
     ("down", 3584, 18944, GemmConfig("gemm_mfma", 256, 128, 64, 8, 8, 3)),
+    ("down", 3584, 18944, GemmConfig("gemm_mfma", 128, 256, 64, 9, 8, 3)),
+    ("down", 3584, 18944, GemmConfig("gemm_mfma", 256, 128, 64, 9, 8, 3)),
 ]
 
 

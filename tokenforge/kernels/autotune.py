@@ -47,7 +47,14 @@ from typing import Any, Final
 import torch
 
 from tokenforge.kernels import _lib
-from tokenforge.kernels.config import M_BUCKETS, GemmConfig, candidate_configs, default_config
+from tokenforge.kernels.config import (
+    M_BUCKETS,
+    NUM_CUS,
+    GemmConfig,
+    candidate_configs,
+    default_config,
+    fill_split_candidates,
+)
 
 log = logging.getLogger(__name__)
 
@@ -424,7 +431,9 @@ def tune_layer(
         ref = w4a16_gemm(x, qweight_t, scales, qzeros, group_size, base_cfg).float()
         tol = 1e-2 * float(ref.abs().max()) + 1e-3
         screened: list[tuple[float, GemmConfig]] = []
-        for cfg in candidates(bucket, group_size):
+        cands = candidates(bucket, group_size)
+        cands = cands + fill_split_candidates(cands, bucket, n, k, NUM_CUS)
+        for cfg in cands:
             try:
                 out = w4a16_gemm(x, qweight_t, scales, qzeros, group_size, cfg)
                 if float((out.float() - ref).abs().max()) > tol:
