@@ -89,6 +89,7 @@ def test_config4_prefill_through_dispatch_and_a_tuned_cache(layer: str, n: int, 
 
 BENCH_M256 = [
     ("gate_up", 37888, 3584, GemmConfig("gemm_mfma", 256, 192, 64, 1, 8, 3)),
+    ("gate_up", 37888, 3584, GemmConfig("gemm_mfma", 256, 192, 64, 1, 16, 3)),
     ("down", 3584, 18944, GemmConfig("gemm_mfma", 128, 256, 64, 8, 8, 3)),
     ("down", 3584, 18944, GemmConfig("gemm_mfma", 256, 128, 64, 8, 8, 3)),
     ("down", 3584, 18944, GemmConfig("gemm_mfma", 128, 256, 64, 9, 8, 3)),

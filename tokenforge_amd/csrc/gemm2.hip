@@ -1,8 +1,10 @@
 // Prefill-shaped W4A16 GEMM, pipelined form (M >= 64, group size 64 or 128).
 //
-// A workgroup of 4 or 8 waves (WM x WN) computes a BM x BN tile of y = x W^T with
+// A workgroup of 4, 8 or 16 waves (WM x WN) computes a BM x BN tile of y = x W^T with
 // v_mfma_f32_32x32x16_f16, K in blocks of 64. With 8 waves two waves share each SIMD, so one
-// wave's MFMAs overlap the other's dequantization, LDS traffic and waits. Per block:
+// wave's MFMAs overlap the other's dequantization, LDS traffic and waits; with 16 (four per
+// SIMD, 32-row wave tiles) the other waves also cover the LDS latency of the fragment reads,
+// at the cost of more of them (gate_up at M = 256: 7% faster than 8 waves). Per block:
 //   * the x tile [BM][64] fp16 streams from global memory straight into LDS (buffer loads
 //     with the LDS destination, 16 bytes per lane, no registers), S stages deep;
 //   * the packed weight tile [BN][64/8] and its scales / zero points are loaded into a
@@ -62,7 +64,7 @@ struct G2 {
   static constexpr int kBChunks = BN * kBK / 32;     // 16-byte packed chunks (32 K of a column)
   static constexpr int kBPer = (kBChunks + kThreads - 1) / kThreads;
   static constexpr int kLds = S * kAStage + 2 * kBStage;
-  static_assert(kWaves == 4 || kWaves == 8, "four or eight waves");
+  static_assert(kWaves == 4 || kWaves == 8 || kWaves == 16, "four, eight or sixteen waves");
   static_assert(TM >= 1 && TN >= 1 && BM % (32 * WM) == 0 && BN % (32 * WN) == 0, "wave tile");
   static_assert(kADma % kWaves == 0, "x stage must split evenly over the waves");
   static_assert(S == 2 || S == 3, "x stages");
@@ -70,8 +72,11 @@ struct G2 {
   // weights kb + 4 - S, then S - 2 whole iterations (x block, weights).
   static constexpr int kAfterA = 3 * kBPer + (S - 2) * (kAPerWave + 3 * kBPer);
   // 16-wide K steps whose operand fragments are in flight ahead of the MFMAs: two where the
-  // registers allow it without lowering occupancy (LDS latency is the exposed cost), else one.
-  static constexpr int kAhead = (kWaves == 8 && TM * TN <= 6) || (kWaves == 4 && TM * TN <= 8) ? 2 : 1;
+  // registers allow it without lowering occupancy (LDS latency is the exposed cost), else one;
+  // none with 16 waves, where the SIMD's other three waves cover the LDS latency and the 128
+  // registers a wave has at that occupancy hold no second step.
+  static constexpr int kAhead =
+      kWaves == 16 ? 0 : (kWaves == 8 && TM * TN <= 6) || (kWaves == 4 && TM * TN <= 8) ? 2 : 1;
 };
 
 // Block barrier at the top of an iteration: at most N vector-memory loads of this wave still
@@ -380,6 +385,8 @@ const Variant kGemm2Variants[] = {
     // eight waves (two per SIMD)
     TF_GEMM2(256, 256, 4, 2, 2), TF_GEMM2(256, 192, 4, 2, 2), TF_GEMM2(256, 192, 4, 2, 3),
     TF_GEMM2(256, 128, 4, 2, 2), TF_GEMM2(128, 256, 2, 4, 2), TF_GEMM2(256, 160, 8, 1, 2),
+    // sixteen waves (four per SIMD): 32-row wave tiles
+    TF_GEMM2(256, 192, 8, 2, 2), TF_GEMM2(256, 192, 8, 2, 3), TF_GEMM2(256, 128, 8, 2, 2),
 };
 
 }  // namespace
