@@ -15,6 +15,10 @@ Config 5 (decoder layer): one layer at M in {8, 32}; every stage is checked agai
 oracle on the input the stage actually received (norm codes and scales bit-exact, each linear
 within the bounds above, the attention stand-in exact), and the fused pass (epilogues, the
 norm's fp16 output) equals the unfused torch composition bit for bit.
+
+Configs 1 and 3 (decode) at full size against the numpy oracle itself: M in {1, 4} on all four
+linears through the op, and the fused RMSNorm+FP8 -> linear of the decode step on qkv and
+gate_up, against ``oracle/reference.py``'s fp64 product (one dequantization per shape).
 """
 
 from __future__ import annotations
@@ -156,3 +160,47 @@ def test_config5_decoder_layer_stage_by_stage(m: int, device: torch.device) -> N
     out = ops.w4a16_linear_residual(act, *down, None, h1, G, "hip")
     assert torch.equal(out, h1 + yd)
     assert bool(torch.isfinite(out).all())
+
+
+@pytest.mark.parametrize(("layer", "n", "k"), [("qkv", QKV, H), ("o", H, H), ("gate_up", 2 * INTER, H), ("down", H, INTER)])
+def test_decode_full_size_against_the_numpy_oracle(layer: str, n: int, k: int, device: torch.device) -> None:
+    """Configs 1 and 3 at full size against ``oracle/reference.py`` itself (the fp64 product of
+    the oracle's dequantized weights), M in {1, 4}: the op on the shipped config (the GEMV
+    stream form), and, where a norm feeds the linear (qkv, gate_up), the fused RMSNorm+FP8 ->
+    linear the decode step runs, against the oracle's linear on the oracle's norm output
+    (codes times scale, rounded to fp16). Bound: c sqrt(K) eps16 max|x| max|w| past half an fp16
+    ulp of the result, and 1e-2 normwise."""
+    from oracle import pack as opack
+
+    qweight, qzeros, scales = cases.baseline_layer(n, k, seed=90)
+    ow = opack.pack_awq(qweight, qzeros, scales, G)
+    w = pack_awq(*(torch.from_numpy(a).to(device) for a in (qweight, qzeros, scales)), G)
+    gen = torch.Generator(device="cpu").manual_seed(n + k)
+    ops = torch.ops.tokenforge
+    runs = []  # (what, device output, oracle input rows)
+    for m in (1, 4):
+        x = torch.randn((m, k), generator=gen).to(torch.float16)
+        y = ops.w4a16_linear(x.to(device), w.qweight_t, w.scales, w.qzeros, None, G, "hip")
+        runs.append((f"{layer} M={m}", y, x.numpy()))
+        if layer in ("qkv", "gate_up"):
+            gamma = (1 + 0.1 * torch.randn((k,), generator=gen)).to(torch.float16)
+            yf = ops.rmsnorm_fp8_w4a16_linear(x.to(device), gamma.to(device), 1e-6, w.qweight_t, w.scales,
+                                              w.qzeros, None, G, "hip", "none")
+            codes, s = oref.rmsnorm_fp8_reference(x.numpy(), gamma.numpy(), 1e-6)
+            a = (oref.e4m3_decode(codes) * s.reshape(m, 1).astype(np.float32)).astype(np.float16)
+            runs.append((f"{layer} M={m} norm+linear", yf, a))
+    rows = np.concatenate([r for _, _, r in runs])
+    ref_all = oref.w4a16_reference(rows, ow)  # one dequantization for every input
+    w_absmax = float(np.abs(opack.dequantize_tf(ow).astype(np.float32)).max())
+    tol_c = contract("cuda").c * math.sqrt(k) * EPS_FP16 * w_absmax
+    at = 0
+    for what, y, xr in runs:
+        ref = ref_all[at: at + xr.shape[0]]
+        at += xr.shape[0]
+        got = y.float().cpu().numpy().astype(np.float64)
+        half_ulp = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64) / 2
+        tol = tol_c * float(np.abs(xr.astype(np.float32)).max())
+        excess = float((np.abs(got - ref) - half_ulp).max())
+        assert excess <= tol, f"{what}: error {excess:.3e} above half an ulp exceeds the derived bound {tol:.3e}"
+        nw = relative_max_error(got, ref)
+        assert nw <= NORMWISE_MAX, f"{what}: normwise error {nw:.3e}"
