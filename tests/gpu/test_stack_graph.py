@@ -7,6 +7,9 @@ Layers at the Qwen2.5-7B shapes (qkv 4608x3584 with bias, o_proj, gate_up 37888x
 (the torch expression, or the norm's own fp16 output in the fused pass),
 attention as the identity on the value slice, SiLU(gate) * up, residual adds. Configs are
 the library defaults for each M (the GEMV, register-streamed and pipelined GEMM families).
+
+At full depth (28 layers, M in {1, 2048}), the benchmark's fused pass (each norm inside the
+op of the linear it feeds) equals the unfused pass bit for bit and replays to the same bits.
 """
 
 from __future__ import annotations
@@ -97,4 +100,47 @@ def test_stack_replay_is_bit_identical_to_eager(m: int, fused: bool, device: tor
         torch.cuda.synchronize()
         assert torch.equal(out, eager), "graph replay differs from the eager pass"
         _pass(other, layers, fused)  # eager work between replays
+        torch.cuda.synchronize()
+
+
+def _pass_norm_in_linear(x: torch.Tensor, layers: list) -> torch.Tensor:  # type: ignore[type-arg]
+    """The benchmark's fused pass: each norm inside the op of the linear it feeds
+    (``rmsnorm_fp8_w4a16_linear``: one launch at M <= 4, the norm kernel then the linear
+    above), residual adds and SiLU*mul as epilogues."""
+    ops = torch.ops.tokenforge
+    m = x.shape[0]
+    for (qkv, o, gu, down), bias, g1, g2 in layers:
+        y = ops.rmsnorm_fp8_w4a16_linear(x, g1, 1e-6, *qkv, bias, G, "hip", "none")
+        attn = y[:, QKV - 512:].reshape(m, 4, 1, 128).expand(m, 4, 7, 128).reshape(m, H)
+        x = ops.w4a16_linear_residual(attn, *o, None, x, G, "hip")
+        act = ops.rmsnorm_fp8_w4a16_linear(x, g2, 1e-6, *gu, None, G, "hip", "silu_mul")
+        x = ops.w4a16_linear_residual(act, *down, None, x, G, "hip")
+    return x
+
+
+@pytest.mark.parametrize("m", [1, 2048])
+def test_28_layer_stack_fused_equals_unfused_and_replays(m: int, device: torch.device) -> None:
+    """BASELINE config 5 at its full depth (28 layers) at the decode and prefill M: the fused
+    pass equals the unfused torch composition bit for bit, a graph of it replays to the same
+    bits (eager work between replays), and the output is finite."""
+    layers = _layers(device, 28)
+    gen = torch.Generator(device=device).manual_seed(1000 + m)
+    x = torch.randn((m, H), generator=gen, device=device).to(torch.float16)
+    ref = _pass(x, layers)
+    assert bool(torch.isfinite(ref).all()), "non-finite output"
+    assert torch.equal(_pass_norm_in_linear(x, layers), ref), "fused pass differs from the unfused one"
+    other = torch.randn((m, H), generator=gen, device=device).to(torch.float16)
+    st = torch.cuda.Stream(device)
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        _pass_norm_in_linear(x, layers)  # warm-up on the capture stream
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=st):
+        out = _pass_norm_in_linear(x, layers)
+    for _ in range(2):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), "replay differs from eager"
+        _pass_norm_in_linear(other, layers)  # eager work between replays
         torch.cuda.synchronize()
