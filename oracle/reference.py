@@ -3,10 +3,12 @@ rounding of rmsnorm_fp8.py:29-41.
 
 Test infrastructure only (see ``oracle/__init__.py``).
 
-One deliberate, documented difference: :func:`rmsnorm` forms the sum of squares exactly
-(every x^2 of an fp16 x is exact; the fp64 sum is exact to ~2^-53) and rounds it once to
-fp32, where reference.py:37 uses torch's fp32 ``mean``, whose own summation order can land
-one ulp away. The HIP kernel sums the same exact way, so kernel and oracle agree bit for bit;
+One deliberate, documented difference: :func:`rmsnorm` forms the sum of squares in fp64 in
+one fixed order (:func:`sum_squares`: every x^2 of an fp16 x is exact, the chunk sums and a
+pairwise tree over the chunks round in fp64) and rounds it once to fp32, where reference.py:37
+uses torch's fp32 ``mean``, whose own summation order can land one ulp away. Every HIP form
+of the norm (the kernel's row per workgroup and row per wave, the decode GEMV's prologue) adds
+in this same order, so kernel and oracle agree bit for bit whatever the batch size or fusion;
 :func:`rmsnorm_torch_order` restates reference.py:37-39 with torch's own reduction for the
 comparison against the reference as written.
 """
@@ -52,13 +54,41 @@ def w4a16_fp32(x: np.ndarray, weights: W4A16Weights, bias: np.ndarray | None = N
     return y.astype(np.float16)
 
 
+def sum_squares(x: np.ndarray) -> np.ndarray:
+    """The row sums of x^2 (fp16 x, last axis) in fp64, in the norm's fixed order: elements in
+    chunks of 8 (the row zero-padded to a multiple of 8), each chunk summed as
+    ((e0 + e1) + (e2 + e3)) + ((e4 + e5) + (e6 + e7)) with e = fp64(x)^2 (exact), then the
+    chunk sums added pairwise, bottom up over the chunk index: (c0 + c1), (c2 + c3), ..., then
+    those pairs, and so on, the chunk count zero-padded to a power of two (adding zeros changes
+    no partial sum). Returns [..., 1]."""
+    x64 = np.asarray(x, dtype=np.float16).astype(np.float64)
+    h = x64.shape[-1]
+    pad = (-h) % 8
+    if pad:
+        x64 = np.concatenate([x64, np.zeros((*x64.shape[:-1], pad))], axis=-1)
+    e = (x64 * x64).reshape(*x64.shape[:-1], -1, 8)
+    pairs = e[..., 0::2] + e[..., 1::2]
+    quads = pairs[..., 0::2] + pairs[..., 1::2]
+    c = quads[..., 0] + quads[..., 1]
+    n = c.shape[-1]
+    width = 1
+    while width < n:
+        width *= 2
+    if width > n:
+        c = np.concatenate([c, np.zeros((*c.shape[:-1], width - n))], axis=-1)
+    while c.shape[-1] > 1:
+        c = c[..., 0::2] + c[..., 1::2]
+    return c
+
+
 def rmsnorm(x: np.ndarray, weight: np.ndarray, eps: float) -> np.ndarray:
     """reference.py:35-39 (HF Qwen2 RMSNorm): fp32 normalize, round to fp16, times weight in
-    fp16. The fp32 mean is the correctly rounded sum divided by H (see module docstring)."""
+    fp16. The fp32 mean is the fixed-order fp64 sum (:func:`sum_squares`) rounded to fp32,
+    divided by H (see module docstring)."""
     x16 = np.asarray(x, dtype=np.float16)
     h = x16.shape[-1]
     xf = x16.astype(np.float32)
-    ss = np.sum(np.square(x16.astype(np.float64)), axis=-1, keepdims=True)
+    ss = sum_squares(x16)
     var = ss.astype(np.float32) / np.float32(h)
     rstd = np.float32(1.0) / np.sqrt(var + np.float32(eps))
     return (xf * rstd).astype(np.float16) * np.asarray(weight, dtype=np.float16)

@@ -1,0 +1,219 @@
+"""Every configuration the product and the benchmark run, at full Qwen2.5-7B size, against the
+pinned references.
+
+* W4A16 through ``torch.ops.tokenforge.w4a16_linear`` with an empty user cache, so the config is
+  the entry shipped for this GPU (``config_source == "shipped"``): gate_up and down at every
+  prefill bucket M in {16, ..., 4096} and qkv at M = 2048 (reference
+  tests/numerics/test_w4a16.py:48-57 checks every bucket through the op the same way). Bar: the
+  derived bound ``c sqrt(K) eps16 max|x| max|w|`` past half an fp16 ulp of the output and 1e-2
+  normwise, against the fp32 product of the exactly dequantized weights (the dequant kernel is
+  bit-exact with the oracle's ``dequantize_tf``); reruns bit-identical.
+* The W4A8 fp8 GEMM at ``fp8_gemm_config(bucket, n, k)`` (the op's choice, down's K split
+  included) for gate_up and down at M in {256, 1024, 4096}, against
+  ``oracle.reference.w4a8_exact_reference`` (fp64, weights never rounded) on rows that cover
+  every M tile, with the same bounds; the op equals the explicit config bit for bit.
+* One W4A8 decoder layer at M in {8, 2048} stage by stage: the norm codes and scales bit-exact
+  against the oracle, each W4A8 linear within the bound of its own oracle (the fp16-weight
+  ``w4a8_reference`` for the GEMV family, the exact-weight one for the fp8 GEMM), each W4A16
+  linear within the W4A16 bound, the epilogues equal to their torch composition.
+"""
+
+from __future__ import annotations
+
+import functools
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import tokenforge.kernels.ops  # noqa: F401  (registers torch.ops.tokenforge)
+from oracle import pack as opack
+from oracle import reference as oref
+from tests.numerics import cases
+from tests.numerics.tolerance import EPS_FP16, NORMWISE_MAX, contract, relative_max_error
+from tokenforge.kernels import autotune, dispatch
+from tokenforge.kernels.config import GemmConfig, fp8_gemm_applies, fp8_gemm_config
+from tokenforge.kernels.device import gpu_identity
+from tokenforge.kernels.hip.w4a16 import w4a8_gemm_ex, w4a16_dequant
+from tokenforge.kernels.pack import pack_awq
+
+pytestmark = pytest.mark.gpu
+G = 128
+H, QKV, INTER = 3584, 4608, 18944
+PREFILL_M = (16, 32, 64, 128, 256, 512, 1024, 2048, 4096)
+SHAPES = {"qkv": (QKV, H), "gate_up": (2 * INTER, H), "down": (H, INTER)}
+
+
+@functools.lru_cache(maxsize=1)
+def _layer(layer: str) -> tuple:  # type: ignore[type-arg]
+    """(numpy AWQ arrays, product weights on the GPU, fp32 dequantized W^T, max|w|) of one
+    BASELINE-distributed layer (one at a time: gate_up's fp32 copy alone is 543 MB)."""
+    n, k = SHAPES[layer]
+    arrays = cases.baseline_layer(n, k, seed=7)
+    dev = torch.device("cuda")
+    w = pack_awq(*(torch.from_numpy(a).to(dev) for a in arrays), G)
+    wt32 = w4a16_dequant(w.qweight_t, w.scales, w.qzeros, G).float().t().contiguous()
+    return arrays, w, wt32, float(wt32.abs().max())
+
+
+def _x_with_outliers(m: int, k: int, seed: int) -> torch.Tensor:
+    """BASELINE configs[3] activations: N(0, 1) with ceil(1% M) rows scaled x10."""
+    gen = torch.Generator(device="cpu").manual_seed(seed)
+    x = torch.randn((m, k), generator=gen)
+    rows = torch.randperm(m, generator=gen)[: math.ceil(0.01 * m)]
+    x[rows] *= 10
+    return x.to(torch.float16)
+
+
+def _bound_check(got: np.ndarray, ref: np.ndarray, x_absmax: float, w_absmax: float, k: int, what: str) -> None:
+    """Derived bound past half an fp16 ulp of the reference, and the normwise bound."""
+    half_ulp = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64) / 2
+    tol = contract("cuda").c * math.sqrt(k) * EPS_FP16 * x_absmax * w_absmax
+    excess = float((np.abs(got - ref) - half_ulp).max())
+    assert excess <= tol, f"{what}: error {excess:.3e} above half an ulp exceeds the derived bound {tol:.3e}"
+    nw = relative_max_error(got, ref)
+    assert nw <= NORMWISE_MAX, f"{what}: normwise error {nw:.3e}"
+
+
+def _check_product(y: torch.Tensor, x: torch.Tensor, wt32: torch.Tensor, w_absmax: float, what: str,
+                   bias: torch.Tensor | None = None) -> None:
+    ref = x.float() @ wt32
+    if bias is not None:
+        ref = ref + bias.float()
+    _bound_check(y.float().cpu().numpy().astype(np.float64), ref.cpu().numpy().astype(np.float64),
+                 float(x.float().abs().max()), w_absmax, x.shape[1], what)
+
+
+W4A16_CASES = [("gate_up", m) for m in PREFILL_M] + [("down", m) for m in PREFILL_M] + [("qkv", 2048)]
+
+
+@pytest.mark.parametrize(("layer", "m"), W4A16_CASES, ids=lambda v: str(v))
+def test_w4a16_on_the_shipped_config(layer: str, m: int, device: torch.device) -> None:
+    n, k = SHAPES[layer]
+    _, w, wt32, w_absmax = _layer(layer)
+    gpu = gpu_identity(device)
+    bucket = dispatch.lookup_bucket(m)
+    assert autotune.config_source(gpu, bucket, n, k, G) == "shipped", "the shipped table has no entry"
+    cfg = autotune.lookup(gpu, bucket, n, k, G)
+    x = _x_with_outliers(m, k, seed=1000 + m).to(device)
+    y = torch.ops.tokenforge.w4a16_linear(x, w.qweight_t, w.scales, w.qzeros, None, G, "hip")
+    _check_product(y, x, wt32, w_absmax, f"{layer} M={m} {cfg}")
+    again = torch.ops.tokenforge.w4a16_linear(x, w.qweight_t, w.scales, w.qzeros, None, G, "hip")
+    assert torch.equal(y, again), f"{layer} M={m} {cfg}: reruns differ"
+
+
+def _codes(x: np.ndarray, gamma: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    q, s = oref.rmsnorm_fp8_reference(x, gamma, 1e-6)
+    return q, s.reshape(-1)
+
+
+def _sample_rows(m: int) -> np.ndarray:
+    """Rows covering every 16-row band of every M tile (two per 32 rows), the first and last."""
+    rows = set(range(0, m, 16)) | set(range(7, m, 32)) | {m - 1}
+    return np.array(sorted(rows))
+
+
+@pytest.mark.parametrize(("layer", "m"), [(la, m) for la in ("gate_up", "down") for m in (256, 1024, 4096)],
+                         ids=lambda v: str(v))
+def test_fp8_gemm_on_its_configs(layer: str, m: int, device: torch.device) -> None:
+    n, k = SHAPES[layer]
+    arrays, w, _, _ = _layer(layer)
+    bucket = dispatch.lookup_bucket(m)
+    assert fp8_gemm_applies(bucket, n, k, G)
+    cfg = fp8_gemm_config(bucket, n, k)
+    gen = torch.Generator().manual_seed(m + n)
+    x = _x_with_outliers(m, k, seed=2000 + m).numpy()
+    gamma = (1 + 0.1 * torch.randn((k,), generator=gen)).to(torch.float16).numpy()
+    codes, xs = _codes(x, gamma)
+    x8 = torch.from_numpy(codes).to(device).view(torch.float8_e4m3fn)
+    s = torch.from_numpy(xs.astype(np.float32)).to(device)
+    y = w4a8_gemm_ex(x8, s, w.qweight_t, w.scales, w.qzeros, G, cfg)
+    yop = torch.ops.tokenforge.w4a8_linear(x8, s.reshape(m, 1), w.qweight_t, w.scales, w.qzeros, None, G, "hip")
+    assert torch.equal(y, yop), f"{layer} M={m}: the op does not run {cfg}"
+    assert torch.equal(y, w4a8_gemm_ex(x8, s, w.qweight_t, w.scales, w.qzeros, G, cfg)), "reruns differ"
+    rows = _sample_rows(m)
+    ow = opack.pack_awq(*arrays, G)
+    exact = oref.w4a8_exact_reference(codes[rows], xs[rows], ow)
+    x_eff = oref.e4m3_decode(codes).astype(np.float64) * xs.reshape(-1, 1).astype(np.float64)
+    w_absmax = 15.0 * float(np.abs(ow.scales.astype(np.float64)).max())
+    got = y.float().cpu().numpy().astype(np.float64)[rows]
+    _bound_check(got, exact, float(np.abs(x_eff).max()), w_absmax, k, f"{layer} M={m} {cfg}")
+
+
+def _w4a8_reference_on_device(codes: torch.Tensor, s: torch.Tensor, wt32: torch.Tensor, exact_wt32: torch.Tensor,
+                              fp8_gemm: bool, bias: torch.Tensor | None) -> torch.Tensor:
+    """fp32 product of the decoded codes with the weights the path computes on (exact (q - z) s
+    for the fp8 GEMM, fp16 (q - z) s otherwise), times the row scale, plus the bias."""
+    xe = codes.float()  # every e4m3fn code is exact in fp32
+    ref = (xe @ (exact_wt32 if fp8_gemm else wt32)) * s.reshape(-1, 1)
+    return ref + bias.float() if bias is not None else ref
+
+
+def _exact_wt32(arrays: tuple, device: torch.device) -> torch.Tensor:  # type: ignore[type-arg]
+    """W^T with (q - z) * s unrounded (exact in fp32: a 5-bit integer times an fp16 scale)."""
+    qweight, qzeros, scales = arrays
+    q = torch.from_numpy(opack.awq_unpack(qweight)).to(device).float()  # [K, N]
+    z = torch.from_numpy(opack.awq_unpack(qzeros)).to(device).float().repeat_interleave(G, dim=0)
+    sc = torch.from_numpy(scales.astype(np.float32)).to(device).repeat_interleave(G, dim=0)
+    return (q - z) * sc
+
+
+@pytest.mark.parametrize("m", [8, 2048])
+def test_w4a8_decoder_layer_stage_by_stage(m: int, device: torch.device) -> None:
+    ops = torch.ops.tokenforge
+    dims = [(QKV, H), (H, H), (2 * INTER, H), (H, INTER)]
+    arrays = [cases.baseline_layer(n, k, seed=60 + i) for i, (n, k) in enumerate(dims)]
+    ws = [pack_awq(*(torch.from_numpy(a).to(device) for a in arr), G) for arr in arrays]
+    wt = [w4a16_dequant(w.qweight_t, w.scales, w.qzeros, G).float().t().contiguous() for w in ws]
+    wmax = [float(t.abs().max()) for t in wt]
+    gen = torch.Generator(device="cpu").manual_seed(m)
+    bias = (0.1 * torch.randn((QKV,), generator=gen)).to(torch.float16).to(device)
+    g1 = (1 + 0.1 * torch.randn((H,), generator=gen)).to(torch.float16)
+    g2 = (1 + 0.1 * torch.randn((H,), generator=gen)).to(torch.float16)
+    x = torch.randn((m, H), generator=gen).to(torch.float16).to(device)
+    qkv, o, gu, down = ((w.qweight_t, w.scales, w.qzeros) for w in ws)
+
+    def norm(t: torch.Tensor, gamma: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        q8, s = ops.rmsnorm_fp8_quant(t, gamma.to(device), 1e-6, None)
+        qo, so = oref.rmsnorm_fp8_reference(t.cpu().numpy(), gamma.numpy(), 1e-6)
+        assert np.array_equal(q8.cpu().view(torch.uint8).numpy(), qo), f"norm codes M={m}"
+        assert np.array_equal(s.cpu().numpy(), so), f"norm scales M={m}"
+        return q8, s
+
+    def w4a8_stage(i: int, q8: torch.Tensor, s: torch.Tensor, b: torch.Tensor | None, what: str) -> torch.Tensor:
+        n, k = dims[i]
+        fp8 = fp8_gemm_applies(dispatch.lookup_bucket(m), n, k, G)
+        y = ops.w4a8_linear(q8, s, *(qkv, o, gu, down)[i], b, G, "hip")
+        exact = _exact_wt32(arrays[i], device) if fp8 else wt[i]
+        ref = _w4a8_reference_on_device(q8, s, wt[i], exact, fp8, b)
+        x_eff_max = float((q8.float() * s.reshape(-1, 1)).abs().max())
+        _bound_check(y.float().cpu().numpy().astype(np.float64), ref.cpu().numpy().astype(np.float64),
+                     x_eff_max, wmax[i], k, f"{what} M={m} ({'fp8 gemm' if fp8 else 'fp16 weights'})")
+        return y
+
+    q8, s = norm(x, g1)
+    y = w4a8_stage(0, q8, s, bias, "qkv")
+    v = y[:, QKV - 512:].reshape(m, 4, 1, 128)
+    attn = v.expand(m, 4, 7, 128).reshape(m, H)
+    yo = ops.w4a16_linear(attn, *o, None, G, "hip")
+    _check_product(yo, attn, wt[1], wmax[1], f"o_proj M={m}")
+    h1 = ops.w4a16_linear_residual(attn, *o, None, x, G, "hip")
+    assert torch.equal(h1, x + yo)
+    q82, s2 = norm(h1, g2)
+    ygu = w4a8_stage(2, q82, s2, None, "gate_up")
+    act = ops.w4a8_linear(q82, s2, *gu, None, G, "hip", "silu_mul")
+    assert torch.equal(act, torch.nn.functional.silu(ygu[:, :INTER]) * ygu[:, INTER:])
+    yd = ops.w4a16_linear(act, *down, None, G, "hip")
+    _check_product(yd, act, wt[3], wmax[3], f"down M={m}")
+    out = ops.w4a16_linear_residual(act, *down, None, h1, G, "hip")
+    assert torch.equal(out, h1 + yd)
+    assert bool(torch.isfinite(out).all())
+
+
+def test_fp8_configs_cover_the_benchmarked_splits() -> None:
+    """The configs above include down's K splits over K = 18944 and gate_up's 256 x 160 tile."""
+    down = {m: fp8_gemm_config(m, H, INTER) for m in (256, 1024, 4096)}
+    assert down[256].split_k > 1 and down[1024].split_k > 1
+    assert any(fp8_gemm_config(m, 2 * INTER, H).block_n == 160 for m in (256, 1024, 4096))
+    assert all(isinstance(c, GemmConfig) for c in down.values())

@@ -49,6 +49,13 @@ def _rows(m: int, k: int, seed: int, special: str, device: torch.device) -> torc
         x[m - 1, k // 5] = float("inf")
     elif special == "large":
         x[0] = (torch.rand(k, generator=gen) * 2 - 1).to(torch.float16) * 60000
+    elif special == "order":
+        # A row whose fp64 sum of squares depends on the order of the adds: 1024^2, 0.25^2 and
+        # two tiny squares (154 * 2^-24)^2 half a row away; two forms adding in different orders
+        # round var differently.
+        x[0] = 0
+        x[0, 0], x[0, 2] = 1024, 0.25
+        x[0, k // 2] = x[0, k // 2 + 2] = 154 * 2.0**-24
     return x.to(device)
 
 
@@ -68,7 +75,7 @@ def test_fused_equals_norm_then_linear(cfg: GemmConfig, device: torch.device) ->
     b = cases.bias(n, 4).to(device)
     gamma = _gamma(k, 0, device)
     for m in (1, 2, 3, 4):
-        for special in ("none", "zero", "nan", "inf", "large"):
+        for special in ("none", "zero", "nan", "inf", "large", "order"):
             x = _rows(m, k, 10 * m + len(special), special, device)
             _, _, a = rmsnorm_fp8_quant_dequant(x, gamma, EPS)
             for epilogue, bias in (("none", b), ("silu_mul", None)):
@@ -109,6 +116,23 @@ def test_op_routes_larger_m_through_two_kernels(device: torch.device) -> None:
         got = ops.rmsnorm_fp8_w4a16_linear(x, gamma, EPS, w.qweight_t, w.scales, w.qzeros, None, G, "hip", "silu_mul")
         assert got.shape == (1, m, n // 2)
         assert torch.equal(got, ref), f"m={m}"
+
+
+def test_op_falls_back_where_the_prologue_does_not_fit(device: torch.device) -> None:
+    """M = 4, K = 12160: the stream form stages this x, but the prologue's scratch does not fit
+    beside it (and K is past the prologue's 8192): the op runs the two kernels, same bits."""
+    from tokenforge.kernels.config import stream_form_applies
+
+    n, k = 256, 12160
+    assert stream_form_applies(4, n, k, 8) and not stream_form_applies(4, n, k, 8, norm=True)
+    w = cases.on_device(cases.layer_weights(n, k, 11), device)
+    gamma = _gamma(k, 3, device)
+    ops = torch.ops.tokenforge
+    x = _rows(4, k, 77, "order", device)
+    _, _, a = ops.rmsnorm_fp8_quant_dequant(x, gamma, EPS, None)
+    ref = ops.w4a16_linear(a, w.qweight_t, w.scales, w.qzeros, None, G, "hip")
+    got = ops.rmsnorm_fp8_w4a16_linear(x, gamma, EPS, w.qweight_t, w.scales, w.qzeros, None, G, "hip", "none")
+    assert torch.equal(got, ref)
 
 
 def test_opcheck(device: torch.device) -> None:

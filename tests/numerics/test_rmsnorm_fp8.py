@@ -100,6 +100,33 @@ def test_dynamic_per_token(t: int, h: int, form: str, device: torch.device) -> N
     assert float(rel.max()) <= 2.0**-3
 
 
+def _order_sensitive(t: int, h: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """Rows whose fp64 sum of squares depends on the order of the adds (1024^2 and 0.25^2 next
+    to tiny squares a long way off, the tiny ones moved from row to row), between N(0, 1) rows."""
+    x, w = _inputs(t, h, seed=t + h)
+    for r in range(0, t, max(1, t // 64)):
+        x[r] = 0
+        x[r, r % 8], x[r, 2 + r % 8] = 1024, 0.25
+        pos = (h // 2 + 8 * r) % (h - 2)
+        x[r, pos] = x[r, pos + 2] = 154 * 2.0**-24
+    return x, w
+
+
+@pytest.mark.parametrize("form", FORMS)
+@pytest.mark.parametrize(("t", "h"), [(1, 3584), (2047, 3584), (2048, 3584), (64, 4096), (3, 1000)])
+def test_order_sensitive_rows_in_every_form(t: int, h: int, form: str, device: torch.device) -> None:
+    """The sum of squares is added in one fixed order in every form (row per workgroup with four
+    waves below 2048 rows and two from 2048 on, row per wave): codes and scales equal the
+    oracle's on rows where another order rounds var differently."""
+    if not _form_applies(form, h):
+        pytest.skip(f"{form} does not apply at h={h}")
+    x, w = _order_sensitive(t, h)
+    q, s = rmsnorm_fp8_quant(x.to(device), w.to(device), EPS, form=form)
+    q_ref, s_ref = oref.rmsnorm_fp8_reference(x.numpy(), w.numpy(), EPS)
+    assert np.array_equal(_codes(q), q_ref)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+
+
 @pytest.mark.parametrize("form", FORMS)
 @pytest.mark.parametrize("t", [1, 16, 512, 4096])
 def test_baseline_config2_bit_exact(t: int, form: str, device: torch.device) -> None:
@@ -222,16 +249,15 @@ def _assert_f16_match_nan_aware(a: torch.Tensor, b: torch.Tensor) -> None:
     assert torch.equal(a[~an].view(torch.int16), b[~bn].view(torch.int16))
 
 
-@pytest.mark.parametrize("form", FORMS)
-@pytest.mark.parametrize(("t", "h", "aligned"), [(1, 3584, True), (7, 896, True), (33, 3584, True), (5, 1000, False)])
+@pytest.mark.parametrize(("form", "t", "h", "aligned"),
+                         [(f, t, h, a) for f in FORMS for t, h, a in ((1, 3584, True), (7, 896, True), (33, 3584, True),
+                                                                       (5, 1000, False)) if a or f != "row_per_wave"])
 def test_dequantized_output_equals_the_torch_expression(t: int, h: int, aligned: bool, form: str,
                                                         device: torch.device) -> None:
     """rmsnorm_fp8_quant_dequant: the codes and scales are rmsnorm_fp8_quant's, bit for bit, and
     the fp16 output is `(q.to(float32) * scale).to(float16)` bit for bit (dynamic and static
     scales, the large one leaving mostly subnormal and zero codes; the scalar path for an
     unaligned x)."""
-    if form == "row_per_wave" and not (aligned and _form_applies(form, h)):
-        pytest.skip("the row-per-wave form needs aligned 16-byte rows")
     x, w = baseline_inputs(t, h, seed=5)[:2] if h == 3584 else _inputs(t, h, seed=5)
     xd = x.to(device)
     if not aligned:

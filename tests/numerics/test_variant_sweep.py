@@ -41,6 +41,10 @@ def _case(index: int, variant: tuple) -> dict:  # type: ignore[type-arg]
         # per wave, M <= block_m.
         n = 32 * rng.randint(2, 24) + (16 if rng.random() < 0.3 else 0)
         k = 128 * rng.randint(max(2, warps), max(2, warps) + 6)
+    if kernel == "gemm_mfma" and bk == 128 and stages >= 6:
+        # The wave-tile form: N % 16 == 0 and K % 128 == 0 (N ragged against its tile).
+        n = 16 * rng.randint(4, 32)
+        k = 128 * rng.randint(2, 6)
     if kernel == "gemv_dot" or (kernel == "gemv_mfma" and bk == 512):
         m = rng.randint(1, bm)
     elif kernel == "gemv_mfma":

@@ -39,7 +39,7 @@ def _order_after_barriers(asm: str) -> tuple[int, int]:
     return good, bad
 
 
-@pytest.mark.parametrize("source", ["gemm2.hip", "gemm3.hip"])
+@pytest.mark.parametrize("source", ["gemm2.hip", "gemm3.hip", "gemm4.hip"])
 def test_x_stage_loads_lead_every_barrier_region(source: str, tmp_path: Path) -> None:
     try:
         cc = build.hipcc()
@@ -60,7 +60,7 @@ def test_x_stage_loads_lead_every_barrier_region(source: str, tmp_path: Path) ->
 
 _VMEM = re.compile(r"^(buffer|global|flat|scratch)_(load|store|atomic)")
 _WAIT = re.compile(r"^s_waitcnt\b.*\bvmcnt\((\d+)\)")
-_KERNEL = re.compile(r"^(_Z\w*(gemm2_kernel|gemm3_kernel|gemm8_kernel)I(\w*?)EEv\w*):")
+_KERNEL = re.compile(r"^(_Z\w*(gemm2_kernel|gemm3_kernel|gemm4_kernel|gemm8_kernel)I(\w*?)EEv\w*):")
 _JUMP = re.compile(r"^s_(c?branch)\w*\s+(\.LBB\w+)")
 _INF = float("inf")
 
@@ -79,9 +79,9 @@ def _instructions(body: list[str]) -> list[str]:
     return out
 
 
-def _stages(template_args: str) -> int:
-    """S: the fifth integer template argument of gemm2/3/8_kernel."""
-    return [int(v) for v in re.findall(r"Li(\d+)E", template_args + "E")][4]
+def _stages(kernel: str, template_args: str) -> int:
+    """S: the fifth integer template argument of gemm2/3/8_kernel, the fourth of gemm4_kernel."""
+    return [int(v) for v in re.findall(r"Li(\d+)E", template_args + "E")][3 if kernel == "gemm4_kernel" else 4]
 
 
 def _block_waits(ins: list[str]) -> dict[int, int]:
@@ -111,16 +111,18 @@ def _sregs(text: str) -> set[int]:
 
 def _wait_checks(ins: list[str], stages: int) -> list[tuple[int, int, float]]:
     """(barrier index, its vmcnt N, the fewest vector-memory instructions issued after the last
-    x load of the stage that barrier's iteration reads, over every path that reaches it; -1
-    where a path issues no stage for it).
+    x load of the stage that barrier guards, over every path that reaches it; -1 where a path
+    has no stage left for it).
 
     Loads return in order, so the wait guarantees the stage iff N <= that count. The code is
-    walked forward over every control-flow path, carrying for each recent x stage the number of
-    vector-memory instructions issued since its last load (capped past the largest N). The x loads
-    (``buffer_load ... lds``) between two barriers are one iteration's stage; the prologue's,
-    before the first barrier, are S - 1 stages of equal size issued in order; the barrier of an
-    iteration reads the stage issued S - 1 stages back. A conditional branch is followed both
-    ways unless its outcome is fixed on that path: ``s_cbranch_vccz``/``vccnz`` after
+    walked forward over every control-flow path, carrying the x stages issued and not yet
+    guarded, oldest first, each with the number of vector-memory instructions issued since its
+    last load (capped past the largest N). The x loads (``buffer_load ... lds``) before the first
+    barrier are S - 1 stages of equal size issued in order; between two later barriers they are
+    one stage (or none: a barrier in the middle of an iteration may guard a stage issued before
+    the previous one). Each barrier guards the oldest stage still pending, so the n-th barrier on
+    a path guards the n-th stage issued. A conditional branch is followed both ways unless its
+    outcome is fixed on that path: ``s_cbranch_vccz``/``vccnz`` after
     ``s_andn2_b64 vcc, exec, s[a:b]`` with s[a:b] set by ``s_mov_b64`` to 0 or -1 (exec is
     nonzero: the stage loads are issued by the whole wave). The compiler writes such a pair of
     correlated branches around the two copies of a load it duplicates (an in-range and an
@@ -147,20 +149,20 @@ def _wait_checks(ins: list[str], stages: int) -> list[tuple[int, int, float]]:
                 live[pc] = changed = True
     best: dict[int, float] = {}
     seen: set[tuple] = set()
-    # (pc, constant pairs, vcc: None unknown / 0 / 1, stage counters, this region's x-load
-    # counters, in the prologue)
+    # (pc, constant pairs, vcc: None unknown / 0 / 1, pending stage counters, this region's
+    # x-load counters, in the prologue)
     todo: list[tuple] = [(0, (), None, (), (), True)]
     while todo:
         state = todo.pop()
         if state in seen:
             continue
         seen.add(state)
-        pc, consts, vcc, done, region, pro = state
+        pc, consts, vcc, pending, region, pro = state
         cmap = dict(consts)
         while pc < len(ins) and live[pc]:
             line = ins[pc]
             if line.endswith(":"):
-                key = (pc + 1, tuple(sorted(cmap.items())), vcc, done, region, pro)
+                key = (pc + 1, tuple(sorted(cmap.items())), vcc, pending, region, pro)
                 if key in seen:
                     break
                 seen.add(key)
@@ -174,19 +176,20 @@ def _wait_checks(ins: list[str], stages: int) -> list[tuple[int, int, float]]:
                         best[pc] = -1
                         break
                     per = len(region) // (stages - 1)
-                    done = tuple(region[(k + 1) * per - 1] for k in range(stages - 1))
+                    pending = tuple(region[(k + 1) * per - 1] for k in range(stages - 1))
                     pro = False
-                else:
-                    if not region:
-                        best[pc] = -1  # an iteration that issued no x stage
-                        break
-                    done = (done + (region[-1],))[-(stages - 1):]
+                elif region:
+                    pending = pending + (region[-1],)
                 region = ()
-                best[pc] = min(best.get(pc, _INF), done[-(stages - 1)])
+                if not pending:
+                    best[pc] = -1  # no stage issued for this barrier
+                    break
+                best[pc] = min(best.get(pc, _INF), pending[0])
+                pending = pending[1:]
                 pc += 1
                 continue
             if _VMEM.match(line):
-                done = tuple(min(c + 1, cap) for c in done)
+                pending = tuple(min(c + 1, cap) for c in pending)
                 region = tuple(min(c + 1, cap) for c in region)
                 if " lds" in line:
                     # the prologue's stages need each load's counter; an iteration's, its last
@@ -212,7 +215,7 @@ def _wait_checks(ins: list[str], stages: int) -> list[tuple[int, int, float]]:
                     continue
                 taken = {"s_cbranch_vccnz": vcc, "s_cbranch_vccz": None if vcc is None else 1 - vcc}.get(op)
                 if taken != 0:
-                    todo.append((target, tuple(sorted(cmap.items())), vcc, done, region, pro))
+                    todo.append((target, tuple(sorted(cmap.items())), vcc, pending, region, pro))
                 if taken == 1:
                     break
             pc += 1
@@ -232,12 +235,12 @@ def _kernel_checks(asm: str) -> dict[str, list[tuple[int, int, float]]]:
         while j < len(lines) and not lines[j].startswith(".Lfunc_end"):
             j += 1
         ins = _instructions(lines[i + 1:j])
-        out[m.group(1)] = _wait_checks(ins, _stages(m.group(3)))
+        out[m.group(1)] = _wait_checks(ins, _stages(m.group(2), m.group(3)))
         i = j
     return out
 
 
-@pytest.mark.parametrize("source", ["gemm2.hip", "gemm3.hip", "gemm8.hip"])
+@pytest.mark.parametrize("source", ["gemm2.hip", "gemm3.hip", "gemm4.hip", "gemm8.hip"])
 def test_stage_waits_cover_the_stage_loads(source: str, tmp_path: Path) -> None:
     """Every block barrier's vmcnt(N) is at most the loads issued after the x stage its
     iteration reads, on every path to it (loop, prologue and the odd tail iteration), so the
@@ -313,3 +316,20 @@ def test_wait_check_follows_correlated_branches() -> None:
                 "s_cbranch_vccnz .LBB0_3", _W, ".LBB0_3:", "s_cbranch_scc0 .LBB0_1", "s_endpgm"]
     assert [(n, a) for _, n, a in _wait_checks(_instructions(body(True)), 2)] == [(1, 1)]
     assert [(n, a) for _, n, a in _wait_checks(_instructions(body(False)), 2)] == [(1, 0)]
+
+
+def test_wait_check_with_a_barrier_inside_the_iteration() -> None:
+    """The wave-tile GEMM's order: the prologue issues S - 1 = 2 stages and the weights, waits for
+    the first stage at a barrier; each iteration then waits (mid-iteration) for the stage after
+    it, which no x load separates from the previous barrier, issues the next stage and then the
+    weights. The n-th barrier guards the n-th stage: from the prologue 2 loads follow the second
+    stage (the weights), around the loop 1 (the weights after the stage issued one iteration
+    back); a wait one too permissive is caught."""
+    def body(loop_wait: int) -> list[str]:
+        return [_X, _X, _W, _W, "s_waitcnt vmcnt(3) lgkmcnt(0)", "s_barrier", ".LBB0_1:",
+                f"s_waitcnt vmcnt({loop_wait}) lgkmcnt(0)", "s_barrier", _X, _W, "s_cbranch_scc0 .LBB0_1",
+                "s_endpgm"]
+    rows = _wait_checks(_instructions(body(1)), 3)
+    assert [(n, a) for _, n, a in rows] == [(3, 3), (1, 1)]
+    loose = _wait_checks(_instructions(body(2)), 3)
+    assert loose[1][1] > loose[1][2]

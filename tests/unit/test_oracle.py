@@ -217,3 +217,56 @@ def test_w4a8_exact_reference_differs_from_the_fp16_weight_form_by_the_weight_ro
     bound = np.abs(R.e4m3_decode(codes).astype(np.float64)) @ (np.spacing(w16.astype(np.float16)).astype(np.float64) / 2).T
     assert np.all(np.abs(exact - rounded) <= bound + 1e-12)
     assert np.abs(exact - rounded).max() > 0  # the two forms are not the same function
+
+
+def _tree_sum_scalar(values: list[float]) -> float:
+    """The norm's sum order restated with Python floats (fp64): chunks of 8 zero-padded, each as
+    ((e0 + e1) + (e2 + e3)) + ((e4 + e5) + (e6 + e7)), then the chunk sums pairwise (recursive
+    halves of a power-of-two count, zero-padded)."""
+    sq = [float(v) * float(v) for v in values]
+    sq += [0.0] * ((-len(sq)) % 8)
+    chunks = []
+    for i in range(0, len(sq), 8):
+        e = sq[i:i + 8]
+        chunks.append(((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7])))
+    width = 1
+    while width < len(chunks):
+        width *= 2
+    chunks += [0.0] * (width - len(chunks))
+
+    def pairwise(lo: int, n: int) -> float:
+        return chunks[lo] if n == 1 else pairwise(lo, n // 2) + pairwise(lo + n // 2, n // 2)
+
+    return pairwise(0, width)
+
+
+def test_sum_squares_order_against_a_scalar_restatement() -> None:
+    """Bit for bit with an independent scalar restatement of the order, on rows with a wide
+    dynamic range (where the order changes the fp64 sum), every length 1..70 and 3584."""
+    rng = np.random.default_rng(7)
+    for h in list(range(1, 71)) + [3584]:
+        mags = rng.choice([2.0**-20, 2.0**-8, 1.0, 2.0**6, 2.0**12], size=(3, h))
+        x = (rng.standard_normal((3, h)) * mags).astype(np.float16)
+        got = R.sum_squares(x)[:, 0]
+        for r in range(3):
+            assert got[r] == _tree_sum_scalar(list(x[r])), (h, r)
+
+
+def test_sum_squares_fixed_order_is_not_any_order() -> None:
+    """A row where the fp64 sum depends on the order (1024^2 next to tiny squares): the fixed
+    order gives one value, a left-to-right sum another, so a kernel adding in another order is
+    caught; the fixed-order sum is within its rounding bound of the exact rational sum."""
+    import fractions
+
+    row = np.zeros(3584, dtype=np.float16)
+    row[0], row[2] = 1024, 0.25
+    row[3584 // 2] = row[3584 // 2 + 2] = np.float16(154 * 2.0**-24)
+    for v in range(5, 3584, 97):
+        row[v] = np.float16(2.0**-12)
+    got = float(R.sum_squares(row[None])[0, 0])
+    seq = 0.0
+    for v in row:
+        seq += float(v) * float(v)
+    assert got != seq
+    exact = sum(fractions.Fraction(float(v)) ** 2 for v in row)
+    assert abs(fractions.Fraction(got) - exact) <= exact * 12 * fractions.Fraction(2) ** -53

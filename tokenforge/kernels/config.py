@@ -44,6 +44,7 @@ Every kernel reads the weights in the gfx950 tile layout that ``pack.pack_awq`` 
 
 from __future__ import annotations
 
+import functools
 from dataclasses import asdict, dataclass, replace
 from typing import Any
 
@@ -96,18 +97,35 @@ def _stream_variants() -> list[tuple[str, int, int, int, int, int]]:
     return [("gemv_mfma", STREAM_MAX_M, 16, STREAM_BLOCK_K, w, p) for p in (2, 4) for w in _WAVES]
 
 
-def stream_form_applies(m: int, n: int, k: int, num_warps: int) -> bool:
+NORM_MAX_K = 8192
+"""Largest K whose RMSNorm the GEMV stream form runs in its prologue."""
+
+
+def norm_scratch_bytes(m: int, k: int) -> int:
+    """LDS the stream form's RMSNorm prologue adds: M rows of chunk sums (fp64), each padded to
+    the power of two >= K / 8 (at least 64), and 256 bytes of maxima."""
+    lpad = 64
+    while lpad < k // 8:
+        lpad *= 2
+    return m * lpad * 8 + 256
+
+
+def stream_form_applies(m: int, n: int, k: int, num_warps: int, norm: bool = False) -> bool:
     """Whether the op runs a call of this shape on the GEMV stream form when its bucket's config
     is that form: M <= 4, N % 32 == 0, K % 128 == 0 with at least one 128-wide step per wave,
     and x small enough to stage in LDS. The rule does not depend on the epilogue, so a plain
     call and its fused SiLU*mul or residual twin run the same kernel and agree bit for bit (the
-    library itself runs plain and residual calls on N % 16 == 0 as well)."""
+    library itself runs plain and residual calls on N % 16 == 0 as well). With ``norm`` (the
+    RMSNorm prologue of ``rmsnorm_fp8_w4a16_linear``) K is at most NORM_MAX_K and the staged x
+    plus the prologue's scratch must fit."""
+    x_bytes = m * (k + 8) * 2 + (norm_scratch_bytes(m, k) if norm else 0)
     return (
         1 <= m <= STREAM_MAX_M
         and n % 32 == 0
         and k % 128 == 0
         and k // 128 >= num_warps
-        and m * (k + 8) * 2 <= STREAM_MAX_X_BYTES
+        and x_bytes <= STREAM_MAX_X_BYTES
+        and (not norm or k <= NORM_MAX_K)
     )
 
 
@@ -132,6 +150,10 @@ def _gemm_variants() -> list[tuple[str, int, int, int, int, int]]:
     out += [("gemm_mfma", 16 * mt, 64 * rt, 128, 4, st) for mt, rt, st in skinny]
     # ... and with two waves along M: 256 x 160 tiles (gate_up at M >= 256: 237 tiles).
     out += [("gemm_mfma", 256, 160, 128, 4, 2)]
+    # block_k 128, num_stages 4 + S: the wave-tile form (one wave per SIMD, 16 MT x 16 RT per
+    # wave, WM waves along M), S x stages (x issued S - 1 steps ahead, weights three).
+    wave_tiles = [(8, 5, 1, 3), (8, 4, 1, 4), (8, 3, 1, 4), (8, 2, 1, 4)]
+    out += [("gemm_mfma", 16 * mt * wm, 16 * rt * (4 // wm), 128, 4, 4 + st) for mt, rt, wm, st in wave_tiles]
     return out
 
 
@@ -396,6 +418,7 @@ _FP8_SPLIT_US = 3.0
 _FP8_PARTIAL_BYTES_PER_US = 4.0e6
 
 
+@functools.lru_cache(maxsize=None)
 def fp8_gemm_config(bucket: int, n: int, k: int) -> GemmConfig:
     """Launch config of the W4A8 fp8 GEMM for one bucket: the tile and K split with the lowest
     modelled time (rounds of workgroups over the CUs x blocks per workgroup x block time, plus

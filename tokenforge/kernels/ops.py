@@ -246,6 +246,10 @@ def w4a8_linear(
         # Prefill M: the e4m3 codes go straight into the fp8 MFMA (weights as exact e4m3
         # (q - z), the group scale applied in fp32) instead of being decoded to fp16.
         cfg = fp8_gemm_config(bucket, n, k)
+        if m > MAX_BUCKET_M and cfg.split_k > 1 and -(-m // cfg.block_m) * -(-n // cfg.block_n) >= NUM_CUS:
+            # As in _decide: past the largest bucket, once the M tiles fill the CUs a K split
+            # only adds its fp32 workspace and reduction.
+            cfg = dataclasses.replace(cfg, split_k=1)
     # One contiguous scale vector: the kernel reads its data pointer with the stride of this view.
     s2 = (x_scale.reshape(-1) if x_scale.numel() > 1 else x_scale.reshape(1)).contiguous()
     r2 = residual.reshape(-1, n) if residual is not None else None
@@ -365,7 +369,7 @@ def rmsnorm_fp8_w4a16_linear(
             f"backend must be 'hip' (or its aliases 'triton', 'cuda') at op level, got {backend!r}"
         )
     cfg = _decide(x2, m, n, k, group_size, backend)
-    if cfg.stream:
+    if cfg.stream and stream_form_applies(m, n, k, cfg.num_warps, norm=True):
         y = _w4a16.rmsnorm_fp8_w4a16_gemm_ex(
             x2, norm_weight, eps, qweight_t, scales, qzeros, group_size, cfg, bias, epilogue
         )

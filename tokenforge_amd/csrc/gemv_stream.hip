@@ -42,7 +42,25 @@ namespace {
 constexpr int kStreamMaxM = 4;                 // D rows 0..3 live in lanes 0..15
 constexpr int kStreamMaxXBytes = 96 * 1024;    // staged x: M rows of K + 8 halfs
 constexpr int kStreamInflightKB = 32;          // weight bytes in flight per CU (KB)
-constexpr int kNormScratchBytes = 1024;        // prologue reductions: [16][4] doubles and words
+constexpr int kNormMaxK = 8192;                // the RMSNorm prologue serves K up to this
+
+// LDS the RMSNorm prologue adds: the chunk sums of the squares of every row, each row padded to
+// lpad = the power of two >= K / 8 (at least 64) entries, then [16][4] words for the maxima.
+__host__ __device__ __forceinline__ int norm_lpad(int k) {
+  int l = 64;
+  while (l < (k >> 3)) l <<= 1;
+  return l;
+}
+__host__ __device__ __forceinline__ size_t norm_scratch_bytes(int m, int k) {
+  return (size_t)m * norm_lpad(k) * 8 + 256;
+}
+
+// The sum of squares of staged row rs in the fixed order of norm_row.h, from its chunk sums at
+// sums[rs * lpad + q] (zeros past the row's chunks; lpad / 64 <= 16 per lane); every lane of the
+// wave takes part and gets the total.
+__device__ __forceinline__ double staged_row_total(const double* sums, int lpad, int rs) {
+  return row_total_lds_rt<16>(sums + rs * lpad, lpad >> 6);
+}
 
 __host__ __device__ __forceinline__ int stream_xstride(int k) { return k + 8; }
 
@@ -63,33 +81,32 @@ struct StreamGeo {
 
 // The RMSNorm + e4m3 prologue over the m rows of x staged in LDS (row r at xs + r * xstride),
 // in place: each row becomes fp16(code * scale) as rmsnorm_fp8.hip computes it for the row
-// (reference.py:35-50; dynamic scale): fp64 sum of squares, var = fp32(sum * (1 / k)), rstd =
-// 1 / sqrt(var + eps), y = fp16(fp32(x * rstd)) * w in fp16, absmax, scale, codes, then the
-// codes times the scale. Thread t takes the 8-element chunks t, t + T, ...; the workgroup's W
-// waves meet in red_d / red_u (W entries each), in wave order.
-__device__ __forceinline__ void norm_rows(const LinearArgs& a, _Float16* xs, int xstride, double* red_d,
+// (reference.py:35-50; dynamic scale): fp64 sum of squares in the fixed order of norm_row.h
+// (all rows' chunk sums into `sums`, one barrier, every wave adds them), var = fp32(sum *
+// (1 / k)), rstd = 1 / sqrt(var + eps), y = fp16(fp32(x * rstd)) * w in fp16, absmax, scale,
+// codes, then the codes times the scale. Thread t takes the 8-element chunks t, t + T, ...; the
+// workgroup's W waves meet for each row's absmax in red_u[r][w].
+__device__ __forceinline__ void norm_rows(const LinearArgs& a, _Float16* xs, int xstride, double* sums,
                                           uint32_t* red_u, int W, int wave, int lane) {
   const int T = W * 64;
   const int chunks = a.k >> 3;
+  const int lpad = norm_lpad(a.k);
+  const int lshift = __builtin_ctz(lpad);
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.norm_w, (uint32_t)a.k * 2u);
+  for (int e = threadIdx.x; e < (a.m << lshift); e += T) {
+    const int r = e >> lshift, q = e & (lpad - 1);
+    double v = 0.0;
+    if (q < chunks) {
+      const u4 x = reinterpret_cast<const u4*>(xs + r * xstride)[q];
+      const h2 p[4] = {as_h2(x[0]), as_h2(x[1]), as_h2(x[2]), as_h2(x[3])};
+      v = chunk_sum_squares(p);
+    }
+    sums[e] = v;
+  }
+  __syncthreads();
   for (int r = 0; r < a.m; ++r) {
     u4* row = reinterpret_cast<u4*>(xs + r * xstride);
-    double ss0 = 0.0, ss1 = 0.0;  // two chains: fp64 adds are long-latency
-    for (int q = threadIdx.x; q < chunks; q += T) {
-      const u4 v = row[q];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const h2 p = as_h2(v[j]);
-        const double d0 = (double)(float)p[0], d1 = (double)(float)p[1];
-        ss0 += d0 * d0;
-        ss1 += d1 * d1;
-      }
-    }
-    const double wsum = wave_sum_f64(ss0 + ss1);
-    if (lane == 0) red_d[wave] = wsum;
-    __syncthreads();
-    double total = red_d[0];
-    for (int w = 1; w < W; ++w) total += red_d[w];
+    const double total = staged_row_total(sums, lpad, r);
     const float var = (float)((double)(float)total * a.norm_inv_k);
     const float rstd = 1.0f / __builtin_sqrtf(var + a.norm_eps);
 
@@ -110,10 +127,10 @@ __device__ __forceinline__ void norm_rows(const LinearArgs& a, _Float16* xs, int
       row[q] = v;
     }
     const uint32_t wmax = wave_max_u32(am);
-    if (lane == 0) red_u[wave] = wmax;
+    if (lane == 0) red_u[r * 16 + wave] = wmax;
     __syncthreads();
-    uint32_t m_bits = red_u[0];
-    for (int w = 1; w < W; ++w) m_bits = __builtin_elementwise_max(m_bits, red_u[w]);
+    uint32_t m_bits = red_u[r * 16];
+    for (int w = 1; w < W; ++w) m_bits = __builtin_elementwise_max(m_bits, red_u[r * 16 + w]);
     const float amax = (float)__builtin_bit_cast(_Float16, (uint16_t)m_bits);
     const float s = dynamic_scale(amax);
     const bool fast = __builtin_isfinite(amax) && __builtin_isfinite(s) && s > 0.0f;
@@ -149,30 +166,25 @@ __device__ __forceinline__ void norm_rows(const LinearArgs& a, _Float16* xs, int
 
 // The same prologue when every thread holds at most one 8-element chunk of x (M * K <= 8 T, the
 // decode case): the thread's chunk x1 (row r, chunk q; ok false past the end) and its weight
-// chunk g1 are already in registers, so the arithmetic runs there and only the M row totals
-// and maxima meet in LDS (red_d / red_u: [W][4], one barrier each). x1 becomes the fp16(code *
-// scale) chunk.
-__device__ __forceinline__ void norm_chunk(const LinearArgs& a, u4& x1, const u4 g1, int r, bool ok, double* red_d,
-                                           uint32_t* red_u, int W, int wave, int lane) {
-  double ss0 = 0.0, ss1 = 0.0;
-  if (ok) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const h2 p = as_h2(x1[j]);
-      const double d0 = (double)(float)p[0], d1 = (double)(float)p[1];
-      ss0 += d0 * d0;
-      ss1 += d1 * d1;
-    }
-  }
-  const double ss = ss0 + ss1;
-  for (int rr = 0; rr < a.m; ++rr) {
-    const double wsum = wave_sum_f64(r == rr ? ss : 0.0);
-    if (lane == 0) red_d[wave * 4 + rr] = wsum;
-  }
+// chunk g1 are already in registers, so the arithmetic runs there; the chunk sums meet in
+// `sums` (the fixed order of norm_row.h: every wave adds each row's), the maxima in red_u[r][w],
+// one barrier each. x1 becomes the fp16(code * scale) chunk.
+__device__ __forceinline__ void norm_chunk(const LinearArgs& a, u4& x1, const u4 g1, int r, int q, bool ok,
+                                           double* sums, uint32_t* red_u, int W, int wave, int lane) {
+  const int chunks = a.k >> 3;
+  const int lpad = norm_lpad(a.k);
+  const int lshift = __builtin_ctz(lpad);
+  const h2 p[4] = {as_h2(x1[0]), as_h2(x1[1]), as_h2(x1[2]), as_h2(x1[3])};
+  if (ok) sums[(r << lshift) + q] = chunk_sum_squares(p);
+  for (int e = threadIdx.x; e < (a.m << lshift); e += W * 64)
+    if ((e & (lpad - 1)) >= chunks) sums[e] = 0.0;
   __syncthreads();
   const int rs = ok ? r : 0;  // threads past the end follow row 0 (their results are not stored)
-  double total = red_d[rs];
-  for (int w = 1; w < W; ++w) total += red_d[w * 4 + rs];
+  double total = 0.0;
+  for (int rr = 0; rr < a.m; ++rr) {
+    const double t = staged_row_total(sums, lpad, rr);  // every lane of the wave takes part
+    total = rr == rs ? t : total;
+  }
   const float var = (float)((double)(float)total * a.norm_inv_k);
   const float rstd = 1.0f / __builtin_sqrtf(var + a.norm_eps);
 
@@ -191,11 +203,11 @@ __device__ __forceinline__ void norm_chunk(const LinearArgs& a, u4& x1, const u4
   if (!ok) am = 0;
   for (int rr = 0; rr < a.m; ++rr) {
     const uint32_t wmax = wave_max_u32(r == rr ? am : 0u);
-    if (lane == 0) red_u[wave * 4 + rr] = wmax;
+    if (lane == 0) red_u[rr * 16 + wave] = wmax;
   }
   __syncthreads();
-  uint32_t m_bits = red_u[rs];
-  for (int w = 1; w < W; ++w) m_bits = __builtin_elementwise_max(m_bits, red_u[w * 4 + rs]);
+  uint32_t m_bits = red_u[rs * 16];
+  for (int w = 1; w < W; ++w) m_bits = __builtin_elementwise_max(m_bits, red_u[rs * 16 + w]);
   const float amax = (float)__builtin_bit_cast(_Float16, (uint16_t)m_bits);
   const float s = dynamic_scale(amax);
   const bool fast = __builtin_isfinite(amax) && __builtin_isfinite(s) && s > 0.0f;
@@ -370,12 +382,13 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_stream_kernel(LinearArgs a, in
     issue(p);
     __builtin_amdgcn_sched_barrier(0);  // slot 0 is the oldest load of the ring
   }
-  double* red_d = reinterpret_cast<double*>(part + W * tpw * 16);  // NORM scratch, [W][4]
-  uint32_t* red_u = reinterpret_cast<uint32_t*>(red_d + 64);
+  // NORM scratch: the rows' chunk sums, then the maxima [4][16]
+  double* sums = reinterpret_cast<double*>(part + W * tpw * 16);
+  uint32_t* red_u = reinterpret_cast<uint32_t*>(sums + (NORM ? a.m * norm_lpad(a.k) : 0));
   if (one) {
     const int e = threadIdx.x;
     const int r = row_of(e), q = e - r * chunks;
-    if (NORM) norm_chunk(a, x1, g1, r, e < total, red_d, red_u, W, wave, lane);
+    if (NORM) norm_chunk(a, x1, g1, r, q, e < total, sums, red_u, W, wave, lane);
     if (e < total) *reinterpret_cast<u4*>(xs + r * xstride + q * 8) = X8 ? e4m3x8_to_f16(u2{x1[0], x1[1]}) : x1;
   } else {
     store_x(threadIdx.x);
@@ -386,7 +399,7 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_stream_kernel(LinearArgs a, in
   }
   if (NORM && !one) {
     __syncthreads();  // every row of x is in LDS
-    norm_rows(a, xs, xstride, red_d, red_u, W, wave, lane);
+    norm_rows(a, xs, xstride, sums, red_u, W, wave, lane);
   }
   for (int e = threadIdx.x; e < W * tpw * 16; e += T) part[e] = f4{0.0f, 0.0f, 0.0f, 0.0f};
   __syncthreads();
@@ -494,7 +507,7 @@ StreamPlan plan_stream(Kernel kernel, const LinearArgs& a, int waves, int depth)
   StreamPlan p;
   const int tiles = a.n >> 4;
   // The staged x, plus the prologue's reduction scratch behind the partials when it has one.
-  const size_t xbytes = (size_t)a.m * stream_xstride(a.k) * 2 + (a.norm_w ? kNormScratchBytes : 0);
+  const size_t xbytes = (size_t)a.m * stream_xstride(a.k) * 2 + (a.norm_w ? norm_scratch_bytes(a.m, a.k) : 0);
   const size_t cap = device_max_lds();
   if (xbytes > (size_t)kStreamMaxXBytes || xbytes + (size_t)waves * 256 > cap) return p;
   const int per_wave = 256;  // bytes of partials per (wave, tile)
@@ -559,6 +572,8 @@ int launch_stream(const LinearArgs& a, const tf_gemm_config& cfg, float*, hipStr
   const bool silu = a.epilogue == TF_EPILOGUE_SILU_MUL, x8 = a.x8 != nullptr, norm = a.norm_w != nullptr;
   const int w = cfg.num_warps;
   if (norm && x8) return fail(TF_EINVAL, "tf_w4a16_linear: the RMSNorm prologue takes fp16 x");
+  if (norm && a.k > kNormMaxK)
+    return fail(TF_EINVAL, "tf_rmsnorm_fp8_w4a16_linear: the RMSNorm prologue serves K <= 8192");
   if (norm)
     return silu ? launch_stream_k<P, MAXW, true, false, true>(a, w, stream)
                 : launch_stream_k<P, MAXW, false, false, true>(a, w, stream);

@@ -152,6 +152,7 @@ const Variant* gemv_stream_variants(int* count);
 const Variant* gemm_variants(int* count);
 const Variant* gemm2_variants(int* count);
 const Variant* gemm3_variants(int* count);
+const Variant* gemm4_variants(int* count);
 const Variant* gemm8_variants(int* count);
 
 int check_group_size(int32_t group_size, int64_t k, const char* name);

@@ -15,6 +15,8 @@ struct Table {
   int n_gemm2;
   const Variant* gemm3;
   int n_gemm3;
+  const Variant* gemm4;
+  int n_gemm4;
   const Variant* gemm8;
   int n_gemm8;
   Table() {
@@ -23,9 +25,10 @@ struct Table {
     gemm = gemm_variants(&n_gemm);
     gemm2 = gemm2_variants(&n_gemm2);
     gemm3 = gemm3_variants(&n_gemm3);
+    gemm4 = gemm4_variants(&n_gemm4);
     gemm8 = gemm8_variants(&n_gemm8);
   }
-  int size() const { return n_gemv + n_stream + n_gemm + n_gemm2 + n_gemm3 + n_gemm8; }
+  int size() const { return n_gemv + n_stream + n_gemm + n_gemm2 + n_gemm3 + n_gemm4 + n_gemm8; }
   const Variant& at(int i) const {
     if (i < n_gemv) return gemv[i];
     i -= n_gemv;
@@ -35,7 +38,9 @@ struct Table {
     i -= n_gemm;
     if (i < n_gemm2) return gemm2[i];
     i -= n_gemm2;
-    return i < n_gemm3 ? gemm3[i] : gemm8[i - n_gemm3];
+    if (i < n_gemm3) return gemm3[i];
+    i -= n_gemm3;
+    return i < n_gemm4 ? gemm4[i] : gemm8[i - n_gemm4];
   }
 };
 

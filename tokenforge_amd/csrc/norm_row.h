@@ -134,13 +134,52 @@ __device__ __forceinline__ double readlane_f64(double v, int lane) {
 }
 
 // Sum of a wave's 64 lanes (every lane active), wave-uniform: four DPP steps leave each row of
-// 16 lanes holding its row's total, then the four row totals are read and added.
+// 16 lanes holding its row's total, then the four row totals are read and added. The order is
+// pairwise over the lane index ((l0 + l1) + (l2 + l3), ...; fp add commutes, so every lane of
+// a step forms the same sums), which the fixed sum-of-squares order below relies on.
 __device__ __forceinline__ double wave_sum_f64(double v) {
   v += dpp_f64<kDppQuadXor1>(v);
   v += dpp_f64<kDppQuadXor2>(v);
   v += dpp_f64<kDppHalfRowMirror>(v);
   v += dpp_f64<kDppRowMirror>(v);
   return (readlane_f64(v, 0) + readlane_f64(v, 16)) + (readlane_f64(v, 32) + readlane_f64(v, 48));
+}
+
+// ------------------------------------------------------------------ sum of squares order
+//
+// Every form of the norm adds the squares of a row in one fixed order, so a row's var does not
+// depend on the form, the batch size or the fusion (reference.py:37 leaves the order to torch):
+// elements in chunks of 8 (the row zero-padded), each chunk as ((e0 + e1) + (e2 + e3)) +
+// ((e4 + e5) + (e6 + e7)) with e = fp64(x)^2 (exact for fp16 x), then the chunk sums pairwise,
+// bottom up over the chunk index, the count zero-padded to a power of two (zeros change no
+// partial sum, so any larger power of two gives the same total). The forms write their chunk
+// sums to LDS and each wave reduces them: lane l adds the R consecutive sums l R .. l R + R - 1
+// pairwise (the low bits of the chunk index), then the 64 lane totals are added pairwise by
+// wave_sum_f64 (the next six bits).
+
+// Sum of squares of one 8-element chunk (four fp16 pairs, element 2j in the low half of pair j).
+// fma(d0, d0, d1 * d1) rounds d0^2 + d1^2 once, as the add of the two exact squares does.
+__device__ __forceinline__ double chunk_sum_squares(const h2 (&v)[4]) {
+  double p[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const double d0 = (double)(float)v[j][0], d1 = (double)(float)v[j][1];
+    p[j] = __builtin_fma(d0, d0, d1 * d1);
+  }
+  return (p[0] + p[1]) + (p[2] + p[3]);
+}
+
+// Pairwise sum of the R values at p[0 .. R) (R a power of two), recursive halves.
+template <int R>
+__device__ __forceinline__ double pairwise_lds(const double* p) {
+  if constexpr (R == 1) {
+    return p[0];
+  } else if constexpr (R == 2) {
+    const double2 v = *reinterpret_cast<const double2*>(p);
+    return v.x + v.y;
+  } else {
+    return pairwise_lds<R / 2>(p) + pairwise_lds<R / 2>(p + R / 2);
+  }
 }
 
 // Unsigned max of a wave's 64 lanes (every lane active), wave-uniform.
@@ -152,6 +191,30 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
   const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
   const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
   return __builtin_elementwise_max(__builtin_elementwise_max(a, b), __builtin_elementwise_max(c, d));
+}
+
+// The row total of 64 R chunk sums in LDS (R a power of two; entries past the row's chunks hold
+// zeros) in the fixed order, computed by one wave (every lane active); wave-uniform.
+template <int R>
+__device__ __forceinline__ double row_total_lds(const double* sums) {
+  const int lane = threadIdx.x & 63;
+  return wave_sum_f64(pairwise_lds<R>(sums + lane * R));
+}
+
+// The same for a runtime count of chunks: R = L / 64 (L, a power of two from 64 to 64 RMAX, at
+// least the chunk count); each lane reads its R sums into a zero-filled set of RMAX, which has
+// the same pairwise total as the R.
+template <int RMAX>
+__device__ __forceinline__ double row_total_lds_rt(const double* sums, int r) {
+  const int lane = threadIdx.x & 63;
+  double v[RMAX];
+#pragma unroll
+  for (int i = 0; i < RMAX; ++i) v[i] = i < r ? sums[lane * r + i] : 0.0;
+#pragma unroll
+  for (int w = RMAX; w > 1; w /= 2)
+#pragma unroll
+    for (int i = 0; i < w / 2; ++i) v[i] = v[2 * i] + v[2 * i + 1];
+  return wave_sum_f64(v[0]);
 }
 
 }  // namespace tf

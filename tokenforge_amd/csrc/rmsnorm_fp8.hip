@@ -11,11 +11,10 @@
 // 8192 the row per wave is ~5% faster. Giving a wave several rows, with the next row requested
 // once the current row's data is in, was slower at every T (fewer waves per SIMD leave the
 // latency of each row's dependent steps exposed), so each wave takes one row.
-// The sum of squares is accumulated in fp64: every x^2 of an fp16 x is exact, so the fp64
-// total is the exact sum up to ~2^-53 relative and its rounding to fp32 does not depend on the
-// summation order. The kernel is therefore deterministic and matches a correctly rounded fp32
-// restatement bit for bit; torch's fp32 `mean` (reference.py:37) can differ from it by an ulp
-// of var on some rows.
+// The sum of squares is accumulated in fp64 (every x^2 of an fp16 x is exact) in the fixed
+// order of norm_row.h, the same in both forms and in the decode GEMV's prologue, so a row's var
+// does not depend on the form or the batch size; torch's fp32 `mean` (reference.py:37) can
+// differ from it by an ulp of var on some rows.
 //
 // Quotient y / scale (reference.py:47-49) and the per-row divisions: exact forms in
 // norm_row.h.
@@ -34,20 +33,6 @@ namespace tf {
 namespace {
 
 typedef unsigned short us2 __attribute__((ext_vector_type(2)));
-
-// Sum over the WAVES waves of the workgroup (every lane active); the result is wave-uniform.
-template <int WAVES>
-__device__ __forceinline__ double block_sum(double v, double* red) {
-  v = wave_sum_f64(v);
-  if (WAVES == 1) return v;  // the row is one wave's: no LDS, no barrier
-  const int wave = threadIdx.x >> 6;
-  if ((threadIdx.x & 63) == 0) red[wave] = v;
-  __syncthreads();
-  double t = red[0];
-#pragma unroll
-  for (int i = 1; i < WAVES; ++i) t += red[i];
-  return t;
-}
 
 // Max of |y| as fp16 bit patterns: for non-NaN values the unsigned order of (bits & 0x7FFF)
 // is the order of |y|, and every NaN pattern is above +inf, so a NaN anywhere wins (the NaN
@@ -96,20 +81,23 @@ __device__ __forceinline__ void load_row(const uint16_t* __restrict__ src, int t
   }
 }
 
-// Sum of squares of one row held in registers, over the WAVES waves that share it.
+// Sum of squares of one row held in registers, over the WAVES waves that share it, in the fixed
+// order of norm_row.h: thread tid's chunk i is chunk tid + 64 WAVES i of the row, its sum goes
+// to sums[chunk] (CPT * 64 * WAVES entries, a power of two; chunks past h hold zeros), and after
+// one barrier every wave adds them all. WAVES == 1 (a row of one wave, no barrier) orders the
+// wave's own LDS writes before its reads with a wavefront fence.
 template <int WAVES, int CPT>
-__device__ __forceinline__ double row_sum_squares(const h2 (&xv)[CPT][4], double* red_d) {
-  double ss[2] = {0.0, 0.0};  // two chains: fp64 adds are long-latency
+__device__ __forceinline__ double row_sum_squares(const h2 (&xv)[CPT][4], double* sums, int tid) {
+  constexpr int kThreads = WAVES * 64;
+  constexpr int R = (CPT * WAVES) < 1 ? 1 : CPT * WAVES;
+  static_assert((CPT & (CPT - 1)) == 0, "chunks per thread: a power of two");
 #pragma unroll
-  for (int i = 0; i < CPT; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int k = 0; k < 2; ++k) {
-        const double d = (double)(float)xv[i][j][k];
-        ss[k] += d * d;
-      }
-  return block_sum<WAVES>(ss[0] + ss[1], red_d);
+  for (int i = 0; i < CPT; ++i) sums[tid + i * kThreads] = chunk_sum_squares(xv[i]);
+  if (WAVES > 1)
+    __syncthreads();
+  else
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  return row_total_lds<R>(sums);
 }
 
 // Everything after the sum of squares (``total``) for one row held in registers (xv is
@@ -235,7 +223,7 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_fp8_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* __restrict__ w,
     uint8_t* __restrict__ q, int64_t ldq, float* __restrict__ scale, int static_scale,
     uint16_t* __restrict__ dq, int64_t lddq, int h, double inv_h, float eps) {
-  __shared__ double red_d[WAVES];
+  __shared__ double sums[CPT * WAVES * 64];
   __shared__ uint32_t red_u[WAVES];
   const int64_t row = blockIdx.x;
   const int tid = threadIdx.x;
@@ -244,7 +232,7 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_fp8_kernel(
   h2 xv[CPT][4], wv[CPT][4];
   load_row<CPT, WAVES * 64, VEC, kLoadOnce>(x + row * ldx, tid, h, xv);
   load_row<CPT, WAVES * 64, VEC, kLoadReused>(w, tid, h, wv);
-  const double total = row_sum_squares<WAVES, CPT>(xv, red_d);
+  const double total = row_sum_squares<WAVES, CPT>(xv, sums, tid);
   finish_row<WAVES, CPT, VEC, DQ>(xv, wv, total, row, tid, q, ldq, scale, static_scale, s_static, dq, lddq, h, inv_h,
                                   eps, red_u);
 }
@@ -255,6 +243,8 @@ __global__ __launch_bounds__(256) void rmsnorm_fp8_wave_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* __restrict__ w,
     uint8_t* __restrict__ q, int64_t ldq, float* __restrict__ scale, int static_scale,
     uint16_t* __restrict__ dq, int64_t lddq, int64_t t, int h, double inv_h, float eps) {
+  constexpr int CP = CPT <= 1 ? 1 : CPT <= 2 ? 2 : CPT <= 4 ? 4 : CPT <= 8 ? 8 : 16;  // power of two >= CPT
+  __shared__ double sums[4][CP * 64];  // one region per wave
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= t) return;  // the whole wave: no row for it, and no barrier follows
@@ -262,7 +252,12 @@ __global__ __launch_bounds__(256) void rmsnorm_fp8_wave_kernel(
   h2 xv[CPT][4], wv[CPT][4];
   load_row<CPT, 64, true, kLoadOnce>(x + row * ldx, lane, h, xv);
   load_row<CPT, 64, true, kLoadReused>(w, lane, h, wv);
-  const double total = row_sum_squares<1, CPT>(xv, nullptr);
+  h2 xp[CP][4];  // the row's chunks padded to a power of two with zero chunks
+#pragma unroll
+  for (int i = 0; i < CP; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) xp[i][j] = i < CPT ? xv[i][j] : as_h2(0u);
+  const double total = row_sum_squares<1, CP>(xp, sums[threadIdx.x >> 6], lane);
   finish_row<1, CPT, true, DQ>(xv, wv, total, row, lane, q, ldq, scale, static_scale, s_static, dq, lddq, h, inv_h,
                                eps, nullptr);
 }
