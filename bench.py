@@ -436,7 +436,7 @@ def probe_summary(probe_log: str) -> int:
         "",
         "Every figure is the median over 5 replays of a HIP graph of launches rotating over the",
         "bench's cold layer copies (HIP events on the replay stream), in us per launch. The probes",
-        "(tokenforge_amd/probes/read_probes.hip, a library of their own) read with the GEMV's grid",
+        "(bench_probes/read_probes.hip, a library of their own) read with the GEMV's grid",
         "and 128-bit buffer loads and do no arithmetic:",
         "",
         "* tile: the gfx950 tile layout, one workgroup per 16-row tile, its waves splitting the",
@@ -781,7 +781,7 @@ def read_probes(dev: torch.device, layers: list, copies: int, xs: list, cfgs: li
     from tokenforge.kernels.config import candidate_configs
     from tokenforge.kernels.hip.w4a16 import w4a16_gemm
 
-    plib = ctypes.CDLL(str(ROOT / "tokenforge_amd" / "lib" / "libtokenforge_probes.so"))
+    plib = ctypes.CDLL(str(ROOT / "bench_probes" / "lib" / "libtokenforge_read_probes.so"))
     p_, i64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32
     plib.tfp_read.argtypes = [i32, p_, p_, p_, i64, i64, i32, i32, p_, p_]
     plib.tfp_out_words.argtypes = [i64, i32]
@@ -898,7 +898,7 @@ def main() -> int:
     ap.add_argument("--kernel-probe", action="store_true",
                     help="eager launches of every kernel the bench line times, in order, for rocprofv3")
     ap.add_argument("--probe", action="store_true",
-                    help="memory floors of the GEMV's access patterns (libtokenforge_probes.so), "
+                    help="memory floors of the GEMV's access patterns (bench_probes/lib/libtokenforge_read_probes.so), "
                          "next to the GEMV itself on the cached or default configs")
     args = ap.parse_args()
     if args.stats_summary:

@@ -1,7 +1,8 @@
 // Memory-system probes behind the GEMV's cost model (bench.py --probe): pure-read kernels with
 // the decode GEMV's grid, wave split, ring depth and access pattern, and no arithmetic, so
-// their time is the floor the memory system sets for that pattern. Built into its own
-// library (libtokenforge_probes.so); the product library never contains or calls them.
+// their time is the floor the memory system sets for that pattern. Built into a library of its
+// own (bench_probes/lib/libtokenforge_read_probes.so); the product library never contains or
+// calls them.
 //
 // Patterns (all loads are 128-bit buffer loads; a lane XORs what it loads and writes one word):
 //   0 tile:    tile layout. A workgroup owns one 16-row tile, its waves split the tile's

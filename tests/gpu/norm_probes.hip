@@ -1,6 +1,6 @@
 // Exhaustive on-device check of the RMSNorm+FP8 dynamic-scale quotient (norm_row.h), run
-// by tests/gpu/test_norm_quotient.py. Built into the probes library
-// (libtokenforge_probes.so), which the product library never contains or calls.
+// by tests/gpu/test_norm_quotient.py. A test fixture: built into a library of its own
+// (tests/gpu/lib/libtokenforge_norm_probes.so), which the product library never contains or calls.
 //
 // Workgroup b takes the fp16 absmax with bits b + 1 (every positive finite fp16), derives the
 // row scale s with dynamic_scale() and r = fp32(1 / s) as the kernel does, and runs every
@@ -11,8 +11,8 @@
 //   bad_scale:   1 when dynamic_scale(amax) != max(IEEE amax / 448, 1 / (448 * 512));
 //   uncorrected: y for which fp32(y * r) alone differs from y / s, which shows that the
 //                correction is needed and that the check sees a wrong quotient.
-#include "../csrc/fp8.h"
-#include "../csrc/norm_row.h"
+#include "../../tokenforge_amd/csrc/fp8.h"
+#include "../../tokenforge_amd/csrc/norm_row.h"
 
 namespace {
 

@@ -3,8 +3,7 @@
 GPU: the dynamic-scale quotient, y / s by Markstein's correction in fp32 followed by the
 v_med3 clamp and the packed e4m3 conversion, gives the codes of the IEEE fp32 division
 clamped and encoded by the torch-pinned encoder, for every positive finite fp16 absmax (every
-scale a row can hold) and every finite fp16 y of both signs (tfp_norm_quotient_check in the
-probes library). The same run counts the y for which the uncorrected product y * (1 / s)
+scale a row can hold) and every finite fp16 y of both signs (tfp_norm_quotient_check in this folder's norm_probes.hip). The same run counts the y for which the uncorrected product y * (1 / s)
 differs from y / s: a nonzero count shows the correction is needed and the check is not
 vacuous. The per-row divisions are checked on the CPU in tests/unit/test_norm_division.py.
 """
@@ -18,13 +17,13 @@ import pytest
 import torch
 
 ROOT = Path(__file__).resolve().parents[2]
-PROBES = ROOT / "tokenforge_amd" / "lib" / "libtokenforge_probes.so"
+PROBES = ROOT / "tests" / "gpu" / "lib" / "libtokenforge_norm_probes.so"
 
 
 @pytest.mark.gpu
 def test_dynamic_quotient_codes_exhaustive(device: torch.device) -> None:
     if not PROBES.exists():
-        pytest.fail(f"{PROBES} is missing: build it with `python -m tokenforge_amd.build`")
+        pytest.fail(f"{PROBES} is missing: build it with `python __graft_entry__.py build`")
     lib = ctypes.CDLL(str(PROBES))
     lib.tfp_norm_quotient_check.restype = ctypes.c_int
     lib.tfp_norm_quotient_check.argtypes = [ctypes.c_void_p] * 4

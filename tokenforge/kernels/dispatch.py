@@ -1,11 +1,10 @@
 """Pure-Python kernel dispatch (dispatch.py:1-104 in the reference).
 
-Two decisions, made at different times:
-
-* :func:`layer_support` runs once per layer at weight-load time. An unsupported layer is
-  left to the caller's own method and increments ``tokenforge_fallback_total{reason}``.
-* :func:`select` runs per call on (M, backend) only. It reads shapes, never tensor values,
-  so it is safe inside HIP-graph capture and opaque to torch.compile.
+:func:`layer_support` is consulted when a layer's weights are loaded: it says whether this
+path can serve the layer at all, and a layer it turns down stays with the caller's own linear
+method (counted in ``tokenforge_fallback_total{reason}``). :func:`select` is consulted on every
+call and looks only at M and the backend string. Since it never reads tensor contents, a
+call through it can be captured into a HIP graph or traced by torch.compile.
 
 There is one device path: hand-written HIP kernels for gfx950. ``backend`` keeps the
 reference's string argument; ``"hip"`` is canonical and the reference's ``"triton"`` and

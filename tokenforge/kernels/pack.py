@@ -33,32 +33,32 @@ import torch
 from tokenforge.kernels.hip import layout as _layout
 
 AWQ_ORDER: tuple[int, ...] = (0, 2, 4, 6, 1, 3, 5, 7)
-"""Nibble ``i`` of a packed word holds offset ``AWQ_ORDER[i]``."""
+"""``AWQ_ORDER[i]`` is the column offset (0..7) stored in bits ``4i..4i+3`` of an AWQ word."""
 
 AWQ_REVERSE_ORDER: tuple[int, ...] = (0, 4, 1, 5, 2, 6, 3, 7)
-"""Offset ``j`` lives in nibble ``AWQ_REVERSE_ORDER[j]``. Equals ``(j % 2) * 4 + j // 2``."""
+"""The nibble that stores column offset ``j``: the inverse permutation, ``(j % 2) * 4 + j // 2``."""
 
 PACK_FACTOR = 8
 SUPPORTED_GROUP_SIZES: tuple[int, ...] = (32, 64, 128)
 
 
 def pack_int4(values: torch.Tensor) -> torch.Tensor:
-    """Pack unsigned 4-bit values along the last dim into int32 words, AWQ interleave."""
+    """Eight 4-bit values of the last dimension per int32 word, placed in the AWQ nibble order."""
     return _layout.pack_int4(values)
 
 
 def unpack_int4(packed: torch.Tensor) -> torch.Tensor:
-    """Inverse of :func:`pack_int4`. Returns int32 values in [0, 15]."""
+    """Every nibble of every word back in column order, as int32 in [0, 15] (undoes :func:`pack_int4`)."""
     return _layout.unpack_int4(packed)
 
 
 def awq_pack(intweight: torch.Tensor, zeros: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    """Pack ``intweight [K, N]`` and ``zeros [K // G, N]`` (both in [0, 15]) into AWQ format."""
+    """AWQ ``(qweight, qzeros)`` from 4-bit ``intweight [K, N]`` and ``zeros [K // G, N]``."""
     return pack_int4(intweight), pack_int4(zeros)
 
 
 def awq_unpack(qweight: torch.Tensor) -> torch.Tensor:
-    """AWQ ``qweight [K, N // 8]`` -> int32 ``[K, N]``. Also works for ``qzeros``."""
+    """The 4-bit values of an AWQ ``qweight [K, N // 8]`` (or ``qzeros``) as int32 ``[K, N]``."""
     return unpack_int4(qweight)
 
 
@@ -94,14 +94,14 @@ def repack_awq_to_tf(qweight: torch.Tensor) -> torch.Tensor:
 
 
 def repack_tf_to_awq(qweight_t: torch.Tensor) -> torch.Tensor:
-    """Inverse of :func:`repack_awq_to_tf`."""
+    """TokenForge ``qweight_t [N, K // 8]`` back to AWQ ``qweight [K, N // 8]`` (bit-exact)."""
     return _layout.tf_to_awq(qweight_t)
 
 
 def validate_awq(
     qweight: torch.Tensor, qzeros: torch.Tensor, scales: torch.Tensor, group_size: int
 ) -> None:
-    """Raise ``ValueError`` with a precise reason if tensors are not a valid AWQ layer."""
+    """Check shapes, dtypes and group size of one AWQ layer; ``ValueError`` names the first violation."""
     if qweight.dtype != torch.int32 or qzeros.dtype != torch.int32:
         raise ValueError("qweight and qzeros must be int32")
     if scales.dtype != torch.float16:
@@ -147,6 +147,6 @@ def dequantize_tf(weights: W4A16Weights) -> torch.Tensor:
 def awq_dequantize(
     qweight: torch.Tensor, qzeros: torch.Tensor, scales: torch.Tensor, group_size: int
 ) -> torch.Tensor:
-    """AWQ format -> fp16 ``[K, N]`` with the single-rounding rule shared by every kernel."""
+    """fp16 ``[K, N]`` weights of an AWQ layer, each ``fp16(q - z) * s`` rounded once, as the kernels do."""
     w = pack_awq(qweight, qzeros, scales, group_size)
     return dequantize_tf(w).t().contiguous()

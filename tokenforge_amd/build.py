@@ -22,8 +22,6 @@ CSRC = PKG / "csrc"
 BUILD_DIR = PKG.parent / "_build"
 LIB_DIR = PKG / "lib"
 LIB_NAME = "libtokenforge_hip.so"
-PROBES = PKG / "probes"
-PROBE_LIB_NAME = "libtokenforge_probes.so"  # bench.py --probe only
 ARCH = "gfx950"
 
 # Packed-FP32 VALU forms are disabled: hipcc -O3 would otherwise emit v_pk_{add,mul,fma}_f32
@@ -70,25 +68,24 @@ def _link(cc: str, objects: list[Path], out: Path, verbose: bool) -> None:
     os.replace(tmp, out)
 
 
-def build(jobs: int | None = None, verbose: bool = False) -> Path:
-    """Compile every kernel source and link the shared library (and, separately, the
-    measurement probes' library, which the product never loads). Returns the library path."""
+def build_library(sources: list[Path], out: Path, jobs: int | None = None, verbose: bool = False,
+                  tag: str = "") -> Path:
+    """Compile ``sources`` (in parallel, objects under ``_build/`` prefixed with ``tag``) and
+    link them into the shared library ``out``."""
     cc = hipcc()
     BUILD_DIR.mkdir(parents=True, exist_ok=True)
-    LIB_DIR.mkdir(parents=True, exist_ok=True)
-    sources = sorted(CSRC.glob("*.hip"))
-    probe_sources = sorted(PROBES.glob("*.hip"))
-    objects = [BUILD_DIR / (s.stem + ".o") for s in sources]
-    probe_objects = [BUILD_DIR / ("probe_" + s.stem + ".o") for s in probe_sources]
-    cmds = [[cc, *HIPCC_FLAGS, "-c", str(s), "-o", str(o)]
-            for s, o in zip(sources + probe_sources, objects + probe_objects)]
+    out.parent.mkdir(parents=True, exist_ok=True)
+    objects = [BUILD_DIR / (tag + s.stem + ".o") for s in sources]
+    cmds = [[cc, *HIPCC_FLAGS, "-c", str(s), "-o", str(o)] for s, o in zip(sources, objects)]
     with ThreadPoolExecutor(max_workers=jobs or min(8, os.cpu_count() or 1)) as pool:
         list(pool.map(lambda c: _run(c, verbose), cmds))
-    out = LIB_DIR / LIB_NAME
     _link(cc, objects, out, verbose)
-    if probe_objects:
-        _link(cc, probe_objects, LIB_DIR / PROBE_LIB_NAME, verbose)
     return out
+
+
+def build(jobs: int | None = None, verbose: bool = False) -> Path:
+    """Compile every kernel source and link the product library. Returns its path."""
+    return build_library(sorted(CSRC.glob("*.hip")), LIB_DIR / LIB_NAME, jobs, verbose)
 
 
 def main() -> int:
