@@ -150,5 +150,5 @@ def test_missing_shard_and_empty_dir(tmp_path: Path) -> None:
 
 def test_load_needs_a_gpu(tmp_path: Path) -> None:
     write_checkpoint(tmp_path, layers=1)
-    with pytest.raises(HipUnavailableError, match="no CPU path"):
+    with pytest.raises(HipUnavailableError, match="on a gfx950 GPU"):
         ck.load_awq_checkpoint(tmp_path, device=torch.device("cpu"))

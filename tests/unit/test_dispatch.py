@@ -103,10 +103,12 @@ def test_select_without_gpu_is_the_reference_decision() -> None:
     assert (d.kernel, d.fallback) == ("hip_gemv", None)
 
 
-def test_torch_reference_decision_raises_at_the_op() -> None:
-    """This build has no CPU path: the op turns a torch_reference decision into an error."""
+def test_torch_reference_decision_raises_for_gpu_calls() -> None:
+    """A GPU call never falls back: a torch_reference decision on GPU tensors (library missing,
+    other GPU) is an error naming the library; host tensors take the ops' torch route before
+    this check is reached, and asking it for them is an error that says so."""
     d = dispatch.select(8, backend="hip", on_gpu=False, triton_ok=False)
-    with pytest.raises(dispatch.HipUnavailableError, match="CPU"):
+    with pytest.raises(dispatch.HipUnavailableError, match="host tensors"):
         dispatch.require_gpu_decision(d, on_gpu=False)
     d = dispatch.select(8, backend="hip", on_gpu=True, triton_ok=False)
     with pytest.raises(dispatch.HipUnavailableError, match="library"):

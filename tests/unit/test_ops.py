@@ -1,7 +1,8 @@
 """T0: op registration is torch.compile- and fake-tensor-safe (test_ops.py in the reference).
 
-Fake-tensor shape propagation runs on CPU; opcheck and torch.compile execute the real op,
-which needs the GPU (there is no CPU implementation behind the ops).
+Fake-tensor shape propagation runs on CPU; opcheck and torch.compile here execute the real op
+on GPU tensors, that is the HIP kernels (tests/unit/test_host_route.py runs the same checks on
+host tensors, through the ops' torch route).
 """
 
 from __future__ import annotations

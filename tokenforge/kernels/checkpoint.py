@@ -21,7 +21,8 @@ local disk, without vLLM:
    ones on the GPU (``pack.pack_awq``), then tunes every distinct (N, K) shape into the
    autotune cache file (``autotune.tune_layer``).
 
-There is no CPU path: step 3 raises for a non-GPU device.
+Step 3 runs on a gfx950 GPU (the layer support check and the tuning need one) and raises for
+a non-GPU device.
 """
 
 from __future__ import annotations
@@ -202,7 +203,7 @@ def load_awq_checkpoint(
 
     if device.type != "cuda":
         raise dispatch.HipUnavailableError(
-            f"AWQ checkpoints are repacked on a gfx950 GPU; got device {device} (this build has no CPU path)"
+            f"AWQ checkpoints are repacked and tuned on a gfx950 GPU; got device {device}"
         )
     cfg = read_quant_config(path)
     if cfg is not None and group_size is not None and group_size != cfg.group_size:

@@ -13,9 +13,10 @@ unchanged. ``"marlin"`` remains the per-layer kill switch.
 
 :func:`select` takes the reference's keywords (``on_gpu``, ``triton_ok``,
 ``cuda_ext_available``) and returns the reference's decision for a call that cannot run on
-the GPU: ``torch_reference``. This build has no CPU path behind that decision; the ops turn
-it into :class:`HipUnavailableError` naming the reason, so such a call fails loudly instead
-of running a slow fallback.
+the GPU: ``torch_reference``. For host tensors the ops follow it into the torch route
+(``tokenforge.kernels.host``), as the reference does. For GPU tensors it means the kernel
+library is missing or the GPU is not gfx950, and the ops raise :class:`HipUnavailableError`
+naming the reason: a GPU call fails loudly instead of running a slow fallback.
 """
 
 from __future__ import annotations
@@ -124,13 +125,14 @@ def select(
 
 
 def require_gpu_decision(decision: Decision, *, on_gpu: bool) -> None:
-    """Raise :class:`HipUnavailableError` for a ``torch_reference`` decision (no CPU path)."""
+    """Raise :class:`HipUnavailableError` for a ``torch_reference`` decision on a call the
+    kernels must run (the ops send host tensors to the torch route before asking)."""
     if decision.kernel != "torch_reference":
         return
     if not on_gpu:
         raise HipUnavailableError(
-            "tokenforge.kernels runs on gfx950 GPU tensors only; got a CPU tensor "
-            "(this build has no CPU path)"
+            "this call needs GPU tensors; host tensors take the ops' torch route "
+            "(tokenforge.kernels.host)"
         )
     raise HipUnavailableError(
         "the HIP kernel library is not loaded or the GPU is not gfx950 "

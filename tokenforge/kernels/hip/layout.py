@@ -3,15 +3,16 @@ layout permutation and the AWQ fixture quantizer.
 
 These run at weight-load time. They accept host tensors too (see
 ``_common.load_time_devices``): the kernel runs on the current GPU and the result comes back on
-the input's device.
+the input's device. With no GPU visible, host tensors take the torch route
+(``tokenforge.kernels.host``), which produces the same bits.
 """
 
 from __future__ import annotations
 
 import torch
 
-from tokenforge.kernels import _lib
-from tokenforge.kernels.hip._common import load_time_devices, on_device, require_gpu, stream_of
+from tokenforge.kernels import _lib, host
+from tokenforge.kernels.hip._common import host_route, load_time_devices, on_device, require_gpu, stream_of
 
 PACK_FACTOR = 8
 
@@ -24,6 +25,8 @@ def pack_int4(values: torch.Tensor) -> torch.Tensor:
     """
     if values.shape[-1] % PACK_FACTOR != 0:
         raise ValueError(f"last dim {values.shape[-1]} is not a multiple of {PACK_FACTOR}")
+    if host_route(values):
+        return host.pack_int4(values)
     run, home = load_time_devices("pack_int4", values)
     dev = require_gpu("pack_int4", values.to(run))
     *lead, n = values.shape
@@ -45,6 +48,8 @@ def unpack_int4(packed: torch.Tensor) -> torch.Tensor:
     """Inverse of :func:`pack_int4`. Returns int32 values in [0, 15] (pack.py:57-67)."""
     if packed.dtype != torch.int32:
         raise TypeError(f"packed tensor must be int32, got {packed.dtype}")
+    if host_route(packed):
+        return host.unpack_int4(packed)
     run, home = load_time_devices("unpack_int4", packed)
     p = packed.to(run).contiguous()
     dev = require_gpu("unpack_int4", p)
@@ -63,6 +68,8 @@ def _repack(src: torch.Tensor, forward: bool) -> torch.Tensor:
         raise TypeError(f"packed tensor must be int32, got {src.dtype}")
     if src.dim() != 2:
         raise ValueError(f"packed weight must be 2-D, got shape {tuple(src.shape)}")
+    if host_route(src):
+        return host.transpose_packed(src)
     run, home = load_time_devices("repack", src)
     s = src.to(run).contiguous()
     dev = require_gpu("repack", s)
@@ -107,6 +114,8 @@ def _tile(qweight: torch.Tensor, scales: torch.Tensor, qzeros: torch.Tensor, gro
         raise ValueError(f"{name}: scales shape {tuple(scales.shape)} != {(k // group_size, n)}")
     if tuple(qzeros.shape) != (k // group_size, n // PACK_FACTOR):
         raise ValueError(f"{name}: qzeros shape {tuple(qzeros.shape)} != {(k // group_size, n // PACK_FACTOR)}")
+    if host_route(qweight, scales, qzeros):
+        return (host.tile_pack if to_tile else host.tile_unpack)(qweight, scales, qzeros, group_size)
     run, home = load_time_devices(name, qweight, scales, qzeros)
     qw, sc, qz = (t.to(run).contiguous() for t in (qweight, scales, qzeros))
     dev = require_gpu(name, qw, sc, qz)
@@ -145,6 +154,8 @@ def awq_quantize(weight: torch.Tensor, group_size: int) -> tuple[torch.Tensor, t
         raise ValueError(f"K={k} is not a multiple of group_size={group_size}")
     if n % PACK_FACTOR != 0:
         raise ValueError(f"N={n} is not a multiple of {PACK_FACTOR}")
+    if host_route(weight):
+        return host.awq_quantize(weight, group_size)
     run, home = load_time_devices("awq_quantize", weight)
     w = weight.to(device=run, dtype=torch.float32).contiguous()
     dev = require_gpu("awq_quantize", w)

@@ -51,12 +51,8 @@ def rmsnorm_fp8_quant_dequant(
     return q, s, a
 
 
-def _launch(
-    x: torch.Tensor, weight: torch.Tensor, eps: float, scale: torch.Tensor | None, dequant: bool,
-    form: str = "auto",
-) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor | None]:
-    if form not in FORMS:
-        raise ValueError(f"form must be one of {sorted(FORMS)}, got {form!r}")
+def check_inputs(x: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor | None) -> tuple[int, int]:
+    """Shape, layout and dtype checks of the norm; returns ``(T, H)``."""
     if x.dim() != 2:
         raise ValueError(f"x must be 2-D [T, H], got {tuple(x.shape)}")
     t, h = x.shape
@@ -68,6 +64,16 @@ def _launch(
         raise TypeError(f"x and weight must be fp16, got {x.dtype} and {weight.dtype}")
     if scale is not None and (scale.numel() != 1 or scale.dtype != torch.float32):
         raise ValueError("static scale must be a single fp32 element")
+    return t, h
+
+
+def _launch(
+    x: torch.Tensor, weight: torch.Tensor, eps: float, scale: torch.Tensor | None, dequant: bool,
+    form: str = "auto",
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor | None]:
+    if form not in FORMS:
+        raise ValueError(f"form must be one of {sorted(FORMS)}, got {form!r}")
+    t, h = check_inputs(x, weight, scale)
     dev = require_gpu("rmsnorm_fp8_quant", x, weight, *(() if scale is None else (scale,)))
     weight = weight.contiguous()
     out = torch.empty((t, h), dtype=torch.float8_e4m3fn, device=dev)

@@ -91,6 +91,73 @@ def w4a16_gemm(
     return w4a16_gemm_ex(x, qweight_t, scales, qzeros, group_size, config, bias)
 
 
+def _check_epilogue(m: int, n: int, epilogue: str,
+                    residual: torch.Tensor | None) -> torch.Tensor | None:
+    if epilogue not in EPILOGUES:
+        raise ValueError(f"epilogue must be one of {sorted(EPILOGUES)}, got {epilogue!r}")
+    if epilogue == "residual":
+        if residual is None or tuple(residual.shape) != (m, n) or residual.dtype != torch.float16:
+            raise ValueError(f"the residual epilogue needs an fp16 residual of shape {(m, n)}")
+        if residual.stride(-1) != 1:
+            residual = residual.contiguous()
+    elif residual is not None:
+        raise ValueError("residual is only used by the residual epilogue")
+    if epilogue == "silu_mul" and n % 16:
+        raise ValueError(f"the silu_mul epilogue needs N to be a multiple of 16, got {n}")
+    return residual
+
+
+def check_linear_args(
+    x: torch.Tensor,
+    qweight_t: torch.Tensor,
+    scales: torch.Tensor,
+    qzeros: torch.Tensor,
+    group_size: int,
+    bias: torch.Tensor | None,
+    epilogue: str,
+    residual: torch.Tensor | None,
+) -> tuple[int, int, int, torch.Tensor | None, torch.Tensor | None]:
+    """Every check of the W4A16 linear with an epilogue, on any device; returns ``(M, N, K)``
+    and the bias and residual as the kernel reads them (contiguous along N)."""
+    m, n, k = _check_inputs(x, qweight_t, scales, qzeros, group_size)
+    if bias is not None:
+        if tuple(bias.shape) != (n,):
+            raise ValueError(f"bias shape {tuple(bias.shape)} != {(n,)}")
+        if bias.dtype != torch.float16:
+            raise TypeError(f"bias must be fp16, got {bias.dtype}")
+        bias = bias.contiguous()
+    return m, n, k, bias, _check_epilogue(m, n, epilogue, residual)
+
+
+def check_w4a8_args(
+    x8: torch.Tensor,
+    x_scale: torch.Tensor,
+    qweight_t: torch.Tensor,
+    scales: torch.Tensor,
+    qzeros: torch.Tensor,
+    group_size: int,
+    bias: torch.Tensor | None,
+    epilogue: str,
+    residual: torch.Tensor | None,
+) -> tuple[int, int, int, torch.Tensor | None, torch.Tensor | None]:
+    """Every check of the W4A8 linear, on any device; returns as :func:`check_linear_args`."""
+    if x8.dim() != 2:
+        raise ValueError(f"x8 must be 2-D [M, K], got shape {tuple(x8.shape)}")
+    if x8.dtype != torch.float8_e4m3fn:
+        raise TypeError(f"x8 must be float8_e4m3fn, got {x8.dtype}")
+    m, k = x8.shape
+    n = qweight_t.shape[0]
+    # Shape checks of the fp16 path on a stand-in of x's shape.
+    _check_inputs(torch.empty((m, k), dtype=torch.float16, device="meta"), qweight_t, scales, qzeros, group_size)
+    if bias is not None:
+        if tuple(bias.shape) != (n,) or bias.dtype != torch.float16:
+            raise ValueError(f"bias must be fp16 of shape {(n,)}")
+        bias = bias.contiguous()
+    residual = _check_epilogue(m, n, epilogue, residual)
+    _row_scales(x_scale, m)
+    return m, n, k, bias, residual
+
+
 def w4a16_gemm_ex(
     x: torch.Tensor,
     qweight_t: torch.Tensor,
@@ -110,25 +177,8 @@ def w4a16_gemm_ex(
     * ``"silu_mul"``: ``silu(y[:, :N/2]) * y[:, N/2:]`` -> ``[M, N/2]`` (torch's fp16 silu and
       multiply on the fp16 ``y``); N a multiple of 16.
     """
-    m, n, k = _check_inputs(x, qweight_t, scales, qzeros, group_size)
+    m, n, k, bias, residual = check_linear_args(x, qweight_t, scales, qzeros, group_size, bias, epilogue, residual)
     config.validate(group_size)
-    if epilogue not in EPILOGUES:
-        raise ValueError(f"epilogue must be one of {sorted(EPILOGUES)}, got {epilogue!r}")
-    if bias is not None:
-        if tuple(bias.shape) != (n,):
-            raise ValueError(f"bias shape {tuple(bias.shape)} != {(n,)}")
-        if bias.dtype != torch.float16:
-            raise TypeError(f"bias must be fp16, got {bias.dtype}")
-        bias = bias.contiguous()
-    if epilogue == "residual":
-        if residual is None or tuple(residual.shape) != (m, n) or residual.dtype != torch.float16:
-            raise ValueError(f"the residual epilogue needs an fp16 residual of shape {(m, n)}")
-        if residual.stride(-1) != 1:
-            residual = residual.contiguous()
-    elif residual is not None:
-        raise ValueError("residual is only used by the residual epilogue")
-    if epilogue == "silu_mul" and n % 16:
-        raise ValueError(f"the silu_mul epilogue needs N to be a multiple of 16, got {n}")
     tensors = (x, qweight_t, scales, qzeros) + tuple(t for t in (bias, residual) if t is not None)
     dev = require_gpu("w4a16_gemm", *tensors)
     n_out = n // 2 if epilogue == "silu_mul" else n
@@ -153,13 +203,9 @@ def w4a16_gemm_ex(
     return out
 
 
-def w4a16_dequant(
-    qweight_t: torch.Tensor,
-    scales: torch.Tensor,
-    qzeros: torch.Tensor,
-    group_size: int,
-) -> torch.Tensor:
-    """TokenForge layout -> fp16 ``[N, K]`` (w4a16.py:235-264), bit-exact with dequantize_tf."""
+def check_dequant_inputs(qweight_t: torch.Tensor, scales: torch.Tensor, qzeros: torch.Tensor,
+                         group_size: int) -> tuple[int, int]:
+    """The dequant kernel's dtype and shape checks; returns ``(N, K)``."""
     n = qweight_t.shape[0]
     k = qweight_t.shape[1] * 8
     if qweight_t.dtype != torch.int32 or qzeros.dtype != torch.int32:
@@ -172,6 +218,17 @@ def w4a16_dequant(
         raise ValueError(f"scales shape {tuple(scales.shape)} != {(k // group_size, n)}")
     if tuple(qzeros.shape) != (k // group_size, n // 8):
         raise ValueError(f"qzeros shape {tuple(qzeros.shape)} != {(k // group_size, n // 8)}")
+    return n, k
+
+
+def w4a16_dequant(
+    qweight_t: torch.Tensor,
+    scales: torch.Tensor,
+    qzeros: torch.Tensor,
+    group_size: int,
+) -> torch.Tensor:
+    """Tile-layout weights -> fp16 ``[N, K]`` (w4a16.py:235-264), bit-exact with dequantize_tf."""
+    n, k = check_dequant_inputs(qweight_t, scales, qzeros, group_size)
     dev = require_gpu("w4a16_dequant", qweight_t, scales, qzeros)
     qweight_t, scales, qzeros = (t.contiguous() for t in (qweight_t, scales, qzeros))
     out = torch.empty((n, k), dtype=torch.float16, device=dev)
@@ -213,30 +270,9 @@ def w4a8_gemm_ex(
     """W4A8: ``x_scale[m] * (e4m3(x8) @ dequant(W)^T) (+ bias)`` -> fp16, with the epilogues of
     :func:`w4a16_gemm_ex` (``tf_w4a8_linear_ex``). ``x8`` float8_e4m3fn ``[M, K]`` (as
     ``rmsnorm_fp8_quant`` returns it), ``x_scale`` fp32 with one value or one per row."""
-    if x8.dim() != 2:
-        raise ValueError(f"x8 must be 2-D [M, K], got shape {tuple(x8.shape)}")
-    if x8.dtype != torch.float8_e4m3fn:
-        raise TypeError(f"x8 must be float8_e4m3fn, got {x8.dtype}")
-    m, k = x8.shape
-    n = qweight_t.shape[0]
-    # Shape checks of the fp16 path on a stand-in of x's shape.
-    _check_inputs(torch.empty((m, k), dtype=torch.float16, device="meta"), qweight_t, scales, qzeros, group_size)
+    m, n, k, bias, residual = check_w4a8_args(x8, x_scale, qweight_t, scales, qzeros, group_size, bias, epilogue,
+                                              residual)
     config.validate(group_size)
-    if epilogue not in EPILOGUES:
-        raise ValueError(f"epilogue must be one of {sorted(EPILOGUES)}, got {epilogue!r}")
-    if bias is not None:
-        if tuple(bias.shape) != (n,) or bias.dtype != torch.float16:
-            raise ValueError(f"bias must be fp16 of shape {(n,)}")
-        bias = bias.contiguous()
-    if epilogue == "residual":
-        if residual is None or tuple(residual.shape) != (m, n) or residual.dtype != torch.float16:
-            raise ValueError(f"the residual epilogue needs an fp16 residual of shape {(m, n)}")
-        if residual.stride(-1) != 1:
-            residual = residual.contiguous()
-    elif residual is not None:
-        raise ValueError("residual is only used by the residual epilogue")
-    if epilogue == "silu_mul" and n % 16:
-        raise ValueError(f"the silu_mul epilogue needs N to be a multiple of 16, got {n}")
     x_scale, xs_stride = _row_scales(x_scale, m)
     tensors = (x8, x_scale, qweight_t, scales, qzeros) + tuple(t for t in (bias, residual) if t is not None)
     dev = require_gpu("w4a8_gemm", *tensors)

@@ -36,9 +36,10 @@ and the decode norm-then-linear in one launch (no counterpart either):
   from ``rmsnorm_fp8_quant_dequant(x, norm_weight, eps, None)``; one kernel where the bucket's
   config is the GEMV stream form (M <= 4), the two kernels otherwise; same bits either way.
 
-All
-run hand-written HIP kernels; a CPU tensor or a missing kernel library raises instead of
-falling back.
+On GPU tensors every op runs the hand-written HIP kernels, and a missing kernel library (or
+a GPU other than gfx950) raises instead of falling back. Host (CPU) tensors take the
+reference's ``torch_reference`` route (ops.py:79-81): the torch expressions of
+``tokenforge.kernels.host``, the same arithmetic the reference runs on the host.
 """
 
 from __future__ import annotations
@@ -48,7 +49,7 @@ import functools
 
 import torch
 
-from tokenforge.kernels import _lib, autotune, dispatch
+from tokenforge.kernels import _lib, autotune, dispatch, host
 from tokenforge.kernels.config import (
     MAX_BUCKET_M,
     NUM_CUS,
@@ -68,12 +69,29 @@ def _gpu_id(device: torch.device) -> str:
     return gpu_identity(device)
 
 
-def _decide(x2: torch.Tensor, m: int, n: int, k: int, group_size: int, backend: str) -> GemmConfig:
-    """Dispatch decision (the reference's ``select`` keywords) and the bucket's launch config.
+def _on_host(op: str, *tensors: torch.Tensor | None) -> bool:
+    """Whether a call takes the torch route: its tensors are host tensors. A call that mixes
+    host and GPU tensors raises."""
+    on_host = [t.device.type == "cpu" for t in tensors if t is not None]
+    if not any(on_host):
+        return False
+    if not all(on_host):
+        raise ValueError(f"{op}: all tensors must be on one device (got host and GPU tensors)")
+    return True
 
-    A ``torch_reference`` decision (CPU tensor, library missing, other GPU) raises: this build
-    has no CPU path. The tuned config may pick the other kernel family in the buckets both
-    serve; the counter records the family that runs.
+
+def _record_host(m: int, backend: str) -> None:
+    """The reference's decision for a host call (``torch_reference``), counted like any other."""
+    dispatch.record(dispatch.select(m, backend=backend, on_gpu=False))  # type: ignore[arg-type]
+
+
+def _decide(x2: torch.Tensor, m: int, n: int, k: int, group_size: int, backend: str) -> GemmConfig:
+    """Dispatch decision (the reference's ``select`` keywords) and the bucket's launch config
+    for a call on GPU tensors.
+
+    A ``torch_reference`` decision here (library missing, other GPU) raises: GPU tensors never
+    fall back. The tuned config may pick the other kernel family in the buckets both serve;
+    the counter records the family that runs.
     """
     decision = dispatch.select(
         m,
@@ -122,12 +140,16 @@ def _linear(
             f"backend must be 'hip' (or its aliases 'triton', 'cuda') at op level, got {backend!r}"
         )
 
-    cfg = _decide(x2, m, n, k, group_size, backend)
     r2 = None
     if residual is not None:
         if tuple(residual.shape) != (*x.shape[:-1], n):
             raise ValueError(f"residual shape {tuple(residual.shape)} != {(*x.shape[:-1], n)}")
         r2 = residual.reshape(-1, n)
+    if _on_host("w4a16_linear", x2, qweight_t, scales, qzeros, bias, r2):
+        _, _, _, bias, r2 = _w4a16.check_linear_args(x2, qweight_t, scales, qzeros, group_size, bias, epilogue, r2)
+        _record_host(m, backend)
+        return host.linear(x2, qweight_t, scales, qzeros, bias, group_size, epilogue, r2).reshape(out_shape)
+    cfg = _decide(x2, m, n, k, group_size, backend)
     y = _w4a16.w4a16_gemm_ex(x2, qweight_t, scales, qzeros, group_size, cfg, bias, epilogue, r2)
     return y.reshape(out_shape)
 
@@ -240,6 +262,13 @@ def w4a8_linear(
         raise ValueError(
             f"backend must be 'hip' (or its aliases 'triton', 'cuda') at op level, got {backend!r}"
         )
+    if _on_host("w4a8_linear", x2, x_scale, qweight_t, scales, qzeros, bias, residual):
+        r2 = residual.reshape(-1, n) if residual is not None else None
+        _, _, _, bias, r2 = _w4a16.check_w4a8_args(x2, x_scale, qweight_t, scales, qzeros, group_size, bias,
+                                                   epilogue, r2)
+        _record_host(m, backend)
+        y = host.w4a8_linear(x2, x_scale.reshape(-1), qweight_t, scales, qzeros, bias, group_size, epilogue, r2)
+        return y.reshape(out_shape)
     cfg = _decide(x2, m, n, k, group_size, backend)
     bucket = dispatch.lookup_bucket(m)
     if cfg.family == "gemm" and fp8_gemm_applies(bucket, n, k, group_size):
@@ -278,6 +307,9 @@ def _w4a8_linear_fake(
 def w4a16_dequant(
     qweight_t: torch.Tensor, scales: torch.Tensor, qzeros: torch.Tensor, group_size: int
 ) -> torch.Tensor:
+    if _on_host("w4a16_dequant", qweight_t, scales, qzeros):
+        _w4a16.check_dequant_inputs(qweight_t, scales, qzeros, group_size)
+        return host.dequantize(qweight_t, scales, qzeros, group_size)
     return _w4a16.w4a16_dequant(qweight_t, scales, qzeros, group_size)
 
 
@@ -296,7 +328,11 @@ def rmsnorm_fp8_quant(
     x2 = x.reshape(-1, h)
     if x2.stride(-1) != 1:
         x2 = x2.contiguous()
-    q, s = _rms.rmsnorm_fp8_quant(x2, weight, eps, scale)
+    if _on_host("rmsnorm_fp8_quant", x2, weight, scale):
+        _rms.check_inputs(x2, weight, scale)
+        q, s = host.rmsnorm_fp8_quant(x2, weight, eps, scale)
+    else:
+        q, s = _rms.rmsnorm_fp8_quant(x2, weight, eps, scale)
     if scale is not None:
         s = s.clone()  # custom ops may not return an alias of an input
     return q.reshape(x.shape), s.reshape((*x.shape[:-1], 1)) if scale is None else s
@@ -322,7 +358,11 @@ def rmsnorm_fp8_quant_dequant(
     x2 = x.reshape(-1, h)
     if x2.stride(-1) != 1:
         x2 = x2.contiguous()
-    q, s, a = _rms.rmsnorm_fp8_quant_dequant(x2, weight, eps, scale)
+    if _on_host("rmsnorm_fp8_quant_dequant", x2, weight, scale):
+        _rms.check_inputs(x2, weight, scale)
+        q, s, a = host.rmsnorm_fp8_quant_dequant(x2, weight, eps, scale)
+    else:
+        q, s, a = _rms.rmsnorm_fp8_quant_dequant(x2, weight, eps, scale)
     if scale is not None:
         s = s.clone()  # custom ops may not return an alias of an input
     return q.reshape(x.shape), s.reshape((*x.shape[:-1], 1)) if scale is None else s, a.reshape(x.shape)
@@ -368,6 +408,12 @@ def rmsnorm_fp8_w4a16_linear(
         raise ValueError(
             f"backend must be 'hip' (or its aliases 'triton', 'cuda') at op level, got {backend!r}"
         )
+    if _on_host("rmsnorm_fp8_w4a16_linear", x2, norm_weight, qweight_t, scales, qzeros, bias):
+        _rms.check_inputs(x2, norm_weight, None)
+        _, _, a = host.rmsnorm_fp8_quant_dequant(x2, norm_weight, eps, None)
+        _, _, _, bias, _ = _w4a16.check_linear_args(a, qweight_t, scales, qzeros, group_size, bias, epilogue, None)
+        _record_host(m, backend)
+        return host.linear(a, qweight_t, scales, qzeros, bias, group_size, epilogue).reshape(out_shape)
     cfg = _decide(x2, m, n, k, group_size, backend)
     if cfg.stream and stream_form_applies(m, n, k, cfg.num_warps, norm=True):
         y = _w4a16.rmsnorm_fp8_w4a16_gemm_ex(

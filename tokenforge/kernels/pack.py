@@ -21,7 +21,8 @@ Dequantization is ``w[k, n] = fp16(q[k, n] - z[k // G, n]) * s[k // G, n]`` (one
 Every tensor-producing function runs a HIP kernel on a gfx950 GPU. These are load-time
 functions, so they also accept host tensors (as the reference's callers pass them): the
 inputs are copied to the current GPU, the kernel runs there, and the results come back on
-the inputs' device. Without a visible GPU they raise; there is no CPU implementation here.
+the inputs' device. Without a visible GPU, host tensors take the torch route
+(``tokenforge.kernels.host``), which gives the same bits.
 """
 
 from __future__ import annotations
@@ -136,9 +137,12 @@ def unpack_to_awq(weights: W4A16Weights) -> tuple[torch.Tensor, torch.Tensor, to
 
 def dequantize_tf(weights: W4A16Weights) -> torch.Tensor:
     """Tile-layout weights -> fp16 ``[N, K]`` (the ``nn.Linear.weight`` layout)."""
-    from tokenforge.kernels.hip._common import load_time_devices
+    from tokenforge.kernels import host
+    from tokenforge.kernels.hip._common import host_route, load_time_devices
     from tokenforge.kernels.hip.w4a16 import w4a16_dequant
 
+    if host_route(weights.qweight_t, weights.scales, weights.qzeros):
+        return host.dequantize(weights.qweight_t, weights.scales, weights.qzeros, weights.group_size)
     run, home = load_time_devices("dequantize_tf", weights.qweight_t, weights.scales, weights.qzeros)
     qw, sc, qz = (t.to(run) for t in (weights.qweight_t, weights.scales, weights.qzeros))
     return w4a16_dequant(qw, sc, qz, weights.group_size).to(home)
