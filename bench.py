@@ -1,7 +1,8 @@
 """Benchmark of the MI355X quantized-linear hot path (one JSON result line on stdout).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--tune] [--no-cpu] [--detail PATH] [--full]
-                    [--stack | --no-stack]
+                    [--no-stack] [--check] [--update-baseline [PATH] --reason TEXT]
+    python bench.py --fingerprint        (the environment fingerprint of this checkout)
     python bench.py --traffic-probe      (eager launches for rocprofv3 --pmc, see below)
     python bench.py --mfma-probe         (the M=256 GEMMs, for rocprofv3 --pmc)
     python bench.py --kernel-probe       (eager launches of every timed kernel, for rocprofv3)
@@ -45,8 +46,10 @@ Extra objects on the same JSON line:
   what those counter passes measure: every candidate in turn on the rotating cold copies, then
   the calibration kernel (torch.neg, 256 MiB in and out); ``--traffic-summary FETCH_DIR
   WRITE_DIR PROBE_LOG`` turns the two counter runs into that summary.
-* ``gemm_m256`` and ``gemm_m1024_m4096``: the prefill GEMM at M=256, 1024 and 4096 on gate_up
-  and down, TFLOP/s and fraction of the 2.5 PFLOP/s fp16 dense MFMA peak.
+* ``gemm_small_m``, ``gemm_m256`` and ``gemm_m1024_m4096``: the GEMM at M = 16,
+  32, 64, 128, 256, 1024 and 4096 on gate_up and down (x ~ N(0, 1) fp16 with 1% of the rows
+  scaled by 10), TFLOP/s and fraction of the 2.5 PFLOP/s fp16 dense MFMA peak; each entry is
+  the whole op (a split-K launch and its reduce kernel are both in the graph).
 * ``gemm_w4a8_fp8``: the W4A8 linear at the same M and shapes on e4m3 activations with per-row
   scales, run by the fp8-MFMA GEMM the op picks there (``fp8_gemm_config``), TFLOP/s against
   the 2.5 PF fp16 and 5 PF fp8 dense peaks.
@@ -55,7 +58,16 @@ Extra objects on the same JSON line:
 * ``device_copy_gbps``: the box's achievable bandwidth of a plain device copy (torch, 1 GiB
   read and written), read + write bytes per second, next to the 8 TB/s peak.
 * ``per_shape`` and ``gemv_m2_m4``: the GEMV on each of the four shapes at
-  M = 1, and at M = 2 and 4 (buckets 2 and 4 autotuned), average launch duration and GB/s.
+  M = 1, and at M = 2 and 4 (buckets 2 and 4 autotuned), average launch duration and GB/s;
+  ``gemv_m8_m32``: the same four shapes at M = 8 and 32, the rest of the reference's l4 suite
+  (micro.py:58, M in {1, 8, 32}).
+* ``vendor_fp16``: the vendor's dense fp16 linear beside them, as micro.py:110-114 runs
+  ``cublas-fp16`` beside every case: ``torch.nn.functional.linear`` with fp16 weights
+  (hipBLASLt) on the four shapes at M in {1, 8, 32} and on gate_up and down at M = 256, 1024
+  and 4096, weights rotating over >= 1.1 GB of copies; GB/s with the dense byte count.
+* ``eager_op``: the M=1 op called eagerly, back to back, without a graph (micro.py:67-79's
+  method): per call, the stream's time (HIP events) and the host's time to issue it, for the
+  custom op and for the launcher under it.
 * ``rmsnorm_fp8``: the fused RMSNorm + e4m3fn quant (configs[1]: H=3584, eight outlier
   channels x20, gamma = 1 + 0.1 N(0,1), eps 1e-6, dynamic per-token scale) at T in
   {1, 16, 512, 4096}; algorithmic bytes T*H*2 + H*2 + T*H + 4*T over rotating cold inputs;
@@ -79,13 +91,23 @@ Extra objects on the same JSON line:
   gate_up take the FP8 codes and scales directly as W4A8 linears ("w4a8", no fp16(q * scale)
   glue; not bit-equal: the scale multiplies each row's sum instead of each element; from M = 128
   these run on the fp8-MFMA GEMM, which also applies the group scale exactly). A pass
-  is one HIP graph, tokens/s = M / time per pass. M=1 on every run; ``--stack`` or ``--full``
-  add M in {8, 32} (decode) and 2048 (prefill).
+  is one HIP graph, tokens/s = M / time per pass, at M in {1, 8, 32} (decode) and 2048
+  (prefill).
 * ``cpu_baseline``: reference.py's CPU path (dequantize per call + fp32 matmul), restated in
   torch on the host cores (``oracle/cpu_path.py``), on a bounded sample of the same step, with
   the host CPU's model name and the threads used. The same restatements are timed beside the
-  M=256 GEMMs (``gemm_m256[i].cpu``), the RMSNorm + FP8 at T=4096 (``rmsnorm_fp8[..].cpu``) and
-  the repack (``repack_gate_up.cpu``).
+  M=16 and M=256 GEMMs (``gemm_small_m[i].cpu``, ``gemm_m256[i].cpu``), the M=8 decode step
+  (``cpu_decode_m8``), the RMSNorm + FP8 at T=4096 (``rmsnorm_fp8[..].cpu``) and the repack
+  (``repack_gate_up.cpu``). The stack has none: one CPU pass of 28 layers takes ~12 s per token.
+* ``env``: the environment fingerprint (env.py:51-85): git commit and dirty flag (null in a
+  copy without ``.git``, such as the GPU box's), the sha256 code-tree hash of the sources under
+  ``CODE_PATHS`` (``--fingerprint`` prints it for a checkout), torch, HIP, the library's ABI,
+  the GPU.
+* ``regression``: every timed entry against the committed baseline for this GPU
+  (``bench_baseline.json``, written by ``--update-baseline --reason``; micro.py:140-181): the
+  entries more than 5% slower and the headline's ratio to the baseline's. ``--check`` exits 1
+  on a regression. The top-level ``vs_baseline`` stays null: it is reserved for a published
+  number for this metric, and the reference publishes none.
 """
 
 from __future__ import annotations
@@ -125,7 +147,15 @@ CALIB_BYTES = 256 << 20
 COPY_BYTES = 1 << 30
 MFMA_LAUNCHES = 8
 PREFILL_M = (256, 1024, 4096)
+SMALL_M = (16, 32, 64, 128)  # configs[3] below the prefill M
+DECODE_EXTRA_M = (8, 32)  # the reference's l4 suite (micro.py:58): M in {1, 8, 32}
 SWEEP_M = (16, 32, 64, 128, 256, 1024, 4096)
+STACK_M = (1, 8, 32, 2048)
+BASELINE_FILE = ROOT / "bench_baseline.json"
+REGRESSION = 0.05  # micro.py:30: an entry more than 5% slower than the committed baseline
+# Files whose content a bench line vouches for (the code-tree hash of the fingerprint).
+CODE_PATHS = ("bench.py", "__graft_entry__.py", "tokenforge", "tokenforge_amd", "include", "bench_probes")
+CODE_SUFFIXES = (".py", ".hip", ".h", ".json")
 NORM_H = 3584
 NORM_T = (1, 16, 512, 4096)
 
@@ -509,6 +539,107 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
+def _git(*args: str) -> str | None:
+    import subprocess
+
+    try:
+        out = subprocess.run(["git", *args], cwd=ROOT, check=True, capture_output=True, text=True, timeout=20)
+    except (OSError, subprocess.SubprocessError):
+        return None
+    return out.stdout.strip()
+
+
+def code_tree_hash() -> str:
+    """sha256 over the path and content of every source file under ``CODE_PATHS`` (sorted):
+    the same value wherever the tree is, including a copy without ``.git``."""
+    import hashlib
+
+    h = hashlib.sha256()
+    files = []
+    for top in CODE_PATHS:
+        p = ROOT / top
+        files += [p] if p.is_file() else [f for f in p.rglob("*") if f.is_file() and f.suffix in CODE_SUFFIXES
+                                          and "__pycache__" not in f.parts]
+    for f in sorted(files):
+        h.update(str(f.relative_to(ROOT)).encode() + b"\0" + f.read_bytes() + b"\0")
+    return h.hexdigest()
+
+
+def fingerprint() -> dict:  # type: ignore[type-arg]
+    """Environment of a bench line (env.py:51-85): commit, dirty flag and code-tree hash (the git
+    fields are null where the tree has no ``.git``, e.g. a copy on the GPU box; the tree hash
+    then ties the line to a commit: ``python bench.py --fingerprint`` in a checkout), software
+    versions, the kernel library's ABI and the device."""
+    import platform
+
+    fp = {"git_sha": _git("rev-parse", "HEAD"), "code_tree": code_tree_hash(), "python": platform.python_version(),
+          "torch": torch.__version__, "hip": torch.version.hip, "host_cpu": cpu_model()}
+    status = _git("status", "--porcelain", "--", *CODE_PATHS)
+    fp["git_dirty"] = None if status is None else bool(status)
+    try:
+        from tokenforge.kernels import _lib
+
+        fp["library_abi"] = _lib.ABI_VERSION
+    except ImportError:
+        fp["library_abi"] = None
+    if torch.cuda.is_available():
+        props = torch.cuda.get_device_properties(0)
+        fp["gpu"] = props.name
+        fp["arch"] = getattr(props, "gcnArchName", None)
+        fp["cus"] = props.multi_processor_count
+    return fp
+
+
+def timed_rows(result: dict) -> dict[str, float]:  # type: ignore[type-arg]
+    """Every timed entry of a bench line as ``impl|layer|m`` -> microseconds (micro.py:133)."""
+    rows: dict[str, float] = {}
+    for key in ("per_shape", "gemv_m2_m4", "gemv_m8_m32", "gemm_small_m", "gemm_m256", "gemm_m1024_m4096"):
+        for r in result.get(key) or ():
+            rows[f"hip|{r['layer']}|{r['m']}"] = r["us"]
+    for r in result.get("gemm_w4a8_fp8") or ():
+        rows[f"hip-fp8|{r['layer']}|{r['m']}"] = r["us"]
+    for r in result.get("rmsnorm_fp8") or ():
+        rows[f"hip|rmsnorm_fp8|{r['t']}"] = r["us"]
+    for r in result.get("vendor_fp16") or ():
+        rows[f"vendor-fp16|{r['layer']}|{r['m']}"] = r["us"]
+    for r in result.get("stack") or ():
+        rows[f"hip-stack|fused|{r['m']}"] = r["fused"]["ms_per_pass"] * 1e3
+    return rows
+
+
+def regression_check(result: dict, path: Path = BASELINE_FILE) -> dict | None:  # type: ignore[type-arg]
+    """Each timed entry against the committed baseline for this GPU (micro.py:140-156): the
+    entries more than 5% slower, and the headline value's ratio to the baseline's."""
+    if not path.exists():
+        return None
+    doc = json.loads(path.read_text()).get(result["gpu"])
+    if doc is None:
+        return {"baseline": path.name, "gpu": result["gpu"], "compared": 0, "note": "no baseline for this GPU"}
+    rows = timed_rows(result)
+    base = doc["us"]
+    slower = [{"entry": key, "us": us, "baseline_us": base[key], "slower_pct": 100 * (us / base[key] - 1)}
+              for key, us in sorted(rows.items()) if key in base and us > base[key] * (1 + REGRESSION)]
+    return {"baseline": path.name, "baseline_code_tree": doc.get("code_tree"), "baseline_reason": doc.get("reason"),
+            "compared": sum(key in base for key in rows), "threshold_pct": 100 * REGRESSION,
+            "regressions": slower, "pass": not slower, "value_vs_baseline": result["value"] / doc["value"]}
+
+
+def update_baseline(result: dict, reason: str, path: Path) -> None:  # type: ignore[type-arg]
+    """Write this line's timed entries as the baseline for its GPU (micro.py:170-181)."""
+    doc = json.loads(path.read_text()) if path.exists() else {}
+    doc[result["gpu"]] = {"reason": reason, "code_tree": result["env"]["code_tree"],
+                          "git_sha": result["env"]["git_sha"], "value": result["value"], "us": timed_rows(result)}
+    path.write_text(json.dumps(doc, indent=1, sort_keys=True) + "\n")
+
+
+def prefill_x(m: int, k: int, gen: torch.Generator, dev: torch.device) -> torch.Tensor:
+    """configs[3]'s activations: fp16 ~N(0, 1) with 1% of the rows (at least one) scaled by 10."""
+    x = torch.randn((m, k), generator=gen, device=dev)
+    rows = torch.randperm(m, generator=gen, device=dev)[: max(1, m // 100)]
+    x[rows] *= 10
+    return x.to(torch.float16)
+
+
 def make_layer(n: int, k: int, dev: torch.device, seed: int):  # type: ignore[no-untyped-def]
     """AWQ-format synthetic layer converted with the GPU repack -> (qweight_t, scales, qzeros)."""
     from tokenforge.kernels.pack import pack_awq, pack_int4
@@ -590,6 +721,69 @@ def rmsnorm_bench(dev: torch.device) -> tuple[list[dict], torch.Tensor]:  # type
             f"  [row/block {by_form['row_per_block']:.2f} us, row/wave {by_form['row_per_wave']:.2f} us]")
         del xs
     return res, gamma
+
+
+def vendor_bench(dev: torch.device, gen: torch.Generator) -> list[dict]:  # type: ignore[type-arg]
+    """The vendor's dense fp16 linear beside the library's calls (micro.py:110-114's
+    ``cublas-fp16`` impl: ``F.linear(x, W)`` with fp16 weights; on ROCm, hipBLASLt). Each of
+    the four shapes at M in {1, 8, 32} (the l4 suite), gate_up and down also at the prefill M;
+    the weights rotate over copies of at least 1.1 GB in all, so every launch reads them from
+    HBM. GB/s uses the reference's dense byte count (N·K·2 + M·K·2 + M·N·2)."""
+    res = []
+    for i, (name, n, k) in enumerate(SHAPES):
+        copies = max(2, int(-(-COLD_BYTES // (n * k * 2))))
+        ws = [(torch.randn((n, k), generator=gen, device=dev) * 0.02).to(torch.float16) for _ in range(copies)]
+        for m in (1,) + DECODE_EXTRA_M + (PREFILL_M if i in (2, 3) else ()):
+            x = torch.randn((m, k), generator=gen, device=dev).to(torch.float16)
+            launches = copies * (2 if m <= 256 else 1)
+            g, _ = capture([lambda r=r, x=x: torch.nn.functional.linear(x, ws[r % copies]) for r in range(launches)],
+                           warm=2)
+            ms = median_replay_ms(g, launches)
+            del g
+            moved = n * k * 2 + m * k * 2 + m * n * 2
+            res.append({"layer": name, "m": m, "n": n, "k": k, "us": ms * 1e3,
+                        "gbps": moved / (ms * 1e-3) / 1e9, "tflops": 2 * m * n * k / (ms * 1e-3) / 1e12,
+                        "impl": "torch.nn.functional.linear fp16 (hipBLASLt)"})
+            log(f"  vendor fp16   {name:13s} M={m:<5d} {ms * 1e3:9.2f} us {moved / (ms * 1e-3) / 1e9:7.0f} GB/s "
+                f"{2 * m * n * k / (ms * 1e-3) / 1e12:7.1f} TFLOP/s")
+        del ws
+        torch.cuda.empty_cache()
+    return res
+
+
+def eager_bench(layers: list, copies: int, xs: list, cfgs: list) -> list[dict]:  # type: ignore[type-arg]
+    """The op called eagerly (no graph), as micro.py:67-79 times it: per M=1 call on each shape,
+    back to back over the rotating copies. ``us_per_call`` is the stream's time per call (HIP
+    events around the loop), ``host_us_per_call`` the Python time to issue one; both for the
+    custom op (``torch.ops.tokenforge.w4a16_linear``: dispatch, bucket lookup, metrics, ctypes)
+    and for the launcher under it (``w4a16_gemm``: checks and ctypes only)."""
+    from tokenforge.kernels.hip.w4a16 import w4a16_gemm
+
+    ops = torch.ops.tokenforge
+    res = []
+    calls = 40 * copies
+    for i, (name, n, k) in enumerate(SHAPES):
+        row = {"layer": name, "m": 1}
+        for label, fn in (
+            ("op", lambda c: ops.w4a16_linear(xs[i], *layers[c][i], None, GROUP, "hip")),
+            ("launcher", lambda c: w4a16_gemm(xs[i], *layers[c][i], GROUP, cfgs[i])),
+        ):
+            for c in range(copies):
+                fn(c)
+            torch.cuda.synchronize()
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+            t0 = time.perf_counter()
+            for r in range(calls):
+                fn(r % copies)
+            host_s = time.perf_counter() - t0
+            end.record()
+            torch.cuda.synchronize()
+            row[label] = {"us_per_call": start.elapsed_time(end) * 1e3 / calls, "host_us_per_call": host_s * 1e6 / calls}
+        res.append(row)
+        log(f"  eager {name:13s} M=1 op {row['op']['us_per_call']:6.2f} us/call (host {row['op']['host_us_per_call']:5.2f}),"
+            f" launcher {row['launcher']['us_per_call']:6.2f} us/call (host {row['launcher']['host_us_per_call']:5.2f})")
+    return res
 
 
 STACK_LAYERS = 28
@@ -725,7 +919,8 @@ def cpu_baselines(layers_tf: list, gate_awq: torch.Tensor, norm_gamma: torch.Ten
     """reference.py's CPU path restated in torch on the host cores (oracle/cpu_path.py), on
     bounded samples of the benchmarked work: the M=1 decode step (the headline baseline), the
     M=256 GEMM of gate_up and down, the fused RMSNorm + FP8 at T=4096 and the AWQ -> TokenForge
-    repack of gate_up. ``layers_tf``: the four linears in the TokenForge layout on the host."""
+    repack of gate_up, and beside the added rows the M=8 decode step and the M=16 GEMMs.
+    ``layers_tf``: the four linears in the TokenForge layout on the host."""
     from oracle.cpu_path import repack_awq_to_tf_cpu, rmsnorm_fp8_torch_cpu, w4a16_torch_cpu
 
     threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
@@ -750,13 +945,24 @@ def cpu_baselines(layers_tf: list, gate_awq: torch.Tensor, norm_gamma: torch.Ten
                   f"matmul, reference.py:24-32 in torch), median of {runs} runs, {med * 1e3:.0f} ms/step",
         "ms_per_step": med * 1e3,
     }
+    xs8 = [torch.randn((8, k), generator=gen).half() for _, _, k in SHAPES]
+
+    def step8() -> None:
+        for (qw, sc, qz), x in zip(layers_tf, xs8):
+            w4a16_torch_cpu(x, qw, sc, qz, GROUP)
+
+    med, runs = _median_s(step8, 3, budget_s / 4)
+    decode_m8 = {"gbps": sum(bytes_moved(8, n, k) for _, n, k in SHAPES) / med / 1e9, "ms_per_step": med * 1e3,
+                 "runs": runs, "sample": "one M=8 step over the 4 linears"}
     gemm = {}
+    gemm16 = {}
     for i in (2, 3):
         name, n, k = SHAPES[i]
-        x = torch.randn((256, k), generator=gen).half()
         qw, sc, qz = layers_tf[i]
-        med, runs = _median_s(lambda: w4a16_torch_cpu(x, qw, sc, qz, GROUP), 3, budget_s / 2)
-        gemm[name] = {"tflops": 2 * 256 * n * k / med / 1e12, "ms": med * 1e3, "runs": runs}
+        for m, table, runs_max in ((256, gemm, 3), (16, gemm16, 2)):
+            x = torch.randn((m, k), generator=gen).half()
+            med, runs = _median_s(lambda x=x: w4a16_torch_cpu(x, qw, sc, qz, GROUP), runs_max, budget_s / 4)
+            table[name] = {"tflops": 2 * m * n * k / med / 1e12, "ms": med * 1e3, "runs": runs}
     t = NORM_T[-1]
     x = torch.randn((t, NORM_H), generator=gen)
     x[:, torch.randperm(NORM_H, generator=gen)[:8]] *= 20
@@ -769,6 +975,7 @@ def cpu_baselines(layers_tf: list, gate_awq: torch.Tensor, norm_gamma: torch.Ten
     repack = {"gvalues_per_s": n * k / med / 1e9, "gbps": n * k / med / 1e9, "ms": med * 1e3, "runs": runs}
     common = {"cores": out["cores"], "kind": "port", "cpu_model": model}
     return {"decode": out, "gemm_m256": {kk: dict(v, **common) for kk, v in gemm.items()},
+            "gemm_m16": {kk: dict(v, **common) for kk, v in gemm16.items()}, "decode_m8": dict(decode_m8, **common),
             "rmsnorm_t4096": dict(norm, **common), "repack_gate_up": dict(repack, **common)}
 
 
@@ -877,9 +1084,9 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--detail", type=str, default=None, help="write per-shape details as JSON")
     ap.add_argument("--full", action="store_true",
-                    help="also sweep the GEMM over M in {16..4096} (configs[3]) into --detail")
+                    help="also sweep the GEMM over M in {16..4096} on cold copies into --detail (gemm_sweep)")
     ap.add_argument("--stack", action="store_true",
-                    help="stack (configs[4]) also at M in {8, 32, 2048}, not only M=1")
+                    help="accepted for older command lines: the stack runs at M in {1, 8, 32, 2048} by default")
     ap.add_argument("--no-stack", action="store_true", help="skip the stack (configs[4])")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="eager gate_up GEMV launches + a calibration kernel, for rocprofv3 --pmc")
@@ -900,7 +1107,19 @@ def main() -> int:
     ap.add_argument("--probe", action="store_true",
                     help="memory floors of the GEMV's access patterns (bench_probes/lib/libtokenforge_read_probes.so), "
                          "next to the GEMV itself on the cached or default configs")
+    ap.add_argument("--check", action="store_true",
+                    help="exit 1 when an entry is more than 5%% slower than the committed baseline")
+    ap.add_argument("--update-baseline", metavar="PATH", nargs="?", const=str(BASELINE_FILE), default=None,
+                    help="write this run's timed entries as the baseline for its GPU (needs --reason)")
+    ap.add_argument("--reason", default="", help="why the baseline changes (with --update-baseline)")
+    ap.add_argument("--fingerprint", action="store_true", help="print the environment fingerprint and exit")
     args = ap.parse_args()
+    if args.fingerprint:
+        print(json.dumps(fingerprint()))
+        return 0
+    if args.update_baseline is not None and not args.reason:
+        print("--update-baseline needs --reason", file=sys.stderr)
+        return 2
     if args.stats_summary:
         return stats_summary(*args.stats_summary)
     if args.probe_summary:
@@ -1070,9 +1289,10 @@ def main() -> int:
         log(f"  {name:13s} M=1 {ms * 1e3:8.2f} us {gbps:7.0f} GB/s ({100 * gbps / HBM_PEAK_GBPS:.1f}% of 8 TB/s)")
     dom = per_shape[2]
 
-    # the GEMV at M = 2 and 4 on the four shapes (M = 1 is per_shape), tuned buckets.
+    # the GEMV at M = 2 and 4 on the four shapes (M = 1 is per_shape), and the
+    # reference's l4 suite's M = 8 and 32 (micro.py:58), with the tuned buckets' configs.
     gemv_m24 = []
-    for m in (2, 4):
+    for m in (2, 4) + DECODE_EXTRA_M:
         xm_all = [torch.randn((m, k), generator=gen, device=dev).to(torch.float16) for _, _, k in SHAPES]
         cfgm, srcm = zip(*(config(m, n, k) for _, n, k in SHAPES))
         for i, (name, n, k) in enumerate(SHAPES):
@@ -1085,14 +1305,18 @@ def main() -> int:
             log(f"  {name:13s} M={m} {ms * 1e3:8.2f} us {gbps:7.0f} GB/s ({100 * gbps / HBM_PEAK_GBPS:.1f}% of 8 TB/s)")
             del g
 
-    # Prefill GEMM at M = 256, 1024 and 4096 on gate_up and down.
+    gemv_m8_m32 = [r for r in gemv_m24 if r["m"] in DECODE_EXTRA_M]
+    gemv_m24 = [r for r in gemv_m24 if r["m"] not in DECODE_EXTRA_M]
+
+    # the GEMM at M = 16..128 and at the prefill M = 256, 1024 and 4096 on gate_up
+    # and down (activations with 1% of the rows scaled by 10).
     gemm = []
-    for m in PREFILL_M:
+    for m in SMALL_M + PREFILL_M:
         for i in (2, 3):
             name, n, k = SHAPES[i]
             cfg, src = config(m, n, k)
             xm = [None] * len(SHAPES)
-            xm[i] = torch.randn((m, k), generator=gen, device=dev).to(torch.float16)
+            xm[i] = prefill_x(m, k, gen, dev)
             launches = 2 * copies if m <= 256 else copies
             g, _ = capture([launcher(r % copies, i, xm, [cfg] * len(SHAPES)) for r in range(launches)])
             ms = median_replay_ms(g, launches)
@@ -1160,27 +1384,12 @@ def main() -> int:
                 log(f"  {name:13s} M={m:<5d} {ms * 1e3:9.2f} us {tflops:7.1f} TFLOP/s {gbps:7.0f} GB/s  {cfg}")
                 del g, xm
 
-    vendor = None
-    if args.full:
-        vendor = []
-        for i in (2, 3):
-            name, n, k = SHAPES[i]
-            wt = (torch.randn((k, n), generator=gen, device=dev) * 0.03).to(torch.float16)
-            for m in (256, 1024, 4096):
-                xm = torch.randn((m, k), generator=gen, device=dev).to(torch.float16)
-                om = torch.empty((m, n), device=dev, dtype=torch.float16)
-                g, _ = capture([lambda xm=xm, om=om: torch.matmul(xm, wt, out=om)] * 8, warm=2)
-                ms = median_replay_ms(g, 8)
-                tflops = 2 * m * n * k / (ms * 1e-3) / 1e12
-                vendor.append({"layer": name, "m": m, "n": n, "k": k, "us": ms * 1e3, "tflops": tflops,
-                               "frac_mfma": tflops / FP16_MFMA_PEAK_TFLOPS})
-                log(f"  vendor fp16   {name:13s} M={m:<5d} {ms * 1e3:9.2f} us {tflops:7.1f} TFLOP/s")
-                del g, xm, om
-            del wt
+    eager = eager_bench(layers, copies, xs, cfg1)
+    vendor = vendor_bench(dev, gen)
 
     stack = None
     if not args.no_stack:
-        stack = stack_bench(dev, gpu, (1, 8, 32, 2048) if (args.stack or args.full) else (1,), args.tune)
+        stack = stack_bench(dev, gpu, STACK_M, args.tune)
 
     gate_n, gate_k = SHAPES[2][1], SHAPES[2][2]
     repack = {"gvalues_per_s": gate_n * gate_k / (rep_ms * 1e-3) / 1e9,
@@ -1194,8 +1403,8 @@ def main() -> int:
         legs = cpu_baselines(layers_tf, gate_awq_host, norm_gamma.cpu())
         cpu = legs["decode"]
         for g in gemm:
-            if g["m"] == 256:
-                g["cpu"] = legs["gemm_m256"][g["layer"]]
+            if g["m"] in (16, 256):
+                g["cpu"] = legs[f"gemm_m{g['m']}"][g["layer"]]
         for r in norm:
             if r["t"] == legs["rmsnorm_t4096"]["t"]:
                 r["cpu"] = legs["rmsnorm_t4096"]
@@ -1241,23 +1450,37 @@ def main() -> int:
             "config": cfg1[2].to_dict(),
             "config_source": src1[2],
         },
+        "gemm_small_m": [g for g in gemm if g["m"] in SMALL_M],
         "gemm_m256": [g for g in gemm if g["m"] == 256],
-        "gemm_m1024_m4096": [g for g in gemm if g["m"] != 256],
+        "gemm_m1024_m4096": [g for g in gemm if g["m"] > 256],
         "gemm_w4a8_fp8": gemm8,
         "rmsnorm_fp8": norm,
         "repack_gate_up": repack,
         "device_copy_gbps": copy_gbps,
         "per_shape": per_shape,
         "gemv_m2_m4": gemv_m24,
+        "gemv_m8_m32": gemv_m8_m32,
+        "vendor_fp16": vendor,
+        "eager_op": eager,
         "stack": stack,
         "cpu_baseline": cpu,
+        "cpu_decode_m8": legs["decode_m8"] if cpu is not None else None,
         "gpu": gpu,
+        "env": fingerprint(),
     }
+    result["regression"] = regression_check(result)
+    if args.update_baseline is not None:
+        update_baseline(result, args.reason, Path(args.update_baseline))
     if args.detail:
-        detail = dict(result, gemm_sweep=sweep, vendor_fp16_gemm=vendor) if sweep is not None else result
+        detail = dict(result, gemm_sweep=sweep) if sweep is not None else result
         Path(args.detail).parent.mkdir(parents=True, exist_ok=True)
         Path(args.detail).write_text(json.dumps(detail, indent=1) + "\n")
     print(json.dumps(result), flush=True)
+    reg = result["regression"]
+    if args.check and reg is not None and reg.get("regressions"):
+        for r in reg["regressions"]:
+            log(f"REGRESSION {r['entry']}: {r['us']:.2f} us vs baseline {r['baseline_us']:.2f} us (+{r['slower_pct']:.1f}%)")
+        return 1
     return 0
 
 
