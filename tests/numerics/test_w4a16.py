@@ -442,11 +442,19 @@ def test_shared_x_variant_rejects_x_larger_than_the_lds(device: torch.device) ->
         _assert_close(y, cases.activations(4, 32768, 1)[:1], cases.layer_weights(16, 32768, 1))
 
 
-def test_cpu_tensors_raise_instead_of_falling_back() -> None:
+def test_cpu_tensors_take_the_torch_route(device: torch.device) -> None:
+    """Host tensors follow the reference's torch_reference decision into the torch route (the
+    GPU kernels never see them) and meet the same contract as the GPU result; a GPU call never
+    falls back to it."""
     w = cases.layer_weights(64, 256, 0)
     wc = cases.on_device(w, torch.device("cpu"))
-    with pytest.raises(RuntimeError, match="CPU"):
-        _linear(cases.activations(2, 256, 0), wc)
+    x = cases.activations(2, 256, 0)
+    y = _linear(x, wc)
+    assert y.device.type == "cpu"
+    _assert_close(y, x, w)
+    y_gpu = _linear(x.to(device), cases.on_device(w, device))
+    assert y_gpu.device.type == "cuda"
+    _assert_close(y_gpu, x, w)
 
 
 # ----------------------------------------------------------------------------- F1 and edges

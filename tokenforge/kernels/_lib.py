@@ -112,6 +112,14 @@ def library_path() -> Path:
     return Path(env) if env else LIB_PATH
 
 
+TORCH_OPS_PATH = LIB_PATH.parent / "libtokenforge_torch.so"
+
+
+def torch_ops_path() -> Path:
+    """The torch operator extension (``tokenforge_amd/ext/torch_ops.cpp``), beside the library."""
+    return TORCH_OPS_PATH
+
+
 @functools.cache
 def lib() -> ctypes.CDLL:
     """Load the library once per process. Raises :class:`HipLibraryError` when missing."""

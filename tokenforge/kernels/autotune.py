@@ -192,12 +192,14 @@ class AutotuneCache:
             return
         with self._mutex:
             self._table = table
+        _changed()
 
     def _reject(self, reason: str) -> None:
         log.warning("autotune cache %s discarded (%s); configs will be retuned", self.path, reason)
         self.discarded_reason = reason
         with self._mutex:
             self._table = {}
+        _changed()
 
     def get(self, bucket: int, n: int, k: int, group_size: int) -> GemmConfig | None:
         return self._table.get(entry_key(bucket, n, k, group_size))
@@ -208,6 +210,7 @@ class AutotuneCache:
             raise ValueError(f"{cfg} does not fit bucket {bucket}")
         with self._mutex:
             self._table = {**self._table, entry_key(bucket, n, k, group_size): cfg}
+        _changed()
 
     def __len__(self) -> int:
         return len(self._table)
@@ -220,6 +223,18 @@ class AutotuneCache:
 
 _REGISTRY: dict[tuple[str, str], AutotuneCache] = {}
 _REGISTRY_MUTEX = threading.Lock()
+_CHANGE_HOOKS: list[Callable[[], None]] = []
+
+
+def on_change(hook: Callable[[], None]) -> None:
+    """Call ``hook`` whenever a config :func:`lookup` returns may change (a cache loaded, put,
+    discarded or reset): holders of launch decisions made from lookups drop them."""
+    _CHANGE_HOOKS.append(hook)
+
+
+def _changed() -> None:
+    for hook in _CHANGE_HOOKS:
+        hook()
 
 
 def get_cache(gpu: str) -> AutotuneCache:
@@ -236,6 +251,7 @@ def get_cache(gpu: str) -> AutotuneCache:
 def reset_caches() -> None:
     with _REGISTRY_MUTEX:
         _REGISTRY.clear()
+    _changed()
 
 
 SHIPPED_DIR: Final = Path(__file__).resolve().parent / "tuned"

@@ -6,15 +6,17 @@
   per-call fallback: an op that cannot run on the GPU raises).
 
 Counts are kept in-process per label tuple and, when ``prometheus_client`` is importable,
-mirrored into a Prometheus counter family of the same name. Only host code counts: under
-HIP-graph replay the host does not run, so a captured call is counted once, at capture.
+mirrored into a Prometheus counter family of the same name. The C++ operators count their
+GPU dispatches natively; those counts are added whenever a counter is read. Only host code
+counts: under HIP-graph replay the host does not run, so a captured call is counted once, at
+capture.
 """
 
 from __future__ import annotations
 
 import threading
 from collections import Counter
-from collections.abc import Mapping
+from collections.abc import Callable, Mapping
 from typing import Any
 
 
@@ -41,6 +43,16 @@ class LabeledCounter:
         self._counts: Counter[tuple[str, ...]] = Counter()
         self._guard = threading.Lock()
         self._family = _prometheus_family(name, documentation, self.labelnames)
+        self._pre_read: Callable[[], None] | None = None
+
+    def set_pre_read(self, hook: Callable[[], None]) -> None:
+        """Run ``hook`` before every read and reset: it adds counts kept elsewhere (the C++
+        operators count their dispatches natively) through :meth:`inc`."""
+        self._pre_read = hook
+
+    def _fold(self) -> None:
+        if self._pre_read is not None:
+            self._pre_read()
 
     def _labels(self, given: Mapping[str, object]) -> tuple[str, ...]:
         missing = [k for k in self.labelnames if k not in given]
@@ -60,19 +72,23 @@ class LabeledCounter:
 
     def value(self, **labels: str) -> float:
         key = self._labels(labels)
+        self._fold()
         with self._guard:
             return float(self._counts[key])
 
     def total(self) -> float:
+        self._fold()
         with self._guard:
             return float(sum(self._counts.values()))
 
     def snapshot(self) -> dict[tuple[str, ...], float]:
+        self._fold()
         with self._guard:
             return {key: float(v) for key, v in self._counts.items()}
 
     def reset(self) -> None:
         """Forget the in-process counts (tests); the Prometheus family stays monotonic."""
+        self._fold()
         with self._guard:
             self._counts = Counter()
 

@@ -84,8 +84,38 @@ def build_library(sources: list[Path], out: Path, jobs: int | None = None, verbo
 
 
 def build(jobs: int | None = None, verbose: bool = False) -> Path:
-    """Compile every kernel source and link the product library. Returns its path."""
-    return build_library(sorted(CSRC.glob("*.hip")), LIB_DIR / LIB_NAME, jobs, verbose)
+    """Compile every kernel source and link the product library, then the torch operator
+    extension. Returns the kernel library's path."""
+    out = build_library(sorted(CSRC.glob("*.hip")), LIB_DIR / LIB_NAME, jobs, verbose)
+    build_torch_ops(verbose)
+    return out
+
+
+TORCH_OPS_SRC = PKG / "ext" / "torch_ops.cpp"
+TORCH_OPS_NAME = "libtokenforge_torch.so"
+
+
+def build_torch_ops(verbose: bool = False) -> Path:
+    """The torch.ops.tokenforge extension (``ext/torch_ops.cpp``): host C++ against PyTorch's
+    headers and libraries, no device code. It calls the kernel library through its C ABI, bound
+    at run time, so it has no link-time dependency on it. The HIP headers that PyTorch's ROCm
+    stream and guard headers include need ``__HIP_PLATFORM_AMD__`` and ``USE_ROCM`` defined."""
+    import torch
+
+    torch_dir = Path(torch.__file__).resolve().parent
+    rocm = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+    out = LIB_DIR / TORCH_OPS_NAME
+    LIB_DIR.mkdir(parents=True, exist_ok=True)
+    cxx = os.environ.get("CXX", "g++")
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    tmp = out.with_suffix(".so.tmp")
+    _run([cxx, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+          "-D__HIP_PLATFORM_AMD__", "-DUSE_ROCM", f"-I{torch_dir / 'include'}",
+          f"-I{torch_dir / 'include' / 'torch' / 'csrc' / 'api' / 'include'}", f"-I{rocm / 'include'}",
+          str(TORCH_OPS_SRC), "-o", str(tmp), f"-L{torch_dir / 'lib'}", f"-Wl,-rpath,{torch_dir / 'lib'}",
+          "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_hip", "-ldl"], verbose)
+    os.replace(tmp, out)
+    return out
 
 
 def main() -> int:
