@@ -10,6 +10,9 @@ the library defaults for each M (the GEMV, register-streamed and pipelined GEMM 
 
 At full depth (28 layers, M in {1, 2048}), the benchmark's fused pass (each norm inside the
 op of the linear it feeds) equals the unfused pass bit for bit and replays to the same bits.
+The W4A8 pass (qkv and gate_up on the e4m3 codes) replays to its eager bits, and its
+divergence from the fused pass stays within the stack's own sensitivity to one rounding of
+its input.
 """
 
 from __future__ import annotations
@@ -144,3 +147,76 @@ def test_28_layer_stack_fused_equals_unfused_and_replays(m: int, device: torch.d
         assert torch.equal(out, ref), "replay differs from eager"
         _pass_norm_in_linear(other, layers)  # eager work between replays
         torch.cuda.synchronize()
+
+
+def _pass_w4a8(x: torch.Tensor, layers: list) -> torch.Tensor:  # type: ignore[type-arg]
+    """The benchmark's W4A8 pass: qkv and gate_up take the norm's e4m3 codes and row scales
+    directly (no fp16(q * scale)); o_proj and down stay W4A16 with the residual epilogue."""
+    ops = torch.ops.tokenforge
+    m = x.shape[0]
+    for (qkv, o, gu, down), bias, g1, g2 in layers:
+        q8, s = ops.rmsnorm_fp8_quant(x, g1, 1e-6, None)
+        y = ops.w4a8_linear(q8, s, *qkv, bias, G, "hip")
+        attn = y[:, QKV - 512:].reshape(m, 4, 1, 128).expand(m, 4, 7, 128).reshape(m, H)
+        x = ops.w4a16_linear_residual(attn, *o, None, x, G, "hip")
+        q8, s = ops.rmsnorm_fp8_quant(x, g2, 1e-6, None)
+        act = ops.w4a8_linear(q8, s, *gu, None, G, "hip", "silu_mul")
+        x = ops.w4a16_linear_residual(act, *down, None, x, G, "hip")
+    return x
+
+
+@pytest.mark.parametrize("m", [1, 24, 300])
+def test_w4a8_stack_replay_is_bit_identical_to_eager(m: int, device: torch.device) -> None:
+    layers = _layers(device, 2)
+    gen = torch.Generator(device=device).manual_seed(50 + m)
+    x = torch.randn((m, H), generator=gen, device=device).to(torch.float16)
+    other = torch.randn((m, H), generator=gen, device=device).to(torch.float16)
+    eager = _pass_w4a8(x, layers)
+    assert bool(torch.isfinite(eager).all())
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        _pass_w4a8(x, layers)  # warm-up on the capture stream
+        stream.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            out = _pass_w4a8(x, layers)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), "graph replay differs from the eager pass"
+        _pass_w4a8(other, layers)
+        torch.cuda.synchronize()
+
+
+def _normwise(a: torch.Tensor, b: torch.Tensor) -> float:
+    return float((a.float() - b.float()).abs().max() / b.float().abs().max())
+
+
+@pytest.mark.parametrize("m", [1, 2048])
+def test_w4a8_stack_divergence_is_within_the_stacks_own_rounding_sensitivity(m: int, device: torch.device) -> None:
+    """The W4A8 pass is not bit-equal to the fused fp16-input pass (the row scale multiplies
+    each row's sum instead of each element, and at prefill M the weights are exact), and after
+    28 layers the two differ by 10-20% normwise. That is the stack's own sensitivity, not an
+    error of the W4A8 kernels: every sublayer re-quantizes its input to e4m3 (3 mantissa bits),
+    so a difference of one rounding in the input moves codes and grows through the layers.
+    Bound: at depths 1, 4, 14 and 28 the W4A8 pass stays within 1.5x of the divergence the fused
+    pass itself shows when each element of its input moves by half an fp16 ulp (measured
+    ratios 0.02-0.85). Each W4A8 linear is held to its own oracle in
+    tests/gpu/test_shipped_configs.py (a decoder layer stage by stage)."""
+    layers = _layers(device, 28)
+    gen = torch.Generator(device=device).manual_seed(700 + m)
+    x0 = torch.randn((m, H), generator=gen, device=device).to(torch.float16)
+    half_ulp = x0.float().abs() * 2.0**-11
+    xp = (x0.float() + half_ulp * torch.sign(torch.randn((m, H), generator=gen, device=device))).to(torch.float16)
+    fused, w4a8, pert = x0, x0, xp
+    for depth, layer in enumerate(layers, start=1):
+        fused = _pass_norm_in_linear(fused, [layer])
+        w4a8 = _pass_w4a8(w4a8, [layer])
+        pert = _pass_norm_in_linear(pert, [layer])
+        if depth in (1, 4, 14, 28):
+            assert bool(torch.isfinite(w4a8).all()), f"non-finite W4A8 output at depth {depth}"
+            d8, dp = _normwise(w4a8, fused), _normwise(pert, fused)
+            assert d8 <= 1.5 * dp, f"depth {depth}: W4A8 diverges by {d8:.3e}, the half-ulp perturbation by {dp:.3e}"
