@@ -5,11 +5,13 @@
     python bench.py --fingerprint        (the environment fingerprint of this checkout)
     python bench.py --traffic-probe      (eager launches for rocprofv3 --pmc, see below)
     python bench.py --mfma-probe         (the M=256 GEMMs, for rocprofv3 --pmc)
-    python bench.py --kernel-probe       (eager launches of every timed kernel, for rocprofv3)
+    python bench.py --entry-probe        (eager launches of every timed op, for rocprofv3)
     python bench.py --probe              (memory floors of the GEMV's access patterns)
     python bench.py --traffic-summary FETCH_DIR WRITE_DIR PROBE_LOG   (write the profiles/ summaries
     python bench.py --mfma-summary PMC_DIR PROBE_LOG TIMING_LOG        from the profiler's output)
     python bench.py --stats-summary PROF_DIR BENCH_LOG PROF_LOG KPROF_DIR KPROBE_LOG
+    python bench.py --counter-summary FETCH_DIR WRITE_DIR PROBE_LOG
+    python bench.py --instr-summary PMC_DIR PROBE_LOG
     python bench.py --probe-summary PROBE_LOG
 
 Configs: every timed launch uses the config ``autotune.lookup`` returns, i.e. the autotune
@@ -140,7 +142,8 @@ COLD_BYTES = 1.1e9
 TRAFFIC_SUMMARY = ROOT / "profiles" / "gemv_gate_up_m1_traffic.md"
 MFMA_SUMMARY = ROOT / "profiles" / "gemm_m256_mfma_busy.md"
 STATS_SUMMARY = ROOT / "profiles" / "bench_decode_m1_kernel_stats.md"
-MFMA_COUNTERS = ("SQ_VALU_MFMA_BUSY_CYCLES", "GRBM_GUI_ACTIVE", "SQ_BUSY_CYCLES", "SQ_WAVES")
+MFMA_COUNTERS = ("SQ_VALU_MFMA_BUSY_CYCLES", "GRBM_GUI_ACTIVE", "SQ_BUSY_CYCLES", "SQ_WAVES", "SQ_INSTS_LDS",
+                 "SQ_ACTIVE_INST_LDS", "SQ_LDS_BANK_CONFLICT")
 NUM_SIMDS = 256 * 4
 NUM_XCDS = 8
 CALIB_BYTES = 256 << 20
@@ -158,6 +161,7 @@ CODE_PATHS = ("bench.py", "__graft_entry__.py", "tokenforge", "tokenforge_amd", 
 CODE_SUFFIXES = (".py", ".hip", ".h", ".json")
 NORM_H = 3584
 NORM_T = (1, 16, 512, 4096)
+TIMED_SECTIONS = ("per_shape", "gemv_m2_m4", "gemv_m8_m32", "gemm_small_m", "gemm_m256", "gemm_m1024_m4096")
 
 
 def committed_traffic(cfg_dict: dict) -> float | None:  # type: ignore[type-arg]
@@ -260,33 +264,94 @@ def _bench_line(log_path: str) -> dict | None:  # type: ignore[type-arg]
 def _configs_of(bench: dict) -> dict:  # type: ignore[type-arg]
     """(section, layer, M) -> config of every timed kernel entry of a bench JSON line."""
     out = {}
-    for sec in ("per_shape", "gemv_m2_m4", "gemm_m256", "gemm_m1024_m4096"):
+    for sec in TIMED_SECTIONS:
         for e in bench.get(sec) or []:
             out[(sec, e["layer"], e["m"])] = e["config"]
     return out
 
 
+MARKER_KERNEL = "bitwise_not"  # the entry probe's separator kernel (torch.bitwise_not on one int)
+CALIB_KERNEL = "neg_kernel"  # the entry probe's calibration kernel (torch.neg, known bytes)
+ENTRY_TRAFFIC_SUMMARY = ROOT / "profiles" / "hbm_traffic_per_entry.md"
+INSTR_SUMMARY = ROOT / "profiles" / "instruction_mix_per_entry.md"
+INSTR_COUNTERS = ("SQ_WAVES", "SQ_INSTS_VALU", "SQ_INSTS_MFMA", "SQ_INSTS_LDS", "SQ_INSTS_VMEM_RD", "SQ_INSTS_SALU",
+                  "SQ_BUSY_CYCLES", "GRBM_GUI_ACTIVE")
+def marker_groups(rows: list, entries: int) -> list[list]:  # type: ignore[type-arg]
+    """Split an entry probe's dispatches (dicts with ``Dispatch_Id`` and ``Kernel_Name``) into
+    one list per entry: the dispatches between consecutive marker kernels, in dispatch order
+    (what follows the last marker is the calibration's setup and the calibration kernel). Rows
+    that share a dispatch (one per counter) stay together."""
+    order = sorted({int(r["Dispatch_Id"]) for r in rows})
+    by_id: dict = {}  # type: ignore[type-arg]
+    for r in rows:
+        by_id.setdefault(int(r["Dispatch_Id"]), []).append(r)
+    groups: list[list] = []  # type: ignore[type-arg]
+    current = None
+    for did in order:
+        name = by_id[did][0]["Kernel_Name"]
+        if MARKER_KERNEL in name:
+            if current is not None:
+                groups.append(current)
+            current = []
+        elif CALIB_KERNEL in name:
+            break
+        elif current is not None:
+            current.extend(by_id[did])
+    if len(groups) != entries:
+        raise ValueError(f"{len(groups)} marked groups of dispatches, expected {entries}")
+    return groups
+
+
+def _event_times(bench: dict) -> dict:  # type: ignore[type-arg]
+    """Entry name -> (event-timed us, config) of a bench JSON line's timed entries."""
+    out = {}
+    for sec in TIMED_SECTIONS:
+        for e in bench.get(sec) or []:
+            out[f"{e['layer']} M={e['m']}"] = (e["us"], e.get("config"))
+    for e in bench.get("gemm_w4a8_fp8") or []:
+        out[f"{e['layer']} M={e['m']} W4A8"] = (e["us"], e.get("config"))
+    for e in bench.get("rmsnorm_fp8") or []:
+        out[f"rmsnorm_fp8 T={e['t']}"] = (e["us"], None)
+    if bench.get("repack_gate_up"):
+        out["repack gate_up_proj"] = (bench["repack_gate_up"]["us"], None)
+    return out
+
+
+def _short(name: str) -> str:
+    name = name.replace("(anonymous namespace)::", "").replace("void ", "")
+    return name.split("(tf::")[0].split("(unsigned")[0].split("(int")[0].split("(float")[0].split("(long")[0]
+
+
+def _cfg_name(c: dict | None) -> str:  # type: ignore[type-arg]
+    if not c:
+        return "-"
+    return (f"{c['kernel']} bm{c['block_m']} bn{c['block_n']} bk{c['block_k']} sk{c['split_k']} "
+            f"w{c['num_warps']} st{c['num_stages']}")
+
+
 def stats_summary(prof_dir: str, bench_log: str, prof_log: str, kprof_dir: str, kprobe_log: str) -> int:
     """Write ``STATS_SUMMARY`` from two ``rocprofv3 --kernel-trace --stats`` runs: one of the
     bench itself (``prof_dir``, its stdout in ``prof_log``: the kernel table) and one of
-    ``--kernel-probe`` (``kprof_dir``, stdout in ``kprobe_log``: each timed entry's launches in
-    dispatch order), next to the event-timed averages of the plain bench run before them
-    (``bench_log``). Refuses to write when the three runs used different configs for any timed
-    shape, or when a probe entry's dispatches are not all of one kernel."""
+    ``--entry-probe`` (``kprof_dir``, stdout in ``kprobe_log``: each timed op's launches between
+    marker kernels), next to the event-timed averages of the plain bench run before them
+    (``bench_log``). An op's time is the sum of all its kernels per launch (a split-K GEMM and
+    its reduce). Refuses to write when the runs used different configs for any timed shape."""
     import csv
     import glob
 
     bench, prof = _bench_line(bench_log), _bench_line(prof_log)
-    kprobe = _probe_line(kprobe_log, "kernel_probe")
-    if bench is None or prof is None or kprobe is None:
-        print(f"no bench JSON line in {bench_log} or {prof_log}, or no kernel_probe line in {kprobe_log}",
+    probe = _probe_line(kprobe_log, "entry_probe")
+    if bench is None or prof is None or probe is None:
+        print(f"no bench JSON line in {bench_log} or {prof_log}, or no entry_probe line in {kprobe_log}",
               file=sys.stderr)
         return 1
     cb, cp = _configs_of(bench), _configs_of(prof)
-    ck = {(e["layer"], e["m"]): e["config"] for e in kprobe["entries"]}
+    ev = _event_times(bench)
+    ck = {e["entry"]: e.get("config") for e in probe["entries"]}
     differ = sorted(str(key) for key in set(cb) & set(cp) if cb[key] != cp[key])
-    differ += sorted(str(key) for key in cb if (key[1], key[2]) in ck and ck[(key[1], key[2])] != cb[key])
-    if differ or not set(cb) & set(cp) or not set(ck) >= {(key[1], key[2]) for key in cb}:
+    differ += sorted(name for name, c in ck.items() if c is not None and name in ev and ev[name][1] is not None
+                     and ev[name][1] != c)
+    if differ or not set(cb) & set(cp):
         print(f"the bench, profiled and probe runs used different configs: {differ}", file=sys.stderr)
         return 1
     PRE = "cd /tmp && export TMPDIR=/tmp && R=<repo root>"
@@ -294,75 +359,197 @@ def stats_summary(prof_dir: str, bench_log: str, prof_log: str, kprof_dir: str, 
     f = glob.glob(f"{prof_dir}/**/*_kernel_stats.csv", recursive=True)[0]
     rows = list(csv.DictReader(open(f)))
     lines = [
-        "# Kernel statistics: decode GEMVs at M = 1, 2, 4 and prefill GEMMs at M = 256, 1024, 4096",
+        "# Kernel statistics of the bench, and each timed op's rocprofv3 time beside its event timing",
         "",
         "Commands (on the MI355X box, fresh autotune cache, so every run takes its configs from",
         "the table shipped in tokenforge/kernels/tuned/; the summary step checks that they agree):",
         "",
         "```",
         PRE,
-        "python $R/bench.py --steps 100 --warmup 10 > $R/gpurun_out/bench.log",
+        "python $R/bench.py --no-cpu > $R/gpurun_out/bench.log",
         "rocprofv3 --kernel-trace --stats --output-format csv -d $R/gpurun_out/prof_bench -- \\",
         "    python $R/bench.py --steps 20 --warmup 5 --no-cpu --no-stack > $R/gpurun_out/prof_bench.log",
-        "rocprofv3 --kernel-trace --stats --output-format csv -d $R/gpurun_out/prof_kprobe -- \\",
-        "    python $R/bench.py --kernel-probe > $R/gpurun_out/kprobe.log",
+        "rocprofv3 --kernel-trace --stats --output-format csv -d $R/gpurun_out/prof_entries -- \\",
+        "    python $R/bench.py --entry-probe > $R/gpurun_out/entries.log",
         "python $R/bench.py --stats-summary $R/gpurun_out/prof_bench $R/gpurun_out/bench.log \\",
-        "    $R/gpurun_out/prof_bench.log $R/gpurun_out/prof_kprobe $R/gpurun_out/kprobe.log",
+        "    $R/gpurun_out/prof_bench.log $R/gpurun_out/prof_entries $R/gpurun_out/entries.log",
         "```",
         "",
-        "Kernel table: `*_kernel_stats.csv` of the profiled bench run, the kernels of this library",
-        "plus the largest setup kernels (torch RNG, fills). The GEMV rows are the decode shapes at",
-        "M = 1, 2 and 4 (graph replays, the per-shape timing graphs and the warmup); the gemm rows",
-        "the prefill timing at M = 256, 1024 and 4096.",
+        "Kernel table: `*_kernel_stats.csv` of the profiled bench run (graph replays of every timed",
+        "entry, the warmups and the setup kernels), the 24 kernels with the most time.",
         "",
         "| kernel | calls | avg us | min us | max us | % time |",
         "|---|---:|---:|---:|---:|---:|",
     ]
-    for r in rows[:18]:
-        name = r["Name"].replace("(anonymous namespace)::", "")
-        name = name.split("(tf::")[0].split("(unsigned")[0].split("(int")[0].split("(float")[0].replace("void ", "")
+    for r in rows[:24]:
+        name = _short(r["Name"])
         if len(name) > 90:
             name = name[:90] + "..."
         lines.append(f"| `{name}` | {r['Calls']} | {float(r['AverageNs'])/1e3:.2f} | {float(r['MinNs'])/1e3:.2f} | "
                      f"{float(r['MaxNs'])/1e3:.2f} | {float(r['Percentage']):.1f} |")
     # ---------------------------------------------------------------- per entry
     tr = glob.glob(f"{kprof_dir}/**/*_kernel_trace.csv", recursive=True)[0]
-    disp = sorted((d for d in csv.DictReader(open(tr))
-                   if ("gemv_" in d["Kernel_Name"] or "gemm" in d["Kernel_Name"])
-                   and "reduce" not in d["Kernel_Name"]),
-                  key=lambda d: int(d["Dispatch_Id"]))
-    n_launch = kprobe["launches"]
-    entries = kprobe["entries"]
-    if len(disp) != n_launch * len(entries):
-        raise ValueError(f"{kprof_dir}: {len(disp)} GEMV/GEMM dispatches, expected {n_launch * len(entries)}")
-    timed = {(e["layer"], e["m"]): e for sec in ("per_shape", "gemv_m2_m4", "gemm_m256", "gemm_m1024_m4096")
-             for e in bench.get(sec) or []}
+    groups = marker_groups(list(csv.DictReader(open(tr))), len(probe["entries"]))
+    n_launch = probe["launches"]
     lines += [
         "",
-        f"Per entry: rocprofv3 average duration of the entry's {n_launch} eager launches in the",
-        "`--kernel-probe` trace (the same kernels on the same rotating cold copies, taken in",
-        "dispatch order; split-K reduce kernels not counted) next to the event-timed average of the",
+        f"Per op: the `--entry-probe` trace, each op launched {n_launch} times eagerly on the rotating",
+        "cold copies between two marker kernels; rocprofv3 time per launch summed over all the op's",
+        "kernels (a split-K GEMM and its reduce both count), next to the event-timed average of the",
         "plain bench run (HIP events around graph replays on the launch stream).",
         "",
-        "| shape | config | kernel instance | rocprofv3 avg us | event-timed avg us | ratio |",
+        "| op | config | kernels per launch | rocprofv3 us / launch | event-timed us | ratio |",
         "|---|---|---|---:|---:|---:|",
     ]
-    for j, e in enumerate(entries):
-        ds = disp[j * n_launch:(j + 1) * n_launch]
-        names = {d["Kernel_Name"] for d in ds}
-        if len(names) != 1:
-            raise ValueError(f"entry {e['layer']} M={e['m']}: dispatches of {len(names)} kernels")
-        inst = names.pop().replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0]
-        avg = statistics.mean((int(d["End_Timestamp"]) - int(d["Start_Timestamp"])) / 1e3 for d in ds)
-        c = e["config"]
-        cfg = (f"{c['kernel']} bm{c['block_m']} bn{c['block_n']} bk{c['block_k']} sk{c['split_k']} "
-               f"w{c['num_warps']} st{c['num_stages']}")
-        ev = timed.get((e["layer"], e["m"]))
-        ev_us = f"{ev['us']:.2f}" if ev else "-"
-        ratio = f"{avg / ev['us']:.2f}" if ev else "-"
-        lines.append(f"| {e['layer']} M={e['m']} | {cfg} | `{inst}` | {avg:.2f} | {ev_us} | {ratio} |")
+    for e, ds in zip(probe["entries"], groups):
+        if len(ds) % n_launch:
+            raise ValueError(f"{e['entry']}: {len(ds)} dispatches for {n_launch} launches")
+        per = statistics.mean((int(d["End_Timestamp"]) - int(d["Start_Timestamp"])) / 1e3 for d in ds) * len(ds) / n_launch
+        kinds: dict = {}  # type: ignore[type-arg]
+        for d in ds:
+            kinds[_short(d["Kernel_Name"])] = kinds.get(_short(d["Kernel_Name"]), 0) + 1
+        kern = ", ".join(f"`{k}`" + (f" x{v // n_launch}" if v // n_launch > 1 else "") for k, v in kinds.items())
+        t = ev.get(e["entry"])
+        ev_us = f"{t[0]:.2f}" if t else "-"
+        ratio = f"{per / t[0]:.2f}" if t else "-"
+        lines.append(f"| {e['entry']} | {_cfg_name(e.get('config'))} | {kern} | {per:.2f} | {ev_us} | {ratio} |")
     STATS_SUMMARY.write_text("\n".join(lines) + "\n")
     print(f"wrote {STATS_SUMMARY}")
+    return 0
+
+
+def counter_summary(fetch_dir: str, write_dir: str, probe_log: str) -> int:
+    """Write ``ENTRY_TRAFFIC_SUMMARY`` from two ``rocprofv3 --pmc`` runs of ``--entry-probe``
+    (FETCH_SIZE, then WRITE_SIZE): each op's HBM bytes per launch (all its kernels), each
+    counter scaled by known bytes / counted bytes of the calibration kernel in the same run,
+    next to the op's algorithmic bytes."""
+    import csv
+    import glob
+
+    probe = _probe_line(probe_log, "entry_probe")
+    if probe is None:
+        print(f"no entry_probe line in {probe_log}", file=sys.stderr)
+        return 1
+    n_launch = probe["launches"]
+
+    def per_entry(d: str, name: str) -> tuple[list[float], float]:
+        rows = []
+        for f in glob.glob(f"{d}/**/*counter_collection.csv", recursive=True):
+            rows += [r for r in csv.DictReader(open(f)) if r["Counter_Name"] == name]
+        calib = [float(r["Counter_Value"]) * 1024 for r in rows if CALIB_KERNEL in r["Kernel_Name"]]
+        if not calib:
+            raise ValueError(f"{d}: no calibration dispatches")
+        groups = marker_groups(rows, len(probe["entries"]))
+        return [sum(float(r["Counter_Value"]) * 1024 for r in g) / n_launch for g in groups], \
+            probe["calibration_bytes_in"] / statistics.mean(calib)
+
+    fetch, f_scale = per_entry(fetch_dir, "FETCH_SIZE")
+    write, w_scale = per_entry(write_dir, "WRITE_SIZE")
+    lines = [
+        "# HBM traffic per op: every timed entry of the bench, FETCH_SIZE + WRITE_SIZE",
+        "",
+        "Commands (on the MI355X box, fresh autotune cache: the configs are the shipped table's; one",
+        "counter per run, each run a separate process):",
+        "",
+        "```",
+        "cd /tmp && export TMPDIR=/tmp && R=<repo root>",
+        "timeout -s KILL 300 rocprofv3 --pmc FETCH_SIZE --output-format csv -d $R/gpurun_out/pmc_entries_fetch -- \\",
+        "    python $R/bench.py --entry-probe > $R/gpurun_out/pmc_entries_fetch.log",
+        "timeout -s KILL 300 rocprofv3 --pmc WRITE_SIZE --output-format csv -d $R/gpurun_out/pmc_entries_write -- \\",
+        "    python $R/bench.py --entry-probe > $R/gpurun_out/pmc_entries_write.log",
+        "python $R/bench.py --counter-summary $R/gpurun_out/pmc_entries_fetch $R/gpurun_out/pmc_entries_write \\",
+        "    $R/gpurun_out/pmc_entries_fetch.log",
+        "```",
+        "",
+        f"`--entry-probe` launches each op {n_launch} times eagerly over the rotating cold copies",
+        "between marker kernels, then the calibration kernel `torch.neg` on a 256 MiB fp32 tensor",
+        "(256 MiB read, 256 MiB written) 4 times. Counters are KiB per dispatch; an op's bytes are",
+        "the sum over its kernels (a split-K GEMM's partials round trip through its reduce shows",
+        "here), per launch; scale = known / counted bytes of the calibration kernel:",
+        f"FETCH_SIZE x {f_scale:.4f}, WRITE_SIZE x {w_scale:.4f}. Algorithmic bytes: micro.py:82-86 for",
+        "the linears (weights, scales, zero points, x, y), x + gamma + codes + scales for the norm,",
+        "qweight in + out for the repack.",
+        "",
+        "| op | config | FETCH bytes | WRITE bytes | traffic / launch | algorithmic | x algorithmic |",
+        "|---|---|---:|---:|---:|---:|---:|",
+    ]
+    for e, fb, wb in zip(probe["entries"], fetch, write):
+        fb, wb = fb * f_scale, wb * w_scale
+        t = fb + wb
+        lines.append(f"| {e['entry']} | {_cfg_name(e.get('config'))} | {fb:.0f} | {wb:.0f} | {t:.0f} | "
+                     f"{e['bytes']} | {t / e['bytes']:.3f} |")
+    ENTRY_TRAFFIC_SUMMARY.write_text("\n".join(lines) + "\n")
+    print(f"wrote {ENTRY_TRAFFIC_SUMMARY} ({len(probe['entries'])} ops)")
+    return 0
+
+
+def _weight_bytes(entry: str) -> int | None:
+    """Packed int4 weight bytes (N·K/2) of an entry named after a layer, None otherwise."""
+    for name, n, k in SHAPES:
+        if entry.startswith(name + " "):
+            return n * k // 2
+    return None
+
+
+def instr_summary(pmc_dir: str, probe_log: str) -> int:
+    """Write ``INSTR_SUMMARY`` from one ``rocprofv3 --pmc`` run of ``--entry-probe`` with
+    ``INSTR_COUNTERS``: per op, the wave instructions it issues by kind (summed over its
+    kernels and over the GPU, per launch), per wave, and for the linears per packed weight word
+    (8 int4 values), next to the kernel cycles."""
+    import csv
+    import glob
+
+    probe = _probe_line(probe_log, "entry_probe")
+    if probe is None:
+        print(f"no entry_probe line in {probe_log}", file=sys.stderr)
+        return 1
+    n_launch = probe["launches"]
+    rows = []
+    for f in glob.glob(f"{pmc_dir}/**/*counter_collection.csv", recursive=True):
+        rows += list(csv.DictReader(open(f)))
+    groups = marker_groups(rows, len(probe["entries"]))
+    lines = [
+        "# Instruction mix per op: every timed entry of the bench (SQ instruction counters)",
+        "",
+        "Command (on the MI355X box, fresh autotune cache: the configs are the shipped table's):",
+        "",
+        "```",
+        "cd /tmp && export TMPDIR=/tmp && R=<repo root>",
+        f"timeout -s KILL 300 rocprofv3 --pmc {' '.join(INSTR_COUNTERS)} --output-format csv \\",
+        "    -d $R/gpurun_out/pmc_entries_instr -- python $R/bench.py --entry-probe > $R/gpurun_out/pmc_entries_instr.log",
+        "python $R/bench.py --instr-summary $R/gpurun_out/pmc_entries_instr $R/gpurun_out/pmc_entries_instr.log",
+        "```",
+        "",
+        f"`--entry-probe` launches each op {n_launch} times eagerly between marker kernels. Counts are",
+        "wave instructions summed over the GPU and over the op's kernels, per launch. For the linears,",
+        "\"VALU per word\" is the lane operations (wave instructions x 64 lanes) per packed weight word",
+        "of the layer (N·K/8 int32 words, 8 int4 values each). The exact dequantization of one word",
+        "is 13 lane operations (four mask-and-merges into fp16 magic numbers, one shift, four packed",
+        "subtractions of the zero point, four packed multiplies by the scale), so a figure near 13",
+        "means little other arithmetic; above it, the rest of the kernel's VALU work (or, where M",
+        "rows of x are tiled, the same word dequantized by several workgroups). \"MFMA per 64",
+        "words\" counts the matrix instructions that consume each 64 words (one 16x16x32 or 32x32x16",
+        "B operand). Kernel cycles: GRBM_GUI_ACTIVE per XCD.",
+        "",
+        "| op | waves | VALU | MFMA | LDS | VMEM rd | SALU | VALU / wave | VALU per word | MFMA per 64 words | cycles |",
+        "|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|",
+    ]
+    for e, g in zip(probe["entries"], groups):
+        tot = {c: 0.0 for c in INSTR_COUNTERS}
+        for r in g:
+            if r["Counter_Name"] in tot:
+                tot[r["Counter_Name"]] += float(r["Counter_Value"])
+        per = {c: v / n_launch for c, v in tot.items()}
+        waves = max(per["SQ_WAVES"], 1.0)
+        wb = _weight_bytes(e["entry"])
+        words = wb / 4 if wb else None
+        vw = f"{per['SQ_INSTS_VALU'] * 64 / words:.1f}" if words else "-"
+        mw = f"{per['SQ_INSTS_MFMA'] * 64 / words:.2f}" if words else "-"
+        lines.append(f"| {e['entry']} | {per['SQ_WAVES']:.0f} | {per['SQ_INSTS_VALU']:.0f} | {per['SQ_INSTS_MFMA']:.0f} | "
+                     f"{per['SQ_INSTS_LDS']:.0f} | {per['SQ_INSTS_VMEM_RD']:.0f} | {per['SQ_INSTS_SALU']:.0f} | "
+                     f"{per['SQ_INSTS_VALU'] / waves:.0f} | {vw} | {mw} | {per['GRBM_GUI_ACTIVE'] / NUM_XCDS:.0f} |")
+    INSTR_SUMMARY.write_text("\n".join(lines) + "\n")
+    print(f"wrote {INSTR_SUMMARY} ({len(probe['entries'])} ops)")
     return 0
 
 
@@ -401,7 +588,7 @@ def mfma_summary(pmc_dir: str, probe_log: str, timing_log: str) -> int:
         raise ValueError(f"{pmc_dir}: {len(ids)} GEMM dispatches, expected >= {n_launch * len(probe['runs'])}")
     ids = ids[: n_launch * len(probe["runs"])]
     lines = [
-        "# MFMA utilisation of the prefill GEMM at M=256 (gate_up and down, the bench's configs)",
+        "# MFMA utilisation and LDS counters of the prefill GEMMs at M=256 (fp16 W4A16 and fp8 W4A8)",
         "",
         "Commands (on the MI355X box, fresh autotune cache: the configs are the shipped table's):",
         "",
@@ -414,23 +601,32 @@ def mfma_summary(pmc_dir: str, probe_log: str, timing_log: str) -> int:
         "    $R/gpurun_out/mfma_timing.log",
         "```",
         "",
-        f"`--mfma-probe` launches each layer's M=256 GEMM {n_launch} times over rotating cold",
-        "weight copies (counters, eager) and times the same launches from a HIP graph (events, taken",
-        "from the run without the profiler).",
+        f"`--mfma-probe` launches each M=256 GEMM (the fp16 GEMM of gate_up and down at the shipped",
+        f"configs, then the W4A8 fp8 GEMM of both at `fp8_gemm_config`) {n_launch} times over",
+        "rotating cold weight copies (counters, eager) and times the same launches from a HIP graph",
+        "(events, taken from the run without the profiler).",
         f"MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / {NUM_XCDS} XCDs x {NUM_SIMDS} SIMDs): the",
         "share of the kernel's cycles in which an average SIMD's matrix core is busy. The split-K",
         "reduce kernel of down runs no MFMA and is not counted. Rows: mean over the launches.",
         "",
-        "| layer | config | MFMA busy (counters) | us / launch (events) | TFLOP/s | of 2.5 PF |",
-        "|---|---|---:|---:|---:|---:|",
+        "LDS bank conflicts = SQ_LDS_BANK_CONFLICT / SQ_INSTS_LDS: cycles lost to bank conflicts per",
+        "LDS instruction.",
+        "",
+        "| layer | GEMM | config | MFMA busy (counters) | us / launch (events) | TFLOP/s | of its dense peak | conflict cycles / LDS instr |",
+        "|---|---|---|---:|---:|---:|---:|---:|",
     ]
     for j, run in enumerate(timing["runs"]):
         vals = [per[d] for d in ids[j * n_launch:(j + 1) * n_launch]]
         busy = statistics.mean(v["SQ_VALU_MFMA_BUSY_CYCLES"] / (v["GRBM_GUI_ACTIVE"] / NUM_XCDS * NUM_SIMDS) for v in vals)
+        conflict = statistics.mean(v.get("SQ_LDS_BANK_CONFLICT", 0.0) / max(v.get("SQ_INSTS_LDS", 0.0), 1.0)
+                                   for v in vals)
         c = run["config"]
         name = f"{c['kernel']} bm{c['block_m']} bn{c['block_n']} bk{c['block_k']} sk{c['split_k']} w{c['num_warps']} st{c['num_stages']}"
-        lines.append(f"| {run['layer']} | {name} | {100 * busy:.1f}% | {run['us']:.2f} | {run['tflops']:.1f} | "
-                     f"{100 * run['tflops'] / FP16_MFMA_PEAK_TFLOPS:.1f}% |")
+        fp8 = run.get("precision") == "fp8"
+        peak = FP8_MFMA_PEAK_TFLOPS if fp8 else FP16_MFMA_PEAK_TFLOPS
+        lines.append(f"| {run['layer']} | {'W4A8 fp8' if fp8 else 'W4A16 fp16'} | {name} | {100 * busy:.1f}% | "
+                     f"{run['us']:.2f} | {run['tflops']:.1f} | {100 * run['tflops'] / peak:.1f}% of "
+                     f"{peak / 1000:.1f} PF | {conflict:.2f} |")
     lines += ["", "Raw counters per launch (mean):", "", "| layer | " + " | ".join(MFMA_COUNTERS) + " |",
               "|---|" + "---:|" * len(MFMA_COUNTERS)]
     for j, run in enumerate(probe["runs"]):
@@ -594,8 +790,9 @@ def timed_rows(result: dict) -> dict[str, float]:  # type: ignore[type-arg]
     """Every timed entry of a bench line as ``impl|layer|m`` -> microseconds (micro.py:133)."""
     rows: dict[str, float] = {}
     for key in ("per_shape", "gemv_m2_m4", "gemv_m8_m32", "gemm_small_m", "gemm_m256", "gemm_m1024_m4096"):
+        impl = "hip-cfg4" if key == "gemm_small_m" else "hip"  # M=32 is in gemv_m8_m32 too
         for r in result.get(key) or ():
-            rows[f"hip|{r['layer']}|{r['m']}"] = r["us"]
+            rows[f"{impl}|{r['layer']}|{r['m']}"] = r["us"]
     for r in result.get("gemm_w4a8_fp8") or ():
         rows[f"hip-fp8|{r['layer']}|{r['m']}"] = r["us"]
     for r in result.get("rmsnorm_fp8") or ():
@@ -1102,8 +1299,12 @@ def main() -> int:
                     help="write the committed kernel-statistics summary from a rocprofv3 kernel-trace run")
     ap.add_argument("--probe-summary", metavar="PROBE_LOG",
                     help="write the committed memory-floor summary from a --probe run's output")
-    ap.add_argument("--kernel-probe", action="store_true",
-                    help="eager launches of every kernel the bench line times, in order, for rocprofv3")
+    ap.add_argument("--entry-probe", action="store_true",
+                    help="eager launches of every op the bench line times, between marker kernels, for rocprofv3")
+    ap.add_argument("--counter-summary", nargs=3, metavar=("FETCH_DIR", "WRITE_DIR", "PROBE_LOG"),
+                    help="write the committed per-op HBM traffic summary from two --entry-probe counter runs")
+    ap.add_argument("--instr-summary", nargs=2, metavar=("PMC_DIR", "PROBE_LOG"),
+                    help="write the committed per-op instruction-mix summary from an --entry-probe counter run")
     ap.add_argument("--probe", action="store_true",
                     help="memory floors of the GEMV's access patterns (bench_probes/lib/libtokenforge_read_probes.so), "
                          "next to the GEMV itself on the cached or default configs")
@@ -1128,6 +1329,10 @@ def main() -> int:
         return traffic_summary(*args.traffic_summary)
     if args.mfma_summary:
         return mfma_summary(*args.mfma_summary)
+    if args.counter_summary:
+        return counter_summary(*args.counter_summary)
+    if args.instr_summary:
+        return instr_summary(*args.instr_summary)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(
             "bench.py measures one GPU: this build's hot path is single-GPU (no collectives); "
@@ -1161,6 +1366,7 @@ def main() -> int:
     rep_ms = median_replay_ms(g_rep, 8)
     del g_rep
     gate_awq_host = None if args.no_cpu else gate_awq.cpu()
+    gate_awq_dev = gate_awq if args.entry_probe else None
     del gate_awq
     for c in range(copies):
         layers[c] = [t[:3] for t in layers[c]]
@@ -1217,48 +1423,102 @@ def main() -> int:
         x, cfg = m_x[i], cfgs[i]
         return lambda: w4a16_gemm(x, qw, s, z, GROUP, cfg)
 
-    if args.kernel_probe:
-        # Eager launches of every kernel the bench line times (the M = 1, 2, 4 GEMVs on the four
-        # shapes, then the prefill GEMMs), each entry `copies` times over the rotating cold
-        # copies, one entry after the other, for rocprofv3 runs that take dispatches in order.
-        entries = []
-        for m in (1, 2, 4):
+    if args.entry_probe:
+        # Eager launches of every op the bench line times, each `copies` times over the rotating
+        # cold copies, with a marker kernel before each op and the calibration kernel at the end,
+        # for rocprofv3 runs (kernel trace, FETCH_SIZE, WRITE_SIZE) that group dispatches by op.
+        from tokenforge.kernels.config import fp8_gemm_config
+        from tokenforge.kernels.hip.rmsnorm_fp8 import rmsnorm_fp8_quant
+        from tokenforge.kernels.hip.w4a16 import w4a8_gemm_ex
+
+        entries: list = []  # type: ignore[type-arg]
+
+        def add(label: dict, fn, nbytes: int) -> None:  # type: ignore[no-untyped-def,type-arg]
+            if all(e[0]["entry"] != label["entry"] for e in entries):  # M=32 of gate_up and down: once
+                entries.append((dict(label, bytes=nbytes), fn))
+
+        for m in (1, 2, 4) + DECODE_EXTRA_M:
             xm = xs if m == 1 else [torch.randn((m, k), generator=gen, device=dev).to(torch.float16) for _, _, k in SHAPES]
             for i, (name, n, k) in enumerate(SHAPES):
                 cfg = config(m, n, k)[0]
-                entries.append(({"layer": name, "m": m, "config": cfg.to_dict()}, i, xm, cfg))
+                add({"entry": f"{name} M={m}", "config": cfg.to_dict()},
+                    lambda c, i=i, xm=xm, cfg=cfg: launcher(c, i, xm, [cfg] * len(SHAPES))(), bytes_moved(m, n, k))
+        for m in SMALL_M + PREFILL_M:
+            for i in (2, 3):
+                name, n, k = SHAPES[i]
+                cfg = config(m, n, k)[0]
+                xm = [None] * len(SHAPES)
+                xm[i] = prefill_x(m, k, gen, dev)
+                add({"entry": f"{name} M={m}", "config": cfg.to_dict()},
+                    lambda c, i=i, xm=xm, cfg=cfg: launcher(c, i, xm, [cfg] * len(SHAPES))(), bytes_moved(m, n, k))
         for m in PREFILL_M:
             for i in (2, 3):
                 name, n, k = SHAPES[i]
-                xm = [None] * len(SHAPES)
-                xm[i] = torch.randn((m, k), generator=gen, device=dev).to(torch.float16)
-                cfg = config(m, n, k)[0]
-                entries.append(({"layer": name, "m": m, "config": cfg.to_dict()}, i, xm, cfg))
-        for _, i, xm, cfg in entries:
+                cfg = fp8_gemm_config(m, n, k)
+                x8 = (torch.randn((m, k), generator=gen, device=dev) * 50).to(torch.float8_e4m3fn)
+                xs8 = torch.rand((m,), generator=gen, device=dev) * 0.01 + 0.001
+                add({"entry": f"{name} M={m} W4A8", "config": cfg.to_dict()},
+                    lambda c, i=i, x8=x8, xs8=xs8, cfg=cfg: w4a8_gemm_ex(x8, xs8, *layers[c][i], GROUP, cfg),
+                    bytes_moved(m, n, k) - m * k + 4 * m)  # e4m3 x (one byte) and its row scales
+        gamma = (1 + 0.1 * torch.randn(NORM_H, generator=gen, device=dev)).to(torch.float16)
+        for t in NORM_T:
+            n_in = max(2, min(64, int(-(-COLD_BYTES // (t * NORM_H * 2)))))
+            xin = [torch.randn((t, NORM_H), generator=gen, device=dev).to(torch.float16) for _ in range(n_in)]
+            add({"entry": f"rmsnorm_fp8 T={t}"},
+                lambda c, xin=xin: rmsnorm_fp8_quant(xin[c % len(xin)], gamma, 1e-6, None),
+                t * NORM_H * 2 + NORM_H * 2 + t * NORM_H + 4 * t)
+        add({"entry": "repack gate_up_proj"}, lambda c: repack_awq_to_tf(gate_awq_dev),
+            SHAPES[2][1] * SHAPES[2][2] // 2 * 2)
+        marker = torch.zeros(1, dtype=torch.int32, device=dev)
+        src = torch.randn(CALIB_BYTES // 4, device=dev)
+        dst = torch.empty_like(src)
+        for _, fn in entries:
+            torch.bitwise_not(marker, out=marker)
             for c in range(copies):
-                launcher(c, i, xm, [cfg] * len(SHAPES))()
+                fn(c)
             torch.cuda.synchronize()
-        print(json.dumps({"kernel_probe": {"launches": copies, "entries": [e[0] for e in entries]}}), flush=True)
+        torch.bitwise_not(marker, out=marker)
+        for _ in range(4):
+            torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        print(json.dumps({"entry_probe": {"launches": copies, "entries": [e[0] for e in entries],
+                                          "calibration": "torch.neg", "calibration_bytes_in": CALIB_BYTES,
+                                          "calibration_bytes_out": CALIB_BYTES}}), flush=True)
         return 0
 
     if args.mfma_probe:
-        # First the eager launches the counters see (each layer's in turn), then the graph
-        # timing of the same launches (its dispatches come after and are not counted).
-        cfgs = {i: config(256, SHAPES[i][1], SHAPES[i][2])[0] for i in (2, 3)}
-        xms = {}
-        for i in (2, 3):
-            xms[i] = [None] * len(SHAPES)
-            xms[i][i] = torch.randn((256, SHAPES[i][2]), generator=gen, device=dev).to(torch.float16)
-            for c in range(MFMA_LAUNCHES):
-                launcher(c % copies, i, xms[i], [cfgs[i]] * len(SHAPES))()
-        torch.cuda.synchronize()
-        runs = []
+        # First the eager launches the counters see (each GEMM's in turn: the fp16 GEMM on
+        # gate_up and down, then the W4A8 fp8 GEMM on both), then the graph timing of the same
+        # launches (its dispatches come after and are not counted).
+        from tokenforge.kernels.config import fp8_gemm_config
+        from tokenforge.kernels.hip.w4a16 import w4a8_gemm_ex
+
+        m = 256
+        gemms = []  # (label, config, fn(c))
         for i in (2, 3):
             name, n, k = SHAPES[i]
-            g, _ = capture([launcher(r % copies, i, xms[i], [cfgs[i]] * len(SHAPES)) for r in range(2 * copies)])
+            cfg = config(m, n, k)[0]
+            xm = [None] * len(SHAPES)
+            xm[i] = prefill_x(m, k, gen, dev)
+            gemms.append(({"layer": name, "m": m, "n": n, "k": k, "precision": "fp16"}, cfg,
+                          lambda c, i=i, xm=xm, cfg=cfg: launcher(c, i, xm, [cfg] * len(SHAPES))()))
+        for i in (2, 3):
+            name, n, k = SHAPES[i]
+            cfg = fp8_gemm_config(m, n, k)
+            x8 = (torch.randn((m, k), generator=gen, device=dev) * 50).to(torch.float8_e4m3fn)
+            xs8 = torch.rand((m,), generator=gen, device=dev) * 0.01 + 0.001
+            gemms.append(({"layer": name, "m": m, "n": n, "k": k, "precision": "fp8"}, cfg,
+                          lambda c, i=i, x8=x8, xs8=xs8, cfg=cfg: w4a8_gemm_ex(x8, xs8, *layers[c][i], GROUP, cfg)))
+        for _, _, fn in gemms:
+            for c in range(MFMA_LAUNCHES):
+                fn(c % copies)
+        torch.cuda.synchronize()
+        runs = []
+        for label, cfg, fn in gemms:
+            g, _ = capture([lambda r=r, fn=fn: fn(r % copies) for r in range(2 * copies)])
             ms = median_replay_ms(g, 2 * copies)
-            runs.append({"layer": name, "m": 256, "n": n, "k": k, "config": cfgs[i].to_dict(), "us": ms * 1e3,
-                         "tflops": 2 * 256 * n * k / (ms * 1e-3) / 1e12})
+            runs.append(dict(label, config=cfg.to_dict(), us=ms * 1e3,
+                             tflops=2 * m * label["n"] * label["k"] / (ms * 1e-3) / 1e12))
             del g
         print(json.dumps({"mfma_probe": {"launches": MFMA_LAUNCHES, "runs": runs}}), flush=True)
         return 0

@@ -28,7 +28,7 @@ def _line(value: float = 100.0, scale: float = 1.0) -> dict:  # type: ignore[typ
 
 def test_timed_rows_keys() -> None:
     rows = bench.timed_rows(_line())
-    assert rows == {"hip|o_proj|1": 4.0, "hip|down_proj|1": 11.0, "hip|gate_up_proj|16": 27.0,
+    assert rows == {"hip|o_proj|1": 4.0, "hip|down_proj|1": 11.0, "hip-cfg4|gate_up_proj|16": 27.0,
                     "hip-fp8|down_proj|256": 46.0, "hip|rmsnorm_fp8|4096": 11.0, "vendor-fp16|o_proj|1": 9.0,
                     "hip-stack|fused|1": pytest.approx(1400.0)}
 

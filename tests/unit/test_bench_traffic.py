@@ -97,7 +97,8 @@ def test_mfma_summary_from_synthetic_counters(tmp_path: Path, monkeypatch: pytes
         for _ in range(bench.MFMA_LAUNCHES):
             for c in bench.MFMA_COUNTERS:
                 v = {"SQ_VALU_MFMA_BUSY_CYCLES": layer_busy * cycles * bench.NUM_SIMDS,
-                     "GRBM_GUI_ACTIVE": cycles * bench.NUM_XCDS}.get(c, 1.0)
+                     "GRBM_GUI_ACTIVE": cycles * bench.NUM_XCDS, "SQ_INSTS_LDS": 1000.0,
+                     "SQ_LDS_BANK_CONFLICT": 500.0}.get(c, 1.0)
                 rows.append({"Dispatch_Id": did, "Kernel_Name": "void tf::gemm2_kernel<256, 192, 4, 2, 3>(...)",
                              "Counter_Name": c, "Counter_Value": v})
             did += 1
@@ -119,15 +120,32 @@ def test_mfma_summary_from_synthetic_counters(tmp_path: Path, monkeypatch: pytes
     log.write_text(json.dumps({"mfma_probe": {"launches": bench.MFMA_LAUNCHES, "runs": runs}}) + "\n")
     assert bench.mfma_summary(str(d), str(log), str(log)) == 0
     text = (tmp_path / "mfma.md").read_text()
-    assert "| gate_up_proj | gemm_mfma bm256 bn192 bk64 sk1 w8 st3 | 30.0% | 100.00 | 700.0 | 28.0% |" in text
-    assert "| down_proj | gemm_mfma bm256 bn192 bk64 sk1 w8 st3 | 20.0% |" in text
+    assert ("| gate_up_proj | W4A16 fp16 | gemm_mfma bm256 bn192 bk64 sk1 w8 st3 | 30.0% | 100.00 | 700.0 | "
+            "28.0% of 2.5 PF | 0.50 |") in text
+    assert "| down_proj | W4A16 fp16 | gemm_mfma bm256 bn192 bk64 sk1 w8 st3 | 20.0% |" in text
 
 
-def test_stats_summary_slices_the_probe_trace_in_dispatch_order(tmp_path: Path,
-                                                                monkeypatch: pytest.MonkeyPatch) -> None:
-    """--stats-summary: the kernel table comes from the bench trace; entry j of the kernel probe
-    owns dispatches j * launches .. (j + 1) * launches of its GEMV/GEMM kernels (reduce kernels
-    and other kernels skipped), averaged and set beside the bench's event-timed average."""
+def _marked_trace(groups: list, t0: int = 0) -> list:  # type: ignore[type-arg]
+    """A kernel trace: setup kernels, then each group's dispatches after a marker kernel, then
+    the calibration kernel (file order reversed: the summary orders by dispatch id)."""
+    trace, did, t = [], 1, t0
+    names = [("fill_kernel", 1000)]
+    for g in groups:
+        names += [("bitwise_not_kernel", 500)] + g
+    names += [("bitwise_not_kernel", 500), ("neg_kernel", 9000)]
+    for name, dur in names:
+        trace.append({"Dispatch_Id": did, "Kernel_Name": f"void tf::(anonymous namespace)::{name}(tf::LinearArgs, int)",
+                      "Start_Timestamp": t, "End_Timestamp": t + dur})
+        did, t = did + 1, t + dur + 1000
+    trace.reverse()
+    return trace
+
+
+def test_stats_summary_sums_each_ops_kernels_between_markers(tmp_path: Path,
+                                                            monkeypatch: pytest.MonkeyPatch) -> None:
+    """--stats-summary: the kernel table comes from the bench trace; the entry probe's dispatches
+    between marker kernels are one op's launches, and an op's time per launch is the sum over
+    its kernels (a split-K GEMM and its reduce), set beside the bench's event-timed average."""
     out = tmp_path / "stats.md"
     monkeypatch.setattr(bench, "STATS_SUMMARY", out)
     d = tmp_path / "prof" / "vm"
@@ -139,17 +157,13 @@ def test_stats_summary_slices_the_probe_trace_in_dispatch_order(tmp_path: Path,
                     "Calls": 3, "AverageNs": 20000, "MinNs": 19000, "MaxNs": 21000, "Percentage": 50.0})
     gemm = {"kernel": "gemm_mfma", "block_m": 128, "block_n": 256, "block_k": 64, "split_k": 8, "num_warps": 8,
             "num_stages": 3}
-    entries = [{"layer": "gate_up_proj", "m": 1, "config": CFGS[0]},
-               {"layer": "down_proj", "m": 256, "config": gemm}]
+    entries = [{"entry": "gate_up_proj M=1", "config": CFGS[0], "bytes": 1},
+               {"entry": "down_proj M=256", "config": gemm, "bytes": 1}]
     launches = 2
-    trace, did, t = [], 1, 0
-    for name, dur in (("gemv_kernel<1, 1, 2, 16, true, false, 1>", 20_000), ("gemv_kernel<1, 1, 2, 16, true, false, 1>", 22_000),
-                      ("gemm2_kernel<128, 256, 4, 2, 3>", 60_000), ("splitk_reduce_kernel", 8_000),
-                      ("gemm2_kernel<128, 256, 4, 2, 3>", 64_000), ("splitk_reduce_kernel", 8_000)):
-        trace.append({"Dispatch_Id": did, "Kernel_Name": f"void tf::(anonymous namespace)::{name}(tf::LinearArgs, int)",
-                      "Start_Timestamp": t, "End_Timestamp": t + dur})
-        did, t = did + 1, t + dur + 1000
-    trace.reverse()  # ordered by dispatch id, not by file order
+    trace = _marked_trace([[("gemv_kernel<1, 1, 2, 16, true, false, 1>", 20_000),
+                            ("gemv_kernel<1, 1, 2, 16, true, false, 1>", 22_000)],
+                           [("gemm2_kernel<128, 256, 4, 2, 3>", 60_000), ("splitk_reduce_kernel", 8_000),
+                            ("gemm2_kernel<128, 256, 4, 2, 3>", 64_000), ("splitk_reduce_kernel", 8_000)]])
     k = tmp_path / "kprof" / "vm"
     k.mkdir(parents=True)
     with open(k / "2_kernel_trace.csv", "w", newline="") as f:
@@ -157,23 +171,53 @@ def test_stats_summary_slices_the_probe_trace_in_dispatch_order(tmp_path: Path,
         w.writeheader()
         w.writerows(trace)
     line = {"metric": "m", "per_shape": [{"layer": "gate_up_proj", "m": 1, "us": 20.5, "config": CFGS[0]}],
-            "gemv_m2_m4": [], "gemm_m256": [{"layer": "down_proj", "m": 256, "us": 63.0, "config": gemm}],
+            "gemv_m2_m4": [], "gemm_m256": [{"layer": "down_proj", "m": 256, "us": 70.0, "config": gemm}],
             "gemm_m1024_m4096": []}
     log = tmp_path / "bench.log"
     log.write_text("noise\n" + json.dumps(line) + "\n")
-    kp = tmp_path / "kprobe.log"
-    kp.write_text(json.dumps({"kernel_probe": {"launches": launches, "entries": entries}}) + "\n")
+    kp = tmp_path / "entries.log"
+    kp.write_text(json.dumps({"entry_probe": {"launches": launches, "entries": entries}}) + "\n")
     args = [str(tmp_path / "prof"), str(log), str(log), str(tmp_path / "kprof"), str(kp)]
     assert bench.stats_summary(*args) == 0
     text = out.read_text()
-    assert "| gate_up_proj M=1 | gemv_dot bm1 bn16 bk128 sk1 w4 st2 | `tf::gemv_kernel<1, 1, 2, 16, true, false, 1>` | 21.00 | 20.50 | 1.02 |" in text
-    assert "| down_proj M=256 | gemm_mfma bm128 bn256 bk64 sk8 w8 st3 | `tf::gemm2_kernel<128, 256, 4, 2, 3>` | 62.00 | 63.00 | 0.98 |" in text
+    assert ("| gate_up_proj M=1 | gemv_dot bm1 bn16 bk128 sk1 w4 st2 | `tf::gemv_kernel<1, 1, 2, 16, true, false, 1>` "
+            "| 21.00 | 20.50 | 1.02 |") in text
+    assert ("| down_proj M=256 | gemm_mfma bm128 bn256 bk64 sk8 w8 st3 | `tf::gemm2_kernel<128, 256, 4, 2, 3>`, "
+            "`tf::splitk_reduce_kernel` | 70.00 | 70.00 | 1.00 |") in text
     # A probe run on another config is refused.
-    kp.write_text(json.dumps({"kernel_probe": {"launches": launches, "entries": [dict(entries[0], config=CFGS[1]),
-                                                                                 entries[1]]}}) + "\n")
+    kp.write_text(json.dumps({"entry_probe": {"launches": launches, "entries": [dict(entries[0], config=CFGS[1]),
+                                                                                entries[1]]}}) + "\n")
     out.unlink()
     assert bench.stats_summary(*args) == 1
     assert not out.exists()
+
+
+def test_counter_summary_sums_each_ops_kernels(tmp_path: Path, monkeypatch: pytest.MonkeyPatch) -> None:
+    """--counter-summary: FETCH/WRITE KiB of every dispatch between two markers, summed per launch
+    and scaled by the calibration kernel's known / counted bytes."""
+    out = tmp_path / "traffic.md"
+    monkeypatch.setattr(bench, "ENTRY_TRAFFIC_SUMMARY", out)
+    entries = [{"entry": "down_proj M=256", "config": CFGS[0], "bytes": 4096},
+               {"entry": "rmsnorm_fp8 T=4096", "bytes": 2048}]
+    for counter, sub in (("FETCH_SIZE", "f"), ("WRITE_SIZE", "w")):
+        d = tmp_path / sub
+        d.mkdir()
+        trace = _marked_trace([[("gemm2_kernel", 1), ("splitk_reduce_kernel", 1)] * 2, [("rmsnorm_kernel", 1)] * 2])
+        rows = [{"Dispatch_Id": r["Dispatch_Id"], "Kernel_Name": r["Kernel_Name"], "Counter_Name": counter,
+                 "Counter_Value": 2.0 if "gemm2" in r["Kernel_Name"] else 1.0 if "reduce" in r["Kernel_Name"] else
+                 (131072.0 if "neg" in r["Kernel_Name"] else 1.0)} for r in trace]
+        with open(d / "pmc_counter_collection.csv", "w", newline="") as f:
+            w = csv.DictWriter(f, fieldnames=list(rows[0]))
+            w.writeheader()
+            w.writerows(rows)
+    log = tmp_path / "probe.log"
+    log.write_text(json.dumps({"entry_probe": {"launches": 2, "entries": entries,
+                                                "calibration_bytes_in": 256 << 20}}) + "\n")
+    assert bench.counter_summary(str(tmp_path / "f"), str(tmp_path / "w"), str(log)) == 0
+    text = out.read_text()
+    # 256 MiB known / 128 MiB counted = scale 2; the GEMM launch is 3 KiB counted -> 6144 bytes.
+    assert "| down_proj M=256 | gemv_dot bm1 bn16 bk128 sk1 w4 st2 | 6144 | 6144 | 12288 | 4096 | 3.000 |" in text
+    assert "| rmsnorm_fp8 T=4096 | - | 2048 | 2048 | 4096 | 2048 | 2.000 |" in text
 
 
 def _bench_log(path: Path, cfg: dict) -> str:  # type: ignore[type-arg]
