@@ -59,17 +59,26 @@ def _x_with_outliers(m: int, k: int, device: torch.device, seed: int) -> torch.T
 
 
 def _check(y: torch.Tensor, x: torch.Tensor, wt32: torch.Tensor, w_absmax: float, what: str,
-           bias: torch.Tensor | None = None) -> None:
-    """y fp16 [M, N] against the fp32 product x @ wt32 (+ bias): derived bound plus half an
-    ulp of the rounded output, and the normwise bound."""
+           bias: torch.Tensor | None = None, half_ulp_allowance: bool = False) -> None:
+    """y fp16 [M, N] against the fp32 product x @ wt32 (+ bias): the derived bound, and the
+    normwise bound.
+
+    On the BASELINE configs' own data (x ~ N(0, 1), 1% of the rows x10) no allowance is added
+    for the output's fp16 rounding: there the vendor fp16 GEMM's error stays below 0.11 of the
+    roundoff scale at every full size (tolerances.json, ``w4a16_baseline_sizes``), inside c. A
+    decoder layer's inner linears read structured inputs (the value heads repeated seven times
+    for o_proj, the SiLU*mul activation for down) whose outputs are large next to the
+    sqrt(K)-scaled bound, so there half an fp16 ulp of each output is allowed on top."""
     ref = x.float() @ wt32
     if bias is not None:
         ref = ref + bias.float()
-    half_ulp = torch.from_numpy(np.spacing(np.abs(ref.cpu().numpy()).astype(np.float16)).astype(np.float32)).to(y.device) / 2
     # c sqrt(K) eps16 max|x| max|w| (tests/numerics/tolerance.py), maxima taken on the device
     tol = contract("cuda").c * math.sqrt(x.shape[1]) * EPS_FP16 * float(x.float().abs().max()) * w_absmax
-    excess = float(((y.float() - ref).abs() - half_ulp).max())
-    assert excess <= tol, f"{what}: error {excess:.3e} above half an ulp exceeds the derived bound {tol:.3e}"
+    err = (y.float() - ref).abs()
+    if half_ulp_allowance:
+        err = err - torch.from_numpy(np.spacing(np.abs(ref.cpu().numpy()).astype(np.float16)).astype(np.float32)).to(y.device) / 2
+    excess = float(err.max())
+    assert excess <= tol, f"{what}: error {excess:.3e} exceeds the derived bound {tol:.3e}"
     nw = relative_max_error(y.float().cpu().numpy(), ref.cpu().numpy())
     assert nw <= NORMWISE_MAX, f"{what}: normwise error {nw:.3e}"
 
@@ -142,21 +151,21 @@ def test_config5_decoder_layer_stage_by_stage(m: int, device: torch.device) -> N
 
     _, _, a = _norm(x, g1)
     y = ops.w4a16_linear(a, *qkv, bias, G, "hip")
-    _check(y, a, wt[0], wmax[0], f"qkv M={m}", bias)
+    _check(y, a, wt[0], wmax[0], f"qkv M={m}", bias, half_ulp_allowance=True)
     v = y[:, QKV - 512:].reshape(m, 4, 1, 128)
     attn = v.expand(m, 4, 7, 128).reshape(m, H)  # query head h reads KV group h // 7
     assert torch.equal(attn.reshape(m, 4, 7, 128)[:, :, 3], y[:, QKV - 512:].reshape(m, 4, 128))
     yo = ops.w4a16_linear(attn, *o, None, G, "hip")
-    _check(yo, attn, wt[1], wmax[1], f"o_proj M={m}")
+    _check(yo, attn, wt[1], wmax[1], f"o_proj M={m}", half_ulp_allowance=True)
     h1 = ops.w4a16_linear_residual(attn, *o, None, x, G, "hip")
     assert torch.equal(h1, x + yo)
     _, _, a2 = _norm(h1, g2)
     ygu = ops.w4a16_linear(a2, *gu, None, G, "hip")
-    _check(ygu, a2, wt[2], wmax[2], f"gate_up M={m}")
+    _check(ygu, a2, wt[2], wmax[2], f"gate_up M={m}", half_ulp_allowance=True)
     act = ops.w4a16_linear_silu_mul(a2, *gu, None, G, "hip")
     assert torch.equal(act, torch.nn.functional.silu(ygu[:, :INTER]) * ygu[:, INTER:])
     yd = ops.w4a16_linear(act, *down, None, G, "hip")
-    _check(yd, act, wt[3], wmax[3], f"down M={m}")
+    _check(yd, act, wt[3], wmax[3], f"down M={m}", half_ulp_allowance=True)
     out = ops.w4a16_linear_residual(act, *down, None, h1, G, "hip")
     assert torch.equal(out, h1 + yd)
     assert bool(torch.isfinite(out).all())

@@ -5,13 +5,14 @@ pinned references.
   the entry shipped for this GPU (``config_source == "shipped"``): gate_up and down at every
   prefill bucket M in {16, ..., 4096} and qkv at M = 2048 (reference
   tests/numerics/test_w4a16.py:48-57 checks every bucket through the op the same way). Bar: the
-  derived bound ``c sqrt(K) eps16 max|x| max|w|`` past half an fp16 ulp of the output and 1e-2
-  normwise, against the fp32 product of the exactly dequantized weights (the dequant kernel is
-  bit-exact with the oracle's ``dequantize_tf``); reruns bit-identical.
+  derived bound ``c sqrt(K) eps16 max|x| max|w|`` and 1e-2 normwise, against the fp32 product
+  of the exactly dequantized weights (the dequant kernel is bit-exact with the oracle's
+  ``dequantize_tf``); reruns bit-identical.
 * The W4A8 fp8 GEMM at ``fp8_gemm_config(bucket, n, k)`` (the op's choice, down's K split
   included) for gate_up and down at M in {256, 1024, 4096}, against
   ``oracle.reference.w4a8_exact_reference`` (fp64, weights never rounded) on rows that cover
-  every M tile, with the same bounds; the op equals the explicit config bit for bit.
+  every M tile, with the derived bound past half an fp16 ulp of the output (the exact-weight
+  oracle is not rounded) and 1e-2 normwise; the op equals the explicit config bit for bit.
 * One W4A8 decoder layer at M in {8, 2048} stage by stage: the norm codes and scales bit-exact
   against the oracle, each W4A8 linear within the bound of its own oracle (the fp16-weight
   ``w4a8_reference`` for the GEMV family, the exact-weight one for the fp8 GEMM), each W4A16
@@ -66,23 +67,32 @@ def _x_with_outliers(m: int, k: int, seed: int) -> torch.Tensor:
     return x.to(torch.float16)
 
 
-def _bound_check(got: np.ndarray, ref: np.ndarray, x_absmax: float, w_absmax: float, k: int, what: str) -> None:
-    """Derived bound past half an fp16 ulp of the reference, and the normwise bound."""
-    half_ulp = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64) / 2
+def _bound_check(got: np.ndarray, ref: np.ndarray, x_absmax: float, w_absmax: float, k: int, what: str,
+                 half_ulp_allowance: bool = True) -> None:
+    """Derived bound (past half an fp16 ulp of the reference, where allowed), and the normwise
+    bound. The W4A16 linears are held to the plain derived bound: at these full sizes the vendor
+    fp16 GEMM's own error stays below 0.11 of the roundoff scale (tolerances.json,
+    ``w4a16_baseline_sizes``), inside c."""
     tol = contract("cuda").c * math.sqrt(k) * EPS_FP16 * x_absmax * w_absmax
-    excess = float((np.abs(got - ref) - half_ulp).max())
-    assert excess <= tol, f"{what}: error {excess:.3e} above half an ulp exceeds the derived bound {tol:.3e}"
+    err = np.abs(got - ref)
+    if half_ulp_allowance:
+        err = err - np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64) / 2
+    excess = float(err.max())
+    assert excess <= tol, f"{what}: error {excess:.3e} exceeds the derived bound {tol:.3e}"
     nw = relative_max_error(got, ref)
     assert nw <= NORMWISE_MAX, f"{what}: normwise error {nw:.3e}"
 
 
 def _check_product(y: torch.Tensor, x: torch.Tensor, wt32: torch.Tensor, w_absmax: float, what: str,
-                   bias: torch.Tensor | None = None) -> None:
+                   bias: torch.Tensor | None = None, half_ulp_allowance: bool = False) -> None:
+    """A W4A16 linear against the fp32 product of its exactly dequantized weights: the plain
+    derived bound on BASELINE data, half an ulp allowed on top for a decoder layer's structured
+    inner inputs (see tests/gpu/test_baseline_configs.py ``_check``)."""
     ref = x.float() @ wt32
     if bias is not None:
         ref = ref + bias.float()
     _bound_check(y.float().cpu().numpy().astype(np.float64), ref.cpu().numpy().astype(np.float64),
-                 float(x.float().abs().max()), w_absmax, x.shape[1], what)
+                 float(x.float().abs().max()), w_absmax, x.shape[1], what, half_ulp_allowance=half_ulp_allowance)
 
 
 W4A16_CASES = [("gate_up", m) for m in PREFILL_M] + [("down", m) for m in PREFILL_M] + [("qkv", 2048)]
@@ -197,7 +207,7 @@ def test_w4a8_decoder_layer_stage_by_stage(m: int, device: torch.device) -> None
     v = y[:, QKV - 512:].reshape(m, 4, 1, 128)
     attn = v.expand(m, 4, 7, 128).reshape(m, H)
     yo = ops.w4a16_linear(attn, *o, None, G, "hip")
-    _check_product(yo, attn, wt[1], wmax[1], f"o_proj M={m}")
+    _check_product(yo, attn, wt[1], wmax[1], f"o_proj M={m}", half_ulp_allowance=True)
     h1 = ops.w4a16_linear_residual(attn, *o, None, x, G, "hip")
     assert torch.equal(h1, x + yo)
     q82, s2 = norm(h1, g2)
@@ -205,7 +215,7 @@ def test_w4a8_decoder_layer_stage_by_stage(m: int, device: torch.device) -> None
     act = ops.w4a8_linear(q82, s2, *gu, None, G, "hip", "silu_mul")
     assert torch.equal(act, torch.nn.functional.silu(ygu[:, :INTER]) * ygu[:, INTER:])
     yd = ops.w4a16_linear(act, *down, None, G, "hip")
-    _check_product(yd, act, wt[3], wmax[3], f"down M={m}")
+    _check_product(yd, act, wt[3], wmax[3], f"down M={m}", half_ulp_allowance=True)
     out = ops.w4a16_linear_residual(act, *down, None, h1, G, "hip")
     assert torch.equal(out, h1 + yd)
     assert bool(torch.isfinite(out).all())
