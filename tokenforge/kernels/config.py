@@ -29,10 +29,11 @@ gemv_mfma  max M (4) / 16 / 512: the    1 / waves per workgroup / steps in fligh
                                         resident; their waves take the range's 128-wide
                                         steps round robin (neighbouring blocks in flight)
 gemm_mfma  LDS tile M / tile N / tile K K slices across workgroups (fp32 workspace,
-                                        fixed-order reduce) / 4 or 8 waves / 2: two LDS
-                                        buffers, 3 and 4: pipelined with 2 and 3 x stages
+                                        fixed-order reduce) / 4, 8 or 16 waves / 2: two
+                                        LDS buffers, 3 and 4: pipelined with 2 and 3 x
+                                        stages, 6 and 7: the same on 16x16 MFMA fragments
                                         (block_k 64); block_k 128: skinny form, num_stages
-                                        = x stages
+                                        = x stages (wave-tile form: 4 + x stages)
 gemm_fp8   LDS tile M / tile N / 128    as gemm_mfma (8 waves, num_stages = x stages +
            (one group per block)        1). W4A8 only: e4m3 x on the fp8 MFMA, the group
                                         scale applied in fp32 after each group; chosen by
@@ -143,6 +144,13 @@ def _gemm_variants() -> list[tuple[str, int, int, int, int, int]]:
             ("gemm_mfma", 128, 256, 64, 8, 3), ("gemm_mfma", 256, 160, 64, 8, 3)]
     # ... and 16 waves (four per SIMD), 32-row wave tiles.
     out += [("gemm_mfma", 256, 192, 64, 16, 3), ("gemm_mfma", 256, 192, 64, 16, 4), ("gemm_mfma", 256, 128, 64, 16, 3)]
+    # num_stages 6 / 7: the same pipeline on 16x16 MFMA fragments (16-column wave-tile
+    # granularity): 256 x 160 tiles with 16 or 8 waves, 256 x 128 .. 256 with 8, 128-row tiles
+    # with 4 or 8.
+    out += [("gemm_mfma", 256, 160, 64, 16, 6), ("gemm_mfma", 256, 160, 64, 16, 7), ("gemm_mfma", 256, 160, 64, 8, 6),
+            ("gemm_mfma", 256, 160, 64, 8, 7), ("gemm_mfma", 256, 192, 64, 8, 6), ("gemm_mfma", 256, 224, 64, 8, 6),
+            ("gemm_mfma", 256, 128, 64, 8, 6), ("gemm_mfma", 256, 256, 64, 8, 6), ("gemm_mfma", 128, 160, 64, 4, 6),
+            ("gemm_mfma", 128, 192, 64, 4, 6), ("gemm_mfma", 128, 256, 64, 8, 6)]
     # block_k 128: skinny form (M <= 128), weights streamed into MFMA registers, 4 waves,
     # num_stages = x stages in LDS.
     skinny = [(1, 1, 3), (1, 2, 3), (1, 4, 3), (2, 1, 3), (2, 2, 3), (2, 4, 3), (4, 1, 3), (4, 2, 3),

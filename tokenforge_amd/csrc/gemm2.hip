@@ -10,8 +10,12 @@
 //   * the packed weight tile [BN][64/8] and its scales / zero points are loaded into a
 //     two-block register ring, dequantized once per workgroup (fp16(q - z) * s, one rounding)
 //     and written to one of two fp16 LDS buffers;
-//   * each wave reads 32x16 operand fragments (8 consecutive K per lane, the 32x32x16 MFMA
-//     layout) and accumulates a (BM/WM) x (BN/WN) sub-tile in fp32.
+//   * each wave reads F x 16 (F = 32) or F x 32 (F = 16) operand fragments, 8 consecutive K
+//     per lane, the layouts of v_mfma_f32_32x32x16_f16 and v_mfma_f32_16x16x32_f16, and
+//     accumulates a (BM/WM) x (BN/WN) sub-tile in fp32. The 16-wide form gives the wave tile a
+//     16-column granularity: 256 x 160 tiles with sixteen waves (32 x 80 wave tiles, about the
+//     LDS bytes per MFMA cycle of the 32 x 96 wave tiles of 256 x 192) cover gate_up at
+//     M = 256 in 237 workgroups instead of 198 on the 256 CUs.
 // Iteration kb waits for x block kb (issued S - 1 iterations earlier), issues x block
 // kb + S - 1, multiplies block kb, dequantizes block kb + 1 into the other B buffer, then issues
 // the weights of block kb + 3: weight latency is covered by two blocks of MFMA work (x comes
@@ -20,9 +24,14 @@
 // with out-of-range offsets and return zeros), so the count of loads in flight is the same on
 // every path and the waits stay exact.
 //
-// LDS rows hold 8 chunks of 16 bytes, two rows to a 256-byte bank line; chunk c of row r sits
-// in slot c ^ ((r / 2) % 8), so 16 consecutive rows at one chunk (the 16 lanes of a 16-byte
-// read or write phase on gfx950) hit 16 distinct 16-byte bank groups.
+// LDS rows hold 8 chunks of 16 bytes; chunk c of row r sits in slot c ^ s(r), with
+// s(r) = (r % 8) ^ ((r / 16) % 2). On gfx950 a 16-byte LDS read serves the wave in four phases
+// of 16 lanes (the wave's halves, each split by the parity of lane bits 2-4) over 16 bank
+// groups of 16 bytes (a 256-byte line), and a 16-byte write in eight phases of 8 consecutive
+// lanes over 8 bank groups (a 128-byte line). Under this s both patterns here are free of
+// bank conflicts: the fragment reads (lane l at row l % 32, chunk l / 32 + 2 kk) and the weight
+// writes (lane l at row 16 (l / 32) + l % 16, chunk 4 ((l / 16) % 2) + j). With
+// s(r) = (r / 2) % 8 the writes cost eight conflict cycles each (SQ_LDS_BANK_CONFLICT).
 //
 // Tile order: the grid is one-dimensional; workgroups are numbered XCD by XCD (xcd_tile) and
 // within an XCD the M tiles of one N tile are adjacent, so a weight panel is fetched into one
@@ -47,16 +56,21 @@ constexpr int kBK = 64;           // K per block
 constexpr int kRowChunks = 8;     // 16-byte chunks per 64-wide fp16 row
 constexpr uint32_t kChunkBytes = 16;
 
+__device__ __forceinline__ int slot_xor(int row) { return (row & 7) ^ ((row >> 4) & 1); }
+
 __device__ __forceinline__ uint32_t swz(int row, int chunk) {
-  return (uint32_t)(row * kRowChunks + (chunk ^ ((row >> 1) & 7))) * kChunkBytes;
+  return (uint32_t)(row * kRowChunks + (chunk ^ slot_xor(row))) * kChunkBytes;
 }
 
-template <int BM, int BN, int WM, int WN, int S>
+template <int BM, int BN, int WM, int WN, int S, int F>
 struct G2 {
+  static_assert(F == 32 || F == 16, "fragment edge");
   static constexpr int kWaves = WM * WN;
   static constexpr int kThreads = 64 * kWaves;
-  static constexpr int TM = BM / WM / 32;
-  static constexpr int TN = BN / WN / 32;
+  static constexpr int TM = BM / WM / F;
+  static constexpr int TN = BN / WN / F;
+  static constexpr int kSteps = kBK / (F == 32 ? 16 : 32);  // MFMA K steps per block
+  static constexpr int kAccRegs = F == 32 ? 16 : 4;         // fp32 accumulators per lane and MFMA tile
   static constexpr int kAStage = BM * kBK * 2;       // bytes of one x stage
   static constexpr int kBStage = BN * kBK * 2;       // bytes of one fp16 weight buffer
   static constexpr int kADma = kAStage / 1024;       // 1 KB LDS-load instructions per stage
@@ -65,18 +79,24 @@ struct G2 {
   static constexpr int kBPer = (kBChunks + kThreads - 1) / kThreads;
   static constexpr int kLds = S * kAStage + 2 * kBStage;
   static_assert(kWaves == 4 || kWaves == 8 || kWaves == 16, "four, eight or sixteen waves");
-  static_assert(TM >= 1 && TN >= 1 && BM % (32 * WM) == 0 && BN % (32 * WN) == 0, "wave tile");
+  static_assert(TM >= 1 && TN >= 1 && BM % (F * WM) == 0 && BN % (F * WN) == 0, "wave tile");
   static_assert(kADma % kWaves == 0, "x stage must split evenly over the waves");
   static_assert(S == 2 || S == 3, "x stages");
   // VMEM issued after x block kb (S - 1 iterations back) when iteration kb waits for it:
   // weights kb + 4 - S, then S - 2 whole iterations (x block, weights).
   static constexpr int kAfterA = 3 * kBPer + (S - 2) * (kAPerWave + 3 * kBPer);
-  // 16-wide K steps whose operand fragments are in flight ahead of the MFMAs: two where the
-  // registers allow it without lowering occupancy (LDS latency is the exposed cost), else one;
-  // none with 16 waves, where the SIMD's other three waves cover the LDS latency and the 128
-  // registers a wave has at that occupancy hold no second step.
-  static constexpr int kAhead =
-      kWaves == 16 ? 0 : (kWaves == 8 && TM * TN <= 6) || (kWaves == 4 && TM * TN <= 8) ? 2 : 1;
+  // K steps whose operand fragments are in flight ahead of the MFMAs: with F = 32 (16-wide
+  // steps) two where the registers allow it without lowering occupancy (LDS latency is the
+  // exposed cost), else one; with F = 16 (32-wide steps, two per block) one; none with 16
+  // waves, where the SIMD's other three waves cover the LDS latency and the 128 registers a
+  // wave has at that occupancy hold no second step.
+  // 16x16 fragments with sixteen waves (128 registers a wave) or more than 24 MFMA tiles a
+  // wave: B fragments streamed one at a time (no spills), not a whole step's set.
+  static constexpr bool kStreamB = F == 16 && (kWaves == 16 || TM * TN > 24);
+  static constexpr int kAhead = kWaves == 16 ? 0
+                                : F == 16    ? 1
+                                : (kWaves == 8 && TM * TN <= 6) || (kWaves == 4 && TM * TN <= 8) ? 2
+                                                                                                 : 1;
 };
 
 // Block barrier at the top of an iteration: at most N vector-memory loads of this wave still
@@ -92,10 +112,10 @@ __device__ __forceinline__ void block_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-template <int BM, int BN, int WM, int WN, int S>
+template <int BM, int BN, int WM, int WN, int S, int F>
 __global__ __launch_bounds__(64 * WM * WN) void gemm2_kernel(LinearArgs a, float* __restrict__ ws, int split_k,
                                                     int tiles_n, int tiles_m) {
-  using C = G2<BM, BN, WM, WN, S>;
+  using C = G2<BM, BN, WM, WN, S, F>;
   constexpr int TM = C::TM, TN = C::TN, BP = C::kBPer;
   constexpr bool kEvenB = C::kBChunks % C::kThreads == 0;  // every thread holds BP chunks
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -134,7 +154,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm2_kernel(LinearArgs a, float
   for (int i = 0; i < C::kAPerWave; ++i) {
     const int p = (wave + C::kWaves * i) * 64 + lane;
     const int row = p >> 3;
-    const int c = (p & 7) ^ ((row >> 1) & 7);
+    const int c = (p & 7) ^ slot_xor(row);
     const int m = m0 + row;
     a_off[i] = m < a.m ? (uint32_t)(((int64_t)m * a.ldx + c * 8) * 2) : kOutOfRange;
   }
@@ -222,31 +242,37 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm2_kernel(LinearArgs a, float
     for (int j = 0; j < 4; ++j) store_b_word(slot, buf, j, qp);
   };
 
-  f16v acc[TM][TN];
+  using Acc = std::conditional_t<F == 32, f16v, f4>;
+  constexpr int AR = C::kAccRegs;
+  Acc acc[TM][TN];
 #pragma unroll
   for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
     for (int tn = 0; tn < TN; ++tn)
 #pragma unroll
-      for (int q = 0; q < 16; ++q) acc[tm][tn][q] = 0.0f;
+      for (int q = 0; q < AR; ++q) acc[tm][tn][q] = 0.0f;
 
-  const int a_row0 = wm * TM * 32 + (lane & 31);
-  const int b_row0 = wn * TN * 32 + (lane & 31);
-  // Operand fragments of the kk-th 16-wide K step: lane l holds row / column l % 32 and the
-  // 8 K values of chunk 2 kk + l / 32.
+  const int a_row0 = wm * TM * F + (lane & (F - 1));
+  const int b_row0 = wn * TN * F + (lane & (F - 1));
+  // Operand fragments of the kk-th MFMA K step: lane l holds row / column l % F and the 8 K
+  // values of chunk 2 kk + l / 32 (F = 32, 16-wide steps) or 4 kk + l / 16 (F = 16, 32-wide).
   auto read_frags = [&](const uint8_t* A, const uint8_t* B, int kk, h8 (&af)[TM], h8 (&bf)[TN]) {
-    const int c = 2 * kk + (lane >> 5);
+    const int c = F == 32 ? 2 * kk + (lane >> 5) : 4 * kk + (lane >> 4);
 #pragma unroll
-    for (int tm = 0; tm < TM; ++tm) af[tm] = *reinterpret_cast<const h8*>(A + swz(a_row0 + tm * 32, c));
+    for (int tm = 0; tm < TM; ++tm) af[tm] = *reinterpret_cast<const h8*>(A + swz(a_row0 + tm * F, c));
 #pragma unroll
-    for (int tn = 0; tn < TN; ++tn) bf[tn] = *reinterpret_cast<const h8*>(B + swz(b_row0 + tn * 32, c));
+    for (int tn = 0; tn < TN; ++tn) bf[tn] = *reinterpret_cast<const h8*>(B + swz(b_row0 + tn * F, c));
   };
   auto mfmas = [&](const h8 (&af)[TM], const h8 (&bf)[TN]) {
 #pragma unroll
     for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
-      for (int tn = 0; tn < TN; ++tn)
-        acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[tm], bf[tn], acc[tm][tn], 0, 0, 0);
+      for (int tn = 0; tn < TN; ++tn) {
+        if constexpr (F == 32)
+          acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[tm], bf[tn], acc[tm][tn], 0, 0, 0);
+        else
+          acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[tm], bf[tn], acc[tm][tn], 0, 0, 0);
+      }
   };
 
   // ---- prologue: x blocks kb0 .. kb0 + S - 2 in flight; block kb0 dequantized into buffer 0;
@@ -278,22 +304,52 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm2_kernel(LinearArgs a, float
     // Fragments of step kk + D are read while the MFMAs of step kk run (D = kAhead steps in
     // flight); one word of each chunk of block kb + 1 is dequantized into the other buffer per
     // step.
-    constexpr int D = C::kAhead;
-    h8 af[kBK / 16][TM], bf[kBK / 16][TN];
-#pragma unroll
-    for (int kk = 0; kk < D; ++kk) read_frags(A, B, kk, af[kk], bf[kk]);
+    constexpr int KS = C::kSteps;
     QuantParams qp[BP];
-    slot_params(odd ^ 1, qp);
+    if constexpr (C::kStreamB) {
+      // 16x16 fragments where the registers hold no whole step of fragments next to the
+      // accumulators: per step the A fragments, then one 16-column B fragment at a time (the
+      // next one read before this one's MFMAs).
+      slot_params(odd ^ 1, qp);
 #pragma unroll
-    for (int kk = 0; kk < kBK / 16; ++kk) {
-      if (kk + D < kBK / 16) read_frags(A, B, kk + D, af[kk + D], bf[kk + D]);
-      // Raised priority while this wave queues its MFMAs: the SIMD's other wave then runs its
-      // LDS reads and dequantization in the shadow of these MFMAs instead of competing for
-      // issue slots with them (measured 6-8% on the M = 256 gate_up shape).
-      __builtin_amdgcn_s_setprio(1);
-      mfmas(af[kk], bf[kk]);
-      __builtin_amdgcn_s_setprio(0);
-      store_b_word(odd ^ 1, odd ^ 1, kk, qp);  // block kb + 1
+      for (int kk = 0; kk < KS; ++kk) {
+        const int c = 4 * kk + (lane >> 4);
+        h8 af[TM], bq[2];
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm) af[tm] = *reinterpret_cast<const h8*>(A + swz(a_row0 + tm * F, c));
+        bq[0] = *reinterpret_cast<const h8*>(B + swz(b_row0, c));
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) {
+          if (tn + 1 < TN) bq[(tn + 1) & 1] = *reinterpret_cast<const h8*>(B + swz(b_row0 + (tn + 1) * F, c));
+          __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+          for (int tm = 0; tm < TM; ++tm)
+            acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[tm], bq[tn & 1], acc[tm][tn], 0, 0, 0);
+          __builtin_amdgcn_s_setprio(0);
+        }
+#pragma unroll
+        for (int j = kk * 4 / KS; j < (kk + 1) * 4 / KS; ++j) store_b_word(odd ^ 1, odd ^ 1, j, qp);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
+      constexpr int D = C::kAhead;
+      h8 af[KS][TM], bf[KS][TN];
+#pragma unroll
+      for (int kk = 0; kk < D; ++kk) read_frags(A, B, kk, af[kk], bf[kk]);
+      slot_params(odd ^ 1, qp);
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) {
+        if (kk + D < KS) read_frags(A, B, kk + D, af[kk + D], bf[kk + D]);
+        // Raised priority while this wave queues its MFMAs: the SIMD's other wave then runs
+        // its LDS reads and dequantization in the shadow of these MFMAs instead of competing
+        // for issue slots with them (measured 6-8% on the M = 256 gate_up shape).
+        __builtin_amdgcn_s_setprio(1);
+        mfmas(af[kk], bf[kk]);
+        __builtin_amdgcn_s_setprio(0);
+        // Block kb + 1: the four words of each chunk, spread over the block's MFMA steps.
+#pragma unroll
+        for (int j = kk * 4 / KS; j < (kk + 1) * 4 / KS; ++j) store_b_word(odd ^ 1, odd ^ 1, j, qp);
+      }
     }
     issue_b(kb + 3, odd ^ 1);
   };
@@ -309,21 +365,23 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm2_kernel(LinearArgs a, float
   if (kb < kb1) iteration(kb, S == 2 ? 0 : st, std::integral_constant<int, 0>{});
 
   // ---- epilogue. D layout of the 32x32 MFMA: register q of lane l is row
-  // 8 (q / 4) + 4 (l / 32) + q % 4, column l % 32. A SiLU*mul epilogue pairs columns of
-  // different tiles: without split-K the fp16 y goes to the workspace for the SiLU*mul
-  // kernel, with split-K the fp32 partials go to the reduce kernel.
+  // 8 (q / 4) + 4 (l / 32) + q % 4, column l % 32; of the 16x16 MFMA: row 4 (l / 16) + q,
+  // column l % 16. A SiLU*mul epilogue pairs columns of different tiles: without split-K the
+  // fp16 y goes to the workspace for the SiLU*mul kernel, with split-K the fp32 partials go to
+  // the reduce kernel.
   const bool partials = split_k > 1;
   const bool stage_y = !partials && a.epilogue == TF_EPILOGUE_SILU_MUL;
 #pragma unroll
   for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
     for (int tn = 0; tn < TN; ++tn) {
-      const int n = n0 + (wn * TN + tn) * 32 + (lane & 31);
+      const int n = n0 + (wn * TN + tn) * F + (lane & (F - 1));
       if (n >= a.n) continue;
       const float b = (!partials && a.bias) ? half_bits_to_float(a.bias[n]) : 0.0f;
 #pragma unroll
-      for (int q = 0; q < 16; ++q) {
-        const int m = m0 + (wm * TM + tm) * 32 + 8 * (q / 4) + 4 * (lane >> 5) + (q % 4);
+      for (int q = 0; q < AR; ++q) {
+        const int m = m0 + (wm * TM + tm) * F +
+                      (F == 32 ? 8 * (q / 4) + 4 * (lane >> 5) + (q % 4) : 4 * (lane >> 4) + q);
         if (m >= a.m) continue;
         const float v = acc[tm][tn][q] * row_scale(a, m) + b;
         if (stage_y)
@@ -345,9 +403,9 @@ int64_t gemm2_workspace(const LinearArgs& a, const tf_gemm_config& cfg) {
   return lds_gemm_workspace(a, effective_split2(a, cfg));
 }
 
-template <int BM, int BN, int WM, int WN, int S>
+template <int BM, int BN, int WM, int WN, int S, int F>
 int launch_gemm2(const LinearArgs& a, const tf_gemm_config& cfg, float* ws, hipStream_t stream) {
-  using C = G2<BM, BN, WM, WN, S>;
+  using C = G2<BM, BN, WM, WN, S, F>;
   if ((1 << a.log2g) < kBK)
     return fail(TF_EINVAL, "tf_w4a16_linear: this gemm_mfma variant needs group_size >= 64 (block_k 64)");
   const int64_t x_bytes = ((int64_t)(a.m - 1) * a.ldx + a.k) * 2;
@@ -361,7 +419,7 @@ int launch_gemm2(const LinearArgs& a, const tf_gemm_config& cfg, float* ws, hipS
   const int tiles_m = (int)cdiv(a.m, BM);
   const int64_t grid = (int64_t)tiles_n * tiles_m * split;
   if (grid > 0x7FFFFFFF) return fail(TF_EINVAL, "tf_w4a16_linear: too many tiles");
-  auto kernel = gemm2_kernel<BM, BN, WM, WN, S>;
+  auto kernel = gemm2_kernel<BM, BN, WM, WN, S, F>;
   if (C::kLds > 64 * 1024 &&
       hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
                           C::kLds) != hipSuccess)
@@ -373,9 +431,11 @@ int launch_gemm2(const LinearArgs& a, const tf_gemm_config& cfg, float* ws, hipS
 }
 
 // num_stages = S + 1 (3: two x stages, 4: three) tells these variants apart from the
-// two-buffer kernel (num_stages 2); num_warps = WM * WN.
+// two-buffer kernel (num_stages 2), S + 4 (6, 7) the 16x16 fragment form; num_warps = WM * WN.
 #define TF_GEMM2(BM, BN, WM, WN, S) \
-  {{TF_KERNEL_GEMM_MFMA, BM, BN, 64, 1, WM * WN, S + 1}, (launch_gemm2<BM, BN, WM, WN, S>), gemm2_workspace}
+  {{TF_KERNEL_GEMM_MFMA, BM, BN, 64, 1, WM * WN, S + 1}, (launch_gemm2<BM, BN, WM, WN, S, 32>), gemm2_workspace}
+#define TF_GEMM2F16(BM, BN, WM, WN, S) \
+  {{TF_KERNEL_GEMM_MFMA, BM, BN, 64, 1, WM * WN, S + 4}, (launch_gemm2<BM, BN, WM, WN, S, 16>), gemm2_workspace}
 
 const Variant kGemm2Variants[] = {
     // four waves, three x stages
@@ -387,6 +447,11 @@ const Variant kGemm2Variants[] = {
     TF_GEMM2(256, 128, 4, 2, 2), TF_GEMM2(128, 256, 2, 4, 2), TF_GEMM2(256, 160, 8, 1, 2),
     // sixteen waves (four per SIMD): 32-row wave tiles
     TF_GEMM2(256, 192, 8, 2, 2), TF_GEMM2(256, 192, 8, 2, 3), TF_GEMM2(256, 128, 8, 2, 2),
+    // 16x16 fragments: sixteen waves (32-row wave tiles, 16-column granularity), eight waves
+    TF_GEMM2F16(256, 160, 8, 2, 2), TF_GEMM2F16(256, 160, 8, 2, 3), TF_GEMM2F16(256, 160, 4, 2, 2),
+    TF_GEMM2F16(256, 160, 4, 2, 3), TF_GEMM2F16(256, 192, 4, 2, 2), TF_GEMM2F16(256, 224, 4, 2, 2),
+    TF_GEMM2F16(256, 128, 4, 2, 2), TF_GEMM2F16(256, 256, 4, 2, 2), TF_GEMM2F16(128, 160, 2, 2, 2),
+    TF_GEMM2F16(128, 192, 2, 2, 2), TF_GEMM2F16(128, 256, 2, 4, 2),
 };
 
 }  // namespace
