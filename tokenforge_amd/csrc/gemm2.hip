@@ -112,8 +112,11 @@ __device__ __forceinline__ void block_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
+// Four-wave 16x16-fragment tiles are compiled for two workgroups per CU (256 registers a
+// wave): their LDS (two x stages, two weight buffers) fits twice, and the two workgroups'
+// barriers then fall at different times.
 template <int BM, int BN, int WM, int WN, int S, int F>
-__global__ __launch_bounds__(64 * WM * WN) void gemm2_kernel(LinearArgs a, float* __restrict__ ws, int split_k,
+__global__ __launch_bounds__(64 * WM * WN, (WM * WN == 4 && F == 16) ? 2 : 1) void gemm2_kernel(LinearArgs a, float* __restrict__ ws, int split_k,
                                                     int tiles_n, int tiles_m) {
   using C = G2<BM, BN, WM, WN, S, F>;
   constexpr int TM = C::TM, TN = C::TN, BP = C::kBPer;
@@ -451,7 +454,7 @@ const Variant kGemm2Variants[] = {
     TF_GEMM2F16(256, 160, 8, 2, 2), TF_GEMM2F16(256, 160, 8, 2, 3), TF_GEMM2F16(256, 160, 4, 2, 2),
     TF_GEMM2F16(256, 160, 4, 2, 3), TF_GEMM2F16(256, 192, 4, 2, 2), TF_GEMM2F16(256, 224, 4, 2, 2),
     TF_GEMM2F16(256, 128, 4, 2, 2), TF_GEMM2F16(256, 256, 4, 2, 2), TF_GEMM2F16(128, 160, 2, 2, 2),
-    TF_GEMM2F16(128, 192, 2, 2, 2), TF_GEMM2F16(128, 256, 2, 4, 2),
+    TF_GEMM2F16(128, 128, 2, 2, 2), TF_GEMM2F16(128, 256, 2, 4, 2),
 };
 
 }  // namespace
