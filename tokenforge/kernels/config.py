@@ -168,7 +168,7 @@ def _gemm_variants() -> list[tuple[str, int, int, int, int, int]]:
 # W4A8 fp8 GEMM tiles (block_m, block_n, waves along M, waves along N, x stages), in the
 # library's order.
 FP8_TILES: tuple[tuple[int, int, int, int, int], ...] = (
-    (256, 192, 4, 2, 2), (256, 128, 4, 2, 2), (128, 256, 2, 4, 2), (256, 160, 8, 1, 2), (128, 128, 2, 4, 2),
+    (256, 192, 4, 2, 2), (256, 128, 4, 2, 2), (128, 256, 2, 4, 2), (256, 160, 4, 2, 2), (128, 128, 2, 4, 2),
     (256, 192, 4, 2, 3),
 )
 

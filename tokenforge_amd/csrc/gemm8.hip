@@ -378,7 +378,7 @@ int launch_gemm8(const LinearArgs& a, const tf_gemm_config& cfg, float* ws, hipS
 
 const Variant kGemm8Variants[] = {
     TF_GEMM8(256, 192, 4, 2, 2), TF_GEMM8(256, 128, 4, 2, 2), TF_GEMM8(128, 256, 2, 4, 2),
-    TF_GEMM8(256, 160, 8, 1, 2), TF_GEMM8(128, 128, 2, 4, 2), TF_GEMM8(256, 192, 4, 2, 3),
+    TF_GEMM8(256, 160, 4, 2, 2), TF_GEMM8(128, 128, 2, 4, 2), TF_GEMM8(256, 192, 4, 2, 3),
 };
 
 }  // namespace
