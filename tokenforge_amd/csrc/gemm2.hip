@@ -13,16 +13,16 @@
 //   * each wave reads F x 16 (F = 32) or F x 32 (F = 16) operand fragments, 8 consecutive K
 //     per lane, the layouts of v_mfma_f32_32x32x16_f16 and v_mfma_f32_16x16x32_f16, and
 //     accumulates a (BM/WM) x (BN/WN) sub-tile in fp32. The 16-wide form gives the wave tile a
-//     16-column granularity: 256 x 160 tiles with sixteen waves (32 x 80 wave tiles, about the
-//     LDS bytes per MFMA cycle of the 32 x 96 wave tiles of 256 x 192) cover gate_up at
-//     M = 256 in 237 workgroups instead of 198 on the 256 CUs.
+//     16-column granularity: 256 x 160 tiles (8 waves, 64 x 80 wave tiles) cover gate_up at
+//     M = 256 in 237 workgroups instead of the 198 of 256 x 192 on the 256 CUs, and
+//     256 x 224 tiles fit gate_up and down at M >= 1024 in fewer rounds.
 // Iteration kb waits for x block kb (issued S - 1 iterations earlier), issues x block
 // kb + S - 1, multiplies block kb, dequantizes block kb + 1 into the other B buffer, then issues
 // the weights of block kb + 3: weight latency is covered by two blocks of MFMA work (x comes
 // from L2 and is covered by S - 1 blocks), and there is one barrier per block. With S = 2 the
-// stage of a block is a compile-time value of the two-iteration loop body. The loop body is straight-line (loads past the K range are issued
-// with out-of-range offsets and return zeros), so the count of loads in flight is the same on
-// every path and the waits stay exact.
+// stage of a block is a compile-time value of the two-iteration loop body. The loop body is
+// straight-line (loads past the K range are issued with out-of-range offsets and return
+// zeros), so the count of loads in flight is the same on every path and the waits stay exact.
 //
 // LDS rows hold 8 chunks of 16 bytes; chunk c of row r sits in slot c ^ s(r), with
 // s(r) = (r % 8) ^ ((r / 16) % 2). On gfx950 a 16-byte LDS read serves the wave in four phases
@@ -30,8 +30,9 @@
 // groups of 16 bytes (a 256-byte line), and a 16-byte write in eight phases of 8 consecutive
 // lanes over 8 bank groups (a 128-byte line). Under this s both patterns here are free of
 // bank conflicts: the fragment reads (lane l at row l % 32, chunk l / 32 + 2 kk) and the weight
-// writes (lane l at row 16 (l / 32) + l % 16, chunk 4 ((l / 16) % 2) + j). With
-// s(r) = (r / 2) % 8 the writes cost eight conflict cycles each (SQ_LDS_BANK_CONFLICT).
+// writes (lane l at row 16 (l / 32) + l % 16, chunk 4 ((l / 16) % 2) + j), and the 16x16
+// fragment reads (lane l at row l % 16, chunk l / 16 + 4 kk) too. With s(r) = (r / 2) % 8
+// the writes cost eight conflict cycles each (SQ_LDS_BANK_CONFLICT).
 //
 // Tile order: the grid is one-dimensional; workgroups are numbered XCD by XCD (xcd_tile) and
 // within an XCD the M tiles of one N tile are adjacent, so a weight panel is fetched into one
