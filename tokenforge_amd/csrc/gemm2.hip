@@ -375,6 +375,61 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN == 4 && F == 16) ? 2 : 1) vo
   // the reduce kernel.
   const bool partials = split_k > 1;
   const bool stage_y = !partials && a.epilogue == TF_EPILOGUE_SILU_MUL;
+  auto row_of = [&](int tm, int q) {
+    return (wm * TM + tm) * F + (F == 32 ? 8 * (q / 4) + 4 * (lane >> 5) + (q % 4) : 4 * (lane >> 4) + q);
+  };
+  // fp16 results (y, or y staged for SiLU*mul) leave through LDS: the tile is written there in
+  // the MFMA layout, then every thread copies whole 16-byte row pieces (8 columns) to global
+  // memory, with the residual read the same way, instead of one 2-byte store per value spread
+  // over four rows. Needs N, the row strides and the pointers in 16-byte units; the values and
+  // their rounding are the per-value path's.
+  uint16_t* const dst = stage_y ? reinterpret_cast<uint16_t*>(ws) : a.out;
+  const int64_t ldd = stage_y ? (int64_t)a.n : a.ldo;
+  const bool residual = !stage_y && a.epilogue == TF_EPILOGUE_RESIDUAL;
+  const bool staged = !partials && (a.n & 7) == 0 && (ldd & 7) == 0 && (reinterpret_cast<uintptr_t>(dst) & 15) == 0 &&
+                      (!residual || ((a.ldr & 7) == 0 && (reinterpret_cast<uintptr_t>(a.residual) & 15) == 0));
+  if (staged) {
+    static_assert(BM * BN * 2 <= C::kLds, "the fp16 tile fits in the kernel's LDS");
+    // Every wave is past its last fragment read and every LDS load of the pipeline (the x
+    // stages past K included) has landed before the stages are overwritten.
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_s_barrier();
+    uint16_t* const tile = reinterpret_cast<uint16_t*>(smem);  // [BM][BN]
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn) {
+        const int c = (wn * TN + tn) * F + (lane & (F - 1));
+        const int n = n0 + c;
+        const float b = (a.bias && n < a.n) ? half_bits_to_float(a.bias[n]) : 0.0f;
+#pragma unroll
+        for (int q = 0; q < AR; ++q) {
+          const int r = row_of(tm, q);
+          tile[r * BN + c] = f16_bits(acc[tm][tn][q] * row_scale(a, m0 + r) + b);
+        }
+      }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    constexpr int kPieces = BM * BN / 8;
+    for (int e = tid; e < kPieces; e += C::kThreads) {
+      const int r = e / (BN / 8);
+      const int c = (e - r * (BN / 8)) * 8;
+      const int m = m0 + r, n = n0 + c;
+      if (m >= a.m || n >= a.n) continue;  // N % 8 == 0: a piece is inside N or past it
+      u4 v = *reinterpret_cast<const u4*>(tile + r * BN + c);
+      if (residual) {
+        const u4 res = *reinterpret_cast<const u4*>(a.residual + (int64_t)m * a.ldr + n);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const uint16_t lo = finish_residual(half_bits_to_float((uint16_t)v[w]), (uint16_t)res[w]);
+          const uint16_t hi = finish_residual(half_bits_to_float((uint16_t)(v[w] >> 16)), (uint16_t)(res[w] >> 16));
+          v[w] = (uint32_t)lo | ((uint32_t)hi << 16);
+        }
+      }
+      *reinterpret_cast<u4*>(dst + (int64_t)m * ldd + n) = v;
+    }
+    return;
+  }
 #pragma unroll
   for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
@@ -384,8 +439,7 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN == 4 && F == 16) ? 2 : 1) vo
       const float b = (!partials && a.bias) ? half_bits_to_float(a.bias[n]) : 0.0f;
 #pragma unroll
       for (int q = 0; q < AR; ++q) {
-        const int m = m0 + (wm * TM + tm) * F +
-                      (F == 32 ? 8 * (q / 4) + 4 * (lane >> 5) + (q % 4) : 4 * (lane >> 4) + q);
+        const int m = m0 + row_of(tm, q);
         if (m >= a.m) continue;
         const float v = acc[tm][tn][q] * row_scale(a, m) + b;
         if (stage_y)
