@@ -378,17 +378,12 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN == 4 && F == 16) ? 2 : 1) vo
   auto row_of = [&](int tm, int q) {
     return (wm * TM + tm) * F + (F == 32 ? 8 * (q / 4) + 4 * (lane >> 5) + (q % 4) : 4 * (lane >> 4) + q);
   };
-  // fp16 results (y, or y staged for SiLU*mul) leave through LDS: the tile is written there in
-  // the MFMA layout, then every thread copies whole 16-byte row pieces (8 columns) to global
-  // memory, with the residual read the same way, instead of one 2-byte store per value spread
-  // over four rows. Needs N, the row strides and the pointers in 16-byte units; the values and
-  // their rounding are the per-value path's.
+  // fp16 results (y, or y staged for SiLU*mul) leave through LDS in 16-byte row pieces
+  // (tile_copy_out); the values and their rounding are the per-value path's below.
   uint16_t* const dst = stage_y ? reinterpret_cast<uint16_t*>(ws) : a.out;
   const int64_t ldd = stage_y ? (int64_t)a.n : a.ldo;
   const bool residual = !stage_y && a.epilogue == TF_EPILOGUE_RESIDUAL;
-  const bool staged = !partials && (a.n & 7) == 0 && (ldd & 7) == 0 && (reinterpret_cast<uintptr_t>(dst) & 15) == 0 &&
-                      (!residual || ((a.ldr & 7) == 0 && (reinterpret_cast<uintptr_t>(a.residual) & 15) == 0));
-  if (staged) {
+  if (!partials && tile_copy_out_ok(a, dst, ldd, residual)) {
     static_assert(BM * BN * 2 <= C::kLds, "the fp16 tile fits in the kernel's LDS");
     // Every wave is past its last fragment read and every LDS load of the pipeline (the x
     // stages past K included) has landed before the stages are overwritten.
@@ -410,24 +405,7 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN == 4 && F == 16) ? 2 : 1) vo
       }
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
     __builtin_amdgcn_s_barrier();
-    constexpr int kPieces = BM * BN / 8;
-    for (int e = tid; e < kPieces; e += C::kThreads) {
-      const int r = e / (BN / 8);
-      const int c = (e - r * (BN / 8)) * 8;
-      const int m = m0 + r, n = n0 + c;
-      if (m >= a.m || n >= a.n) continue;  // N % 8 == 0: a piece is inside N or past it
-      u4 v = *reinterpret_cast<const u4*>(tile + r * BN + c);
-      if (residual) {
-        const u4 res = *reinterpret_cast<const u4*>(a.residual + (int64_t)m * a.ldr + n);
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          const uint16_t lo = finish_residual(half_bits_to_float((uint16_t)v[w]), (uint16_t)res[w]);
-          const uint16_t hi = finish_residual(half_bits_to_float((uint16_t)(v[w] >> 16)), (uint16_t)(res[w] >> 16));
-          v[w] = (uint32_t)lo | ((uint32_t)hi << 16);
-        }
-      }
-      *reinterpret_cast<u4*>(dst + (int64_t)m * ldd + n) = v;
-    }
+    tile_copy_out<BM, BN, C::kThreads>(a, tile, dst, ldd, residual, m0, n0);
     return;
   }
 #pragma unroll

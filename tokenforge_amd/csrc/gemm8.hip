@@ -301,6 +301,36 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm8_kernel(LinearArgs a, float
   // ---- epilogue. D layout: register q of lane l is row 4 (l / 16) + q, column l % 16.
   const bool partials = split_k > 1;
   const bool stage_y = !partials && a.epilogue == TF_EPILOGUE_SILU_MUL;
+  // fp16 results (y, or y staged for SiLU*mul) leave through LDS in 16-byte row pieces
+  // (tile_copy_out); the values and their rounding are the per-value path's below.
+  uint16_t* const dst = stage_y ? reinterpret_cast<uint16_t*>(ws) : a.out;
+  const int64_t ldd = stage_y ? (int64_t)a.n : a.ldo;
+  const bool residual = !stage_y && a.epilogue == TF_EPILOGUE_RESIDUAL;
+  if (!partials && tile_copy_out_ok(a, dst, ldd, residual)) {
+    static_assert(BM * BN * 2 <= C::kLds, "the fp16 tile fits in the kernel's LDS");
+    // Every wave is past its last fragment read and every LDS load of the pipeline (the x
+    // stages past K included) has landed before the stages are overwritten.
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_s_barrier();
+    uint16_t* const tile = reinterpret_cast<uint16_t*>(smem);  // [BM][BN]
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn) {
+        const int c = (wn * TN + tn) * 16 + (lane & 15);
+        const int n = n0 + c;
+        const float b = (a.bias && n < a.n) ? half_bits_to_float(a.bias[n]) : 0.0f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int r = (wm * TM + tm) * 16 + 4 * (lane >> 4) + q;
+          tile[r * BN + c] = f16_bits(acc[tm][tn][q] * row_scale(a, m0 + r) + b);
+        }
+      }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    tile_copy_out<BM, BN, C::kThreads>(a, tile, dst, ldd, residual, m0, n0);
+    return;
+  }
 #pragma unroll
   for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
