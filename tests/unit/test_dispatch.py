@@ -182,8 +182,11 @@ def test_decode_buckets_offer_both_gemv_forms_and_work_splits() -> None:
     # K split over the waves, columns split over the waves, or the stream form
     assert {c.block_k for c in cands} == {128, 256, 512}
     assert {c.kernel for c in candidate_configs(8, 128)} == {"gemv_mfma"}  # dot form: M <= 4
-    assert {c.block_k for c in candidate_configs(8, 128)} == {128, 256}  # stream form: M <= 4
-    assert any(c.stream for c in candidate_configs(4, 128))
+    assert {c.block_k for c in candidate_configs(8, 128)} == {128, 256, 512}
+    # the stream form: block_m 4 for buckets up to 4, block_m 8 for the bucket of 8
+    assert {c.block_m for c in candidate_configs(8, 128) if c.stream} == {8}
+    assert {c.block_m for c in candidate_configs(4, 128) if c.stream} == {4}
+    assert not any(c.stream for c in candidate_configs(16, 128))
     assert {c.block_m for c in candidate_configs(4, 128) if c.kernel == "gemv_dot"} == {4}
     assert {c.block_m for c in candidate_configs(32, 128) if c.family == "gemv"} == {16, 32}
 
@@ -206,13 +209,21 @@ def test_config_validation(kwargs: dict, match: str) -> None:
 
 
 def test_stream_form_rules() -> None:
-    """The stream form serves buckets up to 4; the heuristic default picks it where it applies
-    under every epilogue and keeps the K-split GEMV elsewhere."""
+    """The stream form serves buckets up to 4 (block_m 4) and the bucket of 8 (block_m 8); the
+    heuristic default picks it where it applies under every epilogue and keeps the K-split GEMV
+    elsewhere. The RMSNorm prologue runs on the block_m 4 form only."""
     from tokenforge.kernels.config import default_config, split_k_gemv_config, stream_form_applies
 
     s = GemmConfig("gemv_mfma", 4, 16, 512, 1, 8, 2)
     assert s.stream and s.family == "gemv"
     assert [b for b in M_BUCKETS if s.fits_bucket(b)] == [1, 2, 4]
+    s8 = GemmConfig("gemv_mfma", 8, 16, 512, 1, 8, 2)
+    assert s8.stream and [b for b in M_BUCKETS if s8.fits_bucket(b)] == [8]
+    assert stream_form_applies(8, 37888, 3584, 8, max_m=8)
+    assert stream_form_applies(5, 4608, 3584, 16, max_m=8)
+    assert not stream_form_applies(8, 37888, 3584, 8, norm=True, max_m=8)  # the prologue: M <= 4
+    assert not stream_form_applies(8, 3584, 18944, 8, max_m=8)  # x does not fit 96 KiB of LDS
+    assert not stream_form_applies(9, 4608, 3584, 8, max_m=8)
     assert stream_form_applies(1, 37888, 3584, 8)
     assert stream_form_applies(2, 3584, 18944, 16)
     assert not stream_form_applies(4, 3584, 18944, 8)  # x does not fit 96 KiB of LDS

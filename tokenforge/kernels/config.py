@@ -87,15 +87,19 @@ def _gemv_variants() -> list[tuple[str, int, int, int, int, int]]:
 
 
 STREAM_BLOCK_K = 512
-"""``block_k`` of the GEMV stream form (gemv_mfma, M <= STREAM_MAX_M)."""
+"""``block_k`` of the GEMV stream form (gemv_mfma, M <= its block_m)."""
 STREAM_MAX_M = 4
+"""block_m of the stream form that serves M <= 4 (and runs the RMSNorm prologue)."""
+STREAM_WIDE_M = 8
+"""block_m of the stream form that serves the bucket of M = 5..8 (no RMSNorm prologue)."""
 STREAM_MAX_X_BYTES = 96 * 1024
 """The stream form stages all of x in LDS: M rows of K + 8 fp16 values must fit this."""
 
 
 def _stream_variants() -> list[tuple[str, int, int, int, int, int]]:
-    # Ring depth 2 and 4, every wave count.
-    return [("gemv_mfma", STREAM_MAX_M, 16, STREAM_BLOCK_K, w, p) for p in (2, 4) for w in _WAVES]
+    # block_m 4: ring depth 2 and 4, every wave count; block_m 8: 4, 8 or 16 waves.
+    return ([("gemv_mfma", STREAM_MAX_M, 16, STREAM_BLOCK_K, w, p) for p in (2, 4) for w in _WAVES]
+            + [("gemv_mfma", STREAM_WIDE_M, 16, STREAM_BLOCK_K, w, p) for p in (2, 4) for w in (4, 8, 16)])
 
 
 NORM_MAX_K = 8192
@@ -111,17 +115,19 @@ def norm_scratch_bytes(m: int, k: int) -> int:
     return m * lpad * 8 + 256
 
 
-def stream_form_applies(m: int, n: int, k: int, num_warps: int, norm: bool = False) -> bool:
+def stream_form_applies(m: int, n: int, k: int, num_warps: int, norm: bool = False,
+                        max_m: int = STREAM_MAX_M) -> bool:
     """Whether the op runs a call of this shape on the GEMV stream form when its bucket's config
-    is that form: M <= 4, N % 32 == 0, K % 128 == 0 with at least one 128-wide step per wave,
-    and x small enough to stage in LDS. The rule does not depend on the epilogue, so a plain
-    call and its fused SiLU*mul or residual twin run the same kernel and agree bit for bit (the
-    library itself runs plain and residual calls on N % 16 == 0 as well). With ``norm`` (the
-    RMSNorm prologue of ``rmsnorm_fp8_w4a16_linear``) K is at most NORM_MAX_K and the staged x
-    plus the prologue's scratch must fit."""
+    is that form (``max_m``: the config's block_m): M <= max_m, N % 32 == 0, K % 128 == 0 with
+    at least one 128-wide step per wave, and x small enough to stage in LDS. The rule does not
+    depend on the epilogue, so a plain call and its fused SiLU*mul or residual twin run the same
+    kernel and agree bit for bit (the library itself runs plain and residual calls on N % 16 ==
+    0 as well). With ``norm`` (the RMSNorm prologue of ``rmsnorm_fp8_w4a16_linear``, on the
+    block_m 4 form only) M is at most 4, K at most NORM_MAX_K and the staged x plus the
+    prologue's scratch must fit."""
     x_bytes = m * (k + 8) * 2 + (norm_scratch_bytes(m, k) if norm else 0)
     return (
-        1 <= m <= STREAM_MAX_M
+        1 <= m <= (STREAM_MAX_M if norm else max_m)
         and n % 32 == 0
         and k % 128 == 0
         and k // 128 >= num_warps
@@ -261,8 +267,8 @@ class GemmConfig:
             return bucket >= GEMM_MIN_M
         if bucket > GEMV_MAX_M:
             return False
-        if self.stream:
-            return bucket <= self.block_m
+        if self.stream:  # block_m 4 serves buckets up to 4, block_m 8 the bucket above
+            return bucket <= self.block_m and (self.block_m == STREAM_MAX_M or bucket > STREAM_MAX_M)
         return self.kernel != "gemv_dot" or self.block_m >= bucket
 
     def to_dict(self) -> dict[str, Any]:

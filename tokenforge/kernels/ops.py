@@ -64,6 +64,7 @@ from tokenforge.kernels.config import (
     M_BUCKETS,
     MAX_BUCKET_M,
     NUM_CUS,
+    STREAM_MAX_M,
     GemmConfig,
     fp8_gemm_applies,
     fp8_gemm_config,
@@ -127,7 +128,7 @@ def _gpu_config(device: torch.device, m: int, n: int, k: int, group_size: int) -
         # Above the largest bucket its config is reused; once the M tiles alone fill the CUs a
         # K split only adds the fp32 workspace (split * M * N * 4 bytes) and its reduction.
         cfg = dataclasses.replace(cfg, split_k=1)
-    if cfg.stream and not stream_form_applies(m, n, k, cfg.num_warps):
+    if cfg.stream and not stream_form_applies(m, n, k, cfg.num_warps, max_m=cfg.block_m):
         # The bucket's config is the stream form but this call is outside it (N % 32 == 16, or
         # an x too long to stage): the K-split GEMV runs it, whatever the epilogue.
         cfg = split_k_gemv_config(n, k)
@@ -183,7 +184,8 @@ def _resolve_launch(kind: int, epilogue: int, m: int, n: int, k: int, group_size
         need = int(h.tf_w4a8_workspace_bytes_ex(m, n, k, group_size, ctypes.byref(c), epilogue))
     else:
         if kind == KIND_NORM_LINEAR:
-            fused = int(cfg.stream and stream_form_applies(m, n, k, cfg.num_warps, norm=True))
+            fused = int(cfg.stream and cfg.block_m == STREAM_MAX_M
+                        and stream_form_applies(m, n, k, cfg.num_warps, norm=True))
         c = _w4a16.to_c_config(cfg)
         need = 0 if fused else int(h.tf_w4a16_workspace_bytes_ex(m, n, k, group_size, ctypes.byref(c), epilogue))
     bucket = _BUCKET_LABELS.index(dispatch.bucket_label(m))
@@ -414,7 +416,7 @@ def _rmsnorm_fp8_w4a16_linear(x, norm_weight, eps, qweight_t, scales, qzeros, bi
         _record_host(m, backend)
         return host.linear(a, qweight_t, scales, qzeros, bias, group_size, epilogue).reshape(out_shape)
     cfg = _decide(x2, m, n, k, group_size, backend)
-    if cfg.stream and stream_form_applies(m, n, k, cfg.num_warps, norm=True):
+    if cfg.stream and cfg.block_m == STREAM_MAX_M and stream_form_applies(m, n, k, cfg.num_warps, norm=True):
         y = _w4a16.rmsnorm_fp8_w4a16_gemm_ex(
             x2, norm_weight, eps, qweight_t, scales, qzeros, group_size, cfg, bias, epilogue
         )

@@ -1,4 +1,5 @@
-// Decode W4A16 kernel for M <= 4 in the interleaved-stream form, on the gfx950 tile layout.
+// Decode W4A16 kernel for M <= 4 (and M <= 8, MAXM = 8) in the interleaved-stream form, on the
+// gfx950 tile layout.
 //
 // Work split. Workgroup b owns a contiguous range of 16-row tiles [t0, t1) (XCD-aware order),
 // i.e. (t1 - t0) * nst consecutive 1 KB step blocks of qweight_t (nst = K / 128; in the tile
@@ -14,7 +15,8 @@
 // Per step a lane does what the MFMA GEMV does: lane 16 g + c holds chunk (column c, K block g)
 // of the step block, the 16 bytes that are the B operand of four v_mfma_f32_16x16x32_f16; the
 // exact dequantization fp16(q - z) * s (one rounding) runs in registers; x rows are the A
-// operand, read from one copy of x staged in LDS. D rows 0..3 (lanes 0..15) are the outputs.
+// operand, read from one copy of x staged in LDS. D rows 0..MAXM-1 (lanes 0..4 MAXM - 1; D lane
+// l holds rows 4 (l / 16) .. + 3 of column l % 16) are the outputs.
 // When a wave's next step lies in a later tile it writes its partial sums for the tile to LDS;
 // after one barrier the workgroup adds each tile's partials in wave order and applies bias, row
 // scale and epilogue. A column's sum order depends only on its tile, K and W (not on the grid),
@@ -39,7 +41,7 @@
 namespace tf {
 namespace {
 
-constexpr int kStreamMaxM = 4;                 // D rows 0..3 live in lanes 0..15
+constexpr int kNormMaxM = 4;                   // the RMSNorm prologue serves M <= 4
 constexpr int kStreamMaxXBytes = 96 * 1024;    // staged x: M rows of K + 8 halfs
 constexpr int kStreamInflightKB = 32;          // weight bytes in flight per CU (KB)
 constexpr int kNormMaxK = 8192;                // the RMSNorm prologue serves K up to this
@@ -236,8 +238,11 @@ __device__ __forceinline__ void norm_chunk(const LinearArgs& a, u4& x1, const u4
   x1 = u4{d0[0], d0[1], d1[0], d1[1]};
 }
 
-template <int P, int MAXW, bool SILU, bool X8, bool NORM>
+template <int P, int MAXW, int MAXM, bool SILU, bool X8, bool NORM>
 __global__ __launch_bounds__(MAXW * 64) void gemv_stream_kernel(LinearArgs a, int nwg, int tpw) {
+  static_assert(MAXM == 4 || MAXM == 8, "rows per launch");
+  static_assert(!NORM || MAXM <= kNormMaxM, "the RMSNorm prologue's scratch serves M <= 4");
+  constexpr int kPartLanes = 4 * MAXM;  // lanes whose D registers hold rows < MAXM
   extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
   // Every argument the kernel reads, in SGPRs from the first instruction on: otherwise the
   // compiler loads them next to their first use (x staging, epilogue), each a scalar-memory
@@ -312,7 +317,12 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_stream_kernel(LinearArgs a, in
   const __amdgpu_buffer_rsrc_t rx8 = make_rsrc(a.x8, (uint32_t)((int64_t)(a.m - 1) * a.ldx8 + a.k));
   constexpr int U = 4;
   u4 xv[U];
-  auto row_of = [&](int e) { return (int)(e >= chunks) + (int)(e >= 2 * chunks) + (int)(e >= 3 * chunks); };
+  auto row_of = [&](int e) {
+    int r = 0;
+#pragma unroll
+    for (int i = 1; i < MAXM; ++i) r += (int)(e >= i * chunks);
+    return r;
+  };
   auto load_x = [&](int e0) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -383,7 +393,7 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_stream_kernel(LinearArgs a, in
     __builtin_amdgcn_sched_barrier(0);  // slot 0 is the oldest load of the ring
   }
   // NORM scratch: the rows' chunk sums, then the maxima [4][16]
-  double* sums = reinterpret_cast<double*>(part + W * tpw * 16);
+  double* sums = reinterpret_cast<double*>(part + W * tpw * kPartLanes);
   uint32_t* red_u = reinterpret_cast<uint32_t*>(sums + (NORM ? a.m * norm_lpad(a.k) : 0));
   if (one) {
     const int e = threadIdx.x;
@@ -401,7 +411,7 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_stream_kernel(LinearArgs a, in
     __syncthreads();  // every row of x is in LDS
     norm_rows(a, xs, xstride, sums, red_u, W, wave, lane);
   }
-  for (int e = threadIdx.x; e < W * tpw * 16; e += T) part[e] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int e = threadIdx.x; e < W * tpw * kPartLanes; e += T) part[e] = f4{0.0f, 0.0f, 0.0f, 0.0f};
   __syncthreads();
 
   const UnpackConsts uc = unpack_consts();
@@ -430,7 +440,7 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_stream_kernel(LinearArgs a, in
         }
         cs += W;
         if (cs >= nst) {  // the wave leaves this tile: park its partial sums
-          if (lane < 16) part[(wave * tpw + (cv - t0)) * 16 + lane] = acc;
+          if (lane < kPartLanes) part[(wave * tpw + (cv - t0)) * kPartLanes + lane] = acc;
           acc = f4{0.0f, 0.0f, 0.0f, 0.0f};
           ++cv;
           cs = first_step(cv);
@@ -444,11 +454,12 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_stream_kernel(LinearArgs a, in
   __syncthreads();
 
   // Each tile's partials in wave order, then bias, row scale and the epilogue. Thread e takes
-  // column e % 16 (SiLU*mul: e % 8) of row r and tile tl, (tl, r) = divmod(e / 16, M).
+  // column e % 16 (SiLU*mul: e % 8) of row r and tile tl, (tl, r) = divmod(e / 16, M). Row r
+  // of a column is register r % 4 of the lane 16 (r / 4) above the column's.
   const int ntl = t1 - t0;
   const int m = a.m;
   auto split = [&](int rest, int& tl, int& r) {
-    tl = m == 1 ? rest : m == 2 ? (rest >> 1) : m == 4 ? (rest >> 2) : rest / 3;
+    tl = m == 1 ? rest : m == 2 ? (rest >> 1) : m == 4 ? (rest >> 2) : m == 8 ? (rest >> 3) : rest / m;
     r = rest - tl * m;
   };
   if (SILU) {
@@ -458,8 +469,8 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_stream_kernel(LinearArgs a, in
       const int jc = e & 7;
       float gs = 0.0f, us = 0.0f;
       for (int w = 0; w < W; ++w) {
-        gs += part[(w * tpw + tl) * 16 + jc][r];
-        us += part[(w * tpw + tl) * 16 + 8 + jc][r];
+        gs += part[(w * tpw + tl) * kPartLanes + 16 * (r >> 2) + jc][r & 3];
+        us += part[(w * tpw + tl) * kPartLanes + 16 * (r >> 2) + 8 + jc][r & 3];
       }
       const int ng = 8 * (t0 + tl) + jc, nu = (a.n >> 1) + ng;
       const float rsc = row_scale(a, r);
@@ -473,7 +484,7 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_stream_kernel(LinearArgs a, in
       split(e >> 4, tl, r);
       const int cc = e & 15;
       float sum = 0.0f;
-      for (int w = 0; w < W; ++w) sum += part[(w * tpw + tl) * 16 + cc][r];
+      for (int w = 0; w < W; ++w) sum += part[(w * tpw + tl) * kPartLanes + 16 * (r >> 2) + cc][r & 3];
       const int n = 16 * (t0 + tl) + cc;
       const float v = sum * row_scale(a, r) + (a.bias ? half_bits_to_float(a.bias[n]) : 0.0f);
       store_out(a, r, n, v);
@@ -502,15 +513,15 @@ int device_cus() {
 }
 
 // Workgroups, tiles per workgroup and LDS bytes of a launch (nwg = 0: it does not fit).
-template <typename Kernel>
+template <int MAXM, typename Kernel>
 StreamPlan plan_stream(Kernel kernel, const LinearArgs& a, int waves, int depth) {
   StreamPlan p;
   const int tiles = a.n >> 4;
   // The staged x, plus the prologue's reduction scratch behind the partials when it has one.
   const size_t xbytes = (size_t)a.m * stream_xstride(a.k) * 2 + (a.norm_w ? norm_scratch_bytes(a.m, a.k) : 0);
   const size_t cap = device_max_lds();
-  if (xbytes > (size_t)kStreamMaxXBytes || xbytes + (size_t)waves * 256 > cap) return p;
-  const int per_wave = 256;  // bytes of partials per (wave, tile)
+  const int per_wave = MAXM * 64;  // bytes of partials per (wave, tile): 4 MAXM lanes x 16
+  if (xbytes > (size_t)kStreamMaxXBytes || xbytes + (size_t)waves * per_wave > cap) return p;
   // Fewest tiles per workgroup the LDS allows.
   const int tpw_cap = (int)((cap - xbytes) / ((size_t)waves * per_wave));
   const int min_wg = (int)cdiv(tiles, tpw_cap);
@@ -531,8 +542,11 @@ StreamPlan plan_stream(Kernel kernel, const LinearArgs& a, int waves, int depth)
 }
 
 // The host-side conditions of the form, before any launch.
+template <int MAXM>
 int check_stream_shape(const LinearArgs& a, int waves) {
-  if (a.m > kStreamMaxM) return fail(TF_EINVAL, "tf_w4a16_linear: the gemv stream form (block_k 512) serves M <= 4");
+  if (a.m > MAXM)
+    return fail(TF_EINVAL, MAXM == 4 ? "tf_w4a16_linear: the gemv stream form (block_k 512, block_m 4) serves M <= 4"
+                                     : "tf_w4a16_linear: the gemv stream form (block_k 512, block_m 8) serves M <= 8");
   if ((a.n & 15) || (a.k & 127))
     return fail(TF_EINVAL, "tf_w4a16_linear: the gemv stream form needs N % 16 == 0 and K % 128 == 0");
   if (a.epilogue == TF_EPILOGUE_SILU_MUL && (a.n & 31))
@@ -546,52 +560,63 @@ int check_stream_shape(const LinearArgs& a, int waves) {
   return check_offsets(a);
 }
 
-template <int P, int MAXW>
+template <int P, int MAXW, int MAXM>
 int check_stream(const LinearArgs& a, const tf_gemm_config& cfg) {
-  if (int rc = check_stream_shape(a, cfg.num_warps)) return rc;
+  if (int rc = check_stream_shape<MAXM>(a, cfg.num_warps)) return rc;
+  if (MAXM > kNormMaxM && a.norm_w != nullptr)
+    return fail(TF_EINVAL, "tf_rmsnorm_fp8_w4a16_linear: the RMSNorm prologue runs on the block_m 4 stream form");
   // Every instantiation has the same launch plan (one of them stands for all).
-  const StreamPlan plan = plan_stream(gemv_stream_kernel<P, MAXW, false, false, false>, a, cfg.num_warps, P);
+  const StreamPlan plan = plan_stream<MAXM>(gemv_stream_kernel<P, MAXW, MAXM, false, false, false>, a, cfg.num_warps, P);
   if (plan.nwg == 0)
     return fail(TF_EINVAL, "tf_w4a16_linear: gemv stream variant does not fit the device's LDS");
   return TF_OK;
 }
 
-template <int P, int MAXW, bool SILU, bool X8, bool NORM>
+template <int P, int MAXW, int MAXM, bool SILU, bool X8, bool NORM>
 int launch_stream_k(const LinearArgs& a, int waves, hipStream_t stream) {
-  auto kernel = gemv_stream_kernel<P, MAXW, SILU, X8, NORM>;
-  const StreamPlan plan = plan_stream(kernel, a, waves, P);
+  auto kernel = gemv_stream_kernel<P, MAXW, MAXM, SILU, X8, NORM>;
+  const StreamPlan plan = plan_stream<MAXM>(kernel, a, waves, P);
   if (plan.nwg == 0) return fail(TF_EINVAL, "tf_w4a16_linear: gemv stream variant does not fit the device's LDS");
   if (int rc = reserve_lds(kernel, plan.lds, "gemv_stream")) return rc;
   kernel<<<plan.nwg, waves * 64, plan.lds, stream>>>(a, plan.nwg, plan.tpw);
   return check_launch("tf_w4a16_linear(gemv stream)");
 }
 
-template <int P, int MAXW>
+template <int P, int MAXW, int MAXM>
 int launch_stream(const LinearArgs& a, const tf_gemm_config& cfg, float*, hipStream_t stream) {
-  if (int rc = check_stream_shape(a, cfg.num_warps)) return rc;
+  if (int rc = check_stream_shape<MAXM>(a, cfg.num_warps)) return rc;
   const bool silu = a.epilogue == TF_EPILOGUE_SILU_MUL, x8 = a.x8 != nullptr, norm = a.norm_w != nullptr;
   const int w = cfg.num_warps;
   if (norm && x8) return fail(TF_EINVAL, "tf_w4a16_linear: the RMSNorm prologue takes fp16 x");
   if (norm && a.k > kNormMaxK)
     return fail(TF_EINVAL, "tf_rmsnorm_fp8_w4a16_linear: the RMSNorm prologue serves K <= 8192");
-  if (norm)
-    return silu ? launch_stream_k<P, MAXW, true, false, true>(a, w, stream)
-                : launch_stream_k<P, MAXW, false, false, true>(a, w, stream);
+  if constexpr (MAXM <= kNormMaxM) {
+    if (norm)
+      return silu ? launch_stream_k<P, MAXW, MAXM, true, false, true>(a, w, stream)
+                  : launch_stream_k<P, MAXW, MAXM, false, false, true>(a, w, stream);
+  } else {
+    if (norm)
+      return fail(TF_EINVAL, "tf_rmsnorm_fp8_w4a16_linear: the RMSNorm prologue runs on the block_m 4 stream form");
+  }
   if (silu)
-    return x8 ? launch_stream_k<P, MAXW, true, true, false>(a, w, stream)
-              : launch_stream_k<P, MAXW, true, false, false>(a, w, stream);
-  return x8 ? launch_stream_k<P, MAXW, false, true, false>(a, w, stream)
-            : launch_stream_k<P, MAXW, false, false, false>(a, w, stream);
+    return x8 ? launch_stream_k<P, MAXW, MAXM, true, true, false>(a, w, stream)
+              : launch_stream_k<P, MAXW, MAXM, true, false, false>(a, w, stream);
+  return x8 ? launch_stream_k<P, MAXW, MAXM, false, true, false>(a, w, stream)
+            : launch_stream_k<P, MAXW, MAXM, false, false, false>(a, w, stream);
 }
 
 int64_t no_stream_workspace(const LinearArgs&, const tf_gemm_config&) { return 0; }
 
 #define TF_SW(P, W) \
-  {{TF_KERNEL_GEMV_MFMA, 4, 16, 512, 1, W, P}, launch_stream<P, 16>, no_stream_workspace, check_stream<P, 16>}
+  {{TF_KERNEL_GEMV_MFMA, 4, 16, 512, 1, W, P}, launch_stream<P, 16, 4>, no_stream_workspace, check_stream<P, 16, 4>}
 #define TF_SW5(P) TF_SW(P, 1), TF_SW(P, 2), TF_SW(P, 4), TF_SW(P, 8), TF_SW(P, 16)
+#define TF_SW8(P, W) \
+  {{TF_KERNEL_GEMV_MFMA, 8, 16, 512, 1, W, P}, launch_stream<P, 16, 8>, no_stream_workspace, check_stream<P, 16, 8>}
 
-// block_k 512 marks the stream form; block_m 4 is its largest M; num_stages the ring depth.
-const Variant kStreamVariants[] = {TF_SW5(2), TF_SW5(4)};
+// block_k 512 marks the stream form; block_m its largest M (4, or 8: 4 M lanes of partials per
+// column instead of 1, no RMSNorm prologue); num_stages the ring depth.
+const Variant kStreamVariants[] = {TF_SW5(2), TF_SW5(4),    TF_SW8(2, 4), TF_SW8(2, 8),
+                                   TF_SW8(2, 16), TF_SW8(4, 4), TF_SW8(4, 8), TF_SW8(4, 16)};
 
 }  // namespace
 
