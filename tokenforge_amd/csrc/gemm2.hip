@@ -273,9 +273,9 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN == 4 && F == 16) ? 2 : 1) vo
 #pragma unroll
       for (int tn = 0; tn < TN; ++tn) {
         if constexpr (F == 32)
-          acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[tm], bf[tn], acc[tm][tn], 0, 0, 0);
+          acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[tn], af[tm], acc[tm][tn], 0, 0, 0);
         else
-          acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[tm], bf[tn], acc[tm][tn], 0, 0, 0);
+          acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bf[tn], af[tm], acc[tm][tn], 0, 0, 0);
       }
   };
 
@@ -328,7 +328,7 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN == 4 && F == 16) ? 2 : 1) vo
           __builtin_amdgcn_s_setprio(1);
 #pragma unroll
           for (int tm = 0; tm < TM; ++tm)
-            acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[tm], bq[tn & 1], acc[tm][tn], 0, 0, 0);
+            acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bq[tn & 1], af[tm], acc[tm][tn], 0, 0, 0);
           __builtin_amdgcn_s_setprio(0);
         }
 #pragma unroll
@@ -368,66 +368,53 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN == 4 && F == 16) ? 2 : 1) vo
   }
   if (kb < kb1) iteration(kb, S == 2 ? 0 : st, std::integral_constant<int, 0>{});
 
-  // ---- epilogue. D layout of the 32x32 MFMA: register q of lane l is row
-  // 8 (q / 4) + 4 (l / 32) + q % 4, column l % 32; of the 16x16 MFMA: row 4 (l / 16) + q,
-  // column l % 16. A SiLU*mul epilogue pairs columns of different tiles: without split-K the
-  // fp16 y goes to the workspace for the SiLU*mul kernel, with split-K the fp32 partials go to
-  // the reduce kernel.
+  // ---- epilogue. The MFMAs take the weight fragment as their first operand, so each
+  // accumulator tile is y transposed: register q of lane l is row (m) l % F of the tile and
+  // column (n) 4 (l / 16) + q (16x16) or 8 (q / 4) + 4 (l / 32) + q % 4 (32x32). A lane thus
+  // holds runs of four consecutive columns of one row and stores each straight from registers
+  // as one 8-byte piece (fp32 partials: 16 bytes). A SiLU*mul epilogue pairs columns of
+  // different tiles: without split-K the fp16 y goes to the workspace for the SiLU*mul
+  // kernel, with split-K the fp32 partials go to the reduce kernel.
   const bool partials = split_k > 1;
   const bool stage_y = !partials && a.epilogue == TF_EPILOGUE_SILU_MUL;
-  auto row_of = [&](int tm, int q) {
-    return (wm * TM + tm) * F + (F == 32 ? 8 * (q / 4) + 4 * (lane >> 5) + (q % 4) : 4 * (lane >> 4) + q);
-  };
-  // fp16 results (y, or y staged for SiLU*mul) leave through LDS in 16-byte row pieces
-  // (tile_copy_out); the values and their rounding are the per-value path's below.
   uint16_t* const dst = stage_y ? reinterpret_cast<uint16_t*>(ws) : a.out;
   const int64_t ldd = stage_y ? (int64_t)a.n : a.ldo;
   const bool residual = !stage_y && a.epilogue == TF_EPILOGUE_RESIDUAL;
-  if (!partials && tile_copy_out_ok(a, dst, ldd, residual)) {
-    static_assert(BM * BN * 2 <= C::kLds, "the fp16 tile fits in the kernel's LDS");
-    // Every wave is past its last fragment read and every LDS load of the pipeline (the x
-    // stages past K included) has landed before the stages are overwritten.
-    __builtin_amdgcn_s_waitcnt(0);
-    __builtin_amdgcn_s_barrier();
-    uint16_t* const tile = reinterpret_cast<uint16_t*>(smem);  // [BM][BN]
+  const bool vec = partials ? (a.n & 3) == 0 && (reinterpret_cast<uintptr_t>(ws) & 15) == 0
+                           : run_store_ok(a, dst, ldd, residual);
 #pragma unroll
-    for (int tm = 0; tm < TM; ++tm)
+  for (int tm = 0; tm < TM; ++tm) {
+    const int m = m0 + (wm * TM + tm) * F + (lane & (F - 1));
+    if (m >= a.m) continue;
+    const float rs = row_scale(a, m);
 #pragma unroll
-      for (int tn = 0; tn < TN; ++tn) {
-        const int c = (wn * TN + tn) * F + (lane & (F - 1));
-        const int n = n0 + c;
-        const float b = (a.bias && n < a.n) ? half_bits_to_float(a.bias[n]) : 0.0f;
+    for (int tn = 0; tn < TN; ++tn)
 #pragma unroll
-        for (int q = 0; q < AR; ++q) {
-          const int r = row_of(tm, q);
-          tile[r * BN + c] = f16_bits(acc[tm][tn][q] * row_scale(a, m0 + r) + b);
+      for (int g = 0; g < AR / 4; ++g) {
+        const int n = n0 + (wn * TN + tn) * F + (F == 32 ? 8 * g + 4 * (lane >> 5) : 4 * (lane >> 4));
+        if (n >= a.n) continue;
+        float v[4];
+        if (partials) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) v[j] = acc[tm][tn][4 * g + j];
+          float* const p = ws + ((int64_t)z * a.m + m) * a.n + n;
+          if (vec) {
+            *reinterpret_cast<f4*>(p) = f4{v[0], v[1], v[2], v[3]};
+          } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              if (n + j < a.n) p[j] = v[j];
+          }
+          continue;
         }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float b = (a.bias && n + j < a.n) ? half_bits_to_float(a.bias[n + j]) : 0.0f;
+          v[j] = acc[tm][tn][4 * g + j] * rs + b;
+        }
+        store_run4(a, dst, ldd, residual, m, n, v, vec);
       }
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-    __builtin_amdgcn_s_barrier();
-    tile_copy_out<BM, BN, C::kThreads>(a, tile, dst, ldd, residual, m0, n0);
-    return;
   }
-#pragma unroll
-  for (int tm = 0; tm < TM; ++tm)
-#pragma unroll
-    for (int tn = 0; tn < TN; ++tn) {
-      const int n = n0 + (wn * TN + tn) * F + (lane & (F - 1));
-      if (n >= a.n) continue;
-      const float b = (!partials && a.bias) ? half_bits_to_float(a.bias[n]) : 0.0f;
-#pragma unroll
-      for (int q = 0; q < AR; ++q) {
-        const int m = m0 + row_of(tm, q);
-        if (m >= a.m) continue;
-        const float v = acc[tm][tn][q] * row_scale(a, m) + b;
-        if (stage_y)
-          reinterpret_cast<uint16_t*>(ws)[(int64_t)m * a.n + n] = f16_bits(v);
-        else if (!partials)
-          store_out(a, m, n, v);
-        else
-          ws[((int64_t)z * a.m + m) * a.n + n] = acc[tm][tn][q];
-      }
-    }
 }
 
 int effective_split2(const LinearArgs& a, const tf_gemm_config& cfg) {

@@ -130,6 +130,43 @@ __device__ __forceinline__ void tile_copy_out(const LinearArgs& a, const uint16_
   }
 }
 
+// Kernels whose accumulators hold runs of four consecutive output columns of one row (the
+// MFMA with the weight fragment as its first operand) store each run as one 8-byte piece where
+// N, the row strides and the pointers are in 4-element units.
+__device__ __forceinline__ bool run_store_ok(const LinearArgs& a, const uint16_t* dst, int64_t ldd, bool residual) {
+  return (a.n & 3) == 0 && (ldd & 3) == 0 && (reinterpret_cast<uintptr_t>(dst) & 7) == 0 &&
+         (!residual || ((a.ldr & 3) == 0 && (reinterpret_cast<uintptr_t>(a.residual) & 7) == 0));
+}
+
+// Columns n .. n + 3 of row m (v: acc * row scale + bias in fp32) to dst (row stride ldd) as
+// fp16, or as fp16(residual + fp16(v)) under the residual epilogue: the values store_out
+// writes. vec: run_store_ok holds (then a run is inside N or past it); else per value, the
+// columns past N skipped.
+__device__ __forceinline__ void store_run4(const LinearArgs& a, uint16_t* dst, int64_t ldd, bool residual, int m,
+                                           int n, const float (&v)[4], bool vec) {
+  if (vec) {
+    uint16_t h[4];
+    if (residual) {
+      const u2 res = *reinterpret_cast<const u2*>(a.residual + (int64_t)m * a.ldr + n);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) h[j] = finish_residual(v[j], (uint16_t)(res[j >> 1] >> (16 * (j & 1))));
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) h[j] = f16_bits(v[j]);
+    }
+    *reinterpret_cast<u2*>(dst + (int64_t)m * ldd + n) =
+        u2{(uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16)};
+    return;
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (n + j >= a.n) break;
+    uint16_t r = f16_bits(v[j]);
+    if (residual) r = finish_residual(v[j], a.residual[(int64_t)m * a.ldr + n + j]);
+    dst[(int64_t)m * ldd + n + j] = r;
+  }
+}
+
 // ------------------------------------------------------------------ launch helpers
 
 // LDS bytes one workgroup may use on the current device (160 KiB on gfx950), queried once
