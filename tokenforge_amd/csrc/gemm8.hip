@@ -257,9 +257,10 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm8_kernel(LinearArgs a, float
     v8i af[TM];
 #pragma unroll
     for (int tm = 0; tm < TM; ++tm) af[tm] = frag(A, a_row0 + tm * 16);
-    float sc[TN];
-#pragma unroll
-    for (int tn = 0; tn < TN; ++tn) sc[tn] = s_lds[odd * BN + b_row0 + tn * 16];
+    // The MFMAs take the weight fragment first: register q of lane l then holds column
+    // 4 (l / 16) + q of the fragment, whose group scales are read as one 16-byte piece next to
+    // the fragment's MFMAs.
+    const float* const sc_row = s_lds + odd * BN + wn * TN * 16 + 4 * (lane >> 4);
     // One 16-column fragment at a time: its B operand, its TM MFMAs, then their scale FMAs.
     // The scheduling barriers keep the compiler from hoisting every fragment's MFMA results
     // ahead of the FMAs (TN x TM live accumulators of 4 registers each would spill); the
@@ -269,17 +270,18 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm8_kernel(LinearArgs a, float
 #pragma unroll
     for (int tn = 0; tn < TN; ++tn) {
       if (tn + 1 < TN) bf[(tn + 1) & 1] = frag(B, b_row0 + (tn + 1) * 16);
+      const f4 sc = *reinterpret_cast<const f4*>(sc_row + tn * 16);
       f4 d[TM];
       __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int tm = 0; tm < TM; ++tm)
-        d[tm] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af[tm], bf[tn & 1], f4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0,
+        d[tm] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bf[tn & 1], af[tm], f4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0,
                                                                    0, kNeutralScale, 0, kNeutralScale);
       __builtin_amdgcn_s_setprio(0);
 #pragma unroll
       for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) acc[tm][tn][q] = __builtin_fmaf(sc[tn], d[tm][q], acc[tm][tn][q]);
+        for (int q = 0; q < 4; ++q) acc[tm][tn][q] = __builtin_fmaf(sc[q], d[tm][q], acc[tm][tn][q]);
       // Part of block kb + 1's weights into the other buffer.
 #pragma unroll
       for (int h = tn * kHalves / TN; h < (tn + 1) * kHalves / TN; ++h) store_b_half(odd ^ 1, odd ^ 1, h);
@@ -298,61 +300,46 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm8_kernel(LinearArgs a, float
   }
   if (kb < kb1) iteration(kb, S == 2 ? 0 : st, std::integral_constant<int, 0>{});
 
-  // ---- epilogue. D layout: register q of lane l is row 4 (l / 16) + q, column l % 16.
+  // ---- epilogue. The accumulators hold y transposed (weight fragment first): register q of
+  // lane l is row (m) l % 16 and column (n) 4 (l / 16) + q of its tile, so a lane holds a run
+  // of four consecutive columns of one row and stores it as one 8-byte piece (fp32 partials:
+  // 16 bytes) straight from registers.
   const bool partials = split_k > 1;
   const bool stage_y = !partials && a.epilogue == TF_EPILOGUE_SILU_MUL;
-  // fp16 results (y, or y staged for SiLU*mul) leave through LDS in 16-byte row pieces
-  // (tile_copy_out); the values and their rounding are the per-value path's below.
   uint16_t* const dst = stage_y ? reinterpret_cast<uint16_t*>(ws) : a.out;
   const int64_t ldd = stage_y ? (int64_t)a.n : a.ldo;
   const bool residual = !stage_y && a.epilogue == TF_EPILOGUE_RESIDUAL;
-  if (!partials && tile_copy_out_ok(a, dst, ldd, residual)) {
-    static_assert(BM * BN * 2 <= C::kLds, "the fp16 tile fits in the kernel's LDS");
-    // Every wave is past its last fragment read and every LDS load of the pipeline (the x
-    // stages past K included) has landed before the stages are overwritten.
-    __builtin_amdgcn_s_waitcnt(0);
-    __builtin_amdgcn_s_barrier();
-    uint16_t* const tile = reinterpret_cast<uint16_t*>(smem);  // [BM][BN]
+  const bool vec = partials ? (a.n & 3) == 0 && (reinterpret_cast<uintptr_t>(ws) & 15) == 0
+                            : run_store_ok(a, dst, ldd, residual);
 #pragma unroll
-    for (int tm = 0; tm < TM; ++tm)
-#pragma unroll
-      for (int tn = 0; tn < TN; ++tn) {
-        const int c = (wn * TN + tn) * 16 + (lane & 15);
-        const int n = n0 + c;
-        const float b = (a.bias && n < a.n) ? half_bits_to_float(a.bias[n]) : 0.0f;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int r = (wm * TM + tm) * 16 + 4 * (lane >> 4) + q;
-          tile[r * BN + c] = f16_bits(acc[tm][tn][q] * row_scale(a, m0 + r) + b);
-        }
-      }
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-    __builtin_amdgcn_s_barrier();
-    tile_copy_out<BM, BN, C::kThreads>(a, tile, dst, ldd, residual, m0, n0);
-    return;
-  }
-#pragma unroll
-  for (int tm = 0; tm < TM; ++tm)
+  for (int tm = 0; tm < TM; ++tm) {
+    const int m = m0 + (wm * TM + tm) * 16 + (lane & 15);
+    if (m >= a.m) continue;
+    const float rs = row_scale(a, m);
 #pragma unroll
     for (int tn = 0; tn < TN; ++tn) {
-      const int n = n0 + (wn * TN + tn) * 16 + (lane & 15);
+      const int n = n0 + (wn * TN + tn) * 16 + 4 * (lane >> 4);
       if (n >= a.n) continue;
-      const float b = (!partials && a.bias) ? half_bits_to_float(a.bias[n]) : 0.0f;
+      float v[4];
+      if (partials) {
+        float* const p = ws + ((int64_t)z * a.m + m) * a.n + n;
+        if (vec) {
+          *reinterpret_cast<f4*>(p) = acc[tm][tn];
+        } else {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int m = m0 + (wm * TM + tm) * 16 + 4 * (lane >> 4) + q;
-        if (m >= a.m) continue;
-        if (partials) {
-          ws[((int64_t)z * a.m + m) * a.n + n] = acc[tm][tn][q];
-          continue;
+          for (int j = 0; j < 4; ++j)
+            if (n + j < a.n) p[j] = acc[tm][tn][j];
         }
-        const float v = acc[tm][tn][q] * row_scale(a, m) + b;
-        if (stage_y)
-          reinterpret_cast<uint16_t*>(ws)[(int64_t)m * a.n + n] = f16_bits(v);
-        else
-          store_out(a, m, n, v);
+        continue;
       }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float b = (a.bias && n + j < a.n) ? half_bits_to_float(a.bias[n + j]) : 0.0f;
+        v[j] = acc[tm][tn][j] * rs + b;
+      }
+      store_run4(a, dst, ldd, residual, m, n, v, vec);
     }
+  }
 }
 
 int effective_split8(const LinearArgs& a, const tf_gemm_config& cfg) {

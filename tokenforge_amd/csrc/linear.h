@@ -93,43 +93,6 @@ __device__ __forceinline__ void store_out(const LinearArgs& a, int m, int n, flo
   a.out[(int64_t)m * a.ldo + n] = r;
 }
 
-// fp16 result tiles of the LDS-tile GEMMs can leave through LDS: the kernel writes its tile,
-// [BM][BN] fp16 with row pitch BN, into its (then idle) LDS in the MFMA layout, and every
-// thread copies whole 16-byte row pieces (8 columns) to dst, with the residual read the same
-// way, instead of one 2-byte store per value spread over several rows. That needs N, the row
-// strides and the pointers in 16-byte units.
-__device__ __forceinline__ bool tile_copy_out_ok(const LinearArgs& a, const uint16_t* dst, int64_t ldd, bool residual) {
-  return (a.n & 7) == 0 && (ldd & 7) == 0 && (reinterpret_cast<uintptr_t>(dst) & 15) == 0 &&
-         (!residual || ((a.ldr & 7) == 0 && (reinterpret_cast<uintptr_t>(a.residual) & 15) == 0));
-}
-
-// The copy of a [BM][BN] fp16 tile (LDS, row pitch BN) to rows m0.., columns n0.. of dst (row
-// stride ldd), as fp16(residual + y) under the residual epilogue (finish_residual of the
-// rounded value, which is what the per-value path computes). The LDS writes of the tile must
-// be done and visible (barrier) before the call.
-template <int BM, int BN, int THREADS>
-__device__ __forceinline__ void tile_copy_out(const LinearArgs& a, const uint16_t* tile, uint16_t* dst, int64_t ldd,
-                                              bool residual, int m0, int n0) {
-  static_assert(BN % 8 == 0, "16-byte row pieces");
-  for (int e = threadIdx.x; e < BM * BN / 8; e += THREADS) {
-    const int r = e / (BN / 8);
-    const int c = (e - r * (BN / 8)) * 8;
-    const int m = m0 + r, n = n0 + c;
-    if (m >= a.m || n >= a.n) continue;  // N % 8 == 0: a piece is inside N or past it
-    u4 v = *reinterpret_cast<const u4*>(tile + r * BN + c);
-    if (residual) {
-      const u4 res = *reinterpret_cast<const u4*>(a.residual + (int64_t)m * a.ldr + n);
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const uint16_t lo = finish_residual(half_bits_to_float((uint16_t)v[w]), (uint16_t)res[w]);
-        const uint16_t hi = finish_residual(half_bits_to_float((uint16_t)(v[w] >> 16)), (uint16_t)(res[w] >> 16));
-        v[w] = (uint32_t)lo | ((uint32_t)hi << 16);
-      }
-    }
-    *reinterpret_cast<u4*>(dst + (int64_t)m * ldd + n) = v;
-  }
-}
-
 // Kernels whose accumulators hold runs of four consecutive output columns of one row (the
 // MFMA with the weight fragment as its first operand) store each run as one 8-byte piece where
 // N, the row strides and the pointers are in 4-element units.
