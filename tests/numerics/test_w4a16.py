@@ -267,32 +267,40 @@ STREAM_FORMS = [GemmConfig("gemv_mfma", 4, 16, 512, 1, w, p) for p in (2, 4) for
 STREAM_FORMS_8 = [GemmConfig("gemv_mfma", 8, 16, 512, 1, w, p) for p in (2, 4) for w in (4, 8, 16)]
 
 
+@pytest.mark.parametrize("split", [1, 2, 4])
 @pytest.mark.parametrize("block_m", [4, 8])
 @pytest.mark.parametrize(
     ("layer", "n", "k"),
     [("qkv", 4608, 3584), ("o", 3584, 3584), ("gate_up", 37888, 3584), ("down", 3584, 18944)],
 )
-def test_stream_form_full_size(layer: str, n: int, k: int, block_m: int, device: torch.device) -> None:
+def test_stream_form_full_size(layer: str, n: int, k: int, block_m: int, split: int, device: torch.device) -> None:
     """The GEMV stream form (block_k 512) on every Qwen2.5-7B decoder linear: block_m 4 at M in
-    {1, 2, 4}, block_m 8 at M in {5, 8} (x too long to stage on down_proj at M = 4 and above is
-    rejected before any launch): every ring depth and wave count against an fp32 product of the
-    exactly dequantized weights, bit-identical on a second call; the residual and SiLU*mul
-    epilogues bit-equal to torch applied to its own plain output; the W4A8 form on
-    e4m3-representable x equal to the W4A16 result at unit scale."""
+    {1, 2, 4}, block_m 8 at M in {5, 8}, without and with a K split across workgroups (split_k 2
+    and 4: ring depth 2; each workgroup stages one K slice of x, the split-K reduce adds the
+    slices): every ring depth and wave count against an fp32 product of the exactly dequantized
+    weights, bit-identical on a second call; the residual and SiLU*mul epilogues bit-equal to
+    torch applied to its own plain output; the W4A8 form on e4m3-representable x equal to the
+    W4A16 result at unit scale. Shapes outside the form (x or its slice too long to stage, as
+    on down_proj at M >= 4 without a split, or fewer K steps per slice than waves) are rejected
+    before any launch."""
+    from dataclasses import replace
+
     from tokenforge.kernels.autotune import synthetic_layer
     from tokenforge.kernels.config import stream_form_applies
     from tokenforge.kernels.hip.w4a16 import w4a8_gemm_ex, w4a16_gemm_ex
 
     qweight_t, scales, qzeros = synthetic_layer(n, k, G, device, seed=13)
     wt = w4a16_dequant(qweight_t, scales, qzeros, G).float().t().contiguous()
+    forms = [replace(c, split_k=split) for c in (STREAM_FORMS if block_m == 4 else STREAM_FORMS_8)
+             if split == 1 or c.num_stages == 2]
     for m in ((1, 2, 4) if block_m == 4 else (5, 8)):
         gen = torch.Generator(device=device).manual_seed(20 + m)
         x = torch.randn((m, k), generator=gen, device=device).to(torch.float16)
         ref = x.float() @ wt
         scale = float(ref.abs().max())
-        for cfg in STREAM_FORMS if block_m == 4 else STREAM_FORMS_8:
+        for cfg in forms:
             print(f"{layer} m={m} {cfg}", flush=True)
-            if not stream_form_applies(m, n, k, cfg.num_warps, max_m=block_m) and m * (k + 8) * 2 > 96 * 1024:
+            if not stream_form_applies(m, n, k, cfg.num_warps, max_m=block_m, split_k=split):
                 with pytest.raises(ValueError, match="stream form"):
                     w4a16_gemm(x, qweight_t, scales, qzeros, G, cfg)
                 continue

@@ -187,6 +187,10 @@ def test_decode_buckets_offer_both_gemv_forms_and_work_splits() -> None:
     assert {c.block_m for c in candidate_configs(8, 128) if c.stream} == {8}
     assert {c.block_m for c in candidate_configs(4, 128) if c.stream} == {4}
     assert not any(c.stream for c in candidate_configs(16, 128))
+    # the stream form is also tried with K split across workgroups; no other gemv kernel splits
+    assert {c.split_k for c in candidate_configs(8, 128) if c.stream} == {1, 2, 4}
+    assert {c.split_k for c in candidate_configs(8, 128) if not c.stream} == {1}
+    GemmConfig("gemv_mfma", 8, 16, 512, 4, 16, 2).validate(128)
     assert {c.block_m for c in candidate_configs(4, 128) if c.kernel == "gemv_dot"} == {4}
     assert {c.block_m for c in candidate_configs(32, 128) if c.family == "gemv"} == {16, 32}
 
@@ -224,6 +228,13 @@ def test_stream_form_rules() -> None:
     assert not stream_form_applies(8, 37888, 3584, 8, norm=True, max_m=8)  # the prologue: M <= 4
     assert not stream_form_applies(8, 3584, 18944, 8, max_m=8)  # x does not fit 96 KiB of LDS
     assert not stream_form_applies(9, 4608, 3584, 8, max_m=8)
+    # K split across workgroups: each stages a slice of x (down_proj at M = 4 and 8)
+    assert stream_form_applies(8, 3584, 18944, 16, max_m=8, split_k=4)
+    assert stream_form_applies(4, 3584, 18944, 8, split_k=2)
+    assert not stream_form_applies(8, 3584, 18944, 16, max_m=8, split_k=2)  # the slice does not fit
+    assert not stream_form_applies(4, 4608, 3584, 8, split_k=4)  # 7 steps per slice for 8 waves
+    assert not stream_form_applies(2, 4608, 3584, 8, norm=True, split_k=2)  # the prologue: no split
+    assert stream_form_applies(2, 4608, 3584, 8, norm=True)
     assert stream_form_applies(1, 37888, 3584, 8)
     assert stream_form_applies(2, 3584, 18944, 16)
     assert not stream_form_applies(4, 3584, 18944, 8)  # x does not fit 96 KiB of LDS

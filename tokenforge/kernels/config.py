@@ -93,7 +93,11 @@ STREAM_MAX_M = 4
 STREAM_WIDE_M = 8
 """block_m of the stream form that serves the bucket of M = 5..8 (no RMSNorm prologue)."""
 STREAM_MAX_X_BYTES = 96 * 1024
-"""The stream form stages all of x in LDS: M rows of K + 8 fp16 values must fit this."""
+"""The stream form stages x in LDS: M rows of K + 8 fp16 values (of K / split_k + 8 under a K
+split) must fit this."""
+STREAM_SPLITS = (2, 4)
+"""K splits the tuner tries on the stream form (split_k 1 besides): each workgroup stages and
+multiplies one K slice, the split-K reduce adds the slices."""
 
 
 def _stream_variants() -> list[tuple[str, int, int, int, int, int]]:
@@ -115,24 +119,31 @@ def norm_scratch_bytes(m: int, k: int) -> int:
     return m * lpad * 8 + 256
 
 
+def stream_slice_k(k: int, split_k: int) -> int:
+    """K of the longest slice when the stream form splits K over ``split_k`` workgroup sets."""
+    return -(-(k // 128) // split_k) * 128
+
+
 def stream_form_applies(m: int, n: int, k: int, num_warps: int, norm: bool = False,
-                        max_m: int = STREAM_MAX_M) -> bool:
+                        max_m: int = STREAM_MAX_M, split_k: int = 1) -> bool:
     """Whether the op runs a call of this shape on the GEMV stream form when its bucket's config
-    is that form (``max_m``: the config's block_m): M <= max_m, N % 32 == 0, K % 128 == 0 with
-    at least one 128-wide step per wave, and x small enough to stage in LDS. The rule does not
-    depend on the epilogue, so a plain call and its fused SiLU*mul or residual twin run the same
-    kernel and agree bit for bit (the library itself runs plain and residual calls on N % 16 ==
-    0 as well). With ``norm`` (the RMSNorm prologue of ``rmsnorm_fp8_w4a16_linear``, on the
-    block_m 4 form only) M is at most 4, K at most NORM_MAX_K and the staged x plus the
-    prologue's scratch must fit."""
-    x_bytes = m * (k + 8) * 2 + (norm_scratch_bytes(m, k) if norm else 0)
+    is that form (``max_m``: the config's block_m, ``split_k``: its K split): M <= max_m, N % 32
+    == 0, K % 128 == 0 with at least one 128-wide step per wave in every K slice, and the
+    slice of x small enough to stage in LDS. The rule does not depend on the epilogue, so a
+    plain call and its fused SiLU*mul or residual twin run the same kernel and agree bit for bit
+    (the library itself runs plain and residual calls on N % 16 == 0 as well). With ``norm``
+    (the RMSNorm prologue of ``rmsnorm_fp8_w4a16_linear``, on the block_m 4 form without a K
+    split only) M is at most 4, K at most NORM_MAX_K and the staged x plus the prologue's
+    scratch must fit."""
+    if k % 128 or split_k < 1:
+        return False
+    x_bytes = m * (stream_slice_k(k, split_k) + 8) * 2 + (norm_scratch_bytes(m, k) if norm else 0)
     return (
         1 <= m <= (STREAM_MAX_M if norm else max_m)
         and n % 32 == 0
-        and k % 128 == 0
-        and k // 128 >= num_warps
+        and (k // 128) // split_k >= num_warps
         and x_bytes <= STREAM_MAX_X_BYTES
-        and (not norm or k <= NORM_MAX_K)
+        and (not norm or (k <= NORM_MAX_K and split_k == 1))
     )
 
 
@@ -247,7 +258,7 @@ class GemmConfig:
             raise ValueError(f"block_k={self.block_k} must divide group_size={group_size}")
         if not 1 <= self.split_k <= 16:
             raise ValueError(f"split_k={self.split_k} must be in [1, 16]")
-        if self.family != "gemm" and self.split_k != 1:
+        if self.family != "gemm" and not self.stream and self.split_k != 1:
             raise ValueError(
                 f"split_k={self.split_k}: {self.kernel} splits K across its num_warps waves; "
                 "split_k must be 1"
@@ -369,6 +380,8 @@ def candidate_configs(bucket: int, group_size: int) -> list[GemmConfig]:
             if kernel == "gemv_mfma" and bm > 16 and bucket <= 16:
                 continue
             out.append(cfg)
+            if cfg.stream:  # K split across workgroups: x rows of a long K staged by slices
+                out.extend(replace(cfg, split_k=s) for s in STREAM_SPLITS)
             continue
         if bk != 128 and (bk > group_size or group_size % bk):
             continue

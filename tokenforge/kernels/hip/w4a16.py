@@ -319,8 +319,8 @@ def rmsnorm_fp8_w4a16_gemm_ex(
     <= 4); epilogue ``"none"`` or ``"silu_mul"``."""
     m, n, k = _check_inputs(x, qweight_t, scales, qzeros, group_size)
     config.validate(group_size)
-    if not config.stream:
-        raise ValueError(f"the RMSNorm prologue runs in the gemv stream form (M <= 4), got config {config}")
+    if not config.stream or config.split_k != 1:
+        raise ValueError(f"the RMSNorm prologue runs in the gemv stream form (M <= 4, split_k 1), got config {config}")
     if epilogue not in ("none", "silu_mul"):
         raise ValueError(f"epilogue must be 'none' or 'silu_mul', got {epilogue!r}")
     if tuple(norm_weight.shape) != (k,):

@@ -128,7 +128,7 @@ def _gpu_config(device: torch.device, m: int, n: int, k: int, group_size: int) -
         # Above the largest bucket its config is reused; once the M tiles alone fill the CUs a
         # K split only adds the fp32 workspace (split * M * N * 4 bytes) and its reduction.
         cfg = dataclasses.replace(cfg, split_k=1)
-    if cfg.stream and not stream_form_applies(m, n, k, cfg.num_warps, max_m=cfg.block_m):
+    if cfg.stream and not stream_form_applies(m, n, k, cfg.num_warps, max_m=cfg.block_m, split_k=cfg.split_k):
         # The bucket's config is the stream form but this call is outside it (N % 32 == 16, or
         # an x too long to stage): the K-split GEMV runs it, whatever the epilogue.
         cfg = split_k_gemv_config(n, k)
@@ -185,7 +185,7 @@ def _resolve_launch(kind: int, epilogue: int, m: int, n: int, k: int, group_size
     else:
         if kind == KIND_NORM_LINEAR:
             fused = int(cfg.stream and cfg.block_m == STREAM_MAX_M
-                        and stream_form_applies(m, n, k, cfg.num_warps, norm=True))
+                        and stream_form_applies(m, n, k, cfg.num_warps, norm=True, split_k=cfg.split_k))
         c = _w4a16.to_c_config(cfg)
         need = 0 if fused else int(h.tf_w4a16_workspace_bytes_ex(m, n, k, group_size, ctypes.byref(c), epilogue))
     bucket = _BUCKET_LABELS.index(dispatch.bucket_label(m))
@@ -416,7 +416,8 @@ def _rmsnorm_fp8_w4a16_linear(x, norm_weight, eps, qweight_t, scales, qzeros, bi
         _record_host(m, backend)
         return host.linear(a, qweight_t, scales, qzeros, bias, group_size, epilogue).reshape(out_shape)
     cfg = _decide(x2, m, n, k, group_size, backend)
-    if cfg.stream and cfg.block_m == STREAM_MAX_M and stream_form_applies(m, n, k, cfg.num_warps, norm=True):
+    if cfg.stream and cfg.block_m == STREAM_MAX_M and stream_form_applies(m, n, k, cfg.num_warps, norm=True,
+                                                                          split_k=cfg.split_k):
         y = _w4a16.rmsnorm_fp8_w4a16_gemm_ex(
             x2, norm_weight, eps, qweight_t, scales, qzeros, group_size, cfg, bias, epilogue
         )

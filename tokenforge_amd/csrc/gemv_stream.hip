@@ -27,6 +27,13 @@
 // N/32 + v / 2 (N % 32 == 0). The lane part of every address is then a per-lane constant and
 // the step part a wave-uniform scalar, as without the epilogue.
 //
+// K split (split_k > 1): workgroup b works on K slice z = b / (nwg / split), steps [z nst / split,
+// (z + 1) nst / split) of every tile, and stages only that slice of x, so M rows of a long K
+// (down_proj at M = 4 and 8) fit in LDS. It writes each column's fp32 sum over its slice (no
+// bias or row scale) to the workspace [split][M][N]; splitk_reduce adds the slices in split
+// order, the bias and the row scale and applies the epilogue (SiLU*mul on the physical gate
+// and up columns: the kernel runs without the virtual SiLU tiles then).
+//
 // RMSNorm prologue (NORM, tf_rmsnorm_fp8_w4a16_linear): x holds the rows before an RMSNorm +
 // e4m3 quantization. Once x is staged, every workgroup turns each row in LDS into fp16(code *
 // scale), the activation rmsnorm_fp8_quant_dq writes, with the norm kernel's arithmetic
@@ -39,6 +46,9 @@
 #include <algorithm>
 
 namespace tf {
+
+int splitk_reduce(const LinearArgs& a, const float* ws, int split, hipStream_t stream);
+
 namespace {
 
 constexpr int kNormMaxM = 4;                   // the RMSNorm prologue serves M <= 4
@@ -239,7 +249,8 @@ __device__ __forceinline__ void norm_chunk(const LinearArgs& a, u4& x1, const u4
 }
 
 template <int P, int MAXW, int MAXM, bool SILU, bool X8, bool NORM>
-__global__ __launch_bounds__(MAXW * 64) void gemv_stream_kernel(LinearArgs a, int nwg, int tpw) {
+__global__ __launch_bounds__(MAXW * 64) void gemv_stream_kernel(LinearArgs a, int nwg, int tpw, int split,
+                                                                float* __restrict__ ws) {
   static_assert(MAXM == 4 || MAXM == 8, "rows per launch");
   static_assert(!NORM || MAXM <= kNormMaxM, "the RMSNorm prologue's scratch serves M <= 4");
   constexpr int kPartLanes = 4 * MAXM;  // lanes whose D registers hold rows < MAXM
@@ -250,7 +261,7 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_stream_kernel(LinearArgs a, in
   __asm__ volatile("" ::"s"(a.x), "s"(a.x8), "s"(a.ldx), "s"(a.ldx8), "s"(a.qw), "s"(a.scales), "s"(a.qz),
                    "s"(a.bias), "s"(a.out), "s"(a.ldo), "s"(a.residual), "s"(a.ldr), "s"(a.xscale),
                    "s"(a.xscale_stride), "s"(a.m), "s"(a.n), "s"(a.k), "s"(a.log2g), "s"(a.epilogue), "s"(a.norm_w),
-                   "s"(a.norm_eps), "s"(a.norm_inv_k));
+                   "s"(a.norm_eps), "s"(a.norm_inv_k), "s"(split), "s"(ws));
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int W = blockDim.x >> 6;
@@ -260,17 +271,24 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_stream_kernel(LinearArgs a, in
   geo.nst = a.k >> 7;
   geo.groups = a.k >> a.log2g;
   geo.gps = 128 >> a.log2g;
-  const int nst = geo.nst;
   const int tiles = a.n >> 4;
   const int half_tiles = a.n >> 5;
 
-  const int b = xcd_tile(blockIdx.x, nwg);
-  // tiles * nwg < 2^31 (checked on the host): 32-bit divisions, far shorter than 64-bit ones.
-  const int t0 = (int)((uint32_t)(tiles * b) / (uint32_t)nwg);
-  const int t1 = (int)((uint32_t)(tiles * (b + 1)) / (uint32_t)nwg);
-  const int xstride = stream_xstride(a.k);
+  const int bx = xcd_tile(blockIdx.x, nwg);
+  // The K slice of this workgroup (the whole of K without a split) and its place among the
+  // slice's nps workgroups.
+  const int nps = nwg / split;
+  const int z = bx / nps;
+  const int b = bx - z * nps;
+  const int s0 = (int)((uint32_t)(geo.nst * z) / (uint32_t)split);
+  const int nst = (int)((uint32_t)(geo.nst * (z + 1)) / (uint32_t)split) - s0;  // steps of the slice
+  const int kz = nst * 128;                                                    // K of the slice
+  // tiles * nps < 2^31 (checked on the host): 32-bit divisions, far shorter than 64-bit ones.
+  const int t0 = (int)((uint32_t)(tiles * b) / (uint32_t)nps);
+  const int t1 = (int)((uint32_t)(tiles * (b + 1)) / (uint32_t)nps);
+  const int xstride = stream_xstride(kz);
   _Float16* xs = reinterpret_cast<_Float16*>(lds);
-  f4* part = reinterpret_cast<f4*>(lds + (a.m * xstride) / 2);  // [W][tpw][16]
+  f4* part = reinterpret_cast<f4*>(lds + (a.m * xstride) / 2);  // [W][tpw][4 MAXM]
 
   // Per-lane parts of the three offsets (see the SiLU*mul note above).
   const uint32_t gl = (uint32_t)((g * 32) >> a.log2g);  // the lane's group inside a step
@@ -310,8 +328,9 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_stream_kernel(LinearArgs a, in
   // flattened (row, chunk) index. The first batch is issued before the weight ring: loads
   // return in order, so x issued behind the ring would reach the workgroup barrier only with
   // the slowest wave's HBM reads (x itself comes from L2 after the first workgroups).
-  const int chunks = a.k >> 3;
+  const int chunks = kz >> 3;
   const int total = a.m * chunks;
+  const int64_t kx = (int64_t)s0 * 128;  // first K column of the slice
   const int T = blockDim.x;
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, (uint32_t)(((int64_t)(a.m - 1) * a.ldx + a.k) * 2));
   const __amdgpu_buffer_rsrc_t rx8 = make_rsrc(a.x8, (uint32_t)((int64_t)(a.m - 1) * a.ldx8 + a.k));
@@ -330,10 +349,10 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_stream_kernel(LinearArgs a, in
       const int r = row_of(e), q = e - r * chunks;
       const bool ok = e < total;
       if (X8) {
-        const u2 cd = load_b64(rx8, ok ? (uint32_t)((int64_t)r * a.ldx8 + q * 8) : kOutOfRange);
+        const u2 cd = load_b64(rx8, ok ? (uint32_t)((int64_t)r * a.ldx8 + kx + q * 8) : kOutOfRange);
         xv[u] = u4{cd[0], cd[1], 0u, 0u};
       } else {
-        xv[u] = load_b128(rx, ok ? (uint32_t)(((int64_t)r * a.ldx + q * 8) * 2) : kOutOfRange);
+        xv[u] = load_b128(rx, ok ? (uint32_t)(((int64_t)r * a.ldx + kx + q * 8) * 2) : kOutOfRange);
       }
     }
   };
@@ -355,10 +374,10 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_stream_kernel(LinearArgs a, in
     const int r = row_of(e), q = e - r * chunks;
     const bool ok = e < total;
     if (X8) {
-      const u2 cd = load_b64(rx8, ok ? (uint32_t)((int64_t)r * a.ldx8 + q * 8) : kOutOfRange);
+      const u2 cd = load_b64(rx8, ok ? (uint32_t)((int64_t)r * a.ldx8 + kx + q * 8) : kOutOfRange);
       x1 = u4{cd[0], cd[1], 0u, 0u};
     } else {
-      x1 = load_b128(rx, ok ? (uint32_t)(((int64_t)r * a.ldx + q * 8) * 2) : kOutOfRange);
+      x1 = load_b128(rx, ok ? (uint32_t)(((int64_t)r * a.ldx + kx + q * 8) * 2) : kOutOfRange);
     }
     if (NORM) g1 = load_b128(make_rsrc(a.norm_w, (uint32_t)a.k * 2u), ok ? (uint32_t)q * 16u : kOutOfRange);
   } else {
@@ -371,7 +390,7 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_stream_kernel(LinearArgs a, in
   u4 rw[P];
   uint32_t rs[P], rz[P];
   int iv = t0, is = first_step(t0), ow, os, oz;
-  geo.at(iv, is, ow, os, oz);
+  geo.at(iv, s0 + is, ow, os, oz);
   auto issue = [&](int p) {
     const bool in = iv < t1;
     rw[p] = __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(a.qw, in ? qw_bytes : 0u), (int)wl, in ? ow : 0, 0);
@@ -384,7 +403,7 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_stream_kernel(LinearArgs a, in
     if (is >= nst) {
       ++iv;
       is = first_step(iv);
-      geo.at(iv, is, ow, os, oz);
+      geo.at(iv, s0 + is, ow, os, oz);
     }
   };
 #pragma unroll
@@ -458,14 +477,23 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_stream_kernel(LinearArgs a, in
   // of a column is register r % 4 of the lane 16 (r / 4) above the column's.
   const int ntl = t1 - t0;
   const int m = a.m;
-  auto split = [&](int rest, int& tl, int& r) {
+  auto divm = [&](int rest, int& tl, int& r) {
     tl = m == 1 ? rest : m == 2 ? (rest >> 1) : m == 4 ? (rest >> 2) : m == 8 ? (rest >> 3) : rest / m;
     r = rest - tl * m;
   };
-  if (SILU) {
+  if (split > 1) {  // the slice's fp32 sums, for splitk_reduce
+    for (int e = threadIdx.x; e < ntl * 16 * m; e += T) {
+      int tl, r;
+      divm(e >> 4, tl, r);
+      const int cc = e & 15;
+      float sum = 0.0f;
+      for (int w = 0; w < W; ++w) sum += part[(w * tpw + tl) * kPartLanes + 16 * (r >> 2) + cc][r & 3];
+      ws[((int64_t)z * m + r) * a.n + 16 * (t0 + tl) + cc] = sum;
+    }
+  } else if (SILU) {
     for (int e = threadIdx.x; e < ntl * 8 * m; e += T) {
       int tl, r;
-      split(e >> 3, tl, r);
+      divm(e >> 3, tl, r);
       const int jc = e & 7;
       float gs = 0.0f, us = 0.0f;
       for (int w = 0; w < W; ++w) {
@@ -481,7 +509,7 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_stream_kernel(LinearArgs a, in
   } else {
     for (int e = threadIdx.x; e < ntl * 16 * m; e += T) {
       int tl, r;
-      split(e >> 4, tl, r);
+      divm(e >> 4, tl, r);
       const int cc = e & 15;
       float sum = 0.0f;
       for (int w = 0; w < W; ++w) sum += part[(w * tpw + tl) * kPartLanes + 16 * (r >> 2) + cc][r & 3];
@@ -512,23 +540,33 @@ int device_cus() {
   return cache[dev];
 }
 
-// Workgroups, tiles per workgroup and LDS bytes of a launch (nwg = 0: it does not fit).
+// K of the longest slice of a K split.
+inline int slice_k(int k, int split) { return (int)cdiv(k >> 7, split) * 128; }
+
+// Staged x bytes of a launch: M rows of the longest K slice.
+inline size_t stream_x_bytes(const LinearArgs& a, int split) {
+  return (size_t)a.m * stream_xstride(slice_k(a.k, split)) * 2;
+}
+
+// Workgroups (a multiple of split: the same count on every K slice), tiles per workgroup and
+// LDS bytes of a launch (nwg = 0: it does not fit).
 template <int MAXM, typename Kernel>
-StreamPlan plan_stream(Kernel kernel, const LinearArgs& a, int waves, int depth) {
+StreamPlan plan_stream(Kernel kernel, const LinearArgs& a, int waves, int depth, int split) {
   StreamPlan p;
   const int tiles = a.n >> 4;
   // The staged x, plus the prologue's reduction scratch behind the partials when it has one.
-  const size_t xbytes = (size_t)a.m * stream_xstride(a.k) * 2 + (a.norm_w ? norm_scratch_bytes(a.m, a.k) : 0);
+  const size_t xbytes = stream_x_bytes(a, split) + (a.norm_w ? norm_scratch_bytes(a.m, a.k) : 0);
   const size_t cap = device_max_lds();
   const int per_wave = MAXM * 64;  // bytes of partials per (wave, tile): 4 MAXM lanes x 16
   if (xbytes > (size_t)kStreamMaxXBytes || xbytes + (size_t)waves * per_wave > cap) return p;
   // Fewest tiles per workgroup the LDS allows.
   const int tpw_cap = (int)((cap - xbytes) / ((size_t)waves * per_wave));
-  const int min_wg = (int)cdiv(tiles, tpw_cap);
+  const int min_nps = (int)cdiv(tiles, tpw_cap);
   int per_cu = std::max(1, kStreamInflightKB / (waves * depth));
   for (int pass = 0; pass < 2; ++pass) {
-    p.nwg = std::max(min_wg, std::min(tiles, device_cus() * per_cu));
-    p.tpw = (int)cdiv(tiles, p.nwg);
+    const int nps = std::max(min_nps, std::min(tiles, std::max(1, device_cus() * per_cu / split)));
+    p.nwg = nps * split;
+    p.tpw = (int)cdiv(tiles, nps);
     p.lds = xbytes + (size_t)waves * p.tpw * per_wave;
     int occ = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, waves * 64, p.lds) != hipSuccess || occ <= 0) {
@@ -543,7 +581,7 @@ StreamPlan plan_stream(Kernel kernel, const LinearArgs& a, int waves, int depth)
 
 // The host-side conditions of the form, before any launch.
 template <int MAXM>
-int check_stream_shape(const LinearArgs& a, int waves) {
+int check_stream_shape(const LinearArgs& a, int waves, int split) {
   if (a.m > MAXM)
     return fail(TF_EINVAL, MAXM == 4 ? "tf_w4a16_linear: the gemv stream form (block_k 512, block_m 4) serves M <= 4"
                                      : "tf_w4a16_linear: the gemv stream form (block_k 512, block_m 8) serves M <= 8");
@@ -553,68 +591,81 @@ int check_stream_shape(const LinearArgs& a, int waves) {
     return fail(TF_EINVAL, "tf_w4a16_linear: the gemv stream form's SiLU*mul epilogue needs N % 32 == 0");
   if ((int64_t)(a.n >> 4) * 65536 >= ((int64_t)1 << 31))
     return fail(TF_EINVAL, "tf_w4a16_linear: the gemv stream form needs N < 2^19");
-  if ((a.k >> 7) < waves)
-    return fail(TF_EINVAL, "tf_w4a16_linear: the gemv stream form needs K >= 128 * num_warps");
-  if ((size_t)a.m * stream_xstride(a.k) * 2 > (size_t)kStreamMaxXBytes)
-    return fail(TF_EINVAL, "tf_w4a16_linear: the gemv stream form needs x (M * (K + 8) halfs) to fit 96 KiB of LDS");
+  if ((a.k >> 7) / split < waves)
+    return fail(TF_EINVAL, "tf_w4a16_linear: the gemv stream form needs K / split_k >= 128 * num_warps");
+  if (stream_x_bytes(a, split) > (size_t)kStreamMaxXBytes)
+    return fail(TF_EINVAL,
+                "tf_w4a16_linear: the gemv stream form needs x (M * (K / split_k + 8) halfs) to fit 96 KiB of LDS");
+  if (split > 1 && a.norm_w != nullptr)
+    return fail(TF_EINVAL, "tf_rmsnorm_fp8_w4a16_linear: the RMSNorm prologue runs without a K split (split_k 1)");
   return check_offsets(a);
 }
 
 template <int P, int MAXW, int MAXM>
 int check_stream(const LinearArgs& a, const tf_gemm_config& cfg) {
-  if (int rc = check_stream_shape<MAXM>(a, cfg.num_warps)) return rc;
+  if (int rc = check_stream_shape<MAXM>(a, cfg.num_warps, cfg.split_k)) return rc;
   if (MAXM > kNormMaxM && a.norm_w != nullptr)
     return fail(TF_EINVAL, "tf_rmsnorm_fp8_w4a16_linear: the RMSNorm prologue runs on the block_m 4 stream form");
   // Every instantiation has the same launch plan (one of them stands for all).
-  const StreamPlan plan = plan_stream<MAXM>(gemv_stream_kernel<P, MAXW, MAXM, false, false, false>, a, cfg.num_warps, P);
+  const StreamPlan plan =
+      plan_stream<MAXM>(gemv_stream_kernel<P, MAXW, MAXM, false, false, false>, a, cfg.num_warps, P, cfg.split_k);
   if (plan.nwg == 0)
     return fail(TF_EINVAL, "tf_w4a16_linear: gemv stream variant does not fit the device's LDS");
   return TF_OK;
 }
 
 template <int P, int MAXW, int MAXM, bool SILU, bool X8, bool NORM>
-int launch_stream_k(const LinearArgs& a, int waves, hipStream_t stream) {
+int launch_stream_k(const LinearArgs& a, int waves, int split, float* ws, hipStream_t stream) {
   auto kernel = gemv_stream_kernel<P, MAXW, MAXM, SILU, X8, NORM>;
-  const StreamPlan plan = plan_stream<MAXM>(kernel, a, waves, P);
+  const StreamPlan plan = plan_stream<MAXM>(kernel, a, waves, P, split);
   if (plan.nwg == 0) return fail(TF_EINVAL, "tf_w4a16_linear: gemv stream variant does not fit the device's LDS");
   if (int rc = reserve_lds(kernel, plan.lds, "gemv_stream")) return rc;
-  kernel<<<plan.nwg, waves * 64, plan.lds, stream>>>(a, plan.nwg, plan.tpw);
-  return check_launch("tf_w4a16_linear(gemv stream)");
+  kernel<<<plan.nwg, waves * 64, plan.lds, stream>>>(a, plan.nwg, plan.tpw, split, ws);
+  if (int rc = check_launch("tf_w4a16_linear(gemv stream)")) return rc;
+  return split > 1 ? splitk_reduce(a, ws, split, stream) : TF_OK;
 }
 
 template <int P, int MAXW, int MAXM>
-int launch_stream(const LinearArgs& a, const tf_gemm_config& cfg, float*, hipStream_t stream) {
-  if (int rc = check_stream_shape<MAXM>(a, cfg.num_warps)) return rc;
-  const bool silu = a.epilogue == TF_EPILOGUE_SILU_MUL, x8 = a.x8 != nullptr, norm = a.norm_w != nullptr;
+int launch_stream(const LinearArgs& a, const tf_gemm_config& cfg, float* ws, hipStream_t stream) {
+  const int split = cfg.split_k;
+  if (int rc = check_stream_shape<MAXM>(a, cfg.num_warps, split)) return rc;
+  if (split > 1 && ws == nullptr) return fail(TF_EINVAL, "tf_w4a16_linear: this config needs a workspace");
+  const bool x8 = a.x8 != nullptr, norm = a.norm_w != nullptr;
+  // With a K split the reduce kernel applies the epilogue: the kernel sums physical columns.
+  const bool silu = a.epilogue == TF_EPILOGUE_SILU_MUL && split == 1;
   const int w = cfg.num_warps;
   if (norm && x8) return fail(TF_EINVAL, "tf_w4a16_linear: the RMSNorm prologue takes fp16 x");
   if (norm && a.k > kNormMaxK)
     return fail(TF_EINVAL, "tf_rmsnorm_fp8_w4a16_linear: the RMSNorm prologue serves K <= 8192");
   if constexpr (MAXM <= kNormMaxM) {
     if (norm)
-      return silu ? launch_stream_k<P, MAXW, MAXM, true, false, true>(a, w, stream)
-                  : launch_stream_k<P, MAXW, MAXM, false, false, true>(a, w, stream);
+      return silu ? launch_stream_k<P, MAXW, MAXM, true, false, true>(a, w, split, ws, stream)
+                  : launch_stream_k<P, MAXW, MAXM, false, false, true>(a, w, split, ws, stream);
   } else {
     if (norm)
       return fail(TF_EINVAL, "tf_rmsnorm_fp8_w4a16_linear: the RMSNorm prologue runs on the block_m 4 stream form");
   }
   if (silu)
-    return x8 ? launch_stream_k<P, MAXW, MAXM, true, true, false>(a, w, stream)
-              : launch_stream_k<P, MAXW, MAXM, true, false, false>(a, w, stream);
-  return x8 ? launch_stream_k<P, MAXW, MAXM, false, true, false>(a, w, stream)
-            : launch_stream_k<P, MAXW, MAXM, false, false, false>(a, w, stream);
+    return x8 ? launch_stream_k<P, MAXW, MAXM, true, true, false>(a, w, split, ws, stream)
+              : launch_stream_k<P, MAXW, MAXM, true, false, false>(a, w, split, ws, stream);
+  return x8 ? launch_stream_k<P, MAXW, MAXM, false, true, false>(a, w, split, ws, stream)
+            : launch_stream_k<P, MAXW, MAXM, false, false, false>(a, w, split, ws, stream);
 }
 
-int64_t no_stream_workspace(const LinearArgs&, const tf_gemm_config&) { return 0; }
+// fp32 partials [split][M][N] under a K split, else none.
+int64_t stream_workspace(const LinearArgs& a, const tf_gemm_config& cfg) {
+  return cfg.split_k > 1 ? (int64_t)cfg.split_k * a.m * a.n * (int64_t)sizeof(float) : 0;
+}
 
 #define TF_SW(P, W) \
-  {{TF_KERNEL_GEMV_MFMA, 4, 16, 512, 1, W, P}, launch_stream<P, 16, 4>, no_stream_workspace, check_stream<P, 16, 4>}
+  {{TF_KERNEL_GEMV_MFMA, 4, 16, 512, 1, W, P}, launch_stream<P, 16, 4>, stream_workspace, check_stream<P, 16, 4>}
 #define TF_SW5(P) TF_SW(P, 1), TF_SW(P, 2), TF_SW(P, 4), TF_SW(P, 8), TF_SW(P, 16)
 #define TF_SW8(P, W) \
-  {{TF_KERNEL_GEMV_MFMA, 8, 16, 512, 1, W, P}, launch_stream<P, 16, 8>, no_stream_workspace, check_stream<P, 16, 8>}
+  {{TF_KERNEL_GEMV_MFMA, 8, 16, 512, 1, W, P}, launch_stream<P, 16, 8>, stream_workspace, check_stream<P, 16, 8>}
 
 // block_k 512 marks the stream form; block_m its largest M (4, or 8: 4 M lanes of partials per
-// column instead of 1, no RMSNorm prologue); num_stages the ring depth.
+// column instead of 1, no RMSNorm prologue); num_stages the ring depth; split_k (runtime) the
+// K split across workgroups.
 const Variant kStreamVariants[] = {TF_SW5(2), TF_SW5(4),    TF_SW8(2, 4), TF_SW8(2, 8),
                                    TF_SW8(2, 16), TF_SW8(4, 4), TF_SW8(4, 8), TF_SW8(4, 16)};
 

@@ -66,7 +66,10 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 int check_config(const tf_gemm_config& cfg, int32_t group_size) {
   if (cfg.split_k < 1 || cfg.split_k > kMaxSplitK)
     return fail(TF_EINVAL, "tf_w4a16_linear: split_k must be in [1, 16]");
-  if (cfg.kernel != TF_KERNEL_GEMM_MFMA && cfg.kernel != TF_KERNEL_GEMM_FP8 && cfg.split_k != 1)
+  // The GEMV stream form (gemv_mfma, block_k 512) may split K across workgroups (fp32 partials
+  // and the split-K reduce); the other gemv kernels split K across their waves only.
+  const bool stream_form = cfg.kernel == TF_KERNEL_GEMV_MFMA && cfg.block_k == 512;
+  if (cfg.kernel != TF_KERNEL_GEMM_MFMA && cfg.kernel != TF_KERNEL_GEMM_FP8 && !stream_form && cfg.split_k != 1)
     return fail(TF_EINVAL, "tf_w4a16_linear: gemv kernels split K across waves (num_warps); split_k must be 1");
   // block_k 128 marks the skinny kernel (gemm3.hip), which reads each lane's group itself;
   // the LDS-tile kernels need one scale per column and block.
