@@ -7,7 +7,13 @@ A kernel's fp16 result ``y`` for ``x @ w.T`` (fp16 operands, K = reduction lengt
   error grow like sqrt(K) unit roundoffs of the largest terms, and ``c`` is what the vendor's
   own fp16 GEMM needs on that device class (measured by ``python -m tests.numerics.calibrate``
   and frozen in ``tolerances.json``), so a kernel may be no less accurate than the vendor
-  GEMM. This is the reference's measurement contract (tests/numerics/tolerance.py:1-46).
+  GEMM. This is the reference's measurement contract (tests/numerics/tolerance.py:1-46), with
+  one change: the bound holds each output's error above half an fp16 ulp of its fp64 value.
+  That half ulp is the rounding of the result to the fp16 output, which even the exact
+  product incurs; the reference's form counts it against the bound, so a draw with an output
+  of magnitude >= 2 near a rounding midpoint can fail for every fp16 kernel (with K = 384 and
+  max|ref| = 2.1 the bound is 9.4e-4 and the half ulp 9.8e-4). The full-size tests use the
+  same form.
 * the normwise bound ``max|y - ref| / max|ref| <= 1e-2`` against an fp32 dequant-then-matmul,
   the north-star's accuracy target.
 
@@ -41,6 +47,14 @@ def roundoff_scale(x: np.ndarray, w: np.ndarray) -> float:
     return EPS_FP16 * math.sqrt(x.shape[-1]) * _largest_finite(x) * _largest_finite(w)
 
 
+def half_ulp_fp16(ref: np.ndarray) -> np.ndarray:
+    """Half the fp16 spacing at each |ref| (the largest rounding error of an exact value stored
+    as fp16; subnormal spacing below 2**-14)."""
+    mag = np.abs(np.asarray(ref, dtype=np.float64))
+    binade = np.floor(np.log2(np.maximum(mag, 2.0**-14)))
+    return np.exp2(binade - 11)
+
+
 def relative_max_error(y: np.ndarray, ref: np.ndarray) -> float:
     """``max|y - ref| / max|ref|`` over the entries where ``ref`` is finite (the absolute
     error when ``ref`` is all zero)."""
@@ -66,7 +80,8 @@ class Outcome:
         return self.abs_err <= self.atol and self.normwise <= NORMWISE_MAX
 
     def __str__(self) -> str:
-        return f"abs {self.abs_err:.3e} (bound {self.atol:.3e}), normwise {self.normwise:.3e} (bound {NORMWISE_MAX})"
+        return (f"abs above half an fp16 ulp {self.abs_err:.3e} (bound {self.atol:.3e}), "
+                f"normwise {self.normwise:.3e} (bound {NORMWISE_MAX})")
 
 
 @dataclass(frozen=True)
@@ -80,12 +95,14 @@ class Contract:
         return self.c * roundoff_scale(x, w)
 
     def check(self, y: np.ndarray, ref64: np.ndarray, ref32: np.ndarray, x: np.ndarray, w: np.ndarray) -> Outcome:
-        """``y`` against the fp64 product ``ref64`` (absolute bound, finite entries) and the
-        fp32 dequant-then-matmul ``ref32`` (normwise bound)."""
+        """``y`` against the fp64 product ``ref64`` (absolute bound on the error above half an
+        fp16 ulp of each output, finite entries) and the fp32 dequant-then-matmul ``ref32``
+        (normwise bound)."""
         y64 = np.asarray(y, dtype=np.float64)
         r64 = np.asarray(ref64, dtype=np.float64)
         finite = np.isfinite(r64)
-        abs_err = float(np.max(np.abs(y64[finite] - r64[finite]))) if finite.any() else 0.0
+        excess = np.abs(y64[finite] - r64[finite]) - half_ulp_fp16(r64[finite])
+        abs_err = float(max(0.0, np.max(excess))) if finite.any() else 0.0
         return Outcome(abs_err, self.atol(x, w), relative_max_error(y64, ref32))
 
 

@@ -7,7 +7,7 @@ import pytest
 
 from tests.numerics import shapes
 from tests.numerics.calibrate import two_digits_up
-from tests.numerics.tolerance import EPS_FP16, contract, relative_max_error, roundoff_scale
+from tests.numerics.tolerance import EPS_FP16, contract, half_ulp_fp16, relative_max_error, roundoff_scale
 from tokenforge.kernels.metrics import LabeledCounter
 
 
@@ -60,9 +60,13 @@ def test_contract_check_measures_both_bounds() -> None:
     c = contract("cuda")
     exact = c.check(ref, ref, ref, x, w)
     assert exact.ok and exact.abs_err == 0.0 and exact.normwise == 0.0
-    off = ref + np.array([[0.0, 1e-3]])  # above the derived bound (~7.6e-4), within 1e-2 normwise
+    # 2e-3 off an output of 1.0: 2e-3 - 2**-11 above its half ulp, more than the derived bound
+    # (~7.6e-4), within 1e-2 normwise
+    off = ref + np.array([[0.0, 2e-3]])
     got = c.check(off, ref, ref, x, w)
-    assert not got.ok and got.abs_err == pytest.approx(1e-3) and got.normwise < 1e-2
+    assert not got.ok and got.abs_err == pytest.approx(2e-3 - 2.0**-11) and got.normwise < 1e-2
+    # the output rounding alone is not counted: half an ulp off passes
+    assert c.check(ref + np.array([[0.0, 2.0**-11]]), ref, ref, x, w).ok
     ref_nan = ref.copy()
     ref_nan[0, 1] = np.nan  # a non-finite reference entry takes no part
     assert c.check(off, ref_nan, ref_nan, x, w).ok
@@ -96,3 +100,31 @@ def test_labeled_counter() -> None:
     again = LabeledCounter("tokenforge_test_counter", "test", ("kernel", "bucket"))
     again.inc(kernel="hip_gemv", bucket="1")
     assert again.value(kernel="hip_gemv", bucket="1") == 1.0
+
+
+def test_half_ulp_is_half_the_fp16_spacing() -> None:
+    v = np.array([0.0, 1e-6, 2.0**-14, 0.3, 1.0, 1.999, 2.0, 3.7, 1000.0, -2.5, 60000.0])
+    expect = np.spacing(np.abs(v).astype(np.float16)).astype(np.float64) / 2
+    # a value just below a power of two has the spacing of its own binade
+    expect[5] = 2.0**-11
+    np.testing.assert_array_equal(half_ulp_fp16(v), expect)
+
+
+def test_the_exactly_rounded_product_always_meets_the_bound() -> None:
+    """A draw whose largest output (2.1) sits near an fp16 rounding midpoint: the fp64 product
+    rounded to fp16 is off by 9.74e-4, above c * roundoff scale (9.36e-4) but within half an
+    ulp, so it passes (and so does every kernel whose accumulation error is within the bound)."""
+    import oracle.pack as opack
+    import oracle.reference as oref
+    from tests.numerics import cases
+
+    n, k, m, g, seed = 448, 384, 167, 64, 134
+    w = cases.layer_weights(n, k, seed, g)
+    x = cases.activations(m, k, seed).numpy()
+    b = cases.bias(n, seed).numpy()
+    ref = oref.w4a16_reference(x, w, b)
+    w16 = opack.dequantize_tf(w)
+    rounded = ref.astype(np.float16).astype(np.float64)
+    c = contract("cuda")
+    assert float(np.abs(rounded - ref).max()) > c.atol(x, w16)  # the old form fails every fp16 kernel
+    assert c.check(rounded, ref, ref, x, w16).ok
