@@ -5,8 +5,9 @@ output, with the same config.
 Every stream-form variant (waves 1..16, ring depth 2 and 4) at M = 1..4, epilogues none (with
 bias) and SiLU*mul, on rows that take the kernel's fast path and rows that do not: an all-zero
 row (scale 1/(448*512)), a row holding a NaN or an infinity (NaN codes, the slow encode), a row
-near fp16's maximum, and rows with large outlier channels. The op routes M <= 4 through the
-fused kernel and larger M through the two kernels; both routes equal the unfused ops.
+near fp16's maximum, and rows with large outlier channels. The op routes M = 1 through the
+fused kernel (ring depth 4) and larger M through the two kernels (at M = 2..4 the separate norm
+kernel is faster than every workgroup normalizing the rows); both routes equal the unfused ops.
 """
 
 from __future__ import annotations

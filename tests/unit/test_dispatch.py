@@ -235,6 +235,15 @@ def test_stream_form_rules() -> None:
     assert not stream_form_applies(4, 4608, 3584, 8, split_k=4)  # 7 steps per slice for 8 waves
     assert not stream_form_applies(2, 4608, 3584, 8, norm=True, split_k=2)  # the prologue: no split
     assert stream_form_applies(2, 4608, 3584, 8, norm=True)
+    # the op fuses the norm at M = 1 only, on the bucket's stream config with the ring at depth 4
+    from tokenforge.kernels.config import norm_fused_config
+    s1 = GemmConfig("gemv_mfma", 4, 16, 512, 1, 8, 2)
+    assert norm_fused_config(s1, 1, 4608, 3584) == GemmConfig("gemv_mfma", 4, 16, 512, 1, 8, 4)
+    assert norm_fused_config(GemmConfig("gemv_mfma", 4, 16, 512, 1, 16, 4), 1, 4608, 3584).num_stages == 4
+    assert norm_fused_config(s1, 2, 4608, 3584) is None
+    assert norm_fused_config(GemmConfig("gemv_mfma", 4, 16, 512, 2, 8, 2), 1, 4608, 3584) is None
+    assert norm_fused_config(GemmConfig("gemv_mfma", 16, 16, 128, 1, 8, 2), 1, 4608, 3584) is None
+    assert norm_fused_config(s1, 1, 4608, 12160) is None  # the prologue serves K <= 8192
     assert stream_form_applies(1, 37888, 3584, 8)
     assert stream_form_applies(2, 3584, 18944, 16)
     assert not stream_form_applies(4, 3584, 18944, 8)  # x does not fit 96 KiB of LDS

@@ -147,6 +147,30 @@ def stream_form_applies(m: int, n: int, k: int, num_warps: int, norm: bool = Fal
     )
 
 
+NORM_FUSED_MAX_M = 1
+"""``rmsnorm_fp8_w4a16_linear`` runs the norm inside the GEMV (its prologue) up to this M. Measured
+on MI355X (qkv and gate_up of Qwen2.5-7B): at M = 1 the prologue saves the norm kernel's launch
+(qkv 9.7 us against 7.3 + 3.5 for the two kernels); at M = 2 and 4 every workgroup's norm of
+several rows takes longer than the separate norm kernel (qkv M = 4: 16.2 us against 11.6)."""
+NORM_RING_DEPTH = 4
+"""Ring depth (num_stages) of the stream form when it runs the RMSNorm prologue: the loads in
+flight while the prologue runs keep HBM busy (qkv M = 1: 9.7 us at depth 4 against 10.5 at 2;
+gate_up 19.9 against 21.3; depth 8 no better)."""
+
+
+def norm_fused_config(cfg: GemmConfig, m: int, n: int, k: int) -> GemmConfig | None:
+    """The config ``rmsnorm_fp8_w4a16_linear`` runs the fused kernel on, given the bucket's
+    ``cfg``, or None where it runs the norm kernel and the linear: M <= NORM_FUSED_MAX_M, a
+    stream-form config of block_m 4 without a K split, and the prologue fits
+    (``stream_form_applies(norm=True)``); the ring deepened to NORM_RING_DEPTH. Both routes give
+    the same bits."""
+    if not (1 <= m <= NORM_FUSED_MAX_M and cfg.stream and cfg.block_m == STREAM_MAX_M and cfg.split_k == 1):
+        return None
+    if not stream_form_applies(m, n, k, cfg.num_warps, norm=True):
+        return None
+    return replace(cfg, num_stages=max(cfg.num_stages, NORM_RING_DEPTH))
+
+
 def _gemm_variants() -> list[tuple[str, int, int, int, int, int]]:
     # num_stages 2: two LDS buffers, operands staged through registers (any group size).
     tiles = [(64, 64, 64), (64, 128, 64), (128, 64, 64), (128, 128, 64), (128, 256, 64),

@@ -64,10 +64,10 @@ from tokenforge.kernels.config import (
     M_BUCKETS,
     MAX_BUCKET_M,
     NUM_CUS,
-    STREAM_MAX_M,
     GemmConfig,
     fp8_gemm_applies,
     fp8_gemm_config,
+    norm_fused_config,
     split_k_gemv_config,
     stream_form_applies,
 )
@@ -184,8 +184,9 @@ def _resolve_launch(kind: int, epilogue: int, m: int, n: int, k: int, group_size
         need = int(h.tf_w4a8_workspace_bytes_ex(m, n, k, group_size, ctypes.byref(c), epilogue))
     else:
         if kind == KIND_NORM_LINEAR:
-            fused = int(cfg.stream and cfg.block_m == STREAM_MAX_M
-                        and stream_form_applies(m, n, k, cfg.num_warps, norm=True, split_k=cfg.split_k))
+            fcfg = norm_fused_config(cfg, m, n, k)
+            if fcfg is not None:
+                cfg, fused = fcfg, 1
         c = _w4a16.to_c_config(cfg)
         need = 0 if fused else int(h.tf_w4a16_workspace_bytes_ex(m, n, k, group_size, ctypes.byref(c), epilogue))
     bucket = _BUCKET_LABELS.index(dispatch.bucket_label(m))
@@ -416,10 +417,10 @@ def _rmsnorm_fp8_w4a16_linear(x, norm_weight, eps, qweight_t, scales, qzeros, bi
         _record_host(m, backend)
         return host.linear(a, qweight_t, scales, qzeros, bias, group_size, epilogue).reshape(out_shape)
     cfg = _decide(x2, m, n, k, group_size, backend)
-    if cfg.stream and cfg.block_m == STREAM_MAX_M and stream_form_applies(m, n, k, cfg.num_warps, norm=True,
-                                                                          split_k=cfg.split_k):
+    fcfg = norm_fused_config(cfg, m, n, k)
+    if fcfg is not None:
         y = _w4a16.rmsnorm_fp8_w4a16_gemm_ex(
-            x2, norm_weight, eps, qweight_t, scales, qzeros, group_size, cfg, bias, epilogue
+            x2, norm_weight, eps, qweight_t, scales, qzeros, group_size, fcfg, bias, epilogue
         )
     else:
         _, _, a = _rms.rmsnorm_fp8_quant_dequant(x2, norm_weight, eps, None)
