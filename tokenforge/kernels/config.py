@@ -112,11 +112,12 @@ NORM_MAX_K = 8192
 
 def norm_scratch_bytes(m: int, k: int) -> int:
     """LDS the stream form's RMSNorm prologue adds: M rows of chunk sums (fp64), each padded to
-    the power of two >= K / 8 (at least 64), and 256 bytes of maxima."""
+    the power of two >= K / 8 (at least 64), 256 bytes of maxima and the staged norm weight
+    (K fp16)."""
     lpad = 64
     while lpad < k // 8:
         lpad *= 2
-    return m * lpad * 8 + 256
+    return m * lpad * 8 + 256 + 2 * k
 
 
 def stream_slice_k(k: int, split_k: int) -> int:

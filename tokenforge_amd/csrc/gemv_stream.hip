@@ -57,14 +57,15 @@ constexpr int kStreamInflightKB = 32;          // weight bytes in flight per CU 
 constexpr int kNormMaxK = 8192;                // the RMSNorm prologue serves K up to this
 
 // LDS the RMSNorm prologue adds: the chunk sums of the squares of every row, each row padded to
-// lpad = the power of two >= K / 8 (at least 64) entries, then [16][4] words for the maxima.
+// lpad = the power of two >= K / 8 (at least 64) entries, then [4][16] words for the maxima,
+// then the norm weight (K fp16; staged for the LDS form, which reads it once per row).
 __host__ __device__ __forceinline__ int norm_lpad(int k) {
   int l = 64;
   while (l < (k >> 3)) l <<= 1;
   return l;
 }
 __host__ __device__ __forceinline__ size_t norm_scratch_bytes(int m, int k) {
-  return (size_t)m * norm_lpad(k) * 8 + 256;
+  return (size_t)m * norm_lpad(k) * 8 + 256 + (size_t)k * 2;
 }
 
 // The sum of squares of staged row rs in the fixed order of norm_row.h, from its chunk sums at
@@ -91,21 +92,31 @@ struct StreamGeo {
   }
 };
 
-// The RMSNorm + e4m3 prologue over the m rows of x staged in LDS (row r at xs + r * xstride),
-// in place: each row becomes fp16(code * scale) as rmsnorm_fp8.hip computes it for the row
-// (reference.py:35-50; dynamic scale): fp64 sum of squares in the fixed order of norm_row.h
-// (all rows' chunk sums into `sums`, one barrier, every wave adds them), var = fp32(sum *
-// (1 / k)), rstd = 1 / sqrt(var + eps), y = fp16(fp32(x * rstd)) * w in fp16, absmax, scale,
-// codes, then the codes times the scale. Thread t takes the 8-element chunks t, t + T, ...; the
-// workgroup's W waves meet for each row's absmax in red_u[r][w].
+// The RMSNorm + e4m3 prologue over the m <= 4 rows of x staged in LDS (row r at xs + r *
+// xstride), in place: each row becomes fp16(code * scale) as rmsnorm_fp8.hip computes it for
+// the row (reference.py:35-50; dynamic scale): fp64 sum of squares in the fixed order of
+// norm_row.h, var = fp32(sum * (1 / k)), rstd = 1 / sqrt(var + eps), y = fp16(fp32(x * rstd)) *
+// w in fp16, absmax, scale, codes, then the codes times the scale. All rows go through each
+// phase together, one barrier per phase: every row's chunk sums into `sums` (every wave then
+// adds each row's), the normalized chunks and their maxima (the W waves meet for each row's
+// absmax in red_u[r][w]), then the codes. Thread t takes the 8-element chunks t, t + T, ... of
+// the flattened (row, chunk) index.
 __device__ __forceinline__ void norm_rows(const LinearArgs& a, _Float16* xs, int xstride, double* sums,
-                                          uint32_t* red_u, int W, int wave, int lane) {
+                                          uint32_t* red_u, const u4* gs, int W, int wave, int lane) {
+  constexpr int R = kNormMaxM;
   const int T = W * 64;
+  const int m = a.m;
   const int chunks = a.k >> 3;
+  const int total = m * chunks;
   const int lpad = norm_lpad(a.k);
   const int lshift = __builtin_ctz(lpad);
-  const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.norm_w, (uint32_t)a.k * 2u);
-  for (int e = threadIdx.x; e < (a.m << lshift); e += T) {
+  auto row_q = [&](int e, int& r, int& q) {
+    r = 0;
+#pragma unroll
+    for (int i = 1; i < R; ++i) r += (int)(e >= i * chunks);
+    q = e - r * chunks;
+  };
+  for (int e = threadIdx.x; e < (m << lshift); e += T) {
     const int r = e >> lshift, q = e & (lpad - 1);
     double v = 0.0;
     if (q < chunks) {
@@ -116,63 +127,104 @@ __device__ __forceinline__ void norm_rows(const LinearArgs& a, _Float16* xs, int
     sums[e] = v;
   }
   __syncthreads();
-  for (int r = 0; r < a.m; ++r) {
+  // every row's rstd in every wave (the fixed-order total of norm_row.h)
+  float rstd[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    rstd[r] = 0.0f;
+    if (r < m) {
+      const double t = staged_row_total(sums, lpad, r);  // every lane of the wave takes part
+      const float var = (float)((double)(float)t * a.norm_inv_k);
+      rstd[r] = 1.0f / __builtin_sqrtf(var + a.norm_eps);
+    }
+  }
+  uint32_t am[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) am[r] = 0;
+  for (int e = threadIdx.x; e < total; e += T) {
+    int r, q;
+    row_q(e, r, q);
+    float rs = rstd[0];
+#pragma unroll
+    for (int i = 1; i < R; ++i) rs = r == i ? rstd[i] : rs;
     u4* row = reinterpret_cast<u4*>(xs + r * xstride);
-    const double total = staged_row_total(sums, lpad, r);
-    const float var = (float)((double)(float)total * a.norm_inv_k);
-    const float rstd = 1.0f / __builtin_sqrtf(var + a.norm_eps);
-
-    uint32_t am = 0;
-    for (int q = threadIdx.x; q < chunks; q += T) {
-      u4 v = row[q];
-      const u4 gw = load_b128(rw, (uint32_t)q * 16u);
+    u4 v = row[q];
+    const u4 gw = gs[q];  // the norm weight, staged in LDS
+    uint32_t mx = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const h2 x = as_h2(v[j]);
+      h2 nrm;
+      nrm[0] = mul_round_f32_then_f16((float)x[0], rs);
+      nrm[1] = mul_round_f32_then_f16((float)x[1], rs);
+      v[j] = as_u32(nrm * as_h2(gw[j]));
+      const uint32_t yb = v[j] & 0x7FFF7FFFu;
+      mx = __builtin_elementwise_max(mx, __builtin_elementwise_max(yb & 0xFFFFu, yb >> 16));
+    }
+    row[q] = v;
+#pragma unroll
+    for (int i = 0; i < R; ++i) am[i] = r == i ? __builtin_elementwise_max(am[i], mx) : am[i];
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    if (r < m) {
+      const uint32_t wmax = wave_max_u32(am[r]);
+      if (lane == 0) red_u[r * 16 + wave] = wmax;
+    }
+  }
+  __syncthreads();
+  float sc[R], r32[R];
+  double rcp[R];
+  bool fast[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    sc[r] = 1.0f, r32[r] = 0.0f, rcp[r] = 0.0, fast[r] = true;
+    if (r < m) {
+      uint32_t m_bits = red_u[r * 16];
+      for (int w = 1; w < W; ++w) m_bits = __builtin_elementwise_max(m_bits, red_u[r * 16 + w]);
+      const float amax = (float)__builtin_bit_cast(_Float16, (uint16_t)m_bits);
+      sc[r] = dynamic_scale(amax);
+      fast[r] = __builtin_isfinite(amax) && __builtin_isfinite(sc[r]) && sc[r] > 0.0f;
+      r32[r] = fast[r] ? 1.0f / sc[r] : 0.0f;
+      rcp[r] = fast[r] ? 0.0 : 1.0 / (double)sc[r];
+    }
+  }
+  for (int e = threadIdx.x; e < total; e += T) {
+    int r, q;
+    row_q(e, r, q);
+    float s = sc[0], rr = r32[0];
+    double rc = rcp[0];
+    bool f = fast[0];
+#pragma unroll
+    for (int i = 1; i < R; ++i) {
+      s = r == i ? sc[i] : s;
+      rr = r == i ? r32[i] : rr;
+      rc = r == i ? rcp[i] : rc;
+      f = r == i ? fast[i] : f;
+    }
+    u4* row = reinterpret_cast<u4*>(xs + r * xstride);
+    const u4 v = row[q];
+    uint32_t lo, hi;
+    if (f) {
+      float ev[8];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const h2 x = as_h2(v[j]);
-        h2 nrm;
-        nrm[0] = mul_round_f32_then_f16((float)x[0], rstd);
-        nrm[1] = mul_round_f32_then_f16((float)x[1], rstd);
-        v[j] = as_u32(nrm * as_h2(gw[j]));
-        const uint32_t yb = v[j] & 0x7FFF7FFFu;
-        am = __builtin_elementwise_max(am, __builtin_elementwise_max(yb & 0xFFFFu, yb >> 16));
+        ev[2 * j] = __builtin_amdgcn_fmed3f(quotient_dynamic<false>(as_h2(v[j]), s, rr), -kFp8Max, kFp8Max);
+        ev[2 * j + 1] = __builtin_amdgcn_fmed3f(quotient_dynamic<true>(as_h2(v[j]), s, rr), -kFp8Max, kFp8Max);
       }
-      row[q] = v;
-    }
-    const uint32_t wmax = wave_max_u32(am);
-    if (lane == 0) red_u[r * 16 + wave] = wmax;
-    __syncthreads();
-    uint32_t m_bits = red_u[r * 16];
-    for (int w = 1; w < W; ++w) m_bits = __builtin_elementwise_max(m_bits, red_u[r * 16 + w]);
-    const float amax = (float)__builtin_bit_cast(_Float16, (uint16_t)m_bits);
-    const float s = dynamic_scale(amax);
-    const bool fast = __builtin_isfinite(amax) && __builtin_isfinite(s) && s > 0.0f;
-    const float r32 = fast ? 1.0f / s : 0.0f;
-    const double rcp = fast ? 0.0 : 1.0 / (double)s;
-
-    for (int q = threadIdx.x; q < chunks; q += T) {
-      const u4 v = row[q];
-      uint32_t lo, hi;
-      if (fast) {
-        float e[8];
+      lo = encode4_clamped(ev[0], ev[1], ev[2], ev[3]);
+      hi = encode4_clamped(ev[4], ev[5], ev[6], ev[7]);
+    } else {
+      lo = hi = 0;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          e[2 * j] = __builtin_amdgcn_fmed3f(quotient_dynamic<false>(as_h2(v[j]), s, r32), -kFp8Max, kFp8Max);
-          e[2 * j + 1] = __builtin_amdgcn_fmed3f(quotient_dynamic<true>(as_h2(v[j]), s, r32), -kFp8Max, kFp8Max);
-        }
-        lo = encode4_clamped(e[0], e[1], e[2], e[3]);
-        hi = encode4_clamped(e[4], e[5], e[6], e[7]);
-      } else {
-        lo = hi = 0;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const uint32_t code = encode_slow(as_h2(v[j >> 1])[j & 1], rcp);
-          if (j < 4) lo |= code << (8 * j);
-          else hi |= code << (8 * (j - 4));
-        }
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t code = encode_slow(as_h2(v[j >> 1])[j & 1], rc);
+        if (j < 4) lo |= code << (8 * j);
+        else hi |= code << (8 * (j - 4));
       }
-      const u2 d0 = dequant_codes4(lo, s), d1 = dequant_codes4(hi, s);
-      row[q] = u4{d0[0], d0[1], d1[0], d1[1]};
     }
+    const u2 d0 = dequant_codes4(lo, s), d1 = dequant_codes4(hi, s);
+    row[q] = u4{d0[0], d0[1], d1[0], d1[1]};
   }
 }
 
@@ -382,6 +434,10 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_stream_kernel(LinearArgs a, in
     if (NORM) g1 = load_b128(make_rsrc(a.norm_w, (uint32_t)a.k * 2u), ok ? (uint32_t)q * 16u : kOutOfRange);
   } else {
     load_x(threadIdx.x);
+    // the norm weight's first chunk per thread, issued ahead of the ring like x (NORM)
+    if (NORM)
+      g1 = load_b128(make_rsrc(a.norm_w, (uint32_t)a.k * 2u),
+                     (int)threadIdx.x < chunks ? (uint32_t)threadIdx.x * 16u : kOutOfRange);
   }
   __builtin_amdgcn_sched_barrier(0);
 
@@ -411,9 +467,10 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_stream_kernel(LinearArgs a, in
     issue(p);
     __builtin_amdgcn_sched_barrier(0);  // slot 0 is the oldest load of the ring
   }
-  // NORM scratch: the rows' chunk sums, then the maxima [4][16]
+  // NORM scratch: the rows' chunk sums, the maxima [4][16], the norm weight [K / 8] chunks
   double* sums = reinterpret_cast<double*>(part + W * tpw * kPartLanes);
   uint32_t* red_u = reinterpret_cast<uint32_t*>(sums + (NORM ? a.m * norm_lpad(a.k) : 0));
+  u4* gs = reinterpret_cast<u4*>(red_u + 64);
   if (one) {
     const int e = threadIdx.x;
     const int r = row_of(e), q = e - r * chunks;
@@ -427,8 +484,11 @@ __global__ __launch_bounds__(MAXW * 64) void gemv_stream_kernel(LinearArgs a, in
     }
   }
   if (NORM && !one) {
-    __syncthreads();  // every row of x is in LDS
-    norm_rows(a, xs, xstride, sums, red_u, W, wave, lane);
+    if ((int)threadIdx.x < chunks) gs[threadIdx.x] = g1;
+    for (int q = threadIdx.x + T; q < chunks; q += T)
+      gs[q] = load_b128(make_rsrc(a.norm_w, (uint32_t)a.k * 2u), (uint32_t)q * 16u);
+    __syncthreads();  // every row of x and the norm weight are in LDS
+    norm_rows(a, xs, xstride, sums, red_u, gs, W, wave, lane);
   }
   for (int e = threadIdx.x; e < W * tpw * kPartLanes; e += T) part[e] = f4{0.0f, 0.0f, 0.0f, 0.0f};
   __syncthreads();
