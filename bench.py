@@ -244,7 +244,7 @@ def traffic_summary(fetch_dir: str, write_dir: str, probe_log: str) -> int:
         wb = statistics.mean(write[i * n_launch:(i + 1) * n_launch]) * w_scale
         t = fb + wb
         name = (f"{cfg['kernel']} bm{cfg['block_m']} bn{cfg['block_n']} bk{cfg['block_k']} "
-                f"w{cfg['num_warps']} st{cfg['num_stages']}")
+                f"sk{cfg['split_k']} w{cfg['num_warps']} st{cfg['num_stages']}")
         lines.append(f"| {name} | {fb:.0f} | {wb:.0f} | {t:.0f} | {t / alg:.3f} |")
         machine.append(f"traffic: {t:.0f} {json.dumps(cfg)}")
     lines += ["", "Machine-readable (bench.py reads the row of the config in use):", "", "```", *machine, "```", ""]
@@ -1397,10 +1397,13 @@ def main() -> int:
         return read_probes(dev, layers, copies, xs, cfg1)
 
     if args.traffic_probe:
-        from tokenforge.kernels.config import candidate_configs
+        from tokenforge.kernels.config import candidate_configs, stream_form_applies
 
         qw_s_z = [layers[c][2] for c in range(copies)]
-        cands = candidate_configs(1, GROUP)
+        _, n_g, k_g = SHAPES[2]
+        # the candidates that run on gate_up (a stream form's K split needs a step per wave)
+        cands = [c for c in candidate_configs(1, GROUP)
+                 if not c.stream or stream_form_applies(1, n_g, k_g, c.num_warps, max_m=c.block_m, split_k=c.split_k)]
         for cfg in cands:
             for c in range(copies):  # cold: each launch reads a copy the previous ones evicted
                 qw, sc, qz = qw_s_z[c % copies]
@@ -1410,7 +1413,6 @@ def main() -> int:
         for _ in range(4):
             torch.neg(src, out=dst)
         torch.cuda.synchronize()
-        _, n_g, k_g = SHAPES[2]
         print(json.dumps({"traffic_probe": {"kernel": "gate_up GEMV M=1", "launches": copies,
                                             "configs": [c.to_dict() for c in cands],
                                             "algorithmic_bytes": bytes_moved(1, n_g, k_g),

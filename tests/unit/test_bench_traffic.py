@@ -53,7 +53,7 @@ def test_summary_rows_and_lookup(tmp_path: Path, monkeypatch: pytest.MonkeyPatch
     log.write_text("noise\n" + json.dumps(probe) + "\n")
     assert bench.traffic_summary(str(tmp_path / "f"), str(tmp_path / "w"), str(log)) == 0
     text = summary.read_text()
-    assert "| gemv_dot bm1 bn16 bk128 w4 st2 |" in text
+    assert "| gemv_dot bm1 bn16 bk128 sk1 w4 st2 |" in text
     assert bench.committed_traffic(CFGS[0]) == pytest.approx(1000 * 1024 * 2 + 10 * 1024)
     assert bench.committed_traffic(CFGS[1]) == pytest.approx(2000 * 1024 * 2 + 30 * 1024)
     other = dict(CFGS[0], num_warps=8)
