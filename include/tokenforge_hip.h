@@ -114,7 +114,9 @@ int tf_w4a16_dequant(const int32_t* qweight_t, const uint16_t* scales,
 
 /* Launch configuration; the counterpart of config.py:23-68 GemmConfig. The tuple
  * (kernel, block_m, block_n, block_k, num_warps, num_stages) must name a compiled
- * variant (see tf_num_variants / tf_get_variant); split_k is a runtime value. */
+ * variant (see tf_num_variants / tf_get_variant); split_k is a runtime value (1 for the gemv
+ * kernels except the stream form, gemv_mfma with block_k 512, which splits K across workgroup
+ * sets and adds the slices with the split-K reduce). */
 typedef struct tf_gemm_config {
   int32_t kernel;
   int32_t block_m;
@@ -252,7 +254,8 @@ int tf_rmsnorm_fp8_quant_ex(const uint16_t* x, int64_t ldx, const uint16_t* weig
  * two calls. No counterpart in the reference, which runs rmsnorm_fp8_quant (rmsnorm_fp8.py:76)
  * and the linear (ops.py:48) as separate kernels; for decode callers (M <= 4) that would
  * otherwise launch the norm on its own. Only the gemv stream form runs it (cfg gemv_mfma with
- * block_k 512; M <= 4); epilogue NONE or SILU_MUL; the codes and scales are not written.
+ * block_k 512 and block_m 4, split_k 1; M <= 4); epilogue NONE or SILU_MUL; the codes and
+ * scales are not written.
  * x fp16 [m, k] (row stride ldx), norm_weight fp16 [k] (16-byte aligned); the linear's other
  * arguments as tf_w4a16_linear_ex (no workspace). */
 int tf_rmsnorm_fp8_w4a16_linear(const uint16_t* x, int64_t ldx, const uint16_t* norm_weight, float eps,
