@@ -417,6 +417,256 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN == 4 && F == 16) ? 2 : 1) vo
   }
 }
 
+// ------------------------------------------------------------------ producer / consumer form
+//
+// The same pipeline with the roles split between waves: WM x WN consumer waves only read
+// operand fragments and run v_mfma_f32_16x16x32_f16 on a BM x BN tile, and kProd producer waves
+// (one per SIMD) issue the x stages, load the packed weights and dequantize them into the LDS
+// buffers. Consumers then issue no conversion work between their MFMAs, and the conversion is
+// spread over the four SIMDs. Both roles pass the same block barriers: iteration kb, after the
+// barrier, consumers multiply block kb while producers issue x block kb + S - 1, dequantize
+// block kb + 1 into the other buffer and issue the weights of block kb + 3; the producers'
+// vmcnt wait before the barrier covers the x stage of the next block (consumers issue no loads).
+template <int BM, int BN, int WM, int WN, int S>
+struct G2P {
+  static constexpr int kCons = WM * WN;
+  static constexpr int kProd = 4;
+  static constexpr int kThreads = 64 * (kCons + kProd);
+  static constexpr int kPThreads = 64 * kProd;
+  static constexpr int TM = BM / WM / 16;
+  static constexpr int TN = BN / WN / 16;
+  static constexpr int kAStage = BM * kBK * 2;
+  static constexpr int kBStage = BN * kBK * 2;
+  static constexpr int kADma = kAStage / 1024;
+  static constexpr int kAPerWave = kADma / kProd;
+  static constexpr int kBChunks = BN * kBK / 32;
+  static constexpr int kBPer = (kBChunks + kPThreads - 1) / kPThreads;
+  static constexpr int kLds = S * kAStage + 2 * kBStage;
+  static constexpr int kAfterA = 3 * kBPer + (S - 2) * (kAPerWave + 3 * kBPer);
+  static_assert(kADma % kProd == 0, "x stage must split evenly over the producers");
+  static_assert(S == 2 || S == 3, "x stages");
+  static_assert(BM % (16 * WM) == 0 && BN % (16 * WN) == 0, "wave tile");
+};
+
+template <int BM, int BN, int WM, int WN, int S>
+__global__ __launch_bounds__(64 * (WM * WN + 4), 1) void gemm2pc_kernel(
+    LinearArgs a, float* __restrict__ ws, int split_k, int tiles_n, int tiles_m) {
+  using C = G2P<BM, BN, WM, WN, S>;
+  constexpr int TM = C::TM, TN = C::TN, BP = C::kBPer;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  uint8_t* const a_lds = smem;
+  uint8_t* const b_lds = smem + S * C::kAStage;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool producer = wave >= C::kCons;  // wave-uniform
+  const int pwave = wave - C::kCons;
+  const int ptid = tid - 64 * C::kCons;
+  const int wm = wave / WN;
+  const int wn = wave % WN;
+
+  const int per_split = tiles_n * tiles_m;
+  const int t = xcd_tile(blockIdx.x, gridDim.x);
+  const int z = t / per_split;
+  const int r = t - z * per_split;
+  const int m0 = (r % tiles_m) * BM;
+  const int n0 = (r / tiles_m) * BN;
+  const int nkb = a.k / kBK;
+  const int kb0 = (int)(((int64_t)z * nkb) / split_k);
+  const int kb1 = (int)(((int64_t)(z + 1) * nkb) / split_k);
+
+  if (producer) {
+    const uint32_t row_bytes = (uint32_t)(a.k >> 1);
+    const int groups = a.k >> a.log2g;
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, (uint32_t)(((int64_t)(a.m - 1) * a.ldx + a.k) * 2));
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(a.qw, (uint32_t)a.n * row_bytes);
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.scales, (uint32_t)(groups * a.n * 2));
+    const __amdgpu_buffer_rsrc_t rz = make_rsrc(a.qz, (uint32_t)(groups * (a.n >> 3) * 4));
+    const UnpackConsts uc = unpack_consts();
+    uint32_t a_off[C::kAPerWave];
+#pragma unroll
+    for (int i = 0; i < C::kAPerWave; ++i) {
+      const int p = (pwave + C::kProd * i) * 64 + lane;
+      const int row = p >> 3;
+      const int c = (p & 7) ^ slot_xor(row);
+      const int m = m0 + row;
+      a_off[i] = m < a.m ? (uint32_t)(((int64_t)m * a.ldx + c * 8) * 2) : kOutOfRange;
+    }
+    auto issue_a = [&](int kb, int st) {
+      const bool ok = kb < kb1;
+#pragma unroll
+      for (int i = 0; i < C::kAPerWave; ++i) {
+        const uint32_t off = ok ? a_off[i] + (uint32_t)kb * (kBK * 2) : kOutOfRange;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rx, (__attribute__((address_space(3))) void*)(a_lds + st * C::kAStage + (pwave + C::kProd * i) * 1024), 16,
+            off, 0, 0, 0);
+      }
+    };
+    const uint32_t q_total = (uint32_t)(a.k >> 5);
+    uint32_t b_off[BP], b_step[BP], b_sbase[BP], b_zbase[BP], b_rows[BP];
+    int b_col[BP], b_half[BP];
+    bool b_act[BP];
+#pragma unroll
+    for (int i = 0; i < BP; ++i) {
+      const int id = ptid + i * C::kPThreads;
+      const int col = ((id >> 5) << 4) | (id & 15);
+      const int half = (id >> 4) & 1;
+      const int n = n0 + col;
+      b_act[i] = id < C::kBChunks;
+      b_col[i] = b_act[i] ? col : 0;
+      b_half[i] = half;
+      const uint32_t tt = (uint32_t)n >> 4, cc = (uint32_t)n & 15u;
+      const uint32_t rows = (uint32_t)tile_rows(a.n, tt);
+      b_rows[i] = rows;
+      b_off[i] = (b_act[i] && n < a.n) ? (tt * q_total * 16u + (uint32_t)half * rows + cc) * 16u : kOutOfRange;
+      b_step[i] = rows * 32u;
+      b_sbase[i] = tt * 16u * (uint32_t)groups + cc;
+      b_zbase[i] = tt * 2u * (uint32_t)groups + (cc >> 3);
+    }
+    u4 braw[2][BP];
+    uint32_t bsc[2][BP], bzw[2][BP];
+    auto issue_b = [&](int kb, int slot) {
+      const bool ok = kb < kb1;
+      const uint32_t grp = (uint32_t)((kb * kBK) >> a.log2g);
+#pragma unroll
+      for (int i = 0; i < BP; ++i) {
+        const bool v = ok && b_off[i] != kOutOfRange;
+        const uint32_t wo = b_off[i] + (uint32_t)kb * b_step[i];
+        const uint32_t so = (b_sbase[i] + grp * b_rows[i]) * 2u;
+        const uint32_t zo = (b_zbase[i] + grp * (b_rows[i] >> 3)) * 4u;
+        braw[slot][i] = load_b128(rq, v ? wo : kOutOfRange);
+        bsc[slot][i] = load_b16(rs, v ? so : kOutOfRange);
+        bzw[slot][i] = load_b32(rz, v ? zo : kOutOfRange);
+      }
+    };
+    auto store_b = [&](int slot, int buf) {
+#pragma unroll
+      for (int i = 0; i < BP; ++i) {
+        if (!b_act[i]) continue;
+        const QuantParams qp = make_params(zero_of(bzw[slot][i], (uint32_t)(n0 + b_col[i])), bsc[slot][i]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          h2 d[4];
+          dequant_word(braw[slot][i][j], qp, uc, d);
+          *reinterpret_cast<u4*>(b_lds + buf * C::kBStage + swz(b_col[i], b_half[i] * 4 + j)) =
+              u4{as_u32(d[0]), as_u32(d[1]), as_u32(d[2]), as_u32(d[3])};
+        }
+      }
+    };
+    // prologue: x blocks kb0 .. kb0 + S - 2 in flight; block kb0 dequantized into buffer 0; the
+    // register slots hold blocks kb0 + 1 (slot 1) and kb0 + 2 (slot 0).
+#pragma unroll
+    for (int i = 0; i < S - 1; ++i) issue_a(kb0 + i, i);
+    __builtin_amdgcn_sched_barrier(0);
+    issue_b(kb0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    issue_b(kb0 + 1, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    store_b(0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    issue_b(kb0 + 2, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    auto iteration = [&](int kb, int st, auto odd_tag) {
+      constexpr int odd = decltype(odd_tag)::value;
+      block_barrier<C::kAfterA>();
+      issue_a(kb + S - 1, (st + S - 1) % S);
+      __builtin_amdgcn_sched_barrier(0);
+      store_b(odd ^ 1, odd ^ 1);
+      __builtin_amdgcn_sched_barrier(0);
+      issue_b(kb + 3, odd ^ 1);
+    };
+    int kb = kb0, st = 0;
+    for (; kb + 1 < kb1; kb += 2) {
+      iteration(kb, S == 2 ? 0 : st, std::integral_constant<int, 0>{});
+      st = (st + 1 == S) ? 0 : st + 1;
+      iteration(kb + 1, S == 2 ? 1 : st, std::integral_constant<int, 1>{});
+      st = (st + 1 == S) ? 0 : st + 1;
+    }
+    if (kb < kb1) iteration(kb, S == 2 ? 0 : st, std::integral_constant<int, 0>{});
+    return;  // no barrier follows the main loop
+  }
+
+  // ---- consumers
+  f4 acc[TM][TN];
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) acc[tm][tn] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  const int a_row0 = wm * TM * 16 + (lane & 15);
+  const int b_row0 = wn * TN * 16 + (lane & 15);
+  auto read_frags = [&](const uint8_t* A, const uint8_t* B, int kk, h8 (&af)[TM], h8 (&bf)[TN]) {
+    const int c = 4 * kk + (lane >> 4);
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm) af[tm] = *reinterpret_cast<const h8*>(A + swz(a_row0 + tm * 16, c));
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) bf[tn] = *reinterpret_cast<const h8*>(B + swz(b_row0 + tn * 16, c));
+  };
+  auto iteration = [&](int kb, int st, auto odd_tag) {
+    constexpr int odd = decltype(odd_tag)::value;
+    block_barrier<C::kAfterA>();
+    const uint8_t* A = a_lds + st * C::kAStage;
+    const uint8_t* B = b_lds + odd * C::kBStage;
+    h8 af[2][TM], bf[2][TN];
+    read_frags(A, B, 0, af[0], bf[0]);
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      if (kk + 1 < 2) read_frags(A, B, kk + 1, af[kk + 1], bf[kk + 1]);
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn)
+          acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bf[kk][tn], af[kk][tm], acc[tm][tn], 0, 0, 0);
+    }
+  };
+  int kb = kb0, st = 0;
+  for (; kb + 1 < kb1; kb += 2) {
+    iteration(kb, S == 2 ? 0 : st, std::integral_constant<int, 0>{});
+    st = (st + 1 == S) ? 0 : st + 1;
+    iteration(kb + 1, S == 2 ? 1 : st, std::integral_constant<int, 1>{});
+    st = (st + 1 == S) ? 0 : st + 1;
+  }
+  if (kb < kb1) iteration(kb, S == 2 ? 0 : st, std::integral_constant<int, 0>{});
+
+  // ---- epilogue (the 16x16 form's, transposed accumulators: see gemm2_kernel)
+  const bool partials = split_k > 1;
+  const bool stage_y = !partials && a.epilogue == TF_EPILOGUE_SILU_MUL;
+  uint16_t* const dst = stage_y ? reinterpret_cast<uint16_t*>(ws) : a.out;
+  const int64_t ldd = stage_y ? (int64_t)a.n : a.ldo;
+  const bool residual = !stage_y && a.epilogue == TF_EPILOGUE_RESIDUAL;
+  const bool vec = partials ? (a.n & 3) == 0 && (reinterpret_cast<uintptr_t>(ws) & 15) == 0
+                            : run_store_ok(a, dst, ldd, residual);
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm) {
+    const int m = m0 + (wm * TM + tm) * 16 + (lane & 15);
+    if (m >= a.m) continue;
+    const float rs = row_scale(a, m);
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) {
+      const int n = n0 + (wn * TN + tn) * 16 + 4 * (lane >> 4);
+      if (n >= a.n) continue;
+      float v[4];
+      if (partials) {
+        float* const p = ws + ((int64_t)z * a.m + m) * a.n + n;
+        if (vec) {
+          *reinterpret_cast<f4*>(p) = acc[tm][tn];
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (n + j < a.n) p[j] = acc[tm][tn][j];
+        }
+        continue;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float b = (a.bias && n + j < a.n) ? half_bits_to_float(a.bias[n + j]) : 0.0f;
+        v[j] = acc[tm][tn][j] * rs + b;
+      }
+      store_run4(a, dst, ldd, residual, m, n, v, vec);
+    }
+  }
+}
+
 int effective_split2(const LinearArgs& a, const tf_gemm_config& cfg) {
   const int nkb = a.k / kBK;
   return cfg.split_k < nkb ? cfg.split_k : (nkb > 0 ? nkb : 1);
@@ -453,10 +703,39 @@ int launch_gemm2(const LinearArgs& a, const tf_gemm_config& cfg, float* ws, hipS
   return TF_OK;
 }
 
+template <int BM, int BN, int WM, int WN, int S>
+int launch_gemm2pc(const LinearArgs& a, const tf_gemm_config& cfg, float* ws, hipStream_t stream) {
+  using C = G2P<BM, BN, WM, WN, S>;
+  if ((1 << a.log2g) < kBK)
+    return fail(TF_EINVAL, "tf_w4a16_linear: this gemm_mfma variant needs group_size >= 64 (block_k 64)");
+  const int64_t x_bytes = ((int64_t)(a.m - 1) * a.ldx + a.k) * 2;
+  const int64_t w_bytes = (int64_t)a.n * (a.k / 2);
+  if (x_bytes >= (int64_t)kOutOfRange || w_bytes >= (int64_t)kOutOfRange)
+    return fail(TF_EINVAL, "tf_w4a16_linear: this gemm_mfma variant needs x and qweight_t below 2 GiB");
+  const int split = effective_split2(a, cfg);
+  if (lds_gemm_workspace(a, split) > 0 && ws == nullptr)
+    return fail(TF_EINVAL, "tf_w4a16_linear: this config needs a workspace");
+  const int tiles_n = (int)cdiv(a.n, BN);
+  const int tiles_m = (int)cdiv(a.m, BM);
+  const int64_t grid = (int64_t)tiles_n * tiles_m * split;
+  if (grid > 0x7FFFFFFF) return fail(TF_EINVAL, "tf_w4a16_linear: too many tiles");
+  auto kernel = gemm2pc_kernel<BM, BN, WM, WN, S>;
+  if (C::kLds > 64 * 1024 &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          C::kLds) != hipSuccess)
+    return fail(TF_ELAUNCH, "tf_w4a16_linear: cannot reserve LDS for gemm_mfma");
+  kernel<<<(unsigned)grid, C::kThreads, C::kLds, stream>>>(a, ws, split, tiles_n, tiles_m);
+  if (int rc = check_launch("tf_w4a16_linear(gemm_mfma)")) return rc;
+  return lds_gemm_finish(a, ws, split, stream);
+}
+
 // num_stages = S + 1 (3: two x stages, 4: three) tells these variants apart from the
 // two-buffer kernel (num_stages 2), S + 4 (6, 7) the 16x16 fragment form; num_warps = WM * WN.
 #define TF_GEMM2(BM, BN, WM, WN, S) \
   {{TF_KERNEL_GEMM_MFMA, BM, BN, 64, 1, WM * WN, S + 1}, (launch_gemm2<BM, BN, WM, WN, S, 32>), gemm2_workspace}
+// num_stages 8: the producer / consumer form (two x stages); num_warps counts the consumer waves.
+#define TF_GEMM2PC(BM, BN, WM, WN) \
+  {{TF_KERNEL_GEMM_MFMA, BM, BN, 64, 1, WM * WN, 8}, (launch_gemm2pc<BM, BN, WM, WN, 2>), gemm2_workspace}
 #define TF_GEMM2F16(BM, BN, WM, WN, S) \
   {{TF_KERNEL_GEMM_MFMA, BM, BN, 64, 1, WM * WN, S + 4}, (launch_gemm2<BM, BN, WM, WN, S, 16>), gemm2_workspace}
 
@@ -475,6 +754,8 @@ const Variant kGemm2Variants[] = {
     TF_GEMM2F16(256, 160, 4, 2, 3), TF_GEMM2F16(256, 192, 4, 2, 2), TF_GEMM2F16(256, 224, 4, 2, 2),
     TF_GEMM2F16(256, 128, 4, 2, 2), TF_GEMM2F16(256, 256, 4, 2, 2), TF_GEMM2F16(128, 160, 2, 2, 2),
     TF_GEMM2F16(128, 128, 2, 2, 2), TF_GEMM2F16(128, 256, 2, 4, 2),
+    // producer / consumer form
+    TF_GEMM2PC(256, 160, 4, 2), TF_GEMM2PC(256, 128, 4, 2), TF_GEMM2PC(128, 256, 2, 4), TF_GEMM2PC(128, 128, 2, 2),
 };
 
 }  // namespace
