@@ -196,7 +196,7 @@ def _gemm_variants() -> list[tuple[str, int, int, int, int, int]]:
     # num_stages 8: the producer / consumer form (two x stages): num_warps consumer waves only
     # read fragments and run MFMAs, four producer waves stage x and dequantize the weights.
     out += [("gemm_mfma", 256, 160, 64, 8, 8), ("gemm_mfma", 256, 128, 64, 8, 8), ("gemm_mfma", 128, 256, 64, 8, 8),
-            ("gemm_mfma", 128, 128, 64, 4, 8)]
+            ("gemm_mfma", 128, 128, 64, 4, 8), ("gemm_mfma", 256, 192, 64, 8, 8)]
     # block_k 128: skinny form (M <= 128), weights streamed into MFMA registers, 4 waves,
     # num_stages = x stages in LDS.
     skinny = [(1, 1, 3), (1, 2, 3), (1, 4, 3), (2, 1, 3), (2, 2, 3), (2, 4, 3), (4, 1, 3), (4, 2, 3),

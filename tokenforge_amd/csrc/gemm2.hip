@@ -446,6 +446,9 @@ struct G2P {
   static_assert(kADma % kProd == 0, "x stage must split evenly over the producers");
   static_assert(S == 2 || S == 3, "x stages");
   static_assert(BM % (16 * WM) == 0 && BN % (16 * WN) == 0, "wave tile");
+  // More than 20 MFMA tiles a consumer: its weight fragments are read one 16-column fragment at
+  // a time (the registers of 12 waves a CU hold no two whole steps of fragments beside them).
+  static constexpr bool kStreamB = TM * TN > 20;
 };
 
 template <int BM, int BN, int WM, int WN, int S>
@@ -607,6 +610,26 @@ __global__ __launch_bounds__(64 * (WM * WN + 4), 1) void gemm2pc_kernel(
     block_barrier<C::kAfterA>();
     const uint8_t* A = a_lds + st * C::kAStage;
     const uint8_t* B = b_lds + odd * C::kBStage;
+    if constexpr (C::kStreamB) {
+      // per step the A fragments, then one B fragment at a time (the next read before this
+      // one's MFMAs)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const int c = 4 * kk + (lane >> 4);
+        h8 af[TM], bq[2];
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm) af[tm] = *reinterpret_cast<const h8*>(A + swz(a_row0 + tm * 16, c));
+        bq[0] = *reinterpret_cast<const h8*>(B + swz(b_row0, c));
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) {
+          if (tn + 1 < TN) bq[(tn + 1) & 1] = *reinterpret_cast<const h8*>(B + swz(b_row0 + (tn + 1) * 16, c));
+#pragma unroll
+          for (int tm = 0; tm < TM; ++tm)
+            acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bq[tn & 1], af[tm], acc[tm][tn], 0, 0, 0);
+        }
+      }
+      return;
+    }
     h8 af[2][TM], bf[2][TN];
     read_frags(A, B, 0, af[0], bf[0]);
 #pragma unroll
@@ -756,6 +779,7 @@ const Variant kGemm2Variants[] = {
     TF_GEMM2F16(128, 128, 2, 2, 2), TF_GEMM2F16(128, 256, 2, 4, 2),
     // producer / consumer form
     TF_GEMM2PC(256, 160, 4, 2), TF_GEMM2PC(256, 128, 4, 2), TF_GEMM2PC(128, 256, 2, 4), TF_GEMM2PC(128, 128, 2, 2),
+    TF_GEMM2PC(256, 192, 4, 2),
 };
 
 }  // namespace
