@@ -23,12 +23,13 @@ from oracle import pack as opack
 from oracle import reference as oref
 from tests.numerics import cases
 from tests.numerics.tolerance import EPS_FP16, NORMWISE_MAX, contract, relative_max_error
-from tokenforge.kernels.config import FP8_TILES, GemmConfig, fp8_gemm_applies, fp8_gemm_config
+from tokenforge.kernels.config import FP8_PC_TILES, FP8_TILES, GemmConfig, fp8_gemm_applies, fp8_gemm_config
 from tokenforge.kernels.hip.w4a16 import w4a8_gemm_ex
 
 pytestmark = pytest.mark.gpu
 G = 128
-FP8_CONFIGS = [GemmConfig("gemm_fp8", bm, bn, 128, 1, wm * wn, s + 1) for bm, bn, wm, wn, s in FP8_TILES]
+FP8_CONFIGS = ([GemmConfig("gemm_fp8", bm, bn, 128, 1, wm * wn, s + 1) for bm, bn, wm, wn, s in FP8_TILES]
+               + [GemmConfig("gemm_fp8", bm, bn, 128, 1, wm * wn, 8) for bm, bn, wm, wn in FP8_PC_TILES])
 
 
 def _codes(m: int, k: int, seed: int) -> tuple[np.ndarray, np.ndarray]:

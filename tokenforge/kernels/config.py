@@ -219,8 +219,14 @@ FP8_TILES: tuple[tuple[int, int, int, int, int], ...] = (
 )
 
 
+FP8_PC_TILES: tuple[tuple[int, int, int, int], ...] = ((256, 160, 4, 2), (256, 128, 4, 2), (128, 256, 2, 4), (128, 128, 2, 4))
+"""The fp8 GEMM's producer / consumer form (num_stages 8): (block_m, block_n, consumer waves
+along M, along N), in the library's order after FP8_TILES."""
+
+
 def _fp8_variants() -> list[tuple[str, int, int, int, int, int]]:
-    return [("gemm_fp8", bm, bn, 128, wm * wn, s + 1) for bm, bn, wm, wn, s in FP8_TILES]
+    return ([("gemm_fp8", bm, bn, 128, wm * wn, s + 1) for bm, bn, wm, wn, s in FP8_TILES]
+            + [("gemm_fp8", bm, bn, 128, wm * wn, 8) for bm, bn, wm, wn in FP8_PC_TILES])
 
 
 VARIANTS: tuple[tuple[str, int, int, int, int, int], ...] = tuple(
@@ -478,9 +484,9 @@ _FP8_PARTIAL_BYTES_PER_US = 4.0e6
 def fp8_gemm_config(bucket: int, n: int, k: int) -> GemmConfig:
     """Launch config of the W4A8 fp8 GEMM for one bucket: the tile and K split with the lowest
     modelled time (rounds of workgroups over the CUs x blocks per workgroup x block time, plus
-    the split's partials). On the Qwen2.5-7B shapes it picks the configs measured fastest:
-    gate_up 256 x 160 at M = 256 and 256 x 128 above; down 256 x 128 with split 9 / 2 / 1 at
-    M = 256 / 1024 / 4096."""
+    the split's partials), in its producer / consumer form where the tile has one. On the
+    Qwen2.5-7B shapes it picks the configs measured fastest: gate_up 256 x 160 at M = 256 and
+    256 x 128 above; down 256 x 128 with split 9 / 2 / 1 at M = 256 / 1024 / 4096."""
     tiles_by_m = ((256, 128), (256, 160), (256, 192)) if bucket >= 256 else ((128, 256), (128, 128))
     k_blocks = max(1, k // 128)
     best: tuple[float, int, int, int] | None = None
@@ -501,4 +507,7 @@ def fp8_gemm_config(bucket: int, n: int, k: int) -> GemmConfig:
                 best = (us, bm, bn, split)
     assert best is not None
     _, bm, bn, split = best
-    return GemmConfig("gemm_fp8", bm, bn, 128, split, 8, 3)
+    # the producer / consumer form where the tile has one (same box, Qwen2.5-7B shapes: 3-14%
+    # faster than the shared-role form at M = 256..4096)
+    stages = 8 if any((bm, bn) == (pbm, pbn) for pbm, pbn, _, _ in FP8_PC_TILES) else 3
+    return GemmConfig("gemm_fp8", bm, bn, 128, split, 8, stages)

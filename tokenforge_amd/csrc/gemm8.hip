@@ -342,6 +342,250 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm8_kernel(LinearArgs a, float
   }
 }
 
+// ------------------------------------------------------------------ producer / consumer form
+//
+// As gemm2.hip's producer / consumer form: WM x WN consumer waves read the x and weight
+// fragments and run the fp8 MFMAs with the group-scale FMAs, four producer waves (one per SIMD)
+// issue the x stages, load the packed weights and write their e4m3 (q - z) codes and group
+// scales; both roles pass the same block barriers.
+template <int BM, int BN, int WM, int WN, int S>
+struct G8P {
+  static constexpr int kCons = WM * WN;
+  static constexpr int kProd = 4;
+  static constexpr int kThreads = 64 * (kCons + kProd);
+  static constexpr int kPThreads = 64 * kProd;
+  static constexpr int TM = BM / WM / 16;
+  static constexpr int TN = BN / WN / 16;
+  static constexpr int kAStage = BM * kBK;
+  static constexpr int kBStage = BN * kBK;
+  static constexpr int kScaleBytes = BN * 4;
+  static constexpr int kADma = kAStage / 1024;
+  static constexpr int kAPerWave = kADma / kProd;
+  static constexpr int kBChunks = BN * 4;
+  static constexpr int kBPer = (kBChunks + kPThreads - 1) / kPThreads;
+  static constexpr int kLds = S * kAStage + 2 * kBStage + 2 * kScaleBytes;
+  static constexpr int kAfterA = 3 * kBPer + (S - 2) * (kAPerWave + 3 * kBPer);
+  static_assert(kADma % kProd == 0, "x stage must split evenly over the producers");
+  static_assert(S == 2, "x stages");
+  static_assert(BM % (16 * WM) == 0 && BN % (16 * WN) == 0, "wave tile");
+};
+
+template <int BM, int BN, int WM, int WN, int S>
+__global__ __launch_bounds__(64 * (WM * WN + 4), 1) void gemm8pc_kernel(LinearArgs a, float* __restrict__ ws,
+                                                                         int split_k, int tiles_n, int tiles_m) {
+  using C = G8P<BM, BN, WM, WN, S>;
+  constexpr int TM = C::TM, TN = C::TN, BP = C::kBPer;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  uint8_t* const a_lds = smem;
+  uint8_t* const b_lds = smem + S * C::kAStage;
+  float* const s_lds = reinterpret_cast<float*>(smem + S * C::kAStage + 2 * C::kBStage);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool producer = wave >= C::kCons;  // wave-uniform
+  const int pwave = wave - C::kCons;
+  const int ptid = tid - 64 * C::kCons;
+  const int wm = wave / WN;
+  const int wn = wave % WN;
+
+  const int per_split = tiles_n * tiles_m;
+  const int t = xcd_tile(blockIdx.x, gridDim.x);
+  const int z = t / per_split;
+  const int r = t - z * per_split;
+  const int m0 = (r % tiles_m) * BM;
+  const int n0 = (r / tiles_m) * BN;
+  const int nkb = a.k / kBK;
+  const int kb0 = (int)(((int64_t)z * nkb) / split_k);
+  const int kb1 = (int)(((int64_t)(z + 1) * nkb) / split_k);
+
+  if (producer) {
+    const int groups = a.k >> a.log2g;  // == nkb (group_size 128)
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x8, (uint32_t)((int64_t)(a.m - 1) * a.ldx8 + a.k));
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(a.qw, (uint32_t)((int64_t)a.n * (a.k >> 1)));
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.scales, (uint32_t)(groups * a.n * 2));
+    const __amdgpu_buffer_rsrc_t rz = make_rsrc(a.qz, (uint32_t)(groups * (a.n >> 3) * 4));
+    const UnpackConsts uc = unpack_consts();
+    uint32_t a_off[C::kAPerWave];
+#pragma unroll
+    for (int i = 0; i < C::kAPerWave; ++i) {
+      const int p = (pwave + C::kProd * i) * 64 + lane;
+      const int row = p >> 3;
+      const int c = (p & 7) ^ slot_xor8(row);
+      const int m = m0 + row;
+      a_off[i] = m < a.m ? (uint32_t)((int64_t)m * a.ldx8 + c * 16) : kOutOfRange;
+    }
+    auto issue_a = [&](int kb, int st) {
+      const bool ok = kb < kb1;
+#pragma unroll
+      for (int i = 0; i < C::kAPerWave; ++i) {
+        const uint32_t off = ok ? a_off[i] + (uint32_t)kb * kBK : kOutOfRange;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rx, (__attribute__((address_space(3))) void*)(a_lds + st * C::kAStage + (pwave + C::kProd * i) * 1024), 16,
+            off, 0, 0, 0);
+      }
+    };
+    // chunk (ptid + i * producers) % chunks, as gemm8_kernel assigns them (a few producer
+    // threads redo a chunk another one converts: same data to the same place)
+    const uint32_t q_total = (uint32_t)(a.k >> 5);
+    uint32_t b_off[BP], b_sbase[BP], b_zbase[BP];
+    int b_col[BP], b_g[BP];
+#pragma unroll
+    for (int i = 0; i < BP; ++i) {
+      const int id = (ptid + i * C::kPThreads) % C::kBChunks;
+      const int col = ((id >> 6) << 4) | (id & 15);
+      const int g = (id >> 4) & 3;
+      const int n = n0 + col;
+      b_col[i] = col;
+      b_g[i] = g;
+      const uint32_t tt = (uint32_t)n >> 4, cc = (uint32_t)n & 15u;
+      const bool ok = n < a.n;
+      b_off[i] = ok ? (tt * q_total * 16u + (uint32_t)g * 16u + cc) * 16u : kOutOfRange;
+      b_sbase[i] = ok ? tt * 16u * (uint32_t)groups + cc : kOutOfRange;
+      b_zbase[i] = ok ? tt * 2u * (uint32_t)groups + (cc >> 3) : kOutOfRange;
+    }
+    u4 braw[2][BP];
+    uint32_t bsc[2][BP], bzw[2][BP];
+    auto issue_b = [&](int kb, int slot) {
+      const bool ok = kb < kb1;
+#pragma unroll
+      for (int i = 0; i < BP; ++i) {
+        const bool v = ok && b_off[i] != kOutOfRange;
+        braw[slot][i] = load_b128(rq, v ? b_off[i] + (uint32_t)kb * 1024u : kOutOfRange);
+        bsc[slot][i] = load_b16(rs, v ? (b_sbase[i] + (uint32_t)kb * 16u) * 2u : kOutOfRange);
+        bzw[slot][i] = load_b32(rz, v ? (b_zbase[i] + (uint32_t)kb * 2u) * 4u : kOutOfRange);
+      }
+    };
+    auto store_b = [&](int slot, int buf) {
+#pragma unroll
+      for (int i = 0; i < BP; ++i) {
+        const QuantParams qp = make_params(zero_of(bzw[slot][i], (uint32_t)(n0 + b_col[i])), bsc[slot][i]);
+#pragma unroll
+        for (int part = 0; part < 2; ++part) {
+          const u2 lo = word_to_e4m3(braw[slot][i][2 * part], qp, uc);
+          const u2 hi = word_to_e4m3(braw[slot][i][2 * part + 1], qp, uc);
+          *reinterpret_cast<u4*>(b_lds + buf * C::kBStage + swz8(b_col[i], 2 * b_g[i] + part)) =
+              u4{lo[0], lo[1], hi[0], hi[1]};
+        }
+        s_lds[buf * BN + b_col[i]] = half_bits_to_float((uint16_t)bsc[slot][i]);
+      }
+    };
+#pragma unroll
+    for (int i = 0; i < S - 1; ++i) issue_a(kb0 + i, i);
+    __builtin_amdgcn_sched_barrier(0);
+    issue_b(kb0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    issue_b(kb0 + 1, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    store_b(0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    issue_b(kb0 + 2, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    auto iteration = [&](int kb, int st, auto odd_tag) {
+      constexpr int odd = decltype(odd_tag)::value;
+      block_barrier8<C::kAfterA>();
+      issue_a(kb + S - 1, (st + S - 1) % S);
+      __builtin_amdgcn_sched_barrier(0);
+      store_b(odd ^ 1, odd ^ 1);
+      __builtin_amdgcn_sched_barrier(0);
+      issue_b(kb + 3, odd ^ 1);
+    };
+    int kb = kb0;
+    for (; kb + 1 < kb1; kb += 2) {
+      iteration(kb, 0, std::integral_constant<int, 0>{});
+      iteration(kb + 1, 1, std::integral_constant<int, 1>{});
+    }
+    if (kb < kb1) iteration(kb, 0, std::integral_constant<int, 0>{});
+    return;  // no barrier follows the main loop
+  }
+
+  // ---- consumers
+  f4 acc[TM][TN];
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) acc[tm][tn] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  const int a_row0 = wm * TM * 16 + (lane & 15);
+  const int b_row0 = wn * TN * 16 + (lane & 15);
+  const int kc = 2 * (lane >> 4);
+  auto frag = [&](const uint8_t* base, int row) {
+    const u4 lo = *reinterpret_cast<const u4*>(base + swz8(row, kc));
+    const u4 hi = *reinterpret_cast<const u4*>(base + swz8(row, kc + 1));
+    return v8i{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+  };
+  auto iteration = [&](int kb, int st, auto odd_tag) {
+    constexpr int odd = decltype(odd_tag)::value;
+    block_barrier8<C::kAfterA>();
+    const uint8_t* A = a_lds + st * C::kAStage;
+    const uint8_t* B = b_lds + odd * C::kBStage;
+    v8i af[TM];
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm) af[tm] = frag(A, a_row0 + tm * 16);
+    const float* const sc_row = s_lds + odd * BN + wn * TN * 16 + 4 * (lane >> 4);
+    v8i bf[2];
+    bf[0] = frag(B, b_row0);
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) {
+      if (tn + 1 < TN) bf[(tn + 1) & 1] = frag(B, b_row0 + (tn + 1) * 16);
+      const f4 sc = *reinterpret_cast<const f4*>(sc_row + tn * 16);
+      f4 d[TM];
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm)
+        d[tm] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bf[tn & 1], af[tm], f4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0,
+                                                                   0, kNeutralScale, 0, kNeutralScale);
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc[tm][tn][q] = __builtin_fmaf(sc[q], d[tm][q], acc[tm][tn][q]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  int kb = kb0;
+  for (; kb + 1 < kb1; kb += 2) {
+    iteration(kb, 0, std::integral_constant<int, 0>{});
+    iteration(kb + 1, 1, std::integral_constant<int, 1>{});
+  }
+  if (kb < kb1) iteration(kb, 0, std::integral_constant<int, 0>{});
+
+  // ---- epilogue (gemm8_kernel's)
+  const bool partials = split_k > 1;
+  const bool stage_y = !partials && a.epilogue == TF_EPILOGUE_SILU_MUL;
+  uint16_t* const dst = stage_y ? reinterpret_cast<uint16_t*>(ws) : a.out;
+  const int64_t ldd = stage_y ? (int64_t)a.n : a.ldo;
+  const bool residual = !stage_y && a.epilogue == TF_EPILOGUE_RESIDUAL;
+  const bool vec = partials ? (a.n & 3) == 0 && (reinterpret_cast<uintptr_t>(ws) & 15) == 0
+                            : run_store_ok(a, dst, ldd, residual);
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm) {
+    const int m = m0 + (wm * TM + tm) * 16 + (lane & 15);
+    if (m >= a.m) continue;
+    const float rs = row_scale(a, m);
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) {
+      const int n = n0 + (wn * TN + tn) * 16 + 4 * (lane >> 4);
+      if (n >= a.n) continue;
+      float v[4];
+      if (partials) {
+        float* const p = ws + ((int64_t)z * a.m + m) * a.n + n;
+        if (vec) {
+          *reinterpret_cast<f4*>(p) = acc[tm][tn];
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (n + j < a.n) p[j] = acc[tm][tn][j];
+        }
+        continue;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float b = (a.bias && n + j < a.n) ? half_bits_to_float(a.bias[n + j]) : 0.0f;
+        v[j] = acc[tm][tn][j] * rs + b;
+      }
+      store_run4(a, dst, ldd, residual, m, n, v, vec);
+    }
+  }
+}
+
 int effective_split8(const LinearArgs& a, const tf_gemm_config& cfg) {
   const int nkb = a.k / kBK;
   return cfg.split_k < nkb ? cfg.split_k : (nkb > 0 ? nkb : 1);
@@ -388,14 +632,40 @@ int launch_gemm8(const LinearArgs& a, const tf_gemm_config& cfg, float* ws, hipS
   return lds_gemm_finish(a, ws, split, stream);
 }
 
+template <int BM, int BN, int WM, int WN>
+int launch_gemm8pc(const LinearArgs& a, const tf_gemm_config& cfg, float* ws, hipStream_t stream) {
+  using C = G8P<BM, BN, WM, WN, 2>;
+  if (int rc = check_gemm8<BM, BN, WM, WN, 2>(a, cfg)) return rc;
+  const int split = effective_split8(a, cfg);
+  if (lds_gemm_workspace(a, split) > 0 && ws == nullptr)
+    return fail(TF_EINVAL, "tf_w4a8_linear_ex: this config needs a workspace");
+  const int tiles_n = (int)cdiv(a.n, BN);
+  const int tiles_m = (int)cdiv(a.m, BM);
+  const int64_t grid = (int64_t)tiles_n * tiles_m * split;
+  auto kernel = gemm8pc_kernel<BM, BN, WM, WN, 2>;
+  if (C::kLds > 64 * 1024 &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          C::kLds) != hipSuccess)
+    return fail(TF_ELAUNCH, "tf_w4a8_linear_ex: cannot reserve LDS for gemm_fp8");
+  kernel<<<(unsigned)grid, C::kThreads, C::kLds, stream>>>(a, ws, split, tiles_n, tiles_m);
+  if (int rc = check_launch("tf_w4a8_linear_ex(gemm_fp8)")) return rc;
+  return lds_gemm_finish(a, ws, split, stream);
+}
+
 // block_k 128 (one group per block); num_stages = S + 1, as the fp16 pipelined GEMM counts them.
 #define TF_GEMM8(BM, BN, WM, WN, S)                                                                         \
   {{TF_KERNEL_GEMM_FP8, BM, BN, 128, 1, WM * WN, S + 1}, (launch_gemm8<BM, BN, WM, WN, S>), gemm8_workspace, \
    (check_gemm8<BM, BN, WM, WN, S>)}
 
+// num_stages 8: the producer / consumer form (two x stages); num_warps counts the consumer waves.
+#define TF_GEMM8PC(BM, BN, WM, WN)                                                                          \
+  {{TF_KERNEL_GEMM_FP8, BM, BN, 128, 1, WM * WN, 8}, (launch_gemm8pc<BM, BN, WM, WN>), gemm8_workspace, \
+   (check_gemm8<BM, BN, WM, WN, 2>)}
+
 const Variant kGemm8Variants[] = {
     TF_GEMM8(256, 192, 4, 2, 2), TF_GEMM8(256, 128, 4, 2, 2), TF_GEMM8(128, 256, 2, 4, 2),
     TF_GEMM8(256, 160, 4, 2, 2), TF_GEMM8(128, 128, 2, 4, 2), TF_GEMM8(256, 192, 4, 2, 3),
+    TF_GEMM8PC(256, 160, 4, 2), TF_GEMM8PC(256, 128, 4, 2), TF_GEMM8PC(128, 256, 2, 4), TF_GEMM8PC(128, 128, 2, 4),
 };
 
 }  // namespace
