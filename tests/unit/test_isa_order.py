@@ -60,7 +60,7 @@ def test_x_stage_loads_lead_every_barrier_region(source: str, tmp_path: Path) ->
 
 _VMEM = re.compile(r"^(buffer|global|flat|scratch)_(load|store|atomic)")
 _WAIT = re.compile(r"^s_waitcnt\b.*\bvmcnt\((\d+)\)")
-_KERNEL = re.compile(r"^(_Z\w*(gemm2_kernel|gemm3_kernel|gemm4_kernel|gemm8_kernel)I(\w*?)EEv\w*):")
+_KERNEL = re.compile(r"^(_Z\w*(gemm2_kernel|gemm3_kernel|gemm4_kernel|gemm8_kernel|gemm2pc_kernel|gemm8pc_kernel)I(\w*?)EEv\w*):")
 _JUMP = re.compile(r"^s_(c?branch)\w*\s+(\.LBB\w+)")
 _INF = float("inf")
 
@@ -80,7 +80,8 @@ def _instructions(body: list[str]) -> list[str]:
 
 
 def _stages(kernel: str, template_args: str) -> int:
-    """S: the fifth integer template argument of gemm2/3/8_kernel, the fourth of gemm4_kernel."""
+    """S: the fifth integer template argument of gemm2/3/8_kernel and of the producer / consumer
+    forms, the fourth of gemm4_kernel."""
     return [int(v) for v in re.findall(r"Li(\d+)E", template_args + "E")][3 if kernel == "gemm4_kernel" else 4]
 
 
@@ -109,7 +110,7 @@ def _sregs(text: str) -> set[int]:
     return out
 
 
-def _wait_checks(ins: list[str], stages: int) -> list[tuple[int, int, float]]:
+def _wait_checks(ins: list[str], stages: int, consumers: set[int] | None = None) -> list[tuple[int, int, float]]:
     """(barrier index, its vmcnt N, the fewest vector-memory instructions issued after the last
     x load of the stage that barrier guards, over every path that reaches it; -1 where a path
     has no stage left for it).
@@ -126,7 +127,15 @@ def _wait_checks(ins: list[str], stages: int) -> list[tuple[int, int, float]]:
     ``s_andn2_b64 vcc, exec, s[a:b]`` with s[a:b] set by ``s_mov_b64`` to 0 or -1 (exec is
     nonzero: the stage loads are issued by the whole wave). The compiler writes such a pair of
     correlated branches around the two copies of a load it duplicates (an in-range and an
-    out-of-range offset); following both ways would count a path that skips both copies."""
+    out-of-range offset); following both ways would count a path that skips both copies.
+
+    With ``consumers`` (a set, filled here), the producer / consumer forms: a path that reaches
+    a barrier without having issued any x load is a consumer wave's (those waves load nothing
+    and wait on the producers' barrier): it is followed on as a consumer path and every barrier
+    it reaches is collected in ``consumers``. The walk does not know the wave-uniform role
+    branch, so it also follows role-mixing paths no wave takes; those end up consumer paths as
+    well. Every barrier a producer path reaches (one that issued the prologue's x stages) is
+    checked as above; the caller drops only the barriers no producer path reaches."""
     labels = {l[:-1]: i for i, l in enumerate(ins) if l.endswith(":")}
     waits = _block_waits(ins)
     cap = max(waits.values(), default=0) + 1  # counts past every N compare alike
@@ -150,19 +159,19 @@ def _wait_checks(ins: list[str], stages: int) -> list[tuple[int, int, float]]:
     best: dict[int, float] = {}
     seen: set[tuple] = set()
     # (pc, constant pairs, vcc: None unknown / 0 / 1, pending stage counters, this region's
-    # x-load counters, in the prologue)
-    todo: list[tuple] = [(0, (), None, (), (), True)]
+    # x-load counters, in the prologue, a consumer path)
+    todo: list[tuple] = [(0, (), None, (), (), True, False)]
     while todo:
         state = todo.pop()
         if state in seen:
             continue
         seen.add(state)
-        pc, consts, vcc, pending, region, pro = state
+        pc, consts, vcc, pending, region, pro, cons = state
         cmap = dict(consts)
         while pc < len(ins) and live[pc]:
             line = ins[pc]
             if line.endswith(":"):
-                key = (pc + 1, tuple(sorted(cmap.items())), vcc, pending, region, pro)
+                key = (pc + 1, tuple(sorted(cmap.items())), vcc, pending, region, pro, cons)
                 if key in seen:
                     break
                 seen.add(key)
@@ -171,6 +180,12 @@ def _wait_checks(ins: list[str], stages: int) -> list[tuple[int, int, float]]:
             op = line.split()[0]
             args = [a.strip() for a in line[len(op):].split(",")]
             if pc in waits:
+                if consumers is not None and (cons or (pro and not region)):
+                    consumers.add(pc)  # a consumer wave's barrier: it issues no loads
+                    # a consumer path carries no state: every such walk from a pc is the same
+                    cons, pending, region, pro, cmap, vcc = True, (), (), False, {}, None
+                    pc += 1
+                    continue
                 if pro:
                     if not region or len(region) % (stages - 1):
                         best[pc] = -1
@@ -188,13 +203,15 @@ def _wait_checks(ins: list[str], stages: int) -> list[tuple[int, int, float]]:
                 pending = pending[1:]
                 pc += 1
                 continue
-            if _VMEM.match(line):
+            if _VMEM.match(line) and not cons:
                 pending = tuple(min(c + 1, cap) for c in pending)
                 region = tuple(min(c + 1, cap) for c in region)
                 if " lds" in line:
                     # the prologue's stages need each load's counter; an iteration's, its last
                     region = region + (0,) if pro else (0,)
-            if op == "s_mov_b64" and args[0] in wanted and args[1] in ("0", "-1"):
+            if cons:
+                pass
+            elif op == "s_mov_b64" and args[0] in wanted and args[1] in ("0", "-1"):
                 cmap = {k: v for k, v in cmap.items() if not (_sregs(k) & _sregs(args[0]))}
                 cmap[args[0]] = int(args[1])
             elif op == "s_andn2_b64" and args[:2] == ["vcc", "exec"] and args[2] in cmap:
@@ -215,7 +232,7 @@ def _wait_checks(ins: list[str], stages: int) -> list[tuple[int, int, float]]:
                     continue
                 taken = {"s_cbranch_vccnz": vcc, "s_cbranch_vccz": None if vcc is None else 1 - vcc}.get(op)
                 if taken != 0:
-                    todo.append((target, tuple(sorted(cmap.items())), vcc, pending, region, pro))
+                    todo.append((target, tuple(sorted(cmap.items())), vcc, pending, region, pro, cons))
                 if taken == 1:
                     break
             pc += 1
@@ -235,7 +252,14 @@ def _kernel_checks(asm: str) -> dict[str, list[tuple[int, int, float]]]:
         while j < len(lines) and not lines[j].startswith(".Lfunc_end"):
             j += 1
         ins = _instructions(lines[i + 1:j])
-        out[m.group(1)] = _wait_checks(ins, _stages(m.group(2), m.group(3)))
+        if "pc_kernel" in m.group(2):
+            consumers: set[int] = set()
+            rows = _wait_checks(ins, _stages(m.group(2), m.group(3)), consumers)
+            # the barriers only consumer paths reach; every other one is checked
+            out[m.group(1)] = [row for row in rows if not (row[0] in consumers and row[2] == _INF)]
+            assert consumers and len(out[m.group(1)]) < len(rows), f"{m.group(1)}: no consumer barrier found"
+        else:
+            out[m.group(1)] = _wait_checks(ins, _stages(m.group(2), m.group(3)))
         i = j
     return out
 
