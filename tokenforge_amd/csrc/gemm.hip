@@ -217,6 +217,34 @@ __global__ void splitk_reduce_kernel(LinearArgs a, const float* __restrict__ ws,
   }
 }
 
+// Four consecutive columns per thread (NONE / RESIDUAL epilogues, N and the strides in
+// 4-element units): every split's 16-byte load is issued before the sums, which add in split
+// order as reduce_partials does, and the run is stored as one 8-byte piece.
+__global__ __launch_bounds__(256) void splitk_reduce4_kernel(LinearArgs a, const float* __restrict__ ws, int split) {
+  const int64_t total = (int64_t)a.m * a.n;
+  const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (i >= total) return;
+  const int row = (int)(i / a.n);
+  const int col = (int)(i - (int64_t)row * a.n);
+  f4 p[kMaxSplitK];
+#pragma unroll
+  for (int s = 0; s < kMaxSplitK; ++s)
+    if (s < split) p[s] = *reinterpret_cast<const f4*>(ws + (int64_t)s * total + i);
+  const float rs = row_scale(a, row);
+  float v[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float acc = p[0][j];
+#pragma unroll
+    for (int s = 1; s < kMaxSplitK; ++s)
+      if (s < split) acc += p[s][j];
+    acc = acc * rs;
+    if (a.bias) acc += half_bits_to_float(a.bias[col + j]);
+    v[j] = acc;
+  }
+  store_run4(a, a.out, a.ldo, a.epilogue == TF_EPILOGUE_RESIDUAL, row, col, v, true);
+}
+
 }  // namespace
 
 // SiLU*mul over an fp16 y [m, n] (row stride n) staged in the workspace.
@@ -237,6 +265,14 @@ int silu_mul_staged(const LinearArgs& a, const float* ws, hipStream_t stream) {
 }
 
 int splitk_reduce(const LinearArgs& a, const float* ws, int split, hipStream_t stream) {
+  const bool residual = a.epilogue == TF_EPILOGUE_RESIDUAL;
+  const auto al = [](const void* p, uintptr_t b) { return (reinterpret_cast<uintptr_t>(p) & (b - 1)) == 0; };
+  if (a.epilogue != TF_EPILOGUE_SILU_MUL && split <= kMaxSplitK && (a.n & 3) == 0 && (a.ldo & 3) == 0 &&
+      al(a.out, 8) && al(ws, 16) && (!residual || ((a.ldr & 3) == 0 && al(a.residual, 8)))) {
+    const int64_t runs = (int64_t)a.m * a.n / 4;
+    splitk_reduce4_kernel<<<(unsigned)cdiv(runs, 256), 256, 0, stream>>>(a, ws, split);
+    return check_launch("tf_w4a16_linear(splitk_reduce)");
+  }
   const int64_t total = (int64_t)a.m * (a.epilogue == TF_EPILOGUE_SILU_MUL ? a.n >> 1 : a.n);
   splitk_reduce_kernel<<<(unsigned)cdiv(total, 256), 256, 0, stream>>>(a, ws, split);
   return check_launch("tf_w4a16_linear(splitk_reduce)");
